@@ -1,0 +1,254 @@
+"""Benchmark of the convolution hot path on one MI355X (BASELINE metric: conv fwd+dgrad+wgrad fp32 TFLOP/s and % of
+fp32-MFMA peak).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5|c1] [--no-cpu]
+
+One step = forward + grad-input + grad-weight of every conv layer of the workload, over one synthetic batch already
+resident in HBM:
+  c5 (default): BASELINE config 5, the ResNet-50 body at batch 256, 224x224 input: 3x3 s1 p1 convs at
+                (C=K=64, 56x56), (128, 28x28), (256, 14x14), (512, 7x7) and the 1x1 C->4C / 4C->C convs at the
+                same sizes; x, w, gy ~ N(0,1) / sqrt(C*R*S). 1341.6 GFLOP per step.
+  c1:           BASELINE config 1, AlexNet conv1 (16x3x224x224, 64x11x11, stride 4, pad 2). 6.747 GFLOP per step.
+FLOPs per direction = 2*N*K*OH*OW*C*R*S (never the padded or stride-phase-expanded work).
+
+The roofline object reports the dominant kernel, conv_gather_kernel, from its forward launches (one kernel per
+call): algorithmic FLOPs per launch over the launch's HIP-event duration, measured on the launch stream inside the
+timed steps. cpu_baseline times the CPU oracle (oracle/, a scalar-per-thread float64 restatement of the reference
+algorithm) on a bounded sample of the same workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the
+reference's CPU path) on a sample. Both are baselines, not targets.
+"""
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "omarchy-mac-torch_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP32_MFMA = 157.3e12  # MI355X dense fp32 matrix peak, FLOP/s
+PEAK_HBM = 8.0e12          # bytes/s
+
+C5_LAYERS = [
+    # name, n, c, k, h, ks, stride, pad
+    ("3x3_56", 256, 64, 64, 56, 3, 1, 1), ("3x3_28", 256, 128, 128, 28, 3, 1, 1),
+    ("3x3_14", 256, 256, 256, 14, 3, 1, 1), ("3x3_7", 256, 512, 512, 7, 3, 1, 1),
+    ("1x1_exp_56", 256, 64, 256, 56, 1, 1, 0), ("1x1_red_56", 256, 256, 64, 56, 1, 1, 0),
+    ("1x1_exp_28", 256, 128, 512, 28, 1, 1, 0), ("1x1_red_28", 256, 512, 128, 28, 1, 1, 0),
+    ("1x1_exp_14", 256, 256, 1024, 14, 1, 1, 0), ("1x1_red_14", 256, 1024, 256, 14, 1, 1, 0),
+    ("1x1_exp_7", 256, 512, 2048, 7, 1, 1, 0), ("1x1_red_7", 256, 2048, 512, 7, 1, 1, 0),
+]
+C1_LAYERS = [("alexnet_conv1", 16, 3, 64, 224, 11, 4, 2)]
+
+
+def out_size(h, ks, s, p):
+    return (h + 2 * p - ks) // s + 1
+
+
+def flops_dir(n, c, k, h, ks, s, p):
+    o = out_size(h, ks, s, p)
+    return 2.0 * n * k * o * o * c * ks * ks
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model
+
+
+def oracle_baseline(layers, budget_s=20.0):
+    """The CPU oracle on a bounded sample: each layer at batch 1, fwd+dgrad+wgrad, repeated until ~budget_s."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(0)
+    flops = secs = 0.0
+    t_start = time.time()
+    done = 0
+    while time.time() - t_start < budget_s:
+        for (name, n, c, k, h, ks, s, p) in layers:
+            scale = (c * ks * ks) ** -0.5
+            x = rng.standard_normal((1, c, h, h)).astype(np.float32)
+            w = (rng.standard_normal((k, c, ks, ks)) * scale).astype(np.float32)
+            t0 = time.time()
+            y = orc.conv_fwd(x, w, None, s, p)
+            gy = (rng.standard_normal(y.shape) * scale).astype(np.float32)
+            orc.conv_dgrad(gy, w, x.shape, s, p)
+            orc.conv_wgrad(x, gy, ks, s, p)
+            secs += time.time() - t0
+            flops += 3 * flops_dir(1, c, k, h, ks, s, p)
+            done += 1
+            if time.time() - t_start > budget_s:
+                break
+    threads = int(os.environ.get("OMP_NUM_THREADS", str(len(os.sched_getaffinity(0)))))
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{done} layer passes (fwd+dgrad+wgrad) of the workload's layers at batch 1, "
+                      f"{flops / 1e9:.1f} GFLOP in {secs:.1f} s, float64 OpenMP oracle, {cpu_info()}"}
+
+
+def torch_cpu_baseline(layers, batch, threads):
+    """PyTorch CPU fp32 conv fwd + convolution_backward on the same layer shapes at a reduced batch."""
+    import torch
+
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    flops = secs = 0.0
+    for (name, n, c, k, h, ks, s, p) in layers:
+        scale = (c * ks * ks) ** -0.5
+        x = torch.randn((batch, c, h, h), generator=g)
+        w = torch.randn((k, c, ks, ks), generator=g) * scale
+        o = out_size(h, ks, s, p)
+        gy = torch.randn((batch, k, o, o), generator=g) * scale
+
+        def step():
+            torch.nn.functional.conv2d(x, w, None, s, p)
+            torch.ops.aten.convolution_backward(gy, x, w, None, [s, s], [p, p], [1, 1], False, [0, 0], 1,
+                                                [True, True, False])
+
+        step()
+        reps = 0
+        t0 = time.time()
+        while reps < 2 or time.time() - t0 < 0.5:
+            step()
+            reps += 1
+        secs += (time.time() - t0) / reps
+        flops += 3 * flops_dir(batch, c, k, h, ks, s, p)
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "sample": f"PyTorch {torch.__version__} CPU fp32 conv fwd+convolution_backward over the workload's layers "
+                      f"at batch {batch}, {cpu_info()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=["c5", "c1"], default="c5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
+              "its batch share; see the sharding note in the design document). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from omarchy_mac_torch import hip_ops
+
+    dev = torch.device("cuda:0")
+    layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
+    gen = torch.Generator(device=dev).manual_seed(0)
+    data = []
+    for (name, n, c, k, h, ks, s, p) in layers:
+        scale = (c * ks * ks) ** -0.5
+        o = out_size(h, ks, s, p)
+        x = torch.randn((n, c, h, h), device=dev, generator=gen) * scale
+        w = torch.randn((k, c, ks, ks), device=dev, generator=gen) * scale
+        gy = torch.randn((n, k, o, o), device=dev, generator=gen) * scale
+        data.append((name, n, c, k, h, ks, s, p, x, w, gy))
+
+    stream = torch.cuda.current_stream(dev)
+    fwd_events = []  # (flops, start, end) per forward launch in the timed steps
+    dir_events = {"fwd": [], "dgrad": [], "wgrad": []}
+
+    def step(timed):
+        for (name, n, c, k, h, ks, s, p, x, w, gy) in data:
+            f = flops_dir(n, c, k, h, ks, s, p)
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if timed else None
+            if timed:
+                evs[0].record(stream)
+            hip_ops.conv2d(x, w, None, s, p)
+            if timed:
+                evs[1].record(stream)
+            hip_ops.conv2d_dgrad(gy, w, x.shape, s, p)
+            if timed:
+                evs[2].record(stream)
+            hip_ops.conv2d_wgrad(x, gy, ks, s, p)
+            if timed:
+                evs[3].record(stream)
+                fwd_events.append((f, evs[0], evs[1]))
+                dir_events["fwd"].append((name, f, evs[0], evs[1]))
+                dir_events["dgrad"].append((name, f, evs[1], evs[2]))
+                dir_events["wgrad"].append((name, f, evs[2], evs[3]))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    step_flops = sum(3 * flops_dir(n, c, k, h, ks, s, p) for (_, n, c, k, h, ks, s, p, *_r) in data)
+    ms_per_step = elapsed / args.steps * 1e3
+    value = step_flops * args.steps / elapsed / 1e12
+
+    fwd_ms = [a.elapsed_time(b) for (_, a, b) in fwd_events]
+    fwd_flops = [f for (f, _, _) in fwd_events]
+    avg_launch_ms = sum(fwd_ms) / len(fwd_ms)
+    achieved = sum(fwd_flops) / (sum(fwd_ms) / 1e3) / 1e12  # TFLOP/s over all forward launches
+    per_dir = {}
+    per_layer = {}
+    for d, evs in dir_events.items():
+        tot_f = sum(f for (_, f, _, _) in evs)
+        tot_ms = sum(a.elapsed_time(b) for (_, _, a, b) in evs)
+        per_dir[d] = {"tflops": round(tot_f / (tot_ms / 1e3) / 1e12, 2),
+                      "frac_peak": round(tot_f / (tot_ms / 1e3) / PEAK_FP32_MFMA, 4),
+                      "ms_per_step": round(tot_ms / args.steps, 4)}
+        for (name, f, a, b) in evs:
+            per_layer.setdefault(name, {}).setdefault(d, []).append(a.elapsed_time(b))
+    layer_flops = {l[0]: flops_dir(*l[1:8]) for l in data}
+    layer_tflops = {name: {d: round(layer_flops[name] / (sum(v) / len(v) / 1e3) / 1e12, 1) for d, v in dd.items()}
+                    for name, dd in per_layer.items()}
+
+    out = {
+        "metric": "conv fwd+dgrad+wgrad fp32 TFLOP/s (% of fp32-MFMA peak)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": ("C5 ResNet-50 body b256 224^2: 3x3 s1 convs at (64,56^2),(128,28^2),(256,14^2),"
+                                "(512,7^2) + 1x1 C->4C and 4C->C at the same sizes, fwd+dgrad+wgrad"
+                                if args.workload == "c5" else
+                                "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad"),
+                   "gflop_per_step": round(step_flops / 1e9, 2), "layout": "NCHW"},
+        "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
+        "roofline": {"kernel": "conv_gather_kernel (forward launches)", "bound": "mfma",
+                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "avg_launch_ms": round(avg_launch_ms, 4),
+                     "flop_per_launch_avg": round(sum(fwd_flops) / len(fwd_flops))},
+        "per_direction": per_dir,
+        "per_layer_tflops": layer_tflops,
+        "device": torch.cuda.get_device_name(dev),
+    }
+    if not args.no_cpu:
+        threads = len(os.sched_getaffinity(0))
+        out["cpu_baseline"] = oracle_baseline(layers, budget_s=15.0)
+        out["torch_cpu_baseline"] = torch_cpu_baseline(layers, batch=8 if args.workload == "c5" else 16,
+                                                       threads=threads)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,190 @@
+/*
+ * omt_hip.h -- C ABI of libomt_hip.so, the MI355X (gfx950) implementation of omarchy-mac-torch's convolution hot
+ * path: implicit-GEMM conv forward / grad-input / grad-weight on fp32 MFMA, bias grad, depthwise, BatchNorm
+ * (train / eval / backward, optional fused ReLU), max / average / adaptive-average pooling, and the device memory
+ * and stream services the operator layer needs.
+ *
+ * Conventions
+ *  - Tensors are dense NCHW float32 device pointers (weights [co][ci][ks][ks]); the caller makes inputs contiguous.
+ *  - Every compute entry point is asynchronous on `stream` (a hipStream_t; NULL = the HIP null stream, as in the
+ *    HIP runtime API) and returns an omt_status. OMT_UNSUPPORTED means "this geometry is not covered" (the operator layer then records a
+ *    fallback, as the reference's NEED() does); any other non-zero status carries a message in omt_last_error().
+ *  - Entry points that need scratch memory take a caller-provided workspace; its size comes from the matching
+ *    *_workspace() query. The library never frees or retains caller pointers.
+ *  - Not thread-safe per stream: the caller serializes calls that share a stream (the reference serializes every op
+ *    behind one recursive mutex, csrc/omt.h:62-64).
+ *
+ * Each declaration names the reference interface it replaces (file:line in the omarchy-mac-torch sources).
+ */
+#ifndef OMT_HIP_H
+#define OMT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum omt_status {
+  OMT_OK = 0,
+  OMT_UNSUPPORTED = 1,  /* not covered: the caller falls back (reference: NEED() -> Unsupported, csrc/omt.h:168-176) */
+  OMT_OOM = 2,          /* device allocation failed after emptying the cache (csrc/runtime.cpp:220-225) */
+  OMT_DEVICE_ERROR = 3, /* a HIP runtime error (reference: uncaptured wgpu error, csrc/runtime.cpp:60-81) */
+  OMT_INVALID = 4       /* bad arguments (shape mismatch, null pointer, workspace too small) */
+} omt_status;
+
+/* Convolution geometry: output size oh = (ih + 2*pad - ks) / stride + 1. Replaces Geo (csrc/omt.h:224-229). */
+typedef struct omt_conv_geo {
+  int64_t n, ci, co, ih, iw, oh, ow, ks, stride, pad;
+} omt_conv_geo;
+
+/* conv kinds, as conv_kind() classifies them (csrc/conv.cpp:167-177) */
+enum { OMT_CONV_NONE = 0, OMT_CONV_DENSE = 1, OMT_CONV_DW = 2, OMT_CONV_DWG = 3 };
+
+/* forward epilogue bits (omarchy_mac_torch/gemm.py:38-39) */
+enum { OMT_EPI_BIAS = 1u, OMT_EPI_RELU = 2u };
+
+/* ---- library, errors, geometry ---------------------------------------------------------------------------- */
+
+/* Message of the last non-OK status returned on this thread ("" if none). */
+const char* omt_last_error(void);
+/* ABI version (bumped on any signature change) and the HIP runtime version the library was built against.
+ * Replaces built_with_torch (csrc/module.cpp:59) as the build guard. */
+int omt_abi_version(void);
+int omt_hip_runtime_version(void);
+/* Fills g; replaces conv_geo (csrc/conv.cpp:19-21). */
+void omt_conv_geo_init(omt_conv_geo* g, int64_t n, int64_t ci, int64_t co, int64_t ih, int64_t iw, int64_t ks,
+                       int64_t stride, int64_t pad);
+/* Replaces conv_kind (csrc/conv.cpp:167-177): returns OMT_CONV_*. x_c = input channels, w_o = weight rows. */
+int omt_conv_kind(int64_t x_c, int64_t w_o, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                  int64_t dh, int64_t dw, int transposed, int64_t groups);
+
+/* ---- device memory and streams (replace the wgpu buffer pool and recorder, csrc/runtime.cpp:177-249, 451-527) --- */
+
+/* Caching allocator with size classes; freed blocks are reused in stream order. Replaces alloc_buf/free_buf
+ * (csrc/runtime.cpp:205-231) and the PrivateUse1 Allocator (csrc/device.cpp:18-30). */
+int omt_malloc(void** ptr, size_t bytes);
+int omt_free(void* ptr);
+int omt_empty_cache(void);                 /* csrc/runtime.cpp:233-240 (empty_cache) */
+size_t omt_memory_allocated(void);         /* csrc/runtime.cpp:242 */
+size_t omt_memory_reserved(void);          /* csrc/runtime.cpp:243 */
+/* Caps the bytes the allocator may hold (0 = no cap); exceeding it behaves as an out-of-memory (OMT_OOM). */
+void omt_set_memory_limit(size_t bytes);
+/* A non-blocking stream owned by the library (created on first use), for callers without a stream of their own. */
+void* omt_default_stream(void);
+/* kind: 0 host->device, 1 device->host, 2 device->device. Asynchronous on stream (device->host: synchronous).
+ * Replaces upload/download_bytes and copy_dev (csrc/runtime.cpp:614-676). */
+int omt_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+int omt_memset_zero(void* dst, size_t bytes, void* stream);
+int omt_stream_sync(void* stream);         /* replaces sync_all (csrc/runtime.cpp:520-527) */
+/* Events (replace the submission-index events of the device guard, csrc/device.cpp:124-161). */
+int omt_event_create(void** ev);
+int omt_event_destroy(void* ev);
+int omt_event_record(void* ev, void* stream);
+int omt_event_query(void* ev);             /* 1 = complete, 0 = pending, <0 = error */
+int omt_event_sync(void* ev);
+int omt_event_elapsed_ms(void* start, void* end, float* ms);
+
+/* ---- dense convolution (implicit GEMM on fp32 MFMA) ------------------------------------------------------- */
+
+/* Forward: y[n][co][oh][ow] = sum_{ci,ky,kx} x[n][ci][oy*s+ky-p][ox*s+kx-p] * w[co][ci][ky][kx], then
+ * + bias[co] (epilogue & OMT_EPI_BIAS) and ReLU (epilogue & OMT_EPI_RELU).
+ * bn_mean/var/gamma/beta non-NULL (all four): the input is first mapped through the previous layer's eval BatchNorm
+ * + ReLU, max((x - mean[ci]) * rsqrt(var[ci] + eps) * gamma[ci] + beta[ci], 0), on in-bounds taps only (padding
+ * stays zero). Replaces gemm_forward (csrc/conv.cpp:70-77) with kinds 0 and 3 (omarchy_mac_torch/gemm.py:25-42,
+ * 139-141). Dense means: ks 1..11, stride 1..4, 0 <= pad <= ks. */
+int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
+                 const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta, float bn_eps,
+                 float* y, void* stream);
+
+/* Grad input: gx = conv_transpose(gy, w). Stride 1 is one GEMM over flipped, transposed weights; stride s > 1 is
+ * s*s dense stride-phase GEMMs in one launch (phases no tap reaches write zeros). Replaces gemm_grad_input
+ * (csrc/conv.cpp:78-101; kinds 1 and 5, omarchy_mac_torch/gemm.py:43-80). */
+size_t omt_conv_dgrad_workspace(const omt_conv_geo* g);
+int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Grad weight: gw[co][ci][ky][kx] = sum_{n,oy,ox} gy[n][co][oy][ox] * x[n][ci][oy*s+ky-p][ox*s+kx-p], split-K over
+ * n*oh*ow with a deterministic in-order reduction of the partials. Replaces gemm_grad_weight (csrc/conv.cpp:102-114;
+ * kind 2, omarchy_mac_torch/gemm.py:81-91; gemm_reduce.wgsl). */
+size_t omt_conv_wgrad_workspace(const omt_conv_geo* g);
+int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Bias grad gb[c] = sum_{n,hw} gy[n][c][hw]. Replaces csum_nchw (csrc/conv.cpp:232-235). */
+int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream);
+
+/* BatchNorm folding (fold_bn, csrc/fused.cpp:34-40): scale = gamma / sqrt(var + eps) per output channel,
+ * fw = cw * scale, fb = (cb - mean) * scale + beta (cb may be NULL). per_out = ci * ks * ks. */
+int omt_fold_bn(int64_t co, int64_t per_out, const float* cw, const float* cb, const float* gamma, const float* beta,
+                const float* mean, const float* var, float eps, float* fw, float* fb, void* stream);
+
+/* ---- depthwise (groups = C) ------------------------------------------------------------------------------- */
+
+/* Any ks <= 11, stride 1..4, 0 <= pad <= ks (g->ci == g->co == C). Replace dw_fwd / dwg_fwd / dw_fwd_bn,
+ * dw_gin / dwg_gin, dw_gwt / dwg_gwt (csrc/conv.cpp:194-198, 222-229; csrc/plans.cpp:145-158). bias may be NULL;
+ * bn_* as in omt_conv_fwd (dw_fwd_bn.wgsl). */
+int omt_dw_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias, const float* bn_mean,
+               const float* bn_var, const float* bn_gamma, const float* bn_beta, float bn_eps, float* y, void* stream);
+int omt_dw_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* stream);
+size_t omt_dw_wgrad_workspace(const omt_conv_geo* g);
+int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* ---- BatchNorm (NCHW, affine) ----------------------------------------------------------------------------- */
+
+/* Training forward: per-channel biased mean / variance over n*hw, y = (x - mean) * invstd * gamma + beta
+ * (ReLU if relu), save_mean / save_invstd written, and the running stats updated
+ * rm' = rm + momentum*(mean - rm), rv' = rv + momentum*(var * m/(m-1) - rv) into new_rm / new_rv (which may alias
+ * running_mean / running_var for the in-place native_batch_norm form, or be NULL to skip the update).
+ * Replaces batch_norm_ training (csrc/nn.cpp:38-48) and omt::bn_relu_train (csrc/fused.cpp:68-84). */
+size_t omt_bn_train_workspace(int64_t n, int64_t c, int64_t hw);
+int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
+                     const float* running_mean, const float* running_var, double momentum, double eps, int relu,
+                     float* y, float* save_mean, float* save_invstd, float* new_rm, float* new_rv, void* workspace,
+                     size_t workspace_bytes, void* stream);
+/* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
+ * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
+int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
+                    const float* running_mean, const float* running_var, double eps, int relu, float* y,
+                    void* stream);
+/* Backward (training statistics): with gz = g (or g masked by relu_y > 0 when relu_y is non-NULL),
+ * dgamma = sum gz * xhat, dbeta = sum gz, gx = gamma * invstd / m * (m * gz - dbeta - xhat * dgamma).
+ * gx, dgamma, dbeta may each be NULL. Replaces batch_norm_backward_ (csrc/nn.cpp:60-78) and omt::bn_relu_backward
+ * (csrc/fused.cpp:86-115). */
+size_t omt_bn_bwd_workspace(int64_t n, int64_t c, int64_t hw);
+int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, const float* x, const float* relu_y,
+               const float* save_mean, const float* save_invstd, const float* gamma, float* gx, float* dgamma,
+               float* dbeta, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- pooling (planes = n * c) ----------------------------------------------------------------------------- */
+
+/* Max pool, any window / stride / padding / dilation; idx = int64 flat position in the input plane, first maximum
+ * wins ties, NaN propagates. Replaces max_pool2d_with_indices(_backward) (csrc/nn.cpp:157-178). */
+int omt_maxpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                    int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, const float* x, float* y,
+                    int64_t* idx, void* stream);
+int omt_maxpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                    int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, const float* g,
+                    const int64_t* idx, float* gx, void* stream);
+/* Average pool with PyTorch's divisor rules (count_include_pad, divisor_override > 0). Replaces
+ * avg_pool2d(_backward) (csrc/nn.cpp:180-204). */
+int omt_avgpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                    int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad, int64_t divisor_override,
+                    const float* x, float* y, void* stream);
+int omt_avgpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                    int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad, int64_t divisor_override,
+                    const float* g, float* gx, void* stream);
+/* Adaptive average pool, bins [floor(o*in/out), ceil((o+1)*in/out)). Replaces _adaptive_avg_pool2d(_backward)
+ * (csrc/nn.cpp:206-222). */
+int omt_adapool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* x, float* y,
+                    void* stream);
+int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* g, float* gx,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMT_HIP_H */

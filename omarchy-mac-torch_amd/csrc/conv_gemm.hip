@@ -1,0 +1,670 @@
+// Dense convolution as im2col-free implicit GEMM on gfx950 fp32 MFMA (v_mfma_f32_16x16x4_f32).
+//
+// Forward and grad-input share one kernel, conv_gather_kernel: C[p][q] = sum_k Wt[p][k] * X(k, q), where p is an
+// output channel, q = (n, oy, ox) an output pixel and k = (c, ky, kx) a tap; X(k, q) gathers the source image at
+// (oy*S + ky - PH, ox*S + kx - PW), zero outside. Grad input is the same contraction over gy with re-packed weights,
+// split into stride phases (reference: gemm_grad_input, csrc/conv.cpp:78-101, and the phase loader,
+// omarchy_mac_torch/gemm.py:60-80): for phase (py, px) of stride s,
+//   gx[n, ci, py + s*i, px + s*j] = sum_{co, a < jy, b < jx} gy[n, co, i + qy - a, j + qx - b] * w[co, ci, ky0 + s*a, kx0 + s*b]
+// with ky0 = (py + pad) mod s, jy = ceil((ks - ky0) / s), qy = (py + pad - ky0) / s. Writing a' = jy - 1 - a turns
+// each phase into a stride-1 gather with window jy x jx and padding jy - 1 - qy over weights
+// W'[ci][co][a'][b'] = w[co][ci][ky0 + s*(jy-1-a')][kx0 + s*(jx-1-b')]. Stride 1 is the single phase (0, 0), whose
+// W' is the flipped, transposed filter. All phases run in one launch (grid z).
+//
+// Grad weight, conv_wgrad_kernel: C[co][q'] = sum_k gy[k][co] * X(k, q') with k = (n, oy, ox) the reduction over
+// output pixels and q' = (ci, ky, kx), split over k into grid-z slices whose partials are summed in slice order by
+// split_reduce_kernel (reference: gemm_grad_weight + gemm_reduce, csrc/conv.cpp:102-114).
+//
+// Tiling: a 256-thread workgroup computes a BP x BQ tile of C as 4 waves, each a WP x WQ block of 16x16 MFMA tiles,
+// with the operands staged through double-buffered LDS. MFMA 16x16x4 lane layout: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; the accumulator holds D[4*(l/16) + r][l%16] in element r. Because the reduction order inside a
+// K-block is free, lane group g = l/16 reads K-row g*(BK/4) + s at step s, which spreads the four groups over
+// distinct LDS banks.
+#include "omt_internal.h"
+
+namespace omt {
+
+constexpr int kMaxPhases = 16;
+
+struct Phase {
+  int KH, KW, S, PH, PW;  // gather window, stride and (signed) padding
+  int OH, OW;             // output grid of this phase; q = (n, oy, ox) decomposes over it
+  int K, Q;               // C * KH * KW, n * OH * OW
+  int os, oy0, ox0;       // output scatter: y row = oy * os + oy0, column = ox * os + ox0
+  int woff;               // offset of this phase's [P][K] weights (floats)
+  FastDiv div_ohw, div_ow, div_kk, div_kw;
+};
+
+struct GatherArgs {
+  const float* x;  // gather source [N][C][H][W]
+  const float* w;  // weights, per phase [P][K] at woff
+  const float* bias;
+  const float *bn_mean, *bn_var, *bn_gamma, *bn_beta;  // previous layer's eval BN + ReLU on the source, or null
+  float bn_eps;
+  int relu;
+  float* y;  // [N][P][YH][YW]
+  int C, H, W, P, YH, YW;
+  int nphase;
+  Phase ph[kMaxPhases];
+};
+
+template <int BP, int BQ, int WP, int WQ>
+__global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
+  constexpr int BK = 16, NT = 256;
+  constexpr int WGQ = BQ / WQ;
+  static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
+  static_assert(WP % 16 == 0 && WQ % 16 == 0 && BQ >= 64 && NT % BQ == 0, "tile shape");
+  constexpr int TI = WP / 16, TJ = WQ / 16;
+  constexpr int LA = BP + 4, LB = BQ + 4;  // LDS pitches: 4 * pitch = 16 (mod 32) keeps lane groups on distinct banks
+  constexpr int AR = BP * BK / NT;         // weight elements per thread
+  constexpr int BR = BQ * BK / NT;         // gathered k-rows per thread
+  static_assert(AR >= 1 && BR >= 1, "tile too small");
+  __shared__ float As[2][BK * LA];
+  __shared__ float Bs[2][BK * LB];
+
+  const Phase& ph = a.ph[blockIdx.z];
+  const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
+  if (q0 >= ph.Q) return;  // this phase has fewer pixel tiles than the largest one
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave / WGQ, wq = wave % WGQ;
+  const int KH = ph.KH, KW = ph.KW, K = ph.K, KK = KH * KW;
+  const int H = a.H, W = a.W, HW = H * W, P = a.P;
+  const float* __restrict__ wt = a.w + ph.woff;
+
+  // this thread's output pixel (column of the gathered operand)
+  const int qc = t % BQ;
+  const int rbase = __builtin_amdgcn_readfirstlane((t / BQ) * BR);
+  int iy0 = -(1 << 28), ix0 = -(1 << 28);  // pixels past Q gather nothing
+  const float* __restrict__ xb = a.x;
+  {
+    const int q = q0 + qc;
+    if (q < ph.Q) {
+      const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+      const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+      const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+      iy0 = (int)oy * ph.S - ph.PH;
+      ix0 = (int)ox * ph.S - ph.PW;
+      xb = a.x + (int64_t)n * a.C * HW;
+    }
+  }
+  const int pix = iy0 * W + ix0;
+
+  // wave-uniform tap state (c, ky, kx), decomposed afresh at the start of every K-block
+  int sc = 0, sky = 0, skx = 0;
+  const bool has_bn = a.bn_mean != nullptr;
+
+  float ra[AR], rb[BR];
+  auto gload = [&](int k0) {
+    {
+      const uint32_t kb = (uint32_t)(k0 + rbase);
+      sc = (int)fdiv(kb, ph.div_kk);
+      const uint32_t r = kb - (uint32_t)sc * (uint32_t)KK;
+      sky = (int)fdiv(r, ph.div_kw);
+      skx = (int)r - sky * KW;
+    }
+#pragma unroll
+    for (int i = 0; i < AR; ++i) {
+      const int kk = t % BK, p = p0 + t / BK + (NT / BK) * i, k = k0 + kk;
+      ra[i] = (p < P && k < K) ? wt[p * K + k] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < BR; ++j) {
+      const bool kval = k0 + rbase + j < K;
+      const int iy = iy0 + sky, ix = ix0 + skx;
+      float v = 0.f;
+      if (kval && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) {
+        v = xb[pix + sc * HW + sky * W + skx];
+        if (has_bn) {
+          const float inv = rsqrtf(a.bn_var[sc] + a.bn_eps);
+          v = fmaxf((v - a.bn_mean[sc]) * inv * a.bn_gamma[sc] + a.bn_beta[sc], 0.f);
+        }
+      }
+      rb[j] = v;
+      if (++skx == KW) {
+        skx = 0;
+        if (++sky == KH) {
+          sky = 0;
+          ++sc;
+        }
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AR; ++i) As[buf][(t % BK) * LA + t / BK + (NT / BK) * i] = ra[i];
+#pragma unroll
+    for (int j = 0; j < BR; ++j) Bs[buf][(rbase + j) * LB + qc] = rb[j];
+  };
+
+  omt_f32x4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (K + BK - 1) / BK;
+  if (nk > 0) {
+    gload(0);
+    sstore(0);
+  }
+  __syncthreads();
+  const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
+  for (int it = 0; it < nk; ++it) {
+    const int cur = it & 1;
+    if (it + 1 < nk) gload((it + 1) * BK);
+#pragma unroll
+    for (int s = 0; s < BK / 4; ++s) {
+      const int kr = grp * (BK / 4) + s;
+      float av[TI], bv[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) av[i] = As[cur][kr * LA + la + 16 * i];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) bv[j] = Bs[cur][kr * LB + lb + 16 * j];
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (it + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid)
+  const int64_t yhw = (int64_t)a.YH * a.YW;
+  const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
+    if (q >= ph.Q) continue;
+    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+    const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+    float* yb = a.y + (int64_t)n * P * yhw + (int64_t)((int)oy * ph.os + ph.oy0) * a.YW + (int)ox * ph.os + ph.ox0;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
+        if (p < P) {
+          float v = acc[i][j][r4];
+          if (a.bias) v += a.bias[p];
+          if (a.relu) v = fmaxf(v, 0.f);
+          yb[(int64_t)p * yhw] = v;
+        }
+      }
+  }
+}
+
+// ---- grad weight ------------------------------------------------------------------------------------------------
+
+struct WgradArgs {
+  const float* x;   // [N][C][H][W]
+  const float* gy;  // [N][P][OH][OW]
+  float* out;       // [slices][P][Q]
+  int C, H, W, P, OH, OW, KS, S, PAD;
+  int Q, K;    // C * KS * KS, N * OH * OW
+  int kslice;  // pixels per slice, a multiple of the K-block
+  FastDiv div_ohw, div_ow, div_kk, div_ks;
+};
+
+template <int BP, int BQ, int WP, int WQ>
+__global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
+  constexpr int BK = 64;  // one reduction pixel per lane
+  constexpr int WGQ = BQ / WQ;
+  static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
+  static_assert(WP % 16 == 0 && WQ % 16 == 0 && BP % 4 == 0 && BQ % 4 == 0, "tile shape");
+  constexpr int TI = WP / 16, TJ = WQ / 16;
+  constexpr int LA = BP + 1, LB = BQ + 1;  // odd pitches: lanes writing consecutive K-rows hit distinct banks
+  constexpr int AR = BP / 4, BR = BQ / 4;  // rows (cols) each wave stages per K-block
+  __shared__ float As[BK * LA];
+  __shared__ float Bs[BK * LB];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave / WGQ, wq = wave % WGQ;
+  const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
+  const int kbeg = blockIdx.z * a.kslice;
+  const int kend = min(a.K, kbeg + a.kslice);
+  const int H = a.H, W = a.W, HW = H * W, P = a.P, Q = a.Q;
+  const int ohw = a.OH * a.OW;
+
+  float ra[AR], rb[BR];
+  auto gload = [&](int k0) {
+    const int k = k0 + lane;
+    const bool kval = k < kend;
+    int64_t gbase = 0, xbase = 0;
+    int iy0 = -(1 << 28), ix0 = -(1 << 28);
+    if (kval) {
+      const uint32_t n = fdiv((uint32_t)k, a.div_ohw), r = (uint32_t)k - n * (uint32_t)ohw;
+      const uint32_t oy = fdiv(r, a.div_ow), ox = r - oy * (uint32_t)a.OW;
+      gbase = (int64_t)n * P * ohw + r;
+      iy0 = (int)oy * a.S - a.PAD;
+      ix0 = (int)ox * a.S - a.PAD;
+      xbase = (int64_t)n * a.C * HW + iy0 * W + ix0;
+    }
+#pragma unroll
+    for (int i = 0; i < AR; ++i) {
+      const int p = p0 + wave + 4 * i;
+      ra[i] = (kval && p < P) ? a.gy[gbase + (int64_t)p * ohw] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < BR; ++j) {
+      const int q = q0 + wave + 4 * j;  // wave-uniform tap column (c, ky, kx)
+      const uint32_t c = fdiv((uint32_t)q, a.div_kk), rr = (uint32_t)q - c * (uint32_t)(a.KS * a.KS);
+      const uint32_t ky = fdiv(rr, a.div_ks), kx = rr - ky * (uint32_t)a.KS;
+      const int iy = iy0 + (int)ky, ix = ix0 + (int)kx;
+      float v = 0.f;
+      if (q < Q && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+        v = a.x[xbase + (int64_t)c * HW + (int)ky * W + (int)kx];
+      rb[j] = v;
+    }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < AR; ++i) As[lane * LA + wave + 4 * i] = ra[i];
+#pragma unroll
+    for (int j = 0; j < BR; ++j) Bs[lane * LB + wave + 4 * j] = rb[j];
+  };
+
+  omt_f32x4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
+  if (kbeg < kend) gload(kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    sstore();
+    __syncthreads();
+    if (k0 + BK < kend) gload(k0 + BK);
+#pragma unroll 4
+    for (int s = 0; s < BK / 4; ++s) {
+      const int kr = grp * (BK / 4) + s;
+      float av[TI], bv[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) av[i] = As[kr * LA + la + 16 * i];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) bv[j] = Bs[kr * LB + lb + 16 * j];
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  float* out = a.out + (int64_t)blockIdx.z * P * Q;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
+    if (q >= Q) continue;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
+        if (p < P) out[(int64_t)p * Q + q] = acc[i][j][r4];
+      }
+  }
+}
+
+// Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i].
+__global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                           int64_t n, int slices) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int z = 0; z < slices; ++z) s += part[(int64_t)z * n + i];
+    out[i] = s;
+  }
+}
+
+// Re-packs w[co][ci][ks][ks] into the per-phase grad-input weights W'[ci][co][a'][b'] described at the top.
+struct PackPhase {
+  int ky0, kx0, jy, jx, woff;
+};
+struct PackArgs {
+  const float* w;
+  float* out;
+  int CO, CI, KS, S, nphase;
+  PackPhase ph[kMaxPhases];
+};
+__global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs a) {
+  const int total = a.CO * a.CI * a.KS * a.KS;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    int f = 0;
+    while (f + 1 < a.nphase && e >= a.ph[f + 1].woff) ++f;
+    const PackPhase& p = a.ph[f];
+    const int jj = p.jy * p.jx, kph = a.CO * jj;
+    const int r = e - p.woff;
+    const int ci = r / kph, rem = r % kph, co = rem / jj, tap = rem % jj, ap = tap / p.jx, bp = tap % p.jx;
+    const int ky = p.ky0 + a.S * (p.jy - 1 - ap), kx = p.kx0 + a.S * (p.jx - 1 - bp);
+    a.out[e] = a.w[((co * a.CI + ci) * a.KS + ky) * a.KS + kx];
+  }
+}
+
+// gb[c] = sum over n and hw of gy[n][c][hw]: one workgroup per channel, fp32 lanes, tree reduction.
+__global__ void __launch_bounds__(256) bias_grad_kernel(const float* __restrict__ gy, float* __restrict__ gb, int n,
+                                                        int c, int hw) {
+  const int ch = blockIdx.x;
+  float s = 0.f;
+  for (int nn = 0; nn < n; ++nn) {
+    const float* row = gy + ((int64_t)nn * c + ch) * hw;
+    for (int e = threadIdx.x; e < hw; e += blockDim.x) s += row[e];
+  }
+  __shared__ float red[256];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) gb[ch] = red[0];
+}
+
+__global__ void __launch_bounds__(256) fold_bn_kernel(int co, int per_out, const float* __restrict__ cw,
+                                                      const float* __restrict__ cb, const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta, const float* __restrict__ mean,
+                                                      const float* __restrict__ var, float eps, float* __restrict__ fw,
+                                                      float* __restrict__ fb) {
+  const int64_t total = (int64_t)co * per_out;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int o = (int)(e / per_out);
+    const float scale = gamma[o] / sqrtf(var[o] + eps);
+    fw[e] = cw[e] * scale;
+    if (e % per_out == 0) fb[o] = ((cb ? cb[o] : 0.f) - mean[o]) * scale + beta[o];
+  }
+}
+
+// ---- tile selection ---------------------------------------------------------------------------------------------
+
+struct Tile {
+  int bp, bq, wp, wq;
+  float eff;  // relative MFMA efficiency of the wave tile (operand reuse)
+};
+
+// Picks the tile with the smallest estimated makespan: rounds of `slots` concurrent workgroups times the padded
+// tile work, over the tile's efficiency.
+template <size_t N>
+static int pick_tile(const Tile (&tiles)[N], int64_t P, int64_t Q, int64_t z, int64_t slots) {
+  int best = 0;
+  double best_cost = 1e300;
+  for (size_t i = 0; i < N; ++i) {
+    const Tile& tl = tiles[i];
+    int64_t blocks = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z;
+    int64_t rounds = cdiv(blocks, slots);
+    double cost = (double)rounds * tl.bp * tl.bq / tl.eff;
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = (int)i;
+    }
+  }
+  return best;
+}
+
+static const Tile kGatherTiles[] = {
+    {64, 256, 64, 64, 1.00f}, {128, 128, 64, 64, 1.00f}, {64, 128, 32, 64, 0.92f},
+    {32, 256, 32, 64, 0.90f}, {16, 256, 16, 64, 0.80f},  {64, 64, 32, 32, 0.80f},
+};
+static const Tile kWgradTiles[] = {
+    {64, 128, 32, 64, 1.00f}, {128, 64, 32, 64, 1.00f}, {64, 64, 32, 32, 0.85f}, {32, 128, 16, 64, 0.85f},
+};
+
+constexpr int64_t kCUs = 256;
+
+template <int BP, int BQ, int WP, int WQ>
+static void gather_launch(const GatherArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((conv_gather_kernel<BP, BQ, WP, WQ>), grid, dim3(256), 0, s, a);
+}
+template <int BP, int BQ, int WP, int WQ>
+static void wgrad_launch(const WgradArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((conv_wgrad_kernel<BP, BQ, WP, WQ>), grid, dim3(256), 0, s, a);
+}
+
+static int run_gather(const GatherArgs& a, int64_t maxq, hipStream_t s) {
+  const int ti = pick_tile(kGatherTiles, a.P, maxq, a.nphase, kCUs * 2);
+  const Tile& tl = kGatherTiles[ti];
+  dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)a.nphase);
+  switch (ti) {
+    case 0: gather_launch<64, 256, 64, 64>(a, grid, s); break;
+    case 1: gather_launch<128, 128, 64, 64>(a, grid, s); break;
+    case 2: gather_launch<64, 128, 32, 64>(a, grid, s); break;
+    case 3: gather_launch<32, 256, 32, 64>(a, grid, s); break;
+    case 4: gather_launch<16, 256, 16, 64>(a, grid, s); break;
+    default: gather_launch<64, 64, 32, 32>(a, grid, s); break;
+  }
+  return launch_check("conv_gather_kernel");
+}
+
+static bool dense_geo_ok(const omt_conv_geo* g) {
+  return g->n >= 1 && g->ci >= 1 && g->co >= 1 && g->ks >= 1 && g->ks <= 11 && g->stride >= 1 && g->stride <= 4 &&
+         g->pad >= 0 && g->pad <= g->ks && g->oh >= 1 && g->ow >= 1 &&
+         g->oh == (g->ih + 2 * g->pad - g->ks) / g->stride + 1 && g->ow == (g->iw + 2 * g->pad - g->ks) / g->stride + 1;
+}
+
+// int32 index math inside the kernels: every tensor and GEMM extent must stay below 2^31 elements per image-row
+// product used in 32-bit arithmetic.
+static bool fits_i32(const omt_conv_geo* g) {
+  const int64_t lim = (int64_t)1 << 31;
+  return g->n * g->oh * g->ow < lim && g->n * g->ih * g->iw < lim && g->ci * g->ih * g->iw < lim &&
+         g->co * g->oh * g->ow < lim && g->co * g->ci * g->ks * g->ks < lim;
+}
+
+// Wgrad split: about four waves of workgroups per CU over the tiles, each slice at least four K-blocks long.
+struct WgradPlan {
+  int tile;
+  int64_t slices, kslice;
+};
+static WgradPlan wgrad_plan(const omt_conv_geo* g) {
+  const int64_t P = g->co, Q = g->ci * g->ks * g->ks, K = g->n * g->oh * g->ow;
+  const int ti = pick_tile(kWgradTiles, P, Q, 1, kCUs * 2);
+  const Tile& tl = kWgradTiles[ti];
+  const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq);
+  int64_t slices = cdiv(kCUs * 4, tiles);
+  const int64_t max_slices = cdiv(K, 64 * 4);
+  if (slices > max_slices) slices = max_slices;
+  if (slices < 1) slices = 1;
+  int64_t kslice = cdiv(cdiv(K, slices), 64) * 64;
+  slices = cdiv(K, kslice);
+  return {ti, slices, kslice};
+}
+
+}  // namespace omt
+
+using namespace omt;
+
+OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
+                            unsigned epilogue, const float* bn_mean, const float* bn_var, const float* bn_gamma,
+                            const float* bn_beta, float bn_eps, float* y, void* stream) {
+  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd: null pointer");
+  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: geometry not covered (ks 1..11, stride 1..4, pad 0..ks)");
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: tensor too large for 32-bit indexing");
+  const bool bn = bn_mean || bn_var || bn_gamma || bn_beta;
+  if (bn && !(bn_mean && bn_var && bn_gamma && bn_beta))
+    return fail(OMT_INVALID, "omt_conv_fwd: BN loader needs mean, var, gamma and beta");
+  if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd: bias epilogue without bias");
+  GatherArgs a{};
+  a.x = x;
+  a.w = w;
+  a.bias = (epilogue & OMT_EPI_BIAS) ? bias : nullptr;
+  a.bn_mean = bn ? bn_mean : nullptr;
+  a.bn_var = bn_var;
+  a.bn_gamma = bn_gamma;
+  a.bn_beta = bn_beta;
+  a.bn_eps = bn_eps;
+  a.relu = (epilogue & OMT_EPI_RELU) ? 1 : 0;
+  a.y = y;
+  a.C = (int)g->ci;
+  a.H = (int)g->ih;
+  a.W = (int)g->iw;
+  a.P = (int)g->co;
+  a.YH = (int)g->oh;
+  a.YW = (int)g->ow;
+  a.nphase = 1;
+  Phase& p = a.ph[0];
+  p.KH = p.KW = (int)g->ks;
+  p.S = (int)g->stride;
+  p.PH = p.PW = (int)g->pad;
+  p.OH = (int)g->oh;
+  p.OW = (int)g->ow;
+  p.K = (int)(g->ci * g->ks * g->ks);
+  p.Q = (int)(g->n * g->oh * g->ow);
+  p.os = 1;
+  p.oy0 = p.ox0 = 0;
+  p.woff = 0;
+  p.div_ohw = make_fastdiv((uint32_t)(g->oh * g->ow));
+  p.div_ow = make_fastdiv((uint32_t)g->ow);
+  p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
+  p.div_kw = make_fastdiv((uint32_t)g->ks);
+  return run_gather(a, p.Q, stream_of(stream));
+}
+
+// Stride-phase table of the grad-input GEMMs (see the top of this file).
+static int dgrad_phases(const omt_conv_geo* g, GatherArgs& a, PackArgs& pk, int64_t& maxq) {
+  const int s = (int)g->stride, ks = (int)g->ks, pad = (int)g->pad;
+  int nph = 0, woff = 0;
+  maxq = 0;
+  for (int py = 0; py < s; ++py)
+    for (int px = 0; px < s; ++px) {
+      const int hi = (int)cdiv(g->ih - py, s), wi = (int)cdiv(g->iw - px, s);
+      const int ky0 = (py + pad) % s, kx0 = (px + pad) % s;
+      const int jy = ky0 < ks ? (int)cdiv(ks - ky0, s) : 0, jx = kx0 < ks ? (int)cdiv(ks - kx0, s) : 0;
+      const int qy = (py + pad - ky0) / s, qx = (px + pad - kx0) / s;
+      Phase& p = a.ph[nph];
+      p.KH = jy > 0 ? jy : 1;
+      p.KW = jx > 0 ? jx : 1;
+      p.S = 1;
+      p.PH = jy - 1 - qy;
+      p.PW = jx - 1 - qx;
+      p.OH = hi > 0 ? hi : 1;
+      p.OW = wi > 0 ? wi : 1;
+      p.K = (int)g->co * jy * jx;  // 0: no tap reaches this phase, it writes zeros
+      p.Q = (hi > 0 && wi > 0) ? (int)g->n * hi * wi : 0;
+      p.os = s;
+      p.oy0 = py;
+      p.ox0 = px;
+      p.woff = woff;
+      p.div_ohw = make_fastdiv((uint32_t)(p.OH * p.OW));
+      p.div_ow = make_fastdiv((uint32_t)p.OW);
+      p.div_kk = make_fastdiv((uint32_t)(p.KH * p.KW));
+      p.div_kw = make_fastdiv((uint32_t)p.KW);
+      pk.ph[nph] = PackPhase{ky0, kx0, jy, jx, woff};
+      woff += (int)(g->ci * g->co) * jy * jx;
+      if (p.Q > maxq) maxq = p.Q;
+      ++nph;
+    }
+  a.nphase = nph;
+  pk.nphase = nph;
+  return woff;
+}
+
+OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
+  if (!g) return 0;
+  return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+}
+
+OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad: null pointer");
+  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: geometry not covered");
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: tensor too large for 32-bit indexing");
+  if (!workspace || workspace_bytes < omt_conv_dgrad_workspace(g))
+    return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", omt_conv_dgrad_workspace(g));
+  hipStream_t s = stream_of(stream);
+  GatherArgs a{};
+  PackArgs pk{};
+  int64_t maxq = 0;
+  const int packed = dgrad_phases(g, a, pk, maxq);
+  pk.w = w;
+  pk.out = (float*)workspace;
+  pk.CO = (int)g->co;
+  pk.CI = (int)g->ci;
+  pk.KS = (int)g->ks;
+  pk.S = (int)g->stride;
+  hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
+  if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
+  a.x = gy;
+  a.w = (const float*)workspace;
+  a.y = gx;
+  a.C = (int)g->co;
+  a.H = (int)g->oh;
+  a.W = (int)g->ow;
+  a.P = (int)g->ci;
+  a.YH = (int)g->ih;
+  a.YW = (int)g->iw;
+  return run_gather(a, maxq, s);
+}
+
+OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g)) return 0;
+  WgradPlan pl = wgrad_plan(g);
+  if (pl.slices <= 1) return 0;
+  return (size_t)(pl.slices * g->co * g->ci * g->ks * g->ks) * sizeof(float);
+}
+
+OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
+  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: geometry not covered");
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: tensor too large for 32-bit indexing");
+  const size_t need = omt_conv_wgrad_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  WgradPlan pl = wgrad_plan(g);
+  WgradArgs a{};
+  a.x = x;
+  a.gy = gy;
+  a.out = pl.slices > 1 ? (float*)workspace : gw;
+  a.C = (int)g->ci;
+  a.H = (int)g->ih;
+  a.W = (int)g->iw;
+  a.P = (int)g->co;
+  a.OH = (int)g->oh;
+  a.OW = (int)g->ow;
+  a.KS = (int)g->ks;
+  a.S = (int)g->stride;
+  a.PAD = (int)g->pad;
+  a.Q = (int)(g->ci * g->ks * g->ks);
+  a.K = (int)(g->n * g->oh * g->ow);
+  a.kslice = (int)pl.kslice;
+  a.div_ohw = make_fastdiv((uint32_t)(g->oh * g->ow));
+  a.div_ow = make_fastdiv((uint32_t)g->ow);
+  a.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
+  a.div_ks = make_fastdiv((uint32_t)g->ks);
+  const Tile& tl = kWgradTiles[pl.tile];
+  dim3 grid((unsigned)cdiv(a.Q, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)pl.slices);
+  switch (pl.tile) {
+    case 0: wgrad_launch<64, 128, 32, 64>(a, grid, s); break;
+    case 1: wgrad_launch<128, 64, 32, 64>(a, grid, s); break;
+    case 2: wgrad_launch<64, 64, 32, 32>(a, grid, s); break;
+    default: wgrad_launch<32, 128, 16, 64>(a, grid, s); break;
+  }
+  if (int st = launch_check("conv_wgrad_kernel")) return st;
+  if (pl.slices > 1) {
+    const int64_t n = (int64_t)a.P * a.Q;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(grid1d(n, 256, 8192)), dim3(256), 0, s, (const float*)workspace, gw, n,
+                       (int)pl.slices);
+    if (int st = launch_check("split_reduce_kernel")) return st;
+  }
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream) {
+  if (!gy || !gb) return fail(OMT_INVALID, "omt_bias_grad: null pointer");
+  if (n < 0 || c < 0 || hw < 0 || n * c * hw >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_bias_grad: size");
+  if (c == 0) return OMT_OK;
+  hipLaunchKernelGGL(bias_grad_kernel, dim3((unsigned)c), dim3(256), 0, stream_of(stream), gy, gb, (int)n, (int)c,
+                     (int)hw);
+  return launch_check("bias_grad_kernel");
+}
+
+OMT_EXPORT int omt_fold_bn(int64_t co, int64_t per_out, const float* cw, const float* cb, const float* gamma,
+                           const float* beta, const float* mean, const float* var, float eps, float* fw, float* fb,
+                           void* stream) {
+  if (!cw || !gamma || !beta || !mean || !var || !fw || !fb) return fail(OMT_INVALID, "omt_fold_bn: null pointer");
+  if (co <= 0 || per_out <= 0) return OMT_OK;
+  hipLaunchKernelGGL(fold_bn_kernel, dim3(grid1d(co * per_out, 256, 4096)), dim3(256), 0, stream_of(stream), (int)co,
+                     (int)per_out, cw, cb, gamma, beta, mean, var, eps, fw, fb);
+  return launch_check("fold_bn_kernel");
+}

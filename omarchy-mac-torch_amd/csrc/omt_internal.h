@@ -1,0 +1,65 @@
+// Internal helpers shared by the libomt_hip.so translation units: status/error plumbing, launch checks, fast
+// integer division and the fp32 MFMA vector type.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "omt_hip.h"
+
+namespace omt {
+
+// Sets this thread's last-error message and returns `st`.
+int fail(int st, const char* fmt, ...);
+// Maps a HIP error to OMT_DEVICE_ERROR (with the runtime's message), or OMT_OK.
+int hip_check(hipError_t e, const char* what);
+// Checks the last launch on this thread.
+int launch_check(const char* kernel);
+// The stream a call runs on: the caller's hipStream_t (NULL = the HIP null stream).
+hipStream_t stream_of(void* s);
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline unsigned grid1d(int64_t total, int block, int64_t cap = 1 << 20) {
+  int64_t g = cdiv(total, block);
+  if (g > cap) g = cap;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+// Unsigned 32-bit division by a runtime-invariant divisor as a multiply-high and shifts (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, fig. 4.1): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, t = umulhi(m, n) gives n / d = (t + ((n - t) >> 1)) >> (l - 1) for d >= 2.
+struct FastDiv {
+  uint32_t d, mul, shift;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0, 0};
+  if (d <= 1) return f;
+  uint32_t l = 0;
+  while ((1ull << l) < d) l++;
+  // mul = floor(2^32 * (2^l - d) / d) + 1
+  f.mul = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+  f.shift = l;
+  return f;
+}
+__host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  if (f.d == 1) return n;
+  uint32_t hi = (uint32_t)(((uint64_t)n * f.mul) >> 32);
+  return (hi + ((n - hi) >> 1)) >> (f.shift - 1);
+}
+
+}  // namespace omt
+
+typedef float omt_f32x4 __attribute__((ext_vector_type(4)));
+
+#define OMT_EXPORT extern "C" __attribute__((visibility("default")))
+
+// Runs `expr` (a HIP call) and returns OMT_DEVICE_ERROR from the enclosing function if it fails.
+#define OMT_HIP(expr)                                              \
+  do {                                                             \
+    hipError_t e_ = (expr);                                        \
+    if (e_ != hipSuccess) return ::omt::hip_check(e_, #expr);      \
+  } while (0)

@@ -1,0 +1,263 @@
+// Pooling over NCHW float32 planes (planes = n * c): max (any window / stride / padding / dilation, int64 indices),
+// average (PyTorch divisor rules) and adaptive average. Backward passes gather rather than scatter: each input
+// element sums the gradients of the outputs that selected or covered it, visiting those outputs in row-major order,
+// which is the order PyTorch's CPU backward scatters them in, so no atomics are needed and the sums are
+// deterministic. One thread per output (forward) or input (backward) element; HBM-bandwidth-bound.
+// Reference kernels: maxpool_gen_fwd/bwd, avgpool_gen_fwd/bwd, adapool_fwd/bwd (csrc/nn.cpp:157-222).
+#include "omt_internal.h"
+
+namespace omt {
+
+struct PoolGeo {
+  int ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw;
+};
+
+__global__ void __launch_bounds__(256) maxpool_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                          int64_t* __restrict__ idx, int64_t total, PoolGeo g) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int ox = (int)(i % g.ow), oy = (int)((i / g.ow) % g.oh);
+    const int64_t plane = i / ((int64_t)g.ow * g.oh);
+    const float* xp = x + plane * g.ih * g.iw;
+    float best = -INFINITY;
+    int bi = -1;
+    for (int ky = 0; ky < g.kh; ++ky) {
+      const int yy = oy * g.sh - g.ph + ky * g.dh;
+      if (yy < 0 || yy >= g.ih) continue;
+      for (int kx = 0; kx < g.kw; ++kx) {
+        const int xx = ox * g.sw - g.pw + kx * g.dw;
+        if (xx < 0 || xx >= g.iw) continue;
+        const float v = xp[yy * g.iw + xx];
+        if (bi < 0 || v > best || isnan(v)) {  // first max wins ties; a NaN replaces the running max
+          best = v;
+          bi = yy * g.iw + xx;
+        }
+      }
+    }
+    y[i] = best;
+    idx[i] = bi;
+  }
+}
+
+// Output rows oy whose window row ky lands on input row r: oy * s - p + ky * d = r. Visits oy ascending.
+__global__ void __launch_bounds__(256) maxpool_bwd_kernel(const float* __restrict__ g, const int64_t* __restrict__ idx,
+                                                          float* __restrict__ gx, int64_t total, PoolGeo q) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int xx = (int)(i % q.iw), yy = (int)((i / q.iw) % q.ih);
+    const int64_t plane = i / ((int64_t)q.iw * q.ih);
+    const float* gp = g + plane * q.oh * q.ow;
+    const int64_t* ip = idx + plane * q.oh * q.ow;
+    const int64_t me = (int64_t)yy * q.iw + xx;
+    float acc = 0.f;
+    for (int ky = q.kh - 1; ky >= 0; --ky) {
+      const int ty = yy + q.ph - ky * q.dh;
+      if (ty < 0 || ty % q.sh) continue;
+      const int oy = ty / q.sh;
+      if (oy >= q.oh) continue;
+      for (int kx = q.kw - 1; kx >= 0; --kx) {
+        const int tx = xx + q.pw - kx * q.dw;
+        if (tx < 0 || tx % q.sw) continue;
+        const int ox = tx / q.sw;
+        if (ox >= q.ow) continue;
+        const int o = oy * q.ow + ox;
+        if (ip[o] == me) acc += gp[o];
+      }
+    }
+    gx[i] = acc;
+  }
+}
+
+__device__ __forceinline__ float avg_divisor(int oy, int ox, const PoolGeo& g, int include_pad, int divisor) {
+  if (divisor > 0) return (float)divisor;
+  int hs = oy * g.sh - g.ph, ws = ox * g.sw - g.pw;
+  int he = min(hs + g.kh, g.ih + g.ph), we = min(ws + g.kw, g.iw + g.pw);
+  const int pool = (he - hs) * (we - ws);
+  if (include_pad) return (float)pool;
+  hs = max(hs, 0);
+  ws = max(ws, 0);
+  he = min(he, g.ih);
+  we = min(we, g.iw);
+  return (float)((he - hs) * (we - ws));
+}
+
+__global__ void __launch_bounds__(256) avgpool_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                          int64_t total, PoolGeo g, int include_pad, int divisor) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int ox = (int)(i % g.ow), oy = (int)((i / g.ow) % g.oh);
+    const int64_t plane = i / ((int64_t)g.ow * g.oh);
+    const float* xp = x + plane * g.ih * g.iw;
+    const int hs = oy * g.sh - g.ph, ws = ox * g.sw - g.pw;
+    const int y0 = max(hs, 0), y1 = min(hs + g.kh, g.ih), x0 = max(ws, 0), x1 = min(ws + g.kw, g.iw);
+    float acc = 0.f;
+    for (int yy = y0; yy < y1; ++yy)
+      for (int xx = x0; xx < x1; ++xx) acc += xp[yy * g.iw + xx];
+    y[i] = acc / avg_divisor(oy, ox, g, include_pad, divisor);
+  }
+}
+
+__global__ void __launch_bounds__(256) avgpool_bwd_kernel(const float* __restrict__ gy, float* __restrict__ gx,
+                                                          int64_t total, PoolGeo q, int include_pad, int divisor) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int xx = (int)(i % q.iw), yy = (int)((i / q.iw) % q.ih);
+    const int64_t plane = i / ((int64_t)q.iw * q.ih);
+    const float* gp = gy + plane * q.oh * q.ow;
+    // windows [oy*s - p, oy*s - p + k) containing yy: oy in [ceil((yy + p - k + 1) / s), floor((yy + p) / s)]
+    const int oy0 = max(0, (yy + q.ph - q.kh + q.sh) / q.sh), oy1 = min(q.oh - 1, (yy + q.ph) / q.sh);
+    const int ox0 = max(0, (xx + q.pw - q.kw + q.sw) / q.sw), ox1 = min(q.ow - 1, (xx + q.pw) / q.sw);
+    float acc = 0.f;
+    for (int oy = oy0; oy <= oy1; ++oy) {
+      const int hs = oy * q.sh - q.ph;
+      if (yy < hs || yy >= hs + q.kh) continue;
+      for (int ox = ox0; ox <= ox1; ++ox) {
+        const int ws = ox * q.sw - q.pw;
+        if (xx < ws || xx >= ws + q.kw) continue;
+        acc += gp[oy * q.ow + ox] / avg_divisor(oy, ox, q, include_pad, divisor);
+      }
+    }
+    gx[i] = acc;
+  }
+}
+
+__device__ __forceinline__ int bin_lo(int o, int in, int out) { return (int)(((int64_t)o * in) / out); }
+__device__ __forceinline__ int bin_hi(int o, int in, int out) { return (int)(((int64_t)(o + 1) * in + out - 1) / out); }
+
+__global__ void __launch_bounds__(256) adapool_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                          int64_t total, int ih, int iw, int oh, int ow) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int ox = (int)(i % ow), oy = (int)((i / ow) % oh);
+    const int64_t plane = i / ((int64_t)ow * oh);
+    const float* xp = x + plane * ih * iw;
+    const int y0 = bin_lo(oy, ih, oh), y1 = bin_hi(oy, ih, oh), x0 = bin_lo(ox, iw, ow), x1 = bin_hi(ox, iw, ow);
+    float acc = 0.f;
+    for (int yy = y0; yy < y1; ++yy)
+      for (int xx = x0; xx < x1; ++xx) acc += xp[yy * iw + xx];
+    y[i] = acc / (float)((y1 - y0) * (x1 - x0));
+  }
+}
+
+// Global average pool (oh = ow = 1) as one wave per plane: coalesced reads and a wave reduction.
+__global__ void __launch_bounds__(256) gap_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                      int64_t planes, int hw) {
+  const int64_t plane = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (plane >= planes) return;
+  const int lane = threadIdx.x & 63;
+  const float* xp = x + plane * hw;
+  float acc = 0.f;
+  for (int e = lane; e < hw; e += 64) acc += xp[e];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) y[plane] = acc / (float)hw;
+}
+
+__global__ void __launch_bounds__(256) adapool_bwd_kernel(const float* __restrict__ gy, float* __restrict__ gx,
+                                                          int64_t total, int ih, int iw, int oh, int ow) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int xx = (int)(i % iw), yy = (int)((i / iw) % ih);
+    const int64_t plane = i / ((int64_t)iw * ih);
+    const float* gp = gy + plane * oh * ow;
+    float acc = 0.f;
+    for (int oy = 0; oy < oh; ++oy) {
+      const int y0 = bin_lo(oy, ih, oh), y1 = bin_hi(oy, ih, oh);
+      if (yy < y0 || yy >= y1) continue;
+      for (int ox = 0; ox < ow; ++ox) {
+        const int x0 = bin_lo(ox, iw, ow), x1 = bin_hi(ox, iw, ow);
+        if (xx < x0 || xx >= x1) continue;
+        acc += gp[oy * ow + ox] / (float)((y1 - y0) * (x1 - x0));
+      }
+    }
+    gx[i] = acc;
+  }
+}
+
+static bool pool_ok(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow) {
+  const int64_t lim = (int64_t)1 << 31;
+  return planes >= 0 && ih >= 1 && iw >= 1 && oh >= 1 && ow >= 1 && ih * iw < lim && oh * ow < lim &&
+         planes * ih * iw < ((int64_t)1 << 46);
+}
+
+static PoolGeo pgeo(int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw, int64_t sh, int64_t sw,
+                    int64_t ph, int64_t pw, int64_t dh, int64_t dw) {
+  return PoolGeo{(int)ih, (int)iw, (int)oh, (int)ow, (int)kh, (int)kw, (int)sh, (int)sw, (int)ph, (int)pw, (int)dh, (int)dw};
+}
+
+}  // namespace omt
+
+using namespace omt;
+
+OMT_EXPORT int omt_maxpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                               int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                               const float* x, float* y, int64_t* idx, void* stream) {
+  if (!x || !y || !idx) return fail(OMT_INVALID, "omt_maxpool_fwd: null pointer");
+  if (!pool_ok(planes, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || dh < 1 || dw < 1 || ph < 0 || pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_maxpool_fwd: geometry not covered");
+  const int64_t total = planes * oh * ow;
+  if (total == 0) return OMT_OK;
+  hipLaunchKernelGGL(maxpool_fwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), x, y, idx, total,
+                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+  return launch_check("maxpool_fwd_kernel");
+}
+
+OMT_EXPORT int omt_maxpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                               int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                               const float* g, const int64_t* idx, float* gx, void* stream) {
+  if (!g || !idx || !gx) return fail(OMT_INVALID, "omt_maxpool_bwd: null pointer");
+  if (!pool_ok(planes, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || dh < 1 || dw < 1 || ph < 0 || pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_maxpool_bwd: geometry not covered");
+  const int64_t total = planes * ih * iw;
+  if (total == 0) return OMT_OK;
+  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, idx, gx, total,
+                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+  return launch_check("maxpool_bwd_kernel");
+}
+
+OMT_EXPORT int omt_avgpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                               int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad,
+                               int64_t divisor_override, const float* x, float* y, void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_avgpool_fwd: null pointer");
+  if (!pool_ok(planes, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || ph < 0 || pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_avgpool_fwd: geometry not covered");
+  const int64_t total = planes * oh * ow;
+  if (total == 0) return OMT_OK;
+  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), x, y, total,
+                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), count_include_pad, (int)divisor_override);
+  return launch_check("avgpool_fwd_kernel");
+}
+
+OMT_EXPORT int omt_avgpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                               int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad,
+                               int64_t divisor_override, const float* g, float* gx, void* stream) {
+  if (!g || !gx) return fail(OMT_INVALID, "omt_avgpool_bwd: null pointer");
+  if (!pool_ok(planes, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || ph < 0 || pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_avgpool_bwd: geometry not covered");
+  const int64_t total = planes * ih * iw;
+  if (total == 0) return OMT_OK;
+  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, gx, total,
+                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), count_include_pad, (int)divisor_override);
+  return launch_check("avgpool_bwd_kernel");
+}
+
+OMT_EXPORT int omt_adapool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* x,
+                               float* y, void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_adapool_fwd: null pointer");
+  if (!pool_ok(planes, ih, iw, oh, ow)) return fail(OMT_UNSUPPORTED, "omt_adapool_fwd: geometry not covered");
+  if (planes == 0) return OMT_OK;
+  hipStream_t s = stream_of(stream);
+  if (oh == 1 && ow == 1) {
+    hipLaunchKernelGGL(gap_fwd_kernel, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, s, x, y, planes, (int)(ih * iw));
+    return launch_check("gap_fwd_kernel");
+  }
+  const int64_t total = planes * oh * ow;
+  hipLaunchKernelGGL(adapool_fwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, s, x, y, total, (int)ih, (int)iw,
+                     (int)oh, (int)ow);
+  return launch_check("adapool_fwd_kernel");
+}
+
+OMT_EXPORT int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* g,
+                               float* gx, void* stream) {
+  if (!g || !gx) return fail(OMT_INVALID, "omt_adapool_bwd: null pointer");
+  if (!pool_ok(planes, ih, iw, oh, ow)) return fail(OMT_UNSUPPORTED, "omt_adapool_bwd: geometry not covered");
+  const int64_t total = planes * ih * iw;
+  if (total == 0) return OMT_OK;
+  hipLaunchKernelGGL(adapool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, gx, total,
+                     (int)ih, (int)iw, (int)oh, (int)ow);
+  return launch_check("adapool_bwd_kernel");
+}

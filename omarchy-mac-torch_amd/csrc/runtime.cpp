@@ -1,0 +1,247 @@
+// Device services of libomt_hip.so: per-thread error messages, the library stream, a caching device allocator,
+// copies and events.
+//
+// The allocator replaces the reference's wgpu buffer pool (alloc_buf / free_buf, csrc/runtime.cpp:177-249). Blocks
+// are rounded to size classes (512 B granules up to 1 MiB, then 2 MiB granules) and parked in per-size free lists
+// when freed. Because every op of the operator layer runs on one stream, a parked block can be handed out again at
+// once: any later use is ordered after the earlier user's kernels on that stream. Callers that use several streams
+// must synchronize before freeing memory another stream still reads.
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "omt_internal.h"
+
+namespace omt {
+
+static thread_local std::string t_last_error;
+
+int fail(int st, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  t_last_error = buf;
+  return st;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return OMT_OK;
+  if (e == hipErrorOutOfMemory) return fail(OMT_OOM, "%s: %s", what, hipGetErrorString(e));
+  return fail(OMT_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+int launch_check(const char* kernel) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(OMT_DEVICE_ERROR, "launch of %s failed: %s", kernel, hipGetErrorString(e));
+  return OMT_OK;
+}
+
+static std::mutex g_stream_mu;
+static hipStream_t g_stream = nullptr;
+
+hipStream_t stream_of(void* s) { return (hipStream_t)s; }
+
+// ---- caching allocator -----------------------------------------------------------------------------------------
+
+namespace {
+struct Pool {
+  std::mutex mu;
+  std::map<size_t, std::vector<void*>> free_lists;  // size class -> parked blocks
+  std::unordered_map<void*, size_t> live;            // block -> size class
+  size_t allocated = 0;                              // bytes handed out
+  size_t reserved = 0;                               // bytes held from HIP (live + parked)
+  size_t limit = 0;                                  // 0 = no cap
+
+  static size_t size_class(size_t bytes) {
+    if (bytes == 0) bytes = 1;
+    const size_t small = 512, big = 2u << 20;
+    if (bytes <= (1u << 20)) return (bytes + small - 1) / small * small;
+    return (bytes + big - 1) / big * big;
+  }
+
+  void release_parked() {  // caller holds mu
+    for (auto& kv : free_lists)
+      for (void* p : kv.second) {
+        (void)hipFree(p);
+        reserved -= kv.first;
+      }
+    free_lists.clear();
+  }
+};
+Pool& pool() {
+  static Pool* p = new Pool();  // never destroyed: blocks may be freed from static destructors of other libraries
+  return *p;
+}
+}  // namespace
+
+}  // namespace omt
+
+using namespace omt;
+
+OMT_EXPORT const char* omt_last_error(void) { return t_last_error.c_str(); }
+OMT_EXPORT int omt_abi_version(void) { return 1; }
+OMT_EXPORT int omt_hip_runtime_version(void) {
+  int v = 0;
+  (void)hipRuntimeGetVersion(&v);
+  return v;
+}
+
+OMT_EXPORT int omt_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(OMT_INVALID, "omt_malloc: null out-pointer");
+  Pool& P = pool();
+  size_t cls = Pool::size_class(bytes);
+  std::lock_guard<std::mutex> lk(P.mu);
+  auto it = P.free_lists.find(cls);
+  if (it != P.free_lists.end() && !it->second.empty()) {
+    *ptr = it->second.back();
+    it->second.pop_back();
+    P.live[*ptr] = cls;
+    P.allocated += cls;
+    return OMT_OK;
+  }
+  void* p = nullptr;
+  bool over = P.limit && P.reserved + cls > P.limit;
+  hipError_t e = over ? hipErrorOutOfMemory : hipMalloc(&p, cls);
+  if (e != hipSuccess) {  // empty the cache once and retry (csrc/runtime.cpp:220-225)
+    (void)hipGetLastError();
+    P.release_parked();
+    over = P.limit && P.reserved + cls > P.limit;
+    e = over ? hipErrorOutOfMemory : hipMalloc(&p, cls);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      *ptr = nullptr;
+      return fail(OMT_OOM, "out of device memory allocating %zu bytes (%zu reserved, limit %zu)", cls, P.reserved,
+                  P.limit);
+    }
+  }
+  P.reserved += cls;
+  P.allocated += cls;
+  P.live[p] = cls;
+  *ptr = p;
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_free(void* ptr) {
+  if (!ptr) return OMT_OK;
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  auto it = P.live.find(ptr);
+  if (it == P.live.end()) return fail(OMT_INVALID, "omt_free: %p was not allocated by omt_malloc", ptr);
+  size_t cls = it->second;
+  P.live.erase(it);
+  P.allocated -= cls;
+  P.free_lists[cls].push_back(ptr);
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_empty_cache(void) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  OMT_HIP(hipDeviceSynchronize());  // parked blocks may still be read by queued kernels
+  P.release_parked();
+  return OMT_OK;
+}
+
+OMT_EXPORT size_t omt_memory_allocated(void) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  return P.allocated;
+}
+
+OMT_EXPORT size_t omt_memory_reserved(void) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  return P.reserved;
+}
+
+OMT_EXPORT void omt_set_memory_limit(size_t bytes) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.limit = bytes;
+}
+
+OMT_EXPORT void* omt_default_stream(void) {
+  std::lock_guard<std::mutex> lk(g_stream_mu);
+  if (!g_stream && hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) g_stream = nullptr;
+  return (void*)g_stream;
+}
+
+OMT_EXPORT int omt_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+  if (bytes == 0) return OMT_OK;
+  if (!dst || !src) return fail(OMT_INVALID, "omt_memcpy: null pointer");
+  hipStream_t s = stream_of(stream);
+  hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+  OMT_HIP(hipMemcpyAsync(dst, src, bytes, k, s));
+  if (kind == 1) OMT_HIP(hipStreamSynchronize(s));
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_memset_zero(void* dst, size_t bytes, void* stream) {
+  if (bytes == 0) return OMT_OK;
+  OMT_HIP(hipMemsetAsync(dst, 0, bytes, stream_of(stream)));
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_stream_sync(void* stream) {
+  OMT_HIP(hipStreamSynchronize(stream_of(stream)));
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_event_create(void** ev) {
+  OMT_HIP(hipEventCreate((hipEvent_t*)ev));
+  return OMT_OK;
+}
+OMT_EXPORT int omt_event_destroy(void* ev) {
+  OMT_HIP(hipEventDestroy((hipEvent_t)ev));
+  return OMT_OK;
+}
+OMT_EXPORT int omt_event_record(void* ev, void* stream) {
+  OMT_HIP(hipEventRecord((hipEvent_t)ev, stream_of(stream)));
+  return OMT_OK;
+}
+OMT_EXPORT int omt_event_query(void* ev) {
+  hipError_t e = hipEventQuery((hipEvent_t)ev);
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  hip_check(e, "hipEventQuery");
+  return -1;
+}
+OMT_EXPORT int omt_event_sync(void* ev) {
+  OMT_HIP(hipEventSynchronize((hipEvent_t)ev));
+  return OMT_OK;
+}
+OMT_EXPORT int omt_event_elapsed_ms(void* start, void* end, float* ms) {
+  OMT_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+  return OMT_OK;
+}
+
+OMT_EXPORT void omt_conv_geo_init(omt_conv_geo* g, int64_t n, int64_t ci, int64_t co, int64_t ih, int64_t iw,
+                                  int64_t ks, int64_t stride, int64_t pad) {
+  g->n = n;
+  g->ci = ci;
+  g->co = co;
+  g->ih = ih;
+  g->iw = iw;
+  g->oh = (ih + 2 * pad - ks) / stride + 1;
+  g->ow = (iw + 2 * pad - ks) / stride + 1;
+  g->ks = ks;
+  g->stride = stride;
+  g->pad = pad;
+}
+
+OMT_EXPORT int omt_conv_kind(int64_t x_c, int64_t w_o, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
+                             int64_t pw, int64_t dh, int64_t dw, int transposed, int64_t groups) {
+  if (transposed || dh != 1 || dw != 1 || kh != kw || sh != sw || ph != pw) return OMT_CONV_NONE;
+  int64_t ks = kh, s = sh, p = ph;
+  bool geo_ok = ks >= 1 && ks <= 11 && s >= 1 && s <= 4 && p >= 0 && p <= ks;
+  if (groups == 1 && geo_ok) return OMT_CONV_DENSE;
+  bool depthwise = groups > 1 && groups == x_c && groups == w_o;
+  if (depthwise && (ks == 3 || ks == 5 || ks == 7) && s == 1 && p == ks / 2) return OMT_CONV_DW;
+  if (depthwise && geo_ok) return OMT_CONV_DWG;
+  return OMT_CONV_NONE;
+}

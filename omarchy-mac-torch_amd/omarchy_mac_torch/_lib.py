@@ -1,0 +1,125 @@
+"""ctypes binding of libomt_hip.so (include/omt_hip.h).
+
+The library is required: importing this module raises ImportError when it is missing, so no operator silently runs
+anywhere but the HIP kernels.
+"""
+
+import ctypes
+import pathlib
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libomt_hip.so"
+
+OMT_OK, OMT_UNSUPPORTED, OMT_OOM, OMT_DEVICE_ERROR, OMT_INVALID = range(5)
+OMT_CONV_NONE, OMT_CONV_DENSE, OMT_CONV_DW, OMT_CONV_DWG = range(4)
+OMT_EPI_BIAS, OMT_EPI_RELU = 1, 2
+
+
+class ConvGeo(ctypes.Structure):
+    """omt_conv_geo (reference Geo, csrc/omt.h:224-229)."""
+    _fields_ = [(k, ctypes.c_int64) for k in ("n", "ci", "co", "ih", "iw", "oh", "ow", "ks", "stride", "pad")]
+
+    def astuple(self):
+        return tuple(getattr(self, k) for k, _ in self._fields_)
+
+
+class OmtError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(msg)
+        self.status = status
+
+
+class Unsupported(OmtError):
+    """OMT_UNSUPPORTED: the geometry is outside what the kernels cover (reference: NEED -> Unsupported)."""
+
+
+I64, U32, I32, F32, F64, SZ, VP = (ctypes.c_int64, ctypes.c_uint, ctypes.c_int, ctypes.c_float, ctypes.c_double,
+                                   ctypes.c_size_t, ctypes.c_void_p)
+G = ctypes.POINTER(ConvGeo)
+
+# name -> (restype, argtypes); the full exported surface of include/omt_hip.h
+SIGNATURES = {
+    "omt_last_error": (ctypes.c_char_p, []),
+    "omt_abi_version": (I32, []),
+    "omt_hip_runtime_version": (I32, []),
+    "omt_conv_geo_init": (None, [G, I64, I64, I64, I64, I64, I64, I64, I64]),
+    "omt_conv_kind": (I32, [I64] * 10 + [I32, I64]),
+    "omt_malloc": (I32, [ctypes.POINTER(VP), SZ]),
+    "omt_free": (I32, [VP]),
+    "omt_empty_cache": (I32, []),
+    "omt_memory_allocated": (SZ, []),
+    "omt_memory_reserved": (SZ, []),
+    "omt_set_memory_limit": (None, [SZ]),
+    "omt_default_stream": (VP, []),
+    "omt_memcpy": (I32, [VP, VP, SZ, I32, VP]),
+    "omt_memset_zero": (I32, [VP, SZ, VP]),
+    "omt_stream_sync": (I32, [VP]),
+    "omt_event_create": (I32, [ctypes.POINTER(VP)]),
+    "omt_event_destroy": (I32, [VP]),
+    "omt_event_record": (I32, [VP, VP]),
+    "omt_event_query": (I32, [VP]),
+    "omt_event_sync": (I32, [VP]),
+    "omt_event_elapsed_ms": (I32, [VP, VP, ctypes.POINTER(F32)]),
+    "omt_conv_fwd": (I32, [G, VP, VP, VP, U32, VP, VP, VP, VP, F32, VP, VP]),
+    "omt_conv_dgrad_workspace": (SZ, [G]),
+    "omt_conv_dgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_conv_wgrad_workspace": (SZ, [G]),
+    "omt_conv_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_bias_grad": (I32, [I64, I64, I64, VP, VP, VP]),
+    "omt_fold_bn": (I32, [I64, I64, VP, VP, VP, VP, VP, VP, F32, VP, VP, VP]),
+    "omt_dw_fwd": (I32, [G, VP, VP, VP, VP, VP, VP, VP, F32, VP, VP]),
+    "omt_dw_dgrad": (I32, [G, VP, VP, VP, VP]),
+    "omt_dw_wgrad_workspace": (SZ, [G]),
+    "omt_dw_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_train_workspace": (SZ, [I64, I64, I64]),
+    "omt_bn_train_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
+    "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
+    "omt_bn_bwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_maxpool_fwd": (I32, [I64] * 13 + [VP, VP, VP, VP]),
+    "omt_maxpool_bwd": (I32, [I64] * 13 + [VP, VP, VP, VP]),
+    "omt_avgpool_fwd": (I32, [I64] * 11 + [I32, I64, VP, VP, VP]),
+    "omt_avgpool_bwd": (I32, [I64] * 11 + [I32, I64, VP, VP, VP]),
+    "omt_adapool_fwd": (I32, [I64] * 5 + [VP, VP, VP]),
+    "omt_adapool_bwd": (I32, [I64] * 5 + [VP, VP, VP]),
+}
+
+ABI_VERSION = 1
+
+
+def _load():
+    if not LIB_PATH.exists():
+        raise ImportError(f"omarchy_mac_torch: {LIB_PATH} is not built; run `python omarchy-mac-torch_amd/build_native.py`"
+                          " (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.omt_abi_version() != ABI_VERSION:
+        raise ImportError(f"libomt_hip.so ABI {lib.omt_abi_version()} != {ABI_VERSION}; rebuild it")
+    return lib
+
+
+L = _load()
+
+
+def check(status, what=""):
+    """Raises on a non-OK status, with the library's message."""
+    if status == OMT_OK:
+        return
+    msg = (L.omt_last_error() or b"").decode(errors="replace")
+    if what:
+        msg = f"{what}: {msg}"
+    if status == OMT_UNSUPPORTED:
+        raise Unsupported(status, msg)
+    if status == OMT_OOM:
+        import torch
+        raise torch.OutOfMemoryError(msg)
+    raise OmtError(status, msg)
+
+
+def conv_geo(n, ci, co, ih, iw, ks, stride, pad):
+    g = ConvGeo()
+    L.omt_conv_geo_init(ctypes.byref(g), n, ci, co, ih, iw, ks, stride, pad)
+    return g

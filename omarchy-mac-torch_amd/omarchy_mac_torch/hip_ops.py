@@ -1,0 +1,279 @@
+"""Tensor-level entry points over libomt_hip.so for float32 NCHW tensors on the HIP device.
+
+Each function validates shapes on the host, allocates outputs (and any workspace the C ABI asks for) with torch's
+device allocator, and launches on torch's current stream. They are the operator implementations behind the
+reference's convolution_ / convolution_backward_ (csrc/conv.cpp:179-237), batch_norm_ / batch_norm_backward_
+(csrc/nn.cpp:25-78), the pooling ops (csrc/nn.cpp:157-222) and the fused ops of csrc/fused.cpp.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import L, check
+
+_vp = ctypes.c_void_p
+
+
+def _ptr(t):
+    return None if t is None else _vp(t.data_ptr())
+
+
+def _stream(device=None):
+    return _vp(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need(t, name, dim=None):
+    if t is None:
+        return None
+    if not t.is_cuda or t.dtype != torch.float32:
+        raise TypeError(f"{name}: expected a float32 tensor on the HIP device, got {t.dtype} on {t.device}")
+    if dim is not None and t.dim() != dim:
+        raise ValueError(f"{name}: expected {dim}-D, got {tuple(t.shape)}")
+    return t.contiguous()
+
+
+def _workspace(nbytes, device):
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device), int(nbytes)
+
+
+def _pair(v):
+    return (v, v) if isinstance(v, int) else tuple(v)
+
+
+# ---- dense convolution ------------------------------------------------------------------------------------------
+
+def conv_geo_for(x_shape, w_shape, stride, pad):
+    n, ci, ih, iw = x_shape
+    co, wci, kh, kw = w_shape
+    if wci != ci or kh != kw:
+        raise ValueError(f"conv: weight {tuple(w_shape)} does not match input {tuple(x_shape)}")
+    return _lib.conv_geo(n, ci, co, ih, iw, kh, stride, pad)
+
+
+def conv2d(x, w, bias=None, stride=1, padding=0, relu=False, bn=None, bn_eps=1e-5):
+    """y = conv(x, w) + bias, optional ReLU. bn = (mean, var, gamma, beta) maps the input through eval BatchNorm +
+    ReLU on in-bounds taps first (reference kind-3 loader, omarchy_mac_torch/gemm.py:139-141)."""
+    x, w, bias = _need(x, "x", 4), _need(w, "w", 4), _need(bias, "bias", 1)
+    g = conv_geo_for(x.shape, w.shape, stride, padding)
+    y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32)
+    bnp = [None] * 4 if bn is None else [_need(t, "bn", 1) for t in bn]
+    epi = (_lib.OMT_EPI_BIAS if bias is not None else 0) | (_lib.OMT_EPI_RELU if relu else 0)
+    check(L.omt_conv_fwd(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(bias), epi, *[_ptr(t) for t in bnp], bn_eps,
+                         _ptr(y), _stream(x.device)), "conv2d")
+    return y
+
+
+def conv2d_dgrad(gy, w, x_shape, stride=1, padding=0):
+    gy, w = _need(gy, "gy", 4), _need(w, "w", 4)
+    g = conv_geo_for(x_shape, w.shape, stride, padding)
+    if tuple(gy.shape) != (g.n, g.co, g.oh, g.ow):
+        raise ValueError(f"conv dgrad: gy {tuple(gy.shape)} != {(g.n, g.co, g.oh, g.ow)}")
+    gx = torch.empty(tuple(x_shape), device=gy.device, dtype=torch.float32)
+    ws, nb = _workspace(L.omt_conv_dgrad_workspace(ctypes.byref(g)), gy.device)
+    check(L.omt_conv_dgrad(ctypes.byref(g), _ptr(gy), _ptr(w), _ptr(gx), _ptr(ws), nb, _stream(gy.device)),
+          "conv2d_dgrad")
+    return gx
+
+
+def conv2d_wgrad(x, gy, ks, stride=1, padding=0):
+    x, gy = _need(x, "x", 4), _need(gy, "gy", 4)
+    n, ci, ih, iw = x.shape
+    co = gy.shape[1]
+    g = _lib.conv_geo(n, ci, co, ih, iw, ks, stride, padding)
+    if tuple(gy.shape) != (g.n, g.co, g.oh, g.ow):
+        raise ValueError(f"conv wgrad: gy {tuple(gy.shape)} != {(g.n, g.co, g.oh, g.ow)}")
+    gw = torch.empty((co, ci, ks, ks), device=x.device, dtype=torch.float32)
+    ws, nb = _workspace(L.omt_conv_wgrad_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_conv_wgrad(ctypes.byref(g), _ptr(x), _ptr(gy), _ptr(gw), _ptr(ws), nb, _stream(x.device)),
+          "conv2d_wgrad")
+    return gw
+
+
+def bias_grad(gy):
+    gy = _need(gy, "gy", 4)
+    n, c, h, w = gy.shape
+    gb = torch.empty((c,), device=gy.device, dtype=torch.float32)
+    check(L.omt_bias_grad(n, c, h * w, _ptr(gy), _ptr(gb), _stream(gy.device)), "bias_grad")
+    return gb
+
+
+def fold_bn(cw, cb, gamma, beta, mean, var, eps=1e-5):
+    """Eval BatchNorm folded into the preceding conv (fold_bn, csrc/fused.cpp:34-40)."""
+    cw, cb = _need(cw, "cw"), _need(cb, "cb", 1)
+    gamma, beta, mean, var = (_need(t, "bn", 1) for t in (gamma, beta, mean, var))
+    co = cw.shape[0]
+    fw, fb = torch.empty_like(cw), torch.empty((co,), device=cw.device, dtype=torch.float32)
+    check(L.omt_fold_bn(co, cw.numel() // co, _ptr(cw), _ptr(cb), _ptr(gamma), _ptr(beta), _ptr(mean), _ptr(var),
+                        eps, _ptr(fw), _ptr(fb), _stream(cw.device)), "fold_bn")
+    return fw, fb
+
+
+# ---- depthwise --------------------------------------------------------------------------------------------------
+
+def _dw_geo(x_shape, w_shape, stride, pad):
+    n, c, ih, iw = x_shape
+    if tuple(w_shape[:2]) != (c, 1) or w_shape[2] != w_shape[3]:
+        raise ValueError(f"depthwise: weight {tuple(w_shape)} for input {tuple(x_shape)}")
+    return _lib.conv_geo(n, c, c, ih, iw, w_shape[2], stride, pad)
+
+
+def depthwise_conv2d(x, w, bias=None, stride=1, padding=None, bn=None, bn_eps=1e-5):
+    x, w, bias = _need(x, "x", 4), _need(w, "w", 4), _need(bias, "bias", 1)
+    padding = w.shape[2] // 2 if padding is None else padding
+    g = _dw_geo(x.shape, w.shape, stride, padding)
+    y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32)
+    bnp = [None] * 4 if bn is None else [_need(t, "bn", 1) for t in bn]
+    check(L.omt_dw_fwd(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(bias), *[_ptr(t) for t in bnp], bn_eps, _ptr(y),
+                       _stream(x.device)), "depthwise_conv2d")
+    return y
+
+
+def depthwise_dgrad(gy, w, x_shape, stride=1, padding=None):
+    gy, w = _need(gy, "gy", 4), _need(w, "w", 4)
+    padding = w.shape[2] // 2 if padding is None else padding
+    g = _dw_geo(x_shape, w.shape, stride, padding)
+    gx = torch.empty(tuple(x_shape), device=gy.device, dtype=torch.float32)
+    check(L.omt_dw_dgrad(ctypes.byref(g), _ptr(gy), _ptr(w), _ptr(gx), _stream(gy.device)), "depthwise_dgrad")
+    return gx
+
+
+def depthwise_wgrad(x, gy, ks, stride=1, padding=None):
+    x, gy = _need(x, "x", 4), _need(gy, "gy", 4)
+    padding = ks // 2 if padding is None else padding
+    n, c, ih, iw = x.shape
+    g = _lib.conv_geo(n, c, c, ih, iw, ks, stride, padding)
+    gw = torch.empty((c, 1, ks, ks), device=x.device, dtype=torch.float32)
+    ws, nb = _workspace(L.omt_dw_wgrad_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_dw_wgrad(ctypes.byref(g), _ptr(x), _ptr(gy), _ptr(gw), _ptr(ws), nb, _stream(x.device)),
+          "depthwise_wgrad")
+    return gw
+
+
+# ---- batch norm -------------------------------------------------------------------------------------------------
+
+def batch_norm_train(x, gamma, beta, running_mean=None, running_var=None, momentum=0.1, eps=1e-5, relu=False,
+                     functional=False):
+    """Training BatchNorm. Returns (y, save_mean, save_invstd) and, when functional, also the updated running stats
+    as new tensors (bn_stats_fin_functional); otherwise running_mean / running_var are updated in place."""
+    x = _need(x, "x", 4)
+    gamma, beta = _need(gamma, "gamma", 1), _need(beta, "beta", 1)
+    n, c, h, w = x.shape
+    y = torch.empty_like(x)
+    sm = torch.empty((c,), device=x.device, dtype=torch.float32)
+    si = torch.empty_like(sm)
+    if functional:
+        nrm = torch.empty_like(sm) if running_mean is not None else None
+        nrv = torch.empty_like(sm) if running_var is not None else None
+    else:
+        nrm, nrv = running_mean, running_var
+    ws, nb = _workspace(L.omt_bn_train_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_train_fwd(n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean), _ptr(running_var),
+                             momentum, eps, int(relu), _ptr(y), _ptr(sm), _ptr(si), _ptr(nrm), _ptr(nrv), _ptr(ws), nb,
+                             _stream(x.device)), "batch_norm_train")
+    if functional:
+        return y, sm, si, nrm, nrv
+    return y, sm, si
+
+
+def batch_norm_eval(x, gamma, beta, running_mean, running_var, eps=1e-5, relu=False):
+    x = _need(x, "x", 4)
+    n, c, h, w = x.shape
+    y = torch.empty_like(x)
+    check(L.omt_bn_eval_fwd(n, c, h * w, _ptr(x), _ptr(_need(gamma, "gamma", 1)), _ptr(_need(beta, "beta", 1)),
+                            _ptr(_need(running_mean, "rm", 1)), _ptr(_need(running_var, "rv", 1)), eps, int(relu),
+                            _ptr(y), _stream(x.device)), "batch_norm_eval")
+    return y
+
+
+def batch_norm_backward(g, x, save_mean, save_invstd, gamma, relu_y=None, output_mask=(True, True, True)):
+    g, x = _need(g, "g", 4), _need(x, "x", 4)
+    relu_y = _need(relu_y, "relu_y", 4)
+    n, c, h, w = x.shape
+    gx = torch.empty_like(x) if output_mask[0] else None
+    dg = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[1] else None
+    db = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[2] else None
+    ws, nb = _workspace(L.omt_bn_bwd_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_bwd(n, c, h * w, _ptr(g), _ptr(x), _ptr(relu_y), _ptr(_need(save_mean, "mean", 1)),
+                       _ptr(_need(save_invstd, "invstd", 1)), _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg),
+                       _ptr(db), _ptr(ws), nb, _stream(x.device)), "batch_norm_backward")
+    return gx, dg, db
+
+
+# ---- pooling ----------------------------------------------------------------------------------------------------
+
+def pool_out(size, k, s, p, d=1, ceil=False):
+    """Output extent of a pooling window (PyTorch's pooling_output_shape)."""
+    num = size + 2 * p - d * (k - 1) - 1 + ((s - 1) if ceil else 0)
+    out = num // s + 1
+    if ceil and (out - 1) * s >= size + p:
+        out -= 1
+    return out
+
+
+def max_pool2d(x, kernel, stride=None, padding=0, dilation=1, ceil_mode=False):
+    x = _need(x, "x", 4)
+    k, s = _pair(kernel), _pair(stride if stride else kernel)
+    p, d = _pair(padding), _pair(dilation)
+    n, c, ih, iw = x.shape
+    oh, ow = pool_out(ih, k[0], s[0], p[0], d[0], ceil_mode), pool_out(iw, k[1], s[1], p[1], d[1], ceil_mode)
+    y = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32)
+    idx = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.int64)
+    check(L.omt_maxpool_fwd(n * c, ih, iw, oh, ow, k[0], k[1], s[0], s[1], p[0], p[1], d[0], d[1], _ptr(x), _ptr(y),
+                            _ptr(idx), _stream(x.device)), "max_pool2d")
+    return y, idx
+
+
+def max_pool2d_backward(g, x_shape, idx, kernel, stride=None, padding=0, dilation=1):
+    g = _need(g, "g", 4)
+    idx = idx.contiguous()
+    k, s = _pair(kernel), _pair(stride if stride else kernel)
+    p, d = _pair(padding), _pair(dilation)
+    n, c, ih, iw = x_shape
+    gx = torch.empty(tuple(x_shape), device=g.device, dtype=torch.float32)
+    check(L.omt_maxpool_bwd(n * c, ih, iw, g.shape[2], g.shape[3], k[0], k[1], s[0], s[1], p[0], p[1], d[0], d[1],
+                            _ptr(g), _ptr(idx), _ptr(gx), _stream(g.device)), "max_pool2d_backward")
+    return gx
+
+
+def avg_pool2d(x, kernel, stride=None, padding=0, ceil_mode=False, count_include_pad=True, divisor_override=None):
+    x = _need(x, "x", 4)
+    k, s, p = _pair(kernel), _pair(stride if stride else kernel), _pair(padding)
+    n, c, ih, iw = x.shape
+    oh, ow = pool_out(ih, k[0], s[0], p[0], 1, ceil_mode), pool_out(iw, k[1], s[1], p[1], 1, ceil_mode)
+    y = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32)
+    check(L.omt_avgpool_fwd(n * c, ih, iw, oh, ow, k[0], k[1], s[0], s[1], p[0], p[1], int(count_include_pad),
+                            divisor_override or 0, _ptr(x), _ptr(y), _stream(x.device)), "avg_pool2d")
+    return y
+
+
+def avg_pool2d_backward(g, x_shape, kernel, stride=None, padding=0, count_include_pad=True, divisor_override=None):
+    g = _need(g, "g", 4)
+    k, s, p = _pair(kernel), _pair(stride if stride else kernel), _pair(padding)
+    n, c, ih, iw = x_shape
+    gx = torch.empty(tuple(x_shape), device=g.device, dtype=torch.float32)
+    check(L.omt_avgpool_bwd(n * c, ih, iw, g.shape[2], g.shape[3], k[0], k[1], s[0], s[1], p[0], p[1],
+                            int(count_include_pad), divisor_override or 0, _ptr(g), _ptr(gx), _stream(g.device)),
+          "avg_pool2d_backward")
+    return gx
+
+
+def adaptive_avg_pool2d(x, output_size):
+    x = _need(x, "x", 4)
+    oh, ow = _pair(output_size)
+    n, c, ih, iw = x.shape
+    y = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32)
+    check(L.omt_adapool_fwd(n * c, ih, iw, oh, ow, _ptr(x), _ptr(y), _stream(x.device)), "adaptive_avg_pool2d")
+    return y
+
+
+def adaptive_avg_pool2d_backward(g, x_shape):
+    g = _need(g, "g", 4)
+    n, c, ih, iw = x_shape
+    gx = torch.empty(tuple(x_shape), device=g.device, dtype=torch.float32)
+    check(L.omt_adapool_bwd(n * c, ih, iw, g.shape[2], g.shape[3], _ptr(g), _ptr(gx), _stream(g.device)),
+          "adaptive_avg_pool2d_backward")
+    return gx

@@ -1,0 +1,116 @@
+"""CPU checks of the C ABI (no GPU needed): libomt_hip.so loads and exports every function include/omt_hip.h
+declares, the ctypes table matches the header, host-side argument validation returns the documented statuses before
+any device work, and the fast integer division the kernels use is exact."""
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "omt_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(omt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from omarchy_mac_torch import _lib
+    names = declared_functions()
+    assert len(names) >= 40
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_geometry_and_kind_table():
+    from omarchy_mac_torch import _lib
+    g = _lib.conv_geo(16, 3, 64, 224, 224, 11, 4, 2)
+    assert (g.oh, g.ow) == (55, 55)
+    k = _lib.L.omt_conv_kind
+    # (x_c, w_o, kh, kw, sh, sw, ph, pw, dh, dw, transposed, groups) -> kind (csrc/conv.cpp:167-177)
+    assert k(3, 64, 11, 11, 4, 4, 2, 2, 1, 1, 0, 1) == _lib.OMT_CONV_DENSE
+    assert k(3, 64, 11, 11, 5, 5, 2, 2, 1, 1, 0, 1) == _lib.OMT_CONV_NONE   # stride 5
+    assert k(3, 64, 12, 12, 1, 1, 0, 0, 1, 1, 0, 1) == _lib.OMT_CONV_NONE   # ks 12
+    assert k(3, 64, 3, 3, 1, 1, 4, 4, 1, 1, 0, 1) == _lib.OMT_CONV_NONE     # pad > ks
+    assert k(3, 64, 3, 3, 1, 1, 1, 1, 2, 2, 0, 1) == _lib.OMT_CONV_NONE     # dilated
+    assert k(3, 64, 3, 5, 1, 1, 1, 1, 1, 1, 0, 1) == _lib.OMT_CONV_NONE     # non-square
+    assert k(3, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1) == _lib.OMT_CONV_NONE     # transposed
+    assert k(8, 8, 3, 3, 1, 1, 1, 1, 1, 1, 0, 8) == _lib.OMT_CONV_DW
+    assert k(8, 8, 5, 5, 1, 1, 1, 1, 1, 1, 0, 8) == _lib.OMT_CONV_DWG       # dw with non-"same" pad
+    assert k(8, 8, 3, 3, 2, 2, 1, 1, 1, 1, 0, 8) == _lib.OMT_CONV_DWG
+    assert k(8, 16, 3, 3, 1, 1, 1, 1, 1, 1, 0, 8) == _lib.OMT_CONV_NONE     # channel multiplier
+    assert k(8, 8, 3, 3, 1, 1, 1, 1, 1, 1, 0, 2) == _lib.OMT_CONV_NONE      # grouped
+
+
+def test_host_validation_statuses():
+    """Unsupported geometry and bad arguments are rejected on the host, before any kernel launch."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    g = _lib.ConvGeo(2, 3, 4, 8, 8, 1, 1, 12, 1, 0)  # ks 12
+    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, None, None, None, None, 1e-5, fake, None) == \
+        _lib.OMT_UNSUPPORTED
+    assert b"geometry" in L.omt_last_error()
+    g = _lib.conv_geo(2, 3, 4, 8, 8, 3, 1, 1)
+    assert L.omt_conv_fwd(ctypes.byref(g), None, fake, None, 0, None, None, None, None, 1e-5, fake, None) == \
+        _lib.OMT_INVALID
+    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, _lib.OMT_EPI_BIAS, None, None, None, None, 1e-5, fake,
+                          None) == _lib.OMT_INVALID
+    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, fake, None, None, None, 1e-5, fake, None) == \
+        _lib.OMT_INVALID  # partial BN loader
+    g.oh = 99  # inconsistent geometry
+    assert L.omt_conv_wgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
+    g = _lib.conv_geo(2, 3, 4, 8, 8, 3, 2, 1)
+    assert L.omt_conv_dgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID  # no workspace
+    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 4 * 3 * 3 * 3 * 4
+    with pytest.raises(_lib.Unsupported):
+        _lib.check(_lib.OMT_UNSUPPORTED)
+
+
+FASTDIV_TEST = r"""
+#include "omt_internal.h"
+#include <cstdio>
+#include <random>
+int main() {
+  std::mt19937 rng(1);
+  int bad = 0;
+  for (uint32_t d = 1; d < 70000 && !bad; ++d) {
+    omt::FastDiv f = omt::make_fastdiv(d);
+    for (int i = 0; i < 200; ++i) {
+      uint32_t n = i < 100 ? (uint32_t)(rng() % (1u << 31)) : (uint32_t)(i * 97 + d * (i % 7));
+      if (omt::fdiv(n, f) != n / d) { printf("bad %u / %u\n", n, d); bad = 1; break; }
+    }
+    for (uint32_t k = 1; k < 4 && !bad; ++k) {  // around multiples of d
+      uint64_t m = (uint64_t)d * (k * 1000003u % 30011u);
+      for (int64_t e = -1; e <= 1; ++e) {
+        int64_t n = (int64_t)m + e;
+        if (n < 0 || n >= (1ll << 31)) continue;
+        if (omt::fdiv((uint32_t)n, f) != (uint32_t)n / d) { printf("bad %lld / %u\n", (long long)n, d); bad = 1; }
+      }
+    }
+  }
+  for (uint32_t d : {2147483647u, 1u << 30, 3u, 7u, 802816u, 3136u, 49u, 121u})
+    for (uint32_t n : {0u, 1u, d - 1, d, d + 1, 2147483647u})
+      if (omt::fdiv(n, omt::make_fastdiv(d)) != n / d) { printf("bad %u / %u\n", n, d); bad = 1; }
+  printf(bad ? "FAIL\n" : "OK\n");
+  return bad;
+}
+"""
+
+
+def test_fastdiv_exact(tmp_path):
+    """FastDiv (omt_internal.h) against '/' for divisors 1..70000 and 31-bit numerators, built for the host."""
+    src = tmp_path / "fastdiv.cpp"
+    src.write_text(FASTDIV_TEST)
+    exe = tmp_path / "fastdiv"
+    subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "--offload-arch=gfx950", "-O2", "-std=c++17",
+                    f"-I{ROOT / 'include'}", f"-I{ROOT / 'omarchy-mac-torch_amd' / 'csrc'}", str(src), "-o", str(exe)],
+                   check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "OK", r.stdout

@@ -1,0 +1,300 @@
+"""Parity of the HIP kernels (libomt_hip.so, called through its C ABI) with the CPU oracle (oracle/omt_oracle.c).
+
+Criterion: rel-L2 = ||dev - ref||_2 / ||ref||_2 <= 1e-4 per op for float32 results; int64
+pooling indices must match exactly. Small shapes are checked against the full oracle; the BASELINE full-size shapes
+(config 1 AlexNet conv1 at batch 16, config 5 ResNet-50 body layers at batch 256) against oracle values at sampled
+output points plus the size-independent adjoint identity <conv(x,w), gy> = <x, dgrad(gy,w)> = <w, wgrad(x,gy)>.
+Shape lists follow the reference's own check scripts (notes/scripts/conv_kinds_check.py:5,
+notes/scripts/alexnet_ops_check.py:6-16, tools/gemm_bench.py:8-9).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def rnd(rng, *shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+
+def dev(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from omarchy_mac_torch import hip_ops
+    return hip_ops
+
+
+# ---- dense conv: full oracle at small sizes ----
+
+CONV_SHAPES = [
+    # (n, ci, co, h, w, ks, stride, pad)
+    (4, 6, 10, 14, 14, 5, 1, 2), (4, 6, 10, 14, 14, 3, 1, 1), (4, 6, 10, 14, 14, 1, 1, 0),   # conv_kinds_check.py:5
+    (3, 3, 8, 63, 63, 11, 4, 2), (3, 3, 6, 15, 15, 3, 2, 1), (3, 5, 7, 21, 21, 5, 2, 0),     # alexnet_ops_check.py:6
+    (2, 64, 192, 27, 27, 5, 1, 2), (2, 192, 64, 13, 13, 3, 1, 1), (2, 32, 32, 16, 16, 3, 1, 1),  # gemm_bench.py:8-9
+    (2, 3, 64, 224, 224, 11, 4, 2),                      # config 1 AlexNet conv1 at batch 2
+    (2, 64, 64, 56, 56, 3, 1, 1), (2, 128, 128, 28, 28, 3, 1, 1),  # config 5 layers at batch 2
+    (2, 256, 256, 14, 14, 3, 1, 1), (2, 512, 512, 7, 7, 3, 1, 1),
+    (2, 64, 256, 56, 56, 1, 1, 0), (2, 256, 64, 56, 56, 1, 1, 0),
+    (4, 3, 64, 64, 64, 7, 2, 3), (4, 64, 128, 16, 16, 3, 2, 1), (4, 64, 128, 16, 16, 1, 2, 0),  # ResNet-18 stem/down
+    (4, 512, 512, 2, 2, 3, 1, 1),                        # ResNet-18 layer4 at 64x64 input
+    (3, 7, 9, 13, 11, 3, 3, 2), (2, 5, 3, 9, 17, 4, 4, 4), (2, 17, 33, 10, 7, 2, 1, 0),   # ragged / odd
+]
+
+
+def _ids(s):
+    return "n{}c{}o{}h{}w{}k{}s{}p{}".format(*s)
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=_ids)
+def test_conv_fwd_dgrad_wgrad(cuda, ops, shape):
+    n, ci, co, h, w, ks, s, p = shape
+    rng = np.random.default_rng(hash(shape) % 2**32)
+    scale = (ci * ks * ks) ** -0.5
+    x, wt, b = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=scale), rnd(rng, co, scale=0.1)
+    y = ops.conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), s, p)
+    y_ref = orc.conv_fwd(x, wt, b, s, p)
+    assert orc.rel_l2(host(y), y_ref) <= TOL
+    gy = rnd(rng, *y_ref.shape)
+    gx = ops.conv2d_dgrad(dev(gy, cuda), dev(wt, cuda), x.shape, s, p)
+    assert orc.rel_l2(host(gx), orc.conv_dgrad(gy, wt, x.shape, s, p)) <= TOL
+    gw = ops.conv2d_wgrad(dev(x, cuda), dev(gy, cuda), ks, s, p)
+    assert orc.rel_l2(host(gw), orc.conv_wgrad(x, gy, ks, s, p)) <= TOL
+    gb = ops.bias_grad(dev(gy, cuda))
+    assert orc.rel_l2(host(gb), orc.bias_grad(gy)) <= TOL
+
+
+@pytest.mark.parametrize("ks", range(1, 12))
+def test_conv_geometry_sweep(cuda, ops, ks):
+    """Every stride 1..4 and pad 0..ks the dense path accepts at this kernel size (csrc/conv.cpp:173), on tiny
+    non-square images, including stride phases that no tap reaches."""
+    rng = np.random.default_rng(ks)
+    for s in range(1, 5):
+        for p in range(0, ks + 1):
+            for ih, iw in ((ks + 1, ks + 2), (ks + 5, ks + 3)):
+                if ih + 2 * p < ks or iw + 2 * p < ks:
+                    continue
+                x, wt, b = rnd(rng, 2, 3, ih, iw), rnd(rng, 5, 3, ks, ks), rnd(rng, 5)
+                case = (ks, s, p, ih, iw)
+                y = ops.conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), s, p, relu=True)
+                y_ref = orc.conv_fwd(x, wt, b, s, p, relu=True)
+                assert orc.rel_l2(host(y), y_ref) <= TOL, case
+                gy = rnd(rng, *y_ref.shape)
+                gx = ops.conv2d_dgrad(dev(gy, cuda), dev(wt, cuda), x.shape, s, p)
+                assert orc.rel_l2(host(gx), orc.conv_dgrad(gy, wt, x.shape, s, p)) <= TOL, case
+                gw = ops.conv2d_wgrad(dev(x, cuda), dev(gy, cuda), ks, s, p)
+                assert orc.rel_l2(host(gw), orc.conv_wgrad(x, gy, ks, s, p)) <= TOL, case
+
+
+def test_conv_bn_loader_and_relu_epilogue(cuda, ops):
+    """Kind-3 loader (eval BN + ReLU of the input, padding stays zero) and the bias + ReLU epilogue."""
+    rng = np.random.default_rng(7)
+    for ks, s, p in ((1, 1, 0), (3, 1, 1), (3, 2, 1)):
+        x, wt, b = rnd(rng, 3, 8, 12, 10), rnd(rng, 6, 8, ks, ks), rnd(rng, 6)
+        bn = (rnd(rng, 8), np.abs(rnd(rng, 8)) + 0.5, rnd(rng, 8), rnd(rng, 8))
+        y = ops.conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), s, p, relu=True, bn=[dev(t, cuda) for t in bn])
+        y_ref = orc.conv_fwd(x, wt, b, s, p, relu=True, bn=bn)
+        assert orc.rel_l2(host(y), y_ref) <= TOL, (ks, s, p)
+
+
+def test_fold_bn(cuda, ops):
+    rng = np.random.default_rng(3)
+    cw, cb = rnd(rng, 16, 8, 3, 3), rnd(rng, 16)
+    g, b, m, v = rnd(rng, 16), rnd(rng, 16), rnd(rng, 16), np.abs(rnd(rng, 16)) + 0.2
+    for bias in (cb, None):
+        fw, fb = ops.fold_bn(dev(cw, cuda), None if bias is None else dev(bias, cuda), *[dev(t, cuda) for t in (g, b, m, v)])
+        rw, rb = orc.fold_bn(cw, bias, g, b, m, v)
+        assert orc.rel_l2(host(fw), rw) <= 1e-6 and orc.rel_l2(host(fb), rb) <= 1e-6
+
+
+# ---- dense conv at the BASELINE full sizes ----
+
+FULL = [
+    ("C1_alexnet_conv1", (16, 3, 64, 224, 224, 11, 4, 2)),
+    ("C5_3x3_56", (256, 64, 64, 56, 56, 3, 1, 1)),
+    ("C5_3x3_28", (256, 128, 128, 28, 28, 3, 1, 1)),
+    ("C5_3x3_14", (256, 256, 256, 14, 14, 3, 1, 1)),
+    ("C5_3x3_7", (256, 512, 512, 7, 7, 3, 1, 1)),
+    ("C5_1x1_exp_56", (256, 64, 256, 56, 56, 1, 1, 0)),
+    ("C5_1x1_red_56", (256, 256, 64, 56, 56, 1, 1, 0)),
+    ("C5_1x1_exp_7", (256, 512, 2048, 7, 7, 1, 1, 0)),
+]
+
+
+@pytest.mark.parametrize("name,shape", FULL, ids=[f[0] for f in FULL])
+def test_conv_full_size(cuda, ops, name, shape):
+    n, ci, co, h, w, ks, s, p = shape
+    gen = torch.Generator(device=cuda).manual_seed(1)
+    scale = (ci * ks * ks) ** -0.5
+    x = torch.randn((n, ci, h, w), device=cuda, generator=gen)
+    wt = torch.randn((co, ci, ks, ks), device=cuda, generator=gen) * scale
+    b = torch.rand((co,), device=cuda, generator=gen) * 0.2 - 0.1
+    y = ops.conv2d(x, wt, b, s, p)
+    gy = torch.randn(y.shape, device=cuda, generator=gen) * scale
+    gx = ops.conv2d_dgrad(gy, wt, x.shape, s, p)
+    gw = ops.conv2d_wgrad(x, gy, ks, s, p)
+    torch.cuda.synchronize()
+    # adjoint identity in float64 (bias removed from y)
+    yb = (y - b.view(1, -1, 1, 1)).double()
+    a1 = (yb * gy.double()).sum().item()
+    a2 = (x.double() * gx.double()).sum().item()
+    a3 = (wt.double() * gw.double()).sum().item()
+    norm = (yb.norm() * gy.double().norm()).item()
+    assert abs(a1 - a2) <= 1e-5 * norm and abs(a1 - a3) <= 1e-5 * norm, (a1, a2, a3, norm)
+    # sampled outputs against the oracle
+    rng = np.random.default_rng(0)
+    xh, wh, bh, gyh = host(x), host(wt), host(b), host(gy)
+    pts = rng.integers(0, y.numel(), 3000)
+    ref = orc.conv_fwd_points(xh, wh, pts, bh, s, p)
+    assert orc.rel_l2(host(y).ravel()[pts], ref) <= TOL
+    pts = rng.integers(0, gx.numel(), 3000)
+    ref = orc.conv_dgrad_points(gyh, wh, x.shape, pts, s, p)
+    assert orc.rel_l2(host(gx).ravel()[pts], ref) <= TOL
+    pts = rng.integers(0, gw.numel(), 200)
+    ref = orc.conv_wgrad_points(xh, gyh, ks, pts, s, p)
+    assert orc.rel_l2(host(gw).ravel()[pts], ref) <= TOL
+
+
+# ---- depthwise ----
+
+DW = [(3, 1, 1), (5, 1, 2), (7, 1, 3), (3, 2, 1), (5, 2, 0), (11, 4, 5), (2, 3, 1), (9, 1, 0)]
+
+
+@pytest.mark.parametrize("ks,s,p", DW)
+def test_depthwise(cuda, ops, ks, s, p):
+    rng = np.random.default_rng(ks * 10 + s)
+    c = 12
+    x, wt, b = rnd(rng, 3, c, 17, 15), rnd(rng, c, 1, ks, ks), rnd(rng, c)
+    y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), s, p)
+    y_ref = orc.dw_fwd(x, wt, b, s, p)
+    assert orc.rel_l2(host(y), y_ref) <= TOL
+    gy = rnd(rng, *y_ref.shape)
+    gx = ops.depthwise_dgrad(dev(gy, cuda), dev(wt, cuda), x.shape, s, p)
+    assert orc.rel_l2(host(gx), orc.dw_dgrad(gy, wt, x.shape, s, p)) <= TOL
+    gw = ops.depthwise_wgrad(dev(x, cuda), dev(gy, cuda), ks, s, p)
+    assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, ks, s, p)) <= TOL
+
+
+def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
+    rng = np.random.default_rng(5)
+    c = 8
+    x, wt = rnd(rng, 2, c, 11, 11), rnd(rng, c, 1, 3, 3)
+    bn = (rnd(rng, c), np.abs(rnd(rng, c)) + 0.5, rnd(rng, c), rnd(rng, c))
+    y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), None, 1, 1, bn=[dev(t, cuda) for t in bn])
+    assert orc.rel_l2(host(y), orc.dw_fwd(x, wt, None, 1, 1, bn=bn)) <= TOL
+    # a MobileNetV3-Small-style layer at batch 32 (config 4): dw 5x5 over 96 channels at 28x28
+    x, wt = rnd(rng, 32, 96, 28, 28), rnd(rng, 96, 1, 5, 5)
+    y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), None, 1, 2)
+    y_ref = orc.dw_fwd(x, wt, None, 1, 2)
+    assert orc.rel_l2(host(y), y_ref) <= TOL
+    gy = rnd(rng, *y_ref.shape)
+    gw = ops.depthwise_wgrad(dev(x, cuda), dev(gy, cuda), 5, 1, 2)
+    assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, 5, 1, 2)) <= TOL
+
+
+# ---- batch norm ----
+
+@pytest.mark.parametrize("n,c,h,w", [(4, 6, 5, 7), (16, 8, 4, 4), (2, 3, 1, 1), (9, 4, 3, 3), (128, 32, 32, 32),
+                                     (32, 64, 16, 16), (32, 512, 2, 2), (1, 16, 57, 31)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_batch_norm_train_and_backward(cuda, ops, n, c, h, w, relu):
+    rng = np.random.default_rng(n * 1000 + c)
+    x = rnd(rng, n, c, h, w) * 3 + 5  # large mean: the shifted statistics must stay accurate
+    g, b, rm, rv = rnd(rng, c), rnd(rng, c), rnd(rng, c), np.abs(rnd(rng, c)) + 0.5
+    trm, trv = dev(rm, cuda), dev(rv, cuda)
+    y, sm, si = ops.batch_norm_train(dev(x, cuda), dev(g, cuda), dev(b, cuda), trm, trv, 0.1, 1e-5, relu)
+    y_ref, m_ref, i_ref, nrm, nrv = orc.bn_train(x, g, b, rm, rv, 0.1, 1e-5, relu)
+    assert orc.rel_l2(host(y), y_ref) <= TOL
+    assert orc.rel_l2(host(sm), m_ref) <= 1e-6 and orc.rel_l2(host(si), i_ref) <= 1e-5
+    assert orc.rel_l2(host(trm), nrm) <= 1e-6 and orc.rel_l2(host(trv), nrv) <= 1e-6
+    gy = rnd(rng, n, c, h, w)
+    gx, dg, db = ops.batch_norm_backward(dev(gy, cuda), dev(x, cuda), sm, si, dev(g, cuda),
+                                         relu_y=y if relu else None)
+    gx_ref, dg_ref, db_ref = orc.bn_bwd(gy, x, host(sm), host(si), g, relu_y=host(y) if relu else None)
+    # gx is a difference of near-equal terms (exactly 0 when m = 2), so its error is normalized by the gradient scale
+    gz = gy * (y_ref > 0) if relu else gy
+    scale = np.linalg.norm(gz.astype(np.float64)) * np.abs(g * i_ref).max()
+    assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
+    assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
+
+
+def test_batch_norm_functional_and_eval(cuda, ops):
+    rng = np.random.default_rng(11)
+    x, g, b, rm, rv = rnd(rng, 8, 5, 6, 6), rnd(rng, 5), rnd(rng, 5), rnd(rng, 5), np.abs(rnd(rng, 5)) + 0.2
+    trm, trv = dev(rm, cuda), dev(rv, cuda)
+    y, sm, si, nrm, nrv = ops.batch_norm_train(dev(x, cuda), dev(g, cuda), dev(b, cuda), trm, trv, 0.3, 1e-5,
+                                               functional=True)
+    _, _, _, rnm, rnv = orc.bn_train(x, g, b, rm, rv, 0.3, 1e-5)
+    assert np.array_equal(host(trm), rm) and np.array_equal(host(trv), rv)  # inputs untouched
+    assert orc.rel_l2(host(nrm), rnm) <= 1e-6 and orc.rel_l2(host(nrv), rnv) <= 1e-6
+    for relu in (False, True):
+        ye = ops.batch_norm_eval(dev(x, cuda), dev(g, cuda), dev(b, cuda), trm, trv, 1e-3, relu)
+        assert orc.rel_l2(host(ye), orc.bn_eval(x, g, b, rm, rv, 1e-3, relu)) <= 1e-6
+
+
+# ---- pooling ----
+
+MAXPOOL = [((3, 3), (2, 2), (0, 0), (1, 1), False, 13), ((3, 3), (2, 2), (0, 0), (1, 1), False, 27),
+           ((3, 3), (2, 2), (1, 1), (1, 1), False, 14), ((3, 3), (1, 1), (1, 1), (1, 1), False, 9),
+           ((2, 2), (2, 2), (0, 0), (1, 1), False, 12), ((5, 5), (3, 3), (2, 2), (1, 1), False, 17),
+           ((3, 3), (2, 2), (1, 1), (2, 2), False, 15), ((3, 2), (2, 1), (1, 0), (1, 1), True, 11),
+           ((2, 2), (2, 2), (0, 0), (1, 1), True, 13)]
+
+
+@pytest.mark.parametrize("k,s,p,d,ceil,hw", MAXPOOL)
+def test_maxpool(cuda, ops, k, s, p, d, ceil, hw):
+    rng = np.random.default_rng(hw)
+    x = rnd(rng, 2, 4, hw, hw + 1)
+    x[0, 0, 0, :3] = x[0, 0, 0, 0]  # ties: the first maximum wins
+    x[1, 2, 3, 4] = np.nan          # NaN propagates with its index
+    y, idx = ops.max_pool2d(dev(x, cuda), k, s, p, d, ceil)
+    y_ref, idx_ref = orc.maxpool_fwd(x, k, s, p, d, ceil)
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    yh = host(y)
+    np.testing.assert_array_equal(np.isnan(yh), np.isnan(y_ref))
+    np.testing.assert_array_equal(yh[~np.isnan(yh)], y_ref[~np.isnan(y_ref)])
+    gy = rnd(rng, *y_ref.shape)
+    gx = ops.max_pool2d_backward(dev(gy, cuda), x.shape, idx, k, s, p, d)
+    assert orc.rel_l2(host(gx), orc.maxpool_bwd(gy, idx_ref, x.shape)) <= 1e-6
+
+
+AVGPOOL = [((3, 3), (2, 2), (1, 1), False, True, None, 14), ((3, 3), (2, 2), (1, 1), False, False, None, 14),
+           ((2, 2), (2, 2), (0, 0), False, True, None, 12), ((3, 3), (2, 2), (1, 1), True, False, None, 15),
+           ((3, 2), (1, 2), (1, 1), True, True, None, 9), ((3, 3), (2, 2), (1, 1), False, True, 5, 10)]
+
+
+@pytest.mark.parametrize("k,s,p,ceil,incl,div,hw", AVGPOOL)
+def test_avgpool(cuda, ops, k, s, p, ceil, incl, div, hw):
+    rng = np.random.default_rng(hw + 100)
+    x = rnd(rng, 2, 3, hw, hw + 2)
+    y = ops.avg_pool2d(dev(x, cuda), k, s, p, ceil, incl, div)
+    y_ref = orc.avgpool_fwd(x, k, s, p, ceil, incl, div)
+    assert orc.rel_l2(host(y), y_ref) <= 1e-6
+    gy = rnd(rng, *y_ref.shape)
+    gx = ops.avg_pool2d_backward(dev(gy, cuda), x.shape, k, s, p, incl, div)
+    assert orc.rel_l2(host(gx), orc.avgpool_bwd(gy, x.shape, k, s, p, incl, div)) <= 1e-6
+
+
+@pytest.mark.parametrize("hw,o", [(6, 6), (13, 6), (10, 4), (7, 1), (5, 3), (2, 1), (56, 1)])
+def test_adaptive_avgpool(cuda, ops, hw, o):
+    rng = np.random.default_rng(hw * 7 + o)
+    x = rnd(rng, 3, 5, hw, hw + (0 if o == 1 else 1))
+    y = ops.adaptive_avg_pool2d(dev(x, cuda), o)
+    y_ref = orc.adapool_fwd(x, o, o)
+    assert orc.rel_l2(host(y), y_ref) <= 1e-6
+    gy = rnd(rng, *y_ref.shape)
+    gx = ops.adaptive_avg_pool2d_backward(dev(gy, cuda), x.shape)
+    assert orc.rel_l2(host(gx), orc.adapool_bwd(gy, x.shape)) <= 1e-6
