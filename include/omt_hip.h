@@ -93,10 +93,12 @@ int omt_event_elapsed_ms(void* start, void* end, float* ms);
  * bn_mean/var/gamma/beta non-NULL (all four): the input is first mapped through the previous layer's eval BatchNorm
  * + ReLU, max((x - mean[ci]) * rsqrt(var[ci] + eps) * gamma[ci] + beta[ci], 0), on in-bounds taps only (padding
  * stays zero). Replaces gemm_forward (csrc/conv.cpp:70-77) with kinds 0 and 3 (omarchy_mac_torch/gemm.py:25-42,
- * 139-141). Dense means: ks 1..11, stride 1..4, 0 <= pad <= ks. */
+ * 139-141). Dense means: ks 1..11, stride 1..4, 0 <= pad <= ks. The workspace (omt_conv_fwd_workspace bytes, possibly 0)
+ * holds the filter re-packed for the tap-major reduction order. */
+size_t omt_conv_fwd_workspace(const omt_conv_geo* g);
 int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
                  const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta, float bn_eps,
-                 float* y, void* stream);
+                 float* y, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Grad input: gx = conv_transpose(gy, w). Stride 1 is one GEMM over flipped, transposed weights; stride s > 1 is
  * s*s dense stride-phase GEMMs in one launch (phases no tap reaches write zeros). Replaces gemm_grad_input

@@ -16,15 +16,39 @@
 // split_reduce_kernel (reference: gemm_grad_weight + gemm_reduce, csrc/conv.cpp:102-114).
 //
 // Tiling: a 256-thread workgroup computes a BP x BQ tile of C as 4 waves, each a WP x WQ block of 16x16 MFMA tiles,
-// with the operands staged through double-buffered LDS. MFMA 16x16x4 lane layout: lane l supplies A[l%16][l/16] and
-// B[l/16][l%16]; the accumulator holds D[4*(l/16) + r][l%16] in element r. Because the reduction order inside a
-// K-block is free, lane group g = l/16 reads K-row g*(BK/4) + s at step s, which spreads the four groups over
-// distinct LDS banks.
+// with the operands staged through LDS. MFMA 16x16x4 lane layout: lane l supplies A[l%16][l/16] and B[l/16][l%16];
+// the accumulator holds D[4*(l/16) + r][l%16] in element r. Because the reduction order inside a K-block is free,
+// lane group g = l/16 supplies K-index g*(BK/4) + s at MFMA step s. Both operands sit in LDS as rows of K
+// (k contiguous, pitch BK + 4 floats), so one ds_read_b128 hands a lane four consecutive steps' operands, and the
+// pitch (5 or 17 x 16 bytes) puts the eight rows one b128 access phase touches on distinct banks.
+//
+// Operand loads are raw buffer loads: an offset at or beyond the buffer's byte size returns 0 in hardware, so taps in
+// the zero padding, K-tails and pixels past the end are all loaded branch-free with an out-of-range offset (kOOB),
+// and no computed offset can reach memory outside the tensor. Tensors read this way must stay below 2 GiB.
+//
+// Reduction order. With C a multiple of the K-block, K is ordered tap-major, k = (ky, kx, c), over weights re-packed
+// to [co][ky][kx][ci] (tap-major mode). A K-block (or a wave's run of tap columns in wgrad) then shares one tap: one
+// bounds test per lane per block yields the vector offset, and each element is a bare buffer load whose channel
+// offset c*H*W travels in the scalar offset. Other C use the channel-major order k = (c, ky, kx) of the reference's
+// index maps (generic mode) with a per-element bounds test.
 #include "omt_internal.h"
 
 namespace omt {
 
 constexpr int kMaxPhases = 16;
+constexpr uint32_t kOOB = 0x80000000u;  // byte offset beyond every buffer (buffers are < 2 GiB)
+constexpr int64_t kMaxBufBytes = 0x7fffffffll;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
+__device__ __forceinline__ float f4get(const float4& v, int s) { return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w; }
+
+enum { kGeneric = 0, kTapMajor = 1 };
 
 struct Phase {
   int KH, KW, S, PH, PW;  // gather window, stride and (signed) padding
@@ -43,24 +67,26 @@ struct GatherArgs {
   float bn_eps;
   int relu;
   float* y;  // [N][P][YH][YW]
+  uint32_t x_bytes, w_bytes;
   int C, H, W, P, YH, YW;
+  FastDiv div_c;
   int nphase;
   Phase ph[kMaxPhases];
 };
 
-template <int BP, int BQ, int WP, int WQ>
+template <int BP, int BQ, int WP, int WQ, int MODE, bool BN>
 __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
   constexpr int BK = 16, NT = 256;
   constexpr int WGQ = BQ / WQ;
   static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
   static_assert(WP % 16 == 0 && WQ % 16 == 0 && BQ >= 64 && NT % BQ == 0, "tile shape");
   constexpr int TI = WP / 16, TJ = WQ / 16;
-  constexpr int LA = BP + 4, LB = BQ + 4;  // LDS pitches: 4 * pitch = 16 (mod 32) keeps lane groups on distinct banks
-  constexpr int AR = BP * BK / NT;         // weight elements per thread
-  constexpr int BR = BQ * BK / NT;         // gathered k-rows per thread
-  static_assert(AR >= 1 && BR >= 1, "tile too small");
-  __shared__ float As[2][BK * LA];
-  __shared__ float Bs[2][BK * LB];
+  constexpr int PK = BK + 4;        // LDS row pitch (floats) of both operands: rows are output channels / pixels
+  constexpr int AR = BP * BK / NT;  // weight elements per thread
+  constexpr int BR = BQ * BK / NT;  // gathered k-rows per thread (a multiple of 4: stored as b128)
+  static_assert(AR >= 1 && BR >= 4 && BR % 4 == 0, "tile too small");
+  __shared__ __attribute__((aligned(16))) float As[2][BP * PK];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BQ * PK];
 
   const Phase& ph = a.ph[blockIdx.z];
   const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
@@ -70,13 +96,14 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
   const int wp = wave / WGQ, wq = wave % WGQ;
   const int KH = ph.KH, KW = ph.KW, K = ph.K, KK = KH * KW;
   const int H = a.H, W = a.W, HW = H * W, P = a.P;
-  const float* __restrict__ wt = a.w + ph.woff;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
 
-  // this thread's output pixel (column of the gathered operand)
+  // this thread's output pixel (column of the gathered operand): byte offset of x[n][0][iy0][ix0]
   const int qc = t % BQ;
   const int rbase = __builtin_amdgcn_readfirstlane((t / BQ) * BR);
   int iy0 = -(1 << 28), ix0 = -(1 << 28);  // pixels past Q gather nothing
-  const float* __restrict__ xb = a.x;
+  uint32_t lbase = kOOB;
   {
     const int q = q0 + qc;
     if (q < ph.Q) {
@@ -85,17 +112,33 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
       const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
       iy0 = (int)oy * ph.S - ph.PH;
       ix0 = (int)ox * ph.S - ph.PW;
-      xb = a.x + (int64_t)n * a.C * HW;
+      lbase = (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
     }
   }
-  const int pix = iy0 * W + ix0;
 
   // wave-uniform tap state (c, ky, kx), decomposed afresh at the start of every K-block
   int sc = 0, sky = 0, skx = 0;
-  const bool has_bn = a.bn_mean != nullptr;
+  const int wrow0 = t / BK, wk = t % BK;  // weight tile element: rows wrow0 + 16 i, column wk
 
   float ra[AR], rb[BR];
   auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < AR; ++i) {
+      const int p = p0 + wrow0 + (NT / BK) * i, k = k0 + wk;
+      const uint32_t off = (p < P && k < K) ? (uint32_t)((ph.woff + p * K + k) * 4) : kOOB;
+      ra[i] = bload(wr, off, 0);
+    }
+    if (MODE == kTapMajor) {
+      // k = tap * C + c with C % BK == 0: this thread's BR rows share one tap and K has no tail
+      const uint32_t kb = (uint32_t)(k0 + rbase);
+      const int tap = (int)fdiv(kb, a.div_c), c0 = (int)kb - tap * a.C;
+      const int ky = (int)fdiv((uint32_t)tap, ph.div_kw), kx = tap - ky * KW;
+      const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
+      const uint32_t voff = ok ? lbase + (uint32_t)((ky * W + kx) * 4) : kOOB;
+#pragma unroll
+      for (int j = 0; j < BR; ++j) rb[j] = bload(xr, voff, (uint32_t)((c0 + j) * HW * 4));
+      return;
+    }
     {
       const uint32_t kb = (uint32_t)(k0 + rbase);
       sc = (int)fdiv(kb, ph.div_kk);
@@ -104,37 +147,34 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
       skx = (int)r - sky * KW;
     }
 #pragma unroll
-    for (int i = 0; i < AR; ++i) {
-      const int kk = t % BK, p = p0 + t / BK + (NT / BK) * i, k = k0 + kk;
-      ra[i] = (p < P && k < K) ? wt[p * K + k] : 0.f;
-    }
-#pragma unroll
     for (int j = 0; j < BR; ++j) {
       const bool kval = k0 + rbase + j < K;
-      const int iy = iy0 + sky, ix = ix0 + skx;
       float v = 0.f;
-      if (kval && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) {
-        v = xb[pix + sc * HW + sky * W + skx];
-        if (has_bn) {
+      {
+        const bool ok = kval && (unsigned)(iy0 + sky) < (unsigned)H && (unsigned)(ix0 + skx) < (unsigned)W;
+        v = bload(xr, ok ? lbase + (uint32_t)((sc * HW + sky * W + skx) * 4) : kOOB, 0);
+        if (BN) {
           const float inv = rsqrtf(a.bn_var[sc] + a.bn_eps);
-          v = fmaxf((v - a.bn_mean[sc]) * inv * a.bn_gamma[sc] + a.bn_beta[sc], 0.f);
+          const float z = fmaxf((v - a.bn_mean[sc]) * inv * a.bn_gamma[sc] + a.bn_beta[sc], 0.f);
+          v = ok ? z : 0.f;  // padding taps stay zero: BN + ReLU applies to in-bounds taps only
+        }
+        if (++skx == KW) {
+          skx = 0;
+          if (++sky == KH) {
+            sky = 0;
+            ++sc;
+          }
         }
       }
       rb[j] = v;
-      if (++skx == KW) {
-        skx = 0;
-        if (++sky == KH) {
-          sky = 0;
-          ++sc;
-        }
-      }
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < AR; ++i) As[buf][(t % BK) * LA + t / BK + (NT / BK) * i] = ra[i];
+    for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[i];
 #pragma unroll
-    for (int j = 0; j < BR; ++j) Bs[buf][(rbase + j) * LB + qc] = rb[j];
+    for (int j = 0; j < BR; j += 4)
+      *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) = make_float4(rb[j], rb[j + 1], rb[j + 2], rb[j + 3]);
   };
 
   omt_f32x4 acc[TI][TJ];
@@ -153,19 +193,18 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
   for (int it = 0; it < nk; ++it) {
     const int cur = it & 1;
     if (it + 1 < nk) gload((it + 1) * BK);
+    float4 av[TI], bv[TJ];
 #pragma unroll
-    for (int s = 0; s < BK / 4; ++s) {
-      const int kr = grp * (BK / 4) + s;
-      float av[TI], bv[TJ];
+    for (int i = 0; i < TI; ++i) av[i] = *reinterpret_cast<const float4*>(&As[cur][(la + 16 * i) * PK + grp * 4]);
 #pragma unroll
-      for (int i = 0; i < TI; ++i) av[i] = As[cur][kr * LA + la + 16 * i];
+    for (int j = 0; j < TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(&Bs[cur][(lb + 16 * j) * PK + grp * 4]);
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) bv[j] = Bs[cur][kr * LB + lb + 16 * j];
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
     if (it + 1 < nk) sstore(cur ^ 1);
     __syncthreads();
   }
@@ -201,23 +240,24 @@ struct WgradArgs {
   const float* x;   // [N][C][H][W]
   const float* gy;  // [N][P][OH][OW]
   float* out;       // [slices][P][Q]
+  uint32_t x_bytes, gy_bytes;
   int C, H, W, P, OH, OW, KS, S, PAD;
   int Q, K;    // C * KS * KS, N * OH * OW
   int kslice;  // pixels per slice, a multiple of the K-block
-  FastDiv div_ohw, div_ow, div_kk, div_ks;
+  FastDiv div_ohw, div_ow, div_kk, div_ks, div_c;
 };
 
-template <int BP, int BQ, int WP, int WQ>
+template <int BP, int BQ, int WP, int WQ, int MODE>
 __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   constexpr int BK = 64;  // one reduction pixel per lane
   constexpr int WGQ = BQ / WQ;
   static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
   static_assert(WP % 16 == 0 && WQ % 16 == 0 && BP % 4 == 0 && BQ % 4 == 0, "tile shape");
   constexpr int TI = WP / 16, TJ = WQ / 16;
-  constexpr int LA = BP + 1, LB = BQ + 1;  // odd pitches: lanes writing consecutive K-rows hit distinct banks
-  constexpr int AR = BP / 4, BR = BQ / 4;  // rows (cols) each wave stages per K-block
-  __shared__ float As[BK * LA];
-  __shared__ float Bs[BK * LB];
+  constexpr int PK = BK + 4;               // LDS row pitch (floats): rows are gy channels / tap columns, k contiguous
+  constexpr int AR = BP / 4, BR = BQ / 4;  // rows (cols) each wave stages per K-block, contiguous per wave
+  __shared__ __attribute__((aligned(16))) float As[BP * PK];
+  __shared__ __attribute__((aligned(16))) float Bs[BQ * PK];
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -225,45 +265,73 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
   const int kbeg = blockIdx.z * a.kslice;
   const int kend = min(a.K, kbeg + a.kslice);
-  const int H = a.H, W = a.W, HW = H * W, P = a.P, Q = a.Q;
+  const int H = a.H, W = a.W, HW = H * W, P = a.P, Q = a.Q, KS = a.KS;
   const int ohw = a.OH * a.OW;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gy, a.gy_bytes);
+  const int pw0 = p0 + wave * AR;  // this wave's first staged gy row
+  const int qw0 = q0 + wave * BR;  // this wave's first staged tap column
+  // tap state of column qw0 (wave-uniform, constant over the K loop). Generic: q = (c, ky, kx). Tap-major:
+  // q = (ky, kx, c) with C % BR == 0, so the wave's BR columns share the tap (ky0, kx0) over channels c0 ...
+  int c0, ky0, kx0;
+  if (MODE == kTapMajor) {
+    const int tap = (int)fdiv((uint32_t)qw0, a.div_c);
+    c0 = qw0 - tap * a.C;
+    ky0 = (int)fdiv((uint32_t)tap, a.div_ks);
+    kx0 = tap - ky0 * KS;
+  } else {
+    c0 = (int)fdiv((uint32_t)qw0, a.div_kk);
+    const int r0 = qw0 - c0 * KS * KS;
+    ky0 = (int)fdiv((uint32_t)r0, a.div_ks);
+    kx0 = r0 - ky0 * KS;
+  }
 
   float ra[AR], rb[BR];
   auto gload = [&](int k0) {
     const int k = k0 + lane;
     const bool kval = k < kend;
-    int64_t gbase = 0, xbase = 0;
+    uint32_t gbase = kOOB, xbase = kOOB;
     int iy0 = -(1 << 28), ix0 = -(1 << 28);
     if (kval) {
       const uint32_t n = fdiv((uint32_t)k, a.div_ohw), r = (uint32_t)k - n * (uint32_t)ohw;
       const uint32_t oy = fdiv(r, a.div_ow), ox = r - oy * (uint32_t)a.OW;
-      gbase = (int64_t)n * P * ohw + r;
+      gbase = (uint32_t)(((int)n * P * ohw + (int)r) * 4);
       iy0 = (int)oy * a.S - a.PAD;
       ix0 = (int)ox * a.S - a.PAD;
-      xbase = (int64_t)n * a.C * HW + iy0 * W + ix0;
+      xbase = (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
     }
 #pragma unroll
-    for (int i = 0; i < AR; ++i) {
-      const int p = p0 + wave + 4 * i;
-      ra[i] = (kval && p < P) ? a.gy[gbase + (int64_t)p * ohw] : 0.f;
+    for (int i = 0; i < AR; ++i) ra[i] = (pw0 + i < P) ? bload(gr, gbase, (uint32_t)((pw0 + i) * ohw * 4)) : 0.f;
+    if (MODE == kTapMajor) {
+      const bool ok = (unsigned)(iy0 + ky0) < (unsigned)H && (unsigned)(ix0 + kx0) < (unsigned)W;
+      const uint32_t voff = ok ? xbase + (uint32_t)((ky0 * W + kx0) * 4) : kOOB;
+#pragma unroll
+      for (int j = 0; j < BR; ++j) rb[j] = (qw0 < Q) ? bload(xr, voff, (uint32_t)((c0 + j) * HW * 4)) : 0.f;
+      return;
     }
+    int c = c0, ky = ky0, kx = kx0;
 #pragma unroll
     for (int j = 0; j < BR; ++j) {
-      const int q = q0 + wave + 4 * j;  // wave-uniform tap column (c, ky, kx)
-      const uint32_t c = fdiv((uint32_t)q, a.div_kk), rr = (uint32_t)q - c * (uint32_t)(a.KS * a.KS);
-      const uint32_t ky = fdiv(rr, a.div_ks), kx = rr - ky * (uint32_t)a.KS;
-      const int iy = iy0 + (int)ky, ix = ix0 + (int)kx;
       float v = 0.f;
-      if (q < Q && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
-        v = a.x[xbase + (int64_t)c * HW + (int)ky * W + (int)kx];
+      if (qw0 + j < Q) {
+        const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
+        v = bload(xr, ok ? xbase + (uint32_t)((c * HW + ky * W + kx) * 4) : kOOB, 0);
+      }
       rb[j] = v;
+      if (++kx == KS) {
+        kx = 0;
+        if (++ky == KS) {
+          ky = 0;
+          ++c;
+        }
+      }
     }
   };
   auto sstore = [&]() {
 #pragma unroll
-    for (int i = 0; i < AR; ++i) As[lane * LA + wave + 4 * i] = ra[i];
+    for (int i = 0; i < AR; ++i) As[(wave * AR + i) * PK + lane] = ra[i];
 #pragma unroll
-    for (int j = 0; j < BR; ++j) Bs[lane * LB + wave + 4 * j] = rb[j];
+    for (int j = 0; j < BR; ++j) Bs[(wave * BR + j) * PK + lane] = rb[j];
   };
 
   omt_f32x4 acc[TI][TJ];
@@ -278,33 +346,42 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
     sstore();
     __syncthreads();
     if (k0 + BK < kend) gload(k0 + BK);
-#pragma unroll 4
-    for (int s = 0; s < BK / 4; ++s) {
-      const int kr = grp * (BK / 4) + s;
-      float av[TI], bv[TJ];
 #pragma unroll
-      for (int i = 0; i < TI; ++i) av[i] = As[kr * LA + la + 16 * i];
+    for (int m = 0; m < BK / 16; ++m) {
+      const int kc = grp * (BK / 4) + 4 * m;  // this lane group's next four K-indices
+      float4 av[TI], bv[TJ];
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) bv[j] = Bs[kr * LB + lb + 16 * j];
+      for (int i = 0; i < TI; ++i) av[i] = *reinterpret_cast<const float4*>(&As[(la + 16 * i) * PK + kc]);
 #pragma unroll
-      for (int i = 0; i < TI; ++i)
+      for (int j = 0; j < TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(&Bs[(lb + 16 * j) * PK + kc]);
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
     }
     __syncthreads();
   }
 
+  // store in the [co][ci][ky][kx] order of the weight gradient (tap-major columns are permuted back)
   float* out = a.out + (int64_t)blockIdx.z * P * Q;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int q = q0 + wq * WQ + 16 * j + (lane & 15);
     if (q >= Q) continue;
+    int col = q;
+    if (MODE == kTapMajor) {
+      const int tap = (int)fdiv((uint32_t)q, a.div_c);
+      col = (q - tap * a.C) * KS * KS + tap;
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
-        if (p < P) out[(int64_t)p * Q + q] = acc[i][j][r4];
+        if (p < P) out[(int64_t)p * Q + col] = acc[i][j][r4];
       }
   }
 }
@@ -327,6 +404,7 @@ struct PackArgs {
   const float* w;
   float* out;
   int CO, CI, KS, S, nphase;
+  int tap_major;  // 1: W'[ci][a'][b'][co], else W'[ci][co][a'][b']
   PackPhase ph[kMaxPhases];
 };
 __global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs a) {
@@ -337,9 +415,21 @@ __global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs 
     const PackPhase& p = a.ph[f];
     const int jj = p.jy * p.jx, kph = a.CO * jj;
     const int r = e - p.woff;
-    const int ci = r / kph, rem = r % kph, co = rem / jj, tap = rem % jj, ap = tap / p.jx, bp = tap % p.jx;
+    const int ci = r / kph, rem = r % kph;
+    const int co = a.tap_major ? rem % a.CO : rem / jj, tap = a.tap_major ? rem / a.CO : rem % jj;
+    const int ap = tap / p.jx, bp = tap % p.jx;
     const int ky = p.ky0 + a.S * (p.jy - 1 - ap), kx = p.kx0 + a.S * (p.jx - 1 - bp);
     a.out[e] = a.w[((co * a.CI + ci) * a.KS + ky) * a.KS + kx];
+  }
+}
+
+// Forward weights in tap-major order: wt[co][ky][kx][ci] = w[co][ci][ky][kx].
+__global__ void __launch_bounds__(256) pack_tapmajor_kernel(const float* __restrict__ w, float* __restrict__ out,
+                                                            int co, int ci, int kk) {
+  const int total = co * ci * kk;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const int o = e / (kk * ci), r = e - o * kk * ci, tap = r / ci, c = r - tap * ci;
+    out[e] = w[(o * ci + c) * kk + tap];
   }
 }
 
@@ -376,7 +466,7 @@ __global__ void __launch_bounds__(256) fold_bn_kernel(int co, int per_out, const
   }
 }
 
-// ---- tile selection ---------------------------------------------------------------------------------------------
+// ---- tile selection and launch ----------------------------------------------------------------------------------
 
 struct Tile {
   int bp, bq, wp, wq;
@@ -412,27 +502,31 @@ static const Tile kWgradTiles[] = {
 
 constexpr int64_t kCUs = 256;
 
-template <int BP, int BQ, int WP, int WQ>
-static void gather_launch(const GatherArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((conv_gather_kernel<BP, BQ, WP, WQ>), grid, dim3(256), 0, s, a);
+template <int MODE, bool BN>
+static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
+  switch (ti) {
+    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, MODE, BN>), grid, dim3(256), 0, s, a); break;
+  }
 }
-template <int BP, int BQ, int WP, int WQ>
-static void wgrad_launch(const WgradArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((conv_wgrad_kernel<BP, BQ, WP, WQ>), grid, dim3(256), 0, s, a);
-}
+
+// Tap-major order needs whole K-blocks of channels; the BN loader keeps the channel-major order.
+static bool gather_tap_major(int64_t c, bool bn) { return !bn && c % 16 == 0; }
 
 static int run_gather(const GatherArgs& a, int64_t maxq, hipStream_t s) {
   const int ti = pick_tile(kGatherTiles, a.P, maxq, a.nphase, kCUs * 2);
   const Tile& tl = kGatherTiles[ti];
   dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)a.nphase);
-  switch (ti) {
-    case 0: gather_launch<64, 256, 64, 64>(a, grid, s); break;
-    case 1: gather_launch<128, 128, 64, 64>(a, grid, s); break;
-    case 2: gather_launch<64, 128, 32, 64>(a, grid, s); break;
-    case 3: gather_launch<32, 256, 32, 64>(a, grid, s); break;
-    case 4: gather_launch<16, 256, 16, 64>(a, grid, s); break;
-    default: gather_launch<64, 64, 32, 32>(a, grid, s); break;
-  }
+  if (a.bn_mean)
+    gather_dispatch<kGeneric, true>(ti, a, grid, s);
+  else if (gather_tap_major(a.C, a.bn_mean != nullptr))
+    gather_dispatch<kTapMajor, false>(ti, a, grid, s);
+  else
+    gather_dispatch<kGeneric, false>(ti, a, grid, s);
   return launch_check("conv_gather_kernel");
 }
 
@@ -442,12 +536,10 @@ static bool dense_geo_ok(const omt_conv_geo* g) {
          g->oh == (g->ih + 2 * g->pad - g->ks) / g->stride + 1 && g->ow == (g->iw + 2 * g->pad - g->ks) / g->stride + 1;
 }
 
-// int32 index math inside the kernels: every tensor and GEMM extent must stay below 2^31 elements per image-row
-// product used in 32-bit arithmetic.
+// Offsets inside the kernels are 32-bit: every tensor the kernels read or write must stay below 2 GiB.
 static bool fits_i32(const omt_conv_geo* g) {
-  const int64_t lim = (int64_t)1 << 31;
-  return g->n * g->oh * g->ow < lim && g->n * g->ih * g->iw < lim && g->ci * g->ih * g->iw < lim &&
-         g->co * g->oh * g->ow < lim && g->co * g->ci * g->ks * g->ks < lim;
+  return g->n * g->ci * g->ih * g->iw * 4 <= kMaxBufBytes && g->n * g->co * g->oh * g->ow * 4 <= kMaxBufBytes &&
+         g->co * g->ci * g->ks * g->ks * 4 <= kMaxBufBytes;
 }
 
 // Wgrad split: about four waves of workgroups per CU over the tiles, each slice at least four K-blocks long.
@@ -469,23 +561,51 @@ static WgradPlan wgrad_plan(const omt_conv_geo* g) {
   return {ti, slices, kslice};
 }
 
+template <int MODE>
+static void wgrad_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s) {
+  switch (ti) {
+    case 0: hipLaunchKernelGGL((conv_wgrad_kernel<64, 128, 32, 64, MODE>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_wgrad_kernel<128, 64, 32, 64, MODE>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_wgrad_kernel<64, 64, 32, 32, MODE>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_wgrad_kernel<32, 128, 16, 64, MODE>), grid, dim3(256), 0, s, a); break;
+  }
+}
+
 }  // namespace omt
 
 using namespace omt;
 
+OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
+  if (!g || g->ks == 1 || !gather_tap_major(g->ci, false)) return 0;
+  return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+}
+
 OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
                             unsigned epilogue, const float* bn_mean, const float* bn_var, const float* bn_gamma,
-                            const float* bn_beta, float bn_eps, float* y, void* stream) {
+                            const float* bn_beta, float bn_eps, float* y, void* workspace, size_t workspace_bytes,
+                            void* stream) {
   if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd: null pointer");
   if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: geometry not covered (ks 1..11, stride 1..4, pad 0..ks)");
-  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: tensor too large for 32-bit indexing");
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: a tensor of 2 GiB or more");
   const bool bn = bn_mean || bn_var || bn_gamma || bn_beta;
   if (bn && !(bn_mean && bn_var && bn_gamma && bn_beta))
     return fail(OMT_INVALID, "omt_conv_fwd: BN loader needs mean, var, gamma and beta");
   if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd: bias epilogue without bias");
+  hipStream_t s = stream_of(stream);
   GatherArgs a{};
   a.x = x;
   a.w = w;
+  // tap-major order: re-pack the filter to [co][ky][kx][ci] (1x1 filters already are)
+  if (!bn && g->ks > 1 && gather_tap_major(g->ci, false)) {
+    const size_t need = omt_conv_fwd_workspace(g);
+    if (!workspace || workspace_bytes < need)
+      return fail(OMT_INVALID, "omt_conv_fwd: workspace of %zu bytes needed", need);
+    const int total = (int)(g->co * g->ci * g->ks * g->ks);
+    hipLaunchKernelGGL(pack_tapmajor_kernel, dim3(grid1d(total, 256, 4096)), dim3(256), 0, s, w, (float*)workspace,
+                       (int)g->co, (int)g->ci, (int)(g->ks * g->ks));
+    if (int st = launch_check("pack_tapmajor_kernel")) return st;
+    a.w = (const float*)workspace;
+  }
   a.bias = (epilogue & OMT_EPI_BIAS) ? bias : nullptr;
   a.bn_mean = bn ? bn_mean : nullptr;
   a.bn_var = bn_var;
@@ -494,6 +614,8 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   a.bn_eps = bn_eps;
   a.relu = (epilogue & OMT_EPI_RELU) ? 1 : 0;
   a.y = y;
+  a.x_bytes = (uint32_t)(g->n * g->ci * g->ih * g->iw * 4);
+  a.w_bytes = (uint32_t)(g->co * g->ci * g->ks * g->ks * 4);
   a.C = (int)g->ci;
   a.H = (int)g->ih;
   a.W = (int)g->iw;
@@ -516,7 +638,8 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   p.div_ow = make_fastdiv((uint32_t)g->ow);
   p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   p.div_kw = make_fastdiv((uint32_t)g->ks);
-  return run_gather(a, p.Q, stream_of(stream));
+  a.div_c = make_fastdiv((uint32_t)a.C);
+  return run_gather(a, p.Q, s);
 }
 
 // Stride-phase table of the grad-input GEMMs (see the top of this file).
@@ -567,7 +690,7 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
                               size_t workspace_bytes, void* stream) {
   if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad: null pointer");
   if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: geometry not covered");
-  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: tensor too large for 32-bit indexing");
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: a tensor of 2 GiB or more");
   if (!workspace || workspace_bytes < omt_conv_dgrad_workspace(g))
     return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", omt_conv_dgrad_workspace(g));
   hipStream_t s = stream_of(stream);
@@ -581,17 +704,21 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   pk.CI = (int)g->ci;
   pk.KS = (int)g->ks;
   pk.S = (int)g->stride;
+  pk.tap_major = gather_tap_major(g->co, false) ? 1 : 0;
   hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
   if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
   a.x = gy;
   a.w = (const float*)workspace;
   a.y = gx;
+  a.x_bytes = (uint32_t)(g->n * g->co * g->oh * g->ow * 4);
+  a.w_bytes = (uint32_t)(packed * 4);
   a.C = (int)g->co;
   a.H = (int)g->oh;
   a.W = (int)g->ow;
   a.P = (int)g->ci;
   a.YH = (int)g->ih;
   a.YW = (int)g->iw;
+  a.div_c = make_fastdiv((uint32_t)a.C);
   return run_gather(a, maxq, s);
 }
 
@@ -606,7 +733,7 @@ OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float
                               size_t workspace_bytes, void* stream) {
   if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
   if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: geometry not covered");
-  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: tensor too large for 32-bit indexing");
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: a tensor of 2 GiB or more");
   const size_t need = omt_conv_wgrad_workspace(g);
   if (need && (!workspace || workspace_bytes < need))
     return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
@@ -616,6 +743,8 @@ OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float
   a.x = x;
   a.gy = gy;
   a.out = pl.slices > 1 ? (float*)workspace : gw;
+  a.x_bytes = (uint32_t)(g->n * g->ci * g->ih * g->iw * 4);
+  a.gy_bytes = (uint32_t)(g->n * g->co * g->oh * g->ow * 4);
   a.C = (int)g->ci;
   a.H = (int)g->ih;
   a.W = (int)g->iw;
@@ -632,14 +761,13 @@ OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float
   a.div_ow = make_fastdiv((uint32_t)g->ow);
   a.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   a.div_ks = make_fastdiv((uint32_t)g->ks);
+  a.div_c = make_fastdiv((uint32_t)g->ci);
   const Tile& tl = kWgradTiles[pl.tile];
   dim3 grid((unsigned)cdiv(a.Q, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)pl.slices);
-  switch (pl.tile) {
-    case 0: wgrad_launch<64, 128, 32, 64>(a, grid, s); break;
-    case 1: wgrad_launch<128, 64, 32, 64>(a, grid, s); break;
-    case 2: wgrad_launch<64, 64, 32, 32>(a, grid, s); break;
-    default: wgrad_launch<32, 128, 16, 64>(a, grid, s); break;
-  }
+  if (g->ci % (kWgradTiles[pl.tile].bq / 4) == 0)
+    wgrad_dispatch<kTapMajor>(pl.tile, a, grid, s);
+  else
+    wgrad_dispatch<kGeneric>(pl.tile, a, grid, s);
   if (int st = launch_check("conv_wgrad_kernel")) return st;
   if (pl.slices > 1) {
     const int64_t n = (int64_t)a.P * a.Q;

@@ -60,7 +60,8 @@ SIGNATURES = {
     "omt_event_query": (I32, [VP]),
     "omt_event_sync": (I32, [VP]),
     "omt_event_elapsed_ms": (I32, [VP, VP, ctypes.POINTER(F32)]),
-    "omt_conv_fwd": (I32, [G, VP, VP, VP, U32, VP, VP, VP, VP, F32, VP, VP]),
+    "omt_conv_fwd_workspace": (SZ, [G]),
+    "omt_conv_fwd": (I32, [G, VP, VP, VP, U32, VP, VP, VP, VP, F32, VP, VP, SZ, VP]),
     "omt_conv_dgrad_workspace": (SZ, [G]),
     "omt_conv_dgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_workspace": (SZ, [G]),
@@ -84,7 +85,7 @@ SIGNATURES = {
     "omt_adapool_bwd": (I32, [I64] * 5 + [VP, VP, VP]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def _load():

@@ -62,8 +62,9 @@ def conv2d(x, w, bias=None, stride=1, padding=0, relu=False, bn=None, bn_eps=1e-
     y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32)
     bnp = [None] * 4 if bn is None else [_need(t, "bn", 1) for t in bn]
     epi = (_lib.OMT_EPI_BIAS if bias is not None else 0) | (_lib.OMT_EPI_RELU if relu else 0)
+    ws, nb = _workspace(L.omt_conv_fwd_workspace(ctypes.byref(g)) if bn is None else 0, x.device)
     check(L.omt_conv_fwd(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(bias), epi, *[_ptr(t) for t in bnp], bn_eps,
-                         _ptr(y), _stream(x.device)), "conv2d")
+                         _ptr(y), _ptr(ws), nb, _stream(x.device)), "conv2d")
     return y
 
 

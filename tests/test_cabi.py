@@ -54,16 +54,20 @@ def test_host_validation_statuses():
     L = _lib.L
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     g = _lib.ConvGeo(2, 3, 4, 8, 8, 1, 1, 12, 1, 0)  # ks 12
-    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, None, None, None, None, 1e-5, fake, None) == \
+    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, None, None, None, None, 1e-5, fake, None, 0, None) == \
         _lib.OMT_UNSUPPORTED
     assert b"geometry" in L.omt_last_error()
     g = _lib.conv_geo(2, 3, 4, 8, 8, 3, 1, 1)
-    assert L.omt_conv_fwd(ctypes.byref(g), None, fake, None, 0, None, None, None, None, 1e-5, fake, None) == \
+    assert L.omt_conv_fwd(ctypes.byref(g), None, fake, None, 0, None, None, None, None, 1e-5, fake, None, 0, None) == \
         _lib.OMT_INVALID
     assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, _lib.OMT_EPI_BIAS, None, None, None, None, 1e-5, fake,
-                          None) == _lib.OMT_INVALID
-    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, fake, None, None, None, 1e-5, fake, None) == \
+                          None, 0, None) == _lib.OMT_INVALID
+    assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, fake, None, None, None, 1e-5, fake, None, 0, None) == \
         _lib.OMT_INVALID  # partial BN loader
+    g64 = _lib.conv_geo(2, 64, 8, 8, 8, 3, 1, 1)  # tap-major order: the re-packed filter needs a workspace
+    assert L.omt_conv_fwd_workspace(ctypes.byref(g64)) == 8 * 64 * 9 * 4
+    assert L.omt_conv_fwd(ctypes.byref(g64), fake, fake, None, 0, None, None, None, None, 1e-5, fake, None, 0, None) \
+        == _lib.OMT_INVALID
     g.oh = 99  # inconsistent geometry
     assert L.omt_conv_wgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
     g = _lib.conv_geo(2, 3, 4, 8, 8, 3, 2, 1)
