@@ -130,6 +130,26 @@ def torch_cpu_baseline(layers, batch, threads):
                       f"at batch {batch}, {cpu_info()}"}
 
 
+def pmc_probe(layers, dev):
+    """A 1 GiB device-to-device copy (1 GiB read + 1 GiB written: the FETCH_SIZE / WRITE_SIZE calibration launch),
+    then one forward conv per layer, each on its own freshly written input."""
+    import torch
+
+    from omarchy_mac_torch import hip_ops
+
+    src = torch.ones(256 * 1024 * 1024, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    for (name, n, c, k, h, ks, s, p) in layers:
+        x = torch.randn((n, c, h, h), device=dev)
+        w = torch.randn((k, c, ks, ks), device=dev) * (c * ks * ks) ** -0.5
+        hip_ops.conv2d(x, w, None, s, p)
+        torch.cuda.synchronize()
+    print("pmc probe done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +157,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", choices=["c5", "c1"], default="c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
+                         "launch per layer; prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
@@ -149,6 +172,9 @@ def main():
 
     dev = torch.device("cuda:0")
     layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
+    if args.pmc_probe:
+        pmc_probe(layers, dev)
+        return
     gen = torch.Generator(device=dev).manual_seed(0)
     data = []
     for (name, n, c, k, h, ks, s, p) in layers:
