@@ -1,10 +1,12 @@
-"""Builds libomt_hip.so (the C-ABI HIP library) from csrc/ for gfx950 with hipcc, in-tree.
+"""Builds, in-tree, the two native pieces of the package:
 
-    python omarchy-mac-torch_amd/build_native.py [--jobs N] [--verbose]
+  1. libomt_hip.so, the C-ABI HIP library (csrc/, hipcc for gfx950, no torch headers: include/omt_hip.h);
+  2. _native, the torch extension that registers the "omarchy_mac_torch" PrivateUse1 device on top of it
+     (torch_ext/, host C++ against the installed torch-ROCm, linked to libomt_hip.so).
 
-Every translation unit compiles to an object under _build/ in parallel, then links into
-omarchy_mac_torch/libomt_hip.so next to the Python package that loads it. No torch headers are involved: the library's
-ABI is plain C (include/omt_hip.h).
+    python omarchy-mac-torch_amd/build_native.py [--jobs N] [--verbose] [--lib-only]
+
+Objects go to _build/; both shared objects land in omarchy_mac_torch/ next to the Python package that loads them.
 """
 
 import argparse
@@ -63,7 +65,8 @@ def build(jobs=None, verbose=False):
     with cf.ThreadPoolExecutor(max_workers=jobs or min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: compile_one(s, verbose), srcs))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp)] + [str(o) for o in objs]
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-Wl,-soname,libomt_hip.so", "-o", str(tmp)] + \
+        [str(o) for o in objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -73,9 +76,44 @@ def build(jobs=None, verbose=False):
     return LIB
 
 
+TORCH_EXT = HERE / "torch_ext"
+
+
+def build_torch_ext(verbose=False):
+    """Compiles torch_ext/*.cpp with torch's extension toolchain into omarchy_mac_torch/_native.so."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    import ctypes
+
+    ctypes.CDLL(str(LIB), mode=ctypes.RTLD_GLOBAL)  # the build's import check resolves libomt_hip.so by SONAME
+    tlib = pathlib.Path(torch.__file__).resolve().parent / "lib"
+    bdir = BUILD / "torch_ext"
+    bdir.mkdir(parents=True, exist_ok=True)
+    ce.load(
+        name="_native",
+        sources=sorted(str(p) for p in TORCH_EXT.glob("*.cpp")),
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1", "-Wno-unused-function"],
+        extra_include_paths=[str(ROOT / "include"), str(TORCH_EXT), "/opt/rocm/include"],
+        extra_ldflags=[f"-L{tlib}", "-lc10_hip", "-ltorch_hip", "-lamdhip64", f"-L{PKG}", "-lomt_hip",
+                       "-Wl,-rpath,\\$$ORIGIN"],
+        build_directory=str(bdir),
+        verbose=verbose,
+        is_python_module=True,
+    )
+    out = PKG / "_native.so"
+    tmp = out.with_suffix(".so.tmp")
+    shutil.copyfile(bdir / "_native.so", tmp)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--lib-only", action="store_true", help="build libomt_hip.so only")
     args = ap.parse_args()
     print(build(args.jobs, args.verbose))
+    if not args.lib_only:
+        print(build_torch_ext(args.verbose))

@@ -7,6 +7,8 @@ anywhere but the HIP kernels.
 import ctypes
 import pathlib
 
+import torch  # noqa: F401  (loads torch's HIP runtime first; libomt_hip.so then binds to the same libamdhip64.so.7)
+
 _HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = _HERE / "libomt_hip.so"
 
@@ -115,7 +117,6 @@ def check(status, what=""):
     if status == OMT_UNSUPPORTED:
         raise Unsupported(status, msg)
     if status == OMT_OOM:
-        import torch
         raise torch.OutOfMemoryError(msg)
     raise OmtError(status, msg)
 

@@ -1,0 +1,144 @@
+"""Loads the torch extension (_native) and registers the "omarchy_mac_torch" PrivateUse1 device with PyTorch, as the
+reference's omarchy_mac_torch/native.py does (device module, generated tensor/module methods, FALLBACKS).
+
+The device's memory is HBM on the MI355X, allocated by libomt_hip.so. Its convolution hot path runs that library's
+HIP kernels; every other op is delegated to torch's own HIP kernels on the same memory. Both native libraries are
+required: a missing build raises ImportError instead of running anything elsewhere.
+"""
+
+import os
+import pathlib
+import types
+
+import torch
+
+from omarchy_mac_torch import _lib  # noqa: F401  (loads libomt_hip.so before the extension that links it)
+
+_HERE = pathlib.Path(__file__).resolve().parent
+DEVICE = "omarchy_mac_torch"
+
+
+def _check_build():
+    if not (_HERE / "_native.so").exists():
+        raise ImportError("omarchy-mac-torch: the torch extension is not built; run "
+                          "`python omarchy-mac-torch_amd/build_native.py` (or __graft_entry__.build())")
+
+
+_check_build()
+from omarchy_mac_torch import _native as core  # noqa: E402
+
+if core.built_with_torch.split("+")[0] != torch.__version__.split("+")[0]:
+    raise ImportError(f"omarchy-mac-torch was built against torch {core.built_with_torch} but torch "
+                      f"{torch.__version__} is installed; rebuild with omarchy-mac-torch_amd/build_native.py")
+
+if torch._C._get_privateuse1_backend_name() != DEVICE:
+    torch.utils.rename_privateuse1_backend(DEVICE)
+    # tensor.omarchy_mac_torch(), module.omarchy_mac_torch(), storage methods, is_omarchy_mac_torch
+    torch.utils.generate_methods_for_privateuse1_backend(for_tensor=True, for_module=True, for_packed_sequence=True,
+                                                         for_storage=True)
+
+core.set_fold(int(os.environ.get("OMARCHY_MAC_TORCH_FOLD", "1")))
+core.set_debug(os.environ.get("OMARCHY_MAC_TORCH_DEBUG", "0") == "1")
+
+
+# ---- the device module: torch.omarchy_mac_torch.* ----
+_mod = types.ModuleType("torch." + DEVICE)
+_mod.is_available = lambda: torch.cuda.is_available()
+_mod.is_initialized = lambda: True
+_mod._lazy_init = lambda: None
+_mod._is_in_bad_fork = lambda: False
+_mod.device_count = lambda: 1
+_mod.current_device = lambda: 0
+_mod.set_device = lambda d: None
+_mod.get_amp_supported_dtype = lambda: [torch.float32]
+_mod.synchronize = lambda device=None: core.sync()
+_mod.empty_cache = core.empty_cache
+_mod.memory_allocated = lambda device=None: core.memory_allocated()
+_mod.memory_reserved = lambda device=None: core.memory_reserved()
+# random numbers come from torch's HIP generator (the device's RNG ops run on torch's HIP kernels)
+_mod.manual_seed = lambda seed: torch.cuda.manual_seed(int(seed))
+_mod.manual_seed_all = lambda seed: torch.cuda.manual_seed_all(int(seed))
+_mod.seed = lambda: torch.cuda.seed()
+_mod.seed_all = lambda: torch.cuda.seed_all()
+_mod.initial_seed = lambda: torch.cuda.initial_seed()
+_mod.get_rng_state = lambda device=None: torch.cuda.get_rng_state()
+_mod.set_rng_state = lambda state, device=None: torch.cuda.set_rng_state(state)
+
+
+class _DeviceContext:
+    def __init__(self, device):
+        pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+_mod.device = _DeviceContext
+if not hasattr(torch, DEVICE):
+    torch._register_device_module(DEVICE, _mod)
+
+
+def synchronize():
+    core.sync()
+
+
+def set_queue_depth(depth=3, chunk=64):
+    """Kept for the reference's API (it bounded its Vulkan submission queue). HIP streams are already asynchronous
+    and the driver bounds them, so there is nothing to configure."""
+    return None
+
+
+def empty_cache():
+    core.empty_cache()
+
+
+def memory_allocated():
+    return core.memory_allocated()
+
+
+def memory_reserved():
+    return core.memory_reserved()
+
+
+def validate_kernels():
+    """The reference compiled WGSL at run time; here every kernel is compiled ahead of time for gfx950. Returns the
+    failures: always none once the library has loaded."""
+    return []
+
+
+class _Fallbacks:
+    """Hot-path ops that could not run on the HIP kernels, with why: {"op (reason)": count}. Read-only mapping view.
+    (They ran on torch's HIP kernels instead.)"""
+
+    def _d(self):
+        return core.fallback_counts()
+
+    def keys(self):
+        return self._d().keys()
+
+    def items(self):
+        return self._d().items()
+
+    def __getitem__(self, k):
+        return self._d()[k]
+
+    def __iter__(self):
+        return iter(self._d())
+
+    def __len__(self):
+        return len(self._d())
+
+    def __bool__(self):
+        return bool(self._d())
+
+    def clear(self):
+        core.reset_fallbacks()
+
+    def __repr__(self):
+        return repr(self._d())
+
+
+FALLBACKS = _Fallbacks()

@@ -1,0 +1,47 @@
+// Python bindings (omarchy_mac_torch._native). Reference counterpart: csrc/module.cpp:15-63.
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+#include <torch/extension.h>
+
+#include "omt_torch.h"
+
+namespace omt {
+void bind_plans(pybind11::module_& m);
+}
+
+PYBIND11_MODULE(_native, m) {
+  using namespace omt;
+  m.def("sync", []() {
+    TORCH_CHECK(omt_stream_sync(cur_stream()) == OMT_OK, "omarchy-mac-torch: ", omt_last_error());
+  });
+  m.def("empty_cache", []() {
+    OMT_LOCK;
+    TORCH_CHECK(omt_empty_cache() == OMT_OK, "omarchy-mac-torch: ", omt_last_error());
+  });
+  m.def("memory_allocated", []() { return (int64_t)omt_memory_allocated(); });
+  m.def("memory_reserved", []() { return (int64_t)omt_memory_reserved(); });
+  m.def("set_memory_limit", [](int64_t bytes) { omt_set_memory_limit((size_t)std::max<int64_t>(bytes, 0)); });
+  m.def("fallback_counts", []() {
+    OMT_LOCK;
+    return fallback_counts();
+  });
+  m.def("reset_fallbacks", []() {
+    OMT_LOCK;
+    fallback_counts().clear();
+  });
+  m.def("delegated_counts", []() {
+    OMT_LOCK;
+    return delegated_counts();
+  });
+  m.def("count_delegated", [](bool on) {
+    OMT_LOCK;
+    set_count_delegated(on);
+    if (!on) delegated_counts().clear();
+  });
+  m.def("set_debug", [](bool on) { set_debug_mode(on); });
+  m.def("strict", []() { return strict_mode(); });
+  m.def("abi_version", []() { return omt_abi_version(); });
+  m.def("hip_runtime_version", []() { return omt_hip_runtime_version(); });
+  m.attr("built_with_torch") = TORCH_VERSION;
+  bind_plans(m);
+}

@@ -1,0 +1,424 @@
+// Hot-path operators of the device, each a thin host wrapper over libomt_hip.so's C ABI:
+//   aten::convolution / convolution_backward            reference csrc/conv.cpp:179-237
+//   aten::native_batch_norm / native_batch_norm_backward reference csrc/nn.cpp:25-78
+//   aten::_native_batch_norm_legit{,_no_training}       reference csrc/fused.cpp:173-181, 234-237
+//   aten::max_pool2d_with_indices(_backward), avg_pool2d(_backward), _adaptive_avg_pool2d(_backward)
+//                                                        reference csrc/nn.cpp:157-222, 275-285
+//   omt::bn_relu_train, bn_relu_backward, conv_act, conv_bn_act_eval (composite references + device kernels)
+//                                                        reference csrc/fused.cpp:19-136, 213-233
+// Cases a kernel does not cover fail a NEED() and run on torch's HIP kernels instead, recorded in FALLBACKS.
+#include "omt_torch.h"
+
+namespace omt {
+
+static Tensor contig(const Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
+static bool whole(const Tensor& t) { return f32(t) && t.is_contiguous(); }
+static void need_dev(const Tensor& t, const char* what) { NEED(!t.defined() || is_dev(t), what); }
+
+// ------------------------------------------------------------------------------------------------------------------
+// convolution
+// ------------------------------------------------------------------------------------------------------------------
+
+static int kind_of(const Tensor& x, const Tensor& w, IntArrayRef stride, IntArrayRef padding, IntArrayRef dilation,
+                   bool transposed, int64_t groups) {
+  if (!f32(x) || !f32(w) || x.dim() != 4 || w.dim() != 4 || stride.size() != 2 || padding.size() != 2 ||
+      dilation.size() != 2)
+    return OMT_CONV_NONE;
+  return omt_conv_kind(x.size(1), w.size(0), w.size(2), w.size(3), stride[0], stride[1], padding[0], padding[1],
+                       dilation[0], dilation[1], transposed ? 1 : 0, groups);
+}
+
+// y = conv(x, w) (+ bias) (+ ReLU for dense convs); shared by convolution and omt::conv_act
+static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::optional<Tensor>& bias, IntArrayRef stride,
+                           IntArrayRef padding, IntArrayRef dilation, bool transposed, int64_t groups, bool relu) {
+  const int kind = kind_of(x_, w_, stride, padding, dilation, transposed, groups);
+  NEED(kind != OMT_CONV_NONE, "dilated, transposed, grouped or non-square convolution");
+  NEED(!defined(bias) || (f32(*bias) && bias->dim() == 1), "float32 bias");
+  NEED(!relu || kind == OMT_CONV_DENSE, "ReLU epilogue on a depthwise convolution");
+  Tensor x = contig(x_), w = contig(w_);
+  Tensor b = defined(bias) ? contig(*bias) : Tensor();
+  omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
+  NEED(g.oh >= 1 && g.ow >= 1, "empty output");
+  Tensor y = empty_dev({g.n, g.co, g.oh, g.ow});
+  if (kind == OMT_CONV_DENSE) {
+    Tensor ws = workspace(omt_conv_fwd_workspace(&g));
+    unsigned epi = (b.defined() ? OMT_EPI_BIAS : 0u) | (relu ? OMT_EPI_RELU : 0u);
+    check(omt_conv_fwd(&g, fp(x), fp(w), fp(b), epi, nullptr, nullptr, nullptr, nullptr, 1e-5f, fpm(y), wsptr(ws),
+                       wsbytes(ws), cur_stream()),
+          "convolution");
+  } else {
+    check(omt_dw_fwd(&g, fp(x), fp(w), fp(b), nullptr, nullptr, nullptr, nullptr, 1e-5f, fpm(y), cur_stream()),
+          "convolution (depthwise)");
+  }
+  return y;
+}
+
+static Tensor convolution_(const Tensor& x, const Tensor& w, const std::optional<Tensor>& bias, IntArrayRef stride,
+                           IntArrayRef padding, IntArrayRef dilation, bool transposed, IntArrayRef, int64_t groups) {
+  return conv_forward(x, w, bias, stride, padding, dilation, transposed, groups, false);
+}
+
+static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy_, const Tensor& x_, const Tensor& w_,
+                                                                at::OptionalIntArrayRef, IntArrayRef stride,
+                                                                IntArrayRef padding, IntArrayRef dilation,
+                                                                bool transposed, IntArrayRef, int64_t groups,
+                                                                std::array<bool, 3> mask) {
+  const int kind = kind_of(x_, w_, stride, padding, dilation, transposed, groups);
+  NEED(kind != OMT_CONV_NONE && f32(gy_), "dilated, transposed, grouped or non-square convolution");
+  Tensor gy = contig(gy_), x = contig(x_), w = contig(w_);
+  omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
+  NEED(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");
+  Tensor gx, gw, gb;
+  void* s = cur_stream();
+  if (kind == OMT_CONV_DENSE) {
+    if (mask[0]) {
+      gx = empty_dev(x.sizes());
+      Tensor ws = workspace(omt_conv_dgrad_workspace(&g));
+      check(omt_conv_dgrad(&g, fp(gy), fp(w), fpm(gx), wsptr(ws), wsbytes(ws), s), "convolution_backward (input)");
+    }
+    if (mask[1]) {
+      gw = empty_dev(w.sizes());
+      Tensor ws = workspace(omt_conv_wgrad_workspace(&g));
+      check(omt_conv_wgrad(&g, fp(x), fp(gy), fpm(gw), wsptr(ws), wsbytes(ws), s), "convolution_backward (weight)");
+    }
+  } else {
+    if (mask[0]) {
+      gx = empty_dev(x.sizes());
+      check(omt_dw_dgrad(&g, fp(gy), fp(w), fpm(gx), s), "convolution_backward (depthwise input)");
+    }
+    if (mask[1]) {
+      gw = empty_dev(w.sizes());
+      Tensor ws = workspace(omt_dw_wgrad_workspace(&g));
+      check(omt_dw_wgrad(&g, fp(x), fp(gy), fpm(gw), wsptr(ws), wsbytes(ws), s), "convolution_backward (depthwise weight)");
+    }
+  }
+  if (mask[2]) {
+    gb = empty_dev({g.co});
+    check(omt_bias_grad(g.n, g.co, g.oh * g.ow, fp(gy), fpm(gb), s), "convolution_backward (bias)");
+  }
+  return {gx, gw, gb};
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// batch norm
+// ------------------------------------------------------------------------------------------------------------------
+
+static std::tuple<Tensor, Tensor, Tensor> batch_norm_(const Tensor& x_, const std::optional<Tensor>& weight,
+                                                      const std::optional<Tensor>& bias,
+                                                      const std::optional<Tensor>& rm,
+                                                      const std::optional<Tensor>& rv, bool training,
+                                                      double momentum, double eps) {
+  NEED(defined(weight) && defined(bias) && defined(rm) && defined(rv) && f32(x_) && x_.dim() == 4,
+       "batch norm without affine parameters or running stats, or not 4-D float32");
+  NEED(whole(*weight) && whole(*bias) && whole(*rm) && whole(*rv), "batch norm parameters must be contiguous float32");
+  Tensor x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor y = empty_dev(x.sizes());
+  if (!training) {
+    check(omt_bn_eval_fwd(n, c, hw, fp(x), fp(weight), fp(bias), fp(rm), fp(rv), eps, 0, fpm(y), cur_stream()),
+          "native_batch_norm (eval)");
+    return {y, empty_dev({0}), empty_dev({0})};
+  }
+  Tensor sm = empty_dev({c}), si = empty_dev({c});
+  Tensor ws = workspace(omt_bn_train_workspace(n, c, hw));
+  float* rmp = rm->mutable_data_ptr<float>();
+  float* rvp = rv->mutable_data_ptr<float>();
+  check(omt_bn_train_fwd(n, c, hw, fp(x), fp(weight), fp(bias), rmp, rvp, momentum, eps, 0, fpm(y), fpm(sm), fpm(si),
+                         rmp, rvp, wsptr(ws), wsbytes(ws), cur_stream()),
+        "native_batch_norm");
+  return {y, sm, si};
+}
+
+static std::tuple<Tensor, Tensor, Tensor> batch_norm_backward_(const Tensor& gy_, const Tensor& x_,
+                                                               const std::optional<Tensor>& weight,
+                                                               const std::optional<Tensor>&,
+                                                               const std::optional<Tensor>&,
+                                                               const std::optional<Tensor>& sm,
+                                                               const std::optional<Tensor>& si, bool train, double,
+                                                               std::array<bool, 3> mask) {
+  NEED(train && defined(weight) && defined(sm) && defined(si) && f32(x_) && f32(gy_) && x_.dim() == 4,
+       "eval-mode or non-affine batch norm backward");
+  NEED(whole(*weight) && whole(*sm) && whole(*si), "contiguous float32 parameters");
+  Tensor gy = contig(gy_), x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
+  Tensor dg = mask[1] ? empty_dev({c}) : Tensor();
+  Tensor db = mask[2] ? empty_dev({c}) : Tensor();
+  Tensor ws = workspace(omt_bn_bwd_workspace(n, c, hw));
+  check(omt_bn_bwd(n, c, hw, fp(gy), fp(x), nullptr, fp(sm), fp(si), fp(weight), fpm(gx), fpm(dg), fpm(db), wsptr(ws),
+                   wsbytes(ws), cur_stream()),
+        "native_batch_norm_backward");
+  return {gx, dg, db};
+}
+
+// eager entry points of the non-functional BatchNorm variants that traced / compiled graphs call
+static std::tuple<Tensor, Tensor, Tensor> bn_legit(const Tensor& x, const std::optional<Tensor>& w,
+                                                   const std::optional<Tensor>& b, Tensor& rm, Tensor& rv,
+                                                   bool training, double mom, double eps) {
+  return batch_norm_(x, w, b, rm, rv, training, mom, eps);
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_legit_no_training(const Tensor& x, const std::optional<Tensor>& w,
+                                                               const std::optional<Tensor>& b, const Tensor& rm,
+                                                               const Tensor& rv, double mom, double eps) {
+  return batch_norm_(x, w, b, rm, rv, false, mom, eps);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// pools
+// ------------------------------------------------------------------------------------------------------------------
+
+struct Pool2 {
+  int64_t kh, kw, sh, sw, ph, pw, dh, dw;
+};
+static Pool2 pool_args(IntArrayRef k, IntArrayRef s, IntArrayRef p, IntArrayRef d) {
+  NEED(k.size() == 1 || k.size() == 2, "kernel size");
+  Pool2 r;
+  r.kh = k[0];
+  r.kw = k.size() == 2 ? k[1] : k[0];
+  r.sh = s.empty() ? r.kh : s[0];
+  r.sw = s.empty() ? r.kw : (s.size() == 2 ? s[1] : s[0]);
+  r.ph = p[0];
+  r.pw = p.size() == 2 ? p[1] : p[0];
+  r.dh = d.empty() ? 1 : d[0];
+  r.dw = d.empty() ? 1 : (d.size() == 2 ? d[1] : d[0]);
+  // PyTorch's own argument checks (and their messages) stay with its kernels
+  NEED(r.kh > 0 && r.kw > 0 && r.sh > 0 && r.sw > 0 && r.dh > 0 && r.dw > 0 && r.ph >= 0 && r.pw >= 0 &&
+           r.ph <= ((r.kh - 1) * r.dh + 1) / 2 && r.pw <= ((r.kw - 1) * r.dw + 1) / 2,
+       "pooling arguments");
+  return r;
+}
+
+static std::tuple<Tensor, Tensor> max_pool2d_(const Tensor& x_, IntArrayRef k, IntArrayRef s, IntArrayRef p,
+                                              IntArrayRef d, bool ceil) {
+  NEED(f32(x_) && x_.dim() == 4, "4-D float32");
+  Pool2 a = pool_args(k, s, p, d);
+  Tensor x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
+  const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, a.dh, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, a.dw, ceil);
+  NEED(oh >= 1 && ow >= 1, "empty output");
+  Tensor y = empty_dev({n, c, oh, ow}), idx = empty_dev({n, c, oh, ow}, at::kLong);
+  check(omt_maxpool_fwd(n * c, ih, iw, oh, ow, a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, a.dh, a.dw, fp(x), fpm(y),
+                        idx.mutable_data_ptr<int64_t>(), cur_stream()),
+        "max_pool2d_with_indices");
+  return {y, idx};
+}
+
+static Tensor max_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayRef k, IntArrayRef s, IntArrayRef p,
+                                   IntArrayRef d, bool, const Tensor& idx_) {
+  NEED(f32(gy_) && x.dim() == 4 && idx_.scalar_type() == at::kLong, "4-D float32");
+  Pool2 a = pool_args(k, s, p, d);
+  Tensor gy = contig(gy_), idx = contig(idx_);
+  const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
+  Tensor gx = empty_dev(x.sizes());
+  check(omt_maxpool_bwd(n * c, ih, iw, gy.size(2), gy.size(3), a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, a.dh, a.dw, fp(gy),
+                        idx.data_ptr<int64_t>(), fpm(gx), cur_stream()),
+        "max_pool2d_with_indices_backward");
+  return gx;
+}
+
+static Tensor avg_pool2d_(const Tensor& x_, IntArrayRef k, IntArrayRef s, IntArrayRef p, bool ceil, bool incl,
+                          std::optional<int64_t> div) {
+  NEED(f32(x_) && x_.dim() == 4, "4-D float32");
+  NEED(!div || *div > 0, "divisor_override");
+  Pool2 a = pool_args(k, s, p, {});
+  NEED(a.ph <= a.kh / 2 && a.pw <= a.kw / 2, "pooling arguments");
+  Tensor x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
+  const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, 1, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, 1, ceil);
+  NEED(oh >= 1 && ow >= 1, "empty output");
+  Tensor y = empty_dev({n, c, oh, ow});
+  check(omt_avgpool_fwd(n * c, ih, iw, oh, ow, a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, incl ? 1 : 0, div.value_or(0), fp(x),
+                        fpm(y), cur_stream()),
+        "avg_pool2d");
+  return y;
+}
+
+static Tensor avg_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayRef k, IntArrayRef s, IntArrayRef p,
+                                   bool, bool incl, std::optional<int64_t> div) {
+  NEED(f32(gy_) && x.dim() == 4, "4-D float32");
+  NEED(!div || *div > 0, "divisor_override");
+  Pool2 a = pool_args(k, s, p, {});
+  Tensor gy = contig(gy_);
+  const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
+  Tensor gx = empty_dev(x.sizes());
+  check(omt_avgpool_bwd(n * c, ih, iw, gy.size(2), gy.size(3), a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, incl ? 1 : 0,
+                        div.value_or(0), fp(gy), fpm(gx), cur_stream()),
+        "avg_pool2d_backward");
+  return gx;
+}
+
+static Tensor adaptive_avg_pool2d_(const Tensor& x_, IntArrayRef out) {
+  NEED(f32(x_) && x_.dim() == 4 && out.size() == 2 && out[0] >= 1 && out[1] >= 1, "4-D float32");
+  Tensor x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1);
+  Tensor y = empty_dev({n, c, out[0], out[1]});
+  check(omt_adapool_fwd(n * c, x.size(2), x.size(3), out[0], out[1], fp(x), fpm(y), cur_stream()),
+        "_adaptive_avg_pool2d");
+  return y;
+}
+
+static Tensor adaptive_avg_pool2d_backward_(const Tensor& gy_, const Tensor& x) {
+  NEED(f32(gy_) && x.dim() == 4, "4-D float32");
+  Tensor gy = contig(gy_);
+  Tensor gx = empty_dev(x.sizes());
+  check(omt_adapool_bwd(x.size(0) * x.size(1), x.size(2), x.size(3), gy.size(2), gy.size(3), fp(gy), fpm(gx),
+                        cur_stream()),
+        "_adaptive_avg_pool2d_backward");
+  return gx;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// omt:: fused ops (the torch.compile backend rewrites graphs to them)
+// ------------------------------------------------------------------------------------------------------------------
+
+// composite references in plain aten ops (csrc/fused.cpp:19-46): any device, and the fallback of the fast paths
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_ref(const Tensor& x, const Tensor& w,
+                                                                          const Tensor& b, const Tensor& rm,
+                                                                          const Tensor& rv, double mom, double eps) {
+  auto r = at::_native_batch_norm_legit_functional(x, w, b, rm, rv, true, mom, eps);
+  return {at::relu(std::get<0>(r)), std::get<1>(r), std::get<2>(r), std::get<3>(r), std::get<4>(r)};
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_ref(const Tensor& g, const Tensor& x, const Tensor& y,
+                                                               const Tensor& w, const Tensor& mean,
+                                                               const Tensor& invstd, std::array<bool, 3> mask) {
+  Tensor gz = at::threshold_backward(g, y, 0);
+  return at::native_batch_norm_backward(gz, x, w, std::nullopt, std::nullopt, mean, invstd, true, 0.0, mask);
+}
+static Tensor conv_act_ref(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
+                           IntArrayRef padding, int64_t act) {
+  Tensor y = at::convolution(x, w, b, stride, padding, {1, 1}, false, {0, 0}, 1);
+  return act == 1 ? at::relu(y) : y;
+}
+static std::pair<Tensor, Tensor> fold_bn_ref(const Tensor& cw, const std::optional<Tensor>& cb, const Tensor& w,
+                                             const Tensor& b, const Tensor& rm, const Tensor& rv, double eps) {
+  Tensor scale = w * at::rsqrt(rv + eps);
+  Tensor fw = cw * scale.view({-1, 1, 1, 1});
+  Tensor fb = (defined(cb) ? (*cb - rm) : -rm) * scale + b;
+  return {fw, fb};
+}
+static Tensor conv_bn_act_eval_ref(const Tensor& x, const Tensor& cw, const std::optional<Tensor>& cb,
+                                   const Tensor& w, const Tensor& b, const Tensor& rm, const Tensor& rv, double eps,
+                                   IntArrayRef stride, IntArrayRef padding, int64_t act) {
+  auto f = fold_bn_ref(cw, cb, w, b, rm, rv, eps);
+  return conv_act_ref(x, f.first, f.second, stride, padding, act);
+}
+
+// device paths
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_dev(const Tensor& x_, const Tensor& w,
+                                                                          const Tensor& b, const Tensor& rm,
+                                                                          const Tensor& rv, double mom, double eps) {
+  NEED(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
+       "4-D float32 with contiguous parameters");
+  Tensor x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor y = empty_dev(x.sizes()), sm = empty_dev({c}), si = empty_dev({c}), nrm = empty_dev({c}), nrv = empty_dev({c});
+  Tensor ws = workspace(omt_bn_train_workspace(n, c, hw));
+  check(omt_bn_train_fwd(n, c, hw, fp(x), fp(w), fp(b), fp(rm), fp(rv), mom, eps, 1, fpm(y), fpm(sm), fpm(si),
+                         fpm(nrm), fpm(nrv), wsptr(ws), wsbytes(ws), cur_stream()),
+        "omt::bn_relu_train");
+  return {y, sm, si, nrm, nrv};
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_, const Tensor& x_, const Tensor& y_,
+                                                               const Tensor& w, const Tensor& mean,
+                                                               const Tensor& invstd, std::array<bool, 3> mask) {
+  NEED(f32(g_) && f32(x_) && f32(y_) && x_.dim() == 4 && whole(w) && whole(mean) && whole(invstd), "4-D float32");
+  Tensor g = contig(g_), x = contig(x_), y = contig(y_);
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
+  Tensor dg = mask[1] ? empty_dev({c}) : Tensor();
+  Tensor db = mask[2] ? empty_dev({c}) : Tensor();
+  Tensor ws = workspace(omt_bn_bwd_workspace(n, c, hw));
+  check(omt_bn_bwd(n, c, hw, fp(g), fp(x), fp(y), fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg), fpm(db), wsptr(ws),
+                   wsbytes(ws), cur_stream()),
+        "omt::bn_relu_backward");
+  return {gx, dg, db};
+}
+static Tensor conv_act_dev(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
+                           IntArrayRef padding, int64_t act) {
+  NEED(stride.size() == 2 && padding.size() == 2, "2-D stride and padding");
+  return conv_forward(x, w, b, stride, padding, {1, 1}, false, 1, act == 1);
+}
+static Tensor conv_bn_act_eval_dev(const Tensor& x, const Tensor& cw_, const std::optional<Tensor>& cb_,
+                                   const Tensor& w, const Tensor& b, const Tensor& rm, const Tensor& rv, double eps,
+                                   IntArrayRef stride, IntArrayRef padding, int64_t act) {
+  NEED(f32(cw_) && cw_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv) && (!defined(cb_) || f32(*cb_)),
+       "float32 parameters");
+  Tensor cw = contig(cw_);
+  Tensor cb = defined(cb_) ? contig(*cb_) : Tensor();
+  const int64_t co = cw.size(0);
+  Tensor fw = empty_dev(cw.sizes()), fb = empty_dev({co});
+  check(omt_fold_bn(co, cw.numel() / co, fp(cw), fp(cb), fp(w), fp(b), fp(rm), fp(rv), (float)eps, fpm(fw), fpm(fb),
+                    cur_stream()),
+        "omt::conv_bn_act_eval (fold)");
+  return conv_act_dev(x, fw, fb, stride, padding, act);
+}
+
+// fast path, else the composite reference (whose aten ops dispatch to the device kernels or are delegated)
+#define TRY_DEV(dev, ref, ...)          \
+  OMT_LOCK;                             \
+  try {                                 \
+    return dev(__VA_ARGS__);            \
+  } catch (const Unsupported& e) {      \
+    TORCH_CHECK(!strict_mode(), "omarchy-mac-torch (strict): " #dev ": ", e.why); \
+    note_fallback(#dev, e.why);         \
+    return ref(__VA_ARGS__);            \
+  }
+
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_k(const Tensor& x, const Tensor& w,
+                                                                        const Tensor& b, const Tensor& rm,
+                                                                        const Tensor& rv, double mom, double eps) {
+  TRY_DEV(bn_relu_train_dev, bn_relu_train_ref, x, w, b, rm, rv, mom, eps)
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_k(const Tensor& g, const Tensor& x, const Tensor& y,
+                                                             const Tensor& w, const Tensor& mean,
+                                                             const Tensor& invstd, std::array<bool, 3> mask) {
+  TRY_DEV(bn_relu_backward_dev, bn_relu_backward_ref, g, x, y, w, mean, invstd, mask)
+}
+static Tensor conv_act_k(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef s,
+                         IntArrayRef p, int64_t act) {
+  TRY_DEV(conv_act_dev, conv_act_ref, x, w, b, s, p, act)
+}
+static Tensor conv_bn_act_eval_k(const Tensor& x, const Tensor& cw, const std::optional<Tensor>& cb, const Tensor& w,
+                                 const Tensor& b, const Tensor& rm, const Tensor& rv, double eps, IntArrayRef s,
+                                 IntArrayRef p, int64_t act) {
+  TRY_DEV(conv_bn_act_eval_dev, conv_bn_act_eval_ref, x, cw, cb, w, b, rm, rv, eps, s, p, act)
+}
+
+TORCH_LIBRARY(omt, m) {
+  m.def("bn_relu_train(Tensor x, Tensor w, Tensor b, Tensor rm, Tensor rv, float momentum, float eps) -> "
+        "(Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("bn_relu_backward(Tensor g, Tensor x, Tensor y, Tensor w, Tensor mean, Tensor invstd, bool[3] mask) -> "
+        "(Tensor, Tensor, Tensor)");
+  m.def("conv_act(Tensor x, Tensor w, Tensor? b, int[] stride, int[] padding, int act) -> Tensor");
+  m.def("conv_bn_act_eval(Tensor x, Tensor cw, Tensor? cb, Tensor w, Tensor b, Tensor rm, Tensor rv, float eps, "
+        "int[] stride, int[] padding, int act) -> Tensor");
+}
+TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
+  m.impl("bn_relu_train", &bn_relu_train_ref);
+  m.impl("bn_relu_backward", &bn_relu_backward_ref);
+  m.impl("conv_act", &conv_act_ref);
+  m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
+}
+TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
+  m.impl("bn_relu_train", &bn_relu_train_k);
+  m.impl("bn_relu_backward", &bn_relu_backward_k);
+  m.impl("conv_act", &conv_act_k);
+  m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);
+}
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  OMT_IMPL(m, convolution, convolution_);
+  OMT_IMPL(m, convolution_backward, convolution_backward_);
+  OMT_IMPL(m, native_batch_norm, batch_norm_);
+  OMT_IMPL(m, native_batch_norm_backward, batch_norm_backward_);
+  OMT_IMPL(m, _native_batch_norm_legit, bn_legit);
+  OMT_IMPL(m, _native_batch_norm_legit_no_training, bn_legit_no_training);
+  OMT_IMPL(m, max_pool2d_with_indices, max_pool2d_);
+  OMT_IMPL(m, max_pool2d_with_indices_backward, max_pool2d_backward_);
+  OMT_IMPL(m, avg_pool2d, avg_pool2d_);
+  OMT_IMPL(m, avg_pool2d_backward, avg_pool2d_backward_);
+  OMT_IMPL(m, _adaptive_avg_pool2d, adaptive_avg_pool2d_);
+  OMT_IMPL(m, _adaptive_avg_pool2d_backward, adaptive_avg_pool2d_backward_);
+}
+
+}  // namespace omt
