@@ -150,13 +150,82 @@ def pmc_probe(layers, dev):
     print("pmc probe done", flush=True)
 
 
+def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
+    """ResNet-18 training step, batch 32, 3x64x64 ~ N(0,1), labels in [0, 1000), BatchNorm in train
+    mode, Adam lr 1e-3, Kaiming init; on the omarchy_mac_torch device and, from the same weights and data, on the
+    host CPU. Returns ms/step on both, the speed-up and the largest relative loss difference over the common steps."""
+    import copy
+
+    import torch
+    import torch.nn.functional as F
+
+    from omarchy_mac_torch import models
+
+    torch.manual_seed(0)
+    base = models.resnet18(1000)
+    g = torch.Generator().manual_seed(1)
+    n_batches = max(warmup + steps, cpu_steps + 1)
+    data = [(torch.randn(32, 3, 64, 64, generator=g), torch.randint(0, 1000, (32,), generator=g))
+            for _ in range(n_batches)]
+
+    def run(model, device, batches, timed_from, dtype=torch.float32):
+        opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+        losses, t0 = [], None
+        for i, (x, t) in enumerate(batches):
+            if i == timed_from:
+                if device != "cpu":
+                    torch.cuda.synchronize()
+                t0 = time.perf_counter()
+            opt.zero_grad(set_to_none=True)
+            loss = F.cross_entropy(model(x.to(dtype)), t)
+            loss.backward()
+            opt.step()
+            losses.append(loss.detach())
+        if device != "cpu":
+            torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / (len(batches) - timed_from) * 1e3
+        return ms, [float(l) for l in losses]
+
+    dev_model = copy.deepcopy(base).to(dev_name)
+    dev_batches = [(x.to(dev_name), t.to(dev_name)) for (x, t) in data[:warmup + steps]]
+    if dev_name != "cpu":
+        torch.cuda.synchronize()
+    dev_ms, dev_losses = run(dev_model, dev_name, dev_batches, warmup)
+    out = {"config": "ResNet-18 b32 3x64x64, 1000 classes, BN train, Adam lr 1e-3 (BASELINE config 3)",
+           "ms_per_step": round(dev_ms, 3), "steps": steps, "warmup": warmup}
+    if cpu:
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        cpu_ms, cpu_losses = run(copy.deepcopy(base), "cpu", data[:cpu_steps + 1], 1)
+        k = min(len(cpu_losses), len(dev_losses))
+        rel = max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:k], cpu_losses[:k]))
+        # float64 CPU run of the same steps: the rounding-free trajectory both fp32 runs are compared with (Adam on a
+        # 1000-class batch of 32 amplifies fp32 summation-order differences from step to step)
+        _, f64_losses = run(copy.deepcopy(base).double(), "cpu", data[:k], 0, torch.float64)
+        out.update({"cpu_ms_per_step": round(cpu_ms, 2), "cpu_cores": threads, "cpu_steps": cpu_steps,
+                    "speedup_vs_cpu": round(cpu_ms / dev_ms, 2), "max_rel_loss_diff": rel, "loss_steps_compared": k,
+                    "losses": {"device": [round(v, 6) for v in dev_losses[:k]],
+                               "cpu": [round(v, 6) for v in cpu_losses[:k]],
+                               "cpu_fp64": [round(v, 6) for v in f64_losses]},
+                    "max_rel_loss_diff_vs_fp64": {
+                        "device": max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:k], f64_losses)),
+                        "cpu_fp32": max(abs(a - b) / abs(b) for a, b in zip(cpu_losses[:k], f64_losses))},
+                    "cpu": f"PyTorch {torch.__version__} CPU fp32, {cpu_info()}"})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["c5", "c1"], default="c5")
+    ap.add_argument("--workload", choices=["c5", "c1", "resnet"], default="c5",
+                    help="resnet: only the ResNet-18 training-step measurement (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-resnet", action="store_true", help="skip the ResNet-18 training-step measurement")
+    ap.add_argument("--resnet-steps", type=int, default=20)
+    ap.add_argument("--no-tune", action="store_true",
+                    help="skip plan tuning (tile / K split per layer and direction) before the warmup")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
                          "launch per layer; prints nothing else")
@@ -171,6 +240,12 @@ def main():
     from omarchy_mac_torch import hip_ops
 
     dev = torch.device("cuda:0")
+    if args.workload == "resnet":
+        import omarchy_mac_torch
+
+        print(json.dumps({"resnet18_b32": resnet18_step(omarchy_mac_torch.DEVICE, args.resnet_steps, 5, 5,
+                                                          not args.no_cpu)}), flush=True)
+        return
     layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
     if args.pmc_probe:
         pmc_probe(layers, dev)
@@ -184,6 +259,14 @@ def main():
         w = torch.randn((k, c, ks, ks), device=dev, generator=gen) * scale
         gy = torch.randn((n, k, o, o), device=dev, generator=gen) * scale
         data.append((name, n, c, k, h, ks, s, p, x, w, gy))
+
+    plans = {}
+    for (name, n, c, k, h, ks, s, p, x, w, gy) in data:
+        for d in ("fwd", "dgrad", "wgrad"):
+            if not args.no_tune:  # the reference tunes every new conv shape on first use (csrc/conv.cpp:56)
+                hip_ops.autotune_conv(d, x.shape, w.shape, s, p)
+            plans.setdefault(name, {})[d] = list(hip_ops.conv_plan(d, x.shape, w.shape, s, p)[:2])
+    torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
     fwd_events = []  # (flops, start, end) per forward launch in the timed steps
@@ -241,7 +324,7 @@ def main():
                     for name, dd in per_layer.items()}
 
     out = {
-        "metric": "conv fwd+dgrad+wgrad fp32 TFLOP/s (% of fp32-MFMA peak)",
+        "metric": "conv fwd+dgrad+wgrad fp32 TFLOP/s (% of fp32-MFMA peak); ResNet-18 b32 train ms/step",
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -266,8 +349,13 @@ def main():
                      "flop_per_launch_avg": round(sum(fwd_flops) / len(fwd_flops))},
         "per_direction": per_dir,
         "per_layer_tflops": layer_tflops,
+        "plans": {"tuned": not args.no_tune, "tile_slices": plans},
         "device": torch.cuda.get_device_name(dev),
     }
+    if not args.no_resnet:
+        import omarchy_mac_torch  # noqa: F401  (registers the device)
+
+        out["resnet18_b32"] = resnet18_step(omarchy_mac_torch.DEVICE, args.resnet_steps, 5, 5, not args.no_cpu)
     if not args.no_cpu:
         threads = len(os.sched_getaffinity(0))
         out["cpu_baseline"] = oracle_baseline(layers, budget_s=15.0)

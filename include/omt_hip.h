@@ -45,6 +45,17 @@ enum { OMT_CONV_NONE = 0, OMT_CONV_DENSE = 1, OMT_CONV_DW = 2, OMT_CONV_DWG = 3 
 /* forward epilogue bits (omarchy_mac_torch/gemm.py:38-39) */
 enum { OMT_EPI_BIAS = 1u, OMT_EPI_RELU = 2u };
 
+/* GEMM directions of a dense convolution, the first field of a plan-cache key (the reference's GEMM kinds 0, 1, 2:
+ * omarchy_mac_torch/gemm.py:6-8) */
+enum { OMT_DIR_FWD = 0, OMT_DIR_DGRAD = 1, OMT_DIR_WGRAD = 2 };
+
+/* A dense convolution's launch plan: tile index (into the direction's tile table, omt_conv_num_tiles) and number of
+ * K slices (split K; rounded to whole K-blocks per slice). Replaces ConvPlan's tile and split-K multiplier
+ * (csrc/omt.h:230-236). */
+typedef struct omt_conv_plan {
+  int32_t tile, slices;
+} omt_conv_plan;
+
 /* ---- library, errors, geometry ---------------------------------------------------------------------------- */
 
 /* Message of the last non-OK status returned on this thread ("" if none). */
@@ -93,8 +104,10 @@ int omt_event_elapsed_ms(void* start, void* end, float* ms);
  * bn_mean/var/gamma/beta non-NULL (all four): the input is first mapped through the previous layer's eval BatchNorm
  * + ReLU, max((x - mean[ci]) * rsqrt(var[ci] + eps) * gamma[ci] + beta[ci], 0), on in-bounds taps only (padding
  * stays zero). Replaces gemm_forward (csrc/conv.cpp:70-77) with kinds 0 and 3 (omarchy_mac_torch/gemm.py:25-42,
- * 139-141). Dense means: ks 1..11, stride 1..4, 0 <= pad <= ks. The workspace (omt_conv_fwd_workspace bytes, possibly 0)
- * holds the filter re-packed for the tap-major reduction order. */
+ * 139-141). Dense means: ks 1..11, stride 1..4, 0 <= pad <= ks. The workspace (omt_conv_fwd_workspace bytes, possibly 0,
+ * with or without the BN loader) holds the filter re-packed for the tap-major reduction order and, for layers with too
+ * few output tiles to fill the GPU, the partial sums of a K split (summed in a fixed order: results are deterministic).
+ * The grad-input workspace holds the stride-phase filters and, likewise, any K-split partials. */
 size_t omt_conv_fwd_workspace(const omt_conv_geo* g);
 int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
                  const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta, float bn_eps,
@@ -113,6 +126,23 @@ int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float
 size_t omt_conv_wgrad_workspace(const omt_conv_geo* g);
 int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/* ---- plan cache and tuning (replaces conv_plan / autotune / tune_dump / tune_load / tuned_plans,
+ * csrc/conv.cpp:45-60, 116-155, 243-282) ---------------------------------------------------------------------
+ * Every dense-conv call and workspace query resolves its plan from a process-wide cache keyed by (direction,
+ * geometry); without an entry a cost model picks it. Changing an entry between a workspace query and the launch it
+ * sized can make the launch fail with OMT_INVALID (workspace too small), never overrun the workspace.
+ * omt_conv_autotune times the candidates (every tile of the first max_tiles, <= 0 meaning all, times a few K
+ * splits) on scratch buffers on `stream` with HIP events, stores the fastest in the cache and returns it in *best
+ * (may be NULL). It synchronizes `stream`, allocates through omt_malloc, and refuses (OMT_UNSUPPORTED) while the
+ * stream is capturing. The cache is in key order for omt_conv_plan_entry (i < omt_conv_plan_count()). */
+int omt_conv_num_tiles(int dir);
+int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* plan, int* cached);
+int omt_conv_set_plan(int dir, const omt_conv_geo* g, const omt_conv_plan* plan); /* NULL plan: remove the entry */
+int omt_conv_plan_count(void);
+int omt_conv_plan_entry(int i, int* dir, omt_conv_geo* g, omt_conv_plan* plan);
+void omt_conv_clear_plans(void);
+int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* best);
 
 /* Bias grad gb[c] = sum_{n,hw} gy[n][c][hw]. Replaces csum_nchw (csrc/conv.cpp:232-235). */
 int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream);

@@ -80,7 +80,16 @@ TORCH_EXT = HERE / "torch_ext"
 
 
 def build_torch_ext(verbose=False):
-    """Compiles torch_ext/*.cpp with torch's extension toolchain into omarchy_mac_torch/_native.so."""
+    """Compiles torch_ext/*.cpp with torch's extension toolchain into omarchy_mac_torch/_native.so.
+
+    The compile runs in a child process: torch's extension loader imports what it builds, and the extension registers
+    the PrivateUse1 device once per process, so the caller must stay free to import the package afterwards."""
+    cmd = [sys.executable, str(pathlib.Path(__file__).resolve()), "--torch-ext-child"] + (["--verbose"] if verbose else [])
+    subprocess.run(cmd, check=True)
+    return PKG / "_native.so"
+
+
+def _build_torch_ext_here(verbose=False):
     import torch
     import torch.utils.cpp_extension as ce
 
@@ -113,7 +122,11 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--lib-only", action="store_true", help="build libomt_hip.so only")
+    ap.add_argument("--torch-ext-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.torch_ext_child:
+        _build_torch_ext_here(args.verbose)
+        sys.exit(0)
     print(build(args.jobs, args.verbose))
     if not args.lib_only:
         print(build_torch_ext(args.verbose))

@@ -3,10 +3,11 @@
 // Training statistics follow the reference's shifted sums (csrc/kernels/bn_stats_part.wgsl:21-31,
 // bn_stats_fin.wgsl:11-22): d = x - x[n=0, c, 0], s1 = sum d, s2 = sum d^2, mean = shift + s1/m,
 // var = max(s2/m - (s1/m)^2, 0) (biased), with the running-stat update rm += mom*(mean - rm),
-// rv += mom*(var*m/(m-1) - rv) (csrc/nn.cpp:41-45). Each workgroup reduces one (channel, slice) of the n*hw
-// elements; lanes accumulate in float64 (free on a bandwidth-bound kernel) and the slices are combined in a fixed
-// order, so the statistics are deterministic. Reductions are butterfly shuffles within each wave64, then LDS across
-// the four waves of a workgroup.
+// rv += mom*(var*m/(m-1) - rv) (csrc/nn.cpp:41-45). A channel's n*hw elements are numbered as VEC-wide vectors
+// v = (image, position) (float4 when hw % 4 == 0) and cut into contiguous slices; each workgroup reduces one
+// (channel, slice) with four vector loads in flight per thread; lanes accumulate in float64 (free on a
+// bandwidth-bound kernel) and the slices are combined in a fixed order, so the statistics are deterministic.
+// Reductions are butterfly shuffles within each wave64, then LDS across the four waves of a workgroup.
 //
 // Backward (csrc/nn.cpp:60-78, bnb_reduce.wgsl / bnb_apply.wgsl; ReLU-masked form bn_bwd_part / bn_bwd_fin /
 // bn_bwd_apply of csrc/fused.cpp:86-115): gz = g (or g * [y > 0]), xhat = (x - mean) * invstd,
@@ -17,25 +18,54 @@ namespace omt {
 
 constexpr int kMaxSlices = 64;
 
+// Per-channel vector numbering and slicing of the reductions.
 struct Split {
-  int sn, sh;      // image slices x hw slices
-  int hw_chunk;    // elements of one image row handled per hw slice
+  int vec;        // 4 (float4) when hw % 4 == 0, else 1
+  int hwv;        // vectors per image plane
+  int nv;         // vectors per channel: n * hwv
+  int slices;     // slices per channel
+  int per_slice;  // vectors per slice
+  FastDiv div_hwv;
 };
 
-static Split bn_split(int64_t n, int64_t c, int64_t hw) {
-  // aim for ~2048 workgroups overall, each streaming at least ~4K elements
-  int64_t want = cdiv(2048, c);
-  int64_t by_size = (n * hw) / 4096;
+// ~1024 workgroups overall (four per CU), each at least 1024 vectors (four per thread) unless the channel is smaller.
+static Split bn_split(int64_t n, int64_t c, int64_t hw, bool aligned) {
+  Split sp;
+  sp.vec = (hw % 4 == 0 && aligned) ? 4 : 1;
+  sp.hwv = (int)(hw / sp.vec);
+  sp.nv = (int)(n * sp.hwv);
+  int64_t want = cdiv(1024, c);
+  const int64_t by_size = cdiv(sp.nv, 1024);
   if (want > by_size) want = by_size;
   if (want > kMaxSlices) want = kMaxSlices;
   if (want < 1) want = 1;
-  int64_t sn = want < n ? want : n;
-  int64_t sh = want / sn;
-  if (sh < 1) sh = 1;
-  int64_t chunk = cdiv(hw, sh);
-  chunk = cdiv(chunk, 4) * 4;
-  sh = cdiv(hw, chunk);
-  return {(int)sn, (int)sh, (int)chunk};
+  sp.per_slice = (int)cdiv(sp.nv, want);
+  sp.slices = (int)cdiv(sp.nv, sp.per_slice);
+  sp.div_hwv = make_fastdiv((uint32_t)sp.hwv);
+  return sp;
+}
+
+template <int VEC>
+struct VecT;
+template <>
+struct VecT<4> {
+  using T = float4;
+};
+template <>
+struct VecT<1> {
+  using T = float;
+};
+__device__ __forceinline__ float vget(const float4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+__device__ __forceinline__ float vget(const float& v, int) { return v; }
+__device__ __forceinline__ void vset(float4& v, int i, float f) {
+  if (i == 0) v.x = f; else if (i == 1) v.y = f; else if (i == 2) v.z = f; else v.w = f;
+}
+__device__ __forceinline__ void vset(float& v, int, float f) { v = f; }
+
+// Element offset of vector v of channel ch.
+__device__ __forceinline__ int64_t voffset(int v, int ch, int c, int hw, int hwv, const FastDiv& div_hwv, int vec) {
+  const int nn = (int)fdiv((uint32_t)v, div_hwv), e = v - nn * hwv;
+  return ((int64_t)nn * c + ch) * hw + (int64_t)e * vec;
 }
 
 __device__ __forceinline__ double wave_sum(double v) {
@@ -61,20 +91,35 @@ __device__ __forceinline__ void block_sum2(double& a, double& b) {
   }
 }
 
-// grid (c, sn * sh): partial shifted sums of one (channel, slice)
+// grid (c, slices): partial shifted sums of one (channel, slice)
+template <int VEC>
 __global__ void __launch_bounds__(256) bn_stats_part_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                            int n, int c, int hw, int sn, int sh, int chunk) {
-  const int ch = blockIdx.x, s = blockIdx.y, si = s / sh, sj = s % sh;
+                                                            int c, int hw, const Split sp) {
+  using V = typename VecT<VEC>::T;
+  const int ch = blockIdx.x, s = blockIdx.y;
   const float shift = x[(int64_t)ch * hw];
-  const int e0 = sj * chunk, e1 = min(hw, e0 + chunk);
+  const int v0 = s * sp.per_slice, v1 = min(sp.nv, v0 + sp.per_slice);
   double s1 = 0.0, s2 = 0.0;
-  for (int nn = si; nn < n; nn += sn) {
-    const float* row = x + ((int64_t)nn * c + ch) * hw;
-    for (int e = e0 + threadIdx.x; e < e1; e += 256) {
-      const double d = (double)(row[e] - shift);
-      s1 += d;
-      s2 += d * d;
+  for (int v = v0 + (int)threadIdx.x; v < v1; v += 4 * 256) {
+    V r[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int vv = v + u * 256;
+      if (vv < v1) {
+        r[u] = *reinterpret_cast<const V*>(x + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);  // contributes d = 0
+      }
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const double d = (double)(vget(r[u], i) - shift);
+        s1 += d;
+        s2 += d * d;
+      }
   }
   block_sum2(s1, s2);
   if (threadIdx.x == 0) {
@@ -148,24 +193,70 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
   }
 }
 
+// Small planes: the same affine map over a flat range of VEC-wide vectors, channel = (vector / hwv) mod c.
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_apply_flat_kernel(const float* __restrict__ x, const float* __restrict__ mean,
+                                                            const float* __restrict__ invstd,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta, float* __restrict__ y,
+                                                            int64_t total_v, FastDiv div_hwv, FastDiv div_c, int c,
+                                                            int relu) {
+  using V = typename VecT<VEC>::T;
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
+    const uint32_t plane = fdiv((uint32_t)i, div_hwv), ch = plane - fdiv(plane, div_c) * (uint32_t)c;
+    const float sc = invstd[ch] * gamma[ch];
+    const float sh = beta[ch] - mean[ch] * sc;
+    V v = reinterpret_cast<const V*>(x)[i];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float f = fmaf(vget(v, e), sc, sh);
+      if (relu) f = fmaxf(f, 0.f);
+      vset(v, e, f);
+    }
+    reinterpret_cast<V*>(y)[i] = v;
+  }
+}
+
 // grid (c, slices): partial sum gz and sum gz * xhat
+template <int VEC>
 __global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                           const float* __restrict__ ry, const float* __restrict__ mean,
                                                           const float* __restrict__ invstd, double* __restrict__ part,
-                                                          int n, int c, int hw, int sn, int sh, int chunk) {
-  const int ch = blockIdx.x, s = blockIdx.y, si = s / sh, sj = s % sh;
+                                                          int c, int hw, const Split sp) {
+  using V = typename VecT<VEC>::T;
+  const int ch = blockIdx.x, s = blockIdx.y;
   const float mu = mean[ch], inv = invstd[ch];
-  const int e0 = sj * chunk, e1 = min(hw, e0 + chunk);
+  const int v0 = s * sp.per_slice, v1 = min(sp.nv, v0 + sp.per_slice);
   double s1 = 0.0, s2 = 0.0;
-  for (int nn = si; nn < n; nn += sn) {
-    const int64_t off = ((int64_t)nn * c + ch) * hw;
-    for (int e = e0 + threadIdx.x; e < e1; e += 256) {
-      float gz = g[off + e];
-      if (ry && !(ry[off + e] > 0.f)) gz = 0.f;
-      const float xhat = (x[off + e] - mu) * inv;
-      s1 += (double)gz;
-      s2 += (double)gz * (double)xhat;
+  for (int v = v0 + (int)threadIdx.x; v < v1; v += 4 * 256) {
+    V rg[4], rx[4], rr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int vv = v + u * 256;
+      if (vv < v1) {
+        const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+        rg[u] = *reinterpret_cast<const V*>(g + off);
+        rx[u] = *reinterpret_cast<const V*>(x + off);
+        if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          vset(rg[u], i, 0.f);  // gz = 0 contributes nothing
+          vset(rx[u], i, mu);
+          vset(rr[u], i, 1.f);
+        }
+      }
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float gz = vget(rg[u], i);
+        if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+        const float xhat = (vget(rx[u], i) - mu) * inv;
+        s1 += (double)gz;
+        s2 += (double)gz * (double)xhat;
+      }
   }
   block_sum2(s1, s2);
   if (threadIdx.x == 0) {
@@ -174,8 +265,9 @@ __global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restric
   }
 }
 
-__global__ void bn_bwd_fin_kernel(const double* __restrict__ part, int c, int slices, double* __restrict__ tot,
-                                  float* __restrict__ dgamma, float* __restrict__ dbeta) {
+__global__ void bn_bwd_fin_kernel(const double* __restrict__ part, int c, int slices, const float* __restrict__ mean,
+                                  const float* __restrict__ invstd, const float* __restrict__ gamma, double m,
+                                  float* __restrict__ kc, float* __restrict__ dgamma, float* __restrict__ dbeta) {
   const int ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= c) return;
   double s1 = 0.0, s2 = 0.0;
@@ -183,32 +275,69 @@ __global__ void bn_bwd_fin_kernel(const double* __restrict__ part, int c, int sl
     s1 += part[((int64_t)ch * slices + s) * 2];
     s2 += part[((int64_t)ch * slices + s) * 2 + 1];
   }
-  tot[2 * ch] = s1;
-  tot[2 * ch + 1] = s2;
   if (dbeta) dbeta[ch] = (float)s1;
   if (dgamma) dgamma[ch] = (float)s2;
+  if (gamma) {
+    const double gi = (double)gamma[ch] * (double)invstd[ch];
+    kc[ch * 5 + 0] = (float)gi;
+    kc[ch * 5 + 1] = (float)(gi * s1 / m);
+    kc[ch * 5 + 2] = (float)(gi * s2 / m);
+    kc[ch * 5 + 3] = mean[ch];
+    kc[ch * 5 + 4] = invstd[ch];
+  }
 }
 
-// gx = gamma * invstd / m * (m * gz - sum_gz - xhat * sum_gz_xhat) = k1 * gz - k2 - k3 * xhat
+// gx = gamma * invstd / m * (m * gz - sum_gz - xhat * sum_gz_xhat) = k1 * gz - k2 - k3 * xhat, with the per-channel
+// constants k1..k3 (and mean, invstd) precomputed by bn_bwd_fin_kernel into kc[ch][5].
+__device__ __forceinline__ float bwd_elem(float gz, float xv, float r, bool masked, const float* k) {
+  if (masked && !(r > 0.f)) gz = 0.f;
+  const float xhat = (xv - k[3]) * k[4];
+  return k[0] * gz - k[1] - k[2] * xhat;
+}
+
+// grid x = plane (n * c), grid y = chunks of the plane
+template <int VEC>
 __global__ void __launch_bounds__(256) bn_bwd_apply_kernel(const float* __restrict__ g, const float* __restrict__ x,
-                                                           const float* __restrict__ ry,
-                                                           const float* __restrict__ mean,
-                                                           const float* __restrict__ invstd,
-                                                           const float* __restrict__ gamma,
-                                                           const double* __restrict__ tot, float* __restrict__ gx,
-                                                           int c, int hw, double m) {
+                                                           const float* __restrict__ ry, const float* __restrict__ kc,
+                                                           float* __restrict__ gx, int c, int hwv) {
+  using V = typename VecT<VEC>::T;
   const int plane = blockIdx.x, ch = plane % c;
-  const double gi = (double)gamma[ch] * (double)invstd[ch];
-  const float k1 = (float)gi;
-  const float k2 = (float)(gi * tot[2 * ch] / m);
-  const float k3 = (float)(gi * tot[2 * ch + 1] / m);
-  const float mu = mean[ch], inv = invstd[ch];
-  const int64_t base = (int64_t)plane * hw;
-  for (int e = blockIdx.y * 256 + threadIdx.x; e < hw; e += gridDim.y * 256) {
-    float gz = g[base + e];
-    if (ry && !(ry[base + e] > 0.f)) gz = 0.f;
-    const float xhat = (x[base + e] - mu) * inv;
-    gx[base + e] = k1 * gz - k2 - k3 * xhat;
+  float k[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) k[i] = kc[ch * 5 + i];
+  const int64_t base = (int64_t)plane * hwv;
+  for (int e = blockIdx.y * 256 + threadIdx.x; e < hwv; e += gridDim.y * 256) {
+    const V vg = reinterpret_cast<const V*>(g)[base + e], vx = reinterpret_cast<const V*>(x)[base + e];
+    V vr = vg;
+    if (ry) vr = reinterpret_cast<const V*>(ry)[base + e];
+    V o;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) vset(o, i, bwd_elem(vget(vg, i), vget(vx, i), vget(vr, i), ry != nullptr, k));
+    reinterpret_cast<V*>(gx)[base + e] = o;
+  }
+}
+
+// Small planes: flat over VEC-wide vectors.
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __restrict__ g,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ ry,
+                                                                const float* __restrict__ kc, float* __restrict__ gx,
+                                                                int64_t total_v, FastDiv div_hwv, FastDiv div_c,
+                                                                int c) {
+  using V = typename VecT<VEC>::T;
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
+    const uint32_t plane = fdiv((uint32_t)i, div_hwv), ch = plane - fdiv(plane, div_c) * (uint32_t)c;
+    float k[5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j) k[j] = kc[ch * 5 + j];
+    const V vg = reinterpret_cast<const V*>(g)[i], vx = reinterpret_cast<const V*>(x)[i];
+    V vr = vg;
+    if (ry) vr = reinterpret_cast<const V*>(ry)[i];
+    V o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) vset(o, e, bwd_elem(vget(vg, e), vget(vx, e), vget(vr, e), ry != nullptr, k));
+    reinterpret_cast<V*>(gx)[i] = o;
   }
 }
 
@@ -220,7 +349,47 @@ static dim3 apply_grid(int64_t planes, int64_t hw, int per_thread) {
 }
 
 static bool bn_size_ok(int64_t n, int64_t c, int64_t hw) {
-  return n >= 1 && c >= 1 && c <= 65535 && hw >= 1 && n * c < ((int64_t)1 << 31) && hw < ((int64_t)1 << 31);
+  return n >= 1 && c >= 1 && c <= 65535 && hw >= 1 && n * hw < ((int64_t)1 << 31) && n * c < ((int64_t)1 << 31) &&
+         hw < ((int64_t)1 << 31);
+}
+
+static bool al16(const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; }
+
+// Planes below this many elements use the flat apply kernels (one workgroup per plane would mostly idle).
+constexpr int64_t kFlatPlane = 1024;
+
+static int launch_stats(const Split& sp, const float* x, double* part, int64_t c, int64_t hw, hipStream_t s) {
+  const dim3 grid((unsigned)c, (unsigned)sp.slices);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_stats_part_kernel<4>, grid, dim3(256), 0, s, x, part, (int)c, (int)hw, sp);
+  else
+    hipLaunchKernelGGL(bn_stats_part_kernel<1>, grid, dim3(256), 0, s, x, part, (int)c, (int)hw, sp);
+  return launch_check("bn_stats_part_kernel");
+}
+
+// y = x * (invstd * gamma) + (beta - mean * invstd * gamma) [ReLU] with per-channel mean / invstd arrays.
+static int launch_apply(int64_t n, int64_t c, int64_t hw, const float* x, const float* mean, const float* invstd,
+                        const float* gamma, const float* beta, float* y, int relu, hipStream_t s) {
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y);
+  const int64_t vw = vec ? 4 : 1, total_v = n * c * hw / vw;
+  if (hw < kFlatPlane && total_v < ((int64_t)1 << 31)) {
+    const FastDiv dh = make_fastdiv((uint32_t)(hw / vw)), dc = make_fastdiv((uint32_t)c);
+    const dim3 grid(grid1d(total_v, 256, 16384));
+    if (vec)
+      hipLaunchKernelGGL(bn_apply_flat_kernel<4>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, y, total_v, dh,
+                         dc, (int)c, relu);
+    else
+      hipLaunchKernelGGL(bn_apply_flat_kernel<1>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, y, total_v, dh,
+                         dc, (int)c, relu);
+    return launch_check("bn_apply_flat_kernel");
+  }
+  if (vec)
+    hipLaunchKernelGGL(bn_apply_kernel<true>, apply_grid(n * c, hw, 4), dim3(256), 0, s, x, mean, invstd, nullptr,
+                       0.0, gamma, beta, y, (int)c, (int)hw, relu);
+  else
+    hipLaunchKernelGGL(bn_apply_kernel<false>, apply_grid(n * c, hw, 1), dim3(256), 0, s, x, mean, invstd, nullptr,
+                       0.0, gamma, beta, y, (int)c, (int)hw, relu);
+  return launch_check("bn_apply_kernel");
 }
 
 }  // namespace omt
@@ -242,25 +411,15 @@ OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x
   if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
     return fail(OMT_INVALID, "omt_bn_train_fwd: workspace too small");
   hipStream_t s = stream_of(stream);
-  Split sp = bn_split(n, c, hw);
-  const int slices = sp.sn * sp.sh;
+  const Split sp = bn_split(n, c, hw, al16(x));
   double* part = (double*)workspace;
-  hipLaunchKernelGGL(bn_stats_part_kernel, dim3((unsigned)c, (unsigned)slices), dim3(256), 0, s, x, part, (int)n,
-                     (int)c, (int)hw, sp.sn, sp.sh, sp.hw_chunk);
-  if (int st = launch_check("bn_stats_part_kernel")) return st;
+  if (int st = launch_stats(sp, x, part, c, hw, s)) return st;
   const double m = (double)(n * hw);
   hipLaunchKernelGGL(bn_stats_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, x, (const double*)part, (int)c,
-                     (int)hw, slices, m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm,
+                     (int)hw, sp.slices, m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm,
                      new_rv);
   if (int st = launch_check("bn_stats_fin_kernel")) return st;
-  const bool vec = (hw % 4) == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0;
-  if (vec)
-    hipLaunchKernelGGL(bn_apply_kernel<true>, apply_grid(n * c, hw, 4), dim3(256), 0, s, x, save_mean, save_invstd,
-                       nullptr, eps, gamma, beta, y, (int)c, (int)hw, relu);
-  else
-    hipLaunchKernelGGL(bn_apply_kernel<false>, apply_grid(n * c, hw, 1), dim3(256), 0, s, x, save_mean, save_invstd,
-                       nullptr, eps, gamma, beta, y, (int)c, (int)hw, relu);
-  return launch_check("bn_apply_kernel");
+  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, y, relu, s);
 }
 
 OMT_EXPORT int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
@@ -280,10 +439,11 @@ OMT_EXPORT int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x,
   return launch_check("bn_apply_kernel");
 }
 
+// [c][kMaxSlices][2] double partials, then [c][5] float per-channel constants of the input-gradient map
 OMT_EXPORT size_t omt_bn_bwd_workspace(int64_t n, int64_t c, int64_t hw) {
   (void)n;
   (void)hw;
-  return (size_t)(c * kMaxSlices * 2 + c * 2) * sizeof(double);
+  return (size_t)(c * kMaxSlices * 2) * sizeof(double) + (size_t)(c * 5) * sizeof(float);
 }
 
 OMT_EXPORT int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, const float* x, const float* relu_y,
@@ -294,20 +454,40 @@ OMT_EXPORT int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, cons
   if (!workspace || workspace_bytes < omt_bn_bwd_workspace(n, c, hw))
     return fail(OMT_INVALID, "omt_bn_bwd: workspace too small");
   hipStream_t s = stream_of(stream);
-  Split sp = bn_split(n, c, hw);
-  const int slices = sp.sn * sp.sh;
+  const bool aligned = al16(g) && al16(x) && al16(relu_y) && al16(gx);
+  const Split sp = bn_split(n, c, hw, aligned);
   double* part = (double*)workspace;
-  double* tot = part + c * kMaxSlices * 2;
-  hipLaunchKernelGGL(bn_bwd_part_kernel, dim3((unsigned)c, (unsigned)slices), dim3(256), 0, s, g, x, relu_y,
-                     save_mean, save_invstd, part, (int)n, (int)c, (int)hw, sp.sn, sp.sh, sp.hw_chunk);
+  float* kc = (float*)(part + c * kMaxSlices * 2);
+  const dim3 pgrid((unsigned)c, (unsigned)sp.slices);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_bwd_part_kernel<4>, pgrid, dim3(256), 0, s, g, x, relu_y, save_mean, save_invstd, part,
+                       (int)c, (int)hw, sp);
+  else
+    hipLaunchKernelGGL(bn_bwd_part_kernel<1>, pgrid, dim3(256), 0, s, g, x, relu_y, save_mean, save_invstd, part,
+                       (int)c, (int)hw, sp);
   if (int st = launch_check("bn_bwd_part_kernel")) return st;
-  hipLaunchKernelGGL(bn_bwd_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, slices,
-                     tot, dgamma, dbeta);
+  const double m = (double)(n * hw);
+  hipLaunchKernelGGL(bn_bwd_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, sp.slices,
+                     save_mean, save_invstd, gx ? gamma : nullptr, m, kc, dgamma, dbeta);
   if (int st = launch_check("bn_bwd_fin_kernel")) return st;
-  if (gx) {
-    hipLaunchKernelGGL(bn_bwd_apply_kernel, apply_grid(n * c, hw, 1), dim3(256), 0, s, g, x, relu_y, save_mean,
-                       save_invstd, gamma, (const double*)tot, gx, (int)c, (int)hw, (double)(n * hw));
-    if (int st = launch_check("bn_bwd_apply_kernel")) return st;
+  if (!gx) return OMT_OK;
+  const int64_t total_v = n * c * hw / sp.vec;
+  if (hw < kFlatPlane && total_v < ((int64_t)1 << 31)) {
+    const FastDiv dh = make_fastdiv((uint32_t)sp.hwv), dc = make_fastdiv((uint32_t)c);
+    const dim3 grid(grid1d(total_v, 256, 16384));
+    if (sp.vec == 4)
+      hipLaunchKernelGGL(bn_bwd_apply_flat_kernel<4>, grid, dim3(256), 0, s, g, x, relu_y, kc, gx, total_v, dh, dc,
+                         (int)c);
+    else
+      hipLaunchKernelGGL(bn_bwd_apply_flat_kernel<1>, grid, dim3(256), 0, s, g, x, relu_y, kc, gx, total_v, dh, dc,
+                         (int)c);
+    return launch_check("bn_bwd_apply_flat_kernel");
   }
-  return OMT_OK;
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_bwd_apply_kernel<4>, apply_grid(n * c, hw, 4), dim3(256), 0, s, g, x, relu_y, kc, gx,
+                       (int)c, (int)(hw / 4));
+  else
+    hipLaunchKernelGGL(bn_bwd_apply_kernel<1>, apply_grid(n * c, hw, 1), dim3(256), 0, s, g, x, relu_y, kc, gx,
+                       (int)c, (int)hw);
+  return launch_check("bn_bwd_apply_kernel");
 }

@@ -15,6 +15,10 @@
 // output pixels and q' = (ci, ky, kx), split over k into grid-z slices whose partials are summed in slice order by
 // split_reduce_kernel (reference: gemm_grad_weight + gemm_reduce, csrc/conv.cpp:102-114).
 //
+// Split K. A layer with too few output tiles to fill the chip (late, low-resolution layers) splits its reduction into
+// grid-z slices of whole K-blocks; each slice writes its raw partial tile into a [slices][N][P][YH][YW] workspace and
+// gather_reduce_kernel sums the slices in slice order (deterministic) and applies the bias / ReLU epilogue.
+//
 // Tiling: a 256-thread workgroup computes a BP x BQ tile of C as 4 waves, each a WP x WQ block of 16x16 MFMA tiles,
 // with the operands staged through LDS. MFMA 16x16x4 lane layout: lane l supplies A[l%16][l/16] and B[l/16][l%16];
 // the accumulator holds D[4*(l/16) + r][l%16] in element r. Because the reduction order inside a K-block is free,
@@ -31,6 +35,12 @@
 // bounds test per lane per block yields the vector offset, and each element is a bare buffer load whose channel
 // offset c*H*W travels in the scalar offset. Other C use the channel-major order k = (c, ky, kx) of the reference's
 // index maps (generic mode) with a per-element bounds test.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
 #include "omt_internal.h"
 
 namespace omt {
@@ -71,6 +81,9 @@ struct GatherArgs {
   int C, H, W, P, YH, YW;
   FastDiv div_c;
   int nphase;
+  int kslice;            // K elements per grid-z slice (a multiple of the K-block)
+  float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
+  int64_t part_stride;   // elements per slice
   Phase ph[kMaxPhases];
 };
 
@@ -88,7 +101,8 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
   __shared__ __attribute__((aligned(16))) float As[2][BP * PK];
   __shared__ __attribute__((aligned(16))) float Bs[2][BQ * PK];
 
-  const Phase& ph = a.ph[blockIdx.z];
+  const int zs = (int)blockIdx.z / a.nphase;  // K slice
+  const Phase& ph = a.ph[(int)blockIdx.z - zs * a.nphase];
   const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
   if (q0 >= ph.Q) return;  // this phase has fewer pixel tiles than the largest one
   const int t = threadIdx.x, lane = t & 63;
@@ -183,16 +197,17 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = (K + BK - 1) / BK;
+  const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;  // an empty slice still writes its (zero) tile
   if (nk > 0) {
-    gload(0);
+    gload(kbeg);
     sstore(0);
   }
   __syncthreads();
   const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
   for (int it = 0; it < nk; ++it) {
     const int cur = it & 1;
-    if (it + 1 < nk) gload((it + 1) * BK);
+    if (it + 1 < nk) gload(kbeg + (it + 1) * BK);
     float4 av[TI], bv[TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i) av[i] = *reinterpret_cast<const float4*>(&As[cur][(la + 16 * i) * PK + grp * 4]);
@@ -209,8 +224,9 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
     __syncthreads();
   }
 
-  // epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid)
+  // epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid); split K: raw partials
   const int64_t yhw = (int64_t)a.YH * a.YW;
+  float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
   const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
@@ -218,7 +234,7 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
     if (q >= ph.Q) continue;
     const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
     const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
-    float* yb = a.y + (int64_t)n * P * yhw + (int64_t)((int)oy * ph.os + ph.oy0) * a.YW + (int)ox * ph.os + ph.ox0;
+    float* yb = ydst + (int64_t)n * P * yhw + (int64_t)((int)oy * ph.os + ph.oy0) * a.YW + (int)ox * ph.os + ph.ox0;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -226,8 +242,10 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
         const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
         if (p < P) {
           float v = acc[i][j][r4];
-          if (a.bias) v += a.bias[p];
-          if (a.relu) v = fmaxf(v, 0.f);
+          if (!a.part) {
+            if (a.bias) v += a.bias[p];
+            if (a.relu) v = fmaxf(v, 0.f);
+          }
           yb[(int64_t)p * yhw] = v;
         }
       }
@@ -396,6 +414,42 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
   }
 }
 
+// Split-K gather epilogue: y[i] = act(sum_z part[z][i] + bias[c(i)]), slices summed in order; y is NCHW with
+// planes of `plane` elements over `P` channels. VEC 4 needs plane % 4 == 0 (a float4 then stays in one plane).
+template <int VEC>
+__global__ void __launch_bounds__(256) gather_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                            int64_t n, int slices, int64_t plane, int P,
+                                                            const float* __restrict__ bias, int relu) {
+  const int64_t nv = n / VEC;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
+    float v[VEC];
+    if (VEC == 4) {
+      const float4 t = reinterpret_cast<const float4*>(part)[i];
+      v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+    } else {
+      v[0] = part[i];
+    }
+    for (int z = 1; z < slices; ++z) {
+      if (VEC == 4) {
+        const float4 t = reinterpret_cast<const float4*>(part + z * n)[i];
+        v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w;
+      } else {
+        v[0] += part[z * n + i];
+      }
+    }
+    const float b = bias ? bias[(i * VEC / plane) % P] : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      v[e] += b;
+      if (relu) v[e] = fmaxf(v[e], 0.f);
+    }
+    if (VEC == 4)
+      reinterpret_cast<float4*>(y)[i] = make_float4(v[0], v[1], v[2], v[3]);
+    else
+      y[i] = v[0];
+  }
+}
+
 // Re-packs w[co][ci][ks][ks] into the per-phase grad-input weights W'[ci][co][a'][b'] described at the top.
 struct PackPhase {
   int ky0, kx0, jy, jx, woff;
@@ -517,17 +571,76 @@ static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t 
 // Tap-major order needs whole K-blocks of channels; the BN loader keeps the channel-major order.
 static bool gather_tap_major(int64_t c, bool bn) { return !bn && c % 16 == 0; }
 
-static int run_gather(const GatherArgs& a, int64_t maxq, hipStream_t s) {
-  const int ti = pick_tile(kGatherTiles, a.P, maxq, a.nphase, kCUs * 2);
-  const Tile& tl = kGatherTiles[ti];
-  dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)a.nphase);
+// Tile and K split of a gather launch: P rows, Q columns (the largest phase), K the longest reduction, z phases.
+struct GatherPlan {
+  int tile;
+  int64_t slices, kslice;
+};
+static const int kSliceChoices[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
+
+// Estimated makespan in clocks, over tiles and slice counts:
+// - workgroups run two per CU at ~34 fp32 FMA/clock each times the tile's efficiency, or ~1.6x that alone on a CU;
+// - each carries ~3 K-blocks of fixed cost (prologue, epilogue) and needs >= 6 K-blocks per slice to be worth a split;
+// - a split pays the partial round trip through HBM (~1.7 KB/clock) and one more launch (~7000 clocks).
+// `fixed` (a tuned or requested plan) replaces the estimate: its slice count is rounded to whole K-blocks per slice.
+static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const omt_conv_plan* fixed) {
+  constexpr int BK = 16;
+  const int64_t nkb = cdiv(K > 0 ? K : 1, BK);
+  if (fixed) {
+    const int64_t kb = cdiv(nkb, std::max<int64_t>(1, std::min<int64_t>(fixed->slices, nkb)));
+    return {fixed->tile, cdiv(nkb, kb), kb * BK};
+  }
+  GatherPlan best{0, 1, nkb * BK};
+  double best_cost = 1e300;
+  for (int ti = 0; ti < (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0])); ++ti) {
+    const Tile& tl = kGatherTiles[ti];
+    const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z;
+    for (int sc : kSliceChoices) {
+      const int64_t kb = cdiv(nkb, sc);
+      if (sc > 1 && kb < 6) break;
+      const int64_t slices = cdiv(nkb, kb);
+      if (slices != sc) continue;
+      const int64_t blocks = tiles * slices;
+      const double wg = (double)tl.bp * tl.bq * BK * (kb + 3) / (34.0 * tl.eff);
+      double cost = blocks <= kCUs ? wg / 1.6 : (double)cdiv(blocks, 2 * kCUs) * wg;
+      if (slices > 1) cost += 7000.0 + (double)(2 * slices) * P * Q * z * 4 / 1700.0;
+      if (cost < best_cost * 0.999) {
+        best_cost = cost;
+        best = {ti, slices, kb * BK};
+      }
+    }
+  }
+  return best;
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size.
+static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part, hipStream_t s) {
+  const Tile& tl = kGatherTiles[pl.tile];
+  a.kslice = (int)pl.kslice;
+  const int64_t total = n * a.P * a.YH * a.YW;
+  a.part = pl.slices > 1 ? part : nullptr;
+  a.part_stride = total;
+  dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
   if (a.bn_mean)
-    gather_dispatch<kGeneric, true>(ti, a, grid, s);
+    gather_dispatch<kGeneric, true>(pl.tile, a, grid, s);
   else if (gather_tap_major(a.C, a.bn_mean != nullptr))
-    gather_dispatch<kTapMajor, false>(ti, a, grid, s);
+    gather_dispatch<kTapMajor, false>(pl.tile, a, grid, s);
   else
-    gather_dispatch<kGeneric, false>(ti, a, grid, s);
-  return launch_check("conv_gather_kernel");
+    gather_dispatch<kGeneric, false>(pl.tile, a, grid, s);
+  if (int st = launch_check("conv_gather_kernel")) return st;
+  if (pl.slices > 1) {
+    const int64_t plane = (int64_t)a.YH * a.YW;
+    if (plane % 4 == 0)
+      hipLaunchKernelGGL(gather_reduce_kernel<4>, dim3(grid1d(total / 4, 256, 8192)), dim3(256), 0, s, part, a.y,
+                         total, (int)pl.slices, plane, a.P, a.bias, a.relu);
+    else
+      hipLaunchKernelGGL(gather_reduce_kernel<1>, dim3(grid1d(total, 256, 8192)), dim3(256), 0, s, part, a.y, total,
+                         (int)pl.slices, plane, a.P, a.bias, a.relu);
+    if (int st = launch_check("gather_reduce_kernel")) return st;
+  }
+  return OMT_OK;
 }
 
 static bool dense_geo_ok(const omt_conv_geo* g) {
@@ -547,18 +660,28 @@ struct WgradPlan {
   int tile;
   int64_t slices, kslice;
 };
-static WgradPlan wgrad_plan(const omt_conv_geo* g) {
+// The estimate's slice count for tile ti.
+static int64_t wgrad_model_slices(const omt_conv_geo* g, int ti) {
   const int64_t P = g->co, Q = g->ci * g->ks * g->ks, K = g->n * g->oh * g->ow;
-  const int ti = pick_tile(kWgradTiles, P, Q, 1, kCUs * 2);
   const Tile& tl = kWgradTiles[ti];
   const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq);
-  int64_t slices = cdiv(kCUs * 4, tiles);
-  const int64_t max_slices = cdiv(K, 64 * 4);
-  if (slices > max_slices) slices = max_slices;
-  if (slices < 1) slices = 1;
-  int64_t kslice = cdiv(cdiv(K, slices), 64) * 64;
-  slices = cdiv(K, kslice);
-  return {ti, slices, kslice};
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(kCUs * 4, tiles), cdiv(K, 64 * 4)));
+}
+static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p);
+static WgradPlan wgrad_plan(const omt_conv_geo* g) {
+  const int64_t P = g->co, Q = g->ci * g->ks * g->ks, K = g->n * g->oh * g->ow;
+  omt_conv_plan cp;
+  int ti;
+  int64_t slices;
+  if (cached_plan(OMT_DIR_WGRAD, g, &cp)) {
+    ti = cp.tile;
+    slices = std::max<int64_t>(1, std::min<int64_t>(cp.slices, cdiv(K, 64)));
+  } else {
+    ti = pick_tile(kWgradTiles, P, Q, 1, kCUs * 2);
+    slices = wgrad_model_slices(g, ti);
+  }
+  const int64_t kslice = cdiv(cdiv(K, slices), 64) * 64;
+  return {ti, cdiv(K, kslice), kslice};
 }
 
 template <int MODE>
@@ -571,13 +694,57 @@ static void wgrad_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s)
   }
 }
 
+// ---- plan cache: the tile and K split per (direction, geometry), set by tuning --------------------------------
+
+struct PlanKey {
+  int dir;
+  int64_t n, ci, co, ih, iw, oh, ow, ks, stride, pad;
+  auto tie() const { return std::tie(dir, n, ci, co, ih, iw, oh, ow, ks, stride, pad); }
+  bool operator<(const PlanKey& o) const { return tie() < o.tie(); }
+};
+static std::mutex g_plan_mu;
+static std::map<PlanKey, omt_conv_plan> g_plans;
+static thread_local const omt_conv_plan* t_force = nullptr;  // the candidate under test while tuning
+
+static PlanKey key_of(int dir, const omt_conv_geo* g) {
+  return {dir, g->n, g->ci, g->co, g->ih, g->iw, g->oh, g->ow, g->ks, g->stride, g->pad};
+}
+static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p) {
+  if (t_force) {
+    *p = *t_force;
+    return true;
+  }
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  auto it = g_plans.find(key_of(dir, g));
+  if (it == g_plans.end()) return false;
+  *p = it->second;
+  return true;
+}
+static int num_tiles(int dir) {
+  return dir == OMT_DIR_WGRAD ? (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0]))
+                              : (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0]));
+}
+
 }  // namespace omt
 
 using namespace omt;
 
-OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
-  if (!g || g->ks == 1 || !gather_tap_major(g->ci, false)) return 0;
+// Forward workspace: the tap-major filter (C % 16 == 0, ks > 1), then, 256-byte aligned, the split-K partials.
+static size_t fwd_pack_bytes(const omt_conv_geo* g) {
+  if (g->ks == 1 || !gather_tap_major(g->ci, false)) return 0;
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+}
+static GatherPlan fwd_plan(const omt_conv_geo* g) {
+  omt_conv_plan cp;
+  const bool have = cached_plan(OMT_DIR_FWD, g, &cp);
+  return gather_plan(g->co, g->n * g->oh * g->ow, g->ci * g->ks * g->ks, 1, have ? &cp : nullptr);
+}
+
+OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
+  const GatherPlan pl = fwd_plan(g);
+  const size_t part = pl.slices > 1 ? (size_t)(pl.slices * g->n * g->co * g->oh * g->ow) * sizeof(float) : 0;
+  return part ? align256(fwd_pack_bytes(g)) + part : fwd_pack_bytes(g);
 }
 
 OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
@@ -591,15 +758,16 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   if (bn && !(bn_mean && bn_var && bn_gamma && bn_beta))
     return fail(OMT_INVALID, "omt_conv_fwd: BN loader needs mean, var, gamma and beta");
   if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd: bias epilogue without bias");
+  const size_t need = omt_conv_fwd_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_fwd: workspace of %zu bytes needed", need);
   hipStream_t s = stream_of(stream);
+  const GatherPlan pl = fwd_plan(g);
   GatherArgs a{};
   a.x = x;
   a.w = w;
   // tap-major order: re-pack the filter to [co][ky][kx][ci] (1x1 filters already are)
-  if (!bn && g->ks > 1 && gather_tap_major(g->ci, false)) {
-    const size_t need = omt_conv_fwd_workspace(g);
-    if (!workspace || workspace_bytes < need)
-      return fail(OMT_INVALID, "omt_conv_fwd: workspace of %zu bytes needed", need);
+  if (!bn && fwd_pack_bytes(g)) {
     const int total = (int)(g->co * g->ci * g->ks * g->ks);
     hipLaunchKernelGGL(pack_tapmajor_kernel, dim3(grid1d(total, 256, 4096)), dim3(256), 0, s, w, (float*)workspace,
                        (int)g->co, (int)g->ci, (int)(g->ks * g->ks));
@@ -639,7 +807,7 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   p.div_kw = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather(a, p.Q, s);
+  return run_gather(a, pl, g->n, p.Q, (float*)((char*)workspace + align256(fwd_pack_bytes(g))), s);
 }
 
 // Stride-phase table of the grad-input GEMMs (see the top of this file).
@@ -681,9 +849,23 @@ static int dgrad_phases(const omt_conv_geo* g, GatherArgs& a, PackArgs& pk, int6
   return woff;
 }
 
+// Grad-input workspace: the per-phase packed filters, then, 256-byte aligned, the split-K partials.
+static GatherPlan dgrad_plan(const omt_conv_geo* g) {
+  GatherArgs a{};
+  PackArgs pk{};
+  int64_t maxq = 0, maxk = 0;
+  dgrad_phases(g, a, pk, maxq);
+  for (int i = 0; i < a.nphase; ++i) maxk = a.ph[i].K > maxk ? a.ph[i].K : maxk;
+  omt_conv_plan cp;
+  const bool have = cached_plan(OMT_DIR_DGRAD, g, &cp);
+  return gather_plan(g->ci, maxq, maxk, a.nphase, have ? &cp : nullptr);
+}
+
 OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
-  if (!g) return 0;
-  return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+  if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
+  const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+  const GatherPlan pl = dgrad_plan(g);
+  return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * g->ci * g->ih * g->iw) * sizeof(float) : pack;
 }
 
 OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
@@ -719,7 +901,9 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   a.YH = (int)g->ih;
   a.YW = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather(a, maxq, s);
+  const GatherPlan pl = dgrad_plan(g);
+  const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+  return run_gather(a, pl, g->n, maxq, (float*)((char*)workspace + align256(pack)), s);
 }
 
 OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
@@ -795,4 +979,217 @@ OMT_EXPORT int omt_fold_bn(int64_t co, int64_t per_out, const float* cw, const f
   hipLaunchKernelGGL(fold_bn_kernel, dim3(grid1d(co * per_out, 256, 4096)), dim3(256), 0, stream_of(stream), (int)co,
                      (int)per_out, cw, cb, gamma, beta, mean, var, eps, fw, fb);
   return launch_check("fold_bn_kernel");
+}
+
+// ---- plan cache and tuning --------------------------------------------------------------------------------------
+
+static int plan_args_ok(int dir, const omt_conv_geo* g, const char* what) {
+  if (!g) return fail(OMT_INVALID, "%s: null geometry", what);
+  if (dir < OMT_DIR_FWD || dir > OMT_DIR_WGRAD) return fail(OMT_INVALID, "%s: direction %d", what, dir);
+  if (!dense_geo_ok(g) || !fits_i32(g)) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", what);
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_conv_num_tiles(int dir) {
+  return dir >= OMT_DIR_FWD && dir <= OMT_DIR_WGRAD ? num_tiles(dir) : 0;
+}
+
+OMT_EXPORT int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* plan, int* cached) {
+  if (int st = plan_args_ok(dir, g, "omt_conv_get_plan")) return st;
+  if (!plan) return fail(OMT_INVALID, "omt_conv_get_plan: null plan");
+  omt_conv_plan cp;
+  if (cached) *cached = cached_plan(dir, g, &cp) ? 1 : 0;
+  if (dir == OMT_DIR_WGRAD) {
+    const WgradPlan pl = wgrad_plan(g);
+    *plan = {pl.tile, (int32_t)pl.slices};
+  } else {
+    const GatherPlan pl = dir == OMT_DIR_FWD ? fwd_plan(g) : dgrad_plan(g);
+    *plan = {pl.tile, (int32_t)pl.slices};
+  }
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_conv_set_plan(int dir, const omt_conv_geo* g, const omt_conv_plan* plan) {
+  if (int st = plan_args_ok(dir, g, "omt_conv_set_plan")) return st;
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  if (!plan) {
+    g_plans.erase(key_of(dir, g));
+    return OMT_OK;
+  }
+  if (plan->tile < 0 || plan->tile >= num_tiles(dir) || plan->slices < 1 || plan->slices > 4096)
+    return fail(OMT_INVALID, "omt_conv_set_plan: tile %d (of %d) / slices %d out of range", plan->tile, num_tiles(dir),
+                plan->slices);
+  g_plans[key_of(dir, g)] = *plan;
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_conv_plan_count(void) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  return (int)g_plans.size();
+}
+
+OMT_EXPORT int omt_conv_plan_entry(int i, int* dir, omt_conv_geo* g, omt_conv_plan* plan) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  if (i < 0 || i >= (int)g_plans.size()) return fail(OMT_INVALID, "omt_conv_plan_entry: index %d", i);
+  auto it = g_plans.begin();
+  std::advance(it, i);
+  const PlanKey& k = it->first;
+  if (dir) *dir = k.dir;
+  if (g) *g = omt_conv_geo{k.n, k.ci, k.co, k.ih, k.iw, k.oh, k.ow, k.ks, k.stride, k.pad};
+  if (plan) *plan = it->second;
+  return OMT_OK;
+}
+
+OMT_EXPORT void omt_conv_clear_plans(void) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  g_plans.clear();
+}
+
+namespace {
+
+// Candidate plans of one direction: each tile with the K splits worth timing (distinct after rounding to whole
+// K-blocks, at most 512 MiB of partials); wgrad: the estimate's slice count times 1/4, 1/2, 1 and 2, like the
+// reference's split-K multipliers (csrc/conv.cpp:129).
+std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int ntile) {
+  std::vector<omt_conv_plan> out;
+  if (dir == OMT_DIR_WGRAD) {
+    const int64_t K = g->n * g->oh * g->ow, kmax = cdiv(K, 64);
+    for (int t = 0; t < ntile; ++t) {
+      const int64_t base = wgrad_model_slices(g, t);
+      int64_t last = -1;
+      for (double m : {0.25, 0.5, 1.0, 2.0}) {
+        const int64_t sl = std::max<int64_t>(1, std::min<int64_t>(kmax, (int64_t)(base * m + 0.5)));
+        const int64_t eff = cdiv(K, cdiv(cdiv(K, sl), 64) * 64);
+        if (eff == last || eff * g->co * g->ci * g->ks * g->ks * 4 > ((int64_t)512 << 20)) continue;
+        last = eff;
+        out.push_back({t, (int32_t)eff});
+      }
+    }
+    return out;
+  }
+  int64_t P, Q, K, z = 1, plane;
+  if (dir == OMT_DIR_FWD) {
+    P = g->co, Q = g->n * g->oh * g->ow, K = g->ci * g->ks * g->ks, plane = g->n * g->co * g->oh * g->ow;
+  } else {
+    GatherArgs a{};
+    PackArgs pk{};
+    dgrad_phases(g, a, pk, Q);
+    K = 0;
+    for (int i = 0; i < a.nphase; ++i) K = std::max<int64_t>(K, a.ph[i].K);
+    P = g->ci, z = a.nphase, plane = g->n * g->ci * g->ih * g->iw;
+  }
+  const int64_t nkb = cdiv(std::max<int64_t>(K, 1), 16);
+  for (int t = 0; t < ntile; ++t) {
+    const Tile& tl = kGatherTiles[t];
+    const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z;
+    int64_t last = -1;
+    for (int sc : {1, 2, 4, 8, 16, 32, 64}) {
+      const int64_t kb = cdiv(nkb, sc), eff = cdiv(nkb, kb);
+      if (sc > 1 && (kb < 2 || tiles >= 2 * kCUs)) break;  // a grid that already fills the GPU is not split
+      if (eff == last || (eff > 1 && eff * plane * 4 > ((int64_t)512 << 20))) continue;
+      last = eff;
+      out.push_back({t, (int32_t)eff});
+    }
+  }
+  return out;
+}
+
+struct ForceGuard {
+  ~ForceGuard() { t_force = nullptr; }
+};
+
+}  // namespace
+
+OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* best) {
+  if (int st = plan_args_ok(dir, g, "omt_conv_autotune")) return st;
+  if (t_force) return fail(OMT_INVALID, "omt_conv_autotune: re-entered");
+  hipStream_t s = stream_of(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  OMT_HIP(hipStreamIsCapturing(s, &cs));
+  if (cs != hipStreamCaptureStatusNone) return fail(OMT_UNSUPPORTED, "omt_conv_autotune: stream is capturing");
+  const int ntile = max_tiles <= 0 ? num_tiles(dir) : std::min(max_tiles, num_tiles(dir));
+  const std::vector<omt_conv_plan> cands = tune_candidates(dir, g, ntile);
+  if (cands.empty()) return fail(OMT_UNSUPPORTED, "omt_conv_autotune: no candidate plan");
+
+  ForceGuard guard;
+  size_t ws_bytes = 0;
+  for (const omt_conv_plan& c : cands) {
+    t_force = &c;
+    const size_t b = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
+                     : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
+    ws_bytes = std::max(ws_bytes, b);
+  }
+  t_force = nullptr;
+  const size_t xb = (size_t)(g->n * g->ci * g->ih * g->iw) * 4, wb = (size_t)(g->co * g->ci * g->ks * g->ks) * 4,
+               yb = (size_t)(g->n * g->co * g->oh * g->ow) * 4;
+  const size_t ob = dir == OMT_DIR_FWD ? yb : dir == OMT_DIR_DGRAD ? xb : wb;
+  void *x = nullptr, *w = nullptr, *y = nullptr, *o = nullptr, *ws = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int st = OMT_OK;
+  auto cleanup = [&]() {
+    (void)hipStreamSynchronize(s);  // nothing queued may still use the buffers when they return to the cache
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    for (void* p : {x, w, y, o, ws})
+      if (p) omt_free(p);
+  };
+  if ((st = omt_malloc(&x, xb)) || (st = omt_malloc(&w, wb)) || (st = omt_malloc(&y, yb)) ||
+      (st = omt_malloc(&o, ob)) || (ws_bytes && (st = omt_malloc(&ws, ws_bytes)))) {
+    cleanup();
+    return st;
+  }
+  // zero inputs: fp32 MFMA timing does not depend on the values
+  if ((st = hip_check(hipMemsetAsync(x, 0, xb, s), "hipMemsetAsync")) ||
+      (st = hip_check(hipMemsetAsync(w, 0, wb, s), "hipMemsetAsync")) ||
+      (st = hip_check(hipMemsetAsync(y, 0, yb, s), "hipMemsetAsync")) ||
+      (st = hip_check(hipEventCreate(&e0), "hipEventCreate")) || (st = hip_check(hipEventCreate(&e1), "hipEventCreate"))) {
+    cleanup();
+    return st;
+  }
+  auto run = [&]() -> int {
+    const size_t need = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
+                        : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
+    if (dir == OMT_DIR_FWD)
+      return omt_conv_fwd(g, (const float*)x, (const float*)w, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 1e-5f,
+                          (float*)o, ws, need, s);
+    if (dir == OMT_DIR_DGRAD) return omt_conv_dgrad(g, (const float*)y, (const float*)w, (float*)o, ws, need, s);
+    return omt_conv_wgrad(g, (const float*)x, (const float*)y, (float*)o, ws, need, s);
+  };
+  auto timed = [&](int reps, float* ms) -> int {
+    if (int e = hip_check(hipEventRecord(e0, s), "hipEventRecord")) return e;
+    for (int r = 0; r < reps; ++r)
+      if (int e = run()) return e;
+    if (int e = hip_check(hipEventRecord(e1, s), "hipEventRecord")) return e;
+    if (int e = hip_check(hipEventSynchronize(e1), "hipEventSynchronize")) return e;
+    if (int e = hip_check(hipEventElapsedTime(ms, e0, e1), "hipEventElapsedTime")) return e;
+    *ms /= (float)reps;
+    return OMT_OK;
+  };
+  omt_conv_plan win = cands[0];
+  float win_ms = 1e30f;
+  for (const omt_conv_plan& c : cands) {
+    t_force = &c;
+    float first = 0.f, ms = 0.f;
+    if ((st = run()) || (st = timed(1, &first))) break;  // warm-up, then one timed run
+    // about 2 ms of timing per candidate, at most 8 repetitions
+    const int reps = (int)std::max(1.f, std::min(8.f, 2.f / std::max(first, 1e-3f)));
+    ms = first;
+    if (reps > 1) {
+      if ((st = timed(reps, &ms))) break;
+      ms = std::min(ms, first);
+    }
+    if (ms < win_ms) {
+      win_ms = ms;
+      win = c;
+    }
+  }
+  t_force = nullptr;
+  cleanup();
+  if (st) return st;
+  {
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    g_plans[key_of(dir, g)] = win;
+  }
+  if (best) *best = win;
+  return OMT_OK;
 }

@@ -84,7 +84,7 @@ Pool& pool() {
 using namespace omt;
 
 OMT_EXPORT const char* omt_last_error(void) { return t_last_error.c_str(); }
-OMT_EXPORT int omt_abi_version(void) { return 2; }
+OMT_EXPORT int omt_abi_version(void) { return 3; }
 OMT_EXPORT int omt_hip_runtime_version(void) {
   int v = 0;
   (void)hipRuntimeGetVersion(&v);

@@ -14,6 +14,7 @@ from omarchy_mac_torch import _lib  # noqa: F401  (libomt_hip.so; ImportError wh
 from omarchy_mac_torch import hip_ops  # noqa: F401
 from omarchy_mac_torch import native as _native  # noqa: F401  (registers the device)
 from omarchy_mac_torch import compile as _compile  # noqa: F401  (torch.compile backend "omarchy_mac_torch")
+from omarchy_mac_torch import optim as _optim  # noqa: F401  (fused SGD / Adam / AdamW by default on the device)
 from omarchy_mac_torch.native import (DEVICE, FALLBACKS, empty_cache, memory_allocated, memory_reserved,
                                       set_queue_depth, synchronize, validate_kernels)
 from omarchy_mac_torch.stacks import FusedSequential, accelerate

@@ -15,6 +15,7 @@ LIB_PATH = _HERE / "libomt_hip.so"
 OMT_OK, OMT_UNSUPPORTED, OMT_OOM, OMT_DEVICE_ERROR, OMT_INVALID = range(5)
 OMT_CONV_NONE, OMT_CONV_DENSE, OMT_CONV_DW, OMT_CONV_DWG = range(4)
 OMT_EPI_BIAS, OMT_EPI_RELU = 1, 2
+OMT_DIR_FWD, OMT_DIR_DGRAD, OMT_DIR_WGRAD = range(3)
 
 
 class ConvGeo(ctypes.Structure):
@@ -23,6 +24,11 @@ class ConvGeo(ctypes.Structure):
 
     def astuple(self):
         return tuple(getattr(self, k) for k, _ in self._fields_)
+
+
+class ConvPlan(ctypes.Structure):
+    """omt_conv_plan: tile index and K slices of a dense convolution GEMM (reference ConvPlan, csrc/omt.h:230-236)."""
+    _fields_ = [("tile", ctypes.c_int32), ("slices", ctypes.c_int32)]
 
 
 class OmtError(RuntimeError):
@@ -38,6 +44,7 @@ class Unsupported(OmtError):
 I64, U32, I32, F32, F64, SZ, VP = (ctypes.c_int64, ctypes.c_uint, ctypes.c_int, ctypes.c_float, ctypes.c_double,
                                    ctypes.c_size_t, ctypes.c_void_p)
 G = ctypes.POINTER(ConvGeo)
+PL = ctypes.POINTER(ConvPlan)
 
 # name -> (restype, argtypes); the full exported surface of include/omt_hip.h
 SIGNATURES = {
@@ -68,6 +75,13 @@ SIGNATURES = {
     "omt_conv_dgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_workspace": (SZ, [G]),
     "omt_conv_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_conv_num_tiles": (I32, [I32]),
+    "omt_conv_get_plan": (I32, [I32, G, PL, ctypes.POINTER(I32)]),
+    "omt_conv_set_plan": (I32, [I32, G, PL]),
+    "omt_conv_plan_count": (I32, []),
+    "omt_conv_plan_entry": (I32, [I32, ctypes.POINTER(I32), G, PL]),
+    "omt_conv_clear_plans": (None, []),
+    "omt_conv_autotune": (I32, [I32, G, I32, VP, PL]),
     "omt_bias_grad": (I32, [I64, I64, I64, VP, VP, VP]),
     "omt_fold_bn": (I32, [I64, I64, VP, VP, VP, VP, VP, VP, F32, VP, VP, VP]),
     "omt_dw_fwd": (I32, [G, VP, VP, VP, VP, VP, VP, VP, F32, VP, VP]),
@@ -87,7 +101,7 @@ SIGNATURES = {
     "omt_adapool_bwd": (I32, [I64] * 5 + [VP, VP, VP]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def _load():

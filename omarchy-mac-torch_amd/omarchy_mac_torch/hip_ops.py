@@ -62,7 +62,7 @@ def conv2d(x, w, bias=None, stride=1, padding=0, relu=False, bn=None, bn_eps=1e-
     y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32)
     bnp = [None] * 4 if bn is None else [_need(t, "bn", 1) for t in bn]
     epi = (_lib.OMT_EPI_BIAS if bias is not None else 0) | (_lib.OMT_EPI_RELU if relu else 0)
-    ws, nb = _workspace(L.omt_conv_fwd_workspace(ctypes.byref(g)) if bn is None else 0, x.device)
+    ws, nb = _workspace(L.omt_conv_fwd_workspace(ctypes.byref(g)), x.device)
     check(L.omt_conv_fwd(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(bias), epi, *[_ptr(t) for t in bnp], bn_eps,
                          _ptr(y), _ptr(ws), nb, _stream(x.device)), "conv2d")
     return y
@@ -92,6 +92,55 @@ def conv2d_wgrad(x, gy, ks, stride=1, padding=0):
     check(L.omt_conv_wgrad(ctypes.byref(g), _ptr(x), _ptr(gy), _ptr(gw), _ptr(ws), nb, _stream(x.device)),
           "conv2d_wgrad")
     return gw
+
+
+# ---- plan cache (tile / split-K per geometry) and tuning (reference: conv_plan, autotune, tune_dump, tune_load,
+# csrc/conv.cpp:45-60, 116-155, 243-272) ------------------------------------------------------------------------
+
+DIRECTIONS = {"fwd": _lib.OMT_DIR_FWD, "dgrad": _lib.OMT_DIR_DGRAD, "wgrad": _lib.OMT_DIR_WGRAD}
+
+
+def conv_num_tiles(direction):
+    return L.omt_conv_num_tiles(DIRECTIONS[direction])
+
+
+def conv_plan(direction, x_shape, w_shape, stride=1, padding=0):
+    """(tile, slices, cached): the plan the next call of this direction and geometry uses."""
+    g = conv_geo_for(x_shape, w_shape, stride, padding)
+    p, cached = _lib.ConvPlan(), ctypes.c_int32()
+    check(L.omt_conv_get_plan(DIRECTIONS[direction], ctypes.byref(g), ctypes.byref(p), ctypes.byref(cached)),
+          "conv_plan")
+    return p.tile, p.slices, bool(cached.value)
+
+
+def set_conv_plan(direction, x_shape, w_shape, stride=1, padding=0, tile=None, slices=1):
+    """Pins (tile, slices) for this direction and geometry; tile None removes the entry."""
+    g = conv_geo_for(x_shape, w_shape, stride, padding)
+    p = None if tile is None else ctypes.byref(_lib.ConvPlan(tile, slices))
+    check(L.omt_conv_set_plan(DIRECTIONS[direction], ctypes.byref(g), p), "set_conv_plan")
+
+
+def autotune_conv(direction, x_shape, w_shape, stride=1, padding=0, max_tiles=0, device=None):
+    """Times the candidate plans on scratch buffers and caches the fastest; returns (tile, slices)."""
+    g = conv_geo_for(x_shape, w_shape, stride, padding)
+    p = _lib.ConvPlan()
+    check(L.omt_conv_autotune(DIRECTIONS[direction], ctypes.byref(g), max_tiles, _stream(device), ctypes.byref(p)),
+          "autotune_conv")
+    return p.tile, p.slices
+
+
+def conv_plans():
+    """The plan cache: {"dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad": (tile, slices)} (the reference's tune_dump key)."""
+    out = {}
+    for i in range(L.omt_conv_plan_count()):
+        d, g, p = ctypes.c_int32(), _lib.ConvGeo(), _lib.ConvPlan()
+        if L.omt_conv_plan_entry(i, ctypes.byref(d), ctypes.byref(g), ctypes.byref(p)) == _lib.OMT_OK:
+            out[",".join(str(v) for v in (d.value,) + g.astuple())] = (p.tile, p.slices)
+    return out
+
+
+def clear_conv_plans():
+    L.omt_conv_clear_plans()
 
 
 def bias_grad(gy):

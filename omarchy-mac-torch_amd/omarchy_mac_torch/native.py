@@ -6,6 +6,8 @@ HIP kernels; every other op is delegated to torch's own HIP kernels on the same 
 required: a missing build raises ImportError instead of running anything elsewhere.
 """
 
+import atexit
+import json
 import os
 import pathlib
 import types
@@ -38,6 +40,7 @@ if torch._C._get_privateuse1_backend_name() != DEVICE:
                                                          for_storage=True)
 
 core.set_fold(int(os.environ.get("OMARCHY_MAC_TORCH_FOLD", "1")))
+core.set_tuning(os.environ.get("OMARCHY_MAC_TORCH_TUNE", "1") != "0", 0)
 core.set_debug(os.environ.get("OMARCHY_MAC_TORCH_DEBUG", "0") == "1")
 
 
@@ -142,3 +145,41 @@ class _Fallbacks:
 
 
 FALLBACKS = _Fallbacks()
+
+
+# ---- on-disk cache of the conv plan tuning (reference: omarchy_mac_torch/native.py:185-209) ----
+# Keys "dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad" -> [tile, slices]. The tiles index this library's gfx950 tile tables,
+# so the file is not the reference's (whose entries name its own tiles and a split-K multiplier).
+TUNE_FILE = os.environ.get("OMARCHY_MAC_TORCH_TUNE_FILE",
+                           os.path.expanduser("~/.cache/omarchy-mac-torch/tuning-gfx950.json"))
+
+
+def _load_tuning(path=TUNE_FILE):
+    try:
+        with open(path) as f:
+            return core.tune_load({str(k): (int(v[0]), int(v[1])) for k, v in json.load(f).items()})
+    except (OSError, ValueError, TypeError, KeyError, IndexError):
+        return 0
+
+
+def _save_tuning(path=TUNE_FILE):
+    try:
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        old = {}
+        try:
+            with open(path) as f:
+                old = json.load(f)
+        except (OSError, ValueError):
+            pass
+        old.update({k: list(v) for k, v in core.tune_dump().items()})
+        tmp = f"{path}.{os.getpid()}.tmp"
+        with open(tmp, "w") as f:
+            json.dump(old, f)
+        os.replace(tmp, path)
+    except Exception:
+        pass
+
+
+if core.tuning():
+    _load_tuning()
+    atexit.register(_save_tuning)

@@ -375,6 +375,14 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("unfold", &at::native::unfold);
   m.impl("view_as_real", &at::native::view_as_real);
   m.impl("view_as_complex", &at::native::view_as_complex);
+  // torch's _foreach_* ops carry a CompositeExplicitAutograd kernel that loops over the list one tensor at a time;
+  // for this key it would win over the boxed fallback and cost one delegated op per tensor. Registered here, each list
+  // op goes to torch's HIP kernels whole (one multi-tensor launch).
+  for (const c10::OperatorName& op : c10::Dispatcher::singleton().getAllOpNames()) {
+    if (op.name.rfind("aten::_foreach_", 0) != 0) continue;
+    const std::string name = op.name.substr(6) + (op.overload_name.empty() ? "" : "." + op.overload_name);
+    m.impl(name.c_str(), torch::CppFunction::makeFromBoxedFunction<&hip_fallback>());
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------------------

@@ -7,6 +7,7 @@
 
 namespace omt {
 void bind_plans(pybind11::module_& m);
+void bind_tuning(pybind11::module_& m);
 }
 
 PYBIND11_MODULE(_native, m) {
@@ -44,4 +45,5 @@ PYBIND11_MODULE(_native, m) {
   m.def("hip_runtime_version", []() { return omt_hip_runtime_version(); });
   m.attr("built_with_torch") = TORCH_VERSION;
   bind_plans(m);
+  bind_tuning(m);
 }

@@ -71,6 +71,9 @@ std::recursive_mutex& big_lock();
 std::map<std::string, int64_t>& fallback_counts();   // hot-path ops that could not use the HIP kernels
 std::map<std::string, int64_t>& delegated_counts();  // other ops, run on torch's HIP kernels (counted when enabled)
 void note_fallback(const std::string& op, const std::string& why);
+// Autotunes (direction, geometry) once when tuning is on and the plan cache has no entry (libomt_hip.so times the
+// candidates on the current stream); no-op otherwise.
+void tune_conv(int dir, const omt_conv_geo& g);
 bool strict_mode();
 bool debug_mode();
 void set_debug_mode(bool on);

@@ -41,6 +41,7 @@ static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::option
   NEED(g.oh >= 1 && g.ow >= 1, "empty output");
   Tensor y = empty_dev({g.n, g.co, g.oh, g.ow});
   if (kind == OMT_CONV_DENSE) {
+    tune_conv(OMT_DIR_FWD, g);
     Tensor ws = workspace(omt_conv_fwd_workspace(&g));
     unsigned epi = (b.defined() ? OMT_EPI_BIAS : 0u) | (relu ? OMT_EPI_RELU : 0u);
     check(omt_conv_fwd(&g, fp(x), fp(w), fp(b), epi, nullptr, nullptr, nullptr, nullptr, 1e-5f, fpm(y), wsptr(ws),
@@ -73,11 +74,13 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
   if (kind == OMT_CONV_DENSE) {
     if (mask[0]) {
       gx = empty_dev(x.sizes());
+      tune_conv(OMT_DIR_DGRAD, g);
       Tensor ws = workspace(omt_conv_dgrad_workspace(&g));
       check(omt_conv_dgrad(&g, fp(gy), fp(w), fpm(gx), wsptr(ws), wsbytes(ws), s), "convolution_backward (input)");
     }
     if (mask[1]) {
       gw = empty_dev(w.sizes());
+      tune_conv(OMT_DIR_WGRAD, g);
       Tensor ws = workspace(omt_conv_wgrad_workspace(&g));
       check(omt_conv_wgrad(&g, fp(x), fp(gy), fpm(gw), wsptr(ws), wsbytes(ws), s), "convolution_backward (weight)");
     }

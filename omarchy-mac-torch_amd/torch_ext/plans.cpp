@@ -109,7 +109,8 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
           check(omt_dw_fwd(&g, fp(x), fp(wt), nullptr, bm, bv, bg, bb, 1e-5f, fpm(out), s), "plan: depthwise conv");
         });
       } else {
-        Tensor ws = bm ? Tensor() : own_ws(p, omt_conv_fwd_workspace(&g));
+        tune_conv(OMT_DIR_FWD, g);
+        Tensor ws = own_ws(p, omt_conv_fwd_workspace(&g));
         p.fwd.push_back([g, x = cur, wt, out, bm, bv, bg, bb, ws](Run&, void* s) {
           check(omt_conv_fwd(&g, fp(x), fp(wt), nullptr, 0, bm, bv, bg, bb, 1e-5f, fpm(out), wsptr(ws), wsbytes(ws), s),
                 "plan: conv");
@@ -272,6 +273,7 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       omt_conv_geo geo = conv_geo(n_, c_, r.co, h_, w_, r.ks, 1, r.ks / 2);
       Tensor x = r.x, wt = params[r.param];
       const int gi = r.param;
+      if (!dw) tune_conv(OMT_DIR_WGRAD, geo);
       Tensor wws = own_ws(p, dw ? omt_dw_wgrad_workspace(&geo) : omt_conv_wgrad_workspace(&geo));
       p.bwd.push_back([=](Run& run, void* s) {
         if (dw)
@@ -283,6 +285,7 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       });
       if (!first || input_grad) {
         Tensor gx = own(p, {n_, c_, h_, w_});
+        if (!dw) tune_conv(OMT_DIR_DGRAD, geo);
         Tensor dws = dw ? Tensor() : own_ws(p, omt_conv_dgrad_workspace(&geo));
         p.bwd.push_back([=](Run&, void* s) {
           if (dw)

@@ -65,16 +65,67 @@ def test_host_validation_statuses():
     assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, fake, None, None, None, 1e-5, fake, None, 0, None) == \
         _lib.OMT_INVALID  # partial BN loader
     g64 = _lib.conv_geo(2, 64, 8, 8, 8, 3, 1, 1)  # tap-major order: the re-packed filter needs a workspace
-    assert L.omt_conv_fwd_workspace(ctypes.byref(g64)) == 8 * 64 * 9 * 4
+    assert L.omt_conv_set_plan(_lib.OMT_DIR_FWD, ctypes.byref(g64), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_OK
+    assert L.omt_conv_fwd_workspace(ctypes.byref(g64)) == 8 * 64 * 9 * 4  # one K slice: no partials
     assert L.omt_conv_fwd(ctypes.byref(g64), fake, fake, None, 0, None, None, None, None, 1e-5, fake, None, 0, None) \
         == _lib.OMT_INVALID
+    L.omt_conv_clear_plans()
     g.oh = 99  # inconsistent geometry
     assert L.omt_conv_wgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
     g = _lib.conv_geo(2, 3, 4, 8, 8, 3, 2, 1)
     assert L.omt_conv_dgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID  # no workspace
+    assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_OK
     assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 4 * 3 * 3 * 3 * 4
+    L.omt_conv_clear_plans()
     with pytest.raises(_lib.Unsupported):
         _lib.check(_lib.OMT_UNSUPPORTED)
+
+
+def test_plan_cache_host_side():
+    """The plan cache (tile, K slices per direction and geometry; reference conv_plan / tune_dump / tune_load,
+    csrc/conv.cpp:45-60, 243-272) and the cost model's split choice, all host-side."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    L.omt_conv_clear_plans()
+    fwd, dgrad, wgrad = _lib.OMT_DIR_FWD, _lib.OMT_DIR_DGRAD, _lib.OMT_DIR_WGRAD
+    assert L.omt_conv_num_tiles(fwd) == L.omt_conv_num_tiles(dgrad) >= 4 and L.omt_conv_num_tiles(wgrad) >= 3
+    assert L.omt_conv_num_tiles(7) == 0
+
+    def plan(d, g):
+        p, c = _lib.ConvPlan(), ctypes.c_int32()
+        assert L.omt_conv_get_plan(d, ctypes.byref(g), ctypes.byref(p), ctypes.byref(c)) == _lib.OMT_OK
+        return p.tile, p.slices, c.value
+
+    late = _lib.conv_geo(32, 512, 512, 2, 2, 3, 1, 1)    # ResNet-18 layer4 at 64x64: 128 pixels, K = 4608
+    big = _lib.conv_geo(256, 64, 64, 56, 56, 3, 1, 1)    # ResNet-50 layer1 at batch 256
+    assert plan(fwd, late)[1] > 1 and plan(dgrad, late)[1] > 1 and plan(fwd, late)[2] == 0
+    assert plan(fwd, big)[1] == 1 and plan(dgrad, big)[1] == 1
+    # the workspace grows by the partials of a split: [packed filter | 256-B aligned slices x N*P*OH*OW floats]
+    g = _lib.conv_geo(4, 64, 32, 6, 6, 3, 1, 1)
+    pack = 32 * 64 * 9 * 4
+    assert L.omt_conv_set_plan(fwd, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(2, 4))) == _lib.OMT_OK
+    assert plan(fwd, g) == (2, 4, 1)
+    assert L.omt_conv_fwd_workspace(ctypes.byref(g)) == (pack + 255) // 256 * 256 + 4 * 4 * 32 * 6 * 6 * 4
+    # slices beyond the K-blocks are clamped (K = 576 = 36 blocks of 16)
+    assert L.omt_conv_set_plan(fwd, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 100))) == _lib.OMT_OK
+    assert plan(fwd, g) == (0, 36, 1)
+    assert L.omt_conv_set_plan(wgrad, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(1, 50))) == _lib.OMT_OK
+    assert plan(wgrad, g) == (1, 3, 1)    # K = 144 pixels -> at most 3 slices of 64
+    for bad in (_lib.ConvPlan(-1, 1), _lib.ConvPlan(L.omt_conv_num_tiles(fwd), 1), _lib.ConvPlan(0, 0)):
+        assert L.omt_conv_set_plan(fwd, ctypes.byref(g), ctypes.byref(bad)) == _lib.OMT_INVALID
+    assert L.omt_conv_set_plan(5, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_INVALID
+    bad_geo = _lib.ConvGeo(2, 3, 4, 8, 8, 1, 1, 12, 1, 0)
+    assert L.omt_conv_set_plan(fwd, ctypes.byref(bad_geo), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_UNSUPPORTED
+    # enumeration in key order, removal, clear
+    assert L.omt_conv_plan_count() == 2
+    d, eg, ep = ctypes.c_int32(), _lib.ConvGeo(), _lib.ConvPlan()
+    assert L.omt_conv_plan_entry(1, ctypes.byref(d), ctypes.byref(eg), ctypes.byref(ep)) == _lib.OMT_OK
+    assert (d.value, eg.astuple(), ep.tile, ep.slices) == (wgrad, g.astuple(), 1, 50)
+    assert L.omt_conv_plan_entry(2, None, None, None) == _lib.OMT_INVALID
+    assert L.omt_conv_set_plan(wgrad, ctypes.byref(g), None) == _lib.OMT_OK
+    assert L.omt_conv_plan_count() == 1 and plan(wgrad, g)[2] == 0
+    L.omt_conv_clear_plans()
+    assert L.omt_conv_plan_count() == 0 and plan(fwd, g)[2] == 0
 
 
 FASTDIV_TEST = r"""

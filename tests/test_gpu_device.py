@@ -128,6 +128,39 @@ def test_depthwise_bn_pools_through_modules(clean):
         assert rel(dev(D(x, omt)), ref(x)) <= TOL
 
 
+def test_foreach_lists_and_fused_optimizers(clean):
+    """_foreach_* list ops reach torch's HIP kernels as one delegated op (not one per tensor), and SGD / Adam / AdamW
+    default to their fused kernels for device parameters (reference omarchy_mac_torch/optim.py), tracking the CPU
+    optimizers."""
+    omt = clean
+    ts = [torch.randn(n) for n in (3, 100, 7)]
+    ds = [D(t, omt) for t in ts]
+    omt._native.core.count_delegated(True)
+    try:
+        torch._foreach_add_(ds, 2.0)
+        counts = omt._native.core.delegated_counts()
+        assert counts.get("_foreach_add_.Scalar") == 1 and "add_.Tensor" not in counts, counts
+    finally:
+        omt._native.core.count_delegated(False)
+    for t, d in zip(ts, ds):
+        assert torch.equal(d.cpu(), t + 2)
+    torch.manual_seed(0)
+    for cls, kw in ((torch.optim.SGD, dict(lr=0.1, momentum=0.9)), (torch.optim.Adam, dict(lr=1e-2)),
+                    (torch.optim.AdamW, dict(lr=1e-2, weight_decay=0.1))):
+        p_cpu = [torch.randn(5, 4, requires_grad=True), torch.randn(7, requires_grad=True)]
+        p_dev = [D(p.detach(), omt).requires_grad_() for p in p_cpu]
+        o_cpu, o_dev = cls(p_cpu, **kw), cls(p_dev, **kw)
+        assert o_dev.defaults["fused"] is True and not o_cpu.defaults.get("fused"), cls
+        for _ in range(3):
+            for pc, pd in zip(p_cpu, p_dev):
+                g = torch.randn_like(pc)
+                pc.grad, pd.grad = g, D(g, omt)
+            o_cpu.step()
+            o_dev.step()
+        for pc, pd in zip(p_cpu, p_dev):
+            assert rel(pd, pc) <= 1e-5, cls
+
+
 def test_uncovered_conv_falls_back_and_is_recorded(clean):
     omt = clean
     x, w = torch.randn(2, 4, 11, 11), torch.randn(6, 4, 3, 3)

@@ -99,6 +99,85 @@ def test_conv_geometry_sweep(cuda, ops, ks):
                 assert orc.rel_l2(host(gw), orc.conv_wgrad(x, gy, ks, s, p)) <= TOL, case
 
 
+PLAN_SHAPES = [
+    (4, 512, 512, 2, 2, 3, 1, 1),   # ResNet-18 layer4 at 64x64: the cost model splits K
+    (3, 64, 128, 9, 9, 3, 2, 1),    # stride 2: grad-input phases with different K
+    (2, 24, 20, 7, 7, 3, 1, 1),     # channel-major K order (C % 16 != 0) with a K tail
+    (2, 32, 48, 6, 5, 1, 1, 0),     # 1x1
+]
+
+
+@pytest.mark.parametrize("shape", PLAN_SHAPES, ids=_ids)
+def test_conv_every_plan(cuda, ops, shape):
+    """Every tile with 1, 2, 3 and 7 K slices (split-K partials summed by the slice reduce, bias + ReLU applied
+    there) for forward and grad input; every wgrad tile with 1, 2 and 5 slices: all plans the tuner may pick."""
+    n, ci, co, h, w, ks, s, p = shape
+    rng = np.random.default_rng(sum(shape))
+    x, wt, b = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5), rnd(rng, co)
+    y_ref = orc.conv_fwd(x, wt, b, s, p, relu=True)
+    gy = rnd(rng, *y_ref.shape)
+    gx_ref, gw_ref = orc.conv_dgrad(gy, wt, x.shape, s, p), orc.conv_wgrad(x, gy, ks, s, p)
+    tx, tw, tb, tgy = dev(x, cuda), dev(wt, cuda), dev(b, cuda), dev(gy, cuda)
+    try:
+        for tile in range(ops.conv_num_tiles("fwd")):
+            for slices in (1, 2, 3, 7):
+                case = (tile, slices)
+                ops.set_conv_plan("fwd", x.shape, wt.shape, s, p, tile, slices)
+                ops.set_conv_plan("dgrad", x.shape, wt.shape, s, p, tile, slices)
+                assert ops.conv_plan("fwd", x.shape, wt.shape, s, p)[0] == tile
+                y = ops.conv2d(tx, tw, tb, s, p, relu=True)
+                assert orc.rel_l2(host(y), y_ref) <= TOL, case
+                gx = ops.conv2d_dgrad(tgy, tw, x.shape, s, p)
+                assert orc.rel_l2(host(gx), gx_ref) <= TOL, case
+        for tile in range(ops.conv_num_tiles("wgrad")):
+            for slices in (1, 2, 5):
+                ops.set_conv_plan("wgrad", x.shape, wt.shape, s, p, tile, slices)
+                gw = ops.conv2d_wgrad(tx, tgy, ks, s, p)
+                assert orc.rel_l2(host(gw), gw_ref) <= TOL, (tile, slices)
+    finally:
+        ops.clear_conv_plans()
+
+
+def test_conv_split_k_bn_loader(cuda, ops):
+    """The eval BN + ReLU input loader with K split over slices."""
+    rng = np.random.default_rng(11)
+    x, wt, b = rnd(rng, 2, 40, 4, 4), rnd(rng, 24, 40, 3, 3, scale=0.05), rnd(rng, 24)
+    bn = (rnd(rng, 40), np.abs(rnd(rng, 40)) + 0.5, rnd(rng, 40), rnd(rng, 40))
+    y_ref = orc.conv_fwd(x, wt, b, 1, 1, relu=True, bn=bn)
+    try:
+        for slices in (1, 4, 9):
+            ops.set_conv_plan("fwd", x.shape, wt.shape, 1, 1, 5, slices)
+            y = ops.conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), 1, 1, relu=True, bn=[dev(t, cuda) for t in bn])
+            assert orc.rel_l2(host(y), y_ref) <= TOL, slices
+    finally:
+        ops.clear_conv_plans()
+
+
+def test_autotune_caches_a_plan(cuda, ops):
+    """omt_conv_autotune times the candidates and caches the fastest; calls then use it (reference autotune,
+    csrc/conv.cpp:116-155)."""
+    rng = np.random.default_rng(12)
+    shape = (8, 256, 256, 4, 4, 3, 1, 1)
+    n, ci, co, h, w, ks, s, p = shape
+    x, wt = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * 9) ** -0.5)
+    try:
+        for d in ("fwd", "dgrad", "wgrad"):
+            tile, slices = ops.autotune_conv(d, x.shape, wt.shape, s, p)
+            assert ops.conv_plan(d, x.shape, wt.shape, s, p)[2]
+            assert 0 <= tile < ops.conv_num_tiles(d) and slices >= 1
+        assert len(ops.conv_plans()) == 3
+        y = ops.conv2d(dev(x, cuda), dev(wt, cuda), None, s, p)
+        y_ref = orc.conv_fwd(x, wt, None, s, p)
+        assert orc.rel_l2(host(y), y_ref) <= TOL
+        gy = rnd(rng, *y_ref.shape)
+        gx = ops.conv2d_dgrad(dev(gy, cuda), dev(wt, cuda), x.shape, s, p)
+        assert orc.rel_l2(host(gx), orc.conv_dgrad(gy, wt, x.shape, s, p)) <= TOL
+        gw = ops.conv2d_wgrad(dev(x, cuda), dev(gy, cuda), ks, s, p)
+        assert orc.rel_l2(host(gw), orc.conv_wgrad(x, gy, ks, s, p)) <= TOL
+    finally:
+        ops.clear_conv_plans()
+
+
 def test_conv_bn_loader_and_relu_epilogue(cuda, ops):
     """Kind-3 loader (eval BN + ReLU of the input, padding stays zero) and the bias + ReLU epilogue."""
     rng = np.random.default_rng(7)
@@ -208,7 +287,8 @@ def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
 # ---- batch norm ----
 
 @pytest.mark.parametrize("n,c,h,w", [(4, 6, 5, 7), (16, 8, 4, 4), (2, 3, 1, 1), (9, 4, 3, 3), (128, 32, 32, 32),
-                                     (32, 64, 16, 16), (32, 512, 2, 2), (1, 16, 57, 31)])
+                                     (32, 64, 16, 16), (32, 512, 2, 2), (1, 16, 57, 31), (3, 5, 37, 41),
+                                     (64, 16, 28, 28), (8, 3, 7, 9)])
 @pytest.mark.parametrize("relu", [False, True])
 def test_batch_norm_train_and_backward(cuda, ops, n, c, h, w, relu):
     rng = np.random.default_rng(n * 1000 + c)
