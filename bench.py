@@ -181,10 +181,52 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
             loss.backward()
             opt.step()
             losses.append(loss.detach())
+        host_ms = (time.perf_counter() - t0) / (len(batches) - timed_from) * 1e3  # enqueue time, before the sync
         if device != "cpu":
             torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) / (len(batches) - timed_from) * 1e3
+        run.host_ms = host_ms
         return ms, [float(l) for l in losses]
+
+    def run_graphed(model, batches, timed_from):
+        """The same step captured once as a HIP graph (omarchy_mac_torch.graphs) after `timed_from` eager warm-up
+        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed)."""
+        from omarchy_mac_torch import graphs
+
+        opt = torch.optim.Adam(model.parameters(), lr=1e-3, capturable=True)
+        sx, st = torch.empty_like(batches[0][0]), torch.empty_like(batches[0][1])
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            loss = F.cross_entropy(model(sx), st)
+            loss.backward()
+            opt.step()
+            return loss.detach()
+
+        losses = []
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for x, t in batches[:timed_from]:
+                sx.copy_(x)
+                st.copy_(t)
+                losses.append(step().clone())
+        torch.cuda.current_stream().wait_stream(side)
+        g = graphs.Graph()
+        with g.capture():
+            static_loss = step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for x, t in batches[timed_from:]:
+            sx.copy_(x)
+            st.copy_(t)
+            g.replay()
+            losses.append(static_loss.clone())
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / (len(batches) - timed_from) * 1e3
+        out = [float(l) for l in losses]
+        g.release()
+        return ms, out
 
     dev_model = copy.deepcopy(base).to(dev_name)
     dev_batches = [(x.to(dev_name), t.to(dev_name)) for (x, t) in data[:warmup + steps]]
@@ -192,7 +234,14 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
         torch.cuda.synchronize()
     dev_ms, dev_losses = run(dev_model, dev_name, dev_batches, warmup)
     out = {"config": "ResNet-18 b32 3x64x64, 1000 classes, BN train, Adam lr 1e-3 (BASELINE config 3)",
-           "ms_per_step": round(dev_ms, 3), "steps": steps, "warmup": warmup}
+           "ms_per_step": round(dev_ms, 3), "host_enqueue_ms_per_step": round(run.host_ms, 3), "steps": steps,
+           "warmup": warmup}
+    g_losses = None
+    if dev_name != "cpu":
+        g_ms, g_losses = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3)
+        out["graphed"] = {"ms_per_step": round(g_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
+                          "how": "omarchy_mac_torch.graphs.Graph: forward + backward + fused capturable Adam captured "
+                                 "once, replayed per batch after an in-place copy of the batch"}
     if cpu:
         threads = len(os.sched_getaffinity(0))
         torch.set_num_threads(threads)
@@ -202,6 +251,11 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
         # float64 CPU run of the same steps: the rounding-free trajectory both fp32 runs are compared with (Adam on a
         # 1000-class batch of 32 amplifies fp32 summation-order differences from step to step)
         _, f64_losses = run(copy.deepcopy(base).double(), "cpu", data[:k], 0, torch.float64)
+        if g_losses is not None:
+            out["graphed"].update({
+                "speedup_vs_cpu": round(cpu_ms / out["graphed"]["ms_per_step"], 2),
+                "max_rel_loss_diff": max(abs(a - b) / abs(b) for a, b in zip(g_losses[:k], cpu_losses[:k])),
+                "losses": [round(v, 6) for v in g_losses[:k]]})
         out.update({"cpu_ms_per_step": round(cpu_ms, 2), "cpu_cores": threads, "cpu_steps": cpu_steps,
                     "speedup_vs_cpu": round(cpu_ms / dev_ms, 2), "max_rel_loss_diff": rel, "loss_steps_compared": k,
                     "losses": {"device": [round(v, 6) for v in dev_losses[:k]],

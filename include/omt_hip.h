@@ -88,6 +88,17 @@ void* omt_default_stream(void);
  * Replaces upload/download_bytes and copy_dev (csrc/runtime.cpp:614-676). */
 int omt_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
 int omt_memset_zero(void* dst, size_t bytes, void* stream);
+
+/* Graph pools: memory that a captured HIP graph keeps for its replays. No counterpart in the reference, whose command
+ * recorder batches submissions instead (csrc/runtime.cpp:451-518); here a captured step is replayed as one graph.
+ * Between omt_graph_pool_begin(id) and omt_graph_pool_end() every omt_malloc, from any thread, is served from pool
+ * id, and that pool's blocks return to it (never to the general cache) when freed. omt_graph_pool_release hands
+ * them back to the general cache; call it only once no graph that uses them can be replayed (it synchronizes the
+ * device). One pool receives at a time. omt_graph_pool_create returns the new pool's id (> 0). */
+int omt_graph_pool_create(void);
+int omt_graph_pool_begin(int id);
+int omt_graph_pool_end(void);
+int omt_graph_pool_release(int id);
 int omt_stream_sync(void* stream);         /* replaces sync_all (csrc/runtime.cpp:520-527) */
 /* Events (replace the submission-index events of the device guard, csrc/device.cpp:124-161). */
 int omt_event_create(void** ev);

@@ -87,9 +87,10 @@ struct GatherArgs {
   Phase ph[kMaxPhases];
 };
 
-template <int BP, int BQ, int WP, int WQ, int MODE, bool BN>
+template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN>
 __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
-  constexpr int BK = 16, NT = 256;
+  constexpr int NT = 256;
+  static_assert(BK % 16 == 0 && NT % BK == 0, "K-block");
   constexpr int WGQ = BQ / WQ;
   static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
   static_assert(WP % 16 == 0 && WQ % 16 == 0 && BQ >= 64 && NT % BQ == 0, "tile shape");
@@ -204,22 +205,27 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
     sstore(0);
   }
   __syncthreads();
+  // lane group grp supplies k = grp * (BK / 4) + s at MFMA step s: BK / 16 b128 reads per operand row
   const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
   for (int it = 0; it < nk; ++it) {
     const int cur = it & 1;
     if (it + 1 < nk) gload(kbeg + (it + 1) * BK);
-    float4 av[TI], bv[TJ];
 #pragma unroll
-    for (int i = 0; i < TI; ++i) av[i] = *reinterpret_cast<const float4*>(&As[cur][(la + 16 * i) * PK + grp * 4]);
+    for (int q = 0; q < BK / 16; ++q) {
+      float4 av[TI], bv[TJ];
+      const int ko = grp * (BK / 4) + 4 * q;
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(&Bs[cur][(lb + 16 * j) * PK + grp * 4]);
+      for (int i = 0; i < TI; ++i) av[i] = *reinterpret_cast<const float4*>(&As[cur][(la + 16 * i) * PK + ko]);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+      for (int j = 0; j < TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(&Bs[cur][(lb + 16 * j) * PK + ko]);
 #pragma unroll
-      for (int i = 0; i < TI; ++i)
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
+    }
     if (it + 1 < nk) sstore(cur ^ 1);
     __syncthreads();
   }
@@ -524,7 +530,8 @@ __global__ void __launch_bounds__(256) fold_bn_kernel(int co, int per_out, const
 
 struct Tile {
   int bp, bq, wp, wq;
-  float eff;  // relative MFMA efficiency of the wave tile (operand reuse)
+  float eff;   // relative MFMA efficiency of the wave tile (operand reuse)
+  int bk = 16; // K-block (gather kernels)
 };
 
 // Picks the tile with the smallest estimated makespan: rounds of `slots` concurrent workgroups times the padded
@@ -546,9 +553,12 @@ static int pick_tile(const Tile (&tiles)[N], int64_t P, int64_t Q, int64_t z, in
   return best;
 }
 
+// The last three carry deeper K-blocks: more MFMA work per load round trip for grids of about one workgroup per CU,
+// where the loads' latency is not hidden by other workgroups.
 static const Tile kGatherTiles[] = {
-    {64, 256, 64, 64, 1.00f}, {128, 128, 64, 64, 1.00f}, {64, 128, 32, 64, 0.92f},
-    {32, 256, 32, 64, 0.90f}, {16, 256, 16, 64, 0.80f},  {64, 64, 32, 32, 0.80f},
+    {64, 256, 64, 64, 1.00f},     {128, 128, 64, 64, 1.00f},    {64, 128, 32, 64, 0.92f},
+    {32, 256, 32, 64, 0.90f},     {16, 256, 16, 64, 0.80f},     {64, 64, 32, 32, 0.80f},
+    {64, 64, 32, 32, 0.90f, 64},  {64, 128, 32, 64, 0.95f, 32}, {128, 64, 64, 32, 0.95f, 32},
 };
 static const Tile kWgradTiles[] = {
     {64, 128, 32, 64, 1.00f}, {128, 64, 32, 64, 1.00f}, {64, 64, 32, 32, 0.85f}, {32, 128, 16, 64, 0.85f},
@@ -559,17 +569,20 @@ constexpr int64_t kCUs = 256;
 template <int MODE, bool BN>
 static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
   switch (ti) {
-    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN>), grid, dim3(256), 0, s, a); break;
   }
 }
 
-// Tap-major order needs whole K-blocks of channels; the BN loader keeps the channel-major order.
-static bool gather_tap_major(int64_t c, bool bn) { return !bn && c % 16 == 0; }
+// Tap-major order needs whole K-blocks of channels (so K has no tail); the BN loader keeps the channel-major order.
+static bool gather_tap_major(int64_t c, bool bn, int bk) { return !bn && c % bk == 0; }
 
 // Tile and K split of a gather launch: P rows, Q columns (the largest phase), K the longest reduction, z phases.
 struct GatherPlan {
@@ -580,33 +593,37 @@ static const int kSliceChoices[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
 
 // Estimated makespan in clocks, over tiles and slice counts:
 // - workgroups run two per CU at ~34 fp32 FMA/clock each times the tile's efficiency, or ~1.6x that alone on a CU;
-// - each carries ~3 K-blocks of fixed cost (prologue, epilogue) and needs >= 6 K-blocks per slice to be worth a split;
+// - a K-block takes at least ~2000 clocks alone on a CU (~1000 with a second workgroup to hide behind): the operand
+//   loads' latency, which only deeper K-blocks amortize;
+// - each workgroup carries ~2 K-blocks of fixed cost (prologue, epilogue); a split needs >= 96 K per slice;
 // - a split pays the partial round trip through HBM (~1.7 KB/clock) and one more launch (~7000 clocks).
 // `fixed` (a tuned or requested plan) replaces the estimate: its slice count is rounded to whole K-blocks per slice.
 static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const omt_conv_plan* fixed) {
-  constexpr int BK = 16;
-  const int64_t nkb = cdiv(K > 0 ? K : 1, BK);
+  const int64_t kk = K > 0 ? K : 1;
   if (fixed) {
+    const int64_t nkb = cdiv(kk, kGatherTiles[fixed->tile].bk);
     const int64_t kb = cdiv(nkb, std::max<int64_t>(1, std::min<int64_t>(fixed->slices, nkb)));
-    return {fixed->tile, cdiv(nkb, kb), kb * BK};
+    return {fixed->tile, cdiv(nkb, kb), kb * kGatherTiles[fixed->tile].bk};
   }
-  GatherPlan best{0, 1, nkb * BK};
+  GatherPlan best{0, 1, cdiv(kk, 16) * 16};
   double best_cost = 1e300;
   for (int ti = 0; ti < (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0])); ++ti) {
     const Tile& tl = kGatherTiles[ti];
-    const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z;
+    const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(kk, tl.bk);
     for (int sc : kSliceChoices) {
       const int64_t kb = cdiv(nkb, sc);
-      if (sc > 1 && kb < 6) break;
+      if (sc > 1 && kb * tl.bk < 96) break;
       const int64_t slices = cdiv(nkb, kb);
       if (slices != sc) continue;
       const int64_t blocks = tiles * slices;
-      const double wg = (double)tl.bp * tl.bq * BK * (kb + 3) / (34.0 * tl.eff);
-      double cost = blocks <= kCUs ? wg / 1.6 : (double)cdiv(blocks, 2 * kCUs) * wg;
+      const bool alone = blocks <= kCUs;
+      const double blk = std::max((double)tl.bp * tl.bq * tl.bk / (34.0 * tl.eff) / (alone ? 1.6 : 1.0),
+                                  alone ? 2000.0 : 1000.0);
+      double cost = blk * (kb + 2) * (alone ? 1.0 : (double)cdiv(blocks, 2 * kCUs));
       if (slices > 1) cost += 7000.0 + (double)(2 * slices) * P * Q * z * 4 / 1700.0;
       if (cost < best_cost * 0.999) {
         best_cost = cost;
-        best = {ti, slices, kb * BK};
+        best = {ti, slices, kb * tl.bk};
       }
     }
   }
@@ -625,7 +642,7 @@ static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t ma
   dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
   if (a.bn_mean)
     gather_dispatch<kGeneric, true>(pl.tile, a, grid, s);
-  else if (gather_tap_major(a.C, a.bn_mean != nullptr))
+  else if (gather_tap_major(a.C, false, tl.bk))
     gather_dispatch<kTapMajor, false>(pl.tile, a, grid, s);
   else
     gather_dispatch<kGeneric, false>(pl.tile, a, grid, s);
@@ -729,22 +746,23 @@ static int num_tiles(int dir) {
 
 using namespace omt;
 
-// Forward workspace: the tap-major filter (C % 16 == 0, ks > 1), then, 256-byte aligned, the split-K partials.
-static size_t fwd_pack_bytes(const omt_conv_geo* g) {
-  if (g->ks == 1 || !gather_tap_major(g->ci, false)) return 0;
-  return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
-}
 static GatherPlan fwd_plan(const omt_conv_geo* g) {
   omt_conv_plan cp;
   const bool have = cached_plan(OMT_DIR_FWD, g, &cp);
   return gather_plan(g->co, g->n * g->oh * g->ow, g->ci * g->ks * g->ks, 1, have ? &cp : nullptr);
+}
+// Forward workspace: the tap-major filter (when the plan's K-block divides C and ks > 1), then, 256-byte aligned,
+// the split-K partials.
+static size_t fwd_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
+  if (g->ks == 1 || !gather_tap_major(g->ci, false, kGatherTiles[pl.tile].bk)) return 0;
+  return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
 OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
   if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
   const GatherPlan pl = fwd_plan(g);
   const size_t part = pl.slices > 1 ? (size_t)(pl.slices * g->n * g->co * g->oh * g->ow) * sizeof(float) : 0;
-  return part ? align256(fwd_pack_bytes(g)) + part : fwd_pack_bytes(g);
+  return part ? align256(fwd_pack_bytes(g, pl)) + part : fwd_pack_bytes(g, pl);
 }
 
 OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
@@ -767,7 +785,7 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   a.x = x;
   a.w = w;
   // tap-major order: re-pack the filter to [co][ky][kx][ci] (1x1 filters already are)
-  if (!bn && fwd_pack_bytes(g)) {
+  if (!bn && fwd_pack_bytes(g, pl)) {
     const int total = (int)(g->co * g->ci * g->ks * g->ks);
     hipLaunchKernelGGL(pack_tapmajor_kernel, dim3(grid1d(total, 256, 4096)), dim3(256), 0, s, w, (float*)workspace,
                        (int)g->co, (int)g->ci, (int)(g->ks * g->ks));
@@ -807,7 +825,7 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   p.div_kw = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather(a, pl, g->n, p.Q, (float*)((char*)workspace + align256(fwd_pack_bytes(g))), s);
+  return run_gather(a, pl, g->n, p.Q, (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl))), s);
 }
 
 // Stride-phase table of the grad-input GEMMs (see the top of this file).
@@ -886,7 +904,8 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   pk.CI = (int)g->ci;
   pk.KS = (int)g->ks;
   pk.S = (int)g->stride;
-  pk.tap_major = gather_tap_major(g->co, false) ? 1 : 0;
+  const GatherPlan pl = dgrad_plan(g);
+  pk.tap_major = gather_tap_major(g->co, false, kGatherTiles[pl.tile].bk) ? 1 : 0;
   hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
   if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
   a.x = gy;
@@ -901,7 +920,6 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   a.YH = (int)g->ih;
   a.YW = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
-  const GatherPlan pl = dgrad_plan(g);
   const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
   return run_gather(a, pl, g->n, maxq, (float*)((char*)workspace + align256(pack)), s);
 }
@@ -1078,10 +1096,9 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     for (int i = 0; i < a.nphase; ++i) K = std::max<int64_t>(K, a.ph[i].K);
     P = g->ci, z = a.nphase, plane = g->n * g->ci * g->ih * g->iw;
   }
-  const int64_t nkb = cdiv(std::max<int64_t>(K, 1), 16);
   for (int t = 0; t < ntile; ++t) {
     const Tile& tl = kGatherTiles[t];
-    const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z;
+    const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(std::max<int64_t>(K, 1), tl.bk);
     int64_t last = -1;
     for (int sc : {1, 2, 4, 8, 16, 32, 64}) {
       const int64_t kb = cdiv(nkb, sc), eff = cdiv(nkb, kb);

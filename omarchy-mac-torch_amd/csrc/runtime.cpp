@@ -6,6 +6,12 @@
 // when freed. Because every op of the operator layer runs on one stream, a parked block can be handed out again at
 // once: any later use is ordered after the earlier user's kernels on that stream. Callers that use several streams
 // must synchronize before freeing memory another stream still reads.
+//
+// Graph pools. While a graph is being captured, the memory its kernels touch must stay theirs for every replay. Between
+// omt_graph_pool_begin and omt_graph_pool_end every omt_malloc (from any thread: autograd runs backward on its own
+// thread) is served from that pool: from its own parked blocks, else a block moved over from the general free lists,
+// else hipMalloc. Blocks of a graph pool go back to that pool when freed, never to the general one, until
+// omt_graph_pool_release returns them all (after the graphs that use them are gone).
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -49,10 +55,19 @@ hipStream_t stream_of(void* s) { return (hipStream_t)s; }
 // ---- caching allocator -----------------------------------------------------------------------------------------
 
 namespace {
+struct GraphPool {
+  std::map<size_t, std::vector<void*>> free_lists;  // parked blocks of this pool
+  std::unordered_map<void*, size_t> owned;           // every block of this pool -> size class
+};
+
 struct Pool {
   std::mutex mu;
   std::map<size_t, std::vector<void*>> free_lists;  // size class -> parked blocks
   std::unordered_map<void*, size_t> live;            // block -> size class
+  std::map<int, GraphPool> graph_pools;
+  std::unordered_map<void*, int> graph_owner;        // block of a graph pool -> pool id
+  int active = 0;                                    // graph pool receiving allocations (0: none)
+  int next_id = 1;
   size_t allocated = 0;                              // bytes handed out
   size_t reserved = 0;                               // bytes held from HIP (live + parked)
   size_t limit = 0;                                  // 0 = no cap
@@ -77,6 +92,16 @@ Pool& pool() {
   static Pool* p = new Pool();  // never destroyed: blocks may be freed from static destructors of other libraries
   return *p;
 }
+
+// hipMalloc is a prohibited call while any thread captures a graph in global mode; allocating is still safe (it is no
+// stream operation), so the calling thread switches to relaxed capture mode around it.
+hipError_t malloc_relaxed(void** p, size_t bytes) {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  const hipError_t e = hipMalloc(p, bytes);
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  return e;
+}
 }  // namespace
 
 }  // namespace omt
@@ -96,22 +121,37 @@ OMT_EXPORT int omt_malloc(void** ptr, size_t bytes) {
   Pool& P = pool();
   size_t cls = Pool::size_class(bytes);
   std::lock_guard<std::mutex> lk(P.mu);
+  GraphPool* gp = P.active ? &P.graph_pools[P.active] : nullptr;
+  if (gp) {
+    auto git = gp->free_lists.find(cls);
+    if (git != gp->free_lists.end() && !git->second.empty()) {
+      *ptr = git->second.back();
+      git->second.pop_back();
+      P.live[*ptr] = cls;
+      P.allocated += cls;
+      return OMT_OK;
+    }
+  }
   auto it = P.free_lists.find(cls);
   if (it != P.free_lists.end() && !it->second.empty()) {
     *ptr = it->second.back();
     it->second.pop_back();
     P.live[*ptr] = cls;
     P.allocated += cls;
+    if (gp) {
+      gp->owned[*ptr] = cls;
+      P.graph_owner[*ptr] = P.active;
+    }
     return OMT_OK;
   }
   void* p = nullptr;
   bool over = P.limit && P.reserved + cls > P.limit;
-  hipError_t e = over ? hipErrorOutOfMemory : hipMalloc(&p, cls);
-  if (e != hipSuccess) {  // empty the cache once and retry (csrc/runtime.cpp:220-225)
+  hipError_t e = over ? hipErrorOutOfMemory : malloc_relaxed(&p, cls);
+  if (e != hipSuccess && !gp) {  // empty the cache once and retry (csrc/runtime.cpp:220-225); never while capturing
     (void)hipGetLastError();
     P.release_parked();
     over = P.limit && P.reserved + cls > P.limit;
-    e = over ? hipErrorOutOfMemory : hipMalloc(&p, cls);
+    e = over ? hipErrorOutOfMemory : malloc_relaxed(&p, cls);
     if (e != hipSuccess) {
       (void)hipGetLastError();
       *ptr = nullptr;
@@ -119,9 +159,18 @@ OMT_EXPORT int omt_malloc(void** ptr, size_t bytes) {
                   P.limit);
     }
   }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    *ptr = nullptr;
+    return fail(OMT_OOM, "out of device memory allocating %zu bytes in a graph pool", cls);
+  }
   P.reserved += cls;
   P.allocated += cls;
   P.live[p] = cls;
+  if (gp) {
+    gp->owned[p] = cls;
+    P.graph_owner[p] = P.active;
+  }
   *ptr = p;
   return OMT_OK;
 }
@@ -135,7 +184,49 @@ OMT_EXPORT int omt_free(void* ptr) {
   size_t cls = it->second;
   P.live.erase(it);
   P.allocated -= cls;
-  P.free_lists[cls].push_back(ptr);
+  auto g = P.graph_owner.find(ptr);
+  if (g != P.graph_owner.end())
+    P.graph_pools[g->second].free_lists[cls].push_back(ptr);
+  else
+    P.free_lists[cls].push_back(ptr);
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_graph_pool_create(void) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  const int id = P.next_id++;
+  P.graph_pools[id];
+  return id;
+}
+
+OMT_EXPORT int omt_graph_pool_begin(int id) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  if (!P.graph_pools.count(id)) return fail(OMT_INVALID, "omt_graph_pool_begin: no graph pool %d", id);
+  if (P.active) return fail(OMT_INVALID, "omt_graph_pool_begin: graph pool %d is already receiving", P.active);
+  P.active = id;
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_graph_pool_end(void) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.active = 0;
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_graph_pool_release(int id) {
+  Pool& P = pool();
+  std::lock_guard<std::mutex> lk(P.mu);
+  auto it = P.graph_pools.find(id);
+  if (it == P.graph_pools.end()) return fail(OMT_INVALID, "omt_graph_pool_release: no graph pool %d", id);
+  if (P.active == id) return fail(OMT_INVALID, "omt_graph_pool_release: pool %d is receiving allocations", id);
+  OMT_HIP(hipDeviceSynchronize());  // no replay may still use the blocks
+  for (auto& kv : it->second.free_lists)
+    for (void* b : kv.second) P.free_lists[kv.first].push_back(b);
+  for (auto& kv : it->second.owned) P.graph_owner.erase(kv.first);  // live blocks return to the general pool when freed
+  P.graph_pools.erase(it);
   return OMT_OK;
 }
 

@@ -63,6 +63,10 @@ SIGNATURES = {
     "omt_memcpy": (I32, [VP, VP, SZ, I32, VP]),
     "omt_memset_zero": (I32, [VP, SZ, VP]),
     "omt_stream_sync": (I32, [VP]),
+    "omt_graph_pool_create": (I32, []),
+    "omt_graph_pool_begin": (I32, [I32]),
+    "omt_graph_pool_end": (I32, []),
+    "omt_graph_pool_release": (I32, [I32]),
     "omt_event_create": (I32, [ctypes.POINTER(VP)]),
     "omt_event_destroy": (I32, [VP]),
     "omt_event_record": (I32, [VP, VP]),

@@ -284,23 +284,38 @@ static Tensor& set_storage(Tensor& self, c10::Storage src, int64_t off, IntArray
 // device guard: one device, torch's current HIP stream, HIP events
 // ------------------------------------------------------------------------------------------------------------------
 
+// The device's streams are torch's HIP streams under another device type: a device Stream carries the HIP stream's
+// id, and making it current makes that HIP stream current. The autograd engine records the forward's stream and makes
+// it current on its backward thread, so backward kernels follow the forward's stream (a capturing one included).
+static c10::Stream as_dev_stream(const c10::hip::HIPStream& h) {
+  return c10::Stream(c10::Stream::UNSAFE, c10::Device(kDev, 0), h.id());
+}
+static c10::hip::HIPStream as_hip_stream(const c10::Stream& s) {
+  return c10::hip::HIPStream::unpack3(s.id(), 0, c10::DeviceType::HIP);
+}
+
 struct Guard final : c10::impl::DeviceGuardImplInterface {
   c10::DeviceType type() const override { return kDev; }
   c10::Device exchangeDevice(c10::Device) const override { return {kDev, 0}; }
   c10::Device getDevice() const override { return {kDev, 0}; }
   void setDevice(c10::Device) const override {}
   void uncheckedSetDevice(c10::Device) const noexcept override {}
-  c10::Stream getStream(c10::Device d) const noexcept override { return c10::Stream(c10::Stream::DEFAULT, d); }
-  c10::Stream getDefaultStream(c10::Device d) const override { return c10::Stream(c10::Stream::DEFAULT, d); }
-  c10::Stream getNewStream(c10::Device d, int) const override { return c10::Stream(c10::Stream::DEFAULT, d); }
-  c10::Stream exchangeStream(c10::Stream s) const noexcept override { return s; }
-  c10::DeviceIndex deviceCount() const noexcept override { return 1; }
-  void record(void** event, const c10::Stream&, const c10::DeviceIndex, const c10::EventFlag) const override {
-    if (!*event) TORCH_CHECK(omt_event_create(event) == OMT_OK, omt_last_error());
-    TORCH_CHECK(omt_event_record(*event, cur_stream()) == OMT_OK, omt_last_error());
+  c10::Stream getStream(c10::Device) const noexcept override { return as_dev_stream(c10::hip::getCurrentHIPStream(0)); }
+  c10::Stream getDefaultStream(c10::Device) const override { return as_dev_stream(c10::hip::getDefaultHIPStream(0)); }
+  // streams keep the default priority whatever is asked (mixed priorities are avoided on these GPUs)
+  c10::Stream getNewStream(c10::Device, int) const override { return as_dev_stream(c10::hip::getStreamFromPool(false, 0)); }
+  c10::Stream exchangeStream(c10::Stream s) const noexcept override {
+    const c10::Stream prev = as_dev_stream(c10::hip::getCurrentHIPStream(0));
+    c10::hip::setCurrentHIPStream(as_hip_stream(s));
+    return prev;
   }
-  void block(void* event, const c10::Stream&) const override {
-    if (event) TORCH_CHECK(hipStreamWaitEvent((hipStream_t)cur_stream(), (hipEvent_t)event, 0) == hipSuccess);
+  c10::DeviceIndex deviceCount() const noexcept override { return 1; }
+  void record(void** event, const c10::Stream& s, const c10::DeviceIndex, const c10::EventFlag) const override {
+    if (!*event) TORCH_CHECK(omt_event_create(event) == OMT_OK, omt_last_error());
+    TORCH_CHECK(omt_event_record(*event, as_hip_stream(s).stream()) == OMT_OK, omt_last_error());
+  }
+  void block(void* event, const c10::Stream& s) const override {
+    if (event) TORCH_CHECK(hipStreamWaitEvent(as_hip_stream(s).stream(), (hipEvent_t)event, 0) == hipSuccess);
   }
   bool queryEvent(void* event) const override { return !event || omt_event_query(event) == 1; }
   void destroyEvent(void* event, const c10::DeviceIndex) const noexcept override {
@@ -309,11 +324,11 @@ struct Guard final : c10::impl::DeviceGuardImplInterface {
   void synchronizeEvent(void* event) const override {
     if (event) TORCH_CHECK(omt_event_sync(event) == OMT_OK, omt_last_error());
   }
-  bool queryStream(const c10::Stream&) const override {
-    return hipStreamQuery((hipStream_t)cur_stream()) == hipSuccess;
+  bool queryStream(const c10::Stream& s) const override {
+    return hipStreamQuery(as_hip_stream(s).stream()) == hipSuccess;
   }
-  void synchronizeStream(const c10::Stream&) const override {
-    TORCH_CHECK(omt_stream_sync(cur_stream()) == OMT_OK, omt_last_error());
+  void synchronizeStream(const c10::Stream& s) const override {
+    TORCH_CHECK(omt_stream_sync(as_hip_stream(s).stream()) == OMT_OK, omt_last_error());
   }
   void synchronizeDevice(const c10::DeviceIndex) const override {
     TORCH_CHECK(hipDeviceSynchronize() == hipSuccess, "hipDeviceSynchronize failed");

@@ -39,6 +39,14 @@ PYBIND11_MODULE(_native, m) {
     set_count_delegated(on);
     if (!on) delegated_counts().clear();
   });
+  m.def("graph_pool_create", []() { return omt_graph_pool_create(); });
+  m.def("graph_pool_begin", [](int id) {
+    TORCH_CHECK(omt_graph_pool_begin(id) == OMT_OK, "omarchy-mac-torch: ", omt_last_error());
+  });
+  m.def("graph_pool_end", []() { omt_graph_pool_end(); });
+  m.def("graph_pool_release", [](int id) {
+    TORCH_CHECK(omt_graph_pool_release(id) == OMT_OK, "omarchy-mac-torch: ", omt_last_error());
+  });
   m.def("set_debug", [](bool on) { set_debug_mode(on); });
   m.def("strict", []() { return strict_mode(); });
   m.def("abi_version", []() { return omt_abi_version(); });

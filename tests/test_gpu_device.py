@@ -161,6 +161,70 @@ def test_foreach_lists_and_fused_optimizers(clean):
             assert rel(pd, pc) <= 1e-5, cls
 
 
+def test_graph_replay_of_a_training_step(clean):
+    """A whole training step (forward, backward, fused Adam with capturable=True) captured once as a HIP graph and
+    replayed on new batches matches the same steps run eagerly, replay after replay, with eager device work and host
+    synchronization between the replays; BN running statistics follow too."""
+    omt = clean
+    torch.manual_seed(7)
+    base = nn.Sequential(nn.Conv2d(3, 16, 3, padding=1, bias=False), nn.BatchNorm2d(16), nn.ReLU(), nn.MaxPool2d(2),
+                         nn.Conv2d(16, 32, 3, stride=2, padding=1, bias=False), nn.BatchNorm2d(32), nn.ReLU(),
+                         nn.AdaptiveAvgPool2d(1), nn.Flatten(), nn.Linear(32, 10))
+    g = torch.Generator().manual_seed(8)
+    data = [(torch.randn(8, 3, 16, 16, generator=g), torch.randint(0, 10, (8,), generator=g)) for _ in range(8)]
+
+    def make():
+        m = copy.deepcopy(base).to(omt.DEVICE)
+        return m, torch.optim.Adam(m.parameters(), lr=1e-2, capturable=True)
+
+    eager, opt_e = make()
+    ref = []
+    for x, t in data:
+        opt_e.zero_grad(set_to_none=True)
+        loss = F.cross_entropy(eager(D(x, omt)), D(t, omt))
+        loss.backward()
+        opt_e.step()
+        ref.append(loss.item())
+
+    model, opt = make()
+    sx = torch.empty(8, 3, 16, 16, device=omt.DEVICE)
+    st = torch.empty(8, dtype=torch.long, device=omt.DEVICE)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = F.cross_entropy(model(sx), st)
+        loss.backward()
+        opt.step()
+        return loss.detach()
+
+    got = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up steps, eager
+        for x, t in data[:3]:
+            sx.copy_(x)
+            st.copy_(t)
+            got.append(step().item())
+    torch.cuda.current_stream().wait_stream(side)
+    omt.empty_cache()  # the capture then allocates afresh (hipMalloc while capturing)
+    graph = omt.graphs.Graph()
+    with graph.capture():
+        static_loss = step()
+    for x, t in data[3:]:
+        sx.copy_(x)
+        st.copy_(t)
+        graph.replay()
+        got.append(static_loss.item())
+        assert (D(torch.ones(1000), omt) * 2).sum().item() == 2000.0  # eager work between replays
+    for a, b in zip(got, ref):
+        assert abs(a - b) <= 1e-5 * abs(b), (got, ref)
+    for (n, pa), (_, pb) in zip(model.named_parameters(), eager.named_parameters()):
+        assert rel(pa, pb) <= 1e-5, n
+    for (n, ba), (_, bb) in zip(model.named_buffers(), eager.named_buffers()):
+        assert rel(ba.float(), bb.float()) <= 1e-5, n
+    graph.release()
+
+
 def test_uncovered_conv_falls_back_and_is_recorded(clean):
     omt = clean
     x, w = torch.randn(2, 4, 11, 11), torch.randn(6, 4, 3, 3)
