@@ -130,6 +130,76 @@ def torch_cpu_baseline(layers, batch, threads):
                       f"at batch {batch}, {cpu_info()}"}
 
 
+def bandwidth_kernels(dev, reps=20):
+    """The HBM-bound kernels of the path on shapes from the BASELINE configs: achieved GB/s from algorithmic
+    (compulsory) bytes -- each input read once, each output written once, fp32, int64 pool indices -- over the op's
+    HIP-event time on its launch stream (all of the op's launches: BN's statistics, finalize and apply passes)."""
+    import torch
+
+    from omarchy_mac_torch import hip_ops as H
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape):
+        return torch.randn(shape, device=dev, generator=gen)
+
+    def nbytes(*ts):
+        return sum(t.numel() * t.element_size() for t in ts)
+
+    cases = []
+    # depthwise (config 4, MobileNetV3-Small-style, b32): 3x3 at 72 x 56^2 and 5x5 at 96 x 28^2, stride 1 "same"
+    for (n, c, h, ks) in ((32, 72, 56, 3), (32, 96, 28, 5)):
+        x, w = rnd(n, c, h, h), rnd(c, 1, ks, ks)
+        y = H.depthwise_conv2d(x, w, None, 1, ks // 2)
+        gy = rnd(*y.shape)
+        gx = H.depthwise_dgrad(gy, w, x.shape, 1, ks // 2)
+        gw = H.depthwise_wgrad(x, gy, ks, 1, ks // 2)
+        tag = f"dw{ks}x{ks} [{n},{c},{h},{h}]"
+        cases += [(f"{tag} fwd", lambda x=x, w=w, ks=ks: H.depthwise_conv2d(x, w, None, 1, ks // 2), nbytes(x, w, y)),
+                  (f"{tag} dgrad", lambda gy=gy, w=w, x=x, ks=ks: H.depthwise_dgrad(gy, w, x.shape, 1, ks // 2),
+                   nbytes(gy, w, gx)),
+                  (f"{tag} wgrad", lambda x=x, gy=gy, ks=ks: H.depthwise_wgrad(x, gy, ks, 1, ks // 2),
+                   nbytes(x, gy, gw))]
+    # BatchNorm(+ReLU) train forward / backward: config 2's largest [128,32,32^2] and ResNet-50's [256,64,56^2]
+    for (n, c, h) in ((128, 32, 32), (256, 64, 56)):
+        x, gam, bet, rm, rv = rnd(n, c, h, h), rnd(c), rnd(c), rnd(c), rnd(c).abs() + 0.5
+        y, sm, si = H.batch_norm_train(x, gam, bet, rm, rv, relu=True)
+        g = rnd(n, c, h, h)
+        tag = f"bn+relu [{n},{c},{h},{h}]"
+        cases += [(f"{tag} train fwd", lambda x=x, gam=gam, bet=bet, rm=rm, rv=rv: H.batch_norm_train(
+                       x, gam, bet, rm, rv, relu=True), 2 * nbytes(x)),
+                  (f"{tag} bwd", lambda g=g, x=x, sm=sm, si=si, gam=gam, y=y: H.batch_norm_backward(
+                       g, x, sm, si, gam, relu_y=y), 4 * nbytes(x))]
+    # max pools: config 2's 2x2 on [128,32,32^2], config 3's stem 3x3 s2 p1 on [32,64,32^2]
+    for (n, c, h, k, st, pd) in ((128, 32, 32, 2, 2, 0), (32, 64, 32, 3, 2, 1)):
+        x = rnd(n, c, h, h)
+        y, idx = H.max_pool2d(x, k, st, pd)
+        g = rnd(*y.shape)
+        tag = f"maxpool{k}x{k}s{st} [{n},{c},{h},{h}]"
+        cases += [(f"{tag} fwd", lambda x=x, k=k, st=st, pd=pd: H.max_pool2d(x, k, st, pd), nbytes(x, y, idx)),
+                  (f"{tag} bwd", lambda g=g, x=x, idx=idx, k=k, st=st, pd=pd: H.max_pool2d_backward(
+                       g, x.shape, idx, k, st, pd), nbytes(g, idx, x))]
+    # global average pool (ResNet-50 head, b256)
+    x = rnd(256, 2048, 7, 7)
+    cases.append(("gap [256,2048,7,7] fwd", lambda x=x: H.adaptive_avg_pool2d(x, 1), nbytes(x) + 256 * 2048 * 4))
+
+    stream = torch.cuda.current_stream(dev)
+    out = []
+    for name, fn, b in cases:
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        out.append({"op": name, "bytes": b, "us": round(us, 2), "GB/s": round(b / us / 1e3, 1),
+                    "frac_of_hbm_peak": round(b / (us * 1e-6) / PEAK_HBM, 3)})
+    return out
+
+
 def pmc_probe(layers, dev):
     """A 1 GiB device-to-device copy (1 GiB read + 1 GiB written: the FETCH_SIZE / WRITE_SIZE calibration launch),
     then one forward conv per layer, each on its own freshly written input."""
@@ -273,8 +343,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["c5", "c1", "resnet"], default="c5",
-                    help="resnet: only the ResNet-18 training-step measurement (for profiling)")
+    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "bw"], default="c5",
+                    help="resnet: only the ResNet-18 training-step measurement; bw: only the HBM-bound kernels "
+                         "(both for profiling)")
+    ap.add_argument("--no-bw", action="store_true", help="skip the HBM-bound kernel measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-resnet", action="store_true", help="skip the ResNet-18 training-step measurement")
     ap.add_argument("--resnet-steps", type=int, default=20)
@@ -299,6 +371,9 @@ def main():
 
         print(json.dumps({"resnet18_b32": resnet18_step(omarchy_mac_torch.DEVICE, args.resnet_steps, 5, 5,
                                                           not args.no_cpu)}), flush=True)
+        return
+    if args.workload == "bw":
+        print(json.dumps({"bandwidth_kernels": bandwidth_kernels(dev)}), flush=True)
         return
     layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
     if args.pmc_probe:
@@ -406,6 +481,8 @@ def main():
         "plans": {"tuned": not args.no_tune, "tile_slices": plans},
         "device": torch.cuda.get_device_name(dev),
     }
+    if not args.no_bw:
+        out["bandwidth_kernels"] = bandwidth_kernels(dev)
     if not args.no_resnet:
         import omarchy_mac_torch  # noqa: F401  (registers the device)
 

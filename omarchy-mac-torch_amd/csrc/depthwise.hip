@@ -1,5 +1,12 @@
 // Depthwise convolution (groups = C, one ks x ks filter per channel): any ks <= 11, stride 1..4, 0 <= pad <= ks.
-// These are HBM-bandwidth-bound (ks^2 FLOPs per loaded element), so they run as plain wave64 kernels:
+// These are HBM-bandwidth-bound (ks^2 FLOPs per loaded element).
+//
+// Stride 1 with "same" padding and ks 3, 5 or 7 (every depthwise layer of the benchmark configurations) runs LDS-tiled:
+// a workgroup owns a chunk of R output rows of one (image, channel) plane, stages the R + ks - 1 input rows it reads
+// (zero outside the plane) in LDS with ks/2 zero columns either side, keeps the plane's filter in registers and writes
+// its outputs contiguously. Grad input is the same correlation over gy with the filter flipped (same padding). Grad
+// weight stages x the same way per (channel, image slice) and accumulates all ks^2 taps in registers; the slices are
+// summed in order. Every other geometry uses plain wave64 kernels:
 //  - forward: one thread per output element, the filter in registers (reference dw_fwd / dwg_fwd / dw_fwd_bn,
 //    csrc/conv.cpp:194-198, csrc/plans.cpp:145-158), optional previous-layer eval BN + ReLU on in-bounds taps;
 //  - grad input: one thread per input element, keeping the taps that land on the stride grid (dw_gin / dwg_gin);
@@ -139,6 +146,172 @@ __global__ void __launch_bounds__(256) dw_wgrad_reduce_kernel(const float* __res
   }
 }
 
+// ---- stride 1, "same" padding, ks 3 / 5 / 7: LDS-tiled -----------------------------------------------------------
+
+struct DwTiling {
+  int rows;    // output rows per work unit
+  int chunks;  // work units per plane
+  int pitch;   // LDS row pitch: W + ks - 1
+  FastDiv div_w, div_chunks;
+};
+
+template <int NT>
+__device__ __forceinline__ void dw_stage_rows(float* __restrict__ tile, const float* __restrict__ src_plane, int r0,
+                                              int rows, int H, int W, int pitch, int pad, bool bn, float sc,
+                                              float sh) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int rr = wave; rr < rows; rr += NW) {
+    const int iy = r0 - pad + rr;
+    const bool row_ok = (unsigned)iy < (unsigned)H;
+    for (int cc = lane; cc < pitch; cc += 64) {
+      const int ix = cc - pad;
+      float v = 0.f;
+      if (row_ok && (unsigned)ix < (unsigned)W) {
+        v = src_plane[(int64_t)iy * W + ix];
+        if (bn) v = fmaxf(fmaf(v, sc, sh), 0.f);  // padding stays zero: BN + ReLU of in-bounds taps only
+      }
+      tile[rr * pitch + cc] = v;
+    }
+  }
+}
+
+// FLIP: grad input (gy in, filter flipped, no bias / BN).
+template <int KS, bool FLIP, int NT>
+__global__ void __launch_bounds__(NT) dw_s1_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                   const float* __restrict__ bias, const float* __restrict__ bm,
+                                                   const float* __restrict__ bv, const float* __restrict__ bg,
+                                                   const float* __restrict__ bb, float eps, float* __restrict__ y,
+                                                   int C, int H, int W, const DwTiling t) {
+  extern __shared__ float tile[];
+  constexpr int PAD = KS / 2, KK = KS * KS;
+  const int plane = (int)fdiv(blockIdx.x, t.div_chunks), chunk = (int)blockIdx.x - plane * t.chunks;
+  const int ch = plane % C;
+  const int r0 = chunk * t.rows, R = min(t.rows, H - r0);
+  const int64_t pbase = (int64_t)plane * H * W;
+  float sc = 1.f, sh = 0.f;
+  const bool bn = !FLIP && bm != nullptr;
+  if (bn) {
+    const float inv = rsqrtf(bv[ch] + eps);
+    sc = inv * bg[ch];
+    sh = bb[ch] - bm[ch] * sc;
+  }
+  dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, t.pitch, PAD, bn, sc, sh);
+  float wr[KK];
+#pragma unroll
+  for (int i = 0; i < KK; ++i) wr[i] = w[ch * KK + (FLIP ? KK - 1 - i : i)];
+  const float b = (!FLIP && bias) ? bias[ch] : 0.f;
+  __syncthreads();
+  float* yp = y + pbase + (int64_t)r0 * W;
+  const int nout = R * W, pitch = t.pitch;
+  for (int o = threadIdx.x; o < nout; o += NT) {
+    const int r = (int)fdiv((uint32_t)o, t.div_w), c = o - r * W;
+    const float* tp = tile + r * pitch + c;
+    float acc = 0.f;
+#pragma unroll
+    for (int ky = 0; ky < KS; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < KS; ++kx) acc = fmaf(tp[ky * pitch + kx], wr[ky * KS + kx], acc);
+    yp[o] = acc + b;
+  }
+}
+
+// grid (C, slices): slice sl reduces images sl, sl + slices, ... of channel blockIdx.x into part[sl][ch][KK].
+template <int KS, int NT>
+__global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict__ x, const float* __restrict__ gy,
+                                                         float* __restrict__ part, int N, int C, int H, int W,
+                                                         const DwTiling t) {
+  extern __shared__ float tile[];
+  constexpr int PAD = KS / 2, KK = KS * KS, NW = NT / 64;
+  __shared__ float red[NW][KK];
+  const int ch = blockIdx.x, sl = blockIdx.y, slices = gridDim.y, pitch = t.pitch;
+  float acc[KK];
+#pragma unroll
+  for (int i = 0; i < KK; ++i) acc[i] = 0.f;
+  for (int n = sl; n < N; n += slices) {
+    const int64_t pbase = ((int64_t)n * C + ch) * H * W;
+    for (int chunk = 0; chunk < t.chunks; ++chunk) {
+      const int r0 = chunk * t.rows, R = min(t.rows, H - r0);
+      __syncthreads();  // the previous chunk's tile is consumed
+      dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, pitch, PAD, false, 1.f, 0.f);
+      __syncthreads();
+      const float* gp = gy + pbase + (int64_t)r0 * W;
+      const int nout = R * W;
+      for (int o = threadIdx.x; o < nout; o += NT) {
+        const int r = (int)fdiv((uint32_t)o, t.div_w), c = o - r * W;
+        const float gv = gp[o];
+        const float* tp = tile + r * pitch + c;
+#pragma unroll
+        for (int ky = 0; ky < KS; ++ky)
+#pragma unroll
+          for (int kx = 0; kx < KS; ++kx) acc[ky * KS + kx] = fmaf(gv, tp[ky * pitch + kx], acc[ky * KS + kx]);
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < KK; ++i) {
+    float v = acc[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) red[wave][i] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < KK; i += NT) {
+    float v = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) v += red[wv][i];
+    part[((int64_t)sl * C + ch) * KK + i] = v;
+  }
+}
+
+constexpr int kDwMaxLds = 64 * 1024;
+
+// ~8 outputs per thread; one wave for planes of up to 128 outputs.
+static DwTiling dw_tiling(int H, int W, int ks, int nt) {
+  DwTiling t;
+  int rows = (nt * 8) / W;
+  rows = rows < 1 ? 1 : rows > H ? H : rows;
+  t.rows = rows;
+  t.chunks = (int)cdiv(H, rows);
+  t.pitch = W + ks - 1;
+  t.div_w = make_fastdiv((uint32_t)W);
+  t.div_chunks = make_fastdiv((uint32_t)t.chunks);
+  return t;
+}
+static int dw_threads(const omt_conv_geo* g) { return g->ih * g->iw <= 128 ? 64 : 256; }
+static size_t dw_lds(const DwTiling& t, int ks) { return (size_t)(t.rows + ks - 1) * t.pitch * sizeof(float); }
+
+static bool dw_s1(const omt_conv_geo* g) {
+  if (g->stride != 1 || g->pad != g->ks / 2 || !(g->ks == 3 || g->ks == 5 || g->ks == 7)) return false;
+  if (g->n * g->ci >= ((int64_t)1 << 31)) return false;
+  return dw_lds(dw_tiling((int)g->ih, (int)g->iw, (int)g->ks, dw_threads(g)), (int)g->ks) <= (size_t)kDwMaxLds;
+}
+// (C, slices) grid of the tiled grad weight: about 1024 workgroups, at most one slice per image
+static int64_t dw_s1_slices(const omt_conv_geo* g) {
+  int64_t s = cdiv(1024, g->ci);
+  return s > g->n ? g->n : s < 1 ? 1 : s;
+}
+
+template <bool FLIP>
+static int launch_dw_s1(const omt_conv_geo* g, const float* x, const float* w, const float* bias, const float* bm,
+                        const float* bv, const float* bg, const float* bb, float eps, float* y, hipStream_t s) {
+  const int nt = dw_threads(g), ks = (int)g->ks;
+  const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, ks, nt);
+  const dim3 grid((unsigned)(g->n * g->ci * t.chunks));
+  const size_t lds = dw_lds(t, ks);
+  const int C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
+#define OMT_DW_S1(KS_, NT_) \
+  hipLaunchKernelGGL((dw_s1_kernel<KS_, FLIP, NT_>), grid, dim3(NT_), lds, s, x, w, bias, bm, bv, bg, bb, eps, y, C, H, W, t)
+  if (nt == 64) {
+    if (ks == 3) OMT_DW_S1(3, 64); else if (ks == 5) OMT_DW_S1(5, 64); else OMT_DW_S1(7, 64);
+  } else {
+    if (ks == 3) OMT_DW_S1(3, 256); else if (ks == 5) OMT_DW_S1(5, 256); else OMT_DW_S1(7, 256);
+  }
+#undef OMT_DW_S1
+  return launch_check("dw_s1_kernel");
+}
+
 static bool dw_ok(const omt_conv_geo* g) {
   const int64_t lim = (int64_t)1 << 31;
   return g->ci == g->co && g->n >= 1 && g->ci >= 1 && g->ks >= 1 && g->ks <= 11 && g->stride >= 1 &&
@@ -171,6 +344,9 @@ OMT_EXPORT int omt_dw_fwd(const omt_conv_geo* g, const float* x, const float* w,
   if (!dw_ok(g)) return fail(OMT_UNSUPPORTED, "omt_dw_fwd: geometry not covered");
   const bool bn = bn_mean || bn_var || bn_gamma || bn_beta;
   if (bn && !(bn_mean && bn_var && bn_gamma && bn_beta)) return fail(OMT_INVALID, "omt_dw_fwd: incomplete BN loader");
+  if (dw_s1(g))
+    return launch_dw_s1<false>(g, x, w, bias, bn ? bn_mean : nullptr, bn_var, bn_gamma, bn_beta, bn_eps, y,
+                               stream_of(stream));
   const int64_t total = g->n * g->co * g->oh * g->ow;
   hipLaunchKernelGGL(dw_fwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), x, w, bias,
                      bn ? bn_mean : nullptr, bn_var, bn_gamma, bn_beta, bn_eps, y, total, dgeo(g));
@@ -180,6 +356,8 @@ OMT_EXPORT int omt_dw_fwd(const omt_conv_geo* g, const float* x, const float* w,
 OMT_EXPORT int omt_dw_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* stream) {
   if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_dw_dgrad: null pointer");
   if (!dw_ok(g)) return fail(OMT_UNSUPPORTED, "omt_dw_dgrad: geometry not covered");
+  if (dw_s1(g))
+    return launch_dw_s1<true>(g, gy, w, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, gx, stream_of(stream));
   const int64_t total = g->n * g->ci * g->ih * g->iw;
   hipLaunchKernelGGL(dw_dgrad_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), gy, w, gx, total,
                      dgeo(g));
@@ -188,7 +366,7 @@ OMT_EXPORT int omt_dw_dgrad(const omt_conv_geo* g, const float* gy, const float*
 
 OMT_EXPORT size_t omt_dw_wgrad_workspace(const omt_conv_geo* g) {
   if (!g || !dw_ok(g)) return 0;
-  return (size_t)(dw_slices(g) * g->ci * g->ks * g->ks) * sizeof(float);
+  return (size_t)((dw_s1(g) ? dw_s1_slices(g) : dw_slices(g)) * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
 OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
@@ -198,6 +376,28 @@ OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* 
   if (!workspace || workspace_bytes < omt_dw_wgrad_workspace(g))
     return fail(OMT_INVALID, "omt_dw_wgrad: workspace of %zu bytes needed", omt_dw_wgrad_workspace(g));
   hipStream_t s = stream_of(stream);
+  if (dw_s1(g)) {
+    const int nt = dw_threads(g), ks = (int)g->ks;
+    const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, ks, nt);
+    const int64_t slices = dw_s1_slices(g);
+    const dim3 grid((unsigned)g->ci, (unsigned)slices);
+    const size_t lds = dw_lds(t, ks);
+    const int N = (int)g->n, C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
+    float* part = (float*)workspace;
+#define OMT_DW_WG(KS_, NT_) \
+  hipLaunchKernelGGL((dw_wgrad_s1_kernel<KS_, NT_>), grid, dim3(NT_), lds, s, x, gy, part, N, C, H, W, t)
+    if (nt == 64) {
+      if (ks == 3) OMT_DW_WG(3, 64); else if (ks == 5) OMT_DW_WG(5, 64); else OMT_DW_WG(7, 64);
+    } else {
+      if (ks == 3) OMT_DW_WG(3, 256); else if (ks == 5) OMT_DW_WG(5, 256); else OMT_DW_WG(7, 256);
+    }
+#undef OMT_DW_WG
+    if (int st = launch_check("dw_wgrad_s1_kernel")) return st;
+    const int n = (int)(g->ci * ks * ks);
+    hipLaunchKernelGGL(dw_wgrad_reduce_kernel, dim3(grid1d(n, 256, 4096)), dim3(256), 0, s, (const float*)part, gw,
+                       n, (int)slices);
+    return launch_check("dw_wgrad_reduce_kernel");
+  }
   const int64_t slices = dw_slices(g);
   const int per_slice = (int)cdiv(g->n * g->oh * g->ow, slices);
   dim3 grid((unsigned)g->ci, (unsigned)slices);

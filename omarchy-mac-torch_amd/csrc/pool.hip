@@ -2,7 +2,9 @@
 // average (PyTorch divisor rules) and adaptive average. Backward passes gather rather than scatter: each input
 // element sums the gradients of the outputs that selected or covered it, visiting those outputs in row-major order,
 // which is the order PyTorch's CPU backward scatters them in, so no atomics are needed and the sums are
-// deterministic. One thread per output (forward) or input (backward) element; HBM-bandwidth-bound.
+// deterministic. One thread per output (forward) or input (backward) element; HBM-bandwidth-bound. Tensors below 2^32
+// elements decompose flat indices with 32-bit multiply-high division (the I32 kernels); larger ones with 64-bit
+// arithmetic. Global average pooling stages small planes through LDS (one thread per plane, coalesced loads).
 // Reference kernels: maxpool_gen_fwd/bwd, avgpool_gen_fwd/bwd, adapool_fwd/bwd (csrc/nn.cpp:157-222).
 #include "omt_internal.h"
 
@@ -10,13 +12,37 @@ namespace omt {
 
 struct PoolGeo {
   int ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw;
+  FastDiv d_ow, d_ohw, d_iw, d_ihw, d_sh, d_sw;
 };
 
+struct Pos {
+  int64_t plane;
+  int y, x;
+};
+// (plane, row, col) of flat index i over planes of W columns and HW elements
+template <bool I32>
+__device__ __forceinline__ Pos decompose(int64_t i, int W, int HW, const FastDiv& dw, const FastDiv& dhw) {
+  if (I32) {
+    const uint32_t u = (uint32_t)i, pl = fdiv(u, dhw), r = u - pl * (uint32_t)HW, y = fdiv(r, dw);
+    return {(int64_t)pl, (int)y, (int)(r - y * (uint32_t)W)};
+  }
+  const int64_t pl = i / HW;
+  const int r = (int)(i - pl * HW);
+  return {pl, r / W, r % W};
+}
+// q = t / d when d divides t exactly (t >= 0), else -1
+__device__ __forceinline__ int exact_div(int t, int d, const FastDiv& fd) {
+  const int q = (int)fdiv((uint32_t)t, fd);
+  return q * d == t ? q : -1;
+}
+
+template <bool I32>
 __global__ void __launch_bounds__(256) maxpool_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                           int64_t* __restrict__ idx, int64_t total, PoolGeo g) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int ox = (int)(i % g.ow), oy = (int)((i / g.ow) % g.oh);
-    const int64_t plane = i / ((int64_t)g.ow * g.oh);
+    const Pos o = decompose<I32>(i, g.ow, g.oh * g.ow, g.d_ow, g.d_ohw);
+    const int ox = o.x, oy = o.y;
+    const int64_t plane = o.plane;
     const float* xp = x + plane * g.ih * g.iw;
     float best = -INFINITY;
     int bi = -1;
@@ -39,25 +65,27 @@ __global__ void __launch_bounds__(256) maxpool_fwd_kernel(const float* __restric
 }
 
 // Output rows oy whose window row ky lands on input row r: oy * s - p + ky * d = r. Visits oy ascending.
+template <bool I32>
 __global__ void __launch_bounds__(256) maxpool_bwd_kernel(const float* __restrict__ g, const int64_t* __restrict__ idx,
                                                           float* __restrict__ gx, int64_t total, PoolGeo q) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int xx = (int)(i % q.iw), yy = (int)((i / q.iw) % q.ih);
-    const int64_t plane = i / ((int64_t)q.iw * q.ih);
+    const Pos in = decompose<I32>(i, q.iw, q.ih * q.iw, q.d_iw, q.d_ihw);
+    const int xx = in.x, yy = in.y;
+    const int64_t plane = in.plane;
     const float* gp = g + plane * q.oh * q.ow;
     const int64_t* ip = idx + plane * q.oh * q.ow;
     const int64_t me = (int64_t)yy * q.iw + xx;
     float acc = 0.f;
     for (int ky = q.kh - 1; ky >= 0; --ky) {
       const int ty = yy + q.ph - ky * q.dh;
-      if (ty < 0 || ty % q.sh) continue;
-      const int oy = ty / q.sh;
-      if (oy >= q.oh) continue;
+      if (ty < 0) continue;
+      const int oy = exact_div(ty, q.sh, q.d_sh);
+      if (oy < 0 || oy >= q.oh) continue;
       for (int kx = q.kw - 1; kx >= 0; --kx) {
         const int tx = xx + q.pw - kx * q.dw;
-        if (tx < 0 || tx % q.sw) continue;
-        const int ox = tx / q.sw;
-        if (ox >= q.ow) continue;
+        if (tx < 0) continue;
+        const int ox = exact_div(tx, q.sw, q.d_sw);
+        if (ox < 0 || ox >= q.ow) continue;
         const int o = oy * q.ow + ox;
         if (ip[o] == me) acc += gp[o];
       }
@@ -79,11 +107,13 @@ __device__ __forceinline__ float avg_divisor(int oy, int ox, const PoolGeo& g, i
   return (float)((he - hs) * (we - ws));
 }
 
+template <bool I32>
 __global__ void __launch_bounds__(256) avgpool_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                           int64_t total, PoolGeo g, int include_pad, int divisor) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int ox = (int)(i % g.ow), oy = (int)((i / g.ow) % g.oh);
-    const int64_t plane = i / ((int64_t)g.ow * g.oh);
+    const Pos o = decompose<I32>(i, g.ow, g.oh * g.ow, g.d_ow, g.d_ohw);
+    const int ox = o.x, oy = o.y;
+    const int64_t plane = o.plane;
     const float* xp = x + plane * g.ih * g.iw;
     const int hs = oy * g.sh - g.ph, ws = ox * g.sw - g.pw;
     const int y0 = max(hs, 0), y1 = min(hs + g.kh, g.ih), x0 = max(ws, 0), x1 = min(ws + g.kw, g.iw);
@@ -94,11 +124,13 @@ __global__ void __launch_bounds__(256) avgpool_fwd_kernel(const float* __restric
   }
 }
 
+template <bool I32>
 __global__ void __launch_bounds__(256) avgpool_bwd_kernel(const float* __restrict__ gy, float* __restrict__ gx,
                                                           int64_t total, PoolGeo q, int include_pad, int divisor) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int xx = (int)(i % q.iw), yy = (int)((i / q.iw) % q.ih);
-    const int64_t plane = i / ((int64_t)q.iw * q.ih);
+    const Pos in = decompose<I32>(i, q.iw, q.ih * q.iw, q.d_iw, q.d_ihw);
+    const int xx = in.x, yy = in.y;
+    const int64_t plane = in.plane;
     const float* gp = gy + plane * q.oh * q.ow;
     // windows [oy*s - p, oy*s - p + k) containing yy: oy in [ceil((yy + p - k + 1) / s), floor((yy + p) / s)]
     const int oy0 = max(0, (yy + q.ph - q.kh + q.sh) / q.sh), oy1 = min(q.oh - 1, (yy + q.ph) / q.sh);
@@ -134,7 +166,32 @@ __global__ void __launch_bounds__(256) adapool_fwd_kernel(const float* __restric
   }
 }
 
-// Global average pool (oh = ow = 1) as one wave per plane: coalesced reads and a wave reduction.
+// Global average pool of planes of at most 64 elements: a workgroup stages 256 consecutive planes (one contiguous
+// segment) through LDS with float4 loads, then each thread sums one plane. hw odd keeps the per-thread LDS rows on
+// distinct banks; an even hw costs some bank conflicts, not correctness.
+__global__ void __launch_bounds__(256) gap_small_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                        int64_t planes, int hw) {
+  __shared__ float tile[256 * 64];
+  const int64_t p0 = (int64_t)blockIdx.x * 256;
+  const int np = (int)min<int64_t>(256, planes - p0);
+  const int n = np * hw;
+  const float* src = x + p0 * hw;
+  if ((((uintptr_t)src) & 15) == 0) {
+    const int n4 = n >> 2;
+    for (int e = threadIdx.x; e < n4; e += 256) reinterpret_cast<float4*>(tile)[e] = reinterpret_cast<const float4*>(src)[e];
+    for (int e = (n4 << 2) + threadIdx.x; e < n; e += 256) tile[e] = src[e];
+  } else {
+    for (int e = threadIdx.x; e < n; e += 256) tile[e] = src[e];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < np) {
+    float acc = 0.f;
+    for (int e = 0; e < hw; ++e) acc += tile[threadIdx.x * hw + e];
+    y[p0 + threadIdx.x] = acc / (float)hw;
+  }
+}
+
+// Global average pool of larger planes as one wave per plane: coalesced reads and a wave reduction.
 __global__ void __launch_bounds__(256) gap_fwd_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                       int64_t planes, int hw) {
   const int64_t plane = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -146,6 +203,16 @@ __global__ void __launch_bounds__(256) gap_fwd_kernel(const float* __restrict__ 
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (lane == 0) y[plane] = acc / (float)hw;
+}
+
+// Grad of global average pooling: gx[plane][e] = g[plane] / hw.
+template <bool I32>
+__global__ void __launch_bounds__(256) gap_bwd_kernel(const float* __restrict__ g, float* __restrict__ gx,
+                                                      int64_t total, int hw, FastDiv d_hw) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t plane = I32 ? (int64_t)fdiv((uint32_t)i, d_hw) : i / hw;
+    gx[i] = g[plane] / (float)hw;
+  }
 }
 
 __global__ void __launch_bounds__(256) adapool_bwd_kernel(const float* __restrict__ gy, float* __restrict__ gx,
@@ -176,8 +243,26 @@ static bool pool_ok(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t 
 
 static PoolGeo pgeo(int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw, int64_t sh, int64_t sw,
                     int64_t ph, int64_t pw, int64_t dh, int64_t dw) {
-  return PoolGeo{(int)ih, (int)iw, (int)oh, (int)ow, (int)kh, (int)kw, (int)sh, (int)sw, (int)ph, (int)pw, (int)dh, (int)dw};
+  PoolGeo g{(int)ih, (int)iw, (int)oh, (int)ow, (int)kh, (int)kw, (int)sh, (int)sw, (int)ph, (int)pw, (int)dh, (int)dw};
+  g.d_ow = make_fastdiv((uint32_t)ow);
+  g.d_ohw = make_fastdiv((uint32_t)(oh * ow));
+  g.d_iw = make_fastdiv((uint32_t)iw);
+  g.d_ihw = make_fastdiv((uint32_t)(ih * iw));
+  g.d_sh = make_fastdiv((uint32_t)sh);
+  g.d_sw = make_fastdiv((uint32_t)sw);
+  return g;
 }
+
+static bool idx32(int64_t total) { return total < ((int64_t)1 << 32); }
+
+// Launches K<true> (32-bit indexing) or K<false> over a 1-D grid for `total` elements.
+#define OMT_POOL_LAUNCH(K, total, s, ...)                                                      \
+  do {                                                                                         \
+    if (idx32(total))                                                                          \
+      hipLaunchKernelGGL(K<true>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);    \
+    else                                                                                       \
+      hipLaunchKernelGGL(K<false>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);   \
+  } while (0)
 
 }  // namespace omt
 
@@ -191,8 +276,8 @@ OMT_EXPORT int omt_maxpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
     return fail(OMT_UNSUPPORTED, "omt_maxpool_fwd: geometry not covered");
   const int64_t total = planes * oh * ow;
   if (total == 0) return OMT_OK;
-  hipLaunchKernelGGL(maxpool_fwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), x, y, idx, total,
-                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+  OMT_POOL_LAUNCH(maxpool_fwd_kernel, total, stream_of(stream), x, y, idx, total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
   return launch_check("maxpool_fwd_kernel");
 }
 
@@ -204,8 +289,8 @@ OMT_EXPORT int omt_maxpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
     return fail(OMT_UNSUPPORTED, "omt_maxpool_bwd: geometry not covered");
   const int64_t total = planes * ih * iw;
   if (total == 0) return OMT_OK;
-  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, idx, gx, total,
-                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+  OMT_POOL_LAUNCH(maxpool_bwd_kernel, total, stream_of(stream), g, idx, gx, total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
   return launch_check("maxpool_bwd_kernel");
 }
 
@@ -217,8 +302,8 @@ OMT_EXPORT int omt_avgpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
     return fail(OMT_UNSUPPORTED, "omt_avgpool_fwd: geometry not covered");
   const int64_t total = planes * oh * ow;
   if (total == 0) return OMT_OK;
-  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), x, y, total,
-                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), count_include_pad, (int)divisor_override);
+  OMT_POOL_LAUNCH(avgpool_fwd_kernel, total, stream_of(stream), x, y, total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), count_include_pad, (int)divisor_override);
   return launch_check("avgpool_fwd_kernel");
 }
 
@@ -230,8 +315,8 @@ OMT_EXPORT int omt_avgpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
     return fail(OMT_UNSUPPORTED, "omt_avgpool_bwd: geometry not covered");
   const int64_t total = planes * ih * iw;
   if (total == 0) return OMT_OK;
-  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, gx, total,
-                     pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), count_include_pad, (int)divisor_override);
+  OMT_POOL_LAUNCH(avgpool_bwd_kernel, total, stream_of(stream), g, gx, total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), count_include_pad, (int)divisor_override);
   return launch_check("avgpool_bwd_kernel");
 }
 
@@ -242,6 +327,11 @@ OMT_EXPORT int omt_adapool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
   if (planes == 0) return OMT_OK;
   hipStream_t s = stream_of(stream);
   if (oh == 1 && ow == 1) {
+    if (ih * iw <= 64 && cdiv(planes, 256) < ((int64_t)1 << 31)) {
+      hipLaunchKernelGGL(gap_small_kernel, dim3((unsigned)cdiv(planes, 256)), dim3(256), 0, s, x, y, planes,
+                         (int)(ih * iw));
+      return launch_check("gap_small_kernel");
+    }
     hipLaunchKernelGGL(gap_fwd_kernel, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, s, x, y, planes, (int)(ih * iw));
     return launch_check("gap_fwd_kernel");
   }
@@ -257,6 +347,11 @@ OMT_EXPORT int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
   if (!pool_ok(planes, ih, iw, oh, ow)) return fail(OMT_UNSUPPORTED, "omt_adapool_bwd: geometry not covered");
   const int64_t total = planes * ih * iw;
   if (total == 0) return OMT_OK;
+  if (oh == 1 && ow == 1) {
+    const FastDiv d_hw = make_fastdiv((uint32_t)(ih * iw));
+    OMT_POOL_LAUNCH(gap_bwd_kernel, total, stream_of(stream), g, gx, total, (int)(ih * iw), d_hw);
+    return launch_check("gap_bwd_kernel");
+  }
   hipLaunchKernelGGL(adapool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, gx, total,
                      (int)ih, (int)iw, (int)oh, (int)ow);
   return launch_check("adapool_bwd_kernel");

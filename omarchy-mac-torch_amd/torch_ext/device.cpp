@@ -9,6 +9,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <cstdlib>
+#include <mutex>
 
 #include "omt_torch.h"
 
@@ -63,8 +64,16 @@ Tensor workspace(size_t bytes) { return bytes ? empty_dev({(int64_t)bytes}, at::
 
 // The alias storage is resizable through torch's HIP allocator: an op that grows an output argument (out= forms,
 // resize_) reallocates the alias, and the fallback then adopts the new storage into the device tensor.
+// torch's HIP context (its caching allocator above all) initializes lazily, on the first HIP tensor a program creates;
+// a program that only uses this device reaches torch's HIP kernels through the aliases below, so they initialize it.
+static void init_torch_hip() {
+  static std::once_flag once;
+  std::call_once(once, []() { at::globalContext().lazyInitDevice(c10::DeviceType::CUDA); });
+}
+
 Tensor hip_alias(const Tensor& t) {
   if (!is_dev(t)) return t;
+  init_torch_hip();
   const c10::Storage& s = t.storage();
   c10::DataPtr dp(const_cast<void*>(s.data()), c10::Device(c10::DeviceType::CUDA, 0));  // non-owning
   c10::Storage hs(c10::Storage::use_byte_size_t(), s.nbytes(), std::move(dp),

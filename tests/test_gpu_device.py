@@ -75,6 +75,22 @@ def test_transfer_views_and_delegated_ops(clean):
     assert omt.memory_allocated() > 0
 
 
+def test_first_use_without_torch_cuda(clean):
+    """A program that never touches torch.cuda itself: the first delegated op (a Linear) initializes torch's HIP
+    context through the fallback. Runs in a fresh interpreter (this one has torch.cuda initialized already)."""
+    import pathlib
+    import subprocess
+    import sys
+    root = pathlib.Path(__file__).resolve().parent.parent
+    code = ("import sys; sys.path.insert(0, 'omarchy-mac-torch_amd'); import torch, omarchy_mac_torch as o; "
+            "torch.manual_seed(0); m = torch.nn.Linear(3, 2); x = torch.randn(4, 3); "
+            "d = m.to(o.DEVICE)(x.to(o.DEVICE)).detach().cpu(); "
+            "print(float((d - torch.nn.Linear(3, 2).requires_grad_(False).__class__.forward(m.cpu(), x)).abs().max()))")
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert float(r.stdout.strip().splitlines()[-1]) <= 1e-6
+
+
 def test_conv_through_autograd_uses_hip_kernels(clean):
     omt = clean
     omt._native.core.count_delegated(True)
@@ -272,6 +288,42 @@ def test_plaincnn_five_step_loss_parity(clean, fused):
     if fused:
         assert omt.accelerate(dev_model).startswith("1 fused")
     dev = train_losses(dev_model, omt.DEVICE, 5)
+    for a, b in zip(dev, cpu):
+        assert abs(a - b) <= 1e-3 * abs(b), (dev, cpu)
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
+
+
+@pytest.mark.parametrize("name", ["resnet18", "mobilenet_v3_small"])
+def test_config_models_five_step_loss_parity(clean, name):
+    """BASELINE configs 3 and 4 at full size: ResNet-18 (b32, 3x64x64, 1000 classes, Adam lr 1e-3) and the
+    MobileNetV3-Small-style net (b32, 3x224x224, 1000 classes, AdamW lr 1e-3 wd 0.01), five training steps from the
+    same weights and data on the device and on PyTorch CPU: every loss within 1e-3 relative, no fallbacks."""
+    from omarchy_mac_torch import models
+    omt = clean
+    if name == "resnet18":
+        mk, shape = (lambda: models.resnet18(1000)), (32, 3, 64, 64)
+        make_opt = lambda p: torch.optim.Adam(p, lr=1e-3)  # noqa: E731
+    else:
+        mk, shape = (lambda: models.mobilenet_v3_small(1000)), (32, 3, 224, 224)
+        make_opt = lambda p: torch.optim.AdamW(p, lr=1e-3, weight_decay=0.01)  # noqa: E731
+    torch.manual_seed(0)
+    base = mk()
+    g = torch.Generator().manual_seed(1)
+    data = [(torch.randn(*shape, generator=g), torch.randint(0, 1000, (shape[0],), generator=g)) for _ in range(5)]
+
+    def run(device):
+        model = copy.deepcopy(base).to(device)
+        opt = make_opt(model.parameters())
+        out = []
+        for x, t in data:
+            opt.zero_grad(set_to_none=True)
+            loss = F.cross_entropy(model(x.to(device)), t.to(device))
+            loss.backward()
+            opt.step()
+            out.append(loss.item())
+        return out
+
+    dev, cpu = run(omt.DEVICE), run("cpu")
     for a, b in zip(dev, cpu):
         assert abs(a - b) <= 1e-3 * abs(b), (dev, cpu)
     assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())

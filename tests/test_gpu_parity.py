@@ -267,6 +267,29 @@ def test_depthwise(cuda, ops, ks, s, p):
     assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, ks, s, p)) <= TOL
 
 
+@pytest.mark.parametrize("ks", [3, 5, 7])
+def test_depthwise_tiled_stride1(cuda, ops, ks):
+    """The LDS-tiled stride-1 "same" kernels on plane shapes that exercise one-wave workgroups (<= 128 outputs),
+    several row chunks per plane and wide rows; the eval BN + ReLU loader across chunk boundaries."""
+    rng = np.random.default_rng(ks)
+    p = ks // 2
+    for (n, c, h, w) in ((2, 3, 1, 1), (3, 4, 2, 3), (2, 5, 7, 7), (2, 3, 11, 9), (2, 4, 56, 56), (1, 3, 13, 300),
+                         (1, 2, 70, 41)):
+        case = (ks, n, c, h, w)
+        x, wt, b = rnd(rng, n, c, h, w), rnd(rng, c, 1, ks, ks), rnd(rng, c)
+        y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), 1, p)
+        assert orc.rel_l2(host(y), orc.dw_fwd(x, wt, b, 1, p)) <= TOL, case
+        gy = rnd(rng, n, c, h, w)
+        gx = ops.depthwise_dgrad(dev(gy, cuda), dev(wt, cuda), x.shape, 1, p)
+        assert orc.rel_l2(host(gx), orc.dw_dgrad(gy, wt, x.shape, 1, p)) <= TOL, case
+        gw = ops.depthwise_wgrad(dev(x, cuda), dev(gy, cuda), ks, 1, p)
+        assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, ks, 1, p)) <= TOL, case
+    x, wt = rnd(rng, 2, 6, 60, 33), rnd(rng, 6, 1, ks, ks)
+    bn = (rnd(rng, 6), np.abs(rnd(rng, 6)) + 0.5, rnd(rng, 6), rnd(rng, 6))
+    y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), None, 1, p, bn=[dev(t, cuda) for t in bn])
+    assert orc.rel_l2(host(y), orc.dw_fwd(x, wt, None, 1, p, bn=bn)) <= TOL
+
+
 def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
     rng = np.random.default_rng(5)
     c = 8
@@ -366,6 +389,25 @@ def test_avgpool(cuda, ops, k, s, p, ceil, incl, div, hw):
     gy = rnd(rng, *y_ref.shape)
     gx = ops.avg_pool2d_backward(dev(gy, cuda), x.shape, k, s, p, incl, div)
     assert orc.rel_l2(host(gx), orc.avgpool_bwd(gy, x.shape, k, s, p, incl, div)) <= 1e-6
+
+
+def test_global_avgpool_many_planes(cuda, ops):
+    """Global average pooling over thousands of planes (several LDS-staged workgroups, a partial last one), plane
+    sizes on both sides of the 64-element staging limit, and an input view not aligned to 16 bytes."""
+    rng = np.random.default_rng(3)
+    for (n, c, h, w) in ((3, 700, 7, 7), (2, 300, 4, 4), (5, 129, 1, 1), (2, 260, 7, 9), (2, 300, 8, 8),
+                         (2, 70, 9, 9)):
+        x = rnd(rng, n, c, h, w)
+        y = ops.adaptive_avg_pool2d(dev(x, cuda), 1)
+        assert orc.rel_l2(host(y), orc.adapool_fwd(x, 1, 1)) <= 1e-6, (n, c, h, w)
+        gy = rnd(rng, n, c, 1, 1)
+        gx = ops.adaptive_avg_pool2d_backward(dev(gy, cuda), x.shape)
+        assert orc.rel_l2(host(gx), orc.adapool_bwd(gy, x.shape)) <= 1e-6, (n, c, h, w)
+    x = rnd(rng, 3, 300, 7, 7)
+    flat = torch.from_numpy(np.concatenate([np.zeros(1, np.float32), x.ravel()])).to(cuda)
+    xv = flat[1:].view(3, 300, 7, 7)  # contiguous, 4 bytes past an aligned allocation
+    assert xv.data_ptr() % 16 != 0
+    assert orc.rel_l2(host(ops.adaptive_avg_pool2d(xv, 1)), orc.adapool_fwd(x, 1, 1)) <= 1e-6
 
 
 @pytest.mark.parametrize("hw,o", [(6, 6), (13, 6), (10, 4), (7, 1), (5, 3), (2, 1), (56, 1)])
