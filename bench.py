@@ -318,6 +318,7 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
         cpu_ms, cpu_losses = run(copy.deepcopy(base), "cpu", data[:cpu_steps + 1], 1)
         k = min(len(cpu_losses), len(dev_losses))
         rel = max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:k], cpu_losses[:k]))
+        rel5 = max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:5], cpu_losses[:5]))  # the north-star criterion
         # float64 CPU run of the same steps: the rounding-free trajectory both fp32 runs are compared with (Adam on a
         # 1000-class batch of 32 amplifies fp32 summation-order differences from step to step)
         _, f64_losses = run(copy.deepcopy(base).double(), "cpu", data[:k], 0, torch.float64)
@@ -325,9 +326,11 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
             out["graphed"].update({
                 "speedup_vs_cpu": round(cpu_ms / out["graphed"]["ms_per_step"], 2),
                 "max_rel_loss_diff": max(abs(a - b) / abs(b) for a, b in zip(g_losses[:k], cpu_losses[:k])),
+                "max_rel_loss_diff_5_steps": max(abs(a - b) / abs(b) for a, b in zip(g_losses[:5], cpu_losses[:5])),
                 "losses": [round(v, 6) for v in g_losses[:k]]})
         out.update({"cpu_ms_per_step": round(cpu_ms, 2), "cpu_cores": threads, "cpu_steps": cpu_steps,
                     "speedup_vs_cpu": round(cpu_ms / dev_ms, 2), "max_rel_loss_diff": rel, "loss_steps_compared": k,
+                    "max_rel_loss_diff_5_steps": rel5,
                     "losses": {"device": [round(v, 6) for v in dev_losses[:k]],
                                "cpu": [round(v, 6) for v in cpu_losses[:k]],
                                "cpu_fp64": [round(v, 6) for v in f64_losses]},

@@ -341,6 +341,155 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __r
   }
 }
 
+// ---- one launch per call for small channels ---------------------------------------------------------------------
+// A channel of at most kFusedMax elements is reduced, finalized and mapped by one workgroup: the statistics pass and
+// the apply pass (which re-reads the channel from cache) in one kernel, instead of three launches. The finalize and
+// apply arithmetic is that of the split kernels above, so both paths agree to the float64 summation order.
+constexpr int64_t kFusedMax = 8192;
+
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta,
+                                                             const float* __restrict__ rm,
+                                                             const float* __restrict__ rv, double momentum,
+                                                             double eps, int relu, float* __restrict__ y,
+                                                             float* __restrict__ save_mean,
+                                                             float* __restrict__ save_invstd,
+                                                             float* __restrict__ new_rm, float* __restrict__ new_rv,
+                                                             int c, int hw, const Split sp) {
+  using V = typename VecT<VEC>::T;
+  __shared__ float coef[2];
+  const int ch = blockIdx.x;
+  const float shift = x[(int64_t)ch * hw];
+  double s1 = 0.0, s2 = 0.0;
+  for (int v = (int)threadIdx.x; v < sp.nv; v += 4 * 256) {
+    V r[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int vv = v + u * 256;
+      if (vv < sp.nv) {
+        r[u] = *reinterpret_cast<const V*>(x + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const double d = (double)(vget(r[u], i) - shift);
+        s1 += d;
+        s2 += d * d;
+      }
+  }
+  block_sum2(s1, s2);
+  if (threadIdx.x == 0) {
+    const double m = (double)sp.nv * VEC;
+    const double a = s1 / m, mean = (double)shift + a;
+    double var = s2 / m - a * a;
+    if (var < 0.0) var = 0.0;
+    const float fm = (float)mean, fi = (float)(1.0 / sqrt(var + eps));
+    save_mean[ch] = fm;
+    save_invstd[ch] = fi;
+    if (new_rm && rm) new_rm[ch] = (float)((double)rm[ch] + momentum * (mean - (double)rm[ch]));
+    if (new_rv && rv) {
+      const double corr = (double)(float)(m / (m > 1.0 ? m - 1.0 : 1.0));
+      new_rv[ch] = (float)((double)rv[ch] + momentum * (var * corr - (double)rv[ch]));
+    }
+    const float sc = fi * gamma[ch];
+    coef[0] = sc;
+    coef[1] = beta[ch] - fm * sc;
+  }
+  __syncthreads();
+  const float sc = coef[0], sh = coef[1];
+  for (int v = (int)threadIdx.x; v < sp.nv; v += 256) {
+    const int64_t off = voffset(v, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+    V t = *reinterpret_cast<const V*>(x + off);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float f = fmaf(vget(t, i), sc, sh);
+      if (relu) f = fmaxf(f, 0.f);
+      vset(t, i, f);
+    }
+    *reinterpret_cast<V*>(y + off) = t;
+  }
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ x,
+                                                           const float* __restrict__ ry,
+                                                           const float* __restrict__ mean,
+                                                           const float* __restrict__ invstd,
+                                                           const float* __restrict__ gamma, float* __restrict__ gx,
+                                                           float* __restrict__ dgamma, float* __restrict__ dbeta,
+                                                           int c, int hw, const Split sp) {
+  using V = typename VecT<VEC>::T;
+  __shared__ float kc[5];
+  const int ch = blockIdx.x;
+  const float mu = mean[ch], inv = invstd[ch];
+  double s1 = 0.0, s2 = 0.0;
+  for (int v = (int)threadIdx.x; v < sp.nv; v += 4 * 256) {
+    V rg[4], rx[4], rr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int vv = v + u * 256;
+      if (vv < sp.nv) {
+        const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+        rg[u] = *reinterpret_cast<const V*>(g + off);
+        rx[u] = *reinterpret_cast<const V*>(x + off);
+        if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          vset(rg[u], i, 0.f);
+          vset(rx[u], i, mu);
+          vset(rr[u], i, 1.f);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float gz = vget(rg[u], i);
+        if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+        const float xhat = (vget(rx[u], i) - mu) * inv;
+        s1 += (double)gz;
+        s2 += (double)gz * (double)xhat;
+      }
+  }
+  block_sum2(s1, s2);
+  if (threadIdx.x == 0) {
+    if (dbeta) dbeta[ch] = (float)s1;
+    if (dgamma) dgamma[ch] = (float)s2;
+    if (gx) {
+      const double m = (double)sp.nv * VEC, gi = (double)gamma[ch] * (double)inv;
+      kc[0] = (float)gi;
+      kc[1] = (float)(gi * s1 / m);
+      kc[2] = (float)(gi * s2 / m);
+      kc[3] = mu;
+      kc[4] = inv;
+    }
+  }
+  if (!gx) return;
+  __syncthreads();
+  float k[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) k[i] = kc[i];
+  for (int v = (int)threadIdx.x; v < sp.nv; v += 256) {
+    const int64_t off = voffset(v, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+    const V vg = *reinterpret_cast<const V*>(g + off), vx = *reinterpret_cast<const V*>(x + off);
+    V vr = vg;
+    if (ry) vr = *reinterpret_cast<const V*>(ry + off);
+    V o;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) vset(o, i, bwd_elem(vget(vg, i), vget(vx, i), vget(vr, i), ry != nullptr, k));
+    *reinterpret_cast<V*>(gx + off) = o;
+  }
+}
+
 // grid x = plane (n * c), grid y = chunks of the plane
 static dim3 apply_grid(int64_t planes, int64_t hw, int per_thread) {
   int64_t gy = cdiv(cdiv(hw, per_thread), 256);
@@ -412,6 +561,17 @@ OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x
     return fail(OMT_INVALID, "omt_bn_train_fwd: workspace too small");
   hipStream_t s = stream_of(stream);
   const Split sp = bn_split(n, c, hw, al16(x));
+  if (n * hw <= kFusedMax) {
+    const bool vec = sp.vec == 4 && al16(y);
+    const Split f = vec ? sp : bn_split(n, c, hw, false);
+    if (vec)
+      hipLaunchKernelGGL(bn_train_fused_kernel<4>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
+                         running_var, momentum, eps, relu, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f);
+    else
+      hipLaunchKernelGGL(bn_train_fused_kernel<1>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
+                         running_var, momentum, eps, relu, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f);
+    return launch_check("bn_train_fused_kernel");
+  }
   double* part = (double*)workspace;
   if (int st = launch_stats(sp, x, part, c, hw, s)) return st;
   const double m = (double)(n * hw);
@@ -456,6 +616,15 @@ OMT_EXPORT int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, cons
   hipStream_t s = stream_of(stream);
   const bool aligned = al16(g) && al16(x) && al16(relu_y) && al16(gx);
   const Split sp = bn_split(n, c, hw, aligned);
+  if (n * hw <= kFusedMax) {
+    if (sp.vec == 4)
+      hipLaunchKernelGGL(bn_bwd_fused_kernel<4>, dim3((unsigned)c), dim3(256), 0, s, g, x, relu_y, save_mean,
+                         save_invstd, gamma, gx, dgamma, dbeta, (int)c, (int)hw, sp);
+    else
+      hipLaunchKernelGGL(bn_bwd_fused_kernel<1>, dim3((unsigned)c), dim3(256), 0, s, g, x, relu_y, save_mean,
+                         save_invstd, gamma, gx, dgamma, dbeta, (int)c, (int)hw, sp);
+    return launch_check("bn_bwd_fused_kernel");
+  }
   double* part = (double*)workspace;
   float* kc = (float*)(part + c * kMaxSlices * 2);
   const dim3 pgrid((unsigned)c, (unsigned)sp.slices);
