@@ -66,6 +66,7 @@ struct Phase {
   int K, Q;               // C * KH * KW, n * OH * OW
   int os, oy0, ox0;       // output scatter: y row = oy * os + oy0, column = ox * os + ox0
   int woff;               // offset of this phase's [P][K] weights (floats)
+  int ky0, kx0;           // grad input read straight from w: the phase's first filter tap
   FastDiv div_ohw, div_ow, div_kk, div_kw;
 };
 
@@ -82,6 +83,8 @@ struct GatherArgs {
   FastDiv div_c;
   int nphase;
   int kslice;            // K elements per grid-z slice (a multiple of the K-block)
+  int wdirect;           // grad input, channel-major: A[ci][(co, a', b')] read from w[co][ci][ks][ks] (no re-pack)
+  int ks, s;             //   the filter size and stride for that read
   float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
   int64_t part_stride;   // elements per slice
   Phase ph[kMaxPhases];
@@ -103,13 +106,15 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
   __shared__ __attribute__((aligned(16))) float Bs[2][BQ * PK];
 
   const int zs = (int)blockIdx.z / a.nphase;  // K slice
-  const Phase& ph = a.ph[(int)blockIdx.z - zs * a.nphase];
+  // a register copy: reads through the dynamically indexed kernel argument would each become a scalar load at its
+  // use, some inside the per-element bounds branches of the loaders
+  const Phase ph = a.ph[(int)blockIdx.z - zs * a.nphase];
   const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
   if (q0 >= ph.Q) return;  // this phase has fewer pixel tiles than the largest one
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wp = wave / WGQ, wq = wave % WGQ;
-  const int KH = ph.KH, KW = ph.KW, K = ph.K, KK = KH * KW;
+  const int KH = ph.KH, KW = ph.KW, K = ph.K, KK = KH * KW, woff = ph.woff;
   const int H = a.H, W = a.W, HW = H * W, P = a.P;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
@@ -140,7 +145,17 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
 #pragma unroll
     for (int i = 0; i < AR; ++i) {
       const int p = p0 + wrow0 + (NT / BK) * i, k = k0 + wk;
-      const uint32_t off = (p < P && k < K) ? (uint32_t)((ph.woff + p * K + k) * 4) : kOOB;
+      uint32_t off;
+      if (MODE == kGeneric && !BN && a.wdirect) {
+        // W'[p = ci][k = (co, a', b')] = w[co][ci][ky0 + s (KH-1-a')][kx0 + s (KW-1-b')]
+        const int co = (int)fdiv((uint32_t)k, ph.div_kk), tt = k - co * KK;
+        const int ap = (int)fdiv((uint32_t)tt, ph.div_kw), bp = tt - ap * KW;
+        const int ky = ph.ky0 + a.s * (KH - 1 - ap), kx = ph.kx0 + a.s * (KW - 1 - bp);
+        off = (p < P && k < K) ? (uint32_t)((((co * P + p) * a.ks + ky) * a.ks + kx) * 4) : kOOB;
+      } else {
+        const uint32_t o = (uint32_t)((woff + p * K + k) * 4);
+        off = (p < P && k < K) ? o : kOOB;
+      }
       ra[i] = bload(wr, off, 0);
     }
     if (MODE == kTapMajor) {
@@ -560,6 +575,12 @@ static const Tile kGatherTiles[] = {
     {32, 256, 32, 64, 0.90f},     {16, 256, 16, 64, 0.80f},     {64, 64, 32, 32, 0.80f},
     {64, 64, 32, 32, 0.90f, 64},  {64, 128, 32, 64, 0.95f, 32}, {128, 64, 64, 32, 0.95f, 32},
 };
+// Plan tile index t < 2 * kNGather: kGatherTiles[t % kNGather], and t >= kNGather forces the channel-major K order
+// (no filter re-pack, one launch fewer; the tap-major order gathers faster on large layers).
+constexpr int kNGather = (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0]));
+static const Tile& gtile(int t) { return kGatherTiles[t % kNGather]; }
+static bool gcm(int t) { return t >= kNGather; }
+
 static const Tile kWgradTiles[] = {
     {64, 128, 32, 64, 1.00f}, {128, 64, 32, 64, 1.00f}, {64, 64, 32, 32, 0.85f}, {32, 128, 16, 64, 0.85f},
 };
@@ -601,13 +622,13 @@ static const int kSliceChoices[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
 static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const omt_conv_plan* fixed) {
   const int64_t kk = K > 0 ? K : 1;
   if (fixed) {
-    const int64_t nkb = cdiv(kk, kGatherTiles[fixed->tile].bk);
+    const int64_t nkb = cdiv(kk, gtile(fixed->tile).bk);
     const int64_t kb = cdiv(nkb, std::max<int64_t>(1, std::min<int64_t>(fixed->slices, nkb)));
-    return {fixed->tile, cdiv(nkb, kb), kb * kGatherTiles[fixed->tile].bk};
+    return {fixed->tile, cdiv(nkb, kb), kb * gtile(fixed->tile).bk};
   }
   GatherPlan best{0, 1, cdiv(kk, 16) * 16};
   double best_cost = 1e300;
-  for (int ti = 0; ti < (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0])); ++ti) {
+  for (int ti = 0; ti < kNGather; ++ti) {
     const Tile& tl = kGatherTiles[ti];
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(kk, tl.bk);
     for (int sc : kSliceChoices) {
@@ -634,18 +655,18 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size.
 static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part, hipStream_t s) {
-  const Tile& tl = kGatherTiles[pl.tile];
+  const Tile& tl = gtile(pl.tile);
   a.kslice = (int)pl.kslice;
   const int64_t total = n * a.P * a.YH * a.YW;
   a.part = pl.slices > 1 ? part : nullptr;
   a.part_stride = total;
   dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
   if (a.bn_mean)
-    gather_dispatch<kGeneric, true>(pl.tile, a, grid, s);
-  else if (gather_tap_major(a.C, false, tl.bk))
-    gather_dispatch<kTapMajor, false>(pl.tile, a, grid, s);
+    gather_dispatch<kGeneric, true>(pl.tile % kNGather, a, grid, s);
+  else if (!gcm(pl.tile) && gather_tap_major(a.C, false, tl.bk))
+    gather_dispatch<kTapMajor, false>(pl.tile % kNGather, a, grid, s);
   else
-    gather_dispatch<kGeneric, false>(pl.tile, a, grid, s);
+    gather_dispatch<kGeneric, false>(pl.tile % kNGather, a, grid, s);
   if (int st = launch_check("conv_gather_kernel")) return st;
   if (pl.slices > 1) {
     const int64_t plane = (int64_t)a.YH * a.YW;
@@ -738,8 +759,7 @@ static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p) {
   return true;
 }
 static int num_tiles(int dir) {
-  return dir == OMT_DIR_WGRAD ? (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0]))
-                              : (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0]));
+  return dir == OMT_DIR_WGRAD ? (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0])) : 2 * kNGather;
 }
 
 }  // namespace omt
@@ -754,7 +774,7 @@ static GatherPlan fwd_plan(const omt_conv_geo* g) {
 // Forward workspace: the tap-major filter (when the plan's K-block divides C and ks > 1), then, 256-byte aligned,
 // the split-K partials.
 static size_t fwd_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
-  if (g->ks == 1 || !gather_tap_major(g->ci, false, kGatherTiles[pl.tile].bk)) return 0;
+  if (g->ks == 1 || gcm(pl.tile) || !gather_tap_major(g->ci, false, gtile(pl.tile).bk)) return 0;
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
@@ -853,6 +873,8 @@ static int dgrad_phases(const omt_conv_geo* g, GatherArgs& a, PackArgs& pk, int6
       p.oy0 = py;
       p.ox0 = px;
       p.woff = woff;
+      p.ky0 = ky0;
+      p.kx0 = kx0;
       p.div_ohw = make_fastdiv((uint32_t)(p.OH * p.OW));
       p.div_ow = make_fastdiv((uint32_t)p.OW);
       p.div_kk = make_fastdiv((uint32_t)(p.KH * p.KW));
@@ -879,10 +901,16 @@ static GatherPlan dgrad_plan(const omt_conv_geo* g) {
   return gather_plan(g->ci, maxq, maxk, a.nphase, have ? &cp : nullptr);
 }
 
+// Grad input re-packs its filter for the tap-major order only; the channel-major order reads w directly.
+static size_t dgrad_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
+  if (gcm(pl.tile) || !gather_tap_major(g->co, false, gtile(pl.tile).bk)) return 0;
+  return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+}
+
 OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
   if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
-  const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
   const GatherPlan pl = dgrad_plan(g);
+  const size_t pack = dgrad_pack_bytes(g, pl);
   return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * g->ci * g->ih * g->iw) * sizeof(float) : pack;
 }
 
@@ -891,28 +919,38 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad: null pointer");
   if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: geometry not covered");
   if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: a tensor of 2 GiB or more");
-  if (!workspace || workspace_bytes < omt_conv_dgrad_workspace(g))
-    return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", omt_conv_dgrad_workspace(g));
+  const size_t need = omt_conv_dgrad_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", need);
   hipStream_t s = stream_of(stream);
   GatherArgs a{};
   PackArgs pk{};
   int64_t maxq = 0;
   const int packed = dgrad_phases(g, a, pk, maxq);
-  pk.w = w;
-  pk.out = (float*)workspace;
-  pk.CO = (int)g->co;
-  pk.CI = (int)g->ci;
-  pk.KS = (int)g->ks;
-  pk.S = (int)g->stride;
   const GatherPlan pl = dgrad_plan(g);
-  pk.tap_major = gather_tap_major(g->co, false, kGatherTiles[pl.tile].bk) ? 1 : 0;
-  hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
-  if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
+  const size_t pack = dgrad_pack_bytes(g, pl);
+  if (pack) {
+    pk.w = w;
+    pk.out = (float*)workspace;
+    pk.CO = (int)g->co;
+    pk.CI = (int)g->ci;
+    pk.KS = (int)g->ks;
+    pk.S = (int)g->stride;
+    pk.tap_major = 1;
+    hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
+    if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
+    a.w = (const float*)workspace;
+    a.w_bytes = (uint32_t)(packed * 4);
+  } else {
+    a.w = w;
+    a.w_bytes = (uint32_t)(g->co * g->ci * g->ks * g->ks * 4);
+    a.wdirect = 1;
+    a.ks = (int)g->ks;
+    a.s = (int)g->stride;
+  }
   a.x = gy;
-  a.w = (const float*)workspace;
   a.y = gx;
   a.x_bytes = (uint32_t)(g->n * g->co * g->oh * g->ow * 4);
-  a.w_bytes = (uint32_t)(packed * 4);
   a.C = (int)g->co;
   a.H = (int)g->oh;
   a.W = (int)g->ow;
@@ -920,8 +958,7 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   a.YH = (int)g->ih;
   a.YW = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
-  const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
-  return run_gather(a, pl, g->n, maxq, (float*)((char*)workspace + align256(pack)), s);
+  return run_gather(a, pl, g->n, maxq, workspace ? (float*)((char*)workspace + align256(pack)) : nullptr, s);
 }
 
 OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
@@ -1097,7 +1134,7 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     P = g->ci, z = a.nphase, plane = g->n * g->ci * g->ih * g->iw;
   }
   for (int t = 0; t < ntile; ++t) {
-    const Tile& tl = kGatherTiles[t];
+    const Tile& tl = gtile(t);
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(std::max<int64_t>(K, 1), tl.bk);
     int64_t last = -1;
     for (int sc : {1, 2, 4, 8, 16, 32, 64}) {

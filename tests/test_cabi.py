@@ -72,10 +72,14 @@ def test_host_validation_statuses():
     L.omt_conv_clear_plans()
     g.oh = 99  # inconsistent geometry
     assert L.omt_conv_wgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
-    g = _lib.conv_geo(2, 3, 4, 8, 8, 3, 2, 1)
-    assert L.omt_conv_dgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID  # no workspace
+    g = _lib.conv_geo(2, 3, 16, 8, 8, 3, 2, 1)  # tap-major grad input (C_out % 16 == 0) re-packs its filter
     assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_OK
-    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 4 * 3 * 3 * 3 * 4
+    assert L.omt_conv_dgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID  # no workspace
+    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 16 * 3 * 3 * 3 * 4
+    n_tiles = L.omt_conv_num_tiles(_lib.OMT_DIR_DGRAD)  # the channel-major twin of tile 0 reads w directly
+    assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(n_tiles // 2, 1))) \
+        == _lib.OMT_OK
+    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 0
     L.omt_conv_clear_plans()
     with pytest.raises(_lib.Unsupported):
         _lib.check(_lib.OMT_UNSUPPORTED)
