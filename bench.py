@@ -130,10 +130,63 @@ def torch_cpu_baseline(layers, batch, threads):
                       f"at batch {batch}, {cpu_info()}"}
 
 
+def pmc_summary(fetch_csv, write_csv, layers, workload):
+    """Reads the FETCH_SIZE and WRITE_SIZE counter dumps of two `--pmc-probe` runs: the 1 GiB device copy calibrates
+    each counter (bytes it must move / what the counter reports), then the forward conv_gather_kernel dispatches after
+    it are the workload's layers in order. Writes profiles/conv_gather_<workload>_traffic.json and prints a markdown
+    table."""
+    import csv
+
+    def rows(path, counter):
+        out = []
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                out.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
+        return sorted(out)
+
+    res = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rs = rows(path, counter)
+        ci = max((i for i, r in enumerate(rs) if "copy" in r[1].lower()), key=lambda i: rs[i][2])
+        factor = (1 << 30) / rs[ci][2]
+        gathers = [r for r in rs[ci + 1:] if "conv_gather_kernel" in r[1]]
+        if len(gathers) != len(layers):
+            raise SystemExit(f"{counter}: {len(gathers)} gather dispatches after the copy, {len(layers)} layers")
+        res[counter] = (factor, [g[2] * factor for g in gathers])
+    out = {"workload": workload, "fetch_factor": round(res["FETCH_SIZE"][0], 4),
+           "write_factor": round(res["WRITE_SIZE"][0], 4), "layers": {}}
+    lines = ["| Layer | algorithmic bytes | FETCH (scaled) | WRITE (scaled) | traffic / algorithmic |", "|---|---|---|---|---|"]
+    for i, (name, n, c, k, h, ks, st, pd) in enumerate(layers):
+        o = out_size(h, ks, st, pd)
+        alg = 4 * (n * c * h * h + k * c * ks * ks + n * k * o * o)
+        f, w = res["FETCH_SIZE"][1][i], res["WRITE_SIZE"][1][i]
+        out["layers"][name] = {"algorithmic_bytes": alg, "fetch_bytes": round(f), "write_bytes": round(w)}
+        lines.append(f"| {name} | {alg / 1e6:.1f} MB | {f / 1e6:.1f} MB | {w / 1e6:.1f} MB | {(f + w) / alg:.2f} |")
+    (ROOT / "profiles" / f"conv_gather_{workload}_traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    print(f"FETCH_SIZE factor {out['fetch_factor']}, WRITE_SIZE factor {out['write_factor']}")
+    print("\n".join(lines))
+
+
+def traffic_per_launch(workload):
+    """HBM bytes per forward launch (mean over the workload's layers) from the committed FETCH_SIZE / WRITE_SIZE
+    counter passes (profiles/conv_gather_<workload>_traffic.json, written from `bench.py --pmc-probe` runs and
+    scaled by the copy-kernel calibration), or None when no such measurement exists."""
+    path = ROOT / "profiles" / f"conv_gather_{workload}_traffic.json"
+    try:
+        data = json.loads(path.read_text())
+        per = [v["fetch_bytes"] + v["write_bytes"] for v in data["layers"].values()]
+        return {"bytes": round(sum(per) / len(per)), "algorithmic_bytes": round(
+            sum(v["algorithmic_bytes"] for v in data["layers"].values()) / len(per)), "source": str(path.name)}
+    except (OSError, ValueError, KeyError, ZeroDivisionError):
+        return None
+
+
 def bandwidth_kernels(dev, reps=20):
     """The HBM-bound kernels of the path on shapes from the BASELINE configs: achieved GB/s from algorithmic
     (compulsory) bytes -- each input read once, each output written once, fp32, int64 pool indices -- over the op's
-    HIP-event time on its launch stream (all of the op's launches: BN's statistics, finalize and apply passes)."""
+    GPU time (all of its launches: BN's statistics, finalize and apply passes). The calls are captured into a HIP
+    graph and timed with HIP events around its replays, so host dispatch (which exceeds the smallest kernels' run
+    time) is not counted."""
     import torch
 
     from omarchy_mac_torch import hip_ops as H
@@ -186,27 +239,41 @@ def bandwidth_kernels(dev, reps=20):
     stream = torch.cuda.current_stream(dev)
     out = []
     for name, fn, b in cases:
-        fn()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            fn()
+        stream.wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(reps):
-            fn()
+        for _ in range(3):
+            graph.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / reps * 1e3
+        us = e0.elapsed_time(e1) / (3 * reps) * 1e3
+        del graph
         out.append({"op": name, "bytes": b, "us": round(us, 2), "GB/s": round(b / us / 1e3, 1),
                     "frac_of_hbm_peak": round(b / (us * 1e-6) / PEAK_HBM, 3)})
     return out
 
 
 def pmc_probe(layers, dev):
-    """A 1 GiB device-to-device copy (1 GiB read + 1 GiB written: the FETCH_SIZE / WRITE_SIZE calibration launch),
-    then one forward conv per layer, each on its own freshly written input."""
+    """For the rocprofv3 --pmc passes: the forward plans are tuned first (as in the bench; those dispatches come
+    before the copy), then a 1 GiB device-to-device copy (1 GiB read + 1 GiB written: the FETCH_SIZE / WRITE_SIZE
+    calibration launch), then one forward conv per layer, each on its own freshly written input."""
     import torch
 
     from omarchy_mac_torch import hip_ops
 
+    for (name, n, c, k, h, ks, s, p) in layers:
+        hip_ops.autotune_conv("fwd", (n, c, h, h), (k, c, ks, ks), s, p)
+    torch.cuda.synchronize()
     src = torch.ones(256 * 1024 * 1024, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -355,10 +422,15 @@ def main():
     ap.add_argument("--resnet-steps", type=int, default=20)
     ap.add_argument("--no-tune", action="store_true",
                     help="skip plan tuning (tile / K split per layer and direction) before the warmup")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarize two --pmc-probe counter dumps into profiles/conv_gather_<workload>_traffic.json")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
                          "launch per layer; prints nothing else")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
               "its batch share; see the sharding note in the design document). Run with --gpus 1.", file=sys.stderr)
@@ -476,7 +548,7 @@ def main():
         "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
         "roofline": {"kernel": "conv_gather_kernel (forward launches)", "bound": "mfma",
                      "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4), "traffic": traffic_per_launch(args.workload),
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "flop_per_launch_avg": round(sum(fwd_flops) / len(fwd_flops))},
         "per_direction": per_dir,

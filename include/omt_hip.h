@@ -87,6 +87,7 @@ void* omt_default_stream(void);
 /* kind: 0 host->device, 1 device->host, 2 device->device. Asynchronous on stream (device->host: synchronous).
  * Replaces upload/download_bytes and copy_dev (csrc/runtime.cpp:614-676). */
 int omt_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+/* Zeroes `bytes` at dst on `stream` with a kernel (not a memset node: safe inside a captured HIP graph). */
 int omt_memset_zero(void* dst, size_t bytes, void* stream);
 
 /* Graph pools: memory that a captured HIP graph keeps for its replays. No counterpart in the reference, whose command

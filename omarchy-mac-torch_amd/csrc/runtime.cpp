@@ -272,12 +272,6 @@ OMT_EXPORT int omt_memcpy(void* dst, const void* src, size_t bytes, int kind, vo
   return OMT_OK;
 }
 
-OMT_EXPORT int omt_memset_zero(void* dst, size_t bytes, void* stream) {
-  if (bytes == 0) return OMT_OK;
-  OMT_HIP(hipMemsetAsync(dst, 0, bytes, stream_of(stream)));
-  return OMT_OK;
-}
-
 OMT_EXPORT int omt_stream_sync(void* stream) {
   OMT_HIP(hipStreamSynchronize(stream_of(stream)));
   return OMT_OK;

@@ -99,6 +99,32 @@ def test_conv_geometry_sweep(cuda, ops, ks):
                 assert orc.rel_l2(host(gw), orc.conv_wgrad(x, gy, ks, s, p)) <= TOL, case
 
 
+def test_memset_zero_kernel_and_graph_replay(cuda):
+    """omt_memset_zero on odd sizes and unaligned addresses, eagerly and replayed from a captured HIP graph; the bytes
+    around the range are untouched."""
+    import ctypes
+    from omarchy_mac_torch import _lib
+    buf = torch.full((4096,), 0xAB, dtype=torch.uint8, device=cuda)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for off, n in ((0, 4096 - 16), (3, 1001), (16, 1), (5, 0)):
+        buf.fill_(0xAB)
+        _lib.check(_lib.L.omt_memset_zero(ctypes.c_void_p(buf.data_ptr() + off), n, stream), "omt_memset_zero")
+        h = buf.cpu().numpy()
+        assert (h[off:off + n] == 0).all() and (h[:off] == 0xAB).all() and (h[off + n:] == 0xAB).all(), (off, n)
+    buf.fill_(0xAB)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        _lib.L.omt_memset_zero(ctypes.c_void_p(buf.data_ptr() + 7), 2000,
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for _ in range(3):
+        buf.fill_(0xAB)
+        g.replay()
+        h = buf.cpu().numpy()
+        assert (h[7:2007] == 0).all() and (h[:7] == 0xAB).all() and (h[2007:] == 0xAB).all()
+
+
 PLAN_SHAPES = [
     (4, 512, 512, 2, 2, 3, 1, 1),   # ResNet-18 layer4 at 64x64: the cost model splits K
     (3, 64, 128, 9, 9, 3, 2, 1),    # stride 2: grad-input phases with different K
