@@ -425,13 +425,58 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   }
 }
 
-// Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i].
+// Slice sums load kReduceBatch slices at a time (the loads in flight together, the additions still in slice order),
+// so a launch waits one memory latency per batch rather than per slice.
+constexpr int kReduceBatch = 8;
+
+template <int VEC>
+struct VecF;
+template <>
+struct VecF<1> {
+  using T = float;
+  static __device__ __forceinline__ void add(float* v, T t) { v[0] += t; }
+  static __device__ __forceinline__ void set(float* v, T t) { v[0] = t; }
+  static __device__ __forceinline__ T pack(const float* v) { return v[0]; }
+};
+template <>
+struct VecF<4> {
+  using T = float4;
+  static __device__ __forceinline__ void add(float* v, T t) { v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w; }
+  static __device__ __forceinline__ void set(float* v, T t) { v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w; }
+  static __device__ __forceinline__ T pack(const float* v) { return make_float4(v[0], v[1], v[2], v[3]); }
+};
+
+// v = sum_z part[z * nv + i] over z in slice order (vectors of VEC floats; nv vectors per slice).
+template <int VEC>
+__device__ __forceinline__ void sum_slices(const typename VecF<VEC>::T* __restrict__ part, int64_t nv, int64_t i,
+                                           int slices, float* v) {
+  using T = typename VecF<VEC>::T;
+  for (int z0 = 0; z0 < slices; z0 += kReduceBatch) {
+    T t[kReduceBatch];
+#pragma unroll
+    for (int u = 0; u < kReduceBatch; ++u)
+      if (z0 + u < slices) t[u] = part[(int64_t)(z0 + u) * nv + i];
+#pragma unroll
+    for (int u = 0; u < kReduceBatch; ++u)
+      if (z0 + u < slices) {
+        if (z0 + u == 0)
+          VecF<VEC>::set(v, t[u]);
+        else
+          VecF<VEC>::add(v, t[u]);
+      }
+  }
+}
+
+// Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i]. VEC 4 needs n % 4 == 0.
+template <int VEC>
 __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            int64_t n, int slices) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    float s = 0.f;
-    for (int z = 0; z < slices; ++z) s += part[(int64_t)z * n + i];
-    out[i] = s;
+  using T = typename VecF<VEC>::T;
+  const int64_t nv = n / VEC;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
+    float v[VEC];
+    sum_slices<VEC>(reinterpret_cast<const T*>(part), nv, i, slices, v);
+    reinterpret_cast<T*>(out)[i] = VecF<VEC>::pack(v);
   }
 }
 
@@ -441,33 +486,18 @@ template <int VEC>
 __global__ void __launch_bounds__(256) gather_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
                                                             int64_t n, int slices, int64_t plane, int P,
                                                             const float* __restrict__ bias, int relu) {
+  using T = typename VecF<VEC>::T;
   const int64_t nv = n / VEC;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
     float v[VEC];
-    if (VEC == 4) {
-      const float4 t = reinterpret_cast<const float4*>(part)[i];
-      v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
-    } else {
-      v[0] = part[i];
-    }
-    for (int z = 1; z < slices; ++z) {
-      if (VEC == 4) {
-        const float4 t = reinterpret_cast<const float4*>(part + z * n)[i];
-        v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w;
-      } else {
-        v[0] += part[z * n + i];
-      }
-    }
+    sum_slices<VEC>(reinterpret_cast<const T*>(part), nv, i, slices, v);
     const float b = bias ? bias[(i * VEC / plane) % P] : 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       v[e] += b;
       if (relu) v[e] = fmaxf(v[e], 0.f);
     }
-    if (VEC == 4)
-      reinterpret_cast<float4*>(y)[i] = make_float4(v[0], v[1], v[2], v[3]);
-    else
-      y[i] = v[0];
+    reinterpret_cast<T*>(y)[i] = VecF<VEC>::pack(v);
   }
 }
 
@@ -670,7 +700,7 @@ static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t ma
   if (int st = launch_check("conv_gather_kernel")) return st;
   if (pl.slices > 1) {
     const int64_t plane = (int64_t)a.YH * a.YW;
-    if (plane % 4 == 0)
+    if (plane % 4 == 0 && (uintptr_t)a.y % 16 == 0)
       hipLaunchKernelGGL(gather_reduce_kernel<4>, dim3(grid1d(total / 4, 256, 8192)), dim3(256), 0, s, part, a.y,
                          total, (int)pl.slices, plane, a.P, a.bias, a.relu);
     else
@@ -1010,8 +1040,12 @@ OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float
   if (int st = launch_check("conv_wgrad_kernel")) return st;
   if (pl.slices > 1) {
     const int64_t n = (int64_t)a.P * a.Q;
-    hipLaunchKernelGGL(split_reduce_kernel, dim3(grid1d(n, 256, 8192)), dim3(256), 0, s, (const float*)workspace, gw, n,
-                       (int)pl.slices);
+    if (n % 4 == 0 && (uintptr_t)gw % 16 == 0)
+      hipLaunchKernelGGL(split_reduce_kernel<4>, dim3(grid1d(n / 4, 256, 8192)), dim3(256), 0, s,
+                         (const float*)workspace, gw, n, (int)pl.slices);
+    else
+      hipLaunchKernelGGL(split_reduce_kernel<1>, dim3(grid1d(n, 256, 8192)), dim3(256), 0, s, (const float*)workspace,
+                         gw, n, (int)pl.slices);
     if (int st = launch_check("split_reduce_kernel")) return st;
   }
   return OMT_OK;
