@@ -139,6 +139,14 @@ size_t omt_conv_wgrad_workspace(const omt_conv_geo* g);
 int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Grad input and grad weight together: the dense branch of convolution_backward with both outputs requested
+ * (csrc/conv.cpp:207-220 calls gemm_grad_input, then gemm_grad_weight). Results are those of omt_conv_dgrad and
+ * omt_conv_wgrad (same plans, same summation order). When both plans use 64x64 tiles, the two GEMMs run in one launch,
+ * and so do their split-K sums. Workspace: [grad-input workspace | 256-byte aligned grad-weight workspace]. */
+size_t omt_conv_bwd_workspace(const omt_conv_geo* g);
+int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx, float* gw,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- plan cache and tuning (replaces conv_plan / autotune / tune_dump / tune_load / tuned_plans,
  * csrc/conv.cpp:45-60, 116-155, 243-282) ---------------------------------------------------------------------
  * Every dense-conv call and workspace query resolves its plan from a process-wide cache keyed by (direction,

@@ -90,8 +90,14 @@ struct GatherArgs {
   Phase ph[kMaxPhases];
 };
 
+// LDS floats of a gather tile: both operands double-buffered, rows of BK + 4.
+template <int BP, int BQ, int BK>
+constexpr int gather_lds_floats() { return 2 * (BP + BQ) * (BK + 4); }
+
+// One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats().
 template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN>
-__global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
+__device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, const int by, const int bz,
+                                            float* __restrict__ lds) {
   constexpr int NT = 256;
   static_assert(BK % 16 == 0 && NT % BK == 0, "K-block");
   constexpr int WGQ = BQ / WQ;
@@ -102,14 +108,14 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
   constexpr int AR = BP * BK / NT;  // weight elements per thread
   constexpr int BR = BQ * BK / NT;  // gathered k-rows per thread (a multiple of 4: stored as b128)
   static_assert(AR >= 1 && BR >= 4 && BR % 4 == 0, "tile too small");
-  __shared__ __attribute__((aligned(16))) float As[2][BP * PK];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BQ * PK];
+  float(*const As)[BP * PK] = reinterpret_cast<float(*)[BP * PK]>(lds);
+  float(*const Bs)[BQ * PK] = reinterpret_cast<float(*)[BQ * PK]>(lds + 2 * BP * PK);
 
-  const int zs = (int)blockIdx.z / a.nphase;  // K slice
+  const int zs = bz / a.nphase;  // K slice
   // a register copy: reads through the dynamically indexed kernel argument would each become a scalar load at its
   // use, some inside the per-element bounds branches of the loaders
-  const Phase ph = a.ph[(int)blockIdx.z - zs * a.nphase];
-  const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
+  const Phase ph = a.ph[bz - zs * a.nphase];
+  const int q0 = bx * BQ, p0 = by * BP;
   if (q0 >= ph.Q) return;  // this phase has fewer pixel tiles than the largest one
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -273,6 +279,12 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
   }
 }
 
+template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN>
+__global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[gather_lds_floats<BP, BQ, BK>()];
+  gather_tile<BP, BQ, WP, WQ, BK, MODE, BN>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+}
+
 // ---- grad weight ------------------------------------------------------------------------------------------------
 
 struct WgradArgs {
@@ -286,8 +298,14 @@ struct WgradArgs {
   FastDiv div_ohw, div_ow, div_kk, div_ks, div_c;
 };
 
+// LDS floats of a grad-weight tile: both operands, rows of 64 + 4.
+template <int BP, int BQ>
+constexpr int wgrad_lds_floats() { return (BP + BQ) * (64 + 4); }
+
+// One workgroup's tile (bx, by) of K slice bz; lds holds wgrad_lds_floats().
 template <int BP, int BQ, int WP, int WQ, int MODE>
-__global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
+__device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, const int by, const int bz,
+                                           float* __restrict__ lds) {
   constexpr int BK = 64;  // one reduction pixel per lane
   constexpr int WGQ = BQ / WQ;
   static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
@@ -295,14 +313,14 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   constexpr int TI = WP / 16, TJ = WQ / 16;
   constexpr int PK = BK + 4;               // LDS row pitch (floats): rows are gy channels / tap columns, k contiguous
   constexpr int AR = BP / 4, BR = BQ / 4;  // rows (cols) each wave stages per K-block, contiguous per wave
-  __shared__ __attribute__((aligned(16))) float As[BP * PK];
-  __shared__ __attribute__((aligned(16))) float Bs[BQ * PK];
+  float* const As = lds;
+  float* const Bs = lds + BP * PK;
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wp = wave / WGQ, wq = wave % WGQ;
-  const int q0 = blockIdx.x * BQ, p0 = blockIdx.y * BP;
-  const int kbeg = blockIdx.z * a.kslice;
+  const int q0 = bx * BQ, p0 = by * BP;
+  const int kbeg = bz * a.kslice;
   const int kend = min(a.K, kbeg + a.kslice);
   const int H = a.H, W = a.W, HW = H * W, P = a.P, Q = a.Q, KS = a.KS;
   const int ohw = a.OH * a.OW;
@@ -405,7 +423,7 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   }
 
   // store in the [co][ci][ky][kx] order of the weight gradient (tap-major columns are permuted back)
-  float* out = a.out + (int64_t)blockIdx.z * P * Q;
+  float* out = a.out + (int64_t)bz * P * Q;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int q = q0 + wq * WQ + 16 * j + (lane & 15);
@@ -422,6 +440,37 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
         const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
         if (p < P) out[(int64_t)p * Q + col] = acc[i][j][r4];
       }
+  }
+}
+
+template <int BP, int BQ, int WP, int WQ, int MODE>
+__global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[wgrad_lds_floats<BP, BQ>()];
+  wgrad_tile<BP, BQ, WP, WQ, MODE>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+}
+
+// Grad input and grad weight of one convolution in one launch (omt_conv_bwd), both on 64 x 64 tiles: the first
+// gx * gy * gz workgroups run grad-input tiles (x fastest), the rest grad-weight tiles over wx * wy * wz. On late,
+// low-resolution layers each GEMM alone puts about one workgroup on a CU, which then waits on its loads; in one launch
+// every CU also holds a workgroup of the other GEMM to run meanwhile.
+struct DualGrid {
+  int gx, gy, gz, wx, wy, wz;
+};
+template <int GBK, int GMODE, int WMODE>
+__global__ void __launch_bounds__(256, 2) conv_bwd_dual_kernel(const GatherArgs ga, const WgradArgs wa, const DualGrid d) {
+  constexpr int kG = gather_lds_floats<64, 64, GBK>(), kW = wgrad_lds_floats<64, 64>();
+  __shared__ __attribute__((aligned(16))) float lds[kG > kW ? kG : kW];
+  int b = (int)blockIdx.x;
+  const int ng = d.gx * d.gy * d.gz;
+  if (b < ng) {
+    const int bx = b % d.gx;
+    b /= d.gx;
+    gather_tile<64, 64, 32, 32, GBK, GMODE, false>(ga, bx, b % d.gy, b / d.gy, lds);
+  } else {
+    b -= ng;
+    const int bx = b % d.wx;
+    b /= d.wx;
+    wgrad_tile<64, 64, 32, 32, WMODE>(wa, bx, b % d.wy, b / d.wy, lds);
   }
 }
 
@@ -467,13 +516,14 @@ __device__ __forceinline__ void sum_slices(const typename VecF<VEC>::T* __restri
   }
 }
 
-// Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i]. VEC 4 needs n % 4 == 0.
+// Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i]. VEC 4 needs n % 4 == 0. Workgroups
+// b0 .. b0 + nb - 1 of the launch stride over the vectors.
 template <int VEC>
-__global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                           int64_t n, int slices) {
+__device__ __forceinline__ void split_sum(const float* __restrict__ part, float* __restrict__ out, int64_t n,
+                                          int slices, int64_t b0, int64_t nb) {
   using T = typename VecF<VEC>::T;
   const int64_t nv = n / VEC;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t i = b0 * blockDim.x + threadIdx.x; i < nv; i += nb * blockDim.x) {
     float v[VEC];
     sum_slices<VEC>(reinterpret_cast<const T*>(part), nv, i, slices, v);
     reinterpret_cast<T*>(out)[i] = VecF<VEC>::pack(v);
@@ -482,23 +532,58 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
 
 // Split-K gather epilogue: y[i] = act(sum_z part[z][i] + bias[c(i)]), slices summed in order; y is NCHW with
 // planes of `plane` elements over `P` channels. VEC 4 needs plane % 4 == 0 (a float4 then stays in one plane).
+struct GatherSum {
+  const float* part;
+  float* y;
+  int64_t total, plane;
+  int slices, P;
+  const float* bias;
+  int relu;
+  bool vec4;
+  int64_t blocks;  // workgroups of its launch
+};
 template <int VEC>
-__global__ void __launch_bounds__(256) gather_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
-                                                            int64_t n, int slices, int64_t plane, int P,
-                                                            const float* __restrict__ bias, int relu) {
+__device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64_t nb) {
   using T = typename VecF<VEC>::T;
-  const int64_t nv = n / VEC;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t nv = r.total / VEC;
+  for (int64_t i = b0 * blockDim.x + threadIdx.x; i < nv; i += nb * blockDim.x) {
     float v[VEC];
-    sum_slices<VEC>(reinterpret_cast<const T*>(part), nv, i, slices, v);
-    const float b = bias ? bias[(i * VEC / plane) % P] : 0.f;
+    sum_slices<VEC>(reinterpret_cast<const T*>(r.part), nv, i, r.slices, v);
+    const float b = r.bias ? r.bias[(i * VEC / r.plane) % r.P] : 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       v[e] += b;
-      if (relu) v[e] = fmaxf(v[e], 0.f);
+      if (r.relu) v[e] = fmaxf(v[e], 0.f);
     }
-    reinterpret_cast<T*>(y)[i] = VecF<VEC>::pack(v);
+    reinterpret_cast<T*>(r.y)[i] = VecF<VEC>::pack(v);
   }
+}
+
+struct SplitSum {
+  const float* part;
+  float* out;
+  int64_t n;
+  int slices;
+  bool vec4;
+  int64_t blocks;
+};
+
+template <int VEC>
+__global__ void __launch_bounds__(256) split_reduce_kernel(const SplitSum r) {
+  split_sum<VEC>(r.part, r.out, r.n, r.slices, blockIdx.x, gridDim.x);
+}
+template <int VEC>
+__global__ void __launch_bounds__(256) gather_reduce_kernel(const GatherSum r) {
+  gather_sum<VEC>(r, blockIdx.x, gridDim.x);
+}
+// Both split-K sums of a convolution backward in one launch: the first g.blocks workgroups sum grad input.
+template <int GV, int WV>
+__global__ void __launch_bounds__(256) dual_reduce_kernel(const GatherSum g, const SplitSum w) {
+  const int64_t b = blockIdx.x;
+  if (b < g.blocks)
+    gather_sum<GV>(g, b, g.blocks);
+  else
+    split_sum<WV>(w.part, w.out, w.n, w.slices, b - g.blocks, (int64_t)gridDim.x - g.blocks);
 }
 
 // Re-packs w[co][ci][ks][ks] into the per-phase grad-input weights W'[ci][co][a'][b'] described at the top.
@@ -683,32 +768,55 @@ static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const 
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size.
-static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part, hipStream_t s) {
+// Completes a gather launch's arguments for its plan: K slice length and, split over K, the partials `part` (the
+// workspace of the plan's size). Returns the grid.
+static dim3 gather_grid(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part) {
   const Tile& tl = gtile(pl.tile);
   a.kslice = (int)pl.kslice;
-  const int64_t total = n * a.P * a.YH * a.YW;
   a.part = pl.slices > 1 ? part : nullptr;
-  a.part_stride = total;
-  dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
+  a.part_stride = n * a.P * a.YH * a.YW;
+  return dim3((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
+}
+// Tap-major K order of a gather launch (the BN loader keeps the channel-major order).
+static bool gather_uses_tap_major(const GatherArgs& a, const GatherPlan& pl) {
+  return !a.bn_mean && !gcm(pl.tile) && gather_tap_major(a.C, false, gtile(pl.tile).bk);
+}
+// The slice sum of a split gather launch (blocks 0 if the plan does not split).
+static GatherSum gather_sum_of(const GatherArgs& a, const GatherPlan& pl) {
+  GatherSum r{};
+  if (pl.slices <= 1) return r;
+  r.part = a.part;
+  r.y = a.y;
+  r.total = a.part_stride;
+  r.plane = (int64_t)a.YH * a.YW;
+  r.slices = (int)pl.slices;
+  r.P = a.P;
+  r.bias = a.bias;
+  r.relu = a.relu;
+  r.vec4 = r.plane % 4 == 0 && (uintptr_t)a.y % 16 == 0;
+  r.blocks = grid1d(r.vec4 ? r.total / 4 : r.total, 256, 8192);
+  return r;
+}
+static int launch_gather_sum(const GatherSum& r, hipStream_t s) {
+  if (!r.blocks) return OMT_OK;
+  if (r.vec4)
+    hipLaunchKernelGGL(gather_reduce_kernel<4>, dim3((unsigned)r.blocks), dim3(256), 0, s, r);
+  else
+    hipLaunchKernelGGL(gather_reduce_kernel<1>, dim3((unsigned)r.blocks), dim3(256), 0, s, r);
+  return launch_check("gather_reduce_kernel");
+}
+
+// Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size.
+static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part, hipStream_t s) {
+  const dim3 grid = gather_grid(a, pl, n, maxq, part);
   if (a.bn_mean)
     gather_dispatch<kGeneric, true>(pl.tile % kNGather, a, grid, s);
-  else if (!gcm(pl.tile) && gather_tap_major(a.C, false, tl.bk))
+  else if (gather_uses_tap_major(a, pl))
     gather_dispatch<kTapMajor, false>(pl.tile % kNGather, a, grid, s);
   else
     gather_dispatch<kGeneric, false>(pl.tile % kNGather, a, grid, s);
   if (int st = launch_check("conv_gather_kernel")) return st;
-  if (pl.slices > 1) {
-    const int64_t plane = (int64_t)a.YH * a.YW;
-    if (plane % 4 == 0 && (uintptr_t)a.y % 16 == 0)
-      hipLaunchKernelGGL(gather_reduce_kernel<4>, dim3(grid1d(total / 4, 256, 8192)), dim3(256), 0, s, part, a.y,
-                         total, (int)pl.slices, plane, a.P, a.bias, a.relu);
-    else
-      hipLaunchKernelGGL(gather_reduce_kernel<1>, dim3(grid1d(total, 256, 8192)), dim3(256), 0, s, part, a.y, total,
-                         (int)pl.slices, plane, a.P, a.bias, a.relu);
-    if (int st = launch_check("gather_reduce_kernel")) return st;
-  }
-  return OMT_OK;
+  return launch_gather_sum(gather_sum_of(a, pl), s);
 }
 
 static bool dense_geo_ok(const omt_conv_geo* g) {
@@ -944,20 +1052,20 @@ OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
   return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * g->ci * g->ih * g->iw) * sizeof(float) : pack;
 }
 
-OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
-                              size_t workspace_bytes, void* stream) {
-  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad: null pointer");
-  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: geometry not covered");
-  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad: a tensor of 2 GiB or more");
-  const size_t need = omt_conv_dgrad_workspace(g);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", need);
-  hipStream_t s = stream_of(stream);
-  GatherArgs a{};
+static int geo_check(const omt_conv_geo* g, const char* fn) {
+  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", fn);
+  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "%s: a tensor of 2 GiB or more", fn);
+  return OMT_OK;
+}
+
+// Grad-input launch arguments over `workspace` (of omt_conv_dgrad_workspace's size); launches the filter re-pack of the
+// tap-major order. The gather itself is left to the caller (gather_grid, then a launch).
+static int dgrad_prepare(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                         hipStream_t s, GatherArgs& a, GatherPlan& pl, int64_t& maxq, float*& part) {
   PackArgs pk{};
-  int64_t maxq = 0;
+  a = GatherArgs{};
   const int packed = dgrad_phases(g, a, pk, maxq);
-  const GatherPlan pl = dgrad_plan(g);
+  pl = dgrad_plan(g);
   const size_t pack = dgrad_pack_bytes(g, pl);
   if (pack) {
     pk.w = w;
@@ -988,7 +1096,24 @@ OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const floa
   a.YH = (int)g->ih;
   a.YW = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather(a, pl, g->n, maxq, workspace ? (float*)((char*)workspace + align256(pack)) : nullptr, s);
+  part = workspace ? (float*)((char*)workspace + align256(pack)) : nullptr;
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad: null pointer");
+  if (int st = geo_check(g, "omt_conv_dgrad")) return st;
+  const size_t need = omt_conv_dgrad_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  GatherArgs a;
+  GatherPlan pl;
+  int64_t maxq = 0;
+  float* part = nullptr;
+  if (int st = dgrad_prepare(g, gy, w, gx, workspace, s, a, pl, maxq, part)) return st;
+  return run_gather(a, pl, g->n, maxq, part, s);
 }
 
 OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
@@ -998,17 +1123,11 @@ OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
   return (size_t)(pl.slices * g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
-OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
-                              size_t workspace_bytes, void* stream) {
-  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
-  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: geometry not covered");
-  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad: a tensor of 2 GiB or more");
-  const size_t need = omt_conv_wgrad_workspace(g);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
-  hipStream_t s = stream_of(stream);
-  WgradPlan pl = wgrad_plan(g);
-  WgradArgs a{};
+// Grad-weight launch arguments over `workspace` (of omt_conv_wgrad_workspace's size) and the launch's grid.
+static dim3 wgrad_prepare(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                          WgradArgs& a, WgradPlan& pl) {
+  pl = wgrad_plan(g);
+  a = WgradArgs{};
   a.x = x;
   a.gy = gy;
   a.out = pl.slices > 1 ? (float*)workspace : gw;
@@ -1032,23 +1151,132 @@ OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float
   a.div_ks = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)g->ci);
   const Tile& tl = kWgradTiles[pl.tile];
-  dim3 grid((unsigned)cdiv(a.Q, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)pl.slices);
-  if (g->ci % (kWgradTiles[pl.tile].bq / 4) == 0)
+  return dim3((unsigned)cdiv(a.Q, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)pl.slices);
+}
+// Tap-major column order of a grad-weight launch: each wave's BQ / 4 staged columns share one tap.
+static bool wgrad_uses_tap_major(const omt_conv_geo* g, const WgradPlan& pl) {
+  return g->ci % (kWgradTiles[pl.tile].bq / 4) == 0;
+}
+// The slice sum of a split grad-weight launch (blocks 0 if the plan does not split).
+static SplitSum wgrad_sum_of(const WgradArgs& a, const WgradPlan& pl, float* gw) {
+  SplitSum r{};
+  if (pl.slices <= 1) return r;
+  r.part = a.out;
+  r.out = gw;
+  r.n = (int64_t)a.P * a.Q;
+  r.slices = (int)pl.slices;
+  r.vec4 = r.n % 4 == 0 && (uintptr_t)gw % 16 == 0;
+  r.blocks = grid1d(r.vec4 ? r.n / 4 : r.n, 256, 8192);
+  return r;
+}
+static int launch_split_sum(const SplitSum& r, hipStream_t s) {
+  if (!r.blocks) return OMT_OK;
+  if (r.vec4)
+    hipLaunchKernelGGL(split_reduce_kernel<4>, dim3((unsigned)r.blocks), dim3(256), 0, s, r);
+  else
+    hipLaunchKernelGGL(split_reduce_kernel<1>, dim3((unsigned)r.blocks), dim3(256), 0, s, r);
+  return launch_check("split_reduce_kernel");
+}
+
+OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
+  if (int st = geo_check(g, "omt_conv_wgrad")) return st;
+  const size_t need = omt_conv_wgrad_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  WgradArgs a;
+  WgradPlan pl;
+  const dim3 grid = wgrad_prepare(g, x, gy, gw, workspace, a, pl);
+  if (wgrad_uses_tap_major(g, pl))
     wgrad_dispatch<kTapMajor>(pl.tile, a, grid, s);
   else
     wgrad_dispatch<kGeneric>(pl.tile, a, grid, s);
   if (int st = launch_check("conv_wgrad_kernel")) return st;
-  if (pl.slices > 1) {
-    const int64_t n = (int64_t)a.P * a.Q;
-    if (n % 4 == 0 && (uintptr_t)gw % 16 == 0)
-      hipLaunchKernelGGL(split_reduce_kernel<4>, dim3(grid1d(n / 4, 256, 8192)), dim3(256), 0, s,
-                         (const float*)workspace, gw, n, (int)pl.slices);
+  return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
+}
+
+// ---- grad input and grad weight together ------------------------------------------------------------------------
+
+// One launch for both GEMMs when their plans use the 64 x 64 tiles of conv_bwd_dual_kernel.
+static bool dual_tiles(const GatherPlan& dp, const WgradPlan& wp) {
+  const Tile& gt = gtile(dp.tile);
+  const Tile& wt = kWgradTiles[wp.tile];
+  return gt.bp == 64 && gt.bq == 64 && gt.wp == 32 && gt.wq == 32 && (gt.bk == 16 || gt.bk == 64) && wt.bp == 64 &&
+         wt.bq == 64 && wt.wp == 32 && wt.wq == 32;
+}
+
+OMT_EXPORT size_t omt_conv_bwd_workspace(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
+  const size_t d = omt_conv_dgrad_workspace(g), w = omt_conv_wgrad_workspace(g);
+  return w ? align256(d) + w : d;
+}
+
+OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx,
+                            float* gw, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !w || !gx || !gw) return fail(OMT_INVALID, "omt_conv_bwd: null pointer");
+  if (int st = geo_check(g, "omt_conv_bwd")) return st;
+  const size_t need = omt_conv_bwd_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_bwd: workspace of %zu bytes needed", need);
+  const size_t dbytes = omt_conv_dgrad_workspace(g);
+  void* dws = dbytes ? workspace : nullptr;
+  void* wws = omt_conv_wgrad_workspace(g) ? (char*)workspace + align256(dbytes) : nullptr;
+  hipStream_t s = stream_of(stream);
+  GatherArgs ga;
+  GatherPlan dp;
+  int64_t maxq = 0;
+  float* part = nullptr;
+  if (int st = dgrad_prepare(g, gy, w, gx, dws, s, ga, dp, maxq, part)) return st;
+  WgradArgs wa;
+  WgradPlan wp;
+  const dim3 wgrid = wgrad_prepare(g, x, gy, gw, wws, wa, wp);
+  if (!dual_tiles(dp, wp)) {
+    if (int st = run_gather(ga, dp, g->n, maxq, part, s)) return st;
+    if (wgrad_uses_tap_major(g, wp))
+      wgrad_dispatch<kTapMajor>(wp.tile, wa, wgrid, s);
     else
-      hipLaunchKernelGGL(split_reduce_kernel<1>, dim3(grid1d(n, 256, 8192)), dim3(256), 0, s, (const float*)workspace,
-                         gw, n, (int)pl.slices);
-    if (int st = launch_check("split_reduce_kernel")) return st;
+      wgrad_dispatch<kGeneric>(wp.tile, wa, wgrid, s);
+    if (int st = launch_check("conv_wgrad_kernel")) return st;
+    return launch_split_sum(wgrad_sum_of(wa, wp, gw), s);
   }
-  return OMT_OK;
+  const dim3 ggrid = gather_grid(ga, dp, g->n, maxq, part);
+  const DualGrid d{(int)ggrid.x, (int)ggrid.y, (int)ggrid.z, (int)wgrid.x, (int)wgrid.y, (int)wgrid.z};
+  const int64_t blocks = (int64_t)d.gx * d.gy * d.gz + (int64_t)d.wx * d.wy * d.wz;
+  if (blocks >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_conv_bwd: grid too large");
+  const bool gtap = gather_uses_tap_major(ga, dp), wtap = wgrad_uses_tap_major(g, wp);
+  const bool deep = gtile(dp.tile).bk == 64;
+  const dim3 grid((unsigned)blocks);
+#define OMT_DUAL(BK, GM, WM) hipLaunchKernelGGL((conv_bwd_dual_kernel<BK, GM, WM>), grid, dim3(256), 0, s, ga, wa, d)
+  switch ((deep ? 4 : 0) + (gtap ? 2 : 0) + (wtap ? 1 : 0)) {
+    case 7: OMT_DUAL(64, kTapMajor, kTapMajor); break;
+    case 6: OMT_DUAL(64, kTapMajor, kGeneric); break;
+    case 5: OMT_DUAL(64, kGeneric, kTapMajor); break;
+    case 4: OMT_DUAL(64, kGeneric, kGeneric); break;
+    case 3: OMT_DUAL(16, kTapMajor, kTapMajor); break;
+    case 2: OMT_DUAL(16, kTapMajor, kGeneric); break;
+    case 1: OMT_DUAL(16, kGeneric, kTapMajor); break;
+    default: OMT_DUAL(16, kGeneric, kGeneric); break;
+  }
+#undef OMT_DUAL
+  if (int st = launch_check("conv_bwd_dual_kernel")) return st;
+  const GatherSum gsum = gather_sum_of(ga, dp);
+  const SplitSum wsum = wgrad_sum_of(wa, wp, gw);
+  if (!gsum.blocks || !wsum.blocks) {
+    if (int st = launch_gather_sum(gsum, s)) return st;
+    return launch_split_sum(wsum, s);
+  }
+  const dim3 rgrid((unsigned)(gsum.blocks + wsum.blocks));
+  if (gsum.vec4 && wsum.vec4)
+    hipLaunchKernelGGL((dual_reduce_kernel<4, 4>), rgrid, dim3(256), 0, s, gsum, wsum);
+  else if (gsum.vec4)
+    hipLaunchKernelGGL((dual_reduce_kernel<4, 1>), rgrid, dim3(256), 0, s, gsum, wsum);
+  else if (wsum.vec4)
+    hipLaunchKernelGGL((dual_reduce_kernel<1, 4>), rgrid, dim3(256), 0, s, gsum, wsum);
+  else
+    hipLaunchKernelGGL((dual_reduce_kernel<1, 1>), rgrid, dim3(256), 0, s, gsum, wsum);
+  return launch_check("dual_reduce_kernel");
 }
 
 OMT_EXPORT int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream) {

@@ -79,6 +79,8 @@ SIGNATURES = {
     "omt_conv_dgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_workspace": (SZ, [G]),
     "omt_conv_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_conv_bwd_workspace": (SZ, [G]),
+    "omt_conv_bwd": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_num_tiles": (I32, [I32]),
     "omt_conv_get_plan": (I32, [I32, G, PL, ctypes.POINTER(I32)]),
     "omt_conv_set_plan": (I32, [I32, G, PL]),

@@ -94,6 +94,21 @@ def conv2d_wgrad(x, gy, ks, stride=1, padding=0):
     return gw
 
 
+def conv2d_bwd(x, gy, w, stride=1, padding=0):
+    """(grad input, grad weight) of one dense convolution in one call (omt_conv_bwd: both GEMMs share a launch when
+    their plans allow it)."""
+    x, gy, w = _need(x, "x", 4), _need(gy, "gy", 4), _need(w, "w", 4)
+    g = conv_geo_for(x.shape, w.shape, stride, padding)
+    if tuple(gy.shape) != (g.n, g.co, g.oh, g.ow):
+        raise ValueError(f"conv bwd: gy {tuple(gy.shape)} != {(g.n, g.co, g.oh, g.ow)}")
+    gx = torch.empty(tuple(x.shape), device=x.device, dtype=torch.float32)
+    gw = torch.empty(tuple(w.shape), device=x.device, dtype=torch.float32)
+    ws, nb = _workspace(L.omt_conv_bwd_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_conv_bwd(ctypes.byref(g), _ptr(x), _ptr(gy), _ptr(w), _ptr(gx), _ptr(gw), _ptr(ws), nb,
+                         _stream(x.device)), "conv2d_bwd")
+    return gx, gw
+
+
 # ---- plan cache (tile / split-K per geometry) and tuning (reference: conv_plan, autotune, tune_dump, tune_load,
 # csrc/conv.cpp:45-60, 116-155, 243-272) ------------------------------------------------------------------------
 

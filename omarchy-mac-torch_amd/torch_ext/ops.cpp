@@ -71,7 +71,15 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
   NEED(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");
   Tensor gx, gw, gb;
   void* s = cur_stream();
-  if (kind == OMT_CONV_DENSE) {
+  if (kind == OMT_CONV_DENSE && mask[0] && mask[1]) {
+    // both GEMMs in one call: they share a launch when their plans allow it
+    gx = empty_dev(x.sizes());
+    gw = empty_dev(w.sizes());
+    tune_conv(OMT_DIR_DGRAD, g);
+    tune_conv(OMT_DIR_WGRAD, g);
+    Tensor ws = workspace(omt_conv_bwd_workspace(&g));
+    check(omt_conv_bwd(&g, fp(x), fp(gy), fp(w), fpm(gx), fpm(gw), wsptr(ws), wsbytes(ws), s), "convolution_backward");
+  } else if (kind == OMT_CONV_DENSE) {
     if (mask[0]) {
       gx = empty_dev(x.sizes());
       tune_conv(OMT_DIR_DGRAD, g);

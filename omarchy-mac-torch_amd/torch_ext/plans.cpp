@@ -273,6 +273,19 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       omt_conv_geo geo = conv_geo(n_, c_, r.co, h_, w_, r.ks, 1, r.ks / 2);
       Tensor x = r.x, wt = params[r.param];
       const int gi = r.param;
+      if (!dw && (!first || input_grad)) {
+        // dense with both gradients: one call, the two GEMMs share a launch when their plans allow it
+        tune_conv(OMT_DIR_WGRAD, geo);
+        tune_conv(OMT_DIR_DGRAD, geo);
+        Tensor gx = own(p, {n_, c_, h_, w_});
+        Tensor bws = own_ws(p, omt_conv_bwd_workspace(&geo));
+        p.bwd.push_back([=](Run& run, void* s) {
+          check(omt_conv_bwd(&geo, fp(x), fp(g), fp(wt), fpm(gx), fpm(run.grads[gi]), wsptr(bws), wsbytes(bws), s),
+                "plan: input and weight gradients");
+        });
+        g = gx;
+        continue;
+      }
       if (!dw) tune_conv(OMT_DIR_WGRAD, geo);
       Tensor wws = own_ws(p, dw ? omt_dw_wgrad_workspace(&geo) : omt_conv_wgrad_workspace(&geo));
       p.bwd.push_back([=](Run& run, void* s) {

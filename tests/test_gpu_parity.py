@@ -164,6 +164,46 @@ def test_conv_every_plan(cuda, ops, shape):
         ops.clear_conv_plans()
 
 
+BWD_SHAPES = [
+    (4, 512, 512, 2, 2, 3, 1, 1),   # ResNet-18 layer4: both GEMMs split K
+    (3, 64, 128, 9, 9, 3, 2, 1),    # stride 2: grad-input stride phases
+    (2, 24, 20, 7, 7, 3, 1, 1),     # channel-major K order (C % 16 != 0)
+    (2, 32, 48, 6, 5, 1, 1, 0),     # 1x1
+    (2, 64, 64, 8, 8, 1, 2, 0),     # 1x1 stride 2: phases no tap reaches
+]
+
+
+@pytest.mark.parametrize("shape", BWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv_bwd_matches_separate_calls(cuda, ops, shape):
+    """omt_conv_bwd (grad input and grad weight in one call; one launch when both plans use 64x64 tiles) is
+    bit-identical to omt_conv_dgrad + omt_conv_wgrad under the same plans, and matches the oracle: dual and non-dual
+    plan pairs, tap-major and channel-major grad input, split K on either side."""
+    n, ci, co, h, w, ks, s, p = shape
+    rng = np.random.default_rng(sum(shape) + 5)
+    x, wt = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
+    oh, ow = (h + 2 * p - ks) // s + 1, (w + 2 * p - ks) // s + 1
+    gy = rnd(rng, n, co, oh, ow)
+    gx_ref, gw_ref = orc.conv_dgrad(gy, wt, x.shape, s, p), orc.conv_wgrad(x, gy, ks, s, p)
+    tx, tw, tgy = dev(x, cuda), dev(wt, cuda), dev(gy, cuda)
+    ng = ops.conv_num_tiles("dgrad") // 2
+    try:
+        for dtile in (5, 6, 5 + ng, 6 + ng, 0):
+            for dslices in (1, 3):
+                for wtile, wslices in ((2, 1), (2, 4), (0, 2)):
+                    case = (dtile, dslices, wtile, wslices)
+                    ops.set_conv_plan("dgrad", x.shape, wt.shape, s, p, dtile, dslices)
+                    ops.set_conv_plan("wgrad", x.shape, wt.shape, s, p, wtile, wslices)
+                    gx, gw = ops.conv2d_bwd(tx, tgy, tw, s, p)
+                    gx1 = ops.conv2d_dgrad(tgy, tw, x.shape, s, p)
+                    gw1 = ops.conv2d_wgrad(tx, tgy, ks, s, p)
+                    torch.cuda.synchronize()
+                    assert torch.equal(gx, gx1) and torch.equal(gw, gw1), case
+                    assert orc.rel_l2(host(gx), gx_ref) <= TOL, case
+                    assert orc.rel_l2(host(gw), gw_ref) <= TOL, case
+    finally:
+        ops.clear_conv_plans()
+
+
 def test_conv_split_k_bn_loader(cuda, ops):
     """The eval BN + ReLU input loader with K split over slices."""
     rng = np.random.default_rng(11)
