@@ -163,6 +163,12 @@ int omt_conv_plan_count(void);
 int omt_conv_plan_entry(int i, int* dir, omt_conv_geo* g, omt_conv_plan* plan);
 void omt_conv_clear_plans(void);
 int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* best);
+/* Tunes the grad-input and grad-weight plans together for omt_conv_bwd: the pair tuned one direction at a time
+ * (omt_conv_autotune of each) against every pair of candidates that shares a launch, timed through omt_conv_bwd;
+ * caches the fastest pair in both directions' entries. Same conditions as omt_conv_autotune. Extends the reference's
+ * autotune (csrc/conv.cpp:116-155), which tunes each GEMM alone. */
+int omt_conv_autotune_bwd(const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* dgrad_best,
+                          omt_conv_plan* wgrad_best);
 
 /* Bias grad gb[c] = sum_{n,hw} gy[n][c][hw]. Replaces csum_nchw (csrc/conv.cpp:232-235). */
 int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream);

@@ -880,14 +880,15 @@ struct PlanKey {
 };
 static std::mutex g_plan_mu;
 static std::map<PlanKey, omt_conv_plan> g_plans;
-static thread_local const omt_conv_plan* t_force = nullptr;  // the candidate under test while tuning
+// The candidates under test while tuning, per direction (both dgrad and wgrad when the backward is tuned jointly).
+static thread_local const omt_conv_plan* t_force[3] = {nullptr, nullptr, nullptr};
 
 static PlanKey key_of(int dir, const omt_conv_geo* g) {
   return {dir, g->n, g->ci, g->co, g->ih, g->iw, g->oh, g->ow, g->ks, g->stride, g->pad};
 }
 static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p) {
-  if (t_force) {
-    *p = *t_force;
+  if (t_force[dir]) {
+    *p = *t_force[dir];
     return true;
   }
   std::lock_guard<std::mutex> lk(g_plan_mu);
@@ -1411,18 +1412,81 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
 }
 
 struct ForceGuard {
-  ~ForceGuard() { t_force = nullptr; }
+  ~ForceGuard() { t_force[0] = t_force[1] = t_force[2] = nullptr; }
 };
+
+// Scratch buffers and events of one tuning run: zero inputs (fp32 MFMA timing does not depend on the values). The
+// destructor synchronizes the stream, so nothing queued still uses the buffers when they return to the cache.
+struct TuneScratch {
+  hipStream_t s;
+  void *x = nullptr, *w = nullptr, *gy = nullptr, *o1 = nullptr, *o2 = nullptr, *ws = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  explicit TuneScratch(hipStream_t st) : s(st) {}
+  int init(const omt_conv_geo* g, size_t ws_bytes) {
+    const size_t xb = (size_t)(g->n * g->ci * g->ih * g->iw) * 4, wb = (size_t)(g->co * g->ci * g->ks * g->ks) * 4,
+                 yb = (size_t)(g->n * g->co * g->oh * g->ow) * 4;
+    const size_t ob = std::max(xb, std::max(wb, yb));
+    if (int st = omt_malloc(&x, xb)) return st;
+    if (int st = omt_malloc(&w, wb)) return st;
+    if (int st = omt_malloc(&gy, yb)) return st;
+    if (int st = omt_malloc(&o1, ob)) return st;
+    if (int st = omt_malloc(&o2, wb)) return st;
+    if (ws_bytes)
+      if (int st = omt_malloc(&ws, ws_bytes)) return st;
+    if (int st = hip_check(hipMemsetAsync(x, 0, xb, s), "hipMemsetAsync")) return st;
+    if (int st = hip_check(hipMemsetAsync(w, 0, wb, s), "hipMemsetAsync")) return st;
+    if (int st = hip_check(hipMemsetAsync(gy, 0, yb, s), "hipMemsetAsync")) return st;
+    if (int st = hip_check(hipEventCreate(&e0), "hipEventCreate")) return st;
+    return hip_check(hipEventCreate(&e1), "hipEventCreate");
+  }
+  ~TuneScratch() {
+    (void)hipStreamSynchronize(s);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    for (void* p : {x, w, gy, o1, o2, ws})
+      if (p) omt_free(p);
+  }
+  // Average ms of `run` over about `budget_ms` of repetitions (at most 8) after a warm-up call.
+  template <class Run>
+  int time(Run run, float budget_ms, float* ms) {
+    auto timed = [&](int reps, float* out) -> int {
+      if (int e = hip_check(hipEventRecord(e0, s), "hipEventRecord")) return e;
+      for (int r = 0; r < reps; ++r)
+        if (int e = run()) return e;
+      if (int e = hip_check(hipEventRecord(e1, s), "hipEventRecord")) return e;
+      if (int e = hip_check(hipEventSynchronize(e1), "hipEventSynchronize")) return e;
+      if (int e = hip_check(hipEventElapsedTime(out, e0, e1), "hipEventElapsedTime")) return e;
+      *out /= (float)reps;
+      return OMT_OK;
+    };
+    float first = 0.f;
+    if (int e = run()) return e;
+    if (int e = timed(1, &first)) return e;
+    *ms = first;
+    const int reps = (int)std::max(1.f, std::min(8.f, budget_ms / std::max(first, 1e-3f)));
+    if (reps > 1) {
+      float m = 0.f;
+      if (int e = timed(reps, &m)) return e;
+      *ms = std::min(m, first);
+    }
+    return OMT_OK;
+  }
+};
+
+int refuse_capture(hipStream_t s, const char* what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  OMT_HIP(hipStreamIsCapturing(s, &cs));
+  if (cs != hipStreamCaptureStatusNone) return fail(OMT_UNSUPPORTED, "%s: stream is capturing", what);
+  return OMT_OK;
+}
 
 }  // namespace
 
 OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* best) {
   if (int st = plan_args_ok(dir, g, "omt_conv_autotune")) return st;
-  if (t_force) return fail(OMT_INVALID, "omt_conv_autotune: re-entered");
+  if (t_force[0] || t_force[1] || t_force[2]) return fail(OMT_INVALID, "omt_conv_autotune: re-entered");
   hipStream_t s = stream_of(stream);
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  OMT_HIP(hipStreamIsCapturing(s, &cs));
-  if (cs != hipStreamCaptureStatusNone) return fail(OMT_UNSUPPORTED, "omt_conv_autotune: stream is capturing");
+  if (int st = refuse_capture(s, "omt_conv_autotune")) return st;
   const int ntile = max_tiles <= 0 ? num_tiles(dir) : std::min(max_tiles, num_tiles(dir));
   const std::vector<omt_conv_plan> cands = tune_candidates(dir, g, ntile);
   if (cands.empty()) return fail(OMT_UNSUPPORTED, "omt_conv_autotune: no candidate plan");
@@ -1430,82 +1494,107 @@ OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, 
   ForceGuard guard;
   size_t ws_bytes = 0;
   for (const omt_conv_plan& c : cands) {
-    t_force = &c;
+    t_force[dir] = &c;
     const size_t b = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
                      : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
     ws_bytes = std::max(ws_bytes, b);
   }
-  t_force = nullptr;
-  const size_t xb = (size_t)(g->n * g->ci * g->ih * g->iw) * 4, wb = (size_t)(g->co * g->ci * g->ks * g->ks) * 4,
-               yb = (size_t)(g->n * g->co * g->oh * g->ow) * 4;
-  const size_t ob = dir == OMT_DIR_FWD ? yb : dir == OMT_DIR_DGRAD ? xb : wb;
-  void *x = nullptr, *w = nullptr, *y = nullptr, *o = nullptr, *ws = nullptr;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  int st = OMT_OK;
-  auto cleanup = [&]() {
-    (void)hipStreamSynchronize(s);  // nothing queued may still use the buffers when they return to the cache
-    if (e0) (void)hipEventDestroy(e0);
-    if (e1) (void)hipEventDestroy(e1);
-    for (void* p : {x, w, y, o, ws})
-      if (p) omt_free(p);
-  };
-  if ((st = omt_malloc(&x, xb)) || (st = omt_malloc(&w, wb)) || (st = omt_malloc(&y, yb)) ||
-      (st = omt_malloc(&o, ob)) || (ws_bytes && (st = omt_malloc(&ws, ws_bytes)))) {
-    cleanup();
-    return st;
-  }
-  // zero inputs: fp32 MFMA timing does not depend on the values
-  if ((st = hip_check(hipMemsetAsync(x, 0, xb, s), "hipMemsetAsync")) ||
-      (st = hip_check(hipMemsetAsync(w, 0, wb, s), "hipMemsetAsync")) ||
-      (st = hip_check(hipMemsetAsync(y, 0, yb, s), "hipMemsetAsync")) ||
-      (st = hip_check(hipEventCreate(&e0), "hipEventCreate")) || (st = hip_check(hipEventCreate(&e1), "hipEventCreate"))) {
-    cleanup();
-    return st;
-  }
-  auto run = [&]() -> int {
-    const size_t need = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
-                        : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
-    if (dir == OMT_DIR_FWD)
-      return omt_conv_fwd(g, (const float*)x, (const float*)w, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 1e-5f,
-                          (float*)o, ws, need, s);
-    if (dir == OMT_DIR_DGRAD) return omt_conv_dgrad(g, (const float*)y, (const float*)w, (float*)o, ws, need, s);
-    return omt_conv_wgrad(g, (const float*)x, (const float*)y, (float*)o, ws, need, s);
-  };
-  auto timed = [&](int reps, float* ms) -> int {
-    if (int e = hip_check(hipEventRecord(e0, s), "hipEventRecord")) return e;
-    for (int r = 0; r < reps; ++r)
-      if (int e = run()) return e;
-    if (int e = hip_check(hipEventRecord(e1, s), "hipEventRecord")) return e;
-    if (int e = hip_check(hipEventSynchronize(e1), "hipEventSynchronize")) return e;
-    if (int e = hip_check(hipEventElapsedTime(ms, e0, e1), "hipEventElapsedTime")) return e;
-    *ms /= (float)reps;
-    return OMT_OK;
-  };
+  t_force[dir] = nullptr;
   omt_conv_plan win = cands[0];
-  float win_ms = 1e30f;
-  for (const omt_conv_plan& c : cands) {
-    t_force = &c;
-    float first = 0.f, ms = 0.f;
-    if ((st = run()) || (st = timed(1, &first))) break;  // warm-up, then one timed run
-    // about 2 ms of timing per candidate, at most 8 repetitions
-    const int reps = (int)std::max(1.f, std::min(8.f, 2.f / std::max(first, 1e-3f)));
-    ms = first;
-    if (reps > 1) {
-      if ((st = timed(reps, &ms))) break;
-      ms = std::min(ms, first);
+  {
+    TuneScratch sc(s);
+    if (int st = sc.init(g, ws_bytes)) return st;
+    auto run = [&]() -> int {
+      const size_t need = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
+                          : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
+      if (dir == OMT_DIR_FWD)
+        return omt_conv_fwd(g, (const float*)sc.x, (const float*)sc.w, nullptr, 0, nullptr, nullptr, nullptr, nullptr,
+                            1e-5f, (float*)sc.o1, sc.ws, need, s);
+      if (dir == OMT_DIR_DGRAD)
+        return omt_conv_dgrad(g, (const float*)sc.gy, (const float*)sc.w, (float*)sc.o1, sc.ws, need, s);
+      return omt_conv_wgrad(g, (const float*)sc.x, (const float*)sc.gy, (float*)sc.o1, sc.ws, need, s);
+    };
+    float win_ms = 1e30f;
+    for (const omt_conv_plan& c : cands) {
+      t_force[dir] = &c;
+      float ms = 0.f;
+      if (int st = sc.time(run, 2.f, &ms)) return st;  // about 2 ms of timing per candidate
+      if (ms < win_ms) {
+        win_ms = ms;
+        win = c;
+      }
     }
-    if (ms < win_ms) {
-      win_ms = ms;
-      win = c;
-    }
+    t_force[dir] = nullptr;
   }
-  t_force = nullptr;
-  cleanup();
-  if (st) return st;
   {
     std::lock_guard<std::mutex> lk(g_plan_mu);
     g_plans[key_of(dir, g)] = win;
   }
   if (best) *best = win;
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_conv_autotune_bwd(const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* dgrad_best,
+                                     omt_conv_plan* wgrad_best) {
+  if (int st = plan_args_ok(OMT_DIR_DGRAD, g, "omt_conv_autotune_bwd")) return st;
+  if (t_force[0] || t_force[1] || t_force[2]) return fail(OMT_INVALID, "omt_conv_autotune_bwd: re-entered");
+  hipStream_t s = stream_of(stream);
+  if (int st = refuse_capture(s, "omt_conv_autotune_bwd")) return st;
+  // the pair tuned one direction at a time, then the pairs that share a launch
+  omt_conv_plan dsep, wsep;
+  if (int st = omt_conv_autotune(OMT_DIR_DGRAD, g, max_tiles, stream, &dsep)) return st;
+  if (int st = omt_conv_autotune(OMT_DIR_WGRAD, g, max_tiles, stream, &wsep)) return st;
+  std::vector<std::pair<omt_conv_plan, omt_conv_plan>> cands{{dsep, wsep}};
+  const int dtiles = max_tiles <= 0 ? num_tiles(OMT_DIR_DGRAD) : std::min(max_tiles, num_tiles(OMT_DIR_DGRAD));
+  const int wtiles = max_tiles <= 0 ? num_tiles(OMT_DIR_WGRAD) : std::min(max_tiles, num_tiles(OMT_DIR_WGRAD));
+  {
+    std::vector<omt_conv_plan> ds, wsv;
+    for (const omt_conv_plan& d : tune_candidates(OMT_DIR_DGRAD, g, dtiles)) {
+      const Tile& t = gtile(d.tile);
+      if (t.bp == 64 && t.bq == 64 && t.wp == 32 && t.wq == 32 && (t.bk == 16 || t.bk == 64)) ds.push_back(d);
+    }
+    for (const omt_conv_plan& w : tune_candidates(OMT_DIR_WGRAD, g, wtiles)) {
+      const Tile& t = kWgradTiles[w.tile];
+      if (t.bp == 64 && t.bq == 64 && t.wp == 32 && t.wq == 32) wsv.push_back(w);
+    }
+    for (const omt_conv_plan& d : ds)
+      for (const omt_conv_plan& w : wsv) cands.push_back({d, w});
+  }
+  ForceGuard guard;
+  size_t ws_bytes = 0;
+  for (const auto& c : cands) {
+    t_force[OMT_DIR_DGRAD] = &c.first;
+    t_force[OMT_DIR_WGRAD] = &c.second;
+    ws_bytes = std::max(ws_bytes, omt_conv_bwd_workspace(g));
+  }
+  t_force[OMT_DIR_DGRAD] = t_force[OMT_DIR_WGRAD] = nullptr;
+  std::pair<omt_conv_plan, omt_conv_plan> win = cands[0];
+  {
+    TuneScratch sc(s);
+    if (int st = sc.init(g, ws_bytes)) return st;
+    auto run = [&]() -> int {
+      return omt_conv_bwd(g, (const float*)sc.x, (const float*)sc.gy, (const float*)sc.w, (float*)sc.o1,
+                          (float*)sc.o2, sc.ws, omt_conv_bwd_workspace(g), s);
+    };
+    float win_ms = 1e30f;
+    for (const auto& c : cands) {
+      t_force[OMT_DIR_DGRAD] = &c.first;
+      t_force[OMT_DIR_WGRAD] = &c.second;
+      float ms = 0.f;
+      if (int st = sc.time(run, 0.5f, &ms)) return st;
+      if (ms < win_ms) {
+        win_ms = ms;
+        win = c;
+      }
+    }
+    t_force[OMT_DIR_DGRAD] = t_force[OMT_DIR_WGRAD] = nullptr;
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    g_plans[key_of(OMT_DIR_DGRAD, g)] = win.first;
+    g_plans[key_of(OMT_DIR_WGRAD, g)] = win.second;
+  }
+  if (dgrad_best) *dgrad_best = win.first;
+  if (wgrad_best) *wgrad_best = win.second;
   return OMT_OK;
 }

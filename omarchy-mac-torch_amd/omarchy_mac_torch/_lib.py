@@ -88,6 +88,7 @@ SIGNATURES = {
     "omt_conv_plan_entry": (I32, [I32, ctypes.POINTER(I32), G, PL]),
     "omt_conv_clear_plans": (None, []),
     "omt_conv_autotune": (I32, [I32, G, I32, VP, PL]),
+    "omt_conv_autotune_bwd": (I32, [G, I32, VP, PL, PL]),
     "omt_bias_grad": (I32, [I64, I64, I64, VP, VP, VP]),
     "omt_fold_bn": (I32, [I64, I64, VP, VP, VP, VP, VP, VP, F32, VP, VP, VP]),
     "omt_dw_fwd": (I32, [G, VP, VP, VP, VP, VP, VP, VP, F32, VP, VP]),

@@ -144,6 +144,16 @@ def autotune_conv(direction, x_shape, w_shape, stride=1, padding=0, max_tiles=0,
     return p.tile, p.slices
 
 
+def autotune_conv_bwd(x_shape, w_shape, stride=1, padding=0, max_tiles=0, device=None):
+    """Tunes the grad-input and grad-weight plans together for conv2d_bwd and caches the fastest pair; returns
+    ((tile, slices) of grad input, (tile, slices) of grad weight)."""
+    g = conv_geo_for(x_shape, w_shape, stride, padding)
+    d, w = _lib.ConvPlan(), _lib.ConvPlan()
+    check(L.omt_conv_autotune_bwd(ctypes.byref(g), max_tiles, _stream(device), ctypes.byref(d), ctypes.byref(w)),
+          "autotune_conv_bwd")
+    return (d.tile, d.slices), (w.tile, w.slices)
+
+
 def conv_plans():
     """The plan cache: {"dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad": (tile, slices)} (the reference's tune_dump key)."""
     out = {}

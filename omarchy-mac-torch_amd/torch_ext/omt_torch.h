@@ -73,6 +73,8 @@ std::map<std::string, int64_t>& delegated_counts();  // other ops, run on torch'
 void note_fallback(const std::string& op, const std::string& why);
 // Autotunes (direction, geometry) once when tuning is on and the plan cache has no entry (libomt_hip.so times the
 // candidates on the current stream); no-op otherwise.
+// Tunes grad input and grad weight together (for omt_conv_bwd) unless both already have cached plans.
+void tune_conv_bwd(const omt_conv_geo& g);
 void tune_conv(int dir, const omt_conv_geo& g);
 bool strict_mode();
 bool debug_mode();

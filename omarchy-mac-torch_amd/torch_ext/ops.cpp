@@ -75,8 +75,7 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
     // both GEMMs in one call: they share a launch when their plans allow it
     gx = empty_dev(x.sizes());
     gw = empty_dev(w.sizes());
-    tune_conv(OMT_DIR_DGRAD, g);
-    tune_conv(OMT_DIR_WGRAD, g);
+    tune_conv_bwd(g);
     Tensor ws = workspace(omt_conv_bwd_workspace(&g));
     check(omt_conv_bwd(&g, fp(x), fp(gy), fp(w), fpm(gx), fpm(gw), wsptr(ws), wsbytes(ws), s), "convolution_backward");
   } else if (kind == OMT_CONV_DENSE) {

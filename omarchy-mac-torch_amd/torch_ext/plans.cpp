@@ -275,8 +275,7 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       const int gi = r.param;
       if (!dw && (!first || input_grad)) {
         // dense with both gradients: one call, the two GEMMs share a launch when their plans allow it
-        tune_conv(OMT_DIR_WGRAD, geo);
-        tune_conv(OMT_DIR_DGRAD, geo);
+        tune_conv_bwd(geo);
         Tensor gx = own(p, {n_, c_, h_, w_});
         Tensor bws = own_ws(p, omt_conv_bwd_workspace(&geo));
         p.bwd.push_back([=](Run& run, void* s) {

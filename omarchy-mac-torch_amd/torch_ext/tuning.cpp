@@ -27,6 +27,17 @@ void tune_conv(int dir, const omt_conv_geo& g) {
   if (st != OMT_OK && st != OMT_UNSUPPORTED) check(st, "conv autotune");
 }
 
+void tune_conv_bwd(const omt_conv_geo& g) {
+  if (!g_tune.load(std::memory_order_relaxed)) return;
+  omt_conv_plan p;
+  int dc = 0, wc = 0;
+  if (omt_conv_get_plan(OMT_DIR_DGRAD, &g, &p, &dc) != OMT_OK || omt_conv_get_plan(OMT_DIR_WGRAD, &g, &p, &wc) != OMT_OK ||
+      (dc && wc))
+    return;
+  const int st = omt_conv_autotune_bwd(&g, g_num_tiles.load(), cur_stream(), nullptr, nullptr);
+  if (st != OMT_OK && st != OMT_UNSUPPORTED) check(st, "conv autotune");
+}
+
 static std::string key_string(int dir, const omt_conv_geo& g) {
   std::ostringstream o;
   o << dir << ',' << g.n << ',' << g.ci << ',' << g.co << ',' << g.ih << ',' << g.iw << ',' << g.oh << ',' << g.ow

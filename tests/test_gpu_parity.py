@@ -244,6 +244,26 @@ def test_autotune_caches_a_plan(cuda, ops):
         ops.clear_conv_plans()
 
 
+def test_autotune_bwd_caches_a_pair(cuda, ops):
+    """omt_conv_autotune_bwd tunes grad input and grad weight together (through omt_conv_bwd) and caches the pair;
+    conv2d_bwd then uses it and matches the oracle."""
+    rng = np.random.default_rng(13)
+    for shape in ((32, 128, 128, 8, 8, 3, 1, 1), (8, 64, 128, 9, 9, 3, 2, 1)):
+        n, ci, co, h, w, ks, s, p = shape
+        x, wt = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
+        oh, ow = (h + 2 * p - ks) // s + 1, (w + 2 * p - ks) // s + 1
+        gy = rnd(rng, n, co, oh, ow)
+        try:
+            (dt, ds), (wt_, ws) = ops.autotune_conv_bwd(x.shape, wt.shape, s, p)
+            assert ops.conv_plan("dgrad", x.shape, wt.shape, s, p) == (dt, ds, True), shape
+            assert ops.conv_plan("wgrad", x.shape, wt.shape, s, p) == (wt_, ws, True), shape
+            gx, gw = ops.conv2d_bwd(dev(x, cuda), dev(gy, cuda), dev(wt, cuda), s, p)
+            assert orc.rel_l2(host(gx), orc.conv_dgrad(gy, wt, x.shape, s, p)) <= TOL, shape
+            assert orc.rel_l2(host(gw), orc.conv_wgrad(x, gy, ks, s, p)) <= TOL, shape
+        finally:
+            ops.clear_conv_plans()
+
+
 def test_conv_bn_loader_and_relu_epilogue(cuda, ops):
     """Kind-3 loader (eval BN + ReLU of the input, padding stays zero) and the bias + ReLU epilogue."""
     rng = np.random.default_rng(7)
