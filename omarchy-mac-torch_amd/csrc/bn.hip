@@ -342,9 +342,10 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __r
 }
 
 // ---- one launch per call for small channels ---------------------------------------------------------------------
-// A channel of at most kFusedMax elements is reduced, finalized and mapped by one workgroup: the statistics pass and
-// the apply pass (which re-reads the channel from cache) in one kernel, instead of three launches. The finalize and
-// apply arithmetic is that of the split kernels above, so both paths agree to the float64 summation order.
+// A channel of at most kFusedMax elements is reduced, finalized and mapped by one workgroup, in one kernel instead of
+// three launches. Each thread loads its share of the channel once, every load in flight together, and keeps it in
+// registers for the apply pass (at most kFusedMax / 256 floats per operand). The finalize and apply arithmetic is that
+// of the split kernels above, so both paths agree to the float64 summation order.
 constexpr int64_t kFusedMax = 8192;
 
 template <int VEC>
@@ -362,28 +363,27 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
   __shared__ float coef[2];
   const int ch = blockIdx.x;
   const float shift = x[(int64_t)ch * hw];
-  double s1 = 0.0, s2 = 0.0;
-  for (int v = (int)threadIdx.x; v < sp.nv; v += 4 * 256) {
-    V r[4];
+  constexpr int NR = (int)(kFusedMax / (256 * VEC));  // vectors per thread
+  V r[NR];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int vv = v + u * 256;
-      if (vv < sp.nv) {
-        r[u] = *reinterpret_cast<const V*>(x + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
-      } else {
+  for (int u = 0; u < NR; ++u) {
+    const int vv = (int)threadIdx.x + u * 256;
+    if (vv < sp.nv) {
+      r[u] = *reinterpret_cast<const V*>(x + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
+    } else {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);
-      }
+      for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);
     }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        const double d = (double)(vget(r[u], i) - shift);
-        s1 += d;
-        s2 += d * d;
-      }
   }
+  double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+  for (int u = 0; u < NR; ++u)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const double d = (double)(vget(r[u], i) - shift);
+      s1 += d;
+      s2 += d * d;
+    }
   block_sum2(s1, s2);
   if (threadIdx.x == 0) {
     const double m = (double)sp.nv * VEC;
@@ -404,16 +404,19 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
   }
   __syncthreads();
   const float sc = coef[0], sh = coef[1];
-  for (int v = (int)threadIdx.x; v < sp.nv; v += 256) {
-    const int64_t off = voffset(v, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
-    V t = *reinterpret_cast<const V*>(x + off);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      float f = fmaf(vget(t, i), sc, sh);
-      if (relu) f = fmaxf(f, 0.f);
-      vset(t, i, f);
+  for (int u = 0; u < NR; ++u) {
+    const int vv = (int)threadIdx.x + u * 256;
+    if (vv < sp.nv) {
+      V t = r[u];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float f = fmaf(vget(t, i), sc, sh);
+        if (relu) f = fmaxf(f, 0.f);
+        vset(t, i, f);
+      }
+      *reinterpret_cast<V*>(y + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)) = t;
     }
-    *reinterpret_cast<V*>(y + off) = t;
   }
 }
 
@@ -429,37 +432,36 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   __shared__ float kc[5];
   const int ch = blockIdx.x;
   const float mu = mean[ch], inv = invstd[ch];
-  double s1 = 0.0, s2 = 0.0;
-  for (int v = (int)threadIdx.x; v < sp.nv; v += 4 * 256) {
-    V rg[4], rx[4], rr[4];
+  constexpr int NR = (int)(kFusedMax / (256 * VEC));  // vectors per thread
+  V rg[NR], rx[NR], rr[NR];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int vv = v + u * 256;
-      if (vv < sp.nv) {
-        const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
-        rg[u] = *reinterpret_cast<const V*>(g + off);
-        rx[u] = *reinterpret_cast<const V*>(x + off);
-        if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          vset(rg[u], i, 0.f);
-          vset(rx[u], i, mu);
-          vset(rr[u], i, 1.f);
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < NR; ++u) {
+    const int vv = (int)threadIdx.x + u * 256;
+    if (vv < sp.nv) {
+      const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+      rg[u] = *reinterpret_cast<const V*>(g + off);
+      rx[u] = *reinterpret_cast<const V*>(x + off);
+      if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
+    } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
-        float gz = vget(rg[u], i);
-        if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
-        const float xhat = (vget(rx[u], i) - mu) * inv;
-        s1 += (double)gz;
-        s2 += (double)gz * (double)xhat;
+        vset(rg[u], i, 0.f);
+        vset(rx[u], i, mu);
+        vset(rr[u], i, 1.f);
       }
+    }
   }
+  double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+  for (int u = 0; u < NR; ++u)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float gz = vget(rg[u], i);
+      if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+      const float xhat = (vget(rx[u], i) - mu) * inv;
+      s1 += (double)gz;
+      s2 += (double)gz * (double)xhat;
+    }
   block_sum2(s1, s2);
   if (threadIdx.x == 0) {
     if (dbeta) dbeta[ch] = (float)s1;
@@ -478,15 +480,16 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   float k[5];
 #pragma unroll
   for (int i = 0; i < 5; ++i) k[i] = kc[i];
-  for (int v = (int)threadIdx.x; v < sp.nv; v += 256) {
-    const int64_t off = voffset(v, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
-    const V vg = *reinterpret_cast<const V*>(g + off), vx = *reinterpret_cast<const V*>(x + off);
-    V vr = vg;
-    if (ry) vr = *reinterpret_cast<const V*>(ry + off);
-    V o;
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) vset(o, i, bwd_elem(vget(vg, i), vget(vx, i), vget(vr, i), ry != nullptr, k));
-    *reinterpret_cast<V*>(gx + off) = o;
+  for (int u = 0; u < NR; ++u) {
+    const int vv = (int)threadIdx.x + u * 256;
+    if (vv < sp.nv) {
+      V o;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        vset(o, i, bwd_elem(vget(rg[u], i), vget(rx[u], i), ry ? vget(rr[u], i) : 1.f, ry != nullptr, k));
+      *reinterpret_cast<V*>(gx + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)) = o;
+    }
   }
 }
 
