@@ -202,6 +202,13 @@ int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const flo
                      const float* running_mean, const float* running_var, double momentum, double eps, int relu,
                      float* y, float* save_mean, float* save_invstd, float* new_rm, float* new_rv, void* workspace,
                      size_t workspace_bytes, void* stream);
+/* The same with a residual added before the ReLU: y = act(bn(x) + residual) (residual [n][c][hw] like x, or NULL).
+ * No counterpart in the reference, whose residual add and ReLU are separate ops; the torch.compile backend fuses
+ * BatchNorm -> add -> ReLU (the end of a ResNet basic block) into it. */
+int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
+                         const float* running_mean, const float* running_var, double momentum, double eps, int relu,
+                         const float* residual, float* y, float* save_mean, float* save_invstd, float* new_rm,
+                         float* new_rv, void* workspace, size_t workspace_bytes, void* stream);
 /* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
  * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
 int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,

@@ -129,10 +129,9 @@ __global__ void __launch_bounds__(256) bn_stats_part_kernel(const float* __restr
 }
 
 __global__ void bn_stats_fin_kernel(const float* __restrict__ x, const double* __restrict__ part, int c, int hw,
-                                    int slices, double m, double momentum, double eps, const float* __restrict__ rm,
-                                    const float* __restrict__ rv, float* __restrict__ save_mean,
-                                    float* __restrict__ save_invstd, float* __restrict__ new_rm,
-                                    float* __restrict__ new_rv) {
+                                    int slices, double m, double momentum, double eps, const float* rm,
+                                    const float* rv, float* __restrict__ save_mean, float* __restrict__ save_invstd,
+                                    float* new_rm, float* new_rv) {  // new_rm / new_rv may alias rm / rv
   const int ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= c) return;
   double s1 = 0.0, s2 = 0.0;
@@ -153,14 +152,14 @@ __global__ void bn_stats_fin_kernel(const float* __restrict__ x, const double* _
   }
 }
 
-// y = (x - mean[c]) * invstd[c] * gamma[c] + beta[c], optional ReLU. grid (planes, hw chunks); float4 when hw % 4 == 0.
-// Eval mode passes invstd = null and the running variance in var: invstd = 1 / sqrt(var + eps).
+// y = (x - mean[c]) * invstd[c] * gamma[c] + beta[c] (+ res), optional ReLU. grid (planes, hw chunks); float4 when
+// hw % 4 == 0. Eval mode passes invstd = null and the running variance in var: invstd = 1 / sqrt(var + eps).
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__ x, const float* __restrict__ mean,
                                                        const float* __restrict__ invstd, const float* __restrict__ var,
                                                        double eps, const float* __restrict__ gamma,
-                                                       const float* __restrict__ beta, float* __restrict__ y, int c,
-                                                       int hw, int relu) {
+                                                       const float* __restrict__ beta, const float* __restrict__ res,
+                                                       float* __restrict__ y, int c, int hw, int relu) {
   const int plane = blockIdx.x, ch = plane % c;
   const float inv = invstd ? invstd[ch] : (float)(1.0 / sqrt((double)var[ch] + eps));
   const float sc = inv * gamma[ch];
@@ -176,6 +175,13 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
       v.y = fmaf(v.y, sc, sh);
       v.z = fmaf(v.z, sc, sh);
       v.w = fmaf(v.w, sc, sh);
+      if (res) {
+        const float4 r = reinterpret_cast<const float4*>(res + base)[e];
+        v.x += r.x;
+        v.y += r.y;
+        v.z += r.z;
+        v.w += r.w;
+      }
       if (relu) {
         v.x = fmaxf(v.x, 0.f);
         v.y = fmaxf(v.y, 0.f);
@@ -187,6 +193,7 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
   } else {
     for (int e = blockIdx.y * 256 + threadIdx.x; e < hw; e += gridDim.y * 256) {
       float v = fmaf(x[base + e], sc, sh);
+      if (res) v += res[base + e];
       if (relu) v = fmaxf(v, 0.f);
       y[base + e] = v;
     }
@@ -198,7 +205,8 @@ template <int VEC>
 __global__ void __launch_bounds__(256) bn_apply_flat_kernel(const float* __restrict__ x, const float* __restrict__ mean,
                                                             const float* __restrict__ invstd,
                                                             const float* __restrict__ gamma,
-                                                            const float* __restrict__ beta, float* __restrict__ y,
+                                                            const float* __restrict__ beta,
+                                                            const float* __restrict__ res, float* __restrict__ y,
                                                             int64_t total_v, FastDiv div_hwv, FastDiv div_c, int c,
                                                             int relu) {
   using V = typename VecT<VEC>::T;
@@ -207,9 +215,12 @@ __global__ void __launch_bounds__(256) bn_apply_flat_kernel(const float* __restr
     const float sc = invstd[ch] * gamma[ch];
     const float sh = beta[ch] - mean[ch] * sc;
     V v = reinterpret_cast<const V*>(x)[i];
+    V r;
+    if (res) r = reinterpret_cast<const V*>(res)[i];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       float f = fmaf(vget(v, e), sc, sh);
+      if (res) f += vget(r, e);
       if (relu) f = fmaxf(f, 0.f);
       vset(v, e, f);
     }
@@ -352,12 +363,11 @@ template <int VEC>
 __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
-                                                             const float* __restrict__ rm,
-                                                             const float* __restrict__ rv, double momentum,
-                                                             double eps, int relu, float* __restrict__ y,
-                                                             float* __restrict__ save_mean,
-                                                             float* __restrict__ save_invstd,
-                                                             float* __restrict__ new_rm, float* __restrict__ new_rv,
+                                                             const float* rm, const float* rv, double momentum,
+                                                             double eps, int relu, const float* __restrict__ res,
+                                                             float* __restrict__ y, float* __restrict__ save_mean,
+                                                             float* __restrict__ save_invstd, float* new_rm,
+                                                             float* new_rv,  // may alias rm / rv
                                                              int c, int hw, const Split sp) {
   using V = typename VecT<VEC>::T;
   __shared__ float coef[2];
@@ -408,14 +418,17 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
   for (int u = 0; u < NR; ++u) {
     const int vv = (int)threadIdx.x + u * 256;
     if (vv < sp.nv) {
-      V t = r[u];
+      const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+      V t = r[u], q;
+      if (res) q = *reinterpret_cast<const V*>(res + off);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         float f = fmaf(vget(t, i), sc, sh);
+        if (res) f += vget(q, i);
         if (relu) f = fmaxf(f, 0.f);
         vset(t, i, f);
       }
-      *reinterpret_cast<V*>(y + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)) = t;
+      *reinterpret_cast<V*>(y + off) = t;
     }
   }
 }
@@ -521,26 +534,26 @@ static int launch_stats(const Split& sp, const float* x, double* part, int64_t c
 
 // y = x * (invstd * gamma) + (beta - mean * invstd * gamma) [ReLU] with per-channel mean / invstd arrays.
 static int launch_apply(int64_t n, int64_t c, int64_t hw, const float* x, const float* mean, const float* invstd,
-                        const float* gamma, const float* beta, float* y, int relu, hipStream_t s) {
-  const bool vec = hw % 4 == 0 && al16(x) && al16(y);
+                        const float* gamma, const float* beta, const float* res, float* y, int relu, hipStream_t s) {
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && (!res || al16(res));
   const int64_t vw = vec ? 4 : 1, total_v = n * c * hw / vw;
   if (hw < kFlatPlane && total_v < ((int64_t)1 << 31)) {
     const FastDiv dh = make_fastdiv((uint32_t)(hw / vw)), dc = make_fastdiv((uint32_t)c);
     const dim3 grid(grid1d(total_v, 256, 16384));
     if (vec)
-      hipLaunchKernelGGL(bn_apply_flat_kernel<4>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, y, total_v, dh,
-                         dc, (int)c, relu);
+      hipLaunchKernelGGL(bn_apply_flat_kernel<4>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, res, y, total_v,
+                         dh, dc, (int)c, relu);
     else
-      hipLaunchKernelGGL(bn_apply_flat_kernel<1>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, y, total_v, dh,
-                         dc, (int)c, relu);
+      hipLaunchKernelGGL(bn_apply_flat_kernel<1>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, res, y, total_v,
+                         dh, dc, (int)c, relu);
     return launch_check("bn_apply_flat_kernel");
   }
   if (vec)
     hipLaunchKernelGGL(bn_apply_kernel<true>, apply_grid(n * c, hw, 4), dim3(256), 0, s, x, mean, invstd, nullptr,
-                       0.0, gamma, beta, y, (int)c, (int)hw, relu);
+                       0.0, gamma, beta, res, y, (int)c, (int)hw, relu);
   else
     hipLaunchKernelGGL(bn_apply_kernel<false>, apply_grid(n * c, hw, 1), dim3(256), 0, s, x, mean, invstd, nullptr,
-                       0.0, gamma, beta, y, (int)c, (int)hw, relu);
+                       0.0, gamma, beta, res, y, (int)c, (int)hw, relu);
   return launch_check("bn_apply_kernel");
 }
 
@@ -554,10 +567,11 @@ OMT_EXPORT size_t omt_bn_train_workspace(int64_t n, int64_t c, int64_t hw) {
   return (size_t)(c * kMaxSlices * 2) * sizeof(double);
 }
 
-OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
-                                const float* beta, const float* running_mean, const float* running_var,
-                                double momentum, double eps, int relu, float* y, float* save_mean, float* save_invstd,
-                                float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes, void* stream) {
+OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
+                                    const float* beta, const float* running_mean, const float* running_var,
+                                    double momentum, double eps, int relu, const float* residual, float* y,
+                                    float* save_mean, float* save_invstd, float* new_rm, float* new_rv,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
   if (!x || !gamma || !beta || !y || !save_mean || !save_invstd) return fail(OMT_INVALID, "omt_bn_train_fwd: null pointer");
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd: size not covered");
   if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
@@ -565,14 +579,16 @@ OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x
   hipStream_t s = stream_of(stream);
   const Split sp = bn_split(n, c, hw, al16(x));
   if (n * hw <= kFusedMax) {
-    const bool vec = sp.vec == 4 && al16(y);
+    const bool vec = sp.vec == 4 && al16(y) && (!residual || al16(residual));
     const Split f = vec ? sp : bn_split(n, c, hw, false);
     if (vec)
       hipLaunchKernelGGL(bn_train_fused_kernel<4>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
-                         running_var, momentum, eps, relu, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f);
+                         running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
+                         (int)hw, f);
     else
       hipLaunchKernelGGL(bn_train_fused_kernel<1>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
-                         running_var, momentum, eps, relu, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f);
+                         running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
+                         (int)hw, f);
     return launch_check("bn_train_fused_kernel");
   }
   double* part = (double*)workspace;
@@ -582,7 +598,15 @@ OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x
                      (int)hw, sp.slices, m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm,
                      new_rv);
   if (int st = launch_check("bn_stats_fin_kernel")) return st;
-  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, y, relu, s);
+  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s);
+}
+
+OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
+                                const float* beta, const float* running_mean, const float* running_var,
+                                double momentum, double eps, int relu, float* y, float* save_mean, float* save_invstd,
+                                float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes, void* stream) {
+  return omt_bn_train_fwd_res(n, c, hw, x, gamma, beta, running_mean, running_var, momentum, eps, relu, nullptr, y,
+                              save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
 }
 
 OMT_EXPORT int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
@@ -595,10 +619,10 @@ OMT_EXPORT int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x,
   const bool vec = (hw % 4) == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0;
   if (vec)
     hipLaunchKernelGGL(bn_apply_kernel<true>, apply_grid(n * c, hw, 4), dim3(256), 0, s, x, running_mean, nullptr,
-                       running_var, eps, gamma, beta, y, (int)c, (int)hw, relu);
+                       running_var, eps, gamma, beta, nullptr, y, (int)c, (int)hw, relu);
   else
     hipLaunchKernelGGL(bn_apply_kernel<false>, apply_grid(n * c, hw, 1), dim3(256), 0, s, x, running_mean, nullptr,
-                       running_var, eps, gamma, beta, y, (int)c, (int)hw, relu);
+                       running_var, eps, gamma, beta, nullptr, y, (int)c, (int)hw, relu);
   return launch_check("bn_apply_kernel");
 }
 

@@ -97,6 +97,8 @@ SIGNATURES = {
     "omt_dw_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_bn_train_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_train_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_train_fwd_res": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, VP, SZ,
+                                   VP]),
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
     "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_bwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),

@@ -1,8 +1,13 @@
 """torch.compile backend: `torch.compile(model, backend="omarchy_mac_torch")` (reference: omarchy_mac_torch/compile.py).
 
-Dynamo captures the model and AOTAutograd produces aten graphs for the forward and backward passes. Three rewrites
-then route the hot path to fused device ops, and the graph runs op by op on the device:
+Dynamo captures the model and AOTAutograd produces aten graphs for the forward and backward passes, with the
+buffer updates (BatchNorm running statistics and batch counters) kept inside the graph as copies into the inputs.
+The rewrites then route the hot path to fused device ops, and the graph runs op by op on the device:
 
+  0. training BatchNorm whose new running statistics are only copied back into its running-stat inputs
+     -> omt.bn_train_ (statistics updated in place, no copies), taking along a following ReLU or residual add + ReLU
+     (y = relu(bn(x) + r), the end of a ResNet basic block); the batch counters' increments (one add and one copy
+     each) become a single _foreach_add_;
   1. training BatchNorm (`_native_batch_norm_legit_functional`) whose normalized output only feeds a ReLU
      -> omt.bn_relu_train (statistics, normalize and ReLU in the library's BN kernels);
   2. its backward, `native_batch_norm_backward(threshold_backward(g, y, 0), ...)` -> omt.bn_relu_backward (the ReLU
@@ -65,6 +70,121 @@ def _move_getitems(graph, old, new):
         ngi = _call_before(graph, gi, operator.getitem, (new, i), meta_from=gi)
         gi.replace_all_uses_with(ngi)
         graph.erase_node(gi)
+
+
+# ---- rewrite 0: in-place training BatchNorm (+ residual) (+ ReLU), batch counters ----
+
+def _sole_copy_into(value, dst):
+    """The copy_ of `value` into graph input `dst` when that is value's only use, else None."""
+    users = list(value.users) if value is not None else []
+    if (len(users) == 1 and users[0].op == "call_function" and users[0].target is aten.copy_.default
+            and users[0].args[0] is dst and users[0].args[1] is value):
+        return users[0]
+    return None
+
+
+def _copy_back(value, dst):
+    """The copy_ of `value` into graph input `dst` when value's other uses are graph outputs only (new running
+    statistics saved for the BatchNorm backward, which does not read them in training), else None."""
+    if value is None:
+        return None
+    copies = [u for u in value.users if u.op == "call_function" and u.target is aten.copy_.default
+              and u.args[0] is dst and u.args[1] is value]
+    if len(copies) == 1 and all(u is copies[0] or u.op == "output" for u in value.users):
+        return copies[0]
+    return None
+
+
+def _same_shape(a, b):
+    va, vb = _meta(a), _meta(b)
+    return isinstance(va, torch.Tensor) and isinstance(vb, torch.Tensor) and tuple(va.shape) == tuple(vb.shape)
+
+
+def fuse_bn_train_in_place(graph):
+    count = {"bn": 0, "relu": 0, "add_relu": 0}
+    order = {n: i for i, n in enumerate(graph.nodes)}
+    for n in list(graph.nodes):
+        if n.op != "call_function" or n.target is not aten._native_batch_norm_legit_functional.default:
+            continue
+        x, w, b, rm, rv, training, momentum, eps = n.args[:8]
+        if not training or any(a is None for a in (w, b, rm, rv)) or not _on_device_f32(x, 4):
+            continue
+        if not (isinstance(rm, Node) and rm.op == "placeholder" and isinstance(rv, Node) and rv.op == "placeholder"):
+            continue
+        outs = _getitem_users(n)
+        c3, c4 = _copy_back(outs.get(3), rm), _copy_back(outs.get(4), rv)
+        out0 = outs.get(0)
+        if c3 is None or c4 is None or out0 is None:
+            continue
+        # nothing else may read the running statistics (graph outputs see them after the update in either form)
+        if any(u not in (n, c3) and u.op != "output" for u in rm.users) or \
+                any(u not in (n, c4) and u.op != "output" for u in rv.users):
+            continue
+        act, res, last, add, anchor = 0, None, out0, None, n
+        u = _sole_user(out0)
+        if u is not None and u.op == "call_function" and u.target is aten.relu.default:
+            act, last = 1, u
+        elif (u is not None and u.op == "call_function" and u.target is aten.add.Tensor and len(u.args) == 2
+              and not u.kwargs):
+            other = u.args[1] if u.args[0] is out0 else u.args[0]
+            relu = _sole_user(u)
+            # the fused node sits at the add (the residual may be computed after the BatchNorm): every use of the
+            # saved statistics must come later
+            stats_later = all(order[v] > order[u] for i in (1, 2) if outs.get(i) is not None for v in outs[i].users)
+            if (other is not out0 and isinstance(other, Node) and _on_device_f32(other, 4) and _same_shape(other, x)
+                    and relu is not None and relu.op == "call_function" and relu.target is aten.relu.default
+                    and stats_later):
+                act, res, last, add, anchor = 1, other, relu, u, u
+        fused = _call_before(graph, anchor, omt.bn_train_.default, (x, w, b, rm, rv, momentum, eps, act, res))
+        y = _call_before(graph, anchor, operator.getitem, (fused, 0), meta_from=last)
+        for i in (1, 2):
+            gi = outs.get(i)
+            if gi is not None:
+                ngi = _call_before(graph, anchor, operator.getitem, (fused, i), meta_from=gi)
+                gi.replace_all_uses_with(ngi)
+                graph.erase_node(gi)
+        last.replace_all_uses_with(y)
+        graph.erase_node(last)
+        graph.erase_node(c3)
+        graph.erase_node(c4)
+        outs[3].replace_all_uses_with(rm)  # outputs: the updated buffers
+        outs[4].replace_all_uses_with(rv)
+        if add is not None:
+            graph.erase_node(add)
+        if out0 is not last:
+            graph.erase_node(out0)
+        for dead in (outs[3], outs[4], n):
+            graph.erase_node(dead)
+        count["bn"] += 1
+        if res is not None:
+            count["add_relu"] += 1
+        elif act:
+            count["relu"] += 1
+    return count
+
+
+def merge_batch_counters(graph):
+    """`copy_(t, add(t, 1))` on 0-dim int64 graph inputs (BatchNorm's num_batches_tracked) -> one _foreach_add_."""
+    found = []
+    for n in list(graph.nodes):
+        if n.op != "call_function" or n.target is not aten.add.Tensor or len(n.args) != 2 or n.kwargs:
+            continue
+        t, one = n.args
+        v = _meta(t)
+        if not (isinstance(t, Node) and t.op == "placeholder" and isinstance(v, torch.Tensor) and v.dim() == 0
+                and v.dtype == torch.int64 and one == 1):
+            continue
+        cp = _sole_copy_into(n, t)
+        if cp is not None:
+            found.append((t, n, cp))
+    if len(found) < 2:
+        return 0
+    with graph.inserting_before(found[-1][2]):
+        graph.call_function(aten._foreach_add_.Scalar, ([t for t, _, _ in found], 1))
+    for t, add, cp in found:
+        graph.erase_node(cp)
+        graph.erase_node(add)
+    return len(found)
 
 
 # ---- rewrite 1: training BatchNorm + ReLU ----
@@ -161,7 +281,8 @@ def fuse_conv_epilogues(graph):
 
 def _compile(gm, example_inputs):
     g = gm.graph
-    stats = {"bn_relu": fuse_bn_relu_train(g), "bn_relu_backward": fuse_bn_relu_backward(g),
+    stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
+             "bn_relu": fuse_bn_relu_train(g), "bn_relu_backward": fuse_bn_relu_backward(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()
@@ -172,5 +293,7 @@ def _compile(gm, example_inputs):
     return make_boxed_func(gm.forward)
 
 
-backend = aot_autograd(fw_compiler=_compile, bw_compiler=_compile, inference_compiler=_compile)
+# buffer mutations stay in the graph (as copy_ into the inputs) so that rewrite 0 can turn them into in-place updates
+backend = aot_autograd(fw_compiler=_compile, bw_compiler=_compile, inference_compiler=_compile,
+                       keep_inference_input_mutations=True)
 register_backend(name=DEVICE)(backend)

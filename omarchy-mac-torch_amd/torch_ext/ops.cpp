@@ -288,6 +288,16 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_ref(cons
   auto r = at::_native_batch_norm_legit_functional(x, w, b, rm, rv, true, mom, eps);
   return {at::relu(std::get<0>(r)), std::get<1>(r), std::get<2>(r), std::get<3>(r), std::get<4>(r)};
 }
+static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_ref(const Tensor& x, const Tensor& w, const Tensor& b,
+                                                               const Tensor& rm, const Tensor& rv, double mom,
+                                                               double eps, int64_t act,
+                                                               const std::optional<Tensor>& res) {
+  Tensor rm_ = rm, rv_ = rv;  // _native_batch_norm_legit updates them in place
+  auto r = at::_native_batch_norm_legit(x, w, b, rm_, rv_, true, mom, eps);
+  Tensor y = std::get<0>(r);
+  if (defined(res)) y = y + *res;
+  return {act == 1 ? at::relu(y) : y, std::get<1>(r), std::get<2>(r)};
+}
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_ref(const Tensor& g, const Tensor& x, const Tensor& y,
                                                                const Tensor& w, const Tensor& mean,
                                                                const Tensor& invstd, std::array<bool, 3> mask) {
@@ -327,6 +337,28 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_dev(cons
                          fpm(nrm), fpm(nrv), wsptr(ws), wsbytes(ws), cur_stream()),
         "omt::bn_relu_train");
   return {y, sm, si, nrm, nrv};
+}
+// Training BatchNorm with the running statistics updated in place, then the optional residual and ReLU.
+static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_, const Tensor& w, const Tensor& b,
+                                                               const Tensor& rm, const Tensor& rv, double mom,
+                                                               double eps, int64_t act,
+                                                               const std::optional<Tensor>& res_) {
+  NEED(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
+       "4-D float32 with contiguous parameters");
+  Tensor x = contig(x_);
+  Tensor res;
+  if (defined(res_)) {
+    NEED(f32(*res_) && res_->sizes() == x.sizes(), "residual of the input's shape");
+    res = contig(*res_);
+  }
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor y = empty_dev(x.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  Tensor ws = workspace(omt_bn_train_workspace(n, c, hw));
+  check(omt_bn_train_fwd_res(n, c, hw, fp(x), fp(w), fp(b), fp(rm), fp(rv), mom, eps, act == 1 ? 1 : 0,
+                             res.defined() ? fp(res) : nullptr, fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(ws),
+                             wsbytes(ws), cur_stream()),
+        "omt::bn_train_");
+  return {y, sm, si};
 }
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_, const Tensor& x_, const Tensor& y_,
                                                                const Tensor& w, const Tensor& mean,
@@ -379,6 +411,12 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_k(const 
                                                                         const Tensor& rv, double mom, double eps) {
   TRY_DEV(bn_relu_train_dev, bn_relu_train_ref, x, w, b, rm, rv, mom, eps)
 }
+static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_k(const Tensor& x, const Tensor& w, const Tensor& b,
+                                                             const Tensor& rm, const Tensor& rv, double mom,
+                                                             double eps, int64_t act,
+                                                             const std::optional<Tensor>& res) {
+  TRY_DEV(bn_train_inplace_dev, bn_train_inplace_ref, x, w, b, rm, rv, mom, eps, act, res)
+}
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_k(const Tensor& g, const Tensor& x, const Tensor& y,
                                                              const Tensor& w, const Tensor& mean,
                                                              const Tensor& invstd, std::array<bool, 3> mask) {
@@ -400,17 +438,23 @@ TORCH_LIBRARY(omt, m) {
   m.def("bn_relu_backward(Tensor g, Tensor x, Tensor y, Tensor w, Tensor mean, Tensor invstd, bool[3] mask) -> "
         "(Tensor, Tensor, Tensor)");
   m.def("conv_act(Tensor x, Tensor w, Tensor? b, int[] stride, int[] padding, int act) -> Tensor");
+  // training BatchNorm updating the running statistics in place, then + residual and ReLU (act 1): the compile
+  // backend's form of BatchNorm -> [add] -> [ReLU] with the buffer updates kept in the graph
+  m.def("bn_train_(Tensor x, Tensor w, Tensor b, Tensor(a!) rm, Tensor(b!) rv, float momentum, float eps, int act, "
+        "Tensor? residual) -> (Tensor, Tensor, Tensor)");
   m.def("conv_bn_act_eval(Tensor x, Tensor cw, Tensor? cb, Tensor w, Tensor b, Tensor rm, Tensor rv, float eps, "
         "int[] stride, int[] padding, int act) -> Tensor");
 }
 TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("bn_relu_train", &bn_relu_train_ref);
+  m.impl("bn_train_", &bn_train_inplace_ref);
   m.impl("bn_relu_backward", &bn_relu_backward_ref);
   m.impl("conv_act", &conv_act_ref);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
 }
 TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_train", &bn_relu_train_k);
+  m.impl("bn_train_", &bn_train_inplace_k);
   m.impl("bn_relu_backward", &bn_relu_backward_k);
   m.impl("conv_act", &conv_act_k);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);

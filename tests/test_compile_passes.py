@@ -1,0 +1,114 @@
+"""The torch.compile backend's graph rewrites, on the CPU: hand-built aten graphs of the shape AOTAutograd hands the
+backend (training BatchNorm with its running-stat and batch-counter updates kept in the graph as copies into the
+inputs), with fake device tensors as node metadata so that the rewrites apply. Each rewritten graph is then run on
+CPU tensors (omt.bn_train_ has a composite CPU implementation) against the original graph on the same inputs:
+outputs and every mutated buffer must agree. Reference pattern rules: omarchy_mac_torch/compile.py:67-161."""
+
+import copy
+import operator
+
+import pytest
+import torch
+from torch.fx import Graph, GraphModule
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+aten = torch.ops.aten
+
+
+@pytest.fixture(scope="module")
+def oc():
+    from omarchy_mac_torch import compile as oc
+    return oc
+
+
+def _fake(mode, dev, shape, dtype=torch.float32):
+    with mode:
+        return torch.empty(shape, dtype=dtype, device=dev)
+
+
+def _block_tail_graph(oc, tail, save_stats=False):
+    """Forward graph of BatchNorm(x) followed by `tail` ("relu", "add_relu" or "none"), plus two batch counters.
+    save_stats: the new running statistics are also graph outputs (AOTAutograd saves them for the backward)."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    shp, c = (2, 4, 3, 3), 4
+
+    def ph(name, shape, dtype=torch.float32):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape, dtype)
+        return n
+
+    x, w, b, rm, rv, r = ph("x", shp), ph("w", (c,)), ph("b", (c,)), ph("rm", (c,)), ph("rv", (c,)), ph("r", shp)
+    t1, t2 = ph("nbt1", (), torch.int64), ph("nbt2", (), torch.int64)
+    bn = g.call_function(aten._native_batch_norm_legit_functional.default, (x, w, b, rm, rv, True, 0.1, 1e-5))
+    gi = [g.call_function(operator.getitem, (bn, i)) for i in range(5)]
+    gi[0].meta["val"] = _fake(mode, dev, shp)
+    y = gi[0]
+    if tail == "relu":
+        y = g.call_function(aten.relu.default, (gi[0],))
+    elif tail == "add_relu":
+        s = g.call_function(aten.add.Tensor, (gi[0], r))
+        s.meta["val"] = _fake(mode, dev, shp)
+        y = g.call_function(aten.relu.default, (s,))
+    y.meta["val"] = _fake(mode, dev, shp)
+    a1 = g.call_function(aten.add.Tensor, (t1, 1))
+    a2 = g.call_function(aten.add.Tensor, (t2, 1))
+    g.call_function(aten.copy_.default, (rm, gi[3]))
+    g.call_function(aten.copy_.default, (rv, gi[4]))
+    g.call_function(aten.copy_.default, (t1, a1))
+    g.call_function(aten.copy_.default, (t2, a2))
+    g.output((y, gi[1], gi[2]) + ((gi[3], gi[4]) if save_stats else ()))
+    return GraphModule(torch.nn.Module(), g)
+
+
+def _inputs(seed):
+    gen = torch.Generator().manual_seed(seed)
+    shp, c = (2, 4, 3, 3), 4
+    return [torch.randn(shp, generator=gen), torch.rand(c, generator=gen) + 0.5, torch.randn(c, generator=gen),
+            torch.randn(c, generator=gen), torch.rand(c, generator=gen) + 0.5, torch.randn(shp, generator=gen),
+            torch.tensor(3, dtype=torch.int64), torch.tensor(7, dtype=torch.int64)]
+
+
+def _targets(gm):
+    return [n.target for n in gm.graph.nodes if n.op == "call_function"]
+
+
+@pytest.mark.parametrize("save_stats", [False, True])
+@pytest.mark.parametrize("tail", ["relu", "add_relu", "none"])
+def test_bn_train_in_place_and_counters(oc, tail, save_stats):
+    gm = _block_tail_graph(oc, tail, save_stats)
+    ref = copy.deepcopy(gm)
+    stats = oc.fuse_bn_train_in_place(gm.graph)
+    assert stats["bn"] == 1 and stats["add_relu"] == (tail == "add_relu") and stats["relu"] == (tail == "relu")
+    assert oc.merge_batch_counters(gm.graph) == 2
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    assert t.count(torch.ops.omt.bn_train_.default) == 1 and t.count(aten._foreach_add_.Scalar) == 1
+    assert aten.copy_.default not in t and aten._native_batch_norm_legit_functional.default not in t
+    assert aten.relu.default not in t and aten.add.Tensor not in t
+    fused = next(n for n in gm.graph.nodes if n.target is torch.ops.omt.bn_train_.default)
+    assert fused.args[7] == (0 if tail == "none" else 1) and (fused.args[8] is not None) == (tail == "add_relu")
+    # same results and buffer updates as the original graph, on CPU tensors
+    a, b = _inputs(1), _inputs(1)
+    out_ref, out_new = ref(*a), gm(*b)
+    for o_ref, o_new in zip(out_ref, out_new):
+        torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)
+    for i in (3, 4, 6, 7):  # rm, rv, both counters
+        torch.testing.assert_close(b[i], a[i], rtol=1e-6, atol=1e-7)
+    assert int(b[6]) == 4 and int(b[7]) == 8
+
+
+def test_bn_in_place_needs_sole_copies(oc):
+    """A running-stat input read elsewhere in the graph keeps the functional BatchNorm (no in-place update)."""
+    gm = _block_tail_graph(oc, "relu")
+    rm = next(n for n in gm.graph.nodes if n.op == "placeholder" and n.name == "rm")
+    out = next(n for n in gm.graph.nodes if n.op == "output")
+    with gm.graph.inserting_before(out):
+        extra = gm.graph.call_function(aten.mul.Tensor, (rm, 2))
+    out.args = (out.args[0] + (extra,),)
+    assert oc.fuse_bn_train_in_place(gm.graph)["bn"] == 0
+    # the ReLU still fuses through the functional rewrite
+    assert oc.fuse_bn_relu_train(gm.graph) == 1

@@ -361,6 +361,40 @@ def test_fused_stack_matches_unfused_with_grad_accumulation_and_eval_fold(clean)
         assert rel(fused(xe), ref(xe)) <= TOL
 
 
+def test_compile_backend_residual_block(clean):
+    """The compile backend on ResNet basic blocks (in-place BatchNorm, BN + ReLU and BN + residual add + ReLU
+    rewrites, merged batch counters): two SGD steps match the CPU model in loss, gradients, running statistics and
+    num_batches_tracked."""
+    from omarchy_mac_torch import models
+    omt = clean
+    torch.manual_seed(7)
+    model = nn.Sequential(models.BasicBlock(8, 16, 2), models.BasicBlock(16, 16, 1), nn.AdaptiveAvgPool2d(1),
+                          nn.Flatten(), nn.Linear(16, 5))
+    ref = copy.deepcopy(model)
+    dev = copy.deepcopy(model).to(omt.DEVICE)
+    compiled = torch.compile(dev, backend=omt.DEVICE)
+    o_ref = torch.optim.SGD(ref.parameters(), lr=0.1)
+    o_dev = torch.optim.SGD(dev.parameters(), lr=0.1)
+    for step in range(2):
+        x, t = torch.randn(4, 8, 12, 12), torch.randint(0, 5, (4,))
+        l_ref = nn.functional.cross_entropy(ref(x), t)
+        l_dev = nn.functional.cross_entropy(compiled(D(x, omt)), D(t, omt))
+        assert abs(float(l_dev) - float(l_ref)) <= 1e-4 * max(1.0, abs(float(l_ref))), step
+        o_ref.zero_grad()
+        o_dev.zero_grad()
+        l_ref.backward()
+        l_dev.backward()
+        for (pn, pr), (_, pd) in zip(ref.named_parameters(), dev.named_parameters()):
+            assert rel(pd.grad, pr.grad) <= 1e-3, (step, pn)
+        o_ref.step()
+        o_dev.step()
+        for (bn, br), (_, bd) in zip(ref.named_buffers(), dev.named_buffers()):
+            if br.dtype == torch.int64:
+                assert int(bd) == int(br) == step + 1, (step, bn)
+            else:
+                assert rel(bd, br) <= 1e-5, (step, bn)
+
+
 def test_compile_backend(clean):
     omt = clean
     torch.manual_seed(5)
