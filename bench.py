@@ -325,17 +325,19 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
         run.host_ms = host_ms
         return ms, [float(l) for l in losses]
 
-    def run_graphed(model, batches, timed_from):
+    def run_graphed(model, batches, timed_from, compiled=False):
         """The same step captured once as a HIP graph (omarchy_mac_torch.graphs) after `timed_from` eager warm-up
-        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed)."""
+        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed).
+        compiled: the model runs through torch.compile(backend="omarchy_mac_torch") (fused BatchNorm rewrites)."""
         from omarchy_mac_torch import graphs
 
         opt = torch.optim.Adam(model.parameters(), lr=1e-3, capturable=True)
         sx, st = torch.empty_like(batches[0][0]), torch.empty_like(batches[0][1])
+        fwd = torch.compile(model, backend=dev_name) if compiled else model
 
         def step():
             opt.zero_grad(set_to_none=True)
-            loss = F.cross_entropy(model(sx), st)
+            loss = F.cross_entropy(fwd(sx), st)
             loss.backward()
             opt.step()
             return loss.detach()
@@ -373,12 +375,18 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
     out = {"config": "ResNet-18 b32 3x64x64, 1000 classes, BN train, Adam lr 1e-3 (BASELINE config 3)",
            "ms_per_step": round(dev_ms, 3), "host_enqueue_ms_per_step": round(run.host_ms, 3), "steps": steps,
            "warmup": warmup}
-    g_losses = None
+    g_losses = c_losses = None
     if dev_name != "cpu":
         g_ms, g_losses = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3)
         out["graphed"] = {"ms_per_step": round(g_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
                           "how": "omarchy_mac_torch.graphs.Graph: forward + backward + fused capturable Adam captured "
                                  "once, replayed per batch after an in-place copy of the batch"}
+        c_ms, c_losses = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3, compiled=True)
+        out["compiled_graphed"] = {
+            "ms_per_step": round(c_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
+            "how": "the graphed step with the model under torch.compile(backend=\"omarchy_mac_torch\"): BatchNorm "
+                   "running statistics updated in place, BatchNorm + ReLU and BatchNorm + residual add + ReLU fused, "
+                   "batch counters in one launch"}
     if cpu:
         threads = len(os.sched_getaffinity(0))
         torch.set_num_threads(threads)
@@ -389,12 +397,14 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
         # float64 CPU run of the same steps: the rounding-free trajectory both fp32 runs are compared with (Adam on a
         # 1000-class batch of 32 amplifies fp32 summation-order differences from step to step)
         _, f64_losses = run(copy.deepcopy(base).double(), "cpu", data[:k], 0, torch.float64)
-        if g_losses is not None:
-            out["graphed"].update({
-                "speedup_vs_cpu": round(cpu_ms / out["graphed"]["ms_per_step"], 2),
-                "max_rel_loss_diff": max(abs(a - b) / abs(b) for a, b in zip(g_losses[:k], cpu_losses[:k])),
-                "max_rel_loss_diff_5_steps": max(abs(a - b) / abs(b) for a, b in zip(g_losses[:5], cpu_losses[:5])),
-                "losses": [round(v, 6) for v in g_losses[:k]]})
+        for key, ls in (("graphed", g_losses), ("compiled_graphed", c_losses)):
+            if ls is not None:
+                out[key].update({
+                    "speedup_vs_cpu": round(cpu_ms / out[key]["ms_per_step"], 2),
+                    "max_rel_loss_diff": max(abs(a - b) / abs(b) for a, b in zip(ls[:k], cpu_losses[:k])),
+                    "max_rel_loss_diff_5_steps": max(abs(a - b) / abs(b) for a, b in zip(ls[:5], cpu_losses[:5])),
+                    "max_rel_loss_diff_vs_fp64": max(abs(a - b) / abs(b) for a, b in zip(ls[:k], f64_losses)),
+                    "losses": [round(v, 6) for v in ls[:k]]})
         out.update({"cpu_ms_per_step": round(cpu_ms, 2), "cpu_cores": threads, "cpu_steps": cpu_steps,
                     "speedup_vs_cpu": round(cpu_ms / dev_ms, 2), "max_rel_loss_diff": rel, "loss_steps_compared": k,
                     "max_rel_loss_diff_5_steps": rel5,
