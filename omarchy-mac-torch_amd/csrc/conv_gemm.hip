@@ -39,6 +39,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 #include <vector>
 
 #include "omt_internal.h"
@@ -94,8 +95,9 @@ struct GatherArgs {
 template <int BP, int BQ, int BK>
 constexpr int gather_lds_floats() { return 2 * (BP + BQ) * (BK + 4); }
 
-// One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats().
-template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN>
+// One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats(). PF: K-blocks
+// of operand loads in flight ahead of the MFMAs (2 for the tiles of small, load-latency-bound layers).
+template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF = 1>
 __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, const int by, const int bz,
                                             float* __restrict__ lds) {
   constexpr int NT = 256;
@@ -146,8 +148,8 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   int sc = 0, sky = 0, skx = 0;
   const int wrow0 = t / BK, wk = t % BK;  // weight tile element: rows wrow0 + 16 i, column wk
 
-  float ra[AR], rb[BR];
-  auto gload = [&](int k0) {
+  float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
+  auto gload = [&](int k0, const int set) {
 #pragma unroll
     for (int i = 0; i < AR; ++i) {
       const int p = p0 + wrow0 + (NT / BK) * i, k = k0 + wk;
@@ -162,7 +164,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
         const uint32_t o = (uint32_t)((woff + p * K + k) * 4);
         off = (p < P && k < K) ? o : kOOB;
       }
-      ra[i] = bload(wr, off, 0);
+      ra[set][i] = bload(wr, off, 0);
     }
     if (MODE == kTapMajor) {
       // k = tap * C + c with C % BK == 0: this thread's BR rows share one tap and K has no tail
@@ -172,7 +174,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
       const uint32_t voff = ok ? lbase + (uint32_t)((ky * W + kx) * 4) : kOOB;
 #pragma unroll
-      for (int j = 0; j < BR; ++j) rb[j] = bload(xr, voff, (uint32_t)((c0 + j) * HW * 4));
+      for (int j = 0; j < BR; ++j) rb[set][j] = bload(xr, voff, (uint32_t)((c0 + j) * HW * 4));
       return;
     }
     {
@@ -202,15 +204,16 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
           }
         }
       }
-      rb[j] = v;
+      rb[set][j] = v;
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const int set) {
 #pragma unroll
-    for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[i];
+    for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[set][i];
 #pragma unroll
     for (int j = 0; j < BR; j += 4)
-      *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) = make_float4(rb[j], rb[j + 1], rb[j + 2], rb[j + 3]);
+      *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) =
+          make_float4(rb[set][j], rb[set][j + 1], rb[set][j + 2], rb[set][j + 3]);
   };
 
   omt_f32x4 acc[TI][TJ];
@@ -221,16 +224,9 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
 
   const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;  // an empty slice still writes its (zero) tile
-  if (nk > 0) {
-    gload(kbeg);
-    sstore(0);
-  }
-  __syncthreads();
   // lane group grp supplies k = grp * (BK / 4) + s at MFMA step s: BK / 16 b128 reads per operand row
   const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
-  for (int it = 0; it < nk; ++it) {
-    const int cur = it & 1;
-    if (it + 1 < nk) gload(kbeg + (it + 1) * BK);
+  auto mfma_block = [&](int cur) {
 #pragma unroll
     for (int q = 0; q < BK / 16; ++q) {
       float4 av[TI], bv[TJ];
@@ -247,8 +243,38 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
           for (int j = 0; j < TJ; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
     }
-    if (it + 1 < nk) sstore(cur ^ 1);
+  };
+  if constexpr (PF == 1) {
+    if (nk > 0) {
+      gload(kbeg, 0);
+      sstore(0, 0);
+    }
     __syncthreads();
+    for (int it = 0; it < nk; ++it) {
+      const int cur = it & 1;
+      if (it + 1 < nk) gload(kbeg + (it + 1) * BK, 0);
+      mfma_block(cur);
+      if (it + 1 < nk) sstore(cur ^ 1, 0);
+      __syncthreads();
+    }
+  } else {
+    // K-block b uses register set and LDS buffer b & 1; the loads of b + 2 are issued before the MFMAs of b, so two
+    // blocks' loads are in flight while the MFMAs run
+    if (nk > 0) gload(kbeg, 0);
+    if (nk > 1) gload(kbeg + BK, 1);
+    if (nk > 0) sstore(0, 0);
+    __syncthreads();
+    auto step = [&](int it, auto setc) {
+      constexpr int S = decltype(setc)::value;
+      if (it + 2 < nk) gload(kbeg + (it + 2) * BK, S);
+      mfma_block(S);
+      if (it + 1 < nk) sstore(S ^ 1, S ^ 1);
+      __syncthreads();
+    };
+    for (int it = 0; it < nk; it += 2) {
+      step(it, std::integral_constant<int, 0>{});
+      if (it + 1 < nk) step(it + 1, std::integral_constant<int, 1>{});
+    }
   }
 
   // epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid); split K: raw partials
@@ -279,10 +305,10 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   }
 }
 
-template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN>
+template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF>
 __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[gather_lds_floats<BP, BQ, BK>()];
-  gather_tile<BP, BQ, WP, WQ, BK, MODE, BN>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+  gather_tile<BP, BQ, WP, WQ, BK, MODE, BN, PF>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
 }
 
 // ---- grad weight ------------------------------------------------------------------------------------------------
@@ -302,8 +328,9 @@ struct WgradArgs {
 template <int BP, int BQ>
 constexpr int wgrad_lds_floats() { return (BP + BQ) * (64 + 4); }
 
-// One workgroup's tile (bx, by) of K slice bz; lds holds wgrad_lds_floats().
-template <int BP, int BQ, int WP, int WQ, int MODE>
+// One workgroup's tile (bx, by) of K slice bz; lds holds wgrad_lds_floats(). PF: K-blocks of operand loads in flight
+// ahead of the MFMAs.
+template <int BP, int BQ, int WP, int WQ, int MODE, int PF = 1>
 __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, const int by, const int bz,
                                            float* __restrict__ lds) {
   constexpr int BK = 64;  // one reduction pixel per lane
@@ -343,8 +370,8 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     kx0 = r0 - ky0 * KS;
   }
 
-  float ra[AR], rb[BR];
-  auto gload = [&](int k0) {
+  float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
+  auto gload = [&](int k0, const int set) {
     const int k = k0 + lane;
     const bool kval = k < kend;
     uint32_t gbase = kOOB, xbase = kOOB;
@@ -358,12 +385,13 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
       xbase = (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
     }
 #pragma unroll
-    for (int i = 0; i < AR; ++i) ra[i] = (pw0 + i < P) ? bload(gr, gbase, (uint32_t)((pw0 + i) * ohw * 4)) : 0.f;
+    for (int i = 0; i < AR; ++i)
+      ra[set][i] = (pw0 + i < P) ? bload(gr, gbase, (uint32_t)((pw0 + i) * ohw * 4)) : 0.f;
     if (MODE == kTapMajor) {
       const bool ok = (unsigned)(iy0 + ky0) < (unsigned)H && (unsigned)(ix0 + kx0) < (unsigned)W;
       const uint32_t voff = ok ? xbase + (uint32_t)((ky0 * W + kx0) * 4) : kOOB;
 #pragma unroll
-      for (int j = 0; j < BR; ++j) rb[j] = (qw0 < Q) ? bload(xr, voff, (uint32_t)((c0 + j) * HW * 4)) : 0.f;
+      for (int j = 0; j < BR; ++j) rb[set][j] = (qw0 < Q) ? bload(xr, voff, (uint32_t)((c0 + j) * HW * 4)) : 0.f;
       return;
     }
     int c = c0, ky = ky0, kx = kx0;
@@ -374,7 +402,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
         const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
         v = bload(xr, ok ? xbase + (uint32_t)((c * HW + ky * W + kx) * 4) : kOOB, 0);
       }
-      rb[j] = v;
+      rb[set][j] = v;
       if (++kx == KS) {
         kx = 0;
         if (++ky == KS) {
@@ -384,11 +412,11 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
       }
     }
   };
-  auto sstore = [&]() {
+  auto sstore = [&](const int set) {
 #pragma unroll
-    for (int i = 0; i < AR; ++i) As[(wave * AR + i) * PK + lane] = ra[i];
+    for (int i = 0; i < AR; ++i) As[(wave * AR + i) * PK + lane] = ra[set][i];
 #pragma unroll
-    for (int j = 0; j < BR; ++j) Bs[(wave * BR + j) * PK + lane] = rb[j];
+    for (int j = 0; j < BR; ++j) Bs[(wave * BR + j) * PK + lane] = rb[set][j];
   };
 
   omt_f32x4 acc[TI][TJ];
@@ -398,11 +426,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
-  if (kbeg < kend) gload(kbeg);
-  for (int k0 = kbeg; k0 < kend; k0 += BK) {
-    sstore();
-    __syncthreads();
-    if (k0 + BK < kend) gload(k0 + BK);
+  auto mfma_block = [&]() {
 #pragma unroll
     for (int m = 0; m < BK / 16; ++m) {
       const int kc = grp * (BK / 4) + 4 * m;  // this lane group's next four K-indices
@@ -419,7 +443,33 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
           for (int j = 0; j < TJ; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
     }
-    __syncthreads();
+  };
+  if constexpr (PF == 1) {
+    if (kbeg < kend) gload(kbeg, 0);
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+      sstore(0);
+      __syncthreads();
+      if (k0 + BK < kend) gload(k0 + BK, 0);
+      mfma_block();
+      __syncthreads();
+    }
+  } else {
+    // K-block b is loaded into register set b & 1 two blocks ahead: while the MFMAs of b run, the loads of b + 1
+    // and b + 2 are in flight
+    if (kbeg < kend) gload(kbeg, 0);
+    if (kbeg + BK < kend) gload(kbeg + BK, 1);
+    auto step = [&](int k0, auto setc) {
+      constexpr int S = decltype(setc)::value;
+      sstore(S);
+      __syncthreads();
+      if (k0 + 2 * BK < kend) gload(k0 + 2 * BK, S);
+      mfma_block();
+      __syncthreads();
+    };
+    for (int k0 = kbeg; k0 < kend; k0 += 2 * BK) {
+      step(k0, std::integral_constant<int, 0>{});
+      if (k0 + BK < kend) step(k0 + BK, std::integral_constant<int, 1>{});
+    }
   }
 
   // store in the [co][ci][ky][kx] order of the weight gradient (tap-major columns are permuted back)
@@ -443,10 +493,10 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
   }
 }
 
-template <int BP, int BQ, int WP, int WQ, int MODE>
+template <int BP, int BQ, int WP, int WQ, int MODE, int PF>
 __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[wgrad_lds_floats<BP, BQ>()];
-  wgrad_tile<BP, BQ, WP, WQ, MODE>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+  wgrad_tile<BP, BQ, WP, WQ, MODE, PF>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
 }
 
 // Grad input and grad weight of one convolution in one launch (omt_conv_bwd), both on 64 x 64 tiles: the first
@@ -465,12 +515,12 @@ __global__ void __launch_bounds__(256, 2) conv_bwd_dual_kernel(const GatherArgs 
   if (b < ng) {
     const int bx = b % d.gx;
     b /= d.gx;
-    gather_tile<64, 64, 32, 32, GBK, GMODE, false>(ga, bx, b % d.gy, b / d.gy, lds);
+    gather_tile<64, 64, 32, 32, GBK, GMODE, false, 2>(ga, bx, b % d.gy, b / d.gy, lds);
   } else {
     b -= ng;
     const int bx = b % d.wx;
     b /= d.wx;
-    wgrad_tile<64, 64, 32, 32, WMODE>(wa, bx, b % d.wy, b / d.wy, lds);
+    wgrad_tile<64, 64, 32, 32, WMODE, 2>(wa, bx, b % d.wy, b / d.wy, lds);
   }
 }
 
@@ -705,15 +755,15 @@ constexpr int64_t kCUs = 256;
 template <int MODE, bool BN>
 static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
   switch (ti) {
-    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    case 7: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN>), grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
   }
 }
 
@@ -863,10 +913,10 @@ static WgradPlan wgrad_plan(const omt_conv_geo* g) {
 template <int MODE>
 static void wgrad_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s) {
   switch (ti) {
-    case 0: hipLaunchKernelGGL((conv_wgrad_kernel<64, 128, 32, 64, MODE>), grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((conv_wgrad_kernel<128, 64, 32, 64, MODE>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((conv_wgrad_kernel<64, 64, 32, 32, MODE>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((conv_wgrad_kernel<32, 128, 16, 64, MODE>), grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((conv_wgrad_kernel<64, 128, 32, 64, MODE, 1>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_wgrad_kernel<128, 64, 32, 64, MODE, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_wgrad_kernel<64, 64, 32, 32, MODE, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_wgrad_kernel<32, 128, 16, 64, MODE, 2>), grid, dim3(256), 0, s, a); break;
   }
 }
 
