@@ -95,6 +95,39 @@ struct GatherArgs {
 template <int BP, int BQ, int BK>
 constexpr int gather_lds_floats() { return 2 * (BP + BQ) * (BK + 4); }
 
+// Gather epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid); split K: raw partials of
+// slice zs. acc[i][j] is the wave's 16x16 MFMA tile (i, j): element r4 of lane l is row 4 (l / 16) + r4, column l % 16.
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                                int q0, int p0, int wp, int wq, int lane, int zs) {
+  const int P = a.P, grp = lane >> 4;
+  const int64_t yhw = (int64_t)a.YH * a.YW;
+  float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
+  const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
+    if (q >= ph.Q) continue;
+    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+    const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+    float* yb = ydst + (int64_t)n * P * yhw + (int64_t)((int)oy * ph.os + ph.oy0) * a.YW + (int)ox * ph.os + ph.ox0;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
+        if (p < P) {
+          float v = acc[i][j][r4];
+          if (!a.part) {
+            if (a.bias) v += a.bias[p];
+            if (a.relu) v = fmaxf(v, 0.f);
+          }
+          yb[(int64_t)p * yhw] = v;
+        }
+      }
+  }
+}
+
 // One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats(). PF: K-blocks
 // of operand loads in flight ahead of the MFMAs (2 for the tiles of small, load-latency-bound layers).
 template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF = 1>
@@ -144,9 +177,19 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
     }
   }
 
-  // wave-uniform tap state (c, ky, kx), decomposed afresh at the start of every K-block
+  // channel-major: wave-uniform tap state (c, ky, kx), decomposed afresh at the start of every K-block
   int sc = 0, sky = 0, skx = 0;
+  // tap-major: the wave-uniform tap (ky, kx) and first channel c0 of the next K-block gload reads. gload runs over
+  // consecutive K-blocks, so the state advances by one block per call (set from kbeg below) instead of being divided
+  // out of k every time.
+  int nc0 = 0, nky = 0, nkx = 0;
   const int wrow0 = t / BK, wk = t % BK;  // weight tile element: rows wrow0 + 16 i, column wk
+  uint32_t aoff[AR];  // byte offsets of this thread's weight elements at k = 0 (out of range for rows past P)
+#pragma unroll
+  for (int i = 0; i < AR; ++i) {
+    const int p = p0 + wrow0 + (NT / BK) * i;
+    aoff[i] = p < P ? (uint32_t)((woff + p * K + wk) * 4) : kOOB;
+  }
 
   float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
   auto gload = [&](int k0, const int set) {
@@ -161,16 +204,23 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
         const int ky = ph.ky0 + a.s * (KH - 1 - ap), kx = ph.kx0 + a.s * (KW - 1 - bp);
         off = (p < P && k < K) ? (uint32_t)((((co * P + p) * a.ks + ky) * a.ks + kx) * 4) : kOOB;
       } else {
-        const uint32_t o = (uint32_t)((woff + p * K + k) * 4);
-        off = (p < P && k < K) ? o : kOOB;
+        // tap-major K-blocks are all whole (C, and so K, is a multiple of BK): no K-tail test
+        off = aoff[i] + (uint32_t)(k0 * 4);
+        if (MODE != kTapMajor && k >= K) off = kOOB;
       }
       ra[set][i] = bload(wr, off, 0);
     }
     if (MODE == kTapMajor) {
       // k = tap * C + c with C % BK == 0: this thread's BR rows share one tap and K has no tail
-      const uint32_t kb = (uint32_t)(k0 + rbase);
-      const int tap = (int)fdiv(kb, a.div_c), c0 = (int)kb - tap * a.C;
-      const int ky = (int)fdiv((uint32_t)tap, ph.div_kw), kx = tap - ky * KW;
+      const int c0 = nc0, ky = nky, kx = nkx;
+      nc0 += BK;
+      if (nc0 >= a.C) {
+        nc0 -= a.C;
+        if (++nkx == KW) {
+          nkx = 0;
+          ++nky;
+        }
+      }
       const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
       const uint32_t voff = ok ? lbase + (uint32_t)((ky * W + kx) * 4) : kOOB;
 #pragma unroll
@@ -224,6 +274,13 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
 
   const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;  // an empty slice still writes its (zero) tile
+  if (MODE == kTapMajor) {
+    const uint32_t kb = (uint32_t)(kbeg + rbase);
+    const int tap = (int)fdiv(kb, a.div_c);
+    nc0 = (int)kb - tap * a.C;
+    nky = (int)fdiv((uint32_t)tap, ph.div_kw);
+    nkx = tap - nky * KW;
+  }
   // lane group grp supplies k = grp * (BK / 4) + s at MFMA step s: BK / 16 b128 reads per operand row
   const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
   auto mfma_block = [&](int cur) {
@@ -277,38 +334,189 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
     }
   }
 
-  // epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid); split K: raw partials
-  const int64_t yhw = (int64_t)a.YH * a.YW;
-  float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
-  const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
-    if (q >= ph.Q) continue;
-    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
-    const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
-    float* yb = ydst + (int64_t)n * P * yhw + (int64_t)((int)oy * ph.os + ph.oy0) * a.YW + (int)ox * ph.os + ph.ox0;
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
-        if (p < P) {
-          float v = acc[i][j][r4];
-          if (!a.part) {
-            if (a.bias) v += a.bias[p];
-            if (a.relu) v = fmaxf(v, 0.f);
-          }
-          yb[(int64_t)p * yhw] = v;
-        }
-      }
-  }
+  gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
 }
 
 template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF>
 __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[gather_lds_floats<BP, BQ, BK>()];
   gather_tile<BP, BQ, WP, WQ, BK, MODE, BN, PF>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+}
+
+// ---- gather with direct global -> LDS loads (tap-major order only) ------------------------------------------------
+// The operand loads go straight into an LDS ring of NS K-block stages (buffer_load ... lds), so NS - 1 blocks of loads
+// are in flight while the MFMAs of one run, at no VGPR cost and with no LDS store instructions. Tile: 64 output
+// channels x BQ pixels, K-block 16, four waves of WP x WQ.
+//  - weights, 16-byte loads: wave w loads k = 4w .. 4w+3 for all 64 rows (lane = row) into As[stage][w][row][4];
+//    a lane of MFMA lane group g then reads its four k-steps k = 4g .. 4g+3 of one row with one ds_read_b128;
+//  - gathered input, dword loads: lane = pixel, one instruction per k-row of 64 pixels, into Bs[stage][k][pixel] (row
+//    pitch BQ + 4: the four lane groups' ds_read_b32 of rows 4g + s then fall on disjoint bank ranges).
+// All K-blocks are whole (C is a multiple of 16 in tap-major order). One barrier per K-block: after it, the stage
+// consumed by the previous block is free for the loads NS - 1 blocks ahead.
+constexpr int kDlBK = 16;
+// s_waitcnt immediate that waits for at most n outstanding vector memory operations (vmcnt in bits 3:0 and 15:14),
+// leaving expcnt (6:4) and lgkmcnt (11:8) at their maxima, i.e. not waited for
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | 0x70 | 0xF00; }
+template <int BQ>
+constexpr int gather_dl_stage_floats() { return 64 * kDlBK + kDlBK * (BQ + 4); }
+
+__device__ __forceinline__ void lds_load_b32(__amdgpu_buffer_rsrc_t r, float* lds_wave_base, uint32_t voff,
+                                             uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 4, (int)voff,
+                                           (int)soff, 0, 0);
+}
+__device__ __forceinline__ void lds_load_b128(__amdgpu_buffer_rsrc_t r, float* lds_wave_base, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 16, (int)voff,
+                                           0, 0, 0);
+}
+
+// stg[s]: the NS stages, each its own LDS array (so that the compiler can tell a stage's reads from the loads in
+// flight into the others, and wait for the right ones only); the K loop is unrolled by NS so every access names one.
+template <int BQ, int WP, int WQ, int NS>
+__device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx, const int by, const int bz,
+                                               float* const (&stg)[NS]) {
+  constexpr int BP = 64, BK = kDlBK, NH = BQ / 64;
+  constexpr int WGQ = BQ / WQ;
+  static_assert((BP / WP) * (BQ / WQ) == 4 && WP % 16 == 0 && WQ % 16 == 0 && BQ % 64 == 0, "tile shape");
+  constexpr int TI = WP / 16, TJ = WQ / 16, BPITCH = BQ + 4;
+  constexpr int ASZ = BP * BK;       // floats of a stage's weight part; the gathered part follows
+  constexpr int LOADS = 1 + 4 * NH;  // load instructions per wave per stage
+  static_assert(NS >= 2 && NS <= 4, "stages");
+
+  const int zs = bz / a.nphase;
+  const Phase ph = a.ph[bz - zs * a.nphase];
+  const int q0 = bx * BQ, p0 = by * BP;
+  if (q0 >= ph.Q) return;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave / WGQ, wq = wave % WGQ;
+  const int KW = ph.KW, K = ph.K, H = a.H, W = a.W, HW = H * W, P = a.P, C = a.C;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+
+  // this lane's pixels (one per 64-pixel half) and weight row
+  int iy0[NH], ix0[NH];
+  uint32_t lbase[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    iy0[h] = ix0[h] = -(1 << 28);
+    lbase[h] = kOOB;
+    const int q = q0 + 64 * h + lane;
+    if (q < ph.Q) {
+      const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+      const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+      const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+      iy0[h] = (int)oy * ph.S - ph.PH;
+      ix0[h] = (int)ox * ph.S - ph.PW;
+      lbase[h] = (uint32_t)(((int)n * C * HW + iy0[h] * W + ix0[h]) * 4);
+    }
+  }
+  const int prow = p0 + lane;
+  const uint32_t abase = prow < P ? (uint32_t)((ph.woff + prow * K + 4 * wave) * 4) : kOOB;
+
+  const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
+  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
+  // tap state (c0, ky, kx) of the next K-block to load: consecutive blocks advance it by 16 channels
+  int nc0, nky, nkx;
+  {
+    const int tap = (int)fdiv((uint32_t)kbeg, a.div_c);
+    nc0 = kbeg - tap * C;
+    nky = (int)fdiv((uint32_t)tap, ph.div_kw);
+    nkx = tap - nky * KW;
+  }
+  int kload = kbeg;
+  auto issue = [&](float* st) {
+    lds_load_b128(wr, st + wave * (BP * 4), abase == kOOB ? kOOB : abase + (uint32_t)(kload * 4));
+    const int c0 = nc0, ky = nky, kx = nkx;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const bool ok = (unsigned)(iy0[h] + ky) < (unsigned)H && (unsigned)(ix0[h] + kx) < (unsigned)W;
+      const uint32_t voff = ok ? lbase[h] + (uint32_t)((ky * W + kx) * 4) : kOOB;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = 4 * wave + j;
+        lds_load_b32(xr, st + ASZ + k * BPITCH + 64 * h, voff, (uint32_t)((c0 + k) * HW * 4));
+      }
+    }
+    kload += BK;
+    nc0 += BK;
+    if (nc0 >= C) {
+      nc0 -= C;
+      if (++nkx == KW) {
+        nkx = 0;
+        ++nky;
+      }
+    }
+  };
+
+  omt_f32x4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int grp = lane >> 4, m16 = lane & 15;
+  auto mfma_stage = [&](const float* st) {
+    float4 av[TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+      av[i] = *reinterpret_cast<const float4*>(st + (grp * BP + wp * WP + 16 * i + m16) * 4);
+    float bv[TJ][4];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) bv[j][s] = st[ASZ + (4 * grp + s) * BPITCH + wq * WQ + 16 * j + m16];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), bv[j][s], acc[i][j], 0, 0, 0);
+  };
+  // block it: wait for this wave's loads of it (the blocks issued after it stay in flight), barrier, issue block
+  // it + NS - 1 into the stage block it - 1 used, MFMAs of block it
+  auto step = [&](int it, auto stc) {
+    constexpr int S = decltype(stc)::value;
+    const int after = min(NS - 2, nk - 1 - it);
+    if (after >= 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LOADS));
+    else if (after == 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LOADS));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    // a bare barrier: the wait above covers this wave's loads of block it, and a __syncthreads() fence would wait for
+    // every load in flight, the later blocks' included. After it, block it is in LDS for every wave and no wave still
+    // reads the stage of block it - 1 (its MFMAs consumed their reads before it got here).
+    __builtin_amdgcn_s_barrier();
+    if (it + NS - 1 < nk) issue(stg[(S + NS - 1) % NS]);
+    mfma_stage(stg[S]);
+  };
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(stg[s]);
+  for (int it = 0; it < nk; it += NS) {
+    step(it, std::integral_constant<int, 0>{});
+    if (it + 1 < nk) step(it + 1, std::integral_constant<int, 1>{});
+    if constexpr (NS > 2)
+      if (it + 2 < nk) step(it + 2, std::integral_constant<int, 2 % NS>{});
+    if constexpr (NS > 3)
+      if (it + 3 < nk) step(it + 3, std::integral_constant<int, 3 % NS>{});
+  }
+  gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
+}
+
+template <int BQ, int WP, int WQ, int NS>
+__global__ void __launch_bounds__(256, 2) conv_gather_dl_kernel(const GatherArgs a) {
+  constexpr int F = gather_dl_stage_floats<BQ>();
+  __shared__ __attribute__((aligned(16))) float s0[F];
+  __shared__ __attribute__((aligned(16))) float s1[F];
+  __shared__ __attribute__((aligned(16))) float s2[NS > 2 ? F : 4];
+  __shared__ __attribute__((aligned(16))) float s3[NS > 3 ? F : 4];
+  float* stages[4] = {s0, s1, s2, s3};
+  float* const(&stg)[NS] = *reinterpret_cast<float* const(*)[NS]>(&stages);
+  gather_tile_dl<BQ, WP, WQ, NS>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, stg);
 }
 
 // ---- grad weight ------------------------------------------------------------------------------------------------
@@ -710,8 +918,9 @@ __global__ void __launch_bounds__(256) fold_bn_kernel(int co, int per_out, const
 
 struct Tile {
   int bp, bq, wp, wq;
-  float eff;   // relative MFMA efficiency of the wave tile (operand reuse)
-  int bk = 16; // K-block (gather kernels)
+  float eff;    // relative MFMA efficiency of the wave tile (operand reuse)
+  int bk = 16;  // K-block (gather kernels)
+  int ns = 0;   // > 0: direct global -> LDS loads into an ns-stage ring (tap-major order; else the staged kernel)
 };
 
 // Picks the tile with the smallest estimated makespan: rounds of `slots` concurrent workgroups times the padded
@@ -739,6 +948,7 @@ static const Tile kGatherTiles[] = {
     {64, 256, 64, 64, 1.00f},     {128, 128, 64, 64, 1.00f},    {64, 128, 32, 64, 0.92f},
     {32, 256, 32, 64, 0.90f},     {16, 256, 16, 64, 0.80f},     {64, 64, 32, 32, 0.80f},
     {64, 64, 32, 32, 0.90f, 64},  {64, 128, 32, 64, 0.95f, 32}, {128, 64, 64, 32, 0.95f, 32},
+    {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3},
 };
 // Plan tile index t < 2 * kNGather: kGatherTiles[t % kNGather], and t >= kNGather forces the channel-major K order
 // (no filter re-pack, one launch fewer; the tap-major order gathers faster on large layers).
@@ -763,8 +973,17 @@ static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t 
     case 5: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 7: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    // the direct-LDS tiles when their kernel does not apply (channel-major order, BN loader): the staged kernel
+    case 9: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
   }
+}
+static void gather_dl_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
+  if (ti == 9)
+    hipLaunchKernelGGL((conv_gather_dl_kernel<64, 32, 32, 4>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_gather_dl_kernel<128, 32, 64, 3>), grid, dim3(256), 0, s, a);
 }
 
 // Tap-major order needs whole K-blocks of channels (so K has no tail); the BN loader keeps the channel-major order.
@@ -861,6 +1080,8 @@ static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t ma
   const dim3 grid = gather_grid(a, pl, n, maxq, part);
   if (a.bn_mean)
     gather_dispatch<kGeneric, true>(pl.tile % kNGather, a, grid, s);
+  else if (gather_uses_tap_major(a, pl) && gtile(pl.tile).ns && (uintptr_t)a.w % 16 == 0)
+    gather_dl_dispatch(pl.tile % kNGather, a, grid, s);
   else if (gather_uses_tap_major(a, pl))
     gather_dispatch<kTapMajor, false>(pl.tile % kNGather, a, grid, s);
   else

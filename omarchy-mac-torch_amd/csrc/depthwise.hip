@@ -148,30 +148,46 @@ __global__ void __launch_bounds__(256) dw_wgrad_reduce_kernel(const float* __res
 
 // ---- stride 1, "same" padding, ks 3 / 5 / 7: LDS-tiled -----------------------------------------------------------
 
+constexpr int kDwOutPerThread = 8;  // output elements per thread of a tiled work unit
+
 struct DwTiling {
   int rows;    // output rows per work unit
   int chunks;  // work units per plane
   int pitch;   // LDS row pitch: W + ks - 1
-  FastDiv div_w, div_chunks;
+  FastDiv div_w, div_chunks, div_pitch;
 };
 
+// Stages `rows` rows of a plane, from row r0 - pad, with `pad` zero columns either side, as tile[rr * pitch + cc]. The
+// tile is walked as a flat range, kStageBatch elements per thread at a time: all of a batch's loads are issued before
+// any LDS store, so a workgroup waits about one memory latency per batch rather than one per row.
+constexpr int kStageBatch = 16;
 template <int NT>
 __device__ __forceinline__ void dw_stage_rows(float* __restrict__ tile, const float* __restrict__ src_plane, int r0,
-                                              int rows, int H, int W, int pitch, int pad, bool bn, float sc,
-                                              float sh) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int rr = wave; rr < rows; rr += NW) {
-    const int iy = r0 - pad + rr;
-    const bool row_ok = (unsigned)iy < (unsigned)H;
-    for (int cc = lane; cc < pitch; cc += 64) {
-      const int ix = cc - pad;
-      float v = 0.f;
-      if (row_ok && (unsigned)ix < (unsigned)W) {
-        v = src_plane[(int64_t)iy * W + ix];
-        if (bn) v = fmaxf(fmaf(v, sc, sh), 0.f);  // padding stays zero: BN + ReLU of in-bounds taps only
+                                              int rows, int H, int W, int pitch, const FastDiv& div_pitch, int pad,
+                                              bool bn, float sc, float sh) {
+  const int total = rows * pitch;
+  for (int e0 = 0; e0 < total; e0 += NT * kStageBatch) {
+    float v[kStageBatch];
+#pragma unroll
+    for (int j = 0; j < kStageBatch; ++j) {
+      const int e = e0 + (int)threadIdx.x + j * NT;
+      v[j] = 0.f;
+      if (e < total) {
+        const int rr = (int)fdiv((uint32_t)e, div_pitch), iy = r0 - pad + rr, ix = e - rr * pitch - pad;
+        if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) v[j] = src_plane[(int64_t)iy * W + ix];
       }
-      tile[rr * pitch + cc] = v;
+    }
+#pragma unroll
+    for (int j = 0; j < kStageBatch; ++j) {
+      const int e = e0 + (int)threadIdx.x + j * NT;
+      if (e < total) {
+        float t = v[j];
+        if (bn) {  // padding stays zero: BN + ReLU of in-bounds taps only
+          const int rr = (int)fdiv((uint32_t)e, div_pitch), iy = r0 - pad + rr, ix = e - rr * pitch - pad;
+          if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) t = fmaxf(fmaf(t, sc, sh), 0.f);
+        }
+        tile[e] = t;
+      }
     }
   }
 }
@@ -196,7 +212,7 @@ __global__ void __launch_bounds__(NT) dw_s1_kernel(const float* __restrict__ x, 
     sc = inv * bg[ch];
     sh = bb[ch] - bm[ch] * sc;
   }
-  dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, t.pitch, PAD, bn, sc, sh);
+  dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, t.pitch, t.div_pitch, PAD, bn, sc, sh);
   float wr[KK];
 #pragma unroll
   for (int i = 0; i < KK; ++i) wr[i] = w[ch * KK + (FLIP ? KK - 1 - i : i)];
@@ -232,19 +248,28 @@ __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict
     const int64_t pbase = ((int64_t)n * C + ch) * H * W;
     for (int chunk = 0; chunk < t.chunks; ++chunk) {
       const int r0 = chunk * t.rows, R = min(t.rows, H - r0);
-      __syncthreads();  // the previous chunk's tile is consumed
-      dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, pitch, PAD, false, 1.f, 0.f);
-      __syncthreads();
       const float* gp = gy + pbase + (int64_t)r0 * W;
-      const int nout = R * W;
-      for (int o = threadIdx.x; o < nout; o += NT) {
-        const int r = (int)fdiv((uint32_t)o, t.div_w), c = o - r * W;
-        const float gv = gp[o];
-        const float* tp = tile + r * pitch + c;
+      const int nout = R * W;  // at most kDwOutPerThread * NT (dw_tiling)
+      float gv[kDwOutPerThread];  // this thread's gradients, loaded while the tile is staged
 #pragma unroll
-        for (int ky = 0; ky < KS; ++ky)
+      for (int u = 0; u < kDwOutPerThread; ++u) {
+        const int o = (int)threadIdx.x + u * NT;
+        gv[u] = o < nout ? gp[o] : 0.f;
+      }
+      __syncthreads();  // the previous chunk's tile is consumed
+      dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, pitch, t.div_pitch, PAD, false, 1.f, 0.f);
+      __syncthreads();
 #pragma unroll
-          for (int kx = 0; kx < KS; ++kx) acc[ky * KS + kx] = fmaf(gv, tp[ky * pitch + kx], acc[ky * KS + kx]);
+      for (int u = 0; u < kDwOutPerThread; ++u) {
+        const int o = (int)threadIdx.x + u * NT;
+        if (o < nout) {
+          const int r = (int)fdiv((uint32_t)o, t.div_w), c = o - r * W;
+          const float* tp = tile + r * pitch + c;
+#pragma unroll
+          for (int ky = 0; ky < KS; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < KS; ++kx) acc[ky * KS + kx] = fmaf(gv[u], tp[ky * pitch + kx], acc[ky * KS + kx]);
+        }
       }
     }
   }
@@ -267,16 +292,17 @@ __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict
 
 constexpr int kDwMaxLds = 64 * 1024;
 
-// ~8 outputs per thread; one wave for planes of up to 128 outputs.
+// ~8 outputs per thread (at most kDwOutPerThread); one wave for planes of up to 128 outputs.
 static DwTiling dw_tiling(int H, int W, int ks, int nt) {
   DwTiling t;
-  int rows = (nt * 8) / W;
+  int rows = (nt * kDwOutPerThread) / W;
   rows = rows < 1 ? 1 : rows > H ? H : rows;
   t.rows = rows;
   t.chunks = (int)cdiv(H, rows);
   t.pitch = W + ks - 1;
   t.div_w = make_fastdiv((uint32_t)W);
   t.div_chunks = make_fastdiv((uint32_t)t.chunks);
+  t.div_pitch = make_fastdiv((uint32_t)t.pitch);
   return t;
 }
 static int dw_threads(const omt_conv_geo* g) { return g->ih * g->iw <= 128 ? 64 : 256; }
@@ -285,6 +311,8 @@ static size_t dw_lds(const DwTiling& t, int ks) { return (size_t)(t.rows + ks - 
 static bool dw_s1(const omt_conv_geo* g) {
   if (g->stride != 1 || g->pad != g->ks / 2 || !(g->ks == 3 || g->ks == 5 || g->ks == 7)) return false;
   if (g->n * g->ci >= ((int64_t)1 << 31)) return false;
+  // a work unit (at least one row) must fit kDwOutPerThread outputs per thread
+  if (g->iw > (int64_t)dw_threads(g) * kDwOutPerThread) return false;
   return dw_lds(dw_tiling((int)g->ih, (int)g->iw, (int)g->ks, dw_threads(g)), (int)g->ks) <= (size_t)kDwMaxLds;
 }
 // (C, slices) grid of the tiled grad weight: about 1024 workgroups, at most one slice per image

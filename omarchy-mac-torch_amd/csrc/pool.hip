@@ -64,6 +64,35 @@ __global__ void __launch_bounds__(256) maxpool_fwd_kernel(const float* __restric
   }
 }
 
+// Undilated windows: the outputs whose window covers input (y, x) form the range oy in
+// [ceil((y + p - k + 1) / s), floor((y + p) / s)] (clipped to the output) per axis, visited in ascending (oy, ox)
+// order like the general kernel below, so the sums are bit-identical; no per-tap divisibility tests.
+template <bool I32>
+__global__ void __launch_bounds__(256) maxpool_bwd_d1_kernel(const float* __restrict__ g,
+                                                             const int64_t* __restrict__ idx, float* __restrict__ gx,
+                                                             int64_t total, PoolGeo q) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const Pos in = decompose<I32>(i, q.iw, q.ih * q.iw, q.d_iw, q.d_ihw);
+    const int ty = in.y + q.ph, tx = in.x + q.pw;
+    const int ay = ty - q.kh + 1, ax = tx - q.kw + 1;
+    const int oy0 = ay <= 0 ? 0 : (int)fdiv((uint32_t)(ay + q.sh - 1), q.d_sh);
+    const int ox0 = ax <= 0 ? 0 : (int)fdiv((uint32_t)(ax + q.sw - 1), q.d_sw);
+    const int oy1 = min((int)fdiv((uint32_t)ty, q.d_sh), q.oh - 1);
+    const int ox1 = min((int)fdiv((uint32_t)tx, q.d_sw), q.ow - 1);
+    const float* gp = g + in.plane * q.oh * q.ow;
+    const int64_t* ip = idx + in.plane * q.oh * q.ow;
+    const int64_t me = (int64_t)in.y * q.iw + in.x;
+    float acc = 0.f;
+    for (int oy = oy0; oy <= oy1; ++oy)
+      for (int ox = ox0; ox <= ox1; ++ox) {
+        const int o = oy * q.ow + ox;
+        const float gv = gp[o];  // loaded with the index, not after the compare
+        if (ip[o] == me) acc += gv;
+      }
+    gx[i] = acc;
+  }
+}
+
 // Output rows oy whose window row ky lands on input row r: oy * s - p + ky * d = r. Visits oy ascending.
 template <bool I32>
 __global__ void __launch_bounds__(256) maxpool_bwd_kernel(const float* __restrict__ g, const int64_t* __restrict__ idx,
@@ -289,6 +318,11 @@ OMT_EXPORT int omt_maxpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
     return fail(OMT_UNSUPPORTED, "omt_maxpool_bwd: geometry not covered");
   const int64_t total = planes * ih * iw;
   if (total == 0) return OMT_OK;
+  if (dh == 1 && dw == 1) {
+    OMT_POOL_LAUNCH(maxpool_bwd_d1_kernel, total, stream_of(stream), g, idx, gx, total,
+                    pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+    return launch_check("maxpool_bwd_d1_kernel");
+  }
   OMT_POOL_LAUNCH(maxpool_bwd_kernel, total, stream_of(stream), g, idx, gx, total,
                   pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
   return launch_check("maxpool_bwd_kernel");
