@@ -346,41 +346,64 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
 // ---- gather with direct global -> LDS loads (tap-major order only) ------------------------------------------------
 // The operand loads go straight into an LDS ring of NS K-block stages (buffer_load ... lds), so NS - 1 blocks of loads
 // are in flight while the MFMAs of one run, at no VGPR cost and with no LDS store instructions. Tile: 64 output
-// channels x BQ pixels, K-block 16, four waves of WP x WQ.
-//  - weights, 16-byte loads: wave w loads k = 4w .. 4w+3 for all 64 rows (lane = row) into As[stage][w][row][4];
-//    a lane of MFMA lane group g then reads its four k-steps k = 4g .. 4g+3 of one row with one ds_read_b128;
-//  - gathered input, dword loads: lane = pixel, one instruction per k-row of 64 pixels, into Bs[stage][k][pixel] (row
-//    pitch BQ + 4: the four lane groups' ds_read_b32 of rows 4g + s then fall on disjoint bank ranges).
-// All K-blocks are whole (C is a multiple of 16 in tap-major order). One barrier per K-block: after it, the stage
+// channels x BQ pixels, K-block BK (16 or 32), four waves of WP x WQ. MFMA lane group g supplies k = g BK/4 + s at
+// step s (s < BK/4).
+//  - weights, 16-byte loads (lane = row) of four consecutive k into As[stage][k / 4][row][4]; a lane reads its BK/4
+//    k-steps of one row with BK/16 ds_read_b128;
+//  - gathered input, dword loads: lane = pixel, one instruction per k-row of 64 pixels, into Bs[stage][k][pixel]. Row
+//    pitch BQ + 4 (BK 16) or BQ + 2 (BK 32) makes the stride between the lane groups' rows g BK/4 + s 16 banks mod 64,
+//    so the four groups' ds_read_b32 fall on disjoint bank ranges.
+// All K-blocks are whole (C is a multiple of BK in tap-major order). One barrier per K-block: after it, the stage
 // consumed by the previous block is free for the loads NS - 1 blocks ahead.
-constexpr int kDlBK = 16;
 // s_waitcnt immediate that waits for at most n outstanding vector memory operations (vmcnt in bits 3:0 and 15:14),
 // leaving expcnt (6:4) and lgkmcnt (11:8) at their maxima, i.e. not waited for
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | 0x70 | 0xF00; }
-template <int BQ>
-constexpr int gather_dl_stage_floats() { return 64 * kDlBK + kDlBK * (BQ + 4); }
+template <int BK>
+constexpr int dl_pad() { return BK == 16 ? 4 : 2; }
+template <int BQ, int BK>
+constexpr int gather_dl_stage_floats() { return 64 * BK + BK * (BQ + dl_pad<BK>()); }
 
-__device__ __forceinline__ void lds_load_b32(__amdgpu_buffer_rsrc_t r, float* lds_wave_base, uint32_t voff,
-                                             uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 4, (int)voff,
-                                           (int)soff, 0, 0);
+// The direct-LDS loads are issued as inline assembly. Through the builtin, the compiler tracks them as LDS writes and,
+// unable to tell the stages apart in every step, waits for all loads in flight before some stages' LDS reads, which
+// collapses the ring. Hidden from it, ordering rests on the kernel's explicit waits (vmcnt counts these loads in issue
+// order, so a wait for at most N outstanding covers every load issued before the last N) and barriers, with
+// compiler-level memory barriers ("memory" clobbers) keeping the LDS reads after both.
+typedef uint32_t omt_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ omt_u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return omt_u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xFFFFu, bytes, 0x00020000u};  // stride 0, raw dwords
 }
-__device__ __forceinline__ void lds_load_b128(__amdgpu_buffer_rsrc_t r, float* lds_wave_base, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 16, (int)voff,
-                                           0, 0, 0);
+__device__ __forceinline__ uint32_t lds_addr(const float* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)p);
+}
+// lane i's dword at voff + soff lands at LDS byte address m0 + 4 i
+__device__ __forceinline__ void lds_load_b32(omt_u32x4 r, uint32_t m0, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+// lane i's 16 bytes at voff land at LDS byte address m0 + 16 i
+__device__ __forceinline__ void lds_load_b128(omt_u32x4 r, uint32_t m0, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r)
+               : "memory", "m0");
 }
 
 // stg[s]: the NS stages, each its own LDS array (so that the compiler can tell a stage's reads from the loads in
 // flight into the others, and wait for the right ones only); the K loop is unrolled by NS so every access names one.
-template <int BQ, int WP, int WQ, int NS>
+template <int BQ, int WP, int WQ, int BK, int NS>
 __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx, const int by, const int bz,
                                                float* const (&stg)[NS]) {
-  constexpr int BP = 64, BK = kDlBK, NH = BQ / 64;
+  constexpr int BP = 64, NH = BQ / 64;
   constexpr int WGQ = BQ / WQ;
   static_assert((BP / WP) * (BQ / WQ) == 4 && WP % 16 == 0 && WQ % 16 == 0 && BQ % 64 == 0, "tile shape");
-  constexpr int TI = WP / 16, TJ = WQ / 16, BPITCH = BQ + 4;
-  constexpr int ASZ = BP * BK;       // floats of a stage's weight part; the gathered part follows
-  constexpr int LOADS = 1 + 4 * NH;  // load instructions per wave per stage
+  static_assert(BK == 16 || BK == 32, "K-block");
+  constexpr int TI = WP / 16, TJ = WQ / 16, BPITCH = BQ + dl_pad<BK>();
+  constexpr int KQ = BK / 16;                  // weight loads (16-byte rows of 4 k) per wave; k-rows per wave: 4 KQ
+  constexpr int ASZ = BP * BK;                 // floats of a stage's weight part; the gathered part follows
+  constexpr int LOADS = KQ + BK / 4 * NH;      // load instructions per wave per stage
   static_assert(NS >= 2 && NS <= 4, "stages");
 
   const int zs = bz / a.nphase;
@@ -391,8 +414,8 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wp = wave / WGQ, wq = wave % WGQ;
   const int KW = ph.KW, K = ph.K, H = a.H, W = a.W, HW = H * W, P = a.P, C = a.C;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+  const omt_u32x4 xr = rsrc_words(a.x, a.x_bytes);
+  const omt_u32x4 wr = rsrc_words(a.w, a.w_bytes);
 
   // this lane's pixels (one per 64-pixel half) and weight row
   int iy0[NH], ix0[NH];
@@ -412,7 +435,7 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
     }
   }
   const int prow = p0 + lane;
-  const uint32_t abase = prow < P ? (uint32_t)((ph.woff + prow * K + 4 * wave) * 4) : kOOB;
+  const uint32_t abase = prow < P ? (uint32_t)((ph.woff + prow * K) * 4) : kOOB;
 
   const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
   const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
@@ -426,16 +449,20 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
   }
   int kload = kbeg;
   auto issue = [&](float* st) {
-    lds_load_b128(wr, st + wave * (BP * 4), abase == kOOB ? kOOB : abase + (uint32_t)(kload * 4));
+#pragma unroll
+    for (int u = 0; u < KQ; ++u) {  // weight k-quads wave + 4 u
+      const int kq = wave + 4 * u;
+      lds_load_b128(wr, lds_addr(st + kq * (BP * 4)), abase == kOOB ? kOOB : abase + (uint32_t)((kload + 4 * kq) * 4));
+    }
     const int c0 = nc0, ky = nky, kx = nkx;
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       const bool ok = (unsigned)(iy0[h] + ky) < (unsigned)H && (unsigned)(ix0[h] + kx) < (unsigned)W;
       const uint32_t voff = ok ? lbase[h] + (uint32_t)((ky * W + kx) * 4) : kOOB;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = 4 * wave + j;
-        lds_load_b32(xr, st + ASZ + k * BPITCH + 64 * h, voff, (uint32_t)((c0 + k) * HW * 4));
+      for (int j = 0; j < BK / 4; ++j) {  // input k-rows wave BK/4 + j
+        const int k = wave * (BK / 4) + j;
+        lds_load_b32(xr, lds_addr(st + ASZ + k * BPITCH + 64 * h), voff, (uint32_t)((c0 + k) * HW * 4));
       }
     }
     kload += BK;
@@ -457,28 +484,33 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
 
   const int grp = lane >> 4, m16 = lane & 15;
   auto mfma_stage = [&](const float* st) {
-    float4 av[TI];
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
-      av[i] = *reinterpret_cast<const float4*>(st + (grp * BP + wp * WP + 16 * i + m16) * 4);
-    float bv[TJ][4];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) bv[j][s] = st[ASZ + (4 * grp + s) * BPITCH + wq * WQ + 16 * j + m16];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int q = 0; q < KQ; ++q) {  // k-steps 4 q .. 4 q + 3 of this lane group
+      float4 av[TI];
 #pragma unroll
       for (int i = 0; i < TI; ++i)
+        av[i] = *reinterpret_cast<const float4*>(st + ((grp * KQ + q) * BP + wp * WP + 16 * i + m16) * 4);
+      float bv[TJ][4];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), bv[j][s], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          bv[j][s] = st[ASZ + (grp * (BK / 4) + 4 * q + s) * BPITCH + wq * WQ + 16 * j + m16];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), bv[j][s], acc[i][j], 0, 0, 0);
+    }
   };
   // block it: wait for this wave's loads of it (the blocks issued after it stay in flight), barrier, issue block
   // it + NS - 1 into the stage block it - 1 used, MFMAs of block it
   auto step = [&](int it, auto stc) {
     constexpr int S = decltype(stc)::value;
     const int after = min(NS - 2, nk - 1 - it);
+    asm volatile("" ::: "memory");
     if (after >= 2)
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LOADS));
     else if (after == 1)
@@ -489,6 +521,7 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
     // every load in flight, the later blocks' included. After it, block it is in LDS for every wave and no wave still
     // reads the stage of block it - 1 (its MFMAs consumed their reads before it got here).
     __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     if (it + NS - 1 < nk) issue(stg[(S + NS - 1) % NS]);
     mfma_stage(stg[S]);
   };
@@ -496,27 +529,39 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(stg[s]);
-  for (int it = 0; it < nk; it += NS) {
-    step(it, std::integral_constant<int, 0>{});
-    if (it + 1 < nk) step(it + 1, std::integral_constant<int, 1>{});
-    if constexpr (NS > 2)
-      if (it + 2 < nk) step(it + 2, std::integral_constant<int, 2 % NS>{});
-    if constexpr (NS > 3)
-      if (it + 3 < nk) step(it + 3, std::integral_constant<int, 3 % NS>{});
+  // unrolled by 2 NS: the compiler's own wait bookkeeping for the loads in flight is merged at the loop header, and
+  // the step after the merge waits for them all; the longer body makes that once per 2 NS blocks
+  auto steps = [&](int it0, auto offc) {
+    constexpr int O = decltype(offc)::value;
+    if (it0 + O < nk) step(it0 + O, std::integral_constant<int, O % NS>{});
+  };
+  for (int it = 0; it < nk; it += 2 * NS) {
+    steps(it, std::integral_constant<int, 0>{});
+    steps(it, std::integral_constant<int, 1>{});
+    steps(it, std::integral_constant<int, 2>{});
+    steps(it, std::integral_constant<int, 3>{});
+    if constexpr (NS > 2) {
+      steps(it, std::integral_constant<int, 4>{});
+      steps(it, std::integral_constant<int, 5>{});
+    }
+    if constexpr (NS > 3) {
+      steps(it, std::integral_constant<int, 6>{});
+      steps(it, std::integral_constant<int, 7>{});
+    }
   }
   gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
 }
 
-template <int BQ, int WP, int WQ, int NS>
+template <int BQ, int WP, int WQ, int BK, int NS>
 __global__ void __launch_bounds__(256, 2) conv_gather_dl_kernel(const GatherArgs a) {
-  constexpr int F = gather_dl_stage_floats<BQ>();
+  constexpr int F = gather_dl_stage_floats<BQ, BK>();
   __shared__ __attribute__((aligned(16))) float s0[F];
   __shared__ __attribute__((aligned(16))) float s1[F];
   __shared__ __attribute__((aligned(16))) float s2[NS > 2 ? F : 4];
   __shared__ __attribute__((aligned(16))) float s3[NS > 3 ? F : 4];
   float* stages[4] = {s0, s1, s2, s3};
   float* const(&stg)[NS] = *reinterpret_cast<float* const(*)[NS]>(&stages);
-  gather_tile_dl<BQ, WP, WQ, NS>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, stg);
+  gather_tile_dl<BQ, WP, WQ, BK, NS>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, stg);
 }
 
 // ---- grad weight ------------------------------------------------------------------------------------------------
@@ -948,7 +993,8 @@ static const Tile kGatherTiles[] = {
     {64, 256, 64, 64, 1.00f},     {128, 128, 64, 64, 1.00f},    {64, 128, 32, 64, 0.92f},
     {32, 256, 32, 64, 0.90f},     {16, 256, 16, 64, 0.80f},     {64, 64, 32, 32, 0.80f},
     {64, 64, 32, 32, 0.90f, 64},  {64, 128, 32, 64, 0.95f, 32}, {128, 64, 64, 32, 0.95f, 32},
-    {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3},
+    {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3}, {64, 64, 32, 32, 0.90f, 32, 3},
+    {64, 128, 32, 64, 0.97f, 32, 2},
 };
 // Plan tile index t < 2 * kNGather: kGatherTiles[t % kNGather], and t >= kNGather forces the channel-major K order
 // (no filter re-pack, one launch fewer; the tap-major order gathers faster on large layers).
@@ -976,14 +1022,18 @@ static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t 
     case 8: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     // the direct-LDS tiles when their kernel does not apply (channel-major order, BN loader): the staged kernel
     case 9: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 11: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
   }
 }
 static void gather_dl_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
-  if (ti == 9)
-    hipLaunchKernelGGL((conv_gather_dl_kernel<64, 32, 32, 4>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((conv_gather_dl_kernel<128, 32, 64, 3>), grid, dim3(256), 0, s, a);
+  switch (ti) {
+    case 9: hipLaunchKernelGGL((conv_gather_dl_kernel<64, 32, 32, 16, 4>), grid, dim3(256), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((conv_gather_dl_kernel<128, 32, 64, 16, 3>), grid, dim3(256), 0, s, a); break;
+    case 11: hipLaunchKernelGGL((conv_gather_dl_kernel<64, 32, 32, 32, 3>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_dl_kernel<128, 32, 64, 32, 2>), grid, dim3(256), 0, s, a); break;
+  }
 }
 
 // Tap-major order needs whole K-blocks of channels (so K has no tail); the BN loader keeps the channel-major order.
