@@ -11,9 +11,9 @@ resident in HBM:
   c1:           BASELINE config 1, AlexNet conv1 (16x3x224x224, 64x11x11, stride 4, pad 2). 6.747 GFLOP per step.
 FLOPs per direction = 2*N*K*OH*OW*C*R*S (never the padded or stride-phase-expanded work).
 
-The roofline object reports the dominant kernel, conv_gather_kernel, from its forward launches (one kernel per
-call): algorithmic FLOPs per launch over the launch's HIP-event duration, measured on the launch stream inside the
-timed steps. cpu_baseline times the CPU oracle (oracle/, a scalar-per-thread float64 restatement of the reference
+The roofline object reports the dominant kernel, the implicit-GEMM gather (conv_gather_kernel, or its direct-to-LDS
+form conv_gather_dl_kernel for tap-major plans), from its forward launches: algorithmic FLOPs per launch over the
+launch's HIP-event duration, measured on the launch stream inside the timed steps. cpu_baseline times the CPU oracle (oracle/, a scalar-per-thread float64 restatement of the reference
 algorithm) on a bounded sample of the same workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the
 reference's CPU path) on a sample. Both are baselines, not targets.
 """
@@ -130,9 +130,60 @@ def torch_cpu_baseline(layers, batch, threads):
                       f"at batch {batch}, {cpu_info()}"}
 
 
+def _is_gather(kernel_name):
+    """The implicit-GEMM gather kernels (staged conv_gather_kernel and direct-to-LDS conv_gather_dl_kernel)."""
+    return "conv_gather_kernel" in kernel_name or "conv_gather_dl_kernel" in kernel_name
+
+
+def trace_summary(trace_csv, steps, n_layers):
+    """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of this bench (sweep only) and prints the
+    timed region's per-kernel table as markdown. Warm-up and timed steps launch the same dispatch sequence, so the
+    step length D is the smallest period of the trace's tail; the timed region is the last `steps` x D dispatches.
+    Each layer launches its forward, then its grad input through a gather kernel (the grad weight through the wgrad
+    kernel), so the even-numbered gather dispatches of the region are the forward launches: their mean duration is
+    the figure the bench's roofline.avg_launch_ms measures with HIP events."""
+    import csv
+
+    rows = sorted((int(r["Dispatch_Id"]), r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                  for r in csv.DictReader(open(trace_csv)))
+    names = [r[1] for r in rows]
+    period = None
+    for d in range(1, len(rows) // steps + 1):
+        tail = names[len(names) - steps * d:]
+        if all(tail[i] == tail[i % d] for i in range(len(tail))) and \
+                sum(_is_gather(n) for n in tail[:d]) == 2 * n_layers:
+            period = d
+            break
+    if period is None:
+        raise SystemExit(f"no {steps}-fold periodic tail with {2 * n_layers} gather dispatches per step")
+    region = rows[len(rows) - steps * period:]
+    busy = sum(e - s for (_, _, s, e) in region) / 1e6
+    span = (region[-1][3] - region[0][2]) / 1e6
+    per = {}
+    for (_, n, s, e) in region:
+        per.setdefault(n, []).append((e - s) / 1e6)
+
+    def short(n):
+        n = n.split("(")[0].strip()
+        return n[5:] if n.startswith("void ") else n
+
+    print(f"timed region: {len(region)} dispatches ({period} per step), {busy:.3f} ms of kernel time, "
+          f"span {span:.3f} ms\n")
+    print("| Kernel (timed region) | Calls | Average ms | % of kernel time |\n|---|---|---|---|")
+    for n, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{short(n)}` | {len(v)} | {sum(v) / len(v):.4f} | {100 * sum(v) / busy:.1f} |")
+    gathers = [r for r in region if _is_gather(r[1])]
+    fwd = [(e - s) / 1e6 for (_, _, s, e) in gathers[0::2]]
+    kinds = {}
+    for (_, n, _, _) in gathers[0::2]:
+        kinds[short(n).split("<")[0]] = kinds.get(short(n).split("<")[0], 0) + 1
+    print(f"\nforward launches: {len(fwd)} ({', '.join(f'{k} x{v}' for k, v in sorted(kinds.items()))}), "
+          f"average {sum(fwd) / len(fwd):.4f} ms")
+
+
 def pmc_summary(fetch_csv, write_csv, layers, workload):
     """Reads the FETCH_SIZE and WRITE_SIZE counter dumps of two `--pmc-probe` runs: the 1 GiB device copy calibrates
-    each counter (bytes it must move / what the counter reports), then the forward conv_gather_kernel dispatches after
+    each counter (bytes it must move / what the counter reports), then the forward gather-kernel dispatches after
     it are the workload's layers in order. Writes profiles/conv_gather_<workload>_traffic.json and prints a markdown
     table."""
     import csv
@@ -149,7 +200,7 @@ def pmc_summary(fetch_csv, write_csv, layers, workload):
         rs = rows(path, counter)
         ci = max((i for i, r in enumerate(rs) if "copy" in r[1].lower()), key=lambda i: rs[i][2])
         factor = (1 << 30) / rs[ci][2]
-        gathers = [r for r in rs[ci + 1:] if "conv_gather_kernel" in r[1]]
+        gathers = [r for r in rs[ci + 1:] if _is_gather(r[1])]
         if len(gathers) != len(layers):
             raise SystemExit(f"{counter}: {len(gathers)} gather dispatches after the copy, {len(layers)} layers")
         res[counter] = (factor, [g[2] * factor for g in gathers])
@@ -434,12 +485,18 @@ def main():
                     help="skip plan tuning (tile / K split per layer and direction) before the warmup")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarize two --pmc-probe counter dumps into profiles/conv_gather_<workload>_traffic.json")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel table of the timed steps of a rocprofv3 --kernel-trace run of the sweep "
+                         "(--no-bw --no-resnet --no-cpu, same --steps)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
                          "launch per layer; prints nothing else")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps, len(C5_LAYERS if args.workload == "c5" else C1_LAYERS))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
@@ -556,7 +613,7 @@ def main():
                                 "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad"),
                    "gflop_per_step": round(step_flops / 1e9, 2), "layout": "NCHW"},
         "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
-        "roofline": {"kernel": "conv_gather_kernel (forward launches)", "bound": "mfma",
+        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel (forward launches)", "bound": "mfma",
                      "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4), "traffic": traffic_per_launch(args.workload),
                      "avg_launch_ms": round(avg_launch_ms, 4),

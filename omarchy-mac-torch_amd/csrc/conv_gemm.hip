@@ -43,12 +43,20 @@
 #include <vector>
 
 #include "omt_internal.h"
+#include "tile_map.h"
 
 namespace omt {
 
 constexpr int kMaxPhases = 16;
 constexpr uint32_t kOOB = 0x80000000u;  // byte offset beyond every buffer (buffers are < 2 GiB)
 constexpr int64_t kMaxBufBytes = 0x7fffffffll;
+
+__device__ __forceinline__ TileId xcd_block_tile(int gm) {
+  return xcd_tile((int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)), (int)gridDim.x,
+                  (int)gridDim.y, (int)gridDim.z, gm);
+}
+// Tile rows per group: 8 output-channel (gather) or grad-weight row (wgrad) tiles.
+constexpr int kTileGroup = 8;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
@@ -340,7 +348,8 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
 template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF>
 __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[gather_lds_floats<BP, BQ, BK>()];
-  gather_tile<BP, BQ, WP, WQ, BK, MODE, BN, PF>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+  const TileId t = xcd_block_tile(kTileGroup);
+  gather_tile<BP, BQ, WP, WQ, BK, MODE, BN, PF>(a, t.x, t.y, t.z, lds);
 }
 
 // ---- gather with direct global -> LDS loads (tap-major order only) ------------------------------------------------
@@ -561,7 +570,8 @@ __global__ void __launch_bounds__(256, 2) conv_gather_dl_kernel(const GatherArgs
   __shared__ __attribute__((aligned(16))) float s3[NS > 3 ? F : 4];
   float* stages[4] = {s0, s1, s2, s3};
   float* const(&stg)[NS] = *reinterpret_cast<float* const(*)[NS]>(&stages);
-  gather_tile_dl<BQ, WP, WQ, BK, NS>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, stg);
+  const TileId t = xcd_block_tile(kTileGroup);
+  gather_tile_dl<BQ, WP, WQ, BK, NS>(a, t.x, t.y, t.z, stg);
 }
 
 // ---- grad weight ------------------------------------------------------------------------------------------------
@@ -749,11 +759,13 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
 template <int BP, int BQ, int WP, int WQ, int MODE, int PF>
 __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[wgrad_lds_floats<BP, BQ>()];
-  wgrad_tile<BP, BQ, WP, WQ, MODE, PF>(a, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z, lds);
+  const TileId t = xcd_block_tile(kTileGroup);
+  wgrad_tile<BP, BQ, WP, WQ, MODE, PF>(a, t.x, t.y, t.z, lds);
 }
 
 // Grad input and grad weight of one convolution in one launch (omt_conv_bwd), both on 64 x 64 tiles: the first
-// gx * gy * gz workgroups run grad-input tiles (x fastest), the rest grad-weight tiles over wx * wy * wz. On late,
+// gx * gy * gz workgroups run grad-input tiles, the rest grad-weight tiles over wx * wy * wz (each part through the
+// XCD tile mapping). On late,
 // low-resolution layers each GEMM alone puts about one workgroup on a CU, which then waits on its loads; in one launch
 // every CU also holds a workgroup of the other GEMM to run meanwhile.
 struct DualGrid {
@@ -763,17 +775,14 @@ template <int GBK, int GMODE, int WMODE>
 __global__ void __launch_bounds__(256, 2) conv_bwd_dual_kernel(const GatherArgs ga, const WgradArgs wa, const DualGrid d) {
   constexpr int kG = gather_lds_floats<64, 64, GBK>(), kW = wgrad_lds_floats<64, 64>();
   __shared__ __attribute__((aligned(16))) float lds[kG > kW ? kG : kW];
-  int b = (int)blockIdx.x;
+  const int b = (int)blockIdx.x;
   const int ng = d.gx * d.gy * d.gz;
   if (b < ng) {
-    const int bx = b % d.gx;
-    b /= d.gx;
-    gather_tile<64, 64, 32, 32, GBK, GMODE, false, 2>(ga, bx, b % d.gy, b / d.gy, lds);
+    const TileId t = xcd_tile(b, d.gx, d.gy, d.gz, kTileGroup);
+    gather_tile<64, 64, 32, 32, GBK, GMODE, false, 2>(ga, t.x, t.y, t.z, lds);
   } else {
-    b -= ng;
-    const int bx = b % d.wx;
-    b /= d.wx;
-    wgrad_tile<64, 64, 32, 32, WMODE, 2>(wa, bx, b % d.wy, b / d.wy, lds);
+    const TileId t = xcd_tile(b - ng, d.wx, d.wy, d.wz, kTileGroup);
+    wgrad_tile<64, 64, 32, 32, WMODE, 2>(wa, t.x, t.y, t.z, lds);
   }
 }
 
