@@ -43,13 +43,12 @@
 #include <vector>
 
 #include "omt_internal.h"
+#include "lds_dma.h"
 #include "tile_map.h"
 
 namespace omt {
 
 constexpr int kMaxPhases = 16;
-constexpr uint32_t kOOB = 0x80000000u;  // byte offset beyond every buffer (buffers are < 2 GiB)
-constexpr int64_t kMaxBufBytes = 0x7fffffffll;
 
 __device__ __forceinline__ TileId xcd_block_tile(int gm) {
   return xcd_tile((int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)), (int)gridDim.x,
@@ -58,12 +57,6 @@ __device__ __forceinline__ TileId xcd_block_tile(int gm) {
 // Tile rows per group: 8 output-channel (gather) or grad-weight row (wgrad) tiles.
 constexpr int kTileGroup = 8;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
-}
 
 __device__ __forceinline__ float f4get(const float4& v, int s) { return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w; }
 
@@ -364,41 +357,10 @@ __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a)
 //    so the four groups' ds_read_b32 fall on disjoint bank ranges.
 // All K-blocks are whole (C is a multiple of BK in tap-major order). One barrier per K-block: after it, the stage
 // consumed by the previous block is free for the loads NS - 1 blocks ahead.
-// s_waitcnt immediate that waits for at most n outstanding vector memory operations (vmcnt in bits 3:0 and 15:14),
-// leaving expcnt (6:4) and lgkmcnt (11:8) at their maxima, i.e. not waited for
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | 0x70 | 0xF00; }
 template <int BK>
 constexpr int dl_pad() { return BK == 16 ? 4 : 2; }
 template <int BQ, int BK>
 constexpr int gather_dl_stage_floats() { return 64 * BK + BK * (BQ + dl_pad<BK>()); }
-
-// The direct-LDS loads are issued as inline assembly. Through the builtin, the compiler tracks them as LDS writes and,
-// unable to tell the stages apart in every step, waits for all loads in flight before some stages' LDS reads, which
-// collapses the ring. Hidden from it, ordering rests on the kernel's explicit waits (vmcnt counts these loads in issue
-// order, so a wait for at most N outstanding covers every load issued before the last N) and barriers, with
-// compiler-level memory barriers ("memory" clobbers) keeping the LDS reads after both.
-typedef uint32_t omt_u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ omt_u32x4 rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  return omt_u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xFFFFu, bytes, 0x00020000u};  // stride 0, raw dwords
-}
-__device__ __forceinline__ uint32_t lds_addr(const float* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)p);
-}
-// lane i's dword at voff + soff lands at LDS byte address m0 + 4 i
-__device__ __forceinline__ void lds_load_b32(omt_u32x4 r, uint32_t m0, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               :
-               : "s"(m0), "v"(voff), "s"(r), "s"(soff)
-               : "memory", "m0");
-}
-// lane i's 16 bytes at voff land at LDS byte address m0 + 16 i
-__device__ __forceinline__ void lds_load_b128(omt_u32x4 r, uint32_t m0, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(m0), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
 
 // stg[s]: the NS stages, each its own LDS array (so that the compiler can tell a stage's reads from the loads in
 // flight into the others, and wait for the right ones only); the K loop is unrolled by NS so every access names one.

@@ -12,6 +12,9 @@
 //  - grad input: one thread per input element, keeping the taps that land on the stride grid (dw_gin / dwg_gin);
 //  - grad weight: workgroup (channel, slice) accumulates every tap over its share of n * oh * ow, partials summed in
 //    slice order (dw_gwt / dwg_gwt).
+#include <algorithm>
+
+#include "lds_dma.h"
 #include "omt_internal.h"
 
 namespace omt {
@@ -137,11 +140,20 @@ __global__ void __launch_bounds__(256) dw_wgrad_part_kernel(const float* __restr
     part[((int64_t)sl * g.c + ch) * kk + t] = red[0][t] + red[1][t] + red[2][t] + red[3][t];
 }
 
+// Slice sums in slice order, eight slices' loads in flight at a time (a grid this small waits on memory latency).
 __global__ void __launch_bounds__(256) dw_wgrad_reduce_kernel(const float* __restrict__ part, float* __restrict__ gw,
                                                               int n, int slices) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     float s = 0.f;
-    for (int z = 0; z < slices; ++z) s += part[(int64_t)z * n + i];
+    int z = 0;
+    for (; z + 8 <= slices; z += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(z + u) * n + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; z < slices; ++z) s += part[(int64_t)z * n + i];
     gw[i] = s;
   }
 }
@@ -232,53 +244,127 @@ __global__ void __launch_bounds__(NT) dw_s1_kernel(const float* __restrict__ x, 
   }
 }
 
-// grid (C, slices): slice sl reduces images sl, sl + slices, ... of channel blockIdx.x into part[sl][ch][KK].
+// Grad-weight work of one channel: units u = (image u / chunks, row chunk u % chunks), N * chunks of them. A
+// workgroup takes `group` consecutive units and stages `batch` of them at a time (several whole planes when a plane
+// has few outputs; then chunks == 1): every load of a batch (the output gradients into registers, the input rows
+// into LDS) is issued before its one barrier, so a batch costs one memory round trip.
+struct DwUnits {
+  int units, group, batch, tile;  // tile: LDS floats per staged unit, (rows + ks - 1) * pitch
+  int buf;                        // LDS floats per tile buffer: batch * tile in whole rows of 64
+  FastDiv div_tile, div_out;      // div_out: outputs per unit when batch > 1 (H * W)
+};
+
+// grid (C, groups): workgroup (ch, g) reduces units [g * group, (g + 1) * group) of channel ch into part[g][ch][KK].
+// Output gradients are raw buffer loads into registers; the input rows go straight to LDS (each wave moving one row
+// of 64 consecutive tile floats per load), so no register holds a staged value and an address takes one register.
+// Two tile buffers, each in whole rows of 64 floats (the last row's lanes past a batch write zeros there): the loads
+// of batch b + 1 are issued before the FMAs of batch b. The partial sums of each tap go through wave_sum.
 template <int KS, int NT>
 __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict__ x, const float* __restrict__ gy,
-                                                         float* __restrict__ part, int N, int C, int H, int W,
-                                                         const DwTiling t) {
-  extern __shared__ float tile[];
+                                                         float* __restrict__ part, int C, int H, int W,
+                                                         const DwTiling t, const DwUnits wu) {
+  extern __shared__ float tiles[];
   constexpr int PAD = KS / 2, KK = KS * KS, NW = NT / 64;
   __shared__ float red[NW][KK];
-  const int ch = blockIdx.x, sl = blockIdx.y, slices = gridDim.y, pitch = t.pitch;
+  const int ch = blockIdx.x, pitch = t.pitch, HW = H * W;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const uint32_t cstride = (uint32_t)C * (uint32_t)HW;  // elements from one image's plane of ch to the next's
+  const int ubeg = (int)blockIdx.y * wu.group, uend = min(wu.units, ubeg + wu.group);
+  float* const buf[2] = {tiles, tiles + wu.buf};
+
+  // batch at u0: batch > 1 covers whole planes (chunk 0, rows = H), batch == 1 one chunk of rows
+  struct Batch {
+    int nb, n0, r0, nout;
+  };
+  auto batch_at = [&](int u0) {
+    Batch b;
+    b.nb = min(wu.batch, uend - u0);
+    b.n0 = (int)fdiv((uint32_t)u0, t.div_chunks);
+    b.r0 = (u0 - b.n0 * t.chunks) * t.rows;
+    b.nout = wu.batch > 1 ? b.nb * HW : min(t.rows, H - b.r0) * W;  // at most kDwOutPerThread * NT (dw_units)
+    return b;
+  };
+  // the loads of a batch: its output gradients into g, its input rows into tile (tile float e: tile i = e / wu.tile,
+  // row rr, column cc within it, is input row r0 - PAD + rr, column cc - PAD of unit u0 + i; padding and lanes past
+  // the batch load offset kOOB, which reads 0)
+  auto issue = [&](const Batch& b, float* tile, float (&g)[kDwOutPerThread]) {
+    const int64_t base = ((int64_t)b.n0 * C + ch) * HW;
+    const uint32_t span = ((uint32_t)(b.nb - 1) * cstride + (uint32_t)HW) * 4u;  // < 2^31 (dw_units)
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(gy + base, span);
+#pragma unroll
+    for (int j = 0; j < kDwOutPerThread; ++j) {
+      const int o = (int)threadIdx.x + j * NT;
+      uint32_t off = kOOB;
+      if (o < b.nout) {
+        const int i = wu.batch > 1 ? (int)fdiv((uint32_t)o, wu.div_out) : 0, pix = o - i * (wu.batch > 1 ? HW : 0);
+        off = ((uint32_t)i * cstride + (uint32_t)(b.r0 * W + pix)) * 4u;
+      }
+      g[j] = bload(gr, off, 0);
+    }
+    const omt_u32x4 xr = rsrc_words(x + base, span);
+    const int total = b.nb * wu.tile;
+    for (int e0 = wave * 64; e0 < total; e0 += NT) {
+      const int e = e0 + lane;
+      uint32_t off = kOOB;
+      if (e < total) {
+        const int i = (int)fdiv((uint32_t)e, wu.div_tile), rem = e - i * wu.tile;
+        const int rr = (int)fdiv((uint32_t)rem, t.div_pitch), iy = b.r0 - PAD + rr, ix = rem - rr * pitch - PAD;
+        if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+          off = ((uint32_t)i * cstride + (uint32_t)(iy * W + ix)) * 4u;
+      }
+      lds_load_b32(xr, lds_addr(tile + e0), off, 0);
+    }
+  };
   float acc[KK];
 #pragma unroll
   for (int i = 0; i < KK; ++i) acc[i] = 0.f;
-  for (int n = sl; n < N; n += slices) {
-    const int64_t pbase = ((int64_t)n * C + ch) * H * W;
-    for (int chunk = 0; chunk < t.chunks; ++chunk) {
-      const int r0 = chunk * t.rows, R = min(t.rows, H - r0);
-      const float* gp = gy + pbase + (int64_t)r0 * W;
-      const int nout = R * W;  // at most kDwOutPerThread * NT (dw_tiling)
-      float gv[kDwOutPerThread];  // this thread's gradients, loaded while the tile is staged
+  auto fma_batch = [&](const Batch& b, const float* tile, const float (&g)[kDwOutPerThread]) {
+#pragma unroll 2
+    for (int j = 0; j < kDwOutPerThread; ++j) {
+      const int o = (int)threadIdx.x + j * NT;
+      if (o < b.nout) {
+        const int i = wu.batch > 1 ? (int)fdiv((uint32_t)o, wu.div_out) : 0, pix = o - i * (wu.batch > 1 ? HW : 0);
+        const int r = (int)fdiv((uint32_t)pix, t.div_w), c = pix - r * W;
+        const float* tp = tile + i * wu.tile + r * pitch + c;
+        const float gj = g[j];
 #pragma unroll
-      for (int u = 0; u < kDwOutPerThread; ++u) {
-        const int o = (int)threadIdx.x + u * NT;
-        gv[u] = o < nout ? gp[o] : 0.f;
-      }
-      __syncthreads();  // the previous chunk's tile is consumed
-      dw_stage_rows<NT>(tile, x + pbase, r0, R + KS - 1, H, W, pitch, t.div_pitch, PAD, false, 1.f, 0.f);
-      __syncthreads();
+        for (int ky = 0; ky < KS; ++ky)
 #pragma unroll
-      for (int u = 0; u < kDwOutPerThread; ++u) {
-        const int o = (int)threadIdx.x + u * NT;
-        if (o < nout) {
-          const int r = (int)fdiv((uint32_t)o, t.div_w), c = o - r * W;
-          const float* tp = tile + r * pitch + c;
-#pragma unroll
-          for (int ky = 0; ky < KS; ++ky)
-#pragma unroll
-            for (int kx = 0; kx < KS; ++kx) acc[ky * KS + kx] = fmaf(gv[u], tp[ky * pitch + kx], acc[ky * KS + kx]);
-        }
+          for (int kx = 0; kx < KS; ++kx) acc[ky * KS + kx] = fmaf(gj, tp[ky * pitch + kx], acc[ky * KS + kx]);
       }
     }
+  };
+  // every load issued so far has landed (both kinds count in vmcnt), and then every wave's rows are visible and every
+  // wave is done with the other buffer
+  auto land = [&]() {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    asm volatile("" ::: "memory");
+    __syncthreads();
+  };
+
+  float ga[kDwOutPerThread], gb[kDwOutPerThread];
+  Batch ba = batch_at(ubeg), bb;
+  issue(ba, buf[0], ga);
+  for (int u0 = ubeg; u0 < uend; u0 += 2 * wu.batch) {
+    land();
+    const int u1 = u0 + wu.batch;
+    if (u1 < uend) {
+      bb = batch_at(u1);
+      issue(bb, buf[1], gb);
+    }
+    fma_batch(ba, buf[0], ga);
+    if (u1 >= uend) break;
+    land();
+    const int u2 = u1 + wu.batch;
+    if (u2 < uend) {
+      ba = batch_at(u2);
+      issue(ba, buf[0], ga);
+    }
+    fma_batch(bb, buf[1], gb);
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < KK; ++i) {
-    float v = acc[i];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const float v = wave_sum(acc[i]);
     if (lane == 0) red[wave][i] = v;
   }
   __syncthreads();
@@ -286,7 +372,7 @@ __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict
     float v = 0.f;
 #pragma unroll
     for (int wv = 0; wv < NW; ++wv) v += red[wv][i];
-    part[((int64_t)sl * C + ch) * KK + i] = v;
+    part[((int64_t)blockIdx.y * C + ch) * KK + i] = v;
   }
 }
 
@@ -315,10 +401,42 @@ static bool dw_s1(const omt_conv_geo* g) {
   if (g->iw > (int64_t)dw_threads(g) * kDwOutPerThread) return false;
   return dw_lds(dw_tiling((int)g->ih, (int)g->iw, (int)g->ks, dw_threads(g)), (int)g->ks) <= (size_t)kDwMaxLds;
 }
-// (C, slices) grid of the tiled grad weight: about 1024 workgroups, at most one slice per image
-static int64_t dw_s1_slices(const omt_conv_geo* g) {
-  int64_t s = cdiv(1024, g->ci);
-  return s > g->n ? g->n : s < 1 ? 1 : s;
+// The tiled grad weight reads a plane through one buffer resource (planes below 2 GiB) and holds two tile buffers,
+// each in whole rows of 64 floats, in kDwMaxLds of LDS.
+static bool dw_s1_wgrad(const omt_conv_geo* g) {
+  if (!dw_s1(g) || g->ih * g->iw * 4 > kMaxBufBytes) return false;
+  const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, (int)g->ks, dw_threads(g));
+  return 2 * cdiv((int64_t)(t.rows + g->ks - 1) * t.pitch, 64) * 64 * 4 <= kDwMaxLds;
+}
+// Units of the tiled grad weight: whole planes batched while a batch keeps at most kDwOutPerThread outputs per thread,
+// one load per thread and 64-float row (kStageBatch rows per wave) and two buffers in kDwMaxLds of LDS; groups of
+// batches sized for about 2048 workgroups.
+static DwUnits dw_units(const omt_conv_geo* g) {
+  const int nt = dw_threads(g), ks = (int)g->ks;
+  const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, ks, nt);
+  DwUnits u{};
+  u.units = (int)(g->n * t.chunks);
+  u.tile = (t.rows + ks - 1) * t.pitch;
+  int64_t b = 1;
+  if (t.chunks == 1) {
+    // the batch's planes span ((b - 1) * C + 1) * H * W floats, read through one buffer resource (< 2 GiB)
+    const int64_t span_cap = (kMaxBufBytes / 4 / (g->ih * g->iw) - 1) / g->ci + 1;
+    b = std::min<int64_t>({(int64_t)nt * kDwOutPerThread / (g->ih * g->iw), (int64_t)nt * kStageBatch / u.tile,
+                           ((int64_t)kDwMaxLds / 8 - 64) / u.tile, (int64_t)u.units, span_cap});
+    b = std::max<int64_t>(b, 1);
+  }
+  u.batch = (int)b;
+  u.buf = (int)(cdiv(b * u.tile, 64) * 64);
+  const int64_t batches = cdiv(u.units, b);
+  const int64_t groups = std::max<int64_t>(1, std::min<int64_t>(cdiv(2048, g->ci), batches));
+  u.group = (int)(cdiv(batches, groups) * b);
+  u.div_tile = make_fastdiv((uint32_t)u.tile);
+  u.div_out = make_fastdiv((uint32_t)(g->ih * g->iw));
+  return u;
+}
+static int64_t dw_s1_groups(const omt_conv_geo* g) {
+  const DwUnits u = dw_units(g);
+  return cdiv(u.units, u.group);
 }
 
 template <bool FLIP>
@@ -394,7 +512,7 @@ OMT_EXPORT int omt_dw_dgrad(const omt_conv_geo* g, const float* gy, const float*
 
 OMT_EXPORT size_t omt_dw_wgrad_workspace(const omt_conv_geo* g) {
   if (!g || !dw_ok(g)) return 0;
-  return (size_t)((dw_s1(g) ? dw_s1_slices(g) : dw_slices(g)) * g->ci * g->ks * g->ks) * sizeof(float);
+  return (size_t)((dw_s1_wgrad(g) ? dw_s1_groups(g) : dw_slices(g)) * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
 OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
@@ -404,16 +522,17 @@ OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* 
   if (!workspace || workspace_bytes < omt_dw_wgrad_workspace(g))
     return fail(OMT_INVALID, "omt_dw_wgrad: workspace of %zu bytes needed", omt_dw_wgrad_workspace(g));
   hipStream_t s = stream_of(stream);
-  if (dw_s1(g)) {
+  if (dw_s1_wgrad(g)) {
     const int nt = dw_threads(g), ks = (int)g->ks;
     const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, ks, nt);
-    const int64_t slices = dw_s1_slices(g);
+    const DwUnits wu = dw_units(g);
+    const int64_t slices = cdiv(wu.units, wu.group);
     const dim3 grid((unsigned)g->ci, (unsigned)slices);
-    const size_t lds = dw_lds(t, ks);
-    const int N = (int)g->n, C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
+    const size_t lds = (size_t)2 * wu.buf * sizeof(float);
+    const int C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
     float* part = (float*)workspace;
 #define OMT_DW_WG(KS_, NT_) \
-  hipLaunchKernelGGL((dw_wgrad_s1_kernel<KS_, NT_>), grid, dim3(NT_), lds, s, x, gy, part, N, C, H, W, t)
+  hipLaunchKernelGGL((dw_wgrad_s1_kernel<KS_, NT_>), grid, dim3(NT_), lds, s, x, gy, part, C, H, W, t, wu)
     if (nt == 64) {
       if (ks == 3) OMT_DW_WG(3, 64); else if (ks == 5) OMT_DW_WG(5, 64); else OMT_DW_WG(7, 64);
     } else {

@@ -51,6 +51,39 @@ __host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) 
   return (hi + ((n - hi) >> 1)) >> (f.shift - 1);
 }
 
+// Raw buffer loads: a resource over [base, base + bytes) with the range check on, so a load at a byte offset past
+// `bytes` returns 0 without touching memory. Offsets are 32-bit: every buffer read this way is below 2 GiB, and kOOB
+// is an offset beyond all of them (padding taps, tails).
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int64_t kMaxBufBytes = 0x7fffffffll;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
+// Sum over the 64 lanes of a wave, in every lane: four DPP steps within each row of 16 lanes, each adding a disjoint
+// partner (quad_perm [1,0,3,2] and [2,3,0,1]: every lane holds its quad's sum; row_half_mirror pairs the two quads
+// of each 8-lane half, row_mirror the two halves), then the four row sums read from lanes 0, 16, 32 and 48. All 64
+// lanes must be active. VALU work only: a __shfl_xor butterfly takes six LDS-routed permutes per value.
+__device__ __forceinline__ float dpp_add(float v, int moved) { return v + __builtin_bit_cast(float, moved); }
+__device__ __forceinline__ float wave_sum(float v) {
+  int b = __builtin_bit_cast(int, v);
+  v = dpp_add(v, __builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  b = __builtin_bit_cast(int, v);
+  v = dpp_add(v, __builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  b = __builtin_bit_cast(int, v);
+  v = dpp_add(v, __builtin_amdgcn_update_dpp(0, b, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  b = __builtin_bit_cast(int, v);
+  v = dpp_add(v, __builtin_amdgcn_update_dpp(0, b, 0x140, 0xF, 0xF, false));  // row_mirror
+  b = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
 }  // namespace omt
 
 typedef float omt_f32x4 __attribute__((ext_vector_type(4)));

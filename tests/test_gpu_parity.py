@@ -356,11 +356,13 @@ def test_depthwise(cuda, ops, ks, s, p):
 @pytest.mark.parametrize("ks", [3, 5, 7])
 def test_depthwise_tiled_stride1(cuda, ops, ks):
     """The LDS-tiled stride-1 "same" kernels on plane shapes that exercise one-wave workgroups (<= 128 outputs),
-    several row chunks per plane and wide rows; the eval BN + ReLU loader across chunk boundaries."""
+    several row chunks per plane and wide rows; the eval BN + ReLU loader across chunk boundaries. Grad weight stages
+    several small planes per batch: image counts that leave a short last batch (13 images of 9x9 in batches of 6) and
+    a short last group (37 of 20x20 in batches of 5, 64 of 14x14 in batches of up to 10)."""
     rng = np.random.default_rng(ks)
     p = ks // 2
     for (n, c, h, w) in ((2, 3, 1, 1), (3, 4, 2, 3), (2, 5, 7, 7), (2, 3, 11, 9), (2, 4, 56, 56), (1, 3, 13, 300),
-                         (1, 2, 70, 41)):
+                         (1, 2, 70, 41), (13, 3, 9, 9), (37, 2, 20, 20), (64, 2, 14, 14)):
         case = (ks, n, c, h, w)
         x, wt, b = rnd(rng, n, c, h, w), rnd(rng, c, 1, ks, ks), rnd(rng, c)
         y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), 1, p)
