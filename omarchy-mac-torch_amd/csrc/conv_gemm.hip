@@ -243,8 +243,9 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
         const bool ok = kval && (unsigned)(iy0 + sky) < (unsigned)H && (unsigned)(ix0 + skx) < (unsigned)W;
         v = bload(xr, ok ? lbase + (uint32_t)((sc * HW + sky * W + skx) * 4) : kOOB, 0);
         if (BN) {
-          const float inv = rsqrtf(a.bn_var[sc] + a.bn_eps);
-          const float z = fmaxf((v - a.bn_mean[sc]) * inv * a.bn_gamma[sc] + a.bn_beta[sc], 0.f);
+          const int cc = min(sc, a.C - 1);  // K-tail and look-ahead taps run past the last channel (v is dropped)
+          const float inv = rsqrtf(a.bn_var[cc] + a.bn_eps);
+          const float z = fmaxf((v - a.bn_mean[cc]) * inv * a.bn_gamma[cc] + a.bn_beta[cc], 0.f);
           v = ok ? z : 0.f;  // padding taps stay zero: BN + ReLU applies to in-bounds taps only
         }
         if (++skx == KW) {
@@ -317,14 +318,16 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
     }
   } else {
     // K-block b uses register set and LDS buffer b & 1; the loads of b + 2 are issued before the MFMAs of b, so two
-    // blocks' loads are in flight while the MFMAs run
-    if (nk > 0) gload(kbeg, 0);
-    if (nk > 1) gload(kbeg + BK, 1);
+    // blocks' loads are in flight while the MFMAs run. The loads are issued on every step, past the last block too
+    // (range-checked buffer loads: the values are never stored): behind a branch, the compiler's wait before the LDS
+    // store of block b + 1 cannot count the loads of b + 2 as issued after it and waits for them as well.
+    gload(kbeg, 0);
+    gload(kbeg + BK, 1);
     if (nk > 0) sstore(0, 0);
     __syncthreads();
     auto step = [&](int it, auto setc) {
       constexpr int S = decltype(setc)::value;
-      if (it + 2 < nk) gload(kbeg + (it + 2) * BK, S);
+      gload(kbeg + (it + 2) * BK, S);
       mfma_block(S);
       if (it + 1 < nk) sstore(S ^ 1, S ^ 1);
       __syncthreads();
@@ -609,25 +612,23 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
       ix0 = (int)ox * a.S - a.PAD;
       xbase = (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
     }
+    // every load is issued (rows and columns past the tile's end at offset kOOB, which reads 0): a load behind a
+    // branch leaves the compiler unable to count it at the LDS stores, which then wait for every load in flight
 #pragma unroll
     for (int i = 0; i < AR; ++i)
-      ra[set][i] = (pw0 + i < P) ? bload(gr, gbase, (uint32_t)((pw0 + i) * ohw * 4)) : 0.f;
+      ra[set][i] = bload(gr, pw0 + i < P ? gbase : kOOB, (uint32_t)((pw0 + i) * ohw * 4));
     if (MODE == kTapMajor) {
-      const bool ok = (unsigned)(iy0 + ky0) < (unsigned)H && (unsigned)(ix0 + kx0) < (unsigned)W;
+      const bool ok = qw0 < Q && (unsigned)(iy0 + ky0) < (unsigned)H && (unsigned)(ix0 + kx0) < (unsigned)W;
       const uint32_t voff = ok ? xbase + (uint32_t)((ky0 * W + kx0) * 4) : kOOB;
 #pragma unroll
-      for (int j = 0; j < BR; ++j) rb[set][j] = (qw0 < Q) ? bload(xr, voff, (uint32_t)((c0 + j) * HW * 4)) : 0.f;
+      for (int j = 0; j < BR; ++j) rb[set][j] = bload(xr, voff, (uint32_t)((c0 + j) * HW * 4));
       return;
     }
     int c = c0, ky = ky0, kx = kx0;
 #pragma unroll
     for (int j = 0; j < BR; ++j) {
-      float v = 0.f;
-      if (qw0 + j < Q) {
-        const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
-        v = bload(xr, ok ? xbase + (uint32_t)((c * HW + ky * W + kx) * 4) : kOOB, 0);
-      }
-      rb[set][j] = v;
+      const bool ok = qw0 + j < Q && (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
+      rb[set][j] = bload(xr, ok ? xbase + (uint32_t)((c * HW + ky * W + kx) * 4) : kOOB, 0);
       if (++kx == KS) {
         kx = 0;
         if (++ky == KS) {
@@ -680,14 +681,15 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     }
   } else {
     // K-block b is loaded into register set b & 1 two blocks ahead: while the MFMAs of b run, the loads of b + 1
-    // and b + 2 are in flight
-    if (kbeg < kend) gload(kbeg, 0);
-    if (kbeg + BK < kend) gload(kbeg + BK, 1);
+    // and b + 2 are in flight. The loads are issued on every step (past kend they load zeros): behind a branch, the
+    // compiler's wait before the LDS store of block b + 1 cannot count the loads of b + 2 as issued after it.
+    gload(kbeg, 0);
+    gload(kbeg + BK, 1);
     auto step = [&](int k0, auto setc) {
       constexpr int S = decltype(setc)::value;
       sstore(S);
       __syncthreads();
-      if (k0 + 2 * BK < kend) gload(k0 + 2 * BK, S);
+      gload(k0 + 2 * BK, S);
       mfma_block();
       __syncthreads();
     };
