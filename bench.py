@@ -13,9 +13,10 @@ FLOPs per direction = 2*N*K*OH*OW*C*R*S (never the padded or stride-phase-expand
 
 The roofline object reports the dominant kernel, the implicit-GEMM gather (conv_gather_kernel, or its direct-to-LDS
 form conv_gather_dl_kernel for tap-major plans), from its forward launches: algorithmic FLOPs per launch over the
-launch's HIP-event duration, measured on the launch stream inside the timed steps. cpu_baseline times the CPU oracle (oracle/, a scalar-per-thread float64 restatement of the reference
-algorithm) on a bounded sample of the same workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the
-reference's CPU path) on a sample. Both are baselines, not targets.
+launch's HIP-event duration, measured on the launch stream inside the timed steps. cpu_baseline times the CPU oracle
+(oracle/, a scalar-per-thread float64 restatement of the reference algorithm) on a bounded sample of the same
+workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the reference's CPU path) on a sample. Both are baselines,
+not targets.
 """
 
 import argparse
@@ -179,6 +180,90 @@ def trace_summary(trace_csv, steps, n_layers):
         kinds[short(n).split("<")[0]] = kinds.get(short(n).split("<")[0], 0) + 1
     print(f"\nforward launches: {len(fwd)} ({', '.join(f'{k} x{v}' for k, v in sorted(kinds.items()))}), "
           f"average {sum(fwd) / len(fwd):.4f} ms")
+
+
+def kernel_table(trace_csv, prefix="omt::"):
+    """Per-kernel launch count, mean and median duration (us) of the kernels whose names contain `prefix`, from the
+    kernel_trace.csv of a rocprofv3 --kernel-trace run, as markdown (largest total time first)."""
+    import csv
+
+    per = {}
+    for r in csv.DictReader(open(trace_csv)):
+        if prefix not in r["Kernel_Name"]:
+            continue
+        n = r["Kernel_Name"].split("(")[0].strip()
+        n = n[5:] if n.startswith("void ") else n
+        per.setdefault(n, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| Kernel | Launches | Mean us | Median us |\n|---|---|---|---|")
+    for n, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        m = sorted(v)[len(v) // 2]
+        print(f"| `{n}` | {len(v)} | {sum(v) / len(v):.2f} | {m:.2f} |")
+
+
+RESNET_FAMILIES = [
+    # (family, substrings of the kernel name), first match wins
+    ("omt conv_bwd_dual_kernel (grad input + grad weight, one launch)", ("conv_bwd_dual_kernel",)),
+    ("omt gather (forward; grad input alone)", ("conv_gather_kernel", "conv_gather_dl_kernel")),
+    ("omt conv_wgrad_kernel (grad weight alone)", ("conv_wgrad_kernel",)),
+    ("omt split-K sums (gather_reduce, split_reduce, dual_reduce)", ("gather_reduce", "split_reduce", "dual_reduce")),
+    ("omt filter re-pack", ("pack_tapmajor", "pack_dgrad")),
+    ("omt BatchNorm", ("omt::bn_",)),
+    ("omt pools", ("maxpool", "avgpool", "adapool", "gap_")),
+    ("torch fused Adam (+ its step-count increment)", ("FusedAdam", "BinaryOpScalarFunctor<float")),
+    ("torch foreach (batch counters)", ("BinaryOpScalarFunctor<long", "foreach")),
+    ("hipBLASLt (linear layer)", ("Cijk", "hipblaslt", "gemm")),
+    ("torch softmax / nll / reductions", ("softmax", "nll", "reduce_kernel")),
+    ("runtime copies / fills", ("fill", "copy", "Copy")),
+    ("torch elementwise (ReLU, add, threshold_backward, counters)", ("elementwise",)),
+]
+
+
+def resnet_trace_summary(trace_csv, replays=22):
+    """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` and prints, for
+    the compiled graphed replays (the last run of `replays` identical steps) and the eager-model graphed replays (the
+    run before it), kernel time per step by family as markdown. Replays of one graph launch the same dispatch
+    sequence, so a run is the latest stretch of the trace that repeats with some period D `replays` times; any D
+    consecutive dispatches of it are one step's launches."""
+    import csv
+
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                  for r in csv.DictReader(open(trace_csv)))
+    names = [r[2] for r in rows]
+
+    def periodic_run(end_max, end_min):
+        for end in range(end_max, end_min, -1):
+            for d in range(50, 1000):
+                st = end - replays * d
+                if st < 0:
+                    break
+                if names[end - 1] != names[end - 1 - d]:
+                    continue
+                if all(names[i] == names[i - d] for i in range(st + d, end)):
+                    return st, d
+        return None
+
+    runs = []
+    hi = len(names)
+    for _ in range(2):
+        found = periodic_run(hi, max(0, hi - 20000))
+        if not found:
+            break
+        st, d = found
+        runs.append(rows[st:st + replays * d])
+        hi = st
+    for title, run in zip(("compiled graphed replays", "eager-model graphed replays"), runs):
+        d = len(run) // replays
+        per, cnt = {}, {}
+        for (t0, t1, name) in run:
+            fam = next((f for f, keys in RESNET_FAMILIES if any(k in name for k in keys)), "other")
+            per[fam] = per.get(fam, 0) + (t1 - t0) / 1e3
+            cnt[fam] = cnt.get(fam, 0) + 1
+        busy = sum(per.values()) / replays
+        print(f"## {title}: {replays} steps, {d} dispatches/step, kernel time {busy:.0f} us/step")
+        print("| Family | Launches / step | us / step | share |\n|---|---|---|---|")
+        for fam, us in sorted(per.items(), key=lambda kv: -kv[1]):
+            print(f"| {fam} | {cnt[fam] // replays} | {us / replays:.0f} | {100 * us / replays / busy:.1f}% |")
+        print()
 
 
 def pmc_summary(fetch_csv, write_csv, layers, workload):
@@ -488,12 +573,22 @@ def main():
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel table of the timed steps of a rocprofv3 --kernel-trace run of the sweep "
                          "(--no-bw --no-resnet --no-cpu, same --steps)")
+    ap.add_argument("--resnet-trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="kernel time per step by family of a rocprofv3 --kernel-trace run of --workload resnet")
+    ap.add_argument("--kernel-table", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel launches and mean / median duration of this library's kernels in a kernel trace")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
                          "launch per layer; prints nothing else")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
+        return
+    if args.kernel_table:
+        kernel_table(args.kernel_table)
+        return
+    if args.resnet_trace_summary:
+        resnet_trace_summary(args.resnet_trace_summary)
         return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps, len(C5_LAYERS if args.workload == "c5" else C1_LAYERS))
