@@ -58,14 +58,27 @@ _mod.synchronize = lambda device=None: core.sync()
 _mod.empty_cache = core.empty_cache
 _mod.memory_allocated = lambda device=None: core.memory_allocated()
 _mod.memory_reserved = lambda device=None: core.memory_reserved()
-# random numbers come from torch's HIP generator (the device's RNG ops run on torch's HIP kernels)
-_mod.manual_seed = lambda seed: torch.cuda.manual_seed(int(seed))
-_mod.manual_seed_all = lambda seed: torch.cuda.manual_seed_all(int(seed))
-_mod.seed = lambda: torch.cuda.seed()
-_mod.seed_all = lambda: torch.cuda.seed_all()
-_mod.initial_seed = lambda: torch.cuda.initial_seed()
-_mod.get_rng_state = lambda device=None: torch.cuda.get_rng_state()
-_mod.set_rng_state = lambda state, device=None: torch.cuda.set_rng_state(state)
+# random numbers come from torch's HIP generator (the device's RNG ops run on torch's HIP kernels). torch.cuda only
+# queues a seed until torch.cuda itself is initialized, which a program that uses this device alone never triggers:
+# torch.manual_seed (which calls manual_seed_all below) would then leave the generator unseeded, so every RNG entry
+# initializes torch.cuda first.
+
+
+def _hip_rng(fn):
+    def call(*args, **kwargs):
+        if torch.cuda.is_available():  # without a GPU the calls stay queued, as torch.cuda's own do
+            torch.cuda._lazy_init()
+        return fn(*args, **kwargs)
+    return call
+
+
+_mod.manual_seed = _hip_rng(lambda seed: torch.cuda.manual_seed(int(seed)))
+_mod.manual_seed_all = _hip_rng(lambda seed: torch.cuda.manual_seed_all(int(seed)))
+_mod.seed = _hip_rng(lambda: torch.cuda.seed())
+_mod.seed_all = _hip_rng(lambda: torch.cuda.seed_all())
+_mod.initial_seed = _hip_rng(lambda: torch.cuda.initial_seed())
+_mod.get_rng_state = _hip_rng(lambda device=None: torch.cuda.get_rng_state())
+_mod.set_rng_state = _hip_rng(lambda state, device=None: torch.cuda.set_rng_state(state))
 
 
 class _DeviceContext:

@@ -75,6 +75,60 @@ def test_transfer_views_and_delegated_ops(clean):
     assert omt.memory_allocated() > 0
 
 
+def test_storage_serialization_generators_events(clean):
+    """What PyTorch does through storages rather than ops (reference notes/scripts/storage_check.py): torch.save /
+    torch.load of device tensors (float, int64 beyond 32 bits, bool, a strided view; back onto the device or onto the
+    CPU with map_location), deepcopy of a module with buffers, bit views across dtypes, seeded device generators and
+    the global seed, and events recorded after device work."""
+    import io
+
+    omt = clean
+    dev = omt.DEVICE
+    x = torch.randn(5, 6)
+    big = torch.tensor([-(3 << 31), 0, 5 << 32], dtype=torch.int64)
+    blob = {"x": D(x, omt), "big": D(big, omt), "mask": D(x > 0.5, omt), "view": D(x, omt)[1:4, ::2]}
+    buf = io.BytesIO()
+    torch.save(blob, buf)
+    buf.seek(0)
+    back = torch.load(buf)
+    assert all(v.device.type == dev for v in back.values())
+    assert torch.equal(back["x"].cpu(), x) and back["big"].cpu().tolist() == big.tolist()
+    assert torch.equal(back["mask"].cpu(), x > 0.5) and torch.equal(back["view"].cpu(), x[1:4, ::2])
+    buf.seek(0)
+    host = torch.load(buf, map_location="cpu")
+    assert host["x"].device.type == "cpu" and torch.equal(host["view"], x[1:4, ::2])
+
+    model = nn.Sequential(nn.Conv2d(3, 4, 3), nn.BatchNorm2d(4)).to(dev)
+    model[1].running_mean.add_(0.25)
+    twin = copy.deepcopy(model)
+    assert twin[0].weight.device.type == dev and twin[0].weight.data_ptr() != model[0].weight.data_ptr()
+    for (k, a), b in zip(model.state_dict().items(), twin.state_dict().values()):
+        assert torch.equal(a.cpu(), b.cpu()), k
+
+    f = torch.randn(8)
+    assert torch.equal(D(f, omt).view(torch.int32).cpu(), f.view(torch.int32))
+    assert torch.equal(D(f, omt).view(torch.uint8).cpu(), f.view(torch.uint8))
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    a = torch.empty(64, device=dev).uniform_(generator=g)
+    g.manual_seed(11)
+    b = torch.empty(64, device=dev).uniform_(generator=g)
+    assert torch.equal(a.cpu(), b.cpu())
+    torch.manual_seed(5)
+    a = torch.randn(64, device=dev).cpu()
+    torch.manual_seed(5)
+    assert torch.equal(torch.randn(64, device=dev).cpu(), a)
+
+    ev = torch.Event(device=dev)
+    m = torch.randn(256, 256, device=dev)
+    y = m @ m
+    ev.record()
+    ev.synchronize()
+    assert ev.query() and torch.isfinite(y).all().item()
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS)
+
+
 def test_first_use_without_torch_cuda(clean):
     """A program that never touches torch.cuda itself: the first delegated op (a Linear) initializes torch's HIP
     context through the fallback. Runs in a fresh interpreter (this one has torch.cuda initialized already)."""
