@@ -248,6 +248,51 @@ int omt_adapool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t 
 int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* g, float* gx,
                     void* stream);
 
+/* ---- fused optimizers (float32, contiguous parameters; many tensors per launch) -------------------------------- */
+
+/* One parameter of an Adam / AdamW step: the step count (a float on the device) has already been incremented.
+ * max_exp_avg_sq is read only with amsgrad; grad is written back (unscaled) only with grad_scale. */
+typedef struct omt_adam_tensor {
+  float* param;
+  float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  float* max_exp_avg_sq;
+  const float* step;
+  int64_t numel;
+} omt_adam_tensor;
+/* lr_dev (a float on the device) overrides lr when set; grad_scale divides the gradients, and found_inf == 1 on the
+ * device skips the step (both optional, AMP). decoupled = AdamW. */
+typedef struct omt_adam_params {
+  float lr;
+  const float* lr_dev;
+  float beta1, beta2, weight_decay, eps;
+  int amsgrad, maximize, decoupled;
+  const float* grad_scale;
+  const float* found_inf;
+} omt_adam_params;
+/* Replaces _fused_adam_ / _fused_adamw_ (csrc/optim.cpp:30-67): p -= lr/(1-b1^t) m / (sqrt(v)/sqrt(1-b2^t) + eps). */
+int omt_fused_adam(const omt_adam_params* params, const omt_adam_tensor* tensors, int count, void* stream);
+
+/* One parameter of an SGD step; momentum_buffer is read and written only when momentum != 0. */
+typedef struct omt_sgd_tensor {
+  float* param;
+  float* grad;
+  float* momentum_buffer;
+  int64_t numel;
+} omt_sgd_tensor;
+/* first_step: the momentum buffers start as the (decayed) gradient. lr_dev, grad_scale, found_inf as for Adam. */
+typedef struct omt_sgd_params {
+  float lr;
+  const float* lr_dev;
+  float momentum, dampening, weight_decay;
+  int nesterov, maximize, first_step;
+  const float* grad_scale;
+  const float* found_inf;
+} omt_sgd_params;
+/* Replaces _fused_sgd_ (csrc/optim.cpp:12-28). */
+int omt_fused_sgd(const omt_sgd_params* params, const omt_sgd_tensor* tensors, int count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,35 @@ class Unsupported(OmtError):
     """OMT_UNSUPPORTED: the geometry is outside what the kernels cover (reference: NEED -> Unsupported)."""
 
 
+class AdamTensor(ctypes.Structure):
+    """omt_adam_tensor: one parameter of a fused Adam / AdamW step (reference csrc/optim.cpp:30-50)."""
+    _fields_ = [("param", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("exp_avg", ctypes.c_void_p),
+                ("exp_avg_sq", ctypes.c_void_p), ("max_exp_avg_sq", ctypes.c_void_p), ("step", ctypes.c_void_p),
+                ("numel", ctypes.c_int64)]
+
+
+class AdamParams(ctypes.Structure):
+    """omt_adam_params: hyper-parameters of a fused Adam / AdamW step."""
+    _fields_ = [("lr", ctypes.c_float), ("lr_dev", ctypes.c_void_p), ("beta1", ctypes.c_float),
+                ("beta2", ctypes.c_float), ("weight_decay", ctypes.c_float), ("eps", ctypes.c_float),
+                ("amsgrad", ctypes.c_int), ("maximize", ctypes.c_int), ("decoupled", ctypes.c_int),
+                ("grad_scale", ctypes.c_void_p), ("found_inf", ctypes.c_void_p)]
+
+
+class SgdTensor(ctypes.Structure):
+    """omt_sgd_tensor: one parameter of a fused SGD step (reference csrc/optim.cpp:12-28)."""
+    _fields_ = [("param", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("momentum_buffer", ctypes.c_void_p),
+                ("numel", ctypes.c_int64)]
+
+
+class SgdParams(ctypes.Structure):
+    """omt_sgd_params: hyper-parameters of a fused SGD step."""
+    _fields_ = [("lr", ctypes.c_float), ("lr_dev", ctypes.c_void_p), ("momentum", ctypes.c_float),
+                ("dampening", ctypes.c_float), ("weight_decay", ctypes.c_float), ("nesterov", ctypes.c_int),
+                ("maximize", ctypes.c_int), ("first_step", ctypes.c_int), ("grad_scale", ctypes.c_void_p),
+                ("found_inf", ctypes.c_void_p)]
+
+
 I64, U32, I32, F32, F64, SZ, VP = (ctypes.c_int64, ctypes.c_uint, ctypes.c_int, ctypes.c_float, ctypes.c_double,
                                    ctypes.c_size_t, ctypes.c_void_p)
 G = ctypes.POINTER(ConvGeo)
@@ -108,6 +137,8 @@ SIGNATURES = {
     "omt_avgpool_bwd": (I32, [I64] * 11 + [I32, I64, VP, VP, VP]),
     "omt_adapool_fwd": (I32, [I64] * 5 + [VP, VP, VP]),
     "omt_adapool_bwd": (I32, [I64] * 5 + [VP, VP, VP]),
+    "omt_fused_adam": (I32, [ctypes.POINTER(AdamParams), ctypes.POINTER(AdamTensor), I32, VP]),
+    "omt_fused_sgd": (I32, [ctypes.POINTER(SgdParams), ctypes.POINTER(SgdTensor), I32, VP]),
 }
 
 ABI_VERSION = 3
