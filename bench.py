@@ -371,6 +371,17 @@ def bandwidth_kernels(dev, reps=20):
     # global average pool (ResNet-50 head, b256)
     x = rnd(256, 2048, 7, 7)
     cases.append(("gap [256,2048,7,7] fwd", lambda x=x: H.adaptive_avg_pool2d(x, 1), nbytes(x) + 256 * 2048 * 4))
+    # fused Adam over ResNet-18's parameters (62 tensors, 11.7 M elements): p, g, m, v read, p, m, v written
+    import omarchy_mac_torch  # noqa: F401  (registers the device and its fused optimizer ops)
+    from omarchy_mac_torch import models
+
+    params = [p.detach().to(dev) for p in models.resnet18(1000).parameters()]
+    grads, ms = ([torch.randn_like(p) * 1e-2 for p in params] for _ in range(2))
+    vs = [torch.rand_like(p) * 1e-4 for p in params]
+    steps = [torch.ones((), device=dev) for _ in params]
+    numel = sum(p.numel() for p in params)
+    cases.append((f"fused adam [{len(params)} tensors, {numel / 1e6:.1f}M]",
+                  lambda: H.fused_adam(params, grads, ms, vs, steps), 7 * 4 * numel))
 
     stream = torch.cuda.current_stream(dev)
     out = []

@@ -352,3 +352,58 @@ def adaptive_avg_pool2d_backward(g, x_shape):
     check(L.omt_adapool_bwd(n * c, ih, iw, g.shape[2], g.shape[3], _ptr(g), _ptr(gx), _stream(g.device)),
           "adaptive_avg_pool2d_backward")
     return gx
+
+
+# ---- fused optimizers (reference csrc/optim.cpp:12-67) -----------------------------------------------------------
+
+def _scalar_ptr(t, name):
+    if t is None:
+        return None
+    if not t.is_cuda or t.dtype != torch.float32 or t.numel() != 1:
+        raise TypeError(f"{name}: expected a one-element float32 tensor on the HIP device")
+    return t.data_ptr()
+
+
+def fused_adam(params, grads, exp_avgs, exp_avg_sqs, steps, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
+               amsgrad=False, maximize=False, decoupled=False, max_exp_avg_sqs=None, grad_scale=None, found_inf=None):
+    """One Adam (decoupled: AdamW) step over lists of contiguous float32 tensors, in place; steps are one-element
+    float32 device tensors already incremented for this step. lr may be a one-element device tensor."""
+    n = len(params)
+    lists = [grads, exp_avgs, exp_avg_sqs, steps] + ([max_exp_avg_sqs] if amsgrad else [])
+    if any(len(x) != n for x in lists):
+        raise ValueError("fused_adam: tensor lists of different lengths")
+    arr = (_lib.AdamTensor * max(n, 1))()
+    for i in range(n):
+        ts = [params[i], grads[i], exp_avgs[i], exp_avg_sqs[i]] + ([max_exp_avg_sqs[i]] if amsgrad else [])
+        for t in ts:
+            if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != params[i].numel():
+                raise TypeError("fused_adam: contiguous float32 HIP tensors of matching sizes expected")
+        arr[i] = _lib.AdamTensor(params[i].data_ptr(), grads[i].data_ptr(), exp_avgs[i].data_ptr(),
+                                 exp_avg_sqs[i].data_ptr(), max_exp_avg_sqs[i].data_ptr() if amsgrad else None,
+                                 _scalar_ptr(steps[i], "step"), params[i].numel())
+    lr_dev = _scalar_ptr(lr, "lr") if isinstance(lr, torch.Tensor) else None
+    hp = _lib.AdamParams(0.0 if lr_dev else float(lr), lr_dev, betas[0], betas[1], weight_decay, eps, int(amsgrad),
+                         int(maximize), int(decoupled), _scalar_ptr(grad_scale, "grad_scale"),
+                         _scalar_ptr(found_inf, "found_inf"))
+    check(L.omt_fused_adam(ctypes.byref(hp), arr, n, _stream()), "fused_adam")
+
+
+def fused_sgd(params, grads, momentum_buffers=None, lr=1e-3, momentum=0.0, dampening=0.0, weight_decay=0.0,
+              nesterov=False, maximize=False, first_step=False, grad_scale=None, found_inf=None):
+    """One SGD step over lists of contiguous float32 tensors, in place (momentum_buffers when momentum != 0)."""
+    n = len(params)
+    if len(grads) != n or (momentum and len(momentum_buffers or []) != n):
+        raise ValueError("fused_sgd: tensor lists of different lengths")
+    arr = (_lib.SgdTensor * max(n, 1))()
+    for i in range(n):
+        ts = [params[i], grads[i]] + ([momentum_buffers[i]] if momentum else [])
+        for t in ts:
+            if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != params[i].numel():
+                raise TypeError("fused_sgd: contiguous float32 HIP tensors of matching sizes expected")
+        arr[i] = _lib.SgdTensor(params[i].data_ptr(), grads[i].data_ptr(),
+                                momentum_buffers[i].data_ptr() if momentum else None, params[i].numel())
+    lr_dev = _scalar_ptr(lr, "lr") if isinstance(lr, torch.Tensor) else None
+    hp = _lib.SgdParams(0.0 if lr_dev else float(lr), lr_dev, momentum, dampening, weight_decay, int(nesterov),
+                        int(maximize), int(first_step), _scalar_ptr(grad_scale, "grad_scale"),
+                        _scalar_ptr(found_inf, "found_inf"))
+    check(L.omt_fused_sgd(ctypes.byref(hp), arr, n, _stream()), "fused_sgd")

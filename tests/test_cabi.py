@@ -173,3 +173,30 @@ def test_fastdiv_exact(tmp_path):
                    check=True, capture_output=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip() == "OK", r.stdout
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """Every struct the ctypes layer passes through the C ABI has the header's size and field offsets (a mismatch
+    would hand the library shifted pointers)."""
+    import shutil
+    from omarchy_mac_torch import _lib
+    if shutil.which("g++") is None:
+        pytest.skip("needs g++")
+    structs = {"omt_conv_geo": _lib.ConvGeo, "omt_conv_plan": _lib.ConvPlan, "omt_adam_tensor": _lib.AdamTensor,
+               "omt_adam_params": _lib.AdamParams, "omt_sgd_tensor": _lib.SgdTensor, "omt_sgd_params": _lib.SgdParams}
+    lines = ["#include <cstddef>", "#include <cstdio>", '#include "omt_hip.h"', "int main() {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "structs.cpp"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "structs"
+    subprocess.run(["g++", "-std=c++17", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = dict((" ".join(l.split()[:2]), int(l.split()[2]))
+               for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines())
+    for cname, py in structs.items():
+        assert got[f"{cname} size"] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[f"{cname} {field}"] == getattr(py, field).offset, (cname, field)
