@@ -85,6 +85,8 @@ struct GatherArgs {
   FastDiv div_c;
   int nphase;
   int kslice;            // K elements per grid-z slice (a multiple of the K-block)
+  int tpw;               // conv1x1_stream_kernel: pixel tiles per workgroup
+  int rows;              // row epilogue: one phase written in place, no split K, OH OW % 4 == 0, y 16-byte aligned
   int wdirect;           // grad input, channel-major: A[ci][(co, a', b')] read from w[co][ci][ks][ks] (no re-pack)
   int ks, s;             //   the filter size and stride for that read
   float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
@@ -127,6 +129,52 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
         }
       }
   }
+}
+
+// Row epilogue, where a.rows holds: bias and ReLU, then the wave's WP x WQ outputs pass through its 8 x (WQ + 8)
+// floats of LDS at ep, 8 rows at a time, and leave as float4 runs along the output rows. WQ / 4 lanes write WQ * 4
+// contiguous bytes of one row per instruction, where the MFMA layout writes 64-byte pieces of four rows; that pattern
+// reaches about 70% of the row pattern's store bandwidth. Pass (i, h) stages rows 4 g + 2 h + {0, 1} of MFMA tile row
+// i (lane group g) as staged rows 2 g + {0, 1}; the pitch WQ + 8 puts the four groups on disjoint banks. The caller
+// makes ep free before (no wave still reads it) and, where LDS is used again, waits for the reads after.
+template <int WQ>
+constexpr int row_epi_floats() { return 8 * (WQ + 8); }
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                             int q0, int p0, int wp, int wq, int lane, float* __restrict__ ep) {
+  constexpr int EP = WQ + 8, LPR = WQ / 4, RPI = 64 / LPR;  // LDS row pitch; lanes per row, rows per store
+  static_assert(WQ == 32 || WQ == 64, "row runs");
+  const int P = a.P, grp = lane >> 4;
+  const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+  const int q = q0 + wq * WQ + 4 * (lane % LPR);
+  const uint32_t n = fdiv((uint32_t)min(q, ph.Q - 1), ph.div_ohw);
+  float* const yq = a.y + (int64_t)n * P * ohw + (q - (int)(n * ohw));
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+          const int p = p0 + wp * WP + 16 * i + 4 * grp + 2 * h + r2;
+          float v = acc[i][j][2 * h + r2];
+          if (a.bias && p < P) v += a.bias[p];
+          if (a.relu) v = fmaxf(v, 0.f);
+          ep[(2 * grp + r2) * EP + 16 * j + (lane & 15)] = v;
+        }
+      __builtin_amdgcn_wave_barrier();  // LDS runs one wave's accesses in order: its rows are there for the reads
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int t = 0; t < 8 / RPI; ++t) {
+        const int sr = lane / LPR + RPI * t;  // staged row: tile row 4 (sr / 2) + 2 h + sr % 2
+        const int p = p0 + wp * WP + 16 * i + 4 * (sr >> 1) + 2 * h + (sr & 1);
+        const float4 v = *reinterpret_cast<const float4*>(&ep[sr * EP + 4 * (lane % LPR)]);
+        if (p < P && q < ph.Q) *reinterpret_cast<float4*>(yq + (int64_t)p * ohw) = v;
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_wave_barrier();  // the next pass writes these rows
+    }
 }
 
 // One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats(). PF: K-blocks
@@ -317,28 +365,166 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       __syncthreads();
     }
   } else {
-    // K-block b uses register set and LDS buffer b & 1; the loads of b + 2 are issued before the MFMAs of b, so two
-    // blocks' loads are in flight while the MFMAs run. The loads are issued on every step, past the last block too
-    // (range-checked buffer loads: the values are never stored): behind a branch, the compiler's wait before the LDS
-    // store of block b + 1 cannot count the loads of b + 2 as issued after it and waits for them as well.
-    gload(kbeg, 0);
-    gload(kbeg + BK, 1);
+    // K-block b uses register set b % PF and LDS buffer b & 1; the loads of b + PF are issued before the MFMAs of b,
+    // so PF blocks' loads are in flight while the MFMAs run. The loads are issued on every step, past the last block
+    // too (range-checked buffer loads: the values are never stored): behind a branch, the compiler's wait before the
+    // LDS store of block b + 1 cannot count the later blocks' loads as issued after it and waits for them as well.
+    static_assert(PF == 2 || PF == 4, "register sets");
+#pragma unroll
+    for (int b = 0; b < PF; ++b) gload(kbeg + b * BK, b);
     if (nk > 0) sstore(0, 0);
     __syncthreads();
     auto step = [&](int it, auto setc) {
-      constexpr int S = decltype(setc)::value;
-      gload(kbeg + (it + 2) * BK, S);
-      mfma_block(S);
-      if (it + 1 < nk) sstore(S ^ 1, S ^ 1);
+      constexpr int S = decltype(setc)::value;  // it % PF
+      gload(kbeg + (it + PF) * BK, S);
+      mfma_block(S & 1);
+      if (it + 1 < nk) sstore((S + 1) & 1, (S + 1) % PF);
       __syncthreads();
     };
-    for (int it = 0; it < nk; it += 2) {
+    for (int it = 0; it < nk; it += PF) {
       step(it, std::integral_constant<int, 0>{});
       if (it + 1 < nk) step(it + 1, std::integral_constant<int, 1>{});
+      if constexpr (PF == 4) {
+        if (it + 2 < nk) step(it + 2, std::integral_constant<int, 2>{});
+        if (it + 3 < nk) step(it + 3, std::integral_constant<int, 3>{});
+      }
     }
   }
 
-  gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
+  static_assert(4 * row_epi_floats<WQ>() <= gather_lds_floats<BP, BQ, BK>(), "row epilogue fits the tile's LDS");
+  if (a.rows)  // the K loop's last barrier: no wave reads LDS
+    row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, lds + wave * row_epi_floats<WQ>());
+  else
+    gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
+}
+
+// 1x1, stride 1, unpadded convolutions (and their grad input, a 1x1 convolution with the transposed filter) with a
+// short reduction (K = C of 64 or 128: four or eight K-blocks per tile): Y[n][p][pix] = sum_c A[p][c] X[n][c][pix].
+// Launched one tile at a time, such a GEMM spends about as long in each workgroup's first-load latency and store
+// drain as in its MFMAs. Here a workgroup keeps one output-channel tile and walks `tpw` consecutive pixel tiles, and
+// its two-block prefetch runs on across the tile boundaries: the next tile's first K-blocks are loading while the
+// current tile finishes, and its output stores drain under the next tile's MFMAs. One phase, no split K, no BN
+// loader; K a multiple of the K-block (the host checks). Same LDS layout and MFMA order as the staged gather tiles,
+// so each output sums its K terms in the same order as there.
+template <int BP, int BQ, int WP, int WQ>
+__global__ void __launch_bounds__(256, 2) conv1x1_stream_kernel(const GatherArgs a, const int tpw) {
+  constexpr int NT = 256, BK = 16;
+  constexpr int WGQ = BQ / WQ, TI = WP / 16, TJ = WQ / 16, PK = BK + 4;
+  constexpr int AR = BP * BK / NT, BR = BQ * BK / NT;
+  static_assert((BP / WP) * (BQ / WQ) == 4 && BQ >= 64 && NT % BQ == 0 && BR % 4 == 0 && AR >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) float lds[gather_lds_floats<BP, BQ, BK>()];
+  float(*const As)[BP * PK] = reinterpret_cast<float(*)[BP * PK]>(lds);
+  float(*const Bs)[BQ * PK] = reinterpret_cast<float(*)[BQ * PK]>(lds + 2 * BP * PK);
+
+  const TileId tile = xcd_block_tile(kTileGroup);
+  const Phase ph = a.ph[0];
+  const int ntq = (ph.Q + BQ - 1) / BQ;
+  const int tq0 = tile.x * tpw, ntiles = min(ntq, tq0 + tpw) - tq0;
+  if (ntiles <= 0) return;
+  const int p0 = tile.y * BP, C = a.C, HW = a.H * a.W, P = a.P, K = ph.K;
+  const int nk = K / BK, nv = ntiles * nk;  // K-blocks per tile; virtual blocks (tile, K-block) of this workgroup
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave / WGQ, wq = wave % WGQ;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+
+  const int qc = t % BQ;
+  const int rbase = __builtin_amdgcn_readfirstlane((t / BQ) * BR);
+  const int wrow0 = t / BK, wk = t % BK;
+  uint32_t aoff[AR];
+#pragma unroll
+  for (int i = 0; i < AR; ++i) {
+    const int p = p0 + wrow0 + (NT / BK) * i;
+    aoff[i] = p < P ? (uint32_t)((ph.woff + p * K + wk) * 4) : kOOB;
+  }
+  // byte offset of x[n][0][pix] for this thread's pixel of pixel tile `tq` (past Q: out of range)
+  auto xbase = [&](int tq) -> uint32_t {
+    const int q = tq * BQ + qc;
+    if (q >= ph.Q) return kOOB;
+    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw);
+    return (uint32_t)(((int)n * C * HW + (q - (int)n * HW)) * 4);
+  };
+
+  // load side: the next virtual block to load is K-block lkb of pixel tile ltq. It runs PF = 2 blocks ahead of the
+  // MFMAs and past the workgroup's last tile (those loads read in-range or out-of-range values that are never
+  // stored), so every load is issued unconditionally and the compiler's waits count them exactly.
+  int ltq = tq0, lkb = 0;
+  uint32_t lxb = xbase(ltq);
+  float ra[2][AR], rb[2][BR];
+  auto gload = [&](const int set) {
+#pragma unroll
+    for (int i = 0; i < AR; ++i) ra[set][i] = bload(wr, aoff[i] == kOOB ? kOOB : aoff[i] + (uint32_t)(lkb * BK * 4), 0);
+#pragma unroll
+    for (int j = 0; j < BR; ++j) rb[set][j] = bload(xr, lxb, (uint32_t)((lkb * BK + rbase + j) * HW * 4));
+    if (++lkb == nk) {
+      lkb = 0;
+      lxb = xbase(++ltq);
+    }
+  };
+  auto sstore = [&](int buf, const int set) {
+#pragma unroll
+    for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[set][i];
+#pragma unroll
+    for (int j = 0; j < BR; j += 4)
+      *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) =
+          make_float4(rb[set][j], rb[set][j + 1], rb[set][j + 2], rb[set][j + 3]);
+  };
+
+  omt_f32x4 acc[TI][TJ];
+  auto zero = [&]() {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero();
+  const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
+  auto mfma_block = [&](int cur) {
+    float4 av[TI], bv[TJ];
+    const int ko = grp * (BK / 4);
+#pragma unroll
+    for (int i = 0; i < TI; ++i) av[i] = *reinterpret_cast<const float4*>(&As[cur][(la + 16 * i) * PK + ko]);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) bv[j] = *reinterpret_cast<const float4*>(&Bs[cur][(lb + 16 * j) * PK + ko]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(av[i], s), f4get(bv[j], s), acc[i][j], 0, 0, 0);
+  };
+
+  // the row epilogue stages each wave's rows in the two LDS buffers (both free at a tile's end: the last block's
+  // MFMAs are done after a barrier, and the next block is stored only afterwards); the host checks a.rows
+  static_assert(4 * row_epi_floats<WQ>() <= gather_lds_floats<BP, BQ, BK>(), "row epilogue fits the tile's LDS");
+  float* const ep = lds + wave * row_epi_floats<WQ>();
+
+  gload(0);
+  gload(1);
+  sstore(0, 0);
+  __syncthreads();
+  int ckb = 0, ctq = tq0;  // compute side: K-block and pixel tile of the block the MFMAs take next
+  auto step = [&](int v, auto setc) {
+    constexpr int S = decltype(setc)::value;  // v & 1: register set and LDS buffer of block v
+    gload(S);                                 // block v + 2 into the set block v vacated
+    mfma_block(S);
+    if (++ckb == nk) {
+      __syncthreads();  // every wave's MFMAs of this block have read buffer S
+      row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, ctq * BQ, p0, wp, wq, lane, ep);
+      zero();
+      ckb = 0;
+      ++ctq;
+      __syncthreads();  // the staged rows are read before block v + 1 lands in LDS
+    }
+    if (v + 1 < nv) sstore(S ^ 1, S ^ 1);
+    __syncthreads();
+  };
+  for (int v = 0; v < nv; v += 2) {
+    step(v, std::integral_constant<int, 0>{});
+    if (v + 1 < nv) step(v + 1, std::integral_constant<int, 1>{});
+  }
 }
 
 template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF>
@@ -523,7 +709,13 @@ __device__ __forceinline__ void gather_tile_dl(const GatherArgs& a, const int bx
       steps(it, std::integral_constant<int, 7>{});
     }
   }
-  gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
+  static_assert(4 * row_epi_floats<WQ>() <= gather_dl_stage_floats<BQ, BK>(), "row epilogue fits one stage");
+  if (a.rows) {
+    __syncthreads();  // every wave's MFMAs have read their last stage
+    row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, stg[0] + wave * row_epi_floats<WQ>());
+  } else {
+    gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
+  }
 }
 
 template <int BQ, int WP, int WQ, int BK, int NS>
@@ -680,22 +872,27 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
       __syncthreads();
     }
   } else {
-    // K-block b is loaded into register set b & 1 two blocks ahead: while the MFMAs of b run, the loads of b + 1
-    // and b + 2 are in flight. The loads are issued on every step (past kend they load zeros): behind a branch, the
-    // compiler's wait before the LDS store of block b + 1 cannot count the loads of b + 2 as issued after it.
-    gload(kbeg, 0);
-    gload(kbeg + BK, 1);
+    // K-block b is loaded into register set b % PF, PF blocks ahead: while the MFMAs of b run, the loads of b + 1
+    // .. b + PF are in flight. The loads are issued on every step (past kend they load zeros): behind a branch, the
+    // compiler's wait before the LDS store of block b + 1 cannot count the later blocks' loads as issued after it.
+    static_assert(PF == 2 || PF == 4, "register sets");
+#pragma unroll
+    for (int b = 0; b < PF; ++b) gload(kbeg + b * BK, b);
     auto step = [&](int k0, auto setc) {
-      constexpr int S = decltype(setc)::value;
+      constexpr int S = decltype(setc)::value;  // block % PF
       sstore(S);
       __syncthreads();
-      gload(k0 + 2 * BK, S);
+      gload(k0 + PF * BK, S);
       mfma_block();
       __syncthreads();
     };
-    for (int k0 = kbeg; k0 < kend; k0 += 2 * BK) {
+    for (int k0 = kbeg; k0 < kend; k0 += PF * BK) {
       step(k0, std::integral_constant<int, 0>{});
       if (k0 + BK < kend) step(k0 + BK, std::integral_constant<int, 1>{});
+      if constexpr (PF == 4) {
+        if (k0 + 2 * BK < kend) step(k0 + 2 * BK, std::integral_constant<int, 2>{});
+        if (k0 + 3 * BK < kend) step(k0 + 3 * BK, std::integral_constant<int, 3>{});
+      }
     }
   }
 
@@ -939,6 +1136,7 @@ struct Tile {
   float eff;    // relative MFMA efficiency of the wave tile (operand reuse)
   int bk = 16;  // K-block (gather kernels)
   int ns = 0;   // > 0: direct global -> LDS loads into an ns-stage ring (tap-major order; else the staged kernel)
+  int stream = 0;  // 1x1 stride-1 convolutions only: conv1x1_stream_kernel (runs of pixel tiles per workgroup)
 };
 
 // Picks the tile with the smallest estimated makespan: rounds of `slots` concurrent workgroups times the padded
@@ -967,7 +1165,7 @@ static const Tile kGatherTiles[] = {
     {32, 256, 32, 64, 0.90f},     {16, 256, 16, 64, 0.80f},     {64, 64, 32, 32, 0.80f},
     {64, 64, 32, 32, 0.90f, 64},  {64, 128, 32, 64, 0.95f, 32}, {128, 64, 64, 32, 0.95f, 32},
     {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3}, {64, 64, 32, 32, 0.90f, 32, 3},
-    {64, 128, 32, 64, 0.97f, 32, 2},
+    {64, 128, 32, 64, 0.97f, 32, 2}, {64, 128, 32, 64, 0.95f, 16, 0, 1},
 };
 // Plan tile index t < 2 * kNGather: kGatherTiles[t % kNGather], and t >= kNGather forces the channel-major K order
 // (no filter re-pack, one launch fewer; the tap-major order gathers faster on large layers).
@@ -1037,6 +1235,7 @@ static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const 
   double best_cost = 1e300;
   for (int ti = 0; ti < kNGather; ++ti) {
     const Tile& tl = kGatherTiles[ti];
+    if (tl.stream) continue;  // chosen by tuning only
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(kk, tl.bk);
     for (int sc : kSliceChoices) {
       const int64_t kb = cdiv(nkb, sc);
@@ -1060,6 +1259,13 @@ static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const 
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// The row epilogue applies to one phase written in place (no stride grid, no split K) whose float4 runs of output
+// pixels stay inside one image and are 16-byte aligned.
+static bool rows_ok(const GatherArgs& a, bool split) {
+  const Phase& p = a.ph[0];
+  return !split && a.nphase == 1 && p.os == 1 && p.oy0 == 0 && p.ox0 == 0 && a.YH == p.OH && a.YW == p.OW &&
+         (p.OH * p.OW) % 4 == 0 && (uintptr_t)a.y % 16 == 0;
+}
 // Completes a gather launch's arguments for its plan: K slice length and, split over K, the partials `part` (the
 // workspace of the plan's size). Returns the grid.
 static dim3 gather_grid(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part) {
@@ -1067,7 +1273,26 @@ static dim3 gather_grid(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t 
   a.kslice = (int)pl.kslice;
   a.part = pl.slices > 1 ? part : nullptr;
   a.part_stride = n * a.P * a.YH * a.YW;
+  a.tpw = 0;
+  a.rows = rows_ok(a, pl.slices > 1);
+  if (tl.stream) {  // about four workgroups per CU, each with a run of pixel tiles
+    const int64_t ntq = cdiv(maxq, tl.bq), ntp = cdiv(a.P, tl.bp);
+    a.tpw = (int)std::max<int64_t>(1, cdiv(ntq * ntp, 4 * kCUs));
+    return dim3((unsigned)cdiv(ntq, a.tpw), (unsigned)ntp, 1);
+  }
   return dim3((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
+}
+// The 1x1 streaming tile runs only where its kernel applies (one 1x1 stride-1 unpadded phase, the [P][K] filter in
+// place or re-packed, no BN loader, no split K, whole K-blocks, float4 runs of output pixels inside one image and
+// 16-byte aligned); anywhere else its plan runs as the staged tile of the same shape and K-block (tile 2).
+static bool stream_ok(const GatherArgs& a, const GatherPlan& pl) {
+  const Phase& p = a.ph[0];
+  return !gcm(pl.tile) && pl.slices == 1 && !a.bn_mean && !a.wdirect && p.KH == 1 && p.KW == 1 && p.S == 1 &&
+         p.PH == 0 && p.PW == 0 && p.K % 16 == 0 && rows_ok(a, false);
+}
+static GatherPlan eff_plan(const GatherArgs& a, GatherPlan pl) {
+  if (gtile(pl.tile).stream && !stream_ok(a, pl)) pl.tile = (gcm(pl.tile) ? kNGather : 0) + 2;
+  return pl;
 }
 // Tap-major K order of a gather launch (the BN loader keeps the channel-major order).
 static bool gather_uses_tap_major(const GatherArgs& a, const GatherPlan& pl) {
@@ -1099,8 +1324,13 @@ static int launch_gather_sum(const GatherSum& r, hipStream_t s) {
 }
 
 // Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size.
-static int run_gather(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part, hipStream_t s) {
+static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t maxq, float* part, hipStream_t s) {
+  const GatherPlan pl = eff_plan(a, plan);
   const dim3 grid = gather_grid(a, pl, n, maxq, part);
+  if (gtile(pl.tile).stream) {
+    hipLaunchKernelGGL((conv1x1_stream_kernel<64, 128, 32, 64>), grid, dim3(256), 0, s, a, a.tpw);
+    return launch_check("conv1x1_stream_kernel");
+  }
   if (a.bn_mean)
     gather_dispatch<kGeneric, true>(pl.tile % kNGather, a, grid, s);
   else if (gather_uses_tap_major(a, pl) && gtile(pl.tile).ns && (uintptr_t)a.w % 16 == 0)
@@ -1690,8 +1920,14 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     for (int i = 0; i < a.nphase; ++i) K = std::max<int64_t>(K, a.ph[i].K);
     P = g->ci, z = a.nphase, plane = g->n * g->ci * g->ih * g->iw;
   }
+  // the 1x1 streaming tile: one 1x1 stride-1 unpadded phase with whole K-blocks, tap-major order, no split
+  const bool stream_geo = g->ks == 1 && g->stride == 1 && g->pad == 0 && K % 16 == 0 && (g->ih * g->iw) % 4 == 0;
   for (int t = 0; t < ntile; ++t) {
     const Tile& tl = gtile(t);
+    if (tl.stream) {
+      if (stream_geo && !gcm(t)) out.push_back({t, 1});
+      continue;
+    }
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(std::max<int64_t>(K, 1), tl.bk);
     int64_t last = -1;
     for (int sc : {1, 2, 4, 8, 16, 32, 64}) {

@@ -162,10 +162,10 @@ FALLBACKS = _Fallbacks()
 
 # ---- on-disk cache of the conv plan tuning (reference: omarchy_mac_torch/native.py:185-209) ----
 # Keys "dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad" -> [tile, slices]. The tiles index this library's gfx950 tile tables
-# (the file name carries the table's size: 13 gather tiles, each in two K orders),
+# (the file name carries the table's size: 14 gather tiles, each in two K orders),
 # so the file is not the reference's (whose entries name its own tiles and a split-K multiplier).
 TUNE_FILE = os.environ.get("OMARCHY_MAC_TORCH_TUNE_FILE",
-                           os.path.expanduser("~/.cache/omarchy-mac-torch/tuning-gfx950-t13.json"))
+                           os.path.expanduser("~/.cache/omarchy-mac-torch/tuning-gfx950-t14.json"))
 
 
 def _load_tuning(path=TUNE_FILE):

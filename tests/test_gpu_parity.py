@@ -164,6 +164,37 @@ def test_conv_every_plan(cuda, ops, shape):
         ops.clear_conv_plans()
 
 
+STREAM_TILE = 13  # the 1x1 streaming tile (conv1x1_stream_kernel); tile 2 is the staged tile of the same shape
+STREAM_SHAPES = [
+    (32, 64, 256, 56),   # ResNet-50 1x1 expansion at 56^2: runs of 4 pixel tiles per workgroup
+    (17, 32, 272, 46),   # P not a multiple of 64, N*H*W not a multiple of 128, a short last run
+    (3, 48, 20, 10),     # one run, K of three blocks
+    (17, 32, 272, 45),   # H*W % 4 != 0: the row epilogue does not apply and the plan runs as tile 2
+]
+
+
+@pytest.mark.parametrize("shape", STREAM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv1x1_stream_tile_matches_staged_tile(cuda, ops, shape):
+    """The streaming 1x1 kernel sums each output's K terms in the staged tile's order and stores whole float4 rows
+    through LDS: forward (bias + ReLU) and grad input bit-identical to tile 2, and both against the oracle."""
+    n, ci, co, h = shape
+    rng = np.random.default_rng(sum(shape))
+    x, wt, b = rnd(rng, n, ci, h, h), rnd(rng, co, ci, 1, 1, scale=ci ** -0.5), rnd(rng, co)
+    gy = rnd(rng, n, co, h, h)
+    tx, tw, tb, tgy = dev(x, cuda), dev(wt, cuda), dev(b, cuda), dev(gy, cuda)
+    out = {}
+    try:
+        for tile in (STREAM_TILE, 2):
+            ops.set_conv_plan("fwd", x.shape, wt.shape, 1, 0, tile, 1)
+            ops.set_conv_plan("dgrad", x.shape, wt.shape, 1, 0, tile, 1)
+            out[tile] = (ops.conv2d(tx, tw, tb, 1, 0, relu=True), ops.conv2d_dgrad(tgy, tw, x.shape, 1, 0))
+    finally:
+        ops.clear_conv_plans()
+    assert torch.equal(out[STREAM_TILE][0], out[2][0]) and torch.equal(out[STREAM_TILE][1], out[2][1])
+    assert orc.rel_l2(host(out[STREAM_TILE][0]), orc.conv_fwd(x, wt, b, 1, 0, relu=True)) <= TOL
+    assert orc.rel_l2(host(out[STREAM_TILE][1]), orc.conv_dgrad(gy, wt, x.shape, 1, 0)) <= TOL
+
+
 BWD_SHAPES = [
     (4, 512, 512, 2, 2, 3, 1, 1),   # ResNet-18 layer4: both GEMMs split K
     (3, 64, 128, 9, 9, 3, 2, 1),    # stride 2: grad-input stride phases
