@@ -11,8 +11,9 @@ resident in HBM:
   c1:           BASELINE config 1, AlexNet conv1 (16x3x224x224, 64x11x11, stride 4, pad 2). 6.747 GFLOP per step.
 FLOPs per direction = 2*N*K*OH*OW*C*R*S (never the padded or stride-phase-expanded work).
 
-The roofline object reports the dominant kernel, the implicit-GEMM gather (conv_gather_kernel, or its direct-to-LDS
-form conv_gather_dl_kernel for tap-major plans), from its forward launches: algorithmic FLOPs per launch over the
+The roofline object reports the dominant kernel, the implicit-GEMM gather (conv_gather_kernel, its direct-to-LDS
+form conv_gather_dl_kernel, or the persistent 1x1 conv1x1_stream_kernel, whichever the tuned plan of each layer
+runs), from its forward launches: algorithmic FLOPs per launch over the
 launch's HIP-event duration, measured on the launch stream inside the timed steps. cpu_baseline times the CPU oracle
 (oracle/, a scalar-per-thread float64 restatement of the reference algorithm) on a bounded sample of the same
 workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the reference's CPU path) on a sample. Both are baselines,
@@ -131,9 +132,13 @@ def torch_cpu_baseline(layers, batch, threads):
                       f"at batch {batch}, {cpu_info()}"}
 
 
+GATHER_KERNELS = ("conv_gather_kernel", "conv_gather_dl_kernel", "conv1x1_stream_kernel")
+
+
 def _is_gather(kernel_name):
-    """The implicit-GEMM gather kernels (staged conv_gather_kernel and direct-to-LDS conv_gather_dl_kernel)."""
-    return "conv_gather_kernel" in kernel_name or "conv_gather_dl_kernel" in kernel_name
+    """The implicit-GEMM gather kernels: staged conv_gather_kernel, direct-to-LDS conv_gather_dl_kernel and the
+    persistent 1x1 conv1x1_stream_kernel."""
+    return any(k in kernel_name for k in GATHER_KERNELS)
 
 
 def trace_summary(trace_csv, steps, n_layers):
@@ -203,7 +208,7 @@ def kernel_table(trace_csv, prefix="omt::"):
 RESNET_FAMILIES = [
     # (family, substrings of the kernel name), first match wins
     ("omt conv_bwd_dual_kernel (grad input + grad weight, one launch)", ("conv_bwd_dual_kernel",)),
-    ("omt gather (forward; grad input alone)", ("conv_gather_kernel", "conv_gather_dl_kernel")),
+    ("omt gather (forward; grad input alone)", GATHER_KERNELS),
     ("omt conv_wgrad_kernel (grad weight alone)", ("conv_wgrad_kernel",)),
     ("omt split-K sums (gather_reduce, split_reduce, dual_reduce)", ("gather_reduce", "split_reduce", "dual_reduce")),
     ("omt filter re-pack", ("pack_tapmajor", "pack_dgrad")),
@@ -719,7 +724,7 @@ def main():
                                 "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad"),
                    "gflop_per_step": round(step_flops / 1e9, 2), "layout": "NCHW"},
         "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
-        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel (forward launches)", "bound": "mfma",
+        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel / conv1x1_stream_kernel (forward launches)", "bound": "mfma",
                      "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4), "traffic": traffic_per_launch(args.workload),
                      "avg_launch_ms": round(avg_launch_ms, 4),

@@ -178,8 +178,9 @@ __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& p
 }
 
 // One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats(). PF: K-blocks
-// of operand loads in flight ahead of the MFMAs (2 for the tiles of small, load-latency-bound layers).
-template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF = 1>
+// of operand loads in flight ahead of the MFMAs: 2 (one block measured slower on every layer, four slower still),
+// or 1 where the second register set would spill (the BN loader on the 64 x 256 tile).
+template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF = 2>
 __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, const int by, const int bz,
                                             float* __restrict__ lds) {
   constexpr int NT = 256;
@@ -365,29 +366,25 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       __syncthreads();
     }
   } else {
-    // K-block b uses register set b % PF and LDS buffer b & 1; the loads of b + PF are issued before the MFMAs of b,
-    // so PF blocks' loads are in flight while the MFMAs run. The loads are issued on every step, past the last block
-    // too (range-checked buffer loads: the values are never stored): behind a branch, the compiler's wait before the
-    // LDS store of block b + 1 cannot count the later blocks' loads as issued after it and waits for them as well.
-    static_assert(PF == 2 || PF == 4, "register sets");
-#pragma unroll
-    for (int b = 0; b < PF; ++b) gload(kbeg + b * BK, b);
+    // K-block b uses register set and LDS buffer b & 1; the loads of b + 2 are issued before the MFMAs of b, so two
+    // blocks' loads are in flight while the MFMAs run. The loads are issued on every step, past the last block too
+    // (range-checked buffer loads: the values are never stored): behind a branch, the compiler's wait before the LDS
+    // store of block b + 1 cannot count the later blocks' loads as issued after it and waits for them as well.
+    static_assert(PF == 2, "two register sets");
+    gload(kbeg, 0);
+    gload(kbeg + BK, 1);
     if (nk > 0) sstore(0, 0);
     __syncthreads();
     auto step = [&](int it, auto setc) {
-      constexpr int S = decltype(setc)::value;  // it % PF
-      gload(kbeg + (it + PF) * BK, S);
-      mfma_block(S & 1);
-      if (it + 1 < nk) sstore((S + 1) & 1, (S + 1) % PF);
+      constexpr int S = decltype(setc)::value;  // it & 1
+      gload(kbeg + (it + 2) * BK, S);
+      mfma_block(S);
+      if (it + 1 < nk) sstore(S ^ 1, S ^ 1);
       __syncthreads();
     };
-    for (int it = 0; it < nk; it += PF) {
+    for (int it = 0; it < nk; it += 2) {
       step(it, std::integral_constant<int, 0>{});
       if (it + 1 < nk) step(it + 1, std::integral_constant<int, 1>{});
-      if constexpr (PF == 4) {
-        if (it + 2 < nk) step(it + 2, std::integral_constant<int, 2>{});
-        if (it + 3 < nk) step(it + 3, std::integral_constant<int, 3>{});
-      }
     }
   }
 
@@ -1182,18 +1179,18 @@ constexpr int64_t kCUs = 256;
 template <int MODE, bool BN>
 static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
   switch (ti) {
-    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, MODE, BN, BN ? 1 : 2>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 5: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 7: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 8: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     // the direct-LDS tiles when their kernel does not apply (channel-major order, BN loader): the staged kernel
     case 9: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
-    case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 1>), grid, dim3(256), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 11: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     default: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
   }
