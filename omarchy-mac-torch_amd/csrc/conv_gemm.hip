@@ -240,9 +240,26 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
     const int p = p0 + wrow0 + (NT / BK) * i;
     aoff[i] = p < P ? (uint32_t)((woff + p * K + wk) * 4) : kOOB;
   }
+  // Tap-major weights (whole K-blocks, K and woff multiples of 16): each thread loads runs of four k of one row as
+  // one 16-byte load (a multi-dword buffer load needs 4-byte alignment only, so a filter used in place may sit
+  // anywhere) and stores them with one b128 LDS write: element e = t + NT i of the tile's BP x BK / 4 runs is row
+  // e / (BK / 4), k 4 (e % (BK / 4)).
+  constexpr bool A4 = MODE == kTapMajor && BP * BK >= 4 * NT;
+  constexpr int AR4 = A4 ? BP * BK / (4 * NT) : 1, KQ = BK / 4;
+  uint32_t aoff4[AR4];
+#pragma unroll
+  for (int i = 0; i < AR4; ++i) {
+    const int e = t + NT * i, p = p0 + e / KQ;
+    aoff4[i] = p < P ? (uint32_t)((woff + p * K + 4 * (e % KQ)) * 4) : kOOB;
+  }
 
   float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
+  float4 ra4[PF][AR4];
   auto gload = [&](int k0, const int set) {
+    if constexpr (A4) {
+#pragma unroll
+      for (int i = 0; i < AR4; ++i) ra4[set][i] = bload4(wr, aoff4[i] + (uint32_t)(k0 * 4), 0);
+    } else {
 #pragma unroll
     for (int i = 0; i < AR; ++i) {
       const int p = p0 + wrow0 + (NT / BK) * i, k = k0 + wk;
@@ -259,6 +276,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
         if (MODE != kTapMajor && k >= K) off = kOOB;
       }
       ra[set][i] = bload(wr, off, 0);
+    }
     }
     if (MODE == kTapMajor) {
       // k = tap * C + c with C % BK == 0: this thread's BR rows share one tap and K has no tail
@@ -309,8 +327,16 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
     }
   };
   auto sstore = [&](int buf, const int set) {
+    if constexpr (A4) {
 #pragma unroll
-    for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[set][i];
+      for (int i = 0; i < AR4; ++i) {
+        const int e = t + NT * i;
+        *reinterpret_cast<float4*>(&As[buf][(e / KQ) * PK + 4 * (e % KQ)]) = ra4[set][i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[set][i];
+    }
 #pragma unroll
     for (int j = 0; j < BR; j += 4)
       *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) =

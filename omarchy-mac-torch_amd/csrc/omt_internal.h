@@ -62,6 +62,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
+// Four consecutive floats (a multi-dword buffer load needs 4-byte alignment only; all four in range or all four out).
+__device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
 
 // Sum over the 64 lanes of a wave, in every lane: four DPP steps within each row of 16 lanes, each adding a disjoint
 // partner (quad_perm [1,0,3,2] and [2,3,0,1]: every lane holds its quad's sum; row_half_mirror pairs the two quads
