@@ -17,7 +17,8 @@ runs), from its forward launches: algorithmic FLOPs per launch over the
 launch's HIP-event duration, measured on the launch stream inside the timed steps. cpu_baseline times the CPU oracle
 (oracle/, a scalar-per-thread float64 restatement of the reference algorithm) on a bounded sample of the same
 workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the reference's CPU path) on a sample. Both are baselines,
-not targets.
+not targets. miopen_same_sweep times the same sweep through torch's own convolutions on the same GPU (MIOpen), the
+convolution a PyTorch-ROCm user gets without this library (--no-miopen skips it).
 """
 
 import argparse
@@ -322,6 +323,48 @@ def traffic_per_launch(workload):
         return None
 
 
+def miopen_sweep(layers, dev, reps):
+    """The same sweep through stock PyTorch-ROCm convolutions (MIOpen, its default find mode; fp32): the convolution
+    a user of this GPU gets without this library. TFLOP/s per direction and over the sweep, each direction's time the
+    mean of `reps` calls after one untimed call (which includes MIOpen's own kernel search)."""
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(1)
+    tot, fl_tot, layer = {"fwd": 0.0, "dgrad": 0.0, "wgrad": 0.0}, 0, {}
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    for (name, n, c, k, h, ks, s, p) in layers:
+        o = out_size(h, ks, s, p)
+        x = torch.randn((n, c, h, h), device=dev, generator=gen)
+        w = torch.randn((k, c, ks, ks), device=dev, generator=gen) * (c * ks * ks) ** -0.5
+        gy = torch.randn((n, k, o, o), device=dev, generator=gen)
+        fl = flops_dir(n, c, k, h, ks, s, p)
+
+        def bwd(mask):
+            return lambda: torch.ops.aten.convolution_backward(gy, x, w, None, [s, s], [p, p], [1, 1], False, [0, 0],
+                                                              1, mask)
+        ms = {"fwd": timed(lambda: torch.nn.functional.conv2d(x, w, None, s, p)),
+              "dgrad": timed(bwd([True, False, False])), "wgrad": timed(bwd([False, True, False]))}
+        for d in ms:
+            tot[d] += ms[d]
+        fl_tot += fl
+        layer[name] = {d: round(fl / ms[d] / 1e9, 1) for d in ms}
+        print(f"miopen {name}: {layer[name]}", file=sys.stderr, flush=True)
+    return {"value": round(3 * fl_tot / sum(tot.values()) / 1e9, 3), "unit": "TFLOP/s",
+            "per_direction": {d: round(fl_tot / tot[d] / 1e9, 2) for d in tot}, "per_layer_tflops": layer,
+            "library": f"torch {torch.__version__} conv2d / convolution_backward (MIOpen, default find mode)"}
+
+
 def bandwidth_kernels(dev, reps=20):
     """The HBM-bound kernels of the path on shapes from the BASELINE configs: achieved GB/s from algorithmic
     (compulsory) bytes -- each input read once, each output written once, fp32, int64 pool indices -- over the op's
@@ -579,6 +622,8 @@ def main():
                     help="resnet: only the ResNet-18 training-step measurement; bw: only the HBM-bound kernels "
                          "(both for profiling)")
     ap.add_argument("--no-bw", action="store_true", help="skip the HBM-bound kernel measurements")
+    ap.add_argument("--no-miopen", action="store_true",
+                    help="skip timing the same sweep through torch's own convolutions (MIOpen)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-resnet", action="store_true", help="skip the ResNet-18 training-step measurement")
     ap.add_argument("--resnet-steps", type=int, default=20)
@@ -734,6 +779,8 @@ def main():
         "plans": {"tuned": not args.no_tune, "tile_slices": plans},
         "device": torch.cuda.get_device_name(dev),
     }
+    if not args.no_miopen:
+        out["miopen_same_sweep"] = miopen_sweep(layers, dev, args.steps)
     if not args.no_bw:
         out["bandwidth_kernels"] = bandwidth_kernels(dev)
     if not args.no_resnet:

@@ -1952,10 +1952,16 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
       continue;
     }
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(std::max<int64_t>(K, 1), tl.bk);
+    // A grid that already fills the GPU is split only to even out its last round: a few workgroups per CU, all
+    // resident at once, finish when the CUs holding one more than the rest do (1568 tiles: 7 on some CUs, 6.125 on
+    // average); 2-4 slices of at least 8 K-blocks each spread them more evenly.
+    const bool full = tiles >= 2 * kCUs;
     int64_t last = -1;
-    for (int sc : {1, 2, 4, 8, 16, 32, 64}) {
+    for (int sc : {1, 2, 3, 4, 8, 16, 32, 64}) {
       const int64_t kb = cdiv(nkb, sc), eff = cdiv(nkb, kb);
-      if (sc > 1 && (kb < 2 || tiles >= 2 * kCUs)) break;  // a grid that already fills the GPU is not split
+      if (sc > 1 && kb < 2) break;
+      if (full && sc > 1 && (sc > 4 || tiles >= 16 * kCUs || kb < 8)) break;
+      if (!full && sc == 3) continue;
       if (eff == last || (eff > 1 && eff * plane * 4 > ((int64_t)512 << 20))) continue;
       last = eff;
       out.push_back({t, (int32_t)eff});
