@@ -215,6 +215,7 @@ RESNET_FAMILIES = [
     ("omt filter re-pack", ("pack_tapmajor", "pack_dgrad")),
     ("omt BatchNorm", ("omt::bn_",)),
     ("omt pools", ("maxpool", "avgpool", "adapool", "gap_")),
+    ("omt fused Adam / SGD (multi-tensor)", ("fused_adam_kernel", "fused_sgd_kernel")),
     ("torch fused Adam (+ its step-count increment)", ("FusedAdam", "BinaryOpScalarFunctor<float")),
     ("torch foreach (batch counters)", ("BinaryOpScalarFunctor<long", "foreach")),
     ("hipBLASLt (linear layer)", ("Cijk", "hipblaslt", "gemm")),
