@@ -195,6 +195,28 @@ def test_conv1x1_stream_tile_matches_staged_tile(cuda, ops, shape):
     assert orc.rel_l2(host(out[STREAM_TILE][1]), orc.conv_dgrad(gy, wt, x.shape, 1, 0)) <= TOL
 
 
+@pytest.mark.parametrize("tile", [0, 2, 5, 10, STREAM_TILE])
+def test_conv1x1_filter_used_in_place_off_16_bytes(cuda, ops, tile):
+    """A 1x1 filter is read in place; from a view 4 bytes past a 16-byte boundary the tap-major tiles' 16-byte filter
+    loads (4-byte alignment suffices) and the stream tile give the aligned filter's results, and a direct-to-LDS tile
+    (tile 10) runs as its staged form."""
+    n, ci, co, h = 4, 64, 96, 12
+    rng = np.random.default_rng(11)
+    x, wt = rnd(rng, n, ci, h, h), rnd(rng, co, ci, 1, 1, scale=ci ** -0.5)
+    tx, tw = dev(x, cuda), dev(wt, cuda)
+    base = torch.zeros(co * ci + 1, device=cuda)
+    tw_off = base[1:].view(co, ci, 1, 1)
+    tw_off.copy_(tw)
+    assert tw_off.data_ptr() % 16 == 4
+    try:
+        ops.set_conv_plan("fwd", x.shape, wt.shape, 1, 0, tile, 1)
+        y_off, y = ops.conv2d(tx, tw_off), ops.conv2d(tx, tw)
+    finally:
+        ops.clear_conv_plans()
+    assert torch.equal(y_off, y)
+    assert orc.rel_l2(host(y), orc.conv_fwd(x, wt, None, 1, 0)) <= TOL
+
+
 BWD_SHAPES = [
     (4, 512, 512, 2, 2, 3, 1, 1),   # ResNet-18 layer4: both GEMMs split K
     (3, 64, 128, 9, 9, 3, 2, 1),    # stride 2: grad-input stride phases
