@@ -20,7 +20,7 @@
 
 namespace omt {
 
-constexpr int kOptSlots = 24;    // tensors per launch
+constexpr int kOptSlots = 32;    // tensors per launch (the table: 2.2 KB of kernel arguments)
 constexpr int kOptChunk = 8192;  // elements per workgroup (256 threads x 8 float4)
 constexpr int kOptThreads = 256;
 
@@ -54,6 +54,7 @@ struct SgdTable {
   int first[kOptSlots + 1];
   int count;
 };
+static_assert(sizeof(AdamTable) + sizeof(SgdTable) < 4096, "the tables travel in the kernel arguments");
 struct SgdHyper {
   float lr;
   const float* lr_dev;
