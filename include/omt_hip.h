@@ -6,6 +6,8 @@
  *
  * Conventions
  *  - Tensors are dense NCHW float32 device pointers (weights [co][ci][ks][ks]); the caller makes inputs contiguous.
+ *    Pointers and workspaces need 4-byte alignment only; 16-byte-aligned ones take the vector paths (direct-to-LDS
+ *    filter loads, float4 epilogue stores).
  *  - Every compute entry point is asynchronous on `stream` (a hipStream_t; NULL = the HIP null stream, as in the
  *    HIP runtime API) and returns an omt_status. OMT_UNSUPPORTED means "this geometry is not covered" (the operator layer then records a
  *    fallback, as the reference's NEED() does); any other non-zero status carries a message in omt_last_error().
