@@ -87,6 +87,7 @@ struct GatherArgs {
   int kslice;            // K elements per grid-z slice (a multiple of the K-block)
   int tpw;               // conv1x1_stream_kernel: pixel tiles per workgroup
   int rows;              // row epilogue: one phase written in place, no split K, OH OW % 4 == 0, y 16-byte aligned
+  int d2s, d2s_ci;       // grad input as one super-pixel GEMM: its stride (0: off) and the grad-input channels
   int wdirect;           // grad input, channel-major: A[ci][(co, a', b')] read from w[co][ci][ks][ks] (no re-pack)
   int ks, s;             //   the filter size and stride for that read
   float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
@@ -128,6 +129,43 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
           yb[(int64_t)p * yhw] = v;
         }
       }
+  }
+}
+
+// Grad input as one super-pixel GEMM (a.d2s = stride s > 1, a.d2s_ci = C channels): GEMM row p = (py s + px) C + c
+// at pixel (n, i, j) of the ceil(H / s) x ceil(W / s) grid is grad input (n, c, s i + py, s j + px), stored where it
+// lies inside the image (y: [N][C][YH][YW]). No split K (the host plans one slice).
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void d2s_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                             int q0, int p0, int wp, int wq, int lane) {
+  const int S = a.d2s, CI = a.d2s_ci, grp = lane >> 4;
+  const int64_t yhw = (int64_t)a.YH * a.YW;
+  int64_t off[TI][4];  // c YH YW + py YW + px of each row this lane stores, -1 past the GEMM's rows
+  int dy[TI][4], dx[TI][4];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
+      const int c = p % CI, f = p / CI, py = f / S, px = f - py * S;
+      off[i][r4] = p < a.P ? c * yhw + (int64_t)py * a.YW + px : -1;
+      dy[i][r4] = py;
+      dx[i][r4] = px;
+    }
+  const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
+    if (q >= ph.Q) continue;
+    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+    const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+    const int y0 = (int)oy * S, x0 = (int)ox * S;
+    float* const yb = a.y + (int64_t)n * CI * yhw + (int64_t)y0 * a.YW + x0;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        if (off[i][r4] >= 0 && y0 + dy[i][r4] < a.YH && x0 + dx[i][r4] < a.YW) yb[off[i][r4]] = acc[i][j][r4];
   }
 }
 
@@ -415,7 +453,9 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   }
 
   static_assert(4 * row_epi_floats<WQ>() <= gather_lds_floats<BP, BQ, BK>(), "row epilogue fits the tile's LDS");
-  if (a.rows)  // the K loop's last barrier: no wave reads LDS
+  if (a.d2s)
+    d2s_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
+  else if (a.rows)  // the K loop's last barrier: no wave reads LDS
     row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, lds + wave * row_epi_floats<WQ>());
   else
     gather_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
@@ -1109,6 +1149,32 @@ __global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs 
   }
 }
 
+// Super-pixel grad-input filter W'[p = (py s + px) CI + c][k]: k = (dy L + dx) CO + co (tap-major) or
+// co L L + dy L + dx, the L x L window of gy rows i + dy - PH around grid pixel i. Phase (py, px) reaches gy row
+// i + qy - a' through filter row ky0 + s a' (a' < jy; ky0 = (py + pad) mod s, qy = (py + pad - ky0) / s), so window row
+// dy holds a' = qy - (dy - PH), and zero where no tap of the phase lands.
+struct PackD2S {
+  const float* w;
+  float* out;
+  int CO, CI, KS, S, PAD, L, PH, tap_major;
+};
+__global__ void __launch_bounds__(256) pack_d2s_weights_kernel(const PackD2S a) {
+  const int LL = a.L * a.L, K = a.CO * LL, total = a.S * a.S * a.CI * K;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const int p = e / K, k = e - p * K;
+    const int c = p % a.CI, f = p / a.CI, py = f / a.S, px = f - py * a.S;
+    const int co = a.tap_major ? k % a.CO : k / LL, tap = a.tap_major ? k / a.CO : k % LL;
+    const int dy = tap / a.L, dx = tap - dy * a.L;
+    const int ky0 = (py + a.PAD) % a.S, kx0 = (px + a.PAD) % a.S;
+    const int jy = ky0 < a.KS ? (a.KS - ky0 + a.S - 1) / a.S : 0, jx = kx0 < a.KS ? (a.KS - kx0 + a.S - 1) / a.S : 0;
+    const int ay = (py + a.PAD - ky0) / a.S - (dy - a.PH), ax = (px + a.PAD - kx0) / a.S - (dx - a.PH);
+    float v = 0.f;
+    if (ay >= 0 && ay < jy && ax >= 0 && ax < jx)
+      v = a.w[((co * a.CI + c) * a.KS + ky0 + a.S * ay) * a.KS + kx0 + a.S * ax];
+    a.out[e] = v;
+  }
+}
+
 // Forward weights in tap-major order: wt[co][ky][kx][ci] = w[co][ci][ky][kx].
 __global__ void __launch_bounds__(256) pack_tapmajor_kernel(const float* __restrict__ w, float* __restrict__ out,
                                                             int co, int ci, int kk) {
@@ -1286,7 +1352,7 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 // pixels stay inside one image and are 16-byte aligned.
 static bool rows_ok(const GatherArgs& a, bool split) {
   const Phase& p = a.ph[0];
-  return !split && a.nphase == 1 && p.os == 1 && p.oy0 == 0 && p.ox0 == 0 && a.YH == p.OH && a.YW == p.OW &&
+  return !split && !a.d2s && a.nphase == 1 && p.os == 1 && p.oy0 == 0 && p.ox0 == 0 && a.YH == p.OH && a.YW == p.OW &&
          (p.OH * p.OW) % 4 == 0 && (uintptr_t)a.y % 16 == 0;
 }
 // Completes a gather launch's arguments for its plan: K slice length and, split over K, the partials `part` (the
@@ -1356,7 +1422,7 @@ static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t 
   }
   if (a.bn_mean)
     gather_dispatch<kGeneric, true>(pl.tile % kNGather, a, grid, s);
-  else if (gather_uses_tap_major(a, pl) && gtile(pl.tile).ns && (uintptr_t)a.w % 16 == 0)
+  else if (gather_uses_tap_major(a, pl) && gtile(pl.tile).ns && (uintptr_t)a.w % 16 == 0 && !a.d2s)
     gather_dl_dispatch(pl.tile % kNGather, a, grid, s);
   else if (gather_uses_tap_major(a, pl))
     gather_dispatch<kTapMajor, false>(pl.tile % kNGather, a, grid, s);
@@ -1575,20 +1641,78 @@ static int dgrad_phases(const omt_conv_geo* g, GatherArgs& a, PackArgs& pk, int6
   return woff;
 }
 
+// Grad input as one super-pixel GEMM. With few grad-input channels C and a stride s > 1, each of the s^2 stride phases
+// fills only C of an MFMA tile's 16 rows. Side by side, the phases' s^2 C rows over one L x L window of gy (the union
+// of every phase's taps, zero where a phase has none) fill whole tiles, for L^2 / (taps of a phase) times the FLOPs:
+// AlexNet conv1's grad input (C = 3, s = 4, 11 x 11) becomes 48 rows over a 4 x 4 window, 2.2x the FLOPs on 16x the
+// rows per tile.
+static bool dgrad_d2s(const omt_conv_geo* g) {
+  return g->stride > 1 && g->ci <= 4 && g->stride * g->stride * g->ci <= 64;
+}
+// The window: gy rows i + r for r in [lo, hi] over all phases (phase py reaches rows i + qy - a', a' < jy); L rows
+// starting at PH = -lo above the grid row.
+static void d2s_window(const omt_conv_geo* g, int& L, int& PH) {
+  const int s = (int)g->stride, ks = (int)g->ks, pad = (int)g->pad;
+  int lo = 1 << 30, hi = -(1 << 30);
+  for (int py = 0; py < s; ++py) {
+    const int ky0 = (py + pad) % s;
+    if (ky0 >= ks) continue;
+    const int jy = (int)cdiv(ks - ky0, s), qy = (py + pad - ky0) / s;
+    lo = std::min(lo, qy - jy + 1);
+    hi = std::max(hi, qy);
+  }
+  L = hi - lo + 1;
+  PH = -lo;
+}
+static void dgrad_d2s_phase(const omt_conv_geo* g, GatherArgs& a, int64_t& maxq) {
+  const int s = (int)g->stride;
+  int L = 1, PH = 0;
+  d2s_window(g, L, PH);
+  Phase& p = a.ph[0];
+  p = Phase{};
+  p.KH = p.KW = L;
+  p.S = 1;
+  p.PH = p.PW = PH;
+  p.OH = (int)cdiv(g->ih, s);
+  p.OW = (int)cdiv(g->iw, s);
+  p.K = (int)g->co * L * L;
+  p.Q = (int)g->n * p.OH * p.OW;
+  p.os = 1;
+  p.div_ohw = make_fastdiv((uint32_t)(p.OH * p.OW));
+  p.div_ow = make_fastdiv((uint32_t)p.OW);
+  p.div_kk = make_fastdiv((uint32_t)(L * L));
+  p.div_kw = make_fastdiv((uint32_t)L);
+  a.nphase = 1;
+  maxq = p.Q;
+}
+
 // Grad-input workspace: the per-phase packed filters, then, 256-byte aligned, the split-K partials.
 static GatherPlan dgrad_plan(const omt_conv_geo* g) {
   GatherArgs a{};
   PackArgs pk{};
   int64_t maxq = 0, maxk = 0;
-  dgrad_phases(g, a, pk, maxq);
-  for (int i = 0; i < a.nphase; ++i) maxk = a.ph[i].K > maxk ? a.ph[i].K : maxk;
   omt_conv_plan cp;
   const bool have = cached_plan(OMT_DIR_DGRAD, g, &cp);
+  if (dgrad_d2s(g)) {  // one slice: the super-pixel epilogue scatters final values
+    dgrad_d2s_phase(g, a, maxq);
+    GatherPlan pl = gather_plan(g->stride * g->stride * g->ci, maxq, a.ph[0].K, 1, have ? &cp : nullptr);
+    pl.slices = 1;
+    pl.kslice = cdiv(a.ph[0].K, gtile(pl.tile).bk) * gtile(pl.tile).bk;
+    return pl;
+  }
+  dgrad_phases(g, a, pk, maxq);
+  for (int i = 0; i < a.nphase; ++i) maxk = a.ph[i].K > maxk ? a.ph[i].K : maxk;
   return gather_plan(g->ci, maxq, maxk, a.nphase, have ? &cp : nullptr);
 }
 
-// Grad input re-packs its filter for the tap-major order only; the channel-major order reads w directly.
+// Grad input re-packs its filter for the tap-major order only (the channel-major order reads w directly), and always
+// in the super-pixel form.
 static size_t dgrad_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
+  if (dgrad_d2s(g)) {
+    int L = 1, PH = 0;
+    d2s_window(g, L, PH);
+    return (size_t)(g->stride * g->stride * g->ci * g->co * L * L) * sizeof(float);
+  }
   if (gcm(pl.tile) || !gather_tap_major(g->co, false, gtile(pl.tile).bk)) return 0;
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
@@ -1612,10 +1736,31 @@ static int dgrad_prepare(const omt_conv_geo* g, const float* gy, const float* w,
                          hipStream_t s, GatherArgs& a, GatherPlan& pl, int64_t& maxq, float*& part) {
   PackArgs pk{};
   a = GatherArgs{};
-  const int packed = dgrad_phases(g, a, pk, maxq);
+  const bool d2s = dgrad_d2s(g);
+  const int packed = d2s ? 0 : dgrad_phases(g, a, pk, maxq);
   pl = dgrad_plan(g);
   const size_t pack = dgrad_pack_bytes(g, pl);
-  if (pack) {
+  if (d2s) {
+    dgrad_d2s_phase(g, a, maxq);
+    PackD2S pd{};
+    pd.w = w;
+    pd.out = (float*)workspace;
+    pd.CO = (int)g->co;
+    pd.CI = (int)g->ci;
+    pd.KS = (int)g->ks;
+    pd.S = (int)g->stride;
+    pd.PAD = (int)g->pad;
+    pd.L = a.ph[0].KH;
+    pd.PH = a.ph[0].PH;
+    pd.tap_major = !gcm(pl.tile) && gather_tap_major(g->co, false, gtile(pl.tile).bk);
+    const int64_t total = (int64_t)(pack / sizeof(float));
+    hipLaunchKernelGGL(pack_d2s_weights_kernel, dim3(grid1d(total, 256, 4096)), dim3(256), 0, s, pd);
+    if (int st = launch_check("pack_d2s_weights_kernel")) return st;
+    a.w = (const float*)workspace;
+    a.w_bytes = (uint32_t)pack;
+    a.d2s = (int)g->stride;
+    a.d2s_ci = (int)g->ci;
+  } else if (pack) {
     pk.w = w;
     pk.out = (float*)workspace;
     pk.CO = (int)g->co;
@@ -1640,7 +1785,7 @@ static int dgrad_prepare(const omt_conv_geo* g, const float* gy, const float* w,
   a.C = (int)g->co;
   a.H = (int)g->oh;
   a.W = (int)g->ow;
-  a.P = (int)g->ci;
+  a.P = (int)(d2s ? g->stride * g->stride * g->ci : g->ci);  // GEMM rows
   a.YH = (int)g->ih;
   a.YW = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
@@ -1935,6 +2080,11 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
   int64_t P, Q, K, z = 1, plane;
   if (dir == OMT_DIR_FWD) {
     P = g->co, Q = g->n * g->oh * g->ow, K = g->ci * g->ks * g->ks, plane = g->n * g->co * g->oh * g->ow;
+  } else if (dgrad_d2s(g)) {  // the super-pixel GEMM, one slice
+    GatherArgs a{};
+    dgrad_d2s_phase(g, a, Q);
+    K = a.ph[0].K;
+    P = g->stride * g->stride * g->ci, plane = g->n * g->ci * g->ih * g->iw;
   } else {
     GatherArgs a{};
     PackArgs pk{};
@@ -1943,6 +2093,7 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     for (int i = 0; i < a.nphase; ++i) K = std::max<int64_t>(K, a.ph[i].K);
     P = g->ci, z = a.nphase, plane = g->n * g->ci * g->ih * g->iw;
   }
+  const bool one_slice = dir == OMT_DIR_DGRAD && dgrad_d2s(g);
   // the 1x1 streaming tile: one 1x1 stride-1 unpadded phase with whole K-blocks, tap-major order, no split
   const bool stream_geo = g->ks == 1 && g->stride == 1 && g->pad == 0 && K % 16 == 0 && (g->ih * g->iw) % 4 == 0;
   for (int t = 0; t < ntile; ++t) {
@@ -1959,7 +2110,7 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     int64_t last = -1;
     for (int sc : {1, 2, 3, 4, 8, 16, 32, 64}) {
       const int64_t kb = cdiv(nkb, sc), eff = cdiv(nkb, kb);
-      if (sc > 1 && kb < 2) break;
+      if (sc > 1 && (kb < 2 || one_slice)) break;
       if (full && sc > 1 && (sc > 4 || tiles >= 16 * kCUs || kb < 8)) break;
       if (!full && sc == 3) continue;
       if (eff == last || (eff > 1 && eff * plane * 4 > ((int64_t)512 << 20))) continue;

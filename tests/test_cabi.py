@@ -72,14 +72,22 @@ def test_host_validation_statuses():
     L.omt_conv_clear_plans()
     g.oh = 99  # inconsistent geometry
     assert L.omt_conv_wgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
-    g = _lib.conv_geo(2, 3, 16, 8, 8, 3, 2, 1)  # tap-major grad input (C_out % 16 == 0) re-packs its filter
+    g = _lib.conv_geo(2, 5, 16, 8, 8, 3, 2, 1)  # tap-major grad input (C_out % 16 == 0) re-packs its filter
     assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_OK
     assert L.omt_conv_dgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID  # no workspace
-    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 16 * 3 * 3 * 3 * 4
+    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 16 * 5 * 3 * 3 * 4
     n_tiles = L.omt_conv_num_tiles(_lib.OMT_DIR_DGRAD)  # the channel-major twin of tile 0 reads w directly
     assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(n_tiles // 2, 1))) \
         == _lib.OMT_OK
     assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 0
+    # 3 grad-input channels at stride 2: one super-pixel GEMM of 2 x 2 phases x 3 channels over the 2 x 2 window of gy
+    # the 3 x 3 filter reaches (phase rows 0 and 1 use gy rows i and i, i + 1); its filter is re-packed in both K
+    # orders and it runs as one K slice whatever the plan asks
+    g3 = _lib.conv_geo(2, 3, 16, 8, 8, 3, 2, 1)
+    for plan in ((0, 1), (n_tiles // 2, 1), (5, 4)):
+        assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g3), ctypes.byref(_lib.ConvPlan(*plan))) \
+            == _lib.OMT_OK
+        assert L.omt_conv_dgrad_workspace(ctypes.byref(g3)) == 4 * 3 * 16 * 2 * 2 * 4, plan
     L.omt_conv_clear_plans()
     with pytest.raises(_lib.Unsupported):
         _lib.check(_lib.OMT_UNSUPPORTED)
