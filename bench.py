@@ -657,7 +657,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
-              "its batch share; see the sharding note in the design document). Run with --gpus 1.", file=sys.stderr)
+              "its batch share, the weight gradients summed over the GPUs afterwards). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
