@@ -938,7 +938,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     // K-block b is loaded into register set b % PF, PF blocks ahead: while the MFMAs of b run, the loads of b + 1
     // .. b + PF are in flight. The loads are issued on every step (past kend they load zeros): behind a branch, the
     // compiler's wait before the LDS store of block b + 1 cannot count the later blocks' loads as issued after it.
-    static_assert(PF == 2 || PF == 4, "register sets");
+    static_assert(PF == 2, "two register sets");
 #pragma unroll
     for (int b = 0; b < PF; ++b) gload(kbeg + b * BK, b);
     auto step = [&](int k0, auto setc) {
@@ -952,10 +952,6 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     for (int k0 = kbeg; k0 < kend; k0 += PF * BK) {
       step(k0, std::integral_constant<int, 0>{});
       if (k0 + BK < kend) step(k0 + BK, std::integral_constant<int, 1>{});
-      if constexpr (PF == 4) {
-        if (k0 + 2 * BK < kend) step(k0 + 2 * BK, std::integral_constant<int, 2>{});
-        if (k0 + 3 * BK < kend) step(k0 + 3 * BK, std::integral_constant<int, 3>{});
-      }
     }
   }
 
