@@ -52,6 +52,9 @@ CONV_SHAPES = [
     (4, 3, 64, 64, 64, 7, 2, 3), (4, 64, 128, 16, 16, 3, 2, 1), (4, 64, 128, 16, 16, 1, 2, 0),  # ResNet-18 stem/down
     (4, 512, 512, 2, 2, 3, 1, 1),                        # ResNet-18 layer4 at 64x64 input
     (3, 7, 9, 13, 11, 3, 3, 2), (2, 5, 3, 9, 17, 4, 4, 4), (2, 17, 33, 10, 7, 2, 1, 0),   # ragged / odd
+    # grad input as one super-pixel GEMM (C_in <= 4 at stride > 1): one input channel, 4 x 4 phases x 4 channels
+    # (64 rows), stride 3 on a ragged non-square image
+    (2, 1, 16, 19, 23, 3, 2, 1), (2, 4, 32, 18, 18, 4, 4, 0), (3, 3, 8, 17, 13, 5, 3, 2),
 ]
 
 
@@ -223,6 +226,7 @@ BWD_SHAPES = [
     (2, 24, 20, 7, 7, 3, 1, 1),     # channel-major K order (C % 16 != 0)
     (2, 32, 48, 6, 5, 1, 1, 0),     # 1x1
     (2, 64, 64, 8, 8, 1, 2, 0),     # 1x1 stride 2: phases no tap reaches
+    (2, 3, 64, 20, 20, 3, 2, 1),    # super-pixel grad input (3 channels, stride 2): one slice whatever the plan asks
 ]
 
 
