@@ -752,6 +752,7 @@ def main():
     layer_tflops = {name: {d: round(layer_flops[name] / (sum(v) / len(v) / 1e3) / 1e12, 1) for d, v in dd.items()}
                     for name, dd in per_layer.items()}
 
+    traffic = traffic_per_launch(args.workload)
     out = {
         "metric": "conv fwd+dgrad+wgrad fp32 TFLOP/s (% of fp32-MFMA peak); ResNet-18 b32 train ms/step",
         "value": round(value, 3),
@@ -771,9 +772,12 @@ def main():
                                 "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad"),
                    "gflop_per_step": round(step_flops / 1e9, 2), "layout": "NCHW"},
         "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
-        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel / conv1x1_stream_kernel (forward launches)", "bound": "mfma",
-                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4), "traffic": traffic_per_launch(args.workload),
+        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel / conv1x1_stream_kernel (forward launches)",
+                     "bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4),
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_algorithmic_bytes": traffic["algorithmic_bytes"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
                      "avg_launch_ms": round(avg_launch_ms, 4),
                      "flop_per_launch_avg": round(sum(fwd_flops) / len(fwd_flops))},
         "per_direction": per_dir,
