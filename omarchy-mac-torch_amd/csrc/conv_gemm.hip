@@ -87,7 +87,8 @@ struct GatherArgs {
   int kslice;            // K elements per grid-z slice (a multiple of the K-block)
   int tpw;               // conv1x1_stream_kernel: pixel tiles per workgroup
   int rows;              // row epilogue: one phase written in place, no split K, OH OW % 4 == 0, y 16-byte aligned
-  int d2s, d2s_ci;       // grad input as one super-pixel GEMM: its stride (0: off) and the grad-input channels
+  int d2s, d2s_ci;       // grad input as one super-pixel GEMM: its stride (0: off) and the grad-input channels;
+  int d2s_h, d2s_w;      //   the grad-input image (YH x YW is then the super-pixel grid, as its K-split partials)
   int wdirect;           // grad input, channel-major: A[ci][(co, a', b')] read from w[co][ci][ks][ks] (no re-pack)
   int ks, s;             //   the filter size and stride for that read
   float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
@@ -134,13 +135,14 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
 
 // Grad input as one super-pixel GEMM (a.d2s = stride s > 1, a.d2s_ci = C channels): GEMM row p = (py s + px) C + c
 // at pixel (n, i, j) of the ceil(H / s) x ceil(W / s) grid is grad input (n, c, s i + py, s j + px), stored where it
-// lies inside the image (y: [N][C][YH][YW]). No split K (the host plans one slice).
+// lies inside the image (y: [N][C][d2s_h][d2s_w]). Split over K, the raw partials take the gather epilogue's
+// [N][rows][grid] layout and the slice sum scatters.
 template <int TI, int TJ, int WP, int WQ>
 __device__ __forceinline__ void d2s_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
                                              int q0, int p0, int wp, int wq, int lane) {
-  const int S = a.d2s, CI = a.d2s_ci, grp = lane >> 4;
-  const int64_t yhw = (int64_t)a.YH * a.YW;
-  int64_t off[TI][4];  // c YH YW + py YW + px of each row this lane stores, -1 past the GEMM's rows
+  const int S = a.d2s, CI = a.d2s_ci, grp = lane >> 4, IH = a.d2s_h, IW = a.d2s_w;
+  const int64_t yhw = (int64_t)IH * IW;
+  int64_t off[TI][4];  // c IH IW + py IW + px of each row this lane stores, -1 past the GEMM's rows
   int dy[TI][4], dx[TI][4];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
@@ -148,7 +150,7 @@ __device__ __forceinline__ void d2s_epilogue(const GatherArgs& a, const Phase& p
     for (int r4 = 0; r4 < 4; ++r4) {
       const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
       const int c = p % CI, f = p / CI, py = f / S, px = f - py * S;
-      off[i][r4] = p < a.P ? c * yhw + (int64_t)py * a.YW + px : -1;
+      off[i][r4] = p < a.P ? c * yhw + (int64_t)py * IW + px : -1;
       dy[i][r4] = py;
       dx[i][r4] = px;
     }
@@ -160,12 +162,12 @@ __device__ __forceinline__ void d2s_epilogue(const GatherArgs& a, const Phase& p
     const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
     const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
     const int y0 = (int)oy * S, x0 = (int)ox * S;
-    float* const yb = a.y + (int64_t)n * CI * yhw + (int64_t)y0 * a.YW + x0;
+    float* const yb = a.y + (int64_t)n * CI * yhw + (int64_t)y0 * IW + x0;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
-        if (off[i][r4] >= 0 && y0 + dy[i][r4] < a.YH && x0 + dx[i][r4] < a.YW) yb[off[i][r4]] = acc[i][j][r4];
+        if (off[i][r4] >= 0 && y0 + dy[i][r4] < IH && x0 + dx[i][r4] < IW) yb[off[i][r4]] = acc[i][j][r4];
   }
 }
 
@@ -453,7 +455,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   }
 
   static_assert(4 * row_epi_floats<WQ>() <= gather_lds_floats<BP, BQ, BK>(), "row epilogue fits the tile's LDS");
-  if (a.d2s)
+  if (a.d2s && !a.part)
     d2s_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
   else if (a.rows)  // the K loop's last barrier: no wave reads LDS
     row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, lds + wave * row_epi_floats<WQ>());
@@ -1073,6 +1075,7 @@ struct GatherSum {
   int relu;
   bool vec4;
   int64_t blocks;  // workgroups of its launch
+  int d2s, d2s_ci, img_h, img_w, grid_w;  // super-pixel grad input: scatter [N][s^2 C][grid] to [N][C][img]
 };
 template <int VEC>
 __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64_t nb) {
@@ -1081,6 +1084,16 @@ __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64
   for (int64_t i = b0 * blockDim.x + threadIdx.x; i < nv; i += nb * blockDim.x) {
     float v[VEC];
     sum_slices<VEC>(reinterpret_cast<const T*>(r.part), nv, i, r.slices, v);
+    if (VEC == 1 && r.d2s) {  // partials below 2 GiB: 32-bit index arithmetic
+      const int e = (int)i, pl = (int)r.plane, rows = r.P * pl;
+      const int n = e / rows, p = (e - n * rows) / pl, q = e - n * rows - p * pl;
+      const int oy = q / r.grid_w, ox = q - oy * r.grid_w;
+      const int c = p % r.d2s_ci, f = p / r.d2s_ci, py = f / r.d2s, px = f - py * r.d2s;
+      const int row = oy * r.d2s + py, col = ox * r.d2s + px;
+      if (row < r.img_h && col < r.img_w)
+        r.y[((int64_t)(n * r.d2s_ci + c) * r.img_h + row) * r.img_w + col] = v[0];
+      continue;
+    }
     const float b = r.bias ? r.bias[(i * VEC / r.plane) % r.P] : 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -1395,7 +1408,12 @@ static GatherSum gather_sum_of(const GatherArgs& a, const GatherPlan& pl) {
   r.P = a.P;
   r.bias = a.bias;
   r.relu = a.relu;
-  r.vec4 = r.plane % 4 == 0 && (uintptr_t)a.y % 16 == 0;
+  r.vec4 = r.plane % 4 == 0 && (uintptr_t)a.y % 16 == 0 && !a.d2s;
+  r.d2s = a.d2s;
+  r.d2s_ci = a.d2s_ci;
+  r.img_h = a.d2s_h;
+  r.img_w = a.d2s_w;
+  r.grid_w = a.ph[0].OW;
   r.blocks = grid1d(r.vec4 ? r.total / 4 : r.total, 256, 8192);
   return r;
 }
@@ -1689,12 +1707,9 @@ static GatherPlan dgrad_plan(const omt_conv_geo* g) {
   int64_t maxq = 0, maxk = 0;
   omt_conv_plan cp;
   const bool have = cached_plan(OMT_DIR_DGRAD, g, &cp);
-  if (dgrad_d2s(g)) {  // one slice: the super-pixel epilogue scatters final values
+  if (dgrad_d2s(g)) {
     dgrad_d2s_phase(g, a, maxq);
-    GatherPlan pl = gather_plan(g->stride * g->stride * g->ci, maxq, a.ph[0].K, 1, have ? &cp : nullptr);
-    pl.slices = 1;
-    pl.kslice = cdiv(a.ph[0].K, gtile(pl.tile).bk) * gtile(pl.tile).bk;
-    return pl;
+    return gather_plan(g->stride * g->stride * g->ci, maxq, a.ph[0].K, 1, have ? &cp : nullptr);
   }
   dgrad_phases(g, a, pk, maxq);
   for (int i = 0; i < a.nphase; ++i) maxk = a.ph[i].K > maxk ? a.ph[i].K : maxk;
@@ -1717,7 +1732,10 @@ OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
   if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
   const GatherPlan pl = dgrad_plan(g);
   const size_t pack = dgrad_pack_bytes(g, pl);
-  return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * g->ci * g->ih * g->iw) * sizeof(float) : pack;
+  // the super-pixel form keeps its partials on the ceil(ih / s) x ceil(iw / s) grid, s^2 ci rows
+  const int64_t s = g->stride, plane = dgrad_d2s(g) ? s * s * g->ci * cdiv(g->ih, s) * cdiv(g->iw, s)
+                                                    : g->ci * g->ih * g->iw;
+  return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * plane) * sizeof(float) : pack;
 }
 
 static int geo_check(const omt_conv_geo* g, const char* fn) {
@@ -1782,8 +1800,10 @@ static int dgrad_prepare(const omt_conv_geo* g, const float* gy, const float* w,
   a.H = (int)g->oh;
   a.W = (int)g->ow;
   a.P = (int)(d2s ? g->stride * g->stride * g->ci : g->ci);  // GEMM rows
-  a.YH = (int)g->ih;
-  a.YW = (int)g->iw;
+  a.YH = d2s ? a.ph[0].OH : (int)g->ih;  // super-pixel form: the grid (its partials' plane); the image below
+  a.YW = d2s ? a.ph[0].OW : (int)g->iw;
+  a.d2s_h = (int)g->ih;
+  a.d2s_w = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
   part = workspace ? (float*)((char*)workspace + align256(pack)) : nullptr;
   return OMT_OK;
@@ -2076,11 +2096,11 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
   int64_t P, Q, K, z = 1, plane;
   if (dir == OMT_DIR_FWD) {
     P = g->co, Q = g->n * g->oh * g->ow, K = g->ci * g->ks * g->ks, plane = g->n * g->co * g->oh * g->ow;
-  } else if (dgrad_d2s(g)) {  // the super-pixel GEMM, one slice
+  } else if (dgrad_d2s(g)) {  // the super-pixel GEMM
     GatherArgs a{};
     dgrad_d2s_phase(g, a, Q);
     K = a.ph[0].K;
-    P = g->stride * g->stride * g->ci, plane = g->n * g->ci * g->ih * g->iw;
+    P = g->stride * g->stride * g->ci, plane = P * Q;
   } else {
     GatherArgs a{};
     PackArgs pk{};
@@ -2089,7 +2109,6 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     for (int i = 0; i < a.nphase; ++i) K = std::max<int64_t>(K, a.ph[i].K);
     P = g->ci, z = a.nphase, plane = g->n * g->ci * g->ih * g->iw;
   }
-  const bool one_slice = dir == OMT_DIR_DGRAD && dgrad_d2s(g);
   // the 1x1 streaming tile: one 1x1 stride-1 unpadded phase with whole K-blocks, tap-major order, no split
   const bool stream_geo = g->ks == 1 && g->stride == 1 && g->pad == 0 && K % 16 == 0 && (g->ih * g->iw) % 4 == 0;
   for (int t = 0; t < ntile; ++t) {
@@ -2106,7 +2125,7 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     int64_t last = -1;
     for (int sc : {1, 2, 3, 4, 8, 16, 32, 64}) {
       const int64_t kb = cdiv(nkb, sc), eff = cdiv(nkb, kb);
-      if (sc > 1 && (kb < 2 || one_slice)) break;
+      if (sc > 1 && kb < 2) break;
       if (full && sc > 1 && (sc > 4 || tiles >= 16 * kCUs || kb < 8)) break;
       if (!full && sc == 3) continue;
       if (eff == last || (eff > 1 && eff * plane * 4 > ((int64_t)512 << 20))) continue;

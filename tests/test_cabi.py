@@ -82,12 +82,13 @@ def test_host_validation_statuses():
     assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 0
     # 3 grad-input channels at stride 2: one super-pixel GEMM of 2 x 2 phases x 3 channels over the 2 x 2 window of gy
     # the 3 x 3 filter reaches (phase rows 0 and 1 use gy rows i and i, i + 1); its filter is re-packed in both K
-    # orders and it runs as one K slice whatever the plan asks
+    # orders, and split over K its partials hold the 12 rows on the 4 x 4 grid
     g3 = _lib.conv_geo(2, 3, 16, 8, 8, 3, 2, 1)
-    for plan in ((0, 1), (n_tiles // 2, 1), (5, 4)):
+    pack = 4 * 3 * 16 * 2 * 2 * 4
+    for plan, ws in (((0, 1), pack), ((n_tiles // 2, 1), pack), ((5, 4), pack + 4 * 2 * 12 * 4 * 4 * 4)):
         assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g3), ctypes.byref(_lib.ConvPlan(*plan))) \
             == _lib.OMT_OK
-        assert L.omt_conv_dgrad_workspace(ctypes.byref(g3)) == 4 * 3 * 16 * 2 * 2 * 4, plan
+        assert L.omt_conv_dgrad_workspace(ctypes.byref(g3)) == ws, plan
     L.omt_conv_clear_plans()
     with pytest.raises(_lib.Unsupported):
         _lib.check(_lib.OMT_UNSUPPORTED)

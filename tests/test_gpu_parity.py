@@ -220,13 +220,33 @@ def test_conv1x1_filter_used_in_place_off_16_bytes(cuda, ops, tile):
     assert orc.rel_l2(host(y), orc.conv_fwd(x, wt, None, 1, 0)) <= TOL
 
 
+@pytest.mark.parametrize("slices", [2, 3])
+def test_super_pixel_dgrad_split_k(cuda, ops, slices):
+    """The super-pixel grad input split over K: the slices' partials on the ceil(63 / 4)^2 grid are summed and
+    scattered to the 63 x 63 image (AlexNet conv1's shape), for two tiles."""
+    n, ci, co, h, ks, s, p = 3, 3, 8, 63, 11, 4, 2
+    rng = np.random.default_rng(slices + 40)
+    wt = rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
+    o = (h + 2 * p - ks) // s + 1
+    gy = rnd(rng, n, co, o, o)
+    x_shape = (n, ci, h, h)
+    ref = orc.conv_dgrad(gy, wt, x_shape, s, p)
+    try:
+        for tile in (4, 5):
+            ops.set_conv_plan("dgrad", x_shape, wt.shape, s, p, tile, slices)
+            gx = ops.conv2d_dgrad(dev(gy, cuda), dev(wt, cuda), x_shape, s, p)
+            assert orc.rel_l2(host(gx), ref) <= TOL, tile
+    finally:
+        ops.clear_conv_plans()
+
+
 BWD_SHAPES = [
     (4, 512, 512, 2, 2, 3, 1, 1),   # ResNet-18 layer4: both GEMMs split K
     (3, 64, 128, 9, 9, 3, 2, 1),    # stride 2: grad-input stride phases
     (2, 24, 20, 7, 7, 3, 1, 1),     # channel-major K order (C % 16 != 0)
     (2, 32, 48, 6, 5, 1, 1, 0),     # 1x1
     (2, 64, 64, 8, 8, 1, 2, 0),     # 1x1 stride 2: phases no tap reaches
-    (2, 3, 64, 20, 20, 3, 2, 1),    # super-pixel grad input (3 channels, stride 2): one slice whatever the plan asks
+    (2, 3, 64, 20, 20, 3, 2, 1),    # super-pixel grad input (3 channels, stride 2), split K summed by the scatter
 ]
 
 
