@@ -89,6 +89,11 @@ def test_host_validation_statuses():
         assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g3), ctypes.byref(_lib.ConvPlan(*plan))) \
             == _lib.OMT_OK
         assert L.omt_conv_dgrad_workspace(ctypes.byref(g3)) == ws, plan
+    # AlexNet conv1 (11 x 11, stride 4, pad 2): phase rows py = 0..3 reach gy rows i-2..i, i-1..i, i-1..i+1, i-1..i+1
+    # (ky0 = 2, 3, 0, 1), so the window is 4 x 4 and the filter 16 phases x 3 channels by 64 x 16 taps
+    g1 = _lib.conv_geo(16, 3, 64, 224, 224, 11, 4, 2)
+    assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g1), ctypes.byref(_lib.ConvPlan(4, 1))) == _lib.OMT_OK
+    assert L.omt_conv_dgrad_workspace(ctypes.byref(g1)) == 16 * 3 * 64 * 4 * 4 * 4
     L.omt_conv_clear_plans()
     with pytest.raises(_lib.Unsupported):
         _lib.check(_lib.OMT_UNSUPPORTED)
