@@ -1,7 +1,7 @@
 """Benchmark of the convolution hot path on one MI355X (BASELINE metric: conv fwd+dgrad+wgrad fp32 TFLOP/s and % of
-fp32-MFMA peak).
+fp32-MFMA peak; ResNet-18 b32 train ms/step).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5|c1] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5|c1] [--no-cpu] [--no-models]
 
 One step = forward + grad-input + grad-weight of every conv layer of the workload, over one synthetic batch already
 resident in HBM:
@@ -11,14 +11,19 @@ resident in HBM:
   c1:           BASELINE config 1, AlexNet conv1 (16x3x224x224, 64x11x11, stride 4, pad 2). 6.747 GFLOP per step.
 FLOPs per direction = 2*N*K*OH*OW*C*R*S (never the padded or stride-phase-expanded work).
 
+The one JSON line also carries, as sub-objects, config 1's sweep (alexnet_conv1_b16) and the training steps of
+configs 2, 3 and 4 (plaincnn_b128, resnet18_b32, mobilenetv3_b32): device ms/step eager and replayed as a HIP graph,
+the same steps on PyTorch CPU fp32 from the same weights and data, the speed-up and the 5-step loss agreement.
+
 The roofline object reports the dominant kernel, the implicit-GEMM gather (conv_gather_kernel, its direct-to-LDS
 form conv_gather_dl_kernel, or the persistent 1x1 conv1x1_stream_kernel, whichever the tuned plan of each layer
-runs), from its forward launches: algorithmic FLOPs per launch over the
-launch's HIP-event duration, measured on the launch stream inside the timed steps. cpu_baseline times the CPU oracle
-(oracle/, a scalar-per-thread float64 restatement of the reference algorithm) on a bounded sample of the same
-workload; torch_cpu_baseline times PyTorch's CPU fp32 conv (the reference's CPU path) on a sample. Both are baselines,
-not targets. miopen_same_sweep times the same sweep through torch's own convolutions on the same GPU (MIOpen), the
-convolution a PyTorch-ROCm user gets without this library (--no-miopen skips it).
+runs), from its forward launches: algorithmic FLOPs per launch over the launch's HIP-event duration, measured on the
+launch stream inside the timed steps. cpu_baseline is the reference's CPU path, PyTorch CPU fp32 convolutions (the
+reference runs and checks these ops on PyTorch's CPU kernels), timed on a bounded sample of the same workload with
+every host core and, as the reference's README states its CPU numbers, with 4 threads; oracle_cpu_baseline times
+this repository's float64 CPU oracle (oracle/) on a smaller sample. Both are baselines, not targets.
+miopen_same_sweep times the same sweep through torch's own convolutions on the same GPU (MIOpen), the convolution a
+PyTorch-ROCm user gets without this library (--no-miopen skips it).
 """
 
 import argparse
@@ -70,7 +75,7 @@ def cpu_info():
     return model
 
 
-def oracle_baseline(layers, budget_s=20.0):
+def oracle_baseline(layers, budget_s=8.0):
     """The CPU oracle on a bounded sample: each layer at batch 1, fwd+dgrad+wgrad, repeated until ~budget_s."""
     import numpy as np
 
@@ -101,36 +106,55 @@ def oracle_baseline(layers, budget_s=20.0):
                       f"{flops / 1e9:.1f} GFLOP in {secs:.1f} s, float64 OpenMP oracle, {cpu_info()}"}
 
 
-def torch_cpu_baseline(layers, batch, threads):
-    """PyTorch CPU fp32 conv fwd + convolution_backward on the same layer shapes at a reduced batch."""
+def torch_cpu_sweep(layers, batch, threads, secs_per_layer):
+    """PyTorch CPU fp32 conv2d + convolution_backward (grad input and grad weight) over the layers at `batch`, each
+    layer repeated for about secs_per_layer after one untimed pass. Returns (TFLOP/s, GFLOP timed, seconds)."""
     import torch
 
+    prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     flops = secs = 0.0
-    for (name, n, c, k, h, ks, s, p) in layers:
-        scale = (c * ks * ks) ** -0.5
-        x = torch.randn((batch, c, h, h), generator=g)
-        w = torch.randn((k, c, ks, ks), generator=g) * scale
-        o = out_size(h, ks, s, p)
-        gy = torch.randn((batch, k, o, o), generator=g) * scale
+    try:
+        for (name, n, c, k, h, ks, s, p) in layers:
+            b = min(batch, n)
+            scale = (c * ks * ks) ** -0.5
+            x = torch.randn((b, c, h, h), generator=g)
+            w = torch.randn((k, c, ks, ks), generator=g) * scale
+            o = out_size(h, ks, s, p)
+            gy = torch.randn((b, k, o, o), generator=g) * scale
 
-        def step():
-            torch.nn.functional.conv2d(x, w, None, s, p)
-            torch.ops.aten.convolution_backward(gy, x, w, None, [s, s], [p, p], [1, 1], False, [0, 0], 1,
-                                                [True, True, False])
+            def step():
+                torch.nn.functional.conv2d(x, w, None, s, p)
+                torch.ops.aten.convolution_backward(gy, x, w, None, [s, s], [p, p], [1, 1], False, [0, 0], 1,
+                                                    [True, True, False])
 
-        step()
-        reps = 0
-        t0 = time.time()
-        while reps < 2 or time.time() - t0 < 0.5:
             step()
-            reps += 1
-        secs += (time.time() - t0) / reps
-        flops += 3 * flops_dir(batch, c, k, h, ks, s, p)
-    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads,
-            "sample": f"PyTorch {torch.__version__} CPU fp32 conv fwd+convolution_backward over the workload's layers "
-                      f"at batch {batch}, {cpu_info()}"}
+            reps = 0
+            t0 = time.perf_counter()
+            while reps < 2 or time.perf_counter() - t0 < secs_per_layer:
+                step()
+                reps += 1
+            secs += time.perf_counter() - t0
+            flops += reps * 3 * flops_dir(b, c, k, h, ks, s, p)
+    finally:
+        torch.set_num_threads(prev)
+    return flops / secs / 1e12, flops / 1e9, secs
+
+
+def torch_cpu_baseline(layers, batch, secs_per_layer=0.8):
+    """cpu_baseline: the reference's CPU path (PyTorch CPU fp32 convolutions) on a bounded sample of the workload, with
+    every host core (len(sched_getaffinity)) and with 4 threads (the reference's README convention)."""
+    import torch
+
+    threads = len(os.sched_getaffinity(0))
+    value, gf, secs = torch_cpu_sweep(layers, batch, threads, secs_per_layer)
+    v4, gf4, secs4 = torch_cpu_sweep(layers, batch, 4, secs_per_layer)
+    return {"value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"PyTorch {torch.__version__} CPU fp32 conv2d + convolution_backward (grad input, grad weight), "
+                      f"every layer of the workload at batch {batch}, {gf:.0f} GFLOP in {secs:.1f} s; {cpu_info()}",
+            "at_4_threads": {"value": round(v4, 4), "unit": "TFLOP/s", "cores": 4,
+                             "sample": f"the same at 4 threads, {gf4:.0f} GFLOP in {secs4:.1f} s"}}
 
 
 GATHER_KERNELS = ("conv_gather_kernel", "conv_gather_dl_kernel", "conv1x1_stream_kernel")
@@ -483,26 +507,57 @@ def pmc_probe(layers, dev):
     print("pmc probe done", flush=True)
 
 
-def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
-    """ResNet-18 training step, batch 32, 3x64x64 ~ N(0,1), labels in [0, 1000), BatchNorm in train
-    mode, Adam lr 1e-3, Kaiming init; on the omarchy_mac_torch device and, from the same weights and data, on the
-    host CPU. Returns ms/step on both, the speed-up and the largest relative loss difference over the common steps."""
+def train_configs():
+    """(key, description, model factory, batch, input shape, classes, optimizer factory). The
+    optimizer factory takes capturable=... (a graph-replayed step needs the device-side step counts of Adam / AdamW;
+    SGD keeps no step count)."""
+    import torch
+
+    from omarchy_mac_torch import models
+
+    def sgd(p, capturable=False):
+        return torch.optim.SGD(p, lr=0.01, momentum=0.9)
+
+    def adam(p, capturable=False):
+        return torch.optim.Adam(p, lr=1e-3, capturable=capturable)
+
+    def adamw(p, capturable=False):
+        return torch.optim.AdamW(p, lr=1e-3, weight_decay=0.01, capturable=capturable)
+
+    return [
+        ("plaincnn_b128", "PlainCNN b128 3x32x32: 4 x (conv3x3 + BN + ReLU + maxpool2x2) at 32-64-128-256, GAP, "
+                          "linear 256->10, SGD lr 0.01 momentum 0.9 (BASELINE config 2)",
+         lambda: models.plain_cnn(10), 128, (3, 32, 32), 10, sgd),
+        ("resnet18_b32", "ResNet-18 b32 3x64x64, 1000 classes, BN train, Adam lr 1e-3 (BASELINE config 3)",
+         lambda: models.resnet18(1000), 32, (3, 64, 64), 1000, adam),
+        ("mobilenetv3_b32", "MobileNetV3-Small-style b32 3x224x224: stride-1 depthwise 3x3/5x5, 1x1 expand/project, "
+                            "hardswish, BN, squeeze-excite; 1000 classes, AdamW lr 1e-3 wd 0.01 (BASELINE config 4)",
+         lambda: models.mobilenet_v3_small(1000), 32, (3, 224, 224), 1000, adamw),
+    ]
+
+
+def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=False, fp64=False):
+    """One training configuration on the omarchy_mac_torch device and, from the same weights and data, on the host
+    CPU: ms/step eager (enqueue time too: small steps are host-bound), replayed as a HIP graph (and, with `compiled`,
+    under torch.compile(backend="omarchy_mac_torch") and replayed), PyTorch CPU fp32 with every host core (1 warm-up
+    step, then the mean of `cpu_steps`, as the reference's acceptance tool times it), the speed-ups and the relative
+    loss differences over the common steps (the north-star criterion: 1e-3 over 5 steps). fp64 adds a float64 CPU
+    run of the same steps, the rounding-free trajectory both fp32 runs are compared with."""
     import copy
 
     import torch
     import torch.nn.functional as F
 
-    from omarchy_mac_torch import models
-
+    key, title, make_model, batch, shape, classes, make_opt = cfg
     torch.manual_seed(0)
-    base = models.resnet18(1000)
+    base = make_model()
     g = torch.Generator().manual_seed(1)
     n_batches = max(warmup + steps, cpu_steps + 1)
-    data = [(torch.randn(32, 3, 64, 64, generator=g), torch.randint(0, 1000, (32,), generator=g))
+    data = [(torch.randn(batch, *shape, generator=g), torch.randint(0, classes, (batch,), generator=g))
             for _ in range(n_batches)]
 
     def run(model, device, batches, timed_from, dtype=torch.float32):
-        opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+        opt = make_opt(model.parameters())
         losses, t0 = [], None
         for i, (x, t) in enumerate(batches):
             if i == timed_from:
@@ -521,15 +576,14 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
         run.host_ms = host_ms
         return ms, [float(l) for l in losses]
 
-    def run_graphed(model, batches, timed_from, compiled=False):
+    def run_graphed(model, batches, timed_from, compile_it=False):
         """The same step captured once as a HIP graph (omarchy_mac_torch.graphs) after `timed_from` eager warm-up
-        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed).
-        compiled: the model runs through torch.compile(backend="omarchy_mac_torch") (fused BatchNorm rewrites)."""
+        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed)."""
         from omarchy_mac_torch import graphs
 
-        opt = torch.optim.Adam(model.parameters(), lr=1e-3, capturable=True)
+        opt = make_opt(model.parameters(), capturable=True)
         sx, st = torch.empty_like(batches[0][0]), torch.empty_like(batches[0][1])
-        fwd = torch.compile(model, backend=dev_name) if compiled else model
+        fwd = torch.compile(model, backend=dev_name) if compile_it else model
 
         def step():
             opt.zero_grad(set_to_none=True)
@@ -547,138 +601,79 @@ def resnet18_step(dev_name, steps, warmup, cpu_steps, cpu):
                 st.copy_(t)
                 losses.append(step().clone())
         torch.cuda.current_stream().wait_stream(side)
-        g = graphs.Graph()
-        with g.capture():
+        gr = graphs.Graph()
+        with gr.capture():
             static_loss = step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for x, t in batches[timed_from:]:
             sx.copy_(x)
             st.copy_(t)
-            g.replay()
+            gr.replay()
             losses.append(static_loss.clone())
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) / (len(batches) - timed_from) * 1e3
         out = [float(l) for l in losses]
-        g.release()
+        gr.release()
         return ms, out
 
-    dev_model = copy.deepcopy(base).to(dev_name)
+    def rel_diff(a, b):
+        return max(abs(u - v) / abs(v) for u, v in zip(a, b))
+
     dev_batches = [(x.to(dev_name), t.to(dev_name)) for (x, t) in data[:warmup + steps]]
-    if dev_name != "cpu":
-        torch.cuda.synchronize()
-    dev_ms, dev_losses = run(dev_model, dev_name, dev_batches, warmup)
-    out = {"config": "ResNet-18 b32 3x64x64, 1000 classes, BN train, Adam lr 1e-3 (BASELINE config 3)",
-           "ms_per_step": round(dev_ms, 3), "host_enqueue_ms_per_step": round(run.host_ms, 3), "steps": steps,
-           "warmup": warmup}
-    g_losses = c_losses = None
-    if dev_name != "cpu":
-        g_ms, g_losses = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3)
-        out["graphed"] = {"ms_per_step": round(g_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
-                          "how": "omarchy_mac_torch.graphs.Graph: forward + backward + fused capturable Adam captured "
-                                 "once, replayed per batch after an in-place copy of the batch"}
-        c_ms, c_losses = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3, compiled=True)
+    torch.cuda.synchronize()
+    dev_ms, dev_losses = run(copy.deepcopy(base).to(dev_name), dev_name, dev_batches, warmup)
+    out = {"config": title, "ms_per_step": round(dev_ms, 3), "host_enqueue_ms_per_step": round(run.host_ms, 3),
+           "steps": steps, "warmup": warmup}
+    variants = {}
+    g_ms, variants["graphed"] = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3)
+    out["graphed"] = {"ms_per_step": round(g_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
+                      "how": "omarchy_mac_torch.graphs.Graph: forward + backward + fused optimizer captured once, "
+                             "replayed per batch after an in-place copy of the batch"}
+    if compiled:
+        c_ms, variants["compiled_graphed"] = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3, True)
         out["compiled_graphed"] = {
             "ms_per_step": round(c_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
             "how": "the graphed step with the model under torch.compile(backend=\"omarchy_mac_torch\"): BatchNorm "
                    "running statistics updated in place, BatchNorm + ReLU and BatchNorm + residual add + ReLU fused, "
                    "batch counters in one launch"}
-    if cpu:
-        threads = len(os.sched_getaffinity(0))
-        torch.set_num_threads(threads)
-        cpu_ms, cpu_losses = run(copy.deepcopy(base), "cpu", data[:cpu_steps + 1], 1)
-        k = min(len(cpu_losses), len(dev_losses))
-        rel = max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:k], cpu_losses[:k]))
-        rel5 = max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:5], cpu_losses[:5]))  # the north-star criterion
-        # float64 CPU run of the same steps: the rounding-free trajectory both fp32 runs are compared with (Adam on a
-        # 1000-class batch of 32 amplifies fp32 summation-order differences from step to step)
-        _, f64_losses = run(copy.deepcopy(base).double(), "cpu", data[:k], 0, torch.float64)
-        for key, ls in (("graphed", g_losses), ("compiled_graphed", c_losses)):
-            if ls is not None:
-                out[key].update({
-                    "speedup_vs_cpu": round(cpu_ms / out[key]["ms_per_step"], 2),
-                    "max_rel_loss_diff": max(abs(a - b) / abs(b) for a, b in zip(ls[:k], cpu_losses[:k])),
-                    "max_rel_loss_diff_5_steps": max(abs(a - b) / abs(b) for a, b in zip(ls[:5], cpu_losses[:5])),
-                    "max_rel_loss_diff_vs_fp64": max(abs(a - b) / abs(b) for a, b in zip(ls[:k], f64_losses)),
-                    "losses": [round(v, 6) for v in ls[:k]]})
-        out.update({"cpu_ms_per_step": round(cpu_ms, 2), "cpu_cores": threads, "cpu_steps": cpu_steps,
-                    "speedup_vs_cpu": round(cpu_ms / dev_ms, 2), "max_rel_loss_diff": rel, "loss_steps_compared": k,
-                    "max_rel_loss_diff_5_steps": rel5,
-                    "losses": {"device": [round(v, 6) for v in dev_losses[:k]],
-                               "cpu": [round(v, 6) for v in cpu_losses[:k]],
-                               "cpu_fp64": [round(v, 6) for v in f64_losses]},
-                    "max_rel_loss_diff_vs_fp64": {
-                        "device": max(abs(a - b) / abs(b) for a, b in zip(dev_losses[:k], f64_losses)),
-                        "cpu_fp32": max(abs(a - b) / abs(b) for a, b in zip(cpu_losses[:k], f64_losses))},
-                    "cpu": f"PyTorch {torch.__version__} CPU fp32, {cpu_info()}"})
+    if not cpu:
+        return out
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cpu_ms, cpu_losses = run(copy.deepcopy(base), "cpu", data[:cpu_steps + 1], 1)
+    k = min(len(cpu_losses), len(dev_losses))
+    f64 = None
+    if fp64:
+        _, f64 = run(copy.deepcopy(base).double(), "cpu", data[:k], 0, torch.float64)
+    for name, ls in variants.items():
+        out[name].update({"speedup_vs_cpu": round(cpu_ms / out[name]["ms_per_step"], 2),
+                          "max_rel_loss_diff": rel_diff(ls[:k], cpu_losses[:k]),
+                          "max_rel_loss_diff_5_steps": rel_diff(ls[:5], cpu_losses[:5]),
+                          "losses": [round(v, 6) for v in ls[:k]]})
+        if f64:
+            out[name]["max_rel_loss_diff_vs_fp64"] = rel_diff(ls[:k], f64)
+    out.update({"cpu_ms_per_step": round(cpu_ms, 2), "cpu_cores": threads, "cpu_steps": cpu_steps,
+                "speedup_vs_cpu": round(cpu_ms / dev_ms, 2), "max_rel_loss_diff": rel_diff(dev_losses[:k], cpu_losses[:k]),
+                "loss_steps_compared": k, "max_rel_loss_diff_5_steps": rel_diff(dev_losses[:5], cpu_losses[:5]),
+                "losses": {"device": [round(v, 6) for v in dev_losses[:k]],
+                           "cpu": [round(v, 6) for v in cpu_losses[:k]]},
+                "cpu": f"PyTorch {torch.__version__} CPU fp32, {cpu_info()}"})
+    if f64:
+        out["losses"]["cpu_fp64"] = [round(v, 6) for v in f64]
+        out["max_rel_loss_diff_vs_fp64"] = {"device": rel_diff(dev_losses[:k], f64),
+                                            "cpu_fp32": rel_diff(cpu_losses[:k], f64)}
     return out
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "bw"], default="c5",
-                    help="resnet: only the ResNet-18 training-step measurement; bw: only the HBM-bound kernels "
-                         "(both for profiling)")
-    ap.add_argument("--no-bw", action="store_true", help="skip the HBM-bound kernel measurements")
-    ap.add_argument("--no-miopen", action="store_true",
-                    help="skip timing the same sweep through torch's own convolutions (MIOpen)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--no-resnet", action="store_true", help="skip the ResNet-18 training-step measurement")
-    ap.add_argument("--resnet-steps", type=int, default=20)
-    ap.add_argument("--no-tune", action="store_true",
-                    help="skip plan tuning (tile / K split per layer and direction) before the warmup")
-    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="summarize two --pmc-probe counter dumps into profiles/conv_gather_<workload>_traffic.json")
-    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
-                    help="per-kernel table of the timed steps of a rocprofv3 --kernel-trace run of the sweep "
-                         "(--no-bw --no-resnet --no-cpu, same --steps)")
-    ap.add_argument("--resnet-trace-summary", metavar="KERNEL_TRACE_CSV",
-                    help="kernel time per step by family of a rocprofv3 --kernel-trace run of --workload resnet")
-    ap.add_argument("--kernel-table", metavar="KERNEL_TRACE_CSV",
-                    help="per-kernel launches and mean / median duration of this library's kernels in a kernel trace")
-    ap.add_argument("--pmc-probe", action="store_true",
-                    help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
-                         "launch per layer; prints nothing else")
-    args = ap.parse_args()
-    if args.pmc_summary:
-        pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
-        return
-    if args.kernel_table:
-        kernel_table(args.kernel_table)
-        return
-    if args.resnet_trace_summary:
-        resnet_trace_summary(args.resnet_trace_summary)
-        return
-    if args.trace_summary:
-        trace_summary(args.trace_summary, args.steps, len(C5_LAYERS if args.workload == "c5" else C1_LAYERS))
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
-              "its batch share, the weight gradients summed over the GPUs afterwards). Run with --gpus 1.",
-              file=sys.stderr)
-        sys.exit(2)
-
+def conv_sweep(layers, dev, steps, warmup, tune):
+    """The sweep of `layers` (fwd + dgrad + wgrad each) on synthetic inputs resident in HBM: plans tuned first (as the
+    reference tunes every new shape on first use, csrc/conv.cpp:56), `warmup` untimed steps, then `steps` timed ones
+    with HIP events around every launch on the launch stream. Returns the figures the bench line reports."""
     import torch
 
     from omarchy_mac_torch import hip_ops
 
-    dev = torch.device("cuda:0")
-    if args.workload == "resnet":
-        import omarchy_mac_torch
-
-        print(json.dumps({"resnet18_b32": resnet18_step(omarchy_mac_torch.DEVICE, args.resnet_steps, 5, 5,
-                                                          not args.no_cpu)}), flush=True)
-        return
-    if args.workload == "bw":
-        print(json.dumps({"bandwidth_kernels": bandwidth_kernels(dev)}), flush=True)
-        return
-    layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
-    if args.pmc_probe:
-        pmc_probe(layers, dev)
-        return
     gen = torch.Generator(device=dev).manual_seed(0)
     data = []
     for (name, n, c, k, h, ks, s, p) in layers:
@@ -692,7 +687,7 @@ def main():
     plans = {}
     for (name, n, c, k, h, ks, s, p, x, w, gy) in data:
         for d in ("fwd", "dgrad", "wgrad"):
-            if not args.no_tune:  # the reference tunes every new conv shape on first use (csrc/conv.cpp:56)
+            if tune:
                 hip_ops.autotune_conv(d, x.shape, w.shape, s, p)
             plans.setdefault(name, {})[d] = list(hip_ops.conv_plan(d, x.shape, w.shape, s, p)[:2])
     torch.cuda.synchronize()
@@ -721,37 +716,150 @@ def main():
                 dir_events["dgrad"].append((name, f, evs[1], evs[2]))
                 dir_events["wgrad"].append((name, f, evs[2], evs[3]))
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step(False)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step(True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
     step_flops = sum(3 * flops_dir(n, c, k, h, ks, s, p) for (_, n, c, k, h, ks, s, p, *_r) in data)
-    ms_per_step = elapsed / args.steps * 1e3
-    value = step_flops * args.steps / elapsed / 1e12
-
     fwd_ms = [a.elapsed_time(b) for (_, a, b) in fwd_events]
     fwd_flops = [f for (f, _, _) in fwd_events]
-    avg_launch_ms = sum(fwd_ms) / len(fwd_ms)
-    achieved = sum(fwd_flops) / (sum(fwd_ms) / 1e3) / 1e12  # TFLOP/s over all forward launches
-    per_dir = {}
-    per_layer = {}
+    per_dir, per_layer = {}, {}
     for d, evs in dir_events.items():
         tot_f = sum(f for (_, f, _, _) in evs)
         tot_ms = sum(a.elapsed_time(b) for (_, _, a, b) in evs)
         per_dir[d] = {"tflops": round(tot_f / (tot_ms / 1e3) / 1e12, 2),
                       "frac_peak": round(tot_f / (tot_ms / 1e3) / PEAK_FP32_MFMA, 4),
-                      "ms_per_step": round(tot_ms / args.steps, 4)}
+                      "ms_per_step": round(tot_ms / steps, 4)}
         for (name, f, a, b) in evs:
             per_layer.setdefault(name, {}).setdefault(d, []).append(a.elapsed_time(b))
     layer_flops = {l[0]: flops_dir(*l[1:8]) for l in data}
-    layer_tflops = {name: {d: round(layer_flops[name] / (sum(v) / len(v) / 1e3) / 1e12, 1) for d, v in dd.items()}
-                    for name, dd in per_layer.items()}
+    return {
+        "value": step_flops * steps / elapsed / 1e12,
+        "ms_per_step": elapsed / steps * 1e3,
+        "step_flops": step_flops,
+        "avg_launch_ms": sum(fwd_ms) / len(fwd_ms),
+        "achieved": sum(fwd_flops) / (sum(fwd_ms) / 1e3) / 1e12,  # TFLOP/s over all forward launches
+        "flop_per_launch_avg": sum(fwd_flops) / len(fwd_flops),
+        "per_direction": per_dir,
+        "per_layer_tflops": {name: {d: round(layer_flops[name] / (sum(v) / len(v) / 1e3) / 1e12, 1)
+                                    for d, v in dd.items()} for name, dd in per_layer.items()},
+        "plans": plans,
+    }
 
+
+def c1_sub_object(dev, steps, warmup, cpu):
+    """Config 1 (AlexNet conv1 b16, fwd + dgrad + wgrad) as a sub-object of the bench line: its sweep with tuned plans,
+    parity of y, gx and gw with PyTorch CPU fp32 on the same full-size inputs (rel-L2), and PyTorch CPU at every host
+    core on the same full-size layer."""
+    import torch
+
+    from omarchy_mac_torch import hip_ops
+
+    sw = conv_sweep(C1_LAYERS, dev, steps, warmup, True)
+    out = {"config": "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad (BASELINE config 1)",
+           "value": round(sw["value"], 3), "unit": "TFLOP/s", "frac_of_peak": round(sw["value"] * 1e12 / PEAK_FP32_MFMA, 4),
+           "ms_per_step": round(sw["ms_per_step"], 4), "per_direction": sw["per_direction"], "plans": sw["plans"]}
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(16, 3, 224, 224, generator=g)
+    w = torch.nn.init.kaiming_normal_(torch.empty(64, 3, 11, 11), generator=g)
+    b = torch.rand(64, generator=g) * 0.2 - 0.1
+    gy = torch.randn(16, 64, 55, 55, generator=g)
+    dx, dw_, db, dgy = (t.to(dev) for t in (x, w, b, gy))
+    y = hip_ops.conv2d(dx, dw_, db, 4, 2)
+    gx = hip_ops.conv2d_dgrad(dgy, dw_, x.shape, 4, 2)
+    gw = hip_ops.conv2d_wgrad(dx, dgy, 11, 4, 2)
+    ry = torch.nn.functional.conv2d(x, w, b, 4, 2)
+    rgx, rgw, _ = torch.ops.aten.convolution_backward(gy, x, w, None, [4, 4], [2, 2], [1, 1], False, [0, 0], 1,
+                                                      [True, True, False])
+
+    def rel(a, r):
+        return float((a.cpu().double() - r.double()).norm() / r.double().norm())
+
+    out["rel_l2_vs_torch_cpu"] = {"y": rel(y, ry), "gx": rel(gx, rgx), "gw": rel(gw, rgw)}
+    if cpu:
+        v, gf, secs = torch_cpu_sweep(C1_LAYERS, 16, len(os.sched_getaffinity(0)), 2.0)
+        out["cpu"] = {"value": round(v, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
+                      "sample": f"PyTorch {torch.__version__} CPU fp32, the full layer at batch 16, {gf:.0f} GFLOP in "
+                                f"{secs:.1f} s; {cpu_info()}"}
+        out["speedup_vs_cpu"] = round(sw["value"] / v, 1)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "models", "bw"], default="c5",
+                    help="resnet: only the ResNet-18 training-step measurement; models: only the training steps of "
+                         "configs 2-4; bw: only the HBM-bound kernels (all three for profiling)")
+    ap.add_argument("--no-bw", action="store_true", help="skip the HBM-bound kernel measurements")
+    ap.add_argument("--no-miopen", action="store_true",
+                    help="skip timing the same sweep through torch's own convolutions (MIOpen)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-models", "--no-resnet", dest="no_models", action="store_true",
+                    help="skip config 1's sub-object and the training steps of configs 2-4")
+    ap.add_argument("--model-steps", "--resnet-steps", dest="model_steps", type=int, default=20)
+    ap.add_argument("--no-tune", action="store_true",
+                    help="skip plan tuning (tile / K split per layer and direction) before the warmup")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarize two --pmc-probe counter dumps into profiles/conv_gather_<workload>_traffic.json")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel table of the timed steps of a rocprofv3 --kernel-trace run of the sweep "
+                         "(--no-bw --no-models --no-cpu, same --steps)")
+    ap.add_argument("--resnet-trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="kernel time per step by family of a rocprofv3 --kernel-trace run of --workload resnet")
+    ap.add_argument("--kernel-table", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel launches and mean / median duration of this library's kernels in a kernel trace")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
+                         "launch per layer; prints nothing else")
+    args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
+        return
+    if args.kernel_table:
+        kernel_table(args.kernel_table)
+        return
+    if args.resnet_trace_summary:
+        resnet_trace_summary(args.resnet_trace_summary)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps, len(C5_LAYERS if args.workload == "c5" else C1_LAYERS))
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each MI355X runs the same kernels on "
+              "its batch share, the weight gradients summed over the GPUs afterwards). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    if args.workload in ("resnet", "models"):
+        import omarchy_mac_torch
+
+        cfgs = train_configs()
+        if args.workload == "resnet":
+            cfgs = [c for c in cfgs if c[0] == "resnet18_b32"]
+        print(json.dumps({c[0]: train_step_bench(c, omarchy_mac_torch.DEVICE, args.model_steps, 5, 5, not args.no_cpu,
+                                                 compiled=c[0] == "resnet18_b32", fp64=c[0] == "resnet18_b32")
+                          for c in cfgs}), flush=True)
+        return
+    if args.workload == "bw":
+        print(json.dumps({"bandwidth_kernels": bandwidth_kernels(dev)}), flush=True)
+        return
+    layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
+    if args.pmc_probe:
+        pmc_probe(layers, dev)
+        return
+    sw = conv_sweep(layers, dev, args.steps, args.warmup, not args.no_tune)
+    value = sw["value"]
     traffic = traffic_per_launch(args.workload)
     out = {
         "metric": "conv fwd+dgrad+wgrad fp32 TFLOP/s (% of fp32-MFMA peak); ResNet-18 b32 train ms/step",
@@ -760,7 +868,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 3),
+        "ms_per_step": round(sw["ms_per_step"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -770,34 +878,39 @@ def main():
                                 "(512,7^2) + 1x1 C->4C and 4C->C at the same sizes, fwd+dgrad+wgrad"
                                 if args.workload == "c5" else
                                 "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad"),
-                   "gflop_per_step": round(step_flops / 1e9, 2), "layout": "NCHW"},
+                   "gflop_per_step": round(sw["step_flops"] / 1e9, 2), "layout": "NCHW"},
         "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
         "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel / conv1x1_stream_kernel (forward launches)",
-                     "bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_FP32_MFMA, 4),
+                     "bound": "mfma", "achieved": round(sw["achieved"], 3), "peak": PEAK_FP32_MFMA / 1e12,
+                     "unit": "TFLOP/s", "frac": round(sw["achieved"] * 1e12 / PEAK_FP32_MFMA, 4),
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_algorithmic_bytes": traffic["algorithmic_bytes"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "avg_launch_ms": round(avg_launch_ms, 4),
-                     "flop_per_launch_avg": round(sum(fwd_flops) / len(fwd_flops))},
-        "per_direction": per_dir,
-        "per_layer_tflops": layer_tflops,
-        "plans": {"tuned": not args.no_tune, "tile_slices": plans},
+                     "avg_launch_ms": round(sw["avg_launch_ms"], 4),
+                     "flop_per_launch_avg": round(sw["flop_per_launch_avg"])},
+        "per_direction": sw["per_direction"],
+        "per_layer_tflops": sw["per_layer_tflops"],
+        "plans": {"tuned": not args.no_tune, "tile_slices": sw["plans"]},
         "device": torch.cuda.get_device_name(dev),
     }
+    if not args.no_cpu:
+        print("cpu baselines ...", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = torch_cpu_baseline(layers, batch=16)
+        out["oracle_cpu_baseline"] = oracle_baseline(layers)
     if not args.no_miopen:
         out["miopen_same_sweep"] = miopen_sweep(layers, dev, args.steps)
     if not args.no_bw:
         out["bandwidth_kernels"] = bandwidth_kernels(dev)
-    if not args.no_resnet:
-        import omarchy_mac_torch  # noqa: F401  (registers the device)
+    if not args.no_models:
+        import omarchy_mac_torch
 
-        out["resnet18_b32"] = resnet18_step(omarchy_mac_torch.DEVICE, args.resnet_steps, 5, 5, not args.no_cpu)
-    if not args.no_cpu:
-        threads = len(os.sched_getaffinity(0))
-        out["cpu_baseline"] = oracle_baseline(layers, budget_s=15.0)
-        out["torch_cpu_baseline"] = torch_cpu_baseline(layers, batch=8 if args.workload == "c5" else 16,
-                                                       threads=threads)
+        if args.workload == "c5":
+            print("config 1 ...", file=sys.stderr, flush=True)
+            out["alexnet_conv1_b16"] = c1_sub_object(dev, args.steps, args.warmup, not args.no_cpu)
+        for cfg in train_configs():
+            print(f"{cfg[0]} ...", file=sys.stderr, flush=True)
+            out[cfg[0]] = train_step_bench(cfg, omarchy_mac_torch.DEVICE, args.model_steps, 5, 5, not args.no_cpu,
+                                           compiled=cfg[0] == "resnet18_b32", fp64=cfg[0] == "resnet18_b32")
     print(json.dumps(out), flush=True)
 
 

@@ -7,9 +7,12 @@ required: a missing build raises ImportError instead of running anything elsewhe
 """
 
 import atexit
+import collections.abc
+import contextlib
 import json
 import os
 import pathlib
+import tempfile
 import types
 
 import torch
@@ -125,75 +128,93 @@ def validate_kernels():
     return []
 
 
-class _Fallbacks:
-    """Hot-path ops that could not run on the HIP kernels, with why: {"op (reason)": count}. Read-only mapping view.
-    (They ran on torch's HIP kernels instead.)"""
+class _FallbackView(collections.abc.Mapping):
+    """FALLBACKS: hot-path calls that ran on torch's HIP kernels instead of this library's, as a live read-only mapping
+    {"op (why)": count} over the extension's counters (clear() resets them)."""
 
-    def _d(self):
-        return core.fallback_counts()
-
-    def keys(self):
-        return self._d().keys()
-
-    def items(self):
-        return self._d().items()
-
-    def __getitem__(self, k):
-        return self._d()[k]
+    def __getitem__(self, key):
+        return core.fallback_counts()[key]
 
     def __iter__(self):
-        return iter(self._d())
+        return iter(core.fallback_counts())
 
     def __len__(self):
-        return len(self._d())
-
-    def __bool__(self):
-        return bool(self._d())
+        return len(core.fallback_counts())
 
     def clear(self):
         core.reset_fallbacks()
 
     def __repr__(self):
-        return repr(self._d())
+        return f"FALLBACKS({core.fallback_counts()!r})"
 
 
-FALLBACKS = _Fallbacks()
+FALLBACKS = _FallbackView()
 
 
-# ---- on-disk cache of the conv plan tuning (reference: omarchy_mac_torch/native.py:185-209) ----
-# Keys "dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad" -> [tile, slices]. The tiles index this library's gfx950 tile tables
-# (the file name carries the table's size: 14 gather tiles, each in two K orders),
-# so the file is not the reference's (whose entries name its own tiles and a split-K multiplier).
+# ---- on-disk conv plan cache (reference: omarchy_mac_torch/native.py:185-209) ----
+# One JSON object {"dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad": [tile, slices]}, the reference's key format. The values
+# index this library's gfx950 tile tables (the file name carries the gather table's size), so the file is not the
+# reference's, whose entries name its own tiles and a split-K multiplier.
 TUNE_FILE = os.environ.get("OMARCHY_MAC_TORCH_TUNE_FILE",
                            os.path.expanduser("~/.cache/omarchy-mac-torch/tuning-gfx950-t14.json"))
 
 
-def _load_tuning(path=TUNE_FILE):
-    try:
-        with open(path) as f:
-            return core.tune_load({str(k): (int(v[0]), int(v[1])) for k, v in json.load(f).items()})
-    except (OSError, ValueError, TypeError, KeyError, IndexError):
-        return 0
+class TuningStore:
+    """The conv plan cache's file. `load` feeds the well-formed entries to the plan cache one by one (an entry with a
+    malformed key or value, or a plan the tile tables do not have, is skipped and counted in `skipped`); `save` writes
+    the file's entries merged with the cache's (the cache wins), through a temporary file renamed over the old one so
+    that readers never see half a file."""
 
+    def __init__(self, path=None):
+        self.path = pathlib.Path(path or TUNE_FILE)
+        self.skipped = 0
 
-def _save_tuning(path=TUNE_FILE):
-    try:
-        os.makedirs(os.path.dirname(path), exist_ok=True)
-        old = {}
+    def _read(self):
         try:
-            with open(path) as f:
-                old = json.load(f)
+            data = json.loads(self.path.read_text())
         except (OSError, ValueError):
-            pass
-        old.update({k: list(v) for k, v in core.tune_dump().items()})
-        tmp = f"{path}.{os.getpid()}.tmp"
-        with open(tmp, "w") as f:
-            json.dump(old, f)
-        os.replace(tmp, path)
-    except Exception:
+            return {}
+        return data if isinstance(data, dict) else {}
+
+    def load(self):
+        """Returns the number of entries the plan cache accepted."""
+        good, self.skipped = {}, 0
+        for key, val in self._read().items():
+            fields = key.split(",") if isinstance(key, str) else []
+            plan = val if isinstance(val, list) and len(val) == 2 else None
+            if (len(fields) != 11 or not all(f.strip().lstrip("-").isdigit() for f in fields) or plan is None
+                    or not all(isinstance(v, int) and not isinstance(v, bool) for v in plan)):
+                self.skipped += 1
+                continue
+            good[key] = (plan[0], plan[1])
+        accepted = core.tune_load(good) if good else 0
+        self.skipped += len(good) - accepted
+        return accepted
+
+    def save(self):
+        merged = self._read()
+        merged.update({k: [int(v[0]), int(v[1])] for k, v in core.tune_dump().items()})
+        self.path.parent.mkdir(parents=True, exist_ok=True)
+        fd, tmp = tempfile.mkstemp(prefix=self.path.name + ".", dir=self.path.parent)
+        try:
+            with os.fdopen(fd, "w") as f:
+                json.dump(merged, f, sort_keys=True)
+            os.replace(tmp, self.path)
+        except BaseException:
+            with contextlib.suppress(OSError):
+                os.unlink(tmp)
+            raise
+        return len(merged)
+
+
+def _save_at_exit(store):
+    try:
+        store.save()
+    except OSError:  # a read-only home directory must not fail the interpreter's exit
         pass
 
 
 if core.tuning():
-    _load_tuning()
-    atexit.register(_save_tuning)
+    _store = TuningStore()
+    _store.load()
+    atexit.register(_save_at_exit, _store)

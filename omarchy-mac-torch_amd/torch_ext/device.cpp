@@ -115,7 +115,7 @@ static Tensor dev_view(const Tensor& orig, const Tensor& h) {
 
 void check(int st, const char* what) {
   if (st == OMT_OK) return;
-  if (st == OMT_UNSUPPORTED) throw Unsupported(omt_last_error());
+  if (st == OMT_UNSUPPORTED) throw NotCovered(omt_last_error());
   TORCH_CHECK_WITH(OutOfMemoryError, st != OMT_OOM, what, ": out of device memory: ", omt_last_error());
   TORCH_CHECK(false, what, ": ", omt_last_error());
 }
@@ -132,23 +132,34 @@ std::map<std::string, int64_t>& delegated_counts() {
   static std::map<std::string, int64_t> m;
   return m;
 }
-void note_fallback(const std::string& op, const std::string& why) { fallback_counts()[op + " (" + why + ")"]++; }
 static bool env_on(const char* name) {
   const char* e = std::getenv(name);
   return e && e[0] == '1';
 }
-bool strict_mode() {
-  static bool s = env_on("OMARCHY_MAC_TORCH_STRICT");
-  return s;
-}
+static bool g_strict = env_on("OMARCHY_MAC_TORCH_STRICT");
 static bool g_debug = env_on("OMARCHY_MAC_TORCH_DEBUG");
 static bool g_count_delegated = false;
+static std::string g_forced_sync_error;  // set by tests only: the next debug_point reports it as a device error
+bool strict_mode() { return g_strict; }
+void set_strict_mode(bool on) { g_strict = on; }
 bool debug_mode() { return g_debug; }
 void set_debug_mode(bool on) { g_debug = on; }
 void set_count_delegated(bool on) { g_count_delegated = on; }
-void debug_after(const char* op) {
-  int st = omt_stream_sync(cur_stream());
-  TORCH_CHECK(st == OMT_OK, "omarchy-mac-torch (debug): asynchronous error after ", op, ": ", omt_last_error());
+void force_next_sync_error(const std::string& msg) { g_forced_sync_error = msg; }
+void debug_point(const std::string& op) {
+  std::string err;
+  if (!g_forced_sync_error.empty()) {
+    err.swap(g_forced_sync_error);
+  } else if (omt_stream_sync(cur_stream()) != OMT_OK) {
+    err = omt_last_error();
+  }
+  TORCH_CHECK(err.empty(), "omarchy-mac-torch (debug): asynchronous error after ", op, ": ", err);
+}
+void left_hot_path(const std::string& op, const char* why) {
+  TORCH_CHECK(!strict_mode(), "omarchy-mac-torch (strict): ", op, " is not covered by the HIP kernels: ", why);
+  std::string key = op;
+  ((key += " (") += why) += ')';
+  ++fallback_counts()[key];
 }
 
 // ------------------------------------------------------------------------------------------------------------------

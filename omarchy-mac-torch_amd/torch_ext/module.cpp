@@ -49,6 +49,15 @@ PYBIND11_MODULE(_native, m) {
   });
   m.def("set_debug", [](bool on) { set_debug_mode(on); });
   m.def("strict", []() { return strict_mode(); });
+  m.def("set_strict", [](bool on) {
+    OMT_LOCK;
+    set_strict_mode(on);
+  });
+  m.def("debug", []() { return debug_mode(); });
+  m.def("force_next_sync_error", [](const std::string& msg) {
+    OMT_LOCK;
+    force_next_sync_error(msg);
+  });
   m.def("abi_version", []() { return omt_abi_version(); });
   m.def("hip_runtime_version", []() { return omt_hip_runtime_version(); });
   m.attr("built_with_torch") = TORCH_VERSION;

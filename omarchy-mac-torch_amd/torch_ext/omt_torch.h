@@ -12,7 +12,9 @@
 
 #include <map>
 #include <mutex>
+#include <stdexcept>
 #include <string>
+#include <type_traits>
 
 #include "omt_hip.h"
 
@@ -44,25 +46,24 @@ inline float* fpm(const Tensor& t) { return t.defined() ? t.mutable_data_ptr<flo
 inline const float* fp(const std::optional<Tensor>& t) { return t && t->defined() ? t->data_ptr<float>() : nullptr; }
 inline bool defined(const std::optional<Tensor>& t) { return t && t->defined(); }
 
-// ---- fallback by construction -------------------------------------------------------------------------------------
+// ---- coverage, and where uncovered calls go --------------------------------------------------------------------
 //
-// A hot-path op checks what it covers with NEED(cond, why) before it launches anything; a failed NEED (or an
-// OMT_UNSUPPORTED status from the library) throws Unsupported and Safe<> re-runs the call on torch's HIP kernels,
-// recording "op (why)" in fallback_counts() (the reference's FALLBACKS, csrc/omt.h:161-220). With
-// OMARCHY_MAC_TORCH_STRICT=1 that is an error instead.
+// A hot-path wrapper states what its kernels cover with cover(ok, why) before it launches anything (an OMT_UNSUPPORTED
+// status from the library means the same). A call outside that raises NotCovered, and the wrapper's registration
+// (HotKernel) hands the untouched arguments to torch's HIP kernels over aliases of the same memory, counting
+// "op (why)" in fallback_counts() (the reference's FALLBACKS, csrc/omt.h:161-220). With OMARCHY_MAC_TORCH_STRICT=1 such
+// a call raises instead.
 
-struct Unsupported : std::exception {
-  std::string why;
-  explicit Unsupported(std::string w) : why(std::move(w)) {}
-  const char* what() const noexcept override { return why.c_str(); }
+class NotCovered : public std::runtime_error {
+ public:
+  using std::runtime_error::runtime_error;
 };
-#define NEED(cond, why)                          \
-  do {                                           \
-    if (!(cond)) throw ::omt::Unsupported(why);  \
-  } while (0)
+inline void cover(bool ok, const char* why) {
+  if (!ok) throw NotCovered(why);
+}
 
-// Raises for a non-OK library status: OMT_UNSUPPORTED -> Unsupported, OMT_OOM -> torch.OutOfMemoryError (after
-// emptying the cache, the library already retried once), anything else -> RuntimeError with the library's message.
+// Raises for a non-OK library status: OMT_UNSUPPORTED -> NotCovered, OMT_OOM -> torch.OutOfMemoryError (the library
+// has already emptied its cache and retried once), anything else -> RuntimeError with the library's message.
 void check(int status, const char* what);
 
 std::recursive_mutex& big_lock();
@@ -70,53 +71,88 @@ std::recursive_mutex& big_lock();
 
 std::map<std::string, int64_t>& fallback_counts();   // hot-path ops that could not use the HIP kernels
 std::map<std::string, int64_t>& delegated_counts();  // other ops, run on torch's HIP kernels (counted when enabled)
-void note_fallback(const std::string& op, const std::string& why);
+// The single exit of every uncovered call: raises in strict mode, else counts "op (why)".
+void left_hot_path(const std::string& op, const char* why);
 // Autotunes (direction, geometry) once when tuning is on and the plan cache has no entry (libomt_hip.so times the
 // candidates on the current stream); no-op otherwise.
 // Tunes grad input and grad weight together (for omt_conv_bwd) unless both already have cached plans.
 void tune_conv_bwd(const omt_conv_geo& g);
 void tune_conv(int dir, const omt_conv_geo& g);
 bool strict_mode();
+void set_strict_mode(bool on);
 bool debug_mode();
 void set_debug_mode(bool on);
 void set_count_delegated(bool on);
-void debug_after(const char* op);  // debug mode: synchronize and surface asynchronous errors with the op's name
+// Failure-path tests: the next debug_point reports `msg` as if the stream had returned a device error.
+void force_next_sync_error(const std::string& msg);
+// Debug mode only: synchronizes the current stream and raises any asynchronous device error with the op's name.
+void debug_point(const std::string& op);
 
 void hip_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack);        // counted
-void hip_fallback_quiet(const c10::OperatorHandle& op, torch::jit::Stack* stack);  // used by Safe<> after NEED
+void hip_fallback_quiet(const c10::OperatorHandle& op, torch::jit::Stack* stack);  // the exit of HotKernel
 
-template <class Op, auto Fn, class Sig = typename Op::schema>
-struct Safe;
-template <class Op, auto Fn, class R, class... A>
-struct Safe<Op, Fn, R(A...)> {
-  static R call(typename c10::maybe_keep_symint<false, A>::type... a) {
+// "name.overload" of an aten operator, as FALLBACKS and the registrations spell it.
+template <class Op>
+const std::string& op_label() {
+  static const std::string label = [] {
+    std::string s(Op::name);
+    s.erase(0, s.find("::") + 2);
+    if (*Op::overload_name) (s += '.') += Op::overload_name;
+    return s;
+  }();
+  return label;
+}
+
+// The device kernel of aten operator Op: Impl under the device lock; a call Impl does not cover continues on torch's
+// HIP kernels. Specialized on Impl's own signature, which the registration checks against Op's schema.
+template <class Op, auto Impl>
+struct HotKernel;
+template <class Op, class R, class... A, R (*Impl)(A...)>
+struct HotKernel<Op, Impl> {
+  static R run(A... a) {
     OMT_LOCK;
     try {
       if constexpr (std::is_void_v<R>) {
-        Fn(a...);
-        if (debug_mode()) debug_after(Op::name);
+        Impl(a...);
+        if (debug_mode()) debug_point(op_label<Op>());
       } else {
-        R r = Fn(a...);
-        if (debug_mode()) debug_after(Op::name);
-        return r;
+        R out = Impl(a...);
+        if (debug_mode()) debug_point(op_label<Op>());
+        return out;
       }
-    } catch (const Unsupported& e) {
-      std::string name = std::string(Op::name).substr(6);
-      if (Op::overload_name[0]) name += std::string(".") + Op::overload_name;
-      TORCH_CHECK(!strict_mode(), "omarchy-mac-torch (strict): ", name, " not supported by the HIP kernels: ", e.why);
-      note_fallback(name, e.why);
+    } catch (const NotCovered& e) {
+      left_hot_path(op_label<Op>(), e.what());
       return at::native::call_fallback_fn<&hip_fallback_quiet, Op>::call(a...);
     }
   }
 };
-template <class Op, class F>
-void impl_name(torch::Library& m, F f) {
-  std::string name = std::string(Op::name).substr(6);
-  if (Op::overload_name[0]) name += std::string(".") + Op::overload_name;
-  m.impl(name.c_str(), f);
+
+// Registers HotKernels into a TORCH_LIBRARY_IMPL block: HotOps(m).on<at::_ops::op, &impl>().on<...>();
+class HotOps {
+ public:
+  explicit HotOps(torch::Library& lib) : lib_(lib) {}
+  template <class Op, auto Impl>
+  HotOps& on() {
+    lib_.impl(op_label<Op>().c_str(), &HotKernel<Op, Impl>::run);
+    return *this;
+  }
+
+ private:
+  torch::Library& lib_;
+};
+
+// For the omt:: fused ops, whose way out is their composite reference (plain aten ops, which in turn reach the device
+// kernels or torch's): Dev(a...) if it covers the call, else Ref(a...).
+template <auto Dev, auto Ref, class... A>
+auto dev_or_ref(const char* op, A&&... a) {
+  OMT_LOCK;
+  try {
+    return Dev(a...);
+  } catch (const NotCovered& e) {
+    left_hot_path(op, e.what());
+    return Ref(a...);
+  }
 }
-// register aten::<op> for the device through the fallback wrapper
-#define OMT_IMPL(m, op, fn) ::omt::impl_name<at::_ops::op>(m, &::omt::Safe<at::_ops::op, fn>::call)
 
 // ---- geometry helpers shared by ops.cpp and plans.cpp -------------------------------------------------------------
 

@@ -6,14 +6,13 @@
 //                                                        reference csrc/nn.cpp:157-222, 275-285
 //   omt::bn_relu_train, bn_relu_backward, conv_act, conv_bn_act_eval (composite references + device kernels)
 //                                                        reference csrc/fused.cpp:19-136, 213-233
-// Cases a kernel does not cover fail a NEED() and run on torch's HIP kernels instead, recorded in FALLBACKS.
+// Cases a kernel does not cover fail a cover() and run on torch's HIP kernels instead, recorded in FALLBACKS.
 #include "omt_torch.h"
 
 namespace omt {
 
 static Tensor contig(const Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
 static bool whole(const Tensor& t) { return f32(t) && t.is_contiguous(); }
-static void need_dev(const Tensor& t, const char* what) { NEED(!t.defined() || is_dev(t), what); }
 
 // ------------------------------------------------------------------------------------------------------------------
 // convolution
@@ -32,13 +31,13 @@ static int kind_of(const Tensor& x, const Tensor& w, IntArrayRef stride, IntArra
 static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::optional<Tensor>& bias, IntArrayRef stride,
                            IntArrayRef padding, IntArrayRef dilation, bool transposed, int64_t groups, bool relu) {
   const int kind = kind_of(x_, w_, stride, padding, dilation, transposed, groups);
-  NEED(kind != OMT_CONV_NONE, "dilated, transposed, grouped or non-square convolution");
-  NEED(!defined(bias) || (f32(*bias) && bias->dim() == 1), "float32 bias");
-  NEED(!relu || kind == OMT_CONV_DENSE, "ReLU epilogue on a depthwise convolution");
+  cover(kind != OMT_CONV_NONE, "dilated, transposed, grouped or non-square convolution");
+  cover(!defined(bias) || (f32(*bias) && bias->dim() == 1), "float32 bias");
+  cover(!relu || kind == OMT_CONV_DENSE, "ReLU epilogue on a depthwise convolution");
   Tensor x = contig(x_), w = contig(w_);
   Tensor b = defined(bias) ? contig(*bias) : Tensor();
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
-  NEED(g.oh >= 1 && g.ow >= 1, "empty output");
+  cover(g.oh >= 1 && g.ow >= 1, "empty output");
   Tensor y = empty_dev({g.n, g.co, g.oh, g.ow});
   if (kind == OMT_CONV_DENSE) {
     tune_conv(OMT_DIR_FWD, g);
@@ -65,10 +64,10 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
                                                                 bool transposed, IntArrayRef, int64_t groups,
                                                                 std::array<bool, 3> mask) {
   const int kind = kind_of(x_, w_, stride, padding, dilation, transposed, groups);
-  NEED(kind != OMT_CONV_NONE && f32(gy_), "dilated, transposed, grouped or non-square convolution");
+  cover(kind != OMT_CONV_NONE && f32(gy_), "dilated, transposed, grouped or non-square convolution");
   Tensor gy = contig(gy_), x = contig(x_), w = contig(w_);
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
-  NEED(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");
+  cover(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");
   Tensor gx, gw, gb;
   void* s = cur_stream();
   if (kind == OMT_CONV_DENSE && mask[0] && mask[1]) {
@@ -118,9 +117,9 @@ static std::tuple<Tensor, Tensor, Tensor> batch_norm_(const Tensor& x_, const st
                                                       const std::optional<Tensor>& rm,
                                                       const std::optional<Tensor>& rv, bool training,
                                                       double momentum, double eps) {
-  NEED(defined(weight) && defined(bias) && defined(rm) && defined(rv) && f32(x_) && x_.dim() == 4,
+  cover(defined(weight) && defined(bias) && defined(rm) && defined(rv) && f32(x_) && x_.dim() == 4,
        "batch norm without affine parameters or running stats, or not 4-D float32");
-  NEED(whole(*weight) && whole(*bias) && whole(*rm) && whole(*rv), "batch norm parameters must be contiguous float32");
+  cover(whole(*weight) && whole(*bias) && whole(*rm) && whole(*rv), "batch norm parameters must be contiguous float32");
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor y = empty_dev(x.sizes());
@@ -146,9 +145,9 @@ static std::tuple<Tensor, Tensor, Tensor> batch_norm_backward_(const Tensor& gy_
                                                                const std::optional<Tensor>& sm,
                                                                const std::optional<Tensor>& si, bool train, double,
                                                                std::array<bool, 3> mask) {
-  NEED(train && defined(weight) && defined(sm) && defined(si) && f32(x_) && f32(gy_) && x_.dim() == 4,
+  cover(train && defined(weight) && defined(sm) && defined(si) && f32(x_) && f32(gy_) && x_.dim() == 4,
        "eval-mode or non-affine batch norm backward");
-  NEED(whole(*weight) && whole(*sm) && whole(*si), "contiguous float32 parameters");
+  cover(whole(*weight) && whole(*sm) && whole(*si), "contiguous float32 parameters");
   Tensor gy = contig(gy_), x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
@@ -181,7 +180,7 @@ struct Pool2 {
   int64_t kh, kw, sh, sw, ph, pw, dh, dw;
 };
 static Pool2 pool_args(IntArrayRef k, IntArrayRef s, IntArrayRef p, IntArrayRef d) {
-  NEED(k.size() == 1 || k.size() == 2, "kernel size");
+  cover(k.size() == 1 || k.size() == 2, "kernel size");
   Pool2 r;
   r.kh = k[0];
   r.kw = k.size() == 2 ? k[1] : k[0];
@@ -192,7 +191,7 @@ static Pool2 pool_args(IntArrayRef k, IntArrayRef s, IntArrayRef p, IntArrayRef 
   r.dh = d.empty() ? 1 : d[0];
   r.dw = d.empty() ? 1 : (d.size() == 2 ? d[1] : d[0]);
   // PyTorch's own argument checks (and their messages) stay with its kernels
-  NEED(r.kh > 0 && r.kw > 0 && r.sh > 0 && r.sw > 0 && r.dh > 0 && r.dw > 0 && r.ph >= 0 && r.pw >= 0 &&
+  cover(r.kh > 0 && r.kw > 0 && r.sh > 0 && r.sw > 0 && r.dh > 0 && r.dw > 0 && r.ph >= 0 && r.pw >= 0 &&
            r.ph <= ((r.kh - 1) * r.dh + 1) / 2 && r.pw <= ((r.kw - 1) * r.dw + 1) / 2,
        "pooling arguments");
   return r;
@@ -200,12 +199,12 @@ static Pool2 pool_args(IntArrayRef k, IntArrayRef s, IntArrayRef p, IntArrayRef 
 
 static std::tuple<Tensor, Tensor> max_pool2d_(const Tensor& x_, IntArrayRef k, IntArrayRef s, IntArrayRef p,
                                               IntArrayRef d, bool ceil) {
-  NEED(f32(x_) && x_.dim() == 4, "4-D float32");
+  cover(f32(x_) && x_.dim() == 4, "4-D float32");
   Pool2 a = pool_args(k, s, p, d);
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
   const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, a.dh, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, a.dw, ceil);
-  NEED(oh >= 1 && ow >= 1, "empty output");
+  cover(oh >= 1 && ow >= 1, "empty output");
   Tensor y = empty_dev({n, c, oh, ow}), idx = empty_dev({n, c, oh, ow}, at::kLong);
   check(omt_maxpool_fwd(n * c, ih, iw, oh, ow, a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, a.dh, a.dw, fp(x), fpm(y),
                         idx.mutable_data_ptr<int64_t>(), cur_stream()),
@@ -215,7 +214,7 @@ static std::tuple<Tensor, Tensor> max_pool2d_(const Tensor& x_, IntArrayRef k, I
 
 static Tensor max_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayRef k, IntArrayRef s, IntArrayRef p,
                                    IntArrayRef d, bool, const Tensor& idx_) {
-  NEED(f32(gy_) && x.dim() == 4 && idx_.scalar_type() == at::kLong, "4-D float32");
+  cover(f32(gy_) && x.dim() == 4 && idx_.scalar_type() == at::kLong, "4-D float32");
   Pool2 a = pool_args(k, s, p, d);
   Tensor gy = contig(gy_), idx = contig(idx_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
@@ -228,14 +227,14 @@ static Tensor max_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayR
 
 static Tensor avg_pool2d_(const Tensor& x_, IntArrayRef k, IntArrayRef s, IntArrayRef p, bool ceil, bool incl,
                           std::optional<int64_t> div) {
-  NEED(f32(x_) && x_.dim() == 4, "4-D float32");
-  NEED(!div || *div > 0, "divisor_override");
+  cover(f32(x_) && x_.dim() == 4, "4-D float32");
+  cover(!div || *div > 0, "divisor_override");
   Pool2 a = pool_args(k, s, p, {});
-  NEED(a.ph <= a.kh / 2 && a.pw <= a.kw / 2, "pooling arguments");
+  cover(a.ph <= a.kh / 2 && a.pw <= a.kw / 2, "pooling arguments");
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
   const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, 1, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, 1, ceil);
-  NEED(oh >= 1 && ow >= 1, "empty output");
+  cover(oh >= 1 && ow >= 1, "empty output");
   Tensor y = empty_dev({n, c, oh, ow});
   check(omt_avgpool_fwd(n * c, ih, iw, oh, ow, a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, incl ? 1 : 0, div.value_or(0), fp(x),
                         fpm(y), cur_stream()),
@@ -245,8 +244,8 @@ static Tensor avg_pool2d_(const Tensor& x_, IntArrayRef k, IntArrayRef s, IntArr
 
 static Tensor avg_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayRef k, IntArrayRef s, IntArrayRef p,
                                    bool, bool incl, std::optional<int64_t> div) {
-  NEED(f32(gy_) && x.dim() == 4, "4-D float32");
-  NEED(!div || *div > 0, "divisor_override");
+  cover(f32(gy_) && x.dim() == 4, "4-D float32");
+  cover(!div || *div > 0, "divisor_override");
   Pool2 a = pool_args(k, s, p, {});
   Tensor gy = contig(gy_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
@@ -258,7 +257,7 @@ static Tensor avg_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayR
 }
 
 static Tensor adaptive_avg_pool2d_(const Tensor& x_, IntArrayRef out) {
-  NEED(f32(x_) && x_.dim() == 4 && out.size() == 2 && out[0] >= 1 && out[1] >= 1, "4-D float32");
+  cover(f32(x_) && x_.dim() == 4 && out.size() == 2 && out[0] >= 1 && out[1] >= 1, "4-D float32");
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1);
   Tensor y = empty_dev({n, c, out[0], out[1]});
@@ -268,7 +267,7 @@ static Tensor adaptive_avg_pool2d_(const Tensor& x_, IntArrayRef out) {
 }
 
 static Tensor adaptive_avg_pool2d_backward_(const Tensor& gy_, const Tensor& x) {
-  NEED(f32(gy_) && x.dim() == 4, "4-D float32");
+  cover(f32(gy_) && x.dim() == 4, "4-D float32");
   Tensor gy = contig(gy_);
   Tensor gx = empty_dev(x.sizes());
   check(omt_adapool_bwd(x.size(0) * x.size(1), x.size(2), x.size(3), gy.size(2), gy.size(3), fp(gy), fpm(gx),
@@ -327,7 +326,7 @@ static Tensor conv_bn_act_eval_ref(const Tensor& x, const Tensor& cw, const std:
 static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_dev(const Tensor& x_, const Tensor& w,
                                                                           const Tensor& b, const Tensor& rm,
                                                                           const Tensor& rv, double mom, double eps) {
-  NEED(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
+  cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
        "4-D float32 with contiguous parameters");
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
@@ -343,12 +342,12 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_,
                                                                const Tensor& rm, const Tensor& rv, double mom,
                                                                double eps, int64_t act,
                                                                const std::optional<Tensor>& res_) {
-  NEED(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
+  cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
        "4-D float32 with contiguous parameters");
   Tensor x = contig(x_);
   Tensor res;
   if (defined(res_)) {
-    NEED(f32(*res_) && res_->sizes() == x.sizes(), "residual of the input's shape");
+    cover(f32(*res_) && res_->sizes() == x.sizes(), "residual of the input's shape");
     res = contig(*res_);
   }
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
@@ -363,7 +362,7 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_,
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_, const Tensor& x_, const Tensor& y_,
                                                                const Tensor& w, const Tensor& mean,
                                                                const Tensor& invstd, std::array<bool, 3> mask) {
-  NEED(f32(g_) && f32(x_) && f32(y_) && x_.dim() == 4 && whole(w) && whole(mean) && whole(invstd), "4-D float32");
+  cover(f32(g_) && f32(x_) && f32(y_) && x_.dim() == 4 && whole(w) && whole(mean) && whole(invstd), "4-D float32");
   Tensor g = contig(g_), x = contig(x_), y = contig(y_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
@@ -377,13 +376,13 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_,
 }
 static Tensor conv_act_dev(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
                            IntArrayRef padding, int64_t act) {
-  NEED(stride.size() == 2 && padding.size() == 2, "2-D stride and padding");
+  cover(stride.size() == 2 && padding.size() == 2, "2-D stride and padding");
   return conv_forward(x, w, b, stride, padding, {1, 1}, false, 1, act == 1);
 }
 static Tensor conv_bn_act_eval_dev(const Tensor& x, const Tensor& cw_, const std::optional<Tensor>& cb_,
                                    const Tensor& w, const Tensor& b, const Tensor& rm, const Tensor& rv, double eps,
                                    IntArrayRef stride, IntArrayRef padding, int64_t act) {
-  NEED(f32(cw_) && cw_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv) && (!defined(cb_) || f32(*cb_)),
+  cover(f32(cw_) && cw_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv) && (!defined(cb_) || f32(*cb_)),
        "float32 parameters");
   Tensor cw = contig(cw_);
   Tensor cb = defined(cb_) ? contig(*cb_) : Tensor();
@@ -395,41 +394,35 @@ static Tensor conv_bn_act_eval_dev(const Tensor& x, const Tensor& cw_, const std
   return conv_act_dev(x, fw, fb, stride, padding, act);
 }
 
-// fast path, else the composite reference (whose aten ops dispatch to the device kernels or are delegated)
-#define TRY_DEV(dev, ref, ...)          \
-  OMT_LOCK;                             \
-  try {                                 \
-    return dev(__VA_ARGS__);            \
-  } catch (const Unsupported& e) {      \
-    TORCH_CHECK(!strict_mode(), "omarchy-mac-torch (strict): " #dev ": ", e.why); \
-    note_fallback(#dev, e.why);         \
-    return ref(__VA_ARGS__);            \
-  }
-
+// device kernels when they cover the call, else the composite reference (whose aten ops reach the device kernels or
+// torch's)
 static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_k(const Tensor& x, const Tensor& w,
                                                                         const Tensor& b, const Tensor& rm,
                                                                         const Tensor& rv, double mom, double eps) {
-  TRY_DEV(bn_relu_train_dev, bn_relu_train_ref, x, w, b, rm, rv, mom, eps)
+  return dev_or_ref<&bn_relu_train_dev, &bn_relu_train_ref>("omt::bn_relu_train", x, w, b, rm, rv, mom, eps);
 }
 static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_k(const Tensor& x, const Tensor& w, const Tensor& b,
                                                              const Tensor& rm, const Tensor& rv, double mom,
                                                              double eps, int64_t act,
                                                              const std::optional<Tensor>& res) {
-  TRY_DEV(bn_train_inplace_dev, bn_train_inplace_ref, x, w, b, rm, rv, mom, eps, act, res)
+  return dev_or_ref<&bn_train_inplace_dev, &bn_train_inplace_ref>("omt::bn_train_", x, w, b, rm, rv, mom, eps, act,
+                                                                  res);
 }
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_k(const Tensor& g, const Tensor& x, const Tensor& y,
                                                              const Tensor& w, const Tensor& mean,
                                                              const Tensor& invstd, std::array<bool, 3> mask) {
-  TRY_DEV(bn_relu_backward_dev, bn_relu_backward_ref, g, x, y, w, mean, invstd, mask)
+  return dev_or_ref<&bn_relu_backward_dev, &bn_relu_backward_ref>("omt::bn_relu_backward", g, x, y, w, mean, invstd,
+                                                                  mask);
 }
 static Tensor conv_act_k(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef s,
                          IntArrayRef p, int64_t act) {
-  TRY_DEV(conv_act_dev, conv_act_ref, x, w, b, s, p, act)
+  return dev_or_ref<&conv_act_dev, &conv_act_ref>("omt::conv_act", x, w, b, s, p, act);
 }
 static Tensor conv_bn_act_eval_k(const Tensor& x, const Tensor& cw, const std::optional<Tensor>& cb, const Tensor& w,
                                  const Tensor& b, const Tensor& rm, const Tensor& rv, double eps, IntArrayRef s,
                                  IntArrayRef p, int64_t act) {
-  TRY_DEV(conv_bn_act_eval_dev, conv_bn_act_eval_ref, x, cw, cb, w, b, rm, rv, eps, s, p, act)
+  return dev_or_ref<&conv_bn_act_eval_dev, &conv_bn_act_eval_ref>("omt::conv_bn_act_eval", x, cw, cb, w, b, rm, rv,
+                                                                  eps, s, p, act);
 }
 
 TORCH_LIBRARY(omt, m) {
@@ -461,18 +454,19 @@ TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
 }
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
-  OMT_IMPL(m, convolution, convolution_);
-  OMT_IMPL(m, convolution_backward, convolution_backward_);
-  OMT_IMPL(m, native_batch_norm, batch_norm_);
-  OMT_IMPL(m, native_batch_norm_backward, batch_norm_backward_);
-  OMT_IMPL(m, _native_batch_norm_legit, bn_legit);
-  OMT_IMPL(m, _native_batch_norm_legit_no_training, bn_legit_no_training);
-  OMT_IMPL(m, max_pool2d_with_indices, max_pool2d_);
-  OMT_IMPL(m, max_pool2d_with_indices_backward, max_pool2d_backward_);
-  OMT_IMPL(m, avg_pool2d, avg_pool2d_);
-  OMT_IMPL(m, avg_pool2d_backward, avg_pool2d_backward_);
-  OMT_IMPL(m, _adaptive_avg_pool2d, adaptive_avg_pool2d_);
-  OMT_IMPL(m, _adaptive_avg_pool2d_backward, adaptive_avg_pool2d_backward_);
+  HotOps(m)
+      .on<at::_ops::convolution, &convolution_>()
+      .on<at::_ops::convolution_backward, &convolution_backward_>()
+      .on<at::_ops::native_batch_norm, &batch_norm_>()
+      .on<at::_ops::native_batch_norm_backward, &batch_norm_backward_>()
+      .on<at::_ops::_native_batch_norm_legit, &bn_legit>()
+      .on<at::_ops::_native_batch_norm_legit_no_training, &bn_legit_no_training>()
+      .on<at::_ops::max_pool2d_with_indices, &max_pool2d_>()
+      .on<at::_ops::max_pool2d_with_indices_backward, &max_pool2d_backward_>()
+      .on<at::_ops::avg_pool2d, &avg_pool2d_>()
+      .on<at::_ops::avg_pool2d_backward, &avg_pool2d_backward_>()
+      .on<at::_ops::_adaptive_avg_pool2d, &adaptive_avg_pool2d_>()
+      .on<at::_ops::_adaptive_avg_pool2d_backward, &adaptive_avg_pool2d_backward_>();
 }
 
 }  // namespace omt

@@ -19,17 +19,17 @@ struct Lr {
 };
 Lr lr_of(double lr) { return Lr{(float)lr, nullptr}; }
 Lr lr_of(const Tensor& lr) {
-  NEED(lr.numel() == 1, "a one-element lr tensor");
+  cover(lr.numel() == 1, "a one-element lr tensor");
   if (is_dev(lr)) {
-    NEED(f32(lr), "a float32 lr tensor");
+    cover(f32(lr), "a float32 lr tensor");
     return Lr{0.f, fp(lr)};
   }
-  NEED(lr.device().is_cpu(), "lr on the host or this device");
+  cover(lr.device().is_cpu(), "lr on the host or this device");
   return Lr{(float)lr.item<double>(), nullptr};
 }
 const float* dev_scalar(const std::optional<Tensor>& t, const char* what) {
   if (!defined(t)) return nullptr;
-  NEED(is_dev(*t) && f32(*t) && t->numel() == 1, what);
+  cover(is_dev(*t) && f32(*t) && t->numel() == 1, what);
   return fp(*t);
 }
 
@@ -39,15 +39,15 @@ void adam_impl(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorL
                bool maximize, bool decoupled, const std::optional<Tensor>& grad_scale,
                const std::optional<Tensor>& found_inf) {
   const size_t n = p.size();
-  NEED(g.size() == n && m.size() == n && v.size() == n && steps.size() == n && (!amsgrad || vmax.size() == n),
+  cover(g.size() == n && m.size() == n && v.size() == n && steps.size() == n && (!amsgrad || vmax.size() == n),
        "tensor lists of one length");
   std::vector<omt_adam_tensor> ts(n);
   for (size_t i = 0; i < n; ++i) {
-    NEED(dev_f32c(p[i]) && dev_f32c(g[i]) && dev_f32c(m[i]) && dev_f32c(v[i]), "contiguous float32 device tensors");
+    cover(dev_f32c(p[i]) && dev_f32c(g[i]) && dev_f32c(m[i]) && dev_f32c(v[i]), "contiguous float32 device tensors");
     const int64_t k = p[i].numel();
-    NEED(g[i].numel() == k && m[i].numel() == k && v[i].numel() == k, "matching tensor sizes");
-    NEED(is_dev(steps[i]) && f32(steps[i]) && steps[i].numel() == 1, "float32 step counts on the device");
-    if (amsgrad) NEED(dev_f32c(vmax[i]) && vmax[i].numel() == k, "contiguous float32 max_exp_avg_sqs");
+    cover(g[i].numel() == k && m[i].numel() == k && v[i].numel() == k, "matching tensor sizes");
+    cover(is_dev(steps[i]) && f32(steps[i]) && steps[i].numel() == 1, "float32 step counts on the device");
+    if (amsgrad) cover(dev_f32c(vmax[i]) && vmax[i].numel() == k, "contiguous float32 max_exp_avg_sqs");
     ts[i] = omt_adam_tensor{fpm(p[i]), fpm(g[i]), fpm(m[i]), fpm(v[i]), amsgrad ? fpm(vmax[i]) : nullptr,
                             fp(steps[i]), k};
   }
@@ -65,11 +65,11 @@ void sgd_impl(at::TensorList p, at::TensorList g, at::TensorList bufs, double wd
               const std::optional<Tensor>& found_inf) {
   const size_t n = p.size();
   const bool mom = momentum != 0.0;
-  NEED(g.size() == n && (!mom || bufs.size() == n), "tensor lists of one length");
+  cover(g.size() == n && (!mom || bufs.size() == n), "tensor lists of one length");
   std::vector<omt_sgd_tensor> ts(n);
   for (size_t i = 0; i < n; ++i) {
-    NEED(dev_f32c(p[i]) && dev_f32c(g[i]) && g[i].numel() == p[i].numel(), "contiguous float32 device tensors");
-    if (mom) NEED(dev_f32c(bufs[i]) && bufs[i].numel() == p[i].numel(), "contiguous float32 momentum buffers");
+    cover(dev_f32c(p[i]) && dev_f32c(g[i]) && g[i].numel() == p[i].numel(), "contiguous float32 device tensors");
+    if (mom) cover(dev_f32c(bufs[i]) && bufs[i].numel() == p[i].numel(), "contiguous float32 momentum buffers");
     ts[i] = omt_sgd_tensor{fpm(p[i]), fpm(g[i]), mom ? fpm(bufs[i]) : nullptr, p[i].numel()};
   }
   const Lr l = lr_of(lr);
@@ -119,12 +119,13 @@ void fused_sgd_tlr(at::TensorList p, at::TensorList g, at::TensorList bufs, doub
 }  // namespace
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
-  OMT_IMPL(m, _fused_adam_, fused_adam_);
-  OMT_IMPL(m, _fused_adam__tensor_lr, fused_adam_tlr);
-  OMT_IMPL(m, _fused_adamw_, fused_adamw_);
-  OMT_IMPL(m, _fused_adamw__tensor_lr, fused_adamw_tlr);
-  OMT_IMPL(m, _fused_sgd_, fused_sgd_);
-  OMT_IMPL(m, _fused_sgd__tensor_lr, fused_sgd_tlr);
+  HotOps(m)
+      .on<at::_ops::_fused_adam_, &fused_adam_>()
+      .on<at::_ops::_fused_adam__tensor_lr, &fused_adam_tlr>()
+      .on<at::_ops::_fused_adamw_, &fused_adamw_>()
+      .on<at::_ops::_fused_adamw__tensor_lr, &fused_adamw_tlr>()
+      .on<at::_ops::_fused_sgd_, &fused_sgd_>()
+      .on<at::_ops::_fused_sgd__tensor_lr, &fused_sgd_tlr>();
 }
 
 }  // namespace omt

@@ -64,10 +64,10 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
                                         bool input_grad, std::vector<Tensor> params, std::vector<Tensor> rms,
                                         std::vector<Tensor> rvs) {
   OMT_LOCK;
-  NEED(shape.size() == 4, "4-D input");
-  for (auto& t : params) NEED(is_dev(t) && f32(t) && t.is_contiguous(), "plan parameters must be contiguous float32 device tensors");
-  for (auto& t : rms) NEED(is_dev(t) && f32(t) && t.is_contiguous(), "running statistics on the device");
-  for (auto& t : rvs) NEED(is_dev(t) && f32(t) && t.is_contiguous(), "running statistics on the device");
+  cover(shape.size() == 4, "4-D input");
+  for (auto& t : params) cover(is_dev(t) && f32(t) && t.is_contiguous(), "plan parameters must be contiguous float32 device tensors");
+  for (auto& t : rms) cover(is_dev(t) && f32(t) && t.is_contiguous(), "running statistics on the device");
+  for (auto& t : rvs) cover(is_dev(t) && f32(t) && t.is_contiguous(), "running statistics on the device");
   auto P = std::make_shared<Plan>();
   Plan& p = *P;
   p.train = train;
@@ -91,10 +91,10 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
     if (L.kind == "conv" || L.kind == "dw") {
       const bool dw = L.kind == "dw";
       const int64_t co = dw ? c : L.co, ks = L.ks;
-      NEED(L.ci == c && pi < (int)params.size(), "layer channels");
+      cover(L.ci == c && pi < (int)params.size(), "layer channels");
       Tensor out = own(p, {n, co, h, w});
       omt_conv_geo g = conv_geo(n, c, co, h, w, ks, 1, ks / 2);
-      NEED(g.oh == h && g.ow == w, "'same' convolution");
+      cover(g.oh == h && g.ow == w, "'same' convolution");
       Tensor wt = params[pi];
       const float *bm = nullptr, *bv = nullptr, *bg = nullptr, *bb = nullptr;
       if (pend.on) {  // eval: previous BatchNorm + ReLU applied by this conv's loader
@@ -131,7 +131,7 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       c = co;
       ++pi;
     } else if (L.kind == "bn") {
-      NEED(L.ci == c && pi + 1 < (int)params.size() && bi < (int)rms.size(), "layer channels");
+      cover(L.ci == c && pi + 1 < (int)params.size() && bi < (int)rms.size(), "layer channels");
       bool next_conv = false;
       if (li + 1 < layers.size() && g_fold > 0) {
         const PlanLayer& N = layers[li + 1];
@@ -181,7 +181,7 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       ++bi;
       pi += 2;
     } else if (L.kind == "pool" || L.kind == "apool") {
-      NEED(h >= 2 && w >= 2, "2x2 pool over an image smaller than 2x2");
+      cover(h >= 2 && w >= 2, "2x2 pool over an image smaller than 2x2");
       const int64_t oh = h / 2, ow = w / 2;
       Tensor out = own(p, {n, c, oh, ow});
       BackRec r;
@@ -222,10 +222,10 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       cur = out;
       h = w = 1;
     } else {
-      NEED(false, "unknown layer kind " + L.kind);
+      throw NotCovered("unknown layer kind " + L.kind);
     }
   }
-  NEED(!pend.on, "a folded BatchNorm needs a following convolution");
+  cover(!pend.on, "a folded BatchNorm needs a following convolution");
   p.xout = cur;
   p.out_shape = {n, c, h, w};
   if (!train) return P;
@@ -324,7 +324,7 @@ static Tensor plan_forward(Plan& p, const Tensor& x) {
   for (auto& step : p.fwd) step(run, s);
   Tensor out = empty_dev(p.out_shape);
   check(omt_memcpy(fpm(out), fp(p.xout), (size_t)out.numel() * 4, 2, s), "plan: output copy");
-  if (debug_mode()) debug_after("plan.forward");
+  if (debug_mode()) debug_point("plan.forward");
   return out;
 }
 
@@ -344,7 +344,7 @@ static std::pair<std::optional<Tensor>, std::vector<Tensor>> plan_backward(Plan&
     check(omt_memcpy(fpm(t), fp(p.gin), (size_t)t.numel() * 4, 2, s), "plan: input gradient copy");
     gx = t;
   }
-  if (debug_mode()) debug_after("plan.backward");
+  if (debug_mode()) debug_point("plan.backward");
   return {gx, run.grads};
 }
 
@@ -374,8 +374,8 @@ void bind_plans(pybind11::module_& m) {
     }
     try {
       return build_plan(L, shape, train, input_grad, params, rms, rvs);
-    } catch (const Unsupported& e) {
-      throw std::runtime_error(std::string("omarchy-mac-torch: cannot build a fused stack: ") + e.why);
+    } catch (const NotCovered& e) {
+      throw std::runtime_error(std::string("omarchy-mac-torch: cannot build a fused stack: ") + e.what());
     }
   });
   m.def("set_fold", [](int f) { g_fold = f; });

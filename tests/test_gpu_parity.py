@@ -372,42 +372,108 @@ FULL = [
     ("C5_3x3_7", (256, 512, 512, 7, 7, 3, 1, 1)),
     ("C5_1x1_exp_56", (256, 64, 256, 56, 56, 1, 1, 0)),
     ("C5_1x1_red_56", (256, 256, 64, 56, 56, 1, 1, 0)),
+    ("C5_1x1_exp_28", (256, 128, 512, 28, 28, 1, 1, 0)),
+    ("C5_1x1_red_28", (256, 512, 128, 28, 28, 1, 1, 0)),
+    ("C5_1x1_exp_14", (256, 256, 1024, 14, 14, 1, 1, 0)),
+    ("C5_1x1_red_14", (256, 1024, 256, 14, 14, 1, 1, 0)),
     ("C5_1x1_exp_7", (256, 512, 2048, 7, 7, 1, 1, 0)),
+    ("C5_1x1_red_7", (256, 2048, 512, 7, 7, 1, 1, 0)),
 ]
+# (fwd, dgrad, wgrad) plans [tile, K slices] that bench.py's tuner picked for the C5 layers on an MI355X
+BENCH_PLANS = {
+    "C5_3x3_56": ([5, 1], [5, 1], [2, 114]), "C5_3x3_28": ([5, 1], [5, 1], [0, 112]),
+    "C5_3x3_14": ([5, 1], [5, 1], [2, 16]), "C5_3x3_7": ([5, 4], [5, 4], [2, 4]),
+    "C5_1x1_exp_56": ([13, 1], [2, 1], [2, 256]), "C5_1x1_red_56": ([2, 1], [13, 1], [0, 256]),
+    "C5_1x1_exp_28": ([2, 1], [5, 1], [2, 64]), "C5_1x1_red_28": ([5, 1], [2, 1], [0, 64]),
+    "C5_1x1_exp_14": ([5, 1], [5, 1], [0, 16]), "C5_1x1_red_14": ([5, 1], [5, 1], [2, 16]),
+    "C5_1x1_exp_7": ([5, 1], [5, 1], [0, 4]), "C5_1x1_red_7": ([5, 1], [5, 1], [0, 4]),
+}
+FULL_CASES = [(name, shape, mode) for name, shape in FULL for mode in ("model", "tuned", "bench")
+              if mode != "bench" or name in BENCH_PLANS]
 
 
-@pytest.mark.parametrize("name,shape", FULL, ids=[f[0] for f in FULL])
-def test_conv_full_size(cuda, ops, name, shape):
+def block_points(rng, rows, cols, to_flat, br=16, bc=32):
+    """One random point in every br x bc block of a rows x cols GEMM output (every row tile of every plan is a
+    multiple of 16 rows, every column tile and wave tile a multiple of 32 columns, so each output tile and each
+    wave's part of it holds sampled points), mapped to flat tensor indices by to_flat(row, col)."""
+    r0 = np.arange(0, rows, br)
+    c0 = np.arange(0, cols, bc)
+    rr, cc = np.meshgrid(r0, c0, indexing="ij")
+    r = rr.ravel() + rng.integers(0, br, rr.size) % np.minimum(br, rows - rr.ravel())
+    c = cc.ravel() + rng.integers(0, bc, cc.size) % np.minimum(bc, cols - cc.ravel())
+    return to_flat(r.astype(np.int64), c.astype(np.int64))
+
+
+def nchw_flat(n_ch, hw):
+    """GEMM (channel row, pixel column q = n*hw + pix) -> flat index of an [N][n_ch][hw] tensor."""
+    return lambda r, c: ((c // hw) * n_ch + r) * hw + c % hw
+
+
+@pytest.mark.parametrize("name,shape,mode", FULL_CASES, ids=[f"{c[0]}-{c[2]}" for c in FULL_CASES])
+def test_conv_full_size(cuda, ops, name, shape, mode):
+    """A BASELINE full-size layer (config 1 at batch 16, config 5 at batch 256) under one plan per direction: the
+    cost model's ("model"), the tuner's ("tuned", as bench.py tunes before timing) or the plans bench.py's tuner picked
+    on an MI355X ("bench"). Checked against the oracle at sampled points stratified so that every 16 x 32 block of
+    each direction's GEMM output holds a point (grad weight: in both K orders; grad input: every stride phase), which
+    puts points in every output tile and every wave's part of it; every sampled output sums every K slice of a split
+    plan. Plus the float64 adjoint identity <conv(x, w), gy> = <x, dgrad(gy, w)> = <w, wgrad(x, gy)>."""
     n, ci, co, h, w, ks, s, p = shape
-    gen = torch.Generator(device=cuda).manual_seed(1)
-    scale = (ci * ks * ks) ** -0.5
-    x = torch.randn((n, ci, h, w), device=cuda, generator=gen)
-    wt = torch.randn((co, ci, ks, ks), device=cuda, generator=gen) * scale
-    b = torch.rand((co,), device=cuda, generator=gen) * 0.2 - 0.1
-    y = ops.conv2d(x, wt, b, s, p)
-    gy = torch.randn(y.shape, device=cuda, generator=gen) * scale
-    gx = ops.conv2d_dgrad(gy, wt, x.shape, s, p)
-    gw = ops.conv2d_wgrad(x, gy, ks, s, p)
-    torch.cuda.synchronize()
+    xs, ws = (n, ci, h, w), (co, ci, ks, ks)
+    ops.clear_conv_plans()
+    try:
+        if mode == "tuned":
+            for d in ("fwd", "dgrad", "wgrad"):
+                ops.autotune_conv(d, xs, ws, s, p)
+        elif mode == "bench":
+            for d, plan in zip(("fwd", "dgrad", "wgrad"), BENCH_PLANS[name]):
+                ops.set_conv_plan(d, xs, ws, s, p, *plan)
+        plans = {d: ops.conv_plan(d, xs, ws, s, p)[:2] for d in ("fwd", "dgrad", "wgrad")}
+        gen = torch.Generator(device=cuda).manual_seed(1)
+        scale = (ci * ks * ks) ** -0.5
+        x = torch.randn(xs, device=cuda, generator=gen)
+        wt = torch.randn(ws, device=cuda, generator=gen) * scale
+        b = torch.rand((co,), device=cuda, generator=gen) * 0.2 - 0.1
+        y = ops.conv2d(x, wt, b, s, p)
+        gy = torch.randn(y.shape, device=cuda, generator=gen) * scale
+        gx = ops.conv2d_dgrad(gy, wt, xs, s, p)
+        gw = ops.conv2d_wgrad(x, gy, ks, s, p)
+        torch.cuda.synchronize()
+    finally:
+        ops.clear_conv_plans()
+    case = (name, mode, plans)
     # adjoint identity in float64 (bias removed from y)
     yb = (y - b.view(1, -1, 1, 1)).double()
     a1 = (yb * gy.double()).sum().item()
     a2 = (x.double() * gx.double()).sum().item()
     a3 = (wt.double() * gw.double()).sum().item()
     norm = (yb.norm() * gy.double().norm()).item()
-    assert abs(a1 - a2) <= 1e-5 * norm and abs(a1 - a3) <= 1e-5 * norm, (a1, a2, a3, norm)
-    # sampled outputs against the oracle
+    assert abs(a1 - a2) <= 1e-5 * norm and abs(a1 - a3) <= 1e-5 * norm, (case, a1, a2, a3, norm)
     rng = np.random.default_rng(0)
     xh, wh, bh, gyh = host(x), host(wt), host(b), host(gy)
-    pts = rng.integers(0, y.numel(), 3000)
+    oh, ow = y.shape[2], y.shape[3]
+    # forward: rows = output channels, columns = n * oh * ow pixels
+    pts = block_points(rng, co, n * oh * ow, nchw_flat(co, oh * ow))
     ref = orc.conv_fwd_points(xh, wh, pts, bh, s, p)
-    assert orc.rel_l2(host(y).ravel()[pts], ref) <= TOL
-    pts = rng.integers(0, gx.numel(), 3000)
-    ref = orc.conv_dgrad_points(gyh, wh, x.shape, pts, s, p)
-    assert orc.rel_l2(host(gx).ravel()[pts], ref) <= TOL
-    pts = rng.integers(0, gw.numel(), 200)
+    assert orc.rel_l2(host(y).ravel()[pts], ref) <= TOL, case
+    # grad input: rows = input channels, columns = n * h * w pixels, plus points on every stride phase
+    pts = [block_points(rng, ci, n * h * w, nchw_flat(ci, h * w))]
+    for py in range(s if s > 1 else 0):
+        for px in range(s):
+            ys = rng.integers(0, (h - py + s - 1) // s, 256) * s + py
+            xs_ = rng.integers(0, (w - px + s - 1) // s, 256) * s + px
+            pts.append(((rng.integers(0, n, 256) * ci + rng.integers(0, ci, 256)) * h + ys) * w + xs_)
+    pts = np.concatenate(pts)
+    ref = orc.conv_dgrad_points(gyh, wh, xs, pts, s, p)
+    assert orc.rel_l2(host(gx).ravel()[pts], ref) <= TOL, case
+    # grad weight: rows = output channels, columns = taps in the channel-major order (ci, ky, kx) and in the tap-major
+    # order (ky, kx, ci), topped up with random points to at least 2000
+    kk = ks * ks
+    kcols = ci * kk
+    cm = block_points(rng, co, kcols, lambda r, c: r * kcols + c)
+    tm = block_points(rng, co, kcols, lambda r, c: r * kcols + (c % ci) * kk + c // ci)
+    pts = np.concatenate([cm, tm, rng.integers(0, gw.numel(), max(0, 2000 - cm.size - tm.size))])
     ref = orc.conv_wgrad_points(xh, gyh, ks, pts, s, p)
-    assert orc.rel_l2(host(gw).ravel()[pts], ref) <= TOL
+    assert orc.rel_l2(host(gw).ravel()[pts], ref) <= TOL, case
 
 
 # ---- depthwise ----
