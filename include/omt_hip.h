@@ -141,6 +141,15 @@ size_t omt_conv_wgrad_workspace(const omt_conv_geo* g);
 int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Grad weight for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Same plan, kernels and results as omt_conv_wgrad
+ * (bit-identical), but the split-K partials live in a static device array of OMT_NOALLOC_SCRATCH_BYTES that the
+ * library owns, one per GPU, held until the process ends; the call allocates nothing. A plan whose partials exceed
+ * that size returns OMT_INVALID. Calls that overlap on one GPU (different streams without ordering between them) share
+ * the array and race: order them. */
+#define OMT_NOALLOC_SCRATCH_BYTES (64u << 20)
+int omt_conv_wgrad_noalloc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* stream);
+
 /* Grad input and grad weight together: the dense branch of convolution_backward with both outputs requested
  * (csrc/conv.cpp:207-220 calls gemm_grad_input, then gemm_grad_weight). Results are those of omt_conv_dgrad and
  * omt_conv_wgrad (same plans, same summation order). When both plans use 64x64 tiles, the two GEMMs run in one launch,

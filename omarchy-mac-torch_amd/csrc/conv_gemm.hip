@@ -1887,14 +1887,9 @@ static int launch_split_sum(const SplitSum& r, hipStream_t s) {
   return launch_check("split_reduce_kernel");
 }
 
-OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
-                              size_t workspace_bytes, void* stream) {
-  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
-  if (int st = geo_check(g, "omt_conv_wgrad")) return st;
-  const size_t need = omt_conv_wgrad_workspace(g);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
-  hipStream_t s = stream_of(stream);
+// The grad-weight GEMM and its slice sum over a workspace of the plan's size (already checked by the caller).
+static int run_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                     hipStream_t s) {
   WgradArgs a;
   WgradPlan pl;
   const dim3 grid = wgrad_prepare(g, x, gy, gw, workspace, a, pl);
@@ -1904,6 +1899,61 @@ OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float
     wgrad_dispatch<kGeneric>(pl.tile, a, grid, s);
   if (int st = launch_check("conv_wgrad_kernel")) return st;
   return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
+}
+
+OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
+  if (int st = geo_check(g, "omt_conv_wgrad")) return st;
+  const size_t need = omt_conv_wgrad_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
+  return run_wgrad(g, x, gy, gw, workspace, stream_of(stream));
+}
+
+// ---- grad weight without allocation ------------------------------------------------------------------------------
+//
+// omt_conv_wgrad_noalloc keeps the split-K partials in `scratch`, a static device array the library owns: one copy per
+// GPU, allocated with the code object and held until the process ends. Host code never passes `scratch` itself (on the
+// host the name is a stand-in, not a device address): the first call on a device resolves that device's copy with
+// hipGetSymbolAddress, with the device current, and every launch then takes that address. Every partial a slice sum
+// reads was written by the same call's grad-weight launch, so the array needs no clearing; calls that overlap on one
+// GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[OMT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+// The current device's copy of `scratch` (resolved once per device).
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  OMT_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices) return fail(OMT_INVALID, "omt_conv_wgrad_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    OMT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(OMT_DEVICE_ERROR, "omt_conv_wgrad_noalloc: no address for the scratch array on device %d", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_conv_wgrad_noalloc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad_noalloc: null pointer");
+  if (int st = geo_check(g, "omt_conv_wgrad_noalloc")) return st;
+  const size_t need = omt_conv_wgrad_workspace(g);
+  if (need > (size_t)OMT_NOALLOC_SCRATCH_BYTES)
+    return fail(OMT_INVALID,
+                "omt_conv_wgrad_noalloc: the plan's split-K partials need %zu bytes, more than the %zu-byte static "
+                "scratch (use omt_conv_wgrad with a workspace, or a plan with fewer K slices)",
+                need, (size_t)OMT_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need)
+    if (int st = scratch_of_current_device(&ws)) return st;
+  return run_wgrad(g, x, gy, gw, ws, stream_of(stream));
 }
 
 // ---- grad input and grad weight together ------------------------------------------------------------------------

@@ -16,6 +16,7 @@ OMT_OK, OMT_UNSUPPORTED, OMT_OOM, OMT_DEVICE_ERROR, OMT_INVALID = range(5)
 OMT_CONV_NONE, OMT_CONV_DENSE, OMT_CONV_DW, OMT_CONV_DWG = range(4)
 OMT_EPI_BIAS, OMT_EPI_RELU = 1, 2
 OMT_DIR_FWD, OMT_DIR_DGRAD, OMT_DIR_WGRAD = range(3)
+NOALLOC_SCRATCH_BYTES = 64 << 20  # OMT_NOALLOC_SCRATCH_BYTES
 
 
 class ConvGeo(ctypes.Structure):
@@ -108,6 +109,7 @@ SIGNATURES = {
     "omt_conv_dgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_workspace": (SZ, [G]),
     "omt_conv_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_conv_wgrad_noalloc": (I32, [G, VP, VP, VP, VP]),
     "omt_conv_bwd_workspace": (SZ, [G]),
     "omt_conv_bwd": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_num_tiles": (I32, [I32]),

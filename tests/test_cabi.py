@@ -28,6 +28,12 @@ def test_library_exports_every_declared_symbol():
     assert sorted(_lib.SIGNATURES) == names
 
 
+def test_noalloc_scratch_size_matches_the_header():
+    from omarchy_mac_torch import _lib
+    m = re.search(r"#define OMT_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+
+
 def test_geometry_and_kind_table():
     from omarchy_mac_torch import _lib
     g = _lib.conv_geo(16, 3, 64, 224, 224, 11, 4, 2)
