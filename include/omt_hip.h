@@ -75,9 +75,15 @@ int omt_conv_kind(int64_t x_c, int64_t w_o, int64_t kh, int64_t kw, int64_t sh, 
 
 /* ---- device memory and streams (replace the wgpu buffer pool and recorder, csrc/runtime.cpp:177-249, 451-527) --- */
 
-/* Caching allocator with size classes; freed blocks are reused in stream order. Replaces alloc_buf/free_buf
- * (csrc/runtime.cpp:205-231) and the PrivateUse1 Allocator (csrc/device.cpp:18-30). */
+/* Caching allocator with size classes. Replaces alloc_buf/free_buf (csrc/runtime.cpp:205-231) and the PrivateUse1
+ * Allocator (csrc/device.cpp:18-30). A block belongs to the stream it is allocated on (omt_malloc: the HIP null
+ * stream); once freed it is handed out again only to allocations on that stream, so reuse is ordered after every
+ * earlier use there. Work on other streams that uses a block must be declared with omt_record_stream (as torch's
+ * Tensor.record_stream): freeing such a block records an event on each of those streams, and the block is reused only
+ * after all of them have completed. */
 int omt_malloc(void** ptr, size_t bytes);
+int omt_malloc_on(void** ptr, size_t bytes, void* stream);
+int omt_record_stream(void* ptr, void* stream); /* replaces the guard's recordDataPtrOnStream (csrc/device.cpp) */
 int omt_free(void* ptr);
 int omt_empty_cache(void);                 /* csrc/runtime.cpp:233-240 (empty_cache) */
 size_t omt_memory_allocated(void);         /* csrc/runtime.cpp:242 */

@@ -2201,13 +2201,13 @@ struct TuneScratch {
     const size_t xb = (size_t)(g->n * g->ci * g->ih * g->iw) * 4, wb = (size_t)(g->co * g->ci * g->ks * g->ks) * 4,
                  yb = (size_t)(g->n * g->co * g->oh * g->ow) * 4;
     const size_t ob = std::max(xb, std::max(wb, yb));
-    if (int st = omt_malloc(&x, xb)) return st;
-    if (int st = omt_malloc(&w, wb)) return st;
-    if (int st = omt_malloc(&gy, yb)) return st;
-    if (int st = omt_malloc(&o1, ob)) return st;
-    if (int st = omt_malloc(&o2, wb)) return st;
+    if (int st = omt_malloc_on(&x, xb, s)) return st;
+    if (int st = omt_malloc_on(&w, wb, s)) return st;
+    if (int st = omt_malloc_on(&gy, yb, s)) return st;
+    if (int st = omt_malloc_on(&o1, ob, s)) return st;
+    if (int st = omt_malloc_on(&o2, wb, s)) return st;
     if (ws_bytes)
-      if (int st = omt_malloc(&ws, ws_bytes)) return st;
+      if (int st = omt_malloc_on(&ws, ws_bytes, s)) return st;
     if (int st = hip_check(hipMemsetAsync(x, 0, xb, s), "hipMemsetAsync")) return st;
     if (int st = hip_check(hipMemsetAsync(w, 0, wb, s), "hipMemsetAsync")) return st;
     if (int st = hip_check(hipMemsetAsync(gy, 0, yb, s), "hipMemsetAsync")) return st;

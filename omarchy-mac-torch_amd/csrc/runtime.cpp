@@ -2,21 +2,25 @@
 // copies and events.
 //
 // The allocator replaces the reference's wgpu buffer pool (alloc_buf / free_buf, csrc/runtime.cpp:177-249). Blocks
-// are rounded to size classes (512 B granules up to 1 MiB, then 2 MiB granules) and parked in per-size free lists
-// when freed. Because every op of the operator layer runs on one stream, a parked block can be handed out again at
-// once: any later use is ordered after the earlier user's kernels on that stream. Callers that use several streams
-// must synchronize before freeing memory another stream still reads.
+// are rounded to size classes (512 B granules up to 1 MiB, then 2 MiB granules) and parked when freed. Reuse is stream
+// ordered: a block belongs to the stream it was allocated on, and a parked block is handed out again only to an
+// allocation on that same stream, whose later work is ordered after every earlier use of the block there. A block
+// that other streams also used (omt_record_stream, torch's record_stream) is not parked at once when freed: an event
+// is recorded on each of those streams, and the block waits in a pending list until all of them have completed.
 //
 // Graph pools. While a graph is being captured, the memory its kernels touch must stay theirs for every replay. Between
-// omt_graph_pool_begin and omt_graph_pool_end every omt_malloc (from any thread: autograd runs backward on its own
-// thread) is served from that pool: from its own parked blocks, else a block moved over from the general free lists,
-// else hipMalloc. Blocks of a graph pool go back to that pool when freed, never to the general one, until
-// omt_graph_pool_release returns them all (after the graphs that use them are gone).
+// omt_graph_pool_begin and omt_graph_pool_end every allocation (from any thread: autograd runs backward on its own
+// thread) is served from that pool: from its own parked blocks, else a block of the allocating stream moved over from
+// the general free lists, else hipMalloc. Blocks of a graph pool go back to that pool when freed (its replays run in
+// capture order), never to the general one, until omt_graph_pool_release returns them all (after the graphs that use
+// them are gone).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "omt_internal.h"
@@ -55,22 +59,40 @@ hipStream_t stream_of(void* s) { return (hipStream_t)s; }
 // ---- caching allocator -----------------------------------------------------------------------------------------
 
 namespace {
+struct Block {
+  size_t cls = 0;
+  hipStream_t stream = nullptr;      // the stream it was allocated on
+  std::vector<hipStream_t> uses;     // other streams that used it (omt_record_stream)
+};
+
+using FreeKey = std::pair<hipStream_t, size_t>;  // (stream, size class)
+
 struct GraphPool {
-  std::map<size_t, std::vector<void*>> free_lists;  // parked blocks of this pool
-  std::unordered_map<void*, size_t> owned;           // every block of this pool -> size class
+  std::map<FreeKey, std::vector<void*>> free_lists;  // parked blocks of this pool
+  std::unordered_map<void*, size_t> owned;            // every block of this pool -> size class
+};
+
+// A freed block whose other-stream uses may still be queued: parked once every event has completed.
+struct Pending {
+  void* p;
+  size_t cls;
+  hipStream_t stream;
+  std::vector<hipEvent_t> events;  // empty: a use stream was capturing; released at the next device synchronization
 };
 
 struct Pool {
   std::mutex mu;
-  std::map<size_t, std::vector<void*>> free_lists;  // size class -> parked blocks
-  std::unordered_map<void*, size_t> live;            // block -> size class
+  std::map<FreeKey, std::vector<void*>> free_lists;  // (stream, size class) -> parked blocks
+  std::unordered_map<void*, Block> live;              // block -> its record
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> spare_events;
   std::map<int, GraphPool> graph_pools;
-  std::unordered_map<void*, int> graph_owner;        // block of a graph pool -> pool id
-  int active = 0;                                    // graph pool receiving allocations (0: none)
+  std::unordered_map<void*, int> graph_owner;         // block of a graph pool -> pool id
+  int active = 0;                                     // graph pool receiving allocations (0: none)
   int next_id = 1;
-  size_t allocated = 0;                              // bytes handed out
-  size_t reserved = 0;                               // bytes held from HIP (live + parked)
-  size_t limit = 0;                                  // 0 = no cap
+  size_t allocated = 0;                               // bytes handed out
+  size_t reserved = 0;                                // bytes held from HIP (live + parked + pending)
+  size_t limit = 0;                                   // 0 = no cap
 
   static size_t size_class(size_t bytes) {
     if (bytes == 0) bytes = 1;
@@ -79,13 +101,59 @@ struct Pool {
     return (bytes + big - 1) / big * big;
   }
 
+  // Parks the pending blocks whose events have all completed (caller holds mu). hipEventQuery is a prohibited call
+  // while a thread captures in global mode, so the calling thread switches to relaxed mode around the queries.
+  void collect_pending() {
+    if (pending.empty()) return;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    for (size_t i = 0; i < pending.size();) {
+      Pending& q = pending[i];
+      bool done = !q.events.empty();
+      for (hipEvent_t e : q.events) done = done && hipEventQuery(e) == hipSuccess;
+      (void)hipGetLastError();  // a not-ready query leaves hipErrorNotReady behind
+      if (!done) {
+        ++i;
+        continue;
+      }
+      for (hipEvent_t e : q.events) spare_events.push_back(e);
+      free_lists[{q.stream, q.cls}].push_back(q.p);
+      pending[i] = pending.back();
+      pending.pop_back();
+    }
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+  }
+
+  // After a device synchronization: every pending block is idle; park them all (caller holds mu).
+  void settle_pending() {
+    for (Pending& q : pending) {
+      for (hipEvent_t e : q.events) spare_events.push_back(e);
+      free_lists[{q.stream, q.cls}].push_back(q.p);
+    }
+    pending.clear();
+  }
+
   void release_parked() {  // caller holds mu
     for (auto& kv : free_lists)
       for (void* p : kv.second) {
         (void)hipFree(p);
-        reserved -= kv.first;
+        reserved -= kv.first.second;
       }
     free_lists.clear();
+  }
+
+  hipEvent_t take_event() {
+    if (!spare_events.empty()) {
+      hipEvent_t e = spare_events.back();
+      spare_events.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    return e;
   }
 };
 Pool& pool() {
@@ -102,6 +170,15 @@ hipError_t malloc_relaxed(void** p, size_t bytes) {
   (void)hipThreadExchangeStreamCaptureMode(&mode);
   return e;
 }
+
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return st != hipStreamCaptureStatusNone;
+}
 }  // namespace
 
 }  // namespace omt
@@ -116,33 +193,41 @@ OMT_EXPORT int omt_hip_runtime_version(void) {
   return v;
 }
 
-OMT_EXPORT int omt_malloc(void** ptr, size_t bytes) {
+OMT_EXPORT int omt_malloc_on(void** ptr, size_t bytes, void* stream) {
   if (!ptr) return fail(OMT_INVALID, "omt_malloc: null out-pointer");
   Pool& P = pool();
-  size_t cls = Pool::size_class(bytes);
+  const size_t cls = Pool::size_class(bytes);
+  const hipStream_t s = stream_of(stream);
+  const FreeKey key{s, cls};
   std::lock_guard<std::mutex> lk(P.mu);
+  P.collect_pending();
   GraphPool* gp = P.active ? &P.graph_pools[P.active] : nullptr;
+  auto hand_out = [&](void* p) {
+    Block b;
+    b.cls = cls;
+    b.stream = s;
+    P.live[p] = std::move(b);
+    P.allocated += cls;
+    *ptr = p;
+    return OMT_OK;
+  };
   if (gp) {
-    auto git = gp->free_lists.find(cls);
+    auto git = gp->free_lists.find(key);
     if (git != gp->free_lists.end() && !git->second.empty()) {
-      *ptr = git->second.back();
+      void* p = git->second.back();
       git->second.pop_back();
-      P.live[*ptr] = cls;
-      P.allocated += cls;
-      return OMT_OK;
+      return hand_out(p);
     }
   }
-  auto it = P.free_lists.find(cls);
+  auto it = P.free_lists.find(key);
   if (it != P.free_lists.end() && !it->second.empty()) {
-    *ptr = it->second.back();
+    void* p = it->second.back();
     it->second.pop_back();
-    P.live[*ptr] = cls;
-    P.allocated += cls;
     if (gp) {
-      gp->owned[*ptr] = cls;
-      P.graph_owner[*ptr] = P.active;
+      gp->owned[p] = cls;
+      P.graph_owner[p] = P.active;
     }
-    return OMT_OK;
+    return hand_out(p);
   }
   void* p = nullptr;
   bool over = P.limit && P.reserved + cls > P.limit;
@@ -165,13 +250,24 @@ OMT_EXPORT int omt_malloc(void** ptr, size_t bytes) {
     return fail(OMT_OOM, "out of device memory allocating %zu bytes in a graph pool", cls);
   }
   P.reserved += cls;
-  P.allocated += cls;
-  P.live[p] = cls;
   if (gp) {
     gp->owned[p] = cls;
     P.graph_owner[p] = P.active;
   }
-  *ptr = p;
+  return hand_out(p);
+}
+
+OMT_EXPORT int omt_malloc(void** ptr, size_t bytes) { return omt_malloc_on(ptr, bytes, nullptr); }
+
+OMT_EXPORT int omt_record_stream(void* ptr, void* stream) {
+  if (!ptr) return OMT_OK;
+  Pool& P = pool();
+  const hipStream_t s = stream_of(stream);
+  std::lock_guard<std::mutex> lk(P.mu);
+  auto it = P.live.find(ptr);
+  if (it == P.live.end()) return fail(OMT_INVALID, "omt_record_stream: %p was not allocated by omt_malloc", ptr);
+  Block& b = it->second;
+  if (s != b.stream && std::find(b.uses.begin(), b.uses.end(), s) == b.uses.end()) b.uses.push_back(s);
   return OMT_OK;
 }
 
@@ -181,14 +277,39 @@ OMT_EXPORT int omt_free(void* ptr) {
   std::lock_guard<std::mutex> lk(P.mu);
   auto it = P.live.find(ptr);
   if (it == P.live.end()) return fail(OMT_INVALID, "omt_free: %p was not allocated by omt_malloc", ptr);
-  size_t cls = it->second;
+  Block b = std::move(it->second);
   P.live.erase(it);
-  P.allocated -= cls;
+  P.allocated -= b.cls;
   auto g = P.graph_owner.find(ptr);
-  if (g != P.graph_owner.end())
-    P.graph_pools[g->second].free_lists[cls].push_back(ptr);
-  else
-    P.free_lists[cls].push_back(ptr);
+  if (g != P.graph_owner.end()) {  // a graph pool's replays run in capture order: back to the pool as it is
+    P.graph_pools[g->second].free_lists[{b.stream, b.cls}].push_back(ptr);
+    return OMT_OK;
+  }
+  if (b.uses.empty()) {
+    P.free_lists[{b.stream, b.cls}].push_back(ptr);
+    return OMT_OK;
+  }
+  Pending q{ptr, b.cls, b.stream, {}};
+  bool ok = true;
+  for (hipStream_t u : b.uses) {
+    if (capturing(u)) {  // an event recorded now would become a graph node: wait for a device synchronization
+      ok = false;
+      break;
+    }
+    hipEvent_t e = P.take_event();
+    if (!e || hipEventRecord(e, u) != hipSuccess) {
+      (void)hipGetLastError();
+      if (e) P.spare_events.push_back(e);
+      ok = false;
+      break;
+    }
+    q.events.push_back(e);
+  }
+  if (!ok) {
+    for (hipEvent_t e : q.events) P.spare_events.push_back(e);
+    q.events.clear();
+  }
+  P.pending.push_back(std::move(q));
   return OMT_OK;
 }
 
@@ -223,6 +344,7 @@ OMT_EXPORT int omt_graph_pool_release(int id) {
   if (it == P.graph_pools.end()) return fail(OMT_INVALID, "omt_graph_pool_release: no graph pool %d", id);
   if (P.active == id) return fail(OMT_INVALID, "omt_graph_pool_release: pool %d is receiving allocations", id);
   OMT_HIP(hipDeviceSynchronize());  // no replay may still use the blocks
+  P.settle_pending();
   for (auto& kv : it->second.free_lists)
     for (void* b : kv.second) P.free_lists[kv.first].push_back(b);
   for (auto& kv : it->second.owned) P.graph_owner.erase(kv.first);  // live blocks return to the general pool when freed
@@ -233,7 +355,8 @@ OMT_EXPORT int omt_graph_pool_release(int id) {
 OMT_EXPORT int omt_empty_cache(void) {
   Pool& P = pool();
   std::lock_guard<std::mutex> lk(P.mu);
-  OMT_HIP(hipDeviceSynchronize());  // parked blocks may still be read by queued kernels
+  OMT_HIP(hipDeviceSynchronize());  // parked and pending blocks may still be used by queued kernels
+  P.settle_pending();
   P.release_parked();
   return OMT_OK;
 }

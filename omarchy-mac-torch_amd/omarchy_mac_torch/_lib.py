@@ -84,6 +84,8 @@ SIGNATURES = {
     "omt_conv_geo_init": (None, [G, I64, I64, I64, I64, I64, I64, I64, I64]),
     "omt_conv_kind": (I32, [I64] * 10 + [I32, I64]),
     "omt_malloc": (I32, [ctypes.POINTER(VP), SZ]),
+    "omt_malloc_on": (I32, [ctypes.POINTER(VP), SZ, VP]),
+    "omt_record_stream": (I32, [VP, VP]),
     "omt_free": (I32, [VP]),
     "omt_empty_cache": (I32, []),
     "omt_memory_allocated": (SZ, []),

@@ -6,6 +6,7 @@
 #include <ATen/hip/HIPGeneratorImpl.h>
 #include <ATen/native/Resize.h>
 #include <c10/core/impl/DeviceGuardImplInterface.h>
+#include <c10/hip/HIPCachingAllocator.h>
 #include <c10/hip/HIPStream.h>
 
 #include <cstdlib>
@@ -27,11 +28,11 @@ struct Allocator final : c10::Allocator {
   c10::DataPtr allocate(size_t n) override {
     void* p = nullptr;
     if (n) {
-      int st = omt_malloc(&p, n);
+      void* s = cur_stream();
+      int st = omt_malloc_on(&p, n, s);
       if (st == OMT_OOM) {
-        c10::hip::getCurrentHIPStream().synchronize();  // parked blocks may be in use by queued work
-        omt_empty_cache();
-        st = omt_malloc(&p, n);
+        omt_empty_cache();  // synchronizes the device: parked and pending blocks of every stream become free
+        st = omt_malloc_on(&p, n, s);
       }
       TORCH_CHECK_WITH(OutOfMemoryError, st != OMT_OOM, "omarchy-mac-torch: out of device memory: ", omt_last_error());
       TORCH_CHECK(st == OMT_OK, "omarchy-mac-torch: allocation failed: ", omt_last_error());
@@ -314,6 +315,25 @@ static c10::hip::HIPStream as_hip_stream(const c10::Stream& s) {
   return c10::hip::HIPStream::unpack3(s.id(), 0, c10::DeviceType::HIP);
 }
 
+// The block behind `dp` is not reused before the work queued on `hs` so far has completed. Storage adopted from
+// torch's HIP allocator (results of delegated ops) is that allocator's to track.
+static void record_on_stream(const c10::DataPtr& dp, const c10::hip::HIPStream& hs) {
+  if (!dp.get()) return;
+  if (dp.get_deleter() == &release_keep) {
+    const auto* keep = static_cast<const Keep*>(dp.get_context());
+    c10::hip::HIPCachingAllocator::recordStream(keep->s.data_ptr(), hs);
+    return;
+  }
+  TORCH_CHECK(omt_record_stream(dp.get(), hs.stream()) == OMT_OK, "omarchy-mac-torch: ", omt_last_error());
+}
+
+// aten::record_stream for device tensors; the stream may be one of this device's or the torch HIP stream it wraps.
+static void record_stream_dev(at::Tensor& self, c10::Stream s) {
+  const c10::hip::HIPStream hs = s.device_type() == kDev ? as_hip_stream(s)
+                                                         : c10::hip::HIPStream(c10::hip::HIPStream::UNCHECKED, s);
+  record_on_stream(self.storage().data_ptr(), hs);
+}
+
 struct Guard final : c10::impl::DeviceGuardImplInterface {
   c10::DeviceType type() const override { return kDev; }
   c10::Device exchangeDevice(c10::Device) const override { return {kDev, 0}; }
@@ -358,7 +378,10 @@ struct Guard final : c10::impl::DeviceGuardImplInterface {
     TORCH_CHECK(omt_event_elapsed_ms(start, end, &ms) == OMT_OK, omt_last_error());
     return ms;
   }
-  void recordDataPtrOnStream(const c10::DataPtr&, const c10::Stream&) const override {}
+  // autograd's cross-stream uses of a gradient (and Tensor.record_stream, below): see record_on_stream
+  void recordDataPtrOnStream(const c10::DataPtr& dp, const c10::Stream& s) const override {
+    record_on_stream(dp, as_hip_stream(s));
+  }
 };
 C10_REGISTER_GUARD_IMPL(PrivateUse1, Guard);
 
@@ -402,6 +425,7 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("set_.source_Storage_storage_offset", &set_storage);
   m.impl("set_.source_Storage", &at::native::set_);
   m.impl("resize_", &resize_dev_);
+  m.impl("record_stream", &record_stream_dev);
   // views share the device storage: metadata-only kernels, never delegated
   m.impl("view", &at::native::view);
   m.impl("_unsafe_view", &at::native::_unsafe_view);

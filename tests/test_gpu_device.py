@@ -646,3 +646,45 @@ def test_debug_mode_synchronizes_each_op_and_names_it(clean):
     finally:
         core.set_debug(False)
     assert y.shape == (64, 64, 56, 56)
+
+
+def test_allocator_reuse_is_stream_ordered(clean):
+    """A freed block goes back only to allocations on the stream it was allocated on; a block that another stream used
+    (Tensor.record_stream, reaching the device guard's recordDataPtrOnStream) is not handed out again until the work
+    queued on that stream has completed, so a new allocation cannot overwrite memory a queued kernel still reads."""
+    omt = clean
+    dev = omt.DEVICE
+    n = (8 << 20) // 4
+    main = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    # freed on the main stream: not handed to the side stream, handed back to the main stream
+    t = torch.empty(n, device=dev)
+    p = t.data_ptr()
+    del t
+    with torch.cuda.stream(side):
+        u = torch.empty(n, device=dev)
+    assert u.data_ptr() != p
+    v = torch.empty(n, device=dev)
+    assert v.data_ptr() == p
+    del u, v
+    torch.cuda.synchronize()
+    # used on the side stream behind a long queue, then freed on the main stream
+    x, w = D(torch.randn(64, 64, 56, 56), omt), D(torch.randn(64, 64, 3, 3), omt)
+    t = torch.full((n,), 3.0, device=dev)
+    p = t.data_ptr()
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        for _ in range(30):
+            F.conv2d(x, w, padding=1)
+        s = t * 2.0
+    t.record_stream(side)
+    del t
+    z = torch.empty(n, device=dev)  # main stream, while the side stream may still read the old block
+    assert z.data_ptr() != p
+    z.fill_(-1.0)
+    main.wait_stream(side)
+    torch.cuda.synchronize()
+    assert bool((s == 6.0).all())
+    y = torch.empty(n, device=dev)  # the side stream's work is done: the block is the main stream's again
+    assert y.data_ptr() == p
