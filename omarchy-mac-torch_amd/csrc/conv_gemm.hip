@@ -60,7 +60,9 @@ constexpr int kTileGroup = 8;
 
 __device__ __forceinline__ float f4get(const float4& v, int s) { return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w; }
 
-enum { kGeneric = 0, kTapMajor = 1 };
+// Gather K orders: channel-major (generic), tap-major over a re-packed filter, tap-major reading the filter in place
+// (grad weight uses the first two).
+enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2 };
 
 struct Phase {
   int KH, KW, S, PH, PW;  // gather window, stride and (signed) padding
@@ -90,7 +92,11 @@ struct GatherArgs {
   int d2s, d2s_ci;       // grad input as one super-pixel GEMM: its stride (0: off) and the grad-input channels;
   int d2s_h, d2s_w;      //   the grad-input image (YH x YW is then the super-pixel grid, as its K-split partials)
   int wdirect;           // grad input, channel-major: A[ci][(co, a', b')] read from w[co][ci][ks][ks] (no re-pack)
-  int ks, s;             //   the filter size and stride for that read
+  int ks, s;             //   the filter size and stride for that read (and for wplace 2)
+  int wplace;            // tap-major order with the filter read in place: 1 forward, A[co][(tap, ci)] from
+                         //   w[co][ci][ky][kx]; 2 grad input, A[ci][(a', b', co)] from w[co][ci][ky][kx] through the
+                         //   phase's flip map (ky = ky0 + s (KH - 1 - a')); 0 the [P][K] filter at w (re-packed)
+  uint32_t w_rowst, w_cst;  // wplace: bytes between A rows and between consecutive channels of one tap
   float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
   int64_t part_stride;   // elements per slice
   Phase ph[kMaxPhases];
@@ -284,21 +290,45 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   // one 16-byte load (a multi-dword buffer load needs 4-byte alignment only, so a filter used in place may sit
   // anywhere) and stores them with one b128 LDS write: element e = t + NT i of the tile's BP x BK / 4 runs is row
   // e / (BK / 4), k 4 (e % (BK / 4)).
-  constexpr bool A4 = MODE == kTapMajor && BP * BK >= 4 * NT;
+  // With the filter read in place (a.wplace) a run is four channels of one tap, w_cst bytes apart: four 4-byte loads
+  // whose block-uniform part (first channel, tap) travels in the scalar offset.
+  constexpr bool TAP = MODE != kGeneric;  // tap-major K order
+  constexpr bool A4 = TAP && BP * BK >= 4 * NT;
   constexpr int AR4 = A4 ? BP * BK / (4 * NT) : 1, KQ = BK / 4;
   uint32_t aoff4[AR4];
 #pragma unroll
   for (int i = 0; i < AR4; ++i) {
     const int e = t + NT * i, p = p0 + e / KQ;
-    aoff4[i] = p < P ? (uint32_t)((woff + p * K + 4 * (e % KQ)) * 4) : kOOB;
+    if (MODE == kTapInPlace)
+      aoff4[i] = p < P ? (uint32_t)p * a.w_rowst + (uint32_t)(4 * (e % KQ)) * a.w_cst : kOOB;
+    else
+      aoff4[i] = p < P ? (uint32_t)((woff + p * K + 4 * (e % KQ)) * 4) : kOOB;
   }
 
   float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
   float4 ra4[PF][AR4];
   auto gload = [&](int k0, const int set) {
     if constexpr (A4) {
+      if constexpr (MODE == kTapInPlace) {
+        // this K-block: its channels at tap (nky, nkx) of the gather window (the B loader below advances them).
+        // Look-ahead blocks past the last tap, and phases no tap reaches (their values are never used), read filter
+        // tap (0, 0), so that every address stays inside the filter: nc0 < C always, and a window tap maps into
+        // [0, ks) x [0, ks) (ky0 + s (KH - 1) < ks by the phase's window).
+        int tky = 0, tkx = 0;
+        if (nky < KH && ph.K > 0) {
+          tky = a.wplace == 1 ? nky : ph.ky0 + a.s * (KH - 1 - nky);
+          tkx = a.wplace == 1 ? nkx : ph.kx0 + a.s * (KW - 1 - nkx);
+        }
+        // nc0 is the channel of this thread's first k-row (k0 + rbase, one tap per block): the block starts rbase back
+        const uint32_t sb = (uint32_t)(nc0 - rbase) * a.w_cst + (uint32_t)((tky * a.ks + tkx) * 4);
 #pragma unroll
-      for (int i = 0; i < AR4; ++i) ra4[set][i] = bload4(wr, aoff4[i] + (uint32_t)(k0 * 4), 0);
+        for (int i = 0; i < AR4; ++i)
+          ra4[set][i] = make_float4(bload(wr, aoff4[i], sb), bload(wr, aoff4[i], sb + a.w_cst),
+                                    bload(wr, aoff4[i], sb + 2 * a.w_cst), bload(wr, aoff4[i], sb + 3 * a.w_cst));
+      } else {
+#pragma unroll
+        for (int i = 0; i < AR4; ++i) ra4[set][i] = bload4(wr, aoff4[i] + (uint32_t)(k0 * 4), 0);
+      }
     } else {
 #pragma unroll
     for (int i = 0; i < AR; ++i) {
@@ -313,12 +343,12 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       } else {
         // tap-major K-blocks are all whole (C, and so K, is a multiple of BK): no K-tail test
         off = aoff[i] + (uint32_t)(k0 * 4);
-        if (MODE != kTapMajor && k >= K) off = kOOB;
+        if (!TAP && k >= K) off = kOOB;
       }
       ra[set][i] = bload(wr, off, 0);
     }
     }
-    if (MODE == kTapMajor) {
+    if (TAP) {
       // k = tap * C + c with C % BK == 0: this thread's BR rows share one tap and K has no tail
       const int c0 = nc0, ky = nky, kx = nkx;
       nc0 += BK;
@@ -391,7 +421,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
 
   const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;  // an empty slice still writes its (zero) tile
-  if (MODE == kTapMajor) {
+  if (TAP) {
     const uint32_t kb = (uint32_t)(kbeg + rbase);
     const int tap = (int)fdiv(kb, a.div_c);
     nc0 = (int)kb - tap * a.C;
@@ -1265,11 +1295,19 @@ static const Tile kGatherTiles[] = {
     {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3}, {64, 64, 32, 32, 0.90f, 32, 3},
     {64, 128, 32, 64, 0.97f, 32, 2}, {64, 128, 32, 64, 0.95f, 16, 0, 1},
 };
-// Plan tile index t < 2 * kNGather: kGatherTiles[t % kNGather], and t >= kNGather forces the channel-major K order
-// (no filter re-pack, one launch fewer; the tap-major order gathers faster on large layers).
+// Plan tile index t < 3 * kNGather: kGatherTiles[t % kNGather] in one of three variants. t < kNGather: tap-major K
+// order where it applies, over a re-packed filter; kNGather <= t < 2 kNGather: channel-major order (no filter
+// re-pack, one launch fewer; the tap-major order gathers faster on large layers); t >= 2 kNGather: tap-major order
+// reading the filter in place (no re-pack launch, four 4-byte filter loads per run of four k instead of one 16-byte
+// load), on tiles whose filter tile has whole runs per thread (BP BK >= 1024) and that are not the 1x1 streaming
+// tile; elsewhere it runs as the first variant.
 constexpr int kNGather = (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0]));
 static const Tile& gtile(int t) { return kGatherTiles[t % kNGather]; }
-static bool gcm(int t) { return t >= kNGather; }
+static bool gcm(int t) { return t >= kNGather && t < 2 * kNGather; }
+static bool wplace_tile(int t) {
+  const Tile& tl = gtile(t);
+  return t >= 2 * kNGather && !tl.stream && tl.bp * tl.bk >= 1024;
+}
 
 static const Tile kWgradTiles[] = {
     {64, 128, 32, 64, 1.00f}, {128, 64, 32, 64, 1.00f}, {64, 64, 32, 32, 0.85f}, {32, 128, 16, 64, 0.85f},
@@ -1294,6 +1332,20 @@ static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t 
     case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 11: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     default: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+  }
+}
+// Tap-major tiles reading the filter in place (wplace_tile: whole runs of four k per thread, not the streaming tile);
+// the direct-to-LDS tiles run as the staged kernel of their shape, as in gather_dispatch.
+static void gather_inplace_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
+  constexpr int M = kTapInPlace;
+  switch (ti) {
+    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 2: case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 7: case 12: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;  // 5, 9, 11
   }
 }
 static void gather_dl_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
@@ -1385,11 +1437,11 @@ static dim3 gather_grid(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t 
 // 16-byte aligned); anywhere else its plan runs as the staged tile of the same shape and K-block (tile 2).
 static bool stream_ok(const GatherArgs& a, const GatherPlan& pl) {
   const Phase& p = a.ph[0];
-  return !gcm(pl.tile) && pl.slices == 1 && !a.bn_mean && !a.wdirect && p.KH == 1 && p.KW == 1 && p.S == 1 &&
+  return !gcm(pl.tile) && pl.slices == 1 && !a.bn_mean && !a.wdirect && !a.wplace && p.KH == 1 && p.KW == 1 && p.S == 1 &&
          p.PH == 0 && p.PW == 0 && p.K % 16 == 0 && rows_ok(a, false);
 }
 static GatherPlan eff_plan(const GatherArgs& a, GatherPlan pl) {
-  if (gtile(pl.tile).stream && !stream_ok(a, pl)) pl.tile = (gcm(pl.tile) ? kNGather : 0) + 2;
+  if (gtile(pl.tile).stream && !stream_ok(a, pl)) pl.tile = pl.tile - pl.tile % kNGather + 2;
   return pl;
 }
 // Tap-major K order of a gather launch (the BN loader keeps the channel-major order).
@@ -1436,6 +1488,8 @@ static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t 
   }
   if (a.bn_mean)
     gather_dispatch<kGeneric, true>(pl.tile % kNGather, a, grid, s);
+  else if (a.wplace)
+    gather_inplace_dispatch(pl.tile % kNGather, a, grid, s);
   else if (gather_uses_tap_major(a, pl) && gtile(pl.tile).ns && (uintptr_t)a.w % 16 == 0 && !a.d2s)
     gather_dl_dispatch(pl.tile % kNGather, a, grid, s);
   else if (gather_uses_tap_major(a, pl))
@@ -1525,7 +1579,7 @@ static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p) {
   return true;
 }
 static int num_tiles(int dir) {
-  return dir == OMT_DIR_WGRAD ? (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0])) : 2 * kNGather;
+  return dir == OMT_DIR_WGRAD ? (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0])) : 3 * kNGather;
 }
 
 }  // namespace omt
@@ -1540,7 +1594,8 @@ static GatherPlan fwd_plan(const omt_conv_geo* g) {
 // Forward workspace: the tap-major filter (when the plan's K-block divides C and ks > 1), then, 256-byte aligned,
 // the split-K partials.
 static size_t fwd_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
-  if (g->ks == 1 || gcm(pl.tile) || !gather_tap_major(g->ci, false, gtile(pl.tile).bk)) return 0;
+  if (g->ks == 1 || gcm(pl.tile) || wplace_tile(pl.tile) || !gather_tap_major(g->ci, false, gtile(pl.tile).bk))
+    return 0;
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
@@ -1577,6 +1632,12 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
                        (int)g->co, (int)g->ci, (int)(g->ks * g->ks));
     if (int st = launch_check("pack_tapmajor_kernel")) return st;
     a.w = (const float*)workspace;
+  }
+  if (!bn && g->ks > 1 && wplace_tile(pl.tile) && gather_tap_major(g->ci, false, gtile(pl.tile).bk)) {
+    a.wplace = 1;  // A[co][(ky, kx, ci)] = w[co][ci][ky][kx]
+    a.ks = (int)g->ks;
+    a.w_rowst = (uint32_t)(g->ci * g->ks * g->ks * 4);
+    a.w_cst = (uint32_t)(g->ks * g->ks * 4);
   }
   a.bias = (epilogue & OMT_EPI_BIAS) ? bias : nullptr;
   a.bn_mean = bn ? bn_mean : nullptr;
@@ -1724,7 +1785,7 @@ static size_t dgrad_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
     d2s_window(g, L, PH);
     return (size_t)(g->stride * g->stride * g->ci * g->co * L * L) * sizeof(float);
   }
-  if (gcm(pl.tile) || !gather_tap_major(g->co, false, gtile(pl.tile).bk)) return 0;
+  if (gcm(pl.tile) || wplace_tile(pl.tile) || !gather_tap_major(g->co, false, gtile(pl.tile).bk)) return 0;
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
@@ -1789,9 +1850,15 @@ static int dgrad_prepare(const omt_conv_geo* g, const float* gy, const float* w,
   } else {
     a.w = w;
     a.w_bytes = (uint32_t)(g->co * g->ci * g->ks * g->ks * 4);
-    a.wdirect = 1;
     a.ks = (int)g->ks;
     a.s = (int)g->stride;
+    if (wplace_tile(pl.tile) && gather_tap_major(g->co, false, gtile(pl.tile).bk)) {
+      a.wplace = 2;  // A[ci][(a', b', co)] = w[co][ci][ky0 + s (KH - 1 - a')][kx0 + s (KW - 1 - b')]
+      a.w_rowst = (uint32_t)(g->ks * g->ks * 4);
+      a.w_cst = (uint32_t)(g->ci * g->ks * g->ks * 4);
+    } else {
+      a.wdirect = 1;
+    }
   }
   a.x = gy;
   a.y = gx;
@@ -2008,7 +2075,14 @@ OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* 
   const bool deep = gtile(dp.tile).bk == 64;
   const dim3 grid((unsigned)blocks);
 #define OMT_DUAL(BK, GM, WM) hipLaunchKernelGGL((conv_bwd_dual_kernel<BK, GM, WM>), grid, dim3(256), 0, s, ga, wa, d)
-  switch ((deep ? 4 : 0) + (gtap ? 2 : 0) + (wtap ? 1 : 0)) {
+  if (ga.wplace) {
+    switch ((deep ? 2 : 0) + (wtap ? 1 : 0)) {
+      case 3: OMT_DUAL(64, kTapInPlace, kTapMajor); break;
+      case 2: OMT_DUAL(64, kTapInPlace, kGeneric); break;
+      case 1: OMT_DUAL(16, kTapInPlace, kTapMajor); break;
+      default: OMT_DUAL(16, kTapInPlace, kGeneric); break;
+    }
+  } else switch ((deep ? 4 : 0) + (gtap ? 2 : 0) + (wtap ? 1 : 0)) {
     case 7: OMT_DUAL(64, kTapMajor, kTapMajor); break;
     case 6: OMT_DUAL(64, kTapMajor, kGeneric); break;
     case 5: OMT_DUAL(64, kGeneric, kTapMajor); break;
@@ -2161,10 +2235,15 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
   }
   // the 1x1 streaming tile: one 1x1 stride-1 unpadded phase with whole K-blocks, tap-major order, no split
   const bool stream_geo = g->ks == 1 && g->stride == 1 && g->pad == 0 && K % 16 == 0 && (g->ih * g->iw) % 4 == 0;
+  // the in-place filter variant differs from the re-packing one only where a re-pack would run: tap-major order
+  // (C a multiple of the K-block), no super-pixel grad input, a filter larger than 1x1 in the forward
+  const int64_t gather_c = dir == OMT_DIR_FWD ? g->ci : g->co;
+  const bool packs = !(dir == OMT_DIR_FWD && g->ks == 1) && !(dir == OMT_DIR_DGRAD && dgrad_d2s(g));
   for (int t = 0; t < ntile; ++t) {
     const Tile& tl = gtile(t);
+    if (t >= 2 * kNGather && !(wplace_tile(t) && packs && gather_tap_major(gather_c, false, tl.bk))) continue;
     if (tl.stream) {
-      if (stream_geo && !gcm(t)) out.push_back({t, 1});
+      if (stream_geo && t < kNGather) out.push_back({t, 1});
       continue;
     }
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(std::max<int64_t>(K, 1), tl.bk);

@@ -82,16 +82,25 @@ def test_host_validation_statuses():
     assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_OK
     assert L.omt_conv_dgrad(ctypes.byref(g), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID  # no workspace
     assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 16 * 5 * 3 * 3 * 4
-    n_tiles = L.omt_conv_num_tiles(_lib.OMT_DIR_DGRAD)  # the channel-major twin of tile 0 reads w directly
-    assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(n_tiles // 2, 1))) \
-        == _lib.OMT_OK
-    assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 0
+    n_gather = L.omt_conv_num_tiles(_lib.OMT_DIR_DGRAD) // 3  # tiles, each tap-major / channel-major / in place
+    # the channel-major twin of tile 0 and its in-place tap-major twin both read w directly
+    for tile in (n_gather, 2 * n_gather):
+        assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(tile, 1))) \
+            == _lib.OMT_OK
+        assert L.omt_conv_dgrad_workspace(ctypes.byref(g)) == 0, tile
+    # forward: the 3 x 3 filter re-packed for tile 0, read in place by its third twin; the 1 x 1 filter is never packed
+    gf = _lib.conv_geo(2, 32, 16, 8, 8, 3, 1, 1)
+    for tile, ws in ((0, 16 * 32 * 9 * 4), (2 * n_gather, 0)):
+        assert L.omt_conv_set_plan(_lib.OMT_DIR_FWD, ctypes.byref(gf), ctypes.byref(_lib.ConvPlan(tile, 1))) \
+            == _lib.OMT_OK
+        assert L.omt_conv_fwd_workspace(ctypes.byref(gf)) == ws, tile
     # 3 grad-input channels at stride 2: one super-pixel GEMM of 2 x 2 phases x 3 channels over the 2 x 2 window of gy
     # the 3 x 3 filter reaches (phase rows 0 and 1 use gy rows i and i, i + 1); its filter is re-packed in both K
     # orders, and split over K its partials hold the 12 rows on the 4 x 4 grid
     g3 = _lib.conv_geo(2, 3, 16, 8, 8, 3, 2, 1)
     pack = 4 * 3 * 16 * 2 * 2 * 4
-    for plan, ws in (((0, 1), pack), ((n_tiles // 2, 1), pack), ((5, 4), pack + 4 * 2 * 12 * 4 * 4 * 4)):
+    for plan, ws in (((0, 1), pack), ((n_gather, 1), pack), ((2 * n_gather, 1), pack),
+                     ((5, 4), pack + 4 * 2 * 12 * 4 * 4 * 4)):
         assert L.omt_conv_set_plan(_lib.OMT_DIR_DGRAD, ctypes.byref(g3), ctypes.byref(_lib.ConvPlan(*plan))) \
             == _lib.OMT_OK
         assert L.omt_conv_dgrad_workspace(ctypes.byref(g3)) == ws, plan
