@@ -170,9 +170,10 @@ int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const f
  * geometry); without an entry a cost model picks it. Changing an entry between a workspace query and the launch it
  * sized can make the launch fail with OMT_INVALID (workspace too small), never overrun the workspace.
  * omt_conv_autotune times the candidates (every tile of the first max_tiles, <= 0 meaning all, times a few K
- * splits) on scratch buffers on `stream` with HIP events, stores the fastest in the cache and returns it in *best
- * (may be NULL). It synchronizes `stream`, allocates through omt_malloc, and refuses (OMT_UNSUPPORTED) while the
- * stream is capturing. The cache is in key order for omt_conv_plan_entry (i < omt_conv_plan_count()). */
+ * splits) on scratch buffers, each as replays of a captured HIP graph of several calls on a private stream ordered
+ * after `stream` (so a plan's extra launches cost what they cost in a replayed step), stores the fastest in the cache
+ * and returns it in *best (may be NULL). It synchronizes `stream`, allocates through omt_malloc, and refuses
+ * (OMT_UNSUPPORTED) while `stream` is capturing. The cache is in key order for omt_conv_plan_entry (i < omt_conv_plan_count()). */
 int omt_conv_num_tiles(int dir);
 int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* plan, int* cached);
 int omt_conv_set_plan(int dir, const omt_conv_geo* g, const omt_conv_plan* plan); /* NULL plan: remove the entry */

@@ -2269,10 +2269,13 @@ struct ForceGuard {
   ~ForceGuard() { t_force[0] = t_force[1] = t_force[2] = nullptr; }
 };
 
-// Scratch buffers and events of one tuning run: zero inputs (fp32 MFMA timing does not depend on the values). The
-// destructor synchronizes the stream, so nothing queued still uses the buffers when they return to the cache.
+// Scratch buffers, events and a private stream of one tuning run: zero inputs (fp32 MFMA timing does not depend on
+// the values). Candidates are timed as replays of a captured HIP graph on the private stream, the way a training step
+// runs: each extra launch of a plan (filter re-pack, split-K slice sum) then costs what a graph node costs, which
+// back-to-back stream launches hide. The destructor synchronizes both streams, so nothing queued still uses the buffers
+// when they return to the cache.
 struct TuneScratch {
-  hipStream_t s;
+  hipStream_t s, cs = nullptr;
   void *x = nullptr, *w = nullptr, *gy = nullptr, *o1 = nullptr, *o2 = nullptr, *ws = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   explicit TuneScratch(hipStream_t st) : s(st) {}
@@ -2291,39 +2294,55 @@ struct TuneScratch {
     if (int st = hip_check(hipMemsetAsync(w, 0, wb, s), "hipMemsetAsync")) return st;
     if (int st = hip_check(hipMemsetAsync(gy, 0, yb, s), "hipMemsetAsync")) return st;
     if (int st = hip_check(hipEventCreate(&e0), "hipEventCreate")) return st;
-    return hip_check(hipEventCreate(&e1), "hipEventCreate");
+    if (int st = hip_check(hipEventCreate(&e1), "hipEventCreate")) return st;
+    if (int st = hip_check(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking), "hipStreamCreateWithFlags")) return st;
+    // the private stream starts after the zeroing queued on s
+    if (int st = hip_check(hipEventRecord(e0, s), "hipEventRecord")) return st;
+    return hip_check(hipStreamWaitEvent(cs, e0, 0), "hipStreamWaitEvent");
   }
   ~TuneScratch() {
+    if (cs) (void)hipStreamSynchronize(cs);
     (void)hipStreamSynchronize(s);
+    if (cs) (void)hipStreamDestroy(cs);
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     for (void* p : {x, w, gy, o1, o2, ws})
       if (p) omt_free(p);
   }
-  // Average ms of `run` over about `budget_ms` of repetitions (at most 8) after a warm-up call.
+  // Average ms of one `run(stream)` call: kReps calls captured into a graph on the private stream, replayed once to
+  // warm up and then twice between events.
   template <class Run>
-  int time(Run run, float budget_ms, float* ms) {
-    auto timed = [&](int reps, float* out) -> int {
-      if (int e = hip_check(hipEventRecord(e0, s), "hipEventRecord")) return e;
-      for (int r = 0; r < reps; ++r)
-        if (int e = run()) return e;
-      if (int e = hip_check(hipEventRecord(e1, s), "hipEventRecord")) return e;
+  int time(Run run, float* ms) {
+    constexpr int kReps = 8, kTimed = 2;
+    if (int e = hip_check(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"))
+      return e;
+    int st = OMT_OK;
+    for (int r = 0; r < kReps && st == OMT_OK; ++r) st = run(cs);
+    hipGraph_t graph = nullptr;
+    const hipError_t ce = hipStreamEndCapture(cs, &graph);
+    if (st != OMT_OK || ce != hipSuccess) {
+      if (graph) (void)hipGraphDestroy(graph);
+      (void)hipGetLastError();
+      return st != OMT_OK ? st : hip_check(ce, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (int e = hip_check(ie, "hipGraphInstantiate")) return e;
+    auto replays = [&]() -> int {
+      if (int e = hip_check(hipGraphLaunch(exec, cs), "hipGraphLaunch")) return e;
+      if (int e = hip_check(hipEventRecord(e0, cs), "hipEventRecord")) return e;
+      for (int r = 0; r < kTimed; ++r)
+        if (int e = hip_check(hipGraphLaunch(exec, cs), "hipGraphLaunch")) return e;
+      if (int e = hip_check(hipEventRecord(e1, cs), "hipEventRecord")) return e;
       if (int e = hip_check(hipEventSynchronize(e1), "hipEventSynchronize")) return e;
-      if (int e = hip_check(hipEventElapsedTime(out, e0, e1), "hipEventElapsedTime")) return e;
-      *out /= (float)reps;
+      if (int e = hip_check(hipEventElapsedTime(ms, e0, e1), "hipEventElapsedTime")) return e;
+      *ms /= (float)(kReps * kTimed);
       return OMT_OK;
     };
-    float first = 0.f;
-    if (int e = run()) return e;
-    if (int e = timed(1, &first)) return e;
-    *ms = first;
-    const int reps = (int)std::max(1.f, std::min(8.f, budget_ms / std::max(first, 1e-3f)));
-    if (reps > 1) {
-      float m = 0.f;
-      if (int e = timed(reps, &m)) return e;
-      *ms = std::min(m, first);
-    }
-    return OMT_OK;
+    st = replays();
+    (void)hipGraphExecDestroy(exec);
+    return st;
   }
 };
 
@@ -2358,21 +2377,21 @@ OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, 
   {
     TuneScratch sc(s);
     if (int st = sc.init(g, ws_bytes)) return st;
-    auto run = [&]() -> int {
+    auto run = [&](hipStream_t rs) -> int {
       const size_t need = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
                           : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
       if (dir == OMT_DIR_FWD)
         return omt_conv_fwd(g, (const float*)sc.x, (const float*)sc.w, nullptr, 0, nullptr, nullptr, nullptr, nullptr,
-                            1e-5f, (float*)sc.o1, sc.ws, need, s);
+                            1e-5f, (float*)sc.o1, sc.ws, need, rs);
       if (dir == OMT_DIR_DGRAD)
-        return omt_conv_dgrad(g, (const float*)sc.gy, (const float*)sc.w, (float*)sc.o1, sc.ws, need, s);
-      return omt_conv_wgrad(g, (const float*)sc.x, (const float*)sc.gy, (float*)sc.o1, sc.ws, need, s);
+        return omt_conv_dgrad(g, (const float*)sc.gy, (const float*)sc.w, (float*)sc.o1, sc.ws, need, rs);
+      return omt_conv_wgrad(g, (const float*)sc.x, (const float*)sc.gy, (float*)sc.o1, sc.ws, need, rs);
     };
     float win_ms = 1e30f;
     for (const omt_conv_plan& c : cands) {
       t_force[dir] = &c;
       float ms = 0.f;
-      if (int st = sc.time(run, 2.f, &ms)) return st;  // about 2 ms of timing per candidate
+      if (int st = sc.time(run, &ms)) return st;
       if (ms < win_ms) {
         win_ms = ms;
         win = c;
@@ -2426,16 +2445,16 @@ OMT_EXPORT int omt_conv_autotune_bwd(const omt_conv_geo* g, int max_tiles, void*
   {
     TuneScratch sc(s);
     if (int st = sc.init(g, ws_bytes)) return st;
-    auto run = [&]() -> int {
+    auto run = [&](hipStream_t rs) -> int {
       return omt_conv_bwd(g, (const float*)sc.x, (const float*)sc.gy, (const float*)sc.w, (float*)sc.o1,
-                          (float*)sc.o2, sc.ws, omt_conv_bwd_workspace(g), s);
+                          (float*)sc.o2, sc.ws, omt_conv_bwd_workspace(g), rs);
     };
     float win_ms = 1e30f;
     for (const auto& c : cands) {
       t_force[OMT_DIR_DGRAD] = &c.first;
       t_force[OMT_DIR_WGRAD] = &c.second;
       float ms = 0.f;
-      if (int st = sc.time(run, 0.5f, &ms)) return st;
+      if (int st = sc.time(run, &ms)) return st;
       if (ms < win_ms) {
         win_ms = ms;
         win = c;
