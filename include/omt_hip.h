@@ -266,6 +266,46 @@ int omt_adapool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t 
 int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* g, float* gx,
                     void* stream);
 
+/* ---- pointwise, reduction and loss ops of the training steps (outside the convolution path) ------------------------
+ * Contiguous float32 operands. Replace the reference's general elementwise kernel and op table
+ * (csrc/elementwise.cpp:79-112, 702-817), its softmax / log-softmax and NLL loss (csrc/reduce.cpp:128-202). */
+
+/* out[i] = op(a[i], b[i], alpha); out may alias a or b (the in-place forms). Activations follow PyTorch's definitions:
+ * relu(a) = max(a, 0) (NaN propagates); threshold_backward(grad a, input b) = b <= alpha ? 0 : a;
+ * hardswish(a) = a * min(max(a + 3, 0), 6) / 6 and its gradient g * (a / 3 + 1/2) on (-3, 3) (0 at and below -3,
+ * g at and above 3);
+ * hardsigmoid(a) = min(max(a + 3, 0), 6) / 6 and its gradient g / 6 on (-3, 3) (0 elsewhere). */
+enum {
+  OMT_PW_ADD = 0,             /* a + alpha * b */
+  OMT_PW_MUL = 1,             /* a * b */
+  OMT_PW_RELU = 2,            /* relu(a) */
+  OMT_PW_THRESHOLD_BWD = 3,   /* b <= alpha ? 0 : a */
+  OMT_PW_HARDSWISH = 4,       /* hardswish(a) */
+  OMT_PW_HARDSWISH_BWD = 5,   /* gradient a at input b */
+  OMT_PW_HARDSIGMOID = 6,     /* hardsigmoid(a) */
+  OMT_PW_HARDSIGMOID_BWD = 7, /* gradient a at input b */
+  OMT_PW_SCALE = 8,           /* a * alpha */
+  OMT_PW_FILL = 9             /* alpha (a, b unused) */
+};
+int omt_pointwise(int op, int64_t n, const float* a, const float* b, float alpha, float* out, void* stream);
+/* Squeeze-excite channel scale: y[p][i] = x[p][i] * scale[p] over `planes` planes (n * c) of hw elements. */
+int omt_channel_scale(int64_t planes, int64_t hw, const float* x, const float* scale, float* y, void* stream);
+/* y[p][i] = v[p] * scale: a per-plane value broadcast over its plane (the gradient of a plane mean). */
+int omt_plane_broadcast(int64_t planes, int64_t hw, const float* v, float scale, float* y, void* stream);
+/* y[p] = scale * sum_i x[p][i] (sum or mean over the last two dims of an NCHW tensor). */
+int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float scale, float* y, void* stream);
+/* Row-wise log-softmax of x[rows][cols] and its gradient gx = g - exp(y) * sum_j g (y the forward's output). */
+int omt_log_softmax_fwd(int64_t rows, int64_t cols, const float* x, float* y, void* stream);
+int omt_log_softmax_bwd(int64_t rows, int64_t cols, const float* g, const float* y, float* gx, void* stream);
+/* NLL loss over log-probabilities logp[rows][cols] and int64 targets, optional class weights, rows whose target is
+ * ignore_index excluded. reduction 0 (none): out[rows]; 1 (mean): out[0] = sum / total weight; 2 (sum): out[0].
+ * *total_weight receives the sum of the counted rows' weights (0 for reduction none). Backward: gx[r][t_r] =
+ * -w[t_r] * g' with g' = g[0] / *total_weight (mean), g[0] (sum) or g[r] (none); every other element 0. */
+int omt_nll_loss_fwd(int64_t rows, int64_t cols, const float* logp, const int64_t* target, const float* weight,
+                     int64_t ignore_index, int reduction, float* out, float* total_weight, void* stream);
+int omt_nll_loss_bwd(int64_t rows, int64_t cols, const float* g, const int64_t* target, const float* weight,
+                     int64_t ignore_index, int reduction, const float* total_weight, float* gx, void* stream);
+
 /* ---- fused optimizers (float32, contiguous parameters; many tensors per launch) -------------------------------- */
 
 /* One parameter of an Adam / AdamW step: the step count (a float on the device) has already been incremented.

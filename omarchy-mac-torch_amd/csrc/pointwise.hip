@@ -1,0 +1,335 @@
+// The other device ops of the training configurations (outside the convolution path): pointwise activations and their
+// gradients, residual add, the squeeze-excite channel scale, plane and row reductions, log-softmax and the NLL loss.
+// Reference counterparts: the general elementwise kernel and its op table (csrc/elementwise.cpp:79-112, 702-817;
+// csrc/kernels/ew.wgsl), softmax / log-softmax and the NLL loss (csrc/reduce.cpp:128-202; csrc/kernels/softmax.wgsl,
+// softmax_bwd.wgsl, nll_fwd.wgsl, nll_bwd.wgsl).
+//
+// All of them are HBM- or latency-bound. Pointwise ops stream float4 vectors (16-byte aligned operands) through a
+// grid-stride loop; the reductions give each output one wave (DPP sums, omt_internal.h) or, for the NLL loss, one
+// workgroup summing in a fixed order, so results do not depend on scheduling.
+#include "omt_internal.h"
+
+namespace omt {
+
+// Activation formulas as PyTorch defines them (torch.nn.Hardswish / Hardsigmoid documentation), in the same order of
+// operations as its CPU kernels, so that results agree to the last bit in most cases.
+__device__ __forceinline__ float hardswish_f(float x) { return x * fminf(fmaxf(x + 3.f, 0.f), 6.f) / 6.f; }
+__device__ __forceinline__ float hardswish_grad(float g, float x) {
+  return x <= -3.f ? 0.f : (x < 3.f ? g * (x / 3.f + 0.5f) : g);
+}
+__device__ __forceinline__ float hardsigmoid_f(float x) { return fminf(fmaxf(x + 3.f, 0.f), 6.f) / 6.f; }
+__device__ __forceinline__ float hardsigmoid_grad(float g, float x) {
+  return (x > -3.f && x < 3.f) ? g * (1.f / 6.f) : 0.f;
+}
+
+template <int OP>
+__device__ __forceinline__ float pw_apply(float a, float b, float alpha) {
+  if constexpr (OP == OMT_PW_ADD) return a + alpha * b;
+  if constexpr (OP == OMT_PW_MUL) return a * b;
+  if constexpr (OP == OMT_PW_RELU) return a <= 0.f ? 0.f : a;  // NaN compares false and propagates
+  if constexpr (OP == OMT_PW_THRESHOLD_BWD) return b <= alpha ? 0.f : a;
+  if constexpr (OP == OMT_PW_HARDSWISH) return hardswish_f(a);
+  if constexpr (OP == OMT_PW_HARDSWISH_BWD) return hardswish_grad(a, b);
+  if constexpr (OP == OMT_PW_HARDSIGMOID) return hardsigmoid_f(a);
+  if constexpr (OP == OMT_PW_HARDSIGMOID_BWD) return hardsigmoid_grad(a, b);
+  if constexpr (OP == OMT_PW_SCALE) return a * alpha;
+  return alpha;  // OMT_PW_FILL
+}
+
+// out[i] = op(a[i], b[i]) over n elements; VEC 4: every operand 16-byte aligned (the n % 4 tail element by element).
+template <int OP, int VEC>
+__global__ void __launch_bounds__(256) pointwise_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                        float* __restrict__ out, int64_t n, float alpha) {
+  constexpr bool UNARY = OP == OMT_PW_RELU || OP == OMT_PW_HARDSWISH || OP == OMT_PW_HARDSIGMOID || OP == OMT_PW_SCALE;
+  constexpr bool NULLARY = OP == OMT_PW_FILL;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x, t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (VEC == 4) {
+    const int64_t n4 = n >> 2;
+    for (int64_t i = t0; i < n4; i += stride) {
+      float4 va = NULLARY ? make_float4(0.f, 0.f, 0.f, 0.f) : reinterpret_cast<const float4*>(a)[i];
+      float4 vb = (UNARY || NULLARY) ? va : reinterpret_cast<const float4*>(b)[i];
+      float4 r;
+      r.x = pw_apply<OP>(va.x, vb.x, alpha);
+      r.y = pw_apply<OP>(va.y, vb.y, alpha);
+      r.z = pw_apply<OP>(va.z, vb.z, alpha);
+      r.w = pw_apply<OP>(va.w, vb.w, alpha);
+      reinterpret_cast<float4*>(out)[i] = r;
+    }
+    for (int64_t i = (n4 << 2) + t0; i < n; i += stride)
+      out[i] = pw_apply<OP>(NULLARY ? 0.f : a[i], (UNARY || NULLARY) ? 0.f : b[i], alpha);
+  } else {
+    for (int64_t i = t0; i < n; i += stride)
+      out[i] = pw_apply<OP>(NULLARY ? 0.f : a[i], (UNARY || NULLARY) ? 0.f : b[i], alpha);
+  }
+}
+
+// y[p][i] = x[p][i] * s[p] (squeeze-excite), or with x == nullptr y[p][i] = s[p] * scale (a plane broadcast: the
+// gradient of a plane mean). One workgroup row of the grid per group of planes; VEC 4 when hw % 4 == 0 and aligned.
+template <int VEC, bool SCALE_X>
+__global__ void __launch_bounds__(256) plane_scale_kernel(const float* __restrict__ x, const float* __restrict__ s,
+                                                          float* __restrict__ y, int64_t planes, int hw, float scale,
+                                                          FastDiv dv) {
+  const int hv = hw / VEC;
+  const int64_t total = planes * hv;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t p = total < ((int64_t)1 << 32) ? (int64_t)fdiv((uint32_t)i, dv) : i / hv;
+    const float m = SCALE_X ? s[p] : s[p] * scale;
+    if constexpr (VEC == 4) {
+      float4 v = SCALE_X ? reinterpret_cast<const float4*>(x)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+      reinterpret_cast<float4*>(y)[i] = make_float4(v.x * m, v.y * m, v.z * m, v.w * m);
+    } else {
+      y[i] = SCALE_X ? x[i] * m : m;
+    }
+  }
+}
+
+// y[p] = scale * sum_i x[p][i], one wave per plane, four planes per workgroup. Each lane sums a strided part of the
+// plane in order, then the wave adds the 64 lane sums with DPP (a fixed order).
+__global__ void __launch_bounds__(256) plane_sum_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                        int64_t planes, int hw, float scale) {
+  const int64_t plane = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (plane >= planes) return;  // whole waves leave together: wave_sum below runs with all 64 lanes
+  const int lane = threadIdx.x & 63;
+  const float* xp = x + plane * hw;
+  float acc = 0.f;
+  for (int e = lane; e < hw; e += 64) acc += xp[e];
+  acc = wave_sum(acc);
+  if (lane == 0) y[plane] = acc * scale;
+}
+
+// Maximum over the 64 lanes of a wave, in every lane (the DPP pattern of wave_sum). All 64 lanes must be active.
+__device__ __forceinline__ float dpp_max(float v, int moved) { return fmaxf(v, __builtin_bit_cast(float, moved)); }
+__device__ __forceinline__ float wave_max(float v) {
+  int b = __builtin_bit_cast(int, v);
+  v = dpp_max(v, __builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false));
+  b = __builtin_bit_cast(int, v);
+  v = dpp_max(v, __builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false));
+  b = __builtin_bit_cast(int, v);
+  v = dpp_max(v, __builtin_amdgcn_update_dpp(0, b, 0x141, 0xF, 0xF, false));
+  b = __builtin_bit_cast(int, v);
+  v = dpp_max(v, __builtin_amdgcn_update_dpp(0, b, 0x140, 0xF, 0xF, false));
+  b = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
+}
+
+// y[r][j] = x[r][j] - (m_r + log sum_j exp(x[r][j] - m_r)), m_r = max_j x[r][j]; one wave per row.
+__global__ void __launch_bounds__(256) log_softmax_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                          int64_t rows, int cols) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const float* xr = x + r * cols;
+  float m = -INFINITY;
+  for (int j = lane; j < cols; j += 64) m = fmaxf(m, xr[j]);
+  m = wave_max(m);
+  // a NaN in the row (which fmaxf skips) still reaches every output through the sum of exponentials
+  float s = 0.f;
+  for (int j = lane; j < cols; j += 64) s += expf(xr[j] - m);
+  s = wave_sum(s);
+  const float lse = m + logf(s);
+  float* yr = y + r * cols;
+  for (int j = lane; j < cols; j += 64) yr[j] = xr[j] - lse;
+}
+
+// gx[r][j] = g[r][j] - exp(y[r][j]) * sum_j g[r][j] (y the log-softmax output); one wave per row.
+__global__ void __launch_bounds__(256) log_softmax_bwd_kernel(const float* __restrict__ g, const float* __restrict__ y,
+                                                              float* __restrict__ gx, int64_t rows, int cols) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const float *gr = g + r * cols, *yr = y + r * cols;
+  float s = 0.f;
+  for (int j = lane; j < cols; j += 64) s += gr[j];
+  s = wave_sum(s);
+  float* o = gx + r * cols;
+  for (int j = lane; j < cols; j += 64) o[j] = gr[j] - expf(yr[j]) * s;
+}
+
+// NLL loss forward over log-probabilities logp[rows][cols] and int64 targets. reduction 0 (none): out[r] = -w[t_r]
+// logp[r][t_r] (0 for ignore_index); 1 (mean): sum / total weight; 2 (sum). One workgroup: thread t takes rows t,
+// t + 256, ... in order, then a fixed tree over the threads' partial sums.
+__global__ void __launch_bounds__(256) nll_fwd_kernel(const float* __restrict__ logp, const int64_t* __restrict__ tgt,
+                                                      const float* __restrict__ weight, int64_t rows, int cols,
+                                                      int64_t ignore, int reduction, float* __restrict__ out,
+                                                      float* __restrict__ total_weight) {
+  __shared__ float sl[256], sw[256];
+  float l = 0.f, wsum = 0.f;
+  for (int64_t r = threadIdx.x; r < rows; r += 256) {
+    const int64_t t = tgt[r];
+    float lr = 0.f, wr = 0.f;
+    if (t != ignore && t >= 0 && t < cols) {
+      wr = weight ? weight[t] : 1.f;
+      lr = -wr * logp[r * cols + t];
+    }
+    if (reduction == 0) out[r] = lr;
+    l += lr;
+    wsum += wr;
+  }
+  sl[threadIdx.x] = l;
+  sw[threadIdx.x] = wsum;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h) {
+      sl[threadIdx.x] += sl[threadIdx.x + h];
+      sw[threadIdx.x] += sw[threadIdx.x + h];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (reduction == 1) out[0] = sl[0] / sw[0];
+    if (reduction == 2) out[0] = sl[0];
+    *total_weight = reduction == 0 ? 0.f : sw[0];
+  }
+}
+
+// NLL loss backward: gx[r][j] = j == t_r ? -w[t_r] * g' : 0 with g' = g[0] / total_weight (mean), g[0] (sum) or g[r]
+// (none), and 0 on rows whose target is ignore_index.
+__global__ void __launch_bounds__(256) nll_bwd_kernel(const float* __restrict__ g, const int64_t* __restrict__ tgt,
+                                                      const float* __restrict__ weight, int64_t rows, int cols,
+                                                      int64_t ignore, int reduction,
+                                                      const float* __restrict__ total_weight, float* __restrict__ gx) {
+  const int64_t n = rows * cols, stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / cols, j = i - r * cols;
+    const int64_t t = tgt[r];
+    float v = 0.f;
+    if (j == t && t != ignore) {
+      const float w = weight ? weight[t] : 1.f;
+      const float gr = reduction == 0 ? g[r] : (reduction == 1 ? g[0] / *total_weight : g[0]);
+      v = -w * gr;
+    }
+    gx[i] = v;
+  }
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int OP>
+static void launch_pw(int64_t n, const float* a, const float* b, float alpha, float* out, hipStream_t s) {
+  const bool v4 = al16(out) && (!a || al16(a)) && (!b || al16(b));
+  const unsigned grid = grid1d(v4 ? cdiv(n, 4) : n, 256, 8192);
+  if (v4)
+    hipLaunchKernelGGL((pointwise_kernel<OP, 4>), dim3(grid), dim3(256), 0, s, a, b, out, n, alpha);
+  else
+    hipLaunchKernelGGL((pointwise_kernel<OP, 1>), dim3(grid), dim3(256), 0, s, a, b, out, n, alpha);
+}
+
+}  // namespace omt
+
+using namespace omt;
+
+OMT_EXPORT int omt_pointwise(int op, int64_t n, const float* a, const float* b, float alpha, float* out,
+                             void* stream) {
+  if (n < 0) return fail(OMT_INVALID, "omt_pointwise: n %lld", (long long)n);
+  if (n == 0) return OMT_OK;
+  const bool binary = op == OMT_PW_ADD || op == OMT_PW_MUL || op == OMT_PW_THRESHOLD_BWD ||
+                      op == OMT_PW_HARDSWISH_BWD || op == OMT_PW_HARDSIGMOID_BWD;
+  if (!out || (op != OMT_PW_FILL && !a) || (binary && !b)) return fail(OMT_INVALID, "omt_pointwise: null pointer");
+  hipStream_t s = stream_of(stream);
+  switch (op) {
+    case OMT_PW_ADD: launch_pw<OMT_PW_ADD>(n, a, b, alpha, out, s); break;
+    case OMT_PW_MUL: launch_pw<OMT_PW_MUL>(n, a, b, alpha, out, s); break;
+    case OMT_PW_RELU: launch_pw<OMT_PW_RELU>(n, a, nullptr, alpha, out, s); break;
+    case OMT_PW_THRESHOLD_BWD: launch_pw<OMT_PW_THRESHOLD_BWD>(n, a, b, alpha, out, s); break;
+    case OMT_PW_HARDSWISH: launch_pw<OMT_PW_HARDSWISH>(n, a, nullptr, alpha, out, s); break;
+    case OMT_PW_HARDSWISH_BWD: launch_pw<OMT_PW_HARDSWISH_BWD>(n, a, b, alpha, out, s); break;
+    case OMT_PW_HARDSIGMOID: launch_pw<OMT_PW_HARDSIGMOID>(n, a, nullptr, alpha, out, s); break;
+    case OMT_PW_HARDSIGMOID_BWD: launch_pw<OMT_PW_HARDSIGMOID_BWD>(n, a, b, alpha, out, s); break;
+    case OMT_PW_SCALE: launch_pw<OMT_PW_SCALE>(n, a, nullptr, alpha, out, s); break;
+    case OMT_PW_FILL: launch_pw<OMT_PW_FILL>(n, nullptr, nullptr, alpha, out, s); break;
+    default: return fail(OMT_INVALID, "omt_pointwise: op %d", op);
+  }
+  return launch_check("pointwise_kernel");
+}
+
+static int plane_scale(int64_t planes, int64_t hw, const float* x, const float* sv, float scale, float* y,
+                       void* stream, const char* fn) {
+  if (!sv || !y) return fail(OMT_INVALID, "%s: null pointer", fn);
+  if (planes < 0 || hw < 0 || hw >= ((int64_t)1 << 31)) return fail(OMT_INVALID, "%s: size", fn);
+  if (planes == 0 || hw == 0) return OMT_OK;
+  const bool v4 = hw % 4 == 0 && al16(y) && (!x || al16(x));
+  const int64_t total = planes * (v4 ? hw / 4 : hw);
+  const dim3 grid(grid1d(total, 256, 8192));
+  const FastDiv dv = make_fastdiv((uint32_t)(v4 ? hw / 4 : hw));
+  hipStream_t s = stream_of(stream);
+  if (x) {
+    if (v4)
+      hipLaunchKernelGGL((plane_scale_kernel<4, true>), grid, dim3(256), 0, s, x, sv, y, planes, (int)hw, scale, dv);
+    else
+      hipLaunchKernelGGL((plane_scale_kernel<1, true>), grid, dim3(256), 0, s, x, sv, y, planes, (int)hw, scale, dv);
+  } else {
+    if (v4)
+      hipLaunchKernelGGL((plane_scale_kernel<4, false>), grid, dim3(256), 0, s, x, sv, y, planes, (int)hw, scale, dv);
+    else
+      hipLaunchKernelGGL((plane_scale_kernel<1, false>), grid, dim3(256), 0, s, x, sv, y, planes, (int)hw, scale, dv);
+  }
+  return launch_check("plane_scale_kernel");
+}
+
+OMT_EXPORT int omt_channel_scale(int64_t planes, int64_t hw, const float* x, const float* scale, float* y,
+                                 void* stream) {
+  if (!x) return fail(OMT_INVALID, "omt_channel_scale: null pointer");
+  return plane_scale(planes, hw, x, scale, 1.f, y, stream, "omt_channel_scale");
+}
+
+OMT_EXPORT int omt_plane_broadcast(int64_t planes, int64_t hw, const float* v, float scale, float* y, void* stream) {
+  return plane_scale(planes, hw, nullptr, v, scale, y, stream, "omt_plane_broadcast");
+}
+
+OMT_EXPORT int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float scale, float* y, void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_plane_sum: null pointer");
+  if (planes < 0 || hw < 0 || hw >= ((int64_t)1 << 31) || cdiv(planes, 4) >= ((int64_t)1 << 31))
+    return fail(OMT_INVALID, "omt_plane_sum: size");
+  if (planes == 0) return OMT_OK;
+  hipLaunchKernelGGL(plane_sum_kernel, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, stream_of(stream), x, y, planes,
+                     (int)hw, scale);
+  return launch_check("plane_sum_kernel");
+}
+
+OMT_EXPORT int omt_log_softmax_fwd(int64_t rows, int64_t cols, const float* x, float* y, void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_log_softmax_fwd: null pointer");
+  if (rows < 0 || cols < 1 || cols >= ((int64_t)1 << 31) || cdiv(rows, 4) >= ((int64_t)1 << 31))
+    return fail(OMT_INVALID, "omt_log_softmax_fwd: size");
+  if (rows == 0) return OMT_OK;
+  hipLaunchKernelGGL(log_softmax_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream_of(stream), x, y, rows,
+                     (int)cols);
+  return launch_check("log_softmax_kernel");
+}
+
+OMT_EXPORT int omt_log_softmax_bwd(int64_t rows, int64_t cols, const float* g, const float* y, float* gx,
+                                   void* stream) {
+  if (!g || !y || !gx) return fail(OMT_INVALID, "omt_log_softmax_bwd: null pointer");
+  if (rows < 0 || cols < 1 || cols >= ((int64_t)1 << 31) || cdiv(rows, 4) >= ((int64_t)1 << 31))
+    return fail(OMT_INVALID, "omt_log_softmax_bwd: size");
+  if (rows == 0) return OMT_OK;
+  hipLaunchKernelGGL(log_softmax_bwd_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream_of(stream), g, y, gx,
+                     rows, (int)cols);
+  return launch_check("log_softmax_bwd_kernel");
+}
+
+OMT_EXPORT int omt_nll_loss_fwd(int64_t rows, int64_t cols, const float* logp, const int64_t* target,
+                                const float* weight, int64_t ignore_index, int reduction, float* out,
+                                float* total_weight, void* stream) {
+  if (!logp || !target || !out || !total_weight) return fail(OMT_INVALID, "omt_nll_loss_fwd: null pointer");
+  if (rows < 1 || cols < 1 || cols >= ((int64_t)1 << 31) || reduction < 0 || reduction > 2)
+    return fail(OMT_INVALID, "omt_nll_loss_fwd: rows %lld, cols %lld, reduction %d", (long long)rows, (long long)cols,
+                reduction);
+  hipLaunchKernelGGL(nll_fwd_kernel, dim3(1), dim3(256), 0, stream_of(stream), logp, target, weight, rows, (int)cols,
+                     ignore_index, reduction, out, total_weight);
+  return launch_check("nll_fwd_kernel");
+}
+
+OMT_EXPORT int omt_nll_loss_bwd(int64_t rows, int64_t cols, const float* g, const int64_t* target,
+                                const float* weight, int64_t ignore_index, int reduction, const float* total_weight,
+                                float* gx, void* stream) {
+  if (!g || !target || !gx || (reduction == 1 && !total_weight)) return fail(OMT_INVALID, "omt_nll_loss_bwd: null pointer");
+  if (rows < 1 || cols < 1 || cols >= ((int64_t)1 << 31) || reduction < 0 || reduction > 2)
+    return fail(OMT_INVALID, "omt_nll_loss_bwd: size or reduction");
+  hipLaunchKernelGGL(nll_bwd_kernel, dim3(grid1d(rows * cols, 256, 8192)), dim3(256), 0, stream_of(stream), g, target,
+                     weight, rows, (int)cols, ignore_index, reduction, total_weight, gx);
+  return launch_check("nll_bwd_kernel");
+}

@@ -17,6 +17,8 @@ OMT_CONV_NONE, OMT_CONV_DENSE, OMT_CONV_DW, OMT_CONV_DWG = range(4)
 OMT_EPI_BIAS, OMT_EPI_RELU = 1, 2
 OMT_DIR_FWD, OMT_DIR_DGRAD, OMT_DIR_WGRAD = range(3)
 NOALLOC_SCRATCH_BYTES = 64 << 20  # OMT_NOALLOC_SCRATCH_BYTES
+(OMT_PW_ADD, OMT_PW_MUL, OMT_PW_RELU, OMT_PW_THRESHOLD_BWD, OMT_PW_HARDSWISH, OMT_PW_HARDSWISH_BWD, OMT_PW_HARDSIGMOID,
+ OMT_PW_HARDSIGMOID_BWD, OMT_PW_SCALE, OMT_PW_FILL) = range(10)
 
 
 class ConvGeo(ctypes.Structure):
@@ -112,6 +114,14 @@ SIGNATURES = {
     "omt_conv_wgrad_workspace": (SZ, [G]),
     "omt_conv_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_noalloc": (I32, [G, VP, VP, VP, VP]),
+    "omt_pointwise": (I32, [ctypes.c_int, I64, VP, VP, ctypes.c_float, VP, VP]),
+    "omt_channel_scale": (I32, [I64, I64, VP, VP, VP, VP]),
+    "omt_plane_broadcast": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
+    "omt_plane_sum": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
+    "omt_log_softmax_fwd": (I32, [I64, I64, VP, VP, VP]),
+    "omt_log_softmax_bwd": (I32, [I64, I64, VP, VP, VP, VP]),
+    "omt_nll_loss_fwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
+    "omt_nll_loss_bwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
     "omt_conv_bwd_workspace": (SZ, [G]),
     "omt_conv_bwd": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_num_tiles": (I32, [I32]),

@@ -127,13 +127,43 @@ struct HotKernel<Op, Impl> {
   }
 };
 
-// Registers HotKernels into a TORCH_LIBRARY_IMPL block: HotOps(m).on<at::_ops::op, &impl>().on<...>();
+// The device kernel of an aten op outside the convolution path (pointwise ops, reductions, the loss): Impl where it
+// covers the call, else torch's HIP kernels like any op without a kernel here (counted with the delegated ops when
+// counting is on; neither a FALLBACKS entry nor an error in strict mode).
+template <class Op, auto Impl>
+struct AuxKernel;
+template <class Op, class R, class... A, R (*Impl)(A...)>
+struct AuxKernel<Op, Impl> {
+  static R run(A... a) {
+    OMT_LOCK;
+    try {
+      if constexpr (std::is_void_v<R>) {
+        Impl(a...);
+        if (debug_mode()) debug_point(op_label<Op>());
+      } else {
+        R out = Impl(a...);
+        if (debug_mode()) debug_point(op_label<Op>());
+        return out;
+      }
+    } catch (const NotCovered&) {
+      return at::native::call_fallback_fn<&hip_fallback, Op>::call(a...);
+    }
+  }
+};
+
+// Registers HotKernels into a TORCH_LIBRARY_IMPL block: HotOps(m).on<at::_ops::op, &impl>().on<...>(); aux<> for
+// AuxKernels.
 class HotOps {
  public:
   explicit HotOps(torch::Library& lib) : lib_(lib) {}
   template <class Op, auto Impl>
   HotOps& on() {
     lib_.impl(op_label<Op>().c_str(), &HotKernel<Op, Impl>::run);
+    return *this;
+  }
+  template <class Op, auto Impl>
+  HotOps& aux() {
+    lib_.impl(op_label<Op>().c_str(), &AuxKernel<Op, Impl>::run);
     return *this;
   }
 

@@ -1,0 +1,221 @@
+"""The training steps' ops outside the convolution path (residual add, ReLU / hardswish / hardsigmoid and their
+gradients, the squeeze-excite channel scale, plane means and sums, a linear layer's bias gradient, log-softmax and the
+NLL loss): libomt_hip.so's kernels against PyTorch CPU fp32 (the reference's own oracle for these ops:
+tools/conformance.py:55-103), through the C ABI and through the device's aten registrations, checked to run on the
+library's kernels rather than torch's. Criterion: rel-L2 <= 1e-4 (most results are bit-identical)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def omt(cuda):
+    import omarchy_mac_torch
+    return omarchy_mac_torch
+
+
+def rel(a, b):
+    return orc.rel_l2(a.detach().cpu().double().numpy(), b.detach().cpu().double().numpy())
+
+
+def activations_input(n, seed):
+    """Values around the activations' break points (-3, 0, 3 exactly) plus Gaussian noise at several scales."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, generator=g) * 3
+    edge = torch.tensor([-3.0, 3.0, 0.0, -0.0, -3.0000002, 2.9999998, 1e-30, -1e-30])
+    x[:min(n, 8)] = edge[:min(n, 8)]
+    return x
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+@pytest.mark.parametrize("n,offset", [(4096, 0), (1001, 0), (4099, 1), (7, 3)])
+def test_pointwise_c_abi(cuda, n, offset):
+    """Every omt_pointwise op against PyTorch CPU, on float4-aligned and unaligned operands with ragged tails."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    x = activations_input(n, n)
+    g = torch.randn(n, generator=torch.Generator().manual_seed(n + 1))
+    cases = {
+        _lib.OMT_PW_ADD: (x, g, 0.5, x + 0.5 * g),
+        _lib.OMT_PW_MUL: (x, g, 0.0, x * g),
+        _lib.OMT_PW_RELU: (x, None, 0.0, torch.relu(x)),
+        _lib.OMT_PW_THRESHOLD_BWD: (g, x, 0.25, torch.ops.aten.threshold_backward(g, x, 0.25)),
+        _lib.OMT_PW_HARDSWISH: (x, None, 0.0, F.hardswish(x)),
+        _lib.OMT_PW_HARDSWISH_BWD: (g, x, 0.0, torch.ops.aten.hardswish_backward(g, x)),
+        _lib.OMT_PW_HARDSIGMOID: (x, None, 0.0, F.hardsigmoid(x)),
+        _lib.OMT_PW_HARDSIGMOID_BWD: (g, x, 0.0, torch.ops.aten.hardsigmoid_backward(g, x)),
+        _lib.OMT_PW_SCALE: (x, None, -1.75, x * -1.75),
+        _lib.OMT_PW_FILL: (x, None, 2.5, torch.full((n,), 2.5)),
+    }
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for op, (a, b, alpha, ref) in cases.items():
+        da = torch.empty(n + offset, device=cuda)[offset:].copy_(a)
+        db = torch.empty(n + offset, device=cuda)[offset:].copy_(b) if b is not None else None
+        out = torch.full((n + offset,), float("nan"), device=cuda)[offset:]
+        _lib.check(L.omt_pointwise(op, n, _ptr(da), _ptr(db) if db is not None else None, alpha, _ptr(out), stream),
+                   "omt_pointwise")
+        got = out.cpu()
+        assert torch.equal(got, ref) or rel(got, ref) <= TOL, (op, rel(got, ref))
+    # relu keeps NaN, as PyTorch's does
+    nan = torch.tensor([float("nan"), -1.0, 2.0, float("nan")], device=cuda)
+    _lib.check(L.omt_pointwise(_lib.OMT_PW_RELU, 4, _ptr(nan), None, 0.0, _ptr(nan), stream), "omt_pointwise")
+    assert torch.equal(torch.isnan(nan.cpu()), torch.tensor([True, False, False, True]))
+
+
+@pytest.mark.parametrize("shape", [(32, 16, 112, 112), (4, 96, 7, 7), (3, 5, 3, 5)])
+def test_channel_scale_plane_sum_and_broadcast(cuda, shape):
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    n, c, h, w = shape
+    gen = torch.Generator().manual_seed(sum(shape))
+    x, s = torch.randn(shape, generator=gen), torch.rand(n, c, 1, 1, generator=gen)
+    dx, ds = x.to(cuda), s.to(cuda)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    y = torch.empty(shape, device=cuda)
+    _lib.check(L.omt_channel_scale(n * c, h * w, _ptr(dx), _ptr(ds), _ptr(y), stream), "omt_channel_scale")
+    assert torch.equal(y.cpu(), x * s)
+    m = torch.empty(n, c, device=cuda)
+    _lib.check(L.omt_plane_sum(n * c, h * w, _ptr(dx), 1.0 / (h * w), _ptr(m), stream), "omt_plane_sum")
+    assert rel(m, x.mean((2, 3))) <= 1e-6
+    _lib.check(L.omt_plane_sum(n * c, h * w, _ptr(dx), 1.0, _ptr(m), stream), "omt_plane_sum")
+    assert rel(m, x.double().sum((2, 3))) <= 1e-6
+    b = torch.empty(shape, device=cuda)
+    _lib.check(L.omt_plane_broadcast(n * c, h * w, _ptr(ds), 0.25, _ptr(b), stream), "omt_plane_broadcast")
+    assert torch.equal(b.cpu(), (s * 0.25).expand(shape))
+
+
+@pytest.mark.parametrize("rows,cols", [(32, 1000), (128, 10), (5, 1), (3, 130)])
+def test_log_softmax_and_nll_c_abi(cuda, rows, cols):
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    gen = torch.Generator().manual_seed(rows * cols)
+    x = torch.randn(rows, cols, generator=gen) * 4
+    t = torch.randint(0, cols, (rows,), generator=gen)
+    t[0] = -100  # ignore_index
+    w = torch.rand(cols, generator=gen) + 0.5
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dx, dt, dw = x.to(cuda), t.to(cuda), w.to(cuda)
+    y = torch.empty(rows, cols, device=cuda)
+    _lib.check(L.omt_log_softmax_fwd(rows, cols, _ptr(dx), _ptr(y), stream), "omt_log_softmax_fwd")
+    ref = torch.log_softmax(x, 1)
+    assert rel(y, ref) <= TOL
+    g = torch.randn(rows, cols, generator=gen)
+    gx = torch.empty(rows, cols, device=cuda)
+    _lib.check(L.omt_log_softmax_bwd(rows, cols, _ptr(g.to(cuda)), _ptr(y), _ptr(gx), stream), "omt_log_softmax_bwd")
+    assert rel(gx, torch.ops.aten._log_softmax_backward_data(g, ref, 1, torch.float32)) <= TOL
+    for weight in (None, w):
+        for red in (0, 1, 2):
+            out = torch.empty(rows if red == 0 else 1, device=cuda)
+            tw = torch.empty(1, device=cuda)
+            _lib.check(L.omt_nll_loss_fwd(rows, cols, _ptr(y), _ptr(dt), _ptr(dw) if weight is not None else None,
+                                          -100, red, _ptr(out), _ptr(tw), stream), "omt_nll_loss_fwd")
+            r_out, r_tw = torch.ops.aten.nll_loss_forward(ref, t, weight, red, -100)
+            assert rel(out.cpu().reshape(r_out.shape), r_out) <= TOL and rel(tw.cpu()[0], r_tw) <= TOL, (red, weight)
+            go = torch.randn(r_out.shape, generator=gen)
+            gx = torch.full((rows, cols), float("nan"), device=cuda)
+            _lib.check(L.omt_nll_loss_bwd(rows, cols, _ptr(go.to(cuda).contiguous()), _ptr(dt),
+                                          _ptr(dw) if weight is not None else None, -100, red, _ptr(tw), _ptr(gx),
+                                          stream), "omt_nll_loss_bwd")
+            r_gx = torch.ops.aten.nll_loss_backward(go, ref, t, weight, red, -100, r_tw)
+            assert torch.equal(gx.cpu(), r_gx) or rel(gx, r_gx) <= TOL, (red, weight)
+
+
+DEVICE_OPS = ["add", "add_", "mul", "mul_channel", "div_scalar", "div_plane", "relu", "relu_", "threshold_backward",
+              "hardswish", "hardswish_", "hardswish_backward", "hardsigmoid", "hardsigmoid_backward", "fill_", "zero_",
+              "sum_planes", "sum_rows", "mean_planes", "log_softmax", "log_softmax_backward", "nll", "nll_backward"]
+
+
+@pytest.mark.parametrize("case", DEVICE_OPS)
+def test_device_ops_run_on_the_library_kernels(omt, case):
+    """The aten ops on device tensors: same results as PyTorch CPU, and not delegated to torch's HIP kernels."""
+    core = omt.native.core
+    dev = omt.DEVICE
+    gen = torch.Generator().manual_seed(len(case))
+    x = activations_input(2 * 24 * 9 * 11, len(case)).reshape(2, 24, 9, 11)
+    y = torch.randn(2, 24, 9, 11, generator=gen)
+    s = torch.rand(2, 24, 1, 1, generator=gen)
+    logits = torch.randn(16, 37, generator=gen)
+    t = torch.randint(0, 37, (16,), generator=gen)
+    lp = torch.log_softmax(logits, 1)
+    go = torch.randn(16, 37, generator=gen)
+    D = (lambda v: v.to(dev))
+    fns = {
+        "add": lambda d: d(x) + d(y) if d is D else x + y,
+        "add_": lambda d: d(x).clone().add_(d(y), alpha=-2.0),
+        "mul": lambda d: d(x) * d(y),
+        "mul_channel": lambda d: d(x) * d(s),
+        "div_scalar": lambda d: d(x) / 7.0,
+        "div_plane": lambda d: d(s).expand(2, 24, 9, 11) / 99,
+        "relu": lambda d: torch.relu(d(x)),
+        "relu_": lambda d: d(x).clone().relu_(),
+        "threshold_backward": lambda d: torch.ops.aten.threshold_backward(d(y), d(x), 0.0),
+        "hardswish": lambda d: F.hardswish(d(x)),
+        "hardswish_": lambda d: F.hardswish(d(x).clone(), inplace=True),
+        "hardswish_backward": lambda d: torch.ops.aten.hardswish_backward(d(y), d(x)),
+        "hardsigmoid": lambda d: F.hardsigmoid(d(x)),
+        "hardsigmoid_backward": lambda d: torch.ops.aten.hardsigmoid_backward(d(y), d(x)),
+        "fill_": lambda d: d(x).clone().fill_(-1.5),
+        "zero_": lambda d: d(x).clone().zero_(),
+        "sum_planes": lambda d: d(x).sum((2, 3), keepdim=True),
+        "sum_rows": lambda d: d(logits).sum(0),
+        "mean_planes": lambda d: F.adaptive_avg_pool2d(d(x), 1),
+        "log_softmax": lambda d: torch.log_softmax(d(logits), 1),
+        "log_softmax_backward": lambda d: torch.ops.aten._log_softmax_backward_data(d(go), d(lp), 1, torch.float32),
+        "nll": lambda d: F.nll_loss(d(lp), d(t)),
+        "nll_backward": lambda d: torch.ops.aten.nll_loss_backward(d(torch.tensor(0.7)), d(lp), d(t), None, 1, -100,
+                                                                  d(torch.tensor(16.0))),
+    }
+    ref = fns[case](lambda v: v)
+    torch.cuda.synchronize()
+    core.count_delegated(True)
+    try:
+        got = fns[case](D)
+        torch.cuda.synchronize()
+        delegated = dict(core.delegated_counts())
+    finally:
+        core.count_delegated(False)
+    assert torch.equal(got.cpu(), ref) or rel(got, ref) <= TOL, case
+    ours = ("add", "mul", "div", "relu", "threshold", "hardswish", "hardsigmoid", "fill", "zero", "sum", "mean",
+            "softmax", "nll")
+    assert not [k for k in delegated if any(o in k for o in ours)], delegated
+
+
+def test_cross_entropy_training_step_ops_are_native(omt):
+    """One MobileNetV3-style training step (hardswish, squeeze-excite, residual adds, cross entropy): the only ops left
+    on torch's kernels are the linear layers' GEMMs (hipBLASLt), the batch counters and copies."""
+    from omarchy_mac_torch import models, stacks
+    core = omt.native.core
+    prev = stacks.set_auto_fuse(False)
+    try:
+        torch.manual_seed(0)
+        model = models.mobilenet_v3_small(1000).to(omt.DEVICE)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=0.01)
+        x = torch.randn(4, 3, 64, 64).to(omt.DEVICE)
+        t = torch.randint(0, 1000, (4,)).to(omt.DEVICE)
+        core.count_delegated(True)
+        opt.zero_grad(set_to_none=True)
+        F.cross_entropy(model(x), t).backward()
+        opt.step()
+        torch.cuda.synchronize()
+        delegated = dict(core.delegated_counts())
+    finally:
+        core.count_delegated(False)
+        stacks.set_auto_fuse(prev)
+    # add_ on BatchNorm's int64 batch counters, _foreach_add_ on the optimizer's step counts
+    allowed = ("mm", "addmm", "add_", "_foreach_add_", "_foreach_add")
+    assert [k for k in delegated if k.split(".")[0] not in allowed] == [], \
+        {k: v for k, v in delegated.items() if k.split(".")[0] not in allowed}
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
