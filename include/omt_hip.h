@@ -48,8 +48,15 @@ enum { OMT_CONV_NONE = 0, OMT_CONV_DENSE = 1, OMT_CONV_DW = 2, OMT_CONV_DWG = 3 
 enum { OMT_EPI_BIAS = 1u, OMT_EPI_RELU = 2u };
 
 /* GEMM directions of a dense convolution, the first field of a plan-cache key (the reference's GEMM kinds 0, 1, 2:
- * omarchy_mac_torch/gemm.py:6-8) */
-enum { OMT_DIR_FWD = 0, OMT_DIR_DGRAD = 1, OMT_DIR_WGRAD = 2 };
+ * omarchy_mac_torch/gemm.py:6-8), and the same three over channels-last tensors (omt_conv_*_nhwc) */
+enum {
+  OMT_DIR_FWD = 0,
+  OMT_DIR_DGRAD = 1,
+  OMT_DIR_WGRAD = 2,
+  OMT_DIR_FWD_NHWC = 3,
+  OMT_DIR_DGRAD_NHWC = 4,
+  OMT_DIR_WGRAD_NHWC = 5
+};
 
 /* A dense convolution's launch plan: tile index (into the direction's tile table, omt_conv_num_tiles) and number of
  * K slices (split K; rounded to whole K-blocks per slice). Replaces ConvPlan's tile and split-K multiplier
@@ -163,6 +170,25 @@ int omt_conv_wgrad_noalloc(const omt_conv_geo* g, const float* x, const float* g
 size_t omt_conv_bwd_workspace(const omt_conv_geo* g);
 int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx, float* gw,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- channels-last (NHWC) dense convolution ---------------------------------------------------------------------
+ * The same convolutions over channels-last tensors: x / gx [n][ih][iw][ci], y / gy [n][oh][ow][co], and the filter
+ * and its gradient [co][ks][ks][ci] -- the memory order of PyTorch's channels_last tensors of those shapes, read and
+ * written without a layout change. The reference makes every input contiguous NCHW first (base0,
+ * csrc/device.cpp:60-66, before gemm_forward / gemm_grad_input / gemm_grad_weight, csrc/conv.cpp:70-114); these
+ * entry points replace that copy and those GEMMs for channels-last callers. Coverage beyond the dense geometry:
+ * forward needs ci % 16 == 0, grad input co % 16 == 0, grad weight ci % 4 == 0 and co % 4 == 0 (else
+ * OMT_UNSUPPORTED). Plans: directions OMT_DIR_FWD_NHWC, OMT_DIR_DGRAD_NHWC, OMT_DIR_WGRAD_NHWC (tile indices below
+ * omt_conv_num_tiles of the direction). Bias and ReLU epilogue bits as in omt_conv_fwd; no BN loader. */
+size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g);
+int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
+                      float* y, void* workspace, size_t workspace_bytes, void* stream);
+size_t omt_conv_dgrad_nhwc_workspace(const omt_conv_geo* g);
+int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                        size_t workspace_bytes, void* stream);
+size_t omt_conv_wgrad_nhwc_workspace(const omt_conv_geo* g);
+int omt_conv_wgrad_nhwc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* ---- plan cache and tuning (replaces conv_plan / autotune / tune_dump / tune_load / tuned_plans,
  * csrc/conv.cpp:45-60, 116-155, 243-282) ---------------------------------------------------------------------

@@ -61,8 +61,9 @@ constexpr int kTileGroup = 8;
 __device__ __forceinline__ float f4get(const float4& v, int s) { return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w; }
 
 // Gather K orders: channel-major (generic), tap-major over a re-packed filter, tap-major reading the filter in place
-// (grad weight uses the first two).
-enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2 };
+// (grad weight uses the first two), and tap-major over a channels-last (NHWC) source, whose K-blocks of channels are
+// contiguous runs of each pixel.
+enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2, kNhwc = 3 };
 
 struct Phase {
   int KH, KW, S, PH, PW;  // gather window, stride and (signed) padding
@@ -99,6 +100,8 @@ struct GatherArgs {
   uint32_t w_rowst, w_cst;  // wplace: bytes between A rows and between consecutive channels of one tap
   float* part;           // split K: raw partials [slices][N][P][YH][YW], else null (epilogue writes y)
   int64_t part_stride;   // elements per slice
+  int nhwc;              // channels-last source [N][H][W][C] and output [N][YH][YW][P] (partials likewise)
+  int vec_out;           // nhwc: P % 4 == 0 and y (and the partials) 16-byte aligned: float4 stores of four channels
   Phase ph[kMaxPhases];
 };
 
@@ -136,6 +139,46 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
           yb[(int64_t)p * yhw] = v;
         }
       }
+  }
+}
+
+// Channels-last gather epilogue: output pixel (n, oy os + oy0, ox os + ox0) holds its P channels contiguously, so the
+// four accumulator rows of a lane (channels 4 (l / 16) + r4 of one pixel) are one 16-byte store where a.vec_out holds.
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const Phase& ph,
+                                                     const omt_f32x4 (&acc)[TI][TJ], int q0, int p0, int wp, int wq,
+                                                     int lane, int zs) {
+  const int P = a.P, grp = lane >> 4;
+  float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
+  const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
+    if (q >= ph.Q) continue;
+    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+    const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+    float* const yb =
+        ydst + (((int64_t)n * a.YH + (int)oy * ph.os + ph.oy0) * a.YW + (int)ox * ph.os + ph.ox0) * P;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const int p = p0 + wp * WP + 16 * i + 4 * grp;
+      float v[4];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        v[r4] = acc[i][j][r4];
+        if (!a.part) {
+          if (a.bias && p + r4 < P) v[r4] += a.bias[p + r4];
+          if (a.relu) v[r4] = fmaxf(v[r4], 0.f);
+        }
+      }
+      if (a.vec_out) {
+        if (p < P) *reinterpret_cast<float4*>(yb + p) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          if (p + r4 < P) yb[p + r4] = v[r4];
+      }
+    }
   }
 }
 
@@ -272,6 +315,29 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       lbase = (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
     }
   }
+  // Channels-last source: thread t loads channels 4 (t % KQN) .. + 3 of each K-block at the NPX tile pixels
+  // t / KQN + (NT / KQN) j, so KQN consecutive lanes read one pixel's K-block as one contiguous run of 4 BK bytes.
+  // nlb: byte offset of x[n][iy0][ix0][4 (t % KQN)] (wraps below zero for padding rows; a tap in bounds brings it back).
+  constexpr int KQN = BK / 4, NPX = MODE == kNhwc ? BQ * KQN / NT : 1;
+  static_assert(MODE != kNhwc || (NT % KQN == 0 && BQ % (NT / KQN) == 0), "NHWC pixel slots");
+  int niy[NPX], nix[NPX];
+  uint32_t nlb[NPX];
+  if constexpr (MODE == kNhwc) {
+#pragma unroll
+    for (int j = 0; j < NPX; ++j) {
+      const int q = q0 + t / KQN + (NT / KQN) * j;
+      niy[j] = nix[j] = -(1 << 28);
+      nlb[j] = kOOB;
+      if (q < ph.Q) {
+        const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+        const uint32_t n = fdiv((uint32_t)q, ph.div_ohw), r = (uint32_t)q - n * ohw;
+        const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
+        niy[j] = (int)oy * ph.S - ph.PH;
+        nix[j] = (int)ox * ph.S - ph.PW;
+        nlb[j] = (uint32_t)((((int)n * H + niy[j]) * W + nix[j]) * a.C * 4 + 16 * (t % KQN));
+      }
+    }
+  }
 
   // channel-major: wave-uniform tap state (c, ky, kx), decomposed afresh at the start of every K-block
   int sc = 0, sky = 0, skx = 0;
@@ -306,7 +372,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   }
 
   float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
-  float4 ra4[PF][AR4];
+  float4 ra4[PF][AR4], rb4[PF][NPX];
   auto gload = [&](int k0, const int set) {
     if constexpr (A4) {
       if constexpr (MODE == kTapInPlace) {
@@ -359,6 +425,16 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
           ++nky;
         }
       }
+      if constexpr (MODE == kNhwc) {
+        // the block's channels c0 .. c0 + BK - 1 of tap (ky, kx): the tap moves the pixel, the channel is scalar
+        const uint32_t toff = (uint32_t)((ky * W + kx) * a.C * 4);
+#pragma unroll
+        for (int j = 0; j < NPX; ++j) {
+          const bool ok = (unsigned)(niy[j] + ky) < (unsigned)H && (unsigned)(nix[j] + kx) < (unsigned)W;
+          rb4[set][j] = bload4(xr, ok ? nlb[j] + toff : kOOB, (uint32_t)(c0 * 4));
+        }
+        return;
+      }
       const bool ok = (unsigned)(iy0 + ky) < (unsigned)H && (unsigned)(ix0 + kx) < (unsigned)W;
       const uint32_t voff = ok ? lbase + (uint32_t)((ky * W + kx) * 4) : kOOB;
 #pragma unroll
@@ -407,10 +483,16 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
 #pragma unroll
       for (int i = 0; i < AR; ++i) As[buf][(wrow0 + (NT / BK) * i) * PK + wk] = ra[set][i];
     }
+    if constexpr (MODE == kNhwc) {
 #pragma unroll
-    for (int j = 0; j < BR; j += 4)
-      *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) =
-          make_float4(rb[set][j], rb[set][j + 1], rb[set][j + 2], rb[set][j + 3]);
+      for (int j = 0; j < NPX; ++j)
+        *reinterpret_cast<float4*>(&Bs[buf][(t / KQN + (NT / KQN) * j) * PK + 4 * (t % KQN)]) = rb4[set][j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < BR; j += 4)
+        *reinterpret_cast<float4*>(&Bs[buf][qc * PK + rbase + j]) =
+            make_float4(rb[set][j], rb[set][j + 1], rb[set][j + 2], rb[set][j + 3]);
+    }
   };
 
   omt_f32x4 acc[TI][TJ];
@@ -422,7 +504,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   const int kbeg = zs * a.kslice, kend = min(K, kbeg + a.kslice);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;  // an empty slice still writes its (zero) tile
   if (TAP) {
-    const uint32_t kb = (uint32_t)(kbeg + rbase);
+    const uint32_t kb = (uint32_t)(kbeg + (MODE == kNhwc ? 0 : rbase));  // NHWC: the block's first channel
     const int tap = (int)fdiv(kb, a.div_c);
     nc0 = (int)kb - tap * a.C;
     nky = (int)fdiv((uint32_t)tap, ph.div_kw);
@@ -485,7 +567,9 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   }
 
   static_assert(4 * row_epi_floats<WQ>() <= gather_lds_floats<BP, BQ, BK>(), "row epilogue fits the tile's LDS");
-  if (a.d2s && !a.part)
+  if constexpr (MODE == kNhwc)
+    gather_epilogue_nhwc<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
+  else if (a.d2s && !a.part)
     d2s_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
   else if (a.rows)  // the K loop's last barrier: no wave reads LDS
     row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, lds + wave * row_epi_floats<WQ>());
@@ -1015,6 +1099,156 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
   wgrad_tile<BP, BQ, WP, WQ, MODE, PF>(a, t.x, t.y, t.z, lds);
 }
 
+// Channels-last grad weight: C[co][q'] = sum_k gy[k][co] * X(k, q') with k = (n, oy, ox) and the tap-major column
+// q' = (ky, kx, ci), which is also the column order of a channels-last filter gradient gw[co][ky][kx][ci]. Both
+// operands are contiguous along their GEMM rows / columns (gy along co, x along ci), not along k: each K-block of 64
+// pixels is staged as rows of k (pitch BP + 16 and BQ + 16 floats: the four lane groups of an MFMA operand read, at
+// rows 4 s + g, fall on disjoint banks), loaded as float4 runs of four co / four ci of one pixel, and the MFMA
+// operands are read one float per lane. Lane group g supplies k = 4 s + g of the block at MFMA step s. Needs
+// C % 4 == 0 (a run of four ci stays inside one tap) and P % 4 == 0.
+template <int BP, int BQ>
+constexpr int wgrad_nhwc_lds_floats() { return 64 * ((BP + 16) + (BQ + 16)); }
+
+template <int BP, int BQ, int WP, int WQ, int PF>
+__device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx, const int by, const int bz,
+                                                float* __restrict__ lds) {
+  constexpr int NT = 256, BK = 64;
+  constexpr int WGQ = BQ / WQ;
+  static_assert((BP / WP) * (BQ / WQ) == 4, "four waves per workgroup");
+  static_assert(WP % 16 == 0 && WQ % 16 == 0, "tile shape");
+  constexpr int TI = WP / 16, TJ = WQ / 16;
+  constexpr int PA = BP + 16, PB = BQ + 16;          // LDS row pitches (floats); rows are the K-block's pixels
+  constexpr int AQ = BP / 4, BQN = BQ / 4;           // float4 runs per row
+  constexpr int ARW = NT / AQ, BRW = NT / BQN;       // rows one pass of the workgroup loads
+  constexpr int NA = BK / ARW, NB = BK / BRW;        // float4 loads per thread and K-block
+  static_assert(NT % AQ == 0 && NT % BQN == 0 && BK % ARW == 0 && BK % BRW == 0, "load shape");
+  float* const As = lds;
+  float* const Bs = lds + BK * PA;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave / WGQ, wq = wave % WGQ;
+  const int q0 = bx * BQ, p0 = by * BP;
+  const int kbeg = bz * a.kslice;
+  const int kend = min(a.K, kbeg + a.kslice);
+  const int H = a.H, W = a.W, P = a.P, Q = a.Q, C = a.C;
+  const uint32_t ohw = (uint32_t)(a.OH * a.OW);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gy, a.gy_bytes);
+  // this thread's gy run: channels pa .. pa + 3 of pixel rows ar + ARW i
+  const int ar = t / AQ, pa = p0 + 4 * (t % AQ);
+  const bool pok = pa < P;
+  // this thread's x run: columns qb .. qb + 3 = tap (ky, kx), channels ci .. ci + 3, of pixel rows br + BRW j
+  const int br = t / BQN, qb = q0 + 4 * (t % BQN);
+  const bool qok = qb < Q;
+  int ky = 0, kx = 0, ci = 0;
+  if (qok) {
+    const int tap = (int)fdiv((uint32_t)qb, a.div_c);
+    ci = qb - tap * C;
+    ky = (int)fdiv((uint32_t)tap, a.div_ks);
+    kx = tap - ky * a.KS;
+  }
+
+  float4 ra4[PF][NA], rb4[PF][NB];
+  // every load is issued (out-of-range rows and columns at offset kOOB read 0): see conv_wgrad_kernel
+  auto gload = [&](int k0, const int set) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int k = k0 + ar + ARW * i;
+      ra4[set][i] = bload4(gr, (pok && k < kend) ? (uint32_t)((k * P + pa) * 4) : kOOB, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int k = k0 + br + BRW * j;
+      uint32_t off = kOOB;
+      if (qok && k < kend) {
+        const uint32_t n = fdiv((uint32_t)k, a.div_ohw), r = (uint32_t)k - n * ohw;
+        const uint32_t oy = fdiv(r, a.div_ow), ox = r - oy * (uint32_t)a.OW;
+        const int iy = (int)oy * a.S - a.PAD + ky, ix = (int)ox * a.S - a.PAD + kx;
+        if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+          off = (uint32_t)(((((int)n * H + iy) * W + ix) * C + ci) * 4);
+      }
+      rb4[set][j] = bload4(xr, off, 0);
+    }
+  };
+  auto sstore = [&](const int set) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<float4*>(&As[(ar + ARW * i) * PA + 4 * (t % AQ)]) = ra4[set][i];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) *reinterpret_cast<float4*>(&Bs[(br + BRW * j) * PB + 4 * (t % BQN)]) = rb4[set][j];
+  };
+
+  omt_f32x4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int la = wp * WP + (lane & 15), lb = wq * WQ + (lane & 15), grp = lane >> 4;
+  auto mfma_block = [&]() {
+#pragma unroll
+    for (int s = 0; s < BK / 4; ++s) {
+      const int k = 4 * s + grp;
+      float av[TI], bv[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) av[i] = As[k * PA + la + 16 * i];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) bv[j] = Bs[k * PB + lb + 16 * j];
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  if constexpr (PF == 1) {
+    if (kbeg < kend) gload(kbeg, 0);
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+      sstore(0);
+      __syncthreads();
+      if (k0 + BK < kend) gload(k0 + BK, 0);
+      mfma_block();
+      __syncthreads();
+    }
+  } else {
+    static_assert(PF == 2, "two register sets");
+#pragma unroll
+    for (int b = 0; b < PF; ++b) gload(kbeg + b * BK, b);
+    auto step = [&](int k0, auto setc) {
+      constexpr int S = decltype(setc)::value;
+      sstore(S);
+      __syncthreads();
+      gload(k0 + PF * BK, S);
+      mfma_block();
+      __syncthreads();
+    };
+    for (int k0 = kbeg; k0 < kend; k0 += PF * BK) {
+      step(k0, std::integral_constant<int, 0>{});
+      if (k0 + BK < kend) step(k0 + BK, std::integral_constant<int, 1>{});
+    }
+  }
+
+  float* out = a.out + (int64_t)bz * P * Q;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int q = q0 + wq * WQ + 16 * j + (lane & 15);
+    if (q >= Q) continue;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
+        if (p < P) out[(int64_t)p * Q + q] = acc[i][j][r4];
+      }
+  }
+}
+
+template <int BP, int BQ, int WP, int WQ, int PF>
+__global__ void __launch_bounds__(256, 2) conv_wgrad_nhwc_kernel(const WgradArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[wgrad_nhwc_lds_floats<BP, BQ>()];
+  const TileId t = xcd_block_tile(kTileGroup);
+  wgrad_nhwc_tile<BP, BQ, WP, WQ, PF>(a, t.x, t.y, t.z, lds);
+}
+
 // Grad input and grad weight of one convolution in one launch (omt_conv_bwd), both on 64 x 64 tiles: the first
 // gx * gy * gz workgroups run grad-input tiles, the rest grad-weight tiles over wx * wy * wz (each part through the
 // XCD tile mapping). On late,
@@ -1106,6 +1340,7 @@ struct GatherSum {
   bool vec4;
   int64_t blocks;  // workgroups of its launch
   int d2s, d2s_ci, img_h, img_w, grid_w;  // super-pixel grad input: scatter [N][s^2 C][grid] to [N][C][img]
+  int nhwc;  // channels-last y [N][YH][YW][P]
 };
 template <int VEC>
 __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64_t nb) {
@@ -1122,6 +1357,15 @@ __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64
       const int row = oy * r.d2s + py, col = ox * r.d2s + px;
       if (row < r.img_h && col < r.img_w)
         r.y[((int64_t)(n * r.d2s_ci + c) * r.img_h + row) * r.img_w + col] = v[0];
+      continue;
+    }
+    if (r.nhwc) {  // channels last: element i VEC + e is channel (i VEC + e) % P
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if (r.bias) v[e] += r.bias[(i * VEC + e) % r.P];
+        if (r.relu) v[e] = fmaxf(v[e], 0.f);
+      }
+      reinterpret_cast<T*>(r.y)[i] = VecF<VEC>::pack(v);
       continue;
     }
     const float b = r.bias ? r.bias[(i * VEC / r.plane) % r.P] : 0.f;
@@ -1170,6 +1414,7 @@ struct PackArgs {
   float* out;
   int CO, CI, KS, S, nphase;
   int tap_major;  // 1: W'[ci][a'][b'][co], else W'[ci][co][a'][b']
+  int src_krsc;   // 1: w is a channels-last filter [co][ks][ks][ci]
   PackPhase ph[kMaxPhases];
 };
 __global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs a) {
@@ -1184,7 +1429,8 @@ __global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs 
     const int co = a.tap_major ? rem % a.CO : rem / jj, tap = a.tap_major ? rem / a.CO : rem % jj;
     const int ap = tap / p.jx, bp = tap % p.jx;
     const int ky = p.ky0 + a.S * (p.jy - 1 - ap), kx = p.kx0 + a.S * (p.jx - 1 - bp);
-    a.out[e] = a.w[((co * a.CI + ci) * a.KS + ky) * a.KS + kx];
+    a.out[e] = a.src_krsc ? a.w[((co * a.KS + ky) * a.KS + kx) * a.CI + ci]
+                          : a.w[((co * a.CI + ci) * a.KS + ky) * a.KS + kx];
   }
 }
 
@@ -1357,6 +1603,22 @@ static void gather_dl_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream
   }
 }
 
+// Channels-last gathers: the staged tiles 0 .. 8 (the tile's K-block divides the source channels).
+static void gather_nhwc_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t s) {
+  constexpr int M = kNhwc;
+  switch (ti) {
+    case 0: hipLaunchKernelGGL((conv_gather_kernel<64, 256, 64, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_gather_kernel<128, 128, 64, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((conv_gather_kernel<32, 256, 32, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((conv_gather_kernel<16, 256, 16, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 64, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
+  }
+}
+
 // Tap-major order needs whole K-blocks of channels (so K has no tail); the BN loader keeps the channel-major order.
 static bool gather_tap_major(int64_t c, bool bn, int bk) { return !bn && c % bk == 0; }
 
@@ -1374,18 +1636,25 @@ static const int kSliceChoices[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
 // - each workgroup carries ~2 K-blocks of fixed cost (prologue, epilogue); a split needs >= 96 K per slice;
 // - a split pays the partial round trip through HBM (~1.7 KB/clock) and one more launch (~7000 clocks).
 // `fixed` (a tuned or requested plan) replaces the estimate: its slice count is rounded to whole K-blocks per slice.
-static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const omt_conv_plan* fixed) {
+// nhwc_c > 0: a channels-last gather over nhwc_c source channels, which runs the staged tiles 0 .. kNhwcTiles - 1 whose
+// K-block divides nhwc_c (a fixed plan outside them runs as tile kNhwcDefault).
+constexpr int kNhwcTiles = 9, kNhwcDefault = 5;
+static bool nhwc_tile_ok(int t, int64_t c) { return t >= 0 && t < kNhwcTiles && c % kGatherTiles[t].bk == 0; }
+static GatherPlan gather_plan(int64_t P, int64_t Q, int64_t K, int64_t z, const omt_conv_plan* fixed,
+                              int64_t nhwc_c = 0) {
   const int64_t kk = K > 0 ? K : 1;
   if (fixed) {
-    const int64_t nkb = cdiv(kk, gtile(fixed->tile).bk);
+    const int tile = nhwc_c && !nhwc_tile_ok(fixed->tile, nhwc_c) ? kNhwcDefault : fixed->tile;
+    const int64_t nkb = cdiv(kk, gtile(tile).bk);
     const int64_t kb = cdiv(nkb, std::max<int64_t>(1, std::min<int64_t>(fixed->slices, nkb)));
-    return {fixed->tile, cdiv(nkb, kb), kb * gtile(fixed->tile).bk};
+    return {tile, cdiv(nkb, kb), kb * gtile(tile).bk};
   }
-  GatherPlan best{0, 1, cdiv(kk, 16) * 16};
+  GatherPlan best{nhwc_c ? kNhwcDefault : 0, 1, cdiv(kk, 16) * 16};
   double best_cost = 1e300;
   for (int ti = 0; ti < kNGather; ++ti) {
     const Tile& tl = kGatherTiles[ti];
     if (tl.stream) continue;  // chosen by tuning only
+    if (nhwc_c && !nhwc_tile_ok(ti, nhwc_c)) continue;
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(kk, tl.bk);
     for (int sc : kSliceChoices) {
       const int64_t kb = cdiv(nkb, sc);
@@ -1460,7 +1729,8 @@ static GatherSum gather_sum_of(const GatherArgs& a, const GatherPlan& pl) {
   r.P = a.P;
   r.bias = a.bias;
   r.relu = a.relu;
-  r.vec4 = r.plane % 4 == 0 && (uintptr_t)a.y % 16 == 0 && !a.d2s;
+  r.nhwc = a.nhwc;
+  r.vec4 = (a.nhwc ? r.total % 4 == 0 : r.plane % 4 == 0) && (uintptr_t)a.y % 16 == 0 && !a.d2s;
   r.d2s = a.d2s;
   r.d2s_ci = a.d2s_ci;
   r.img_h = a.d2s_h;
@@ -1525,12 +1795,12 @@ static int64_t wgrad_model_slices(const omt_conv_geo* g, int ti) {
   return std::max<int64_t>(1, std::min<int64_t>(cdiv(kCUs * 4, tiles), cdiv(K, 64 * 4)));
 }
 static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p);
-static WgradPlan wgrad_plan(const omt_conv_geo* g) {
+static WgradPlan wgrad_plan(const omt_conv_geo* g, int dir = OMT_DIR_WGRAD) {
   const int64_t P = g->co, Q = g->ci * g->ks * g->ks, K = g->n * g->oh * g->ow;
   omt_conv_plan cp;
   int ti;
   int64_t slices;
-  if (cached_plan(OMT_DIR_WGRAD, g, &cp)) {
+  if (cached_plan(dir, g, &cp)) {
     ti = cp.tile;
     slices = std::max<int64_t>(1, std::min<int64_t>(cp.slices, cdiv(K, 64)));
   } else {
@@ -1551,6 +1821,15 @@ static void wgrad_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s)
   }
 }
 
+static void wgrad_nhwc_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s) {
+  switch (ti) {
+    case 0: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<64, 128, 32, 64, 1>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<128, 64, 32, 64, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<64, 64, 32, 32, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<32, 128, 16, 64, 2>), grid, dim3(256), 0, s, a); break;
+  }
+}
+
 // ---- plan cache: the tile and K split per (direction, geometry), set by tuning --------------------------------
 
 struct PlanKey {
@@ -1562,7 +1841,8 @@ struct PlanKey {
 static std::mutex g_plan_mu;
 static std::map<PlanKey, omt_conv_plan> g_plans;
 // The candidates under test while tuning, per direction (both dgrad and wgrad when the backward is tuned jointly).
-static thread_local const omt_conv_plan* t_force[3] = {nullptr, nullptr, nullptr};
+constexpr int kNDirs = 6;  // OMT_DIR_FWD .. OMT_DIR_WGRAD_NHWC
+static thread_local const omt_conv_plan* t_force[kNDirs] = {};
 
 static PlanKey key_of(int dir, const omt_conv_geo* g) {
   return {dir, g->n, g->ci, g->co, g->ih, g->iw, g->oh, g->ow, g->ks, g->stride, g->pad};
@@ -1578,8 +1858,10 @@ static bool cached_plan(int dir, const omt_conv_geo* g, omt_conv_plan* p) {
   *p = it->second;
   return true;
 }
+static bool wgrad_dir(int dir) { return dir == OMT_DIR_WGRAD || dir == OMT_DIR_WGRAD_NHWC; }
 static int num_tiles(int dir) {
-  return dir == OMT_DIR_WGRAD ? (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0])) : 3 * kNGather;
+  if (wgrad_dir(dir)) return (int)(sizeof(kWgradTiles) / sizeof(kWgradTiles[0]));
+  return dir == OMT_DIR_FWD_NHWC || dir == OMT_DIR_DGRAD_NHWC ? kNhwcTiles : 3 * kNGather;
 }
 
 }  // namespace omt
@@ -1901,8 +2183,8 @@ OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
 
 // Grad-weight launch arguments over `workspace` (of omt_conv_wgrad_workspace's size) and the launch's grid.
 static dim3 wgrad_prepare(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
-                          WgradArgs& a, WgradPlan& pl) {
-  pl = wgrad_plan(g);
+                          WgradArgs& a, WgradPlan& pl, int dir = OMT_DIR_WGRAD) {
+  pl = wgrad_plan(g, dir);
   a = WgradArgs{};
   a.x = x;
   a.gy = gy;
@@ -2112,6 +2394,170 @@ OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* 
   return launch_check("dual_reduce_kernel");
 }
 
+// ---- channels-last (NHWC) convolution --------------------------------------------------------------------------
+//
+// The same three GEMMs over channels-last tensors: x [n][ih][iw][ci], y / gy [n][oh][ow][co], filter and filter
+// gradient [co][ks][ks][ci] (the memory order of channels-last tensors of those shapes). The filter already is the
+// tap-major [P][K] operand of the forward gather; the grad-input phases re-pack it; grad weight writes its
+// tap-major columns in place. Plans live under their own directions (OMT_DIR_*_NHWC).
+
+static bool nhwc_fwd_ok(const omt_conv_geo* g) { return g->ci % 16 == 0; }
+static bool nhwc_dgrad_ok(const omt_conv_geo* g) { return g->co % 16 == 0; }
+static bool nhwc_wgrad_ok(const omt_conv_geo* g) { return g->ci % 4 == 0 && g->co % 4 == 0; }
+
+static GatherPlan fwd_nhwc_plan(const omt_conv_geo* g) {
+  omt_conv_plan cp;
+  const bool have = cached_plan(OMT_DIR_FWD_NHWC, g, &cp);
+  return gather_plan(g->co, g->n * g->oh * g->ow, g->ci * g->ks * g->ks, 1, have ? &cp : nullptr, g->ci);
+}
+static GatherPlan dgrad_nhwc_plan(const omt_conv_geo* g) {
+  GatherArgs a{};
+  PackArgs pk{};
+  int64_t maxq = 0, maxk = 0;
+  dgrad_phases(g, a, pk, maxq);
+  for (int i = 0; i < a.nphase; ++i) maxk = std::max<int64_t>(maxk, a.ph[i].K);
+  omt_conv_plan cp;
+  const bool have = cached_plan(OMT_DIR_DGRAD_NHWC, g, &cp);
+  return gather_plan(g->ci, maxq, maxk, a.nphase, have ? &cp : nullptr, g->co);
+}
+
+// Launches a channels-last gather (and, split over K, its slice sum); `part`: the partials of the plan's size.
+static int run_gather_nhwc(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part,
+                           hipStream_t s) {
+  const Tile& tl = gtile(pl.tile);
+  a.nhwc = 1;
+  a.kslice = (int)pl.kslice;
+  a.part = pl.slices > 1 ? part : nullptr;
+  a.part_stride = n * a.P * a.YH * a.YW;
+  a.tpw = 0;
+  a.rows = 0;
+  a.vec_out = a.P % 4 == 0 && (uintptr_t)a.y % 16 == 0 && (uintptr_t)a.part % 16 == 0;
+  const dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
+  gather_nhwc_dispatch(pl.tile, a, grid, s);
+  if (int st = launch_check("conv_gather_kernel (nhwc)")) return st;
+  return launch_gather_sum(gather_sum_of(a, pl), s);
+}
+
+OMT_EXPORT size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g) || !fits_i32(g) || !nhwc_fwd_ok(g)) return 0;
+  const GatherPlan pl = fwd_nhwc_plan(g);
+  return pl.slices > 1 ? (size_t)(pl.slices * g->n * g->co * g->oh * g->ow) * sizeof(float) : 0;
+}
+
+OMT_EXPORT int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
+                                 unsigned epilogue, float* y, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: null pointer");
+  if (int st = geo_check(g, "omt_conv_fwd_nhwc")) return st;
+  if (!nhwc_fwd_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_nhwc: input channels not a multiple of 16");
+  if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: bias epilogue without bias");
+  const size_t need = omt_conv_fwd_nhwc_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_fwd_nhwc: workspace of %zu bytes needed", need);
+  const GatherPlan pl = fwd_nhwc_plan(g);
+  GatherArgs a{};
+  a.x = x;
+  a.w = w;  // [co][ky][kx][ci]: the tap-major [P][K] operand as it is
+  a.bias = (epilogue & OMT_EPI_BIAS) ? bias : nullptr;
+  a.relu = (epilogue & OMT_EPI_RELU) ? 1 : 0;
+  a.y = y;
+  a.x_bytes = (uint32_t)(g->n * g->ci * g->ih * g->iw * 4);
+  a.w_bytes = (uint32_t)(g->co * g->ci * g->ks * g->ks * 4);
+  a.C = (int)g->ci;
+  a.H = (int)g->ih;
+  a.W = (int)g->iw;
+  a.P = (int)g->co;
+  a.YH = (int)g->oh;
+  a.YW = (int)g->ow;
+  a.nphase = 1;
+  Phase& p = a.ph[0];
+  p.KH = p.KW = (int)g->ks;
+  p.S = (int)g->stride;
+  p.PH = p.PW = (int)g->pad;
+  p.OH = (int)g->oh;
+  p.OW = (int)g->ow;
+  p.K = (int)(g->ci * g->ks * g->ks);
+  p.Q = (int)(g->n * g->oh * g->ow);
+  p.os = 1;
+  p.div_ohw = make_fastdiv((uint32_t)(g->oh * g->ow));
+  p.div_ow = make_fastdiv((uint32_t)g->ow);
+  p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
+  p.div_kw = make_fastdiv((uint32_t)g->ks);
+  a.div_c = make_fastdiv((uint32_t)a.C);
+  return run_gather_nhwc(a, pl, g->n, p.Q, (float*)workspace, stream_of(stream));
+}
+
+// Grad-input workspace: the per-phase filters W'[ci][a'][b'][co] (all of the filter's elements), then, 256-byte
+// aligned, any split-K partials [slices][n][ih][iw][ci].
+OMT_EXPORT size_t omt_conv_dgrad_nhwc_workspace(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g) || !fits_i32(g) || !nhwc_dgrad_ok(g)) return 0;
+  const GatherPlan pl = dgrad_nhwc_plan(g);
+  const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
+  return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * g->ci * g->ih * g->iw) * sizeof(float) : pack;
+}
+
+OMT_EXPORT int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: null pointer");
+  if (int st = geo_check(g, "omt_conv_dgrad_nhwc")) return st;
+  if (!nhwc_dgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad_nhwc: output channels not a multiple of 16");
+  const size_t need = omt_conv_dgrad_nhwc_workspace(g);
+  if (!workspace || workspace_bytes < need)
+    return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  GatherArgs a{};
+  PackArgs pk{};
+  int64_t maxq = 0;
+  const int packed = dgrad_phases(g, a, pk, maxq);
+  const GatherPlan pl = dgrad_nhwc_plan(g);
+  pk.w = w;
+  pk.out = (float*)workspace;
+  pk.CO = (int)g->co;
+  pk.CI = (int)g->ci;
+  pk.KS = (int)g->ks;
+  pk.S = (int)g->stride;
+  pk.tap_major = 1;
+  pk.src_krsc = 1;
+  hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
+  if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
+  a.x = gy;
+  a.w = (const float*)workspace;
+  a.w_bytes = (uint32_t)(packed * 4);
+  a.y = gx;
+  a.x_bytes = (uint32_t)(g->n * g->co * g->oh * g->ow * 4);
+  a.C = (int)g->co;
+  a.H = (int)g->oh;
+  a.W = (int)g->ow;
+  a.P = (int)g->ci;
+  a.YH = (int)g->ih;
+  a.YW = (int)g->iw;
+  a.div_c = make_fastdiv((uint32_t)a.C);
+  float* part = (float*)((char*)workspace + align256((size_t)packed * sizeof(float)));
+  return run_gather_nhwc(a, pl, g->n, maxq, part, s);
+}
+
+OMT_EXPORT size_t omt_conv_wgrad_nhwc_workspace(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g) || !nhwc_wgrad_ok(g)) return 0;
+  const WgradPlan pl = wgrad_plan(g, OMT_DIR_WGRAD_NHWC);
+  return pl.slices > 1 ? (size_t)(pl.slices * g->co * g->ci * g->ks * g->ks) * sizeof(float) : 0;
+}
+
+OMT_EXPORT int omt_conv_wgrad_nhwc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: null pointer");
+  if (int st = geo_check(g, "omt_conv_wgrad_nhwc")) return st;
+  if (!nhwc_wgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad_nhwc: channels not multiples of 4");
+  const size_t need = omt_conv_wgrad_nhwc_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  WgradArgs a;
+  WgradPlan pl;
+  const dim3 grid = wgrad_prepare(g, x, gy, gw, workspace, a, pl, OMT_DIR_WGRAD_NHWC);
+  wgrad_nhwc_dispatch(pl.tile, a, grid, s);
+  if (int st = launch_check("conv_wgrad_nhwc_kernel")) return st;
+  return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
+}
+
 OMT_EXPORT int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream) {
   if (!gy || !gb) return fail(OMT_INVALID, "omt_bias_grad: null pointer");
   if (n < 0 || c < 0 || hw < 0 || n * c * hw >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_bias_grad: size");
@@ -2135,13 +2581,13 @@ OMT_EXPORT int omt_fold_bn(int64_t co, int64_t per_out, const float* cw, const f
 
 static int plan_args_ok(int dir, const omt_conv_geo* g, const char* what) {
   if (!g) return fail(OMT_INVALID, "%s: null geometry", what);
-  if (dir < OMT_DIR_FWD || dir > OMT_DIR_WGRAD) return fail(OMT_INVALID, "%s: direction %d", what, dir);
+  if (dir < OMT_DIR_FWD || dir > OMT_DIR_WGRAD_NHWC) return fail(OMT_INVALID, "%s: direction %d", what, dir);
   if (!dense_geo_ok(g) || !fits_i32(g)) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", what);
   return OMT_OK;
 }
 
 OMT_EXPORT int omt_conv_num_tiles(int dir) {
-  return dir >= OMT_DIR_FWD && dir <= OMT_DIR_WGRAD ? num_tiles(dir) : 0;
+  return dir >= OMT_DIR_FWD && dir <= OMT_DIR_WGRAD_NHWC ? num_tiles(dir) : 0;
 }
 
 OMT_EXPORT int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* plan, int* cached) {
@@ -2149,11 +2595,14 @@ OMT_EXPORT int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* 
   if (!plan) return fail(OMT_INVALID, "omt_conv_get_plan: null plan");
   omt_conv_plan cp;
   if (cached) *cached = cached_plan(dir, g, &cp) ? 1 : 0;
-  if (dir == OMT_DIR_WGRAD) {
-    const WgradPlan pl = wgrad_plan(g);
+  if (wgrad_dir(dir)) {
+    const WgradPlan pl = wgrad_plan(g, dir);
     *plan = {pl.tile, (int32_t)pl.slices};
   } else {
-    const GatherPlan pl = dir == OMT_DIR_FWD ? fwd_plan(g) : dgrad_plan(g);
+    const GatherPlan pl = dir == OMT_DIR_FWD        ? fwd_plan(g)
+                          : dir == OMT_DIR_DGRAD    ? dgrad_plan(g)
+                          : dir == OMT_DIR_FWD_NHWC ? fwd_nhwc_plan(g)
+                                                    : dgrad_nhwc_plan(g);
     *plan = {pl.tile, (int32_t)pl.slices};
   }
   return OMT_OK;
@@ -2202,7 +2651,7 @@ namespace {
 // reference's split-K multipliers (csrc/conv.cpp:129).
 std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int ntile) {
   std::vector<omt_conv_plan> out;
-  if (dir == OMT_DIR_WGRAD) {
+  if (wgrad_dir(dir)) {
     const int64_t K = g->n * g->oh * g->ow, kmax = cdiv(K, 64);
     for (int t = 0; t < ntile; ++t) {
       const int64_t base = wgrad_model_slices(g, t);
@@ -2217,10 +2666,12 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     }
     return out;
   }
+  const bool nhwc = dir == OMT_DIR_FWD_NHWC || dir == OMT_DIR_DGRAD_NHWC;
+  const bool fwd = dir == OMT_DIR_FWD || dir == OMT_DIR_FWD_NHWC;
   int64_t P, Q, K, z = 1, plane;
-  if (dir == OMT_DIR_FWD) {
+  if (fwd) {
     P = g->co, Q = g->n * g->oh * g->ow, K = g->ci * g->ks * g->ks, plane = g->n * g->co * g->oh * g->ow;
-  } else if (dgrad_d2s(g)) {  // the super-pixel GEMM
+  } else if (!nhwc && dgrad_d2s(g)) {  // the super-pixel GEMM
     GatherArgs a{};
     dgrad_d2s_phase(g, a, Q);
     K = a.ph[0].K;
@@ -2237,10 +2688,11 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
   const bool stream_geo = g->ks == 1 && g->stride == 1 && g->pad == 0 && K % 16 == 0 && (g->ih * g->iw) % 4 == 0;
   // the in-place filter variant differs from the re-packing one only where a re-pack would run: tap-major order
   // (C a multiple of the K-block), no super-pixel grad input, a filter larger than 1x1 in the forward
-  const int64_t gather_c = dir == OMT_DIR_FWD ? g->ci : g->co;
+  const int64_t gather_c = fwd ? g->ci : g->co;
   const bool packs = !(dir == OMT_DIR_FWD && g->ks == 1) && !(dir == OMT_DIR_DGRAD && dgrad_d2s(g));
   for (int t = 0; t < ntile; ++t) {
     const Tile& tl = gtile(t);
+    if (nhwc && !nhwc_tile_ok(t, gather_c)) continue;
     if (t >= 2 * kNGather && !(wplace_tile(t) && packs && gather_tap_major(gather_c, false, tl.bk))) continue;
     if (tl.stream) {
       if (stream_geo && t < kNGather) out.push_back({t, 1});
@@ -2265,8 +2717,16 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
   return out;
 }
 
+bool forcing() {
+  for (const auto* f : t_force)
+    if (f) return true;
+  return false;
+}
+
 struct ForceGuard {
-  ~ForceGuard() { t_force[0] = t_force[1] = t_force[2] = nullptr; }
+  ~ForceGuard() {
+    for (auto& f : t_force) f = nullptr;
+  }
 };
 
 // Scratch buffers, events and a private stream of one tuning run: zero inputs (fp32 MFMA timing does not depend on
@@ -2346,6 +2806,17 @@ struct TuneScratch {
   }
 };
 
+size_t dir_workspace(int dir, const omt_conv_geo* g) {
+  switch (dir) {
+    case OMT_DIR_FWD: return omt_conv_fwd_workspace(g);
+    case OMT_DIR_DGRAD: return omt_conv_dgrad_workspace(g);
+    case OMT_DIR_WGRAD: return omt_conv_wgrad_workspace(g);
+    case OMT_DIR_FWD_NHWC: return omt_conv_fwd_nhwc_workspace(g);
+    case OMT_DIR_DGRAD_NHWC: return omt_conv_dgrad_nhwc_workspace(g);
+    default: return omt_conv_wgrad_nhwc_workspace(g);
+  }
+}
+
 int refuse_capture(hipStream_t s, const char* what) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   OMT_HIP(hipStreamIsCapturing(s, &cs));
@@ -2357,7 +2828,7 @@ int refuse_capture(hipStream_t s, const char* what) {
 
 OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* best) {
   if (int st = plan_args_ok(dir, g, "omt_conv_autotune")) return st;
-  if (t_force[0] || t_force[1] || t_force[2]) return fail(OMT_INVALID, "omt_conv_autotune: re-entered");
+  if (forcing()) return fail(OMT_INVALID, "omt_conv_autotune: re-entered");
   hipStream_t s = stream_of(stream);
   if (int st = refuse_capture(s, "omt_conv_autotune")) return st;
   const int ntile = max_tiles <= 0 ? num_tiles(dir) : std::min(max_tiles, num_tiles(dir));
@@ -2368,9 +2839,7 @@ OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, 
   size_t ws_bytes = 0;
   for (const omt_conv_plan& c : cands) {
     t_force[dir] = &c;
-    const size_t b = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
-                     : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
-    ws_bytes = std::max(ws_bytes, b);
+    ws_bytes = std::max(ws_bytes, dir_workspace(dir, g));
   }
   t_force[dir] = nullptr;
   omt_conv_plan win = cands[0];
@@ -2378,14 +2847,18 @@ OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, 
     TuneScratch sc(s);
     if (int st = sc.init(g, ws_bytes)) return st;
     auto run = [&](hipStream_t rs) -> int {
-      const size_t need = dir == OMT_DIR_FWD ? omt_conv_fwd_workspace(g)
-                          : dir == OMT_DIR_DGRAD ? omt_conv_dgrad_workspace(g) : omt_conv_wgrad_workspace(g);
-      if (dir == OMT_DIR_FWD)
-        return omt_conv_fwd(g, (const float*)sc.x, (const float*)sc.w, nullptr, 0, nullptr, nullptr, nullptr, nullptr,
-                            1e-5f, (float*)sc.o1, sc.ws, need, rs);
-      if (dir == OMT_DIR_DGRAD)
-        return omt_conv_dgrad(g, (const float*)sc.gy, (const float*)sc.w, (float*)sc.o1, sc.ws, need, rs);
-      return omt_conv_wgrad(g, (const float*)sc.x, (const float*)sc.gy, (float*)sc.o1, sc.ws, need, rs);
+      const size_t need = dir_workspace(dir, g);
+      const float *x = (const float*)sc.x, *w = (const float*)sc.w, *gy = (const float*)sc.gy;
+      float* o = (float*)sc.o1;
+      switch (dir) {
+        case OMT_DIR_FWD:
+          return omt_conv_fwd(g, x, w, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 1e-5f, o, sc.ws, need, rs);
+        case OMT_DIR_DGRAD: return omt_conv_dgrad(g, gy, w, o, sc.ws, need, rs);
+        case OMT_DIR_WGRAD: return omt_conv_wgrad(g, x, gy, o, sc.ws, need, rs);
+        case OMT_DIR_FWD_NHWC: return omt_conv_fwd_nhwc(g, x, w, nullptr, 0, o, sc.ws, need, rs);
+        case OMT_DIR_DGRAD_NHWC: return omt_conv_dgrad_nhwc(g, gy, w, o, sc.ws, need, rs);
+        default: return omt_conv_wgrad_nhwc(g, x, gy, o, sc.ws, need, rs);
+      }
     };
     float win_ms = 1e30f;
     for (const omt_conv_plan& c : cands) {
@@ -2410,7 +2883,7 @@ OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, 
 OMT_EXPORT int omt_conv_autotune_bwd(const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* dgrad_best,
                                      omt_conv_plan* wgrad_best) {
   if (int st = plan_args_ok(OMT_DIR_DGRAD, g, "omt_conv_autotune_bwd")) return st;
-  if (t_force[0] || t_force[1] || t_force[2]) return fail(OMT_INVALID, "omt_conv_autotune_bwd: re-entered");
+  if (forcing()) return fail(OMT_INVALID, "omt_conv_autotune_bwd: re-entered");
   hipStream_t s = stream_of(stream);
   if (int st = refuse_capture(s, "omt_conv_autotune_bwd")) return st;
   // the pair tuned one direction at a time, then the pairs that share a launch

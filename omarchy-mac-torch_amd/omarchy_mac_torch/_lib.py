@@ -15,7 +15,7 @@ LIB_PATH = _HERE / "libomt_hip.so"
 OMT_OK, OMT_UNSUPPORTED, OMT_OOM, OMT_DEVICE_ERROR, OMT_INVALID = range(5)
 OMT_CONV_NONE, OMT_CONV_DENSE, OMT_CONV_DW, OMT_CONV_DWG = range(4)
 OMT_EPI_BIAS, OMT_EPI_RELU = 1, 2
-OMT_DIR_FWD, OMT_DIR_DGRAD, OMT_DIR_WGRAD = range(3)
+OMT_DIR_FWD, OMT_DIR_DGRAD, OMT_DIR_WGRAD, OMT_DIR_FWD_NHWC, OMT_DIR_DGRAD_NHWC, OMT_DIR_WGRAD_NHWC = range(6)
 NOALLOC_SCRATCH_BYTES = 64 << 20  # OMT_NOALLOC_SCRATCH_BYTES
 (OMT_PW_ADD, OMT_PW_MUL, OMT_PW_RELU, OMT_PW_THRESHOLD_BWD, OMT_PW_HARDSWISH, OMT_PW_HARDSWISH_BWD, OMT_PW_HARDSIGMOID,
  OMT_PW_HARDSIGMOID_BWD, OMT_PW_SCALE, OMT_PW_FILL) = range(10)
@@ -114,6 +114,12 @@ SIGNATURES = {
     "omt_conv_wgrad_workspace": (SZ, [G]),
     "omt_conv_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_noalloc": (I32, [G, VP, VP, VP, VP]),
+    "omt_conv_fwd_nhwc_workspace": (SZ, [G]),
+    "omt_conv_fwd_nhwc": (I32, [G, VP, VP, VP, U32, VP, VP, SZ, VP]),
+    "omt_conv_dgrad_nhwc_workspace": (SZ, [G]),
+    "omt_conv_dgrad_nhwc": (I32, [G, VP, VP, VP, VP, SZ, VP]),
+    "omt_conv_wgrad_nhwc_workspace": (SZ, [G]),
+    "omt_conv_wgrad_nhwc": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_pointwise": (I32, [ctypes.c_int, I64, VP, VP, ctypes.c_float, VP, VP]),
     "omt_channel_scale": (I32, [I64, I64, VP, VP, VP, VP]),
     "omt_plane_broadcast": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),

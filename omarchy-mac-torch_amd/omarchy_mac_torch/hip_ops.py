@@ -109,10 +109,63 @@ def conv2d_bwd(x, gy, w, stride=1, padding=0):
     return gx, gw
 
 
+# ---- channels-last (NHWC) dense convolution: tensors of the usual NCHW shapes in torch.channels_last memory order
+# (filters [co][ky][kx][ci] in memory); outputs come back channels_last -----------------------------------------
+
+_CL = torch.channels_last
+
+
+def _need_cl(t, name):
+    if t is None:
+        return None
+    if not t.is_cuda or t.dtype != torch.float32 or t.dim() != 4:
+        raise TypeError(f"{name}: expected a 4-D float32 tensor on the HIP device")
+    return t.contiguous(memory_format=_CL)
+
+
+def conv2d_nhwc(x, w, bias=None, stride=1, padding=0, relu=False):
+    x, w, bias = _need_cl(x, "x"), _need_cl(w, "w"), _need(bias, "bias", 1)
+    g = conv_geo_for(x.shape, w.shape, stride, padding)
+    y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32, memory_format=_CL)
+    epi = (_lib.OMT_EPI_BIAS if bias is not None else 0) | (_lib.OMT_EPI_RELU if relu else 0)
+    ws, nb = _workspace(L.omt_conv_fwd_nhwc_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_conv_fwd_nhwc(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(bias), epi, _ptr(y), _ptr(ws), nb,
+                              _stream(x.device)), "conv2d_nhwc")
+    return y
+
+
+def conv2d_dgrad_nhwc(gy, w, x_shape, stride=1, padding=0):
+    gy, w = _need_cl(gy, "gy"), _need_cl(w, "w")
+    g = conv_geo_for(x_shape, w.shape, stride, padding)
+    if tuple(gy.shape) != (g.n, g.co, g.oh, g.ow):
+        raise ValueError(f"conv dgrad: gy {tuple(gy.shape)} != {(g.n, g.co, g.oh, g.ow)}")
+    gx = torch.empty(tuple(x_shape), device=gy.device, dtype=torch.float32, memory_format=_CL)
+    ws, nb = _workspace(L.omt_conv_dgrad_nhwc_workspace(ctypes.byref(g)), gy.device)
+    check(L.omt_conv_dgrad_nhwc(ctypes.byref(g), _ptr(gy), _ptr(w), _ptr(gx), _ptr(ws), nb, _stream(gy.device)),
+          "conv2d_dgrad_nhwc")
+    return gx
+
+
+def conv2d_wgrad_nhwc(x, gy, ks, stride=1, padding=0):
+    x, gy = _need_cl(x, "x"), _need_cl(gy, "gy")
+    n, ci, ih, iw = x.shape
+    co = gy.shape[1]
+    g = _lib.conv_geo(n, ci, co, ih, iw, ks, stride, padding)
+    if tuple(gy.shape) != (g.n, g.co, g.oh, g.ow):
+        raise ValueError(f"conv wgrad: gy {tuple(gy.shape)} != {(g.n, g.co, g.oh, g.ow)}")
+    gw = torch.empty((co, ci, ks, ks), device=x.device, dtype=torch.float32, memory_format=_CL)
+    ws, nb = _workspace(L.omt_conv_wgrad_nhwc_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_conv_wgrad_nhwc(ctypes.byref(g), _ptr(x), _ptr(gy), _ptr(gw), _ptr(ws), nb, _stream(x.device)),
+          "conv2d_wgrad_nhwc")
+    return gw
+
+
 # ---- plan cache (tile / split-K per geometry) and tuning (reference: conv_plan, autotune, tune_dump, tune_load,
 # csrc/conv.cpp:45-60, 116-155, 243-272) ------------------------------------------------------------------------
 
-DIRECTIONS = {"fwd": _lib.OMT_DIR_FWD, "dgrad": _lib.OMT_DIR_DGRAD, "wgrad": _lib.OMT_DIR_WGRAD}
+DIRECTIONS = {"fwd": _lib.OMT_DIR_FWD, "dgrad": _lib.OMT_DIR_DGRAD, "wgrad": _lib.OMT_DIR_WGRAD,
+              "fwd_nhwc": _lib.OMT_DIR_FWD_NHWC, "dgrad_nhwc": _lib.OMT_DIR_DGRAD_NHWC,
+              "wgrad_nhwc": _lib.OMT_DIR_WGRAD_NHWC}
 
 
 def conv_num_tiles(direction):

@@ -57,6 +57,11 @@ Tensor empty_dev(IntArrayRef size, at::ScalarType dt) {
                                    std::nullopt);
 }
 
+Tensor empty_dev_cl(IntArrayRef size) {
+  return at::detail::empty_generic(size, &g_alloc, c10::DispatchKeySet(c10::DispatchKey::PrivateUse1), at::kFloat,
+                                   at::MemoryFormat::ChannelsLast);
+}
+
 Tensor workspace(size_t bytes) { return bytes ? empty_dev({(int64_t)bytes}, at::kByte) : Tensor(); }
 
 // ------------------------------------------------------------------------------------------------------------------

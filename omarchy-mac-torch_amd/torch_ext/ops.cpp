@@ -12,6 +12,16 @@
 namespace omt {
 
 static Tensor contig(const Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
+static Tensor contig_cl(const Tensor& t) {
+  return t.is_contiguous(at::MemoryFormat::ChannelsLast) ? t : t.contiguous(at::MemoryFormat::ChannelsLast);
+}
+// A dense convolution runs channels-last when its input or filter is (torch's convolutions pick their output memory
+// format the same way): the NHWC kernels read and write that order in place. The reference makes every operand
+// contiguous NCHW instead (base0, csrc/device.cpp:60-66).
+static bool channels_last(const Tensor& x, const Tensor& w) {
+  return x.suggest_memory_format() == at::MemoryFormat::ChannelsLast ||
+         w.suggest_memory_format() == at::MemoryFormat::ChannelsLast;
+}
 static bool whole(const Tensor& t) { return f32(t) && t.is_contiguous(); }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -34,15 +44,27 @@ static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::option
   cover(kind != OMT_CONV_NONE, "dilated, transposed, grouped or non-square convolution");
   cover(!defined(bias) || (f32(*bias) && bias->dim() == 1), "float32 bias");
   cover(!relu || kind == OMT_CONV_DENSE, "ReLU epilogue on a depthwise convolution");
-  Tensor x = contig(x_), w = contig(w_);
   Tensor b = defined(bias) ? contig(*bias) : Tensor();
+  const bool cl = kind == OMT_CONV_DENSE && channels_last(x_, w_);
+  unsigned epi = (b.defined() ? OMT_EPI_BIAS : 0u) | (relu ? OMT_EPI_RELU : 0u);
+  if (cl && x_.size(1) % 16 == 0) {
+    Tensor x = contig_cl(x_), w = contig_cl(w_);
+    omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
+    cover(g.oh >= 1 && g.ow >= 1, "empty output");
+    Tensor y = empty_dev_cl({g.n, g.co, g.oh, g.ow});
+    tune_conv(OMT_DIR_FWD_NHWC, g);
+    Tensor ws = workspace(omt_conv_fwd_nhwc_workspace(&g));
+    check(omt_conv_fwd_nhwc(&g, fp(x), fp(w), fp(b), epi, fpm(y), wsptr(ws), wsbytes(ws), cur_stream()),
+          "convolution (channels last)");
+    return y;
+  }
+  Tensor x = contig(x_), w = contig(w_);
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
   cover(g.oh >= 1 && g.ow >= 1, "empty output");
   Tensor y = empty_dev({g.n, g.co, g.oh, g.ow});
   if (kind == OMT_CONV_DENSE) {
     tune_conv(OMT_DIR_FWD, g);
     Tensor ws = workspace(omt_conv_fwd_workspace(&g));
-    unsigned epi = (b.defined() ? OMT_EPI_BIAS : 0u) | (relu ? OMT_EPI_RELU : 0u);
     check(omt_conv_fwd(&g, fp(x), fp(w), fp(b), epi, nullptr, nullptr, nullptr, nullptr, 1e-5f, fpm(y), wsptr(ws),
                        wsbytes(ws), cur_stream()),
           "convolution");
@@ -50,12 +72,66 @@ static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::option
     check(omt_dw_fwd(&g, fp(x), fp(w), fp(b), nullptr, nullptr, nullptr, nullptr, 1e-5f, fpm(y), cur_stream()),
           "convolution (depthwise)");
   }
-  return y;
+  // a channels-last convolution the NHWC kernels do not cover (input channels not a multiple of 16) ran in NCHW
+  return cl ? contig_cl(y) : y;
 }
 
 static Tensor convolution_(const Tensor& x, const Tensor& w, const std::optional<Tensor>& bias, IntArrayRef stride,
                            IntArrayRef padding, IntArrayRef dilation, bool transposed, IntArrayRef, int64_t groups) {
   return conv_forward(x, w, bias, stride, padding, dilation, transposed, groups, false);
+}
+
+// Backward of a channels-last dense convolution: grads in channels-last order, each from the NHWC kernels where they
+// cover it (grad input: co % 16 == 0; grad weight: ci and co multiples of 4), else from the NCHW kernels.
+static std::tuple<Tensor, Tensor, Tensor> conv_backward_cl(const Tensor& gy_, const Tensor& x_, const Tensor& w_,
+                                                           IntArrayRef stride, IntArrayRef padding,
+                                                           std::array<bool, 3> mask) {
+  omt_conv_geo g = conv_geo(x_.size(0), x_.size(1), w_.size(0), x_.size(2), x_.size(3), w_.size(2), stride[0],
+                            padding[0]);
+  cover(gy_.size(0) == g.n && gy_.size(1) == g.co && gy_.size(2) == g.oh && gy_.size(3) == g.ow, "gradient shape");
+  Tensor gy = contig_cl(gy_);
+  Tensor gx, gw, gb;
+  void* s = cur_stream();
+  if (mask[0]) {
+    if (g.co % 16 == 0) {
+      Tensor w = contig_cl(w_);
+      gx = empty_dev_cl(x_.sizes());
+      tune_conv(OMT_DIR_DGRAD_NHWC, g);
+      Tensor ws = workspace(omt_conv_dgrad_nhwc_workspace(&g));
+      check(omt_conv_dgrad_nhwc(&g, fp(gy), fp(w), fpm(gx), wsptr(ws), wsbytes(ws), s),
+            "convolution_backward (input, channels last)");
+    } else {
+      Tensor gyc = contig(gy_), w = contig(w_);
+      Tensor t = empty_dev(x_.sizes());
+      tune_conv(OMT_DIR_DGRAD, g);
+      Tensor ws = workspace(omt_conv_dgrad_workspace(&g));
+      check(omt_conv_dgrad(&g, fp(gyc), fp(w), fpm(t), wsptr(ws), wsbytes(ws), s), "convolution_backward (input)");
+      gx = contig_cl(t);
+    }
+  }
+  if (mask[1]) {
+    if (g.ci % 4 == 0 && g.co % 4 == 0) {
+      Tensor x = contig_cl(x_);
+      gw = empty_dev_cl(w_.sizes());
+      tune_conv(OMT_DIR_WGRAD_NHWC, g);
+      Tensor ws = workspace(omt_conv_wgrad_nhwc_workspace(&g));
+      check(omt_conv_wgrad_nhwc(&g, fp(x), fp(gy), fpm(gw), wsptr(ws), wsbytes(ws), s),
+            "convolution_backward (weight, channels last)");
+    } else {
+      Tensor x = contig(x_), gyc = contig(gy_);
+      Tensor t = empty_dev(w_.sizes());
+      tune_conv(OMT_DIR_WGRAD, g);
+      Tensor ws = workspace(omt_conv_wgrad_workspace(&g));
+      check(omt_conv_wgrad(&g, fp(x), fp(gyc), fpm(t), wsptr(ws), wsbytes(ws), s), "convolution_backward (weight)");
+      gw = contig_cl(t);
+    }
+  }
+  if (mask[2]) {  // the bias-grad kernel sums NCHW planes (one workgroup per channel)
+    Tensor gyc = contig(gy_);
+    gb = empty_dev({g.co});
+    check(omt_bias_grad(g.n, g.co, g.oh * g.ow, fp(gyc), fpm(gb), s), "convolution_backward (bias)");
+  }
+  return {gx, gw, gb};
 }
 
 static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy_, const Tensor& x_, const Tensor& w_,
@@ -65,6 +141,7 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
                                                                 std::array<bool, 3> mask) {
   const int kind = kind_of(x_, w_, stride, padding, dilation, transposed, groups);
   cover(kind != OMT_CONV_NONE && f32(gy_), "dilated, transposed, grouped or non-square convolution");
+  if (kind == OMT_CONV_DENSE && channels_last(x_, w_)) return conv_backward_cl(gy_, x_, w_, stride, padding, mask);
   Tensor gy = contig(gy_), x = contig(x_), w = contig(w_);
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
   cover(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");

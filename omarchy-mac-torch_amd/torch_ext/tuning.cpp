@@ -90,7 +90,7 @@ void bind_tuning(pybind11::module_& m) {
   });
   m.def("tuned_plans", []() {
     std::map<std::string, std::string> r;
-    static const char* names[] = {"fwd", "dgrad", "wgrad"};
+    static const char* names[] = {"fwd", "dgrad", "wgrad", "fwd_nhwc", "dgrad_nhwc", "wgrad_nhwc"};
     const int n = omt_conv_plan_count();
     for (int i = 0; i < n; ++i) {
       int dir = 0;

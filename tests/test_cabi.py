@@ -122,7 +122,7 @@ def test_plan_cache_host_side():
     L.omt_conv_clear_plans()
     fwd, dgrad, wgrad = _lib.OMT_DIR_FWD, _lib.OMT_DIR_DGRAD, _lib.OMT_DIR_WGRAD
     assert L.omt_conv_num_tiles(fwd) == L.omt_conv_num_tiles(dgrad) >= 4 and L.omt_conv_num_tiles(wgrad) >= 3
-    assert L.omt_conv_num_tiles(7) == 0
+    assert L.omt_conv_num_tiles(7) == 0 and L.omt_conv_num_tiles(6) == 0
 
     def plan(d, g):
         p, c = _lib.ConvPlan(), ctypes.c_int32()
@@ -146,7 +146,7 @@ def test_plan_cache_host_side():
     assert plan(wgrad, g) == (1, 3, 1)    # K = 144 pixels -> at most 3 slices of 64
     for bad in (_lib.ConvPlan(-1, 1), _lib.ConvPlan(L.omt_conv_num_tiles(fwd), 1), _lib.ConvPlan(0, 0)):
         assert L.omt_conv_set_plan(fwd, ctypes.byref(g), ctypes.byref(bad)) == _lib.OMT_INVALID
-    assert L.omt_conv_set_plan(5, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_INVALID
+    assert L.omt_conv_set_plan(6, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_INVALID
     bad_geo = _lib.ConvGeo(2, 3, 4, 8, 8, 1, 1, 12, 1, 0)
     assert L.omt_conv_set_plan(fwd, ctypes.byref(bad_geo), ctypes.byref(_lib.ConvPlan(0, 1))) == _lib.OMT_UNSUPPORTED
     # enumeration in key order, removal, clear
@@ -229,3 +229,52 @@ def test_ctypes_structs_match_the_header(tmp_path):
         assert got[f"{cname} size"] == ctypes.sizeof(py), cname
         for field, _ in py._fields_:
             assert got[f"{cname} {field}"] == getattr(py, field).offset, (cname, field)
+
+
+def test_nhwc_plans_and_workspaces_host_side():
+    """Channels-last directions: their own tile tables (the nine staged gather tiles; the four grad-weight tiles), a
+    plan whose K-block does not divide the gathered channels runs as tile 5, workspaces of the plans' sizes (grad
+    input always re-packs the filter), and the coverage conditions (forward ci % 16, grad input co % 16, grad weight
+    ci and co % 4) as empty workspaces and OMT_UNSUPPORTED, all without a GPU."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    L.omt_conv_clear_plans()
+    F, D, W = _lib.OMT_DIR_FWD_NHWC, _lib.OMT_DIR_DGRAD_NHWC, _lib.OMT_DIR_WGRAD_NHWC
+    assert L.omt_conv_num_tiles(F) == L.omt_conv_num_tiles(D) == 9 and L.omt_conv_num_tiles(W) == 4
+
+    def plan(d, g):
+        p, c = _lib.ConvPlan(), ctypes.c_int32()
+        assert L.omt_conv_get_plan(d, ctypes.byref(g), ctypes.byref(p), ctypes.byref(c)) == _lib.OMT_OK
+        return p.tile, p.slices, c.value
+
+    try:
+        g = _lib.conv_geo(4, 48, 32, 6, 6, 3, 1, 1)      # 48 channels: the 32- and 64-deep K-blocks do not divide them
+        for t in (6, 7, 8):
+            assert L.omt_conv_set_plan(F, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(t, 1))) == _lib.OMT_OK
+            assert plan(F, g)[:2] == (5, 1)
+        assert L.omt_conv_set_plan(F, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(2, 3))) == _lib.OMT_OK
+        assert plan(F, g) == (2, 3, 1)
+        assert L.omt_conv_fwd_nhwc_workspace(ctypes.byref(g)) == 3 * 4 * 32 * 6 * 6 * 4
+        assert L.omt_conv_plan_count() == 1   # the NCHW directions keep their own entries
+        assert plan(_lib.OMT_DIR_FWD, g)[2] == 0
+        pack = 32 * 48 * 9 * 4
+        assert L.omt_conv_set_plan(D, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(5, 1))) == _lib.OMT_OK
+        assert L.omt_conv_dgrad_nhwc_workspace(ctypes.byref(g)) == pack
+        assert L.omt_conv_set_plan(D, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(5, 2))) == _lib.OMT_OK
+        assert L.omt_conv_dgrad_nhwc_workspace(ctypes.byref(g)) == (pack + 255) // 256 * 256 + 2 * 4 * 48 * 6 * 6 * 4
+        assert L.omt_conv_set_plan(W, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(1, 2))) == _lib.OMT_OK
+        assert L.omt_conv_wgrad_nhwc_workspace(ctypes.byref(g)) == 2 * 32 * 48 * 9 * 4
+        for bad in (_lib.ConvPlan(9, 1), _lib.ConvPlan(-1, 1)):
+            assert L.omt_conv_set_plan(F, ctypes.byref(g), ctypes.byref(bad)) == _lib.OMT_INVALID
+        assert L.omt_conv_set_plan(W, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(4, 1))) == _lib.OMT_INVALID
+        # coverage: no workspace and OMT_UNSUPPORTED before anything is launched (pointers are never touched)
+        odd = _lib.conv_geo(2, 6, 18, 8, 8, 3, 1, 1)
+        for ws in (L.omt_conv_fwd_nhwc_workspace, L.omt_conv_dgrad_nhwc_workspace, L.omt_conv_wgrad_nhwc_workspace):
+            assert ws(ctypes.byref(odd)) == 0
+        fake = ctypes.c_void_p(16)
+        assert L.omt_conv_fwd_nhwc(ctypes.byref(odd), fake, fake, None, 0, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
+        assert L.omt_conv_dgrad_nhwc(ctypes.byref(odd), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
+        assert L.omt_conv_wgrad_nhwc(ctypes.byref(odd), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
+        assert L.omt_conv_fwd_nhwc(ctypes.byref(g), None, fake, None, 0, fake, None, 0, None) == _lib.OMT_INVALID
+    finally:
+        L.omt_conv_clear_plans()
