@@ -1,7 +1,7 @@
 """Benchmark of the convolution hot path on one MI355X (BASELINE metric: conv fwd+dgrad+wgrad fp32 TFLOP/s and % of
 fp32-MFMA peak; ResNet-18 b32 train ms/step).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5|c1] [--no-cpu] [--no-models]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5|c1] [--no-cpu] [--no-models] [--no-nhwc]
 
 One step = forward + grad-input + grad-weight of every conv layer of the workload, over one synthetic batch already
 resident in HBM:
@@ -11,7 +11,8 @@ resident in HBM:
   c1:           BASELINE config 1, AlexNet conv1 (16x3x224x224, 64x11x11, stride 4, pad 2). 6.747 GFLOP per step.
 FLOPs per direction = 2*N*K*OH*OW*C*R*S (never the padded or stride-phase-expanded work).
 
-The one JSON line also carries, as sub-objects, config 1's sweep (alexnet_conv1_b16) and the training steps of
+The one JSON line also carries, as sub-objects, the same C5 sweep in channels-last layout (c5_nhwc: NHWC activations
+through the channels-last kernels), config 1's sweep (alexnet_conv1_b16) and the training steps of
 configs 2, 3 and 4 (plaincnn_b128, resnet18_b32, mobilenetv3_b32): device ms/step eager and replayed as a HIP graph,
 the same steps on PyTorch CPU fp32 from the same weights and data, the speed-up and the 5-step loss agreement.
 
@@ -666,30 +667,36 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
     return out
 
 
-def conv_sweep(layers, dev, steps, warmup, tune):
+def conv_sweep(layers, dev, steps, warmup, tune, nhwc=False):
     """The sweep of `layers` (fwd + dgrad + wgrad each) on synthetic inputs resident in HBM: plans tuned first (as the
     reference tunes every new shape on first use, csrc/conv.cpp:56), `warmup` untimed steps, then `steps` timed ones
-    with HIP events around every launch on the launch stream. Returns the figures the bench line reports."""
+    with HIP events around every launch on the launch stream. nhwc: every tensor channels_last, through the
+    channels-last kernels. Returns the figures the bench line reports."""
     import torch
 
     from omarchy_mac_torch import hip_ops
 
     gen = torch.Generator(device=dev).manual_seed(0)
+    fmt = torch.channels_last if nhwc else torch.contiguous_format
     data = []
     for (name, n, c, k, h, ks, s, p) in layers:
         scale = (c * ks * ks) ** -0.5
         o = out_size(h, ks, s, p)
-        x = torch.randn((n, c, h, h), device=dev, generator=gen) * scale
-        w = torch.randn((k, c, ks, ks), device=dev, generator=gen) * scale
-        gy = torch.randn((n, k, o, o), device=dev, generator=gen) * scale
+        x = (torch.randn((n, c, h, h), device=dev, generator=gen) * scale).contiguous(memory_format=fmt)
+        w = (torch.randn((k, c, ks, ks), device=dev, generator=gen) * scale).contiguous(memory_format=fmt)
+        gy = (torch.randn((n, k, o, o), device=dev, generator=gen) * scale).contiguous(memory_format=fmt)
         data.append((name, n, c, k, h, ks, s, p, x, w, gy))
+    sfx = "_nhwc" if nhwc else ""
+    fwd_op = hip_ops.conv2d_nhwc if nhwc else hip_ops.conv2d
+    dgrad_op = hip_ops.conv2d_dgrad_nhwc if nhwc else hip_ops.conv2d_dgrad
+    wgrad_op = hip_ops.conv2d_wgrad_nhwc if nhwc else hip_ops.conv2d_wgrad
 
     plans = {}
     for (name, n, c, k, h, ks, s, p, x, w, gy) in data:
         for d in ("fwd", "dgrad", "wgrad"):
             if tune:
-                hip_ops.autotune_conv(d, x.shape, w.shape, s, p)
-            plans.setdefault(name, {})[d] = list(hip_ops.conv_plan(d, x.shape, w.shape, s, p)[:2])
+                hip_ops.autotune_conv(d + sfx, x.shape, w.shape, s, p)
+            plans.setdefault(name, {})[d] = list(hip_ops.conv_plan(d + sfx, x.shape, w.shape, s, p)[:2])
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
@@ -702,13 +709,13 @@ def conv_sweep(layers, dev, steps, warmup, tune):
             evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if timed else None
             if timed:
                 evs[0].record(stream)
-            hip_ops.conv2d(x, w, None, s, p)
+            fwd_op(x, w, None, s, p)
             if timed:
                 evs[1].record(stream)
-            hip_ops.conv2d_dgrad(gy, w, x.shape, s, p)
+            dgrad_op(gy, w, x.shape, s, p)
             if timed:
                 evs[2].record(stream)
-            hip_ops.conv2d_wgrad(x, gy, ks, s, p)
+            wgrad_op(x, gy, ks, s, p)
             if timed:
                 evs[3].record(stream)
                 fwd_events.append((f, evs[0], evs[1]))
@@ -802,6 +809,7 @@ def main():
     ap.add_argument("--no-miopen", action="store_true",
                     help="skip timing the same sweep through torch's own convolutions (MIOpen)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-nhwc", action="store_true", help="skip the channels-last C5 sweep")
     ap.add_argument("--no-models", "--no-resnet", dest="no_models", action="store_true",
                     help="skip config 1's sub-object and the training steps of configs 2-4")
     ap.add_argument("--model-steps", "--resnet-steps", dest="model_steps", type=int, default=20)
@@ -893,6 +901,15 @@ def main():
         "plans": {"tuned": not args.no_tune, "tile_slices": sw["plans"]},
         "device": torch.cuda.get_device_name(dev),
     }
+    if args.workload == "c5" and not args.no_nhwc:
+        print("channels-last sweep ...", file=sys.stderr, flush=True)
+        nw = conv_sweep(layers, dev, args.steps, args.warmup, not args.no_tune, nhwc=True)
+        out["c5_nhwc"] = {
+            "config": "the same C5 sweep with every tensor channels_last (NHWC activations, [co][ky][kx][ci] filters) "
+                      "through the channels-last kernels",
+            "value": round(nw["value"], 3), "unit": "TFLOP/s", "frac_of_peak": round(nw["value"] * 1e12 / PEAK_FP32_MFMA, 4),
+            "ms_per_step": round(nw["ms_per_step"], 3), "per_direction": nw["per_direction"],
+            "per_layer_tflops": nw["per_layer_tflops"], "plans": nw["plans"]}
     if not args.no_cpu:
         print("cpu baselines ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = torch_cpu_baseline(layers, batch=16)

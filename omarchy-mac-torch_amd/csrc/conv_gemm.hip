@@ -921,6 +921,7 @@ struct WgradArgs {
   int Q, K;    // C * KS * KS, N * OH * OW
   int kslice;  // pixels per slice, a multiple of the K-block
   FastDiv div_ohw, div_ow, div_kk, div_ks, div_c;
+  int step_n, step_oy, step_ox;  // 64 output pixels as (images, rows, columns): 64 = (step_n OH + step_oy) OW + step_ox
 };
 
 // LDS floats of a grad-weight tile: both operands, rows of 64 + 4.
@@ -1149,26 +1150,48 @@ __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx
     kx = tap - ky * a.KS;
   }
 
+  // The pixel (n, oy, ox) of each of this thread's x rows, for the next K-block gload reads: decomposed once, then
+  // advanced by one block (64 pixels) per call as a mixed-radix addition with one carry per digit.
+  int rn[NB], roy[NB], rox[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const uint32_t k = (uint32_t)min(kbeg + br + BRW * j, a.K - 1);
+    const uint32_t n = fdiv(k, a.div_ohw), r = k - n * ohw;
+    const uint32_t oy = fdiv(r, a.div_ow);
+    rn[j] = (int)n;
+    roy[j] = (int)oy;
+    rox[j] = (int)(r - oy * (uint32_t)a.OW);
+  }
+
   float4 ra4[PF][NA], rb4[PF][NB];
-  // every load is issued (out-of-range rows and columns at offset kOOB read 0): see conv_wgrad_kernel
+  // Every load is issued and the loaders are branch-free (out-of-range rows and columns select offset kOOB, which
+  // reads 0): a load or an index computation behind a branch splits the loop into blocks, and the compiler's waits
+  // before the LDS stores then drain every load in flight (see conv_wgrad_kernel).
   auto gload = [&](int k0, const int set) {
+    // (the conditions combine with & rather than &&: a short-circuit turns into branches around the offsets)
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int k = k0 + ar + ARW * i;
-      ra4[set][i] = bload4(gr, (pok && k < kend) ? (uint32_t)((k * P + pa) * 4) : kOOB, 0);
+      const uint32_t off = (uint32_t)((k * P + pa) * 4);
+      ra4[set][i] = bload4(gr, (pok & (k < kend)) ? off : kOOB, 0);
     }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int k = k0 + br + BRW * j;
-      uint32_t off = kOOB;
-      if (qok && k < kend) {
-        const uint32_t n = fdiv((uint32_t)k, a.div_ohw), r = (uint32_t)k - n * ohw;
-        const uint32_t oy = fdiv(r, a.div_ow), ox = r - oy * (uint32_t)a.OW;
-        const int iy = (int)oy * a.S - a.PAD + ky, ix = (int)ox * a.S - a.PAD + kx;
-        if ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
-          off = (uint32_t)(((((int)n * H + iy) * W + ix) * C + ci) * 4);
-      }
-      rb4[set][j] = bload4(xr, off, 0);
+      const int iy = roy[j] * a.S - a.PAD + ky, ix = rox[j] * a.S - a.PAD + kx;
+      const bool ok = qok & (k < kend) & ((unsigned)iy < (unsigned)H) & ((unsigned)ix < (unsigned)W);
+      const uint32_t off = (uint32_t)((((rn[j] * H + iy) * W + ix) * C + ci) * 4);
+      rb4[set][j] = bload4(xr, ok ? off : kOOB, 0);
+      // the next block's pixel of this row
+      int ox = rox[j] + a.step_ox, oy = roy[j] + a.step_oy, n = rn[j] + a.step_n;
+      const int cx = ox >= a.OW;
+      ox -= cx ? a.OW : 0;
+      oy += cx;
+      const int cy = oy >= a.OH;
+      oy -= cy ? a.OH : 0;
+      rox[j] = ox;
+      roy[j] = oy;
+      rn[j] = n + cy;
     }
   };
   auto sstore = [&](const int set) {
@@ -1210,6 +1233,8 @@ __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx
       __syncthreads();
     }
   } else {
+    // Whole pairs of blocks in the loop and an odd last block after it: a conditional second step in the loop body
+    // merges two load histories at the loop head, where the compiler then waits for every load in flight.
     static_assert(PF == 2, "two register sets");
 #pragma unroll
     for (int b = 0; b < PF; ++b) gload(kbeg + b * BK, b);
@@ -1221,10 +1246,12 @@ __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx
       mfma_block();
       __syncthreads();
     };
-    for (int k0 = kbeg; k0 < kend; k0 += PF * BK) {
+    int k0 = kbeg;
+    for (; k0 + BK < kend; k0 += PF * BK) {
       step(k0, std::integral_constant<int, 0>{});
-      if (k0 + BK < kend) step(k0 + BK, std::integral_constant<int, 1>{});
+      step(k0 + BK, std::integral_constant<int, 1>{});
     }
+    if (k0 < kend) step(k0, std::integral_constant<int, 0>{});
   }
 
   float* out = a.out + (int64_t)bz * P * Q;
@@ -2208,6 +2235,9 @@ static dim3 wgrad_prepare(const omt_conv_geo* g, const float* x, const float* gy
   a.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   a.div_ks = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)g->ci);
+  a.step_ox = (int)(64 % g->ow);
+  a.step_oy = (int)((64 / g->ow) % g->oh);
+  a.step_n = (int)((64 / g->ow) / g->oh);
   const Tile& tl = kWgradTiles[pl.tile];
   return dim3((unsigned)cdiv(a.Q, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)pl.slices);
 }
