@@ -391,12 +391,10 @@ def miopen_sweep(layers, dev, reps):
             "library": f"torch {torch.__version__} conv2d / convolution_backward (MIOpen, default find mode)"}
 
 
-def bandwidth_kernels(dev, reps=20):
-    """The HBM-bound kernels of the path on shapes from the BASELINE configs: achieved GB/s from algorithmic
-    (compulsory) bytes -- each input read once, each output written once, fp32, int64 pool indices -- over the op's
-    GPU time (all of its launches: BN's statistics, finalize and apply passes). The calls are captured into a HIP
-    graph and timed with HIP events around its replays, so host dispatch (which exceeds the smallest kernels' run
-    time) is not counted."""
+def bandwidth_cases(dev):
+    """(name, fn, algorithmic bytes) of the HBM-bound ops measured by bandwidth_kernels and bw_pmc_probe: shapes from
+    the BASELINE configs; bytes are compulsory traffic -- each input read once, each output written once, fp32, int64
+    pool indices."""
     import torch
 
     from omarchy_mac_torch import hip_ops as H
@@ -456,7 +454,20 @@ def bandwidth_kernels(dev, reps=20):
     numel = sum(p.numel() for p in params)
     cases.append((f"fused adam [{len(params)} tensors, {numel / 1e6:.1f}M]",
                   lambda: H.fused_adam(params, grads, ms, vs, steps), 7 * 4 * numel))
+    # the floor of the method: a one-element fill kernel timed the same way (kernel boundary, ramp and drain)
+    one = torch.empty(1, device=dev)
+    cases.append(("launch floor (one-element fill)", lambda: H.fill_(one, 1.0), 4))
+    return cases
 
+
+def bandwidth_kernels(dev, reps=20):
+    """The HBM-bound kernels of the path (bandwidth_cases): achieved GB/s from algorithmic bytes over the op's GPU time
+    (all of its launches: BN's statistics, finalize and apply passes). The calls are captured into a HIP graph and
+    timed with HIP events around its replays, so host dispatch (which exceeds the smallest kernels' run time) is not
+    counted."""
+    import torch
+
+    cases = bandwidth_cases(dev)
     stream = torch.cuda.current_stream(dev)
     out = []
     for name, fn, b in cases:
@@ -482,6 +493,69 @@ def bandwidth_kernels(dev, reps=20):
         out.append({"op": name, "bytes": b, "us": round(us, 2), "GB/s": round(b / us / 1e3, 1),
                     "frac_of_hbm_peak": round(b / (us * 1e-6) / PEAK_HBM, 3)})
     return out
+
+
+def bw_pmc_probe(dev):
+    """For rocprofv3 --pmc passes over the HBM-bound ops: a 1 GiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE
+    calibration), then each op of bandwidth_cases once, each preceded by a one-element fill (torch's fill kernel: the
+    marker that separates the ops' dispatches in the counter dump)."""
+    import torch
+
+    cases = bandwidth_cases(dev)
+    src = torch.ones(256 * 1024 * 1024, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    mark = torch.empty(1, device=dev)
+    for name, fn, _ in cases:
+        mark.fill_(1.0)
+        fn()
+        torch.cuda.synchronize()
+    print("bw pmc probe done:", len(cases), "ops", flush=True)
+
+
+def bw_pmc_summary(fetch_csv, write_csv):
+    """Reads the FETCH_SIZE and WRITE_SIZE dumps of two `--workload bw --pmc-probe` runs: the copy calibrates each
+    counter; the dispatches between consecutive fill markers are one op's (all of its kernels). Writes
+    profiles/hbm_kernels_traffic.json and prints a markdown table of HBM bytes against the algorithmic bytes."""
+    import csv
+
+    import torch
+
+    names = [(c[0], c[2]) for c in bandwidth_cases(torch.device("cuda:0"))] if torch.cuda.is_available() else None
+    res = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rs = sorted((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0)
+                    for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter)
+        ci = max((i for i, r in enumerate(rs) if "copy" in r[1].lower()), key=lambda i: rs[i][2])
+        factor = (1 << 30) / rs[ci][2]
+        ops, cur = [], None
+        for _, kname, v in rs[ci + 1:]:
+            if "FillFunctor" in kname:
+                cur = {"bytes": 0.0, "kernels": []}
+                ops.append(cur)
+            elif cur is not None:
+                cur["bytes"] += v * factor
+                short = kname.split("(")[0].replace("void ", "")
+                if short not in cur["kernels"]:
+                    cur["kernels"].append(short)
+        res[counter] = (factor, ops)
+    n_ops = len(res["FETCH_SIZE"][1])
+    if names is None or len(names) != n_ops or len(res["WRITE_SIZE"][1]) != n_ops:
+        raise SystemExit(f"{n_ops} ops in the dump; expected {len(names) if names else '?'} (run on the GPU box)")
+    out = {"fetch_factor": round(res["FETCH_SIZE"][0], 4), "write_factor": round(res["WRITE_SIZE"][0], 4), "ops": {}}
+    lines = ["| Op | kernels | algorithmic | FETCH (scaled) | WRITE (scaled) | traffic / algorithmic |",
+             "|---|---|---|---|---|---|"]
+    for i, (name, alg) in enumerate(names):
+        f, w = res["FETCH_SIZE"][1][i], res["WRITE_SIZE"][1][i]
+        out["ops"][name] = {"algorithmic_bytes": alg, "fetch_bytes": round(f["bytes"]), "write_bytes": round(w["bytes"]),
+                            "kernels": f["kernels"]}
+        lines.append(f"| {name} | {', '.join('`' + k + '`' for k in f['kernels'])} | {alg / 1e6:.1f} MB | "
+                     f"{f['bytes'] / 1e6:.1f} MB | {w['bytes'] / 1e6:.1f} MB | {(f['bytes'] + w['bytes']) / alg:.2f} |")
+    (ROOT / "profiles" / "hbm_kernels_traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    print(f"FETCH_SIZE factor {out['fetch_factor']}, WRITE_SIZE factor {out['write_factor']}")
+    print("\n".join(lines))
 
 
 def pmc_probe(layers, dev):
@@ -826,10 +900,13 @@ def main():
                     help="per-kernel launches and mean / median duration of this library's kernels in a kernel trace")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
-                         "launch per layer; prints nothing else")
+                         "launch per layer (with --workload bw: each HBM-bound op once, after a fill marker)")
     args = ap.parse_args()
     if args.pmc_summary:
-        pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
+        if args.workload == "bw":
+            bw_pmc_summary(*args.pmc_summary)
+        else:
+            pmc_summary(*args.pmc_summary, C5_LAYERS if args.workload == "c5" else C1_LAYERS, args.workload)
         return
     if args.kernel_table:
         kernel_table(args.kernel_table)
@@ -860,7 +937,10 @@ def main():
                           for c in cfgs}), flush=True)
         return
     if args.workload == "bw":
-        print(json.dumps({"bandwidth_kernels": bandwidth_kernels(dev)}), flush=True)
+        if args.pmc_probe:
+            bw_pmc_probe(dev)
+        else:
+            print(json.dumps({"bandwidth_kernels": bandwidth_kernels(dev)}), flush=True)
         return
     layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
     if args.pmc_probe:

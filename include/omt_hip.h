@@ -267,6 +267,14 @@ int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, const float* x,
                const float* save_mean, const float* save_invstd, const float* gamma, float* gx, float* dgamma,
                float* dbeta, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same with a residual branch's gradient: gz = (g + g2) masked by relu_y > 0 (g2 may be NULL), written to gz for
+ * the residual branch, and the BatchNorm backward of gz. No counterpart in the reference, whose ReLU backward, residual
+ * add and BatchNorm backward are separate ops; the torch.compile backend fuses add -> threshold_backward ->
+ * native_batch_norm_backward (the backward of a ResNet basic block's end) into it. gz must not be NULL. */
+int omt_bn_bwd_res(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
+                   const float* relu_y, const float* save_mean, const float* save_invstd, const float* gamma, float* gx,
+                   float* dgamma, float* dbeta, float* gz, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- pooling (planes = n * c) ----------------------------------------------------------------------------- */
 
 /* Max pool, any window / stride / padding / dilation; idx = int64 flat position in the input plane, first maximum

@@ -61,6 +61,8 @@ __device__ __forceinline__ void vset(float4& v, int i, float f) {
   if (i == 0) v.x = f; else if (i == 1) v.y = f; else if (i == 2) v.z = f; else v.w = f;
 }
 __device__ __forceinline__ void vset(float& v, int, float f) { v = f; }
+__device__ __forceinline__ void vadd(float4& a, const float4& b) { a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w; }
+__device__ __forceinline__ void vadd(float& a, const float& b) { a += b; }
 
 // Element offset of vector v of channel ch.
 __device__ __forceinline__ int64_t voffset(int v, int ch, int c, int hw, int hwv, const FastDiv& div_hwv, int vec) {
@@ -228,9 +230,11 @@ __global__ void __launch_bounds__(256) bn_apply_flat_kernel(const float* __restr
   }
 }
 
-// grid (c, slices): partial sum gz and sum gz * xhat
-template <int VEC>
-__global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restrict__ g, const float* __restrict__ x,
+// grid (c, slices): partial sum gz and sum gz * xhat. RES: the incoming gradient is g + g2 (a residual branch's
+// gradient added before the ReLU mask).
+template <int VEC, bool RES>
+__global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restrict__ g, const float* __restrict__ g2,
+                                                          const float* __restrict__ x,
                                                           const float* __restrict__ ry, const float* __restrict__ mean,
                                                           const float* __restrict__ invstd, double* __restrict__ part,
                                                           int c, int hw, const Split sp) {
@@ -247,6 +251,7 @@ __global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restric
       if (vv < v1) {
         const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
         rg[u] = *reinterpret_cast<const V*>(g + off);
+        if (RES && g2) vadd(rg[u], *reinterpret_cast<const V*>(g2 + off));
         rx[u] = *reinterpret_cast<const V*>(x + off);
         if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
       } else {
@@ -306,49 +311,60 @@ __device__ __forceinline__ float bwd_elem(float gz, float xv, float r, bool mask
   return k[0] * gz - k[1] - k[2] * xhat;
 }
 
-// grid x = plane (n * c), grid y = chunks of the plane
-template <int VEC>
-__global__ void __launch_bounds__(256) bn_bwd_apply_kernel(const float* __restrict__ g, const float* __restrict__ x,
-                                                           const float* __restrict__ ry, const float* __restrict__ kc,
-                                                           float* __restrict__ gx, int c, int hwv) {
+// Vector i of the backward map: gx (and, RES, the masked incoming gradient gz = (g + g2) [y > 0]).
+template <int VEC, bool RES>
+__device__ __forceinline__ void bwd_vec(const float* __restrict__ g, const float* __restrict__ g2,
+                                        const float* __restrict__ x, const float* __restrict__ ry, const float* k,
+                                        float* __restrict__ gx, float* __restrict__ gzo, int64_t i) {
   using V = typename VecT<VEC>::T;
+  V vg = reinterpret_cast<const V*>(g)[i];
+  if (RES && g2) vadd(vg, reinterpret_cast<const V*>(g2)[i]);
+  const V vx = reinterpret_cast<const V*>(x)[i];
+  V vr = vg;
+  if (ry) vr = reinterpret_cast<const V*>(ry)[i];
+  V o, z;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    float gz = vget(vg, e);
+    if (ry && !(vget(vr, e) > 0.f)) gz = 0.f;
+    vset(z, e, gz);
+    vset(o, e, bwd_elem(gz, vget(vx, e), 1.f, false, k));
+  }
+  if (gx) reinterpret_cast<V*>(gx)[i] = o;
+  if (RES) reinterpret_cast<V*>(gzo)[i] = z;
+}
+
+// grid x = plane (n * c), grid y = chunks of the plane
+template <int VEC, bool RES>
+__global__ void __launch_bounds__(256) bn_bwd_apply_kernel(const float* __restrict__ g, const float* __restrict__ g2,
+                                                           const float* __restrict__ x,
+                                                           const float* __restrict__ ry, const float* __restrict__ kc,
+                                                           float* __restrict__ gx, float* __restrict__ gzo, int c,
+                                                           int hwv) {
   const int plane = blockIdx.x, ch = plane % c;
   float k[5];
 #pragma unroll
   for (int i = 0; i < 5; ++i) k[i] = kc[ch * 5 + i];
   const int64_t base = (int64_t)plane * hwv;
-  for (int e = blockIdx.y * 256 + threadIdx.x; e < hwv; e += gridDim.y * 256) {
-    const V vg = reinterpret_cast<const V*>(g)[base + e], vx = reinterpret_cast<const V*>(x)[base + e];
-    V vr = vg;
-    if (ry) vr = reinterpret_cast<const V*>(ry)[base + e];
-    V o;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) vset(o, i, bwd_elem(vget(vg, i), vget(vx, i), vget(vr, i), ry != nullptr, k));
-    reinterpret_cast<V*>(gx)[base + e] = o;
-  }
+  for (int e = blockIdx.y * 256 + threadIdx.x; e < hwv; e += gridDim.y * 256)
+    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e);
 }
 
 // Small planes: flat over VEC-wide vectors.
-template <int VEC>
+template <int VEC, bool RES>
 __global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __restrict__ g,
+                                                                const float* __restrict__ g2,
                                                                 const float* __restrict__ x,
                                                                 const float* __restrict__ ry,
                                                                 const float* __restrict__ kc, float* __restrict__ gx,
-                                                                int64_t total_v, FastDiv div_hwv, FastDiv div_c,
-                                                                int c) {
-  using V = typename VecT<VEC>::T;
+                                                                float* __restrict__ gzo, int64_t total_v,
+                                                                FastDiv div_hwv, FastDiv div_c, int c) {
   for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
     const uint32_t plane = fdiv((uint32_t)i, div_hwv), ch = plane - fdiv(plane, div_c) * (uint32_t)c;
     float k[5];
 #pragma unroll
     for (int j = 0; j < 5; ++j) k[j] = kc[ch * 5 + j];
-    const V vg = reinterpret_cast<const V*>(g)[i], vx = reinterpret_cast<const V*>(x)[i];
-    V vr = vg;
-    if (ry) vr = reinterpret_cast<const V*>(ry)[i];
-    V o;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) vset(o, e, bwd_elem(vget(vg, e), vget(vx, e), vget(vr, e), ry != nullptr, k));
-    reinterpret_cast<V*>(gx)[i] = o;
+    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, i);
   }
 }
 
@@ -433,14 +449,15 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
   }
 }
 
-template <int VEC>
-__global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ x,
+template <int VEC, bool RES>
+__global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ g2,
+                                                           const float* __restrict__ x,
                                                            const float* __restrict__ ry,
                                                            const float* __restrict__ mean,
                                                            const float* __restrict__ invstd,
                                                            const float* __restrict__ gamma, float* __restrict__ gx,
                                                            float* __restrict__ dgamma, float* __restrict__ dbeta,
-                                                           int c, int hw, const Split sp) {
+                                                           float* __restrict__ gzo, int c, int hw, const Split sp) {
   using V = typename VecT<VEC>::T;
   __shared__ float kc[5];
   const int ch = blockIdx.x;
@@ -453,6 +470,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
       rg[u] = *reinterpret_cast<const V*>(g + off);
+      if (RES && g2) vadd(rg[u], *reinterpret_cast<const V*>(g2 + off));
       rx[u] = *reinterpret_cast<const V*>(x + off);
       if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
     } else {
@@ -488,7 +506,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       kc[4] = inv;
     }
   }
-  if (!gx) return;
+  if (!gx && !RES) return;
   __syncthreads();
   float k[5];
 #pragma unroll
@@ -497,11 +515,17 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   for (int u = 0; u < NR; ++u) {
     const int vv = (int)threadIdx.x + u * 256;
     if (vv < sp.nv) {
-      V o;
+      V o, z;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i)
-        vset(o, i, bwd_elem(vget(rg[u], i), vget(rx[u], i), ry ? vget(rr[u], i) : 1.f, ry != nullptr, k));
-      *reinterpret_cast<V*>(gx + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)) = o;
+      for (int i = 0; i < VEC; ++i) {
+        float gz = vget(rg[u], i);
+        if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+        vset(z, i, gz);
+        vset(o, i, bwd_elem(gz, vget(rx[u], i), 1.f, false, k));
+      }
+      const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+      if (gx) *reinterpret_cast<V*>(gx + off) = o;
+      if (RES) *reinterpret_cast<V*>(gzo + off) = z;
     }
   }
 }
@@ -633,6 +657,60 @@ OMT_EXPORT size_t omt_bn_bwd_workspace(int64_t n, int64_t c, int64_t hw) {
   return (size_t)(c * kMaxSlices * 2) * sizeof(double) + (size_t)(c * 5) * sizeof(float);
 }
 
+// The backward of every BN entry point: gz = g (+ g2) masked by relu_y > 0; RES also writes gz to gzo.
+template <bool RES>
+static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
+                       const float* relu_y, const float* save_mean, const float* save_invstd, const float* gamma,
+                       float* gx, float* dgamma, float* dbeta, float* gzo, void* workspace, hipStream_t s) {
+  const bool aligned = al16(g) && al16(g2) && al16(x) && al16(relu_y) && al16(gx) && al16(gzo);
+  const Split sp = bn_split(n, c, hw, aligned);
+  if (n * hw <= kFusedMax) {
+    if (sp.vec == 4)
+      hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y,
+                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp);
+    else
+      hipLaunchKernelGGL((bn_bwd_fused_kernel<1, RES>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y,
+                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp);
+    return launch_check("bn_bwd_fused_kernel");
+  }
+  double* part = (double*)workspace;
+  float* kc = (float*)(part + c * kMaxSlices * 2);
+  const dim3 pgrid((unsigned)c, (unsigned)sp.slices);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL((bn_bwd_part_kernel<4, RES>), pgrid, dim3(256), 0, s, g, g2, x, relu_y, save_mean, save_invstd,
+                       part, (int)c, (int)hw, sp);
+  else
+    hipLaunchKernelGGL((bn_bwd_part_kernel<1, RES>), pgrid, dim3(256), 0, s, g, g2, x, relu_y, save_mean, save_invstd,
+                       part, (int)c, (int)hw, sp);
+  if (int st = launch_check("bn_bwd_part_kernel")) return st;
+  const double m = (double)(n * hw);
+  // the apply pass needs the per-channel constants (gamma) whenever it runs: for gx, or for gzo
+  hipLaunchKernelGGL(bn_bwd_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, sp.slices,
+                     save_mean, save_invstd, (gx || RES) ? gamma : nullptr, m, kc, dgamma, dbeta);
+  if (int st = launch_check("bn_bwd_fin_kernel")) return st;
+  if (!gx && !RES) return OMT_OK;
+  float* gxo = gx;
+  const int64_t total_v = n * c * hw / sp.vec;
+  if (hw < kFlatPlane && total_v < ((int64_t)1 << 31)) {
+    const FastDiv dh = make_fastdiv((uint32_t)sp.hwv), dc = make_fastdiv((uint32_t)c);
+    const dim3 grid(grid1d(total_v, 256, 16384));
+    if (sp.vec == 4)
+      hipLaunchKernelGGL((bn_bwd_apply_flat_kernel<4, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y, kc, gxo, gzo,
+                         total_v, dh, dc, (int)c);
+    else
+      hipLaunchKernelGGL((bn_bwd_apply_flat_kernel<1, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y, kc, gxo, gzo,
+                         total_v, dh, dc, (int)c);
+    return launch_check("bn_bwd_apply_flat_kernel");
+  }
+  if (sp.vec == 4)
+    hipLaunchKernelGGL((bn_bwd_apply_kernel<4, RES>), apply_grid(n * c, hw, 4), dim3(256), 0, s, g, g2, x, relu_y, kc,
+                       gxo, gzo, (int)c, (int)(hw / 4));
+  else
+    hipLaunchKernelGGL((bn_bwd_apply_kernel<1, RES>), apply_grid(n * c, hw, 1), dim3(256), 0, s, g, g2, x, relu_y, kc,
+                       gxo, gzo, (int)c, (int)hw);
+  return launch_check("bn_bwd_apply_kernel");
+}
+
 OMT_EXPORT int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, const float* x, const float* relu_y,
                           const float* save_mean, const float* save_invstd, const float* gamma, float* gx,
                           float* dgamma, float* dbeta, void* workspace, size_t workspace_bytes, void* stream) {
@@ -640,50 +718,18 @@ OMT_EXPORT int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, cons
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_bwd: size not covered");
   if (!workspace || workspace_bytes < omt_bn_bwd_workspace(n, c, hw))
     return fail(OMT_INVALID, "omt_bn_bwd: workspace too small");
-  hipStream_t s = stream_of(stream);
-  const bool aligned = al16(g) && al16(x) && al16(relu_y) && al16(gx);
-  const Split sp = bn_split(n, c, hw, aligned);
-  if (n * hw <= kFusedMax) {
-    if (sp.vec == 4)
-      hipLaunchKernelGGL(bn_bwd_fused_kernel<4>, dim3((unsigned)c), dim3(256), 0, s, g, x, relu_y, save_mean,
-                         save_invstd, gamma, gx, dgamma, dbeta, (int)c, (int)hw, sp);
-    else
-      hipLaunchKernelGGL(bn_bwd_fused_kernel<1>, dim3((unsigned)c), dim3(256), 0, s, g, x, relu_y, save_mean,
-                         save_invstd, gamma, gx, dgamma, dbeta, (int)c, (int)hw, sp);
-    return launch_check("bn_bwd_fused_kernel");
-  }
-  double* part = (double*)workspace;
-  float* kc = (float*)(part + c * kMaxSlices * 2);
-  const dim3 pgrid((unsigned)c, (unsigned)sp.slices);
-  if (sp.vec == 4)
-    hipLaunchKernelGGL(bn_bwd_part_kernel<4>, pgrid, dim3(256), 0, s, g, x, relu_y, save_mean, save_invstd, part,
-                       (int)c, (int)hw, sp);
-  else
-    hipLaunchKernelGGL(bn_bwd_part_kernel<1>, pgrid, dim3(256), 0, s, g, x, relu_y, save_mean, save_invstd, part,
-                       (int)c, (int)hw, sp);
-  if (int st = launch_check("bn_bwd_part_kernel")) return st;
-  const double m = (double)(n * hw);
-  hipLaunchKernelGGL(bn_bwd_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, sp.slices,
-                     save_mean, save_invstd, gx ? gamma : nullptr, m, kc, dgamma, dbeta);
-  if (int st = launch_check("bn_bwd_fin_kernel")) return st;
-  if (!gx) return OMT_OK;
-  const int64_t total_v = n * c * hw / sp.vec;
-  if (hw < kFlatPlane && total_v < ((int64_t)1 << 31)) {
-    const FastDiv dh = make_fastdiv((uint32_t)sp.hwv), dc = make_fastdiv((uint32_t)c);
-    const dim3 grid(grid1d(total_v, 256, 16384));
-    if (sp.vec == 4)
-      hipLaunchKernelGGL(bn_bwd_apply_flat_kernel<4>, grid, dim3(256), 0, s, g, x, relu_y, kc, gx, total_v, dh, dc,
-                         (int)c);
-    else
-      hipLaunchKernelGGL(bn_bwd_apply_flat_kernel<1>, grid, dim3(256), 0, s, g, x, relu_y, kc, gx, total_v, dh, dc,
-                         (int)c);
-    return launch_check("bn_bwd_apply_flat_kernel");
-  }
-  if (sp.vec == 4)
-    hipLaunchKernelGGL(bn_bwd_apply_kernel<4>, apply_grid(n * c, hw, 4), dim3(256), 0, s, g, x, relu_y, kc, gx,
-                       (int)c, (int)(hw / 4));
-  else
-    hipLaunchKernelGGL(bn_bwd_apply_kernel<1>, apply_grid(n * c, hw, 1), dim3(256), 0, s, g, x, relu_y, kc, gx,
-                       (int)c, (int)hw);
-  return launch_check("bn_bwd_apply_kernel");
+  return bn_bwd_impl<false>(n, c, hw, g, nullptr, x, relu_y, save_mean, save_invstd, gamma, gx, dgamma, dbeta, nullptr,
+                            workspace, stream_of(stream));
+}
+
+OMT_EXPORT int omt_bn_bwd_res(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
+                              const float* relu_y, const float* save_mean, const float* save_invstd,
+                              const float* gamma, float* gx, float* dgamma, float* dbeta, float* gz,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (!g || !x || !save_mean || !save_invstd || !gz || !gamma) return fail(OMT_INVALID, "omt_bn_bwd_res: null pointer");
+  if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_bwd_res: size not covered");
+  if (!workspace || workspace_bytes < omt_bn_bwd_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_bwd_res: workspace too small");
+  return bn_bwd_impl<true>(n, c, hw, g, g2, x, relu_y, save_mean, save_invstd, gamma, gx, dgamma, dbeta, gz, workspace,
+                           stream_of(stream));
 }

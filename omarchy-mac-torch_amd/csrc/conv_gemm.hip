@@ -1559,14 +1559,17 @@ static int pick_tile(const Tile (&tiles)[N], int64_t P, int64_t Q, int64_t z, in
   return best;
 }
 
-// The last three carry deeper K-blocks: more MFMA work per load round trip for grids of about one workgroup per CU,
-// where the loads' latency is not hidden by other workgroups.
+// Tiles 6-8 carry deeper K-blocks: more MFMA work per load round trip for grids of about one workgroup per CU,
+// where the loads' latency is not hidden by other workgroups. Tiles 14-16 (32 x 64) give small layers (ResNet-18 at
+// 64x64 input: 64 channels over 8192 pixels) twice the workgroups of the 64 x 64 tile, so that every CU holds one
+// without a K split.
 static const Tile kGatherTiles[] = {
     {64, 256, 64, 64, 1.00f},     {128, 128, 64, 64, 1.00f},    {64, 128, 32, 64, 0.92f},
     {32, 256, 32, 64, 0.90f},     {16, 256, 16, 64, 0.80f},     {64, 64, 32, 32, 0.80f},
     {64, 64, 32, 32, 0.90f, 64},  {64, 128, 32, 64, 0.95f, 32}, {128, 64, 64, 32, 0.95f, 32},
     {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3}, {64, 64, 32, 32, 0.90f, 32, 3},
     {64, 128, 32, 64, 0.97f, 32, 2}, {64, 128, 32, 64, 0.95f, 16, 0, 1},
+    {32, 64, 16, 32, 0.60f}, {32, 64, 16, 32, 0.65f, 32}, {32, 64, 16, 32, 0.65f, 64},
 };
 // Plan tile index t < 3 * kNGather: kGatherTiles[t % kNGather] in one of three variants. t < kNGather: tap-major K
 // order where it applies, over a re-packed filter; kNGather <= t < 2 kNGather: channel-major order (no filter
@@ -1604,6 +1607,9 @@ static void gather_dispatch(int ti, const GatherArgs& a, dim3 grid, hipStream_t 
     case 9: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     case 11: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 14: hipLaunchKernelGGL((conv_gather_kernel<32, 64, 16, 32, 16, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 15: hipLaunchKernelGGL((conv_gather_kernel<32, 64, 16, 32, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((conv_gather_kernel<32, 64, 16, 32, 64, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
     default: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, MODE, BN, 2>), grid, dim3(256), 0, s, a); break;
   }
 }
@@ -1618,6 +1624,8 @@ static void gather_inplace_dispatch(int ti, const GatherArgs& a, dim3 grid, hipS
     case 8: hipLaunchKernelGGL((conv_gather_kernel<128, 64, 64, 32, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
     case 2: case 10: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;
     case 7: case 12: hipLaunchKernelGGL((conv_gather_kernel<64, 128, 32, 64, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 15: hipLaunchKernelGGL((conv_gather_kernel<32, 64, 16, 32, 32, M, false, 2>), grid, dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((conv_gather_kernel<32, 64, 16, 32, 64, M, false, 2>), grid, dim3(256), 0, s, a); break;
     default: hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, M, false, 2>), grid, dim3(256), 0, s, a); break;  // 5, 9, 11
   }
 }

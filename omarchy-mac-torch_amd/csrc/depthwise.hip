@@ -160,7 +160,8 @@ __global__ void __launch_bounds__(256) dw_wgrad_reduce_kernel(const float* __res
 
 // ---- stride 1, "same" padding, ks 3 / 5 / 7: LDS-tiled -----------------------------------------------------------
 
-constexpr int kDwOutPerThread = 8;  // output elements per thread of a tiled work unit
+constexpr int kDwOutPerThread = 8;  // output elements per thread of a tiled forward / grad-input work unit
+constexpr int kDwWgOut = 16;        // output gradients per thread of a tiled grad-weight batch
 
 struct DwTiling {
   int rows;    // output rows per work unit
@@ -244,6 +245,82 @@ __global__ void __launch_bounds__(NT) dw_s1_kernel(const float* __restrict__ x, 
   }
 }
 
+// Whole small planes, several images of one channel per workgroup. A workgroup of this kernel takes images
+// n0 .. n0 + nb - 1 (nb <= B) of channel ch: every thread issues the loads of its kDwBatchEPT interior elements of
+// the batch first (consecutive threads on consecutive elements of a plane), zeroes the batch's LDS tiles meanwhile
+// (one (H + KS - 1) x (W + KS - 1) tile per plane: the zero border is the padding), stores the values into the tiles'
+// interiors and computes every output of the batch from LDS with the channel's filter in registers. Several planes
+// per workgroup keep kDwBatchEPT loads per thread in flight where a plane alone would give each thread a few.
+constexpr int kDwBatchEPT = 16;
+struct DwBatch {
+  int B, tile, pitch;  // images per workgroup, LDS floats per plane, LDS row pitch W + KS - 1
+  FastDiv div_hw, div_w, div_c;
+};
+template <int KS, bool FLIP, int NT>
+__global__ void __launch_bounds__(NT) dw_s1_batch_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                         const float* __restrict__ bias, const float* __restrict__ bm,
+                                                         const float* __restrict__ bv, const float* __restrict__ bg,
+                                                         const float* __restrict__ bb, float eps,
+                                                         float* __restrict__ y, int N, int C, int H, int W,
+                                                         const DwBatch d) {
+  extern __shared__ float tile[];
+  constexpr int PAD = KS / 2, KK = KS * KS, EPT = kDwBatchEPT;
+  const int grp = (int)fdiv(blockIdx.x, d.div_c), ch = (int)blockIdx.x - grp * C;
+  const int n0 = grp * d.B, nb = min(d.B, N - n0);
+  const int HW = H * W, total = nb * HW, pitch = d.pitch;
+  const int64_t cstride = (int64_t)C * HW;
+  const float* src = x + ((int64_t)n0 * C + ch) * HW;
+  float v[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = (int)threadIdx.x + j * NT;
+    v[j] = 0.f;
+    if (e < total) {
+      const int i = (int)fdiv((uint32_t)e, d.div_hw);
+      v[j] = src[i * cstride + (e - i * HW)];
+    }
+  }
+  for (int e = threadIdx.x; e < nb * d.tile; e += NT) tile[e] = 0.f;
+  float sc = 1.f, sh = 0.f;
+  const bool bn = !FLIP && bm != nullptr;
+  if (bn) {
+    const float inv = rsqrtf(bv[ch] + eps);
+    sc = inv * bg[ch];
+    sh = bb[ch] - bm[ch] * sc;
+  }
+  __syncthreads();  // the zero fill is done before the interiors are written
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = (int)threadIdx.x + j * NT;
+    if (e < total) {
+      const int i = (int)fdiv((uint32_t)e, d.div_hw), rem = e - i * HW;
+      const int r = (int)fdiv((uint32_t)rem, d.div_w), c = rem - r * W;
+      tile[i * d.tile + (r + PAD) * pitch + c + PAD] = bn ? fmaxf(fmaf(v[j], sc, sh), 0.f) : v[j];
+    }
+  }
+  float wr[KK];
+#pragma unroll
+  for (int i = 0; i < KK; ++i) wr[i] = w[ch * KK + (FLIP ? KK - 1 - i : i)];
+  const float b = (!FLIP && bias) ? bias[ch] : 0.f;
+  __syncthreads();
+  float* dst = y + ((int64_t)n0 * C + ch) * HW;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int o = (int)threadIdx.x + j * NT;
+    if (o < total) {
+      const int i = (int)fdiv((uint32_t)o, d.div_hw), rem = o - i * HW;
+      const int r = (int)fdiv((uint32_t)rem, d.div_w), c = rem - r * W;
+      const float* tp = tile + i * d.tile + r * pitch + c;
+      float acc = 0.f;
+#pragma unroll
+      for (int ky = 0; ky < KS; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < KS; ++kx) acc = fmaf(tp[ky * pitch + kx], wr[ky * KS + kx], acc);
+      dst[i * cstride + rem] = acc + b;
+    }
+  }
+}
+
 // Grad-weight work of one channel: units u = (image u / chunks, row chunk u % chunks), N * chunks of them. A
 // workgroup takes `group` consecutive units and stages `batch` of them at a time (several whole planes when a plane
 // has few outputs; then chunks == 1): every load of a batch (the output gradients into registers, the input rows
@@ -281,18 +358,18 @@ __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict
     b.nb = min(wu.batch, uend - u0);
     b.n0 = (int)fdiv((uint32_t)u0, t.div_chunks);
     b.r0 = (u0 - b.n0 * t.chunks) * t.rows;
-    b.nout = wu.batch > 1 ? b.nb * HW : min(t.rows, H - b.r0) * W;  // at most kDwOutPerThread * NT (dw_units)
+    b.nout = wu.batch > 1 ? b.nb * HW : min(t.rows, H - b.r0) * W;  // at most kDwWgOut * NT (dw_units)
     return b;
   };
   // the loads of a batch: its output gradients into g, its input rows into tile (tile float e: tile i = e / wu.tile,
   // row rr, column cc within it, is input row r0 - PAD + rr, column cc - PAD of unit u0 + i; padding and lanes past
   // the batch load offset kOOB, which reads 0)
-  auto issue = [&](const Batch& b, float* tile, float (&g)[kDwOutPerThread]) {
+  auto issue = [&](const Batch& b, float* tile, float (&g)[kDwWgOut]) {
     const int64_t base = ((int64_t)b.n0 * C + ch) * HW;
     const uint32_t span = ((uint32_t)(b.nb - 1) * cstride + (uint32_t)HW) * 4u;  // < 2^31 (dw_units)
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(gy + base, span);
 #pragma unroll
-    for (int j = 0; j < kDwOutPerThread; ++j) {
+    for (int j = 0; j < kDwWgOut; ++j) {
       const int o = (int)threadIdx.x + j * NT;
       uint32_t off = kOOB;
       if (o < b.nout) {
@@ -318,9 +395,9 @@ __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict
   float acc[KK];
 #pragma unroll
   for (int i = 0; i < KK; ++i) acc[i] = 0.f;
-  auto fma_batch = [&](const Batch& b, const float* tile, const float (&g)[kDwOutPerThread]) {
+  auto fma_batch = [&](const Batch& b, const float* tile, const float (&g)[kDwWgOut]) {
 #pragma unroll 2
-    for (int j = 0; j < kDwOutPerThread; ++j) {
+    for (int j = 0; j < kDwWgOut; ++j) {
       const int o = (int)threadIdx.x + j * NT;
       if (o < b.nout) {
         const int i = wu.batch > 1 ? (int)fdiv((uint32_t)o, wu.div_out) : 0, pix = o - i * (wu.batch > 1 ? HW : 0);
@@ -342,7 +419,7 @@ __global__ void __launch_bounds__(NT) dw_wgrad_s1_kernel(const float* __restrict
     __syncthreads();
   };
 
-  float ga[kDwOutPerThread], gb[kDwOutPerThread];
+  float ga[kDwWgOut], gb[kDwWgOut];
   Batch ba = batch_at(ubeg), bb;
   issue(ba, buf[0], ga);
   for (int u0 = ubeg; u0 < uend; u0 += 2 * wu.batch) {
@@ -408,7 +485,7 @@ static bool dw_s1_wgrad(const omt_conv_geo* g) {
   const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, (int)g->ks, dw_threads(g));
   return 2 * cdiv((int64_t)(t.rows + g->ks - 1) * t.pitch, 64) * 64 * 4 <= kDwMaxLds;
 }
-// Units of the tiled grad weight: whole planes batched while a batch keeps at most kDwOutPerThread outputs per thread,
+// Units of the tiled grad weight: whole planes batched while a batch keeps at most kDwWgOut outputs per thread,
 // one load per thread and 64-float row (kStageBatch rows per wave) and two buffers in kDwMaxLds of LDS; groups of
 // batches sized for about 2048 workgroups.
 static DwUnits dw_units(const omt_conv_geo* g) {
@@ -421,7 +498,7 @@ static DwUnits dw_units(const omt_conv_geo* g) {
   if (t.chunks == 1) {
     // the batch's planes span ((b - 1) * C + 1) * H * W floats, read through one buffer resource (< 2 GiB)
     const int64_t span_cap = (kMaxBufBytes / 4 / (g->ih * g->iw) - 1) / g->ci + 1;
-    b = std::min<int64_t>({(int64_t)nt * kDwOutPerThread / (g->ih * g->iw), (int64_t)nt * kStageBatch / u.tile,
+    b = std::min<int64_t>({(int64_t)nt * kDwWgOut / (g->ih * g->iw), (int64_t)nt * kStageBatch / u.tile,
                            ((int64_t)kDwMaxLds / 8 - 64) / u.tile, (int64_t)u.units, span_cap});
     b = std::max<int64_t>(b, 1);
   }
@@ -439,9 +516,39 @@ static int64_t dw_s1_groups(const omt_conv_geo* g) {
   return cdiv(u.units, u.group);
 }
 
+// The batched small-plane kernel: B images per workgroup with their tiles in kDwMaxLds, for planes of at most
+// kDwBatchMaxHW elements. Measured against the row-chunk kernel (graph replays, b32): 7x7 planes 11.9 -> 8.5 us
+// (576 channels, 5x5), 14x14 18.5 -> 11.9 us (240 channels, 5x5); from 28x28 up the row-chunk kernel is faster
+// (28x28: 12.9 against 16.1 us), so larger planes keep it.
+constexpr int kDwBatchNT = 256, kDwBatchMaxHW = 256;
+static DwBatch dw_batch(const omt_conv_geo* g) {
+  DwBatch d{};
+  const int64_t hw = g->ih * g->iw, tile = (g->ih + g->ks - 1) * (g->iw + g->ks - 1);
+  int64_t b = std::min<int64_t>({(int64_t)kDwBatchEPT * kDwBatchNT / hw, g->n, (int64_t)kDwMaxLds / 4 / tile});
+  d.B = (int)std::max<int64_t>(b, 0);
+  d.tile = (int)tile;
+  d.pitch = (int)(g->iw + g->ks - 1);
+  d.div_hw = make_fastdiv((uint32_t)hw);
+  d.div_w = make_fastdiv((uint32_t)g->iw);
+  d.div_c = make_fastdiv((uint32_t)g->ci);
+  return d;
+}
+
 template <bool FLIP>
 static int launch_dw_s1(const omt_conv_geo* g, const float* x, const float* w, const float* bias, const float* bm,
                         const float* bv, const float* bg, const float* bb, float eps, float* y, hipStream_t s) {
+  const DwBatch d = dw_batch(g);
+  if (d.B >= 1 && g->ih * g->iw <= kDwBatchMaxHW && g->n * g->ci * g->ih * g->iw < ((int64_t)1 << 31)) {
+    const dim3 grid((unsigned)(cdiv(g->n, d.B) * g->ci));
+    const size_t lds = (size_t)d.B * d.tile * sizeof(float);
+    const int N = (int)g->n, C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
+#define OMT_DW_B(KS_) \
+  hipLaunchKernelGGL((dw_s1_batch_kernel<KS_, FLIP, kDwBatchNT>), grid, dim3(kDwBatchNT), lds, s, x, w, bias, bm, bv, \
+                     bg, bb, eps, y, N, C, H, W, d)
+    if (g->ks == 3) OMT_DW_B(3); else if (g->ks == 5) OMT_DW_B(5); else OMT_DW_B(7);
+#undef OMT_DW_B
+    return launch_check("dw_s1_batch_kernel");
+  }
   const int nt = dw_threads(g), ks = (int)g->ks;
   const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, ks, nt);
   const dim3 grid((unsigned)(g->n * g->ci * t.chunks));

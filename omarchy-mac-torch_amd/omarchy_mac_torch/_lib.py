@@ -151,6 +151,7 @@ SIGNATURES = {
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
     "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_bwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_bwd_res": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_maxpool_fwd": (I32, [I64] * 13 + [VP, VP, VP, VP]),
     "omt_maxpool_bwd": (I32, [I64] * 13 + [VP, VP, VP, VP]),
     "omt_avgpool_fwd": (I32, [I64] * 11 + [I32, I64, VP, VP, VP]),

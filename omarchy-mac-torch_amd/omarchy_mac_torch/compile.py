@@ -11,7 +11,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
   1. training BatchNorm (`_native_batch_norm_legit_functional`) whose normalized output only feeds a ReLU
      -> omt.bn_relu_train (statistics, normalize and ReLU in the library's BN kernels);
   2. its backward, `native_batch_norm_backward(threshold_backward(g, y, 0), ...)` -> omt.bn_relu_backward (the ReLU
-     mask read from y inside the BN backward reductions and apply);
+     mask read from y inside the BN backward reductions and apply); where the masked gradient also feeds a residual
+     branch (the end of a ResNet basic block) -> omt.bn_relu_res_backward, which returns it as a fourth output and
+     takes along the add of the block output's two gradients in front of the mask;
   3. a dense convolution whose only user is a ReLU -> omt.conv_act (ReLU in the GEMM epilogue), or an eval BatchNorm
      (`_native_batch_norm_legit_no_training`, optionally followed by ReLU) -> omt.conv_bn_act_eval (BatchNorm folded
      into the conv's weights and bias).
@@ -234,6 +236,44 @@ def fuse_bn_relu_backward(graph):
     return count
 
 
+def fuse_bn_relu_res_backward(graph):
+    """t = threshold_backward(a, y, 0) with several users, one of them native_batch_norm_backward(t, ...): that BN
+    backward and the mask become one omt.bn_relu_res_backward(g, g2, ...), whose fourth output replaces t for the other
+    users; a = add(g, g2) feeding only t goes in as well. The fused node takes t's place in the graph (the BN
+    backward's other operands are saved tensors, defined earlier; y, often a detach of one, comes before t)."""
+    count = 0
+    for t in list(graph.nodes):
+        if t.op != "call_function" or t.target is not aten.threshold_backward.default or t.args[2] != 0:
+            continue
+        if len(t.users) < 2 or not _on_device_f32(t, 4):
+            continue
+        bn = next((u for u in t.users if u.op == "call_function" and u.target is aten.native_batch_norm_backward.default
+                   and u.args[0] is t and u.args[7] and u.args[2] is not None and _on_device_f32(u.args[1], 4)), None)
+        if bn is None:
+            continue
+        a, y = t.args[0], t.args[1]
+        g, g2 = a, None
+        if (isinstance(a, Node) and a.op == "call_function" and a.target is aten.add.Tensor and len(a.users) == 1
+                and len(a.args) == 2 and not a.kwargs and _meta(a.args[0]) is not None and _meta(a.args[1]) is not None
+                and tuple(_meta(a.args[0]).shape) == tuple(_meta(a.args[1]).shape)
+                and _on_device_f32(a.args[0], 4) and _on_device_f32(a.args[1], 4)):
+            g, g2 = a.args
+        _, x, w, rm, rv, mean, invstd, train, eps, mask = bn.args[:10]
+        order = {nd: i for i, nd in enumerate(graph.nodes)}
+        if any(isinstance(v, Node) and order[v] >= order[t] for v in (x, w, mean, invstd)):
+            continue
+        fused = _call_before(graph, t, omt.bn_relu_res_backward.default, (g, g2, x, y, w, mean, invstd, list(mask)))
+        gz = _call_before(graph, t, operator.getitem, (fused, 3), meta_from=t)
+        _move_getitems(graph, bn, fused)
+        graph.erase_node(bn)
+        t.replace_all_uses_with(gz)
+        graph.erase_node(t)
+        if g2 is not None:
+            graph.erase_node(a)
+        count += 1
+    return count
+
+
 # ---- rewrite 3: conv epilogues ----
 
 def _is_dense_conv(n):
@@ -282,7 +322,8 @@ def fuse_conv_epilogues(graph):
 def _compile(gm, example_inputs):
     g = gm.graph
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
-             "bn_relu": fuse_bn_relu_train(g), "bn_relu_backward": fuse_bn_relu_backward(g),
+             "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
+             "bn_relu_backward": fuse_bn_relu_backward(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()

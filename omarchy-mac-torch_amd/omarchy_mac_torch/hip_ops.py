@@ -331,6 +331,22 @@ def batch_norm_backward(g, x, save_mean, save_invstd, gamma, relu_y=None, output
     return gx, dg, db
 
 
+def batch_norm_backward_res(g, g2, x, save_mean, save_invstd, gamma, relu_y, output_mask=(True, True, True)):
+    """The backward of a residual block's end: gz = (g + g2) masked by relu_y > 0 (g2 may be None), BatchNorm's
+    (gx, dgamma, dbeta) of gz, and gz. Returns (gx, dgamma, dbeta, gz)."""
+    g, g2, x, relu_y = _need(g, "g", 4), _need(g2, "g2", 4), _need(x, "x", 4), _need(relu_y, "relu_y", 4)
+    n, c, h, w = x.shape
+    gx = torch.empty_like(x) if output_mask[0] else None
+    dg = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[1] else None
+    db = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[2] else None
+    gz = torch.empty_like(x)
+    ws, nb = _workspace(L.omt_bn_bwd_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_bwd_res(n, c, h * w, _ptr(g), _ptr(g2), _ptr(x), _ptr(relu_y), _ptr(_need(save_mean, "mean", 1)),
+                           _ptr(_need(save_invstd, "invstd", 1)), _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg),
+                           _ptr(db), _ptr(gz), _ptr(ws), nb, _stream(x.device)), "batch_norm_backward_res")
+    return gx, dg, db, gz
+
+
 # ---- pooling ----------------------------------------------------------------------------------------------------
 
 def pool_out(size, k, s, p, d=1, ceil=False):
@@ -405,6 +421,16 @@ def adaptive_avg_pool2d_backward(g, x_shape):
     check(L.omt_adapool_bwd(n * c, ih, iw, g.shape[2], g.shape[3], _ptr(g), _ptr(gx), _stream(g.device)),
           "adaptive_avg_pool2d_backward")
     return gx
+
+
+# ---- pointwise (reference csrc/elementwise.cpp:702-817) ---------------------------------------------------------
+
+def fill_(t, value):
+    """t[:] = value (a contiguous float32 device tensor), through omt_pointwise's fill."""
+    if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+        raise TypeError("fill_: a contiguous float32 tensor on the HIP device expected")
+    check(L.omt_pointwise(_lib.OMT_PW_FILL, t.numel(), None, None, float(value), _ptr(t), _stream(t.device)), "fill_")
+    return t
 
 
 # ---- fused optimizers (reference csrc/optim.cpp:12-67) -----------------------------------------------------------

@@ -155,8 +155,9 @@ FALLBACKS = _FallbackView()
 # One JSON object {"dir,n,ci,co,ih,iw,oh,ow,ks,stride,pad": [tile, slices]}, the reference's key format. The values
 # index this library's gfx950 tile tables (the file name carries the gather table's size), so the file is not the
 # reference's, whose entries name its own tiles and a split-K multiplier.
-TUNE_FILE = os.environ.get("OMARCHY_MAC_TORCH_TUNE_FILE",
-                           os.path.expanduser("~/.cache/omarchy-mac-torch/tuning-gfx950-t14.json"))
+TUNE_FILE = os.environ.get(
+    "OMARCHY_MAC_TORCH_TUNE_FILE",
+    os.path.expanduser(f"~/.cache/omarchy-mac-torch/tuning-gfx950-t{_lib.L.omt_conv_num_tiles(_lib.OMT_DIR_FWD) // 3}.json"))
 
 
 class TuningStore:

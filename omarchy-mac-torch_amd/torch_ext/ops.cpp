@@ -380,6 +380,16 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_ref(const Tensor& g, 
   Tensor gz = at::threshold_backward(g, y, 0);
   return at::native_batch_norm_backward(gz, x, w, std::nullopt, std::nullopt, mean, invstd, true, 0.0, mask);
 }
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_ref(const Tensor& g,
+                                                                           const std::optional<Tensor>& g2,
+                                                                           const Tensor& x, const Tensor& y,
+                                                                           const Tensor& w, const Tensor& mean,
+                                                                           const Tensor& invstd,
+                                                                           std::array<bool, 3> mask) {
+  Tensor gz = at::threshold_backward(defined(g2) ? g + *g2 : g, y, 0);
+  auto r = at::native_batch_norm_backward(gz, x, w, std::nullopt, std::nullopt, mean, invstd, true, 0.0, mask);
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), gz};
+}
 static Tensor conv_act_ref(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
                            IntArrayRef padding, int64_t act) {
   Tensor y = at::convolution(x, w, b, stride, padding, {1, 1}, false, {0, 0}, 1);
@@ -451,6 +461,31 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_,
         "omt::bn_relu_backward");
   return {gx, dg, db};
 }
+// The backward of BatchNorm -> [+ residual] -> ReLU at a residual block's end, with the incoming gradient the sum of
+// the block output's two uses (g + g2): gz = (g + g2) [y > 0] for the residual branch, and BatchNorm's grads of gz.
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_dev(const Tensor& g_,
+                                                                           const std::optional<Tensor>& g2_,
+                                                                           const Tensor& x_, const Tensor& y_,
+                                                                           const Tensor& w, const Tensor& mean,
+                                                                           const Tensor& invstd,
+                                                                           std::array<bool, 3> mask) {
+  cover(f32(g_) && f32(x_) && f32(y_) && x_.dim() == 4 && whole(w) && whole(mean) && whole(invstd) &&
+            g_.sizes() == x_.sizes() && y_.sizes() == x_.sizes() &&
+            (!defined(g2_) || (f32(*g2_) && g2_->sizes() == x_.sizes())),
+        "4-D float32 operands of one shape");
+  Tensor g = contig(g_), x = contig(x_), y = contig(y_);
+  Tensor g2 = defined(g2_) ? contig(*g2_) : Tensor();
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
+  Tensor dg = mask[1] ? empty_dev({c}) : Tensor();
+  Tensor db = mask[2] ? empty_dev({c}) : Tensor();
+  Tensor gz = empty_dev(x.sizes());
+  Tensor ws = workspace(omt_bn_bwd_workspace(n, c, hw));
+  check(omt_bn_bwd_res(n, c, hw, fp(g), g2.defined() ? fp(g2) : nullptr, fp(x), fp(y), fp(mean), fp(invstd), fp(w),
+                       fpm(gx), fpm(dg), fpm(db), fpm(gz), wsptr(ws), wsbytes(ws), cur_stream()),
+        "omt::bn_relu_res_backward");
+  return {gx, dg, db, gz};
+}
 static Tensor conv_act_dev(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
                            IntArrayRef padding, int64_t act) {
   cover(stride.size() == 2 && padding.size() == 2, "2-D stride and padding");
@@ -491,6 +526,15 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_k(const Tensor& g, co
   return dev_or_ref<&bn_relu_backward_dev, &bn_relu_backward_ref>("omt::bn_relu_backward", g, x, y, w, mean, invstd,
                                                                   mask);
 }
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_k(const Tensor& g,
+                                                                         const std::optional<Tensor>& g2,
+                                                                         const Tensor& x, const Tensor& y,
+                                                                         const Tensor& w, const Tensor& mean,
+                                                                         const Tensor& invstd,
+                                                                         std::array<bool, 3> mask) {
+  return dev_or_ref<&bn_relu_res_backward_dev, &bn_relu_res_backward_ref>("omt::bn_relu_res_backward", g, g2, x, y, w,
+                                                                          mean, invstd, mask);
+}
 static Tensor conv_act_k(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef s,
                          IntArrayRef p, int64_t act) {
   return dev_or_ref<&conv_act_dev, &conv_act_ref>("omt::conv_act", x, w, b, s, p, act);
@@ -507,6 +551,9 @@ TORCH_LIBRARY(omt, m) {
         "(Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("bn_relu_backward(Tensor g, Tensor x, Tensor y, Tensor w, Tensor mean, Tensor invstd, bool[3] mask) -> "
         "(Tensor, Tensor, Tensor)");
+  // the backward of a residual block's end: gz = (g + g2) [y > 0], BatchNorm's (gx, dgamma, dbeta) of gz, and gz
+  m.def("bn_relu_res_backward(Tensor g, Tensor? g2, Tensor x, Tensor y, Tensor w, Tensor mean, Tensor invstd, "
+        "bool[3] mask) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("conv_act(Tensor x, Tensor w, Tensor? b, int[] stride, int[] padding, int act) -> Tensor");
   // training BatchNorm updating the running statistics in place, then + residual and ReLU (act 1): the compile
   // backend's form of BatchNorm -> [add] -> [ReLU] with the buffer updates kept in the graph
@@ -519,6 +566,7 @@ TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("bn_relu_train", &bn_relu_train_ref);
   m.impl("bn_train_", &bn_train_inplace_ref);
   m.impl("bn_relu_backward", &bn_relu_backward_ref);
+  m.impl("bn_relu_res_backward", &bn_relu_res_backward_ref);
   m.impl("conv_act", &conv_act_ref);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
 }
@@ -526,6 +574,7 @@ TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_train", &bn_relu_train_k);
   m.impl("bn_train_", &bn_train_inplace_k);
   m.impl("bn_relu_backward", &bn_relu_backward_k);
+  m.impl("bn_relu_res_backward", &bn_relu_res_backward_k);
   m.impl("conv_act", &conv_act_k);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);
 }

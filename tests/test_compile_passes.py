@@ -112,3 +112,71 @@ def test_bn_in_place_needs_sole_copies(oc):
     assert oc.fuse_bn_train_in_place(gm.graph)["bn"] == 0
     # the ReLU still fuses through the functional rewrite
     assert oc.fuse_bn_relu_train(gm.graph) == 1
+
+
+def _block_end_backward_graph(oc, with_add, second_user):
+    """Backward graph of a residual block's end, relu(bn(x) + r): t = threshold_backward(a, y, 0) with
+    a = g_main + g_res (with_add) or a plain input, feeding the block's BatchNorm backward and a second user:
+    the shortcut's add ("add") or the projection shortcut's BatchNorm backward ("bn")."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    shp, c = (2, 4, 3, 3), 4
+
+    def ph(name, shape):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape)
+        return n
+
+    gm_, gr, y, x, w, mean, invstd = (ph("g_main", shp), ph("g_res", shp), ph("y", shp), ph("x", shp), ph("w", (c,)),
+                                      ph("mean", (c,)), ph("invstd", (c,)))
+    x2, w2, mean2, invstd2, other = ph("x2", shp), ph("w2", (c,)), ph("mean2", (c,)), ph("invstd2", (c,)), ph("o", shp)
+    a = gm_
+    if with_add:
+        a = g.call_function(aten.add.Tensor, (gm_, gr))
+        a.meta["val"] = _fake(mode, dev, shp)
+    yd = g.call_function(aten.detach.default, (y,))  # as AOTAutograd emits it: after the add, right before the mask
+    yd.meta["val"] = _fake(mode, dev, shp)
+    t = g.call_function(aten.threshold_backward.default, (a, yd, 0))
+    t.meta["val"] = _fake(mode, dev, shp)
+    bn = g.call_function(aten.native_batch_norm_backward.default,
+                         (t, x, w, None, None, mean, invstd, True, 1e-5, [True, True, True]))
+    outs = [g.call_function(operator.getitem, (bn, i)) for i in range(3)]
+    if second_user == "add":
+        u = g.call_function(aten.add.Tensor, (t, other))
+        extra = (u,)
+    else:
+        bn2 = g.call_function(aten.native_batch_norm_backward.default,
+                              (t, x2, w2, None, None, mean2, invstd2, True, 1e-5, [True, True, True]))
+        extra = tuple(g.call_function(operator.getitem, (bn2, i)) for i in range(3))
+    g.output(tuple(outs) + extra)
+    return GraphModule(torch.nn.Module(), g)
+
+
+@pytest.mark.parametrize("with_add", [True, False])
+@pytest.mark.parametrize("second_user", ["add", "bn"])
+def test_bn_relu_res_backward(oc, with_add, second_user):
+    """The masked gradient of a block's end feeds its BatchNorm backward and the shortcut: add + threshold_backward +
+    that BatchNorm backward become one omt.bn_relu_res_backward whose fourth output feeds the shortcut; the rewritten
+    graph gives the original's results on CPU tensors."""
+    gm = _block_end_backward_graph(oc, with_add, second_user)
+    ref = copy.deepcopy(gm)
+    assert oc.fuse_bn_relu_res_backward(gm.graph) == 1
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    assert t.count(torch.ops.omt.bn_relu_res_backward.default) == 1 and aten.threshold_backward.default not in t
+    assert t.count(aten.native_batch_norm_backward.default) == (1 if second_user == "bn" else 0)
+    assert t.count(aten.add.Tensor) == (1 if second_user == "add" else 0)
+    fused = next(n for n in gm.graph.nodes if n.target is torch.ops.omt.bn_relu_res_backward.default)
+    assert (fused.args[1] is not None) == with_add
+    gen = torch.Generator().manual_seed(3)
+    shp, c = (2, 4, 3, 3), 4
+    args = [torch.randn(shp, generator=gen) for _ in range(4)] + [torch.rand(c, generator=gen) + 0.5,
+                                                                  torch.randn(c, generator=gen),
+                                                                  torch.rand(c, generator=gen) + 0.5]
+    args += [torch.randn(shp, generator=gen), torch.rand(c, generator=gen) + 0.5, torch.randn(c, generator=gen),
+             torch.rand(c, generator=gen) + 0.5, torch.randn(shp, generator=gen)]
+    for o_ref, o_new in zip(ref(*args), gm(*args)):
+        torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)

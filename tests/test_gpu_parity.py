@@ -498,14 +498,16 @@ def test_depthwise(cuda, ops, ks, s, p):
 
 @pytest.mark.parametrize("ks", [3, 5, 7])
 def test_depthwise_tiled_stride1(cuda, ops, ks):
-    """The LDS-tiled stride-1 "same" kernels on plane shapes that exercise one-wave workgroups (<= 128 outputs),
-    several row chunks per plane and wide rows; the eval BN + ReLU loader across chunk boundaries. Grad weight stages
-    several small planes per batch: image counts that leave a short last batch (13 images of 9x9 in batches of 6) and
-    a short last group (37 of 20x20 in batches of 5, 64 of 14x14 in batches of up to 10)."""
+    """The LDS-tiled stride-1 "same" kernels. Forward and grad input: planes of up to 256 elements run several images
+    of a channel per workgroup (fewer images than a batch holds; 64 of 14x14 in batches of 20, leaving a short last
+    batch), larger planes run in row chunks (one or several per plane: 56x56, 13x300, 72x65, 70x400 with wide rows). Grad weight stages several small planes per batch: image counts that leave a short
+    last batch (13 images of 9x9 in batches of 6) and a short last group (37 of 20x20 in batches of 5, 64 of 14x14 in
+    batches of up to 10). The eval BN + ReLU loader on both forward kernels."""
     rng = np.random.default_rng(ks)
     p = ks // 2
     for (n, c, h, w) in ((2, 3, 1, 1), (3, 4, 2, 3), (2, 5, 7, 7), (2, 3, 11, 9), (2, 4, 56, 56), (1, 3, 13, 300),
-                         (1, 2, 70, 41), (13, 3, 9, 9), (37, 2, 20, 20), (64, 2, 14, 14)):
+                         (1, 2, 70, 41), (13, 3, 9, 9), (37, 2, 20, 20), (64, 2, 14, 14), (1, 2, 72, 65),
+                         (1, 1, 70, 400)):
         case = (ks, n, c, h, w)
         x, wt, b = rnd(rng, n, c, h, w), rnd(rng, c, 1, ks, ks), rnd(rng, c)
         y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), 1, p)
@@ -515,10 +517,12 @@ def test_depthwise_tiled_stride1(cuda, ops, ks):
         assert orc.rel_l2(host(gx), orc.dw_dgrad(gy, wt, x.shape, 1, p)) <= TOL, case
         gw = ops.depthwise_wgrad(dev(x, cuda), dev(gy, cuda), ks, 1, p)
         assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, ks, 1, p)) <= TOL, case
-    x, wt = rnd(rng, 2, 6, 60, 33), rnd(rng, 6, 1, ks, ks)
-    bn = (rnd(rng, 6), np.abs(rnd(rng, 6)) + 0.5, rnd(rng, 6), rnd(rng, 6))
-    y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), None, 1, p, bn=[dev(t, cuda) for t in bn])
-    assert orc.rel_l2(host(y), orc.dw_fwd(x, wt, None, 1, p, bn=bn)) <= TOL
+    for shape in ((2, 6, 60, 33), (3, 5, 12, 9), (1, 3, 80, 70)):
+        x, wt = rnd(rng, *shape), rnd(rng, shape[1], 1, ks, ks)
+        c = shape[1]
+        bn = (rnd(rng, c), np.abs(rnd(rng, c)) + 0.5, rnd(rng, c), rnd(rng, c))
+        y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), None, 1, p, bn=[dev(t, cuda) for t in bn])
+        assert orc.rel_l2(host(y), orc.dw_fwd(x, wt, None, 1, p, bn=bn)) <= TOL, shape
 
 
 def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
@@ -563,6 +567,33 @@ def test_batch_norm_train_and_backward(cuda, ops, n, c, h, w, relu):
     scale = np.linalg.norm(gz.astype(np.float64)) * np.abs(g * i_ref).max()
     assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
     assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
+
+
+@pytest.mark.parametrize("n,c,h,w", [(32, 64, 4, 4), (8, 3, 7, 9), (16, 8, 32, 32), (4, 6, 5, 7), (1024, 2, 3, 3)])
+@pytest.mark.parametrize("with_g2", [True, False])
+def test_batch_norm_backward_res(cuda, ops, n, c, h, w, with_g2):
+    """omt_bn_bwd_res: gz = (g + g2) masked by y > 0 returned exactly as the masked sum, and BatchNorm's grads of gz
+    against the oracle's backward of that gz, on the one-launch (<= 8192 elements per channel) and split paths, with
+    and without grad input."""
+    rng = np.random.default_rng(n + c + h)
+    x = rnd(rng, n, c, h, w) * 2 + 1
+    gam, bet, rm, rv = rnd(rng, c), rnd(rng, c), rnd(rng, c), np.abs(rnd(rng, c)) + 0.5
+    y, sm, si = ops.batch_norm_train(dev(x, cuda), dev(gam, cuda), dev(bet, cuda), dev(rm, cuda), dev(rv, cuda), 0.1,
+                                     1e-5, True)
+    g, g2 = rnd(rng, n, c, h, w), rnd(rng, n, c, h, w) if with_g2 else None
+    for mask in ((True, True, True), (False, True, True)):
+        gx, dg, db, gz = ops.batch_norm_backward_res(dev(g, cuda), None if g2 is None else dev(g2, cuda), dev(x, cuda),
+                                                     sm, si, dev(gam, cuda), y, mask)
+        gsum = g + g2 if with_g2 else g
+        gz_ref = np.where(host(y) > 0, gsum, np.float32(0)).astype(np.float32)
+        assert np.array_equal(host(gz), gz_ref), mask
+        gx_ref, dg_ref, db_ref = orc.bn_bwd(gz_ref, x, host(sm), host(si), gam)
+        assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
+        if mask[0]:
+            scale = np.linalg.norm(gz_ref.astype(np.float64)) * np.abs(gam * host(si)).max()
+            assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
+        else:
+            assert gx is None
 
 
 def test_batch_norm_functional_and_eval(cuda, ops):
