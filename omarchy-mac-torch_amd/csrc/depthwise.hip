@@ -321,6 +321,214 @@ __global__ void __launch_bounds__(NT) dw_s1_batch_kernel(const float* __restrict
   }
 }
 
+// Rows of a multiple of 4 (every W % 4 == 0 plane, tensors below 2 GiB): no LDS. A thread owns a 4-column x RB-row
+// block of one plane's outputs and loads the RB + KS - 1 input rows it reads straight into registers, each row as one
+// 16-byte run over the block's columns plus a KS / 2-float run either side (buffer loads: rows and runs outside the
+// plane read 0, the zero padding), all before its first FMA, so a thread keeps (RB + KS - 1) * 3 loads in flight
+// where the staged kernels wait one memory round trip per stage. Neighbouring threads read overlapping runs; the
+// overlap is served by the caches, not HBM. Each output sums its taps in the staged kernels' order (ky, then kx, from
+// 0; bias last), so the results are identical to theirs. The filter comes in 16-byte runs too (per lane: a wave can
+// span planes of two channels).
+struct DwReg {
+  uint32_t threads;           // planes * row blocks * W / 4
+  uint32_t bytes;             // bytes of x (and y), below 2^31
+  FastDiv div_cg, div_rb, div_c;
+};
+template <int N>
+__device__ __forceinline__ void bload_run(__amdgpu_buffer_rsrc_t r, uint32_t off, float* v) {
+  if constexpr (N == 1) {
+    v[0] = bload(r, off, 0);
+  } else if constexpr (N == 2) {
+    // whole-vector bit casts: subscripting the builtin's result directly has compiled to two copies of element 0
+    const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+    v[0] = t.x;
+    v[1] = t.y;
+  } else {
+    static_assert(N == 3, "runs of 1 to 3 floats");
+    typedef float f32x3 __attribute__((ext_vector_type(3)));
+    const f32x3 t = __builtin_bit_cast(f32x3, __builtin_amdgcn_raw_buffer_load_b96(r, (int)off, 0, 0));
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+  }
+}
+// The input window of a 4-column x RB-row output block at (r0, c0) of the plane starting at element pbase:
+// v[i][j] = x[r0 - KS / 2 + i][c0 - KS / 2 + j], zero outside the plane.
+template <int KS, int RB>
+__device__ __forceinline__ void dw_window(__amdgpu_buffer_rsrc_t xr, uint32_t pbase, int r0, int c0, int H, int W,
+                                          float (&v)[RB + KS - 1][4 + 2 * (KS / 2)]) {
+  constexpr int PAD = KS / 2, NR = RB + KS - 1;
+  const bool lok = c0 > 0, rok = c0 + 4 < W;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int iy = r0 - PAD + i;
+    const bool ok = (unsigned)iy < (unsigned)H;
+    const uint32_t off = (pbase + (uint32_t)(iy * W + c0)) * 4u;
+    const float4 m = bload4(xr, ok ? off : kOOB, 0);
+    v[i][PAD] = m.x;
+    v[i][PAD + 1] = m.y;
+    v[i][PAD + 2] = m.z;
+    v[i][PAD + 3] = m.w;
+    if constexpr (PAD > 0) {
+      bload_run<PAD>(xr, ok & lok ? off - PAD * 4u : kOOB, &v[i][0]);
+      bload_run<PAD>(xr, ok & rok ? off + 16u : kOOB, &v[i][PAD + 4]);
+    }
+  }
+}
+
+template <int KS, bool FLIP, int RB>
+__global__ void __launch_bounds__(256) dw_s1_reg_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                        const float* __restrict__ bias, const float* __restrict__ bm,
+                                                        const float* __restrict__ bv, const float* __restrict__ bg,
+                                                        const float* __restrict__ bb, float eps, float* __restrict__ y,
+                                                        int C, int H, int W, const DwReg d) {
+  constexpr int PAD = KS / 2, KK = KS * KS, NR = RB + KS - 1, NC = 4 + 2 * PAD;
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= d.threads) return;
+  const uint32_t CG = (uint32_t)W >> 2, u = fdiv(t, d.div_cg), cg = t - u * CG;
+  const uint32_t nrb = (uint32_t)(H + RB - 1) / RB, plane = fdiv(u, d.div_rb), rb = u - plane * nrb;
+  const int ch = (int)(plane - fdiv(plane, d.div_c) * (uint32_t)C);
+  const int c0 = (int)cg * 4, r0 = (int)rb * RB;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, d.bytes);
+  const uint32_t pbase = plane * (uint32_t)H * (uint32_t)W;  // elements; below 2^29
+  const bool lok = c0 > 0, rok = c0 + 4 < W;
+  float v[NR][NC];
+  dw_window<KS, RB>(xr, pbase, r0, c0, H, W, v);
+  // the filter: KK floats of channel ch in 16-byte runs (the last run's floats past KK belong to the next channel or
+  // lie past the tensor; a run is loaded whole only when it ends inside the filter)
+  float wr[KK];
+  {
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, (uint32_t)(C * KK * 4));
+    const uint32_t wb = (uint32_t)(ch * KK) * 4u;
+    float wl[KK];
+#pragma unroll
+    for (int k = 0; k + 4 <= KK; k += 4) {
+      const float4 q = bload4(wrs, wb + k * 4u, 0);
+      wl[k] = q.x;
+      wl[k + 1] = q.y;
+      wl[k + 2] = q.z;
+      wl[k + 3] = q.w;
+    }
+#pragma unroll
+    for (int k = KK & ~3; k < KK; ++k) wl[k] = bload(wrs, wb + k * 4u, 0);
+#pragma unroll
+    for (int k = 0; k < KK; ++k) wr[k] = wl[FLIP ? KK - 1 - k : k];
+  }
+  const bool bn = !FLIP && bm != nullptr;
+  if (bn) {  // previous layer's eval BN + ReLU on in-plane taps; the padding stays zero
+    const float inv = rsqrtf(bv[ch] + eps), sc = inv * bg[ch], sh = bb[ch] - bm[ch] * sc;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int iy = r0 - PAD + i;
+      const bool ok = (unsigned)iy < (unsigned)H;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const bool in = ok & (j < PAD ? lok : j >= PAD + 4 ? rok : true);
+        if (in) v[i][j] = fmaxf(fmaf(v[i][j], sc, sh), 0.f);
+      }
+    }
+  }
+  float acc[RB][4];
+#pragma unroll
+  for (int o = 0; o < RB; ++o)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[o][e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int ky = KS - 1; ky >= 0; --ky) {  // output row i - ky: taps in ascending ky as i ascends
+      const int o = i - ky;
+      if (o < 0 || o >= RB) continue;
+#pragma unroll
+      for (int kx = 0; kx < KS; ++kx)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[o][e] = fmaf(v[i][e + kx], wr[ky * KS + kx], acc[o][e]);
+    }
+  const float b = (!FLIP && bias) ? bias[ch] : 0.f;
+#pragma unroll
+  for (int o = 0; o < RB; ++o)
+    if (r0 + o < H)
+      *reinterpret_cast<float4*>(y + pbase + (uint32_t)((r0 + o) * W + c0)) =
+          make_float4(acc[o][0] + b, acc[o][1] + b, acc[o][2] + b, acc[o][3] + b);
+}
+
+// Grad weight, rows of a multiple of 4: workgroup (ch, slice) sums every tap over images [slice * ipw, ...) of
+// channel ch. Each thread takes 4-column x RB-row blocks of gy in turn (stride NT over the slice's blocks), loads the
+// block and the input window it meets (as the forward kernel does: no LDS, zero padding from the buffer range check)
+// and accumulates all KS^2 taps in registers; the taps are then summed over the workgroup (wave_sum, then the waves
+// in order). One slice writes gw; several write part[slice][ch] and the channel's last workgroup to finish sums the
+// slices in order into gw (split_arrive). A fixed thread-to-block map and fixed sum orders make the result
+// deterministic.
+struct DwRegW {
+  int ipw, CG, nrb, slices;  // images per slice, column groups W / 4, row blocks, slices
+  int rb, nt;                // rows per block, threads per workgroup
+  uint32_t bytes, tag;       // bytes of x (and gy), below 2^31; the call's split tag
+  FastDiv div_img, div_cg;   // blocks per image (nrb * CG), CG
+};
+template <int KS, int RB, int NT>
+__global__ void __launch_bounds__(NT) dw_wgrad_reg_kernel(const float* __restrict__ x, const float* __restrict__ gy,
+                                                           float* __restrict__ gw, float* __restrict__ part,
+                                                           unsigned long long* __restrict__ slots, int N, int C, int H,
+                                                           int W, const DwRegW d) {
+  constexpr int PAD = KS / 2, KK = KS * KS, NR = RB + KS - 1, NC = 4 + 2 * PAD, NW = NT / 64;
+  __shared__ float red[NW][KK];
+  const int ch = blockIdx.x, sl = blockIdx.y;
+  const int n0 = sl * d.ipw, nimg = min(N - n0, d.ipw);
+  const uint32_t per_img = (uint32_t)(d.nrb * d.CG), units = (uint32_t)nimg * per_img;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, d.bytes), gr = make_rsrc(gy, d.bytes);
+  float acc[KK];
+#pragma unroll
+  for (int k = 0; k < KK; ++k) acc[k] = 0.f;
+  for (uint32_t u = threadIdx.x; u < units; u += NT) {
+    const uint32_t i = fdiv(u, d.div_img), rem = u - i * per_img, rb = fdiv(rem, d.div_cg);
+    const int c0 = (int)(rem - rb * (uint32_t)d.CG) * 4, r0 = (int)rb * RB;
+    const uint32_t pbase = ((uint32_t)(n0 + (int)i) * (uint32_t)C + (uint32_t)ch) * (uint32_t)H * (uint32_t)W;
+    float gv[RB][4];
+#pragma unroll
+    for (int o = 0; o < RB; ++o) {
+      const float4 q = bload4(gr, r0 + o < H ? (pbase + (uint32_t)((r0 + o) * W + c0)) * 4u : kOOB, 0);
+      gv[o][0] = q.x;
+      gv[o][1] = q.y;
+      gv[o][2] = q.z;
+      gv[o][3] = q.w;
+    }
+    float v[NR][NC];
+    dw_window<KS, RB>(xr, pbase, r0, c0, H, W, v);
+#pragma unroll
+    for (int o = 0; o < RB; ++o)
+#pragma unroll
+      for (int ky = 0; ky < KS; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < KS; ++kx)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[ky * KS + kx] = fmaf(gv[o][e], v[o + ky][e + kx], acc[ky * KS + kx]);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < KK; ++k) {
+    const float t = wave_sum(acc[k]);
+    if (lane == 0) red[wave][k] = t;
+  }
+  __syncthreads();
+  const int k = threadIdx.x;
+  float t = 0.f;
+  if (k < KK) {
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) t += red[wv][k];
+  }
+  if (d.slices == 1) {
+    if (k < KK) gw[ch * KK + k] = t;
+    return;
+  }
+  if (k < KK) part[((int64_t)sl * C + ch) * KK + k] = t;
+  if (!split_arrive(slots + ch, d.tag, (uint32_t)d.slices)) return;
+  if (k < KK) {
+    float s = 0.f;
+    for (int j = 0; j < d.slices; ++j) s += part[((int64_t)j * C + ch) * KK + k];
+    gw[ch * KK + k] = s;
+  }
+}
+
 // Grad-weight work of one channel: units u = (image u / chunks, row chunk u % chunks), N * chunks of them. A
 // workgroup takes `group` consecutive units and stages `batch` of them at a time (several whole planes when a plane
 // has few outputs; then chunks == 1): every load of a batch (the output gradients into registers, the input rows
@@ -511,6 +719,50 @@ static DwUnits dw_units(const omt_conv_geo* g) {
   u.div_out = make_fastdiv((uint32_t)(g->ih * g->iw));
   return u;
 }
+// The register-blocked kernel: rows of a multiple of 4 floats, the tensor read through one buffer resource.
+static int dw_reg_rows(int ks) { return ks == 7 ? 2 : 4; }
+static bool dw_reg_ok(const omt_conv_geo* g) {
+  return g->iw % 4 == 0 && g->n * g->ci * g->ih * g->iw * 4 <= kMaxBufBytes && g->ci * g->ks * g->ks * 4 <= kMaxBufBytes;
+}
+
+// The register-blocked grad weight. Slices of images give up to about kDwRegWgs workgroups (a workgroup per channel
+// leaves most CUs idle when there are few channels), but no more slices than keep 1024 blocks of 4 rows in each (every
+// slice costs a device-scope release and each channel's last one an acquire, both whole-cache operations; measured at
+// b32: dw 3x3 over 72 x 56^2 in 1 / 2 / 4 / 11 slices 24.1 / 18.0 / 23.2 / 38.5 us, dw 5x5 over 96 x 28^2 in 1 / 2 / 3
+// slices 12.1 / 14.4 / 19.1 us). Workgroups of 1024 threads when a slice has that many blocks of 4 rows, or of 2 rows
+// (more waves per CU keep more loads in flight); else 256 threads.
+constexpr int kDwRegWgs = 128;
+static DwRegW dw_wreg(const omt_conv_geo* g) {
+  DwRegW d{};
+  const int ks = (int)g->ks;
+  d.CG = (int)(g->iw / 4);
+  const int64_t blocks4 = g->n * cdiv(g->ih, dw_reg_rows(ks)) * d.CG;
+  const int64_t slices = std::min<int64_t>({g->n, cdiv(kDwRegWgs, g->ci), std::max<int64_t>(1, blocks4 / 1024)});
+  d.ipw = (int)cdiv(g->n, slices);
+  d.slices = (int)cdiv(g->n, d.ipw);
+  auto units = [&](int rb) { return (int64_t)d.ipw * cdiv(g->ih, rb) * d.CG; };
+  if (ks != 7 && units(4) >= 1024) {
+    d.rb = 4, d.nt = 1024;
+  } else if (units(2) >= 1024) {
+    d.rb = 2, d.nt = 1024;
+  } else {
+    d.rb = dw_reg_rows(ks), d.nt = 256;
+  }
+  d.nrb = (int)cdiv(g->ih, d.rb);
+  d.bytes = (uint32_t)(g->n * g->ci * g->ih * g->iw * 4);
+  d.div_img = make_fastdiv((uint32_t)(d.nrb * d.CG));
+  d.div_cg = make_fastdiv((uint32_t)d.CG);
+  return d;
+}
+// partials [slices][C][ks^2] floats, then C arrival slots (8-byte aligned); nothing for one slice
+static size_t dw_wreg_part_bytes(const omt_conv_geo* g, const DwRegW& d) {
+  return (size_t)cdiv((int64_t)d.slices * g->ci * g->ks * g->ks * 4, 8) * 8;
+}
+static size_t dw_wreg_workspace(const omt_conv_geo* g) {
+  const DwRegW d = dw_wreg(g);
+  return d.slices == 1 ? 0 : dw_wreg_part_bytes(g, d) + (size_t)g->ci * 8;
+}
+
 static int64_t dw_s1_groups(const omt_conv_geo* g) {
   const DwUnits u = dw_units(g);
   return cdiv(u.units, u.group);
@@ -537,6 +789,24 @@ static DwBatch dw_batch(const omt_conv_geo* g) {
 template <bool FLIP>
 static int launch_dw_s1(const omt_conv_geo* g, const float* x, const float* w, const float* bias, const float* bm,
                         const float* bv, const float* bg, const float* bb, float eps, float* y, hipStream_t s) {
+  if (dw_reg_ok(g) && (uintptr_t)y % 16 == 0) {
+    const int ks = (int)g->ks, rb = dw_reg_rows(ks);
+    DwReg d{};
+    const int64_t nrb = cdiv(g->ih, rb);
+    d.threads = (uint32_t)(g->n * g->ci * nrb * (g->iw / 4));
+    d.bytes = (uint32_t)(g->n * g->ci * g->ih * g->iw * 4);
+    d.div_cg = make_fastdiv((uint32_t)(g->iw / 4));
+    d.div_rb = make_fastdiv((uint32_t)nrb);
+    d.div_c = make_fastdiv((uint32_t)g->ci);
+    const dim3 grid((unsigned)cdiv(d.threads, 256));
+    const int C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
+#define OMT_DW_R(KS_, RB_) \
+  hipLaunchKernelGGL((dw_s1_reg_kernel<KS_, FLIP, RB_>), grid, dim3(256), 0, s, x, w, bias, bm, bv, bg, bb, eps, y, C, \
+                     H, W, d)
+    if (ks == 3) OMT_DW_R(3, 4); else if (ks == 5) OMT_DW_R(5, 4); else OMT_DW_R(7, 2);
+#undef OMT_DW_R
+    return launch_check("dw_s1_reg_kernel");
+  }
   const DwBatch d = dw_batch(g);
   if (d.B >= 1 && g->ih * g->iw <= kDwBatchMaxHW && g->n * g->ci * g->ih * g->iw < ((int64_t)1 << 31)) {
     const dim3 grid((unsigned)(cdiv(g->n, d.B) * g->ci));
@@ -619,6 +889,7 @@ OMT_EXPORT int omt_dw_dgrad(const omt_conv_geo* g, const float* gy, const float*
 
 OMT_EXPORT size_t omt_dw_wgrad_workspace(const omt_conv_geo* g) {
   if (!g || !dw_ok(g)) return 0;
+  if (dw_s1(g) && dw_reg_ok(g)) return dw_wreg_workspace(g);
   return (size_t)((dw_s1_wgrad(g) ? dw_s1_groups(g) : dw_slices(g)) * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
@@ -626,9 +897,36 @@ OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* 
                             size_t workspace_bytes, void* stream) {
   if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_dw_wgrad: null pointer");
   if (!dw_ok(g)) return fail(OMT_UNSUPPORTED, "omt_dw_wgrad: geometry not covered");
-  if (!workspace || workspace_bytes < omt_dw_wgrad_workspace(g))
-    return fail(OMT_INVALID, "omt_dw_wgrad: workspace of %zu bytes needed", omt_dw_wgrad_workspace(g));
+  const size_t need = omt_dw_wgrad_workspace(g);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_dw_wgrad: workspace of %zu bytes needed", need);
   hipStream_t s = stream_of(stream);
+  if (dw_s1(g) && dw_reg_ok(g)) {
+    DwRegW d = dw_wreg(g);
+    d.tag = split_tag();
+    const int ks = (int)g->ks;
+    const int N = (int)g->n, C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
+    float* part = (float*)workspace;
+    unsigned long long* slots =
+        d.slices == 1 ? nullptr : (unsigned long long*)((char*)workspace + dw_wreg_part_bytes(g, d));
+    const dim3 grid((unsigned)g->ci, (unsigned)d.slices);
+#define OMT_DW_WR(KS_, RB_, NT_) \
+  hipLaunchKernelGGL((dw_wgrad_reg_kernel<KS_, RB_, NT_>), grid, dim3(NT_), 0, s, x, gy, gw, part, slots, N, C, H, W, d)
+#define OMT_DW_WR_KS(KS_)                                   \
+  if (d.nt == 256) OMT_DW_WR(KS_, (KS_ == 7 ? 2 : 4), 256); \
+  else if (d.rb == 2) OMT_DW_WR(KS_, 2, 1024);              \
+  else OMT_DW_WR(KS_, (KS_ == 7 ? 2 : 4), 1024)
+    if (ks == 3) {
+      OMT_DW_WR_KS(3);
+    } else if (ks == 5) {
+      OMT_DW_WR_KS(5);
+    } else {
+      OMT_DW_WR_KS(7);
+    }
+#undef OMT_DW_WR_KS
+#undef OMT_DW_WR
+    return launch_check("dw_wgrad_reg_kernel");
+  }
   if (dw_s1_wgrad(g)) {
     const int nt = dw_threads(g), ks = (int)g->ks;
     const DwTiling t = dw_tiling((int)g->ih, (int)g->iw, ks, nt);

@@ -6,6 +6,8 @@
 // elements decompose flat indices with 32-bit multiply-high division (the I32 kernels); larger ones with 64-bit
 // arithmetic. Global average pooling stages small planes through LDS (one thread per plane, coalesced loads).
 // Reference kernels: maxpool_gen_fwd/bwd, avgpool_gen_fwd/bwd, adapool_fwd/bwd (csrc/nn.cpp:157-222).
+#include <algorithm>
+
 #include "omt_internal.h"
 
 namespace omt {
@@ -64,6 +66,39 @@ __global__ void __launch_bounds__(256) maxpool_fwd_kernel(const float* __restric
   }
 }
 
+// Square undilated K x K windows (K = 2, 3): the window is unrolled, so all of a thread's in-plane taps are loaded
+// before the first compare (the loop above waits on one tap at a time); the compares run in the same row-major
+// order with the same rule, so values and indices are those of the general kernel.
+template <bool I32, int K>
+__global__ void __launch_bounds__(256) maxpool_fwd_k_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t* __restrict__ idx, int64_t total, PoolGeo g) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const Pos o = decompose<I32>(i, g.ow, g.oh * g.ow, g.d_ow, g.d_ohw);
+    const float* xp = x + o.plane * g.ih * g.iw;
+    const int y0 = o.y * g.sh - g.ph, x0 = o.x * g.sw - g.pw;
+    float v[K * K];
+    bool ok[K * K];
+#pragma unroll
+    for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < K; ++kx) {
+        const int yy = y0 + ky, xx = x0 + kx, t = ky * K + kx;
+        ok[t] = (unsigned)yy < (unsigned)g.ih && (unsigned)xx < (unsigned)g.iw;
+        v[t] = ok[t] ? xp[yy * g.iw + xx] : 0.f;
+      }
+    float best = -INFINITY;
+    int bi = -1;
+#pragma unroll
+    for (int t = 0; t < K * K; ++t)
+      if (ok[t] && (bi < 0 || v[t] > best || isnan(v[t]))) {
+        best = v[t];
+        bi = (y0 + t / K) * g.iw + x0 + t % K;
+      }
+    y[i] = best;
+    idx[i] = bi;
+  }
+}
+
 // Undilated windows: the outputs whose window covers input (y, x) form the range oy in
 // [ceil((y + p - k + 1) / s), floor((y + p) / s)] (clipped to the output) per axis, visited in ascending (oy, ox)
 // order like the general kernel below, so the sums are bit-identical; no per-tap divisibility tests.
@@ -90,6 +125,49 @@ __global__ void __launch_bounds__(256) maxpool_bwd_d1_kernel(const float* __rest
         if (ip[o] == me) acc += gv;
       }
     gx[i] = acc;
+  }
+}
+
+// Undilated windows, four consecutive inputs of a row per thread (iw % 4 == 0, float4 store): the outputs whose
+// windows cover any of the four form an NY x NX block (NY, NX at least the largest such block of the geometry, checked
+// on the host); all of its gradients and indices are loaded first, then each input sums, in ascending (oy, ox) order,
+// the gradients of the block's outputs whose index names it. An output whose index names an input covers that input,
+// so each sum visits the same outputs in the same order as the per-input kernel above: the results are identical.
+template <int NY, int NX>
+__global__ void __launch_bounds__(256) maxpool_bwd_v4_kernel(const float* __restrict__ g,
+                                                             const int64_t* __restrict__ idx, float* __restrict__ gx,
+                                                             uint32_t total4, PoolGeo q, FastDiv d_iw4, FastDiv d_ih) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total4; i += gridDim.x * blockDim.x) {
+    const uint32_t row = fdiv(i, d_iw4), x = (i - row * (uint32_t)(q.iw >> 2)) * 4u;
+    const uint32_t plane = fdiv(row, d_ih), yy = row - plane * (uint32_t)q.ih;
+    const int ty = (int)yy + q.ph, ay = ty - q.kh + 1;
+    const int oy0 = ay <= 0 ? 0 : (int)fdiv((uint32_t)(ay + q.sh - 1), q.d_sh);
+    const int oy1 = min((int)fdiv((uint32_t)ty, q.d_sh), q.oh - 1);
+    const int ax = (int)x + q.pw - q.kw + 1, tx = (int)x + 3 + q.pw;
+    const int ox0 = ax <= 0 ? 0 : (int)fdiv((uint32_t)(ax + q.sw - 1), q.d_sw);
+    const int ox1 = min((int)fdiv((uint32_t)tx, q.d_sw), q.ow - 1);
+    const int64_t obase = (int64_t)plane * q.oh * q.ow;
+    float gv[NY][NX];
+    int64_t iv[NY][NX];
+#pragma unroll
+    for (int jy = 0; jy < NY; ++jy)
+#pragma unroll
+      for (int jx = 0; jx < NX; ++jx) {
+        const bool ok = oy0 + jy <= oy1 && ox0 + jx <= ox1;
+        const int64_t o = obase + (int64_t)(oy0 + jy) * q.ow + ox0 + jx;
+        gv[jy][jx] = ok ? g[o] : 0.f;
+        iv[jy][jx] = ok ? idx[o] : -1;
+      }
+    const int64_t me = (int64_t)yy * q.iw + x;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jy = 0; jy < NY; ++jy)
+#pragma unroll
+      for (int jx = 0; jx < NX; ++jx)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (iv[jy][jx] == me + e) acc[e] += gv[jy][jx];
+    *reinterpret_cast<float4*>(gx + (int64_t)row * q.iw + x) = make_float4(acc[0], acc[1], acc[2], acc[3]);
   }
 }
 
@@ -292,6 +370,26 @@ static bool idx32(int64_t total) { return total < ((int64_t)1 << 32); }
     else                                                                                       \
       hipLaunchKernelGGL(K<false>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);   \
   } while (0)
+#define OMT_POOL_LAUNCH_K(K, W, total, s, ...)                                                    \
+  do {                                                                                           \
+    if (idx32(total))                                                                            \
+      hipLaunchKernelGGL((K<true, W>), dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);  \
+    else                                                                                         \
+      hipLaunchKernelGGL((K<false, W>), dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__); \
+  } while (0)
+
+// Largest number of outputs whose undilated windows (extent k, stride s, padding p, n outputs) cover any of `span`
+// consecutive inputs starting at a multiple of `span` (span 1: any single input), over all such runs of a length-`len`
+// axis.
+static int max_cover(int64_t len, int64_t n, int64_t k, int64_t s, int64_t p, int64_t span) {
+  int64_t best = 0;
+  for (int64_t a = 0; a < len; a += span) {
+    const int64_t lo_t = a + p - k + 1, hi_t = std::min(a + span - 1, len - 1) + p;
+    const int64_t lo = lo_t <= 0 ? 0 : (lo_t + s - 1) / s, hi = std::min(hi_t / s, n - 1);
+    best = std::max(best, hi - lo + 1);
+  }
+  return (int)best;
+}
 
 }  // namespace omt
 
@@ -305,8 +403,15 @@ OMT_EXPORT int omt_maxpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
     return fail(OMT_UNSUPPORTED, "omt_maxpool_fwd: geometry not covered");
   const int64_t total = planes * oh * ow;
   if (total == 0) return OMT_OK;
-  OMT_POOL_LAUNCH(maxpool_fwd_kernel, total, stream_of(stream), x, y, idx, total,
-                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+  const PoolGeo q = pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw);
+  if (kh == kw && dh == 1 && dw == 1 && (kh == 2 || kh == 3)) {
+    if (kh == 2)
+      OMT_POOL_LAUNCH_K(maxpool_fwd_k_kernel, 2, total, stream_of(stream), x, y, idx, total, q);
+    else
+      OMT_POOL_LAUNCH_K(maxpool_fwd_k_kernel, 3, total, stream_of(stream), x, y, idx, total, q);
+    return launch_check("maxpool_fwd_k_kernel");
+  }
+  OMT_POOL_LAUNCH(maxpool_fwd_kernel, total, stream_of(stream), x, y, idx, total, q);
   return launch_check("maxpool_fwd_kernel");
 }
 
@@ -319,8 +424,22 @@ OMT_EXPORT int omt_maxpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
   const int64_t total = planes * ih * iw;
   if (total == 0) return OMT_OK;
   if (dh == 1 && dw == 1) {
-    OMT_POOL_LAUNCH(maxpool_bwd_d1_kernel, total, stream_of(stream), g, idx, gx, total,
-                    pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw));
+    const PoolGeo q = pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw);
+    if (iw % 4 == 0 && total < ((int64_t)1 << 32) && (uintptr_t)gx % 16 == 0) {
+      const int ny = max_cover(ih, oh, kh, sh, ph, 1), nx = max_cover(iw, ow, kw, sw, pw, 4);
+      const uint32_t total4 = (uint32_t)(total / 4);
+      const FastDiv d_iw4 = make_fastdiv((uint32_t)(iw / 4)), d_ih = make_fastdiv((uint32_t)ih);
+#define OMT_MP_V4(NY_, NX_)                                                                                  \
+  hipLaunchKernelGGL((maxpool_bwd_v4_kernel<NY_, NX_>), dim3(grid1d(total4, 256)), dim3(256), 0, stream_of(stream), \
+                     g, idx, gx, total4, q, d_iw4, d_ih)
+      bool launched = true;
+      if (ny <= 1 && nx <= 2) OMT_MP_V4(1, 2);
+      else if (ny <= 2 && nx <= 3) OMT_MP_V4(2, 3);
+      else launched = false;
+#undef OMT_MP_V4
+      if (launched) return launch_check("maxpool_bwd_v4_kernel");
+    }
+    OMT_POOL_LAUNCH(maxpool_bwd_d1_kernel, total, stream_of(stream), g, idx, gx, total, q);
     return launch_check("maxpool_bwd_d1_kernel");
   }
   OMT_POOL_LAUNCH(maxpool_bwd_kernel, total, stream_of(stream), g, idx, gx, total,

@@ -498,16 +498,18 @@ def test_depthwise(cuda, ops, ks, s, p):
 
 @pytest.mark.parametrize("ks", [3, 5, 7])
 def test_depthwise_tiled_stride1(cuda, ops, ks):
-    """The LDS-tiled stride-1 "same" kernels. Forward and grad input: planes of up to 256 elements run several images
-    of a channel per workgroup (fewer images than a batch holds; 64 of 14x14 in batches of 20, leaving a short last
-    batch), larger planes run in row chunks (one or several per plane: 56x56, 13x300, 72x65, 70x400 with wide rows). Grad weight stages several small planes per batch: image counts that leave a short
-    last batch (13 images of 9x9 in batches of 6) and a short last group (37 of 20x20 in batches of 5, 64 of 14x14 in
-    batches of up to 10). The eval BN + ReLU loader on both forward kernels."""
+    """The stride-1 "same" kernels. Forward and grad input: rows of a multiple of 4 run register-blocked (56x56,
+    13x300, 20x20, 70x400; rows of exactly 4, where both side runs are padding; 6 and 1 rows, a partial last row
+    block); other planes of up to 256 elements run several images of a channel per workgroup (64 of 14x14 in batches
+    of 20, leaving a short last batch), larger ones LDS-tiled in row chunks (72x65, 70x41). Grad weight stages several
+    small planes per batch: image counts that leave a short last batch (13 images of 9x9 in batches of 6) and a short
+    last group (37 of 20x20 in batches of 5, 64 of 14x14 in batches of up to 10). The eval BN + ReLU loader on every
+    forward kernel."""
     rng = np.random.default_rng(ks)
     p = ks // 2
     for (n, c, h, w) in ((2, 3, 1, 1), (3, 4, 2, 3), (2, 5, 7, 7), (2, 3, 11, 9), (2, 4, 56, 56), (1, 3, 13, 300),
                          (1, 2, 70, 41), (13, 3, 9, 9), (37, 2, 20, 20), (64, 2, 14, 14), (1, 2, 72, 65),
-                         (1, 1, 70, 400)):
+                         (1, 1, 70, 400), (2, 3, 5, 4), (3, 2, 6, 8), (1, 2, 1, 12)):
         case = (ks, n, c, h, w)
         x, wt, b = rnd(rng, n, c, h, w), rnd(rng, c, 1, ks, ks), rnd(rng, c)
         y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), dev(b, cuda), 1, p)
@@ -517,12 +519,55 @@ def test_depthwise_tiled_stride1(cuda, ops, ks):
         assert orc.rel_l2(host(gx), orc.dw_dgrad(gy, wt, x.shape, 1, p)) <= TOL, case
         gw = ops.depthwise_wgrad(dev(x, cuda), dev(gy, cuda), ks, 1, p)
         assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, ks, 1, p)) <= TOL, case
-    for shape in ((2, 6, 60, 33), (3, 5, 12, 9), (1, 3, 80, 70)):
+    for shape in ((2, 6, 60, 33), (3, 5, 12, 9), (1, 3, 80, 70), (2, 4, 28, 28), (3, 2, 5, 4)):
         x, wt = rnd(rng, *shape), rnd(rng, shape[1], 1, ks, ks)
         c = shape[1]
         bn = (rnd(rng, c), np.abs(rnd(rng, c)) + 0.5, rnd(rng, c), rnd(rng, c))
         y = ops.depthwise_conv2d(dev(x, cuda), dev(wt, cuda), None, 1, p, bn=[dev(t, cuda) for t in bn])
         assert orc.rel_l2(host(y), orc.dw_fwd(x, wt, None, 1, p, bn=bn)) <= TOL, shape
+
+
+@pytest.mark.parametrize("ks", [3, 5, 7])
+def test_depthwise_wgrad_split_in_kernel(cuda, ops, ks):
+    """Grad weight over image slices whose last workgroup per channel sums the slices (arrival counts in the
+    workspace): 13 images in 5 + 5 + 3 slices (3 + 3 + 3 + 3 + 1 at ks 7), 27 in 5 x 5 + 2 (1024-thread workgroups, 4-
+    or 2-row blocks); one slice at 1024 threads (9 x 128 x 64^2) and at 256 (13 x 64 x 12^2). A workspace left full
+    of other bytes, results bit-identical across calls (each with its own tag) and across replays of a captured graph
+    (one tag, the slots left ready by the previous replay) with other grad-weight calls in between."""
+    import ctypes
+    from omarchy_mac_torch import _lib
+    rng = np.random.default_rng(100 + ks)
+    p = ks // 2
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    for (n, c, h, w) in ((13, 16, 64, 64), (27, 24, 64, 64), (9, 128, 64, 64), (13, 64, 12, 12)):
+        x, gy = rnd(rng, n, c, h, w), rnd(rng, n, c, h, w)
+        ref = orc.dw_wgrad(x, gy, ks, 1, p)
+        tx, tgy = dev(x, cuda), dev(gy, cuda)
+        g = _lib.conv_geo(n, c, c, h, w, ks, 1, p)
+        nb = _lib.L.omt_dw_wgrad_workspace(ctypes.byref(g))
+        assert (nb > 0) == (c < 64), ("split exactly where the channels are few", n, c, h, w, nb)
+        outs = []
+        for fill in (0xFF, 0x00, 0x3F):
+            ws = torch.full((max(nb, 1),), fill, dtype=torch.uint8, device=cuda)
+            gw = torch.empty((c, 1, ks, ks), device=cuda)
+            _lib.check(_lib.L.omt_dw_wgrad(ctypes.byref(g), ctypes.c_void_p(tx.data_ptr()),
+                                           ctypes.c_void_p(tgy.data_ptr()), ctypes.c_void_p(gw.data_ptr()),
+                                           ctypes.c_void_p(ws.data_ptr()), nb, stream()), "omt_dw_wgrad")
+            outs.append(host(gw))
+        assert orc.rel_l2(outs[0], ref) <= TOL, (ks, n, c, h, w)
+        assert all(np.array_equal(o, outs[0]) for o in outs[1:])
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            gw_g = ops.depthwise_wgrad(tx, tgy, ks, 1, p)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(host(gw_g), outs[0]), (ks, n, c, h, w)
+            other = ops.depthwise_wgrad(tgy, tx, ks, 1, p)  # an eager call with another tag in between
+            torch.cuda.synchronize()
+            assert orc.rel_l2(host(other), orc.dw_wgrad(gy, x, ks, 1, p)) <= TOL
 
 
 def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
@@ -616,7 +661,12 @@ MAXPOOL = [((3, 3), (2, 2), (0, 0), (1, 1), False, 13), ((3, 3), (2, 2), (0, 0),
            ((3, 3), (2, 2), (1, 1), (1, 1), False, 14), ((3, 3), (1, 1), (1, 1), (1, 1), False, 9),
            ((2, 2), (2, 2), (0, 0), (1, 1), False, 12), ((5, 5), (3, 3), (2, 2), (1, 1), False, 17),
            ((3, 3), (2, 2), (1, 1), (2, 2), False, 15), ((3, 2), (2, 1), (1, 0), (1, 1), True, 11),
-           ((2, 2), (2, 2), (0, 0), (1, 1), True, 13)]
+           ((2, 2), (2, 2), (0, 0), (1, 1), True, 13),
+           # rows of a multiple of 4 (four inputs per thread in the backward): 2x2 s2 (one output per four inputs'
+           # rows, two across), 3x3 s2 p1 (two by three), the same 2x2 with a partial last window, and 3x3 s1 whose
+           # cover (three by six) takes the per-input kernel
+           ((2, 2), (2, 2), (0, 0), (1, 1), False, 15), ((3, 3), (2, 2), (1, 1), (1, 1), False, 31),
+           ((2, 2), (2, 2), (0, 0), (1, 1), True, 15), ((3, 3), (1, 1), (1, 1), (1, 1), False, 11)]
 
 
 @pytest.mark.parametrize("k,s,p,d,ceil,hw", MAXPOOL)
