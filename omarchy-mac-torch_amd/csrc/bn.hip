@@ -70,10 +70,29 @@ __device__ __forceinline__ int64_t voffset(int v, int ch, int c, int hw, int hwv
   return ((int64_t)nn * c + ch) * hw + (int64_t)e * vec;
 }
 
+// Sum of a double over the 64 lanes of a wave, in every lane: the float wave_sum's DPP steps (quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror: each row of 16 lanes ends with its sum in every lane), moving both 32-bit
+// halves of each double with the same DPP control, then the four row sums from lanes 0, 16, 32 and 48. VALU work only;
+// all 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ double dpp_move(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ double read_lane(double v, int lane) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
 }
 
 // Block-wide sum of two doubles over 256 threads; result valid in thread 0.
@@ -130,10 +149,34 @@ __global__ void __launch_bounds__(256) bn_stats_part_kernel(const float* __restr
   }
 }
 
+// A channel's statistics from its shifted sums over m elements: mean, biased variance and invstd; `write` also
+// stores save_mean / save_invstd and the running-statistics update (new_rm / new_rv may alias rm / rv).
+struct BnStats {
+  float mean, invstd;
+};
+__device__ __forceinline__ BnStats bn_finalize(double s1, double s2, double shift, double m, double momentum,
+                                               double eps, const float* rm, const float* rv, float* save_mean,
+                                               float* save_invstd, float* new_rm, float* new_rv, int ch, bool write) {
+  const double a = s1 / m, mean = shift + a;
+  double var = s2 / m - a * a;
+  if (var < 0.0) var = 0.0;
+  const BnStats st{(float)mean, (float)(1.0 / sqrt(var + eps))};
+  if (write) {
+    save_mean[ch] = st.mean;
+    save_invstd[ch] = st.invstd;
+    if (new_rm && rm) new_rm[ch] = (float)((double)rm[ch] + momentum * (mean - (double)rm[ch]));
+    if (new_rv && rv) {
+      const double corr = (double)(float)(m / (m > 1.0 ? m - 1.0 : 1.0));
+      new_rv[ch] = (float)((double)rv[ch] + momentum * (var * corr - (double)rv[ch]));
+    }
+  }
+  return st;
+}
+
 __global__ void bn_stats_fin_kernel(const float* __restrict__ x, const double* __restrict__ part, int c, int hw,
                                     int slices, double m, double momentum, double eps, const float* rm,
                                     const float* rv, float* __restrict__ save_mean, float* __restrict__ save_invstd,
-                                    float* new_rm, float* new_rv) {  // new_rm / new_rv may alias rm / rv
+                                    float* new_rm, float* new_rv) {
   const int ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= c) return;
   double s1 = 0.0, s2 = 0.0;
@@ -141,17 +184,26 @@ __global__ void bn_stats_fin_kernel(const float* __restrict__ x, const double* _
     s1 += part[((int64_t)ch * slices + s) * 2];
     s2 += part[((int64_t)ch * slices + s) * 2 + 1];
   }
-  const double shift = (double)x[(int64_t)ch * hw];
-  const double a = s1 / m, mean = shift + a;
-  double var = s2 / m - a * a;
-  if (var < 0.0) var = 0.0;
-  save_mean[ch] = (float)mean;
-  save_invstd[ch] = (float)(1.0 / sqrt(var + eps));
-  if (new_rm && rm) new_rm[ch] = (float)((double)rm[ch] + momentum * (mean - (double)rm[ch]));
-  if (new_rv && rv) {
-    const double corr = (double)(float)(m / (m > 1.0 ? m - 1.0 : 1.0));
-    new_rv[ch] = (float)((double)rv[ch] + momentum * (var * corr - (double)rv[ch]));
+  bn_finalize(s1, s2, (double)x[(int64_t)ch * hw], m, momentum, eps, rm, rv, save_mean, save_invstd, new_rm, new_rv,
+              ch, true);
+}
+
+// The slices' partial sums of channel ch summed in slice order by thread 0 (every lane of the first wave loads one
+// slice's pair first, so the loads overlap). Valid in thread 0 after the call; all threads must call it.
+__device__ __forceinline__ void bn_sum_slices(const double* __restrict__ part, int ch, int slices, double& s1,
+                                              double& s2) {
+  __shared__ double ps[kMaxSlices][2];
+  if ((int)threadIdx.x < slices) {
+    ps[threadIdx.x][0] = part[((int64_t)ch * slices + threadIdx.x) * 2];
+    ps[threadIdx.x][1] = part[((int64_t)ch * slices + threadIdx.x) * 2 + 1];
   }
+  __syncthreads();
+  s1 = 0.0, s2 = 0.0;
+  if (threadIdx.x == 0)
+    for (int s = 0; s < slices; ++s) {
+      s1 += ps[s][0];
+      s2 += ps[s][1];
+    }
 }
 
 // y = (x - mean[c]) * invstd[c] * gamma[c] + beta[c] (+ res), optional ReLU. grid (planes, hw chunks); float4 when
@@ -195,6 +247,92 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
   } else {
     for (int e = blockIdx.y * 256 + threadIdx.x; e < hw; e += gridDim.y * 256) {
       float v = fmaf(x[base + e], sc, sh);
+      if (res) v += res[base + e];
+      if (relu) v = fmaxf(v, 0.f);
+      y[base + e] = v;
+    }
+  }
+}
+
+// Plane and chunk of a training-apply workgroup (1-D grid). Forward order (rev = 0): planes fastest, then chunks, the
+// order of a (planes, chunks) grid, which puts a workgroup on the XCD (workgroup id mod 8) whose L2 holds its plane
+// from the reduction pass when the channels are a multiple of 8 (that pass's workgroup (channel, slice) has id
+// slice * c + channel): what tensors that fit the L2s want. Reverse order (rev = 1, large tensors): the planes last to
+// first, each plane's chunks together; the reduction pass read the planes first to last, so the apply starts on what
+// is most likely still in the memory-side cache. Measured (b256 x 64 x 56^2 backward 275 -> 256 us; at 128 x 32 x
+// 32^2, 16 MB, the forward order is faster: 10.7 against 12.8 us).
+__device__ __forceinline__ int apply_plane(int planes, int chunks, int rev, int& chunk) {
+  const int q = (int)blockIdx.x;
+  if (rev) {
+    const int p = q / chunks;
+    chunk = q - p * chunks;
+    return planes - 1 - p;
+  }
+  chunk = q / planes;
+  return q - chunk * planes;
+}
+// Tensors from this size up take the reverse apply order.
+constexpr int64_t kRevApplyBytes = (int64_t)64 << 20;
+
+// Training apply with the finalize folded in (one launch fewer): every workgroup derives its channel's mean and
+// invstd from the statistics partials with bn_stats_fin_kernel's arithmetic (so all of a channel's workgroups get the
+// same values), and the channel's first workgroup (image 0, chunk 0) also writes save_mean / save_invstd and the
+// running statistics. A thread's first vector is loaded before the partials are summed. Plane order: apply_plane.
+template <bool VEC>
+__global__ void __launch_bounds__(256) bn_train_apply_kernel(const float* __restrict__ x, const double* __restrict__ part,
+                                                             int slices, double m, double momentum, double eps,
+                                                             const float* rm, const float* rv,
+                                                             float* __restrict__ save_mean,
+                                                             float* __restrict__ save_invstd, float* new_rm,
+                                                             float* new_rv, const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta,
+                                                             const float* __restrict__ res, float* __restrict__ y,
+                                                             int c, int hw, int relu, int planes, int chunks,
+                                                             int rev) {
+  __shared__ float coef[2];
+  int chunk;
+  const int plane = apply_plane(planes, chunks, rev, chunk), ch = plane % c;
+  const int64_t base = (int64_t)plane * hw;
+  const int nv = VEC ? hw >> 2 : hw, e0 = chunk * 256 + threadIdx.x, stride = chunks * 256;
+  float4 first = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (e0 < nv) {
+    if (VEC) first = reinterpret_cast<const float4*>(x + base)[e0];
+    else first.x = x[base + e0];
+  }
+  double s1, s2;
+  bn_sum_slices(part, ch, slices, s1, s2);
+  if (threadIdx.x == 0) {
+    const BnStats st = bn_finalize(s1, s2, (double)x[(int64_t)ch * hw], m, momentum, eps, rm, rv, save_mean,
+                                   save_invstd, new_rm, new_rv, ch, plane < c && chunk == 0);
+    const float sc = st.invstd * gamma[ch];
+    coef[0] = sc;
+    coef[1] = beta[ch] - st.mean * sc;
+  }
+  __syncthreads();
+  const float sc = coef[0], sh = coef[1];
+  for (int e = e0; e < nv; e += stride) {
+    if (VEC) {
+      float4 v = e == e0 ? first : reinterpret_cast<const float4*>(x + base)[e];
+      v.x = fmaf(v.x, sc, sh);
+      v.y = fmaf(v.y, sc, sh);
+      v.z = fmaf(v.z, sc, sh);
+      v.w = fmaf(v.w, sc, sh);
+      if (res) {
+        const float4 r = reinterpret_cast<const float4*>(res + base)[e];
+        v.x += r.x;
+        v.y += r.y;
+        v.z += r.z;
+        v.w += r.w;
+      }
+      if (relu) {
+        v.x = fmaxf(v.x, 0.f);
+        v.y = fmaxf(v.y, 0.f);
+        v.z = fmaxf(v.z, 0.f);
+        v.w = fmaxf(v.w, 0.f);
+      }
+      reinterpret_cast<float4*>(y + base)[e] = v;
+    } else {
+      float v = fmaf(e == e0 ? first.x : x[base + e], sc, sh);
       if (res) v += res[base + e];
       if (relu) v = fmaxf(v, 0.f);
       y[base + e] = v;
@@ -281,6 +419,18 @@ __global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restric
   }
 }
 
+// The per-channel constants of the input-gradient map from sum gz (s1) and sum gz * xhat (s2):
+// k = {gamma * invstd, gamma * invstd * s1 / m, gamma * invstd * s2 / m, mean, invstd}.
+__device__ __forceinline__ void bn_bwd_consts(double s1, double s2, double m, float gamma, float mean, float invstd,
+                                              float* k) {
+  const double gi = (double)gamma * (double)invstd;
+  k[0] = (float)gi;
+  k[1] = (float)(gi * s1 / m);
+  k[2] = (float)(gi * s2 / m);
+  k[3] = mean;
+  k[4] = invstd;
+}
+
 __global__ void bn_bwd_fin_kernel(const double* __restrict__ part, int c, int slices, const float* __restrict__ mean,
                                   const float* __restrict__ invstd, const float* __restrict__ gamma, double m,
                                   float* __restrict__ kc, float* __restrict__ dgamma, float* __restrict__ dbeta) {
@@ -293,14 +443,7 @@ __global__ void bn_bwd_fin_kernel(const double* __restrict__ part, int c, int sl
   }
   if (dbeta) dbeta[ch] = (float)s1;
   if (dgamma) dgamma[ch] = (float)s2;
-  if (gamma) {
-    const double gi = (double)gamma[ch] * (double)invstd[ch];
-    kc[ch * 5 + 0] = (float)gi;
-    kc[ch * 5 + 1] = (float)(gi * s1 / m);
-    kc[ch * 5 + 2] = (float)(gi * s2 / m);
-    kc[ch * 5 + 3] = mean[ch];
-    kc[ch * 5 + 4] = invstd[ch];
-  }
+  if (gamma) bn_bwd_consts(s1, s2, m, gamma[ch], mean[ch], invstd[ch], kc + ch * 5);
 }
 
 // gx = gamma * invstd / m * (m * gz - sum_gz - xhat * sum_gz_xhat) = k1 * gz - k2 - k3 * xhat, with the per-channel
@@ -348,6 +491,41 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_kernel(const float* __restri
   const int64_t base = (int64_t)plane * hwv;
   for (int e = blockIdx.y * 256 + threadIdx.x; e < hwv; e += gridDim.y * 256)
     bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e);
+}
+
+// bn_bwd_apply_kernel with the finalize folded in (one launch fewer): every workgroup derives its channel's constants
+// from the partials with bn_bwd_fin_kernel's arithmetic, and the channel's first workgroup (image 0, chunk 0) writes
+// dgamma / dbeta. Plane order: apply_plane.
+template <int VEC, bool RES>
+__global__ void __launch_bounds__(256) bn_bwd_train_apply_kernel(const float* __restrict__ g,
+                                                                 const float* __restrict__ g2,
+                                                                 const float* __restrict__ x,
+                                                                 const float* __restrict__ ry,
+                                                                 const double* __restrict__ part, int slices, double m,
+                                                                 const float* __restrict__ mean,
+                                                                 const float* __restrict__ invstd,
+                                                                 const float* __restrict__ gamma,
+                                                                 float* __restrict__ dgamma, float* __restrict__ dbeta,
+                                                                 float* __restrict__ gx, float* __restrict__ gzo, int c,
+                                                                 int hwv, int planes, int chunks, int rev) {
+  __shared__ float kc[5];
+  int chunk;
+  const int plane = apply_plane(planes, chunks, rev, chunk), ch = plane % c;
+  double s1, s2;
+  bn_sum_slices(part, ch, slices, s1, s2);
+  if (threadIdx.x == 0) {
+    if (plane < c && chunk == 0) {
+      if (dbeta) dbeta[ch] = (float)s1;
+      if (dgamma) dgamma[ch] = (float)s2;
+    }
+    bn_bwd_consts(s1, s2, m, gamma[ch], mean[ch], invstd[ch], kc);
+  }
+  __syncthreads();
+  float k[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) k[i] = kc[i];
+  const int64_t base = (int64_t)plane * hwv;
+  for (int e = chunk * 256 + threadIdx.x; e < hwv; e += chunks * 256) bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e);
 }
 
 // Small planes: flat over VEC-wide vectors.
@@ -412,21 +590,11 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
     }
   block_sum2(s1, s2);
   if (threadIdx.x == 0) {
-    const double m = (double)sp.nv * VEC;
-    const double a = s1 / m, mean = (double)shift + a;
-    double var = s2 / m - a * a;
-    if (var < 0.0) var = 0.0;
-    const float fm = (float)mean, fi = (float)(1.0 / sqrt(var + eps));
-    save_mean[ch] = fm;
-    save_invstd[ch] = fi;
-    if (new_rm && rm) new_rm[ch] = (float)((double)rm[ch] + momentum * (mean - (double)rm[ch]));
-    if (new_rv && rv) {
-      const double corr = (double)(float)(m / (m > 1.0 ? m - 1.0 : 1.0));
-      new_rv[ch] = (float)((double)rv[ch] + momentum * (var * corr - (double)rv[ch]));
-    }
-    const float sc = fi * gamma[ch];
+    const BnStats st = bn_finalize(s1, s2, (double)shift, (double)sp.nv * VEC, momentum, eps, rm, rv, save_mean,
+                                   save_invstd, new_rm, new_rv, ch, true);
+    const float sc = st.invstd * gamma[ch];
     coef[0] = sc;
-    coef[1] = beta[ch] - fm * sc;
+    coef[1] = beta[ch] - st.mean * sc;
   }
   __syncthreads();
   const float sc = coef[0], sh = coef[1];
@@ -497,14 +665,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   if (threadIdx.x == 0) {
     if (dbeta) dbeta[ch] = (float)s1;
     if (dgamma) dgamma[ch] = (float)s2;
-    if (gx) {
-      const double m = (double)sp.nv * VEC, gi = (double)gamma[ch] * (double)inv;
-      kc[0] = (float)gi;
-      kc[1] = (float)(gi * s1 / m);
-      kc[2] = (float)(gi * s2 / m);
-      kc[3] = mu;
-      kc[4] = inv;
-    }
+    if (gx) bn_bwd_consts(s1, s2, (double)sp.nv * VEC, gamma[ch], mu, inv, kc);
   }
   if (!gx && !RES) return;
   __syncthreads();
@@ -618,6 +779,20 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
   double* part = (double*)workspace;
   if (int st = launch_stats(sp, x, part, c, hw, s)) return st;
   const double m = (double)(n * hw);
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && al16(residual);
+  const dim3 ag = apply_grid(n * c, hw, vec ? 4 : 1), grid(ag.x * ag.y);
+  if (hw >= kFlatPlane && (int64_t)ag.x * ag.y < ((int64_t)1 << 31)) {  // the apply finalizes its own channel
+    const int rev = n * c * hw * 4 >= kRevApplyBytes;
+    if (vec)
+      hipLaunchKernelGGL(bn_train_apply_kernel<true>, grid, dim3(256), 0, s, x, (const double*)part, sp.slices, m,
+                         momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta,
+                         residual, y, (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev);
+    else
+      hipLaunchKernelGGL(bn_train_apply_kernel<false>, grid, dim3(256), 0, s, x, (const double*)part, sp.slices, m,
+                         momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta,
+                         residual, y, (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev);
+    return launch_check("bn_train_apply_kernel");
+  }
   hipLaunchKernelGGL(bn_stats_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, x, (const double*)part, (int)c,
                      (int)hw, sp.slices, m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm,
                      new_rv);
@@ -684,6 +859,19 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
                        part, (int)c, (int)hw, sp);
   if (int st = launch_check("bn_bwd_part_kernel")) return st;
   const double m = (double)(n * hw);
+  const dim3 ag = apply_grid(n * c, hw, sp.vec), grid(ag.x * ag.y);
+  if ((gx || RES) && hw >= kFlatPlane && (int64_t)ag.x * ag.y < ((int64_t)1 << 31)) {  // the apply finalizes its channel
+    const int rev = n * c * hw * 4 >= kRevApplyBytes;
+    if (sp.vec == 4)
+      hipLaunchKernelGGL((bn_bwd_train_apply_kernel<4, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y,
+                         (const double*)part, sp.slices, m, save_mean, save_invstd, gamma, dgamma, dbeta, gx, gzo,
+                         (int)c, (int)(hw / 4), (int)ag.x, (int)ag.y, rev);
+    else
+      hipLaunchKernelGGL((bn_bwd_train_apply_kernel<1, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y,
+                         (const double*)part, sp.slices, m, save_mean, save_invstd, gamma, dgamma, dbeta, gx, gzo,
+                         (int)c, (int)hw, (int)ag.x, (int)ag.y, rev);
+    return launch_check("bn_bwd_train_apply_kernel");
+  }
   // the apply pass needs the per-channel constants (gamma) whenever it runs: for gx, or for gzo
   hipLaunchKernelGGL(bn_bwd_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, sp.slices,
                      save_mean, save_invstd, (gx || RES) ? gamma : nullptr, m, kc, dgamma, dbeta);

@@ -591,7 +591,8 @@ def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
 
 @pytest.mark.parametrize("n,c,h,w", [(4, 6, 5, 7), (16, 8, 4, 4), (2, 3, 1, 1), (9, 4, 3, 3), (128, 32, 32, 32),
                                      (32, 64, 16, 16), (32, 512, 2, 2), (1, 16, 57, 31), (3, 5, 37, 41),
-                                     (64, 16, 28, 28), (8, 3, 7, 9)])
+                                     (64, 16, 28, 28), (8, 3, 7, 9), (9, 5, 33, 35), (4, 8, 56, 56),
+                                     (64, 64, 64, 64), (64, 64, 63, 65)])
 @pytest.mark.parametrize("relu", [False, True])
 def test_batch_norm_train_and_backward(cuda, ops, n, c, h, w, relu):
     rng = np.random.default_rng(n * 1000 + c)
@@ -614,7 +615,8 @@ def test_batch_norm_train_and_backward(cuda, ops, n, c, h, w, relu):
     assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
 
 
-@pytest.mark.parametrize("n,c,h,w", [(32, 64, 4, 4), (8, 3, 7, 9), (16, 8, 32, 32), (4, 6, 5, 7), (1024, 2, 3, 3)])
+@pytest.mark.parametrize("n,c,h,w", [(32, 64, 4, 4), (8, 3, 7, 9), (16, 8, 32, 32), (4, 6, 5, 7), (1024, 2, 3, 3),
+                                     (5, 3, 45, 41)])
 @pytest.mark.parametrize("with_g2", [True, False])
 def test_batch_norm_backward_res(cuda, ops, n, c, h, w, with_g2):
     """omt_bn_bwd_res: gz = (g + g2) masked by y > 0 returned exactly as the masked sum, and BatchNorm's grads of gz
