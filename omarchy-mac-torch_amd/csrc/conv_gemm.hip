@@ -1516,6 +1516,29 @@ __global__ void __launch_bounds__(256) bias_grad_kernel(const float* __restrict_
   if (threadIdx.x == 0) gb[ch] = red[0];
 }
 
+// Small planes (a linear layer's bias: hw = 1): thread per channel, summing n then hw in order; consecutive threads
+// read consecutive channels of a row, and every load of a group of 8 is in flight together.
+__global__ void __launch_bounds__(256) bias_grad_cols_kernel(const float* __restrict__ gy, float* __restrict__ gb, int n,
+                                                             int c, int hw) {
+  const int ch = blockIdx.x * 256 + threadIdx.x;
+  if (ch >= c) return;
+  const int total = n * hw;
+  float s = 0.f;
+  for (int i0 = 0; i0 < total; i0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u, nn = i / hw, e = i - nn * hw;
+      v[u] = i < total ? gy[((int64_t)nn * c + ch) * hw + e] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + u < total) s += v[u];
+  }
+  gb[ch] = s;
+}
+constexpr int kBiasColsHW = 16;  // planes up to this size take bias_grad_cols_kernel
+
 __global__ void __launch_bounds__(256) fold_bn_kernel(int co, int per_out, const float* __restrict__ cw,
                                                       const float* __restrict__ cb, const float* __restrict__ gamma,
                                                       const float* __restrict__ beta, const float* __restrict__ mean,
@@ -2600,6 +2623,11 @@ OMT_EXPORT int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, 
   if (!gy || !gb) return fail(OMT_INVALID, "omt_bias_grad: null pointer");
   if (n < 0 || c < 0 || hw < 0 || n * c * hw >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_bias_grad: size");
   if (c == 0) return OMT_OK;
+  if (hw <= kBiasColsHW) {
+    hipLaunchKernelGGL(bias_grad_cols_kernel, dim3((unsigned)cdiv(c, 256)), dim3(256), 0, stream_of(stream), gy, gb,
+                       (int)n, (int)c, (int)hw);
+    return launch_check("bias_grad_cols_kernel");
+  }
   hipLaunchKernelGGL(bias_grad_kernel, dim3((unsigned)c), dim3(256), 0, stream_of(stream), gy, gb, (int)n, (int)c,
                      (int)hw);
   return launch_check("bias_grad_kernel");

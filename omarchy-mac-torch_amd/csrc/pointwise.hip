@@ -149,6 +149,60 @@ __global__ void __launch_bounds__(256) log_softmax_bwd_kernel(const float* __res
   for (int j = lane; j < cols; j += 64) o[j] = gr[j] - expf(yr[j]) * s;
 }
 
+// The same two maps for rows of at most 64 R columns: a lane loads its R elements of the row at once (all loads in
+// flight together, where the loops above wait on the row once per pass) and every pass reads them from registers.
+// Each lane visits its columns in the loops' order, so the results are identical.
+template <int R>
+__global__ void __launch_bounds__(256) log_softmax_reg_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                              int64_t rows, int cols) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const float* xr = x + r * cols;
+  float v[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) v[i] = lane + 64 * i < cols ? xr[lane + 64 * i] : -INFINITY;
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < R; ++i) m = fmaxf(m, v[i]);
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (lane + 64 * i < cols) s += expf(v[i] - m);
+  s = wave_sum(s);
+  const float lse = m + logf(s);
+  float* yr = y + r * cols;
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (lane + 64 * i < cols) yr[lane + 64 * i] = v[i] - lse;
+}
+template <int R>
+__global__ void __launch_bounds__(256) log_softmax_bwd_reg_kernel(const float* __restrict__ g,
+                                                                  const float* __restrict__ y, float* __restrict__ gx,
+                                                                  int64_t rows, int cols) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const float *gr = g + r * cols, *yr = y + r * cols;
+  float gv[R], yv[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const bool in = lane + 64 * i < cols;
+    gv[i] = in ? gr[lane + 64 * i] : 0.f;
+    yv[i] = in ? yr[lane + 64 * i] : 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (lane + 64 * i < cols) s += gv[i];
+  s = wave_sum(s);
+  float* o = gx + r * cols;
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (lane + 64 * i < cols) o[lane + 64 * i] = gv[i] - expf(yv[i]) * s;
+}
+
 // NLL loss forward over log-probabilities logp[rows][cols] and int64 targets. reduction 0 (none): out[r] = -w[t_r]
 // logp[r][t_r] (0 for ignore_index); 1 (mean): sum / total weight; 2 (sum). One workgroup: thread t takes rows t,
 // t + 256, ... in order, then a fixed tree over the threads' partial sums.
@@ -295,8 +349,12 @@ OMT_EXPORT int omt_log_softmax_fwd(int64_t rows, int64_t cols, const float* x, f
   if (rows < 0 || cols < 1 || cols >= ((int64_t)1 << 31) || cdiv(rows, 4) >= ((int64_t)1 << 31))
     return fail(OMT_INVALID, "omt_log_softmax_fwd: size");
   if (rows == 0) return OMT_OK;
-  hipLaunchKernelGGL(log_softmax_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream_of(stream), x, y, rows,
-                     (int)cols);
+  const dim3 grid((unsigned)cdiv(rows, 4));
+  hipStream_t s = stream_of(stream);
+  if (cols <= 256) hipLaunchKernelGGL(log_softmax_reg_kernel<4>, grid, dim3(256), 0, s, x, y, rows, (int)cols);
+  else if (cols <= 1024) hipLaunchKernelGGL(log_softmax_reg_kernel<16>, grid, dim3(256), 0, s, x, y, rows, (int)cols);
+  else if (cols <= 4096) hipLaunchKernelGGL(log_softmax_reg_kernel<64>, grid, dim3(256), 0, s, x, y, rows, (int)cols);
+  else hipLaunchKernelGGL(log_softmax_kernel, grid, dim3(256), 0, s, x, y, rows, (int)cols);
   return launch_check("log_softmax_kernel");
 }
 
@@ -306,8 +364,16 @@ OMT_EXPORT int omt_log_softmax_bwd(int64_t rows, int64_t cols, const float* g, c
   if (rows < 0 || cols < 1 || cols >= ((int64_t)1 << 31) || cdiv(rows, 4) >= ((int64_t)1 << 31))
     return fail(OMT_INVALID, "omt_log_softmax_bwd: size");
   if (rows == 0) return OMT_OK;
-  hipLaunchKernelGGL(log_softmax_bwd_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream_of(stream), g, y, gx,
-                     rows, (int)cols);
+  const dim3 grid((unsigned)cdiv(rows, 4));
+  hipStream_t s = stream_of(stream);
+  if (cols <= 256)
+    hipLaunchKernelGGL(log_softmax_bwd_reg_kernel<4>, grid, dim3(256), 0, s, g, y, gx, rows, (int)cols);
+  else if (cols <= 1024)
+    hipLaunchKernelGGL(log_softmax_bwd_reg_kernel<16>, grid, dim3(256), 0, s, g, y, gx, rows, (int)cols);
+  else if (cols <= 4096)
+    hipLaunchKernelGGL(log_softmax_bwd_reg_kernel<64>, grid, dim3(256), 0, s, g, y, gx, rows, (int)cols);
+  else
+    hipLaunchKernelGGL(log_softmax_bwd_kernel, grid, dim3(256), 0, s, g, y, gx, rows, (int)cols);
   return launch_check("log_softmax_bwd_kernel");
 }
 

@@ -80,6 +80,15 @@ def test_conv_fwd_dgrad_wgrad(cuda, ops, shape):
     assert orc.rel_l2(host(gb), orc.bias_grad(gy)) <= TOL
 
 
+@pytest.mark.parametrize("n,c,hw", [(32, 1000, 1), (7, 5, 3), (3, 300, 16), (2, 4, 17), (1, 1, 1), (5, 70, 9)])
+def test_bias_grad(cuda, ops, n, c, hw):
+    """Bias gradient: per-channel columns for planes of up to 16 elements (a linear layer's bias, hw = 1), one
+    workgroup per channel above."""
+    rng = np.random.default_rng(n * c + hw)
+    gy = rnd(rng, n, c, hw, 1)
+    assert orc.rel_l2(host(ops.bias_grad(dev(gy, cuda))), orc.bias_grad(gy)) <= TOL
+
+
 @pytest.mark.parametrize("ks", range(1, 12))
 def test_conv_geometry_sweep(cuda, ops, ks):
     """Every stride 1..4 and pad 0..ks the dense path accepts at this kernel size (csrc/conv.cpp:173), on tiny

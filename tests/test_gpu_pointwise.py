@@ -97,7 +97,7 @@ def test_channel_scale_plane_sum_and_broadcast(cuda, shape):
     assert torch.equal(b.cpu(), (s * 0.25).expand(shape))
 
 
-@pytest.mark.parametrize("rows,cols", [(32, 1000), (128, 10), (5, 1), (3, 130)])
+@pytest.mark.parametrize("rows,cols", [(32, 1000), (128, 10), (5, 1), (3, 130), (4, 3000), (3, 5000), (7, 1024)])
 def test_log_softmax_and_nll_c_abi(cuda, rows, cols):
     from omarchy_mac_torch import _lib
     L = _lib.L
