@@ -139,6 +139,15 @@ size_t omt_conv_fwd_workspace(const omt_conv_geo* g);
 int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
                  const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta, float bn_eps,
                  float* y, void* workspace, size_t workspace_bytes, void* stream);
+/* Forward without bias, epilogue or BN loader whose K-split partial sums stay unsummed, for a consumer that sums
+ * them itself (omt_bn_train_fwd_parts): when the plan splits K into 2..max_slices slices, *partials points at the
+ * [*slices][n][co][oh][ow] partials inside the workspace and y is not written; otherwise (no split, or more slices:
+ * a consumer reading many slices per element is slower than the slice-sum launch) *slices = 1, *partials = NULL and
+ * y holds the output, as from omt_conv_fwd. Same workspace as omt_conv_fwd. No counterpart in the reference, whose
+ * convolution and BatchNorm are separate ops; the torch.compile backend fuses convolution -> training BatchNorm into
+ * the pair, which saves the slice-sum launch. */
+int omt_conv_fwd_unsummed(const omt_conv_geo* g, const float* x, const float* w, float* y, void* workspace,
+                          size_t workspace_bytes, int max_slices, const float** partials, int* slices, void* stream);
 
 /* Grad input: gx = conv_transpose(gy, w). Stride 1 is one GEMM over flipped, transposed weights; stride s > 1 is
  * s*s dense stride-phase GEMMs in one launch (phases no tap reaches write zeros). Replaces gemm_grad_input
@@ -253,6 +262,16 @@ int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const float* x, const
                          const float* running_mean, const float* running_var, double momentum, double eps, int relu,
                          const float* residual, float* y, float* save_mean, float* save_invstd, float* new_rm,
                          float* new_rv, void* workspace, size_t workspace_bytes, void* stream);
+/* omt_bn_train_fwd_res over a convolution's unsummed K-split partials (omt_conv_fwd_unsummed): x = the sum of the
+ * `slices` partials of n*c*hw elements each, in slice order (the convolution's own slice sum, so x is bit-identical
+ * to the summed convolution output), is written to x and normalized as by omt_bn_train_fwd_res. Channels of up to
+ * 8192 elements run the sum, the statistics and the apply in one launch. parts must not overlap x, y or residual.
+ * No counterpart in the reference (see omt_conv_fwd_unsummed). */
+int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts, int slices, float* x,
+                           const float* gamma, const float* beta, const float* running_mean, const float* running_var,
+                           double momentum, double eps, int relu, const float* residual, float* y, float* save_mean,
+                           float* save_invstd, float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
+                           void* stream);
 /* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
  * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
 int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,

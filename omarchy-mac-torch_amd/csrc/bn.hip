@@ -553,7 +553,9 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __r
 // of the split kernels above, so both paths agree to the float64 summation order.
 constexpr int64_t kFusedMax = 8192;
 
-template <int VEC>
+// PARTS: x holds `slices` convolution partials of pstride elements each; every element is summed over them in slice
+// order (the convolution slice sum's order, so xo, written with the sums, equals the summed convolution output).
+template <int VEC, bool PARTS = false>
 __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
@@ -562,11 +564,14 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
                                                              float* __restrict__ y, float* __restrict__ save_mean,
                                                              float* __restrict__ save_invstd, float* new_rm,
                                                              float* new_rv,  // may alias rm / rv
-                                                             int c, int hw, const Split sp) {
+                                                             int c, int hw, const Split sp, int slices = 1,
+                                                             int64_t pstride = 0, float* __restrict__ xo = nullptr) {
   using V = typename VecT<VEC>::T;
   __shared__ float coef[2];
   const int ch = blockIdx.x;
-  const float shift = x[(int64_t)ch * hw];
+  float shift = x[(int64_t)ch * hw];
+  if (PARTS)
+    for (int z = 1; z < slices; ++z) shift += x[z * pstride + (int64_t)ch * hw];
   constexpr int NR = (int)(kFusedMax / (256 * VEC));  // vectors per thread
   V r[NR];
 #pragma unroll
@@ -577,6 +582,24 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
     } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);
+    }
+  }
+  if (PARTS) {  // slice by slice, each slice's loads of all NR vectors in flight together
+    for (int z = 1; z < slices; ++z) {
+      V t[NR];
+#pragma unroll
+      for (int u = 0; u < NR; ++u) {
+        const int vv = (int)threadIdx.x + u * 256;
+        if (vv < sp.nv) t[u] = *reinterpret_cast<const V*>(x + z * pstride + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
+      }
+#pragma unroll
+      for (int u = 0; u < NR; ++u)
+        if ((int)threadIdx.x + u * 256 < sp.nv) vadd(r[u], t[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      const int vv = (int)threadIdx.x + u * 256;
+      if (vv < sp.nv) *reinterpret_cast<V*>(xo + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)) = r[u];
     }
   }
   double s1 = 0.0, s2 = 0.0;
@@ -614,6 +637,18 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       }
       *reinterpret_cast<V*>(y + off) = t;
     }
+  }
+}
+
+// xo[i] = sum of the slices' element i in slice order (VEC-wide vectors; nv vectors per slice).
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_sum_parts_kernel(const float* __restrict__ parts, int slices, int64_t nv,
+                                                           float* __restrict__ xo) {
+  using V = typename VecT<VEC>::T;
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < nv; i += (int64_t)gridDim.x * 256) {
+    V v = reinterpret_cast<const V*>(parts)[i];
+    for (int z = 1; z < slices; ++z) vadd(v, reinterpret_cast<const V*>(parts)[z * nv + i]);
+    reinterpret_cast<V*>(xo)[i] = v;
   }
 }
 
@@ -798,6 +833,44 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
                      new_rv);
   if (int st = launch_check("bn_stats_fin_kernel")) return st;
   return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s);
+}
+
+OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts, int slices, float* x,
+                                      const float* gamma, const float* beta, const float* running_mean,
+                                      const float* running_var, double momentum, double eps, int relu,
+                                      const float* residual, float* y, float* save_mean, float* save_invstd,
+                                      float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  if (!parts || !x || !gamma || !beta || !y || !save_mean || !save_invstd)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_parts: null pointer");
+  if (slices < 1) return fail(OMT_INVALID, "omt_bn_train_fwd_parts: %d slices", slices);
+  if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_parts: size not covered");
+  if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_train_fwd_parts: workspace too small");
+  hipStream_t s = stream_of(stream);
+  const int64_t total = n * c * hw;
+  const bool vec = hw % 4 == 0 && al16(parts) && al16(x) && al16(y) && al16(residual);
+  if (n * hw <= kFusedMax) {  // one launch: the slice sums, the statistics and the apply
+    const Split f = bn_split(n, c, hw, vec);
+    if (vec)
+      hipLaunchKernelGGL((bn_train_fused_kernel<4, true>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma, beta,
+                         running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,
+                         new_rv, (int)c, (int)hw, f, slices, total, x);
+    else
+      hipLaunchKernelGGL((bn_train_fused_kernel<1, true>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma, beta,
+                         running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,
+                         new_rv, (int)c, (int)hw, f, slices, total, x);
+    return launch_check("bn_train_fused_kernel");
+  }
+  const bool v4 = total % 4 == 0 && al16(parts) && al16(x);
+  const int64_t nv = v4 ? total / 4 : total;
+  if (v4)
+    hipLaunchKernelGGL(bn_sum_parts_kernel<4>, dim3(grid1d(nv, 256, 16384)), dim3(256), 0, s, parts, slices, nv, x);
+  else
+    hipLaunchKernelGGL(bn_sum_parts_kernel<1>, dim3(grid1d(nv, 256, 16384)), dim3(256), 0, s, parts, slices, nv, x);
+  if (int st = launch_check("bn_sum_parts_kernel")) return st;
+  return omt_bn_train_fwd_res(n, c, hw, x, gamma, beta, running_mean, running_var, momentum, eps, relu, residual, y,
+                              save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
 }
 
 OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,

@@ -1806,9 +1806,18 @@ static int launch_gather_sum(const GatherSum& r, hipStream_t s) {
   return launch_check("gather_reduce_kernel");
 }
 
-// Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size.
-static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t maxq, float* part, hipStream_t s) {
+// Launches the gather (and, split over K, the slice reduce); `part` is the partial workspace of the plan's size. With
+// `unsummed` set to a slice limit, a launch split into at most that many slices leaves its partials unsummed; the
+// count is reported back there (1: y was written).
+static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t maxq, float* part, hipStream_t s,
+                      int* unsummed = nullptr) {
   const GatherPlan pl = eff_plan(a, plan);
+  if (unsummed) {
+    const int lim = *unsummed;
+    *unsummed = 1;
+    if (pl.slices > 1 && pl.slices <= lim) *unsummed = (int)pl.slices;
+    else unsummed = nullptr;
+  }
   const dim3 grid = gather_grid(a, pl, n, maxq, part);
   if (gtile(pl.tile).stream) {
     hipLaunchKernelGGL((conv1x1_stream_kernel<64, 128, 32, 64>), grid, dim3(256), 0, s, a, a.tpw);
@@ -1825,6 +1834,7 @@ static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t 
   else
     gather_dispatch<kGeneric, false>(pl.tile % kNGather, a, grid, s);
   if (int st = launch_check("conv_gather_kernel")) return st;
+  if (unsummed) return OMT_OK;  // the partials stay for the caller
   return launch_gather_sum(gather_sum_of(a, pl), s);
 }
 
@@ -1946,10 +1956,12 @@ OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
   return part ? align256(fwd_pack_bytes(g, pl)) + part : fwd_pack_bytes(g, pl);
 }
 
-OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
-                            unsigned epilogue, const float* bn_mean, const float* bn_var, const float* bn_gamma,
-                            const float* bn_beta, float bn_eps, float* y, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+// The forward GEMM; with `unsummed` (no bias, epilogue or BN loader), a plan that splits K leaves its partials in the
+// workspace (*parts) and sets *unsummed to its slice count, else writes y and sets it to 1.
+static int conv_fwd_impl(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
+                         const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta,
+                         float bn_eps, float* y, void* workspace, size_t workspace_bytes, void* stream,
+                         const float** parts, int* unsummed) {
   if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd: null pointer");
   if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: geometry not covered (ks 1..11, stride 1..4, pad 0..ks)");
   if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: a tensor of 2 GiB or more");
@@ -2012,7 +2024,30 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
   p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   p.div_kw = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather(a, pl, g->n, p.Q, (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl))), s);
+  float* part = (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl)));
+  if (parts) *parts = part;
+  return run_gather(a, pl, g->n, p.Q, part, s, unsummed);
+}
+
+OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
+                            unsigned epilogue, const float* bn_mean, const float* bn_var, const float* bn_gamma,
+                            const float* bn_beta, float bn_eps, float* y, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return conv_fwd_impl(g, x, w, bias, epilogue, bn_mean, bn_var, bn_gamma, bn_beta, bn_eps, y, workspace,
+                       workspace_bytes, stream, nullptr, nullptr);
+}
+
+OMT_EXPORT int omt_conv_fwd_unsummed(const omt_conv_geo* g, const float* x, const float* w, float* y, void* workspace,
+                                     size_t workspace_bytes, int max_slices, const float** partials, int* slices,
+                                     void* stream) {
+  if (!partials || !slices) return fail(OMT_INVALID, "omt_conv_fwd_unsummed: null pointer");
+  *partials = nullptr;
+  int lim = max_slices < 1 ? 1 : max_slices;  // in: the slice limit; out: the slices left unsummed, or 1
+  const int st = conv_fwd_impl(g, x, w, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0.f, y, workspace,
+                               workspace_bytes, stream, partials, &lim);
+  *slices = lim;
+  if (lim == 1) *partials = nullptr;
+  return st;
 }
 
 // Stride-phase table of the grad-input GEMMs (see the top of this file).

@@ -16,7 +16,8 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
      takes along the add of the block output's two gradients in front of the mask;
   3. a dense convolution whose only user is a ReLU -> omt.conv_act (ReLU in the GEMM epilogue), or an eval BatchNorm
      (`_native_batch_norm_legit_no_training`, optionally followed by ReLU) -> omt.conv_bn_act_eval (BatchNorm folded
-     into the conv's weights and bias).
+     into the conv's weights and bias); a bias-free dense convolution feeding omt.bn_train_ -> omt.conv_bn_train_,
+     where the BatchNorm sums a K-split convolution's partials itself (no slice-sum launch).
 
 Each omt op falls back to its plain aten composition when the device kernels do not cover the case, so a rewritten
 graph is always correct. OMARCHY_MAC_TORCH_COMPILE_DEBUG=1 prints what each rewrite did. (The reference's fourth
@@ -319,11 +320,38 @@ def fuse_conv_epilogues(graph):
     return count
 
 
+def fuse_conv_bn_train(graph):
+    """bn_train_(convolution(x, cw, None, ...), ...) -> omt.conv_bn_train_(x, cw, stride, padding, ...), whose fourth
+    output is the convolution's (the BatchNorm backward reads it): with a K-split plan the BatchNorm sums the
+    convolution's partials itself (one launch fewer). The convolution's other uses must come after the BatchNorm."""
+    count = 0
+    order = {n: i for i, n in enumerate(graph.nodes)}
+    for n in list(graph.nodes):
+        if n.op != "call_function" or n.target is not omt.bn_train_.default:
+            continue
+        conv = n.args[0]
+        if not (isinstance(conv, Node) and _is_dense_conv(conv) and conv.args[2] is None):
+            continue
+        if any(u is not n and u.op != "output" and order[u] < order[n] for u in conv.users):
+            continue
+        cx, cw, _, stride, padding = conv.args[:5]
+        w, b, rm, rv, momentum, eps, act, res = n.args[1:9]
+        fused = _call_before(graph, n, omt.conv_bn_train_.default,
+                             (cx, cw, list(stride), list(padding), w, b, rm, rv, momentum, eps, act, res))
+        out = _call_before(graph, n, operator.getitem, (fused, 3), meta_from=conv)
+        n.replace_all_uses_with(fused)  # its users are getitems 0-2, the same outputs of the fused node
+        graph.erase_node(n)
+        conv.replace_all_uses_with(out)
+        graph.erase_node(conv)
+        count += 1
+    return count
+
+
 def _compile(gm, example_inputs):
     g = gm.graph
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
              "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
-             "bn_relu_backward": fuse_bn_relu_backward(g),
+             "bn_relu_backward": fuse_bn_relu_backward(g), "conv_bn_train": fuse_conv_bn_train(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()

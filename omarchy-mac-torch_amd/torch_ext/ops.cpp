@@ -374,6 +374,17 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_ref(const Tensor& x, 
   if (defined(res)) y = y + *res;
   return {act == 1 ? at::relu(y) : y, std::get<1>(r), std::get<2>(r)};
 }
+// convolution (no bias) -> training BatchNorm (in place) [-> + residual] [-> ReLU]; also returns the convolution's
+// output, which the BatchNorm backward reads
+static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_ref(const Tensor& x, const Tensor& cw,
+                                                                    IntArrayRef stride, IntArrayRef padding,
+                                                                    const Tensor& w, const Tensor& b, const Tensor& rm,
+                                                                    const Tensor& rv, double mom, double eps,
+                                                                    int64_t act, const std::optional<Tensor>& res) {
+  Tensor conv = at::convolution(x, cw, std::nullopt, stride, padding, {1, 1}, false, {0, 0}, 1);
+  auto r = bn_train_inplace_ref(conv, w, b, rm, rv, mom, eps, act, res);
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), conv};
+}
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_ref(const Tensor& g, const Tensor& x, const Tensor& y,
                                                                const Tensor& w, const Tensor& mean,
                                                                const Tensor& invstd, std::array<bool, 3> mask) {
@@ -445,6 +456,52 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_,
                              wsbytes(ws), cur_stream()),
         "omt::bn_train_");
   return {y, sm, si};
+}
+// The convolution leaves a K split of up to kFoldSlices slices unsummed and the BatchNorm sums them as it reads them
+// (in the slice order of the convolution's own slice sum: the convolution output and everything after it are
+// bit-identical to convolution + omt::bn_train_), one launch fewer; other plans run the two as they are. (With 16-32
+// slices of a 2x2-plane layer the BatchNorm's scattered partial reads took longer than the slice-sum launch.)
+constexpr int kFoldSlices = 4;
+static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor& x_, const Tensor& cw_,
+                                                                    IntArrayRef stride, IntArrayRef padding,
+                                                                    const Tensor& w, const Tensor& b, const Tensor& rm,
+                                                                    const Tensor& rv, double mom, double eps,
+                                                                    int64_t act, const std::optional<Tensor>& res_) {
+  cover(stride.size() == 2 && padding.size() == 2 && stride[0] == stride[1] && padding[0] == padding[1],
+        "uniform 2-D stride and padding");
+  cover(kind_of(x_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && !channels_last(x_, cw_),
+        "dense NCHW convolution");
+  cover(whole(w) && whole(b) && whole(rm) && whole(rv), "contiguous float32 BatchNorm parameters");
+  Tensor x = contig(x_), cw = contig(cw_);
+  omt_conv_geo g = conv_geo(x.size(0), x.size(1), cw.size(0), x.size(2), x.size(3), cw.size(2), stride[0], padding[0]);
+  cover(g.oh >= 1 && g.ow >= 1, "empty output");
+  Tensor res;
+  if (defined(res_)) {
+    cover(f32(*res_) && res_->sizes() == IntArrayRef({g.n, g.co, g.oh, g.ow}), "residual of the output's shape");
+    res = contig(*res_);
+  }
+  tune_conv(OMT_DIR_FWD, g);
+  Tensor conv = empty_dev({g.n, g.co, g.oh, g.ow});
+  Tensor ws = workspace(omt_conv_fwd_workspace(&g));
+  const float* parts = nullptr;
+  int slices = 1;
+  check(omt_conv_fwd_unsummed(&g, fp(x), fp(cw), fpm(conv), wsptr(ws), wsbytes(ws), kFoldSlices, &parts, &slices,
+                              cur_stream()),
+        "omt::conv_bn_train_ (convolution)");
+  const int64_t n = g.n, c = g.co, hw = g.oh * g.ow;
+  Tensor y = empty_dev(conv.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
+  const float* r = res.defined() ? fp(res) : nullptr;
+  const int relu = act == 1 ? 1 : 0;
+  if (slices > 1)
+    check(omt_bn_train_fwd_parts(n, c, hw, parts, slices, fpm(conv), fp(w), fp(b), fp(rm), fp(rv), mom, eps, relu, r,
+                                 fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws), cur_stream()),
+          "omt::conv_bn_train_ (BatchNorm of the partials)");
+  else
+    check(omt_bn_train_fwd_res(n, c, hw, fp(conv), fp(w), fp(b), fp(rm), fp(rv), mom, eps, relu, r, fpm(y), fpm(sm),
+                               fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws), cur_stream()),
+          "omt::conv_bn_train_ (BatchNorm)");
+  return {y, sm, si, conv};
 }
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_, const Tensor& x_, const Tensor& y_,
                                                                const Tensor& w, const Tensor& mean,
@@ -520,6 +577,14 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_k(const Tensor& x, co
   return dev_or_ref<&bn_train_inplace_dev, &bn_train_inplace_ref>("omt::bn_train_", x, w, b, rm, rv, mom, eps, act,
                                                                   res);
 }
+static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_k(const Tensor& x, const Tensor& cw, IntArrayRef s,
+                                                                  IntArrayRef p, const Tensor& w, const Tensor& b,
+                                                                  const Tensor& rm, const Tensor& rv, double mom,
+                                                                  double eps, int64_t act,
+                                                                  const std::optional<Tensor>& res) {
+  return dev_or_ref<&conv_bn_train_dev, &conv_bn_train_ref>("omt::conv_bn_train_", x, cw, s, p, w, b, rm, rv, mom, eps,
+                                                            act, res);
+}
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_k(const Tensor& g, const Tensor& x, const Tensor& y,
                                                              const Tensor& w, const Tensor& mean,
                                                              const Tensor& invstd, std::array<bool, 3> mask) {
@@ -561,6 +626,9 @@ TORCH_LIBRARY(omt, m) {
         "Tensor? residual) -> (Tensor, Tensor, Tensor)");
   m.def("conv_bn_act_eval(Tensor x, Tensor cw, Tensor? cb, Tensor w, Tensor b, Tensor rm, Tensor rv, float eps, "
         "int[] stride, int[] padding, int act) -> Tensor");
+  // convolution (no bias) -> bn_train_: (y, save_mean, save_invstd, convolution output)
+  m.def("conv_bn_train_(Tensor x, Tensor cw, int[] stride, int[] padding, Tensor w, Tensor b, Tensor(a!) rm, "
+        "Tensor(b!) rv, float momentum, float eps, int act, Tensor? residual) -> (Tensor, Tensor, Tensor, Tensor)");
 }
 TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("bn_relu_train", &bn_relu_train_ref);
@@ -569,6 +637,7 @@ TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("bn_relu_res_backward", &bn_relu_res_backward_ref);
   m.impl("conv_act", &conv_act_ref);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
+  m.impl("conv_bn_train_", &conv_bn_train_ref);
 }
 TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_train", &bn_relu_train_k);
@@ -577,6 +646,7 @@ TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_res_backward", &bn_relu_res_backward_k);
   m.impl("conv_act", &conv_act_k);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);
+  m.impl("conv_bn_train_", &conv_bn_train_k);
 }
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {

@@ -180,3 +180,62 @@ def test_bn_relu_res_backward(oc, with_add, second_user):
              torch.rand(c, generator=gen) + 0.5, torch.randn(shp, generator=gen)]
     for o_ref, o_new in zip(ref(*args), gm(*args)):
         torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)
+
+
+def _conv_bn_graph(oc, bias, early_user, res):
+    """Forward graph of convolution -> omt.bn_train_ (as rewrite 0 leaves it), the convolution's output also a graph
+    output (saved for the BatchNorm backward); `early_user`: an op reads the convolution output before the BatchNorm."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    xs, ws, ys, c = (2, 3, 6, 6), (4, 3, 3, 3), (2, 4, 6, 6), 4
+
+    def ph(name, shape):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape)
+        return n
+
+    x, cw, cb, w, b, rm, rv, r = (ph("x", xs), ph("cw", ws), ph("cb", (c,)), ph("w", (c,)), ph("b", (c,)),
+                                  ph("rm", (c,)), ph("rv", (c,)), ph("r", ys))
+    conv = g.call_function(aten.convolution.default, (x, cw, cb if bias else None, [1, 1], [1, 1], [1, 1], False,
+                                                      [0, 0], 1))
+    conv.meta["val"] = _fake(mode, dev, ys)
+    extra = ()
+    if early_user:
+        e = g.call_function(aten.mul.Tensor, (conv, 2.0))
+        e.meta["val"] = _fake(mode, dev, ys)
+        extra = (e,)
+    bn = g.call_function(torch.ops.omt.bn_train_.default, (conv, w, b, rm, rv, 0.1, 1e-5, 1, r if res else None))
+    outs = []
+    for i, shp in enumerate((ys, (c,), (c,))):
+        gi = g.call_function(operator.getitem, (bn, i))
+        gi.meta["val"] = _fake(mode, dev, shp)
+        outs.append(gi)
+    g.output(tuple(outs) + (conv,) + extra)
+    return GraphModule(torch.nn.Module(), g)
+
+
+@pytest.mark.parametrize("case", ["plain", "residual", "bias", "early_user"])
+def test_conv_bn_train(oc, case):
+    """A bias-free dense convolution feeding omt.bn_train_ becomes one omt.conv_bn_train_ whose fourth output replaces
+    the convolution's other uses; with a bias, or a use of the convolution before the BatchNorm, the graph stays as it
+    is. The rewritten graph gives the original's outputs and running statistics on CPU tensors."""
+    gm = _conv_bn_graph(oc, case == "bias", case == "early_user", case == "residual")
+    ref = copy.deepcopy(gm)
+    expect = 1 if case in ("plain", "residual") else 0
+    assert oc.fuse_conv_bn_train(gm.graph) == expect
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    assert t.count(torch.ops.omt.conv_bn_train_.default) == expect
+    assert t.count(aten.convolution.default) == 1 - expect and t.count(torch.ops.omt.bn_train_.default) == 1 - expect
+    gen = torch.Generator().manual_seed(5)
+    args = [torch.randn(2, 3, 6, 6, generator=gen), torch.randn(4, 3, 3, 3, generator=gen) * 0.3,
+            torch.randn(4, generator=gen), torch.rand(4, generator=gen) + 0.5, torch.randn(4, generator=gen),
+            torch.randn(4, generator=gen), torch.rand(4, generator=gen) + 0.5, torch.randn(2, 4, 6, 6, generator=gen)]
+    a, b = [t.clone() for t in args], [t.clone() for t in args]
+    for o_ref, o_new in zip(ref(*a), gm(*b)):
+        torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)
+    for i in (5, 6):  # running statistics, updated in place
+        torch.testing.assert_close(b[i], a[i], rtol=1e-6, atol=1e-7)

@@ -583,6 +583,49 @@ def test_native_batch_norm_legit_shims_on_device(clean, shape):
     assert not [k for k in delegated if "batch_norm" in k], delegated
 
 
+@pytest.mark.parametrize("shape", [(4, 16, 32, 8, 8, 3, 1, 1), (32, 64, 64, 16, 16, 3, 1, 1),
+                                   (8, 16, 16, 40, 40, 3, 1, 1), (16, 32, 32, 14, 14, 3, 2, 1),
+                                   (6, 24, 20, 9, 9, 1, 1, 0), (8, 64, 64, 2, 2, 3, 1, 1)])
+def test_conv_bn_train_matches_conv_then_bn(clean, shape):
+    """omt::conv_bn_train_ (the compile backend's convolution -> training BatchNorm) against the convolution followed
+    by omt::bn_train_, bit for bit (outputs, convolution output, statistics, running statistics), under unsplit and
+    K-split plans (the BatchNorm sums the convolution's partials itself up to 4 slices; 16 are summed by the
+    convolution): channels of at most 8192 elements (one launch), larger ones (slice sum, then the two-pass
+    BatchNorm), 7x7 planes (scalar loads), 2x2 planes, with a residual and ReLU; and against the oracle."""
+    omt = clean
+    from omarchy_mac_torch import hip_ops
+    n, ci, co, h, w, ks, st, pd = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.standard_normal((n, ci, h, w)).astype(np.float32)
+    cw = (rng.standard_normal((co, ci, ks, ks)) * (ci * ks * ks) ** -0.5).astype(np.float32)
+    g, b = rng.standard_normal(co).astype(np.float32), rng.standard_normal(co).astype(np.float32)
+    rm, rv = rng.standard_normal(co).astype(np.float32), (rng.random(co) + 0.5).astype(np.float32)
+    oh = (h + 2 * pd - ks) // st + 1
+    r = rng.standard_normal((n, co, oh, oh)).astype(np.float32)
+    dx, dcw, dg, db, dr = (D(torch.from_numpy(a), omt) for a in (x, cw, g, b, r))
+    conv_ref = orc.conv_fwd(x, cw, None, st, pd)
+    try:
+        for slices in (1, 2, 4, 16):
+            hip_ops.set_conv_plan("fwd", x.shape, cw.shape, st, pd, 5, slices)
+            for act, res in ((1, None), (1, dr), (0, None)):
+                rm1, rv1 = D(torch.from_numpy(rm.copy()), omt), D(torch.from_numpy(rv.copy()), omt)
+                rm2, rv2 = D(torch.from_numpy(rm.copy()), omt), D(torch.from_numpy(rv.copy()), omt)
+                y1, m1, i1, c1 = torch.ops.omt.conv_bn_train_(dx, dcw, [st, st], [pd, pd], dg, db, rm1, rv1, 0.1, 1e-5,
+                                                              act, res)
+                c2 = torch.ops.aten.convolution(dx, dcw, None, [st, st], [pd, pd], [1, 1], False, [0, 0], 1)
+                y2, m2, i2 = torch.ops.omt.bn_train_(c2, dg, db, rm2, rv2, 0.1, 1e-5, act, res)
+                case = (slices, act, res is not None)
+                for a, bb in ((y1, y2), (m1, m2), (i1, i2), (c1, c2), (rm1, rm2), (rv1, rv2)):
+                    assert torch.equal(a.cpu(), bb.cpu()), case
+                assert rel(c1, conv_ref) <= TOL, case
+                if res is None and act == 1:
+                    y_ref = orc.bn_train(conv_ref, g, b, rm, rv, 0.1, 1e-5, True)[0]
+                    assert rel(y1, y_ref) <= TOL, case
+    finally:
+        hip_ops.clear_conv_plans()
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
+
+
 def test_strict_mode_turns_a_fallback_into_an_error(clean):
     """OMARCHY_MAC_TORCH_STRICT (reference csrc/device.cpp:213-216): an uncovered call raises instead of running on
     torch's kernels, and nothing is counted."""
