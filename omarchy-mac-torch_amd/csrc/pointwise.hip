@@ -7,6 +7,8 @@
 // All of them are HBM- or latency-bound. Pointwise ops stream float4 vectors (16-byte aligned operands) through a
 // grid-stride loop; the reductions give each output one wave (DPP sums, omt_internal.h) or, for the NLL loss, one
 // workgroup summing in a fixed order, so results do not depend on scheduling.
+#include <type_traits>
+
 #include "omt_internal.h"
 
 namespace omt {
@@ -93,9 +95,46 @@ __global__ void __launch_bounds__(256) plane_sum_kernel(const float* __restrict_
   const int lane = threadIdx.x & 63;
   const float* xp = x + plane * hw;
   float acc = 0.f;
-  for (int e = lane; e < hw; e += 64) acc += xp[e];
+  for (int e0 = lane; e0 < hw; e0 += 256) {  // four loads in flight, added in the same order as one at a time
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = e0 + 64 * j < hw ? xp[e0 + 64 * j] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (e0 + 64 * j < hw) acc += v[j];
+  }
   acc = wave_sum(acc);
   if (lane == 0) y[plane] = acc * scale;
+}
+
+// Large planes (kPlaneWG elements and more): one workgroup per plane. Each thread sums its float4 vectors (stride
+// 256, four loads in flight), then the wave sums (DPP) are added in wave order.
+constexpr int kPlaneWG = 1024;
+template <int VEC>
+__global__ void __launch_bounds__(256) plane_sum_wg_kernel(const float* __restrict__ x, float* __restrict__ y, int hw,
+                                                           float scale) {
+  using V = typename std::conditional<VEC == 4, float4, float>::type;
+  __shared__ float red[4];
+  const int64_t plane = blockIdx.x;
+  const V* xp = reinterpret_cast<const V*>(x + plane * hw);
+  const int nv = hw / VEC;
+  float acc = 0.f;
+  for (int e0 = threadIdx.x; e0 < nv; e0 += 1024) {
+    V v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (e0 + 256 * j < nv) v[j] = xp[e0 + 256 * j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (e0 + 256 * j < nv) {
+        if constexpr (VEC == 4) acc += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+        else acc += v[j];
+      }
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) y[plane] = ((red[0] + red[1]) + (red[2] + red[3])) * scale;
 }
 
 // Maximum over the 64 lanes of a wave, in every lane (the DPP pattern of wave_sum). All 64 lanes must be active.
@@ -339,6 +378,15 @@ OMT_EXPORT int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float s
   if (planes < 0 || hw < 0 || hw >= ((int64_t)1 << 31) || cdiv(planes, 4) >= ((int64_t)1 << 31))
     return fail(OMT_INVALID, "omt_plane_sum: size");
   if (planes == 0) return OMT_OK;
+  if (hw >= kPlaneWG && planes < ((int64_t)1 << 31)) {
+    if (hw % 4 == 0 && ((uintptr_t)x & 15) == 0)
+      hipLaunchKernelGGL(plane_sum_wg_kernel<4>, dim3((unsigned)planes), dim3(256), 0, stream_of(stream), x, y, (int)hw,
+                         scale);
+    else
+      hipLaunchKernelGGL(plane_sum_wg_kernel<1>, dim3((unsigned)planes), dim3(256), 0, stream_of(stream), x, y, (int)hw,
+                         scale);
+    return launch_check("plane_sum_wg_kernel");
+  }
   hipLaunchKernelGGL(plane_sum_kernel, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, stream_of(stream), x, y, planes,
                      (int)hw, scale);
   return launch_check("plane_sum_kernel");

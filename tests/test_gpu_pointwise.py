@@ -75,8 +75,10 @@ def test_pointwise_c_abi(cuda, n, offset):
     assert torch.equal(torch.isnan(nan.cpu()), torch.tensor([True, False, False, True]))
 
 
-@pytest.mark.parametrize("shape", [(32, 16, 112, 112), (4, 96, 7, 7), (3, 5, 3, 5)])
+@pytest.mark.parametrize("shape", [(32, 16, 112, 112), (4, 96, 7, 7), (3, 5, 3, 5), (2, 3, 33, 35), (2, 4, 20, 20)])
 def test_channel_scale_plane_sum_and_broadcast(cuda, shape):
+    """Channel scale, plane sums (a wave per plane below 1024 elements, a workgroup per plane from there, float4 or
+    scalar loads) and the plane broadcast of the mean's gradient."""
     from omarchy_mac_torch import _lib
     L = _lib.L
     n, c, h, w = shape
