@@ -1405,6 +1405,57 @@ __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64
   }
 }
 
+// Many slices (kGroupSlices and more): a workgroup takes 16 consecutive vectors, and each of its 16 groups of 16
+// threads sums a contiguous range of about slices / 16 slices in slice order (eight loads in flight); the group sums
+// are then added in group order. A fixed order, so still deterministic, and a sixteenth of the dependent load batches
+// per thread (a grad weight of 16 x 16 outputs over 251 slices waited 32 batches long in the plain order).
+constexpr int kGroupSlices = 32;
+template <int VEC>
+__device__ __forceinline__ void split_sum_grouped(const float* __restrict__ part, float* __restrict__ out, int64_t n,
+                                                  int slices, int64_t b0, int64_t nb) {
+  using T = typename VecF<VEC>::T;
+  __shared__ float red[16][16][VEC];
+  const int64_t nv = n / VEC;
+  const int tv = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int per = (slices + 15) / 16, z0 = grp * per, z1 = min(slices, z0 + per);
+  const T* p = reinterpret_cast<const T*>(part);
+  for (int64_t base = b0 * 16; base < nv; base += nb * 16) {
+    const int64_t i = base + tv;
+    float v[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = 0.f;
+    if (i < nv) {
+      for (int z = z0; z < z1; z += kReduceBatch) {
+        T t[kReduceBatch];
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u)
+          if (z + u < z1) t[u] = p[(int64_t)(z + u) * nv + i];
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u)
+          if (z + u < z1) {
+            if (z + u == z0)
+              VecF<VEC>::set(v, t[u]);
+            else
+              VecF<VEC>::add(v, t[u]);
+          }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[grp][tv][e] = v[e];
+    __syncthreads();
+    if (grp == 0 && i < nv) {
+      float sum[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum[e] = red[0][tv][e];
+      for (int g2 = 1; g2 < 16; ++g2)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sum[e] += red[g2][tv][e];
+      reinterpret_cast<T*>(out)[i] = VecF<VEC>::pack(sum);
+    }
+    __syncthreads();
+  }
+}
+
 struct SplitSum {
   const float* part;
   float* out;
@@ -1413,10 +1464,17 @@ struct SplitSum {
   bool vec4;
   int64_t blocks;
 };
+template <int VEC>
+__device__ __forceinline__ void split_sum_any(const SplitSum& r, int64_t b0, int64_t nb) {
+  if (r.slices >= kGroupSlices)
+    split_sum_grouped<VEC>(r.part, r.out, r.n, r.slices, b0, nb);
+  else
+    split_sum<VEC>(r.part, r.out, r.n, r.slices, b0, nb);
+}
 
 template <int VEC>
 __global__ void __launch_bounds__(256) split_reduce_kernel(const SplitSum r) {
-  split_sum<VEC>(r.part, r.out, r.n, r.slices, blockIdx.x, gridDim.x);
+  split_sum_any<VEC>(r, blockIdx.x, gridDim.x);
 }
 template <int VEC>
 __global__ void __launch_bounds__(256) gather_reduce_kernel(const GatherSum r) {
@@ -1429,7 +1487,7 @@ __global__ void __launch_bounds__(256) dual_reduce_kernel(const GatherSum g, con
   if (b < g.blocks)
     gather_sum<GV>(g, b, g.blocks);
   else
-    split_sum<WV>(w.part, w.out, w.n, w.slices, b - g.blocks, (int64_t)gridDim.x - g.blocks);
+    split_sum_any<WV>(w, b - g.blocks, (int64_t)gridDim.x - g.blocks);
 }
 
 // Re-packs w[co][ci][ks][ks] into the per-phase grad-input weights W'[ci][co][a'][b'] described at the top.
@@ -2320,7 +2378,8 @@ static SplitSum wgrad_sum_of(const WgradArgs& a, const WgradPlan& pl, float* gw)
   r.n = (int64_t)a.P * a.Q;
   r.slices = (int)pl.slices;
   r.vec4 = r.n % 4 == 0 && (uintptr_t)gw % 16 == 0;
-  r.blocks = grid1d(r.vec4 ? r.n / 4 : r.n, 256, 8192);
+  const int64_t nv = r.vec4 ? r.n / 4 : r.n;
+  r.blocks = r.slices >= kGroupSlices ? std::min<int64_t>(cdiv(nv, 16), 8192) : grid1d(nv, 256, 8192);
   return r;
 }
 static int launch_split_sum(const SplitSum& r, hipStream_t s) {

@@ -256,6 +256,8 @@ BWD_SHAPES = [
     (2, 32, 48, 6, 5, 1, 1, 0),     # 1x1
     (2, 64, 64, 8, 8, 1, 2, 0),     # 1x1 stride 2: phases no tap reaches
     (2, 3, 64, 20, 20, 3, 2, 1),    # super-pixel grad input (3 channels, stride 2), split K summed by the scatter
+    (16, 16, 24, 32, 32, 3, 1, 1),  # grad weight over 16384 pixels: 40 and 100 slices take the grouped slice sum
+    (16, 3, 5, 32, 32, 3, 1, 1),    # the same with 135 outputs (scalar vectors, a partial last group)
 ]
 
 
@@ -263,7 +265,8 @@ BWD_SHAPES = [
 def test_conv_bwd_matches_separate_calls(cuda, ops, shape):
     """omt_conv_bwd (grad input and grad weight in one call; one launch when both plans use 64x64 tiles) is
     bit-identical to omt_conv_dgrad + omt_conv_wgrad under the same plans, and matches the oracle: dual and non-dual
-    plan pairs, tap-major and channel-major grad input, split K on either side."""
+    plan pairs, tap-major and channel-major grad input, split K on either side (grad weight up to 100 slices, whose
+    sums go by groups of slices)."""
     n, ci, co, h, w, ks, s, p = shape
     rng = np.random.default_rng(sum(shape) + 5)
     x, wt = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
@@ -275,7 +278,7 @@ def test_conv_bwd_matches_separate_calls(cuda, ops, shape):
     try:
         for dtile in (5, 6, 5 + ng, 6 + ng, 0):
             for dslices in (1, 3):
-                for wtile, wslices in ((2, 1), (2, 4), (0, 2)):
+                for wtile, wslices in ((2, 1), (2, 4), (0, 2), (2, 40), (2, 100)):
                     case = (dtile, dslices, wtile, wslices)
                     ops.set_conv_plan("dgrad", x.shape, wt.shape, s, p, dtile, dslices)
                     ops.set_conv_plan("wgrad", x.shape, wt.shape, s, p, wtile, wslices)
