@@ -1376,14 +1376,13 @@ __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64
   for (int64_t i = b0 * blockDim.x + threadIdx.x; i < nv; i += nb * blockDim.x) {
     float v[VEC];
     sum_slices<VEC>(reinterpret_cast<const T*>(r.part), nv, i, r.slices, v);
-    if (VEC == 1 && r.d2s) {  // partials below 2 GiB: 32-bit index arithmetic
-      const int e = (int)i, pl = (int)r.plane, rows = r.P * pl;
-      const int n = e / rows, p = (e - n * rows) / pl, q = e - n * rows - p * pl;
+    if (VEC == 1 && r.d2s) {  // 64-bit image index: the grid of s^2 C rows can exceed the image on tiny images
+      const int64_t pl = r.plane, rows = (int64_t)r.P * pl, n = i / rows, rem = i - n * rows;
+      const int p = (int)(rem / pl), q = (int)(rem - p * pl);
       const int oy = q / r.grid_w, ox = q - oy * r.grid_w;
       const int c = p % r.d2s_ci, f = p / r.d2s_ci, py = f / r.d2s, px = f - py * r.d2s;
       const int row = oy * r.d2s + py, col = ox * r.d2s + px;
-      if (row < r.img_h && col < r.img_w)
-        r.y[((int64_t)(n * r.d2s_ci + c) * r.img_h + row) * r.img_w + col] = v[0];
+      if (row < r.img_h && col < r.img_w) r.y[((n * r.d2s_ci + c) * r.img_h + row) * r.img_w + col] = v[0];
       continue;
     }
     if (r.nhwc) {  // channels last: element i VEC + e is channel (i VEC + e) % P
