@@ -109,6 +109,21 @@ struct GatherArgs {
 template <int BP, int BQ, int BK>
 constexpr int gather_lds_floats() { return 2 * (BP + BQ) * (BK + 4); }
 
+// The bias of a lane's accumulator rows (channel p0 + wp WP + 16 i + 4 (lane / 16) + r4), loaded together before the
+// epilogue: a bias load per element inside the stores' bounds branches compiled to one `s_waitcnt vmcnt(0)` per
+// element, each draining every load and store in flight. 0 where there is no bias or the channel is past P.
+template <int TI, int WP>
+__device__ __forceinline__ void epilogue_bias(const GatherArgs& a, int p0, int wp, int lane, float (&bv)[TI][4]) {
+  const int pb = p0 + wp * WP + 4 * (lane >> 4);
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int p = pb + 16 * i + r4;
+      bv[i][r4] = a.bias && p < a.P ? a.bias[p] : 0.f;
+    }
+}
+
 // Gather epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid); split K: raw partials of
 // slice zs. acc[i][j] is the wave's 16x16 MFMA tile (i, j): element r4 of lane l is row 4 (l / 16) + r4, column l % 16.
 template <int TI, int TJ, int WP, int WQ>
@@ -118,6 +133,8 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
   const int64_t yhw = (int64_t)a.YH * a.YW;
   float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
   const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+  float bv[TI][4];
+  epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int q = q0 + wq * WQ + 16 * j + (lane & 15);
@@ -133,7 +150,7 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
         if (p < P) {
           float v = acc[i][j][r4];
           if (!a.part) {
-            if (a.bias) v += a.bias[p];
+            if (a.bias) v += bv[i][r4];
             if (a.relu) v = fmaxf(v, 0.f);
           }
           yb[(int64_t)p * yhw] = v;
@@ -151,6 +168,8 @@ __device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const 
   const int P = a.P, grp = lane >> 4;
   float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
   const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
+  float bv[TI][4];
+  epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int q = q0 + wq * WQ + 16 * j + (lane & 15);
@@ -167,7 +186,7 @@ __device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const 
       for (int r4 = 0; r4 < 4; ++r4) {
         v[r4] = acc[i][j][r4];
         if (!a.part) {
-          if (a.bias && p + r4 < P) v[r4] += a.bias[p + r4];
+          if (a.bias && p + r4 < P) v[r4] += bv[i][r4];
           if (a.relu) v[r4] = fmaxf(v[r4], 0.f);
         }
       }
@@ -238,6 +257,8 @@ __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& p
   const int q = q0 + wq * WQ + 4 * (lane % LPR);
   const uint32_t n = fdiv((uint32_t)min(q, ph.Q - 1), ph.div_ohw);
   float* const yq = a.y + (int64_t)n * P * ohw + (q - (int)(n * ohw));
+  float bv[TI][4];
+  epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -248,7 +269,7 @@ __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& p
         for (int r2 = 0; r2 < 2; ++r2) {
           const int p = p0 + wp * WP + 16 * i + 4 * grp + 2 * h + r2;
           float v = acc[i][j][2 * h + r2];
-          if (a.bias && p < P) v += a.bias[p];
+          if (a.bias && p < P) v += bv[i][2 * h + r2];
           if (a.relu) v = fmaxf(v, 0.f);
           ep[(2 * grp + r2) * EP + 16 * j + (lane & 15)] = v;
         }
