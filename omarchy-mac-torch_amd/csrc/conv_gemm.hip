@@ -126,15 +126,14 @@ __device__ __forceinline__ void epilogue_bias(const GatherArgs& a, int p0, int w
 
 // Gather epilogue: bias, ReLU, scatter to NCHW (phase outputs land on their stride grid); split K: raw partials of
 // slice zs. acc[i][j] is the wave's 16x16 MFMA tile (i, j): element r4 of lane l is row 4 (l / 16) + r4, column l % 16.
-template <int TI, int TJ, int WP, int WQ>
-__device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
-                                                int q0, int p0, int wp, int wq, int lane, int zs) {
+template <int TI, int TJ, int WP, int WQ, bool BIAS>
+__device__ __forceinline__ void gather_epilogue_b(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                                  int q0, int p0, int wp, int wq, int lane, int zs,
+                                                  const float (&bv)[TI][4]) {
   const int P = a.P, grp = lane >> 4;
   const int64_t yhw = (int64_t)a.YH * a.YW;
   float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
   const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
-  float bv[TI][4];
-  epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int q = q0 + wq * WQ + 16 * j + (lane & 15);
@@ -150,7 +149,7 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
         if (p < P) {
           float v = acc[i][j][r4];
           if (!a.part) {
-            if (a.bias) v += bv[i][r4];
+            if (BIAS) v += bv[i][r4];
             if (a.relu) v = fmaxf(v, 0.f);
           }
           yb[(int64_t)p * yhw] = v;
@@ -158,18 +157,29 @@ __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase
       }
   }
 }
+// The epilogues branch once on the bias: with one, its loads are issued together and waited for once; without, no
+// load is pending at the stores (a merged path would wait for every load and store in flight at each tile's end).
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                                int q0, int p0, int wp, int wq, int lane, int zs) {
+  float bv[TI][4];
+  if (a.bias && !a.part) {
+    epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
+    gather_epilogue_b<TI, TJ, WP, WQ, true>(a, ph, acc, q0, p0, wp, wq, lane, zs, bv);
+  } else {
+    gather_epilogue_b<TI, TJ, WP, WQ, false>(a, ph, acc, q0, p0, wp, wq, lane, zs, bv);
+  }
+}
 
 // Channels-last gather epilogue: output pixel (n, oy os + oy0, ox os + ox0) holds its P channels contiguously, so the
 // four accumulator rows of a lane (channels 4 (l / 16) + r4 of one pixel) are one 16-byte store where a.vec_out holds.
-template <int TI, int TJ, int WP, int WQ>
-__device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const Phase& ph,
-                                                     const omt_f32x4 (&acc)[TI][TJ], int q0, int p0, int wp, int wq,
-                                                     int lane, int zs) {
+template <int TI, int TJ, int WP, int WQ, bool BIAS>
+__device__ __forceinline__ void gather_epilogue_nhwc_b(const GatherArgs& a, const Phase& ph,
+                                                       const omt_f32x4 (&acc)[TI][TJ], int q0, int p0, int wp, int wq,
+                                                       int lane, int zs, const float (&bv)[TI][4]) {
   const int P = a.P, grp = lane >> 4;
   float* const ydst = a.part ? a.part + zs * a.part_stride : a.y;
   const uint32_t ohw = (uint32_t)(ph.OH * ph.OW);
-  float bv[TI][4];
-  epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int q = q0 + wq * WQ + 16 * j + (lane & 15);
@@ -186,7 +196,7 @@ __device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const 
       for (int r4 = 0; r4 < 4; ++r4) {
         v[r4] = acc[i][j][r4];
         if (!a.part) {
-          if (a.bias && p + r4 < P) v[r4] += bv[i][r4];
+          if (BIAS && p + r4 < P) v[r4] += bv[i][r4];
           if (a.relu) v[r4] = fmaxf(v[r4], 0.f);
         }
       }
@@ -198,6 +208,18 @@ __device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const 
           if (p + r4 < P) yb[p + r4] = v[r4];
       }
     }
+  }
+}
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void gather_epilogue_nhwc(const GatherArgs& a, const Phase& ph,
+                                                     const omt_f32x4 (&acc)[TI][TJ], int q0, int p0, int wp, int wq,
+                                                     int lane, int zs) {
+  float bv[TI][4];
+  if (a.bias && !a.part) {
+    epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
+    gather_epilogue_nhwc_b<TI, TJ, WP, WQ, true>(a, ph, acc, q0, p0, wp, wq, lane, zs, bv);
+  } else {
+    gather_epilogue_nhwc_b<TI, TJ, WP, WQ, false>(a, ph, acc, q0, p0, wp, wq, lane, zs, bv);
   }
 }
 
@@ -247,9 +269,10 @@ __device__ __forceinline__ void d2s_epilogue(const GatherArgs& a, const Phase& p
 // makes ep free before (no wave still reads it) and, where LDS is used again, waits for the reads after.
 template <int WQ>
 constexpr int row_epi_floats() { return 8 * (WQ + 8); }
-template <int TI, int TJ, int WP, int WQ>
-__device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
-                                             int q0, int p0, int wp, int wq, int lane, float* __restrict__ ep) {
+template <int TI, int TJ, int WP, int WQ, bool BIAS>
+__device__ __forceinline__ void row_epilogue_b(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                               int q0, int p0, int wp, int wq, int lane, float* __restrict__ ep,
+                                               const float (&bv)[TI][4]) {
   constexpr int EP = WQ + 8, LPR = WQ / 4, RPI = 64 / LPR;  // LDS row pitch; lanes per row, rows per store
   static_assert(WQ == 32 || WQ == 64, "row runs");
   const int P = a.P, grp = lane >> 4;
@@ -257,8 +280,6 @@ __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& p
   const int q = q0 + wq * WQ + 4 * (lane % LPR);
   const uint32_t n = fdiv((uint32_t)min(q, ph.Q - 1), ph.div_ohw);
   float* const yq = a.y + (int64_t)n * P * ohw + (q - (int)(n * ohw));
-  float bv[TI][4];
-  epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -269,7 +290,7 @@ __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& p
         for (int r2 = 0; r2 < 2; ++r2) {
           const int p = p0 + wp * WP + 16 * i + 4 * grp + 2 * h + r2;
           float v = acc[i][j][2 * h + r2];
-          if (a.bias && p < P) v += bv[i][2 * h + r2];
+          if (BIAS && p < P) v += bv[i][2 * h + r2];
           if (a.relu) v = fmaxf(v, 0.f);
           ep[(2 * grp + r2) * EP + 16 * j + (lane & 15)] = v;
         }
@@ -285,6 +306,17 @@ __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& p
       asm volatile("" ::: "memory");
       __builtin_amdgcn_wave_barrier();  // the next pass writes these rows
     }
+}
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                             int q0, int p0, int wp, int wq, int lane, float* __restrict__ ep) {
+  float bv[TI][4];
+  if (a.bias) {
+    epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
+    row_epilogue_b<TI, TJ, WP, WQ, true>(a, ph, acc, q0, p0, wp, wq, lane, ep, bv);
+  } else {
+    row_epilogue_b<TI, TJ, WP, WQ, false>(a, ph, acc, q0, p0, wp, wq, lane, ep, bv);
+  }
 }
 
 // One workgroup's tile (bx, by) of grid-z index bz (slice * nphase + phase); lds holds gather_lds_floats(). PF: K-blocks
