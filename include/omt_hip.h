@@ -13,6 +13,9 @@
  *    fallback, as the reference's NEED() does); any other non-zero status carries a message in omt_last_error().
  *  - Entry points that need scratch memory take a caller-provided workspace; its size comes from the matching
  *    *_workspace() query. The library never frees or retains caller pointers.
+ *  - Dense convolutions whose input or output reaches 2 GiB run as consecutive batch chunks below 2 GiB (the kernels'
+ *    offsets are 32-bit); plan and tuning calls on such a geometry act on its first chunk's. One image or a filter of
+ *    2 GiB or more is OMT_UNSUPPORTED.
  *  - Not thread-safe per stream: the caller serializes calls that share a stream (the reference serializes every op
  *    behind one recursive mutex, csrc/omt.h:62-64).
  *

@@ -1960,6 +1960,54 @@ static bool fits_i32(const omt_conv_geo* g) {
          g->co * g->ci * g->ks * g->ks * 4 <= kMaxBufBytes;
 }
 
+// ---- batches past 2 GiB ------------------------------------------------------------------------------------------
+//
+// A batch whose input or output reaches 2 GiB runs as consecutive batch chunks that each fit the 32-bit offsets (the
+// batch index is the outermost dimension in both memory formats, so a chunk is a contiguous run of images). Forward
+// and grad input convolve chunk by chunk; grad weight writes each chunk's filter gradient to the workspace and sums
+// the chunks in chunk order. One image and the filter must each stay below 2 GiB. Chunks are as equal as the batch
+// allows (at most two sizes: the first count - 1 chunks, then the last), and each runs under its own geometry's plan.
+struct Chunks {
+  int64_t count, size;  // count 1: the batch fits as it is; count 0: one image or the filter does not fit
+};
+static Chunks batch_chunks(const omt_conv_geo* g) {
+  if (fits_i32(g)) return {1, g->n};
+  const int64_t img = std::max(g->ci * g->ih * g->iw, g->co * g->oh * g->ow) * 4;
+  if (img > kMaxBufBytes || g->co * g->ci * g->ks * g->ks * 4 > kMaxBufBytes) return {0, 0};
+  const int64_t count = cdiv(g->n, kMaxBufBytes / img);
+  return {count, cdiv(g->n, count)};
+}
+static omt_conv_geo chunk_geo(const omt_conv_geo* g, const Chunks& c, int64_t i) {
+  omt_conv_geo r = *g;
+  r.n = std::min(c.size, g->n - i * c.size);
+  return r;
+}
+// The largest of the chunks' workspaces by `one`, the workspace of a geometry that fits (0 when nothing fits).
+template <class F>
+static size_t chunks_max(const omt_conv_geo* g, F one) {
+  const Chunks c = batch_chunks(g);
+  if (!c.count) return 0;
+  if (c.count == 1) return one(g);
+  const omt_conv_geo a = chunk_geo(g, c, 0), b = chunk_geo(g, c, c.count - 1);
+  return std::max(one(&a), one(&b));
+}
+// Runs one(chunk geometry, first image) over the chunks in order.
+template <class F>
+static int for_chunks(const omt_conv_geo* g, const Chunks& c, F one) {
+  for (int64_t i = 0; i < c.count; ++i) {
+    const omt_conv_geo cg = chunk_geo(g, c, i);
+    if (int st = one(&cg, i * c.size)) return st;
+  }
+  return OMT_OK;
+}
+// The geometry plans are kept and tuned under: the first chunk's when the batch is chunked.
+static const omt_conv_geo* plan_geo(const omt_conv_geo* g, omt_conv_geo& tmp) {
+  const Chunks c = batch_chunks(g);
+  if (c.count <= 1) return g;
+  tmp = chunk_geo(g, c, 0);
+  return &tmp;
+}
+
 // Wgrad split: about four waves of workgroups per CU over the tiles, each slice at least four K-blocks long.
 struct WgradPlan {
   int tile;
@@ -2059,22 +2107,23 @@ static size_t fwd_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
-OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
+static size_t fwd_workspace_one(const omt_conv_geo* g) {
   const GatherPlan pl = fwd_plan(g);
   const size_t part = pl.slices > 1 ? (size_t)(pl.slices * g->n * g->co * g->oh * g->ow) * sizeof(float) : 0;
   return part ? align256(fwd_pack_bytes(g, pl)) + part : fwd_pack_bytes(g, pl);
 }
 
-// The forward GEMM; with `unsummed` (no bias, epilogue or BN loader), a plan that splits K leaves its partials in the
-// workspace (*parts) and sets *unsummed to its slice count, else writes y and sets it to 1.
-static int conv_fwd_impl(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
-                         const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta,
-                         float bn_eps, float* y, void* workspace, size_t workspace_bytes, void* stream,
-                         const float** parts, int* unsummed) {
-  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd: null pointer");
-  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: geometry not covered (ks 1..11, stride 1..4, pad 0..ks)");
-  if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: a tensor of 2 GiB or more");
+OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) ? chunks_max(g, fwd_workspace_one) : 0;
+}
+
+// The forward GEMM over a batch that fits the 32-bit offsets; with `unsummed` (no bias, epilogue or BN loader), a plan
+// that splits K leaves its partials in the workspace (*parts) and sets *unsummed to its slice count, else writes y and
+// sets it to 1.
+static int conv_fwd_one(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
+                        const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta,
+                        float bn_eps, float* y, void* workspace, size_t workspace_bytes, void* stream,
+                        const float** parts, int* unsummed) {
   const bool bn = bn_mean || bn_var || bn_gamma || bn_beta;
   if (bn && !(bn_mean && bn_var && bn_gamma && bn_beta))
     return fail(OMT_INVALID, "omt_conv_fwd: BN loader needs mean, var, gamma and beta");
@@ -2137,6 +2186,26 @@ static int conv_fwd_impl(const omt_conv_geo* g, const float* x, const float* w, 
   float* part = (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl)));
   if (parts) *parts = part;
   return run_gather(a, pl, g->n, p.Q, part, s, unsummed);
+}
+
+// The forward GEMM, chunk by chunk past 2 GiB (a chunked batch is always summed: *unsummed 1).
+static int conv_fwd_impl(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
+                         const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta,
+                         float bn_eps, float* y, void* workspace, size_t workspace_bytes, void* stream,
+                         const float** parts, int* unsummed) {
+  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd: null pointer");
+  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: geometry not covered (ks 1..11, stride 1..4, pad 0..ks)");
+  const Chunks ch = batch_chunks(g);
+  if (!ch.count) return fail(OMT_UNSUPPORTED, "omt_conv_fwd: one image or the filter is 2 GiB or more");
+  if (ch.count == 1)
+    return conv_fwd_one(g, x, w, bias, epilogue, bn_mean, bn_var, bn_gamma, bn_beta, bn_eps, y, workspace,
+                        workspace_bytes, stream, parts, unsummed);
+  if (unsummed) *unsummed = 1;
+  const int64_t xi = g->ci * g->ih * g->iw, yi = g->co * g->oh * g->ow;
+  return for_chunks(g, ch, [&](const omt_conv_geo* c, int64_t n0) {
+    return conv_fwd_one(c, x + n0 * xi, w, bias, epilogue, bn_mean, bn_var, bn_gamma, bn_beta, bn_eps, y + n0 * yi,
+                        workspace, workspace_bytes, stream, nullptr, nullptr);
+  });
 }
 
 OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
@@ -2274,8 +2343,7 @@ static size_t dgrad_pack_bytes(const omt_conv_geo* g, const GatherPlan& pl) {
   return (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
-OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
+static size_t dgrad_workspace_one(const omt_conv_geo* g) {
   const GatherPlan pl = dgrad_plan(g);
   const size_t pack = dgrad_pack_bytes(g, pl);
   // the super-pixel form keeps its partials on the ceil(ih / s) x ceil(iw / s) grid, s^2 ci rows
@@ -2284,9 +2352,21 @@ OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
   return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * plane) * sizeof(float) : pack;
 }
 
+OMT_EXPORT size_t omt_conv_dgrad_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) ? chunks_max(g, dgrad_workspace_one) : 0;
+}
+
+// Geometry check of an entry point that runs whole batches only.
 static int geo_check(const omt_conv_geo* g, const char* fn) {
   if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", fn);
   if (!fits_i32(g)) return fail(OMT_UNSUPPORTED, "%s: a tensor of 2 GiB or more", fn);
+  return OMT_OK;
+}
+// Geometry check of an entry point that runs a batch past 2 GiB in chunks: the chunks (count 1: the whole batch).
+static int chunk_check(const omt_conv_geo* g, const char* fn, Chunks& c) {
+  if (!dense_geo_ok(g)) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", fn);
+  c = batch_chunks(g);
+  if (!c.count) return fail(OMT_UNSUPPORTED, "%s: one image or the filter is 2 GiB or more", fn);
   return OMT_OK;
 }
 
@@ -2364,24 +2444,39 @@ static int dgrad_prepare(const omt_conv_geo* g, const float* gy, const float* w,
 OMT_EXPORT int omt_conv_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
                               size_t workspace_bytes, void* stream) {
   if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad: null pointer");
-  if (int st = geo_check(g, "omt_conv_dgrad")) return st;
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_dgrad", ch)) return st;
   const size_t need = omt_conv_dgrad_workspace(g);
   if (need && (!workspace || workspace_bytes < need))
     return fail(OMT_INVALID, "omt_conv_dgrad: workspace of %zu bytes needed", need);
   hipStream_t s = stream_of(stream);
-  GatherArgs a;
-  GatherPlan pl;
-  int64_t maxq = 0;
-  float* part = nullptr;
-  if (int st = dgrad_prepare(g, gy, w, gx, workspace, s, a, pl, maxq, part)) return st;
-  return run_gather(a, pl, g->n, maxq, part, s);
+  const int64_t yi = g->co * g->oh * g->ow, xi = g->ci * g->ih * g->iw;
+  return for_chunks(g, ch, [&](const omt_conv_geo* c, int64_t n0) {
+    GatherArgs a;
+    GatherPlan pl;
+    int64_t maxq = 0;
+    float* part = nullptr;
+    if (int st = dgrad_prepare(c, gy + n0 * yi, w, gx + n0 * xi, workspace, s, a, pl, maxq, part)) return st;
+    return run_gather(a, pl, c->n, maxq, part, s);
+  });
 }
 
-OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g)) return 0;
+static size_t wgrad_workspace_one(const omt_conv_geo* g) {
   WgradPlan pl = wgrad_plan(g);
   if (pl.slices <= 1) return 0;
   return (size_t)(pl.slices * g->co * g->ci * g->ks * g->ks) * sizeof(float);
+}
+// Workspace of a grad weight over batch chunks: the chunks' filter gradients [count][filter], then, 256-byte aligned,
+// the largest workspace `one` gives a chunk.
+template <class F>
+static size_t wgrad_chunks_workspace(const omt_conv_geo* g, F one) {
+  const Chunks c = batch_chunks(g);
+  if (c.count <= 1) return c.count ? one(g) : 0;
+  return align256((size_t)(c.count * g->co * g->ci * g->ks * g->ks) * sizeof(float)) + chunks_max(g, one);
+}
+
+OMT_EXPORT size_t omt_conv_wgrad_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) ? wgrad_chunks_workspace(g, wgrad_workspace_one) : 0;
 }
 
 // Grad-weight launch arguments over `workspace` (of omt_conv_wgrad_workspace's size) and the launch's grid.
@@ -2422,17 +2517,21 @@ static bool wgrad_uses_tap_major(const omt_conv_geo* g, const WgradPlan& pl) {
   return g->ci % (kWgradTiles[pl.tile].bq / 4) == 0;
 }
 // The slice sum of a split grad-weight launch (blocks 0 if the plan does not split).
-static SplitSum wgrad_sum_of(const WgradArgs& a, const WgradPlan& pl, float* gw) {
+// The in-order sum of `slices` consecutive arrays of n floats at `part` (16-byte aligned) into `out`.
+static SplitSum split_sum_of(const float* part, float* out, int64_t n, int64_t slices) {
   SplitSum r{};
-  if (pl.slices <= 1) return r;
-  r.part = a.out;
-  r.out = gw;
-  r.n = (int64_t)a.P * a.Q;
-  r.slices = (int)pl.slices;
-  r.vec4 = r.n % 4 == 0 && (uintptr_t)gw % 16 == 0;
+  r.part = part;
+  r.out = out;
+  r.n = n;
+  r.slices = (int)slices;
+  r.vec4 = r.n % 4 == 0 && (uintptr_t)out % 16 == 0;
   const int64_t nv = r.vec4 ? r.n / 4 : r.n;
   r.blocks = r.slices >= kGroupSlices ? std::min<int64_t>(cdiv(nv, 16), 8192) : grid1d(nv, 256, 8192);
   return r;
+}
+static SplitSum wgrad_sum_of(const WgradArgs& a, const WgradPlan& pl, float* gw) {
+  if (pl.slices <= 1) return SplitSum{};
+  return split_sum_of(a.out, gw, (int64_t)a.P * a.Q, pl.slices);
 }
 static int launch_split_sum(const SplitSum& r, hipStream_t s) {
   if (!r.blocks) return OMT_OK;
@@ -2457,14 +2556,32 @@ static int run_wgrad(const omt_conv_geo* g, const float* x, const float* gy, flo
   return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
 }
 
+// Grad weight over batch chunks (more than one): one(chunk geometry, first image, filter gradient out, workspace) for
+// each chunk into the workspace's chunk gradients, then their sum in chunk order into gw.
+template <class F>
+static int wgrad_chunks(const omt_conv_geo* g, const Chunks& ch, float* gw, void* workspace, hipStream_t s, F one) {
+  const int64_t f = g->co * g->ci * g->ks * g->ks;
+  float* parts = (float*)workspace;
+  void* ws = (char*)workspace + align256((size_t)(ch.count * f) * sizeof(float));
+  if (int st = for_chunks(g, ch, [&](const omt_conv_geo* c, int64_t n0) { return one(c, n0, parts + n0 / ch.size * f, ws); }))
+    return st;
+  return launch_split_sum(split_sum_of(parts, gw, f, ch.count), s);
+}
+
 OMT_EXPORT int omt_conv_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
                               size_t workspace_bytes, void* stream) {
   if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad: null pointer");
-  if (int st = geo_check(g, "omt_conv_wgrad")) return st;
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_wgrad", ch)) return st;
   const size_t need = omt_conv_wgrad_workspace(g);
   if (need && (!workspace || workspace_bytes < need))
     return fail(OMT_INVALID, "omt_conv_wgrad: workspace of %zu bytes needed", need);
-  return run_wgrad(g, x, gy, gw, workspace, stream_of(stream));
+  hipStream_t s = stream_of(stream);
+  if (ch.count == 1) return run_wgrad(g, x, gy, gw, workspace, s);
+  const int64_t xi = g->ci * g->ih * g->iw, yi = g->co * g->oh * g->ow;
+  return wgrad_chunks(g, ch, gw, workspace, s, [&](const omt_conv_geo* c, int64_t n0, float* out, void* ws) {
+    return run_wgrad(c, x + n0 * xi, gy + n0 * yi, out, ws, s);
+  });
 }
 
 // ---- grad weight without allocation ------------------------------------------------------------------------------
@@ -2522,23 +2639,21 @@ static bool dual_tiles(const GatherPlan& dp, const WgradPlan& wp) {
          wt.bq == 64 && wt.wp == 32 && wt.wq == 32;
 }
 
-OMT_EXPORT size_t omt_conv_bwd_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g) || !fits_i32(g)) return 0;
-  const size_t d = omt_conv_dgrad_workspace(g), w = omt_conv_wgrad_workspace(g);
+static size_t bwd_workspace_one(const omt_conv_geo* g) {
+  const size_t d = dgrad_workspace_one(g), w = wgrad_workspace_one(g);
   return w ? align256(d) + w : d;
 }
 
-OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx,
-                            float* gw, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!g || !x || !gy || !w || !gx || !gw) return fail(OMT_INVALID, "omt_conv_bwd: null pointer");
-  if (int st = geo_check(g, "omt_conv_bwd")) return st;
-  const size_t need = omt_conv_bwd_workspace(g);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(OMT_INVALID, "omt_conv_bwd: workspace of %zu bytes needed", need);
-  const size_t dbytes = omt_conv_dgrad_workspace(g);
+OMT_EXPORT size_t omt_conv_bwd_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) ? wgrad_chunks_workspace(g, bwd_workspace_one) : 0;
+}
+
+// Grad input and grad weight of a batch that fits the 32-bit offsets, over a workspace of bwd_workspace_one's size.
+static int conv_bwd_one(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx, float* gw,
+                        void* workspace, hipStream_t s) {
+  const size_t dbytes = dgrad_workspace_one(g);
   void* dws = dbytes ? workspace : nullptr;
-  void* wws = omt_conv_wgrad_workspace(g) ? (char*)workspace + align256(dbytes) : nullptr;
-  hipStream_t s = stream_of(stream);
+  void* wws = wgrad_workspace_one(g) ? (char*)workspace + align256(dbytes) : nullptr;
   GatherArgs ga;
   GatherPlan dp;
   int64_t maxq = 0;
@@ -2601,6 +2716,22 @@ OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* 
   return launch_check("dual_reduce_kernel");
 }
 
+OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx,
+                            float* gw, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !w || !gx || !gw) return fail(OMT_INVALID, "omt_conv_bwd: null pointer");
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_bwd", ch)) return st;
+  const size_t need = omt_conv_bwd_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_bwd: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  if (ch.count == 1) return conv_bwd_one(g, x, gy, w, gx, gw, workspace, s);
+  const int64_t xi = g->ci * g->ih * g->iw, yi = g->co * g->oh * g->ow;
+  return wgrad_chunks(g, ch, gw, workspace, s, [&](const omt_conv_geo* c, int64_t n0, float* out, void* ws) {
+    return conv_bwd_one(c, x + n0 * xi, gy + n0 * yi, w, gx + n0 * xi, out, ws, s);
+  });
+}
+
 // ---- channels-last (NHWC) convolution --------------------------------------------------------------------------
 //
 // The same three GEMMs over channels-last tensors: x [n][ih][iw][ci], y / gy [n][oh][ow][co], filter and filter
@@ -2645,21 +2776,17 @@ static int run_gather_nhwc(GatherArgs& a, const GatherPlan& pl, int64_t n, int64
   return launch_gather_sum(gather_sum_of(a, pl), s);
 }
 
-OMT_EXPORT size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g) || !fits_i32(g) || !nhwc_fwd_ok(g)) return 0;
+static size_t fwd_nhwc_workspace_one(const omt_conv_geo* g) {
   const GatherPlan pl = fwd_nhwc_plan(g);
   return pl.slices > 1 ? (size_t)(pl.slices * g->n * g->co * g->oh * g->ow) * sizeof(float) : 0;
 }
 
-OMT_EXPORT int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
-                                 unsigned epilogue, float* y, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: null pointer");
-  if (int st = geo_check(g, "omt_conv_fwd_nhwc")) return st;
-  if (!nhwc_fwd_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_nhwc: input channels not a multiple of 16");
-  if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: bias epilogue without bias");
-  const size_t need = omt_conv_fwd_nhwc_workspace(g);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(OMT_INVALID, "omt_conv_fwd_nhwc: workspace of %zu bytes needed", need);
+OMT_EXPORT size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) && nhwc_fwd_ok(g) ? chunks_max(g, fwd_nhwc_workspace_one) : 0;
+}
+
+static int conv_fwd_nhwc_one(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
+                             unsigned epilogue, float* y, void* workspace, hipStream_t s) {
   const GatherPlan pl = fwd_nhwc_plan(g);
   GatherArgs a{};
   a.x = x;
@@ -2690,27 +2817,40 @@ OMT_EXPORT int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const fl
   p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   p.div_kw = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather_nhwc(a, pl, g->n, p.Q, (float*)workspace, stream_of(stream));
+  return run_gather_nhwc(a, pl, g->n, p.Q, (float*)workspace, s);
+}
+
+OMT_EXPORT int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
+                                 unsigned epilogue, float* y, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: null pointer");
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_fwd_nhwc", ch)) return st;
+  if (!nhwc_fwd_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_nhwc: input channels not a multiple of 16");
+  if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: bias epilogue without bias");
+  const size_t need = omt_conv_fwd_nhwc_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_fwd_nhwc: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  const int64_t xi = g->ci * g->ih * g->iw, yi = g->co * g->oh * g->ow;
+  return for_chunks(g, ch, [&](const omt_conv_geo* c, int64_t n0) {
+    return conv_fwd_nhwc_one(c, x + n0 * xi, w, bias, epilogue, y + n0 * yi, workspace, s);
+  });
 }
 
 // Grad-input workspace: the per-phase filters W'[ci][a'][b'][co] (all of the filter's elements), then, 256-byte
 // aligned, any split-K partials [slices][n][ih][iw][ci].
-OMT_EXPORT size_t omt_conv_dgrad_nhwc_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g) || !fits_i32(g) || !nhwc_dgrad_ok(g)) return 0;
+static size_t dgrad_nhwc_workspace_one(const omt_conv_geo* g) {
   const GatherPlan pl = dgrad_nhwc_plan(g);
   const size_t pack = (size_t)(g->co * g->ci * g->ks * g->ks) * sizeof(float);
   return pl.slices > 1 ? align256(pack) + (size_t)(pl.slices * g->n * g->ci * g->ih * g->iw) * sizeof(float) : pack;
 }
 
-OMT_EXPORT int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: null pointer");
-  if (int st = geo_check(g, "omt_conv_dgrad_nhwc")) return st;
-  if (!nhwc_dgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad_nhwc: output channels not a multiple of 16");
-  const size_t need = omt_conv_dgrad_nhwc_workspace(g);
-  if (!workspace || workspace_bytes < need)
-    return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: workspace of %zu bytes needed", need);
-  hipStream_t s = stream_of(stream);
+OMT_EXPORT size_t omt_conv_dgrad_nhwc_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) && nhwc_dgrad_ok(g) ? chunks_max(g, dgrad_nhwc_workspace_one) : 0;
+}
+
+static int conv_dgrad_nhwc_one(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                               hipStream_t s) {
   GatherArgs a{};
   PackArgs pk{};
   int64_t maxq = 0;
@@ -2742,27 +2882,56 @@ OMT_EXPORT int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const
   return run_gather_nhwc(a, pl, g->n, maxq, part, s);
 }
 
-OMT_EXPORT size_t omt_conv_wgrad_nhwc_workspace(const omt_conv_geo* g) {
-  if (!g || !dense_geo_ok(g) || !nhwc_wgrad_ok(g)) return 0;
+OMT_EXPORT int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: null pointer");
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_dgrad_nhwc", ch)) return st;
+  if (!nhwc_dgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad_nhwc: output channels not a multiple of 16");
+  const size_t need = omt_conv_dgrad_nhwc_workspace(g);
+  if (!workspace || workspace_bytes < need)
+    return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  const int64_t yi = g->co * g->oh * g->ow, xi = g->ci * g->ih * g->iw;
+  return for_chunks(g, ch, [&](const omt_conv_geo* c, int64_t n0) {
+    return conv_dgrad_nhwc_one(c, gy + n0 * yi, w, gx + n0 * xi, workspace, s);
+  });
+}
+
+static size_t wgrad_nhwc_workspace_one(const omt_conv_geo* g) {
   const WgradPlan pl = wgrad_plan(g, OMT_DIR_WGRAD_NHWC);
   return pl.slices > 1 ? (size_t)(pl.slices * g->co * g->ci * g->ks * g->ks) * sizeof(float) : 0;
 }
 
-OMT_EXPORT int omt_conv_wgrad_nhwc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: null pointer");
-  if (int st = geo_check(g, "omt_conv_wgrad_nhwc")) return st;
-  if (!nhwc_wgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad_nhwc: channels not multiples of 4");
-  const size_t need = omt_conv_wgrad_nhwc_workspace(g);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: workspace of %zu bytes needed", need);
-  hipStream_t s = stream_of(stream);
+OMT_EXPORT size_t omt_conv_wgrad_nhwc_workspace(const omt_conv_geo* g) {
+  return g && dense_geo_ok(g) && nhwc_wgrad_ok(g) ? wgrad_chunks_workspace(g, wgrad_nhwc_workspace_one) : 0;
+}
+
+static int conv_wgrad_nhwc_one(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                               hipStream_t s) {
   WgradArgs a;
   WgradPlan pl;
   const dim3 grid = wgrad_prepare(g, x, gy, gw, workspace, a, pl, OMT_DIR_WGRAD_NHWC);
   wgrad_nhwc_dispatch(pl.tile, a, grid, s);
   if (int st = launch_check("conv_wgrad_nhwc_kernel")) return st;
   return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
+}
+
+OMT_EXPORT int omt_conv_wgrad_nhwc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: null pointer");
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_wgrad_nhwc", ch)) return st;
+  if (!nhwc_wgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad_nhwc: channels not multiples of 4");
+  const size_t need = omt_conv_wgrad_nhwc_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  if (ch.count == 1) return conv_wgrad_nhwc_one(g, x, gy, gw, workspace, s);
+  const int64_t xi = g->ci * g->ih * g->iw, yi = g->co * g->oh * g->ow;
+  return wgrad_chunks(g, ch, gw, workspace, s, [&](const omt_conv_geo* c, int64_t n0, float* out, void* ws) {
+    return conv_wgrad_nhwc_one(c, x + n0 * xi, gy + n0 * yi, out, ws, s);
+  });
 }
 
 OMT_EXPORT int omt_bias_grad(int64_t n, int64_t c, int64_t hw, const float* gy, float* gb, void* stream) {
@@ -2791,10 +2960,13 @@ OMT_EXPORT int omt_fold_bn(int64_t co, int64_t per_out, const float* cw, const f
 
 // ---- plan cache and tuning --------------------------------------------------------------------------------------
 
-static int plan_args_ok(int dir, const omt_conv_geo* g, const char* what) {
+// Checks a plan call's arguments and points g at the geometry its plans are kept under (for a batch past 2 GiB, the
+// first chunk's, in `tmp`).
+static int plan_args_ok(int dir, const omt_conv_geo*& g, omt_conv_geo& tmp, const char* what) {
   if (!g) return fail(OMT_INVALID, "%s: null geometry", what);
   if (dir < OMT_DIR_FWD || dir > OMT_DIR_WGRAD_NHWC) return fail(OMT_INVALID, "%s: direction %d", what, dir);
-  if (!dense_geo_ok(g) || !fits_i32(g)) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", what);
+  if (!dense_geo_ok(g) || !batch_chunks(g).count) return fail(OMT_UNSUPPORTED, "%s: geometry not covered", what);
+  g = plan_geo(g, tmp);
   return OMT_OK;
 }
 
@@ -2803,7 +2975,8 @@ OMT_EXPORT int omt_conv_num_tiles(int dir) {
 }
 
 OMT_EXPORT int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* plan, int* cached) {
-  if (int st = plan_args_ok(dir, g, "omt_conv_get_plan")) return st;
+  omt_conv_geo tmp;
+  if (int st = plan_args_ok(dir, g, tmp, "omt_conv_get_plan")) return st;
   if (!plan) return fail(OMT_INVALID, "omt_conv_get_plan: null plan");
   omt_conv_plan cp;
   if (cached) *cached = cached_plan(dir, g, &cp) ? 1 : 0;
@@ -2821,7 +2994,8 @@ OMT_EXPORT int omt_conv_get_plan(int dir, const omt_conv_geo* g, omt_conv_plan* 
 }
 
 OMT_EXPORT int omt_conv_set_plan(int dir, const omt_conv_geo* g, const omt_conv_plan* plan) {
-  if (int st = plan_args_ok(dir, g, "omt_conv_set_plan")) return st;
+  omt_conv_geo tmp;
+  if (int st = plan_args_ok(dir, g, tmp, "omt_conv_set_plan")) return st;
   std::lock_guard<std::mutex> lk(g_plan_mu);
   if (!plan) {
     g_plans.erase(key_of(dir, g));
@@ -3039,7 +3213,8 @@ int refuse_capture(hipStream_t s, const char* what) {
 }  // namespace
 
 OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* best) {
-  if (int st = plan_args_ok(dir, g, "omt_conv_autotune")) return st;
+  omt_conv_geo tmp;
+  if (int st = plan_args_ok(dir, g, tmp, "omt_conv_autotune")) return st;
   if (forcing()) return fail(OMT_INVALID, "omt_conv_autotune: re-entered");
   hipStream_t s = stream_of(stream);
   if (int st = refuse_capture(s, "omt_conv_autotune")) return st;
@@ -3094,7 +3269,8 @@ OMT_EXPORT int omt_conv_autotune(int dir, const omt_conv_geo* g, int max_tiles, 
 
 OMT_EXPORT int omt_conv_autotune_bwd(const omt_conv_geo* g, int max_tiles, void* stream, omt_conv_plan* dgrad_best,
                                      omt_conv_plan* wgrad_best) {
-  if (int st = plan_args_ok(OMT_DIR_DGRAD, g, "omt_conv_autotune_bwd")) return st;
+  omt_conv_geo tmp;
+  if (int st = plan_args_ok(OMT_DIR_DGRAD, g, tmp, "omt_conv_autotune_bwd")) return st;
   if (forcing()) return fail(OMT_INVALID, "omt_conv_autotune_bwd: re-entered");
   hipStream_t s = stream_of(stream);
   if (int st = refuse_capture(s, "omt_conv_autotune_bwd")) return st;

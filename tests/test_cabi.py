@@ -114,6 +114,57 @@ def test_host_validation_statuses():
         _lib.check(_lib.OMT_UNSUPPORTED)
 
 
+def test_batch_chunks_host_side():
+    """A batch past 2 GiB (3 images of 876 MB in and out) is planned as batch chunks of 2 images, then 1: plan calls
+    on it act on the first chunk's geometry, its workspaces are the larger chunk's (grad weight: plus the chunks'
+    filter gradients, 256-byte aligned), and one image or a filter of 2 GiB or more is OMT_UNSUPPORTED with no
+    workspace, all without a GPU."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    L.omt_conv_clear_plans()
+    big, two, one = (_lib.conv_geo(n, 16, 16, 3700, 3700, 3, 1, 1) for n in (3, 2, 1))
+
+    def plan(d, g):
+        p, c = _lib.ConvPlan(), ctypes.c_int32()
+        assert L.omt_conv_get_plan(d, ctypes.byref(g), ctypes.byref(p), ctypes.byref(c)) == _lib.OMT_OK
+        return p.tile, p.slices, c.value
+
+    try:
+        for d in (_lib.OMT_DIR_FWD, _lib.OMT_DIR_DGRAD, _lib.OMT_DIR_WGRAD, _lib.OMT_DIR_FWD_NHWC):
+            assert plan(d, big) == plan(d, two), d
+        # a plan set on the whole batch is the first chunk's
+        assert L.omt_conv_set_plan(_lib.OMT_DIR_WGRAD, ctypes.byref(big), ctypes.byref(_lib.ConvPlan(2, 3))) == \
+            _lib.OMT_OK
+        assert plan(_lib.OMT_DIR_WGRAD, two) == (2, 3, 1)
+        ws1 = L.omt_conv_wgrad_workspace(ctypes.byref(one))
+        ws2 = L.omt_conv_wgrad_workspace(ctypes.byref(two))
+        assert ws2 == 3 * 16 * 16 * 9 * 4
+        filt = (2 * 16 * 16 * 9 * 4 + 255) // 256 * 256
+        assert L.omt_conv_wgrad_workspace(ctypes.byref(big)) == filt + max(ws1, ws2)
+        assert L.omt_conv_bwd_workspace(ctypes.byref(big)) == filt + max(L.omt_conv_bwd_workspace(ctypes.byref(g))
+                                                                          for g in (one, two))
+        for ws in (L.omt_conv_fwd_workspace, L.omt_conv_dgrad_workspace, L.omt_conv_fwd_nhwc_workspace,
+                   L.omt_conv_dgrad_nhwc_workspace):
+            assert ws(ctypes.byref(big)) == max(ws(ctypes.byref(one)), ws(ctypes.byref(two))), ws
+        # the whole-batch check of the entry points accepts it (a missing workspace is the next error)
+        assert L.omt_conv_wgrad(ctypes.byref(big), fake, fake, fake, None, 0, None) == _lib.OMT_INVALID
+        assert b"workspace" in L.omt_last_error()
+        # no chunk fits: one image of 4.5 GB, or a 2.4 GB filter
+        for g in (_lib.conv_geo(2, 64, 64, 4200, 4200, 3, 1, 1), _lib.conv_geo(2, 8192, 8192, 8, 8, 3, 1, 1)):
+            assert L.omt_conv_fwd_workspace(ctypes.byref(g)) == 0
+            assert L.omt_conv_wgrad_workspace(ctypes.byref(g)) == 0
+            assert L.omt_conv_fwd(ctypes.byref(g), fake, fake, None, 0, None, None, None, None, 1e-5, fake, None, 0,
+                                  None) == _lib.OMT_UNSUPPORTED
+            assert b"2 GiB" in L.omt_last_error()
+            assert L.omt_conv_bwd(ctypes.byref(g), fake, fake, fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
+            p = _lib.ConvPlan()
+            assert L.omt_conv_get_plan(_lib.OMT_DIR_FWD, ctypes.byref(g), ctypes.byref(p), None) == \
+                _lib.OMT_UNSUPPORTED
+    finally:
+        L.omt_conv_clear_plans()
+
+
 def test_plan_cache_host_side():
     """The plan cache (tile, K slices per direction and geometry; reference conv_plan / tune_dump / tune_load,
     csrc/conv.cpp:45-60, 243-272) and the cost model's split choice, all host-side."""

@@ -375,6 +375,34 @@ def test_graph_replay_of_a_training_step(clean):
     graph.release()
 
 
+def test_conv_batch_past_2gib_stays_on_hip_kernels(clean):
+    """A convolution whose input and output pass 2 GiB (3 x 16 x 3700^2 float32: 2.6 GB each) runs forward and
+    backward through autograd on the HIP kernels in batch chunks: no FALLBACKS entry, nothing delegated, and the same
+    results as the C-ABI calls (whose chunked results the parity tests pin to the oracle)."""
+    omt = clean
+    from omarchy_mac_torch import hip_ops
+    n, c, h = 3, 16, 3700
+    omt._native.core.count_delegated(True)
+    try:
+        tx = torch.randn(n, c, h, h, device=omt.DEVICE).requires_grad_()
+        tw = (torch.randn(c, c, 3, 3, device=omt.DEVICE) * (c * 9) ** -0.5).requires_grad_()
+        tb = torch.randn(c, device=omt.DEVICE).requires_grad_()
+        gy = torch.randn(n, c, h, h, device=omt.DEVICE)
+        print(f"device conv {tuple(tx.shape)}", flush=True)
+        y = F.conv2d(tx, tw, tb, 1, 1)
+        y.backward(gy)
+        delegated = omt._native.core.delegated_counts()
+        assert not any(k.startswith("convolution") for k in delegated), delegated
+        assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
+    finally:
+        omt._native.core.count_delegated(False)
+    cx, cw, cb, cgy = (t.detach().to("cuda") for t in (tx, tw, tb, gy))
+    ry = hip_ops.conv2d(cx, cw, cb, 1, 1)
+    rgx, rgw = hip_ops.conv2d_bwd(cx, cgy, cw, 1, 1)
+    for got, ref in ((y, ry), (tx.grad, rgx), (tw.grad, rgw), (tb.grad, cgy.sum((0, 2, 3)))):
+        assert rel(got, ref) <= TOL
+
+
 def test_uncovered_conv_falls_back_and_is_recorded(clean):
     omt = clean
     x, w = torch.randn(2, 4, 11, 11), torch.randn(6, 4, 3, 3)

@@ -488,6 +488,66 @@ def test_conv_full_size(cuda, ops, name, shape, mode):
     assert orc.rel_l2(host(gw).ravel()[pts], ref) <= TOL, case
 
 
+def test_conv_batch_past_2gib_runs_in_chunks(cuda, ops):
+    """A batch whose input and output pass 2 GiB (3 images of 876 MB: the kernels' offsets are 32-bit) runs on the
+    HIP kernels as batch chunks of 2 images, then 1. Forward and grad input are bit-identical to the chunks convolved
+    one by one; grad weight (alone and through the one-call backward) to the in-order sum of the chunks' filter
+    gradients; the channels-last entry points likewise. Checked against the oracle at sampled points of every image
+    and by the float64 adjoint identity."""
+    n, c, h, ks, s, p = 3, 16, 3700, 3, 1, 1
+    xs, ws = (n, c, h, h), (c, c, ks, ks)
+    assert n * c * h * h * 4 >= 2**31 and 2 * c * h * h * 4 < 2**31
+    chunks = ((0, 2), (2, 3))
+    assert ops.conv_plan("fwd", xs, ws, s, p)[:2] == ops.conv_plan("fwd", (2, c, h, h), ws, s, p)[:2]
+    gen = torch.Generator(device=cuda).manual_seed(3)
+    x = torch.randn(xs, device=cuda, generator=gen)
+    wt = torch.randn(ws, device=cuda, generator=gen) * (c * ks * ks) ** -0.5
+    gy = torch.randn(xs, device=cuda, generator=gen)
+    print(f"chunked conv {xs} x {ws}", flush=True)
+    y = ops.conv2d(x, wt, None, s, p)
+    gx = ops.conv2d_dgrad(gy, wt, xs, s, p)
+    gw = ops.conv2d_wgrad(x, gy, ks, s, p)
+    gx2, gw2 = ops.conv2d_bwd(x, gy, wt, s, p)
+    gws = []
+    for a, b in chunks:
+        assert torch.equal(y[a:b], ops.conv2d(x[a:b], wt, None, s, p)), (a, b)
+        assert torch.equal(gx[a:b], ops.conv2d_dgrad(gy[a:b], wt, (b - a, c, h, h), s, p)), (a, b)
+        gws.append(ops.conv2d_wgrad(x[a:b], gy[a:b], ks, s, p))
+    assert torch.equal(gw, gws[0] + gws[1])
+    gxb, gwb = zip(*(ops.conv2d_bwd(x[a:b], gy[a:b], wt, s, p) for a, b in chunks))
+    assert torch.equal(gx2, torch.cat(gxb)) and torch.equal(gw2, gwb[0] + gwb[1])
+    # adjoint identity in float64
+    a1 = (y.double() * gy.double()).sum().item()
+    a2 = (x.double() * gx.double()).sum().item()
+    a3 = (wt.double() * gw.double()).sum().item()
+    norm = (y.double().norm() * gy.double().norm()).item()
+    assert abs(a1 - a2) <= 1e-5 * norm and abs(a1 - a3) <= 1e-5 * norm, (a1, a2, a3, norm)
+    # the oracle at points of every image (and the first and last element)
+    rng = np.random.default_rng(7)
+    xh, wh, gyh = host(x), host(wt), host(gy)
+    per = c * h * h
+    pts = np.concatenate([[0, n * per - 1], rng.integers(0, per, 3 * 256) + np.repeat(np.arange(n) * per, 256)])
+    assert orc.rel_l2(host(y).ravel()[pts], orc.conv_fwd_points(xh, wh, pts, None, s, p)) <= TOL
+    assert orc.rel_l2(host(gx).ravel()[pts], orc.conv_dgrad_points(gyh, wh, xs, pts, s, p)) <= TOL
+    wpts = rng.integers(0, gw.numel(), 24)
+    assert orc.rel_l2(host(gw).ravel()[wpts], orc.conv_wgrad_points(xh, gyh, ks, wpts, s, p)) <= TOL
+    del xh, gyh
+    # channels-last: chunks of the same images, against the NCHW results
+    xc, wc, gyc = (t.contiguous(memory_format=torch.channels_last) for t in (x, wt, gy))
+    del gx2, gxb
+    yc = ops.conv2d_nhwc(xc, wc, None, s, p)
+    gxc = ops.conv2d_dgrad_nhwc(gyc, wc, xs, s, p)
+    gwc = ops.conv2d_wgrad_nhwc(xc, gyc, ks, s, p)
+    gwcs = []
+    for a, b in chunks:
+        assert torch.equal(yc[a:b], ops.conv2d_nhwc(xc[a:b], wc, None, s, p)), (a, b)
+        assert torch.equal(gxc[a:b], ops.conv2d_dgrad_nhwc(gyc[a:b], wc, (b - a, c, h, h), s, p)), (a, b)
+        gwcs.append(ops.conv2d_wgrad_nhwc(xc[a:b], gyc[a:b], ks, s, p))
+    assert torch.equal(gwc, gwcs[0] + gwcs[1])
+    for got, ref in ((yc, y), (gxc, gx), (gwc, gw)):
+        assert orc.rel_l2(host(got.contiguous()), host(ref)) <= TOL
+
+
 # ---- depthwise ----
 
 DW = [(3, 1, 1), (5, 1, 2), (7, 1, 3), (3, 2, 1), (5, 2, 0), (11, 4, 5), (2, 3, 1), (9, 1, 0)]
