@@ -456,20 +456,18 @@ __global__ void __launch_bounds__(256) dw_s1_reg_kernel(const float* __restrict_
 // channel ch. Each thread takes 4-column x RB-row blocks of gy in turn (stride NT over the slice's blocks), loads the
 // block and the input window it meets (as the forward kernel does: no LDS, zero padding from the buffer range check)
 // and accumulates all KS^2 taps in registers; the taps are then summed over the workgroup (wave_sum, then the waves
-// in order). One slice writes gw; several write part[slice][ch] and the channel's last workgroup to finish sums the
-// slices in order into gw (split_arrive). A fixed thread-to-block map and fixed sum orders make the result
-// deterministic.
+// in order). One slice writes gw; several write part[slice][ch], summed in slice order by dw_wgrad_reduce_kernel. A
+// fixed thread-to-block map and fixed sum orders make the result deterministic.
 struct DwRegW {
   int ipw, CG, nrb, slices;  // images per slice, column groups W / 4, row blocks, slices
   int rb, nt;                // rows per block, threads per workgroup
-  uint32_t bytes, tag;       // bytes of x (and gy), below 2^31; the call's split tag
+  uint32_t bytes;            // bytes of x (and gy), below 2^31
   FastDiv div_img, div_cg;   // blocks per image (nrb * CG), CG
 };
 template <int KS, int RB, int NT>
 __global__ void __launch_bounds__(NT) dw_wgrad_reg_kernel(const float* __restrict__ x, const float* __restrict__ gy,
-                                                           float* __restrict__ gw, float* __restrict__ part,
-                                                           unsigned long long* __restrict__ slots, int N, int C, int H,
-                                                           int W, const DwRegW d) {
+                                                           float* __restrict__ gw, float* __restrict__ part, int N,
+                                                           int C, int H, int W, const DwRegW d) {
   constexpr int PAD = KS / 2, KK = KS * KS, NR = RB + KS - 1, NC = 4 + 2 * PAD, NW = NT / 64;
   __shared__ float red[NW][KK];
   const int ch = blockIdx.x, sl = blockIdx.y;
@@ -521,12 +519,6 @@ __global__ void __launch_bounds__(NT) dw_wgrad_reg_kernel(const float* __restric
     return;
   }
   if (k < KK) part[((int64_t)sl * C + ch) * KK + k] = t;
-  if (!split_arrive(slots + ch, d.tag, (uint32_t)d.slices)) return;
-  if (k < KK) {
-    float s = 0.f;
-    for (int j = 0; j < d.slices; ++j) s += part[((int64_t)j * C + ch) * KK + k];
-    gw[ch * KK + k] = s;
-  }
 }
 
 // Grad-weight work of one channel: units u = (image u / chunks, row chunk u % chunks), N * chunks of them. A
@@ -725,19 +717,22 @@ static bool dw_reg_ok(const omt_conv_geo* g) {
   return g->iw % 4 == 0 && g->n * g->ci * g->ih * g->iw * 4 <= kMaxBufBytes && g->ci * g->ks * g->ks * 4 <= kMaxBufBytes;
 }
 
-// The register-blocked grad weight. Slices of images give up to about kDwRegWgs workgroups (a workgroup per channel
-// leaves most CUs idle when there are few channels), but no more slices than keep 1024 blocks of 4 rows in each (every
-// slice costs a device-scope release and each channel's last one an acquire, both whole-cache operations; measured at
-// b32: dw 3x3 over 72 x 56^2 in 1 / 2 / 4 / 11 slices 24.1 / 18.0 / 23.2 / 38.5 us, dw 5x5 over 96 x 28^2 in 1 / 2 / 3
-// slices 12.1 / 14.4 / 19.1 us). Workgroups of 1024 threads when a slice has that many blocks of 4 rows, or of 2 rows
+// The register-blocked grad weight: slices of images of about kDwRegUnits blocks each (a workgroup per channel
+// leaves most CUs idle when there are few channels), at most kDwRegWgs workgroups, summed by a second launch (an
+// in-kernel last-arrival sum costs a device-scope release per workgroup, whole-cache write-backs that serialize:
+// measured at b32, dw 3x3 over 72 x 56^2 in 2 / 4 slices 21 / 21 us against 20 / 18 us with the second launch).
+// Graph replays at b32 (one slice, 1024 threads -> this split, 256 threads): dw 3x3 over 72 x 56^2 17.8 -> 13.8 us,
+// 16 x 56^2 14.2 -> 6.4 us, 88 x 28^2 8.3 -> 6.8 us; dw 5x5 over 96 x 28^2 12.1 -> 10.3 us; b128 dw 3x3 over
+// 32 x 28^2 16.0 -> 8.7 us. Workgroups of 1024 threads when a slice still has 1024 blocks of 4 rows, or of 2 rows
 // (more waves per CU keep more loads in flight); else 256 threads.
-constexpr int kDwRegWgs = 128;
+constexpr int kDwRegUnits = 196, kDwRegWgs = 1280;
 static DwRegW dw_wreg(const omt_conv_geo* g) {
   DwRegW d{};
   const int ks = (int)g->ks;
   d.CG = (int)(g->iw / 4);
-  const int64_t blocks4 = g->n * cdiv(g->ih, dw_reg_rows(ks)) * d.CG;
-  const int64_t slices = std::min<int64_t>({g->n, cdiv(kDwRegWgs, g->ci), std::max<int64_t>(1, blocks4 / 1024)});
+  const int64_t per_img = cdiv(g->ih, dw_reg_rows(ks)) * d.CG;
+  const int64_t slices = std::max<int64_t>(
+      1, std::min<int64_t>({g->n, cdiv(g->n * per_img, kDwRegUnits), kDwRegWgs / g->ci}));
   d.ipw = (int)cdiv(g->n, slices);
   d.slices = (int)cdiv(g->n, d.ipw);
   auto units = [&](int rb) { return (int64_t)d.ipw * cdiv(g->ih, rb) * d.CG; };
@@ -754,13 +749,10 @@ static DwRegW dw_wreg(const omt_conv_geo* g) {
   d.div_cg = make_fastdiv((uint32_t)d.CG);
   return d;
 }
-// partials [slices][C][ks^2] floats, then C arrival slots (8-byte aligned); nothing for one slice
-static size_t dw_wreg_part_bytes(const omt_conv_geo* g, const DwRegW& d) {
-  return (size_t)cdiv((int64_t)d.slices * g->ci * g->ks * g->ks * 4, 8) * 8;
-}
+// partials [slices][C][ks^2] floats; nothing for one slice
 static size_t dw_wreg_workspace(const omt_conv_geo* g) {
   const DwRegW d = dw_wreg(g);
-  return d.slices == 1 ? 0 : dw_wreg_part_bytes(g, d) + (size_t)g->ci * 8;
+  return d.slices == 1 ? 0 : (size_t)(d.slices * g->ci * g->ks * g->ks) * sizeof(float);
 }
 
 static int64_t dw_s1_groups(const omt_conv_geo* g) {
@@ -902,16 +894,13 @@ OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* 
     return fail(OMT_INVALID, "omt_dw_wgrad: workspace of %zu bytes needed", need);
   hipStream_t s = stream_of(stream);
   if (dw_s1(g) && dw_reg_ok(g)) {
-    DwRegW d = dw_wreg(g);
-    d.tag = split_tag();
+    const DwRegW d = dw_wreg(g);
     const int ks = (int)g->ks;
     const int N = (int)g->n, C = (int)g->ci, H = (int)g->ih, W = (int)g->iw;
     float* part = (float*)workspace;
-    unsigned long long* slots =
-        d.slices == 1 ? nullptr : (unsigned long long*)((char*)workspace + dw_wreg_part_bytes(g, d));
     const dim3 grid((unsigned)g->ci, (unsigned)d.slices);
 #define OMT_DW_WR(KS_, RB_, NT_) \
-  hipLaunchKernelGGL((dw_wgrad_reg_kernel<KS_, RB_, NT_>), grid, dim3(NT_), 0, s, x, gy, gw, part, slots, N, C, H, W, d)
+  hipLaunchKernelGGL((dw_wgrad_reg_kernel<KS_, RB_, NT_>), grid, dim3(NT_), 0, s, x, gy, gw, part, N, C, H, W, d)
 #define OMT_DW_WR_KS(KS_)                                   \
   if (d.nt == 256) OMT_DW_WR(KS_, (KS_ == 7 ? 2 : 4), 256); \
   else if (d.rb == 2) OMT_DW_WR(KS_, 2, 1024);              \
@@ -925,7 +914,12 @@ OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* 
     }
 #undef OMT_DW_WR_KS
 #undef OMT_DW_WR
-    return launch_check("dw_wgrad_reg_kernel");
+    if (int st = launch_check("dw_wgrad_reg_kernel")) return st;
+    if (d.slices == 1) return OMT_OK;
+    const int n = (int)(g->ci * ks * ks);
+    hipLaunchKernelGGL(dw_wgrad_reduce_kernel, dim3(grid1d(n, 256, 4096)), dim3(256), 0, s, (const float*)part, gw,
+                       n, d.slices);
+    return launch_check("dw_wgrad_reduce_kernel");
   }
   if (dw_s1_wgrad(g)) {
     const int nt = dw_threads(g), ks = (int)g->ks;

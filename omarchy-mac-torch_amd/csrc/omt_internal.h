@@ -88,40 +88,6 @@ __device__ __forceinline__ float wave_sum(float v) {
           __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 
-// Split reductions without a second launch. Each workgroup of a split writes its partial result to the workspace and
-// then counts its arrival in a 64-bit slot of the workspace (high word: the call's tag from split_tag(), low word: the
-// arrivals so far; a slot whose high word is not the tag holds other data and counts as zero). The last workgroup to
-// arrive returns true: it sums the partials in split order, so the result does not depend on the arrival order, and
-// it leaves the slot at (tag, 0), ready for a graph replay of the same call. Ordering: every wave waits for its own
-// partial stores to complete (vmcnt 0) before the workgroup barrier; one thread then makes a device-scope release
-// (the write-back of its XCD's L2 makes every wave's partials visible to the other XCDs) and counts the arrival; only
-// the last workgroup makes the acquire, which invalidates its CU's L1 and its XCD's L2 copies before any of its waves
-// reads partials. One release per workgroup and one acquire per split: these write back or invalidate whole caches
-// (a fence per thread, or a full fence per workgroup, made the kernel several times slower). The
-// CAS loop ends: a failed exchange means another workgroup's arrival was counted, and at most `splits` arrive.
-uint32_t split_tag();
-__device__ __forceinline__ bool split_arrive(unsigned long long* slot, uint32_t tag, uint32_t splits) {
-  __shared__ int last;
-  __builtin_amdgcn_s_waitcnt((0 & 0xF) | 0x70 | 0xF00);  // vmcnt(0): this wave's partial stores are done
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    unsigned long long old = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t n;
-    while (true) {
-      n = ((uint32_t)(old >> 32) == tag ? (uint32_t)old : 0u) + 1u;
-      const unsigned long long nw = ((unsigned long long)tag << 32) | (n == splits ? 0u : n);
-      const unsigned long long got = atomicCAS(slot, old, nw);
-      if (got == old) break;
-      old = got;
-    }
-    last = n == splits;
-    if (n == splits) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  }
-  __syncthreads();
-  return last != 0;
-}
-
 }  // namespace omt
 
 typedef float omt_f32x4 __attribute__((ext_vector_type(4)));

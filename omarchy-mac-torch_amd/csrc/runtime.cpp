@@ -52,13 +52,6 @@ int launch_check(const char* kernel) {
   return OMT_OK;
 }
 
-// Tags of split reductions (split_arrive): 1 .. 2^24, so a slot's high word never reads as a normal float or as the
-// high word of a small non-negative int64, the likeliest contents of a reused workspace.
-uint32_t split_tag() {
-  static std::atomic<uint32_t> next{0};
-  return next.fetch_add(1, std::memory_order_relaxed) % 0xFFFFFFu + 1u;
-}
-
 static std::mutex g_stream_mu;
 static hipStream_t g_stream = nullptr;
 

@@ -600,24 +600,25 @@ def test_depthwise_tiled_stride1(cuda, ops, ks):
 
 
 @pytest.mark.parametrize("ks", [3, 5, 7])
-def test_depthwise_wgrad_split_in_kernel(cuda, ops, ks):
-    """Grad weight over image slices whose last workgroup per channel sums the slices (arrival counts in the
-    workspace): 13 images in 5 + 5 + 3 slices (3 + 3 + 3 + 3 + 1 at ks 7), 27 in 5 x 5 + 2 (1024-thread workgroups, 4-
-    or 2-row blocks); one slice at 1024 threads (9 x 128 x 64^2) and at 256 (13 x 64 x 12^2). A workspace left full
-    of other bytes, results bit-identical across calls (each with its own tag) and across replays of a captured graph
-    (one tag, the slots left ready by the previous replay) with other grad-weight calls in between."""
+def test_depthwise_wgrad_image_slices(cuda, ops, ks):
+    """Grad weight over image slices summed in slice order by a second launch: 13 images in 13 slices, 27 in 27
+    (256-thread workgroups), 4 in 2 slices of 1024-thread workgroups (4- or 2-row blocks; the slice count capped by
+    the 640 channels); one slice at 1024 threads (1 x 1280 x 128^2) and at 256 (5 x 64 x 12^2). A workspace left
+    full of other bytes, results bit-identical across calls and across replays of a captured graph with other
+    grad-weight calls in between."""
     import ctypes
     from omarchy_mac_torch import _lib
     rng = np.random.default_rng(100 + ks)
     p = ks // 2
     stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
-    for (n, c, h, w) in ((13, 16, 64, 64), (27, 24, 64, 64), (9, 128, 64, 64), (13, 64, 12, 12)):
+    for (n, c, h, w), split in (((13, 16, 64, 64), 13), ((27, 24, 64, 64), 27), ((4, 640, 96, 96), 2),
+                                ((1, 1280, 128, 128), 1), ((5, 64, 12, 12), 1)):
         x, gy = rnd(rng, n, c, h, w), rnd(rng, n, c, h, w)
         ref = orc.dw_wgrad(x, gy, ks, 1, p)
         tx, tgy = dev(x, cuda), dev(gy, cuda)
         g = _lib.conv_geo(n, c, c, h, w, ks, 1, p)
         nb = _lib.L.omt_dw_wgrad_workspace(ctypes.byref(g))
-        assert (nb > 0) == (c < 64), ("split exactly where the channels are few", n, c, h, w, nb)
+        assert nb == (0 if split == 1 else split * c * ks * ks * 4), ("slices", n, c, h, w, nb)
         outs = []
         for fill in (0xFF, 0x00, 0x3F):
             ws = torch.full((max(nb, 1),), fill, dtype=torch.uint8, device=cuda)
@@ -637,7 +638,7 @@ def test_depthwise_wgrad_split_in_kernel(cuda, ops, ks):
             graph.replay()
             torch.cuda.synchronize()
             assert np.array_equal(host(gw_g), outs[0]), (ks, n, c, h, w)
-            other = ops.depthwise_wgrad(tgy, tx, ks, 1, p)  # an eager call with another tag in between
+            other = ops.depthwise_wgrad(tgy, tx, ks, 1, p)  # an eager grad-weight call in between
             torch.cuda.synchronize()
             assert orc.rel_l2(host(other), orc.dw_wgrad(gy, x, ks, 1, p)) <= TOL
 
