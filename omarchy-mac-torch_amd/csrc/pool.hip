@@ -99,6 +99,66 @@ __global__ void __launch_bounds__(256) maxpool_fwd_k_kernel(const float* __restr
   }
 }
 
+// Square undilated K x K windows at stride S, four consecutive outputs of a row per thread (ow % 4 == 0, iw % 4 == 0,
+// x below 2 GiB, x / y / idx 16-byte aligned): each input row the four windows cover is loaded as NV aligned float4
+// runs starting at a = x0 - OFF (x0 rounded down to a multiple of 4, so OFF = (-pw) mod 4); runs outside the row or
+// the plane read 0 through the buffer range check and the same bounds test as the per-output kernel excludes them.
+// Each output compares its taps in row-major order with that kernel's rule, so values and indices are identical.
+typedef long long omt_i64x2 __attribute__((ext_vector_type(2)));
+template <int K, int S, int OFF>
+__global__ void __launch_bounds__(256) maxpool_fwd_v4_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                             int64_t* __restrict__ idx, uint32_t total4, PoolGeo g,
+                                                             uint32_t xbytes, FastDiv d_ow4, FastDiv d_oh) {
+  constexpr int NV = (OFF + 3 * S + K + 3) / 4;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, xbytes);
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total4; i += gridDim.x * blockDim.x) {
+    const uint32_t row = fdiv(i, d_ow4), ox = (i - row * (uint32_t)(g.ow >> 2)) * 4u;
+    const uint32_t plane = fdiv(row, d_oh), oy = row - plane * (uint32_t)g.oh;
+    const int y0 = (int)oy * S - g.ph, x0 = (int)ox * S - g.pw, a = x0 - OFF;
+    const uint32_t pbase = plane * (uint32_t)g.ih * (uint32_t)g.iw;
+    float v[K][4 * NV];
+#pragma unroll
+    for (int ky = 0; ky < K; ++ky) {
+      const int yy = y0 + ky;
+      const bool rin = (unsigned)yy < (unsigned)g.ih;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = a + 4 * j;
+        const bool in = rin && (unsigned)c < (unsigned)g.iw;
+        const float4 q = bload4(xr, in ? (pbase + (uint32_t)(yy * g.iw + c)) * 4u : kOOB, 0);
+        v[ky][4 * j] = q.x;
+        v[ky][4 * j + 1] = q.y;
+        v[ky][4 * j + 2] = q.z;
+        v[ky][4 * j + 3] = q.w;
+      }
+    }
+    float best[4];
+    int bi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      best[e] = -INFINITY;
+      bi[e] = -1;
+#pragma unroll
+      for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx) {
+          const int yy = y0 + ky, xx = x0 + e * S + kx;
+          const float val = v[ky][OFF + e * S + kx];
+          if ((unsigned)yy < (unsigned)g.ih && (unsigned)xx < (unsigned)g.iw &&
+              (bi[e] < 0 || val > best[e] || isnan(val))) {
+            best[e] = val;
+            bi[e] = yy * g.iw + xx;
+          }
+        }
+    }
+    const uint32_t o = row * (uint32_t)g.ow + ox;
+    *reinterpret_cast<float4*>(y + o) = make_float4(best[0], best[1], best[2], best[3]);
+    omt_i64x2* ip = reinterpret_cast<omt_i64x2*>(idx + o);
+    ip[0] = omt_i64x2{bi[0], bi[1]};
+    ip[1] = omt_i64x2{bi[2], bi[3]};
+  }
+}
+
 // Undilated windows: the outputs whose window covers input (y, x) form the range oy in
 // [ceil((y + p - k + 1) / s), floor((y + p) / s)] (clipped to the output) per axis, visited in ascending (oy, ox)
 // order like the general kernel below, so the sums are bit-identical; no per-tap divisibility tests.
@@ -168,6 +228,70 @@ __global__ void __launch_bounds__(256) maxpool_bwd_v4_kernel(const float* __rest
         for (int e = 0; e < 4; ++e)
           if (iv[jy][jx] == me + e) acc[e] += gv[jy][jx];
     *reinterpret_cast<float4*>(gx + (int64_t)row * q.iw + x) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
+// Stride-2 square windows whose covering outputs of every 8 inputs start at a multiple of 4 (K 3 pad 1: five
+// outputs from x / 2 across, up to two rows; K 2 pad 0: four across, one row; iw % 8 == 0, ow % 4 == 0, g, idx and gx
+// below 2 GiB and 16-byte aligned): eight consecutive inputs of a row per thread. Each covering output row's
+// gradients and indices are loaded as aligned runs (float4 + float, two int64 pairs + int64; runs past the row or
+// the plane read 0 and are masked out), then each input sums, in ascending (oy, ox) order, the gradients of the
+// outputs whose index names it: the same outputs in the same order as the per-input kernel, so identical results.
+template <int K, int P>
+__global__ void __launch_bounds__(256) maxpool_bwd_s2x8_kernel(const float* __restrict__ g,
+                                                               const int64_t* __restrict__ idx,
+                                                               float* __restrict__ gx, uint32_t total8, PoolGeo q,
+                                                               FastDiv d_iw8, FastDiv d_ih, uint32_t gbytes) {
+  constexpr int NX = K == 3 ? 5 : 4, NY = K == 3 ? 2 : 1;
+  static_assert((K == 3 && P == 1) || (K == 2 && P == 0), "stride-2 windows 3 x 3 pad 1 or 2 x 2 pad 0");
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(g, gbytes), ir = make_rsrc(idx, gbytes * 2u);
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total8; i += gridDim.x * blockDim.x) {
+    const uint32_t row = fdiv(i, d_iw8), x = (i - row * (uint32_t)(q.iw >> 3)) * 8u;
+    const uint32_t plane = fdiv(row, d_ih), yy = row - plane * (uint32_t)q.ih;
+    const int ty = (int)yy + P, ay = ty - K + 1;
+    const int oy0 = ay <= 0 ? 0 : (ay + 1) >> 1, oy1 = min(ty >> 1, q.oh - 1);
+    const int ox0 = (int)(x >> 1), nx = min(NX, q.ow - ox0);
+    float gv[NY][NX];
+    long long iv[NY][NX];
+#pragma unroll
+    for (int jy = 0; jy < NY; ++jy) {
+      const bool rok = oy0 + jy <= oy1;
+      const uint32_t o = (plane * (uint32_t)q.oh + (uint32_t)(oy0 + jy)) * (uint32_t)q.ow + (uint32_t)ox0;
+      const float4 g4 = bload4(gr, rok ? o * 4u : kOOB, 0);
+      const omt_i64x2 i01 = __builtin_bit_cast(omt_i64x2, __builtin_amdgcn_raw_buffer_load_b128(ir, (int)(rok ? o * 8u : kOOB), 0, 0));
+      const omt_i64x2 i23 =
+          __builtin_bit_cast(omt_i64x2, __builtin_amdgcn_raw_buffer_load_b128(ir, (int)(rok ? o * 8u + 16u : kOOB), 0, 0));
+      gv[jy][0] = g4.x;
+      gv[jy][1] = g4.y;
+      gv[jy][2] = g4.z;
+      gv[jy][3] = g4.w;
+      iv[jy][0] = i01.x;
+      iv[jy][1] = i01.y;
+      iv[jy][2] = i23.x;
+      iv[jy][3] = i23.y;
+      if constexpr (NX == 5) {
+        const bool ok4 = rok && nx == 5;
+        gv[jy][4] = bload(gr, ok4 ? o * 4u + 16u : kOOB, 0);
+        iv[jy][4] = __builtin_bit_cast(long long, __builtin_amdgcn_raw_buffer_load_b64(ir, (int)(ok4 ? o * 8u + 32u : kOOB), 0, 0));
+      }
+#pragma unroll
+      for (int jx = 0; jx < NX; ++jx)
+        if (!rok || jx >= nx) iv[jy][jx] = -1;
+    }
+    const long long me = (long long)yy * q.iw + x;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int jy = 0; jy < NY; ++jy)
+#pragma unroll
+      for (int jx = 0; jx < NX; ++jx)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (iv[jy][jx] == me + e) acc[e] += gv[jy][jx];
+    float4* out = reinterpret_cast<float4*>(gx + (size_t)row * q.iw + x);
+    out[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    out[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
 }
 
@@ -404,6 +528,21 @@ OMT_EXPORT int omt_maxpool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
   const int64_t total = planes * oh * ow;
   if (total == 0) return OMT_OK;
   const PoolGeo q = pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw);
+  const int off = (int)((4 - pw % 4) % 4);
+  if (kh == kw && sh == sw && dh == 1 && dw == 1 && ow % 4 == 0 && iw % 4 == 0 && planes * ih * iw * 4 < ((int64_t)1 << 31) &&
+      (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)idx % 16 == 0 &&
+      ((kh == 2 && sh == 2 && off == 0) || (kh == 3 && sh == 2 && (off == 0 || off == 3)))) {
+    const uint32_t total4 = (uint32_t)(total / 4), xbytes = (uint32_t)(planes * ih * iw * 4);
+    const FastDiv d_ow4 = make_fastdiv((uint32_t)(ow / 4)), d_oh = make_fastdiv((uint32_t)oh);
+#define OMT_MP_F4(K_, S_, OFF_)                                                                                    \
+  hipLaunchKernelGGL((maxpool_fwd_v4_kernel<K_, S_, OFF_>), dim3(grid1d(total4, 256)), dim3(256), 0, stream_of(stream), \
+                     x, y, idx, total4, q, xbytes, d_ow4, d_oh)
+    if (kh == 2) OMT_MP_F4(2, 2, 0);
+    else if (off == 0) OMT_MP_F4(3, 2, 0);
+    else OMT_MP_F4(3, 2, 3);
+#undef OMT_MP_F4
+    return launch_check("maxpool_fwd_v4_kernel");
+  }
   if (kh == kw && dh == 1 && dw == 1 && (kh == 2 || kh == 3)) {
     if (kh == 2)
       OMT_POOL_LAUNCH_K(maxpool_fwd_k_kernel, 2, total, stream_of(stream), x, y, idx, total, q);
@@ -425,6 +564,20 @@ OMT_EXPORT int omt_maxpool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
   if (total == 0) return OMT_OK;
   if (dh == 1 && dw == 1) {
     const PoolGeo q = pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw);
+    const int64_t gbytes = planes * oh * ow * 4;
+    if (sh == 2 && sw == 2 && kh == kw && ((kh == 3 && ph == 1 && pw == 1) || (kh == 2 && ph == 0 && pw == 0)) &&
+        iw % 8 == 0 && ow % 4 == 0 && 2 * gbytes < ((int64_t)1 << 31) && total * 4 < ((int64_t)1 << 31) &&
+        (uintptr_t)gx % 16 == 0 && (uintptr_t)g % 16 == 0 && (uintptr_t)idx % 16 == 0) {
+      const uint32_t total8 = (uint32_t)(total / 8);
+      const FastDiv d_iw8 = make_fastdiv((uint32_t)(iw / 8)), d_ih = make_fastdiv((uint32_t)ih);
+      if (kh == 3)
+        hipLaunchKernelGGL((maxpool_bwd_s2x8_kernel<3, 1>), dim3(grid1d(total8, 256)), dim3(256), 0, stream_of(stream),
+                           g, idx, gx, total8, q, d_iw8, d_ih, (uint32_t)gbytes);
+      else
+        hipLaunchKernelGGL((maxpool_bwd_s2x8_kernel<2, 0>), dim3(grid1d(total8, 256)), dim3(256), 0, stream_of(stream),
+                           g, idx, gx, total8, q, d_iw8, d_ih, (uint32_t)gbytes);
+      return launch_check("maxpool_bwd_s2x8_kernel");
+    }
     if (iw % 4 == 0 && total < ((int64_t)1 << 32) && (uintptr_t)gx % 16 == 0) {
       const int ny = max_cover(ih, oh, kh, sh, ph, 1), nx = max_cover(iw, ow, kw, sw, pw, 4);
       const uint32_t total4 = (uint32_t)(total / 4);

@@ -737,11 +737,13 @@ MAXPOOL = [((3, 3), (2, 2), (0, 0), (1, 1), False, 13), ((3, 3), (2, 2), (0, 0),
            ((2, 2), (2, 2), (0, 0), (1, 1), False, 12), ((5, 5), (3, 3), (2, 2), (1, 1), False, 17),
            ((3, 3), (2, 2), (1, 1), (2, 2), False, 15), ((3, 2), (2, 1), (1, 0), (1, 1), True, 11),
            ((2, 2), (2, 2), (0, 0), (1, 1), True, 13),
-           # rows of a multiple of 4 (four inputs per thread in the backward): 2x2 s2 (one output per four inputs'
-           # rows, two across), 3x3 s2 p1 (two by three), the same 2x2 with a partial last window, and 3x3 s1 whose
-           # cover (three by six) takes the per-input kernel
+           # rows of a multiple of 4 (four inputs per thread in the backward; with output rows of a multiple of 4,
+           # four outputs per thread in the forward): 2x2 s2 (one output per four inputs' rows, two across), 3x3 s2 p1
+           # (two by three), the same 2x2 with a partial last window, 3x3 s2 p0 in ceil mode (partial last window,
+           # aligned runs), and 3x3 s1 whose cover (three by six) takes the per-input kernel
            ((2, 2), (2, 2), (0, 0), (1, 1), False, 15), ((3, 3), (2, 2), (1, 1), (1, 1), False, 31),
-           ((2, 2), (2, 2), (0, 0), (1, 1), True, 15), ((3, 3), (1, 1), (1, 1), (1, 1), False, 11)]
+           ((2, 2), (2, 2), (0, 0), (1, 1), True, 15), ((3, 3), (2, 2), (0, 0), (1, 1), True, 15),
+           ((3, 3), (1, 1), (1, 1), (1, 1), False, 11)]
 
 
 @pytest.mark.parametrize("k,s,p,d,ceil,hw", MAXPOOL)
