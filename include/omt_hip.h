@@ -151,6 +151,16 @@ int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* w, const fl
  * the pair, which saves the slice-sum launch. */
 int omt_conv_fwd_unsummed(const omt_conv_geo* g, const float* x, const float* w, float* y, void* workspace,
                           size_t workspace_bytes, int max_slices, const float** partials, int* slices, void* stream);
+/* Forward without bias, epilogue or BN loader that also writes the training-BatchNorm sums of its output: stats
+ * [co][*groups][2] doubles, for each output channel and group of 32 or 64 consecutive output pixels (n-major, as in
+ * y; *groups set by the call from the plan's tile) the sum of y and the sum of y^2 over the group, from the
+ * accumulators in the epilogue, so omt_bn_train_fwd_stats normalizes y without reading it for its statistics.
+ * stats_bytes >= omt_conv_fwd_stats_bytes(g); same workspace as omt_conv_fwd. A plan that splits K, or a batch that
+ * would run in chunks, is OMT_UNSUPPORTED (nothing launched). No counterpart in the reference (see
+ * omt_conv_fwd_unsummed); the torch.compile backend's convolution -> training BatchNorm op uses it. */
+size_t omt_conv_fwd_stats_bytes(const omt_conv_geo* g);
+int omt_conv_fwd_stats(const omt_conv_geo* g, const float* x, const float* w, float* y, double* stats,
+                       size_t stats_bytes, int* groups, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Grad input: gx = conv_transpose(gy, w). Stride 1 is one GEMM over flipped, transposed weights; stride s > 1 is
  * s*s dense stride-phase GEMMs in one launch (phases no tap reaches write zeros). Replaces gemm_grad_input
@@ -275,6 +285,14 @@ int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts,
                            double momentum, double eps, int relu, const float* residual, float* y, float* save_mean,
                            float* save_invstd, float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
                            void* stream);
+/* omt_bn_train_fwd_res with the statistics from omt_conv_fwd_stats (stats [c][groups][2] over x = that call's y):
+ * one launch sums each channel's groups (in a fixed order) and finalizes mean / invstd and the running statistics,
+ * the next applies, so x is read once. The variance is E[x^2] - E[x]^2 in double (the sums are unshifted). No
+ * counterpart in the reference (see omt_conv_fwd_stats). */
+int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats, int groups,
+                           const float* gamma, const float* beta, const float* running_mean, const float* running_var,
+                           double momentum, double eps, int relu, const float* residual, float* y, float* save_mean,
+                           float* save_invstd, float* new_rm, float* new_rv, void* stream);
 /* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
  * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
 int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,

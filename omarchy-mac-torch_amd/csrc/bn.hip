@@ -70,31 +70,6 @@ __device__ __forceinline__ int64_t voffset(int v, int ch, int c, int hw, int hwv
   return ((int64_t)nn * c + ch) * hw + (int64_t)e * vec;
 }
 
-// Sum of a double over the 64 lanes of a wave, in every lane: the float wave_sum's DPP steps (quad_perm [1,0,3,2],
-// [2,3,0,1], row_half_mirror, row_mirror: each row of 16 lanes ends with its sum in every lane), moving both 32-bit
-// halves of each double with the same DPP control, then the four row sums from lanes 0, 16, 32 and 48. VALU work only;
-// all 64 lanes must be active.
-template <int CTRL>
-__device__ __forceinline__ double dpp_move(double v) {
-  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
-  return __builtin_bit_cast(double, ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo);
-}
-__device__ __forceinline__ double read_lane(double v, int lane) {
-  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
-  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
-}
-__device__ __forceinline__ double wave_sum(double v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_move<0x141>(v);  // row_half_mirror
-  v += dpp_move<0x140>(v);  // row_mirror
-  return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
-}
-
 // Block-wide sum of two doubles over 256 threads; result valid in thread 0.
 __device__ __forceinline__ void block_sum2(double& a, double& b) {
   __shared__ double sa[4], sb[4];
@@ -871,6 +846,43 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
   if (int st = launch_check("bn_sum_parts_kernel")) return st;
   return omt_bn_train_fwd_res(n, c, hw, x, gamma, beta, running_mean, running_var, momentum, eps, relu, residual, y,
                               save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
+}
+
+// Statistics from a convolution's epilogue (omt_conv_fwd_stats): stats[ch][g][2] holds the unshifted double sums of
+// x and x^2 over column group g of channel ch. Workgroup ch: thread t sums the contiguous run of groups
+// [t G / 256, (t + 1) G / 256) in order, block_sum2 adds the 256 run sums in its fixed order, and thread 0 finalizes
+// (shift 0: the mean is s1 / m, the variance s2 / m - mean^2, both in double).
+__global__ void __launch_bounds__(256) bn_stats_groups_fin_kernel(const double* __restrict__ stats, int groups, double m,
+                                                                  double momentum, double eps, const float* rm,
+                                                                  const float* rv, float* __restrict__ save_mean,
+                                                                  float* __restrict__ save_invstd, float* new_rm,
+                                                                  float* new_rv) {
+  const int ch = blockIdx.x, t = threadIdx.x;
+  const int g0 = (int)((int64_t)groups * t / 256), g1 = (int)((int64_t)groups * (t + 1) / 256);
+  const double* sp = stats + (int64_t)ch * groups * 2;
+  double s1 = 0.0, s2 = 0.0;
+  for (int g = g0; g < g1; ++g) {
+    s1 += sp[2 * g];
+    s2 += sp[2 * g + 1];
+  }
+  block_sum2(s1, s2);
+  if (t == 0) bn_finalize(s1, s2, 0.0, m, momentum, eps, rm, rv, save_mean, save_invstd, new_rm, new_rv, ch, true);
+}
+
+OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats,
+                                      int groups, const float* gamma, const float* beta, const float* running_mean,
+                                      const float* running_var, double momentum, double eps, int relu,
+                                      const float* residual, float* y, float* save_mean, float* save_invstd,
+                                      float* new_rm, float* new_rv, void* stream) {
+  if (!x || !stats || !gamma || !beta || !y || !save_mean || !save_invstd)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_stats: null pointer");
+  if (groups < 1) return fail(OMT_INVALID, "omt_bn_train_fwd_stats: %d column groups", groups);
+  if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_stats: size not covered");
+  hipStream_t s = stream_of(stream);
+  hipLaunchKernelGGL(bn_stats_groups_fin_kernel, dim3((unsigned)c), dim3(256), 0, s, stats, groups, (double)(n * hw),
+                     momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv);
+  if (int st = launch_check("bn_stats_groups_fin_kernel")) return st;
+  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s);
 }
 
 OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,

@@ -102,6 +102,8 @@ struct GatherArgs {
   int64_t part_stride;   // elements per slice
   int nhwc;              // channels-last source [N][H][W][C] and output [N][YH][YW][P] (partials likewise)
   int vec_out;           // nhwc: P % 4 == 0 and y (and the partials) 16-byte aligned: float4 stores of four channels
+  double* stats;         // forward, one phase, no split K, bias or ReLU: training-BN sums of y (epilogue_stats)
+  int stats_groups;      //   over column groups of WQ GEMM columns: [P][stats_groups][2]
   Phase ph[kMaxPhases];
 };
 
@@ -121,6 +123,41 @@ __device__ __forceinline__ void epilogue_bias(const GatherArgs& a, int p0, int w
     for (int r4 = 0; r4 < 4; ++r4) {
       const int p = pb + 16 * i + r4;
       bv[i][r4] = a.bias && p < a.P ? a.bias[p] : 0.f;
+    }
+}
+
+// Training-BatchNorm statistics of a forward's output (a.stats; one phase, no split K, no bias or ReLU): for output
+// channel p and column group cg (the WQ consecutive GEMM columns of one wave of one tile: cg = (q0 + wq WQ) / WQ),
+// the double sums of y and y^2 over the group's valid columns go to a.stats[(p groups + cg) 2 + {0, 1}] (each
+// channel's groups contiguous, for the BatchNorm's per-channel sum). Each lane sums its
+// TJ columns of a row (the squares of floats are exact in double), the 16 lanes of its lane group (the MFMA tile's
+// columns) combine by DPP steps within the row, in a fixed order, and the group's first lane writes the pair: every
+// (cg, p) pair has one writer, so the result does not depend on scheduling. Every lane of the wave takes part.
+template <int TI, int TJ, int WP, int WQ>
+__device__ __forceinline__ void epilogue_stats(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
+                                               int q0, int p0, int wp, int wq, int lane) {
+  const int grp = lane >> 4, cg = q0 / WQ + wq;
+  bool qok[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) qok[j] = q0 + wq * WQ + 16 * j + (lane & 15) < ph.Q;
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const double v = qok[j] ? (double)acc[i][j][r4] : 0.0;
+        s1 += v;
+        s2 += v * v;
+      }
+      s1 = row16_sum(s1);
+      s2 = row16_sum(s2);
+      const int p = p0 + wp * WP + 16 * i + 4 * grp + r4;
+      if ((lane & 15) == 0 && p < a.P && cg < a.stats_groups) {  // a wave past the last column writes nothing
+        typedef double f64x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<f64x2*>(a.stats + ((int64_t)p * a.stats_groups + cg) * 2) = f64x2{s1, s2};
+      }
     }
 }
 
@@ -163,6 +200,7 @@ template <int TI, int TJ, int WP, int WQ>
 __device__ __forceinline__ void gather_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
                                                 int q0, int p0, int wp, int wq, int lane, int zs) {
   float bv[TI][4];
+  if (a.stats) epilogue_stats<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
   if (a.bias && !a.part) {
     epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
     gather_epilogue_b<TI, TJ, WP, WQ, true>(a, ph, acc, q0, p0, wp, wq, lane, zs, bv);
@@ -311,6 +349,7 @@ template <int TI, int TJ, int WP, int WQ>
 __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
                                              int q0, int p0, int wp, int wq, int lane, float* __restrict__ ep) {
   float bv[TI][4];
+  if (a.stats) epilogue_stats<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
   if (a.bias) {
     epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
     row_epilogue_b<TI, TJ, WP, WQ, true>(a, ph, acc, q0, p0, wp, wq, lane, ep, bv);
@@ -2123,7 +2162,7 @@ OMT_EXPORT size_t omt_conv_fwd_workspace(const omt_conv_geo* g) {
 static int conv_fwd_one(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
                         const float* bn_mean, const float* bn_var, const float* bn_gamma, const float* bn_beta,
                         float bn_eps, float* y, void* workspace, size_t workspace_bytes, void* stream,
-                        const float** parts, int* unsummed) {
+                        const float** parts, int* unsummed, double* stats = nullptr, int* groups = nullptr) {
   const bool bn = bn_mean || bn_var || bn_gamma || bn_beta;
   if (bn && !(bn_mean && bn_var && bn_gamma && bn_beta))
     return fail(OMT_INVALID, "omt_conv_fwd: BN loader needs mean, var, gamma and beta");
@@ -2185,6 +2224,13 @@ static int conv_fwd_one(const omt_conv_geo* g, const float* x, const float* w, c
   a.div_c = make_fastdiv((uint32_t)a.C);
   float* part = (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl)));
   if (parts) *parts = part;
+  if (stats) {  // the statistics come from the epilogue of an unsplit plan
+    const GatherPlan ep = eff_plan(a, pl);
+    if (ep.slices > 1) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_stats: the plan splits K");
+    a.stats = stats;
+    a.stats_groups = (int)cdiv(p.Q, gtile(ep.tile).wq);
+    *groups = a.stats_groups;
+  }
   return run_gather(a, pl, g->n, p.Q, part, s, unsummed);
 }
 
@@ -2214,6 +2260,24 @@ OMT_EXPORT int omt_conv_fwd(const omt_conv_geo* g, const float* x, const float* 
                             void* stream) {
   return conv_fwd_impl(g, x, w, bias, epilogue, bn_mean, bn_var, bn_gamma, bn_beta, bn_eps, y, workspace,
                        workspace_bytes, stream, nullptr, nullptr);
+}
+
+OMT_EXPORT size_t omt_conv_fwd_stats_bytes(const omt_conv_geo* g) {
+  if (!g || !dense_geo_ok(g)) return 0;
+  return (size_t)(cdiv(g->n * g->oh * g->ow, 32) * g->co) * 2 * sizeof(double);
+}
+
+OMT_EXPORT int omt_conv_fwd_stats(const omt_conv_geo* g, const float* x, const float* w, float* y, double* stats,
+                                  size_t stats_bytes, int* groups, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (!g || !x || !w || !y || !stats || !groups) return fail(OMT_INVALID, "omt_conv_fwd_stats: null pointer");
+  *groups = 0;
+  if (!dense_geo_ok(g) || !fits_i32(g))
+    return fail(OMT_UNSUPPORTED, "omt_conv_fwd_stats: geometry not covered (a batch below 2 GiB)");
+  if (stats_bytes < omt_conv_fwd_stats_bytes(g))
+    return fail(OMT_INVALID, "omt_conv_fwd_stats: %zu bytes of statistics needed", omt_conv_fwd_stats_bytes(g));
+  return conv_fwd_one(g, x, w, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0.f, y, workspace, workspace_bytes,
+                      stream, nullptr, nullptr, stats, groups);
 }
 
 OMT_EXPORT int omt_conv_fwd_unsummed(const omt_conv_geo* g, const float* x, const float* w, float* y, void* workspace,

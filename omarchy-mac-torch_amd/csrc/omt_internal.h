@@ -88,6 +88,34 @@ __device__ __forceinline__ float wave_sum(float v) {
           __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 
+// Doubles through the same DPP steps, both 32-bit halves moved with one control. row16_sum: the sum over each row of
+// 16 lanes, in every lane of the row (the four steps above); wave_sum: then the four row sums from lanes 0, 16, 32, 48.
+// All 64 lanes must be active. VALU work only.
+template <int CTRL>
+__device__ __forceinline__ double dpp_move(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ double read_lane(double v, int lane) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double row16_sum(double v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+  v = row16_sum(v);
+  return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
+}
+
 }  // namespace omt
 
 typedef float omt_f32x4 __attribute__((ext_vector_type(4)));

@@ -110,6 +110,8 @@ SIGNATURES = {
     "omt_conv_fwd_workspace": (SZ, [G]),
     "omt_conv_fwd": (I32, [G, VP, VP, VP, U32, VP, VP, VP, VP, F32, VP, VP, SZ, VP]),
     "omt_conv_fwd_unsummed": (I32, [G, VP, VP, VP, VP, SZ, I32, ctypes.POINTER(VP), ctypes.POINTER(I32), VP]),
+    "omt_conv_fwd_stats_bytes": (SZ, [G]),
+    "omt_conv_fwd_stats": (I32, [G, VP, VP, VP, VP, SZ, ctypes.POINTER(I32), VP, SZ, VP]),
     "omt_conv_dgrad_workspace": (SZ, [G]),
     "omt_conv_dgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_wgrad_workspace": (SZ, [G]),
@@ -151,6 +153,8 @@ SIGNATURES = {
                                    VP]),
     "omt_bn_train_fwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
                                      VP, VP, SZ, VP]),
+    "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
+                                     VP, VP]),
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
     "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_bwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),

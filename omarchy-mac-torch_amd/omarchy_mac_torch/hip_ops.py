@@ -68,6 +68,22 @@ def conv2d(x, w, bias=None, stride=1, padding=0, relu=False, bn=None, bn_eps=1e-
     return y
 
 
+def conv2d_stats(x, w, stride=1, padding=0):
+    """y = conv(x, w) and the training-BatchNorm sums of y from the epilogue (omt_conv_fwd_stats): returns
+    (y, stats [co][groups][2] float64, groups). Raises Unsupported when the layer's plan splits K."""
+    x, w = _need(x, "x", 4), _need(w, "w", 4)
+    g = conv_geo_for(x.shape, w.shape, stride, padding)
+    y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32)
+    sb = L.omt_conv_fwd_stats_bytes(ctypes.byref(g))
+    stats = torch.empty((sb // 8,), device=x.device, dtype=torch.float64)
+    groups = ctypes.c_int32(0)
+    ws, nb = _workspace(L.omt_conv_fwd_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_conv_fwd_stats(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(y), _ptr(stats), sb, ctypes.byref(groups),
+                               _ptr(ws), nb, _stream(x.device)), "conv2d_stats")
+    gr = groups.value
+    return y, stats[:g.co * gr * 2].view(g.co, gr, 2), gr
+
+
 def conv2d_dgrad(gy, w, x_shape, stride=1, padding=0):
     gy, w = _need(gy, "gy", 4), _need(w, "w", 4)
     g = conv_geo_for(x_shape, w.shape, stride, padding)
@@ -304,6 +320,25 @@ def batch_norm_train(x, gamma, beta, running_mean=None, running_var=None, moment
                              _stream(x.device)), "batch_norm_train")
     if functional:
         return y, sm, si, nrm, nrv
+    return y, sm, si
+
+
+def batch_norm_train_stats(x, stats, groups, gamma, beta, running_mean=None, running_var=None, momentum=0.1,
+                           eps=1e-5, relu=False, residual=None):
+    """Training BatchNorm (+ residual, ReLU) of a conv2d_stats output from its epilogue sums (omt_bn_train_fwd_stats:
+    x is read once). Updates running_mean / running_var in place; returns (y, save_mean, save_invstd)."""
+    x, residual = _need(x, "x", 4), _need(residual, "residual", 4)
+    gamma, beta = _need(gamma, "gamma", 1), _need(beta, "beta", 1)
+    if not stats.is_contiguous() or stats.dtype != torch.float64:
+        raise TypeError("stats: contiguous float64 from conv2d_stats")
+    n, c, h, w = x.shape
+    y = torch.empty_like(x)
+    sm = torch.empty((c,), device=x.device, dtype=torch.float32)
+    si = torch.empty_like(sm)
+    check(L.omt_bn_train_fwd_stats(n, c, h * w, _ptr(x), _ptr(stats), int(groups), _ptr(gamma), _ptr(beta),
+                                   _ptr(running_mean), _ptr(running_var), momentum, eps, int(relu), _ptr(residual),
+                                   _ptr(y), _ptr(sm), _ptr(si), _ptr(running_mean), _ptr(running_var),
+                                   _stream(x.device)), "batch_norm_train_stats")
     return y, sm, si
 
 

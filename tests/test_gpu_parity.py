@@ -308,6 +308,67 @@ def test_conv_split_k_bn_loader(cuda, ops):
         ops.clear_conv_plans()
 
 
+STATS_SHAPES = [
+    (4, 16, 32, 20, 20, 3, 1, 1), (3, 24, 40, 33, 35, 3, 1, 1),   # column groups with a partial last one
+    (4, 16, 24, 17, 17, 3, 2, 1), (2, 64, 256, 28, 28, 1, 1, 0),  # stride 2; 1x1 (the streaming tile applies)
+    (2, 40, 72, 9, 9, 5, 1, 2),                                   # channels not a multiple of the tile's rows
+]
+
+
+@pytest.mark.parametrize("shape", STATS_SHAPES, ids=_ids)
+def test_conv_epilogue_bn_statistics(cuda, ops, shape):
+    """omt_conv_fwd_stats under every tile (tap-major, channel-major and in-place variants, the direct-to-LDS and
+    streaming tiles) with one K slice: y bit-identical to omt_conv_fwd under the same plan; the epilogue's sums of y
+    and y^2 per (output channel, group of the tile's wave columns) equal float64 sums of y over the same groups; then
+    omt_bn_train_fwd_stats (with ReLU, and with a residual) matches the oracle's training BatchNorm of the conv output,
+    running statistics included. A plan that splits K is refused."""
+    n, ci, co, h, w, ks, s, p = shape
+    rng = np.random.default_rng(sum(shape) + 77)
+    x, wt = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
+    gam, bet, rm, rv = rnd(rng, co), rnd(rng, co), rnd(rng, co), np.abs(rnd(rng, co)) + 0.5
+    tx, tw = dev(x, cuda), dev(wt, cuda)
+    ntile = ops.conv_num_tiles("fwd")
+    try:
+        for tile in range(ntile):
+            ops.set_conv_plan("fwd", x.shape, wt.shape, s, p, tile, 1)
+            y, st, groups = ops.conv2d_stats(tx, tw, s, p)
+            y1 = ops.conv2d(tx, tw, None, s, p)
+            torch.cuda.synchronize()
+            assert torch.equal(y, y1), tile
+            yh = host(y).astype(np.float64)
+            q = n * y.shape[2] * y.shape[3]
+            wq = 32 if groups == -(-q // 32) else 64
+            assert groups == -(-q // wq), (tile, groups, q)
+            cols = yh.transpose(1, 0, 2, 3).reshape(co, q)  # GEMM columns: n-major output pixels
+            pad = np.zeros((co, groups * wq))
+            pad[:, :q] = cols
+            g = pad.reshape(co, groups, wq)
+            ref = np.stack([g.sum(2), (g * g).sum(2)], 2)
+            got = host(st)
+            assert np.allclose(got, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max()), tile
+        y_ref_in = orc.conv_fwd(x, wt, None, s, p)
+        r = rnd(rng, *y_ref_in.shape)
+        for relu, res in ((True, None), (False, None), (True, r)):
+            trm, trv = dev(rm, cuda), dev(rv, cuda)
+            yb, sm, si = ops.batch_norm_train_stats(y, st, groups, dev(gam, cuda), dev(bet, cuda), trm, trv, 0.1,
+                                                    1e-5, relu, None if res is None else dev(res, cuda))
+            y_bn, m_ref, i_ref, nrm, nrv = orc.bn_train(y_ref_in, gam, bet, rm, rv, 0.1, 1e-5, False)
+            want = y_bn + (0 if res is None else res)
+            if relu:
+                want = np.maximum(want, 0)
+            case = (relu, res is not None)
+            assert orc.rel_l2(host(yb), want) <= TOL, case
+            assert orc.rel_l2(host(sm), m_ref) <= 1e-5 and orc.rel_l2(host(si), i_ref) <= 1e-5, case
+            assert orc.rel_l2(host(trm), nrm) <= 1e-5 and orc.rel_l2(host(trv), nrv) <= 1e-5, case
+        ops.set_conv_plan("fwd", x.shape, wt.shape, s, p, 5, 3)
+        if ops.conv_plan("fwd", x.shape, wt.shape, s, p)[1] > 1:
+            from omarchy_mac_torch import _lib
+            with pytest.raises(_lib.Unsupported):
+                ops.conv2d_stats(tx, tw, s, p)
+    finally:
+        ops.clear_conv_plans()
+
+
 def test_autotune_caches_a_plan(cuda, ops):
     """omt_conv_autotune times the candidates and caches the fastest; calls then use it (reference autotune,
     csrc/conv.cpp:116-155)."""
