@@ -431,6 +431,17 @@ def bandwidth_cases(dev):
                        x, gam, bet, rm, rv, relu=True), 2 * nbytes(x)),
                   (f"{tag} bwd", lambda g=g, x=x, sm=sm, si=si, gam=gam, y=y: H.batch_norm_backward(
                        g, x, sm, si, gam, relu_y=y), 4 * nbytes(x))]
+    # the same BatchNorm(+ReLU) train forward over a convolution's output with the statistics from that convolution's
+    # epilogue (omt_conv_fwd_stats -> omt_bn_train_fwd_stats, as the compile backend's conv -> BN op runs it for
+    # channels past 8192 elements): the finalize, then one read of the input
+    for (n, c, h) in ((128, 32, 32), (256, 64, 56)):
+        xc, wc = rnd(n, c, h, h), rnd(c, c, 3, 3) * (9 * c) ** -0.5
+        y, st, groups = H.conv2d_stats(xc, wc, 1, 1)
+        del xc
+        gam, bet, rm, rv = rnd(c), rnd(c), rnd(c), rnd(c).abs() + 0.5
+        cases.append((f"bn+relu [{n},{c},{h},{h}] train fwd, conv-epilogue statistics",
+                      lambda y=y, st=st, groups=groups, gam=gam, bet=bet, rm=rm, rv=rv: H.batch_norm_train_stats(
+                          y, st, groups, gam, bet, rm, rv, relu=True), 2 * nbytes(y)))
     # max pools: config 2's 2x2 on [128,32,32^2], config 3's stem 3x3 s2 p1 on [32,64,32^2]
     for (n, c, h, k, st, pd) in ((128, 32, 32, 2, 2, 0), (32, 64, 32, 3, 2, 1)):
         x = rnd(n, c, h, h)

@@ -286,13 +286,15 @@ int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts,
                            float* save_invstd, float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
                            void* stream);
 /* omt_bn_train_fwd_res with the statistics from omt_conv_fwd_stats (stats [c][groups][2] over x = that call's y):
- * one launch sums each channel's groups (in a fixed order) and finalizes mean / invstd and the running statistics,
- * the next applies, so x is read once. The variance is E[x^2] - E[x]^2 in double (the sums are unshifted). No
- * counterpart in the reference (see omt_conv_fwd_stats). */
+ * one launch reduces each channel's groups to a few partial sums (in a fixed order, into the workspace of
+ * omt_bn_train_workspace's size), the next finalizes mean / invstd and the running statistics as it applies, so x is
+ * read once. The variance is E[x^2] - E[x]^2 in double (the sums are unshifted). No counterpart in the reference (see
+ * omt_conv_fwd_stats). */
 int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats, int groups,
                            const float* gamma, const float* beta, const float* running_mean, const float* running_var,
                            double momentum, double eps, int relu, const float* residual, float* y, float* save_mean,
-                           float* save_invstd, float* new_rm, float* new_rv, void* stream);
+                           float* save_invstd, float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
+                           void* stream);
 /* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
  * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
 int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,

@@ -163,6 +163,21 @@ __global__ void bn_stats_fin_kernel(const float* __restrict__ x, const double* _
               ch, true);
 }
 
+// bn_stats_fin_kernel for unshifted partial sums (the epilogue statistics reduced by bn_stats_groups_kernel).
+__global__ void bn_stats_shift0_fin_kernel(const double* __restrict__ part, int c, int slices, double m,
+                                           double momentum, double eps, const float* rm, const float* rv,
+                                           float* __restrict__ save_mean, float* __restrict__ save_invstd,
+                                           float* new_rm, float* new_rv) {
+  const int ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch >= c) return;
+  double s1 = 0.0, s2 = 0.0;
+  for (int s = 0; s < slices; ++s) {
+    s1 += part[((int64_t)ch * slices + s) * 2];
+    s2 += part[((int64_t)ch * slices + s) * 2 + 1];
+  }
+  bn_finalize(s1, s2, 0.0, m, momentum, eps, rm, rv, save_mean, save_invstd, new_rm, new_rv, ch, true);
+}
+
 // The slices' partial sums of channel ch summed in slice order by thread 0 (every lane of the first wave loads one
 // slice's pair first, so the loads overlap). Valid in thread 0 after the call; all threads must call it.
 __device__ __forceinline__ void bn_sum_slices(const double* __restrict__ part, int ch, int slices, double& s1,
@@ -263,7 +278,7 @@ __global__ void __launch_bounds__(256) bn_train_apply_kernel(const float* __rest
                                                              const float* __restrict__ beta,
                                                              const float* __restrict__ res, float* __restrict__ y,
                                                              int c, int hw, int relu, int planes, int chunks,
-                                                             int rev) {
+                                                             int rev, int shift0 = 0) {
   __shared__ float coef[2];
   int chunk;
   const int plane = apply_plane(planes, chunks, rev, chunk), ch = plane % c;
@@ -277,8 +292,8 @@ __global__ void __launch_bounds__(256) bn_train_apply_kernel(const float* __rest
   double s1, s2;
   bn_sum_slices(part, ch, slices, s1, s2);
   if (threadIdx.x == 0) {
-    const BnStats st = bn_finalize(s1, s2, (double)x[(int64_t)ch * hw], m, momentum, eps, rm, rv, save_mean,
-                                   save_invstd, new_rm, new_rv, ch, plane < c && chunk == 0);
+    const BnStats st = bn_finalize(s1, s2, shift0 ? 0.0 : (double)x[(int64_t)ch * hw], m, momentum, eps, rm, rv,
+                                   save_mean, save_invstd, new_rm, new_rv, ch, plane < c && chunk == 0);
     const float sc = st.invstd * gamma[ch];
     coef[0] = sc;
     coef[1] = beta[ch] - st.mean * sc;
@@ -849,39 +864,63 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
 }
 
 // Statistics from a convolution's epilogue (omt_conv_fwd_stats): stats[ch][g][2] holds the unshifted double sums of
-// x and x^2 over column group g of channel ch. Workgroup ch: thread t sums the contiguous run of groups
-// [t G / 256, (t + 1) G / 256) in order, block_sum2 adds the 256 run sums in its fixed order, and thread 0 finalizes
-// (shift 0: the mean is s1 / m, the variance s2 / m - mean^2, both in double).
-__global__ void __launch_bounds__(256) bn_stats_groups_fin_kernel(const double* __restrict__ stats, int groups, double m,
-                                                                  double momentum, double eps, const float* rm,
-                                                                  const float* rv, float* __restrict__ save_mean,
-                                                                  float* __restrict__ save_invstd, float* new_rm,
-                                                                  float* new_rv) {
-  const int ch = blockIdx.x, t = threadIdx.x;
-  const int g0 = (int)((int64_t)groups * t / 256), g1 = (int)((int64_t)groups * (t + 1) / 256);
+// x and x^2 over column group g of channel ch. Workgroup (s, ch) reduces slice s of the channel's groups, [s G / S,
+// (s + 1) G / S): thread t sums its contiguous run of them in order and block_sum2 adds the 256 run sums in its fixed
+// order, into part[ch][s][2] (the layout of bn_stats_part_kernel's partials, with shift 0).
+__global__ void __launch_bounds__(256) bn_stats_groups_kernel(const double* __restrict__ stats, int groups,
+                                                              double* __restrict__ part) {
+  const int s = blockIdx.x, ch = blockIdx.y, S = gridDim.x, t = threadIdx.x;
+  const int64_t lo = (int64_t)groups * s / S, hi = (int64_t)groups * (s + 1) / S, len = hi - lo;
+  const int64_t g0 = lo + len * t / 256, g1 = lo + len * (t + 1) / 256;
   const double* sp = stats + (int64_t)ch * groups * 2;
   double s1 = 0.0, s2 = 0.0;
-  for (int g = g0; g < g1; ++g) {
+  for (int64_t g = g0; g < g1; ++g) {
     s1 += sp[2 * g];
     s2 += sp[2 * g + 1];
   }
   block_sum2(s1, s2);
-  if (t == 0) bn_finalize(s1, s2, 0.0, m, momentum, eps, rm, rv, save_mean, save_invstd, new_rm, new_rv, ch, true);
+  if (t == 0) {
+    part[((int64_t)ch * S + s) * 2] = s1;
+    part[((int64_t)ch * S + s) * 2 + 1] = s2;
+  }
 }
 
 OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats,
                                       int groups, const float* gamma, const float* beta, const float* running_mean,
                                       const float* running_var, double momentum, double eps, int relu,
                                       const float* residual, float* y, float* save_mean, float* save_invstd,
-                                      float* new_rm, float* new_rv, void* stream) {
+                                      float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
   if (!x || !stats || !gamma || !beta || !y || !save_mean || !save_invstd)
     return fail(OMT_INVALID, "omt_bn_train_fwd_stats: null pointer");
   if (groups < 1) return fail(OMT_INVALID, "omt_bn_train_fwd_stats: %d column groups", groups);
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_stats: size not covered");
+  if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_train_fwd_stats: workspace too small");
   hipStream_t s = stream_of(stream);
-  hipLaunchKernelGGL(bn_stats_groups_fin_kernel, dim3((unsigned)c), dim3(256), 0, s, stats, groups, (double)(n * hw),
-                     momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv);
-  if (int st = launch_check("bn_stats_groups_fin_kernel")) return st;
+  // the groups reduced to S slices per channel (about 1024 workgroups), then the apply that finalizes its channel
+  const int S = (int)std::max<int64_t>(1, std::min<int64_t>({(int64_t)kMaxSlices, cdiv(1024, c), (int64_t)groups}));
+  double* part = (double*)workspace;
+  hipLaunchKernelGGL(bn_stats_groups_kernel, dim3((unsigned)S, (unsigned)c), dim3(256), 0, s, stats, groups, part);
+  if (int st = launch_check("bn_stats_groups_kernel")) return st;
+  const double m = (double)(n * hw);
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && al16(residual);
+  const dim3 ag = apply_grid(n * c, hw, vec ? 4 : 1), grid(ag.x * ag.y);
+  if (hw >= kFlatPlane && (int64_t)ag.x * ag.y < ((int64_t)1 << 31)) {
+    const int rev = n * c * hw * 4 >= kRevApplyBytes;
+    if (vec)
+      hipLaunchKernelGGL(bn_train_apply_kernel<true>, grid, dim3(256), 0, s, x, (const double*)part, S, m, momentum,
+                         eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta, residual, y,
+                         (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 1);
+    else
+      hipLaunchKernelGGL(bn_train_apply_kernel<false>, grid, dim3(256), 0, s, x, (const double*)part, S, m, momentum,
+                         eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta, residual, y,
+                         (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 1);
+    return launch_check("bn_train_apply_kernel");
+  }
+  hipLaunchKernelGGL(bn_stats_shift0_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, S,
+                     m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv);
+  if (int st = launch_check("bn_stats_shift0_fin_kernel")) return st;
   return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s);
 }
 

@@ -2172,6 +2172,7 @@ static int conv_fwd_one(const omt_conv_geo* g, const float* x, const float* w, c
     return fail(OMT_INVALID, "omt_conv_fwd: workspace of %zu bytes needed", need);
   hipStream_t s = stream_of(stream);
   const GatherPlan pl = fwd_plan(g);
+  if (stats && pl.slices > 1) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_stats: the plan splits K");
   GatherArgs a{};
   a.x = x;
   a.w = w;
@@ -2224,9 +2225,8 @@ static int conv_fwd_one(const omt_conv_geo* g, const float* x, const float* w, c
   a.div_c = make_fastdiv((uint32_t)a.C);
   float* part = (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl)));
   if (parts) *parts = part;
-  if (stats) {  // the statistics come from the epilogue of an unsplit plan
+  if (stats) {  // the statistics come from the epilogue of an unsplit plan (checked above, before any launch)
     const GatherPlan ep = eff_plan(a, pl);
-    if (ep.slices > 1) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_stats: the plan splits K");
     a.stats = stats;
     a.stats_groups = (int)cdiv(p.Q, gtile(ep.tile).wq);
     *groups = a.stats_groups;

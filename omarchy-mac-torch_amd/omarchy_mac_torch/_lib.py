@@ -154,7 +154,7 @@ SIGNATURES = {
     "omt_bn_train_fwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
                                      VP, VP, SZ, VP]),
     "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
-                                     VP, VP]),
+                                     VP, VP, SZ, VP]),
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
     "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_bwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),

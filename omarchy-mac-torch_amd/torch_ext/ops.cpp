@@ -462,6 +462,12 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_,
 // bit-identical to convolution + omt::bn_train_), one launch fewer; other plans run the two as they are. (With 16-32
 // slices of a 2x2-plane layer the BatchNorm's scattered partial reads took longer than the slice-sum launch.)
 constexpr int kFoldSlices = 4;
+// Channels of up to this many elements (n * oh * ow) are normalized by one BatchNorm launch that holds the channel in
+// registers (one read of the input already). Larger ones take the statistics from the convolution's epilogue when
+// the output has at least kStatsMinBytes: below that the epilogue's sums cost the convolution more than the skipped
+// read saves (graph replays, conv + BN + ReLU: [32,64,56^2] 3x3 +5.3 / -1.6 us, [128,32,32^2] +2.6 / -0.6 us;
+// [256,64,56^2] 3x3 +12 / -17 us, 1x1 from 256 channels -8 / -22 us).
+constexpr int64_t kBnOneLaunchMax = 8192, kStatsMinBytes = 64ll << 20;
 static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor& x_, const Tensor& cw_,
                                                                     IntArrayRef stride, IntArrayRef padding,
                                                                     const Tensor& w, const Tensor& b, const Tensor& rm,
@@ -483,16 +489,33 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor
   tune_conv(OMT_DIR_FWD, g);
   Tensor conv = empty_dev({g.n, g.co, g.oh, g.ow});
   Tensor ws = workspace(omt_conv_fwd_workspace(&g));
+  const int64_t n = g.n, c = g.co, hw = g.oh * g.ow;
+  Tensor y = empty_dev(conv.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  const float* r = res.defined() ? fp(res) : nullptr;
+  const int relu = act == 1 ? 1 : 0;
+  if (n * hw > kBnOneLaunchMax && n * c * hw * 4 >= kStatsMinBytes) {
+    // the statistics from the convolution's epilogue, so the BatchNorm reads the convolution output once; a plan
+    // that splits K (or a batch run in chunks) is refused before any launch and takes the path below
+    Tensor stats = workspace(omt_conv_fwd_stats_bytes(&g));
+    int groups = 0;
+    const int st = omt_conv_fwd_stats(&g, fp(x), fp(cw), fpm(conv), (double*)wsptr(stats), wsbytes(stats), &groups,
+                                      wsptr(ws), wsbytes(ws), cur_stream());
+    if (st == OMT_OK) {
+      Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
+      check(omt_bn_train_fwd_stats(n, c, hw, fp(conv), (const double*)wsptr(stats), groups, fp(w), fp(b), fp(rm),
+                                   fp(rv), mom, eps, relu, r, fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws),
+                                   wsbytes(bws), cur_stream()),
+            "omt::conv_bn_train_ (BatchNorm from the epilogue statistics)");
+      return {y, sm, si, conv};
+    }
+    if (st != OMT_UNSUPPORTED) check(st, "omt::conv_bn_train_ (convolution with statistics)");
+  }
   const float* parts = nullptr;
   int slices = 1;
   check(omt_conv_fwd_unsummed(&g, fp(x), fp(cw), fpm(conv), wsptr(ws), wsbytes(ws), kFoldSlices, &parts, &slices,
                               cur_stream()),
         "omt::conv_bn_train_ (convolution)");
-  const int64_t n = g.n, c = g.co, hw = g.oh * g.ow;
-  Tensor y = empty_dev(conv.sizes()), sm = empty_dev({c}), si = empty_dev({c});
   Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
-  const float* r = res.defined() ? fp(res) : nullptr;
-  const int relu = act == 1 ? 1 : 0;
   if (slices > 1)
     check(omt_bn_train_fwd_parts(n, c, hw, parts, slices, fpm(conv), fp(w), fp(b), fp(rm), fp(rv), mom, eps, relu, r,
                                  fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws), cur_stream()),

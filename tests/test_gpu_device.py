@@ -613,13 +613,17 @@ def test_native_batch_norm_legit_shims_on_device(clean, shape):
 
 @pytest.mark.parametrize("shape", [(4, 16, 32, 8, 8, 3, 1, 1), (32, 64, 64, 16, 16, 3, 1, 1),
                                    (8, 16, 16, 40, 40, 3, 1, 1), (16, 32, 32, 14, 14, 3, 2, 1),
-                                   (6, 24, 20, 9, 9, 1, 1, 0), (8, 64, 64, 2, 2, 3, 1, 1)])
+                                   (6, 24, 20, 9, 9, 1, 1, 0), (8, 64, 64, 2, 2, 3, 1, 1),
+                                   (16, 16, 64, 128, 128, 3, 1, 1)])
 def test_conv_bn_train_matches_conv_then_bn(clean, shape):
     """omt::conv_bn_train_ (the compile backend's convolution -> training BatchNorm) against the convolution followed
     by omt::bn_train_, bit for bit (outputs, convolution output, statistics, running statistics), under unsplit and
     K-split plans (the BatchNorm sums the convolution's partials itself up to 4 slices; 16 are summed by the
     convolution): channels of at most 8192 elements (one launch), larger ones (slice sum, then the two-pass
-    BatchNorm), 7x7 planes (scalar loads), 2x2 planes, with a residual and ReLU; and against the oracle."""
+    BatchNorm), 7x7 planes (scalar loads), 2x2 planes, with a residual and ReLU; and against the oracle. Outputs of
+    64 MB or more with channels past 8192 elements, under an unsplit plan, take their statistics from the
+    convolution's epilogue (summed in another order): there the convolution output is bit-identical and the rest
+    agrees to 1e-5."""
     omt = clean
     from omarchy_mac_torch import hip_ops
     n, ci, co, h, w, ks, st, pd = shape
@@ -643,8 +647,14 @@ def test_conv_bn_train_matches_conv_then_bn(clean, shape):
                 c2 = torch.ops.aten.convolution(dx, dcw, None, [st, st], [pd, pd], [1, 1], False, [0, 0], 1)
                 y2, m2, i2 = torch.ops.omt.bn_train_(c2, dg, db, rm2, rv2, 0.1, 1e-5, act, res)
                 case = (slices, act, res is not None)
-                for a, bb in ((y1, y2), (m1, m2), (i1, i2), (c1, c2), (rm1, rm2), (rv1, rv2)):
-                    assert torch.equal(a.cpu(), bb.cpu()), case
+                from_stats = (n * oh * oh > 8192 and n * co * oh * oh * 4 >= 64 << 20 and
+                              hip_ops.conv_plan("fwd", x.shape, cw.shape, st, pd)[1] == 1)
+                assert torch.equal(c1.cpu(), c2.cpu()), case
+                for a, bb in ((y1, y2), (m1, m2), (i1, i2), (rm1, rm2), (rv1, rv2)):
+                    if from_stats:
+                        assert rel(a, bb) <= 1e-5, case
+                    else:
+                        assert torch.equal(a.cpu(), bb.cpu()), case
                 assert rel(c1, conv_ref) <= TOL, case
                 if res is None and act == 1:
                     y_ref = orc.bn_train(conv_ref, g, b, rm, rv, 0.1, 1e-5, True)[0]
