@@ -345,11 +345,13 @@ __device__ __forceinline__ void row_epilogue_b(const GatherArgs& a, const Phase&
       __builtin_amdgcn_wave_barrier();  // the next pass writes these rows
     }
 }
-template <int TI, int TJ, int WP, int WQ>
+// STATS false: no statistics code at all (the persistent 1x1 kernel keeps its register budget without it).
+template <int TI, int TJ, int WP, int WQ, bool STATS = true>
 __device__ __forceinline__ void row_epilogue(const GatherArgs& a, const Phase& ph, const omt_f32x4 (&acc)[TI][TJ],
                                              int q0, int p0, int wp, int wq, int lane, float* __restrict__ ep) {
   float bv[TI][4];
-  if (a.stats) epilogue_stats<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
+  if constexpr (STATS)
+    if (a.stats) epilogue_stats<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
   if (a.bias) {
     epilogue_bias<TI, WP>(a, p0, wp, lane, bv);
     row_epilogue_b<TI, TJ, WP, WQ, true>(a, ph, acc, q0, p0, wp, wq, lane, ep, bv);
@@ -677,7 +679,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
 // current tile finishes, and its output stores drain under the next tile's MFMAs. One phase, no split K, no BN
 // loader; K a multiple of the K-block (the host checks). Same LDS layout and MFMA order as the staged gather tiles,
 // so each output sums its K terms in the same order as there.
-template <int BP, int BQ, int WP, int WQ>
+template <int BP, int BQ, int WP, int WQ, bool STATS>
 __global__ void __launch_bounds__(256, 2) conv1x1_stream_kernel(const GatherArgs a, const int tpw) {
   constexpr int NT = 256, BK = 16;
   constexpr int WGQ = BQ / WQ, TI = WP / 16, TJ = WQ / 16, PK = BK + 4;
@@ -783,7 +785,7 @@ __global__ void __launch_bounds__(256, 2) conv1x1_stream_kernel(const GatherArgs
     mfma_block(S);
     if (++ckb == nk) {
       __syncthreads();  // every wave's MFMAs of this block have read buffer S
-      row_epilogue<TI, TJ, WP, WQ>(a, ph, acc, ctq * BQ, p0, wp, wq, lane, ep);
+      row_epilogue<TI, TJ, WP, WQ, STATS>(a, ph, acc, ctq * BQ, p0, wp, wq, lane, ep);
       zero();
       ckb = 0;
       ++ctq;
@@ -1901,9 +1903,9 @@ static dim3 gather_grid(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t 
   a.part_stride = n * a.P * a.YH * a.YW;
   a.tpw = 0;
   a.rows = rows_ok(a, pl.slices > 1);
-  if (tl.stream) {  // about four workgroups per CU, each with a run of pixel tiles
+  if (tl.stream) {  // a workgroup per resident slot (four per CU, three with the statistics' registers)
     const int64_t ntq = cdiv(maxq, tl.bq), ntp = cdiv(a.P, tl.bp);
-    a.tpw = (int)std::max<int64_t>(1, cdiv(ntq * ntp, 4 * kCUs));
+    a.tpw = (int)std::max<int64_t>(1, cdiv(ntq * ntp, (a.stats ? 3 : 4) * kCUs));
     return dim3((unsigned)cdiv(ntq, a.tpw), (unsigned)ntp, 1);
   }
   return dim3((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
@@ -1969,7 +1971,10 @@ static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t 
   }
   const dim3 grid = gather_grid(a, pl, n, maxq, part);
   if (gtile(pl.tile).stream) {
-    hipLaunchKernelGGL((conv1x1_stream_kernel<64, 128, 32, 64>), grid, dim3(256), 0, s, a, a.tpw);
+    if (a.stats)
+      hipLaunchKernelGGL((conv1x1_stream_kernel<64, 128, 32, 64, true>), grid, dim3(256), 0, s, a, a.tpw);
+    else
+      hipLaunchKernelGGL((conv1x1_stream_kernel<64, 128, 32, 64, false>), grid, dim3(256), 0, s, a, a.tpw);
     return launch_check("conv1x1_stream_kernel");
   }
   if (a.bn_mean)
