@@ -767,6 +767,28 @@ static int launch_apply(int64_t n, int64_t c, int64_t hw, const float* x, const 
   return launch_check("bn_apply_kernel");
 }
 
+// Statistics from a convolution's epilogue (omt_conv_fwd_stats): stats[ch][g][2] holds the unshifted double sums of
+// x and x^2 over column group g of channel ch. Workgroup (s, ch) reduces slice s of the channel's groups, [s G / S,
+// (s + 1) G / S): thread t sums its contiguous run of them in order and block_sum2 adds the 256 run sums in its fixed
+// order, into part[ch][s][2] (the layout of bn_stats_part_kernel's partials, with shift 0).
+__global__ void __launch_bounds__(256) bn_stats_groups_kernel(const double* __restrict__ stats, int groups,
+                                                              double* __restrict__ part) {
+  const int s = blockIdx.x, ch = blockIdx.y, S = gridDim.x, t = threadIdx.x;
+  const int64_t lo = (int64_t)groups * s / S, hi = (int64_t)groups * (s + 1) / S, len = hi - lo;
+  const int64_t g0 = lo + len * t / 256, g1 = lo + len * (t + 1) / 256;
+  const double* sp = stats + (int64_t)ch * groups * 2;
+  double s1 = 0.0, s2 = 0.0;
+  for (int64_t g = g0; g < g1; ++g) {
+    s1 += sp[2 * g];
+    s2 += sp[2 * g + 1];
+  }
+  block_sum2(s1, s2);
+  if (t == 0) {
+    part[((int64_t)ch * S + s) * 2] = s1;
+    part[((int64_t)ch * S + s) * 2 + 1] = s2;
+  }
+}
+
 }  // namespace omt
 
 using namespace omt;
@@ -861,28 +883,6 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
   if (int st = launch_check("bn_sum_parts_kernel")) return st;
   return omt_bn_train_fwd_res(n, c, hw, x, gamma, beta, running_mean, running_var, momentum, eps, relu, residual, y,
                               save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
-}
-
-// Statistics from a convolution's epilogue (omt_conv_fwd_stats): stats[ch][g][2] holds the unshifted double sums of
-// x and x^2 over column group g of channel ch. Workgroup (s, ch) reduces slice s of the channel's groups, [s G / S,
-// (s + 1) G / S): thread t sums its contiguous run of them in order and block_sum2 adds the 256 run sums in its fixed
-// order, into part[ch][s][2] (the layout of bn_stats_part_kernel's partials, with shift 0).
-__global__ void __launch_bounds__(256) bn_stats_groups_kernel(const double* __restrict__ stats, int groups,
-                                                              double* __restrict__ part) {
-  const int s = blockIdx.x, ch = blockIdx.y, S = gridDim.x, t = threadIdx.x;
-  const int64_t lo = (int64_t)groups * s / S, hi = (int64_t)groups * (s + 1) / S, len = hi - lo;
-  const int64_t g0 = lo + len * t / 256, g1 = lo + len * (t + 1) / 256;
-  const double* sp = stats + (int64_t)ch * groups * 2;
-  double s1 = 0.0, s2 = 0.0;
-  for (int64_t g = g0; g < g1; ++g) {
-    s1 += sp[2 * g];
-    s2 += sp[2 * g + 1];
-  }
-  block_sum2(s1, s2);
-  if (t == 0) {
-    part[((int64_t)ch * S + s) * 2] = s1;
-    part[((int64_t)ch * S + s) * 2 + 1] = s2;
-  }
 }
 
 OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats,
