@@ -165,6 +165,47 @@ def test_batch_chunks_host_side():
         L.omt_conv_clear_plans()
 
 
+def test_epilogue_statistics_validation_host_side():
+    """omt_conv_fwd_stats / omt_bn_train_fwd_stats reject bad arguments on the host, before any launch: null
+    pointers, a statistics buffer smaller than omt_conv_fwd_stats_bytes (one pair per channel and 32 output pixels), a
+    plan that splits K, a batch that would run in chunks, and zero column groups."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    groups = ctypes.c_int32(7)
+    g = _lib.conv_geo(2, 16, 24, 10, 10, 3, 1, 1)
+    need = L.omt_conv_fwd_stats_bytes(ctypes.byref(g))
+    assert need == -(-2 * 10 * 10 // 32) * 24 * 2 * 8
+    L.omt_conv_clear_plans()
+    try:
+        assert L.omt_conv_fwd_stats(ctypes.byref(g), fake, fake, fake, None, need, ctypes.byref(groups), fake, 1 << 30,
+                                    None) == _lib.OMT_INVALID
+        assert L.omt_conv_fwd_stats(ctypes.byref(g), fake, fake, fake, fake, need - 8, ctypes.byref(groups), fake,
+                                    1 << 30, None) == _lib.OMT_INVALID
+        assert groups.value == 0
+        assert L.omt_conv_set_plan(_lib.OMT_DIR_FWD, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(5, 3))) == _lib.OMT_OK
+        assert L.omt_conv_fwd_stats(ctypes.byref(g), fake, fake, fake, fake, need, ctypes.byref(groups), fake, 1 << 30,
+                                    None) == _lib.OMT_UNSUPPORTED
+        assert b"splits K" in L.omt_last_error()
+        big = _lib.conv_geo(3, 16, 16, 3700, 3700, 3, 1, 1)  # past 2 GiB: the batch would run in chunks
+        assert L.omt_conv_fwd_stats(ctypes.byref(big), fake, fake, fake, fake, 1 << 40, ctypes.byref(groups), fake,
+                                    1 << 30, None) == _lib.OMT_UNSUPPORTED
+    finally:
+        L.omt_conv_clear_plans()
+    ws = L.omt_bn_train_workspace(2, 24, 100)
+    args = [2, 24, 100, fake, fake, 3, fake, fake, None, None, 0.1, 1e-5, 1, None, fake, fake, fake, None, None, fake,
+            ws, None]
+    bad_groups = list(args)
+    bad_groups[5] = 0
+    assert L.omt_bn_train_fwd_stats(*bad_groups) == _lib.OMT_INVALID
+    no_stats = list(args)
+    no_stats[4] = None
+    assert L.omt_bn_train_fwd_stats(*no_stats) == _lib.OMT_INVALID
+    small_ws = list(args)
+    small_ws[20] = ws - 8
+    assert L.omt_bn_train_fwd_stats(*small_ws) == _lib.OMT_INVALID
+
+
 def test_plan_cache_host_side():
     """The plan cache (tile, K slices per direction and geometry; reference conv_plan / tune_dump / tune_load,
     csrc/conv.cpp:45-60, 243-272) and the cost model's split choice, all host-side."""
