@@ -804,7 +804,9 @@ MAXPOOL = [((3, 3), (2, 2), (0, 0), (1, 1), False, 13), ((3, 3), (2, 2), (0, 0),
            # aligned runs), and 3x3 s1 whose cover (three by six) takes the per-input kernel
            ((2, 2), (2, 2), (0, 0), (1, 1), False, 15), ((3, 3), (2, 2), (1, 1), (1, 1), False, 31),
            ((2, 2), (2, 2), (0, 0), (1, 1), True, 15), ((3, 3), (2, 2), (0, 0), (1, 1), True, 15),
-           ((3, 3), (1, 1), (1, 1), (1, 1), False, 11)]
+           ((3, 3), (1, 1), (1, 1), (1, 1), False, 11),
+           # output rows of 12 (three four-output runs per row; eight-input backward on rows of 24)
+           ((3, 3), (2, 2), (1, 1), (1, 1), False, 23)]
 
 
 @pytest.mark.parametrize("k,s,p,d,ceil,hw", MAXPOOL)
