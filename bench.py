@@ -944,7 +944,7 @@ def main():
         if args.workload == "resnet":
             cfgs = [c for c in cfgs if c[0] == "resnet18_b32"]
         print(json.dumps({c[0]: train_step_bench(c, omarchy_mac_torch.DEVICE, args.model_steps, 5, 5, not args.no_cpu,
-                                                 compiled=c[0] == "resnet18_b32", fp64=c[0] == "resnet18_b32")
+                                                 compiled=c[0] in ("resnet18_b32", "mobilenetv3_b32"), fp64=c[0] == "resnet18_b32")
                           for c in cfgs}), flush=True)
         return
     if args.workload == "bw":
@@ -1018,7 +1018,8 @@ def main():
         for cfg in train_configs():
             print(f"{cfg[0]} ...", file=sys.stderr, flush=True)
             out[cfg[0]] = train_step_bench(cfg, omarchy_mac_torch.DEVICE, args.model_steps, 5, 5, not args.no_cpu,
-                                           compiled=cfg[0] == "resnet18_b32", fp64=cfg[0] == "resnet18_b32")
+                                           compiled=cfg[0] in ("resnet18_b32", "mobilenetv3_b32"),
+                                           fp64=cfg[0] == "resnet18_b32")
     print(json.dumps(out), flush=True)
 
 
