@@ -944,7 +944,8 @@ def main():
         if args.workload == "resnet":
             cfgs = [c for c in cfgs if c[0] == "resnet18_b32"]
         print(json.dumps({c[0]: train_step_bench(c, omarchy_mac_torch.DEVICE, args.model_steps, 5, 5, not args.no_cpu,
-                                                 compiled=c[0] in ("resnet18_b32", "mobilenetv3_b32"), fp64=c[0] == "resnet18_b32")
+                                                 compiled=c[0] in ("resnet18_b32", "mobilenetv3_b32"),
+                                                 fp64=c[0] == "resnet18_b32")
                           for c in cfgs}), flush=True)
         return
     if args.workload == "bw":
