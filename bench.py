@@ -28,6 +28,7 @@ PyTorch-ROCm user gets without this library (--no-miopen skips it).
 """
 
 import argparse
+import contextlib
 import json
 import os
 import pathlib
@@ -241,19 +242,22 @@ RESNET_FAMILIES = [
     ("omt BatchNorm", ("omt::bn_",)),
     ("omt pools", ("maxpool", "avgpool", "adapool", "gap_")),
     ("omt fused Adam / SGD (multi-tensor)", ("fused_adam_kernel", "fused_sgd_kernel")),
-    ("torch fused Adam (+ its step-count increment)", ("FusedAdam", "BinaryOpScalarFunctor<float")),
-    ("torch foreach (batch counters)", ("BinaryOpScalarFunctor<long", "foreach")),
-    ("hipBLASLt (linear layer)", ("Cijk", "hipblaslt", "gemm")),
+    ("omt log-softmax / NLL loss", ("log_softmax_", "nll_fwd_kernel", "nll_bwd_kernel")),
+    ("omt pointwise, plane sums, bias gradient, step counts and batch counters",
+     ("pointwise_kernel", "plane_s", "foreach_add_kernel", "zero_fill_kernel", "bias_grad_kernel")),
+    ("torch fused Adam", ("FusedAdam",)),
+    ("torch foreach / elementwise (counters, ReLU, add)", ("BinaryOpScalarFunctor", "foreach", "elementwise")),
+    ("hipBLASLt / rocBLAS GEMM (linear layer)", ("Cijk", "hipblaslt", "rocblas")),
     ("torch softmax / nll / reductions", ("softmax", "nll", "reduce_kernel")),
     ("runtime copies / fills", ("fill", "copy", "Copy")),
-    ("torch elementwise (ReLU, add, threshold_backward, counters)", ("elementwise",)),
 ]
 
 
 def resnet_trace_summary(trace_csv, replays=22):
     """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` and prints, for
-    the compiled graphed replays (the last run of `replays` identical steps) and the eager-model graphed replays (the
-    run before it), kernel time per step by family as markdown. Replays of one graph launch the same dispatch
+    the compiled graphed replays (the last run of `replays` identical steps), the eager-model graphed replays (the
+    run before it) and the compiled model with the backend's own graph replay (the run before that), kernel time per
+    step by family as markdown. Replays of one graph launch the same dispatch
     sequence, so a run is the latest stretch of the trace that repeats with some period D `replays` times; any D
     consecutive dispatches of it are one step's launches."""
     import csv
@@ -276,14 +280,17 @@ def resnet_trace_summary(trace_csv, replays=22):
 
     runs = []
     hi = len(names)
-    for _ in range(2):
+    for _ in range(3):
         found = periodic_run(hi, max(0, hi - 20000))
         if not found:
             break
         st, d = found
         runs.append(rows[st:st + replays * d])
         hi = st
-    for title, run in zip(("compiled graphed replays", "eager-model graphed replays"), runs):
+    titles = ("compiled model, whole step captured by the caller (graphs.Graph) and replayed",
+              "eager model, whole step captured by the caller and replayed",
+              "compiled model alone: the backend replays its forward and backward graphs, the rest runs eagerly")
+    for title, run in zip(titles, runs):
         d = len(run) // replays
         per, cnt = {}, {}
         for (t0, t1, name) in run:
@@ -642,8 +649,9 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
     data = [(torch.randn(batch, *shape, generator=g), torch.randint(0, classes, (batch,), generator=g))
             for _ in range(n_batches)]
 
-    def run(model, device, batches, timed_from, dtype=torch.float32):
+    def run(model, device, batches, timed_from, dtype=torch.float32, compile_it=False):
         opt = make_opt(model.parameters())
+        fwd = torch.compile(model, backend=dev_name) if compile_it else model
         losses, t0 = [], None
         for i, (x, t) in enumerate(batches):
             if i == timed_from:
@@ -651,7 +659,7 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
                     torch.cuda.synchronize()
                 t0 = time.perf_counter()
             opt.zero_grad(set_to_none=True)
-            loss = F.cross_entropy(model(x.to(dtype)), t)
+            loss = F.cross_entropy(fwd(x.to(dtype)), t)
             loss.backward()
             opt.step()
             losses.append(loss.detach())
@@ -664,9 +672,17 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
 
     def run_graphed(model, batches, timed_from, compile_it=False):
         """The same step captured once as a HIP graph (omarchy_mac_torch.graphs) after `timed_from` eager warm-up
-        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed)."""
-        from omarchy_mac_torch import graphs
+        steps, then replayed per batch; each batch is copied into the captured input tensors first (timed). The
+        compiled model's own graph replay is off here (the whole step is the graph)."""
+        from omarchy_mac_torch import graphs, replay
 
+        prev = replay.set_enabled(False)
+        try:
+            return _run_graphed(model, batches, timed_from, compile_it, graphs)
+        finally:
+            replay.set_enabled(prev)
+
+    def _run_graphed(model, batches, timed_from, compile_it, graphs):
         opt = make_opt(model.parameters(), capturable=True)
         sx, st = torch.empty_like(batches[0][0]), torch.empty_like(batches[0][1])
         fwd = torch.compile(model, backend=dev_name) if compile_it else model
@@ -711,7 +727,21 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
     dev_ms, dev_losses = run(copy.deepcopy(base).to(dev_name), dev_name, dev_batches, warmup)
     out = {"config": title, "ms_per_step": round(dev_ms, 3), "host_enqueue_ms_per_step": round(run.host_ms, 3),
            "steps": steps, "warmup": warmup}
+    n_ops = aten_ops_per_step(copy.deepcopy(base).to(dev_name), make_opt, dev_batches[0])
+    out.update({"aten_ops_per_step": n_ops, "host_us_per_aten_op": round(run.host_ms * 1e3 / n_ops, 2)})
     variants = {}
+    if compiled:
+        from omarchy_mac_torch import replay
+
+        replay.reset_stats()
+        c_ms, variants["compiled"] = run(copy.deepcopy(base).to(dev_name), dev_name, dev_batches, warmup,
+                                         compile_it=True)
+        out["compiled"] = {
+            "ms_per_step": round(c_ms, 3), "host_enqueue_ms_per_step": round(run.host_ms, 3), "steps": steps,
+            "warmup": warmup, "graph_replay": {k: replay.STATS[k] for k in ("captures", "replays", "eager")},
+            "how": "torch.compile(model, backend=\"omarchy_mac_torch\") and nothing else: the backend's rewrites, its "
+                   "forward and backward graphs replayed as HIP graphs from the third step on; loss, log-softmax, "
+                   "the optimizer and zero_grad run eagerly around them"}
     g_ms, variants["graphed"] = run_graphed(copy.deepcopy(base).to(dev_name), dev_batches, 3)
     out["graphed"] = {"ms_per_step": round(g_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
                       "how": "omarchy_mac_torch.graphs.Graph: forward + backward + fused optimizer captured once, "
@@ -750,6 +780,31 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
         out["max_rel_loss_diff_vs_fp64"] = {"device": rel_diff(dev_losses[:k], f64),
                                             "cpu_fp32": rel_diff(cpu_losses[:k], f64)}
     return out
+
+
+def aten_ops_per_step(model, make_opt, batch):
+    """The aten operators one eager training step dispatches (forward, loss, backward, optimizer; views included):
+    the host-side work per step that graph replay removes."""
+    import torch
+    import torch.nn.functional as F
+    from torch.utils._python_dispatch import TorchDispatchMode
+
+    class Count(TorchDispatchMode):
+        n = 0
+
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            Count.n += 1
+            return func(*args, **(kwargs or {}))
+
+    opt = make_opt(model.parameters())
+    x, t = batch
+    for counting in (False, True):  # the first step creates the optimizer state
+        with Count() if counting else contextlib.nullcontext():
+            opt.zero_grad(set_to_none=True)
+            F.cross_entropy(model(x), t).backward()
+            opt.step()
+    torch.cuda.synchronize()
+    return Count.n
 
 
 def conv_sweep(layers, dev, steps, warmup, tune, nhwc=False):
@@ -817,6 +872,7 @@ def conv_sweep(layers, dev, steps, warmup, tune, nhwc=False):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
+    check = verify_sweep(data, fwd_op, dgrad_op, wgrad_op)
     step_flops = sum(3 * flops_dir(n, c, k, h, ks, s, p) for (_, n, c, k, h, ks, s, p, *_r) in data)
     fwd_ms = [a.elapsed_time(b) for (_, a, b) in fwd_events]
     fwd_flops = [f for (f, _, _) in fwd_events]
@@ -841,7 +897,46 @@ def conv_sweep(layers, dev, steps, warmup, tune, nhwc=False):
         "per_layer_tflops": {name: {d: round(layer_flops[name] / (sum(v) / len(v) / 1e3) / 1e12, 1)
                                     for d, v in dd.items()} for name, dd in per_layer.items()},
         "plans": plans,
+        "rel_l2_vs_torch_cpu": check,
     }
+
+
+def verify_sweep(data, fwd_op, dgrad_op, wgrad_op, images=(0, -1), samples=24):
+    """The outputs of the timed launches (same inputs, same plans) against PyTorch CPU in float64, per layer: y and gx
+    on two images of the batch (each image's output depends on that image alone), and `samples` random entries of gw
+    (each a float64 sum over the whole batch of gy[:, co] times the shifted x[:, ci]). Returns {layer: {"y", "gx", "gw":
+    rel-L2}}; the bench line carries it."""
+    import torch
+    import torch.nn.functional as F
+
+    out = {}
+    gen = torch.Generator().manual_seed(1)
+    for (name, n, c, k, h, ks, s, p, x, w, gy) in data:
+        y = fwd_op(x, w, None, s, p)
+        gx = dgrad_op(gy, w, x.shape, s, p)
+        gw = wgrad_op(x, gy, ks, s, p)
+        wc = w.double().cpu().contiguous()
+        r = {}
+        idx = [i % n for i in images]
+        xi, gyi = x[idx].double().cpu().contiguous(), gy[idx].double().cpu().contiguous()
+        ry = F.conv2d(xi, wc, None, s, p)
+        r["y"] = float((y[idx].double().cpu() - ry).norm() / ry.norm())
+        rgx = torch.ops.aten.convolution_backward(gyi, xi, wc, None, [s, s], [p, p], [1, 1], False, [0, 0], 1,
+                                                  [True, False, False])[0]
+        r["gx"] = float((gx[idx].double().cpu() - rgx).norm() / rgx.norm())
+        pick = [tuple(int(torch.randint(0, m, (1,), generator=gen)) for m in (k, c, ks, ks)) for _ in range(samples)]
+        got, ref = [], []
+        for (co, ci, ky, kx) in pick:
+            g = gy[:, co].double().cpu()
+            xs = F.pad(x[:, ci].double().cpu(), (p, p, p, p))
+            o = g.shape[-1]
+            xs = xs[:, ky:ky + s * (o - 1) + 1:s, kx:kx + s * (o - 1) + 1:s]
+            ref.append(float((g * xs).sum()))
+            got.append(float(gw[co, ci, ky, kx]))
+        got, ref = torch.tensor(got, dtype=torch.float64), torch.tensor(ref, dtype=torch.float64)
+        r["gw"] = float((got - ref).norm() / ref.norm())
+        out[name] = {key: float(f"{v:.2e}") for key, v in r.items()}
+    return out
 
 
 def c1_sub_object(dev, steps, warmup, cpu):
@@ -991,6 +1086,10 @@ def main():
         "per_direction": sw["per_direction"],
         "per_layer_tflops": sw["per_layer_tflops"],
         "plans": {"tuned": not args.no_tune, "tile_slices": sw["plans"]},
+        "parity": {"what": "outputs of the timed plans on the same inputs against PyTorch CPU float64: y and gx on "
+                           "images 0 and N-1, 24 random entries of gw (whole-batch sums); rel-L2, bound 1e-4",
+                   "max_rel_l2": max(v for d in sw["rel_l2_vs_torch_cpu"].values() for v in d.values()),
+                   "per_layer": sw["rel_l2_vs_torch_cpu"]},
         "device": torch.cuda.get_device_name(dev),
     }
     if args.workload == "c5" and not args.no_nhwc:
@@ -1001,7 +1100,8 @@ def main():
                       "through the channels-last kernels",
             "value": round(nw["value"], 3), "unit": "TFLOP/s", "frac_of_peak": round(nw["value"] * 1e12 / PEAK_FP32_MFMA, 4),
             "ms_per_step": round(nw["ms_per_step"], 3), "per_direction": nw["per_direction"],
-            "per_layer_tflops": nw["per_layer_tflops"], "plans": nw["plans"]}
+            "per_layer_tflops": nw["per_layer_tflops"], "plans": nw["plans"],
+            "parity_max_rel_l2": max(v for d in nw["rel_l2_vs_torch_cpu"].values() for v in d.values())}
     if not args.no_cpu:
         print("cpu baselines ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = torch_cpu_baseline(layers, batch=16)

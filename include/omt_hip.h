@@ -127,6 +127,19 @@ int omt_event_query(void* ev);             /* 1 = complete, 0 = pending, <0 = er
 int omt_event_sync(void* ev);
 int omt_event_elapsed_ms(void* start, void* end, float* ms);
 
+/* ---- per-kernel launch counts and timings (replace kcount / ktime, kernel_counts / kernel_times /
+ * debug_time_kernels: csrc/runtime.cpp:570-610, csrc/module.cpp:30-33) ---------------------------------------------
+ * Every launch is counted under its kernel's name. With timing on, each launch is followed by a device
+ * synchronization and the wall time since the previous one is added to the kernel: a debug measurement that
+ * serializes the program (not for code under stream capture). omt_kernel_stat_count merges the counters by name into a
+ * snapshot (name order) and returns its size; omt_kernel_stat_entry reads entry i of it (the name stays valid until the
+ * next omt_kernel_stat_count or reset). omt_kernel_stats_reset zeroes the launch counts and / or the times (bits). */
+enum { OMT_KSTAT_LAUNCHES = 1, OMT_KSTAT_TIMES = 2 };
+void omt_set_kernel_timing(int on);
+void omt_kernel_stats_reset(int what);
+int omt_kernel_stat_count(void);
+int omt_kernel_stat_entry(int i, const char** name, int64_t* launches, double* ms);
+
 /* ---- dense convolution (implicit GEMM on fp32 MFMA) ------------------------------------------------------- */
 
 /* Forward: y[n][co][oh][ow] = sum_{ci,ky,kx} x[n][ci][oy*s+ky-p][ox*s+kx-p] * w[co][ci][ky][kx], then
@@ -288,13 +301,13 @@ int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts,
 /* omt_bn_train_fwd_res with the statistics from omt_conv_fwd_stats (stats [c][groups][2] over x = that call's y):
  * one launch reduces each channel's groups to a few partial sums (in a fixed order, into the workspace of
  * omt_bn_train_workspace's size), the next finalizes mean / invstd and the running statistics as it applies, so x is
- * read once. The variance is E[x^2] - E[x]^2 in double (the sums are unshifted). No counterpart in the reference (see
- * omt_conv_fwd_stats). */
+ * read once. The variance is E[x^2] - E[x]^2 in double (the sums are unshifted). c * groups * 2 doubles must fit in
+ * stats_bytes (OMT_INVALID otherwise, before any launch). No counterpart in the reference (see omt_conv_fwd_stats). */
 int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats, int groups,
-                           const float* gamma, const float* beta, const float* running_mean, const float* running_var,
-                           double momentum, double eps, int relu, const float* residual, float* y, float* save_mean,
-                           float* save_invstd, float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           size_t stats_bytes, const float* gamma, const float* beta, const float* running_mean,
+                           const float* running_var, double momentum, double eps, int relu, const float* residual,
+                           float* y, float* save_mean, float* save_invstd, float* new_rm, float* new_rv,
+                           void* workspace, size_t workspace_bytes, void* stream);
 /* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
  * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
 int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
@@ -361,9 +374,18 @@ enum {
   OMT_PW_HARDSIGMOID = 6,     /* hardsigmoid(a) */
   OMT_PW_HARDSIGMOID_BWD = 7, /* gradient a at input b */
   OMT_PW_SCALE = 8,           /* a * alpha */
-  OMT_PW_FILL = 9             /* alpha (a, b unused) */
+  OMT_PW_FILL = 9,            /* alpha (a, b unused) */
+  OMT_PW_ADD_SCALAR = 10      /* a + alpha */
 };
 int omt_pointwise(int op, int64_t n, const float* a, const float* b, float alpha, float* out, void* stream);
+/* t += value for each of `count` small contiguous tensors (ptrs[i], numels[i] elements, at most
+ * OMT_FOREACH_MAX_NUMEL each; host arrays) in one launch per 64 tensors: dtype OMT_DT_F32 adds fvalue, OMT_DT_I64 adds
+ * ivalue. The optimizers' step counts and BatchNorm's batch counters. Replaces the reference's _foreach_* handling,
+ * which loops the per-tensor add on the device (csrc/device.cpp:220-225). */
+enum { OMT_DT_F32 = 0, OMT_DT_I64 = 1 };
+#define OMT_FOREACH_MAX_NUMEL (1 << 16)
+int omt_foreach_add_scalar(int count, void* const* ptrs, const int64_t* numels, int dtype, int64_t ivalue,
+                           float fvalue, void* stream);
 /* Squeeze-excite channel scale: y[p][i] = x[p][i] * scale[p] over `planes` planes (n * c) of hw elements. */
 int omt_channel_scale(int64_t planes, int64_t hw, const float* x, const float* scale, float* y, void* stream);
 /* y[p][i] = v[p] * scale: a per-plane value broadcast over its plane (the gradient of a plane mean). */

@@ -886,7 +886,7 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
 }
 
 OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats,
-                                      int groups, const float* gamma, const float* beta, const float* running_mean,
+                                      int groups, size_t stats_bytes, const float* gamma, const float* beta, const float* running_mean,
                                       const float* running_var, double momentum, double eps, int relu,
                                       const float* residual, float* y, float* save_mean, float* save_invstd,
                                       float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
@@ -894,6 +894,9 @@ OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const fl
   if (!x || !stats || !gamma || !beta || !y || !save_mean || !save_invstd)
     return fail(OMT_INVALID, "omt_bn_train_fwd_stats: null pointer");
   if (groups < 1) return fail(OMT_INVALID, "omt_bn_train_fwd_stats: %d column groups", groups);
+  if (c < 0 || (uint64_t)c * (uint64_t)groups * 2 * sizeof(double) > stats_bytes)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_stats: %d groups of %lld channels exceed the %zu-byte stats buffer",
+                groups, (long long)c, stats_bytes);
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_stats: size not covered");
   if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
     return fail(OMT_INVALID, "omt_bn_train_fwd_stats: workspace too small");

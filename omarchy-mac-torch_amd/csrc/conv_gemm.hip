@@ -2674,8 +2674,14 @@ static int scratch_of_current_device(void** out) {
   if (dev < 0 || dev >= kMaxScratchDevices) return fail(OMT_INVALID, "omt_conv_wgrad_noalloc: device %d", dev);
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // a first call may come under stream capture: the lookup runs in relaxed capture mode, which lets this thread
+    // make the (non-stream) runtime call while a capture is in progress, then the caller's mode is restored
     void* p = nullptr;
-    OMT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    OMT_HIP(hipThreadExchangeStreamCaptureMode(&mode));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    OMT_HIP(hipThreadExchangeStreamCaptureMode(&mode));
+    OMT_HIP(e);
     if (!p) return fail(OMT_DEVICE_ERROR, "omt_conv_wgrad_noalloc: no address for the scratch array on device %d", dev);
     g_scratch_ptr[dev] = p;
   }

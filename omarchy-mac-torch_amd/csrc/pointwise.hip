@@ -35,6 +35,7 @@ __device__ __forceinline__ float pw_apply(float a, float b, float alpha) {
   if constexpr (OP == OMT_PW_HARDSIGMOID) return hardsigmoid_f(a);
   if constexpr (OP == OMT_PW_HARDSIGMOID_BWD) return hardsigmoid_grad(a, b);
   if constexpr (OP == OMT_PW_SCALE) return a * alpha;
+  if constexpr (OP == OMT_PW_ADD_SCALAR) return a + alpha;
   return alpha;  // OMT_PW_FILL
 }
 
@@ -42,7 +43,8 @@ __device__ __forceinline__ float pw_apply(float a, float b, float alpha) {
 template <int OP, int VEC>
 __global__ void __launch_bounds__(256) pointwise_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                         float* __restrict__ out, int64_t n, float alpha) {
-  constexpr bool UNARY = OP == OMT_PW_RELU || OP == OMT_PW_HARDSWISH || OP == OMT_PW_HARDSIGMOID || OP == OMT_PW_SCALE;
+  constexpr bool UNARY = OP == OMT_PW_RELU || OP == OMT_PW_HARDSWISH || OP == OMT_PW_HARDSIGMOID ||
+                         OP == OMT_PW_SCALE || OP == OMT_PW_ADD_SCALAR;
   constexpr bool NULLARY = OP == OMT_PW_FILL;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x, t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if constexpr (VEC == 4) {
@@ -299,6 +301,20 @@ __global__ void __launch_bounds__(256) nll_bwd_kernel(const float* __restrict__ 
   }
 }
 
+// t += value over a list of small tensors (step counts, batch counters), one wave per tensor; the table travels in
+// the kernel arguments, so a captured graph replays it unchanged.
+constexpr int kForeachMax = 64;
+struct ForeachTable {
+  void* ptr[kForeachMax];
+  int64_t numel[kForeachMax];
+};
+template <class T>
+__global__ void __launch_bounds__(64) foreach_add_kernel(ForeachTable tab, T value) {
+  T* p = static_cast<T*>(tab.ptr[blockIdx.x]);
+  const int64_t n = tab.numel[blockIdx.x];
+  for (int64_t i = threadIdx.x; i < n; i += 64) p[i] += value;
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <int OP>
@@ -334,9 +350,36 @@ OMT_EXPORT int omt_pointwise(int op, int64_t n, const float* a, const float* b, 
     case OMT_PW_HARDSIGMOID_BWD: launch_pw<OMT_PW_HARDSIGMOID_BWD>(n, a, b, alpha, out, s); break;
     case OMT_PW_SCALE: launch_pw<OMT_PW_SCALE>(n, a, nullptr, alpha, out, s); break;
     case OMT_PW_FILL: launch_pw<OMT_PW_FILL>(n, nullptr, nullptr, alpha, out, s); break;
+    case OMT_PW_ADD_SCALAR: launch_pw<OMT_PW_ADD_SCALAR>(n, a, nullptr, alpha, out, s); break;
     default: return fail(OMT_INVALID, "omt_pointwise: op %d", op);
   }
   return launch_check("pointwise_kernel");
+}
+
+OMT_EXPORT int omt_foreach_add_scalar(int count, void* const* ptrs, const int64_t* numels, int dtype, int64_t ivalue,
+                                      float fvalue, void* stream) {
+  if (count < 0 || (count > 0 && (!ptrs || !numels))) return fail(OMT_INVALID, "omt_foreach_add_scalar: arguments");
+  if (dtype != OMT_DT_F32 && dtype != OMT_DT_I64) return fail(OMT_INVALID, "omt_foreach_add_scalar: dtype %d", dtype);
+  for (int i = 0; i < count; ++i)
+    if (numels[i] < 0 || (numels[i] > 0 && !ptrs[i]) || numels[i] > OMT_FOREACH_MAX_NUMEL)
+      return fail(OMT_INVALID, "omt_foreach_add_scalar: tensor %d (numel %lld)", i, (long long)numels[i]);
+  hipStream_t s = stream_of(stream);
+  for (int i0 = 0; i0 < count; i0 += kForeachMax) {
+    ForeachTable tab{};
+    int k = 0;
+    for (int i = i0; i < count && i < i0 + kForeachMax; ++i) {
+      if (numels[i] == 0) continue;
+      tab.ptr[k] = ptrs[i];
+      tab.numel[k++] = numels[i];
+    }
+    if (k == 0) continue;
+    if (dtype == OMT_DT_F32)
+      hipLaunchKernelGGL((foreach_add_kernel<float>), dim3(k), dim3(64), 0, s, tab, fvalue);
+    else
+      hipLaunchKernelGGL((foreach_add_kernel<int64_t>), dim3(k), dim3(64), 0, s, tab, ivalue);
+    if (int st = launch_check("foreach_add_kernel")) return st;
+  }
+  return OMT_OK;
 }
 
 static int plane_scale(int64_t planes, int64_t hw, const float* x, const float* sv, float scale, float* y,

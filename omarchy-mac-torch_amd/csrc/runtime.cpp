@@ -18,6 +18,8 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
+#include <string>
 #include <map>
 #include <mutex>
 #include <unordered_map>
@@ -46,9 +48,38 @@ int hip_check(hipError_t e, const char* what) {
   return fail(OMT_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
 }
 
+// ---- per-kernel launch counts and timings ----------------------------------------------------------------------
+//
+// Every launch site reports its kernel's name through launch_check; the counts are kept per name pointer (the
+// literals of one translation unit) and merged by name when read. With timing on, each report first synchronizes the
+// device and adds the wall time since the previous report to the kernel: that launch's enqueue and run, a debug
+// measurement that serializes the program (the reference times each dispatch the same way, re-running it after a
+// synchronization, csrc/runtime.cpp:573-610).
+namespace {
+struct KernelStat {
+  int64_t launches = 0;
+  double ms = 0;
+};
+std::mutex g_kstat_mu;
+std::unordered_map<const char*, KernelStat> g_kstats;
+std::vector<std::pair<std::string, KernelStat>> g_kstat_view;  // merged by name at omt_kernel_stat_count
+std::atomic<bool> g_ktime{false};
+std::chrono::steady_clock::time_point g_klast;
+}  // namespace
+
 int launch_check(const char* kernel) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(OMT_DEVICE_ERROR, "launch of %s failed: %s", kernel, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_kstat_mu);
+  KernelStat& st = g_kstats[kernel];
+  ++st.launches;
+  if (g_ktime.load(std::memory_order_relaxed)) {
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(OMT_DEVICE_ERROR, "%s: %s", kernel, hipGetErrorString(e));
+    const auto now = std::chrono::steady_clock::now();
+    st.ms += std::chrono::duration<double, std::milli>(now - g_klast).count();
+    g_klast = now;
+  }
   return OMT_OK;
 }
 
@@ -187,7 +218,7 @@ bool capturing(hipStream_t s) {
 using namespace omt;
 
 OMT_EXPORT const char* omt_last_error(void) { return t_last_error.c_str(); }
-OMT_EXPORT int omt_abi_version(void) { return 3; }
+OMT_EXPORT int omt_abi_version(void) { return 4; }
 OMT_EXPORT int omt_hip_runtime_version(void) {
   int v = 0;
   (void)hipRuntimeGetVersion(&v);
@@ -453,4 +484,45 @@ OMT_EXPORT int omt_conv_kind(int64_t x_c, int64_t w_o, int64_t kh, int64_t kw, i
   if (depthwise && (ks == 3 || ks == 5 || ks == 7) && s == 1 && p == ks / 2) return OMT_CONV_DW;
   if (depthwise && geo_ok) return OMT_CONV_DWG;
   return OMT_CONV_NONE;
+}
+
+OMT_EXPORT void omt_set_kernel_timing(int on) {
+  std::lock_guard<std::mutex> lk(g_kstat_mu);
+  if (on) {
+    (void)hipDeviceSynchronize();
+    g_klast = std::chrono::steady_clock::now();
+  }
+  g_ktime.store(on != 0);
+}
+
+OMT_EXPORT void omt_kernel_stats_reset(int what) {
+  std::lock_guard<std::mutex> lk(g_kstat_mu);
+  for (auto& kv : g_kstats) {
+    if (what & OMT_KSTAT_LAUNCHES) kv.second.launches = 0;
+    if (what & OMT_KSTAT_TIMES) kv.second.ms = 0;
+  }
+  g_kstat_view.clear();
+  if (g_ktime.load()) g_klast = std::chrono::steady_clock::now();
+}
+
+OMT_EXPORT int omt_kernel_stat_count(void) {
+  std::lock_guard<std::mutex> lk(g_kstat_mu);
+  std::map<std::string, KernelStat> merged;
+  for (const auto& [name, st] : g_kstats) {
+    KernelStat& m = merged[name];
+    m.launches += st.launches;
+    m.ms += st.ms;
+  }
+  g_kstat_view.assign(merged.begin(), merged.end());
+  return (int)g_kstat_view.size();
+}
+
+OMT_EXPORT int omt_kernel_stat_entry(int i, const char** name, int64_t* launches, double* ms) {
+  std::lock_guard<std::mutex> lk(g_kstat_mu);
+  if (i < 0 || i >= (int)g_kstat_view.size() || !name || !launches || !ms)
+    return fail(OMT_INVALID, "omt_kernel_stat_entry: entry %d of %zu", i, g_kstat_view.size());
+  *name = g_kstat_view[i].first.c_str();
+  *launches = g_kstat_view[i].second.launches;
+  *ms = g_kstat_view[i].second.ms;
+  return OMT_OK;
 }

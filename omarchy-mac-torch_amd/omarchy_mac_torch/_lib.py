@@ -18,7 +18,9 @@ OMT_EPI_BIAS, OMT_EPI_RELU = 1, 2
 OMT_DIR_FWD, OMT_DIR_DGRAD, OMT_DIR_WGRAD, OMT_DIR_FWD_NHWC, OMT_DIR_DGRAD_NHWC, OMT_DIR_WGRAD_NHWC = range(6)
 NOALLOC_SCRATCH_BYTES = 64 << 20  # OMT_NOALLOC_SCRATCH_BYTES
 (OMT_PW_ADD, OMT_PW_MUL, OMT_PW_RELU, OMT_PW_THRESHOLD_BWD, OMT_PW_HARDSWISH, OMT_PW_HARDSWISH_BWD, OMT_PW_HARDSIGMOID,
- OMT_PW_HARDSIGMOID_BWD, OMT_PW_SCALE, OMT_PW_FILL) = range(10)
+ OMT_PW_HARDSIGMOID_BWD, OMT_PW_SCALE, OMT_PW_FILL, OMT_PW_ADD_SCALAR) = range(11)
+OMT_DT_F32, OMT_DT_I64 = 0, 1
+FOREACH_MAX_NUMEL = 1 << 16  # OMT_FOREACH_MAX_NUMEL
 
 
 class ConvGeo(ctypes.Structure):
@@ -82,6 +84,11 @@ PL = ctypes.POINTER(ConvPlan)
 SIGNATURES = {
     "omt_last_error": (ctypes.c_char_p, []),
     "omt_abi_version": (I32, []),
+    "omt_set_kernel_timing": (None, [I32]),
+    "omt_kernel_stats_reset": (None, [I32]),
+    "omt_kernel_stat_count": (I32, []),
+    "omt_kernel_stat_entry": (I32, [I32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(I64),
+                                    ctypes.POINTER(F64)]),
     "omt_hip_runtime_version": (I32, []),
     "omt_conv_geo_init": (None, [G, I64, I64, I64, I64, I64, I64, I64, I64]),
     "omt_conv_kind": (I32, [I64] * 10 + [I32, I64]),
@@ -124,6 +131,8 @@ SIGNATURES = {
     "omt_conv_wgrad_nhwc_workspace": (SZ, [G]),
     "omt_conv_wgrad_nhwc": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_pointwise": (I32, [ctypes.c_int, I64, VP, VP, ctypes.c_float, VP, VP]),
+    "omt_foreach_add_scalar": (I32, [ctypes.c_int, ctypes.POINTER(VP), ctypes.POINTER(I64), ctypes.c_int, I64,
+                                     ctypes.c_float, VP]),
     "omt_channel_scale": (I32, [I64, I64, VP, VP, VP, VP]),
     "omt_plane_broadcast": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
     "omt_plane_sum": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
@@ -153,7 +162,7 @@ SIGNATURES = {
                                    VP]),
     "omt_bn_train_fwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
                                      VP, VP, SZ, VP]),
-    "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
+    "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, SZ, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
                                      VP, VP, SZ, VP]),
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
     "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
@@ -169,7 +178,7 @@ SIGNATURES = {
     "omt_fused_sgd": (I32, [ctypes.POINTER(SgdParams), ctypes.POINTER(SgdTensor), I32, VP]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def _load():

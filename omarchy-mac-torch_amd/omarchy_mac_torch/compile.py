@@ -20,7 +20,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
      where the BatchNorm sums a K-split convolution's partials itself (no slice-sum launch).
 
 Each omt op falls back to its plain aten composition when the device kernels do not cover the case, so a rewritten
-graph is always correct. OMARCHY_MAC_TORCH_COMPILE_DEBUG=1 prints what each rewrite did. (The reference's fourth
+graph is always correct. The rewritten graphs then run as HIP graphs: a few calls op by op, then captured once and
+replayed (omarchy_mac_torch/replay.py; OMARCHY_MAC_TORCH_COMPILE_GRAPHS=0 keeps them op by op).
+OMARCHY_MAC_TORCH_COMPILE_DEBUG=1 prints what each rewrite did. (The reference's fourth
 pass, generated pointwise kernels, is elementwise work outside the convolution path.)
 """
 
@@ -32,6 +34,7 @@ from torch._dynamo import register_backend
 from torch._dynamo.backends.common import aot_autograd
 from torch.fx import Node
 
+from omarchy_mac_torch import replay
 from omarchy_mac_torch.native import DEVICE
 
 aten = torch.ops.aten
@@ -105,10 +108,10 @@ def _same_shape(a, b):
 
 def fuse_bn_train_in_place(graph):
     count = {"bn": 0, "relu": 0, "add_relu": 0}
-    order = {n: i for i, n in enumerate(graph.nodes)}
     for n in list(graph.nodes):
         if n.op != "call_function" or n.target is not aten._native_batch_norm_legit_functional.default:
             continue
+        order = {v: i for i, v in enumerate(graph.nodes)}  # fresh: earlier rewrites inserted nodes
         x, w, b, rm, rv, training, momentum, eps = n.args[:8]
         if not training or any(a is None for a in (w, b, rm, rv)) or not _on_device_f32(x, 4):
             continue
@@ -325,10 +328,10 @@ def fuse_conv_bn_train(graph):
     output is the convolution's (the BatchNorm backward reads it): with a K-split plan the BatchNorm sums the
     convolution's partials itself (one launch fewer). The convolution's other uses must come after the BatchNorm."""
     count = 0
-    order = {n: i for i, n in enumerate(graph.nodes)}
     for n in list(graph.nodes):
         if n.op != "call_function" or n.target is not omt.bn_train_.default:
             continue
+        order = {v: i for i, v in enumerate(graph.nodes)}  # fresh: earlier rewrites inserted nodes
         conv = n.args[0]
         if not (isinstance(conv, Node) and _is_dense_conv(conv) and conv.args[2] is None):
             continue
@@ -347,7 +350,7 @@ def fuse_conv_bn_train(graph):
     return count
 
 
-def _compile(gm, example_inputs):
+def _rewrite(gm):
     g = gm.graph
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
              "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
@@ -358,11 +361,17 @@ def _compile(gm, example_inputs):
     gm.recompile()
     if _DEBUG:
         print("[omarchy-mac-torch compile]", stats)
-    from functorch.compile import make_boxed_func
-    return make_boxed_func(gm.forward)
+    return gm
 
 
-# buffer mutations stay in the graph (as copy_ into the inputs) so that rewrite 0 can turn them into in-place updates
-backend = aot_autograd(fw_compiler=_compile, bw_compiler=_compile, inference_compiler=_compile,
-                       keep_inference_input_mutations=True)
+def _compiler(kind):
+    def compile_graph(gm, example_inputs):
+        return replay.wrap(_rewrite(gm).forward, kind)
+    return compile_graph
+
+
+# buffer mutations stay in the graph (as copy_ into the inputs) so that rewrite 0 can turn them into in-place updates;
+# every rewritten graph is replayed as a HIP graph after its warm-up calls (replay.py)
+backend = aot_autograd(fw_compiler=_compiler("forward"), bw_compiler=_compiler("backward"),
+                       inference_compiler=_compiler("inference"), keep_inference_input_mutations=True)
 register_backend(name=DEVICE)(backend)

@@ -336,7 +336,8 @@ def batch_norm_train_stats(x, stats, groups, gamma, beta, running_mean=None, run
     sm = torch.empty((c,), device=x.device, dtype=torch.float32)
     si = torch.empty_like(sm)
     ws, nb = _workspace(L.omt_bn_train_workspace(n, c, h * w), x.device)
-    check(L.omt_bn_train_fwd_stats(n, c, h * w, _ptr(x), _ptr(stats), int(groups), _ptr(gamma), _ptr(beta),
+    check(L.omt_bn_train_fwd_stats(n, c, h * w, _ptr(x), _ptr(stats), int(groups), stats.numel() * 8, _ptr(gamma),
+                                   _ptr(beta),
                                    _ptr(running_mean), _ptr(running_var), momentum, eps, int(relu), _ptr(residual),
                                    _ptr(y), _ptr(sm), _ptr(si), _ptr(running_mean), _ptr(running_var), _ptr(ws), nb,
                                    _stream(x.device)), "batch_norm_train_stats")

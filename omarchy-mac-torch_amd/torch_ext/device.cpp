@@ -441,9 +441,11 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("view_as_complex", &at::native::view_as_complex);
   // torch's _foreach_* ops carry a CompositeExplicitAutograd kernel that loops over the list one tensor at a time;
   // for this key it would win over the boxed fallback and cost one delegated op per tensor. Registered here, each list
-  // op goes to torch's HIP kernels whole (one multi-tensor launch).
+  // op goes to torch's HIP kernels whole (one multi-tensor launch). _foreach_add_.Scalar has a kernel of this library
+  // (pointwise.cpp: step counts and batch counters), registered there instead.
   for (const c10::OperatorName& op : c10::Dispatcher::singleton().getAllOpNames()) {
     if (op.name.rfind("aten::_foreach_", 0) != 0) continue;
+    if (op.name == "aten::_foreach_add_" && op.overload_name == "Scalar") continue;
     const std::string name = op.name.substr(6) + (op.overload_name.empty() ? "" : "." + op.overload_name);
     m.impl(name.c_str(), torch::CppFunction::makeFromBoxedFunction<&hip_fallback>());
   }

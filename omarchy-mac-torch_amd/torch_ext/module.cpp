@@ -8,6 +8,7 @@
 namespace omt {
 void bind_plans(pybind11::module_& m);
 void bind_tuning(pybind11::module_& m);
+void bind_replay(pybind11::module_& m);
 }
 
 PYBIND11_MODULE(_native, m) {
@@ -58,9 +59,33 @@ PYBIND11_MODULE(_native, m) {
     OMT_LOCK;
     force_next_sync_error(msg);
   });
+  // per-kernel launch counts and timings, as the reference's kernel_counts / kernel_times / debug_time_kernels
+  // (csrc/module.cpp:30-33): {kernel name: launches} and {kernel name: ms}, each optionally reset after reading
+  auto kernel_stats = [](int what, bool reset) {
+    std::map<std::string, double> out;
+    const int n = omt_kernel_stat_count();
+    for (int i = 0; i < n; ++i) {
+      const char* name = nullptr;
+      int64_t launches = 0;
+      double ms = 0;
+      if (omt_kernel_stat_entry(i, &name, &launches, &ms) != OMT_OK) break;
+      if (what == OMT_KSTAT_LAUNCHES ? launches > 0 : ms > 0) out[name] = what == OMT_KSTAT_LAUNCHES ? launches : ms;
+    }
+    if (reset) omt_kernel_stats_reset(what);
+    return out;
+  };
+  m.def("kernel_counts", [kernel_stats](bool reset) {
+    std::map<std::string, int64_t> out;
+    for (const auto& [k, v] : kernel_stats(OMT_KSTAT_LAUNCHES, reset)) out[k] = (int64_t)v;
+    return out;
+  }, pybind11::arg("reset") = false);
+  m.def("kernel_times", [kernel_stats](bool reset) { return kernel_stats(OMT_KSTAT_TIMES, reset); },
+        pybind11::arg("reset") = false);
+  m.def("debug_time_kernels", [](bool on) { omt_set_kernel_timing(on ? 1 : 0); });
   m.def("abi_version", []() { return omt_abi_version(); });
   m.def("hip_runtime_version", []() { return omt_hip_runtime_version(); });
   m.attr("built_with_torch") = TORCH_VERSION;
   bind_plans(m);
   bind_tuning(m);
+  bind_replay(m);
 }

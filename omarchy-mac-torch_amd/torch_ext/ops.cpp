@@ -502,7 +502,8 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor
                                       wsptr(ws), wsbytes(ws), cur_stream());
     if (st == OMT_OK) {
       Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
-      check(omt_bn_train_fwd_stats(n, c, hw, fp(conv), (const double*)wsptr(stats), groups, fp(w), fp(b), fp(rm),
+      check(omt_bn_train_fwd_stats(n, c, hw, fp(conv), (const double*)wsptr(stats), groups, wsbytes(stats), fp(w),
+                                   fp(b), fp(rm),
                                    fp(rv), mom, eps, relu, r, fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws),
                                    wsbytes(bws), cur_stream()),
             "omt::conv_bn_train_ (BatchNorm from the epilogue statistics)");

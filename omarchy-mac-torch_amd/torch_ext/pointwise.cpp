@@ -2,9 +2,10 @@
 // and loss entry points: residual add, ReLU / hardswish / hardsigmoid and their gradients, the squeeze-excite channel
 // scale, plane means and sums (AdaptiveAvgPool2d(1) lowers to mean over the last two dims) and their gradients, a
 // linear layer's bias gradient, log-softmax and the NLL loss. Reference counterparts: csrc/elementwise.cpp:702-817
-// (registrations), csrc/reduce.cpp:128-202 (softmax, nll_loss). The linear layers' matrix products (addmm, mm) stay
-// on torch's hipBLASLt GEMMs. Calls these kernels do not cover (other dtypes, broadcasts, layouts) run on torch's HIP
-// kernels, like every op without a kernel here.
+// (registrations), csrc/reduce.cpp:128-202 (softmax, nll_loss); the scalar adds of the optimizers' step counts and
+// BatchNorm's batch counters (the reference loops _foreach_ ops over its per-tensor kernels, csrc/device.cpp:220-225).
+// The linear layers' matrix products are in linalg.cpp. Calls these kernels do not cover (other dtypes, broadcasts,
+// layouts) run on torch's HIP kernels, like every op without a kernel here.
 #include "omt_torch.h"
 
 namespace omt {
@@ -41,15 +42,59 @@ Tensor binary(int op, const Tensor& a, const Tensor& b, float alpha = 0.f) {
 
 // ---- pointwise ----
 
+bool real(const at::Scalar& v) { return v.isFloatingPoint() || v.isIntegral(false); }
+
+// t += v for contiguous int64 / float32 device tensors of at most OMT_FOREACH_MAX_NUMEL elements (counters, steps)
+void add_small(at::TensorList ts, const at::Scalar& v) {
+  cover(!ts.empty(), "non-empty list");
+  const at::ScalarType dt = ts[0].scalar_type();
+  cover((dt == at::kLong && v.isIntegral(false)) || (dt == at::kFloat && real(v)), "int64 or float32 tensors");
+  std::vector<void*> ptrs;
+  std::vector<int64_t> numels;
+  for (const Tensor& t : ts) {
+    cover(is_dev(t) && t.scalar_type() == dt && t.is_contiguous() && t.numel() <= OMT_FOREACH_MAX_NUMEL,
+          "small contiguous device tensors of one dtype");
+    ptrs.push_back(t.numel() ? t.data_ptr() : nullptr);
+    numels.push_back(t.numel());
+  }
+  check(omt_foreach_add_scalar((int)ts.size(), ptrs.data(), numels.data(), dt == at::kLong ? OMT_DT_I64 : OMT_DT_F32,
+                               dt == at::kLong ? v.toLong() : 0, dt == at::kFloat ? v.toFloat() : 0.f, cur_stream()),
+        "add (scalar)");
+}
+
 Tensor add_t(const Tensor& a, const Tensor& b, const at::Scalar& alpha) {
-  cover(alpha.isFloatingPoint() || alpha.isIntegral(false), "real alpha");
+  cover(real(alpha), "real alpha");
+  if (host_scalar(b) && dense(a) && b.is_floating_point())  // a + alpha * b with b a number
+    return unary(OMT_PW_ADD_SCALAR, a, (float)(alpha.toDouble() * b.item<double>()));
   return binary(OMT_PW_ADD, a, b, alpha.toFloat());
 }
 Tensor& add_t_(Tensor& a, const Tensor& b, const at::Scalar& alpha) {
-  cover(same(a, b) && (alpha.isFloatingPoint() || alpha.isIntegral(false)), "contiguous float32, one shape");
+  cover(real(alpha), "real alpha");
+  if (host_scalar(b) && is_dev(a)) {  // a += alpha * b with b a number (BatchNorm's num_batches_tracked.add_(1))
+    if (a.scalar_type() == at::kLong && alpha.isIntegral(false) && !b.is_floating_point()) {
+      add_small({a}, b.item<int64_t>() * alpha.toLong());
+      return a;
+    }
+    cover(dense(a), "contiguous float32");
+    pw(OMT_PW_ADD_SCALAR, a, nullptr, (float)(alpha.toDouble() * b.item<double>()), a);
+    return a;
+  }
+  cover(same(a, b), "contiguous float32, one shape");
   pw(OMT_PW_ADD, a, &b, alpha.toFloat(), a);
   return a;
 }
+Tensor& add_s_(Tensor& a, const at::Scalar& v, const at::Scalar& alpha) {
+  cover(real(v) && real(alpha), "real operands");
+  if (a.scalar_type() == at::kLong && v.isIntegral(false) && alpha.isIntegral(false)) {
+    add_small({a}, v.toLong() * alpha.toLong());
+    return a;
+  }
+  cover(dense(a), "contiguous float32");
+  pw(OMT_PW_ADD_SCALAR, a, nullptr, (float)(v.toDouble() * alpha.toDouble()), a);
+  return a;
+}
+// torch._foreach_add_(tensors, scalar): the optimizers' step counts, the compiled graph's merged batch counters
+void foreach_add_s_(at::TensorList ts, const at::Scalar& v) { add_small(ts, v); }
 
 // x [N, C, H, W] times s [N, C, 1, 1] (squeeze-excite, and the gradient of that product with respect to x)
 bool channel_pair(const Tensor& big, const Tensor& s) {
@@ -207,6 +252,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   HotOps(m)
       .aux<at::_ops::add_Tensor, &add_t>()
       .aux<at::_ops::add__Tensor, &add_t_>()
+      .aux<at::_ops::add__Scalar, &add_s_>()
+      .aux<at::_ops::_foreach_add__Scalar, &foreach_add_s_>()
       .aux<at::_ops::mul_Tensor, &mul_t>()
       .aux<at::_ops::div_Tensor, &div_t>()
       .aux<at::_ops::relu, &relu_>()

@@ -168,7 +168,8 @@ def test_batch_chunks_host_side():
 def test_epilogue_statistics_validation_host_side():
     """omt_conv_fwd_stats / omt_bn_train_fwd_stats reject bad arguments on the host, before any launch: null
     pointers, a statistics buffer smaller than omt_conv_fwd_stats_bytes (one pair per channel and 32 output pixels), a
-    plan that splits K, a batch that would run in chunks, and zero column groups."""
+    plan that splits K, a batch that would run in chunks, zero column groups, and more column groups than the
+    statistics buffer holds."""
     from omarchy_mac_torch import _lib
     L = _lib.L
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
@@ -193,8 +194,9 @@ def test_epilogue_statistics_validation_host_side():
     finally:
         L.omt_conv_clear_plans()
     ws = L.omt_bn_train_workspace(2, 24, 100)
-    args = [2, 24, 100, fake, fake, 3, fake, fake, None, None, 0.1, 1e-5, 1, None, fake, fake, fake, None, None, fake,
-            ws, None]
+    stats_bytes = 24 * 3 * 2 * 8  # 24 channels x 3 column groups x (sum, sum of squares)
+    args = [2, 24, 100, fake, fake, 3, stats_bytes, fake, fake, None, None, 0.1, 1e-5, 1, None, fake, fake, fake, None,
+            None, fake, ws, None]
     bad_groups = list(args)
     bad_groups[5] = 0
     assert L.omt_bn_train_fwd_stats(*bad_groups) == _lib.OMT_INVALID
@@ -202,8 +204,15 @@ def test_epilogue_statistics_validation_host_side():
     no_stats[4] = None
     assert L.omt_bn_train_fwd_stats(*no_stats) == _lib.OMT_INVALID
     small_ws = list(args)
-    small_ws[20] = ws - 8
+    small_ws[21] = ws - 8
     assert L.omt_bn_train_fwd_stats(*small_ws) == _lib.OMT_INVALID
+    small_stats = list(args)  # a stats buffer sized for fewer groups than claimed
+    small_stats[6] = stats_bytes - 8
+    assert L.omt_bn_train_fwd_stats(*small_stats) == _lib.OMT_INVALID
+    assert b"stats buffer" in L.omt_last_error()
+    more_groups = list(args)
+    more_groups[5] = 4
+    assert L.omt_bn_train_fwd_stats(*more_groups) == _lib.OMT_INVALID
 
 
 def test_plan_cache_host_side():

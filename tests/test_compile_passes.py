@@ -239,3 +239,54 @@ def test_conv_bn_train(oc, case):
         torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)
     for i in (5, 6):  # running statistics, updated in place
         torch.testing.assert_close(b[i], a[i], rtol=1e-6, atol=1e-7)
+
+
+def test_conv_bn_train_after_a_rewrite_that_uses_the_conv(oc):
+    """Two bias-free convolutions of x: the first feeds a BatchNorm whose residual is the second convolution's raw
+    output, and the second feeds a BatchNorm of its own. Rewriting the first pair inserts a fused node that uses the
+    second convolution before its BatchNorm, so the second pair must stay as it is (the pass looks nodes up in a fresh
+    order after each rewrite). The rewritten graph gives the original's outputs and running statistics on CPU."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    xs, ys, c = (2, 3, 6, 6), (2, 4, 6, 6), 4
+
+    def ph(name, shape):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape)
+        return n
+
+    x, wa, wb = ph("x", xs), ph("wa", (c, 3, 3, 3)), ph("wb", (c, 3, 3, 3))
+    bn_args = [[ph(f"{k}{j}", (c,)) for k in ("w", "b", "rm", "rv")] for j in (1, 2)]
+    convs = []
+    for w in (wa, wb):
+        cv = g.call_function(aten.convolution.default, (x, w, None, [1, 1], [1, 1], [1, 1], False, [0, 0], 1))
+        cv.meta["val"] = _fake(mode, dev, ys)
+        convs.append(cv)
+    outs = []
+    for (w, b, rm, rv), src, res in zip(bn_args, convs, (convs[1], None)):
+        bn = g.call_function(torch.ops.omt.bn_train_.default, (src, w, b, rm, rv, 0.1, 1e-5, 1, res))
+        for i, shp in enumerate((ys, (c,), (c,))):
+            gi = g.call_function(operator.getitem, (bn, i))
+            gi.meta["val"] = _fake(mode, dev, shp)
+            outs.append(gi)
+    g.output(tuple(outs))
+    gm = GraphModule(torch.nn.Module(), g)
+    ref = copy.deepcopy(gm)
+    assert oc.fuse_conv_bn_train(gm.graph) == 1
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    assert t.count(torch.ops.omt.conv_bn_train_.default) == 1 and t.count(aten.convolution.default) == 1
+    gen = torch.Generator().manual_seed(9)
+    args = [torch.randn(xs, generator=gen), torch.randn(c, 3, 3, 3, generator=gen) * 0.3,
+            torch.randn(c, 3, 3, 3, generator=gen) * 0.3]
+    for _ in range(2):
+        args += [torch.rand(c, generator=gen) + 0.5, torch.randn(c, generator=gen), torch.randn(c, generator=gen),
+                 torch.rand(c, generator=gen) + 0.5]
+    a, b = [v.clone() for v in args], [v.clone() for v in args]
+    for o_ref, o_new in zip(ref(*a), gm(*b)):
+        torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)
+    for i in (5, 6, 9, 10):  # running statistics, updated in place
+        torch.testing.assert_close(b[i], a[i], rtol=1e-6, atol=1e-7)

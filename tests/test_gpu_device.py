@@ -199,7 +199,8 @@ def test_depthwise_bn_pools_through_modules(clean):
 
 
 def test_foreach_lists_and_fused_optimizers(clean):
-    """_foreach_* list ops reach torch's HIP kernels as one delegated op (not one per tensor), and SGD / Adam / AdamW
+    """_foreach_* list ops reach torch's HIP kernels as one delegated op (not one per tensor; _foreach_add_ with a
+    scalar runs on this library's kernel), and SGD / Adam / AdamW
     default to their fused kernels for device parameters (reference omarchy_mac_torch/optim.py), tracking the CPU
     optimizers."""
     omt = clean
@@ -207,13 +208,15 @@ def test_foreach_lists_and_fused_optimizers(clean):
     ds = [D(t, omt) for t in ts]
     omt._native.core.count_delegated(True)
     try:
-        torch._foreach_add_(ds, 2.0)
+        torch._foreach_mul_(ds, 3.0)
         counts = omt._native.core.delegated_counts()
-        assert counts.get("_foreach_add_.Scalar") == 1 and "add_.Tensor" not in counts, counts
+        assert counts.get("_foreach_mul_.Scalar") == 1 and "mul_.Tensor" not in counts, counts
+        torch._foreach_add_(ds, 2.0)  # a kernel of this library: not delegated at all
+        assert omt._native.core.delegated_counts() == counts
     finally:
         omt._native.core.count_delegated(False)
     for t, d in zip(ts, ds):
-        assert torch.equal(d.cpu(), t + 2)
+        assert torch.equal(d.cpu(), t * 3 + 2)
     torch.manual_seed(0)
     for cls, kw in ((torch.optim.SGD, dict(lr=0.1, momentum=0.9)), (torch.optim.Adam, dict(lr=1e-2)),
                     (torch.optim.AdamW, dict(lr=1e-2, weight_decay=0.1))):
@@ -314,7 +317,8 @@ def test_native_fused_adam_grad_scale_and_found_inf(clean, inf):
 def test_graph_replay_of_a_training_step(clean):
     """A whole training step (forward, backward, fused Adam with capturable=True) captured once as a HIP graph and
     replayed on new batches matches the same steps run eagerly, replay after replay, with eager device work and host
-    synchronization between the replays; BN running statistics follow too."""
+    synchronization between the replays; BN running statistics follow too. The replayed losses match PyTorch CPU within
+    1e-3 relative."""
     omt = clean
     torch.manual_seed(7)
     base = nn.Sequential(nn.Conv2d(3, 16, 3, padding=1, bias=False), nn.BatchNorm2d(16), nn.ReLU(), nn.MaxPool2d(2),
@@ -373,6 +377,14 @@ def test_graph_replay_of_a_training_step(clean):
     for (n, ba), (_, bb) in zip(model.named_buffers(), eager.named_buffers()):
         assert rel(ba.float(), bb.float()) <= 1e-5, n
     graph.release()
+    cpu = copy.deepcopy(base)
+    opt_c = torch.optim.Adam(cpu.parameters(), lr=1e-2)
+    for (x, t), a in zip(data, got):
+        opt_c.zero_grad(set_to_none=True)
+        loss = F.cross_entropy(cpu(x), t)
+        loss.backward()
+        opt_c.step()
+        assert abs(a - loss.item()) <= 1e-3 * abs(loss.item()), (got, loss.item())
 
 
 def test_conv_batch_past_2gib_stays_on_hip_kernels(clean):
@@ -455,42 +467,143 @@ def test_plaincnn_five_step_loss_parity(clean, fused):
     assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
 
 
-@pytest.mark.parametrize("name", ["resnet18", "mobilenet_v3_small"])
-def test_config_models_five_step_loss_parity(clean, name):
-    """BASELINE configs 3 and 4 at full size: ResNet-18 (b32, 3x64x64, 1000 classes, Adam lr 1e-3) and the
-    MobileNetV3-Small-style net (b32, 3x224x224, 1000 classes, AdamW lr 1e-3 wd 0.01), five training steps from the
-    same weights and data on the device and on PyTorch CPU: every loss within 1e-3 relative of PyTorch CPU fp32, the
-    tolerance widened at a step by twice PyTorch CPU fp32's own distance from the float64 trajectory there (the size of
-    fp32 summation-order effects, which Adam amplifies from step to step: ResNet-18's fifth loss moves by up to 2e-3
-    between fp32 implementations and plans, CPU fp32 itself lying 1.9e-3 from float64); no fallbacks."""
+def _config(name):
+    """BASELINE config 3 (ResNet-18: b32, 3x64x64, 1000 classes, Adam lr 1e-3) or 4 (the MobileNetV3-Small-style net:
+    b32, 3x224x224, 1000 classes, AdamW lr 1e-3 wd 0.01): (model factory, input shape, optimizer factory)."""
     from omarchy_mac_torch import models
-    omt = clean
     if name == "resnet18":
-        mk, shape = (lambda: models.resnet18(1000)), (32, 3, 64, 64)
-        make_opt = lambda p: torch.optim.Adam(p, lr=1e-3)  # noqa: E731
-    else:
-        mk, shape = (lambda: models.mobilenet_v3_small(1000)), (32, 3, 224, 224)
-        make_opt = lambda p: torch.optim.AdamW(p, lr=1e-3, weight_decay=0.01)  # noqa: E731
+        return (lambda: models.resnet18(1000)), (32, 3, 64, 64), \
+            (lambda p, capturable=False: torch.optim.Adam(p, lr=1e-3, capturable=capturable))
+    return (lambda: models.mobilenet_v3_small(1000)), (32, 3, 224, 224), \
+        (lambda p, capturable=False: torch.optim.AdamW(p, lr=1e-3, weight_decay=0.01, capturable=capturable))
+
+
+def _config_data(name, steps=6):
+    mk, shape, make_opt = _config(name)
     torch.manual_seed(0)
     base = mk()
     g = torch.Generator().manual_seed(1)
-    data = [(torch.randn(*shape, generator=g), torch.randint(0, 1000, (shape[0],), generator=g)) for _ in range(5)]
+    data = [(torch.randn(*shape, generator=g), torch.randint(0, 1000, (shape[0],), generator=g)) for _ in range(steps)]
+    return base, data, make_opt
 
-    def run(device, dtype=torch.float32):
-        model = copy.deepcopy(base).to(device=device, dtype=dtype)
-        opt = make_opt(model.parameters())
-        out = []
-        for x, t in data:
-            opt.zero_grad(set_to_none=True)
-            loss = F.cross_entropy(model(x.to(device=device, dtype=dtype)), t.to(device))
-            loss.backward()
-            opt.step()
-            out.append(loss.item())
-        return out
 
-    dev, cpu, cpu64 = run(omt.DEVICE), run("cpu"), run("cpu", torch.float64)
-    for a, b, c in zip(dev, cpu, cpu64):
-        assert abs(a - b) <= 1e-3 * abs(b) + 2 * abs(b - c), (dev, cpu, cpu64)
+def _train(base, data, make_opt, device, dtype=torch.float32, compiled=False):
+    """Losses of len(data) training steps from a copy of base (one batch per step)."""
+    model = copy.deepcopy(base).to(device=device, dtype=dtype)
+    opt = make_opt(model.parameters())
+    fwd = torch.compile(model, backend=device) if compiled else model
+    out = []
+    for x, t in data:
+        opt.zero_grad(set_to_none=True)
+        loss = F.cross_entropy(fwd(x.to(device=device, dtype=dtype)), t.to(device))
+        loss.backward()
+        opt.step()
+        out.append(loss.item())
+    return out
+
+
+def _train_graphed(base, data, make_opt, device, compiled=False, warmup=3):
+    """The same steps with the whole step (forward, backward, optimizer) captured once as a HIP graph after `warmup`
+    eager steps and replayed for the rest (omarchy_mac_torch.graphs), as the benchmark times it."""
+    from omarchy_mac_torch import graphs, replay
+    model = copy.deepcopy(base).to(device)
+    opt = make_opt(model.parameters(), capturable=True)
+    fwd = torch.compile(model, backend=device) if compiled else model
+    sx, st = torch.empty(data[0][0].shape, device=device), torch.empty(data[0][1].shape, dtype=torch.long, device=device)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = F.cross_entropy(fwd(sx), st)
+        loss.backward()
+        opt.step()
+        return loss.detach()
+
+    out = []
+    prev = replay.set_enabled(False)  # the whole step is captured here, not the compiled graphs alone
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for x, t in data[:warmup]:
+                sx.copy_(x)
+                st.copy_(t)
+                out.append(step().item())
+        torch.cuda.current_stream().wait_stream(side)
+        graph = graphs.Graph()
+        with graph.capture():
+            static_loss = step()
+        for x, t in data[warmup:]:
+            sx.copy_(x)
+            st.copy_(t)
+            graph.replay()
+            out.append(static_loss.item())
+        graph.release()
+    finally:
+        replay.set_enabled(prev)
+    return out
+
+
+def _assert_north_star(dev, cpu, cpu64, what):
+    """BASELINE's criterion: every loss within 1e-3 relative of PyTorch CPU fp32 (the reference's acceptance tool
+    compares its warm-up step and 5 more, tools/acceptance.py:51-103). The distance of both from a float64 CPU run is
+    printed for context: fp32 summation order moves these losses by up to ~2e-3 by the fifth Adam step on random
+    1000-class labels, so the bound is tight."""
+    rel_dev = [abs(a - b) / abs(b) for a, b in zip(dev, cpu)]
+    print(f"\n{what}: device {dev}\n  cpu {cpu}\n  cpu fp64 {cpu64}\n  |dev - cpu| / |cpu| "
+          f"{[f'{r:.1e}' for r in rel_dev]}; vs fp64: device "
+          f"{[f'{abs(a - c) / abs(c):.1e}' for a, c in zip(dev, cpu64)]}, cpu "
+          f"{[f'{abs(b - c) / abs(c):.1e}' for b, c in zip(cpu, cpu64)]}", flush=True)
+    assert all(r <= 1e-3 for r in rel_dev), (what, rel_dev, dev, cpu)
+
+
+@pytest.fixture()
+def model_plans(clean):
+    """Plans from the library's cost model (no timing-based tuning), so that the device's summation orders, and so
+    its losses, are the same on every box: the loss tests assert a tight bound on a chaotic trajectory, and every
+    plan the tuner may pick is checked against the oracle per op elsewhere."""
+    core = clean.native.core
+    core.set_tuning(False, 0)
+    try:
+        yield clean
+    finally:
+        core.set_tuning(True, 0)
+
+
+@pytest.mark.parametrize("name", ["resnet18", "mobilenet_v3_small"])
+def test_config_models_five_step_loss_parity(model_plans, name):
+    """BASELINE configs 3 and 4 at full size, eager: six training steps (the reference's warm-up step and five more)
+    from the same weights and data on the device and on PyTorch CPU, every loss within 1e-3 relative of CPU fp32;
+    no fallbacks."""
+    omt = model_plans
+    base, data, make_opt = _config_data(name)
+    cpu, cpu64 = _train(base, data, make_opt, "cpu"), _train(base, data, make_opt, "cpu", torch.float64)
+    dev = _train(base, data, make_opt, omt.DEVICE)
+    _assert_north_star(dev, cpu, cpu64, f"{name} eager")
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
+
+
+@pytest.mark.parametrize("name", ["resnet18", "mobilenet_v3_small"])
+def test_config_models_fast_paths_against_cpu(model_plans, name):
+    """The paths the benchmark times, at full size against PyTorch CPU under the north-star bound: the model under
+    torch.compile(backend="omarchy_mac_torch") (its forward and backward graphs replayed as HIP graphs from the third
+    step on), and the whole step captured as one HIP graph with the model compiled or not. Same plans as the eager
+    run, whose losses each path reproduces to 1e-6."""
+    from omarchy_mac_torch import replay
+    omt = model_plans
+    base, data, make_opt = _config_data(name)
+    cpu, cpu64 = _train(base, data, make_opt, "cpu"), _train(base, data, make_opt, "cpu", torch.float64)
+    eager = _train(base, data, make_opt, omt.DEVICE)
+    replay.reset_stats()
+    paths = {"compiled": _train(base, data, make_opt, omt.DEVICE, compiled=True)}
+    # one forward and one backward graph per Dynamo graph, replayed from the third step on
+    graphs = replay.STATS["captures"] // 2
+    assert replay.STATS["captures"] == 2 * graphs and replay.STATS["replays"] == 2 * graphs * (len(data) - 2) and \
+        replay.STATS["eager"] == 2 * graphs * 2, replay.STATS
+    paths["graphed"] = _train_graphed(base, data, make_opt, omt.DEVICE)
+    paths["compiled + graphed"] = _train_graphed(base, data, make_opt, omt.DEVICE, compiled=True)
+    for what, dev in paths.items():
+        _assert_north_star(dev, cpu, cpu64, f"{name} {what}")
+        assert all(abs(a - b) <= 1e-6 * abs(b) for a, b in zip(dev, eager)), (what, dev, eager)
     assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
 
 
@@ -772,3 +885,121 @@ def test_allocator_reuse_is_stream_ordered(clean):
     assert bool((s == 6.0).all())
     y = torch.empty(n, device=dev)  # the side stream's work is done: the block is the main stream's again
     assert y.data_ptr() == p
+
+
+def test_compiled_graph_replay_semantics(clean):
+    """The compile backend's graph replay on ResNet basic blocks (SGD with momentum): losses, gradients, running
+    statistics and batch counters match PyTorch CPU step by step while the forward and backward replay; a batch of
+    another size recompiles and warms up anew; gradients accumulated over two backward passes without zero_grad and two
+    forward passes before their backward run op by op (the last replay's outputs are still in use) and stay correct;
+    the model's outputs are the caller's own tensors, unchanged by later replays."""
+    from omarchy_mac_torch import models, replay
+    omt = clean
+    torch.manual_seed(11)
+    model = nn.Sequential(models.BasicBlock(8, 16, 2), models.BasicBlock(16, 16, 1), nn.AdaptiveAvgPool2d(1),
+                          nn.Flatten(), nn.Linear(16, 5))
+    ref, dev = copy.deepcopy(model), copy.deepcopy(model).to(omt.DEVICE)
+    compiled = torch.compile(dev, backend=omt.DEVICE, dynamic=False)  # one graph per batch size, each replayed
+    o_ref = torch.optim.SGD(ref.parameters(), lr=0.05, momentum=0.9)
+    o_dev = torch.optim.SGD(dev.parameters(), lr=0.05, momentum=0.9)
+    gen = torch.Generator().manual_seed(12)
+
+    def batch(n=6):
+        return torch.randn(n, 8, 12, 12, generator=gen), torch.randint(0, 5, (n,), generator=gen)
+
+    def check(step, l_dev, l_ref):
+        assert abs(float(l_dev) - float(l_ref)) <= 1e-4 * max(1.0, abs(float(l_ref))), step
+        for (pn, pr), (_, pd) in zip(ref.named_parameters(), dev.named_parameters()):
+            assert rel(pd.grad, pr.grad) <= TOL, (step, pn)
+
+    replay.reset_stats()
+    outs = []
+    for step in range(5):
+        x, t = batch()
+        o_ref.zero_grad(set_to_none=True)
+        o_dev.zero_grad(set_to_none=True)
+        y_ref, y_dev = ref(x), compiled(D(x, omt))
+        outs.append((y_dev, y_ref.detach().clone()))
+        l_ref, l_dev = F.cross_entropy(y_ref, t), F.cross_entropy(y_dev, D(t, omt))
+        l_ref.backward()
+        l_dev.backward()
+        check(step, l_dev, l_ref)
+        o_ref.step()
+        o_dev.step()
+    assert replay.STATS["captures"] == 2 and replay.STATS["replays"] == 6, replay.STATS
+    for y_dev, y_ref in outs:  # earlier outputs kept their values through later replays
+        assert rel(y_dev, y_ref) <= TOL
+    for (bn, br), (_, bd) in zip(ref.named_buffers(), dev.named_buffers()):
+        if br.dtype == torch.int64:
+            assert int(bd) == int(br) == 5, bn
+        else:
+            assert rel(bd, br) <= 1e-5, bn
+    # gradient accumulation: the second backward finds the first one's gradients in .grad
+    o_ref.zero_grad(set_to_none=True)
+    o_dev.zero_grad(set_to_none=True)
+    for _ in range(2):
+        x, t = batch()
+        F.cross_entropy(ref(x), t).backward()
+        F.cross_entropy(compiled(D(x, omt)), D(t, omt)).backward()
+    for (pn, pr), (_, pd) in zip(ref.named_parameters(), dev.named_parameters()):
+        assert rel(pd.grad, pr.grad) <= TOL, pn
+    # two forward passes, then both backward passes
+    o_ref.zero_grad(set_to_none=True)
+    o_dev.zero_grad(set_to_none=True)
+    (x1, t1), (x2, t2) = batch(), batch()
+    la, lb = F.cross_entropy(ref(x1), t1), F.cross_entropy(ref(x2), t2)
+    da, db = F.cross_entropy(compiled(D(x1, omt)), D(t1, omt)), F.cross_entropy(compiled(D(x2, omt)), D(t2, omt))
+    (la + lb).backward()
+    (da + db).backward()
+    assert abs(float(da) - float(la)) <= 1e-4 * max(1.0, abs(float(la)))
+    for (pn, pr), (_, pd) in zip(ref.named_parameters(), dev.named_parameters()):
+        assert rel(pd.grad, pr.grad) <= TOL, pn
+    assert replay.STATS["reasons"].get("outputs of the last replay still in use", 0) >= 2, replay.STATS
+    # another batch size: a new graph pair, warmed up and captured anew
+    before = replay.STATS["captures"]
+    for step in range(4):
+        x, t = batch(3)
+        o_ref.zero_grad(set_to_none=True)
+        o_dev.zero_grad(set_to_none=True)
+        l_ref, l_dev = F.cross_entropy(ref(x), t), F.cross_entropy(compiled(D(x, omt)), D(t, omt))
+        l_ref.backward()
+        l_dev.backward()
+        check(("b3", step), l_dev, l_ref)
+        o_ref.step()
+        o_dev.step()
+    assert replay.STATS["captures"] == before + 2, replay.STATS
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
+
+
+def test_kernel_counts_and_times(clean):
+    """Per-kernel launch counts and (debug) timings, the reference's kernel_counts / kernel_times /
+    debug_time_kernels (csrc/module.cpp:30-33): a convolution forward + backward and a BatchNorm through the device
+    count their launches by kernel; with timing on every launch has a positive time; each reset clears its own
+    counter only."""
+    omt = clean
+    core = omt.native.core
+    x = D(torch.randn(4, 8, 16, 16), omt).requires_grad_()
+    conv, bn = nn.Conv2d(8, 16, 3, padding=1, bias=False).to(omt.DEVICE), nn.BatchNorm2d(16).to(omt.DEVICE)
+
+    def step():
+        bn(conv(x)).sum().backward()
+
+    step()
+    omt.synchronize()
+    core.kernel_counts(True)
+    core.kernel_times(True)
+    step()
+    omt.synchronize()
+    counts = core.kernel_counts(False)
+    assert any("conv" in k for k in counts) and any("bn" in k for k in counts), counts
+    assert all(v >= 1 for v in counts.values())
+    assert core.kernel_times(False) == {}  # timing off: nothing timed
+    core.debug_time_kernels(True)
+    try:
+        step()
+    finally:
+        core.debug_time_kernels(False)
+    times = core.kernel_times(True)
+    assert set(times) <= set(core.kernel_counts(False)) and times and all(v > 0 for v in times.values()), times
+    assert core.kernel_times(False) == {} and core.kernel_counts(False)  # the times reset, the counts kept
+    assert core.kernel_counts(True) and core.kernel_counts(False) == {}

@@ -1,6 +1,6 @@
 """The training steps' ops outside the convolution path (residual add, ReLU / hardswish / hardsigmoid and their
-gradients, the squeeze-excite channel scale, plane means and sums, a linear layer's bias gradient, log-softmax and the
-NLL loss): libomt_hip.so's kernels against PyTorch CPU fp32 (the reference's own oracle for these ops:
+gradients, the squeeze-excite channel scale, plane means and sums, the linear layers' matrix products and bias
+gradient, log-softmax and the NLL loss, scalar adds of step counts and batch counters): libomt_hip.so's kernels against PyTorch CPU fp32 (the reference's own oracle for these ops:
 tools/conformance.py:55-103), through the C ABI and through the device's aten registrations, checked to run on the
 library's kernels rather than torch's. Criterion: rel-L2 <= 1e-4 (most results are bit-identical)."""
 
@@ -196,8 +196,8 @@ def test_device_ops_run_on_the_library_kernels(omt, case):
 
 
 def test_cross_entropy_training_step_ops_are_native(omt):
-    """One MobileNetV3-style training step (hardswish, squeeze-excite, residual adds, cross entropy): the only ops left
-    on torch's kernels are the linear layers' GEMMs (hipBLASLt), the batch counters and copies."""
+    """One MobileNetV3-style training step (hardswish, squeeze-excite, residual adds, linear layers, cross entropy,
+    BatchNorm batch counters, AdamW's step counts): no op is left on torch's kernels."""
     from omarchy_mac_torch import models, stacks
     core = omt.native.core
     prev = stacks.set_auto_fuse(False)
@@ -216,8 +216,96 @@ def test_cross_entropy_training_step_ops_are_native(omt):
     finally:
         core.count_delegated(False)
         stacks.set_auto_fuse(prev)
-    # add_ on BatchNorm's int64 batch counters, _foreach_add_ on the optimizer's step counts
-    allowed = ("mm", "addmm", "add_", "_foreach_add_", "_foreach_add")
-    assert [k for k in delegated if k.split(".")[0] not in allowed] == [], \
-        {k: v for k, v in delegated.items() if k.split(".")[0] not in allowed}
+    assert not delegated, delegated
     assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
+
+
+LINEAR_SHAPES = [(32, 512, 1000), (128, 256, 10), (32, 16, 8), (32, 8, 16), (32, 576, 1024), (1, 7, 3), (5, 1, 9),
+                 (3, 9, 1)]
+
+
+@pytest.mark.parametrize("m,k,n", LINEAR_SHAPES)
+def test_linear_products_run_on_the_convolution_gemms(omt, m, k, n):
+    """The three matrix products of a linear layer's training step (forward addmm with bias, grad input mm, grad
+    weight mm in the layouts PyTorch's autograd requests them) against PyTorch CPU, through the device's aten
+    registrations, none delegated to torch's GEMMs; ResNet-18's FC (32 x 512 -> 1000), PlainCNN's (128 x 256 -> 10),
+    squeeze-excite FCs and single rows / columns."""
+    core = omt.native.core
+    gen = torch.Generator().manual_seed(m * 7919 + k * 31 + n)
+    x, w, b = torch.randn(m, k, generator=gen), torch.randn(n, k, generator=gen), torch.randn(n, generator=gen)
+    gy = torch.randn(m, n, generator=gen)
+    D = (lambda v: v.to(omt.DEVICE))
+    refs = {"forward": torch.addmm(b, x, w.t()), "grad_input": gy @ w, "grad_weight": gy.t() @ x,
+            "no_bias": x @ w.t(), "beta0": torch.addmm(torch.full((n,), float("nan")), x, w.t(), beta=0)}
+    torch.cuda.synchronize()
+    core.count_delegated(True)
+    try:
+        got = {"forward": torch.addmm(D(b), D(x), D(w).t()), "grad_input": D(gy) @ D(w),
+               "grad_weight": D(gy).t() @ D(x), "no_bias": D(x) @ D(w).t(),
+               "beta0": torch.addmm(D(torch.full((n,), float("nan"))), D(x), D(w).t(), beta=0)}
+        torch.cuda.synchronize()
+        delegated = dict(core.delegated_counts())
+    finally:
+        core.count_delegated(False)
+    for key, ref in refs.items():
+        assert got[key].shape == ref.shape and rel(got[key], ref) <= TOL, (key, rel(got[key], ref))
+    assert not [k for k in delegated if k.split(".")[0] in ("mm", "addmm")], delegated
+
+
+def test_linear_products_outside_the_covered_layouts(omt):
+    """Both operands column-major, strided rows and a general addmm (alpha, beta, a matrix) still give PyTorch's
+    results (on torch's GEMMs)."""
+    gen = torch.Generator().manual_seed(3)
+    a, b = torch.randn(6, 5, generator=gen), torch.randn(7, 6, generator=gen)
+    D = (lambda v: v.to(omt.DEVICE))
+    assert rel(D(a).t() @ D(b).t(), a.t() @ b.t()) <= TOL
+    big = torch.randn(12, 10, generator=gen)
+    assert rel(D(big)[::2, :6] @ D(a), big[::2, :6] @ a) <= TOL
+    c = torch.randn(6, 7, generator=gen)
+    assert rel(torch.addmm(D(c), D(a), D(b).t()[:5], beta=0.5, alpha=2.0),
+               torch.addmm(c, a, b.t()[:5], beta=0.5, alpha=2.0)) <= TOL
+
+
+@pytest.mark.parametrize("m,k,n", [(32, 512, 1000), (128, 256, 10), (32, 16, 8)])
+def test_linear_layer_autograd(omt, m, k, n):
+    """nn.Linear forward and backward (input, weight and bias gradients) on the device against PyTorch CPU."""
+    torch.manual_seed(m + k + n)
+    lin = torch.nn.Linear(k, n)
+    dlin = torch.nn.Linear(k, n).to(omt.DEVICE)
+    dlin.load_state_dict(lin.state_dict())
+    x = torch.randn(m, k, requires_grad=True)
+    dx = x.detach().to(omt.DEVICE).requires_grad_()
+    gy = torch.randn(m, n)
+    y, dy = lin(x), dlin(dx)
+    y.backward(gy)
+    dy.backward(gy.to(omt.DEVICE))
+    for got, ref in ((dy, y), (dx.grad, x.grad), (dlin.weight.grad, lin.weight.grad), (dlin.bias.grad, lin.bias.grad)):
+        assert got.shape == ref.shape and rel(got, ref) <= TOL
+    assert dlin.weight.grad.is_contiguous()
+
+
+def test_foreach_and_scalar_adds(omt):
+    """_foreach_add_ over float32 step counts and int64 batch counters (one launch per 64 tensors; 70 tensors here),
+    add_(1) on a 0-dim int64 counter, x + 1.5 and x += 2: exact, and on the library's kernels."""
+    core = omt.native.core
+    D = (lambda v: v.to(omt.DEVICE))
+    steps = [torch.tensor(float(i)) for i in range(70)]
+    counts = [torch.tensor(10 ** 12 + i, dtype=torch.int64) for i in range(70)]
+    small = torch.arange(300, dtype=torch.float32)
+    dsteps, dcounts, dsmall = [D(t) for t in steps], [D(t) for t in counts], D(small)
+    torch.cuda.synchronize()
+    core.count_delegated(True)
+    try:
+        torch._foreach_add_(dsteps, 1)
+        torch._foreach_add_(dcounts, 3)
+        dcounts[0].add_(1)
+        y = dsmall + 1.5
+        dsmall += 2
+        torch.cuda.synchronize()
+        delegated = dict(core.delegated_counts())
+    finally:
+        core.count_delegated(False)
+    assert [float(t) for t in dsteps] == [float(i) + 1 for i in range(70)]
+    assert [int(t) for t in dcounts] == [10 ** 12 + i + 3 + (i == 0) for i in range(70)]
+    assert torch.equal(y.cpu(), small + 1.5) and torch.equal(dsmall.cpu(), small + 2)
+    assert not delegated, delegated
