@@ -54,6 +54,15 @@ C5_LAYERS = [
     ("1x1_exp_7", 256, 512, 2048, 7, 1, 1, 0), ("1x1_red_7", 256, 2048, 512, 7, 1, 1, 0),
 ]
 C1_LAYERS = [("alexnet_conv1", 16, 3, 64, 224, 11, 4, 2)]
+# ResNet-18 at batch 32 on 64x64 inputs (config 3): name, n, c, k, h, ks, stride, pad, uses per training step
+RESNET18_LAYERS = [
+    ("stem_7x7s2", 32, 3, 64, 64, 7, 2, 3, 1), ("l1_3x3", 32, 64, 64, 16, 3, 1, 1, 4),
+    ("l2_3x3s2", 32, 64, 128, 16, 3, 2, 1, 1), ("l2_1x1s2", 32, 64, 128, 16, 1, 2, 0, 1),
+    ("l2_3x3", 32, 128, 128, 8, 3, 1, 1, 3), ("l3_3x3s2", 32, 128, 256, 8, 3, 2, 1, 1),
+    ("l3_1x1s2", 32, 128, 256, 8, 1, 2, 0, 1), ("l3_3x3", 32, 256, 256, 4, 3, 1, 1, 3),
+    ("l4_3x3s2", 32, 256, 512, 4, 3, 2, 1, 1), ("l4_1x1s2", 32, 256, 512, 4, 1, 2, 0, 1),
+    ("l4_3x3", 32, 512, 512, 2, 3, 1, 1, 3),
+]
 
 
 def out_size(h, ks, s, p):
@@ -807,6 +816,76 @@ def aten_ops_per_step(model, make_opt, batch):
     return Count.n
 
 
+def resnet_layer_table(dev, tune=True, calls=20, reps=5):
+    """ResNet-18's convolutions (config 3) one by one with the plans the device tunes for them: forward (omt_conv_fwd,
+    with its slice sum) and backward (omt_conv_bwd: grad input and grad weight; the stem, whose input needs no
+    gradient, grad weight alone), each timed as replays of a captured HIP graph of `calls` calls (GPU time per call,
+    as in a replayed training step). tune=False keeps the plans the cache holds (a tuning file of an earlier run:
+    a profiled run then traces the timed calls alone). Prints a markdown table and returns it as a dict."""
+    import torch
+
+    from omarchy_mac_torch import hip_ops
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rows, total = {}, {"fwd": 0.0, "bwd": 0.0}
+
+    def per_call_us(fn):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(calls):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * calls)
+        g.reset()
+        return us
+
+    print("| Layer | n x c x h^2 -> k, ks/s | uses | fwd us | fwd TFLOP/s | fwd plan | bwd us | bwd TFLOP/s | "
+          "bwd plans (dgrad, wgrad) |\n|---|---|---|---|---|---|---|---|---|")
+    for (name, n, c, k, h, ks, s, p, uses) in RESNET18_LAYERS:
+        o = out_size(h, ks, s, p)
+        x = torch.randn((n, c, h, h), device=dev, generator=gen)
+        w = torch.randn((k, c, ks, ks), device=dev, generator=gen) * (c * ks * ks) ** -0.5
+        gy = torch.randn((n, k, o, o), device=dev, generator=gen)
+        f = flops_dir(n, c, k, h, ks, s, p)
+        if tune:
+            hip_ops.autotune_conv("fwd", x.shape, w.shape, s, p)
+        stem = name.startswith("stem")
+        if stem:
+            if tune:
+                hip_ops.autotune_conv("wgrad", x.shape, w.shape, s, p)
+            bwd = lambda: hip_ops.conv2d_wgrad(x, gy, ks, s, p)  # noqa: E731
+            bf = f
+        else:
+            if tune:
+                hip_ops.autotune_conv_bwd(x.shape, w.shape, s, p)
+            bwd = lambda: hip_ops.conv2d_bwd(x, gy, w, s, p)  # noqa: E731
+            bf = 2 * f
+        tf = per_call_us(lambda: hip_ops.conv2d(x, w, None, s, p))
+        tb = per_call_us(bwd)
+        plans = {d: hip_ops.conv_plan(d, x.shape, w.shape, s, p)[:2] for d in ("fwd", "dgrad", "wgrad")}
+        rows[name] = {"uses": uses, "fwd_us": round(tf, 2), "fwd_tflops": round(f / tf / 1e6, 1), "bwd_us": round(tb, 2),
+                      "bwd_tflops": round(bf / tb / 1e6, 1), "plans": plans}
+        total["fwd"] += uses * tf
+        total["bwd"] += uses * tb
+        print(f"| {name} | {n}x{c}x{h}^2 -> {k}, {ks}/{s} | {uses} | {tf:.1f} | {f / tf / 1e6:.1f} | {plans['fwd']} | "
+              f"{tb:.1f} | {bf / tb / 1e6:.1f} | {'-' if stem else plans['dgrad']}, {plans['wgrad']} |", flush=True)
+    flops = sum(u * flops_dir(n, c, k, h, ks, s, p) * (2 if name.startswith("stem") else 3)
+                for (name, n, c, k, h, ks, s, p, u) in RESNET18_LAYERS)
+    us = total["fwd"] + total["bwd"]
+    print(f"\nper training step: forward {total['fwd']:.0f} us, backward {total['bwd']:.0f} us, "
+          f"{us:.0f} us for {flops / 1e9:.2f} GFLOP = {flops / us / 1e6:.1f} TFLOP/s", flush=True)
+    return {"layers": rows, "step_us": {k: round(v, 1) for k, v in total.items()}, "step_gflop": round(flops / 1e9, 3)}
+
+
 def conv_sweep(layers, dev, steps, warmup, tune, nhwc=False):
     """The sweep of `layers` (fwd + dgrad + wgrad each) on synthetic inputs resident in HBM: plans tuned first (as the
     reference tunes every new shape on first use, csrc/conv.cpp:56), `warmup` untimed steps, then `steps` timed ones
@@ -982,9 +1061,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "models", "bw"], default="c5",
-                    help="resnet: only the ResNet-18 training-step measurement; models: only the training steps of "
-                         "configs 2-4; bw: only the HBM-bound kernels (all three for profiling)")
+    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "resnet-layers", "models", "bw"], default="c5",
+                    help="resnet: only the ResNet-18 training-step measurement; resnet-layers: ResNet-18's "
+                         "convolutions one by one (tuned plans, per-call GPU time); models: only the training steps "
+                         "of configs 2-4; bw: only the HBM-bound kernels (all three for profiling)")
     ap.add_argument("--no-bw", action="store_true", help="skip the HBM-bound kernel measurements")
     ap.add_argument("--no-miopen", action="store_true",
                     help="skip timing the same sweep through torch's own convolutions (MIOpen)")
@@ -1032,6 +1112,9 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    if args.workload == "resnet-layers":
+        print(json.dumps({"resnet18_conv_layers": resnet_layer_table(dev, not args.no_tune)}), flush=True)
+        return
     if args.workload in ("resnet", "models"):
         import omarchy_mac_torch
 

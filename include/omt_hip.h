@@ -206,6 +206,30 @@ size_t omt_conv_bwd_workspace(const omt_conv_geo* g);
 int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx, float* gw,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* A deferred in-order slice sum: out[i] = sum over s = 0 .. slices-1, in order, of parts[s * n + i] (slices 0: none).
+ * The sum omt_conv_bwd_parts leaves to its caller, which runs it in a later launch (omt_bn_bwd_parts) or alone
+ * (omt_slice_sums). */
+typedef struct omt_slice_sum {
+  const float* parts;
+  float* out;
+  int64_t n;
+  int slices;
+} omt_slice_sum;
+
+/* omt_conv_bwd without its slice-sum launch, for a consumer that sums the partials itself: when the grad-input plan
+ * splits K into 2..max_gx_slices slices, *gx_parts points at its [*gx_slices][n][ci][ih][iw] partials (inside the
+ * workspace) and gx is not written; otherwise gx holds grad input (summed here if split further) and *gx_slices = 1,
+ * *gx_parts = NULL. When the grad-weight plan splits K, *gw_sum describes the in-order sum of its partials into gw,
+ * which the caller must run (gw_sum->slices = 0 when gw was written). Partials and sums are those of omt_conv_bwd
+ * (same plans, same order): the results, once summed, are bit-identical. Same workspace as omt_conv_bwd; a batch that
+ * would run in chunks is OMT_UNSUPPORTED. No counterpart in the reference (its convolution backward and BatchNorm
+ * backward are separate ops); the torch.compile backend's convolution backward -> BatchNorm backward op uses it. */
+int omt_conv_bwd_parts(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx, float* gw,
+                       void* workspace, size_t workspace_bytes, int max_gx_slices, const float** gx_parts,
+                       int* gx_slices, omt_slice_sum* gw_sum, void* stream);
+/* Runs count deferred slice sums (one launch each). */
+int omt_slice_sums(const omt_slice_sum* sums, int count, void* stream);
+
 /* ---- channels-last (NHWC) dense convolution ---------------------------------------------------------------------
  * The same convolutions over channels-last tensors: x / gx [n][ih][iw][ci], y / gy [n][oh][ow][co], and the filter
  * and its gradient [co][ks][ks][ci] -- the memory order of PyTorch's channels_last tensors of those shapes, read and
@@ -271,8 +295,13 @@ int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* 
 
 /* ---- BatchNorm (NCHW, affine) ----------------------------------------------------------------------------- */
 
-/* Training forward: per-channel biased mean / variance over n*hw, y = (x - mean) * invstd * gamma + beta
- * (ReLU if relu), save_mean / save_invstd written, and the running stats updated
+/* The activation a BatchNorm entry point applies after the normalization (its `relu` / `act` argument): 0 none, 1 ReLU
+ * (y = max(z, 0), NaN propagates), 2 hardswish (y = z * min(max(z + 3, 0), 6) / 6, PyTorch's definition). The
+ * reference fuses ReLU only (omt::bn_relu_train, csrc/fused.cpp:68-84); hardswish follows MobileNetV3's BatchNorms. */
+enum { OMT_ACT_NONE = 0, OMT_ACT_RELU = 1, OMT_ACT_HARDSWISH = 2 };
+
+/* Training forward: per-channel biased mean / variance over n*hw, y = act((x - mean) * invstd * gamma + beta)
+ * (relu: the activation, OMT_ACT_*; 1 = ReLU), save_mean / save_invstd written, and the running stats updated
  * rm' = rm + momentum*(mean - rm), rv' = rv + momentum*(var * m/(m-1) - rv) into new_rm / new_rv (which may alias
  * running_mean / running_var for the in-place native_batch_norm form, or be NULL to skip the update).
  * Replaces batch_norm_ training (csrc/nn.cpp:38-48) and omt::bn_relu_train (csrc/fused.cpp:68-84). */
@@ -281,13 +310,14 @@ int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const flo
                      const float* running_mean, const float* running_var, double momentum, double eps, int relu,
                      float* y, float* save_mean, float* save_invstd, float* new_rm, float* new_rv, void* workspace,
                      size_t workspace_bytes, void* stream);
-/* The same with a residual added before the ReLU: y = act(bn(x) + residual) (residual [n][c][hw] like x, or NULL).
- * No counterpart in the reference, whose residual add and ReLU are separate ops; the torch.compile backend fuses
- * BatchNorm -> add -> ReLU (the end of a ResNet basic block) into it. */
+/* The same with a residual added before the activation: y = act(bn(x) + residual) (residual [n][c][hw] like x, or
+ * NULL), and z (NULL to skip) receiving bn(x) + residual, the activation's input (the hardswish backward reads it).
+ * No counterpart in the reference, whose residual add and activations are separate ops; the torch.compile backend
+ * fuses BatchNorm -> add -> ReLU (the end of a ResNet basic block) and BatchNorm -> hardswish into it. */
 int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
                          const float* running_mean, const float* running_var, double momentum, double eps, int relu,
-                         const float* residual, float* y, float* save_mean, float* save_invstd, float* new_rm,
-                         float* new_rv, void* workspace, size_t workspace_bytes, void* stream);
+                         const float* residual, float* y, float* z, float* save_mean, float* save_invstd,
+                         float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes, void* stream);
 /* omt_bn_train_fwd_res over a convolution's unsummed K-split partials (omt_conv_fwd_unsummed): x = the sum of the
  * `slices` partials of n*c*hw elements each, in slice order (the convolution's own slice sum, so x is bit-identical
  * to the summed convolution output), is written to x and normalized as by omt_bn_train_fwd_res. Channels of up to
@@ -295,9 +325,9 @@ int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const float* x, const
  * No counterpart in the reference (see omt_conv_fwd_unsummed). */
 int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts, int slices, float* x,
                            const float* gamma, const float* beta, const float* running_mean, const float* running_var,
-                           double momentum, double eps, int relu, const float* residual, float* y, float* save_mean,
-                           float* save_invstd, float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           double momentum, double eps, int relu, const float* residual, float* y, float* z,
+                           float* save_mean, float* save_invstd, float* new_rm, float* new_rv, void* workspace,
+                           size_t workspace_bytes, void* stream);
 /* omt_bn_train_fwd_res with the statistics from omt_conv_fwd_stats (stats [c][groups][2] over x = that call's y):
  * one launch reduces each channel's groups to a few partial sums (in a fixed order, into the workspace of
  * omt_bn_train_workspace's size), the next finalizes mean / invstd and the running statistics as it applies, so x is
@@ -306,9 +336,9 @@ int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts,
 int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats, int groups,
                            size_t stats_bytes, const float* gamma, const float* beta, const float* running_mean,
                            const float* running_var, double momentum, double eps, int relu, const float* residual,
-                           float* y, float* save_mean, float* save_invstd, float* new_rm, float* new_rv,
+                           float* y, float* z, float* save_mean, float* save_invstd, float* new_rm, float* new_rv,
                            void* workspace, size_t workspace_bytes, void* stream);
-/* Eval forward: y = (x - rm) * rsqrt(rv + eps) * gamma + beta (ReLU if relu). Replaces batch_norm_ eval
+/* Eval forward: y = act((x - rm) * rsqrt(rv + eps) * gamma + beta) (relu: OMT_ACT_*). Replaces batch_norm_ eval
  * (csrc/nn.cpp:49-54) and bn_relu_rv.wgsl. */
 int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
                     const float* running_mean, const float* running_var, double eps, int relu, float* y,
@@ -322,6 +352,15 @@ int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, const float* x,
                const float* save_mean, const float* save_invstd, const float* gamma, float* gx, float* dgamma,
                float* dbeta, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The backward of BatchNorm -> activation: gz = g through the activation's gradient, act_in its operand (act
+ * OMT_ACT_RELU: the ReLU's output, gz = g where act_in > 0, else 0, as omt_bn_bwd's relu_y; OMT_ACT_HARDSWISH: the
+ * hardswish's input z, gz = g * hardswish'(z), 0 at and below -3, g at and above 3; OMT_ACT_NONE: act_in unused), then
+ * the BatchNorm backward of gz, as omt_bn_bwd. Replaces hardswish_backward -> native_batch_norm_backward (the
+ * reference runs them as two ops; it fuses ReLU only, csrc/fused.cpp:86-115). */
+int omt_bn_bwd_act(int64_t n, int64_t c, int64_t hw, const float* g, const float* x, int act, const float* act_in,
+                   const float* save_mean, const float* save_invstd, const float* gamma, float* gx, float* dgamma,
+                   float* dbeta, void* workspace, size_t workspace_bytes, void* stream);
+
 /* The same with a residual branch's gradient: gz = (g + g2) masked by relu_y > 0 (g2 may be NULL), written to gz for
  * the residual branch, and the BatchNorm backward of gz. No counterpart in the reference, whose ReLU backward, residual
  * add and BatchNorm backward are separate ops; the torch.compile backend fuses add -> threshold_backward ->
@@ -329,6 +368,19 @@ int omt_bn_bwd(int64_t n, int64_t c, int64_t hw, const float* g, const float* x,
 int omt_bn_bwd_res(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
                    const float* relu_y, const float* save_mean, const float* save_invstd, const float* gamma, float* gx,
                    float* dgamma, float* dbeta, float* gz, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The BatchNorm backward of omt_bn_bwd_act (gz NULL) or omt_bn_bwd_res (gz not NULL; g2 only then) with its incoming
+ * gradient g given as `slices` consecutive arrays of n*c*hw floats, g = their sum in slice order (omt_conv_bwd_parts'
+ * grad-input partials; slices 1: g itself), to which g2 is added after the sum. Runs the `count` (at most 2) deferred
+ * slice sums in the same launch, on workgroups of their own. One launch: channels of n*hw <= 8192 elements only
+ * (OMT_UNSUPPORTED above). With the partials of omt_conv_bwd_parts the results equal omt_conv_bwd followed by
+ * omt_bn_bwd_act / omt_bn_bwd_res (the same additions in the same order). No counterpart in the reference (its
+ * convolution backward and BatchNorm backward are separate ops); the torch.compile backend's fused convolution
+ * backward -> BatchNorm backward op (omt::conv_bn_backward) uses it. No workspace. */
+int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g_parts, int slices, const float* g2,
+                     const float* x, int act, const float* act_in, const float* save_mean, const float* save_invstd,
+                     const float* gamma, float* gx, float* dgamma, float* dbeta, float* gz, const omt_slice_sum* sums,
+                     int count, void* stream);
 
 /* ---- pooling (planes = n * c) ----------------------------------------------------------------------------- */
 

@@ -13,6 +13,7 @@
 // bn_bwd_apply of csrc/fused.cpp:86-115): gz = g (or g * [y > 0]), xhat = (x - mean) * invstd,
 // dgamma = sum gz * xhat, dbeta = sum gz, gx = gamma * invstd / m * (m * gz - dbeta - xhat * dgamma).
 #include "omt_internal.h"
+#include "slice_sum.h"
 
 namespace omt {
 
@@ -196,14 +197,16 @@ __device__ __forceinline__ void bn_sum_slices(const double* __restrict__ part, i
     }
 }
 
-// y = (x - mean[c]) * invstd[c] * gamma[c] + beta[c] (+ res), optional ReLU. grid (planes, hw chunks); float4 when
-// hw % 4 == 0. Eval mode passes invstd = null and the running variance in var: invstd = 1 / sqrt(var + eps).
+// y = act((x - mean[c]) * invstd[c] * gamma[c] + beta[c] (+ res)) (act: OMT_ACT_*; zo, when set, receives the value
+// before the activation). grid (planes, hw chunks); float4 when hw % 4 == 0. Eval mode passes invstd = null and the
+// running variance in var: invstd = 1 / sqrt(var + eps).
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__ x, const float* __restrict__ mean,
                                                        const float* __restrict__ invstd, const float* __restrict__ var,
                                                        double eps, const float* __restrict__ gamma,
                                                        const float* __restrict__ beta, const float* __restrict__ res,
-                                                       float* __restrict__ y, int c, int hw, int relu) {
+                                                       float* __restrict__ y, int c, int hw, int relu,
+                                                       float* __restrict__ zo = nullptr) {
   const int plane = blockIdx.x, ch = plane % c;
   const float inv = invstd ? invstd[ch] : (float)(1.0 / sqrt((double)var[ch] + eps));
   const float sc = inv * gamma[ch];
@@ -226,11 +229,12 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
         v.z += r.z;
         v.w += r.w;
       }
+      if (zo) reinterpret_cast<float4*>(zo + base)[e] = v;
       if (relu) {
-        v.x = fmaxf(v.x, 0.f);
-        v.y = fmaxf(v.y, 0.f);
-        v.z = fmaxf(v.z, 0.f);
-        v.w = fmaxf(v.w, 0.f);
+        v.x = bn_act(v.x, relu);
+        v.y = bn_act(v.y, relu);
+        v.z = bn_act(v.z, relu);
+        v.w = bn_act(v.w, relu);
       }
       yv[e] = v;
     }
@@ -238,8 +242,8 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
     for (int e = blockIdx.y * 256 + threadIdx.x; e < hw; e += gridDim.y * 256) {
       float v = fmaf(x[base + e], sc, sh);
       if (res) v += res[base + e];
-      if (relu) v = fmaxf(v, 0.f);
-      y[base + e] = v;
+      if (zo) zo[base + e] = v;
+      y[base + e] = bn_act(v, relu);
     }
   }
 }
@@ -278,7 +282,7 @@ __global__ void __launch_bounds__(256) bn_train_apply_kernel(const float* __rest
                                                              const float* __restrict__ beta,
                                                              const float* __restrict__ res, float* __restrict__ y,
                                                              int c, int hw, int relu, int planes, int chunks,
-                                                             int rev, int shift0 = 0) {
+                                                             int rev, int shift0 = 0, float* __restrict__ zo = nullptr) {
   __shared__ float coef[2];
   int chunk;
   const int plane = apply_plane(planes, chunks, rev, chunk), ch = plane % c;
@@ -314,18 +318,19 @@ __global__ void __launch_bounds__(256) bn_train_apply_kernel(const float* __rest
         v.z += r.z;
         v.w += r.w;
       }
+      if (zo) reinterpret_cast<float4*>(zo + base)[e] = v;
       if (relu) {
-        v.x = fmaxf(v.x, 0.f);
-        v.y = fmaxf(v.y, 0.f);
-        v.z = fmaxf(v.z, 0.f);
-        v.w = fmaxf(v.w, 0.f);
+        v.x = bn_act(v.x, relu);
+        v.y = bn_act(v.y, relu);
+        v.z = bn_act(v.z, relu);
+        v.w = bn_act(v.w, relu);
       }
       reinterpret_cast<float4*>(y + base)[e] = v;
     } else {
       float v = fmaf(e == e0 ? first.x : x[base + e], sc, sh);
       if (res) v += res[base + e];
-      if (relu) v = fmaxf(v, 0.f);
-      y[base + e] = v;
+      if (zo) zo[base + e] = v;
+      y[base + e] = bn_act(v, relu);
     }
   }
 }
@@ -338,22 +343,23 @@ __global__ void __launch_bounds__(256) bn_apply_flat_kernel(const float* __restr
                                                             const float* __restrict__ beta,
                                                             const float* __restrict__ res, float* __restrict__ y,
                                                             int64_t total_v, FastDiv div_hwv, FastDiv div_c, int c,
-                                                            int relu) {
+                                                            int relu, float* __restrict__ zo = nullptr) {
   using V = typename VecT<VEC>::T;
   for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
     const uint32_t plane = fdiv((uint32_t)i, div_hwv), ch = plane - fdiv(plane, div_c) * (uint32_t)c;
     const float sc = invstd[ch] * gamma[ch];
     const float sh = beta[ch] - mean[ch] * sc;
     V v = reinterpret_cast<const V*>(x)[i];
-    V r;
+    V r, z;
     if (res) r = reinterpret_cast<const V*>(res)[i];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       float f = fmaf(vget(v, e), sc, sh);
       if (res) f += vget(r, e);
-      if (relu) f = fmaxf(f, 0.f);
-      vset(v, e, f);
+      vset(z, e, f);
+      vset(v, e, bn_act(f, relu));
     }
+    if (zo) reinterpret_cast<V*>(zo)[i] = z;
     reinterpret_cast<V*>(y)[i] = v;
   }
 }
@@ -365,7 +371,7 @@ __global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restric
                                                           const float* __restrict__ x,
                                                           const float* __restrict__ ry, const float* __restrict__ mean,
                                                           const float* __restrict__ invstd, double* __restrict__ part,
-                                                          int c, int hw, const Split sp) {
+                                                          int c, int hw, const Split sp, int act) {
   using V = typename VecT<VEC>::T;
   const int ch = blockIdx.x, s = blockIdx.y;
   const float mu = mean[ch], inv = invstd[ch];
@@ -396,7 +402,7 @@ __global__ void __launch_bounds__(256) bn_bwd_part_kernel(const float* __restric
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         float gz = vget(rg[u], i);
-        if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+        if (ry) gz = bn_act_grad(gz, vget(rr[u], i), act);
         const float xhat = (vget(rx[u], i) - mu) * inv;
         s1 += (double)gz;
         s2 += (double)gz * (double)xhat;
@@ -448,7 +454,7 @@ __device__ __forceinline__ float bwd_elem(float gz, float xv, float r, bool mask
 template <int VEC, bool RES>
 __device__ __forceinline__ void bwd_vec(const float* __restrict__ g, const float* __restrict__ g2,
                                         const float* __restrict__ x, const float* __restrict__ ry, const float* k,
-                                        float* __restrict__ gx, float* __restrict__ gzo, int64_t i) {
+                                        float* __restrict__ gx, float* __restrict__ gzo, int64_t i, int act) {
   using V = typename VecT<VEC>::T;
   V vg = reinterpret_cast<const V*>(g)[i];
   if (RES && g2) vadd(vg, reinterpret_cast<const V*>(g2)[i]);
@@ -459,7 +465,7 @@ __device__ __forceinline__ void bwd_vec(const float* __restrict__ g, const float
 #pragma unroll
   for (int e = 0; e < VEC; ++e) {
     float gz = vget(vg, e);
-    if (ry && !(vget(vr, e) > 0.f)) gz = 0.f;
+    if (ry) gz = bn_act_grad(gz, vget(vr, e), act);
     vset(z, e, gz);
     vset(o, e, bwd_elem(gz, vget(vx, e), 1.f, false, k));
   }
@@ -473,14 +479,14 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_kernel(const float* __restri
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ ry, const float* __restrict__ kc,
                                                            float* __restrict__ gx, float* __restrict__ gzo, int c,
-                                                           int hwv) {
+                                                           int hwv, int act) {
   const int plane = blockIdx.x, ch = plane % c;
   float k[5];
 #pragma unroll
   for (int i = 0; i < 5; ++i) k[i] = kc[ch * 5 + i];
   const int64_t base = (int64_t)plane * hwv;
   for (int e = blockIdx.y * 256 + threadIdx.x; e < hwv; e += gridDim.y * 256)
-    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e);
+    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e, act);
 }
 
 // bn_bwd_apply_kernel with the finalize folded in (one launch fewer): every workgroup derives its channel's constants
@@ -497,7 +503,7 @@ __global__ void __launch_bounds__(256) bn_bwd_train_apply_kernel(const float* __
                                                                  const float* __restrict__ gamma,
                                                                  float* __restrict__ dgamma, float* __restrict__ dbeta,
                                                                  float* __restrict__ gx, float* __restrict__ gzo, int c,
-                                                                 int hwv, int planes, int chunks, int rev) {
+                                                                 int hwv, int planes, int chunks, int rev, int act) {
   __shared__ float kc[5];
   int chunk;
   const int plane = apply_plane(planes, chunks, rev, chunk), ch = plane % c;
@@ -515,7 +521,8 @@ __global__ void __launch_bounds__(256) bn_bwd_train_apply_kernel(const float* __
 #pragma unroll
   for (int i = 0; i < 5; ++i) k[i] = kc[i];
   const int64_t base = (int64_t)plane * hwv;
-  for (int e = chunk * 256 + threadIdx.x; e < hwv; e += chunks * 256) bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e);
+  for (int e = chunk * 256 + threadIdx.x; e < hwv; e += chunks * 256)
+    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, base + e, act);
 }
 
 // Small planes: flat over VEC-wide vectors.
@@ -526,13 +533,13 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __r
                                                                 const float* __restrict__ ry,
                                                                 const float* __restrict__ kc, float* __restrict__ gx,
                                                                 float* __restrict__ gzo, int64_t total_v,
-                                                                FastDiv div_hwv, FastDiv div_c, int c) {
+                                                                FastDiv div_hwv, FastDiv div_c, int c, int act) {
   for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
     const uint32_t plane = fdiv((uint32_t)i, div_hwv), ch = plane - fdiv(plane, div_c) * (uint32_t)c;
     float k[5];
 #pragma unroll
     for (int j = 0; j < 5; ++j) k[j] = kc[ch * 5 + j];
-    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, i);
+    bwd_vec<VEC, RES>(g, g2, x, ry, k, gx, gzo, i, act);
   }
 }
 
@@ -555,7 +562,8 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
                                                              float* __restrict__ save_invstd, float* new_rm,
                                                              float* new_rv,  // may alias rm / rv
                                                              int c, int hw, const Split sp, int slices = 1,
-                                                             int64_t pstride = 0, float* __restrict__ xo = nullptr) {
+                                                             int64_t pstride = 0, float* __restrict__ xo = nullptr,
+                                                             float* __restrict__ zo = nullptr) {
   using V = typename VecT<VEC>::T;
   __shared__ float coef[2];
   const int ch = blockIdx.x;
@@ -616,15 +624,16 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
     const int vv = (int)threadIdx.x + u * 256;
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
-      V t = r[u], q;
+      V t = r[u], q, z;
       if (res) q = *reinterpret_cast<const V*>(res + off);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         float f = fmaf(vget(t, i), sc, sh);
         if (res) f += vget(q, i);
-        if (relu) f = fmaxf(f, 0.f);
-        vset(t, i, f);
+        vset(z, i, f);
+        vset(t, i, bn_act(f, relu));
       }
+      if (zo) *reinterpret_cast<V*>(zo + off) = z;
       *reinterpret_cast<V*>(y + off) = t;
     }
   }
@@ -642,7 +651,29 @@ __global__ void __launch_bounds__(256) bn_sum_parts_kernel(const float* __restri
   }
 }
 
-template <int VEC, bool RES>
+// Slice sums that ride along in another kernel's launch: workgroups past the kernel's own run them, job after job.
+constexpr int kMaxSideSums = 2;
+struct SideSums {
+  SplitSum job[kMaxSideSums];
+  int64_t end[kMaxSideSums];  // workgroups of jobs 0..k together
+  int count;
+};
+__device__ __forceinline__ void run_side_sum(const SideSums& ss, int64_t b) {
+#pragma unroll
+  for (int k = 0; k < kMaxSideSums; ++k) {
+    const int64_t start = k ? ss.end[k - 1] : 0;
+    if (k < ss.count && b >= start && b < ss.end[k]) {
+      if (ss.job[k].vec4)
+        split_sum_any<4>(ss.job[k], b - start, ss.end[k] - start);
+      else
+        split_sum_any<1>(ss.job[k], b - start, ss.end[k] - start);
+    }
+  }
+}
+
+// PARTS: g holds `slices` convolution partials of pstride elements each, summed here in slice order (the convolution
+// slice sum's order) before g2 is added; workgroups past the c channels run the side slice sums.
+template <int VEC, bool RES, bool PARTS = false>
 __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ g2,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ ry,
@@ -650,9 +681,15 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
                                                            const float* __restrict__ invstd,
                                                            const float* __restrict__ gamma, float* __restrict__ gx,
                                                            float* __restrict__ dgamma, float* __restrict__ dbeta,
-                                                           float* __restrict__ gzo, int c, int hw, const Split sp) {
+                                                           float* __restrict__ gzo, int c, int hw, const Split sp,
+                                                           int act, int slices = 1, int64_t pstride = 0,
+                                                           const SideSums side = SideSums{}) {
   using V = typename VecT<VEC>::T;
   __shared__ float kc[5];
+  if (PARTS && (int)blockIdx.x >= c) {
+    run_side_sum(side, (int64_t)blockIdx.x - c);
+    return;
+  }
   const int ch = blockIdx.x;
   const float mu = mean[ch], inv = invstd[ch];
   constexpr int NR = (int)(kFusedMax / (256 * VEC));  // vectors per thread
@@ -663,7 +700,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
       rg[u] = *reinterpret_cast<const V*>(g + off);
-      if (RES && g2) vadd(rg[u], *reinterpret_cast<const V*>(g2 + off));
+      if (RES && !PARTS && g2) vadd(rg[u], *reinterpret_cast<const V*>(g2 + off));
       rx[u] = *reinterpret_cast<const V*>(x + off);
       if (ry) rr[u] = *reinterpret_cast<const V*>(ry + off);
     } else {
@@ -675,13 +712,33 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       }
     }
   }
+  if (PARTS) {  // slice by slice, each slice's loads of all NR vectors in flight together; then g2
+    for (int z = 1; z < slices; ++z) {
+      V t[NR];
+#pragma unroll
+      for (int u = 0; u < NR; ++u) {
+        const int vv = (int)threadIdx.x + u * 256;
+        if (vv < sp.nv) t[u] = *reinterpret_cast<const V*>(g + z * pstride + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
+      }
+#pragma unroll
+      for (int u = 0; u < NR; ++u)
+        if ((int)threadIdx.x + u * 256 < sp.nv) vadd(rg[u], t[u]);
+    }
+    if (RES && g2) {
+#pragma unroll
+      for (int u = 0; u < NR; ++u) {
+        const int vv = (int)threadIdx.x + u * 256;
+        if (vv < sp.nv) vadd(rg[u], *reinterpret_cast<const V*>(g2 + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)));
+      }
+    }
+  }
   double s1 = 0.0, s2 = 0.0;
 #pragma unroll
   for (int u = 0; u < NR; ++u)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       float gz = vget(rg[u], i);
-      if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+      if (ry) gz = bn_act_grad(gz, vget(rr[u], i), act);
       const float xhat = (vget(rx[u], i) - mu) * inv;
       s1 += (double)gz;
       s2 += (double)gz * (double)xhat;
@@ -705,7 +762,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         float gz = vget(rg[u], i);
-        if (ry && !(vget(rr[u], i) > 0.f)) gz = 0.f;
+        if (ry) gz = bn_act_grad(gz, vget(rr[u], i), act);
         vset(z, i, gz);
         vset(o, i, bwd_elem(gz, vget(rx[u], i), 1.f, false, k));
       }
@@ -744,26 +801,27 @@ static int launch_stats(const Split& sp, const float* x, double* part, int64_t c
 
 // y = x * (invstd * gamma) + (beta - mean * invstd * gamma) [ReLU] with per-channel mean / invstd arrays.
 static int launch_apply(int64_t n, int64_t c, int64_t hw, const float* x, const float* mean, const float* invstd,
-                        const float* gamma, const float* beta, const float* res, float* y, int relu, hipStream_t s) {
-  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && (!res || al16(res));
+                        const float* gamma, const float* beta, const float* res, float* y, int relu, hipStream_t s,
+                        float* zo = nullptr) {
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && (!res || al16(res)) && al16(zo);
   const int64_t vw = vec ? 4 : 1, total_v = n * c * hw / vw;
   if (hw < kFlatPlane && total_v < ((int64_t)1 << 31)) {
     const FastDiv dh = make_fastdiv((uint32_t)(hw / vw)), dc = make_fastdiv((uint32_t)c);
     const dim3 grid(grid1d(total_v, 256, 16384));
     if (vec)
       hipLaunchKernelGGL(bn_apply_flat_kernel<4>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, res, y, total_v,
-                         dh, dc, (int)c, relu);
+                         dh, dc, (int)c, relu, zo);
     else
       hipLaunchKernelGGL(bn_apply_flat_kernel<1>, grid, dim3(256), 0, s, x, mean, invstd, gamma, beta, res, y, total_v,
-                         dh, dc, (int)c, relu);
+                         dh, dc, (int)c, relu, zo);
     return launch_check("bn_apply_flat_kernel");
   }
   if (vec)
     hipLaunchKernelGGL(bn_apply_kernel<true>, apply_grid(n * c, hw, 4), dim3(256), 0, s, x, mean, invstd, nullptr,
-                       0.0, gamma, beta, res, y, (int)c, (int)hw, relu);
+                       0.0, gamma, beta, res, y, (int)c, (int)hw, relu, zo);
   else
     hipLaunchKernelGGL(bn_apply_kernel<false>, apply_grid(n * c, hw, 1), dim3(256), 0, s, x, mean, invstd, nullptr,
-                       0.0, gamma, beta, res, y, (int)c, (int)hw, relu);
+                       0.0, gamma, beta, res, y, (int)c, (int)hw, relu, zo);
   return launch_check("bn_apply_kernel");
 }
 
@@ -801,77 +859,80 @@ OMT_EXPORT size_t omt_bn_train_workspace(int64_t n, int64_t c, int64_t hw) {
 
 OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
                                     const float* beta, const float* running_mean, const float* running_var,
-                                    double momentum, double eps, int relu, const float* residual, float* y,
+                                    double momentum, double eps, int relu, const float* residual, float* y, float* z,
                                     float* save_mean, float* save_invstd, float* new_rm, float* new_rv,
                                     void* workspace, size_t workspace_bytes, void* stream) {
   if (!x || !gamma || !beta || !y || !save_mean || !save_invstd) return fail(OMT_INVALID, "omt_bn_train_fwd: null pointer");
+  if (relu < OMT_ACT_NONE || relu > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_train_fwd: activation %d", relu);
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd: size not covered");
   if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
     return fail(OMT_INVALID, "omt_bn_train_fwd: workspace too small");
   hipStream_t s = stream_of(stream);
   const Split sp = bn_split(n, c, hw, al16(x));
   if (n * hw <= kFusedMax) {
-    const bool vec = sp.vec == 4 && al16(y) && (!residual || al16(residual));
+    const bool vec = sp.vec == 4 && al16(y) && (!residual || al16(residual)) && al16(z);
     const Split f = vec ? sp : bn_split(n, c, hw, false);
     if (vec)
       hipLaunchKernelGGL(bn_train_fused_kernel<4>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
                          running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
-                         (int)hw, f);
+                         (int)hw, f, 1, 0, nullptr, z);
     else
       hipLaunchKernelGGL(bn_train_fused_kernel<1>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
                          running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
-                         (int)hw, f);
+                         (int)hw, f, 1, 0, nullptr, z);
     return launch_check("bn_train_fused_kernel");
   }
   double* part = (double*)workspace;
   if (int st = launch_stats(sp, x, part, c, hw, s)) return st;
   const double m = (double)(n * hw);
-  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && al16(residual);
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && al16(residual) && al16(z);
   const dim3 ag = apply_grid(n * c, hw, vec ? 4 : 1), grid(ag.x * ag.y);
   if (hw >= kFlatPlane && (int64_t)ag.x * ag.y < ((int64_t)1 << 31)) {  // the apply finalizes its own channel
     const int rev = n * c * hw * 4 >= kRevApplyBytes;
     if (vec)
       hipLaunchKernelGGL(bn_train_apply_kernel<true>, grid, dim3(256), 0, s, x, (const double*)part, sp.slices, m,
                          momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta,
-                         residual, y, (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev);
+                         residual, y, (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 0, z);
     else
       hipLaunchKernelGGL(bn_train_apply_kernel<false>, grid, dim3(256), 0, s, x, (const double*)part, sp.slices, m,
                          momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta,
-                         residual, y, (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev);
+                         residual, y, (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 0, z);
     return launch_check("bn_train_apply_kernel");
   }
   hipLaunchKernelGGL(bn_stats_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, x, (const double*)part, (int)c,
                      (int)hw, sp.slices, m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm,
                      new_rv);
   if (int st = launch_check("bn_stats_fin_kernel")) return st;
-  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s);
+  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s, z);
 }
 
 OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts, int slices, float* x,
                                       const float* gamma, const float* beta, const float* running_mean,
                                       const float* running_var, double momentum, double eps, int relu,
-                                      const float* residual, float* y, float* save_mean, float* save_invstd,
+                                      const float* residual, float* y, float* z, float* save_mean, float* save_invstd,
                                       float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
                                       void* stream) {
   if (!parts || !x || !gamma || !beta || !y || !save_mean || !save_invstd)
     return fail(OMT_INVALID, "omt_bn_train_fwd_parts: null pointer");
+  if (relu < OMT_ACT_NONE || relu > OMT_ACT_HARDSWISH)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_parts: activation %d", relu);
   if (slices < 1) return fail(OMT_INVALID, "omt_bn_train_fwd_parts: %d slices", slices);
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_parts: size not covered");
   if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
     return fail(OMT_INVALID, "omt_bn_train_fwd_parts: workspace too small");
   hipStream_t s = stream_of(stream);
   const int64_t total = n * c * hw;
-  const bool vec = hw % 4 == 0 && al16(parts) && al16(x) && al16(y) && al16(residual);
+  const bool vec = hw % 4 == 0 && al16(parts) && al16(x) && al16(y) && al16(residual) && al16(z);
   if (n * hw <= kFusedMax) {  // one launch: the slice sums, the statistics and the apply
     const Split f = bn_split(n, c, hw, vec);
     if (vec)
       hipLaunchKernelGGL((bn_train_fused_kernel<4, true>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma, beta,
                          running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, (int)hw, f, slices, total, x);
+                         new_rv, (int)c, (int)hw, f, slices, total, x, z);
     else
       hipLaunchKernelGGL((bn_train_fused_kernel<1, true>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma, beta,
                          running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, (int)hw, f, slices, total, x);
+                         new_rv, (int)c, (int)hw, f, slices, total, x, z);
     return launch_check("bn_train_fused_kernel");
   }
   const bool v4 = total % 4 == 0 && al16(parts) && al16(x);
@@ -882,17 +943,19 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
     hipLaunchKernelGGL(bn_sum_parts_kernel<1>, dim3(grid1d(nv, 256, 16384)), dim3(256), 0, s, parts, slices, nv, x);
   if (int st = launch_check("bn_sum_parts_kernel")) return st;
   return omt_bn_train_fwd_res(n, c, hw, x, gamma, beta, running_mean, running_var, momentum, eps, relu, residual, y,
-                              save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
+                              z, save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
 }
 
 OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const float* x, const double* stats,
                                       int groups, size_t stats_bytes, const float* gamma, const float* beta, const float* running_mean,
                                       const float* running_var, double momentum, double eps, int relu,
-                                      const float* residual, float* y, float* save_mean, float* save_invstd,
+                                      const float* residual, float* y, float* z, float* save_mean, float* save_invstd,
                                       float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes,
                                       void* stream) {
   if (!x || !stats || !gamma || !beta || !y || !save_mean || !save_invstd)
     return fail(OMT_INVALID, "omt_bn_train_fwd_stats: null pointer");
+  if (relu < OMT_ACT_NONE || relu > OMT_ACT_HARDSWISH)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_stats: activation %d", relu);
   if (groups < 1) return fail(OMT_INVALID, "omt_bn_train_fwd_stats: %d column groups", groups);
   if (c < 0 || (uint64_t)c * (uint64_t)groups * 2 * sizeof(double) > stats_bytes)
     return fail(OMT_INVALID, "omt_bn_train_fwd_stats: %d groups of %lld channels exceed the %zu-byte stats buffer",
@@ -907,24 +970,24 @@ OMT_EXPORT int omt_bn_train_fwd_stats(int64_t n, int64_t c, int64_t hw, const fl
   hipLaunchKernelGGL(bn_stats_groups_kernel, dim3((unsigned)S, (unsigned)c), dim3(256), 0, s, stats, groups, part);
   if (int st = launch_check("bn_stats_groups_kernel")) return st;
   const double m = (double)(n * hw);
-  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && al16(residual);
+  const bool vec = hw % 4 == 0 && al16(x) && al16(y) && al16(residual) && al16(z);
   const dim3 ag = apply_grid(n * c, hw, vec ? 4 : 1), grid(ag.x * ag.y);
   if (hw >= kFlatPlane && (int64_t)ag.x * ag.y < ((int64_t)1 << 31)) {
     const int rev = n * c * hw * 4 >= kRevApplyBytes;
     if (vec)
       hipLaunchKernelGGL(bn_train_apply_kernel<true>, grid, dim3(256), 0, s, x, (const double*)part, S, m, momentum,
                          eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta, residual, y,
-                         (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 1);
+                         (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 1, z);
     else
       hipLaunchKernelGGL(bn_train_apply_kernel<false>, grid, dim3(256), 0, s, x, (const double*)part, S, m, momentum,
                          eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv, gamma, beta, residual, y,
-                         (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 1);
+                         (int)c, (int)hw, relu, (int)ag.x, (int)ag.y, rev, 1, z);
     return launch_check("bn_train_apply_kernel");
   }
   hipLaunchKernelGGL(bn_stats_shift0_fin_kernel, dim3(grid1d(c, 256)), dim3(256), 0, s, (const double*)part, (int)c, S,
                      m, momentum, eps, running_mean, running_var, save_mean, save_invstd, new_rm, new_rv);
   if (int st = launch_check("bn_stats_shift0_fin_kernel")) return st;
-  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s);
+  return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s, z);
 }
 
 OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
@@ -932,7 +995,7 @@ OMT_EXPORT int omt_bn_train_fwd(int64_t n, int64_t c, int64_t hw, const float* x
                                 double momentum, double eps, int relu, float* y, float* save_mean, float* save_invstd,
                                 float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes, void* stream) {
   return omt_bn_train_fwd_res(n, c, hw, x, gamma, beta, running_mean, running_var, momentum, eps, relu, nullptr, y,
-                              save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
+                              nullptr, save_mean, save_invstd, new_rm, new_rv, workspace, workspace_bytes, stream);
 }
 
 OMT_EXPORT int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
@@ -940,6 +1003,7 @@ OMT_EXPORT int omt_bn_eval_fwd(int64_t n, int64_t c, int64_t hw, const float* x,
                                int relu, float* y, void* stream) {
   if (!x || !gamma || !beta || !running_mean || !running_var || !y)
     return fail(OMT_INVALID, "omt_bn_eval_fwd: null pointer");
+  if (relu < OMT_ACT_NONE || relu > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_eval_fwd: activation %d", relu);
   if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_eval_fwd: size not covered");
   hipStream_t s = stream_of(stream);
   const bool vec = (hw % 4) == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0;
@@ -959,20 +1023,23 @@ OMT_EXPORT size_t omt_bn_bwd_workspace(int64_t n, int64_t c, int64_t hw) {
   return (size_t)(c * kMaxSlices * 2) * sizeof(double) + (size_t)(c * 5) * sizeof(float);
 }
 
-// The backward of every BN entry point: gz = g (+ g2) masked by relu_y > 0; RES also writes gz to gzo.
+// The backward of every BN entry point: gz = g (+ g2) through the activation's gradient (relu_y: the ReLU's output,
+// masked where not > 0, or the hardswish's input: bn_act_grad), or as it is when relu_y is null; RES also writes gz to
+// gzo.
 template <bool RES>
 static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
                        const float* relu_y, const float* save_mean, const float* save_invstd, const float* gamma,
-                       float* gx, float* dgamma, float* dbeta, float* gzo, void* workspace, hipStream_t s) {
+                       float* gx, float* dgamma, float* dbeta, float* gzo, void* workspace, hipStream_t s,
+                       int act = OMT_ACT_RELU) {
   const bool aligned = al16(g) && al16(g2) && al16(x) && al16(relu_y) && al16(gx) && al16(gzo);
   const Split sp = bn_split(n, c, hw, aligned);
   if (n * hw <= kFusedMax) {
     if (sp.vec == 4)
       hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y,
-                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp);
+                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act);
     else
       hipLaunchKernelGGL((bn_bwd_fused_kernel<1, RES>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y,
-                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp);
+                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act);
     return launch_check("bn_bwd_fused_kernel");
   }
   double* part = (double*)workspace;
@@ -980,10 +1047,10 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
   const dim3 pgrid((unsigned)c, (unsigned)sp.slices);
   if (sp.vec == 4)
     hipLaunchKernelGGL((bn_bwd_part_kernel<4, RES>), pgrid, dim3(256), 0, s, g, g2, x, relu_y, save_mean, save_invstd,
-                       part, (int)c, (int)hw, sp);
+                       part, (int)c, (int)hw, sp, act);
   else
     hipLaunchKernelGGL((bn_bwd_part_kernel<1, RES>), pgrid, dim3(256), 0, s, g, g2, x, relu_y, save_mean, save_invstd,
-                       part, (int)c, (int)hw, sp);
+                       part, (int)c, (int)hw, sp, act);
   if (int st = launch_check("bn_bwd_part_kernel")) return st;
   const double m = (double)(n * hw);
   const dim3 ag = apply_grid(n * c, hw, sp.vec), grid(ag.x * ag.y);
@@ -992,11 +1059,11 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
     if (sp.vec == 4)
       hipLaunchKernelGGL((bn_bwd_train_apply_kernel<4, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y,
                          (const double*)part, sp.slices, m, save_mean, save_invstd, gamma, dgamma, dbeta, gx, gzo,
-                         (int)c, (int)(hw / 4), (int)ag.x, (int)ag.y, rev);
+                         (int)c, (int)(hw / 4), (int)ag.x, (int)ag.y, rev, act);
     else
       hipLaunchKernelGGL((bn_bwd_train_apply_kernel<1, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y,
                          (const double*)part, sp.slices, m, save_mean, save_invstd, gamma, dgamma, dbeta, gx, gzo,
-                         (int)c, (int)hw, (int)ag.x, (int)ag.y, rev);
+                         (int)c, (int)hw, (int)ag.x, (int)ag.y, rev, act);
     return launch_check("bn_bwd_train_apply_kernel");
   }
   // the apply pass needs the per-channel constants (gamma) whenever it runs: for gx, or for gzo
@@ -1011,18 +1078,18 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
     const dim3 grid(grid1d(total_v, 256, 16384));
     if (sp.vec == 4)
       hipLaunchKernelGGL((bn_bwd_apply_flat_kernel<4, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y, kc, gxo, gzo,
-                         total_v, dh, dc, (int)c);
+                         total_v, dh, dc, (int)c, act);
     else
       hipLaunchKernelGGL((bn_bwd_apply_flat_kernel<1, RES>), grid, dim3(256), 0, s, g, g2, x, relu_y, kc, gxo, gzo,
-                         total_v, dh, dc, (int)c);
+                         total_v, dh, dc, (int)c, act);
     return launch_check("bn_bwd_apply_flat_kernel");
   }
   if (sp.vec == 4)
     hipLaunchKernelGGL((bn_bwd_apply_kernel<4, RES>), apply_grid(n * c, hw, 4), dim3(256), 0, s, g, g2, x, relu_y, kc,
-                       gxo, gzo, (int)c, (int)(hw / 4));
+                       gxo, gzo, (int)c, (int)(hw / 4), act);
   else
     hipLaunchKernelGGL((bn_bwd_apply_kernel<1, RES>), apply_grid(n * c, hw, 1), dim3(256), 0, s, g, g2, x, relu_y, kc,
-                       gxo, gzo, (int)c, (int)hw);
+                       gxo, gzo, (int)c, (int)hw, act);
   return launch_check("bn_bwd_apply_kernel");
 }
 
@@ -1047,4 +1114,60 @@ OMT_EXPORT int omt_bn_bwd_res(int64_t n, int64_t c, int64_t hw, const float* g, 
     return fail(OMT_INVALID, "omt_bn_bwd_res: workspace too small");
   return bn_bwd_impl<true>(n, c, hw, g, g2, x, relu_y, save_mean, save_invstd, gamma, gx, dgamma, dbeta, gz, workspace,
                            stream_of(stream));
+}
+
+OMT_EXPORT int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g_parts, int slices, const float* g2,
+                                const float* x, int act, const float* act_in, const float* save_mean,
+                                const float* save_invstd, const float* gamma, float* gx, float* dgamma, float* dbeta,
+                                float* gz, const omt_slice_sum* sums, int count, void* stream) {
+  if (!g_parts || !x || !save_mean || !save_invstd || (gx && !gamma) || (act != OMT_ACT_NONE && !act_in) ||
+      (g2 && !gz) || (count > 0 && !sums))
+    return fail(OMT_INVALID, "omt_bn_bwd_parts: null pointer");
+  if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_bwd_parts: activation %d", act);
+  if (slices < 1 || slices > kMaxSlices) return fail(OMT_INVALID, "omt_bn_bwd_parts: %d slices", slices);
+  if (count < 0 || count > kMaxSideSums) return fail(OMT_INVALID, "omt_bn_bwd_parts: %d slice sums", count);
+  if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_bwd_parts: size not covered");
+  if (n * hw > kFusedMax) return fail(OMT_UNSUPPORTED, "omt_bn_bwd_parts: channels above %lld elements",
+                                      (long long)kFusedMax);
+  SideSums side{};
+  int64_t blocks = c;
+  for (int k = 0; k < count; ++k) {
+    const omt_slice_sum& j = sums[k];
+    if (j.slices < 0 || j.n < 0 || (j.slices > 0 && (!j.parts || !j.out)))
+      return fail(OMT_INVALID, "omt_bn_bwd_parts: slice sum %d", k);
+    if (j.slices == 0 || j.n == 0) continue;
+    side.job[side.count] = split_sum_of(j.parts, j.out, j.n, j.slices);
+    blocks += side.job[side.count].blocks;
+    side.end[side.count++] = blocks - c;
+  }
+  if (blocks >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_bn_bwd_parts: grid too large");
+  const bool aligned = al16(g_parts) && al16(g2) && al16(x) && al16(act_in) && al16(gx) && al16(gz);
+  const Split sp = bn_split(n, c, hw, aligned);
+  const float* ry = act == OMT_ACT_NONE ? nullptr : act_in;
+  const int64_t pstride = n * c * hw;
+  hipStream_t s = stream_of(stream);
+#define OMT_BWD_PARTS(V, R)                                                                                      \
+  hipLaunchKernelGGL((bn_bwd_fused_kernel<V, R, true>), dim3((unsigned)blocks), dim3(256), 0, s, g_parts, g2, x, ry, \
+                     save_mean, save_invstd, gamma, gx, dgamma, dbeta, gz, (int)c, (int)hw, sp, act, slices, pstride, side)
+  if (sp.vec == 4) {
+    if (gz) OMT_BWD_PARTS(4, true); else OMT_BWD_PARTS(4, false);
+  } else {
+    if (gz) OMT_BWD_PARTS(1, true); else OMT_BWD_PARTS(1, false);
+  }
+#undef OMT_BWD_PARTS
+  return launch_check("bn_bwd_fused_kernel");
+}
+
+OMT_EXPORT int omt_bn_bwd_act(int64_t n, int64_t c, int64_t hw, const float* g, const float* x, int act,
+                              const float* act_in, const float* save_mean, const float* save_invstd,
+                              const float* gamma, float* gx, float* dgamma, float* dbeta, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!g || !x || !save_mean || !save_invstd || (gx && !gamma) || (act != OMT_ACT_NONE && !act_in))
+    return fail(OMT_INVALID, "omt_bn_bwd_act: null pointer");
+  if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_bwd_act: activation %d", act);
+  if (!bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_bwd_act: size not covered");
+  if (!workspace || workspace_bytes < omt_bn_bwd_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_bwd_act: workspace too small");
+  return bn_bwd_impl<false>(n, c, hw, g, nullptr, x, act == OMT_ACT_NONE ? nullptr : act_in, save_mean, save_invstd,
+                            gamma, gx, dgamma, dbeta, nullptr, workspace, stream_of(stream), act);
 }

@@ -43,6 +43,7 @@
 #include <vector>
 
 #include "omt_internal.h"
+#include "slice_sum.h"
 #include "lds_dma.h"
 #include "tile_map.h"
 
@@ -1393,62 +1394,6 @@ __global__ void __launch_bounds__(256, 2) conv_bwd_dual_kernel(const GatherArgs 
   }
 }
 
-// Slice sums load kReduceBatch slices at a time (the loads in flight together, the additions still in slice order),
-// so a launch waits one memory latency per batch rather than per slice.
-constexpr int kReduceBatch = 8;
-
-template <int VEC>
-struct VecF;
-template <>
-struct VecF<1> {
-  using T = float;
-  static __device__ __forceinline__ void add(float* v, T t) { v[0] += t; }
-  static __device__ __forceinline__ void set(float* v, T t) { v[0] = t; }
-  static __device__ __forceinline__ T pack(const float* v) { return v[0]; }
-};
-template <>
-struct VecF<4> {
-  using T = float4;
-  static __device__ __forceinline__ void add(float* v, T t) { v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w; }
-  static __device__ __forceinline__ void set(float* v, T t) { v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w; }
-  static __device__ __forceinline__ T pack(const float* v) { return make_float4(v[0], v[1], v[2], v[3]); }
-};
-
-// v = sum_z part[z * nv + i] over z in slice order (vectors of VEC floats; nv vectors per slice).
-template <int VEC>
-__device__ __forceinline__ void sum_slices(const typename VecF<VEC>::T* __restrict__ part, int64_t nv, int64_t i,
-                                           int slices, float* v) {
-  using T = typename VecF<VEC>::T;
-  for (int z0 = 0; z0 < slices; z0 += kReduceBatch) {
-    T t[kReduceBatch];
-#pragma unroll
-    for (int u = 0; u < kReduceBatch; ++u)
-      if (z0 + u < slices) t[u] = part[(int64_t)(z0 + u) * nv + i];
-#pragma unroll
-    for (int u = 0; u < kReduceBatch; ++u)
-      if (z0 + u < slices) {
-        if (z0 + u == 0)
-          VecF<VEC>::set(v, t[u]);
-        else
-          VecF<VEC>::add(v, t[u]);
-      }
-  }
-}
-
-// Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i]. VEC 4 needs n % 4 == 0. Workgroups
-// b0 .. b0 + nb - 1 of the launch stride over the vectors.
-template <int VEC>
-__device__ __forceinline__ void split_sum(const float* __restrict__ part, float* __restrict__ out, int64_t n,
-                                          int slices, int64_t b0, int64_t nb) {
-  using T = typename VecF<VEC>::T;
-  const int64_t nv = n / VEC;
-  for (int64_t i = b0 * blockDim.x + threadIdx.x; i < nv; i += nb * blockDim.x) {
-    float v[VEC];
-    sum_slices<VEC>(reinterpret_cast<const T*>(part), nv, i, slices, v);
-    reinterpret_cast<T*>(out)[i] = VecF<VEC>::pack(v);
-  }
-}
-
 // Split-K gather epilogue: y[i] = act(sum_z part[z][i] + bias[c(i)]), slices summed in order; y is NCHW with
 // planes of `plane` elements over `P` channels. VEC 4 needs plane % 4 == 0 (a float4 then stays in one plane).
 struct GatherSum {
@@ -1496,73 +1441,6 @@ __device__ __forceinline__ void gather_sum(const GatherSum& r, int64_t b0, int64
     }
     reinterpret_cast<T*>(r.y)[i] = VecF<VEC>::pack(v);
   }
-}
-
-// Many slices (kGroupSlices and more): a workgroup takes 16 consecutive vectors, and each of its 16 groups of 16
-// threads sums a contiguous range of about slices / 16 slices in slice order (eight loads in flight); the group sums
-// are then added in group order. A fixed order, so still deterministic, and a sixteenth of the dependent load batches
-// per thread (a grad weight of 16 x 16 outputs over 251 slices waited 32 batches long in the plain order).
-constexpr int kGroupSlices = 32;
-template <int VEC>
-__device__ __forceinline__ void split_sum_grouped(const float* __restrict__ part, float* __restrict__ out, int64_t n,
-                                                  int slices, int64_t b0, int64_t nb) {
-  using T = typename VecF<VEC>::T;
-  __shared__ float red[16][16][VEC];
-  const int64_t nv = n / VEC;
-  const int tv = threadIdx.x & 15, grp = threadIdx.x >> 4;
-  const int per = (slices + 15) / 16, z0 = grp * per, z1 = min(slices, z0 + per);
-  const T* p = reinterpret_cast<const T*>(part);
-  for (int64_t base = b0 * 16; base < nv; base += nb * 16) {
-    const int64_t i = base + tv;
-    float v[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) v[e] = 0.f;
-    if (i < nv) {
-      for (int z = z0; z < z1; z += kReduceBatch) {
-        T t[kReduceBatch];
-#pragma unroll
-        for (int u = 0; u < kReduceBatch; ++u)
-          if (z + u < z1) t[u] = p[(int64_t)(z + u) * nv + i];
-#pragma unroll
-        for (int u = 0; u < kReduceBatch; ++u)
-          if (z + u < z1) {
-            if (z + u == z0)
-              VecF<VEC>::set(v, t[u]);
-            else
-              VecF<VEC>::add(v, t[u]);
-          }
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) red[grp][tv][e] = v[e];
-    __syncthreads();
-    if (grp == 0 && i < nv) {
-      float sum[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) sum[e] = red[0][tv][e];
-      for (int g2 = 1; g2 < 16; ++g2)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) sum[e] += red[g2][tv][e];
-      reinterpret_cast<T*>(out)[i] = VecF<VEC>::pack(sum);
-    }
-    __syncthreads();
-  }
-}
-
-struct SplitSum {
-  const float* part;
-  float* out;
-  int64_t n;
-  int slices;
-  bool vec4;
-  int64_t blocks;
-};
-template <int VEC>
-__device__ __forceinline__ void split_sum_any(const SplitSum& r, int64_t b0, int64_t nb) {
-  if (r.slices >= kGroupSlices)
-    split_sum_grouped<VEC>(r.part, r.out, r.n, r.slices, b0, nb);
-  else
-    split_sum<VEC>(r.part, r.out, r.n, r.slices, b0, nb);
 }
 
 template <int VEC>
@@ -2586,18 +2464,6 @@ static bool wgrad_uses_tap_major(const omt_conv_geo* g, const WgradPlan& pl) {
   return g->ci % (kWgradTiles[pl.tile].bq / 4) == 0;
 }
 // The slice sum of a split grad-weight launch (blocks 0 if the plan does not split).
-// The in-order sum of `slices` consecutive arrays of n floats at `part` (16-byte aligned) into `out`.
-static SplitSum split_sum_of(const float* part, float* out, int64_t n, int64_t slices) {
-  SplitSum r{};
-  r.part = part;
-  r.out = out;
-  r.n = n;
-  r.slices = (int)slices;
-  r.vec4 = r.n % 4 == 0 && (uintptr_t)out % 16 == 0;
-  const int64_t nv = r.vec4 ? r.n / 4 : r.n;
-  r.blocks = r.slices >= kGroupSlices ? std::min<int64_t>(cdiv(nv, 16), 8192) : grid1d(nv, 256, 8192);
-  return r;
-}
 static SplitSum wgrad_sum_of(const WgradArgs& a, const WgradPlan& pl, float* gw) {
   if (pl.slices <= 1) return SplitSum{};
   return split_sum_of(a.out, gw, (int64_t)a.P * a.Q, pl.slices);
@@ -2789,6 +2655,105 @@ static int conv_bwd_one(const omt_conv_geo* g, const float* x, const float* gy, 
   else
     hipLaunchKernelGGL((dual_reduce_kernel<1, 1>), rgrid, dim3(256), 0, s, gsum, wsum);
   return launch_check("dual_reduce_kernel");
+}
+
+// conv_bwd_one without its slice sums: grad input's partials stay unsummed when split into 2..max_gx slices and their
+// sum is plain (no bias, ReLU or super-pixel scatter: a grad input's always is); grad weight's sum is returned as a job.
+static int conv_bwd_one_parts(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx,
+                              float* gw, void* workspace, hipStream_t s, int max_gx, const float** gx_parts,
+                              int* gx_slices, SplitSum& wjob) {
+  const size_t dbytes = dgrad_workspace_one(g);
+  void* dws = dbytes ? workspace : nullptr;
+  void* wws = wgrad_workspace_one(g) ? (char*)workspace + align256(dbytes) : nullptr;
+  GatherArgs ga;
+  GatherPlan dp;
+  int64_t maxq = 0;
+  float* part = nullptr;
+  if (int st = dgrad_prepare(g, gy, w, gx, dws, s, ga, dp, maxq, part)) return st;
+  WgradArgs wa;
+  WgradPlan wp;
+  const dim3 wgrid = wgrad_prepare(g, x, gy, gw, wws, wa, wp);
+  *gx_parts = nullptr;
+  *gx_slices = 1;
+  wjob = wgrad_sum_of(wa, wp, gw);
+  if (!dual_tiles(dp, wp)) {
+    int unsummed = ga.d2s ? 1 : max_gx;
+    if (int st = run_gather(ga, dp, g->n, maxq, part, s, &unsummed)) return st;
+    if (unsummed > 1) {
+      *gx_parts = ga.part;
+      *gx_slices = unsummed;
+    }
+    if (wgrad_uses_tap_major(g, wp))
+      wgrad_dispatch<kTapMajor>(wp.tile, wa, wgrid, s);
+    else
+      wgrad_dispatch<kGeneric>(wp.tile, wa, wgrid, s);
+    return launch_check("conv_wgrad_kernel");
+  }
+  const dim3 ggrid = gather_grid(ga, dp, g->n, maxq, part);
+  const DualGrid d{(int)ggrid.x, (int)ggrid.y, (int)ggrid.z, (int)wgrid.x, (int)wgrid.y, (int)wgrid.z};
+  const int64_t blocks = (int64_t)d.gx * d.gy * d.gz + (int64_t)d.wx * d.wy * d.wz;
+  if (blocks >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_conv_bwd_parts: grid too large");
+  const bool gtap = gather_uses_tap_major(ga, dp), wtap = wgrad_uses_tap_major(g, wp);
+  const bool deep = gtile(dp.tile).bk == 64;
+  const dim3 grid((unsigned)blocks);
+#define OMT_DUAL(BK, GM, WM) hipLaunchKernelGGL((conv_bwd_dual_kernel<BK, GM, WM>), grid, dim3(256), 0, s, ga, wa, d)
+  if (ga.wplace) {
+    switch ((deep ? 2 : 0) + (wtap ? 1 : 0)) {
+      case 3: OMT_DUAL(64, kTapInPlace, kTapMajor); break;
+      case 2: OMT_DUAL(64, kTapInPlace, kGeneric); break;
+      case 1: OMT_DUAL(16, kTapInPlace, kTapMajor); break;
+      default: OMT_DUAL(16, kTapInPlace, kGeneric); break;
+    }
+  } else switch ((deep ? 4 : 0) + (gtap ? 2 : 0) + (wtap ? 1 : 0)) {
+    case 7: OMT_DUAL(64, kTapMajor, kTapMajor); break;
+    case 6: OMT_DUAL(64, kTapMajor, kGeneric); break;
+    case 5: OMT_DUAL(64, kGeneric, kTapMajor); break;
+    case 4: OMT_DUAL(64, kGeneric, kGeneric); break;
+    case 3: OMT_DUAL(16, kTapMajor, kTapMajor); break;
+    case 2: OMT_DUAL(16, kTapMajor, kGeneric); break;
+    case 1: OMT_DUAL(16, kGeneric, kTapMajor); break;
+    default: OMT_DUAL(16, kGeneric, kGeneric); break;
+  }
+#undef OMT_DUAL
+  if (int st = launch_check("conv_bwd_dual_kernel")) return st;
+  const GatherSum gsum = gather_sum_of(ga, dp);
+  if (!gsum.blocks) return OMT_OK;
+  if (gsum.slices <= max_gx && !gsum.bias && !gsum.relu && !gsum.d2s && !gsum.nhwc) {
+    *gx_parts = gsum.part;
+    *gx_slices = gsum.slices;
+    return OMT_OK;
+  }
+  return launch_gather_sum(gsum, s);
+}
+
+OMT_EXPORT int omt_conv_bwd_parts(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx,
+                                  float* gw, void* workspace, size_t workspace_bytes, int max_gx_slices,
+                                  const float** gx_parts, int* gx_slices, omt_slice_sum* gw_sum, void* stream) {
+  if (!g || !x || !gy || !w || !gx || !gw || !gx_parts || !gx_slices || !gw_sum)
+    return fail(OMT_INVALID, "omt_conv_bwd_parts: null pointer");
+  Chunks ch;
+  if (int st = chunk_check(g, "omt_conv_bwd_parts", ch)) return st;
+  if (ch.count != 1) return fail(OMT_UNSUPPORTED, "omt_conv_bwd_parts: the batch runs in chunks");
+  const size_t need = omt_conv_bwd_workspace(g);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OMT_INVALID, "omt_conv_bwd_parts: workspace of %zu bytes needed", need);
+  SplitSum job{};
+  if (int st = conv_bwd_one_parts(g, x, gy, w, gx, gw, workspace, stream_of(stream), max_gx_slices, gx_parts,
+                                  gx_slices, job))
+    return st;
+  *gw_sum = omt_slice_sum{job.part, job.out, job.blocks ? job.n : 0, job.blocks ? job.slices : 0};
+  return OMT_OK;
+}
+
+OMT_EXPORT int omt_slice_sums(const omt_slice_sum* sums, int count, void* stream) {
+  if (count < 0 || (count > 0 && !sums)) return fail(OMT_INVALID, "omt_slice_sums: arguments");
+  for (int i = 0; i < count; ++i) {
+    const omt_slice_sum& j = sums[i];
+    if (j.slices <= 0) continue;
+    if (!j.parts || !j.out || j.n < 0) return fail(OMT_INVALID, "omt_slice_sums: sum %d", i);
+    if (int st = launch_split_sum(split_sum_of(j.parts, j.out, j.n, j.slices), stream_of(stream))) return st;
+  }
+  return OMT_OK;
 }
 
 OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* gy, const float* w, float* gx,

@@ -67,6 +67,22 @@ __device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
 
+// Hardswish and its gradient as PyTorch defines them (torch.nn.Hardswish documentation), in the same order of
+// operations as its CPU kernels, so that results agree to the last bit in most cases. Shared by the pointwise kernels
+// and the BatchNorm kernels that apply it after the normalization.
+__device__ __forceinline__ float hardswish_f(float x) { return x * fminf(fmaxf(x + 3.f, 0.f), 6.f) / 6.f; }
+__device__ __forceinline__ float hardswish_grad(float g, float x) {
+  return x <= -3.f ? 0.f : (x < 3.f ? g * (x / 3.f + 0.5f) : g);
+}
+// The activation after a BatchNorm: act OMT_ACT_NONE, OMT_ACT_RELU or OMT_ACT_HARDSWISH.
+__device__ __forceinline__ float bn_act(float v, int act) {
+  return act == OMT_ACT_RELU ? fmaxf(v, 0.f) : (act == OMT_ACT_HARDSWISH ? hardswish_f(v) : v);
+}
+// The gradient through that activation: r is the ReLU's output (masked where not > 0) or the hardswish's input.
+__device__ __forceinline__ float bn_act_grad(float g, float r, int act) {
+  return act == OMT_ACT_RELU ? (r > 0.f ? g : 0.f) : (act == OMT_ACT_HARDSWISH ? hardswish_grad(g, r) : g);
+}
+
 // Sum over the 64 lanes of a wave, in every lane: four DPP steps within each row of 16 lanes, each adding a disjoint
 // partner (quad_perm [1,0,3,2] and [2,3,0,1]: every lane holds its quad's sum; row_half_mirror pairs the two quads
 // of each 8-lane half, row_mirror the two halves), then the four row sums read from lanes 0, 16, 32 and 48. All 64

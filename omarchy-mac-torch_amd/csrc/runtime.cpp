@@ -218,7 +218,7 @@ bool capturing(hipStream_t s) {
 using namespace omt;
 
 OMT_EXPORT const char* omt_last_error(void) { return t_last_error.c_str(); }
-OMT_EXPORT int omt_abi_version(void) { return 4; }
+OMT_EXPORT int omt_abi_version(void) { return 5; }
 OMT_EXPORT int omt_hip_runtime_version(void) {
   int v = 0;
   (void)hipRuntimeGetVersion(&v);

@@ -20,6 +20,7 @@ NOALLOC_SCRATCH_BYTES = 64 << 20  # OMT_NOALLOC_SCRATCH_BYTES
 (OMT_PW_ADD, OMT_PW_MUL, OMT_PW_RELU, OMT_PW_THRESHOLD_BWD, OMT_PW_HARDSWISH, OMT_PW_HARDSWISH_BWD, OMT_PW_HARDSIGMOID,
  OMT_PW_HARDSIGMOID_BWD, OMT_PW_SCALE, OMT_PW_FILL, OMT_PW_ADD_SCALAR) = range(11)
 OMT_DT_F32, OMT_DT_I64 = 0, 1
+OMT_ACT_NONE, OMT_ACT_RELU, OMT_ACT_HARDSWISH = 0, 1, 2
 FOREACH_MAX_NUMEL = 1 << 16  # OMT_FOREACH_MAX_NUMEL
 
 
@@ -34,6 +35,11 @@ class ConvGeo(ctypes.Structure):
 class ConvPlan(ctypes.Structure):
     """omt_conv_plan: tile index and K slices of a dense convolution GEMM (reference ConvPlan, csrc/omt.h:230-236)."""
     _fields_ = [("tile", ctypes.c_int32), ("slices", ctypes.c_int32)]
+
+
+class SliceSum(ctypes.Structure):
+    """omt_slice_sum: a deferred in-order sum of `slices` arrays of n floats at `parts` into `out`."""
+    _fields_ = [("parts", ctypes.c_void_p), ("out", ctypes.c_void_p), ("n", ctypes.c_int64), ("slices", ctypes.c_int32)]
 
 
 class OmtError(RuntimeError):
@@ -142,6 +148,9 @@ SIGNATURES = {
     "omt_nll_loss_bwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
     "omt_conv_bwd_workspace": (SZ, [G]),
     "omt_conv_bwd": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_conv_bwd_parts": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, I32, ctypes.POINTER(VP), ctypes.POINTER(I32),
+                                 ctypes.POINTER(SliceSum), VP]),
+    "omt_slice_sums": (I32, [ctypes.POINTER(SliceSum), I32, VP]),
     "omt_conv_num_tiles": (I32, [I32]),
     "omt_conv_get_plan": (I32, [I32, G, PL, ctypes.POINTER(I32)]),
     "omt_conv_set_plan": (I32, [I32, G, PL]),
@@ -158,15 +167,16 @@ SIGNATURES = {
     "omt_dw_wgrad": (I32, [G, VP, VP, VP, VP, SZ, VP]),
     "omt_bn_train_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_train_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, SZ, VP]),
-    "omt_bn_train_fwd_res": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, VP, SZ,
-                                   VP]),
-    "omt_bn_train_fwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
-                                     VP, VP, SZ, VP]),
-    "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, SZ, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP,
-                                     VP, VP, SZ, VP]),
+    "omt_bn_train_fwd_res": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32] + [VP] * 8 + [SZ, VP]),
+    "omt_bn_train_fwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, VP, VP, VP, F64, F64, I32] + [VP] * 8 + [SZ, VP]),
+    "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, SZ, VP, VP, VP, VP, F64, F64, I32] + [VP] * 8 +
+                               [SZ, VP]),
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
     "omt_bn_bwd_workspace": (SZ, [I64, I64, I64]),
     "omt_bn_bwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_bwd_act": (I32, [I64, I64, I64, VP, VP, I32, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_bwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, I32, VP, VP, VP, VP, VP, VP, VP, VP,
+                               ctypes.POINTER(SliceSum), I32, VP]),
     "omt_bn_bwd_res": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_maxpool_fwd": (I32, [I64] * 13 + [VP, VP, VP, VP]),
     "omt_maxpool_bwd": (I32, [I64] * 13 + [VP, VP, VP, VP]),
@@ -178,7 +188,7 @@ SIGNATURES = {
     "omt_fused_sgd": (I32, [ctypes.POINTER(SgdParams), ctypes.POINTER(SgdTensor), I32, VP]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def _load():

@@ -5,13 +5,15 @@ buffer updates (BatchNorm running statistics and batch counters) kept inside the
 The rewrites then route the hot path to fused device ops, and the graph runs op by op on the device:
 
   0. training BatchNorm whose new running statistics are only copied back into its running-stat inputs
-     -> omt.bn_train_ (statistics updated in place, no copies), taking along a following ReLU or residual add + ReLU
-     (y = relu(bn(x) + r), the end of a ResNet basic block); the batch counters' increments (one add and one copy
-     each) become a single _foreach_add_;
+     -> omt.bn_train_ (statistics updated in place, no copies), taking along a following ReLU, residual add + ReLU
+     (y = relu(bn(x) + r), the end of a ResNet basic block) or hardswish (MobileNetV3; the hardswish's input, saved
+     for its backward, comes out as a fourth output); the batch counters' increments (one add and one copy each)
+     become a single _foreach_add_;
   1. training BatchNorm (`_native_batch_norm_legit_functional`) whose normalized output only feeds a ReLU
      -> omt.bn_relu_train (statistics, normalize and ReLU in the library's BN kernels);
   2. its backward, `native_batch_norm_backward(threshold_backward(g, y, 0), ...)` -> omt.bn_relu_backward (the ReLU
-     mask read from y inside the BN backward reductions and apply); where the masked gradient also feeds a residual
+     mask read from y inside the BN backward reductions and apply), `native_batch_norm_backward(hardswish_backward(g,
+     z), ...)` -> omt.bn_act_backward (the hardswish gradient likewise); where the masked gradient also feeds a residual
      branch (the end of a ResNet basic block) -> omt.bn_relu_res_backward, which returns it as a fourth output and
      takes along the add of the block output's two gradients in front of the mask;
   3. a dense convolution whose only user is a ReLU -> omt.conv_act (ReLU in the GEMM epilogue), or an eval BatchNorm
@@ -107,7 +109,7 @@ def _same_shape(a, b):
 
 
 def fuse_bn_train_in_place(graph):
-    count = {"bn": 0, "relu": 0, "add_relu": 0}
+    count = {"bn": 0, "relu": 0, "add_relu": 0, "hardswish": 0}
     for n in list(graph.nodes):
         if n.op != "call_function" or n.target is not aten._native_batch_norm_legit_functional.default:
             continue
@@ -128,8 +130,12 @@ def fuse_bn_train_in_place(graph):
             continue
         act, res, last, add, anchor = 0, None, out0, None, n
         u = _sole_user(out0)
+        hs = [v for v in out0.users if v.op == "call_function" and v.target is aten.hardswish.default]
         if u is not None and u.op == "call_function" and u.target is aten.relu.default:
             act, last = 1, u
+        elif len(hs) == 1 and all(v is hs[0] or v.op == "output" for v in out0.users):
+            # hardswish, its input saved for the backward (a graph output) or not: the fused node returns it as z
+            act, last = 2, hs[0]
         elif (u is not None and u.op == "call_function" and u.target is aten.add.Tensor and len(u.args) == 2
               and not u.kwargs):
             other = u.args[1] if u.args[0] is out0 else u.args[0]
@@ -151,6 +157,9 @@ def fuse_bn_train_in_place(graph):
                 graph.erase_node(gi)
         last.replace_all_uses_with(y)
         graph.erase_node(last)
+        if act == 2 and out0.users:
+            z = _call_before(graph, anchor, operator.getitem, (fused, 3), meta_from=out0)
+            out0.replace_all_uses_with(z)
         graph.erase_node(c3)
         graph.erase_node(c4)
         outs[3].replace_all_uses_with(rm)  # outputs: the updated buffers
@@ -165,7 +174,7 @@ def fuse_bn_train_in_place(graph):
         if res is not None:
             count["add_relu"] += 1
         elif act:
-            count["relu"] += 1
+            count["relu" if act == 1 else "hardswish"] += 1
     return count
 
 
@@ -233,6 +242,29 @@ def fuse_bn_relu_backward(graph):
             continue
         gout, y = g.args[0], g.args[1]
         fused = _call_before(graph, n, omt.bn_relu_backward.default, (gout, x, y, w, mean, invstd, list(mask)))
+        _move_getitems(graph, n, fused)
+        graph.erase_node(n)
+        graph.erase_node(g)
+        count += 1
+    return count
+
+
+def fuse_bn_hardswish_backward(graph):
+    """native_batch_norm_backward(hardswish_backward(g, z), x, ...) -> omt.bn_act_backward(g, x, z, ..., act 2): the
+    hardswish gradient taken inside the BatchNorm backward's reads (z, the hardswish's input, is the fused forward's
+    fourth output)."""
+    count = 0
+    for n in list(graph.nodes):
+        if n.op != "call_function" or n.target is not aten.native_batch_norm_backward.default:
+            continue
+        g, x, w, rm, rv, mean, invstd, train, eps, mask = n.args[:10]
+        if not train or w is None or not _on_device_f32(x, 4):
+            continue
+        if not (isinstance(g, Node) and g.op == "call_function" and g.target is aten.hardswish_backward.default
+                and len(g.users) == 1 and _on_device_f32(g.args[1], 4)):
+            continue
+        gout, z = g.args[0], g.args[1]
+        fused = _call_before(graph, n, omt.bn_act_backward.default, (gout, x, z, w, mean, invstd, 2, list(mask)))
         _move_getitems(graph, n, fused)
         graph.erase_node(n)
         graph.erase_node(g)
@@ -324,7 +356,7 @@ def fuse_conv_epilogues(graph):
 
 
 def fuse_conv_bn_train(graph):
-    """bn_train_(convolution(x, cw, None, ...), ...) -> omt.conv_bn_train_(x, cw, stride, padding, ...), whose fourth
+    """bn_train_(convolution(x, cw, None, ...), ...) -> omt.conv_bn_train_(x, cw, stride, padding, ...), whose fifth
     output is the convolution's (the BatchNorm backward reads it): with a K-split plan the BatchNorm sums the
     convolution's partials itself (one launch fewer). The convolution's other uses must come after the BatchNorm."""
     count = 0
@@ -341,8 +373,8 @@ def fuse_conv_bn_train(graph):
         w, b, rm, rv, momentum, eps, act, res = n.args[1:9]
         fused = _call_before(graph, n, omt.conv_bn_train_.default,
                              (cx, cw, list(stride), list(padding), w, b, rm, rv, momentum, eps, act, res))
-        out = _call_before(graph, n, operator.getitem, (fused, 3), meta_from=conv)
-        n.replace_all_uses_with(fused)  # its users are getitems 0-2, the same outputs of the fused node
+        out = _call_before(graph, n, operator.getitem, (fused, 4), meta_from=conv)
+        n.replace_all_uses_with(fused)  # its users are getitems 0-3, the same outputs of the fused node
         graph.erase_node(n)
         conv.replace_all_uses_with(out)
         graph.erase_node(conv)
@@ -354,7 +386,8 @@ def _rewrite(gm):
     g = gm.graph
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
              "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
-             "bn_relu_backward": fuse_bn_relu_backward(g), "conv_bn_train": fuse_conv_bn_train(g),
+             "bn_relu_backward": fuse_bn_relu_backward(g), "bn_hardswish_backward": fuse_bn_hardswish_backward(g),
+             "conv_bn_train": fuse_conv_bn_train(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()

@@ -300,13 +300,17 @@ def depthwise_wgrad(x, gy, ks, stride=1, padding=None):
 # ---- batch norm -------------------------------------------------------------------------------------------------
 
 def batch_norm_train(x, gamma, beta, running_mean=None, running_var=None, momentum=0.1, eps=1e-5, relu=False,
-                     functional=False):
-    """Training BatchNorm. Returns (y, save_mean, save_invstd) and, when functional, also the updated running stats
-    as new tensors (bn_stats_fin_functional); otherwise running_mean / running_var are updated in place."""
-    x = _need(x, "x", 4)
+                     functional=False, act=None, residual=None, return_z=False):
+    """Training BatchNorm, y = act(bn(x) + residual). Returns (y, save_mean, save_invstd) and, when functional, also
+    the updated running stats as new tensors (bn_stats_fin_functional); otherwise running_mean / running_var are
+    updated in place. act: _lib.OMT_ACT_* (default: ReLU if relu else none); return_z appends the activation's input
+    bn(x) + residual."""
+    x, residual = _need(x, "x", 4), _need(residual, "residual", 4)
     gamma, beta = _need(gamma, "gamma", 1), _need(beta, "beta", 1)
+    act = (_lib.OMT_ACT_RELU if relu else _lib.OMT_ACT_NONE) if act is None else int(act)
     n, c, h, w = x.shape
     y = torch.empty_like(x)
+    z = torch.empty_like(x) if return_z else None
     sm = torch.empty((c,), device=x.device, dtype=torch.float32)
     si = torch.empty_like(sm)
     if functional:
@@ -315,12 +319,11 @@ def batch_norm_train(x, gamma, beta, running_mean=None, running_var=None, moment
     else:
         nrm, nrv = running_mean, running_var
     ws, nb = _workspace(L.omt_bn_train_workspace(n, c, h * w), x.device)
-    check(L.omt_bn_train_fwd(n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean), _ptr(running_var),
-                             momentum, eps, int(relu), _ptr(y), _ptr(sm), _ptr(si), _ptr(nrm), _ptr(nrv), _ptr(ws), nb,
-                             _stream(x.device)), "batch_norm_train")
-    if functional:
-        return y, sm, si, nrm, nrv
-    return y, sm, si
+    check(L.omt_bn_train_fwd_res(n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean),
+                                 _ptr(running_var), momentum, eps, act, _ptr(residual), _ptr(y), _ptr(z), _ptr(sm),
+                                 _ptr(si), _ptr(nrm), _ptr(nrv), _ptr(ws), nb, _stream(x.device)), "batch_norm_train")
+    out = (y, sm, si, nrm, nrv) if functional else (y, sm, si)
+    return out + (z,) if return_z else out
 
 
 def batch_norm_train_stats(x, stats, groups, gamma, beta, running_mean=None, running_var=None, momentum=0.1,
@@ -339,8 +342,8 @@ def batch_norm_train_stats(x, stats, groups, gamma, beta, running_mean=None, run
     check(L.omt_bn_train_fwd_stats(n, c, h * w, _ptr(x), _ptr(stats), int(groups), stats.numel() * 8, _ptr(gamma),
                                    _ptr(beta),
                                    _ptr(running_mean), _ptr(running_var), momentum, eps, int(relu), _ptr(residual),
-                                   _ptr(y), _ptr(sm), _ptr(si), _ptr(running_mean), _ptr(running_var), _ptr(ws), nb,
-                                   _stream(x.device)), "batch_norm_train_stats")
+                                   _ptr(y), None, _ptr(sm), _ptr(si), _ptr(running_mean), _ptr(running_var), _ptr(ws),
+                                   nb, _stream(x.device)), "batch_norm_train_stats")
     return y, sm, si
 
 
@@ -365,6 +368,21 @@ def batch_norm_backward(g, x, save_mean, save_invstd, gamma, relu_y=None, output
     check(L.omt_bn_bwd(n, c, h * w, _ptr(g), _ptr(x), _ptr(relu_y), _ptr(_need(save_mean, "mean", 1)),
                        _ptr(_need(save_invstd, "invstd", 1)), _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg),
                        _ptr(db), _ptr(ws), nb, _stream(x.device)), "batch_norm_backward")
+    return gx, dg, db
+
+
+def batch_norm_backward_act(g, x, act, act_in, save_mean, save_invstd, gamma, output_mask=(True, True, True)):
+    """BatchNorm backward through its activation (omt_bn_bwd_act): act _lib.OMT_ACT_RELU with act_in the ReLU's output,
+    OMT_ACT_HARDSWISH with act_in the hardswish's input, OMT_ACT_NONE. Returns (gx, dgamma, dbeta)."""
+    g, x, act_in = _need(g, "g", 4), _need(x, "x", 4), _need(act_in, "act_in", 4)
+    n, c, h, w = x.shape
+    gx = torch.empty_like(x) if output_mask[0] else None
+    dg = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[1] else None
+    db = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[2] else None
+    ws, nb = _workspace(L.omt_bn_bwd_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_bwd_act(n, c, h * w, _ptr(g), _ptr(x), int(act), _ptr(act_in), _ptr(_need(save_mean, "mean", 1)),
+                           _ptr(_need(save_invstd, "invstd", 1)), _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg),
+                           _ptr(db), _ptr(ws), nb, _stream(x.device)), "batch_norm_backward_act")
     return gx, dg, db
 
 

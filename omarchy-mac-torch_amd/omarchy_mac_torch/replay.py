@@ -102,7 +102,7 @@ class ReplayedGraph:
             self.eager_only = "inputs that are not device tensors (CPU tensors, symbolic sizes)"
             return self._eager(a, self.eager_only)
         self.calls += 1
-        ptrs = [_ptr(t) for t in a]
+        ptrs = core.storage_ptrs(a)
         self.seen = ptrs if self.seen is None else [p if p == q else None for p, q in zip(ptrs, self.seen)]
         if self.calls <= WARMUP_CALLS:
             return self._eager(a, "warm-up")
@@ -151,7 +151,7 @@ class ReplayedGraph:
         return self._run(a)
 
     def _setup(self, a):
-        ptrs = [_ptr(t) for t in a]
+        ptrs = core.storage_ptrs(a)
         static = [self._in_place(i, p) for i, p in enumerate(ptrs)]
         inputs = [t if keep else _buffer_like(t) for t, keep in zip(a, static)]
         graph = graphs.Graph()
@@ -164,7 +164,9 @@ class ReplayedGraph:
         outs = list(outs)
         self.user = range(self.user_span[0], min(self.user_span[1], len(outs)))
         in_ptrs = {_ptr(t) for t, keep in zip(inputs, static) if keep}
-        self.captured_ptrs = [_ptr(t) for t in inputs]
+        self.captured_ptrs = core.storage_ptrs(inputs)
+        self.expected = [p if keep else 0 for p, keep in zip(self.captured_ptrs, static)]  # checked at each replay
+        self.dynamic = [i for i, keep in enumerate(static) if not keep]
         # only the input buffers are kept: a reference to an input read in place (a saved tensor the forward handed
         # out, a parameter) would count as a use of it, and the graph needs its address alone
         self.inputs = [None if keep else t for t, keep in zip(inputs, static)]
@@ -192,7 +194,7 @@ class ReplayedGraph:
     # ---- replay ----
 
     def _replay(self, a):
-        moved = [i for i, keep in enumerate(self.static) if keep and _ptr(a[i]) != self.captured_ptrs[i]]
+        moved = core.moved_inputs(a, self.expected)
         if moved:
             if self.kind == "backward":
                 # saved tensors of a forward that ran op by op: this call too; of a forward captured again: again
@@ -207,8 +209,8 @@ class ReplayedGraph:
         return self._run(a)
 
     def _run(self, a):
-        for i, keep in enumerate(self.static):
-            if not keep and a[i].data_ptr() != self.inputs[i].data_ptr():
+        for i in self.dynamic:
+            if a[i].data_ptr() != self.inputs[i].data_ptr():
                 self.inputs[i].copy_(a[i])
         self.graph.replay()
         STATS["replays"] += 1

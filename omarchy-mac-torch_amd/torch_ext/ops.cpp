@@ -364,31 +364,43 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_ref(cons
   auto r = at::_native_batch_norm_legit_functional(x, w, b, rm, rv, true, mom, eps);
   return {at::relu(std::get<0>(r)), std::get<1>(r), std::get<2>(r), std::get<3>(r), std::get<4>(r)};
 }
-static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_ref(const Tensor& x, const Tensor& w, const Tensor& b,
-                                                               const Tensor& rm, const Tensor& rv, double mom,
-                                                               double eps, int64_t act,
-                                                               const std::optional<Tensor>& res) {
+// act 1: ReLU, 2: hardswish (whose input z is also returned: its backward reads it), else none
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_train_inplace_ref(const Tensor& x, const Tensor& w,
+                                                                       const Tensor& b, const Tensor& rm,
+                                                                       const Tensor& rv, double mom, double eps,
+                                                                       int64_t act, const std::optional<Tensor>& res) {
   Tensor rm_ = rm, rv_ = rv;  // _native_batch_norm_legit updates them in place
   auto r = at::_native_batch_norm_legit(x, w, b, rm_, rv_, true, mom, eps);
-  Tensor y = std::get<0>(r);
-  if (defined(res)) y = y + *res;
-  return {act == 1 ? at::relu(y) : y, std::get<1>(r), std::get<2>(r)};
+  Tensor z = std::get<0>(r);
+  if (defined(res)) z = z + *res;
+  Tensor y = act == OMT_ACT_RELU ? at::relu(z) : act == OMT_ACT_HARDSWISH ? at::hardswish(z) : z;
+  return {y, std::get<1>(r), std::get<2>(r), act == OMT_ACT_HARDSWISH ? z : Tensor()};
 }
-// convolution (no bias) -> training BatchNorm (in place) [-> + residual] [-> ReLU]; also returns the convolution's
-// output, which the BatchNorm backward reads
-static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_ref(const Tensor& x, const Tensor& cw,
-                                                                    IntArrayRef stride, IntArrayRef padding,
-                                                                    const Tensor& w, const Tensor& b, const Tensor& rm,
-                                                                    const Tensor& rv, double mom, double eps,
-                                                                    int64_t act, const std::optional<Tensor>& res) {
+// convolution (no bias) -> training BatchNorm (in place) [-> + residual] [-> activation]; also returns the
+// convolution's output, which the BatchNorm backward reads
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_train_ref(const Tensor& x, const Tensor& cw,
+                                                                            IntArrayRef stride, IntArrayRef padding,
+                                                                            const Tensor& w, const Tensor& b,
+                                                                            const Tensor& rm, const Tensor& rv,
+                                                                            double mom, double eps, int64_t act,
+                                                                            const std::optional<Tensor>& res) {
   Tensor conv = at::convolution(x, cw, std::nullopt, stride, padding, {1, 1}, false, {0, 0}, 1);
   auto r = bn_train_inplace_ref(conv, w, b, rm, rv, mom, eps, act, res);
-  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), conv};
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r), conv};
 }
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_ref(const Tensor& g, const Tensor& x, const Tensor& y,
                                                                const Tensor& w, const Tensor& mean,
                                                                const Tensor& invstd, std::array<bool, 3> mask) {
   Tensor gz = at::threshold_backward(g, y, 0);
+  return at::native_batch_norm_backward(gz, x, w, std::nullopt, std::nullopt, mean, invstd, true, 0.0, mask);
+}
+// r: the ReLU's output (act 1) or the hardswish's input (act 2)
+static std::tuple<Tensor, Tensor, Tensor> bn_act_backward_ref(const Tensor& g, const Tensor& x, const Tensor& r,
+                                                              const Tensor& w, const Tensor& mean,
+                                                              const Tensor& invstd, int64_t act,
+                                                              std::array<bool, 3> mask) {
+  Tensor gz = act == OMT_ACT_RELU ? at::threshold_backward(g, r, 0)
+              : act == OMT_ACT_HARDSWISH ? at::hardswish_backward(g, r) : g;
   return at::native_batch_norm_backward(gz, x, w, std::nullopt, std::nullopt, mean, invstd, true, 0.0, mask);
 }
 static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_ref(const Tensor& g,
@@ -436,10 +448,12 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_dev(cons
   return {y, sm, si, nrm, nrv};
 }
 // Training BatchNorm with the running statistics updated in place, then the optional residual and ReLU.
-static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_, const Tensor& w, const Tensor& b,
-                                                               const Tensor& rm, const Tensor& rv, double mom,
-                                                               double eps, int64_t act,
-                                                               const std::optional<Tensor>& res_) {
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_, const Tensor& w,
+                                                                       const Tensor& b, const Tensor& rm,
+                                                                       const Tensor& rv, double mom, double eps,
+                                                                       int64_t act,
+                                                                       const std::optional<Tensor>& res_) {
+  cover(act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH, "activation none, ReLU or hardswish");
   cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
        "4-D float32 with contiguous parameters");
   Tensor x = contig(x_);
@@ -450,12 +464,13 @@ static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_dev(const Tensor& x_,
   }
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor y = empty_dev(x.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  Tensor z = act == OMT_ACT_HARDSWISH ? empty_dev(x.sizes()) : Tensor();
   Tensor ws = workspace(omt_bn_train_workspace(n, c, hw));
-  check(omt_bn_train_fwd_res(n, c, hw, fp(x), fp(w), fp(b), fp(rm), fp(rv), mom, eps, act == 1 ? 1 : 0,
-                             res.defined() ? fp(res) : nullptr, fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(ws),
-                             wsbytes(ws), cur_stream()),
+  check(omt_bn_train_fwd_res(n, c, hw, fp(x), fp(w), fp(b), fp(rm), fp(rv), mom, eps, (int)act,
+                             res.defined() ? fp(res) : nullptr, fpm(y), fpm(z), fpm(sm), fpm(si), fpm(rm), fpm(rv),
+                             wsptr(ws), wsbytes(ws), cur_stream()),
         "omt::bn_train_");
-  return {y, sm, si};
+  return {y, sm, si, z};
 }
 // The convolution leaves a K split of up to kFoldSlices slices unsummed and the BatchNorm sums them as it reads them
 // (in the slice order of the convolution's own slice sum: the convolution output and everything after it are
@@ -468,11 +483,13 @@ constexpr int kFoldSlices = 4;
 // read saves (graph replays, conv + BN + ReLU: [32,64,56^2] 3x3 +5.3 / -1.6 us, [128,32,32^2] +2.6 / -0.6 us;
 // [256,64,56^2] 3x3 +12 / -17 us, 1x1 from 256 channels -8 / -22 us).
 constexpr int64_t kBnOneLaunchMax = 8192, kStatsMinBytes = 64ll << 20;
-static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor& x_, const Tensor& cw_,
-                                                                    IntArrayRef stride, IntArrayRef padding,
-                                                                    const Tensor& w, const Tensor& b, const Tensor& rm,
-                                                                    const Tensor& rv, double mom, double eps,
-                                                                    int64_t act, const std::optional<Tensor>& res_) {
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor& x_, const Tensor& cw_,
+                                                                            IntArrayRef stride, IntArrayRef padding,
+                                                                            const Tensor& w, const Tensor& b,
+                                                                            const Tensor& rm, const Tensor& rv,
+                                                                            double mom, double eps, int64_t act,
+                                                                            const std::optional<Tensor>& res_) {
+  cover(act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH, "activation none, ReLU or hardswish");
   cover(stride.size() == 2 && padding.size() == 2 && stride[0] == stride[1] && padding[0] == padding[1],
         "uniform 2-D stride and padding");
   cover(kind_of(x_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && !channels_last(x_, cw_),
@@ -491,8 +508,9 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor
   Tensor ws = workspace(omt_conv_fwd_workspace(&g));
   const int64_t n = g.n, c = g.co, hw = g.oh * g.ow;
   Tensor y = empty_dev(conv.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  Tensor z = act == OMT_ACT_HARDSWISH ? empty_dev(conv.sizes()) : Tensor();
   const float* r = res.defined() ? fp(res) : nullptr;
-  const int relu = act == 1 ? 1 : 0;
+  const int relu = (int)act;
   if (n * hw > kBnOneLaunchMax && n * c * hw * 4 >= kStatsMinBytes) {
     // the statistics from the convolution's epilogue, so the BatchNorm reads the convolution output once; a plan
     // that splits K (or a batch run in chunks) is refused before any launch and takes the path below
@@ -504,10 +522,10 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor
       Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
       check(omt_bn_train_fwd_stats(n, c, hw, fp(conv), (const double*)wsptr(stats), groups, wsbytes(stats), fp(w),
                                    fp(b), fp(rm),
-                                   fp(rv), mom, eps, relu, r, fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws),
-                                   wsbytes(bws), cur_stream()),
+                                   fp(rv), mom, eps, relu, r, fpm(y), fpm(z), fpm(sm), fpm(si), fpm(rm), fpm(rv),
+                                   wsptr(bws), wsbytes(bws), cur_stream()),
             "omt::conv_bn_train_ (BatchNorm from the epilogue statistics)");
-      return {y, sm, si, conv};
+      return {y, sm, si, z, conv};
     }
     if (st != OMT_UNSUPPORTED) check(st, "omt::conv_bn_train_ (convolution with statistics)");
   }
@@ -519,13 +537,14 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(const Tensor
   Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
   if (slices > 1)
     check(omt_bn_train_fwd_parts(n, c, hw, parts, slices, fpm(conv), fp(w), fp(b), fp(rm), fp(rv), mom, eps, relu, r,
-                                 fpm(y), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws), cur_stream()),
+                                 fpm(y), fpm(z), fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws),
+                                 cur_stream()),
           "omt::conv_bn_train_ (BatchNorm of the partials)");
   else
-    check(omt_bn_train_fwd_res(n, c, hw, fp(conv), fp(w), fp(b), fp(rm), fp(rv), mom, eps, relu, r, fpm(y), fpm(sm),
-                               fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws), cur_stream()),
+    check(omt_bn_train_fwd_res(n, c, hw, fp(conv), fp(w), fp(b), fp(rm), fp(rv), mom, eps, relu, r, fpm(y), fpm(z),
+                               fpm(sm), fpm(si), fpm(rm), fpm(rv), wsptr(bws), wsbytes(bws), cur_stream()),
           "omt::conv_bn_train_ (BatchNorm)");
-  return {y, sm, si, conv};
+  return {y, sm, si, z, conv};
 }
 static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_, const Tensor& x_, const Tensor& y_,
                                                                const Tensor& w, const Tensor& mean,
@@ -540,6 +559,25 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_,
   check(omt_bn_bwd(n, c, hw, fp(g), fp(x), fp(y), fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg), fpm(db), wsptr(ws),
                    wsbytes(ws), cur_stream()),
         "omt::bn_relu_backward");
+  return {gx, dg, db};
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_act_backward_dev(const Tensor& g_, const Tensor& x_, const Tensor& r_,
+                                                              const Tensor& w, const Tensor& mean,
+                                                              const Tensor& invstd, int64_t act,
+                                                              std::array<bool, 3> mask) {
+  cover(act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH, "activation none, ReLU or hardswish");
+  cover(f32(g_) && f32(x_) && f32(r_) && x_.dim() == 4 && g_.sizes() == x_.sizes() && r_.sizes() == x_.sizes() &&
+            whole(w) && whole(mean) && whole(invstd),
+        "4-D float32 operands of one shape");
+  Tensor g = contig(g_), x = contig(x_), r = contig(r_);
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
+  Tensor dg = mask[1] ? empty_dev({c}) : Tensor();
+  Tensor db = mask[2] ? empty_dev({c}) : Tensor();
+  Tensor ws = workspace(omt_bn_bwd_workspace(n, c, hw));
+  check(omt_bn_bwd_act(n, c, hw, fp(g), fp(x), (int)act, fp(r), fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg),
+                       fpm(db), wsptr(ws), wsbytes(ws), cur_stream()),
+        "omt::bn_act_backward");
   return {gx, dg, db};
 }
 // The backward of BatchNorm -> [+ residual] -> ReLU at a residual block's end, with the incoming gradient the sum of
@@ -594,18 +632,19 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_k(const 
                                                                         const Tensor& rv, double mom, double eps) {
   return dev_or_ref<&bn_relu_train_dev, &bn_relu_train_ref>("omt::bn_relu_train", x, w, b, rm, rv, mom, eps);
 }
-static std::tuple<Tensor, Tensor, Tensor> bn_train_inplace_k(const Tensor& x, const Tensor& w, const Tensor& b,
-                                                             const Tensor& rm, const Tensor& rv, double mom,
-                                                             double eps, int64_t act,
-                                                             const std::optional<Tensor>& res) {
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_train_inplace_k(const Tensor& x, const Tensor& w,
+                                                                     const Tensor& b, const Tensor& rm,
+                                                                     const Tensor& rv, double mom, double eps,
+                                                                     int64_t act, const std::optional<Tensor>& res) {
   return dev_or_ref<&bn_train_inplace_dev, &bn_train_inplace_ref>("omt::bn_train_", x, w, b, rm, rv, mom, eps, act,
                                                                   res);
 }
-static std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bn_train_k(const Tensor& x, const Tensor& cw, IntArrayRef s,
-                                                                  IntArrayRef p, const Tensor& w, const Tensor& b,
-                                                                  const Tensor& rm, const Tensor& rv, double mom,
-                                                                  double eps, int64_t act,
-                                                                  const std::optional<Tensor>& res) {
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_train_k(const Tensor& x, const Tensor& cw,
+                                                                          IntArrayRef s, IntArrayRef p,
+                                                                          const Tensor& w, const Tensor& b,
+                                                                          const Tensor& rm, const Tensor& rv,
+                                                                          double mom, double eps, int64_t act,
+                                                                          const std::optional<Tensor>& res) {
   return dev_or_ref<&conv_bn_train_dev, &conv_bn_train_ref>("omt::conv_bn_train_", x, cw, s, p, w, b, rm, rv, mom, eps,
                                                             act, res);
 }
@@ -614,6 +653,12 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_k(const Tensor& g, co
                                                              const Tensor& invstd, std::array<bool, 3> mask) {
   return dev_or_ref<&bn_relu_backward_dev, &bn_relu_backward_ref>("omt::bn_relu_backward", g, x, y, w, mean, invstd,
                                                                   mask);
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_act_backward_k(const Tensor& g, const Tensor& x, const Tensor& r,
+                                                            const Tensor& w, const Tensor& mean, const Tensor& invstd,
+                                                            int64_t act, std::array<bool, 3> mask) {
+  return dev_or_ref<&bn_act_backward_dev, &bn_act_backward_ref>("omt::bn_act_backward", g, x, r, w, mean, invstd, act,
+                                                                mask);
 }
 static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_k(const Tensor& g,
                                                                          const std::optional<Tensor>& g2,
@@ -644,20 +689,26 @@ TORCH_LIBRARY(omt, m) {
   m.def("bn_relu_res_backward(Tensor g, Tensor? g2, Tensor x, Tensor y, Tensor w, Tensor mean, Tensor invstd, "
         "bool[3] mask) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("conv_act(Tensor x, Tensor w, Tensor? b, int[] stride, int[] padding, int act) -> Tensor");
-  // training BatchNorm updating the running statistics in place, then + residual and ReLU (act 1): the compile
-  // backend's form of BatchNorm -> [add] -> [ReLU] with the buffer updates kept in the graph
+  // training BatchNorm updating the running statistics in place, then + residual and the activation (act 1 ReLU,
+  // 2 hardswish): the compile backend's form of BatchNorm -> [add] -> [activation] with the buffer updates kept in the
+  // graph. Returns (y, save_mean, save_invstd, z) with z the hardswish's input (act 2; undefined otherwise)
   m.def("bn_train_(Tensor x, Tensor w, Tensor b, Tensor(a!) rm, Tensor(b!) rv, float momentum, float eps, int act, "
-        "Tensor? residual) -> (Tensor, Tensor, Tensor)");
+        "Tensor? residual) -> (Tensor, Tensor, Tensor, Tensor)");
+  // BatchNorm backward through the activation: r is the ReLU's output (act 1) or the hardswish's input (act 2)
+  m.def("bn_act_backward(Tensor g, Tensor x, Tensor r, Tensor w, Tensor mean, Tensor invstd, int act, bool[3] mask) "
+        "-> (Tensor, Tensor, Tensor)");
   m.def("conv_bn_act_eval(Tensor x, Tensor cw, Tensor? cb, Tensor w, Tensor b, Tensor rm, Tensor rv, float eps, "
         "int[] stride, int[] padding, int act) -> Tensor");
-  // convolution (no bias) -> bn_train_: (y, save_mean, save_invstd, convolution output)
+  // convolution (no bias) -> bn_train_: (y, save_mean, save_invstd, z, convolution output)
   m.def("conv_bn_train_(Tensor x, Tensor cw, int[] stride, int[] padding, Tensor w, Tensor b, Tensor(a!) rm, "
-        "Tensor(b!) rv, float momentum, float eps, int act, Tensor? residual) -> (Tensor, Tensor, Tensor, Tensor)");
+        "Tensor(b!) rv, float momentum, float eps, int act, Tensor? residual) -> (Tensor, Tensor, Tensor, Tensor, "
+        "Tensor)");
 }
 TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("bn_relu_train", &bn_relu_train_ref);
   m.impl("bn_train_", &bn_train_inplace_ref);
   m.impl("bn_relu_backward", &bn_relu_backward_ref);
+  m.impl("bn_act_backward", &bn_act_backward_ref);
   m.impl("bn_relu_res_backward", &bn_relu_res_backward_ref);
   m.impl("conv_act", &conv_act_ref);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
@@ -667,6 +718,7 @@ TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_train", &bn_relu_train_k);
   m.impl("bn_train_", &bn_train_inplace_k);
   m.impl("bn_relu_backward", &bn_relu_backward_k);
+  m.impl("bn_act_backward", &bn_act_backward_k);
   m.impl("bn_relu_res_backward", &bn_relu_res_backward_k);
   m.impl("conv_act", &conv_act_k);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);

@@ -74,6 +74,23 @@ class StaticTensors {
 
 void bind_replay(pybind11::module_& m) {
   namespace py = pybind11;
+  // per tensor, the base address of its storage (0 for an undefined tensor)
+  m.def("storage_ptrs", [](const std::vector<Tensor>& ts) {
+    std::vector<int64_t> out;
+    out.reserve(ts.size());
+    for (const Tensor& t : ts) out.push_back(t.defined() ? (int64_t)(intptr_t)t.storage().data() : 0);
+    return out;
+  });
+  // the indices i with expected[i] != 0 whose tensor's storage no longer starts at expected[i]: a replay's check
+  // that the inputs it reads in place are where the capture found them
+  m.def("moved_inputs", [](const std::vector<Tensor>& ts, const std::vector<int64_t>& expected) {
+    TORCH_CHECK(ts.size() == expected.size(), "moved_inputs: ", ts.size(), " tensors, ", expected.size(), " addresses");
+    std::vector<int64_t> out;
+    for (size_t i = 0; i < ts.size(); ++i)
+      if (expected[i] != 0 && (!ts[i].defined() || (int64_t)(intptr_t)ts[i].storage().data() != expected[i]))
+        out.push_back((int64_t)i);
+    return out;
+  });
   py::class_<StaticTensors>(m, "StaticTensors")
       .def(py::init<const std::vector<Tensor>&>())
       .def("aliases", &StaticTensors::aliases)

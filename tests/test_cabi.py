@@ -114,6 +114,42 @@ def test_host_validation_statuses():
         _lib.check(_lib.OMT_UNSUPPORTED)
 
 
+def test_unsummed_backward_validation_host_side():
+    """omt_conv_bwd_parts / omt_bn_bwd_parts / omt_slice_sums reject bad arguments on the host, before any launch."""
+    from omarchy_mac_torch import _lib
+    L = _lib.L
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    parts, slices, job = ctypes.c_void_p(), ctypes.c_int32(), _lib.SliceSum()
+    g = _lib.conv_geo(2, 8, 8, 8, 8, 3, 1, 1)
+    out = (ctypes.byref(parts), ctypes.byref(slices), ctypes.byref(job))
+    assert L.omt_conv_bwd_parts(ctypes.byref(g), fake, fake, fake, fake, None, None, 0, 4, *out, None) == \
+        _lib.OMT_INVALID  # no grad weight
+    assert L.omt_conv_bwd_parts(ctypes.byref(g), fake, fake, fake, fake, fake, None, 0, 4, None, ctypes.byref(slices),
+                                ctypes.byref(job), None) == _lib.OMT_INVALID
+    g.oh = 99
+    assert L.omt_conv_bwd_parts(ctypes.byref(g), fake, fake, fake, fake, fake, None, 0, 4, *out, None) == \
+        _lib.OMT_UNSUPPORTED
+    bad = (_lib.SliceSum * 1)(_lib.SliceSum(None, fake, 16, 2))
+    assert L.omt_slice_sums(bad, 1, None) == _lib.OMT_INVALID
+    assert L.omt_slice_sums(None, 1, None) == _lib.OMT_INVALID
+    assert L.omt_slice_sums(None, 0, None) == _lib.OMT_OK
+    none = (_lib.SliceSum * 1)(_lib.SliceSum(None, None, 0, 0))
+    assert L.omt_slice_sums(none, 1, None) == _lib.OMT_OK  # nothing to sum: no launch
+
+    def bn(n=2, c=4, hw=16, slices=2, g2=None, act=_lib.OMT_ACT_RELU, act_in=fake, gz=None, sums=None, count=0):
+        return L.omt_bn_bwd_parts(n, c, hw, fake, slices, g2, fake, act, act_in, fake, fake, fake, fake, fake, fake,
+                                  gz, sums, count, None)
+    assert bn(slices=0) == _lib.OMT_INVALID
+    assert bn(slices=65) == _lib.OMT_INVALID
+    assert bn(act=3) == _lib.OMT_INVALID
+    assert bn(act_in=None) == _lib.OMT_INVALID      # ReLU without its output
+    assert bn(g2=fake) == _lib.OMT_INVALID          # a second gradient only with gz
+    assert bn(count=1) == _lib.OMT_INVALID          # no sums array
+    assert bn(count=3, sums=bad) == _lib.OMT_INVALID  # at most two
+    assert bn(count=1, sums=bad) == _lib.OMT_INVALID  # a sum without its partials
+    assert bn(n=2, hw=4097) == _lib.OMT_UNSUPPORTED  # channels of more than 8192 elements
+
+
 def test_batch_chunks_host_side():
     """A batch past 2 GiB (3 images of 876 MB in and out) is planned as batch chunks of 2 images, then 1: plan calls
     on it act on the first chunk's geometry, its workspaces are the larger chunk's (grad weight: plus the chunks'
@@ -195,8 +231,8 @@ def test_epilogue_statistics_validation_host_side():
         L.omt_conv_clear_plans()
     ws = L.omt_bn_train_workspace(2, 24, 100)
     stats_bytes = 24 * 3 * 2 * 8  # 24 channels x 3 column groups x (sum, sum of squares)
-    args = [2, 24, 100, fake, fake, 3, stats_bytes, fake, fake, None, None, 0.1, 1e-5, 1, None, fake, fake, fake, None,
-            None, fake, ws, None]
+    args = [2, 24, 100, fake, fake, 3, stats_bytes, fake, fake, None, None, 0.1, 1e-5, 1, None, fake, None, fake, fake,
+            None, None, fake, ws, None]
     bad_groups = list(args)
     bad_groups[5] = 0
     assert L.omt_bn_train_fwd_stats(*bad_groups) == _lib.OMT_INVALID
@@ -204,7 +240,7 @@ def test_epilogue_statistics_validation_host_side():
     no_stats[4] = None
     assert L.omt_bn_train_fwd_stats(*no_stats) == _lib.OMT_INVALID
     small_ws = list(args)
-    small_ws[21] = ws - 8
+    small_ws[22] = ws - 8
     assert L.omt_bn_train_fwd_stats(*small_ws) == _lib.OMT_INVALID
     small_stats = list(args)  # a stats buffer sized for fewer groups than claimed
     small_stats[6] = stats_bytes - 8
@@ -213,6 +249,9 @@ def test_epilogue_statistics_validation_host_side():
     more_groups = list(args)
     more_groups[5] = 4
     assert L.omt_bn_train_fwd_stats(*more_groups) == _lib.OMT_INVALID
+    bad_act = list(args)  # activations are 0 (none), 1 (ReLU) and 2 (hardswish)
+    bad_act[13] = 3
+    assert L.omt_bn_train_fwd_stats(*bad_act) == _lib.OMT_INVALID and b"activation" in L.omt_last_error()
 
 
 def test_plan_cache_host_side():
@@ -313,7 +352,8 @@ def test_ctypes_structs_match_the_header(tmp_path):
     if shutil.which("g++") is None:
         pytest.skip("needs g++")
     structs = {"omt_conv_geo": _lib.ConvGeo, "omt_conv_plan": _lib.ConvPlan, "omt_adam_tensor": _lib.AdamTensor,
-               "omt_adam_params": _lib.AdamParams, "omt_sgd_tensor": _lib.SgdTensor, "omt_sgd_params": _lib.SgdParams}
+               "omt_adam_params": _lib.AdamParams, "omt_sgd_tensor": _lib.SgdTensor, "omt_sgd_params": _lib.SgdParams,
+               "omt_slice_sum": _lib.SliceSum}
     lines = ["#include <cstddef>", "#include <cstdio>", '#include "omt_hip.h"', "int main() {"]
     for cname, py in structs.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')

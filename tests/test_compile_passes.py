@@ -47,6 +47,8 @@ def _block_tail_graph(oc, tail, save_stats=False):
     y = gi[0]
     if tail == "relu":
         y = g.call_function(aten.relu.default, (gi[0],))
+    elif tail == "hardswish":
+        y = g.call_function(aten.hardswish.default, (gi[0],))
     elif tail == "add_relu":
         s = g.call_function(aten.add.Tensor, (gi[0], r))
         s.meta["val"] = _fake(mode, dev, shp)
@@ -58,7 +60,8 @@ def _block_tail_graph(oc, tail, save_stats=False):
     g.call_function(aten.copy_.default, (rv, gi[4]))
     g.call_function(aten.copy_.default, (t1, a1))
     g.call_function(aten.copy_.default, (t2, a2))
-    g.output((y, gi[1], gi[2]) + ((gi[3], gi[4]) if save_stats else ()))
+    # hardswish: its input is saved for its backward, a graph output too
+    g.output((y, gi[1], gi[2]) + ((gi[3], gi[4]) if save_stats else ()) + ((gi[0],) if tail == "hardswish" else ()))
     return GraphModule(torch.nn.Module(), g)
 
 
@@ -75,12 +78,13 @@ def _targets(gm):
 
 
 @pytest.mark.parametrize("save_stats", [False, True])
-@pytest.mark.parametrize("tail", ["relu", "add_relu", "none"])
+@pytest.mark.parametrize("tail", ["relu", "add_relu", "none", "hardswish"])
 def test_bn_train_in_place_and_counters(oc, tail, save_stats):
     gm = _block_tail_graph(oc, tail, save_stats)
     ref = copy.deepcopy(gm)
     stats = oc.fuse_bn_train_in_place(gm.graph)
     assert stats["bn"] == 1 and stats["add_relu"] == (tail == "add_relu") and stats["relu"] == (tail == "relu")
+    assert stats["hardswish"] == (tail == "hardswish")
     assert oc.merge_batch_counters(gm.graph) == 2
     gm.graph.eliminate_dead_code()
     gm.graph.lint()
@@ -88,9 +92,10 @@ def test_bn_train_in_place_and_counters(oc, tail, save_stats):
     t = _targets(gm)
     assert t.count(torch.ops.omt.bn_train_.default) == 1 and t.count(aten._foreach_add_.Scalar) == 1
     assert aten.copy_.default not in t and aten._native_batch_norm_legit_functional.default not in t
-    assert aten.relu.default not in t and aten.add.Tensor not in t
+    assert aten.relu.default not in t and aten.add.Tensor not in t and aten.hardswish.default not in t
     fused = next(n for n in gm.graph.nodes if n.target is torch.ops.omt.bn_train_.default)
-    assert fused.args[7] == (0 if tail == "none" else 1) and (fused.args[8] is not None) == (tail == "add_relu")
+    assert fused.args[7] == {"none": 0, "relu": 1, "add_relu": 1, "hardswish": 2}[tail]
+    assert (fused.args[8] is not None) == (tail == "add_relu")
     # same results and buffer updates as the original graph, on CPU tensors
     a, b = _inputs(1), _inputs(1)
     out_ref, out_new = ref(*a), gm(*b)
@@ -112,6 +117,45 @@ def test_bn_in_place_needs_sole_copies(oc):
     assert oc.fuse_bn_train_in_place(gm.graph)["bn"] == 0
     # the ReLU still fuses through the functional rewrite
     assert oc.fuse_bn_relu_train(gm.graph) == 1
+
+
+def test_bn_hardswish_backward(oc):
+    """native_batch_norm_backward(hardswish_backward(g, z), x, ...) becomes one omt.bn_act_backward (act 2) that takes
+    the hardswish gradient itself; the rewritten graph gives the original's gradients on CPU tensors, with z at the
+    hardswish's break points -3 and 3 and between them."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    shp, c = (2, 4, 3, 3), 4
+
+    def ph(name, shape):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape)
+        return n
+
+    gy, z, x, w, mean, invstd = ph("g", shp), ph("z", shp), ph("x", shp), ph("w", (c,)), ph("mean", (c,)), \
+        ph("invstd", (c,))
+    hb = g.call_function(aten.hardswish_backward.default, (gy, z))
+    hb.meta["val"] = _fake(mode, dev, shp)
+    bn = g.call_function(aten.native_batch_norm_backward.default,
+                         (hb, x, w, None, None, mean, invstd, True, 1e-5, [True, True, True]))
+    g.output(tuple(g.call_function(operator.getitem, (bn, i)) for i in range(3)))
+    gm = GraphModule(torch.nn.Module(), g)
+    ref = copy.deepcopy(gm)
+    assert oc.fuse_bn_hardswish_backward(gm.graph) == 1
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    assert torch.ops.omt.bn_act_backward.default in t and aten.hardswish_backward.default not in t
+    assert aten.native_batch_norm_backward.default not in t
+    gen = torch.Generator().manual_seed(4)
+    zv = torch.randn(shp, generator=gen) * 3
+    zv.view(-1)[:4] = torch.tensor([-3.0, 3.0, 0.0, -1.5])
+    args = [torch.randn(shp, generator=gen), zv, torch.randn(shp, generator=gen), torch.rand(c, generator=gen) + 0.5,
+            torch.randn(c, generator=gen), torch.rand(c, generator=gen) + 0.5]
+    for o_ref, o_new in zip(ref(*args), gm(*args)):
+        torch.testing.assert_close(o_new, o_ref, rtol=1e-6, atol=1e-7)
 
 
 def _block_end_backward_graph(oc, with_add, second_user):
@@ -217,7 +261,7 @@ def _conv_bn_graph(oc, bias, early_user, res):
 
 @pytest.mark.parametrize("case", ["plain", "residual", "bias", "early_user"])
 def test_conv_bn_train(oc, case):
-    """A bias-free dense convolution feeding omt.bn_train_ becomes one omt.conv_bn_train_ whose fourth output replaces
+    """A bias-free dense convolution feeding omt.bn_train_ becomes one omt.conv_bn_train_ whose fifth output replaces
     the convolution's other uses; with a bias, or a use of the convolution before the BatchNorm, the graph stays as it
     is. The rewritten graph gives the original's outputs and running statistics on CPU tensors."""
     gm = _conv_bn_graph(oc, case == "bias", case == "early_user", case == "residual")

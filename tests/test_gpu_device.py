@@ -739,7 +739,7 @@ def test_conv_bn_train_matches_conv_then_bn(clean, shape):
     BatchNorm), 7x7 planes (scalar loads), 2x2 planes, with a residual and ReLU; and against the oracle. Outputs of
     64 MB or more with channels past 8192 elements, under an unsplit plan, take their statistics from the
     convolution's epilogue (summed in another order): there the convolution output is bit-identical and the rest
-    agrees to 1e-5."""
+    agrees to 1e-5. With hardswish (act 2) both also return the hardswish's input z."""
     omt = clean
     from omarchy_mac_torch import hip_ops
     n, ci, co, h, w, ks, st, pd = shape
@@ -755,18 +755,20 @@ def test_conv_bn_train_matches_conv_then_bn(clean, shape):
     try:
         for slices in (1, 2, 4, 16):
             hip_ops.set_conv_plan("fwd", x.shape, cw.shape, st, pd, 5, slices)
-            for act, res in ((1, None), (1, dr), (0, None)):
+            for act, res in ((1, None), (1, dr), (0, None), (2, None)):
                 rm1, rv1 = D(torch.from_numpy(rm.copy()), omt), D(torch.from_numpy(rv.copy()), omt)
                 rm2, rv2 = D(torch.from_numpy(rm.copy()), omt), D(torch.from_numpy(rv.copy()), omt)
-                y1, m1, i1, c1 = torch.ops.omt.conv_bn_train_(dx, dcw, [st, st], [pd, pd], dg, db, rm1, rv1, 0.1, 1e-5,
-                                                              act, res)
+                y1, m1, i1, z1, c1 = torch.ops.omt.conv_bn_train_(dx, dcw, [st, st], [pd, pd], dg, db, rm1, rv1, 0.1,
+                                                                  1e-5, act, res)
                 c2 = torch.ops.aten.convolution(dx, dcw, None, [st, st], [pd, pd], [1, 1], False, [0, 0], 1)
-                y2, m2, i2 = torch.ops.omt.bn_train_(c2, dg, db, rm2, rv2, 0.1, 1e-5, act, res)
+                y2, m2, i2, z2 = torch.ops.omt.bn_train_(c2, dg, db, rm2, rv2, 0.1, 1e-5, act, res)
                 case = (slices, act, res is not None)
                 from_stats = (n * oh * oh > 8192 and n * co * oh * oh * 4 >= 64 << 20 and
                               hip_ops.conv_plan("fwd", x.shape, cw.shape, st, pd)[1] == 1)
                 assert torch.equal(c1.cpu(), c2.cpu()), case
-                for a, bb in ((y1, y2), (m1, m2), (i1, i2), (rm1, rm2), (rv1, rv2)):
+                assert (z1 is None) == (z2 is None) == (act != 2), case  # the hardswish's input, act 2 only
+                pairs = ((y1, y2), (m1, m2), (i1, i2), (rm1, rm2), (rv1, rv2)) + (((z1, z2),) if act == 2 else ())
+                for a, bb in pairs:
                     if from_stats:
                         assert rel(a, bb) <= 1e-5, case
                     else:
@@ -775,6 +777,9 @@ def test_conv_bn_train_matches_conv_then_bn(clean, shape):
                 if res is None and act == 1:
                     y_ref = orc.bn_train(conv_ref, g, b, rm, rv, 0.1, 1e-5, True)[0]
                     assert rel(y1, y_ref) <= TOL, case
+                if act == 2:
+                    z_ref = orc.bn_train(conv_ref, g, b, rm, rv, 0.1, 1e-5)[0]
+                    assert rel(z1, z_ref) <= TOL and rel(y1, F.hardswish(torch.from_numpy(z_ref))) <= TOL, case
     finally:
         hip_ops.clear_conv_plans()
     assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())

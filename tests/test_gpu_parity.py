@@ -777,6 +777,38 @@ def test_batch_norm_backward_res(cuda, ops, n, c, h, w, with_g2):
             assert gx is None
 
 
+@pytest.mark.parametrize("n,c,h,w", [(32, 16, 16, 16), (8, 24, 56, 56), (64, 8, 20, 20), (3, 5, 37, 41),
+                                     (32, 96, 7, 7)])
+def test_batch_norm_hardswish(cuda, ops, n, c, h, w):
+    """BatchNorm with hardswish fused into its apply (MobileNetV3's BatchNorms): z = the BatchNorm output against the
+    oracle, y = hardswish(z) as PyTorch CPU computes it from z, and the backward through the hardswish (gradient from z,
+    0 at and below -3, unchanged at and above 3) against PyTorch CPU's hardswish_backward followed by the oracle's
+    BatchNorm backward; on the one-launch, two-pass and flat-apply paths, the same via ReLU as act 1."""
+    from omarchy_mac_torch import _lib
+    rng = np.random.default_rng(n + 7 * c + h)
+    x = rnd(rng, n, c, h, w) * 2 + 1
+    gam, bet, rm, rv = rnd(rng, c) * 2, rnd(rng, c), rnd(rng, c), np.abs(rnd(rng, c)) + 0.5
+    tx, tg = dev(x, cuda), dev(gam, cuda)
+    z_ref = orc.bn_train(x, gam, bet, rm, rv, 0.1, 1e-5)[0]
+    gy = rnd(rng, n, c, h, w)
+    for act in (_lib.OMT_ACT_HARDSWISH, _lib.OMT_ACT_RELU):
+        y, sm, si, z = ops.batch_norm_train(tx, tg, dev(bet, cuda), dev(rm, cuda), dev(rv, cuda), 0.1, 1e-5, act=act,
+                                            return_z=True)
+        assert orc.rel_l2(host(z), z_ref) <= TOL
+        tz = torch.from_numpy(host(z))
+        y_ref = torch.nn.functional.hardswish(tz) if act == _lib.OMT_ACT_HARDSWISH else torch.relu(tz)
+        yd = torch.from_numpy(host(y))
+        assert torch.equal(yd, y_ref) or orc.rel_l2(yd.numpy(), y_ref.numpy()) <= 1e-6, act
+        gx, dg, db = ops.batch_norm_backward_act(dev(gy, cuda), tx, act, z if act == _lib.OMT_ACT_HARDSWISH else y,
+                                                 sm, si, tg)
+        gz = (torch.ops.aten.hardswish_backward(torch.from_numpy(gy), tz) if act == _lib.OMT_ACT_HARDSWISH
+              else torch.ops.aten.threshold_backward(torch.from_numpy(gy), y_ref, 0)).numpy()
+        gx_ref, dg_ref, db_ref = orc.bn_bwd(gz, x, host(sm), host(si), gam)
+        assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
+        scale = np.linalg.norm(gz.astype(np.float64)) * np.abs(gam * host(si)).max()
+        assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
+
+
 def test_batch_norm_functional_and_eval(cuda, ops):
     rng = np.random.default_rng(11)
     x, g, b, rm, rv = rnd(rng, 8, 5, 6, 6), rnd(rng, 5), rnd(rng, 5), rnd(rng, 5), np.abs(rnd(rng, 5)) + 0.2
