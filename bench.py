@@ -265,9 +265,9 @@ RESNET_FAMILIES = [
 def resnet_trace_summary(trace_csv, replays=22):
     """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` and prints, for
     the compiled graphed replays (the last run of `replays` identical steps), the eager-model graphed replays (the
-    run before it) and the compiled model with the backend's own graph replay (the run before that), kernel time per
-    step by family as markdown. Replays of one graph launch the same dispatch
-    sequence, so a run is the latest stretch of the trace that repeats with some period D `replays` times; any D
+    run before it) and the compiled model with the backend's own graph replay (the run before that: its 20 timed
+    steps), kernel time per step by family as markdown. Replays of one graph launch the same dispatch sequence, so a
+    run is the latest stretch of the trace that repeats with some period D `replays` times (20 for the third); any D
     consecutive dispatches of it are one step's launches."""
     import csv
 
@@ -275,7 +275,7 @@ def resnet_trace_summary(trace_csv, replays=22):
                   for r in csv.DictReader(open(trace_csv)))
     names = [r[2] for r in rows]
 
-    def periodic_run(end_max, end_min):
+    def periodic_run(end_max, end_min, replays):
         for end in range(end_max, end_min, -1):
             for d in range(50, 1000):
                 st = end - replays * d
@@ -289,17 +289,17 @@ def resnet_trace_summary(trace_csv, replays=22):
 
     runs = []
     hi = len(names)
-    for _ in range(3):
-        found = periodic_run(hi, max(0, hi - 20000))
+    for reps in (replays, replays, 20):
+        found = periodic_run(hi, max(0, hi - 20000), reps)
         if not found:
             break
         st, d = found
-        runs.append(rows[st:st + replays * d])
+        runs.append((reps, rows[st:st + reps * d]))
         hi = st
     titles = ("compiled model, whole step captured by the caller (graphs.Graph) and replayed",
               "eager model, whole step captured by the caller and replayed",
               "compiled model alone: the backend replays its forward and backward graphs, the rest runs eagerly")
-    for title, run in zip(titles, runs):
+    for title, (replays, run) in zip(titles, runs):
         d = len(run) // replays
         per, cnt = {}, {}
         for (t0, t1, name) in run:

@@ -712,7 +712,21 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       }
     }
   }
-  if (PARTS) {  // slice by slice, each slice's loads of all NR vectors in flight together; then g2
+  if (PARTS && sp.nv <= 256) {  // one vector per thread: kReduceBatch slices' loads in flight, added in slice order
+    const int vv = (int)threadIdx.x;
+    if (vv < sp.nv) {
+      const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+      for (int z0 = 1; z0 < slices; z0 += kReduceBatch) {
+        V t[kReduceBatch];
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u)
+          if (z0 + u < slices) t[u] = *reinterpret_cast<const V*>(g + (z0 + u) * pstride + off);
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u)
+          if (z0 + u < slices) vadd(rg[0], t[u]);
+      }
+    }
+  } else if (PARTS) {  // slice by slice, each slice's loads of all NR vectors in flight together
     for (int z = 1; z < slices; ++z) {
       V t[NR];
 #pragma unroll
@@ -724,6 +738,8 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       for (int u = 0; u < NR; ++u)
         if ((int)threadIdx.x + u * 256 < sp.nv) vadd(rg[u], t[u]);
     }
+  }
+  if (PARTS) {  // then g2
     if (RES && g2) {
 #pragma unroll
       for (int u = 0; u < NR; ++u) {

@@ -19,7 +19,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
   3. a dense convolution whose only user is a ReLU -> omt.conv_act (ReLU in the GEMM epilogue), or an eval BatchNorm
      (`_native_batch_norm_legit_no_training`, optionally followed by ReLU) -> omt.conv_bn_act_eval (BatchNorm folded
      into the conv's weights and bias); a bias-free dense convolution feeding omt.bn_train_ -> omt.conv_bn_train_,
-     where the BatchNorm sums a K-split convolution's partials itself (no slice-sum launch).
+     where the BatchNorm sums a K-split convolution's partials itself (no slice-sum launch); a BatchNorm backward
+     (2, or a plain training one) whose incoming gradient is a dense convolution's grad input -> omt.conv_bn_backward,
+     where the BatchNorm backward sums the convolution's grad-input partials and runs its grad-weight slice sum.
 
 Each omt op falls back to its plain aten composition when the device kernels do not cover the case, so a rewritten
 graph is always correct. The rewritten graphs then run as HIP graphs: a few calls op by op, then captured once and
@@ -382,12 +384,91 @@ def fuse_conv_bn_train(graph):
     return count
 
 
+def _dgrad_of(gi, before, order):
+    """The convolution_backward node when gi is its grad input and the fused op can take it over: a dense convolution,
+    both grads asked for and no bias grad, gi used once, and every use of its grad weight after node `before`."""
+    if not (isinstance(gi, Node) and gi.op == "call_function" and gi.target is operator.getitem and gi.args[1] == 0
+            and len(gi.users) == 1):
+        return None
+    cb = gi.args[0]
+    if not (isinstance(cb, Node) and cb.op == "call_function" and cb.target is aten.convolution_backward.default):
+        return None
+    gy, cx, cw, _, stride, padding, dilation, transposed, _, groups, mask = cb.args[:11]
+    outs = _getitem_users(cb)
+    wv = _meta(cw)
+    if not (mask[0] and mask[1] and not mask[2]) or set(outs) - {0, 1}:
+        return None
+    if (transposed or groups != 1 or list(dilation) != [1, 1] or wv is None or wv.dim() != 4
+            or wv.shape[2] != wv.shape[3] or len(set(stride)) != 1 or len(set(padding)) != 1
+            or not _on_device_f32(cx, 4) or not _on_device_f32(gy, 4)):
+        return None
+    if 1 in outs and any(order[u] < order[before] for u in outs[1].users):
+        return None
+    return cb
+
+
+def fuse_conv_bn_backward(graph):
+    """A BatchNorm backward (omt.bn_relu_backward, bn_act_backward, bn_relu_res_backward, or a training
+    native_batch_norm_backward) whose incoming gradient is a dense convolution's grad input -> one
+    omt.conv_bn_backward: the BatchNorm backward sums the convolution's K-split grad-input partials as it reads them and
+    runs the grad weight's slice sum on workgroups of its own launch (the convolution's slice-sum launch goes). Its
+    outputs: the convolution's grad weight, then the BatchNorm backward's. At a residual block's end either of the two
+    gradients may be the convolution's (the other goes in as `other`)."""
+    count = 0
+    for bn in list(graph.nodes):
+        if bn.op != "call_function":
+            continue
+        if bn.target is omt.bn_relu_backward.default:
+            g, x, r, w, mean, invstd, mask = bn.args
+            cands, act, res = [(g, None)], 1, False
+        elif bn.target is omt.bn_act_backward.default:
+            g, x, r, w, mean, invstd, act, mask = bn.args
+            cands, res = [(g, None)], False
+        elif bn.target is omt.bn_relu_res_backward.default:
+            g, g2, x, r, w, mean, invstd, mask = bn.args
+            cands, act, res = [(g, g2), (g2, g)], 1, True
+        elif bn.target is aten.native_batch_norm_backward.default:
+            g, x, w, _, _, mean, invstd, train, _, mask = bn.args[:10]
+            if not train or w is None or not _on_device_f32(x, 4):
+                continue
+            cands, act, res, r = [(g, None)], 0, False, x
+        else:
+            continue
+        order = {v: i for i, v in enumerate(graph.nodes)}
+        cb = other = None
+        for gi, o in cands:
+            cb = _dgrad_of(gi, bn, order)
+            if cb is not None:
+                other = o
+                break
+        if cb is None:
+            continue
+        gy, cx, cw, _, stride, padding = cb.args[:6]
+        fused = _call_before(graph, bn, omt.conv_bn_backward.default,
+                             (gy, cx, cw, list(stride), list(padding), other, x, r, w, mean, invstd, act, res,
+                              list(mask)))
+        outs = _getitem_users(cb)
+        if 1 in outs:
+            gw = _call_before(graph, bn, operator.getitem, (fused, 0), meta_from=outs[1])
+            outs[1].replace_all_uses_with(gw)
+            graph.erase_node(outs[1])
+        for i, gi in _getitem_users(bn).items():
+            new = _call_before(graph, gi, operator.getitem, (fused, i + 1), meta_from=gi)
+            gi.replace_all_uses_with(new)
+            graph.erase_node(gi)
+        graph.erase_node(bn)
+        graph.erase_node(outs[0])
+        graph.erase_node(cb)
+        count += 1
+    return count
+
+
 def _rewrite(gm):
     g = gm.graph
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
              "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
              "bn_relu_backward": fuse_bn_relu_backward(g), "bn_hardswish_backward": fuse_bn_hardswish_backward(g),
-             "conv_bn_train": fuse_conv_bn_train(g),
+             "conv_bn_train": fuse_conv_bn_train(g), "conv_bn_backward": fuse_conv_bn_backward(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()

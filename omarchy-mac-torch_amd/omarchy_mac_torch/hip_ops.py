@@ -125,6 +125,44 @@ def conv2d_bwd(x, gy, w, stride=1, padding=0):
     return gx, gw
 
 
+def conv2d_bwd_bn(cx, gy, cw, stride, padding, x, save_mean, save_invstd, gamma, act=_lib.OMT_ACT_NONE, act_in=None,
+                  g2=None, res=False, output_mask=(True, True, True), max_gx_slices=4, side_sum=True):
+    """A convolution backward (input cx, filter cw) whose grad input is the incoming gradient of a BatchNorm backward
+    (input x), as one pair of launches: omt_conv_bwd_parts leaves grad input's K-split partials (up to max_gx_slices
+    slices) unsummed, and omt_bn_bwd_parts sums them as it reads them, adds g2 (res only), takes the activation's
+    gradient and runs the grad weight's slice sum on extra workgroups (side_sum; else omt_slice_sums runs it first).
+    res: the backward of omt_bn_bwd_res (act ReLU), which also returns gz. Returns (convolution grad weight, gx,
+    dgamma, dbeta, gz or None, the number of grad-input slices the BatchNorm summed)."""
+    cx, gy, cw = _need(cx, "cx", 4), _need(gy, "gy", 4), _need(cw, "cw", 4)
+    x, act_in, g2 = _need(x, "x", 4), _need(act_in, "act_in", 4), _need(g2, "g2", 4)
+    g = conv_geo_for(cx.shape, cw.shape, stride, padding)
+    if tuple(gy.shape) != (g.n, g.co, g.oh, g.ow) or x.shape != cx.shape:
+        raise ValueError(f"conv2d_bwd_bn: gy {tuple(gy.shape)} or x {tuple(x.shape)} does not fit the convolution")
+    n, c, h, w = x.shape
+    dev = x.device
+    cgx, cgw = torch.empty_like(cx), torch.empty(tuple(cw.shape), device=dev, dtype=torch.float32)
+    ws, nb = _workspace(L.omt_conv_bwd_workspace(ctypes.byref(g)), dev)
+    parts, slices, job = _vp(), ctypes.c_int32(), _lib.SliceSum()
+    s = _stream(dev)
+    check(L.omt_conv_bwd_parts(ctypes.byref(g), _ptr(cx), _ptr(gy), _ptr(cw), _ptr(cgx), _ptr(cgw), _ptr(ws), nb,
+                               int(max_gx_slices), ctypes.byref(parts), ctypes.byref(slices), ctypes.byref(job), s),
+          "conv2d_bwd_bn (convolution)")
+    count = 1 if job.slices > 0 else 0
+    if count and not side_sum:
+        check(L.omt_slice_sums(ctypes.byref(job), 1, s), "conv2d_bwd_bn (slice sum)")
+        count = 0
+    gx = torch.empty_like(x) if output_mask[0] else None
+    dg = torch.empty((c,), device=dev, dtype=torch.float32) if output_mask[1] else None
+    db = torch.empty((c,), device=dev, dtype=torch.float32) if output_mask[2] else None
+    gz = torch.empty_like(x) if res else None
+    src = parts if parts.value else _ptr(cgx)
+    check(L.omt_bn_bwd_parts(n, c, h * w, src, slices.value, _ptr(g2), _ptr(x), int(act), _ptr(act_in),
+                             _ptr(_need(save_mean, "mean", 1)), _ptr(_need(save_invstd, "invstd", 1)),
+                             _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg), _ptr(db), _ptr(gz),
+                             ctypes.byref(job), count, s), "conv2d_bwd_bn (BatchNorm)")
+    return cgw, gx, dg, db, gz, slices.value
+
+
 # ---- channels-last (NHWC) dense convolution: tensors of the usual NCHW shapes in torch.channels_last memory order
 # (filters [co][ky][kx][ci] in memory); outputs come back channels_last -----------------------------------------
 

@@ -17,6 +17,9 @@ pool of idle plans per (shape, training, input-grad). A training forward leases 
 its autograd graph lives: the lease returns the plan after backward, or when the graph is freed without one, so a
 stack applied twice before backward runs two plans and none is lost. Reassigning a parameter or buffer (a new
 tensor, or new `.data`) drops the program's plans, which hold the tensors they were built with.
+
+From its second run on, a plan replays each of its step lists (forward, backward) as one captured HIP graph (the
+input copied into the plan's input buffer first); OMARCHY_MAC_TORCH_PLAN_GRAPHS=0 keeps them step by step.
 """
 
 import os

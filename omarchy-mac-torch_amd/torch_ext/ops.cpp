@@ -413,6 +413,23 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_ref(const
   auto r = at::native_batch_norm_backward(gz, x, w, std::nullopt, std::nullopt, mean, invstd, true, 0.0, mask);
   return {std::get<0>(r), std::get<1>(r), std::get<2>(r), gz};
 }
+// A convolution backward whose grad input g is a BatchNorm backward's incoming gradient (BatchNorm -> activation ->
+// convolution in the forward): the convolution's grad weight, then omt::bn_relu_res_backward(g, other, x, r, ...)
+// (res) or omt::bn_act_backward(g, x, r, ..., act), as (grad weight, gx, dgamma, dbeta, gz; gz undefined unless res)
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_backward_ref(
+    const Tensor& gy, const Tensor& cx, const Tensor& cw, IntArrayRef stride, IntArrayRef padding,
+    const std::optional<Tensor>& other, const Tensor& x, const Tensor& r, const Tensor& w, const Tensor& mean,
+    const Tensor& invstd, int64_t act, bool res, std::array<bool, 3> mask) {
+  auto cb = at::convolution_backward(gy, cx, cw, std::nullopt, stride, padding, {1, 1}, false, {0, 0}, 1,
+                                     {true, true, false});
+  if (res) {
+    auto b = bn_relu_res_backward_ref(std::get<0>(cb), other, x, r, w, mean, invstd, mask);
+    return {std::get<1>(cb), std::get<0>(b), std::get<1>(b), std::get<2>(b), std::get<3>(b)};
+  }
+  TORCH_CHECK(!defined(other), "omt::conv_bn_backward: a second gradient needs res");
+  auto b = bn_act_backward_ref(std::get<0>(cb), x, r, w, mean, invstd, act, mask);
+  return {std::get<1>(cb), std::get<0>(b), std::get<1>(b), std::get<2>(b), Tensor()};
+}
 static Tensor conv_act_ref(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
                            IntArrayRef padding, int64_t act) {
   Tensor y = at::convolution(x, w, b, stride, padding, {1, 1}, false, {0, 0}, 1);
@@ -605,6 +622,72 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_dev(const
         "omt::bn_relu_res_backward");
   return {gx, dg, db, gz};
 }
+// The convolution leaves its grad input unsummed (up to kFoldBwdSlices slices, kFoldBwdSlicesSmall for channels of
+// at most 1024 elements, which the BatchNorm reads one vector per thread with eight slices' loads in flight) and the
+// one-launch BatchNorm backward sums the partials as it reads them, in the convolution's slice order, and runs the
+// grad weight's slice sum on extra workgroups: one launch (the convolution's slice sums) fewer, results equal to the
+// two ops run apart. Channels of more than kBnOneLaunchMax elements run the two as they are. (Graph replays of
+// ResNet-18 at 64x64: a 2x2-plane layer's BatchNorm reading 32 slices took 16.7 us against 4.7 + 7.4 us for the slice
+// sum and the BatchNorm apart; with 2-4 slices the BatchNorm took 2-4 us longer and saved a 4.7 us launch.)
+constexpr int kFoldBwdSlices = 4, kFoldBwdSlicesSmall = 8;
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_backward_dev(
+    const Tensor& gy_, const Tensor& cx_, const Tensor& cw_, IntArrayRef stride, IntArrayRef padding,
+    const std::optional<Tensor>& other_, const Tensor& x_, const Tensor& r_, const Tensor& w, const Tensor& mean,
+    const Tensor& invstd, int64_t act, bool res, std::array<bool, 3> mask) {
+  cover(res ? act == OMT_ACT_RELU : (act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH),
+        "activation none, ReLU or hardswish (ReLU with a residual branch)");
+  cover(res || !defined(other_), "a second gradient only with a residual branch");
+  cover(stride.size() == 2 && padding.size() == 2 && stride[0] == stride[1] && padding[0] == padding[1],
+        "uniform 2-D stride and padding");
+  cover(kind_of(cx_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && !channels_last(cx_, cw_) &&
+            f32(gy_) && gy_.dim() == 4,
+        "dense NCHW convolution");
+  cover(f32(x_) && f32(r_) && x_.dim() == 4 && cx_.sizes() == x_.sizes() && r_.sizes() == x_.sizes() && whole(w) &&
+            whole(mean) && whole(invstd) && (!defined(other_) || (f32(*other_) && other_->sizes() == x_.sizes())),
+        "4-D float32 BatchNorm operands of the convolution input's shape");
+  Tensor gy = contig(gy_), cx = contig(cx_), cw = contig(cw_), x = contig(x_), r = contig(r_);
+  Tensor other = defined(other_) ? contig(*other_) : Tensor();
+  omt_conv_geo g = conv_geo(cx.size(0), cx.size(1), cw.size(0), cx.size(2), cx.size(3), cw.size(2), stride[0],
+                            padding[0]);
+  cover(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor cgx = empty_dev(cx.sizes()), cgw = empty_dev(cw.sizes());
+  Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
+  Tensor dg = mask[1] ? empty_dev({c}) : Tensor();
+  Tensor db = mask[2] ? empty_dev({c}) : Tensor();
+  Tensor gz = res ? empty_dev(x.sizes()) : Tensor();
+  const float* o = other.defined() ? fp(other) : nullptr;
+  void* s = cur_stream();
+  tune_conv_bwd(g);
+  Tensor ws = workspace(omt_conv_bwd_workspace(&g));
+  if (n * hw <= kBnOneLaunchMax) {
+    const float* parts = nullptr;
+    int slices = 1;
+    omt_slice_sum job{};
+    const int fold = n * hw <= 1024 ? kFoldBwdSlicesSmall : kFoldBwdSlices;
+    const int st = omt_conv_bwd_parts(&g, fp(cx), fp(gy), fp(cw), fpm(cgx), fpm(cgw), wsptr(ws), wsbytes(ws), fold,
+                                      &parts, &slices, &job, s);
+    if (st == OMT_OK) {
+      check(omt_bn_bwd_parts(n, c, hw, parts ? parts : fp(cgx), slices, o, fp(x), (int)act, fp(r), fp(mean),
+                             fp(invstd), fp(w), fpm(gx), fpm(dg), fpm(db), fpm(gz), &job, job.slices > 0 ? 1 : 0, s),
+            "omt::conv_bn_backward (BatchNorm over the partials)");
+      return {cgw, gx, dg, db, gz};
+    }
+    if (st != OMT_UNSUPPORTED) check(st, "omt::conv_bn_backward (convolution)");
+  }
+  check(omt_conv_bwd(&g, fp(cx), fp(gy), fp(cw), fpm(cgx), fpm(cgw), wsptr(ws), wsbytes(ws), s),
+        "omt::conv_bn_backward (convolution)");
+  Tensor bws = workspace(omt_bn_bwd_workspace(n, c, hw));
+  if (res)
+    check(omt_bn_bwd_res(n, c, hw, fp(cgx), o, fp(x), fp(r), fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg), fpm(db),
+                         fpm(gz), wsptr(bws), wsbytes(bws), s),
+          "omt::conv_bn_backward (BatchNorm)");
+  else
+    check(omt_bn_bwd_act(n, c, hw, fp(cgx), fp(x), (int)act, fp(r), fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg),
+                         fpm(db), wsptr(bws), wsbytes(bws), s),
+          "omt::conv_bn_backward (BatchNorm)");
+  return {cgw, gx, dg, db, gz};
+}
 static Tensor conv_act_dev(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
                            IntArrayRef padding, int64_t act) {
   cover(stride.size() == 2 && padding.size() == 2, "2-D stride and padding");
@@ -669,6 +752,13 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_k(const T
   return dev_or_ref<&bn_relu_res_backward_dev, &bn_relu_res_backward_ref>("omt::bn_relu_res_backward", g, g2, x, y, w,
                                                                           mean, invstd, mask);
 }
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_backward_k(
+    const Tensor& gy, const Tensor& cx, const Tensor& cw, IntArrayRef s, IntArrayRef p,
+    const std::optional<Tensor>& other, const Tensor& x, const Tensor& r, const Tensor& w, const Tensor& mean,
+    const Tensor& invstd, int64_t act, bool res, std::array<bool, 3> mask) {
+  return dev_or_ref<&conv_bn_backward_dev, &conv_bn_backward_ref>("omt::conv_bn_backward", gy, cx, cw, s, p, other, x,
+                                                                  r, w, mean, invstd, act, res, mask);
+}
 static Tensor conv_act_k(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef s,
                          IntArrayRef p, int64_t act) {
   return dev_or_ref<&conv_act_dev, &conv_act_ref>("omt::conv_act", x, w, b, s, p, act);
@@ -703,6 +793,11 @@ TORCH_LIBRARY(omt, m) {
   m.def("conv_bn_train_(Tensor x, Tensor cw, int[] stride, int[] padding, Tensor w, Tensor b, Tensor(a!) rm, "
         "Tensor(b!) rv, float momentum, float eps, int act, Tensor? residual) -> (Tensor, Tensor, Tensor, Tensor, "
         "Tensor)");
+  // a convolution backward feeding its grad input to a BatchNorm backward (res: omt::bn_relu_res_backward with
+  // `other` its g2; else omt::bn_act_backward): (convolution grad weight, gx, dgamma, dbeta, gz)
+  m.def("conv_bn_backward(Tensor gy, Tensor cx, Tensor cw, int[] stride, int[] padding, Tensor? other, Tensor x, "
+        "Tensor r, Tensor w, Tensor mean, Tensor invstd, int act, bool res, bool[3] mask) -> (Tensor, Tensor, Tensor, "
+        "Tensor, Tensor)");
 }
 TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("bn_relu_train", &bn_relu_train_ref);
@@ -713,6 +808,7 @@ TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("conv_act", &conv_act_ref);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
   m.impl("conv_bn_train_", &conv_bn_train_ref);
+  m.impl("conv_bn_backward", &conv_bn_backward_ref);
 }
 TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_train", &bn_relu_train_k);
@@ -723,6 +819,7 @@ TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("conv_act", &conv_act_k);
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);
   m.impl("conv_bn_train_", &conv_bn_train_k);
+  m.impl("conv_bn_backward", &conv_bn_backward_k);
 }
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {

@@ -8,11 +8,22 @@
 // dw (depthwise 3/5/7), bn (BatchNorm2d with its ReLU fused), pool (2x2 max), apool (2x2 avg), gap (global avg).
 // Eval plans fold a BatchNorm+ReLU into the next conv's input loader: fold policy 0 never, 1 only 1x1 convs
 // (the default), 2 every conv and depthwise conv (csrc/plans.cpp:162-170).
+//
+// Graph replay: after kPlanWarmup runs step by step, each step list is captured once as a HIP graph and every later
+// run is one graph launch (the reference's plans replay their recorded dispatch list the same way,
+// csrc/plans.cpp:280-294). The graph reads and writes plan-owned buffers and the module's tensors, which stay put
+// (reassigning one drops the plans, stacks.py). The backward's parameter gradients then go to plan-owned buffers as
+// well: a run finds them still held by someone (a gradient kept from the last backward) runs step by step into new
+// tensors instead. Inside a capture of the caller's own the steps run one by one (into that capture).
+// OMARCHY_MAC_TORCH_PLAN_GRAPHS=0 keeps every plan step by step.
+#include <hip/hip_runtime_api.h>
 #include <pybind11/functional.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 #include <torch/extension.h>
 
+#include <cstdlib>
+#include <cstring>
 #include <functional>
 #include <memory>
 
@@ -21,6 +32,11 @@
 namespace omt {
 
 static int g_fold = 1;
+constexpr int kPlanWarmup = 1;  // step-by-step runs of a step list before it is captured
+static bool g_plan_graphs = [] {
+  const char* e = std::getenv("OMARCHY_MAC_TORCH_PLAN_GRAPHS");
+  return !(e && std::strcmp(e, "0") == 0);
+}();
 
 struct PlanLayer {
   std::string kind;
@@ -32,15 +48,86 @@ struct Run {
   std::vector<Tensor> grads;  // per parameter, filled by the backward steps
 };
 
+using Steps = std::vector<std::function<void(Run&, void*)>>;
+
+// One step list's graph: its step-by-step runs so far, and once captured, the executable graph.
+struct StepGraph {
+  int runs = 0;
+  bool off = false;  // a step could not be captured: step by step from now on
+  hipGraphExec_t exec = nullptr;
+};
+
 struct Plan {
   bool train = false, input_grad = false, busy = false;
   std::vector<int64_t> in_shape, out_shape;
   std::vector<Tensor> params, rms, rvs;  // the module's tensors (updated in place by optimizers)
   std::vector<Tensor> bufs;              // plan-owned activations, statistics, indices, workspaces
   Tensor xin, xout, gout, gin;
-  std::vector<std::function<void(Run&, void*)>> fwd, bwd;
+  Steps fwd, bwd;
   std::vector<std::vector<int64_t>> grad_shapes;  // per parameter
+  StepGraph fgraph, bgraph;
+  std::vector<Tensor> gbufs;  // parameter gradients of a backward that replays its graph
+  Plan() = default;
+  Plan(const Plan&) = delete;
+  Plan& operator=(const Plan&) = delete;
+  ~Plan() {
+    // a launch still running keeps its resources until it completes; the buffers go back to the caching allocator,
+    // whose later users on this stream run after it
+    for (StepGraph* g : {&fgraph, &bgraph})
+      if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  }
 };
+
+static bool stream_capturing(void* s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing((hipStream_t)s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
+}
+
+// Captures `steps` run with `run` on a private stream as a HIP graph; nullptr if a step cannot be captured (a call
+// that synchronizes or allocates fails under capture, and its error ends the capture).
+static hipGraphExec_t capture_steps(Steps& steps, Run& run) {
+  hipStream_t cs = nullptr;
+  if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool ok = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) == hipSuccess;
+  if (ok) {
+    try {
+      for (auto& step : steps) step(run, cs);
+    } catch (const std::exception&) {
+      ok = false;
+    }
+    ok = hipStreamEndCapture(cs, &graph) == hipSuccess && ok && graph;
+  }
+  if (ok) ok = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+  if (graph) (void)hipGraphDestroy(graph);
+  (void)hipStreamDestroy(cs);
+  (void)hipGetLastError();
+  return ok ? exec : nullptr;
+}
+
+// Whether this run of the list replays (capturing it first when its warm-up is over).
+static bool replays(StepGraph& sg, Steps& steps, Run& run, void* s) {
+  if (!g_plan_graphs || sg.off || stream_capturing(s)) return false;
+  if (!sg.exec && sg.runs >= kPlanWarmup) {
+    sg.exec = capture_steps(steps, run);
+    sg.off = sg.exec == nullptr;
+  }
+  return sg.exec != nullptr;
+}
+
+static void run_list(StepGraph& sg, Steps& steps, Run& run, void* s, bool graph) {
+  ++sg.runs;
+  if (graph) {
+    const hipError_t e = hipGraphLaunch(sg.exec, (hipStream_t)s);
+    TORCH_CHECK(e == hipSuccess, "omarchy-mac-torch plan: graph launch failed: ", hipGetErrorString(e));
+    return;
+  }
+  for (auto& step : steps) step(run, s);
+}
 
 static Tensor own(Plan& p, IntArrayRef shape, at::ScalarType dt = at::kFloat) {
   p.bufs.push_back(empty_dev(shape, dt));
@@ -321,7 +408,7 @@ static Tensor plan_forward(Plan& p, const Tensor& x) {
   Tensor xc = x.is_contiguous() ? x : x.contiguous();
   check(omt_memcpy(fpm(p.xin), fp(xc), (size_t)xc.numel() * 4, 2, s), "plan: input copy");
   Run run;
-  for (auto& step : p.fwd) step(run, s);
+  run_list(p.fgraph, p.fwd, run, s, replays(p.fgraph, p.fwd, run, s));
   Tensor out = empty_dev(p.out_shape);
   check(omt_memcpy(fpm(out), fp(p.xout), (size_t)out.numel() * 4, 2, s), "plan: output copy");
   if (debug_mode()) debug_point("plan.forward");
@@ -336,8 +423,20 @@ static std::pair<std::optional<Tensor>, std::vector<Tensor>> plan_backward(Plan&
   Tensor gc = g.is_contiguous() ? g : g.contiguous();
   check(omt_memcpy(fpm(p.gout), fp(gc), (size_t)gc.numel() * 4, 2, s), "plan: gradient copy");
   Run run;
-  for (auto& shape : p.grad_shapes) run.grads.push_back(empty_dev(shape));
-  for (auto& step : p.bwd) step(run, s);
+  // the graph writes the gradients to the plan's buffers: only when nobody holds them from the last backward
+  bool free = g_plan_graphs;
+  for (const Tensor& t : p.gbufs) free = free && t.use_count() == 1;
+  if (free && p.gbufs.empty() && !p.bgraph.off && p.bgraph.runs >= kPlanWarmup)
+    for (auto& shape : p.grad_shapes) p.gbufs.push_back(empty_dev(shape));
+  bool graph = false;
+  if (free && !p.gbufs.empty()) {
+    run.grads = p.gbufs;
+    graph = replays(p.bgraph, p.bwd, run, s);
+    if (!graph) run.grads.clear();
+  }
+  if (!graph)
+    for (auto& shape : p.grad_shapes) run.grads.push_back(empty_dev(shape));
+  run_list(p.bgraph, p.bwd, run, s, graph);
   std::optional<Tensor> gx;
   if (p.input_grad) {
     Tensor t = empty_dev(p.in_shape);
@@ -354,6 +453,8 @@ void bind_plans(pybind11::module_& m) {
       .def_readwrite("busy", &Plan::busy)
       .def_readonly("out_shape", &Plan::out_shape)
       .def("num_steps", [](const Plan& p) { return py::make_tuple(p.fwd.size(), p.bwd.size()); })
+      // whether the forward and backward step lists replay captured graphs
+      .def("graphed", [](const Plan& p) { return py::make_tuple(p.fgraph.exec != nullptr, p.bgraph.exec != nullptr); })
       .def("forward", [](Plan& p, const Tensor& x) { return plan_forward(p, x); })
       .def("backward", [](Plan& p, const Tensor& g) {
         auto r = plan_backward(p, g);
@@ -379,6 +480,13 @@ void bind_plans(pybind11::module_& m) {
     }
   });
   m.def("set_fold", [](int f) { g_fold = f; });
+  // turns graph replay of the plans' step lists on or off (plans already captured stop replaying when off); returns
+  // the previous setting
+  m.def("set_plan_graphs", [](bool on) {
+    const bool prev = g_plan_graphs;
+    g_plan_graphs = on;
+    return prev;
+  });
   m.def("get_fold", []() { return g_fold; });
 }
 

@@ -334,3 +334,86 @@ def test_conv_bn_train_after_a_rewrite_that_uses_the_conv(oc):
         torch.testing.assert_close(o_new, o_ref, rtol=1e-5, atol=1e-6)
     for i in (5, 6, 9, 10):  # running statistics, updated in place
         torch.testing.assert_close(b[i], a[i], rtol=1e-6, atol=1e-7)
+
+
+def _conv_bn_backward_graph(oc, kind, case):
+    """Backward graph of BatchNorm -> activation -> convolution: convolution_backward(gy, cx, cw) whose grad input
+    feeds the BatchNorm backward `kind` ("relu", "hardswish", "res_g", "res_g2", "plain"). case: "fusable", or what
+    keeps it apart: "second_use" (the grad input used elsewhere too), "bias" (a bias grad asked for), "early_gw" (the
+    grad weight used before the BatchNorm backward)."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    xs, c, ys = (2, 4, 5, 5), 4, (2, 6, 3, 3)
+
+    def ph(name, shape):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape)
+        return n
+
+    gy, cx, cw = ph("gy", ys), ph("cx", xs), ph("cw", (6, 4, 3, 3))
+    x, r, w, mean, invstd, other = ph("x", xs), ph("r", xs), ph("w", (c,)), ph("mean", (c,)), ph("invstd", (c,)), \
+        ph("other", xs)
+    mask = [True, True, case == "bias"]
+    cb = g.call_function(aten.convolution_backward.default,
+                         (gy, cx, cw, [6] if case == "bias" else None, [2, 2], [1, 1], [1, 1], False, [0, 0], 1, mask))
+    gx = g.call_function(operator.getitem, (cb, 0))
+    gx.meta["val"] = _fake(mode, dev, xs)
+    gw = g.call_function(operator.getitem, (cb, 1))
+    gw.meta["val"] = _fake(mode, dev, (6, 4, 3, 3))
+    extra = ()
+    if case == "bias":
+        extra = (g.call_function(operator.getitem, (cb, 2)),)
+    if case == "early_gw":
+        extra = (g.call_function(aten.mul.Tensor, (gw, 2.0)),)
+    if case == "second_use":
+        extra = (g.call_function(aten.mul.Tensor, (gx, 3.0)),)
+    m3 = [True, True, True]
+    if kind == "relu":
+        bn = g.call_function(torch.ops.omt.bn_relu_backward.default, (gx, x, r, w, mean, invstd, m3))
+    elif kind == "hardswish":
+        bn = g.call_function(torch.ops.omt.bn_act_backward.default, (gx, x, r, w, mean, invstd, 2, m3))
+    elif kind == "res_g":
+        bn = g.call_function(torch.ops.omt.bn_relu_res_backward.default, (gx, other, x, r, w, mean, invstd, m3))
+    elif kind == "res_g2":
+        bn = g.call_function(torch.ops.omt.bn_relu_res_backward.default, (other, gx, x, r, w, mean, invstd, m3))
+    else:
+        bn = g.call_function(aten.native_batch_norm_backward.default,
+                             (gx, x, w, None, None, mean, invstd, True, 1e-5, m3))
+    outs = tuple(g.call_function(operator.getitem, (bn, i)) for i in range(4 if kind.startswith("res") else 3))
+    g.output((gw,) + outs + extra)
+    return GraphModule(torch.nn.Module(), g)
+
+
+@pytest.mark.parametrize("kind", ["relu", "hardswish", "res_g", "res_g2", "plain"])
+@pytest.mark.parametrize("case", ["fusable", "second_use", "bias", "early_gw"])
+def test_conv_bn_backward(oc, kind, case):
+    """A convolution backward whose grad input only feeds a BatchNorm backward becomes, with it, one
+    omt.conv_bn_backward (outputs: the grad weight, then the BatchNorm backward's); at a block's end either gradient may
+    be the convolution's. The rewritten graph gives the original's results on CPU tensors (the composite reference);
+    a grad input used elsewhere, a bias grad, or a grad weight used before the BatchNorm backward keeps them apart."""
+    gm = _conv_bn_backward_graph(oc, kind, case)
+    ref = copy.deepcopy(gm)
+    fused = oc.fuse_conv_bn_backward(gm.graph)
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    assert fused == (1 if case == "fusable" else 0)
+    assert t.count(torch.ops.omt.conv_bn_backward.default) == fused
+    assert t.count(aten.convolution_backward.default) == 1 - fused
+    if fused:
+        node = next(n for n in gm.graph.nodes if n.target is torch.ops.omt.conv_bn_backward.default)
+        assert node.args[11] == {"relu": 1, "hardswish": 2, "plain": 0}.get(kind, 1)
+        assert node.args[12] == kind.startswith("res") and (node.args[5] is not None) == kind.startswith("res")
+    gen = torch.Generator().manual_seed(5)
+    xs, c = (2, 4, 5, 5), 4
+    r = torch.randn(xs, generator=gen) * 3
+    if kind != "hardswish":
+        r = r.relu()  # a ReLU's output, zeros included
+    args = [torch.randn((2, 6, 3, 3), generator=gen), torch.randn(xs, generator=gen),
+            torch.randn((6, 4, 3, 3), generator=gen), torch.randn(xs, generator=gen), r,
+            torch.rand(c, generator=gen) + 0.5, torch.randn(c, generator=gen), torch.rand(c, generator=gen) + 0.5,
+            torch.randn(xs, generator=gen)]
+    for o_ref, o_new in zip(ref(*args), gm(*args)):
+        torch.testing.assert_close(o_new, o_ref, rtol=1e-6, atol=1e-6)

@@ -1008,3 +1008,113 @@ def test_kernel_counts_and_times(clean):
     assert set(times) <= set(core.kernel_counts(False)) and times and all(v > 0 for v in times.values()), times
     assert core.kernel_times(False) == {} and core.kernel_counts(False)  # the times reset, the counts kept
     assert core.kernel_counts(True) and core.kernel_counts(False) == {}
+
+
+@pytest.mark.parametrize("shape", [(4, 512, 512, 2, 2, 3, 1, 1), (8, 64, 128, 16, 16, 3, 2, 1),
+                                   (32, 24, 20, 7, 7, 3, 1, 1), (2, 16, 16, 64, 96, 3, 1, 1)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_conv_bn_backward_matches_conv_then_bn(clean, shape):
+    """omt::conv_bn_backward (the compile backend's convolution backward -> BatchNorm backward) against
+    convolution_backward followed by omt::bn_act_backward / omt::bn_relu_res_backward on the device, bit for bit, under
+    grad-input plans of 1, 2 and 8 slices (the BatchNorm sums the partials itself up to 4 slices, up to 32 in channels
+    of at most 1024 elements); channels past 8192 elements run the two apart; and against the op's composite on
+    PyTorch CPU at rel-L2 1e-4, with no fallback."""
+    omt = clean
+    from omarchy_mac_torch import hip_ops
+    n, ci, co, h, w, ks, st, pd = shape
+    rng = np.random.default_rng(sum(shape) + 3)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    oh = (h + 2 * pd - ks) // st + 1
+    cx, cw, gy = f(n, ci, h, w), f(co, ci, ks, ks) * (ci * ks * ks) ** -0.5, f(n, co, oh, (w + 2 * pd - ks) // st + 1)
+    x, r, other = f(n, ci, h, w) * 2 + 1, f(n, ci, h, w) * 3, f(n, ci, h, w)
+    wb, mean, invstd = f(ci), f(ci) * 0.1, np.abs(f(ci)) + 0.5
+    cpu = [torch.from_numpy(a) for a in (gy, cx, cw, x, r, other, wb, mean, invstd)]
+    dgy, dcx, dcw, dx, dr, dother, dw, dmean, dinv = (D(t, omt) for t in cpu)
+    drelu = D(cpu[4].relu(), omt)
+    try:
+        for slices in (1, 2, 8):
+            hip_ops.set_conv_plan("dgrad", cx.shape, cw.shape, st, pd, 5, slices)
+            for act, res, with_other in ((0, False, False), (1, False, False), (2, False, False), (1, True, True),
+                                         (1, True, False)):
+                case = (slices, act, res, with_other)
+                rr = drelu if act == 1 else dr
+                o = dother if with_other else None
+                mask = [True, True, True]
+                out = torch.ops.omt.conv_bn_backward(dgy, dcx, dcw, [st, st], [pd, pd], o, dx, rr, dw, dmean, dinv,
+                                                     act, res, mask)
+                cg, cgw, _ = torch.ops.aten.convolution_backward(dgy, dcx, dcw, None, [st, st], [pd, pd], [1, 1],
+                                                                 False, [0, 0], 1, [True, True, False])
+                if res:
+                    ref = torch.ops.omt.bn_relu_res_backward(cg, o, dx, rr, dw, dmean, dinv, mask)
+                else:
+                    ref = tuple(torch.ops.omt.bn_act_backward(cg, dx, rr, dw, dmean, dinv, act, mask)) + (None,)
+                assert torch.equal(out[0].cpu(), cgw.cpu()), case
+                for a, b in zip(out[1:], ref):
+                    assert (a is None) == (b is None), case
+                    if a is not None:
+                        assert torch.equal(a.cpu(), b.cpu()), case
+                rr_cpu = cpu[4].relu() if act == 1 else cpu[4]
+                ref_cpu = torch.ops.omt.conv_bn_backward(cpu[0], cpu[1], cpu[2], [st, st], [pd, pd],
+                                                         cpu[5] if with_other else None, cpu[3], rr_cpu, cpu[6],
+                                                         cpu[7], cpu[8], act, res, mask)
+                for a, b in zip(out, ref_cpu):
+                    if b is not None:
+                        assert rel(a, b.numpy()) <= TOL, case
+        assert not omt.FALLBACKS, dict(omt.FALLBACKS)
+    finally:
+        hip_ops.clear_conv_plans()
+
+
+def test_fused_stack_graph_replay(clean):
+    """A FusedSequential's plan replays its forward and backward step lists as HIP graphs from the second run on:
+    four SGD steps give the outputs, gradients and running statistics of the same plans run step by step, bit for
+    bit, and against the unfused model at 1e-4; a gradient held past its backward (a tensor hook keeps it) is not
+    overwritten by the next one, which then runs step by step into new tensors."""
+    omt = clean
+    from omarchy_mac_torch import stacks
+    from omarchy_mac_torch.native import core
+    torch.manual_seed(11)
+    seq = nn.Sequential(nn.Conv2d(3, 16, 3, padding=1, bias=False), nn.BatchNorm2d(16), nn.ReLU(), nn.MaxPool2d(2),
+                        nn.Conv2d(16, 32, 3, padding=1, bias=False), nn.BatchNorm2d(32), nn.ReLU(),
+                        nn.AdaptiveAvgPool2d(1))
+    data = [(torch.randn(8, 3, 16, 16), torch.randn(8, 32, 1, 1)) for _ in range(4)]
+
+    def run(graphs, hold=False, fuse=True):
+        prev = core.set_plan_graphs(graphs)
+        try:
+            m = copy.deepcopy(seq).to(omt.DEVICE)
+            if fuse:
+                omt.accelerate(m)
+            opt = torch.optim.SGD(m.parameters(), lr=0.1, momentum=0.9)
+            kept = []
+            if hold:
+                m[0].weight.register_hook(lambda g: kept.append(g))
+            outs = []
+            for x, r in data:
+                opt.zero_grad()
+                y = m(D(x, omt))
+                (y * D(r, omt)).sum().backward()
+                outs.append([y.cpu()] + [p.grad.cpu() for p in m.parameters()])
+                opt.step()
+            outs.append([b.cpu() for b in m.buffers()])
+            plans = [p for ps in stacks._programs[m].idle.values() for p in ps] if fuse else []
+            return outs, plans, [k.cpu() for k in kept]
+        finally:
+            core.set_plan_graphs(prev)
+
+    step_by_step, plans0, _ = run(False)
+    assert plans0 and all(p.graphed() == (False, False) for p in plans0)
+    unfused, _, _ = run(False, fuse=False)
+    graphed, plans, _ = run(True)
+    assert plans and all(p.graphed() == (True, True) for p in plans)
+    for i, (a, b, c) in enumerate(zip(graphed, step_by_step, unfused)):
+        for u, v, w in zip(a, b, c):
+            assert torch.equal(u, v), i
+            assert rel(u.float(), w.float()) <= TOL, i
+    held, _, kept = run(True, hold=True)
+    assert len(kept) == len(data)
+    for i, k in enumerate(kept):
+        assert torch.equal(k, step_by_step[i][1]), i  # each backward's conv weight gradient, as it was
+    for a, b in zip(held, step_by_step):
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)

@@ -293,6 +293,66 @@ def test_conv_bwd_matches_separate_calls(cuda, ops, shape):
         ops.clear_conv_plans()
 
 
+CONV_BN_BWD_SHAPES = [
+    (4, 512, 512, 2, 2, 3, 1, 1),    # ResNet-18 layer4: channels of 16 elements, one vector per thread
+    (8, 64, 64, 16, 16, 3, 1, 1),    # channels of 2048 elements: several vectors per thread
+    (8, 64, 128, 16, 16, 3, 2, 1),   # stride 2: grad-input stride phases
+    (32, 24, 20, 7, 7, 3, 1, 1),     # 7x7 planes (scalar vectors), channel-major K order
+    (32, 64, 64, 16, 16, 1, 1, 0),   # 1x1, channels of exactly 8192 elements
+]
+
+
+@pytest.mark.parametrize("shape", CONV_BN_BWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv_bwd_into_bn_bwd_matches_separate_calls(cuda, ops, shape):
+    """omt_conv_bwd_parts + omt_bn_bwd_parts (the BatchNorm backward summing the convolution's grad-input partials,
+    the grad weight's slice sum on its extra workgroups or through omt_slice_sums) equal omt_conv_bwd followed by
+    omt_bn_bwd_act / omt_bn_bwd_res: every output, bit for bit, under grad-input plans of 1 to 32 slices (past the
+    fold limit the convolution sums them itself) and grad-weight plans of 1 to 40 slices, for activations none, ReLU
+    and hardswish and a residual block's end with and without g2; the grad weight against the oracle."""
+    from omarchy_mac_torch import _lib
+    n, ci, co, h, w, ks, s, p = shape
+    rng = np.random.default_rng(sum(shape) + 9)
+    cx, cw = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
+    oh = (h + 2 * p - ks) // s + 1
+    gy = rnd(rng, n, co, oh, (w + 2 * p - ks) // s + 1)
+    x, a_in, g2 = rnd(rng, n, ci, h, w) * 2 + 1, rnd(rng, n, ci, h, w) * 3, rnd(rng, n, ci, h, w)
+    gam, bet = rnd(rng, ci), rnd(rng, ci)
+    tcx, tcw, tgy, tx, tg2, tgam = (dev(a, cuda) for a in (cx, cw, gy, x, g2, gam))
+    y, sm, si = ops.batch_norm_train(tx, tgam, dev(bet, cuda), dev(rnd(rng, ci), cuda),
+                                     dev(np.abs(rnd(rng, ci)) + 0.5, cuda), 0.1, 1e-5, True)
+    relu_y = dev(np.maximum(a_in, 0), cuda)
+    gw_ref = orc.conv_wgrad(cx, gy, ks, s, p)
+    ng = ops.conv_num_tiles("dgrad") // 3
+    folded = set()
+    try:
+        for dtile, dslices in ((5, 1), (5, 2), (5 + ng, 3), (6, 4), (0, 8), (5, 32)):
+            for wtile, wslices in ((2, 1), (2, 4), (2, 40)):
+                ops.set_conv_plan("dgrad", cx.shape, cw.shape, s, p, dtile, dslices)
+                ops.set_conv_plan("wgrad", cx.shape, cw.shape, s, p, wtile, wslices)
+                gx_c, gw_c = ops.conv2d_bwd(tcx, tgy, tcw, s, p)
+                for act, res, with_g2 in ((_lib.OMT_ACT_NONE, False, False), (_lib.OMT_ACT_RELU, False, False),
+                                          (_lib.OMT_ACT_HARDSWISH, False, False), (_lib.OMT_ACT_RELU, True, True),
+                                          (_lib.OMT_ACT_RELU, True, False)):
+                    case = (dtile, dslices, wtile, wslices, act, res, with_g2)
+                    ain = relu_y if act == _lib.OMT_ACT_RELU else dev(a_in, cuda)
+                    if res:
+                        ref = ops.batch_norm_backward_res(gx_c, tg2 if with_g2 else None, tx, sm, si, tgam, ain)
+                    else:
+                        ref = ops.batch_norm_backward_act(gx_c, tx, act, ain, sm, si, tgam) + (None,)
+                    out = ops.conv2d_bwd_bn(tcx, tgy, tcw, s, p, tx, sm, si, tgam, act, ain,
+                                            tg2 if with_g2 else None, res, max_gx_slices=32 if dslices == 32 else 8,
+                                            side_sum=wslices != 4)
+                    if out[5] > 1:
+                        folded.add(out[5])
+                    assert torch.equal(out[0], gw_c), case
+                    for a, b in zip(out[1:5], ref):
+                        assert (a is None) == (b is None) and (a is None or torch.equal(a, b)), case
+                assert orc.rel_l2(host(gw_c), gw_ref) <= TOL
+    finally:
+        ops.clear_conv_plans()
+    assert folded, "no plan left its grad input unsummed"
+
+
 def test_conv_split_k_bn_loader(cuda, ops):
     """The eval BN + ReLU input loader with K split over slices."""
     rng = np.random.default_rng(11)
