@@ -328,6 +328,19 @@ int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts,
                            double momentum, double eps, int relu, const float* residual, float* y, float* z,
                            float* save_mean, float* save_invstd, float* new_rm, float* new_rv, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/* Training BatchNorm -> activation -> max pool in one pass over x [n][c][h][w]: y, save_mean, save_invstd and the
+ * running statistics as omt_bn_train_fwd_res (no residual), and pooled / idx as omt_maxpool_fwd over y (window kh x kw,
+ * stride, padding 2 pad <= window, no dilation, floor mode: [n][c][oh][ow]), bit-identical to those two calls. Channels
+ * of up to 8192 elements take one launch (the pool read from LDS), larger ones two (statistics, then the apply with
+ * the pool). Same workspace as omt_bn_train_fwd. Replaces native_batch_norm -> relu -> max_pool2d_with_indices (the
+ * reference's BatchNorm + ReLU and pool are separate steps of its stack plans, csrc/plans.cpp:110-200; the
+ * torch.compile backend and the fused stacks call this for the ResNet stem and PlainCNN's blocks). */
+int omt_bn_train_fwd_pool(int64_t n, int64_t c, int64_t h, int64_t w, const float* x, const float* gamma,
+                          const float* beta, const float* running_mean, const float* running_var, double momentum,
+                          double eps, int act, float* y, float* save_mean, float* save_invstd, float* new_rm,
+                          float* new_rv, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                          float* pooled, int64_t* idx, void* workspace, size_t workspace_bytes, void* stream);
 /* omt_bn_train_fwd_res with the statistics from omt_conv_fwd_stats (stats [c][groups][2] over x = that call's y):
  * one launch reduces each channel's groups to a few partial sums (in a fixed order, into the workspace of
  * omt_bn_train_workspace's size), the next finalizes mean / invstd and the running statistics as it applies, so x is

@@ -552,7 +552,38 @@ constexpr int64_t kFusedMax = 8192;
 
 // PARTS: x holds `slices` convolution partials of pstride elements each; every element is summed over them in slice
 // order (the convolution slice sum's order, so xo, written with the sums, equals the summed convolution output).
-template <int VEC, bool PARTS = false>
+// Max pooling of a BatchNorm's output inside its apply pass (BatchNorm -> activation -> max pool: the ResNet stem,
+// PlainCNN's blocks): window kh x kw, stride (sh, sw), padding (ph, pw), no dilation, over planes of h x w.
+struct PoolArgs {
+  float* out;
+  int64_t* idx;
+  int h, w, oh, ow, kh, kw, sh, sw, ph, pw;
+};
+
+// The maximum of v(row, col) over pooled output (oy, ox)'s window and its flat in-plane index: the first maximum in
+// row-major order wins ties and a NaN replaces the running maximum (omt_maxpool_fwd's rule, so the values and indices
+// equal that op's over the same plane).
+template <class F>
+__device__ __forceinline__ void pool_window(const PoolArgs& pa, int oy, int ox, F v, float& best, int& bi) {
+  best = -INFINITY;
+  bi = -1;
+  for (int ky = 0; ky < pa.kh; ++ky) {
+    const int yy = oy * pa.sh - pa.ph + ky;
+    if (yy < 0 || yy >= pa.h) continue;
+    for (int kx = 0; kx < pa.kw; ++kx) {
+      const int xx = ox * pa.sw - pa.pw + kx;
+      if (xx < 0 || xx >= pa.w) continue;
+      const float f = v(yy, xx);
+      if (bi < 0 || f > best || isnan(f)) {
+        best = f;
+        bi = yy * pa.w + xx;
+      }
+    }
+  }
+}
+
+// POOL: the channel's outputs also go to LDS, from which the workgroup max-pools every image of the channel.
+template <int VEC, bool PARTS = false, bool POOL = false>
 __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
@@ -563,9 +594,11 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
                                                              float* new_rv,  // may alias rm / rv
                                                              int c, int hw, const Split sp, int slices = 1,
                                                              int64_t pstride = 0, float* __restrict__ xo = nullptr,
-                                                             float* __restrict__ zo = nullptr) {
+                                                             float* __restrict__ zo = nullptr,
+                                                             const PoolArgs pool = PoolArgs{}) {
   using V = typename VecT<VEC>::T;
   __shared__ float coef[2];
+  __shared__ float chan[POOL ? kFusedMax : 1];  // POOL: the channel's outputs, image by image
   const int ch = blockIdx.x;
   float shift = x[(int64_t)ch * hw];
   if (PARTS)
@@ -635,7 +668,80 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       }
       if (zo) *reinterpret_cast<V*>(zo + off) = z;
       *reinterpret_cast<V*>(y + off) = t;
+      if (POOL)  // element vv VEC + i of the channel is image (vv VEC + i) / hw, position (vv VEC + i) % hw
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) chan[vv * VEC + i] = vget(t, i);
     }
+  }
+  if constexpr (POOL) {
+    __syncthreads();
+    const int per = pool.oh * pool.ow, total = sp.nv * VEC / hw * per;
+    for (int o = (int)threadIdx.x; o < total; o += 256) {
+      const int img = o / per, r = o - img * per, oy = r / pool.ow, ox = r - oy * pool.ow;
+      const float* cp = chan + img * hw;
+      float best;
+      int bi;
+      pool_window(pool, oy, ox, [&](int yy, int xx) { return cp[yy * pool.w + xx]; }, best, bi);
+      const int64_t oo = ((int64_t)img * c + ch) * per + r;
+      pool.out[oo] = best;
+      pool.idx[oo] = bi;
+    }
+  }
+}
+
+// The apply pass of a training BatchNorm too large for one launch, with the max pool of its output: workgroup
+// (plane, run of pooled rows [r0, r1)) finalizes its channel as bn_train_apply_kernel does (the same sums and
+// arithmetic), writes y over the rows the run owns (r0 sh up to r1 sh, the last run to the plane's end) and the
+// run's pooled outputs, each window's values recomputed from x the way y's are.
+template <bool VEC>
+__global__ void __launch_bounds__(256) bn_apply_pool_kernel(const float* __restrict__ x,
+                                                            const double* __restrict__ part, int slices, double m,
+                                                            double momentum, double eps, const float* rm,
+                                                            const float* rv, float* __restrict__ save_mean,
+                                                            float* __restrict__ save_invstd, float* new_rm,
+                                                            float* new_rv, const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta, float* __restrict__ y,
+                                                            int c, int act, int planes, int rows_per_run,
+                                                            const PoolArgs pa) {
+  __shared__ float coef[2];
+  const int q = (int)blockIdx.x, run = q / planes, plane = q - run * planes, ch = plane % c;
+  const int hw = pa.h * pa.w;
+  const int64_t base = (int64_t)plane * hw;
+  double s1, s2;
+  bn_sum_slices(part, ch, slices, s1, s2);
+  if (threadIdx.x == 0) {
+    const BnStats st = bn_finalize(s1, s2, (double)x[(int64_t)ch * hw], m, momentum, eps, rm, rv, save_mean,
+                                   save_invstd, new_rm, new_rv, ch, plane < c && run == 0);
+    const float sc = st.invstd * gamma[ch];
+    coef[0] = sc;
+    coef[1] = beta[ch] - st.mean * sc;
+  }
+  __syncthreads();
+  const float sc = coef[0], sh = coef[1];
+  const int r0 = run * rows_per_run, r1 = min(pa.oh, r0 + rows_per_run);
+  const int y0 = r0 * pa.sh, y1 = r1 == pa.oh ? pa.h : min(pa.h, r1 * pa.sh);
+  const float* xp = x + base;
+  float* yp = y + base;
+  if (VEC) {  // w % 4 == 0: whole rows are whole vectors
+    for (int e = y0 * pa.w / 4 + (int)threadIdx.x; e < y1 * pa.w / 4; e += 256) {
+      float4 v = reinterpret_cast<const float4*>(xp)[e];
+      v.x = bn_act(fmaf(v.x, sc, sh), act);
+      v.y = bn_act(fmaf(v.y, sc, sh), act);
+      v.z = bn_act(fmaf(v.z, sc, sh), act);
+      v.w = bn_act(fmaf(v.w, sc, sh), act);
+      reinterpret_cast<float4*>(yp)[e] = v;
+    }
+  } else {
+    for (int e = y0 * pa.w + (int)threadIdx.x; e < y1 * pa.w; e += 256) yp[e] = bn_act(fmaf(xp[e], sc, sh), act);
+  }
+  const int64_t obase = (int64_t)plane * pa.oh * pa.ow;
+  for (int o = r0 * pa.ow + (int)threadIdx.x; o < r1 * pa.ow; o += 256) {
+    const int oy = o / pa.ow, ox = o - oy * pa.ow;
+    float best;
+    int bi;
+    pool_window(pa, oy, ox, [&](int yy, int xx) { return bn_act(fmaf(xp[yy * pa.w + xx], sc, sh), act); }, best, bi);
+    pa.out[obase + o] = best;
+    pa.idx[obase + o] = bi;
   }
 }
 
@@ -920,6 +1026,58 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
                      new_rv);
   if (int st = launch_check("bn_stats_fin_kernel")) return st;
   return launch_apply(n, c, hw, x, save_mean, save_invstd, gamma, beta, residual, y, relu, s, z);
+}
+
+OMT_EXPORT int omt_bn_train_fwd_pool(int64_t n, int64_t c, int64_t h, int64_t w, const float* x, const float* gamma,
+                                     const float* beta, const float* running_mean, const float* running_var,
+                                     double momentum, double eps, int act, float* y, float* save_mean,
+                                     float* save_invstd, float* new_rm, float* new_rv, int64_t kh, int64_t kw,
+                                     int64_t sh, int64_t sw, int64_t ph, int64_t pw, float* pooled, int64_t* idx,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !gamma || !beta || !y || !save_mean || !save_invstd || !pooled || !idx)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_pool: null pointer");
+  if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_train_fwd_pool: activation %d", act);
+  const int64_t hw = h * w;
+  if (h < 1 || w < 1 || !bn_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_pool: size not covered");
+  if (kh < 1 || kw < 1 || sh < 1 || sw < 1 || ph < 0 || pw < 0 || 2 * ph > kh || 2 * pw > kw || h + 2 * ph < kh ||
+      w + 2 * pw < kw)
+    return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_pool: pooling window not covered");
+  if (!workspace || workspace_bytes < omt_bn_train_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_train_fwd_pool: workspace too small");
+  const int64_t oh = (h + 2 * ph - kh) / sh + 1, ow = (w + 2 * pw - kw) / sw + 1;
+  if (n * c * oh * ow >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_pool: output too large");
+  const PoolArgs pa{pooled, idx, (int)h, (int)w, (int)oh, (int)ow, (int)kh, (int)kw, (int)sh, (int)sw, (int)ph, (int)pw};
+  hipStream_t s = stream_of(stream);
+  const Split sp = bn_split(n, c, hw, al16(x));
+  if (n * hw <= kFusedMax) {  // one launch: statistics, apply and the pool from LDS
+    const bool vec = sp.vec == 4 && al16(y);
+    const Split f = vec ? sp : bn_split(n, c, hw, false);
+    if (vec)
+      hipLaunchKernelGGL((bn_train_fused_kernel<4, false, true>), dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta,
+                         running_mean, running_var, momentum, eps, act, nullptr, y, save_mean, save_invstd, new_rm,
+                         new_rv, (int)c, (int)hw, f, 1, 0, nullptr, nullptr, pa);
+    else
+      hipLaunchKernelGGL((bn_train_fused_kernel<1, false, true>), dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta,
+                         running_mean, running_var, momentum, eps, act, nullptr, y, save_mean, save_invstd, new_rm,
+                         new_rv, (int)c, (int)hw, f, 1, 0, nullptr, nullptr, pa);
+    return launch_check("bn_train_fused_kernel (pool)");
+  }
+  double* part = (double*)workspace;
+  if (int st = launch_stats(sp, x, part, c, hw, s)) return st;
+  // runs of pooled rows owning about 1024 elements of y each
+  const int rows = (int)std::max<int64_t>(1, std::min<int64_t>(oh, cdiv(1024, sh * w)));
+  const int64_t runs = cdiv(oh, rows), grid = n * c * runs;
+  if (grid >= ((int64_t)1 << 31)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_pool: grid too large");
+  const bool vec = w % 4 == 0 && al16(x) && al16(y);
+  if (vec)
+    hipLaunchKernelGGL(bn_apply_pool_kernel<true>, dim3((unsigned)grid), dim3(256), 0, s, x, (const double*)part,
+                       sp.slices, (double)(n * hw), momentum, eps, running_mean, running_var, save_mean, save_invstd,
+                       new_rm, new_rv, gamma, beta, y, (int)c, act, (int)(n * c), rows, pa);
+  else
+    hipLaunchKernelGGL(bn_apply_pool_kernel<false>, dim3((unsigned)grid), dim3(256), 0, s, x, (const double*)part,
+                       sp.slices, (double)(n * hw), momentum, eps, running_mean, running_var, save_mean, save_invstd,
+                       new_rm, new_rv, gamma, beta, y, (int)c, act, (int)(n * c), rows, pa);
+  return launch_check("bn_apply_pool_kernel");
 }
 
 OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const float* parts, int slices, float* x,

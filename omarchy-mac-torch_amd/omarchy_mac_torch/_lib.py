@@ -169,6 +169,8 @@ SIGNATURES = {
     "omt_bn_train_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_bn_train_fwd_res": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32] + [VP] * 8 + [SZ, VP]),
     "omt_bn_train_fwd_parts": (I32, [I64, I64, I64, VP, I32, VP, VP, VP, VP, VP, F64, F64, I32] + [VP] * 8 + [SZ, VP]),
+    "omt_bn_train_fwd_pool": (I32, [I64, I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32] + [VP] * 5 + [I64] * 6 +
+                              [VP, VP, VP, SZ, VP]),
     "omt_bn_train_fwd_stats": (I32, [I64, I64, I64, VP, VP, I32, SZ, VP, VP, VP, VP, F64, F64, I32] + [VP] * 8 +
                                [SZ, VP]),
     "omt_bn_eval_fwd": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),

@@ -19,7 +19,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
   3. a dense convolution whose only user is a ReLU -> omt.conv_act (ReLU in the GEMM epilogue), or an eval BatchNorm
      (`_native_batch_norm_legit_no_training`, optionally followed by ReLU) -> omt.conv_bn_act_eval (BatchNorm folded
      into the conv's weights and bias); a bias-free dense convolution feeding omt.bn_train_ -> omt.conv_bn_train_,
-     where the BatchNorm sums a K-split convolution's partials itself (no slice-sum launch); a BatchNorm backward
+     where the BatchNorm sums a K-split convolution's partials itself (no slice-sum launch), unless its output is
+     max-pooled: omt.bn_train_ -> max_pool2d_with_indices -> omt.bn_train_pool_ (the pool inside the BatchNorm's
+     apply pass: the ResNet stem); a BatchNorm backward
      (2, or a plain training one) whose incoming gradient is a dense convolution's grad input -> omt.conv_bn_backward,
      where the BatchNorm backward sums the convolution's grad-input partials and runs its grad-weight slice sum.
 
@@ -357,6 +359,59 @@ def fuse_conv_epilogues(graph):
     return count
 
 
+def _two(v, default=()):
+    """A 2-D pooling argument as a list of two ints (one int stands for both; empty or missing: default)."""
+    if not v:
+        return list(default)
+    v = [int(t) for t in v]
+    return v * 2 if len(v) == 1 else v
+
+
+def _pool_args(mp):
+    """(kernel, stride, padding) of a max_pool2d_with_indices node without dilation or ceil mode, else None."""
+    a = list(mp.args) + [None] * (6 - len(mp.args))
+    k = _two(a[1])
+    s = _two(a[2], k)
+    p = _two(a[3], [0, 0])
+    d = _two(a[4], [1, 1])
+    if mp.kwargs or len(k) != 2 or len(s) != 2 or len(p) != 2 or d != [1, 1] or bool(a[5]):
+        return None
+    return k, s, p
+
+
+def fuse_bn_train_pool(graph):
+    """max_pool2d_with_indices(y) of an omt.bn_train_ output y (no residual) -> one omt.bn_train_pool_, whose outputs 0-2
+    are the BatchNorm's (y stays for its other users: the backward's activation mask) and 3-4 the pool's: the pool
+    runs inside the BatchNorm's apply pass (the ResNet stem). Before fuse_conv_bn_train, which would otherwise take
+    the BatchNorm."""
+    count = 0
+    for bn in list(graph.nodes):
+        if bn.op != "call_function" or bn.target is not omt.bn_train_.default or bn.args[8] is not None:
+            continue
+        outs = _getitem_users(bn)
+        y = outs.get(0)
+        if y is None or 3 in outs:
+            continue
+        mp = next((u for u in y.users if u.op == "call_function" and u.target is aten.max_pool2d_with_indices.default
+                   and u.args[0] is y), None)
+        if mp is None:
+            continue
+        pa = _pool_args(mp)
+        if pa is None:
+            continue
+        x, w, b, rm, rv, momentum, eps, act = bn.args[:8]
+        fused = _call_before(graph, bn, omt.bn_train_pool_.default, (x, w, b, rm, rv, momentum, eps, act) + pa)
+        _move_getitems(graph, bn, fused)
+        graph.erase_node(bn)
+        for i, gi in _getitem_users(mp).items():
+            new = _call_before(graph, gi, operator.getitem, (fused, 3 + i), meta_from=gi)
+            gi.replace_all_uses_with(new)
+            graph.erase_node(gi)
+        graph.erase_node(mp)
+        count += 1
+    return count
+
+
 def fuse_conv_bn_train(graph):
     """bn_train_(convolution(x, cw, None, ...), ...) -> omt.conv_bn_train_(x, cw, stride, padding, ...), whose fifth
     output is the convolution's (the BatchNorm backward reads it): with a K-split plan the BatchNorm sums the
@@ -468,7 +523,8 @@ def _rewrite(gm):
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
              "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
              "bn_relu_backward": fuse_bn_relu_backward(g), "bn_hardswish_backward": fuse_bn_hardswish_backward(g),
-             "conv_bn_train": fuse_conv_bn_train(g), "conv_bn_backward": fuse_conv_bn_backward(g),
+             "bn_train_pool": fuse_bn_train_pool(g), "conv_bn_train": fuse_conv_bn_train(g),
+             "conv_bn_backward": fuse_conv_bn_backward(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()

@@ -364,6 +364,26 @@ def batch_norm_train(x, gamma, beta, running_mean=None, running_var=None, moment
     return out + (z,) if return_z else out
 
 
+def batch_norm_train_pool(x, gamma, beta, running_mean, running_var, momentum=0.1, eps=1e-5, act=_lib.OMT_ACT_RELU,
+                          kernel=2, stride=None, padding=0):
+    """Training BatchNorm -> activation -> max pool in one pass (omt_bn_train_fwd_pool): running statistics updated in
+    place. Returns (y, save_mean, save_invstd, pooled, indices)."""
+    x, gamma, beta = _need(x, "x", 4), _need(gamma, "gamma", 1), _need(beta, "beta", 1)
+    (kh, kw), (sh, sw), (ph, pw) = _pair(kernel), _pair(stride if stride is not None else kernel), _pair(padding)
+    n, c, h, w = x.shape
+    oh, ow = (h + 2 * ph - kh) // sh + 1, (w + 2 * pw - kw) // sw + 1
+    y = torch.empty_like(x)
+    sm, si = (torch.empty((c,), device=x.device, dtype=torch.float32) for _ in range(2))
+    out = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32)
+    idx = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.int64)
+    ws, nb = _workspace(L.omt_bn_train_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_train_fwd_pool(n, c, h, w, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean), _ptr(running_var),
+                                  momentum, eps, int(act), _ptr(y), _ptr(sm), _ptr(si), _ptr(running_mean),
+                                  _ptr(running_var), kh, kw, sh, sw, ph, pw, _ptr(out), _ptr(idx), _ptr(ws), nb,
+                                  _stream(x.device)), "batch_norm_train_pool")
+    return y, sm, si, out, idx
+
+
 def batch_norm_train_stats(x, stats, groups, gamma, beta, running_mean=None, running_var=None, momentum=0.1,
                            eps=1e-5, relu=False, residual=None):
     """Training BatchNorm (+ residual, ReLU) of a conv2d_stats output from its epilogue sums (omt_bn_train_fwd_stats:

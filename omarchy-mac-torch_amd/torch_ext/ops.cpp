@@ -430,6 +430,17 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_backward_ref(
   auto b = bn_act_backward_ref(std::get<0>(cb), x, r, w, mean, invstd, act, mask);
   return {std::get<1>(cb), std::get<0>(b), std::get<1>(b), std::get<2>(b), Tensor()};
 }
+// omt::bn_train_ (no residual) followed by max_pool2d_with_indices of its output (no dilation, floor mode):
+// (y, save_mean, save_invstd, pooled, indices)
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_train_pool_ref(const Tensor& x, const Tensor& w,
+                                                                            const Tensor& b, const Tensor& rm,
+                                                                            const Tensor& rv, double mom, double eps,
+                                                                            int64_t act, IntArrayRef kernel,
+                                                                            IntArrayRef stride, IntArrayRef padding) {
+  auto r = bn_train_inplace_ref(x, w, b, rm, rv, mom, eps, act, std::nullopt);
+  auto mp = at::max_pool2d_with_indices(std::get<0>(r), kernel, stride, padding, {1, 1}, false);
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<0>(mp), std::get<1>(mp)};
+}
 static Tensor conv_act_ref(const Tensor& x, const Tensor& w, const std::optional<Tensor>& b, IntArrayRef stride,
                            IntArrayRef padding, int64_t act) {
   Tensor y = at::convolution(x, w, b, stride, padding, {1, 1}, false, {0, 0}, 1);
@@ -622,6 +633,31 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_dev(const
         "omt::bn_relu_res_backward");
   return {gx, dg, db, gz};
 }
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_train_pool_dev(const Tensor& x_, const Tensor& w,
+                                                                            const Tensor& b, const Tensor& rm,
+                                                                            const Tensor& rv, double mom, double eps,
+                                                                            int64_t act, IntArrayRef kernel,
+                                                                            IntArrayRef stride, IntArrayRef padding) {
+  cover(act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH, "activation none, ReLU or hardswish");
+  cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
+        "4-D float32 with contiguous parameters");
+  cover(kernel.size() == 2 && stride.size() == 2 && padding.size() == 2, "2-D pooling window");
+  Tensor x = contig(x_);
+  const int64_t n = x.size(0), c = x.size(1), h = x.size(2), wd = x.size(3);
+  const int64_t kh = kernel[0], kw = kernel[1], sh = stride[0], sw = stride[1], ph = padding[0], pw = padding[1];
+  cover(kh >= 1 && kw >= 1 && sh >= 1 && sw >= 1 && ph >= 0 && pw >= 0 && 2 * ph <= kh && 2 * pw <= kw &&
+            h + 2 * ph >= kh && wd + 2 * pw >= kw,
+        "pooling window");
+  const int64_t oh = (h + 2 * ph - kh) / sh + 1, ow = (wd + 2 * pw - kw) / sw + 1;
+  Tensor y = empty_dev(x.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  Tensor out = empty_dev({n, c, oh, ow}), idx = empty_dev({n, c, oh, ow}, at::kLong);
+  Tensor ws = workspace(omt_bn_train_workspace(n, c, h * wd));
+  check(omt_bn_train_fwd_pool(n, c, h, wd, fp(x), fp(w), fp(b), fp(rm), fp(rv), mom, eps, (int)act, fpm(y), fpm(sm),
+                              fpm(si), fpm(rm), fpm(rv), kh, kw, sh, sw, ph, pw, fpm(out),
+                              idx.mutable_data_ptr<int64_t>(), wsptr(ws), wsbytes(ws), cur_stream()),
+        "omt::bn_train_pool_");
+  return {y, sm, si, out, idx};
+}
 // The convolution leaves its grad input unsummed (up to kFoldBwdSlices slices, kFoldBwdSlicesSmall for channels of
 // at most 1024 elements, which the BatchNorm reads one vector per thread with eight slices' loads in flight) and the
 // one-launch BatchNorm backward sums the partials as it reads them, in the convolution's slice order, and runs the
@@ -752,6 +788,14 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_k(const T
   return dev_or_ref<&bn_relu_res_backward_dev, &bn_relu_res_backward_ref>("omt::bn_relu_res_backward", g, g2, x, y, w,
                                                                           mean, invstd, mask);
 }
+static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_train_pool_k(const Tensor& x, const Tensor& w,
+                                                                          const Tensor& b, const Tensor& rm,
+                                                                          const Tensor& rv, double mom, double eps,
+                                                                          int64_t act, IntArrayRef k, IntArrayRef s,
+                                                                          IntArrayRef p) {
+  return dev_or_ref<&bn_train_pool_dev, &bn_train_pool_ref>("omt::bn_train_pool_", x, w, b, rm, rv, mom, eps, act, k,
+                                                            s, p);
+}
 static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_backward_k(
     const Tensor& gy, const Tensor& cx, const Tensor& cw, IntArrayRef s, IntArrayRef p,
     const std::optional<Tensor>& other, const Tensor& x, const Tensor& r, const Tensor& w, const Tensor& mean,
@@ -793,6 +837,10 @@ TORCH_LIBRARY(omt, m) {
   m.def("conv_bn_train_(Tensor x, Tensor cw, int[] stride, int[] padding, Tensor w, Tensor b, Tensor(a!) rm, "
         "Tensor(b!) rv, float momentum, float eps, int act, Tensor? residual) -> (Tensor, Tensor, Tensor, Tensor, "
         "Tensor)");
+  // bn_train_ (no residual) -> max_pool2d_with_indices (no dilation, floor mode) of its output in one pass:
+  // (y, save_mean, save_invstd, pooled, indices)
+  m.def("bn_train_pool_(Tensor x, Tensor w, Tensor b, Tensor(a!) rm, Tensor(b!) rv, float momentum, float eps, "
+        "int act, int[] kernel, int[] stride, int[] padding) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
   // a convolution backward feeding its grad input to a BatchNorm backward (res: omt::bn_relu_res_backward with
   // `other` its g2; else omt::bn_act_backward): (convolution grad weight, gx, dgamma, dbeta, gz)
   m.def("conv_bn_backward(Tensor gy, Tensor cx, Tensor cw, int[] stride, int[] padding, Tensor? other, Tensor x, "
@@ -809,6 +857,7 @@ TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_ref);
   m.impl("conv_bn_train_", &conv_bn_train_ref);
   m.impl("conv_bn_backward", &conv_bn_backward_ref);
+  m.impl("bn_train_pool_", &bn_train_pool_ref);
 }
 TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("bn_relu_train", &bn_relu_train_k);
@@ -820,6 +869,7 @@ TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
   m.impl("conv_bn_act_eval", &conv_bn_act_eval_k);
   m.impl("conv_bn_train_", &conv_bn_train_k);
   m.impl("conv_bn_backward", &conv_bn_backward_k);
+  m.impl("bn_train_pool_", &bn_train_pool_k);
 }
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {

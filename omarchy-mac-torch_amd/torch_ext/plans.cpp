@@ -236,16 +236,30 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       Tensor y = own(p, {n, c, h, w});
       Tensor gamma = params[pi], beta = params[pi + 1], rm = rms[bi], rv = rvs[bi];
       BackRec r;
+      // training: a following 2x2 max pool runs inside the BatchNorm's apply pass (one launch fewer, y not re-read)
+      const bool fuse_pool = train && li + 1 < layers.size() && layers[li + 1].kind == "pool" && h >= 2 && w >= 2;
+      Tensor pout, pidx;
+      if (fuse_pool) {
+        pout = own(p, {n, c, h / 2, w / 2});
+        pidx = own(p, {n, c, h / 2, w / 2}, at::kLong);
+      }
       if (train) {
         Tensor sm = own(p, {c}), si = own(p, {c});
         Tensor ws = own_ws(p, omt_bn_train_workspace(n, c, hw));
         const double mom = L.momentum;
+        const int64_t h0 = h, w0 = w;
         p.fwd.push_back([=](Run&, void* s) {
           float* rmp = rm.mutable_data_ptr<float>();
           float* rvp = rv.mutable_data_ptr<float>();
-          check(omt_bn_train_fwd(n, c, hw, fp(cur), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y), fpm(sm),
-                                 fpm(si), rmp, rvp, wsptr(ws), wsbytes(ws), s),
-                "plan: batch norm");
+          if (fuse_pool)
+            check(omt_bn_train_fwd_pool(n, c, h0, w0, fp(cur), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y),
+                                        fpm(sm), fpm(si), rmp, rvp, 2, 2, 2, 2, 0, 0, fpm(pout),
+                                        pidx.mutable_data_ptr<int64_t>(), wsptr(ws), wsbytes(ws), s),
+                  "plan: batch norm + max pool");
+          else
+            check(omt_bn_train_fwd(n, c, hw, fp(cur), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y), fpm(sm),
+                                   fpm(si), rmp, rvp, wsptr(ws), wsbytes(ws), s),
+                  "plan: batch norm");
         });
         r.sm = sm;
         r.si = si;
@@ -267,6 +281,20 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
       cur = y;
       ++bi;
       pi += 2;
+      if (fuse_pool) {  // the pool layer's record (its backward step is unchanged); the layer itself is done
+        BackRec pr;
+        pr.kind = "pool";
+        pr.idx = pidx;
+        pr.n = n;
+        pr.c = c;
+        pr.h = h;
+        pr.w = w;
+        recs.push_back(pr);
+        cur = pout;
+        h /= 2;
+        w /= 2;
+        ++li;
+      }
     } else if (L.kind == "pool" || L.kind == "apool") {
       cover(h >= 2 && w >= 2, "2x2 pool over an image smaller than 2x2");
       const int64_t oh = h / 2, ow = w / 2;

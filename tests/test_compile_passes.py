@@ -417,3 +417,58 @@ def test_conv_bn_backward(oc, kind, case):
             torch.randn(xs, generator=gen)]
     for o_ref, o_new in zip(ref(*args), gm(*args)):
         torch.testing.assert_close(o_new, o_ref, rtol=1e-6, atol=1e-6)
+
+
+def _bn_pool_graph(oc, residual, z_used, pool_args):
+    """Forward graph of omt.bn_train_ (as rewrite 0 leaves it) whose output feeds max_pool2d_with_indices and is also
+    a graph output (saved for the backward's mask)."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    shp, c = (2, 4, 9, 9), 4
+
+    def ph(name, shape):
+        n = g.placeholder(name)
+        n.meta["val"] = _fake(mode, dev, shape)
+        return n
+
+    x, w, b, rm, rv, r = ph("x", shp), ph("w", (c,)), ph("b", (c,)), ph("rm", (c,)), ph("rv", (c,)), ph("r", shp)
+    bn = g.call_function(torch.ops.omt.bn_train_.default, (x, w, b, rm, rv, 0.1, 1e-5, 1, r if residual else None))
+    outs = [g.call_function(operator.getitem, (bn, i)) for i in range(4 if z_used else 3)]
+    outs[0].meta["val"] = _fake(mode, dev, shp)
+    mp = g.call_function(aten.max_pool2d_with_indices.default, (outs[0],) + pool_args)
+    pooled = [g.call_function(operator.getitem, (mp, i)) for i in range(2)]
+    g.output(tuple(outs) + tuple(pooled))
+    return GraphModule(torch.nn.Module(), g)
+
+
+@pytest.mark.parametrize("case", ["3x3s2p1", "2x2", "k1_list", "residual", "z_used", "dilated", "ceil"])
+def test_bn_train_pool(oc, case):
+    """omt.bn_train_ -> max_pool2d_with_indices of its output becomes one omt.bn_train_pool_ (outputs: the BatchNorm's,
+    then the pool's), the BatchNorm output kept for its other users; the rewritten graph gives the original's outputs
+    and running statistics on CPU tensors. A residual, a used fourth output, dilation or ceil mode keeps them apart."""
+    pool_args = {"3x3s2p1": ([3, 3], [2, 2], [1, 1]), "2x2": ([2, 2],), "k1_list": ([2], [2]),
+                 "dilated": ([3, 3], [2, 2], [1, 1], [2, 2]), "ceil": ([3, 3], [2, 2], [0, 0], [1, 1], True)}
+    args = pool_args.get(case, ([3, 3], [2, 2], [1, 1]))
+    gm = _bn_pool_graph(oc, case == "residual", case == "z_used", tuple(args))
+    ref = copy.deepcopy(gm)
+    fused = oc.fuse_bn_train_pool(gm.graph)
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    t = _targets(gm)
+    apart = case in ("residual", "z_used", "dilated", "ceil")
+    assert fused == (0 if apart else 1)
+    assert t.count(aten.max_pool2d_with_indices.default) == (1 if apart else 0)
+    gen = torch.Generator().manual_seed(6)
+    shp, c = (2, 4, 9, 9), 4
+    inputs = [torch.randn(shp, generator=gen), torch.rand(c, generator=gen) + 0.5, torch.randn(c, generator=gen),
+              torch.randn(c, generator=gen), torch.rand(c, generator=gen) + 0.5, torch.randn(shp, generator=gen)]
+    a1, a2 = [t.clone() for t in inputs], [t.clone() for t in inputs]
+    for o_ref, o_new in zip(ref(*a1), gm(*a2)):
+        if o_ref is None:
+            assert o_new is None
+            continue
+        assert torch.equal(o_new, o_ref)
+    for i in (3, 4):  # running statistics updated in place the same way
+        assert torch.equal(a1[i], a2[i])

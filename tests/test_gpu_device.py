@@ -1118,3 +1118,31 @@ def test_fused_stack_graph_replay(clean):
     for a, b in zip(held, step_by_step):
         for u, v in zip(a, b):
             assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("shape,k,s,p", [((32, 64, 32, 32), 3, 2, 1), ((16, 8, 8, 8), 2, 2, 0),
+                                         ((3, 5, 13, 9), 3, 2, 1)], ids=["stem", "one_launch", "odd"])
+def test_bn_train_pool_matches_bn_then_pool(clean, shape, k, s, p):
+    """omt::bn_train_pool_ (the compile backend's BatchNorm -> ReLU -> max pool) against omt::bn_train_ followed by
+    max_pool2d_with_indices on the device, bit for bit (outputs, statistics, running statistics, indices), and against
+    its composite on PyTorch CPU (values at rel-L2 1e-4, equal indices where the CPU picks the same maxima), with no
+    fallback."""
+    omt = clean
+    rng = np.random.default_rng(sum(shape))
+    n, c, h, w = shape
+    f = lambda *s_: rng.standard_normal(s_).astype(np.float32)
+    x, g, b, rm, rv = f(*shape) * 2 + 0.3, f(c), f(c), f(c), np.abs(f(c)) + 0.5
+    dx, dg, db = (D(torch.from_numpy(a), omt) for a in (x, g, b))
+    rm1, rv1, rm2, rv2 = (D(torch.from_numpy(a.copy()), omt) for a in (rm, rv, rm, rv))
+    y1, m1, i1, o1, x1 = torch.ops.omt.bn_train_pool_(dx, dg, db, rm1, rv1, 0.1, 1e-5, 1, [k, k], [s, s], [p, p])
+    y2, m2, i2, _ = torch.ops.omt.bn_train_(dx, dg, db, rm2, rv2, 0.1, 1e-5, 1, None)
+    o2, x2 = torch.ops.aten.max_pool2d_with_indices(y2, [k, k], [s, s], [p, p], [1, 1], False)
+    for a, bb in ((y1, y2), (m1, m2), (i1, i2), (rm1, rm2), (rv1, rv2), (o1, o2), (x1, x2)):
+        assert torch.equal(a.cpu(), bb.cpu())
+    cpu = [torch.from_numpy(a.copy()) for a in (x, g, b, rm, rv)]
+    ref = torch.ops.omt.bn_train_pool_(*cpu, 0.1, 1e-5, 1, [k, k], [s, s], [p, p])
+    for a, bb in zip((y1, m1, i1, o1), ref[:4]):
+        assert rel(a, bb.numpy()) <= TOL
+    assert rel(rm1, cpu[3].numpy()) <= TOL and rel(rv1, cpu[4].numpy()) <= TOL
+    assert (x1.cpu() == ref[4]).float().mean() >= 0.99  # rounding can move a near-tie's maximum
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS)

@@ -869,6 +869,45 @@ def test_batch_norm_hardswish(cuda, ops, n, c, h, w):
         assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
 
 
+BN_POOL = [
+    ((32, 16, 16, 16), 2, 2, 0), ((8, 24, 7, 7), 2, 2, 0), ((16, 8, 12, 12), 3, 2, 1), ((2, 4, 64, 64), 3, 2, 1),
+    ((32, 64, 32, 32), 3, 2, 1), ((128, 32, 32, 32), 2, 2, 0), ((4, 8, 45, 37), 3, 2, 1), ((2, 3, 150, 150), 3, 2, 0),
+    ((3, 5, 9, 11), 3, 3, 1),
+]
+
+
+@pytest.mark.parametrize("shape,k,s,p", BN_POOL, ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_batch_norm_train_pool_matches_separate_calls(cuda, ops, shape, k, s, p):
+    """omt_bn_train_fwd_pool (training BatchNorm -> activation -> max pool in one pass) against omt_bn_train_fwd_res
+    followed by omt_maxpool_fwd, bit for bit (y, statistics, running statistics, pooled values, indices): channels of
+    up to 8192 elements (one launch, pooled from LDS; scalar loads on odd planes) and larger ones (runs of pooled
+    rows, odd planes, many runs), 2x2 / 3x3 windows with and without padding, activations none (NaN inputs
+    propagating through the pool), ReLU and hardswish; and against PyTorch CPU's max_pool2d_with_indices."""
+    from omarchy_mac_torch import _lib
+    n, c, h, w = shape
+    rng = np.random.default_rng(n + c + h + w + k)
+    x = rnd(rng, *shape) * 2 + 0.5
+    flat = x.reshape(-1)
+    tie = np.arange(0, flat.size - 1, 97)
+    flat[tie] = flat[tie + 1]  # repeated neighbours: ties inside windows
+    gam, bet, rm, rv = rnd(rng, c), rnd(rng, c), rnd(rng, c), np.abs(rnd(rng, c)) + 0.5
+    for act in (_lib.OMT_ACT_NONE, _lib.OMT_ACT_RELU, _lib.OMT_ACT_HARDSWISH):
+        xa = x.copy()
+        if act == _lib.OMT_ACT_NONE:
+            xa.reshape(-1)[5] = np.nan
+        tx = dev(xa, cuda)
+        rm1, rv1, rm2, rv2 = dev(rm, cuda), dev(rv, cuda), dev(rm, cuda), dev(rv, cuda)
+        y1, m1, i1, out1, idx1 = ops.batch_norm_train_pool(tx, dev(gam, cuda), dev(bet, cuda), rm1, rv1, 0.1, 1e-5,
+                                                           act, k, s, p)
+        y2, m2, i2 = ops.batch_norm_train(tx, dev(gam, cuda), dev(bet, cuda), rm2, rv2, 0.1, 1e-5, act=act)
+        out2, idx2 = ops.max_pool2d(y2, k, s, p)
+        for a, b in ((y1, y2), (m1, m2), (i1, i2), (rm1, rm2), (rv1, rv2), (out1, out2), (idx1, idx2)):
+            assert torch.equal(a.cpu(), b.cpu()) or (act == _lib.OMT_ACT_NONE and torch.equal(a.cpu().nan_to_num(7.0),
+                                                                                          b.cpu().nan_to_num(7.0))), act
+        ref, ref_idx = torch.nn.functional.max_pool2d(y2.cpu(), k, s, p, return_indices=True)
+        assert torch.equal(out1.cpu().nan_to_num(7.0), ref.nan_to_num(7.0)) and torch.equal(idx1.cpu(), ref_idx), act
+
+
 def test_batch_norm_functional_and_eval(cuda, ops):
     rng = np.random.default_rng(11)
     x, g, b, rm, rv = rnd(rng, 8, 5, 6, 6), rnd(rng, 5), rnd(rng, 5), rnd(rng, 5), np.abs(rnd(rng, 5)) + 0.2
