@@ -9,6 +9,7 @@ required: a missing build raises ImportError instead of running anything elsewhe
 import atexit
 import collections.abc
 import contextlib
+import functools
 import json
 import os
 import pathlib
@@ -98,6 +99,49 @@ class _DeviceContext:
 _mod.device = _DeviceContext
 if not hasattr(torch, DEVICE):
     torch._register_device_module(DEVICE, _mod)
+
+
+# ---- autograd over torch.cuda tensors ----
+# With this PrivateUse1 device registered, PyTorch takes it as the process's accelerator and its autograd engine keeps
+# streams for this device type only: a backward pass over torch.cuda tensors then stops on an internal assertion of
+# the engine ("opt_ready_stream && opt_parent_stream", torch/csrc/autograd/engine.cpp). A backward or grad call whose
+# roots (or requested inputs) are torch.cuda tensors is refused up front with an error that says why.
+
+CUDA_AUTOGRAD_MSG = ("omarchy-mac-torch: autograd over torch.cuda tensors is not supported in a process that has "
+                     "registered the omarchy_mac_torch device (PyTorch then takes that device as the accelerator, and "
+                     "its autograd engine stops on an internal assertion for cuda tensors). Train on the "
+                     "omarchy_mac_torch device (model.to('omarchy_mac_torch')); forward work and explicit aten calls "
+                     "on cuda tensors are unaffected.")
+
+
+def _checked(g):
+    """g (a tensor, a gradient edge or a collection of them; an iterator is read into a tuple, which the caller passes
+    on), after refusing torch.cuda tensors in it."""
+    if g is None:
+        return g
+    items = (g,) if isinstance(g, torch.Tensor) else g if isinstance(g, (list, tuple)) else tuple(g)
+    if any(isinstance(t, torch.Tensor) and t.device.type == "cuda" for t in items):
+        raise RuntimeError(CUDA_AUTOGRAD_MSG)
+    return g if isinstance(g, (torch.Tensor, list, tuple)) else items
+
+
+_autograd_backward, _autograd_grad = torch.autograd.backward, torch.autograd.grad
+
+
+@functools.wraps(_autograd_backward)
+def _backward(tensors, grad_tensors=None, retain_graph=None, create_graph=False, grad_variables=None, inputs=None):
+    return _autograd_backward(_checked(tensors), grad_tensors, retain_graph, create_graph, grad_variables,
+                              inputs=_checked(inputs))
+
+
+@functools.wraps(_autograd_grad)
+def _grad(outputs, inputs, *args, **kwargs):
+    return _autograd_grad(_checked(outputs), _checked(inputs), *args, **kwargs)
+
+
+_backward.omt_cuda_guard = _grad.omt_cuda_guard = True
+if not getattr(torch.autograd.backward, "omt_cuda_guard", False):
+    torch.autograd.backward, torch.autograd.grad = _backward, _grad
 
 
 def synchronize():

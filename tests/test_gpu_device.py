@@ -1146,3 +1146,17 @@ def test_bn_train_pool_matches_bn_then_pool(clean, shape, k, s, p):
     assert rel(rm1, cpu[3].numpy()) <= TOL and rel(rv1, cpu[4].numpy()) <= TOL
     assert (x1.cpu() == ref[4]).float().mean() >= 0.99  # rounding can move a near-tie's maximum
     assert not omt.FALLBACKS, dict(omt.FALLBACKS)
+
+
+def test_autograd_over_cuda_tensors_is_refused_clearly(clean):
+    """With the device registered, a backward or grad call over torch.cuda tensors raises the library's explanation
+    before PyTorch's engine would stop on its internal assertion; device training is unaffected."""
+    x = torch.randn(8, device="cuda", requires_grad=True)
+    loss = (x * 2).sum()
+    with pytest.raises(RuntimeError, match="omarchy_mac_torch device"):
+        loss.backward()
+    with pytest.raises(RuntimeError, match="omarchy_mac_torch device"):
+        torch.autograd.grad(loss, [x])
+    d = D(torch.randn(8), clean).requires_grad_()
+    (d * 2).sum().backward()
+    assert torch.equal(d.grad.cpu(), torch.full((8,), 2.0))

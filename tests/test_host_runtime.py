@@ -140,3 +140,23 @@ def test_fusability_rules(layers, ok):
         bns = [m for m in layers if isinstance(m, nn.BatchNorm2d)]
         assert len(prog.params) == len(convs) + 2 * len(bns) and prog.bns == bns
         assert len(prog.records) == len(layers) - len(bns)  # each BatchNorm's ReLU is part of its step
+
+
+def test_autograd_over_cuda_tensors_is_refused_up_front():
+    """backward / grad whose roots or requested inputs are torch.cuda tensors raise the library's explanation (PyTorch's
+    engine would stop on an internal assertion once the device is registered); CPU autograd, gradient edges and
+    iterators of inputs pass through unchanged. Fake cuda tensors stand in for real ones (no GPU here)."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from omarchy_mac_torch import native
+    assert torch.autograd.backward.omt_cuda_guard and torch.autograd.grad.omt_cuda_guard
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        fake = torch.empty(3, device="cuda")
+    for roots in (fake, [fake], (torch.ones(1), fake), iter([fake])):
+        with pytest.raises(RuntimeError, match="omarchy_mac_torch device"):
+            native._checked(roots)
+    x = torch.randn(4, requires_grad=True)
+    (x * 3).sum().backward(inputs=iter([x]))  # an iterator of inputs is read once and handed on
+    assert torch.equal(x.grad, torch.full((4,), 3.0))
+    (gx,) = torch.autograd.grad((x * x).sum(), [x])
+    assert torch.allclose(gx, 2 * x.detach())
