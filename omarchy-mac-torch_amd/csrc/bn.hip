@@ -549,6 +549,11 @@ __global__ void __launch_bounds__(256) bn_bwd_apply_flat_kernel(const float* __r
 // registers for the apply pass (at most kFusedMax / 256 floats per operand). The finalize and apply arithmetic is that
 // of the split kernels above, so both paths agree to the float64 summation order.
 constexpr int64_t kFusedMax = 8192;
+// Channels of at most kFusedSmall elements run the same kernels sized for that (MAXE): a quarter of the registers per
+// operand, so every channel's workgroup is resident at once (the 8192-element variants hold 2-3 waves per SIMD,
+// leaving ResNet-18's 512-channel layers and MobileNet's 576-channel 7x7 layers two rounds of workgroups). Unused
+// register slots hold values that add exact zeros, so both sizes give the same results.
+constexpr int64_t kFusedSmall = 2048;
 
 // PARTS: x holds `slices` convolution partials of pstride elements each; every element is summed over them in slice
 // order (the convolution slice sum's order, so xo, written with the sums, equals the summed convolution output).
@@ -583,7 +588,7 @@ __device__ __forceinline__ void pool_window(const PoolArgs& pa, int oy, int ox, 
 }
 
 // POOL: the channel's outputs also go to LDS, from which the workgroup max-pools every image of the channel.
-template <int VEC, bool PARTS = false, bool POOL = false>
+template <int VEC, bool PARTS = false, bool POOL = false, int MAXE = (int)kFusedMax>
 __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
@@ -598,12 +603,12 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
                                                              const PoolArgs pool = PoolArgs{}) {
   using V = typename VecT<VEC>::T;
   __shared__ float coef[2];
-  __shared__ float chan[POOL ? kFusedMax : 1];  // POOL: the channel's outputs, image by image
+  __shared__ float chan[POOL ? MAXE : 1];  // POOL: the channel's outputs, image by image
   const int ch = blockIdx.x;
   float shift = x[(int64_t)ch * hw];
   if (PARTS)
     for (int z = 1; z < slices; ++z) shift += x[z * pstride + (int64_t)ch * hw];
-  constexpr int NR = (int)(kFusedMax / (256 * VEC));  // vectors per thread
+  constexpr int NR = MAXE / (256 * VEC);  // vectors per thread
   V r[NR];
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
@@ -779,7 +784,7 @@ __device__ __forceinline__ void run_side_sum(const SideSums& ss, int64_t b) {
 
 // PARTS: g holds `slices` convolution partials of pstride elements each, summed here in slice order (the convolution
 // slice sum's order) before g2 is added; workgroups past the c channels run the side slice sums.
-template <int VEC, bool RES, bool PARTS = false>
+template <int VEC, bool RES, bool PARTS = false, int MAXE = (int)kFusedMax>
 __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ g2,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ ry,
@@ -798,7 +803,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   }
   const int ch = blockIdx.x;
   const float mu = mean[ch], inv = invstd[ch];
-  constexpr int NR = (int)(kFusedMax / (256 * VEC));  // vectors per thread
+  constexpr int NR = MAXE / (256 * VEC);  // vectors per thread
   V rg[NR], rx[NR], rr[NR];
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
@@ -994,14 +999,17 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
   if (n * hw <= kFusedMax) {
     const bool vec = sp.vec == 4 && al16(y) && (!residual || al16(residual)) && al16(z);
     const Split f = vec ? sp : bn_split(n, c, hw, false);
-    if (vec)
-      hipLaunchKernelGGL(bn_train_fused_kernel<4>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
-                         running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
-                         (int)hw, f, 1, 0, nullptr, z);
-    else
-      hipLaunchKernelGGL(bn_train_fused_kernel<1>, dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, running_mean,
-                         running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
-                         (int)hw, f, 1, 0, nullptr, z);
+#define OMT_BN_FUSED(V, E)                                                                                      \
+  hipLaunchKernelGGL((bn_train_fused_kernel<V, false, false, E>), dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta, \
+                     running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,      \
+                     new_rv, (int)c, (int)hw, f, 1, 0, nullptr, z)
+    const bool sm = n * hw <= kFusedSmall;
+    if (vec) {
+      if (sm) OMT_BN_FUSED(4, (int)kFusedSmall); else OMT_BN_FUSED(4, (int)kFusedMax);
+    } else {
+      if (sm) OMT_BN_FUSED(1, (int)kFusedSmall); else OMT_BN_FUSED(1, (int)kFusedMax);
+    }
+#undef OMT_BN_FUSED
     return launch_check("bn_train_fused_kernel");
   }
   double* part = (double*)workspace;
@@ -1052,14 +1060,17 @@ OMT_EXPORT int omt_bn_train_fwd_pool(int64_t n, int64_t c, int64_t h, int64_t w,
   if (n * hw <= kFusedMax) {  // one launch: statistics, apply and the pool from LDS
     const bool vec = sp.vec == 4 && al16(y);
     const Split f = vec ? sp : bn_split(n, c, hw, false);
-    if (vec)
-      hipLaunchKernelGGL((bn_train_fused_kernel<4, false, true>), dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta,
-                         running_mean, running_var, momentum, eps, act, nullptr, y, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, (int)hw, f, 1, 0, nullptr, nullptr, pa);
-    else
-      hipLaunchKernelGGL((bn_train_fused_kernel<1, false, true>), dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta,
-                         running_mean, running_var, momentum, eps, act, nullptr, y, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, (int)hw, f, 1, 0, nullptr, nullptr, pa);
+#define OMT_BN_POOL(V, E)                                                                                        \
+  hipLaunchKernelGGL((bn_train_fused_kernel<V, false, true, E>), dim3((unsigned)c), dim3(256), 0, s, x, gamma, beta,  \
+                     running_mean, running_var, momentum, eps, act, nullptr, y, save_mean, save_invstd, new_rm, new_rv, \
+                     (int)c, (int)hw, f, 1, 0, nullptr, nullptr, pa)
+    const bool sm = n * hw <= kFusedSmall;
+    if (vec) {
+      if (sm) OMT_BN_POOL(4, (int)kFusedSmall); else OMT_BN_POOL(4, (int)kFusedMax);
+    } else {
+      if (sm) OMT_BN_POOL(1, (int)kFusedSmall); else OMT_BN_POOL(1, (int)kFusedMax);
+    }
+#undef OMT_BN_POOL
     return launch_check("bn_train_fused_kernel (pool)");
   }
   double* part = (double*)workspace;
@@ -1099,14 +1110,17 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
   const bool vec = hw % 4 == 0 && al16(parts) && al16(x) && al16(y) && al16(residual) && al16(z);
   if (n * hw <= kFusedMax) {  // one launch: the slice sums, the statistics and the apply
     const Split f = bn_split(n, c, hw, vec);
-    if (vec)
-      hipLaunchKernelGGL((bn_train_fused_kernel<4, true>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma, beta,
-                         running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, (int)hw, f, slices, total, x, z);
-    else
-      hipLaunchKernelGGL((bn_train_fused_kernel<1, true>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma, beta,
-                         running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, (int)hw, f, slices, total, x, z);
+#define OMT_BN_PARTS(V, E)                                                                                       \
+  hipLaunchKernelGGL((bn_train_fused_kernel<V, true, false, E>), dim3((unsigned)c), dim3(256), 0, s, parts, gamma,    \
+                     beta, running_mean, running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, \
+                     new_rv, (int)c, (int)hw, f, slices, total, x, z)
+    const bool sm = n * hw <= kFusedSmall;
+    if (vec) {
+      if (sm) OMT_BN_PARTS(4, (int)kFusedSmall); else OMT_BN_PARTS(4, (int)kFusedMax);
+    } else {
+      if (sm) OMT_BN_PARTS(1, (int)kFusedSmall); else OMT_BN_PARTS(1, (int)kFusedMax);
+    }
+#undef OMT_BN_PARTS
     return launch_check("bn_train_fused_kernel");
   }
   const bool v4 = total % 4 == 0 && al16(parts) && al16(x);
@@ -1208,12 +1222,16 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
   const bool aligned = al16(g) && al16(g2) && al16(x) && al16(relu_y) && al16(gx) && al16(gzo);
   const Split sp = bn_split(n, c, hw, aligned);
   if (n * hw <= kFusedMax) {
-    if (sp.vec == 4)
-      hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y,
-                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act);
-    else
-      hipLaunchKernelGGL((bn_bwd_fused_kernel<1, RES>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y,
-                         save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act);
+#define OMT_BN_BWD(V, E)                                                                                        \
+  hipLaunchKernelGGL((bn_bwd_fused_kernel<V, RES, false, E>), dim3((unsigned)c), dim3(256), 0, s, g, g2, x, relu_y, \
+                     save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act)
+    const bool sm = n * hw <= kFusedSmall;
+    if (sp.vec == 4) {
+      if (sm) OMT_BN_BWD(4, (int)kFusedSmall); else OMT_BN_BWD(4, (int)kFusedMax);
+    } else {
+      if (sm) OMT_BN_BWD(1, (int)kFusedSmall); else OMT_BN_BWD(1, (int)kFusedMax);
+    }
+#undef OMT_BN_BWD
     return launch_check("bn_bwd_fused_kernel");
   }
   double* part = (double*)workspace;
@@ -1320,14 +1338,21 @@ OMT_EXPORT int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g
   const float* ry = act == OMT_ACT_NONE ? nullptr : act_in;
   const int64_t pstride = n * c * hw;
   hipStream_t s = stream_of(stream);
-#define OMT_BWD_PARTS(V, R)                                                                                      \
-  hipLaunchKernelGGL((bn_bwd_fused_kernel<V, R, true>), dim3((unsigned)blocks), dim3(256), 0, s, g_parts, g2, x, ry, \
-                     save_mean, save_invstd, gamma, gx, dgamma, dbeta, gz, (int)c, (int)hw, sp, act, slices, pstride, side)
+#define OMT_BWD_PARTS(V, R, E)                                                                                   \
+  hipLaunchKernelGGL((bn_bwd_fused_kernel<V, R, true, E>), dim3((unsigned)blocks), dim3(256), 0, s, g_parts, g2, x,  \
+                     ry, save_mean, save_invstd, gamma, gx, dgamma, dbeta, gz, (int)c, (int)hw, sp, act, slices,        \
+                     pstride, side)
+#define OMT_BWD_PARTS_E(V, R)                                                        \
+  do {                                                                               \
+    if (n * hw <= kFusedSmall) OMT_BWD_PARTS(V, R, (int)kFusedSmall);               \
+    else OMT_BWD_PARTS(V, R, (int)kFusedMax);                                        \
+  } while (0)
   if (sp.vec == 4) {
-    if (gz) OMT_BWD_PARTS(4, true); else OMT_BWD_PARTS(4, false);
+    if (gz) OMT_BWD_PARTS_E(4, true); else OMT_BWD_PARTS_E(4, false);
   } else {
-    if (gz) OMT_BWD_PARTS(1, true); else OMT_BWD_PARTS(1, false);
+    if (gz) OMT_BWD_PARTS_E(1, true); else OMT_BWD_PARTS_E(1, false);
   }
+#undef OMT_BWD_PARTS_E
 #undef OMT_BWD_PARTS
   return launch_check("bn_bwd_fused_kernel");
 }
