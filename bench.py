@@ -314,6 +314,59 @@ def resnet_trace_summary(trace_csv, replays=22):
         print()
 
 
+def resnet_layer_trace(trace_csv, reps=100):
+    """Reads the kernel_trace.csv of a rocprofv3 --kernel-trace run of `bench.py --workload resnet-layers --no-tune`
+    (plans from the tuning file of an earlier run, so the trace holds the timed calls alone) and prints ResNet-18's
+    convolution launches layer by layer as markdown: for each layer and direction, every kernel of one call with its
+    workgroups and median duration, the call's total and its TFLOP/s. Each op of the table runs its kernel sequence
+    121 times in a row (one eager call, then 121 replayed calls of a 20-call graph: 1 warm + 5 timed replays), so the
+    trace is 22 periodic runs in the table's order; durations are medians over the last `reps` calls."""
+    import csv
+    import statistics
+
+    rows = []
+    for r in csv.DictReader(open(trace_csv)):
+        wg = 1
+        for d in "XYZ":
+            wg *= max(1, int(r[f"Grid_Size_{d}"]) // max(1, int(r[f"Workgroup_Size_{d}"])))
+        rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], wg))
+    rows.sort()
+    names = [r[2] for r in rows]
+    ops, i = [], 0
+    while i < len(rows) and len(ops) < 2 * len(RESNET18_LAYERS):
+        found = None
+        for d in range(1, 9):
+            end = i + d * reps
+            if end <= len(names) and all(names[j] == names[j - d] for j in range(i + d, end)):
+                found = d
+                break
+        if found is None:
+            i += 1
+            continue
+        d, end = found, i + found * reps
+        while end + d <= len(names) and names[end:end + d] == names[end - d:end]:
+            end += d
+        ops.append(rows[end - reps * d:end])
+        i = end
+    print("| Layer | Direction | Kernel | Workgroups | us (median) |\n|---|---|---|---|---|")
+    total = {"fwd": 0.0, "bwd": 0.0}
+    for k, run in enumerate(ops):
+        name, n, c, kk, h, ks, s, p, uses = RESNET18_LAYERS[k // 2]
+        direction = "fwd" if k % 2 == 0 else ("wgrad" if name.startswith("stem") else "bwd (dgrad + wgrad)")
+        d = len(run) // reps
+        call_us = 0.0
+        for pos in range(d):
+            us = statistics.median((run[j * d + pos][1] - run[j * d + pos][0]) / 1e3 for j in range(reps))
+            call_us += us
+            kname = run[pos][2].split("(")[0].replace("void ", "")
+            print(f"| {name if pos == 0 else ''} | {direction if pos == 0 else ''} | `{kname}` | {run[pos][3]} | "
+                  f"{us:.1f} |")
+        f = flops_dir(n, c, kk, h, ks, s, p) * (1 if k % 2 == 0 or name.startswith("stem") else 2)
+        total["fwd" if k % 2 == 0 else "bwd"] += uses * call_us
+        print(f"| | | **call: {call_us:.1f} us, {f / call_us / 1e6:.1f} TFLOP/s, used {uses}x per step** | | |")
+    print(f"\nper step (each layer times its uses): forward {total['fwd']:.0f} us, backward {total['bwd']:.0f} us")
+
+
 def pmc_summary(fetch_csv, write_csv, layers, workload):
     """Reads the FETCH_SIZE and WRITE_SIZE counter dumps of two `--pmc-probe` runs: the 1 GiB device copy calibrates
     each counter (bytes it must move / what the counter reports), then the forward gather-kernel dispatches after
@@ -1082,6 +1135,9 @@ def main():
                          "(--no-bw --no-models --no-cpu, same --steps)")
     ap.add_argument("--resnet-trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="kernel time per step by family of a rocprofv3 --kernel-trace run of --workload resnet")
+    ap.add_argument("--resnet-layer-trace", metavar="KERNEL_TRACE_CSV",
+                    help="ResNet-18's convolution launches per layer (workgroups, us) from a rocprofv3 --kernel-trace "
+                         "run of --workload resnet-layers --no-tune")
     ap.add_argument("--kernel-table", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel launches and mean / median duration of this library's kernels in a kernel trace")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -1096,6 +1152,9 @@ def main():
         return
     if args.kernel_table:
         kernel_table(args.kernel_table)
+        return
+    if args.resnet_layer_trace:
+        resnet_layer_trace(args.resnet_layer_trace)
         return
     if args.resnet_trace_summary:
         resnet_trace_summary(args.resnet_trace_summary)
