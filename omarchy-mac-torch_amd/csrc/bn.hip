@@ -620,7 +620,21 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);
     }
   }
-  if (PARTS) {  // slice by slice, each slice's loads of all NR vectors in flight together
+  if (PARTS && sp.nv <= 256) {  // one vector per thread: kReduceBatch slices' loads in flight, added in slice order
+    const int vv = (int)threadIdx.x;
+    if (vv < sp.nv) {
+      const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
+      for (int z0 = 1; z0 < slices; z0 += kReduceBatch) {
+        V t[kReduceBatch];
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u)
+          if (z0 + u < slices) t[u] = *reinterpret_cast<const V*>(x + (z0 + u) * pstride + off);
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u)
+          if (z0 + u < slices) vadd(r[0], t[u]);
+      }
+    }
+  } else if (PARTS) {  // slice by slice, each slice's loads of all NR vectors in flight together
     for (int z = 1; z < slices; ++z) {
       V t[NR];
 #pragma unroll
@@ -632,6 +646,8 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       for (int u = 0; u < NR; ++u)
         if ((int)threadIdx.x + u * 256 < sp.nv) vadd(r[u], t[u]);
     }
+  }
+  if (PARTS) {
 #pragma unroll
     for (int u = 0; u < NR; ++u) {
       const int vv = (int)threadIdx.x + u * 256;

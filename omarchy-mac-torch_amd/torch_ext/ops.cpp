@@ -500,11 +500,13 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_train_inplace_dev(const Ten
         "omt::bn_train_");
   return {y, sm, si, z};
 }
-// The convolution leaves a K split of up to kFoldSlices slices unsummed and the BatchNorm sums them as it reads them
-// (in the slice order of the convolution's own slice sum: the convolution output and everything after it are
-// bit-identical to convolution + omt::bn_train_), one launch fewer; other plans run the two as they are. (With 16-32
-// slices of a 2x2-plane layer the BatchNorm's scattered partial reads took longer than the slice-sum launch.)
-constexpr int kFoldSlices = 4;
+// The convolution leaves a K split of up to kFoldSlices slices (kFoldSlicesSmall in channels of at most 1024
+// elements, which the BatchNorm reads one vector per thread with eight slices' loads in flight) unsummed and the
+// BatchNorm sums them as it reads them (in the slice order of the convolution's own slice sum: the convolution output
+// and everything after it are bit-identical to convolution + omt::bn_train_), one launch fewer; other plans run the two
+// as they are. (Reading 16-32 slices one at a time, a 2x2-plane layer's BatchNorm took longer than the slice-sum
+// launch.)
+constexpr int kFoldSlices = 4, kFoldSlicesSmall = 16;
 // Channels of up to this many elements (n * oh * ow) are normalized by one BatchNorm launch that holds the channel in
 // registers (one read of the input already). Larger ones take the statistics from the convolution's epilogue when
 // the output has at least kStatsMinBytes: below that the epilogue's sums cost the convolution more than the skipped
@@ -559,8 +561,8 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(cons
   }
   const float* parts = nullptr;
   int slices = 1;
-  check(omt_conv_fwd_unsummed(&g, fp(x), fp(cw), fpm(conv), wsptr(ws), wsbytes(ws), kFoldSlices, &parts, &slices,
-                              cur_stream()),
+  check(omt_conv_fwd_unsummed(&g, fp(x), fp(cw), fpm(conv), wsptr(ws), wsbytes(ws),
+                              n * hw <= 1024 ? kFoldSlicesSmall : kFoldSlices, &parts, &slices, cur_stream()),
         "omt::conv_bn_train_ (convolution)");
   Tensor bws = workspace(omt_bn_train_workspace(n, c, hw));
   if (slices > 1)

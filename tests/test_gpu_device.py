@@ -734,8 +734,8 @@ def test_native_batch_norm_legit_shims_on_device(clean, shape):
 def test_conv_bn_train_matches_conv_then_bn(clean, shape):
     """omt::conv_bn_train_ (the compile backend's convolution -> training BatchNorm) against the convolution followed
     by omt::bn_train_, bit for bit (outputs, convolution output, statistics, running statistics), under unsplit and
-    K-split plans (the BatchNorm sums the convolution's partials itself up to 4 slices; 16 are summed by the
-    convolution): channels of at most 8192 elements (one launch), larger ones (slice sum, then the two-pass
+    K-split plans (the BatchNorm sums the convolution's partials itself up to 4 slices, up to 16 in channels of at
+    most 1024 elements; more are summed by the convolution): channels of at most 8192 elements (one launch), larger ones (slice sum, then the two-pass
     BatchNorm), 7x7 planes (scalar loads), 2x2 planes, with a residual and ReLU; and against the oracle. Outputs of
     64 MB or more with channels past 8192 elements, under an unsplit plan, take their statistics from the
     convolution's epilogue (summed in another order): there the convolution output is bit-identical and the rest
@@ -753,7 +753,7 @@ def test_conv_bn_train_matches_conv_then_bn(clean, shape):
     dx, dcw, dg, db, dr = (D(torch.from_numpy(a), omt) for a in (x, cw, g, b, r))
     conv_ref = orc.conv_fwd(x, cw, None, st, pd)
     try:
-        for slices in (1, 2, 4, 16):
+        for slices in (1, 2, 4, 12, 16):
             hip_ops.set_conv_plan("fwd", x.shape, cw.shape, st, pd, 5, slices)
             for act, res in ((1, None), (1, dr), (0, None), (2, None)):
                 rm1, rv1 = D(torch.from_numpy(rm.copy()), omt), D(torch.from_numpy(rv.copy()), omt)
