@@ -469,6 +469,20 @@ int omt_nll_loss_fwd(int64_t rows, int64_t cols, const float* logp, const int64_
 int omt_nll_loss_bwd(int64_t rows, int64_t cols, const float* g, const int64_t* target, const float* weight,
                      int64_t ignore_index, int reduction, const float* total_weight, float* gx, void* stream);
 
+/* The squeeze-excite block's excitation MLP, per image n: h[n] = relu(W1 z[n] + b1), a2[n] = W2 h[n] + b2,
+ * s[n] = hardsigmoid(a2[n]), z [n][c] the squeezed channels, W1 [r][c], b1 [r], W2 [c][r], b2 [c] (nn.Linear
+ * layouts), c <= 2048, r <= 1024 (OMT_UNSUPPORTED otherwise); h [n][r] and a2 [n][c] are kept for the backward. Two
+ * launches. The backward, from gs = dL/ds and the forward's z, h, a2: gz [n][c], gw1, gb1, gw2, gb2 (two launches;
+ * workspace of omt_se_bwd_workspace bytes). Every sum runs in a fixed order. No counterpart in the reference, whose
+ * squeeze-excite runs as linear -> relu -> linear -> hardsigmoid ops (csrc/linalg.cpp:25-79, elementwise.cpp); the
+ * torch.compile backend's omt::se_mlp. */
+size_t omt_se_bwd_workspace(int64_t n, int64_t c, int64_t r);
+int omt_se_fwd(int64_t n, int64_t c, int64_t r, const float* z, const float* w1, const float* b1, const float* w2,
+               const float* b2, float* s, float* h, float* a2, void* stream);
+int omt_se_bwd(int64_t n, int64_t c, int64_t r, const float* gs, const float* z, const float* h, const float* a2,
+               const float* w1, const float* w2, float* gz, float* gw1, float* gb1, float* gw2, float* gb2,
+               void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- fused optimizers (float32, contiguous parameters; many tensors per launch) -------------------------------- */
 
 /* One parameter of an Adam / AdamW step: the step count (a float on the device) has already been incremented.

@@ -74,6 +74,12 @@ __device__ __forceinline__ float hardswish_f(float x) { return x * fminf(fmaxf(x
 __device__ __forceinline__ float hardswish_grad(float g, float x) {
   return x <= -3.f ? 0.f : (x < 3.f ? g * (x / 3.f + 0.5f) : g);
 }
+// Hardsigmoid as PyTorch defines it (torch.nn.Hardsigmoid documentation), in the same order of operations as its CPU
+// kernels, so that results agree to the last bit in most cases.
+__device__ __forceinline__ float hardsigmoid_f(float x) { return fminf(fmaxf(x + 3.f, 0.f), 6.f) / 6.f; }
+__device__ __forceinline__ float hardsigmoid_grad(float g, float x) {
+  return (x > -3.f && x < 3.f) ? g * (1.f / 6.f) : 0.f;
+}
 // The activation after a BatchNorm: act OMT_ACT_NONE, OMT_ACT_RELU or OMT_ACT_HARDSWISH.
 __device__ __forceinline__ float bn_act(float v, int act) {
   return act == OMT_ACT_RELU ? fmaxf(v, 0.f) : (act == OMT_ACT_HARDSWISH ? hardswish_f(v) : v);

@@ -13,12 +13,6 @@
 
 namespace omt {
 
-// Activation formulas as PyTorch defines them (torch.nn.Hardsigmoid documentation), in the same order of operations as
-// its CPU kernels, so that results agree to the last bit in most cases (hardswish: omt_internal.h).
-__device__ __forceinline__ float hardsigmoid_f(float x) { return fminf(fmaxf(x + 3.f, 0.f), 6.f) / 6.f; }
-__device__ __forceinline__ float hardsigmoid_grad(float g, float x) {
-  return (x > -3.f && x < 3.f) ? g * (1.f / 6.f) : 0.f;
-}
 
 template <int OP>
 __device__ __forceinline__ float pw_apply(float a, float b, float alpha) {

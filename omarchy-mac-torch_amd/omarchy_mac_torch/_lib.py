@@ -146,6 +146,9 @@ SIGNATURES = {
     "omt_log_softmax_bwd": (I32, [I64, I64, VP, VP, VP, VP]),
     "omt_nll_loss_fwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
     "omt_nll_loss_bwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
+    "omt_se_bwd_workspace": (SZ, [I64, I64, I64]),
+    "omt_se_fwd": (I32, [I64, I64, I64] + [VP] * 9),
+    "omt_se_bwd": (I32, [I64, I64, I64] + [VP] * 12 + [SZ, VP]),
     "omt_conv_bwd_workspace": (SZ, [G]),
     "omt_conv_bwd": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_conv_bwd_parts": (I32, [G, VP, VP, VP, VP, VP, VP, SZ, I32, ctypes.POINTER(VP), ctypes.POINTER(I32),

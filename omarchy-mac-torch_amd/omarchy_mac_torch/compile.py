@@ -25,6 +25,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
      (2, or a plain training one) whose incoming gradient is a dense convolution's grad input -> omt.conv_bn_backward,
      where the BatchNorm backward sums the convolution's grad-input partials and runs its grad-weight slice sum.
 
+Before AOTAutograd, on the graph Dynamo hands the backend: a squeeze-excite block's excitation MLP,
+hardsigmoid(linear(relu(linear(z)))) -> omt.se_mlp (two launches; its registered backward, omt.se_mlp_backward, two).
+
 Each omt op falls back to its plain aten composition when the device kernels do not cover the case, so a rewritten
 graph is always correct. The rewritten graphs then run as HIP graphs: a few calls op by op, then captured once and
 replayed (omarchy_mac_torch/replay.py; OMARCHY_MAC_TORCH_COMPILE_GRAPHS=0 keeps them op by op).
@@ -540,8 +543,98 @@ def _compiler(kind):
     return compile_graph
 
 
+# ---- before AOTAutograd: the squeeze-excite MLP ----
+
+def _se_setup(ctx, inputs, output):
+    z, w1, _, w2, _ = inputs
+    _, h, a2 = output
+    ctx.mark_non_differentiable(h, a2)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(z, h, a2, w1, w2)
+
+
+def _se_backward(ctx, gs, _gh, _ga2):
+    return tuple(omt.se_mlp_backward(gs, *ctx.saved_tensors))
+
+
+# omt::se_mlp's backward is omt::se_mlp_backward (both defined in the extension): AOTAutograd traces through this
+# formula, so the forward graph holds omt.se_mlp and the backward graph omt.se_mlp_backward; the op's second and third
+# outputs (the hidden layer and the pre-activation) are saved for the backward, not differentiated
+torch.library.register_autograd("omt::se_mlp", _se_backward, setup_context=_se_setup)
+
+_LINEAR = (torch._C._nn.linear, torch.nn.functional.linear)
+_RELU = (torch.nn.functional.relu, torch.relu)
+_HARDSIGMOID = (torch.nn.functional.hardsigmoid,)
+_SE_MAX_C, _SE_MAX_R = 2048, 1024  # the kernels' limits (omt_se_fwd)
+
+
+def _example(n):
+    return n.meta.get("example_value") if isinstance(n, Node) else None
+
+
+def _only_use(n, user):
+    return isinstance(n, Node) and list(n.users) == [user]
+
+
+def _plain_call(n, targets, nargs):
+    """n calls one of `targets` with `nargs` positional arguments and no in-place flag."""
+    return (n.op == "call_function" and n.target in targets and len(n.args) == nargs
+            and not n.kwargs.get("inplace", False) and all(k == "inplace" for k in n.kwargs))
+
+
+def fuse_squeeze_excite(graph):
+    """hardsigmoid(linear(relu(linear(z, w1, b1)), w2, b2)), the excitation MLP of a squeeze-excite block, over float32
+    device tensors -> omt.se_mlp(z, w1, b1, w2, b2), in the graph Dynamo hands the backend (before AOTAutograd, which
+    then traces the op's registered backward, omt.se_mlp_backward, into the backward graph). The two intermediate
+    values must have no other use, both biases be present, and the sizes be within the kernels' (C <= 2048,
+    R <= 1024): two launches forward and two backward instead of about five and ten."""
+    count = 0
+    for hs in list(graph.nodes):
+        if not _plain_call(hs, _HARDSIGMOID, 1):
+            continue
+        l2 = hs.args[0]
+        if not (_only_use(l2, hs) and _plain_call(l2, _LINEAR, 3)):
+            continue
+        h, w2, b2 = l2.args
+        if not (_only_use(h, l2) and _plain_call(h, _RELU, 1)):
+            continue
+        l1 = h.args[0]
+        if not (_only_use(l1, h) and _plain_call(l1, _LINEAR, 3)):
+            continue
+        z, w1, b1 = l1.args
+        ez, e1, eb1, e2, eb2 = (_example(v) for v in (z, w1, b1, w2, b2))
+        if not all(isinstance(v, torch.Tensor) and v.device.type == DEVICE and v.dtype == torch.float32
+                   for v in (ez, e1, eb1, e2, eb2)):
+            continue
+        if ez.dim() != 2 or e1.dim() != 2 or e2.dim() != 2:
+            continue
+        c, r = ez.shape[1], e1.shape[0]
+        if c > _SE_MAX_C or r > _SE_MAX_R or tuple(e2.shape) != (c, r):
+            continue
+        with graph.inserting_before(hs):
+            fused = graph.call_function(omt.se_mlp.default, (z, w1, b1, w2, b2))
+            out = graph.call_function(operator.getitem, (fused, 0))
+        out.meta = dict(hs.meta)
+        hs.replace_all_uses_with(out)
+        for dead in (hs, l2, h, l1):
+            graph.erase_node(dead)
+        count += 1
+    return count
+
+
 # buffer mutations stay in the graph (as copy_ into the inputs) so that rewrite 0 can turn them into in-place updates;
 # every rewritten graph is replayed as a HIP graph after its warm-up calls (replay.py)
-backend = aot_autograd(fw_compiler=_compiler("forward"), bw_compiler=_compiler("backward"),
-                       inference_compiler=_compiler("inference"), keep_inference_input_mutations=True)
+_aot = aot_autograd(fw_compiler=_compiler("forward"), bw_compiler=_compiler("backward"),
+                    inference_compiler=_compiler("inference"), keep_inference_input_mutations=True)
+
+
+def backend(gm, example_inputs):
+    """The backend: the squeeze-excite rewrite on Dynamo's graph, then AOTAutograd with the rewrites above on its
+    forward and backward graphs."""
+    if fuse_squeeze_excite(gm.graph):
+        gm.graph.lint()
+        gm.recompile()
+    return _aot(gm, example_inputs)
+
+
 register_backend(name=DEVICE)(backend)

@@ -472,3 +472,50 @@ def test_bn_train_pool(oc, case):
         assert torch.equal(o_new, o_ref)
     for i in (3, 4):  # running statistics updated in place the same way
         assert torch.equal(a1[i], a2[i])
+
+
+def _se_graph(oc, case):
+    """Dynamo-style graph (torch-level calls, example values on the device) of a squeeze-excite excitation:
+    hardsigmoid(linear(relu(linear(z, w1, b1)), w2, b2)), with the variations `case` names."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    n, c, r = 4, (2100 if case == "too_wide" else 16), 4
+
+    def ph(name, shape):
+        node = g.placeholder(name)
+        node.meta["example_value"] = _fake(mode, dev, shape)
+        return node
+
+    z, w1, b1, w2, b2 = ph("z", (n, c)), ph("w1", (r, c)), ph("b1", (r,)), ph("w2", (c, r)), ph("b2", (c,))
+    l1 = g.call_function(torch._C._nn.linear, (z, w1, None if case == "no_bias" else b1))
+    h = g.call_function(torch.nn.functional.relu, (l1,), {"inplace": True} if case == "inplace" else {})
+    l2 = g.call_function(torch._C._nn.linear, (h, w2, b2))
+    s = g.call_function(torch.nn.functional.hardsigmoid, (l2,))
+    outs = (s,) + ((h,) if case == "second_use" else ())
+    g.output(outs)
+    return GraphModule(torch.nn.Module(), g), (n, c, r)
+
+
+@pytest.mark.parametrize("case", ["fusable", "second_use", "no_bias", "inplace", "too_wide"])
+def test_squeeze_excite_rewrite(oc, case):
+    """Dynamo's graph of a squeeze-excite excitation (linear -> relu -> linear -> hardsigmoid) becomes one omt.se_mlp,
+    whose output and gradients (its registered backward, omt.se_mlp_backward) equal the original's on CPU tensors;
+    a second use of an intermediate, a missing bias, an in-place ReLU or more than 2048 channels keeps it apart."""
+    gm, (n, c, r) = _se_graph(oc, case)
+    ref = copy.deepcopy(gm)
+    fused = oc.fuse_squeeze_excite(gm.graph)
+    gm.graph.lint()
+    gm.recompile()
+    assert fused == (1 if case == "fusable" else 0)
+    assert _targets(gm).count(torch.ops.omt.se_mlp.default) == fused
+    if case != "fusable":
+        return
+    gen = torch.Generator().manual_seed(8)
+    args = [torch.randn(s, generator=gen, requires_grad=True) for s in ((n, c), (r, c), (r,), (c, r), (c,))]
+    args2 = [a.detach().clone().requires_grad_() for a in args]
+    (y_ref,), (y,) = ref(*args), gm(*args2)
+    assert torch.equal(y, y_ref)
+    gy = torch.randn(y.shape, generator=gen)
+    for a, b in zip(torch.autograd.grad(y_ref, args, gy), torch.autograd.grad(y, args2, gy)):
+        torch.testing.assert_close(b, a, rtol=1e-6, atol=1e-6)

@@ -587,7 +587,8 @@ def test_config_models_fast_paths_against_cpu(model_plans, name):
     """The paths the benchmark times, at full size against PyTorch CPU under the north-star bound: the model under
     torch.compile(backend="omarchy_mac_torch") (its forward and backward graphs replayed as HIP graphs from the third
     step on), and the whole step captured as one HIP graph with the model compiled or not. Same plans as the eager
-    run, whose losses each path reproduces to 1e-6."""
+    run, whose losses each path reproduces to 1e-6, except MobileNetV3's compiled paths: their squeeze-excite MLP
+    (omt.se_mlp) sums in another order than the eager linear layers' GEMMs, and they are held to the CPU bound alone."""
     from omarchy_mac_torch import replay
     omt = model_plans
     base, data, make_opt = _config_data(name)
@@ -603,7 +604,8 @@ def test_config_models_fast_paths_against_cpu(model_plans, name):
     paths["compiled + graphed"] = _train_graphed(base, data, make_opt, omt.DEVICE, compiled=True)
     for what, dev in paths.items():
         _assert_north_star(dev, cpu, cpu64, f"{name} {what}")
-        assert all(abs(a - b) <= 1e-6 * abs(b) for a, b in zip(dev, eager)), (what, dev, eager)
+        if name == "resnet18" or "compiled" not in what:
+            assert all(abs(a - b) <= 1e-6 * abs(b) for a, b in zip(dev, eager)), (what, dev, eager)
     assert not omt.FALLBACKS, dict(omt.FALLBACKS.items())
 
 
@@ -1160,3 +1162,38 @@ def test_autograd_over_cuda_tensors_is_refused_clearly(clean):
     d = D(torch.randn(8), clean).requires_grad_()
     (d * 2).sum().backward()
     assert torch.equal(d.grad.cpu(), torch.full((8,), 2.0))
+
+
+def test_compiled_squeeze_excite_runs_fused(clean):
+    """Under the compile backend each of MobileNetV3's six squeeze-excite MLPs runs as omt.se_mlp (two launches forward,
+    two backward: counted per kernel), with the loss and the gradients matching the model run op by op: all gradients
+    together at rel-L2 1e-4, each parameter's within 1e-3 of its norm plus 1e-6 of the whole gradient's (the bias of a
+    BatchNorm that feeds a convolution and another BatchNorm has a gradient that is zero but for rounding, ~1e-8,
+    where both paths' rounding differs entirely), and no fallback."""
+    from omarchy_mac_torch import models
+    omt = clean
+    core = omt.native.core
+    torch.manual_seed(4)
+    base = models.mobilenet_v3_small(1000)
+    x, t = torch.randn(4, 3, 64, 64), torch.randint(0, 1000, (4,))
+    eager = copy.deepcopy(base).to(omt.DEVICE)
+    comp = copy.deepcopy(base).to(omt.DEVICE)
+    compiled = torch.compile(comp, backend=omt.DEVICE, dynamic=False)
+    l_eager = F.cross_entropy(eager(D(x, omt)), D(t, omt))
+    l_eager.backward()
+    core.kernel_counts(True)
+    l_comp = F.cross_entropy(compiled(D(x, omt)), D(t, omt))
+    l_comp.backward()
+    torch.cuda.synchronize()
+    counts = core.kernel_counts(True)
+    se = {k: v for k, v in counts.items() if k.startswith("se_")}
+    assert se == {k: 6 for k in ("se_hidden_kernel", "se_out_kernel", "se_bwd_hidden_kernel", "se_bwd_input_kernel")}, se
+    assert abs(float(l_comp) - float(l_eager)) <= 1e-4 * abs(float(l_eager))
+    ge = torch.cat([p.grad.cpu().reshape(-1) for p in eager.parameters()])
+    gc = torch.cat([p.grad.cpu().reshape(-1) for p in comp.parameters()])
+    assert rel(gc, ge.numpy()) <= 1e-4
+    floor = 1e-6 * float(ge.norm())
+    for (pn, pe), (_, pc) in zip(eager.named_parameters(), comp.named_parameters()):
+        err, size = float((pc.grad - pe.grad).norm()), float(pe.grad.norm())
+        assert err <= 1e-3 * size + floor, (pn, err, size)
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS)

@@ -309,3 +309,32 @@ def test_foreach_and_scalar_adds(omt):
     assert [int(t) for t in dcounts] == [10 ** 12 + i + 3 + (i == 0) for i in range(70)]
     assert torch.equal(y.cpu(), small + 1.5) and torch.equal(dsmall.cpu(), small + 2)
     assert not delegated, delegated
+
+
+@pytest.mark.parametrize("n,c,r", [(32, 16, 8), (32, 96, 24), (32, 576, 144), (5, 2048, 1024), (3, 40, 10), (1, 7, 1)])
+def test_squeeze_excite_mlp(omt, n, c, r):
+    """omt::se_mlp (s = hardsigmoid(a2), a2 = W2 h + b2, h = relu(W1 z + b1), two launches, returning s, h, a2) and
+    omt::se_mlp_backward (two launches, from the saved z, h, a2) on the device against PyTorch CPU's linear -> relu ->
+    linear -> hardsigmoid and its autograd, at rel-L2 1e-5 (the sums run in another order than the CPU's GEMMs), at
+    MobileNetV3's sizes and the kernels' limits (2048 channels, 1024 hidden); a hidden unit exactly zero (the ReLU
+    mask) for every image; no fallback."""
+    omt.FALLBACKS.clear()
+    g = torch.Generator().manual_seed(n + c + r)
+    z = torch.randn(n, c, generator=g)
+    w1, b1 = torch.randn(r, c, generator=g) * c ** -0.5, torch.randn(r, generator=g)
+    w2, b2 = torch.randn(c, r, generator=g) * r ** -0.5 * 3, torch.randn(c, generator=g)
+    b1[0] = -1e4  # hidden unit 0 exactly zero (ReLU mask) for every image
+    cpu = [t.clone().requires_grad_() for t in (z, w1, b1, w2, b2)]
+    h = F.relu(F.linear(cpu[0], cpu[1], cpu[2]))
+    a2 = F.linear(h, cpu[3], cpu[4])
+    s = F.hardsigmoid(a2)
+    gs = torch.randn(n, c, generator=g)
+    grads = torch.autograd.grad(s, cpu, gs)
+    dev = [t.to(omt.DEVICE) for t in (z, w1, b1, w2, b2)]
+    ds, dh, da2 = torch.ops.omt.se_mlp(*dev)
+    assert rel(ds, s) <= 1e-5 and rel(dh, h) <= 1e-5 and rel(da2, a2) <= 1e-5
+    assert torch.all(dh.cpu()[:, 0] == 0)
+    dgrads = torch.ops.omt.se_mlp_backward(gs.to(omt.DEVICE), dev[0], dh, da2, dev[1], dev[3])
+    for got, ref in zip(dgrads, grads):
+        assert got.shape == ref.shape and rel(got, ref) <= 1e-5
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS)
