@@ -395,6 +395,27 @@ int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g_parts, int
                      const float* gamma, float* gx, float* dgamma, float* dbeta, float* gz, const omt_slice_sum* sums,
                      int count, void* stream);
 
+/* Channels-last (NHWC) BatchNorm: x, y, z, residual, g, g2, act_in, gx, gz [n][hw][c] (the memory of a channels_last
+ * [n][c][h][w] tensor). Same operations, arguments and statistics as omt_bn_train_fwd_res, omt_bn_eval_fwd and the
+ * backward of omt_bn_bwd_act / omt_bn_bwd_res (g2 and gz may be NULL; gz, when set, receives the gradient through
+ * the activation, for a residual branch); the shifted float64 sums run in another order than the NCHW kernels', so
+ * the results agree with theirs to float64 rounding. Three launches each way (partial sums, finalize, apply; the
+ * backward with gx and gz NULL stops after the finalize); workspace of omt_bn_nhwc_workspace bytes. No counterpart
+ * in the reference, which makes every operand contiguous NCHW (csrc/device.cpp:60-66) and runs batch_norm_ /
+ * batch_norm_backward_ (csrc/nn.cpp:25-78) on that. */
+size_t omt_bn_nhwc_workspace(int64_t n, int64_t c, int64_t hw);
+int omt_bn_train_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
+                          const float* running_mean, const float* running_var, double momentum, double eps, int act,
+                          const float* residual, float* y, float* z, float* save_mean, float* save_invstd,
+                          float* new_rm, float* new_rv, void* workspace, size_t workspace_bytes, void* stream);
+int omt_bn_eval_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
+                         const float* running_mean, const float* running_var, double eps, int act, float* y,
+                         void* stream);
+int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x, int act,
+                    const float* act_in, const float* save_mean, const float* save_invstd, const float* gamma,
+                    float* gx, float* dgamma, float* dbeta, float* gz, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* ---- pooling (planes = n * c) ----------------------------------------------------------------------------- */
 
 /* Max pool, any window / stride / padding / dilation; idx = int64 flat position in the input plane, first maximum
@@ -419,6 +440,28 @@ int omt_adapool_fwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t 
                     void* stream);
 int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* g, float* gx,
                     void* stream);
+
+/* Channels-last (NHWC) pools: x, gx [n][ih][iw][c], y, g, idx [n][oh][ow][c] (channels_last tensors' memory). The
+ * same windows, rules and index meaning (flat y * iw + x within a plane) as the NCHW entry points above, and the same
+ * visiting order, so the results are theirs transposed, bit for bit. n * ih * iw * c and n * oh * ow * c below 2^31
+ * (OMT_UNSUPPORTED otherwise). No counterpart in the reference, which pools contiguous NCHW copies (csrc/nn.cpp:157-222,
+ * csrc/device.cpp:60-66). */
+int omt_maxpool_fwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                         int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, const float* x,
+                         float* y, int64_t* idx, void* stream);
+int omt_maxpool_bwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                         int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, const float* g,
+                         const int64_t* idx, float* gx, void* stream);
+int omt_avgpool_fwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                         int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad,
+                         int64_t divisor_override, const float* x, float* y, void* stream);
+int omt_avgpool_bwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh, int64_t kw,
+                         int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad,
+                         int64_t divisor_override, const float* g, float* gx, void* stream);
+int omt_adapool_fwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* x,
+                         float* y, void* stream);
+int omt_adapool_bwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, const float* g,
+                         float* gx, void* stream);
 
 /* ---- pointwise, reduction and loss ops of the training steps (outside the convolution path) ------------------------
  * Contiguous float32 operands. Replace the reference's general elementwise kernel and op table
@@ -457,6 +500,17 @@ int omt_channel_scale(int64_t planes, int64_t hw, const float* x, const float* s
 int omt_plane_broadcast(int64_t planes, int64_t hw, const float* v, float scale, float* y, void* stream);
 /* y[p] = scale * sum_i x[p][i] (sum or mean over the last two dims of an NCHW tensor). */
 int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float scale, float* y, void* stream);
+/* The same over channels-last planes: y[img][ch] = scale * sum_p x[img][p][ch], x [n][hw][c] (a channels_last
+ * tensor's memory), y [n][c]; n <= 65535. No counterpart in the reference, which reduces contiguous NCHW copies
+ * (csrc/reduce.cpp, csrc/device.cpp:60-66). */
+int omt_plane_sum_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, float scale, float* y, void* stream);
+/* omt_pointwise over [n][c][hw] operands stored in different orders: each of a, b and out NCHW (flag 0) or
+ * channels-last NHWC (flag 1); out[i] = op(a, b) at the same logical element. Unary and binary ops only (not
+ * OMT_PW_FILL). For the one op per step where a channels-last model meets an NCHW gradient (a global average pool's
+ * backward, broadcast over its planes, meeting the ReLU mask). No counterpart in the reference (its operands are
+ * contiguous NCHW copies, csrc/device.cpp:60-66). */
+int omt_pointwise_layouts(int op, int64_t n, int64_t c, int64_t hw, const float* a, int a_nhwc, const float* b,
+                          int b_nhwc, float alpha, float* out, int out_nhwc, void* stream);
 /* Row-wise log-softmax of x[rows][cols] and its gradient gx = g - exp(y) * sum_j g (y the forward's output). */
 int omt_log_softmax_fwd(int64_t rows, int64_t cols, const float* x, float* y, void* stream);
 int omt_log_softmax_bwd(int64_t rows, int64_t cols, const float* g, const float* y, float* gx, void* stream);

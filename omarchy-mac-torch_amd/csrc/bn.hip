@@ -1386,3 +1386,421 @@ OMT_EXPORT int omt_bn_bwd_act(int64_t n, int64_t c, int64_t hw, const float* g, 
   return bn_bwd_impl<false>(n, c, hw, g, nullptr, x, act == OMT_ACT_NONE ? nullptr : act_in, save_mean, save_invstd,
                             gamma, gx, dgamma, dbeta, nullptr, workspace, stream_of(stream), act);
 }
+
+namespace omt {
+
+// ---- channels-last (NHWC) BatchNorm -----------------------------------------------------------------------------
+// x [rows = n * hw][c], a channel's elements c apart. Workgroup (channel block, row slice): thread t owns channel
+// vector j = block * cb + t % cb (VEC channels: float4 when c % 4 == 0 and the operands are 16-byte aligned) and walks
+// rows t / cb, + rl, ... of the slice, so a wave reads whole rows (64 vectors of one row, or several rows of a
+// narrower tensor) and every thread keeps its channels' sums, coefficients or constants in registers. The statistics
+// are the NCHW kernels' shifted float64 sums (shift x[row 0][ch] = x[n=0, ch, 0, 0], the same element) in another
+// order: each thread's rows in order, the row lanes added in lane order, the slices by one wave per channel (lane-
+// strided, then the DPP wave sum); finalize and apply arithmetic are the NCHW kernels' (bn_finalize, bn_bwd_consts,
+// bwd_elem), so y and gx agree with the NCHW path to the float64 rounding of the sums. Three launches each way:
+// partial sums, finalize, apply.
+constexpr int kNhwcMaxSlices = 256;
+
+__host__ __device__ __forceinline__ int64_t min64(int64_t a, int64_t b) { return a < b ? a : b; }
+
+struct NhwcSplit {
+  int vec;          // channels per vector: 4 or 1
+  int cv;           // vectors per row: c / vec
+  int cb;           // vectors per workgroup row: min(cv, 64)
+  int rl;           // row lanes: 256 / cb
+  int cblocks;      // workgroups across a row: cv / cb rounded up
+  int slices;       // row slices of the reductions
+  int64_t rows;     // n * hw
+  int64_t per_slice;
+};
+
+static NhwcSplit nhwc_split(int64_t n, int64_t c, int64_t hw, bool aligned) {
+  NhwcSplit sp;
+  sp.vec = (c % 4 == 0 && aligned) ? 4 : 1;
+  sp.cv = (int)(c / sp.vec);
+  sp.cb = sp.cv < 64 ? sp.cv : 64;
+  sp.rl = 256 / sp.cb;
+  sp.cblocks = (int)cdiv(sp.cv, sp.cb);
+  sp.rows = n * hw;
+  int64_t want = cdiv(1024, sp.cblocks);                        // ~1024 workgroups
+  const int64_t by_rows = sp.rows / (4 * (int64_t)sp.rl) > 1 ? sp.rows / (4 * (int64_t)sp.rl) : 1;  // at least 4 rows per thread
+  want = min64(min64(want, by_rows), kNhwcMaxSlices);
+  sp.per_slice = cdiv(sp.rows, want);
+  sp.slices = (int)cdiv(sp.rows, sp.per_slice);
+  return sp;
+}
+
+// Row lanes' sums of the block's channels added in lane order: thread t < cb * VEC ends with channel vector t / VEC,
+// element t % VEC. All threads call it.
+template <int VEC>
+__device__ __forceinline__ void nhwc_lane_sums(const NhwcSplit& sp, const double* s1, const double* s2, double& o1,
+                                               double& o2) {
+  __shared__ double r1[256 * VEC], r2[256 * VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    r1[threadIdx.x * VEC + i] = s1[i];
+    r2[threadIdx.x * VEC + i] = s2[i];
+  }
+  __syncthreads();
+  o1 = 0.0, o2 = 0.0;
+  const int q = threadIdx.x;
+  if (q < sp.cb * VEC) {
+    const int jl = q / VEC, i = q - jl * VEC;
+    for (int r = 0; r < sp.rl; ++r) {
+      o1 += r1[(r * sp.cb + jl) * VEC + i];
+      o2 += r2[(r * sp.cb + jl) * VEC + i];
+    }
+  }
+}
+
+// grid (cblocks, slices): shifted partial sums per (channel, slice) into part[ch][slices][2]
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_nhwc_stats_kernel(const float* __restrict__ x, double* __restrict__ part,
+                                                            int c, const NhwcSplit sp) {
+  using V = typename VecT<VEC>::T;
+  const int jl = threadIdx.x % sp.cb, lane = threadIdx.x / sp.cb, j = blockIdx.x * sp.cb + jl;
+  const bool on = lane < sp.rl && j < sp.cv;
+  double s1[VEC], s2[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) s1[i] = 0.0, s2[i] = 0.0;
+  if (on) {
+    const V shift = *reinterpret_cast<const V*>(x + (int64_t)j * VEC);
+    const int64_t r0 = blockIdx.y * sp.per_slice, r1 = min64(sp.rows, r0 + sp.per_slice);
+    const int64_t step = sp.rl;
+    for (int64_t r = r0 + lane; r < r1; r += 4 * step) {
+      V v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = r + u * step < r1 ? *reinterpret_cast<const V*>(x + (r + u * step) * c + (int64_t)j * VEC) : shift;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          const double d = (double)(vget(v[u], i) - vget(shift, i));  // 0 past the slice's end
+          s1[i] += d;
+          s2[i] += d * d;
+        }
+    }
+  }
+  double o1, o2;
+  nhwc_lane_sums<VEC>(sp, s1, s2, o1, o2);
+  const int q = threadIdx.x;
+  if (q < sp.cb * VEC) {
+    const int ch = (blockIdx.x * sp.cb + q / VEC) * VEC + q % VEC;
+    if (ch < c) {
+      part[((int64_t)ch * sp.slices + blockIdx.y) * 2] = o1;
+      part[((int64_t)ch * sp.slices + blockIdx.y) * 2 + 1] = o2;
+    }
+  }
+}
+
+// A channel's slices summed by one wave (lane-strided, then the wave sum); valid in every lane. Whole waves call it.
+__device__ __forceinline__ void nhwc_wave_slices(const double* __restrict__ part, int ch, int slices, double& s1,
+                                                 double& s2) {
+  s1 = 0.0, s2 = 0.0;
+  for (int s = threadIdx.x & 63; s < slices; s += 64) {
+    s1 += part[((int64_t)ch * slices + s) * 2];
+    s2 += part[((int64_t)ch * slices + s) * 2 + 1];
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+}
+
+// one wave per channel: mean, invstd, the running statistics
+__global__ void __launch_bounds__(256) bn_nhwc_fin_kernel(const float* __restrict__ x, const double* __restrict__ part,
+                                                          int c, int slices, double m, double momentum, double eps,
+                                                          const float* rm, const float* rv,
+                                                          float* __restrict__ save_mean,
+                                                          float* __restrict__ save_invstd, float* new_rm,
+                                                          float* new_rv) {
+  const int ch = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (ch >= c) return;  // whole waves
+  double s1, s2;
+  nhwc_wave_slices(part, ch, slices, s1, s2);
+  if ((threadIdx.x & 63) == 0)
+    bn_finalize(s1, s2, (double)x[ch], m, momentum, eps, rm, rv, save_mean, save_invstd, new_rm, new_rv, ch, true);
+}
+
+// grid (cblocks, chunks of rows): y = act(x * sc + sh (+ res)) with sc = invstd * gamma, sh = beta - mean * sc per
+// channel (invstd null: eval, 1 / sqrt(var + eps)); zo, when set, receives the activation's input.
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_nhwc_apply_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ mean,
+                                                            const float* __restrict__ invstd,
+                                                            const float* __restrict__ var, double eps,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta,
+                                                            const float* __restrict__ res, float* __restrict__ y,
+                                                            float* __restrict__ zo, int c, int act, const NhwcSplit sp,
+                                                            int64_t rows_per_chunk) {
+  using V = typename VecT<VEC>::T;
+  const int jl = threadIdx.x % sp.cb, lane = threadIdx.x / sp.cb, j = blockIdx.x * sp.cb + jl;
+  if (lane >= sp.rl || j >= sp.cv) return;
+  float sc[VEC], sh[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int ch = j * VEC + i;
+    const float inv = invstd ? invstd[ch] : (float)(1.0 / sqrt((double)var[ch] + eps));
+    sc[i] = inv * gamma[ch];
+    sh[i] = beta[ch] - mean[ch] * sc[i];
+  }
+  const int64_t r0 = blockIdx.y * rows_per_chunk, r1 = min64(sp.rows, r0 + rows_per_chunk);
+  for (int64_t r = r0 + lane; r < r1; r += sp.rl) {
+    const int64_t off = r * c + (int64_t)j * VEC;
+    V v = *reinterpret_cast<const V*>(x + off), q, z;
+    if (res) q = *reinterpret_cast<const V*>(res + off);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float f = fmaf(vget(v, i), sc[i], sh[i]);
+      if (res) f += vget(q, i);
+      vset(z, i, f);
+      vset(v, i, bn_act(f, act));
+    }
+    if (zo) *reinterpret_cast<V*>(zo + off) = z;
+    *reinterpret_cast<V*>(y + off) = v;
+  }
+}
+
+// grid (cblocks, slices): per (channel, slice) sum gz and sum gz * xhat, gz = (g + g2) through the activation's
+// gradient (ry: the ReLU's output or the hardswish's input; null: none)
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_nhwc_bwd_part_kernel(const float* __restrict__ g,
+                                                               const float* __restrict__ g2,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ ry,
+                                                               const float* __restrict__ mean,
+                                                               const float* __restrict__ invstd,
+                                                               double* __restrict__ part, int c, int act,
+                                                               const NhwcSplit sp) {
+  using V = typename VecT<VEC>::T;
+  const int jl = threadIdx.x % sp.cb, lane = threadIdx.x / sp.cb, j = blockIdx.x * sp.cb + jl;
+  const bool on = lane < sp.rl && j < sp.cv;
+  double s1[VEC], s2[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) s1[i] = 0.0, s2[i] = 0.0;
+  if (on) {
+    float mu[VEC], inv[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) mu[i] = mean[j * VEC + i], inv[i] = invstd[j * VEC + i];
+    const int64_t r0 = blockIdx.y * sp.per_slice, r1 = min64(sp.rows, r0 + sp.per_slice);
+    const int64_t step = sp.rl;
+    for (int64_t r = r0 + lane; r < r1; r += 4 * step) {
+      V vg[4], vx[4], vr[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (r + u * step < r1) {
+          const int64_t off = (r + u * step) * c + (int64_t)j * VEC;
+          vg[u] = *reinterpret_cast<const V*>(g + off);
+          if (g2) vadd(vg[u], *reinterpret_cast<const V*>(g2 + off));
+          vx[u] = *reinterpret_cast<const V*>(x + off);
+          if (ry) vr[u] = *reinterpret_cast<const V*>(ry + off);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            vset(vg[u], i, 0.f);  // gz = 0 contributes nothing
+            vset(vx[u], i, mu[i]);
+            vset(vr[u], i, 1.f);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          float gz = vget(vg[u], i);
+          if (ry) gz = bn_act_grad(gz, vget(vr[u], i), act);
+          const float xhat = (vget(vx[u], i) - mu[i]) * inv[i];
+          s1[i] += (double)gz;
+          s2[i] += (double)gz * (double)xhat;
+        }
+    }
+  }
+  double o1, o2;
+  nhwc_lane_sums<VEC>(sp, s1, s2, o1, o2);
+  const int q = threadIdx.x;
+  if (q < sp.cb * VEC) {
+    const int ch = (blockIdx.x * sp.cb + q / VEC) * VEC + q % VEC;
+    if (ch < c) {
+      part[((int64_t)ch * sp.slices + blockIdx.y) * 2] = o1;
+      part[((int64_t)ch * sp.slices + blockIdx.y) * 2 + 1] = o2;
+    }
+  }
+}
+
+// one wave per channel: dbeta = sum gz, dgamma = sum gz * xhat, and the input-gradient constants kc[ch][5]
+__global__ void __launch_bounds__(256) bn_nhwc_bwd_fin_kernel(const double* __restrict__ part, int c, int slices,
+                                                              const float* __restrict__ mean,
+                                                              const float* __restrict__ invstd,
+                                                              const float* __restrict__ gamma, double m,
+                                                              float* __restrict__ kc, float* __restrict__ dgamma,
+                                                              float* __restrict__ dbeta) {
+  const int ch = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (ch >= c) return;  // whole waves
+  double s1, s2;
+  nhwc_wave_slices(part, ch, slices, s1, s2);
+  if ((threadIdx.x & 63) == 0) {
+    if (dbeta) dbeta[ch] = (float)s1;
+    if (dgamma) dgamma[ch] = (float)s2;
+    if (gamma) bn_bwd_consts(s1, s2, m, gamma[ch], mean[ch], invstd[ch], kc + ch * 5);
+  }
+}
+
+// grid (cblocks, chunks of rows): gx = k1 gz - k2 - k3 xhat per channel; gzo, when set, receives gz
+template <int VEC>
+__global__ void __launch_bounds__(256) bn_nhwc_bwd_apply_kernel(const float* __restrict__ g,
+                                                                const float* __restrict__ g2,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ ry,
+                                                                const float* __restrict__ kc, float* __restrict__ gx,
+                                                                float* __restrict__ gzo, int c, int act,
+                                                                const NhwcSplit sp, int64_t rows_per_chunk) {
+  using V = typename VecT<VEC>::T;
+  const int jl = threadIdx.x % sp.cb, lane = threadIdx.x / sp.cb, j = blockIdx.x * sp.cb + jl;
+  if (lane >= sp.rl || j >= sp.cv) return;
+  float k[VEC][5];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int e = 0; e < 5; ++e) k[i][e] = kc[(j * VEC + i) * 5 + e];
+  const int64_t r0 = blockIdx.y * rows_per_chunk, r1 = min64(sp.rows, r0 + rows_per_chunk);
+  for (int64_t r = r0 + lane; r < r1; r += sp.rl) {
+    const int64_t off = r * c + (int64_t)j * VEC;
+    V vg = *reinterpret_cast<const V*>(g + off);
+    if (g2) vadd(vg, *reinterpret_cast<const V*>(g2 + off));
+    const V vx = *reinterpret_cast<const V*>(x + off);
+    V vr = vg;
+    if (ry) vr = *reinterpret_cast<const V*>(ry + off);
+    V o, z;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float gz = vget(vg, i);
+      if (ry) gz = bn_act_grad(gz, vget(vr, i), act);
+      vset(z, i, gz);
+      vset(o, i, bwd_elem(gz, vget(vx, i), 1.f, false, k[i]));
+    }
+    if (gx) *reinterpret_cast<V*>(gx + off) = o;
+    if (gzo) *reinterpret_cast<V*>(gzo + off) = z;
+  }
+}
+
+// apply-pass grid: (cblocks, chunks of about 8 rows per thread)
+static dim3 nhwc_apply_grid(const NhwcSplit& sp, int64_t& rows_per_chunk) {
+  rows_per_chunk = 8 * (int64_t)sp.rl;
+  int64_t chunks = cdiv(sp.rows, rows_per_chunk);
+  if (chunks > 65535) {
+    chunks = 65535;
+    rows_per_chunk = cdiv(sp.rows, chunks);
+  }
+  return dim3((unsigned)sp.cblocks, (unsigned)chunks);
+}
+
+static bool nhwc_size_ok(int64_t n, int64_t c, int64_t hw) {
+  return bn_size_ok(n, c, hw) && n * hw * c < ((int64_t)1 << 46);
+}
+
+}  // namespace omt
+
+using namespace omt;
+
+// [c][kNhwcMaxSlices][2] double partials, then [c][5] float constants of the input-gradient map
+OMT_EXPORT size_t omt_bn_nhwc_workspace(int64_t n, int64_t c, int64_t hw) {
+  (void)n;
+  (void)hw;
+  return (size_t)(c * kNhwcMaxSlices * 2) * sizeof(double) + (size_t)(c * 5) * sizeof(float);
+}
+
+OMT_EXPORT int omt_bn_train_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
+                                     const float* beta, const float* running_mean, const float* running_var,
+                                     double momentum, double eps, int act, const float* residual, float* y, float* z,
+                                     float* save_mean, float* save_invstd, float* new_rm, float* new_rv,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !gamma || !beta || !y || !save_mean || !save_invstd)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_nhwc: null pointer");
+  if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH)
+    return fail(OMT_INVALID, "omt_bn_train_fwd_nhwc: activation %d", act);
+  if (!nhwc_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_train_fwd_nhwc: size not covered");
+  if (!workspace || workspace_bytes < omt_bn_nhwc_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_train_fwd_nhwc: workspace too small");
+  hipStream_t s = stream_of(stream);
+  const NhwcSplit sp = nhwc_split(n, c, hw, al16(x) && al16(y) && al16(residual) && al16(z));
+  double* part = (double*)workspace;
+  const dim3 sg((unsigned)sp.cblocks, (unsigned)sp.slices);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_nhwc_stats_kernel<4>, sg, dim3(256), 0, s, x, part, (int)c, sp);
+  else
+    hipLaunchKernelGGL(bn_nhwc_stats_kernel<1>, sg, dim3(256), 0, s, x, part, (int)c, sp);
+  if (int st = launch_check("bn_nhwc_stats_kernel")) return st;
+  hipLaunchKernelGGL(bn_nhwc_fin_kernel, dim3((unsigned)cdiv(c, 4)), dim3(256), 0, s, x, (const double*)part, (int)c,
+                     sp.slices, (double)(n * hw), momentum, eps, running_mean, running_var, save_mean, save_invstd,
+                     new_rm, new_rv);
+  if (int st = launch_check("bn_nhwc_fin_kernel")) return st;
+  int64_t rpc;
+  const dim3 ag = nhwc_apply_grid(sp, rpc);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_nhwc_apply_kernel<4>, ag, dim3(256), 0, s, x, save_mean, save_invstd, nullptr, 0.0, gamma,
+                       beta, residual, y, z, (int)c, act, sp, rpc);
+  else
+    hipLaunchKernelGGL(bn_nhwc_apply_kernel<1>, ag, dim3(256), 0, s, x, save_mean, save_invstd, nullptr, 0.0, gamma,
+                       beta, residual, y, z, (int)c, act, sp, rpc);
+  return launch_check("bn_nhwc_apply_kernel");
+}
+
+OMT_EXPORT int omt_bn_eval_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma,
+                                    const float* beta, const float* running_mean, const float* running_var,
+                                    double eps, int act, float* y, void* stream) {
+  if (!x || !gamma || !beta || !running_mean || !running_var || !y)
+    return fail(OMT_INVALID, "omt_bn_eval_fwd_nhwc: null pointer");
+  if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH)
+    return fail(OMT_INVALID, "omt_bn_eval_fwd_nhwc: activation %d", act);
+  if (!nhwc_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_eval_fwd_nhwc: size not covered");
+  hipStream_t s = stream_of(stream);
+  const NhwcSplit sp = nhwc_split(n, c, hw, al16(x) && al16(y));
+  int64_t rpc;
+  const dim3 ag = nhwc_apply_grid(sp, rpc);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_nhwc_apply_kernel<4>, ag, dim3(256), 0, s, x, running_mean, nullptr, running_var, eps, gamma,
+                       beta, nullptr, y, nullptr, (int)c, act, sp, rpc);
+  else
+    hipLaunchKernelGGL(bn_nhwc_apply_kernel<1>, ag, dim3(256), 0, s, x, running_mean, nullptr, running_var, eps, gamma,
+                       beta, nullptr, y, nullptr, (int)c, act, sp, rpc);
+  return launch_check("bn_nhwc_apply_kernel");
+}
+
+OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
+                               int act, const float* act_in, const float* save_mean, const float* save_invstd,
+                               const float* gamma, float* gx, float* dgamma, float* dbeta, float* gz, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (!g || !x || !save_mean || !save_invstd || ((gx || gz) && !gamma) || (act != OMT_ACT_NONE && !act_in))
+    return fail(OMT_INVALID, "omt_bn_bwd_nhwc: null pointer");
+  if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_bwd_nhwc: activation %d", act);
+  if (!nhwc_size_ok(n, c, hw)) return fail(OMT_UNSUPPORTED, "omt_bn_bwd_nhwc: size not covered");
+  if (!workspace || workspace_bytes < omt_bn_nhwc_workspace(n, c, hw))
+    return fail(OMT_INVALID, "omt_bn_bwd_nhwc: workspace too small");
+  hipStream_t s = stream_of(stream);
+  const float* ry = act == OMT_ACT_NONE ? nullptr : act_in;
+  const NhwcSplit sp = nhwc_split(n, c, hw, al16(g) && al16(g2) && al16(x) && al16(ry) && al16(gx) && al16(gz));
+  double* part = (double*)workspace;
+  float* kc = (float*)(part + c * kNhwcMaxSlices * 2);
+  const dim3 pg((unsigned)sp.cblocks, (unsigned)sp.slices);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_nhwc_bwd_part_kernel<4>, pg, dim3(256), 0, s, g, g2, x, ry, save_mean, save_invstd, part,
+                       (int)c, act, sp);
+  else
+    hipLaunchKernelGGL(bn_nhwc_bwd_part_kernel<1>, pg, dim3(256), 0, s, g, g2, x, ry, save_mean, save_invstd, part,
+                       (int)c, act, sp);
+  if (int st = launch_check("bn_nhwc_bwd_part_kernel")) return st;
+  hipLaunchKernelGGL(bn_nhwc_bwd_fin_kernel, dim3((unsigned)cdiv(c, 4)), dim3(256), 0, s, (const double*)part, (int)c,
+                     sp.slices, save_mean, save_invstd, (gx || gz) ? gamma : nullptr, (double)(n * hw), kc, dgamma,
+                     dbeta);
+  if (int st = launch_check("bn_nhwc_bwd_fin_kernel")) return st;
+  if (!gx && !gz) return OMT_OK;
+  int64_t rpc;
+  const dim3 ag = nhwc_apply_grid(sp, rpc);
+  if (sp.vec == 4)
+    hipLaunchKernelGGL(bn_nhwc_bwd_apply_kernel<4>, ag, dim3(256), 0, s, g, g2, x, ry, (const float*)kc, gx, gz,
+                       (int)c, act, sp, rpc);
+  else
+    hipLaunchKernelGGL(bn_nhwc_bwd_apply_kernel<1>, ag, dim3(256), 0, s, g, g2, x, ry, (const float*)kc, gx, gz,
+                       (int)c, act, sp, rpc);
+  return launch_check("bn_nhwc_bwd_apply_kernel");
+}

@@ -305,6 +305,66 @@ __global__ void __launch_bounds__(64) foreach_add_kernel(ForeachTable tab, T val
   for (int64_t i = threadIdx.x; i < n; i += 64) p[i] += value;
 }
 
+
+// ---- operands in different memory orders (NCHW and channels-last NHWC) ----------------------------------------
+// out = op(a, b) over [n][c][hw] tensors whose memory orders differ (each flag: 1 = NHWC); one thread per output
+// element, in the output's order, reading the operand stored the other way at the transposed index.
+template <int OP>
+__global__ void __launch_bounds__(256) pointwise_layouts_kernel(const float* __restrict__ a, int a_nhwc,
+                                                                const float* __restrict__ b, int b_nhwc,
+                                                                float* __restrict__ out, int out_nhwc, int64_t total,
+                                                                int64_t c, int64_t hw, float alpha) {
+  constexpr bool UNARY = OP == OMT_PW_RELU || OP == OMT_PW_HARDSWISH || OP == OMT_PW_HARDSIGMOID ||
+                         OP == OMT_PW_SCALE || OP == OMT_PW_ADD_SCALAR;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    int64_t img, ch, p;
+    if (out_nhwc) {
+      const int64_t pix = i / c;
+      ch = i - pix * c;
+      img = pix / hw;
+      p = pix - img * hw;
+    } else {
+      const int64_t pl = i / hw;
+      p = i - pl * hw;
+      img = pl / c;
+      ch = pl - img * c;
+    }
+    const int64_t nchw = (img * c + ch) * hw + p, nhwc = (img * hw + p) * c + ch;
+    const float va = a[a_nhwc ? nhwc : nchw];
+    const float vb = UNARY ? 0.f : b[b_nhwc ? nhwc : nchw];
+    out[i] = pw_apply<OP>(va, vb, alpha);
+  }
+}
+
+// y[img][ch] = scale * sum over the hw positions of x [n][hw][c] (channels-last planes). Workgroup (channel block,
+// image): thread t owns channel j = block * cb + t % cb and sums positions t / cb, + rl, ... (four loads in flight),
+// then the row lanes' sums are added in lane order: a fixed order.
+__global__ void __launch_bounds__(256) plane_sum_nhwc_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                             int c, int hw, int cb, float scale) {
+  __shared__ float red[256];
+  const int rl = 256 / cb, jl = threadIdx.x % cb, lane = threadIdx.x / cb, j = blockIdx.x * cb + jl;
+  const int64_t img = blockIdx.y;
+  float acc = 0.f;
+  if (lane < rl && j < c) {
+    const float* xp = x + img * hw * (int64_t)c + j;
+    for (int p0 = lane; p0 < hw; p0 += 4 * rl) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = p0 + u * rl < hw ? xp[(int64_t)(p0 + u * rl) * c] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (p0 + u * rl < hw) acc += v[u];
+    }
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if ((int)threadIdx.x < cb && j < c) {
+    float s = 0.f;
+    for (int r = 0; r < rl; ++r) s += red[r * cb + jl];
+    y[img * c + j] = s * scale;
+  }
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <int OP>
@@ -479,4 +539,52 @@ OMT_EXPORT int omt_nll_loss_bwd(int64_t rows, int64_t cols, const float* g, cons
   hipLaunchKernelGGL(nll_bwd_kernel, dim3(grid1d(rows * cols, 256, 8192)), dim3(256), 0, stream_of(stream), g, target,
                      weight, rows, (int)cols, ignore_index, reduction, total_weight, gx);
   return launch_check("nll_bwd_kernel");
+}
+
+OMT_EXPORT int omt_pointwise_layouts(int op, int64_t n, int64_t c, int64_t hw, const float* a, int a_nhwc,
+                                     const float* b, int b_nhwc, float alpha, float* out, int out_nhwc, void* stream) {
+  if (n < 0 || c < 0 || hw < 0) return fail(OMT_INVALID, "omt_pointwise_layouts: size");
+  const int64_t total = n * c * hw;
+  if (total == 0) return OMT_OK;
+  const bool binary = op == OMT_PW_ADD || op == OMT_PW_MUL || op == OMT_PW_THRESHOLD_BWD ||
+                      op == OMT_PW_HARDSWISH_BWD || op == OMT_PW_HARDSIGMOID_BWD;
+  const bool unary = op == OMT_PW_RELU || op == OMT_PW_HARDSWISH || op == OMT_PW_HARDSIGMOID || op == OMT_PW_SCALE ||
+                     op == OMT_PW_ADD_SCALAR;
+  if (!binary && !unary) return fail(OMT_INVALID, "omt_pointwise_layouts: op %d", op);
+  if (!out || !a || (binary && !b)) return fail(OMT_INVALID, "omt_pointwise_layouts: null pointer");
+  hipStream_t s = stream_of(stream);
+  const dim3 grid(grid1d(total, 256, 8192));
+#define OMT_PWL(OP_)                                                                                         \
+  case OP_:                                                                                                  \
+    hipLaunchKernelGGL(pointwise_layouts_kernel<OP_>, grid, dim3(256), 0, s, a, a_nhwc, b, b_nhwc, out,     \
+                       out_nhwc, total, c, hw, alpha);                                                       \
+    break
+  switch (op) {
+    OMT_PWL(OMT_PW_ADD);
+    OMT_PWL(OMT_PW_MUL);
+    OMT_PWL(OMT_PW_RELU);
+    OMT_PWL(OMT_PW_THRESHOLD_BWD);
+    OMT_PWL(OMT_PW_HARDSWISH);
+    OMT_PWL(OMT_PW_HARDSWISH_BWD);
+    OMT_PWL(OMT_PW_HARDSIGMOID);
+    OMT_PWL(OMT_PW_HARDSIGMOID_BWD);
+    OMT_PWL(OMT_PW_SCALE);
+    OMT_PWL(OMT_PW_ADD_SCALAR);
+    default: break;
+  }
+#undef OMT_PWL
+  return launch_check("pointwise_layouts_kernel");
+}
+
+OMT_EXPORT int omt_plane_sum_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, float scale, float* y,
+                                  void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_plane_sum_nhwc: null pointer");
+  if (n < 0 || c < 1 || hw < 0 || hw >= ((int64_t)1 << 31) || c >= ((int64_t)1 << 31) || n > 65535 ||
+      n * c * hw >= ((int64_t)1 << 46))
+    return fail(OMT_INVALID, "omt_plane_sum_nhwc: size");
+  if (n == 0) return OMT_OK;
+  const int cb = (int)(c < 64 ? c : 64);
+  const dim3 grid((unsigned)cdiv(c, cb), (unsigned)n);
+  hipLaunchKernelGGL(plane_sum_nhwc_kernel, grid, dim3(256), 0, stream_of(stream), x, y, (int)c, (int)hw, cb, scale);
+  return launch_check("plane_sum_nhwc_kernel");
 }

@@ -515,6 +515,277 @@ static int max_cover(int64_t len, int64_t n, int64_t k, int64_t s, int64_t p, in
   return (int)best;
 }
 
+
+// ---- channels-last (NHWC) pools ---------------------------------------------------------------------------------
+// x [n][ih][iw][c], outputs [n][oh][ow][c] (indices int64 in the same order); one thread per (pixel, vector of VEC
+// channels: float4 when c % 4 == 0 and the operands are 16-byte aligned), so a wave reads whole runs of channels. The
+// windows, the visiting orders and the max / NaN / tie rules are the NCHW kernels' above, so values, indices (flat
+// in-plane y * iw + x, as PyTorch's channels-last max pool returns them) and sums are the NCHW results transposed,
+// bit for bit.
+template <int VEC>
+struct PoolVec;
+template <>
+struct PoolVec<4> {
+  using T = float4;
+  static __device__ __forceinline__ float get(const float4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+  }
+  static __device__ __forceinline__ void set(float4& v, int i, float f) {
+    if (i == 0) v.x = f; else if (i == 1) v.y = f; else if (i == 2) v.z = f; else v.w = f;
+  }
+};
+template <>
+struct PoolVec<1> {
+  using T = float;
+  static __device__ __forceinline__ float get(const float& v, int) { return v; }
+  static __device__ __forceinline__ void set(float& v, int, float f) { v = f; }
+};
+
+struct NhwcPool {
+  int c, cv;              // channels, channel vectors per pixel
+  FastDiv d_cv, d_w, d_h;  // by cv, and the width and height of the plane a thread's pixel lies in
+};
+
+// (image, row, column, channel vector) of thread index i over planes of W x H pixels
+__device__ __forceinline__ void nhwc_pos(uint32_t i, const NhwcPool& p, int W, int H, int64_t& img, int& y, int& x,
+                                         int& j) {
+  const uint32_t pix = fdiv(i, p.d_cv), t = fdiv(pix, p.d_w), im = fdiv(t, p.d_h);
+  j = (int)(i - pix * (uint32_t)p.cv);
+  x = (int)(pix - t * (uint32_t)W);
+  y = (int)(t - im * (uint32_t)H);
+  img = im;
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) maxpool_fwd_nhwc_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                               int64_t* __restrict__ idx, uint32_t total, PoolGeo g,
+                                                               NhwcPool p) {
+  using PV = PoolVec<VEC>;
+  using V = typename PV::T;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int oy, ox, j;
+    nhwc_pos(i, p, g.ow, g.oh, img, oy, ox, j);
+    float best[VEC];
+    int bi[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) best[e] = -INFINITY, bi[e] = -1;
+    for (int ky = 0; ky < g.kh; ++ky) {
+      const int yy = oy * g.sh - g.ph + ky * g.dh;
+      if (yy < 0 || yy >= g.ih) continue;
+      for (int kx = 0; kx < g.kw; ++kx) {
+        const int xx = ox * g.sw - g.pw + kx * g.dw;
+        if (xx < 0 || xx >= g.iw) continue;
+        const V v = *reinterpret_cast<const V*>(x + ((img * g.ih + yy) * g.iw + xx) * p.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float f = PV::get(v, e);
+          if (bi[e] < 0 || f > best[e] || isnan(f)) {  // first max wins ties; a NaN replaces the running max
+            best[e] = f;
+            bi[e] = yy * g.iw + xx;
+          }
+        }
+      }
+    }
+    const int64_t o = ((img * g.oh + oy) * g.ow + ox) * p.c + (int64_t)j * VEC;
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      PV::set(out, e, best[e]);
+      idx[o + e] = bi[e];
+    }
+    *reinterpret_cast<V*>(y + o) = out;
+  }
+}
+
+// Gather form of maxpool_bwd_kernel: the outputs whose window holds input (iy, ix), visited oy, ox ascending.
+template <int VEC>
+__global__ void __launch_bounds__(256) maxpool_bwd_nhwc_kernel(const float* __restrict__ g,
+                                                               const int64_t* __restrict__ idx,
+                                                               float* __restrict__ gx, uint32_t total, PoolGeo q,
+                                                               NhwcPool p) {
+  using PV = PoolVec<VEC>;
+  using V = typename PV::T;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int yy, xx, j;
+    nhwc_pos(i, p, q.iw, q.ih, img, yy, xx, j);
+    const int64_t me = (int64_t)yy * q.iw + xx;
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int ky = q.kh - 1; ky >= 0; --ky) {
+      const int ty = yy + q.ph - ky * q.dh;
+      if (ty < 0) continue;
+      const int oy = exact_div(ty, q.sh, q.d_sh);
+      if (oy < 0 || oy >= q.oh) continue;
+      for (int kx = q.kw - 1; kx >= 0; --kx) {
+        const int tx = xx + q.pw - kx * q.dw;
+        if (tx < 0) continue;
+        const int ox = exact_div(tx, q.sw, q.d_sw);
+        if (ox < 0 || ox >= q.ow) continue;
+        const int64_t o = ((img * q.oh + oy) * q.ow + ox) * p.c + (int64_t)j * VEC;
+        const V gv = *reinterpret_cast<const V*>(g + o);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          if (idx[o + e] == me) acc[e] += PV::get(gv, e);
+      }
+    }
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) PV::set(out, e, acc[e]);
+    *reinterpret_cast<V*>(gx + ((img * q.ih + yy) * q.iw + xx) * p.c + (int64_t)j * VEC) = out;
+  }
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) avgpool_fwd_nhwc_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                               uint32_t total, PoolGeo g, NhwcPool p,
+                                                               int include_pad, int divisor) {
+  using PV = PoolVec<VEC>;
+  using V = typename PV::T;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int oy, ox, j;
+    nhwc_pos(i, p, g.ow, g.oh, img, oy, ox, j);
+    const int hs = oy * g.sh - g.ph, ws = ox * g.sw - g.pw;
+    const int y0 = max(hs, 0), y1 = min(hs + g.kh, g.ih), x0 = max(ws, 0), x1 = min(ws + g.kw, g.iw);
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int yy = y0; yy < y1; ++yy)
+      for (int xx = x0; xx < x1; ++xx) {
+        const V v = *reinterpret_cast<const V*>(x + ((img * g.ih + yy) * g.iw + xx) * p.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += PV::get(v, e);
+      }
+    const float d = avg_divisor(oy, ox, g, include_pad, divisor);
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) PV::set(out, e, acc[e] / d);
+    *reinterpret_cast<V*>(y + ((img * g.oh + oy) * g.ow + ox) * p.c + (int64_t)j * VEC) = out;
+  }
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) avgpool_bwd_nhwc_kernel(const float* __restrict__ gy, float* __restrict__ gx,
+                                                               uint32_t total, PoolGeo q, NhwcPool p,
+                                                               int include_pad, int divisor) {
+  using PV = PoolVec<VEC>;
+  using V = typename PV::T;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int yy, xx, j;
+    nhwc_pos(i, p, q.iw, q.ih, img, yy, xx, j);
+    const int oy0 = max(0, (yy + q.ph - q.kh + q.sh) / q.sh), oy1 = min(q.oh - 1, (yy + q.ph) / q.sh);
+    const int ox0 = max(0, (xx + q.pw - q.kw + q.sw) / q.sw), ox1 = min(q.ow - 1, (xx + q.pw) / q.sw);
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int oy = oy0; oy <= oy1; ++oy) {
+      const int hs = oy * q.sh - q.ph;
+      if (yy < hs || yy >= hs + q.kh) continue;
+      for (int ox = ox0; ox <= ox1; ++ox) {
+        const int ws = ox * q.sw - q.pw;
+        if (xx < ws || xx >= ws + q.kw) continue;
+        const float d = avg_divisor(oy, ox, q, include_pad, divisor);
+        const V v = *reinterpret_cast<const V*>(gy + ((img * q.oh + oy) * q.ow + ox) * p.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += PV::get(v, e) / d;
+      }
+    }
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) PV::set(out, e, acc[e]);
+    *reinterpret_cast<V*>(gx + ((img * q.ih + yy) * q.iw + xx) * p.c + (int64_t)j * VEC) = out;
+  }
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) adapool_fwd_nhwc_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                               uint32_t total, int ih, int iw, int oh, int ow,
+                                                               NhwcPool p) {
+  using PV = PoolVec<VEC>;
+  using V = typename PV::T;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int oy, ox, j;
+    nhwc_pos(i, p, ow, oh, img, oy, ox, j);
+    const int y0 = bin_lo(oy, ih, oh), y1 = bin_hi(oy, ih, oh), x0 = bin_lo(ox, iw, ow), x1 = bin_hi(ox, iw, ow);
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int yy = y0; yy < y1; ++yy)
+      for (int xx = x0; xx < x1; ++xx) {
+        const V v = *reinterpret_cast<const V*>(x + ((img * ih + yy) * iw + xx) * p.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += PV::get(v, e);
+      }
+    const float d = (float)((y1 - y0) * (x1 - x0));
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) PV::set(out, e, acc[e] / d);
+    *reinterpret_cast<V*>(y + ((img * oh + oy) * ow + ox) * p.c + (int64_t)j * VEC) = out;
+  }
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) adapool_bwd_nhwc_kernel(const float* __restrict__ gy, float* __restrict__ gx,
+                                                               uint32_t total, int ih, int iw, int oh, int ow,
+                                                               NhwcPool p) {
+  using PV = PoolVec<VEC>;
+  using V = typename PV::T;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int yy, xx, j;
+    nhwc_pos(i, p, iw, ih, img, yy, xx, j);
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int oy = 0; oy < oh; ++oy) {
+      const int y0 = bin_lo(oy, ih, oh), y1 = bin_hi(oy, ih, oh);
+      if (yy < y0 || yy >= y1) continue;
+      for (int ox = 0; ox < ow; ++ox) {
+        const int x0 = bin_lo(ox, iw, ow), x1 = bin_hi(ox, iw, ow);
+        if (xx < x0 || xx >= x1) continue;
+        const float d = (float)((y1 - y0) * (x1 - x0));
+        const V v = *reinterpret_cast<const V*>(gy + ((img * oh + oy) * ow + ox) * p.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += PV::get(v, e) / d;
+      }
+    }
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) PV::set(out, e, acc[e]);
+    *reinterpret_cast<V*>(gx + ((img * ih + yy) * iw + xx) * p.c + (int64_t)j * VEC) = out;
+  }
+}
+
+// VEC 4 when c % 4 == 0 and every pointer is 16-byte aligned; the plane (W x H) the threads decompose
+static NhwcPool nhwc_pool(int64_t c, bool aligned, int64_t W, int64_t H) {
+  NhwcPool p;
+  p.c = (int)c;
+  p.cv = (int)((c % 4 == 0 && aligned) ? c / 4 : c);
+  p.d_cv = make_fastdiv((uint32_t)p.cv);
+  p.d_w = make_fastdiv((uint32_t)W);
+  p.d_h = make_fastdiv((uint32_t)H);
+  return p;
+}
+static bool a16(const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; }
+// thread counts (pixels x channel vectors) below 2^31, so a grid-stride step (at most 2^28) never wraps 32 bits
+static bool nhwc_pool_ok(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow) {
+  return n >= 0 && c >= 1 && c < ((int64_t)1 << 24) && pool_ok(n * c, ih, iw, oh, ow) &&
+         n * ih * iw * c < ((int64_t)1 << 31) && n * oh * ow * c < ((int64_t)1 << 31);
+}
+
+#define OMT_NHWC_LAUNCH(K, total, s, vec, ...)                                                               \
+  do {                                                                                                       \
+    if (vec)                                                                                                 \
+      hipLaunchKernelGGL(K<4>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);                      \
+    else                                                                                                     \
+      hipLaunchKernelGGL(K<1>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);                      \
+  } while (0)
+
 }  // namespace omt
 
 using namespace omt;
@@ -661,4 +932,92 @@ OMT_EXPORT int omt_adapool_bwd(int64_t planes, int64_t ih, int64_t iw, int64_t o
   hipLaunchKernelGGL(adapool_bwd_kernel, dim3(grid1d(total, 256)), dim3(256), 0, stream_of(stream), g, gx, total,
                      (int)ih, (int)iw, (int)oh, (int)ow);
   return launch_check("adapool_bwd_kernel");
+}
+
+OMT_EXPORT int omt_maxpool_fwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                                    int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                                    const float* x, float* y, int64_t* idx, void* stream) {
+  if (!x || !y || !idx) return fail(OMT_INVALID, "omt_maxpool_fwd_nhwc: null pointer");
+  if (!nhwc_pool_ok(n, c, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || dh < 1 || dw < 1 || ph < 0 ||
+      pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_maxpool_fwd_nhwc: geometry not covered");
+  const bool vec = c % 4 == 0 && a16(x) && a16(y);
+  const NhwcPool p = nhwc_pool(c, vec, ow, oh);
+  const int64_t total = n * oh * ow * p.cv;
+  if (total == 0) return OMT_OK;
+  OMT_NHWC_LAUNCH(maxpool_fwd_nhwc_kernel, total, stream_of(stream), vec, x, y, idx, (uint32_t)total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw), p);
+  return launch_check("maxpool_fwd_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_maxpool_bwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                                    int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                                    const float* g, const int64_t* idx, float* gx, void* stream) {
+  if (!g || !idx || !gx) return fail(OMT_INVALID, "omt_maxpool_bwd_nhwc: null pointer");
+  if (!nhwc_pool_ok(n, c, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || dh < 1 || dw < 1 || ph < 0 ||
+      pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_maxpool_bwd_nhwc: geometry not covered");
+  const bool vec = c % 4 == 0 && a16(g) && a16(gx);
+  const NhwcPool p = nhwc_pool(c, vec, iw, ih);
+  const int64_t total = n * ih * iw * p.cv;
+  if (total == 0) return OMT_OK;
+  OMT_NHWC_LAUNCH(maxpool_bwd_nhwc_kernel, total, stream_of(stream), vec, g, idx, gx, (uint32_t)total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw), p);
+  return launch_check("maxpool_bwd_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_avgpool_fwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                                    int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad,
+                                    int64_t divisor_override, const float* x, float* y, void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_avgpool_fwd_nhwc: null pointer");
+  if (!nhwc_pool_ok(n, c, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || ph < 0 || pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_avgpool_fwd_nhwc: geometry not covered");
+  const bool vec = c % 4 == 0 && a16(x) && a16(y);
+  const NhwcPool p = nhwc_pool(c, vec, ow, oh);
+  const int64_t total = n * oh * ow * p.cv;
+  if (total == 0) return OMT_OK;
+  OMT_NHWC_LAUNCH(avgpool_fwd_nhwc_kernel, total, stream_of(stream), vec, x, y, (uint32_t)total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), p, count_include_pad, (int)divisor_override);
+  return launch_check("avgpool_fwd_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_avgpool_bwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow, int64_t kh,
+                                    int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int count_include_pad,
+                                    int64_t divisor_override, const float* g, float* gx, void* stream) {
+  if (!g || !gx) return fail(OMT_INVALID, "omt_avgpool_bwd_nhwc: null pointer");
+  if (!nhwc_pool_ok(n, c, ih, iw, oh, ow) || kh < 1 || kw < 1 || sh < 1 || sw < 1 || ph < 0 || pw < 0)
+    return fail(OMT_UNSUPPORTED, "omt_avgpool_bwd_nhwc: geometry not covered");
+  const bool vec = c % 4 == 0 && a16(g) && a16(gx);
+  const NhwcPool p = nhwc_pool(c, vec, iw, ih);
+  const int64_t total = n * ih * iw * p.cv;
+  if (total == 0) return OMT_OK;
+  OMT_NHWC_LAUNCH(avgpool_bwd_nhwc_kernel, total, stream_of(stream), vec, g, gx, (uint32_t)total,
+                  pgeo(ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, 1, 1), p, count_include_pad, (int)divisor_override);
+  return launch_check("avgpool_bwd_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_adapool_fwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow,
+                                    const float* x, float* y, void* stream) {
+  if (!x || !y) return fail(OMT_INVALID, "omt_adapool_fwd_nhwc: null pointer");
+  if (!nhwc_pool_ok(n, c, ih, iw, oh, ow)) return fail(OMT_UNSUPPORTED, "omt_adapool_fwd_nhwc: geometry not covered");
+  const bool vec = c % 4 == 0 && a16(x) && a16(y);
+  const NhwcPool p = nhwc_pool(c, vec, ow, oh);
+  const int64_t total = n * oh * ow * p.cv;
+  if (total == 0) return OMT_OK;
+  OMT_NHWC_LAUNCH(adapool_fwd_nhwc_kernel, total, stream_of(stream), vec, x, y, (uint32_t)total, (int)ih, (int)iw,
+                  (int)oh, (int)ow, p);
+  return launch_check("adapool_fwd_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_adapool_bwd_nhwc(int64_t n, int64_t c, int64_t ih, int64_t iw, int64_t oh, int64_t ow,
+                                    const float* g, float* gx, void* stream) {
+  if (!g || !gx) return fail(OMT_INVALID, "omt_adapool_bwd_nhwc: null pointer");
+  if (!nhwc_pool_ok(n, c, ih, iw, oh, ow)) return fail(OMT_UNSUPPORTED, "omt_adapool_bwd_nhwc: geometry not covered");
+  const bool vec = c % 4 == 0 && a16(g) && a16(gx);
+  const NhwcPool p = nhwc_pool(c, vec, iw, ih);
+  const int64_t total = n * ih * iw * p.cv;
+  if (total == 0) return OMT_OK;
+  OMT_NHWC_LAUNCH(adapool_bwd_nhwc_kernel, total, stream_of(stream), vec, g, gx, (uint32_t)total, (int)ih, (int)iw,
+                  (int)oh, (int)ow, p);
+  return launch_check("adapool_bwd_nhwc_kernel");
 }

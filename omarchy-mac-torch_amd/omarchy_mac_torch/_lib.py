@@ -142,10 +142,24 @@ SIGNATURES = {
     "omt_channel_scale": (I32, [I64, I64, VP, VP, VP, VP]),
     "omt_plane_broadcast": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
     "omt_plane_sum": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
+    "omt_plane_sum_nhwc": (I32, [I64, I64, I64, VP, ctypes.c_float, VP, VP]),
+    "omt_pointwise_layouts": (I32, [ctypes.c_int, I64, I64, I64, VP, ctypes.c_int, VP, ctypes.c_int, ctypes.c_float, VP,
+                                    ctypes.c_int, VP]),
     "omt_log_softmax_fwd": (I32, [I64, I64, VP, VP, VP]),
     "omt_log_softmax_bwd": (I32, [I64, I64, VP, VP, VP, VP]),
     "omt_nll_loss_fwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
     "omt_nll_loss_bwd": (I32, [I64, I64, VP, VP, VP, I64, ctypes.c_int, VP, VP, VP]),
+    "omt_bn_nhwc_workspace": (SZ, [I64, I64, I64]),
+    "omt_bn_train_fwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, VP, VP,
+                                    SZ, VP]),
+    "omt_bn_eval_fwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
+    "omt_bn_bwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, I32, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_maxpool_fwd_nhwc": (I32, [I64] * 14 + [VP, VP, VP, VP]),
+    "omt_maxpool_bwd_nhwc": (I32, [I64] * 14 + [VP, VP, VP, VP]),
+    "omt_avgpool_fwd_nhwc": (I32, [I64] * 12 + [I32, I64, VP, VP, VP]),
+    "omt_avgpool_bwd_nhwc": (I32, [I64] * 12 + [I32, I64, VP, VP, VP]),
+    "omt_adapool_fwd_nhwc": (I32, [I64] * 6 + [VP, VP, VP]),
+    "omt_adapool_bwd_nhwc": (I32, [I64] * 6 + [VP, VP, VP]),
     "omt_se_bwd_workspace": (SZ, [I64, I64, I64]),
     "omt_se_fwd": (I32, [I64, I64, I64] + [VP] * 9),
     "omt_se_bwd": (I32, [I64, I64, I64] + [VP] * 12 + [SZ, VP]),

@@ -536,6 +536,156 @@ def adaptive_avg_pool2d_backward(g, x_shape):
     return gx
 
 
+# ---- channels-last (NHWC) BatchNorm, pools and plane sums: tensors of the usual NCHW shapes in torch.channels_last
+# memory order; outputs come back channels_last ----------------------------------------------------------------------
+
+def batch_norm_train_nhwc(x, gamma, beta, running_mean=None, running_var=None, momentum=0.1, eps=1e-5,
+                          act=_lib.OMT_ACT_NONE, residual=None, return_z=False):
+    """Training BatchNorm over channels-last x (omt_bn_train_fwd_nhwc), y = act(bn(x) + residual); running statistics
+    updated in place. Returns (y, save_mean, save_invstd) and, with return_z, the activation's input."""
+    x, residual = _need_cl(x, "x"), _need_cl(residual, "residual")
+    gamma, beta = _need(gamma, "gamma", 1), _need(beta, "beta", 1)
+    n, c, h, w = x.shape
+    y = torch.empty_like(x, memory_format=_CL)
+    z = torch.empty_like(x, memory_format=_CL) if return_z else None
+    sm = torch.empty((c,), device=x.device, dtype=torch.float32)
+    si = torch.empty_like(sm)
+    ws, nb = _workspace(L.omt_bn_nhwc_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_train_fwd_nhwc(n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean),
+                                  _ptr(running_var), momentum, eps, int(act), _ptr(residual), _ptr(y), _ptr(z),
+                                  _ptr(sm), _ptr(si), _ptr(running_mean), _ptr(running_var), _ptr(ws), nb,
+                                  _stream(x.device)), "batch_norm_train_nhwc")
+    return (y, sm, si, z) if return_z else (y, sm, si)
+
+
+def batch_norm_eval_nhwc(x, gamma, beta, running_mean, running_var, eps=1e-5, act=_lib.OMT_ACT_NONE):
+    x = _need_cl(x, "x")
+    n, c, h, w = x.shape
+    y = torch.empty_like(x, memory_format=_CL)
+    check(L.omt_bn_eval_fwd_nhwc(n, c, h * w, _ptr(x), _ptr(_need(gamma, "gamma", 1)), _ptr(_need(beta, "beta", 1)),
+                                 _ptr(_need(running_mean, "rm", 1)), _ptr(_need(running_var, "rv", 1)), eps, int(act),
+                                 _ptr(y), _stream(x.device)), "batch_norm_eval_nhwc")
+    return y
+
+
+def batch_norm_backward_nhwc(g, x, save_mean, save_invstd, gamma, act=_lib.OMT_ACT_NONE, act_in=None, g2=None,
+                             want_gz=False, output_mask=(True, True, True)):
+    """BatchNorm backward over channels-last tensors (omt_bn_bwd_nhwc): gz = (g + g2) through the activation's
+    gradient, then (gx, dgamma, dbeta) of gz, and gz itself when want_gz. Returns (gx, dgamma, dbeta, gz)."""
+    g, x, act_in, g2 = _need_cl(g, "g"), _need_cl(x, "x"), _need_cl(act_in, "act_in"), _need_cl(g2, "g2")
+    n, c, h, w = x.shape
+    gx = torch.empty_like(x, memory_format=_CL) if output_mask[0] else None
+    dg = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[1] else None
+    db = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[2] else None
+    gz = torch.empty_like(x, memory_format=_CL) if want_gz else None
+    ws, nb = _workspace(L.omt_bn_nhwc_workspace(n, c, h * w), x.device)
+    check(L.omt_bn_bwd_nhwc(n, c, h * w, _ptr(g), _ptr(g2), _ptr(x), int(act), _ptr(act_in),
+                            _ptr(_need(save_mean, "mean", 1)), _ptr(_need(save_invstd, "invstd", 1)),
+                            _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg), _ptr(db), _ptr(gz), _ptr(ws), nb,
+                            _stream(x.device)), "batch_norm_backward_nhwc")
+    return gx, dg, db, gz
+
+
+def max_pool2d_nhwc(x, kernel, stride=None, padding=0, dilation=1, ceil_mode=False):
+    x = _need_cl(x, "x")
+    k, s = _pair(kernel), _pair(stride if stride else kernel)
+    p, d = _pair(padding), _pair(dilation)
+    n, c, ih, iw = x.shape
+    oh, ow = pool_out(ih, k[0], s[0], p[0], d[0], ceil_mode), pool_out(iw, k[1], s[1], p[1], d[1], ceil_mode)
+    y = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32, memory_format=_CL)
+    idx = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.int64, memory_format=_CL)
+    check(L.omt_maxpool_fwd_nhwc(n, c, ih, iw, oh, ow, k[0], k[1], s[0], s[1], p[0], p[1], d[0], d[1], _ptr(x),
+                                 _ptr(y), _ptr(idx), _stream(x.device)), "max_pool2d_nhwc")
+    return y, idx
+
+
+def max_pool2d_backward_nhwc(g, x_shape, idx, kernel, stride=None, padding=0, dilation=1):
+    g = _need_cl(g, "g")
+    idx = idx.contiguous(memory_format=_CL)
+    k, s = _pair(kernel), _pair(stride if stride else kernel)
+    p, d = _pair(padding), _pair(dilation)
+    n, c, ih, iw = x_shape
+    gx = torch.empty(tuple(x_shape), device=g.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_maxpool_bwd_nhwc(n, c, ih, iw, g.shape[2], g.shape[3], k[0], k[1], s[0], s[1], p[0], p[1], d[0], d[1],
+                                 _ptr(g), _ptr(idx), _ptr(gx), _stream(g.device)), "max_pool2d_backward_nhwc")
+    return gx
+
+
+def avg_pool2d_nhwc(x, kernel, stride=None, padding=0, ceil_mode=False, count_include_pad=True,
+                    divisor_override=None):
+    x = _need_cl(x, "x")
+    k, s, p = _pair(kernel), _pair(stride if stride else kernel), _pair(padding)
+    n, c, ih, iw = x.shape
+    oh, ow = pool_out(ih, k[0], s[0], p[0], 1, ceil_mode), pool_out(iw, k[1], s[1], p[1], 1, ceil_mode)
+    y = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_avgpool_fwd_nhwc(n, c, ih, iw, oh, ow, k[0], k[1], s[0], s[1], p[0], p[1], int(count_include_pad),
+                                 divisor_override or 0, _ptr(x), _ptr(y), _stream(x.device)), "avg_pool2d_nhwc")
+    return y
+
+
+def avg_pool2d_backward_nhwc(g, x_shape, kernel, stride=None, padding=0, count_include_pad=True,
+                             divisor_override=None):
+    g = _need_cl(g, "g")
+    k, s, p = _pair(kernel), _pair(stride if stride else kernel), _pair(padding)
+    n, c, ih, iw = x_shape
+    gx = torch.empty(tuple(x_shape), device=g.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_avgpool_bwd_nhwc(n, c, ih, iw, g.shape[2], g.shape[3], k[0], k[1], s[0], s[1], p[0], p[1],
+                                 int(count_include_pad), divisor_override or 0, _ptr(g), _ptr(gx), _stream(g.device)),
+          "avg_pool2d_backward_nhwc")
+    return gx
+
+
+def adaptive_avg_pool2d_nhwc(x, output_size):
+    x = _need_cl(x, "x")
+    oh, ow = _pair(output_size)
+    n, c, ih, iw = x.shape
+    y = torch.empty((n, c, oh, ow), device=x.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_adapool_fwd_nhwc(n, c, ih, iw, oh, ow, _ptr(x), _ptr(y), _stream(x.device)),
+          "adaptive_avg_pool2d_nhwc")
+    return y
+
+
+def adaptive_avg_pool2d_backward_nhwc(g, x_shape):
+    g = _need_cl(g, "g")
+    n, c, ih, iw = x_shape
+    gx = torch.empty(tuple(x_shape), device=g.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_adapool_bwd_nhwc(n, c, ih, iw, g.shape[2], g.shape[3], _ptr(g), _ptr(gx), _stream(g.device)),
+          "adaptive_avg_pool2d_backward_nhwc")
+    return gx
+
+
+def plane_sum_nhwc(x, scale=1.0):
+    """scale * the sum of each channels-last plane of x: [n, c] (omt_plane_sum_nhwc)."""
+    x = _need_cl(x, "x")
+    n, c, h, w = x.shape
+    y = torch.empty((n, c), device=x.device, dtype=torch.float32)
+    check(L.omt_plane_sum_nhwc(n, c, h * w, _ptr(x), float(scale), _ptr(y), _stream(x.device)), "plane_sum_nhwc")
+    return y
+
+
+def pointwise_layouts(op, a, b=None, alpha=0.0, out_nhwc=True):
+    """omt_pointwise_layouts: op over two 4-D tensors of one shape, each NCHW-contiguous or channels_last (read in
+    place); the output in channels_last (out_nhwc) or NCHW order."""
+    def order(t):
+        if t is None:
+            return None, 0
+        if not t.is_cuda or t.dtype != torch.float32 or t.dim() != 4:
+            raise TypeError("pointwise_layouts: 4-D float32 tensors on the HIP device expected")
+        if t.is_contiguous():
+            return t, 0
+        if t.is_contiguous(memory_format=_CL):
+            return t, 1
+        return t.contiguous(), 0
+    a, an = order(a)
+    b, bn = order(b)
+    n, c, h, w = a.shape
+    out = torch.empty(a.shape, device=a.device, dtype=torch.float32,
+                      memory_format=_CL if out_nhwc else torch.contiguous_format)
+    check(L.omt_pointwise_layouts(int(op), n, c, h * w, _ptr(a), an, _ptr(b), bn, float(alpha), _ptr(out),
+                                  int(out_nhwc), _stream(a.device)), "pointwise_layouts")
+    return out
+
+
 # ---- pointwise (reference csrc/elementwise.cpp:702-817) ---------------------------------------------------------
 
 def fill_(t, value):

@@ -191,7 +191,10 @@ class FusedSequential(nn.Sequential):
     """The nn.Sequential it replaces (same modules and state_dict), run from a native plan on device tensors."""
 
     def forward(self, x):
-        on_device = x.device.type == DEVICE and x.dtype == torch.float32 and x.dim() == 4
+        # the plans run NCHW: a channels-last input or layer (model.to(memory_format=torch.channels_last)) runs the
+        # layers one by one, on the device's channels-last kernels
+        on_device = (x.device.type == DEVICE and x.dtype == torch.float32 and x.dim() == 4 and x.is_contiguous()
+                     and all(p.is_contiguous() for p in self.parameters()))
         grad = torch.is_grad_enabled()
         if on_device and self.training and grad:
             prog = _program_of(self)

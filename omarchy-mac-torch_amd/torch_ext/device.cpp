@@ -57,8 +57,8 @@ Tensor empty_dev(IntArrayRef size, at::ScalarType dt) {
                                    std::nullopt);
 }
 
-Tensor empty_dev_cl(IntArrayRef size) {
-  return at::detail::empty_generic(size, &g_alloc, c10::DispatchKeySet(c10::DispatchKey::PrivateUse1), at::kFloat,
+Tensor empty_dev_cl(IntArrayRef size, at::ScalarType dt) {
+  return at::detail::empty_generic(size, &g_alloc, c10::DispatchKeySet(c10::DispatchKey::PrivateUse1), dt,
                                    at::MemoryFormat::ChannelsLast);
 }
 
@@ -271,8 +271,14 @@ static Tensor empty_strided(IntArrayRef size, IntArrayRef stride, std::optional<
 }
 
 // copy self -> dst (host <-> device, device <-> device, any dtype, strides and broadcast): torch's HIP copy kernel
-// over aliases
+// over aliases. A device-to-device copy between two memory orders (a layout conversion, e.g. .contiguous() of a
+// channels_last tensor) is counted with the delegated ops when they are counted, under its sizes.
 static Tensor copy_from(const Tensor& self, const Tensor& dst, bool non_blocking) {
+  if (g_count_delegated && is_dev(self) && is_dev(dst) && self.sizes().equals(dst.sizes()) &&
+      !self.strides().equals(dst.strides())) {
+    OMT_LOCK;
+    delegated_counts()["copy_ (layout conversion) " + c10::str(self.sizes())]++;
+  }
   Tensor d = hip_alias(dst);
   d.copy_(hip_alias(self), non_blocking);
   return dst;

@@ -30,8 +30,13 @@ c10::Allocator* allocator();
 inline bool is_dev(const Tensor& t) { return t.defined() && t.device().type() == kDev; }
 inline bool f32(const Tensor& t) { return t.defined() && t.scalar_type() == at::kFloat; }
 Tensor empty_dev(IntArrayRef size, at::ScalarType dt = at::kFloat);
-// float32 device tensor of a 4-D size in channels_last memory order
-Tensor empty_dev_cl(IntArrayRef size);
+// device tensor of a 4-D size in channels_last memory order
+Tensor empty_dev_cl(IntArrayRef size, at::ScalarType dt = at::kFloat);
+// 4-D tensor whose memory is channels-last (NHWC) and not also plain NCHW (with c == 1 or h * w == 1 the two orders
+// are one and the NCHW kernels read it as it is)
+inline bool is_cl(const Tensor& t) {
+  return t.defined() && t.dim() == 4 && !t.is_contiguous() && t.is_contiguous(at::MemoryFormat::ChannelsLast);
+}
 // byte workspace for a C-ABI call (undefined tensor when bytes == 0)
 Tensor workspace(size_t bytes);
 inline void* wsptr(const Tensor& ws) { return ws.defined() ? ws.data_ptr() : nullptr; }

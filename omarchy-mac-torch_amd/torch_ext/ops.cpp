@@ -189,6 +189,54 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
 // batch norm
 // ------------------------------------------------------------------------------------------------------------------
 
+// The channels-last BatchNorm backward (omt_bn_bwd_nhwc): gz = (g + g2) through the activation's gradient (act_in:
+// the ReLU's output or the hardswish's input), the BatchNorm grads of gz, and gz itself when want_gz (a residual
+// branch's gradient). Operands not already channels-last are converted (none are in a channels-last model).
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_backward_cl4(const Tensor& g_, const Tensor* g2_,
+                                                                  const Tensor& x, int act, const Tensor* act_in_,
+                                                                  const Tensor& w, const Tensor& mean,
+                                                                  const Tensor& invstd, std::array<bool, 3> mask,
+                                                                  bool want_gz, const char* what) {
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor g = contig_cl(g_);
+  Tensor g2 = g2_ ? contig_cl(*g2_) : Tensor();
+  Tensor r = act_in_ ? contig_cl(*act_in_) : Tensor();
+  Tensor gx = mask[0] ? empty_dev_cl(x.sizes()) : Tensor();
+  Tensor dg = mask[1] ? empty_dev({c}) : Tensor();
+  Tensor db = mask[2] ? empty_dev({c}) : Tensor();
+  Tensor gz = want_gz ? empty_dev_cl(x.sizes()) : Tensor();
+  Tensor ws = workspace(omt_bn_nhwc_workspace(n, c, hw));
+  check(omt_bn_bwd_nhwc(n, c, hw, fp(g), g2.defined() ? fp(g2) : nullptr, fp(x), act, r.defined() ? fp(r) : nullptr,
+                        fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg), fpm(db), fpm(gz), wsptr(ws), wsbytes(ws),
+                        cur_stream()),
+        what);
+  return {gx, dg, db, gz};
+}
+static std::tuple<Tensor, Tensor, Tensor> bn_backward_cl(const Tensor& g, const Tensor* g2, const Tensor& x, int act,
+                                                         const Tensor* act_in, const Tensor& w, const Tensor& mean,
+                                                         const Tensor& invstd, std::array<bool, 3> mask, bool want_gz,
+                                                         const char* what) {
+  auto r = bn_backward_cl4(g, g2, x, act, act_in, w, mean, invstd, mask, want_gz, what);
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r)};
+}
+// The channels-last training BatchNorm (omt_bn_train_fwd_nhwc): y = act(bn(x) + res), z = its activation's input
+// when want_z; running statistics rm / rv updated into nrm / nrv (which may be them).
+static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_train_cl(const Tensor& x, const Tensor& w, const Tensor& b,
+                                                              const Tensor& rm, const Tensor& rv, const Tensor& nrm,
+                                                              const Tensor& nrv, double mom, double eps, int act,
+                                                              const Tensor* res_, bool want_z, const char* what) {
+  const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+  Tensor res = res_ ? contig_cl(*res_) : Tensor();
+  Tensor y = empty_dev_cl(x.sizes()), sm = empty_dev({c}), si = empty_dev({c});
+  Tensor z = want_z ? empty_dev_cl(x.sizes()) : Tensor();
+  Tensor ws = workspace(omt_bn_nhwc_workspace(n, c, hw));
+  check(omt_bn_train_fwd_nhwc(n, c, hw, fp(x), fp(w), fp(b), fp(rm), fp(rv), mom, eps, act,
+                              res.defined() ? fp(res) : nullptr, fpm(y), fpm(z), fpm(sm), fpm(si), fpm(nrm), fpm(nrv),
+                              wsptr(ws), wsbytes(ws), cur_stream()),
+        what);
+  return {y, sm, si, z};
+}
+
 static std::tuple<Tensor, Tensor, Tensor> batch_norm_(const Tensor& x_, const std::optional<Tensor>& weight,
                                                       const std::optional<Tensor>& bias,
                                                       const std::optional<Tensor>& rm,
@@ -197,6 +245,23 @@ static std::tuple<Tensor, Tensor, Tensor> batch_norm_(const Tensor& x_, const st
   cover(defined(weight) && defined(bias) && defined(rm) && defined(rv) && f32(x_) && x_.dim() == 4,
        "batch norm without affine parameters or running stats, or not 4-D float32");
   cover(whole(*weight) && whole(*bias) && whole(*rm) && whole(*rv), "batch norm parameters must be contiguous float32");
+  if (is_cl(x_)) {  // channels-last input: the NHWC kernels, a channels-last output
+    const int64_t n = x_.size(0), c = x_.size(1), hw = x_.size(2) * x_.size(3);
+    Tensor y = empty_dev_cl(x_.sizes());
+    if (!training) {
+      check(omt_bn_eval_fwd_nhwc(n, c, hw, fp(x_), fp(weight), fp(bias), fp(rm), fp(rv), eps, 0, fpm(y), cur_stream()),
+            "native_batch_norm (eval, channels last)");
+      return {y, empty_dev({0}), empty_dev({0})};
+    }
+    Tensor sm = empty_dev({c}), si = empty_dev({c});
+    Tensor ws = workspace(omt_bn_nhwc_workspace(n, c, hw));
+    float* rmp = rm->mutable_data_ptr<float>();
+    float* rvp = rv->mutable_data_ptr<float>();
+    check(omt_bn_train_fwd_nhwc(n, c, hw, fp(x_), fp(weight), fp(bias), rmp, rvp, momentum, eps, 0, nullptr, fpm(y),
+                                nullptr, fpm(sm), fpm(si), rmp, rvp, wsptr(ws), wsbytes(ws), cur_stream()),
+          "native_batch_norm (channels last)");
+    return {y, sm, si};
+  }
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor y = empty_dev(x.sizes());
@@ -225,6 +290,8 @@ static std::tuple<Tensor, Tensor, Tensor> batch_norm_backward_(const Tensor& gy_
   cover(train && defined(weight) && defined(sm) && defined(si) && f32(x_) && f32(gy_) && x_.dim() == 4,
        "eval-mode or non-affine batch norm backward");
   cover(whole(*weight) && whole(*sm) && whole(*si), "contiguous float32 parameters");
+  if (is_cl(x_)) return bn_backward_cl(gy_, nullptr, x_, OMT_ACT_NONE, nullptr, *weight, *sm, *si, mask, false,
+                                       "native_batch_norm_backward (channels last)");
   Tensor gy = contig(gy_), x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
@@ -278,6 +345,17 @@ static std::tuple<Tensor, Tensor> max_pool2d_(const Tensor& x_, IntArrayRef k, I
                                               IntArrayRef d, bool ceil) {
   cover(f32(x_) && x_.dim() == 4, "4-D float32");
   Pool2 a = pool_args(k, s, p, d);
+  if (is_cl(x_)) {  // channels-last input and outputs
+    const int64_t n = x_.size(0), c = x_.size(1), ih = x_.size(2), iw = x_.size(3);
+    const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, a.dh, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, a.dw, ceil);
+    cover(oh >= 1 && ow >= 1, "empty output");
+    Tensor y = empty_dev_cl({n, c, oh, ow}), idx = empty_dev_cl({n, c, oh, ow}, at::kLong);
+    const int st = omt_maxpool_fwd_nhwc(n, c, ih, iw, oh, ow, a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, a.dh, a.dw, fp(x_),
+                                        fpm(y), idx.mutable_data_ptr<int64_t>(), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last pool size");
+    check(st, "max_pool2d_with_indices (channels last)");
+    return {y, idx};
+  }
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
   const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, a.dh, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, a.dw, ceil);
@@ -293,8 +371,19 @@ static Tensor max_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayR
                                    IntArrayRef d, bool, const Tensor& idx_) {
   cover(f32(gy_) && x.dim() == 4 && idx_.scalar_type() == at::kLong, "4-D float32");
   Pool2 a = pool_args(k, s, p, d);
-  Tensor gy = contig(gy_), idx = contig(idx_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
+  if (is_cl(x)) {
+    Tensor gy = contig_cl(gy_), idx = idx_.is_contiguous(at::MemoryFormat::ChannelsLast)
+                                          ? idx_
+                                          : idx_.contiguous(at::MemoryFormat::ChannelsLast);
+    Tensor gx = empty_dev_cl(x.sizes());
+    const int st = omt_maxpool_bwd_nhwc(n, c, ih, iw, gy.size(2), gy.size(3), a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, a.dh,
+                                        a.dw, fp(gy), idx.data_ptr<int64_t>(), fpm(gx), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last pool size");
+    check(st, "max_pool2d_with_indices_backward (channels last)");
+    return gx;
+  }
+  Tensor gy = contig(gy_), idx = contig(idx_);
   Tensor gx = empty_dev(x.sizes());
   check(omt_maxpool_bwd(n * c, ih, iw, gy.size(2), gy.size(3), a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, a.dh, a.dw, fp(gy),
                         idx.data_ptr<int64_t>(), fpm(gx), cur_stream()),
@@ -308,6 +397,17 @@ static Tensor avg_pool2d_(const Tensor& x_, IntArrayRef k, IntArrayRef s, IntArr
   cover(!div || *div > 0, "divisor_override");
   Pool2 a = pool_args(k, s, p, {});
   cover(a.ph <= a.kh / 2 && a.pw <= a.kw / 2, "pooling arguments");
+  if (is_cl(x_)) {
+    const int64_t n = x_.size(0), c = x_.size(1), ih = x_.size(2), iw = x_.size(3);
+    const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, 1, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, 1, ceil);
+    cover(oh >= 1 && ow >= 1, "empty output");
+    Tensor y = empty_dev_cl({n, c, oh, ow});
+    const int st = omt_avgpool_fwd_nhwc(n, c, ih, iw, oh, ow, a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, incl ? 1 : 0,
+                                        div.value_or(0), fp(x_), fpm(y), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last pool size");
+    check(st, "avg_pool2d (channels last)");
+    return y;
+  }
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
   const int64_t oh = pool_out(ih, a.kh, a.sh, a.ph, 1, ceil), ow = pool_out(iw, a.kw, a.sw, a.pw, 1, ceil);
@@ -324,8 +424,17 @@ static Tensor avg_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayR
   cover(f32(gy_) && x.dim() == 4, "4-D float32");
   cover(!div || *div > 0, "divisor_override");
   Pool2 a = pool_args(k, s, p, {});
-  Tensor gy = contig(gy_);
   const int64_t n = x.size(0), c = x.size(1), ih = x.size(2), iw = x.size(3);
+  if (is_cl(x)) {
+    Tensor gy = contig_cl(gy_);
+    Tensor gx = empty_dev_cl(x.sizes());
+    const int st = omt_avgpool_bwd_nhwc(n, c, ih, iw, gy.size(2), gy.size(3), a.kh, a.kw, a.sh, a.sw, a.ph, a.pw,
+                                        incl ? 1 : 0, div.value_or(0), fp(gy), fpm(gx), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last pool size");
+    check(st, "avg_pool2d_backward (channels last)");
+    return gx;
+  }
+  Tensor gy = contig(gy_);
   Tensor gx = empty_dev(x.sizes());
   check(omt_avgpool_bwd(n * c, ih, iw, gy.size(2), gy.size(3), a.kh, a.kw, a.sh, a.sw, a.ph, a.pw, incl ? 1 : 0,
                         div.value_or(0), fp(gy), fpm(gx), cur_stream()),
@@ -335,6 +444,14 @@ static Tensor avg_pool2d_backward_(const Tensor& gy_, const Tensor& x, IntArrayR
 
 static Tensor adaptive_avg_pool2d_(const Tensor& x_, IntArrayRef out) {
   cover(f32(x_) && x_.dim() == 4 && out.size() == 2 && out[0] >= 1 && out[1] >= 1, "4-D float32");
+  if (is_cl(x_)) {
+    const int64_t n = x_.size(0), c = x_.size(1);
+    Tensor y = empty_dev_cl({n, c, out[0], out[1]});
+    const int st = omt_adapool_fwd_nhwc(n, c, x_.size(2), x_.size(3), out[0], out[1], fp(x_), fpm(y), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last pool size");
+    check(st, "_adaptive_avg_pool2d (channels last)");
+    return y;
+  }
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1);
   Tensor y = empty_dev({n, c, out[0], out[1]});
@@ -345,6 +462,15 @@ static Tensor adaptive_avg_pool2d_(const Tensor& x_, IntArrayRef out) {
 
 static Tensor adaptive_avg_pool2d_backward_(const Tensor& gy_, const Tensor& x) {
   cover(f32(gy_) && x.dim() == 4, "4-D float32");
+  if (is_cl(x)) {
+    Tensor gy = contig_cl(gy_);
+    Tensor gx = empty_dev_cl(x.sizes());
+    const int st = omt_adapool_bwd_nhwc(x.size(0), x.size(1), x.size(2), x.size(3), gy.size(2), gy.size(3), fp(gy),
+                                        fpm(gx), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last pool size");
+    check(st, "_adaptive_avg_pool2d_backward (channels last)");
+    return gx;
+  }
   Tensor gy = contig(gy_);
   Tensor gx = empty_dev(x.sizes());
   check(omt_adapool_bwd(x.size(0) * x.size(1), x.size(2), x.size(3), gy.size(2), gy.size(3), fp(gy), fpm(gx),
@@ -466,6 +592,13 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_relu_train_dev(cons
                                                                           const Tensor& rv, double mom, double eps) {
   cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
        "4-D float32 with contiguous parameters");
+  if (is_cl(x_)) {
+    const int64_t c = x_.size(1);
+    Tensor nrm = empty_dev({c}), nrv = empty_dev({c});
+    auto r = bn_train_cl(x_, w, b, rm, rv, nrm, nrv, mom, eps, OMT_ACT_RELU, nullptr, false,
+                         "omt::bn_relu_train (channels last)");
+    return {std::get<0>(r), std::get<1>(r), std::get<2>(r), nrm, nrv};
+  }
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor y = empty_dev(x.sizes()), sm = empty_dev({c}), si = empty_dev({c}), nrm = empty_dev({c}), nrv = empty_dev({c});
@@ -484,12 +617,13 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_train_inplace_dev(const Ten
   cover(act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH, "activation none, ReLU or hardswish");
   cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
        "4-D float32 with contiguous parameters");
+  cover(!defined(res_) || (f32(*res_) && res_->sizes() == x_.sizes()), "residual of the input's shape");
+  if (is_cl(x_))
+    return bn_train_cl(x_, w, b, rm, rv, rm, rv, mom, eps, (int)act, defined(res_) ? &*res_ : nullptr,
+                       act == OMT_ACT_HARDSWISH, "omt::bn_train_ (channels last)");
   Tensor x = contig(x_);
   Tensor res;
-  if (defined(res_)) {
-    cover(f32(*res_) && res_->sizes() == x.sizes(), "residual of the input's shape");
-    res = contig(*res_);
-  }
+  if (defined(res_)) res = contig(*res_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor y = empty_dev(x.sizes()), sm = empty_dev({c}), si = empty_dev({c});
   Tensor z = act == OMT_ACT_HARDSWISH ? empty_dev(x.sizes()) : Tensor();
@@ -580,6 +714,9 @@ static std::tuple<Tensor, Tensor, Tensor> bn_relu_backward_dev(const Tensor& g_,
                                                                const Tensor& w, const Tensor& mean,
                                                                const Tensor& invstd, std::array<bool, 3> mask) {
   cover(f32(g_) && f32(x_) && f32(y_) && x_.dim() == 4 && whole(w) && whole(mean) && whole(invstd), "4-D float32");
+  if (is_cl(x_))
+    return bn_backward_cl(g_, nullptr, x_, OMT_ACT_RELU, &y_, w, mean, invstd, mask, false,
+                          "omt::bn_relu_backward (channels last)");
   Tensor g = contig(g_), x = contig(x_), y = contig(y_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
@@ -599,6 +736,9 @@ static std::tuple<Tensor, Tensor, Tensor> bn_act_backward_dev(const Tensor& g_, 
   cover(f32(g_) && f32(x_) && f32(r_) && x_.dim() == 4 && g_.sizes() == x_.sizes() && r_.sizes() == x_.sizes() &&
             whole(w) && whole(mean) && whole(invstd),
         "4-D float32 operands of one shape");
+  if (is_cl(x_))
+    return bn_backward_cl(g_, nullptr, x_, (int)act, act == OMT_ACT_NONE ? nullptr : &r_, w, mean, invstd, mask,
+                          false, "omt::bn_act_backward (channels last)");
   Tensor g = contig(g_), x = contig(x_), r = contig(r_);
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
   Tensor gx = mask[0] ? empty_dev(x.sizes()) : Tensor();
@@ -622,6 +762,9 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_relu_res_backward_dev(const
             g_.sizes() == x_.sizes() && y_.sizes() == x_.sizes() &&
             (!defined(g2_) || (f32(*g2_) && g2_->sizes() == x_.sizes())),
         "4-D float32 operands of one shape");
+  if (is_cl(x_))
+    return bn_backward_cl4(g_, defined(g2_) ? &*g2_ : nullptr, x_, OMT_ACT_RELU, &y_, w, mean, invstd, mask, true,
+                           "omt::bn_relu_res_backward (channels last)");
   Tensor g = contig(g_), x = contig(x_), y = contig(y_);
   Tensor g2 = defined(g2_) ? contig(*g2_) : Tensor();
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
@@ -644,6 +787,12 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> bn_train_pool_dev(cons
   cover(f32(x_) && x_.dim() == 4 && whole(w) && whole(b) && whole(rm) && whole(rv),
         "4-D float32 with contiguous parameters");
   cover(kernel.size() == 2 && stride.size() == 2 && padding.size() == 2, "2-D pooling window");
+  if (is_cl(x_)) {  // channels-last: the NHWC BatchNorm, then the NHWC max pool of its output
+    auto r = bn_train_cl(x_, w, b, rm, rv, rm, rv, mom, eps, (int)act, nullptr, false,
+                         "omt::bn_train_pool_ (channels last)");
+    auto mp = max_pool2d_(std::get<0>(r), kernel, stride, padding, {1, 1}, false);
+    return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<0>(mp), std::get<1>(mp)};
+  }
   Tensor x = contig(x_);
   const int64_t n = x.size(0), c = x.size(1), h = x.size(2), wd = x.size(3);
   const int64_t kh = kernel[0], kw = kernel[1], sh = stride[0], sw = stride[1], ph = padding[0], pw = padding[1];

@@ -9,7 +9,11 @@
 namespace omt {
 namespace {
 
-bool dev_f32c(const Tensor& t) { return is_dev(t) && f32(t) && t.is_contiguous(); }
+// one dense float32 block on the device, NCHW-contiguous or channels-last (a channels-last model's filters, their
+// gradients and optimizer states): the kernels run elementwise over the memory, so every tensor of one parameter
+// must share the parameter's memory order (ordered_like)
+bool dev_f32c(const Tensor& t) { return is_dev(t) && f32(t) && (t.is_contiguous() || is_cl(t)); }
+bool ordered_like(const Tensor& t, const Tensor& p) { return dev_f32c(t) && is_cl(t) == is_cl(p); }
 
 // learning rate: a value, or a float on the device (read by the kernel, so a captured graph sees its updates); a
 // host tensor is read here
@@ -43,11 +47,12 @@ void adam_impl(at::TensorList p, at::TensorList g, at::TensorList m, at::TensorL
        "tensor lists of one length");
   std::vector<omt_adam_tensor> ts(n);
   for (size_t i = 0; i < n; ++i) {
-    cover(dev_f32c(p[i]) && dev_f32c(g[i]) && dev_f32c(m[i]) && dev_f32c(v[i]), "contiguous float32 device tensors");
+    cover(dev_f32c(p[i]) && ordered_like(g[i], p[i]) && ordered_like(m[i], p[i]) && ordered_like(v[i], p[i]),
+          "contiguous float32 device tensors");
     const int64_t k = p[i].numel();
     cover(g[i].numel() == k && m[i].numel() == k && v[i].numel() == k, "matching tensor sizes");
     cover(is_dev(steps[i]) && f32(steps[i]) && steps[i].numel() == 1, "float32 step counts on the device");
-    if (amsgrad) cover(dev_f32c(vmax[i]) && vmax[i].numel() == k, "contiguous float32 max_exp_avg_sqs");
+    if (amsgrad) cover(ordered_like(vmax[i], p[i]) && vmax[i].numel() == k, "contiguous float32 max_exp_avg_sqs");
     ts[i] = omt_adam_tensor{fpm(p[i]), fpm(g[i]), fpm(m[i]), fpm(v[i]), amsgrad ? fpm(vmax[i]) : nullptr,
                             fp(steps[i]), k};
   }
@@ -68,8 +73,10 @@ void sgd_impl(at::TensorList p, at::TensorList g, at::TensorList bufs, double wd
   cover(g.size() == n && (!mom || bufs.size() == n), "tensor lists of one length");
   std::vector<omt_sgd_tensor> ts(n);
   for (size_t i = 0; i < n; ++i) {
-    cover(dev_f32c(p[i]) && dev_f32c(g[i]) && g[i].numel() == p[i].numel(), "contiguous float32 device tensors");
-    if (mom) cover(dev_f32c(bufs[i]) && bufs[i].numel() == p[i].numel(), "contiguous float32 momentum buffers");
+    cover(dev_f32c(p[i]) && ordered_like(g[i], p[i]) && g[i].numel() == p[i].numel(),
+          "contiguous float32 device tensors");
+    if (mom)
+      cover(ordered_like(bufs[i], p[i]) && bufs[i].numel() == p[i].numel(), "contiguous float32 momentum buffers");
     ts[i] = omt_sgd_tensor{fpm(p[i]), fpm(g[i]), mom ? fpm(bufs[i]) : nullptr, p[i].numel()};
   }
   const Lr l = lr_of(lr);

@@ -12,8 +12,20 @@ namespace omt {
 
 namespace {
 
+// contiguous NCHW float32 (the order-dependent ops: planes, rows, channel scales)
 bool dense(const Tensor& t) { return is_dev(t) && f32(t) && t.is_contiguous(); }
 bool same(const Tensor& a, const Tensor& b) { return dense(a) && dense(b) && a.sizes().equals(b.sizes()); }
+// one dense block in NCHW or channels-last order (elementwise ops, which run over the memory in its own order)
+bool flat(const Tensor& t) { return is_dev(t) && f32(t) && (t.is_contiguous() || is_cl(t)); }
+Tensor empty_like_dev(const Tensor& t) { return is_cl(t) ? empty_dev_cl(t.sizes()) : empty_dev(t.sizes()); }
+// both flat, one shape, one memory order
+bool same_flat(const Tensor& a, const Tensor& b) {
+  return flat(a) && flat(b) && a.sizes().equals(b.sizes()) && is_cl(a) == is_cl(b);
+}
+// one shape, 4-D, one operand NCHW and the other channels-last
+bool mixed_flat(const Tensor& a, const Tensor& b) {
+  return flat(a) && flat(b) && a.dim() == 4 && a.sizes().equals(b.sizes()) && is_cl(a) != is_cl(b);
+}
 // a 0-dim CPU tensor: a Python number the dispatcher wrapped, or a host scalar
 bool host_scalar(const Tensor& t) { return t.defined() && t.dim() == 0 && t.device().is_cpu(); }
 
@@ -23,19 +35,29 @@ void pw(int op, const Tensor& a, const Tensor* b, float alpha, const Tensor& out
         "pointwise");
 }
 Tensor unary(int op, const Tensor& x, float alpha = 0.f) {
-  cover(dense(x), "contiguous float32");
-  Tensor y = empty_dev(x.sizes());
+  cover(flat(x), "contiguous float32");
+  Tensor y = empty_like_dev(x);
   pw(op, x, nullptr, alpha, y);
   return y;
 }
 Tensor& unary_(int op, Tensor& x) {
-  cover(dense(x), "contiguous float32");
+  cover(flat(x), "contiguous float32");
   pw(op, x, nullptr, 0.f, x);
   return x;
 }
+// Operands in one memory order run over the memory as it is. An NCHW operand meeting a channels-last one (a
+// channels-last model's global-average-pool gradient, broadcast over its planes, meeting the ReLU mask) runs the
+// mixed-order kernel, its output channels-last, so the model stays channels-last without a conversion.
 Tensor binary(int op, const Tensor& a, const Tensor& b, float alpha = 0.f) {
-  cover(same(a, b), "contiguous float32 operands of one shape");
-  Tensor y = empty_dev(a.sizes());
+  if (mixed_flat(a, b)) {
+    Tensor y = empty_dev_cl(a.sizes());
+    check(omt_pointwise_layouts(op, a.size(0), a.size(1), a.size(2) * a.size(3), fp(a), is_cl(a) ? 1 : 0, fp(b),
+                                is_cl(b) ? 1 : 0, alpha, fpm(y), 1, cur_stream()),
+          "pointwise (mixed memory orders)");
+    return y;
+  }
+  cover(same_flat(a, b), "contiguous float32 operands of one shape");
+  Tensor y = empty_like_dev(a);
   pw(op, a, &b, alpha, y);
   return y;
 }
@@ -64,7 +86,7 @@ void add_small(at::TensorList ts, const at::Scalar& v) {
 
 Tensor add_t(const Tensor& a, const Tensor& b, const at::Scalar& alpha) {
   cover(real(alpha), "real alpha");
-  if (host_scalar(b) && dense(a) && b.is_floating_point())  // a + alpha * b with b a number
+  if (host_scalar(b) && flat(a) && b.is_floating_point())  // a + alpha * b with b a number
     return unary(OMT_PW_ADD_SCALAR, a, (float)(alpha.toDouble() * b.item<double>()));
   return binary(OMT_PW_ADD, a, b, alpha.toFloat());
 }
@@ -75,11 +97,11 @@ Tensor& add_t_(Tensor& a, const Tensor& b, const at::Scalar& alpha) {
       add_small({a}, b.item<int64_t>() * alpha.toLong());
       return a;
     }
-    cover(dense(a), "contiguous float32");
+    cover(flat(a), "contiguous float32");
     pw(OMT_PW_ADD_SCALAR, a, nullptr, (float)(alpha.toDouble() * b.item<double>()), a);
     return a;
   }
-  cover(same(a, b), "contiguous float32, one shape");
+  cover(same_flat(a, b), "contiguous float32, one shape");
   pw(OMT_PW_ADD, a, &b, alpha.toFloat(), a);
   return a;
 }
@@ -89,7 +111,7 @@ Tensor& add_s_(Tensor& a, const at::Scalar& v, const at::Scalar& alpha) {
     add_small({a}, v.toLong() * alpha.toLong());
     return a;
   }
-  cover(dense(a), "contiguous float32");
+  cover(flat(a), "contiguous float32");
   pw(OMT_PW_ADD_SCALAR, a, nullptr, (float)(v.toDouble() * alpha.toDouble()), a);
   return a;
 }
@@ -102,7 +124,7 @@ bool channel_pair(const Tensor& big, const Tensor& s) {
          s.size(1) == big.size(1) && s.size(2) == 1 && s.size(3) == 1 && big.numel() > s.numel();
 }
 Tensor mul_t(const Tensor& a, const Tensor& b) {
-  if (host_scalar(b) && dense(a) && b.is_floating_point()) return unary(OMT_PW_SCALE, a, b.item<float>());
+  if (host_scalar(b) && flat(a) && b.is_floating_point()) return unary(OMT_PW_SCALE, a, b.item<float>());
   const bool ab = channel_pair(a, b), ba = channel_pair(b, a);
   if (ab || ba) {
     const Tensor& big = ab ? a : b;
@@ -123,7 +145,7 @@ Tensor div_t(const Tensor& a, const Tensor& b) {
   const double d = b.item<double>();
   cover(d != 0.0, "non-zero divisor");
   const float inv = (float)(1.0 / d);
-  if (dense(a)) return unary(OMT_PW_SCALE, a, inv);
+  if (flat(a)) return unary(OMT_PW_SCALE, a, inv);
   cover(is_dev(a) && f32(a) && a.dim() == 4 && a.stride(3) == 0 && a.stride(2) == 0 && a.stride(1) == 1 &&
             a.stride(0) == a.size(1),
         "contiguous, or an [N, C] tensor expanded over H x W");
@@ -146,14 +168,14 @@ Tensor hardsigmoid_(const Tensor& x) { return unary(OMT_PW_HARDSIGMOID, x); }
 Tensor& hardsigmoid_ip(Tensor& x) { return unary_(OMT_PW_HARDSIGMOID, x); }
 Tensor hardsigmoid_bwd(const Tensor& g, const Tensor& x) { return binary(OMT_PW_HARDSIGMOID_BWD, g, x); }
 Tensor& fill_s(Tensor& x, const at::Scalar& v) {
-  cover(dense(x) && (v.isFloatingPoint() || v.isIntegral(false)), "contiguous float32");
+  cover(flat(x) && (v.isFloatingPoint() || v.isIntegral(false)), "contiguous float32");
   pw(OMT_PW_FILL, Tensor(), nullptr, v.toFloat(), x);
   return x;
 }
 
 // any contiguous dtype: the bytes are zero (a fill kernel, not a memset node: safe inside a captured graph)
 Tensor& zero_ip(Tensor& x) {
-  cover(is_dev(x) && x.is_contiguous(), "contiguous");
+  cover(is_dev(x) && (x.is_contiguous() || is_cl(x)), "contiguous");
   check(omt_memset_zero(x.data_ptr(), (size_t)x.nbytes(), cur_stream()), "zero_");
   return x;
 }
@@ -173,8 +195,17 @@ std::vector<int64_t> reduced(at::OptionalIntArrayRef dims, int64_t nd) {
 // sum or mean over the last two dims of [N, C, H, W] (scale 1 or 1 / (H W)), or sum over dim 0 of [R, F]
 Tensor plane_or_rows(const Tensor& x, at::OptionalIntArrayRef dims, bool keepdim, std::optional<at::ScalarType> dt,
                      bool mean) {
-  cover(dense(x) && (!dt || *dt == at::kFloat), "contiguous float32");
+  cover((dense(x) || (is_dev(x) && f32(x) && is_cl(x))) && (!dt || *dt == at::kFloat), "contiguous float32");
   const std::vector<int64_t> r = reduced(dims, x.dim());
+  if (is_cl(x)) {  // channels-last planes
+    cover(r == std::vector<int64_t>{2, 3}, "sum / mean over the last two dims");
+    const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
+    cover(hw > 0 && n <= 65535, "non-empty planes, at most 65535 images");
+    Tensor y = keepdim ? empty_dev({n, c, 1, 1}) : empty_dev({n, c});
+    check(omt_plane_sum_nhwc(n, c, hw, fp(x), mean ? 1.f / (float)hw : 1.f, fpm(y), cur_stream()),
+          "sum / mean (channels-last planes)");
+    return y;
+  }
   if (x.dim() == 4 && r == std::vector<int64_t>{2, 3}) {
     const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
     cover(hw > 0, "non-empty planes");

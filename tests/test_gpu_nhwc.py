@@ -278,3 +278,149 @@ def test_channels_last_conv_through_autograd(cuda, case):
         omt._native.core.count_delegated(False)
         omt.FALLBACKS.clear()
         stacks.set_auto_fuse(prev)
+
+
+# ---- channels-last BatchNorm, pools, plane sums and mixed-order pointwise -------------------------------------------
+
+def dev(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+BN_NHWC = [(4, 6, 5, 7), (16, 8, 4, 4), (32, 64, 16, 16), (32, 512, 2, 2), (3, 5, 37, 41), (64, 16, 28, 28),
+           (8, 3, 7, 9), (4, 8, 56, 56), (32, 96, 7, 7), (2, 576, 7, 7), (1, 16, 57, 31), (9, 12, 15, 15),
+           (128, 32, 32, 32), (2, 260, 3, 5)]
+
+
+@pytest.mark.parametrize("n,c,h,w", BN_NHWC, ids=lambda v: str(v))
+def test_batch_norm_nhwc(cuda, ops, n, c, h, w):
+    """omt_bn_train_fwd_nhwc / omt_bn_eval_fwd_nhwc / omt_bn_bwd_nhwc over channels_last tensors (float4 channel runs
+    when c % 4 == 0, scalar otherwise; one and several channel blocks per row) against the oracle (the statistics
+    from inputs of large mean), and against the NCHW kernels on the same data: the statistics agree to float64
+    rounding (rel 1e-6), eval is the same arithmetic bit for bit, and the backward's gz (the gradient through the
+    activation, with a second gradient added) is exact."""
+    from omarchy_mac_torch import _lib
+    rng = np.random.default_rng(n * 7 + c * 3 + h)
+    x = rnd(rng, n, c, h, w) * 3 + 5
+    gam, bet, rm, rv = rnd(rng, c), rnd(rng, c), rnd(rng, c), np.abs(rnd(rng, c)) + 0.5
+    res = rnd(rng, n, c, h, w)
+    z_plain, m_ref, i_ref, nrm, nrv = orc.bn_train(x, gam, bet, rm, rv, 0.1, 1e-5)
+    tg, tb = dev(gam, cuda), dev(bet, cuda)
+    for act in (_lib.OMT_ACT_NONE, _lib.OMT_ACT_RELU, _lib.OMT_ACT_HARDSWISH):
+        r = res if act == _lib.OMT_ACT_RELU else None
+        trm, trv = dev(rm, cuda), dev(rv, cuda)
+        y, sm, si, z = ops.batch_norm_train_nhwc(dev_cl(x, cuda), tg, tb, trm, trv, 0.1, 1e-5, act=act,
+                                                 residual=None if r is None else dev_cl(r, cuda), return_z=True)
+        assert y.is_contiguous(memory_format=CL) and z.is_contiguous(memory_format=CL)
+        z_ref = z_plain + r if r is not None else z_plain
+        assert orc.rel_l2(host(z), z_ref) <= TOL, act
+        assert orc.rel_l2(host(sm), m_ref) <= 1e-6 and orc.rel_l2(host(si), i_ref) <= 1e-5
+        assert orc.rel_l2(host(trm), nrm) <= 1e-6 and orc.rel_l2(host(trv), nrv) <= 1e-6
+        y2, sm2, si2, z2 = ops.batch_norm_train(dev(x, cuda), tg, tb, dev(rm, cuda), dev(rv, cuda), 0.1, 1e-5,
+                                                act=act, residual=None if r is None else dev(r, cuda), return_z=True)
+        assert orc.rel_l2(host(sm), host(sm2)) <= 1e-6 and orc.rel_l2(host(si), host(si2)) <= 1e-6
+        assert orc.rel_l2(host(z), host(z2)) <= 1e-6 and orc.rel_l2(host(y), host(y2)) <= 1e-6
+        tz = torch.from_numpy(host(z))
+        want = {_lib.OMT_ACT_NONE: tz, _lib.OMT_ACT_RELU: torch.relu(tz),
+                _lib.OMT_ACT_HARDSWISH: torch.nn.functional.hardswish(tz)}[act]
+        yd = torch.from_numpy(host(y))
+        assert torch.equal(yd, want) or (act == _lib.OMT_ACT_HARDSWISH and orc.rel_l2(yd.numpy(), want.numpy()) <= 1e-6)
+        # backward through the activation, with a second incoming gradient and gz returned
+        g, g2 = rnd(rng, n, c, h, w), rnd(rng, n, c, h, w)
+        act_in = y if act == _lib.OMT_ACT_RELU else z
+        gx, dg, db, gz = ops.batch_norm_backward_nhwc(dev_cl(g, cuda), dev_cl(x, cuda), sm, si, tg, act=act,
+                                                      act_in=act_in, g2=dev_cl(g2, cuda), want_gz=True)
+        assert gx.is_contiguous(memory_format=CL) and gz.is_contiguous(memory_format=CL)
+        gsum = torch.from_numpy(g + g2)
+        gz_ref = {_lib.OMT_ACT_NONE: gsum, _lib.OMT_ACT_RELU: torch.ops.aten.threshold_backward(gsum, want, 0),
+                  _lib.OMT_ACT_HARDSWISH: torch.ops.aten.hardswish_backward(gsum, tz)}[act].numpy()
+        assert np.array_equal(host(gz), gz_ref) or (act == _lib.OMT_ACT_HARDSWISH and
+                                                     orc.rel_l2(host(gz), gz_ref) <= 1e-6), act
+        gx_ref, dg_ref, db_ref = orc.bn_bwd(gz_ref, x, host(sm), host(si), gam)
+        assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
+        scale = np.linalg.norm(gz_ref.astype(np.float64)) * np.abs(gam * host(si)).max()
+        assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
+        # grads only (no gx, no gz): the apply pass is skipped
+        _, dg3, db3, _ = ops.batch_norm_backward_nhwc(dev_cl(g, cuda), dev_cl(x, cuda), sm, si, tg, act=act,
+                                                      act_in=act_in, g2=dev_cl(g2, cuda),
+                                                      output_mask=(False, True, True))
+        assert torch.equal(dg3.cpu(), dg.cpu()) and torch.equal(db3.cpu(), db.cpu())
+    ye = ops.batch_norm_eval_nhwc(dev_cl(x, cuda), tg, tb, dev(rm, cuda), dev(rv, cuda), 1e-5, act=_lib.OMT_ACT_RELU)
+    ye2 = ops.batch_norm_eval(dev(x, cuda), tg, tb, dev(rm, cuda), dev(rv, cuda), 1e-5, relu=True)
+    assert np.array_equal(host(ye), host(ye2))
+    assert orc.rel_l2(host(ye), orc.bn_eval(x, gam, bet, rm, rv, 1e-5, True)) <= TOL
+
+
+POOL_NHWC = [
+    # (n, c, h, w, kernel, stride, padding, dilation, ceil)
+    (2, 64, 32, 32, 3, 2, 1, 1, False),  # the ResNet stem's pool
+    (4, 16, 16, 16, 2, 2, 0, 1, False),
+    (3, 5, 13, 11, 3, 2, 1, 1, True),    # c % 4 != 0, ceil mode
+    (2, 8, 15, 17, 3, 1, 1, 2, False),   # dilation
+    (2, 12, 9, 9, 4, 3, 2, 1, False),
+]
+
+
+@pytest.mark.parametrize("case", POOL_NHWC, ids=lambda c: "n{}c{}h{}w{}k{}s{}p{}d{}ceil{}".format(*c))
+def test_pools_nhwc_match_nchw_bit_for_bit(cuda, ops, case):
+    """Max pool (with ties and a NaN), average pool (padding counted or not, a divisor override) and adaptive
+    average pool, forward and backward, over channels_last tensors: the NCHW kernels' values and int64 indices
+    transposed, bit for bit (the NCHW kernels are pinned to the oracle in tests/test_gpu_parity.py)."""
+    n, c, h, w, k, s, p, d, ceil = case
+    rng = np.random.default_rng(sum(case[:8]))
+    x = rnd(rng, n, c, h, w)
+    x[0, 0, 0, :4] = 7.0  # ties: the first maximum in row-major order wins
+    x[-1, -1, h // 2, w // 2] = np.nan
+    tx, tcl = dev(x, cuda), dev_cl(x, cuda)
+    y, idx = ops.max_pool2d_nhwc(tcl, k, s, p, d, ceil)
+    y2, idx2 = ops.max_pool2d(tx, k, s, p, d, ceil)
+    assert y.is_contiguous(memory_format=CL) and idx.is_contiguous(memory_format=CL)
+    assert np.array_equal(host(y), host(y2), equal_nan=True)
+    assert np.array_equal(idx.cpu().contiguous().numpy(), idx2.cpu().numpy())
+    gy = rnd(rng, *y2.shape)
+    gx = ops.max_pool2d_backward_nhwc(dev_cl(gy, cuda), x.shape, idx, k, s, p, d)
+    gx2 = ops.max_pool2d_backward(dev(gy, cuda), x.shape, idx2, k, s, p, d)
+    assert gx.is_contiguous(memory_format=CL) and np.array_equal(host(gx), host(gx2))
+    x = rnd(rng, n, c, h, w)
+    tx, tcl = dev(x, cuda), dev_cl(x, cuda)
+    if d == 1 and 2 * p <= k:
+        for incl, div in ((True, None), (False, None), (True, 3)):
+            ya = ops.avg_pool2d_nhwc(tcl, k, s, p, ceil, incl, div)
+            ya2 = ops.avg_pool2d(tx, k, s, p, ceil, incl, div)
+            assert np.array_equal(host(ya), host(ya2)), (incl, div)
+            gy = rnd(rng, *ya2.shape)
+            ga = ops.avg_pool2d_backward_nhwc(dev_cl(gy, cuda), x.shape, k, s, p, incl, div)
+            ga2 = ops.avg_pool2d_backward(dev(gy, cuda), x.shape, k, s, p, incl, div)
+            assert np.array_equal(host(ga), host(ga2)), (incl, div)
+    for out in ((1, 1), (3, 2), (max(1, h // 2), max(1, w // 3))):
+        yd = ops.adaptive_avg_pool2d_nhwc(tcl, out)
+        yd2 = ops.adaptive_avg_pool2d(tx, out)
+        if out != (1, 1) or h * w <= 64:  # larger global pools: the NCHW kernel reduces by wave, in another order
+            assert np.array_equal(host(yd), host(yd2)), out
+        assert orc.rel_l2(host(yd), orc.adapool_fwd(x, *out)) <= 1e-6
+        gy = rnd(rng, n, c, *out)
+        gd = ops.adaptive_avg_pool2d_backward_nhwc(dev_cl(gy, cuda), x.shape)
+        gd2 = ops.adaptive_avg_pool2d_backward(dev(gy, cuda), x.shape)
+        assert np.array_equal(host(gd), host(gd2)), out
+
+
+def test_plane_sum_nhwc_and_mixed_order_pointwise(cuda, ops):
+    """omt_plane_sum_nhwc (a channels_last model's global average pool through mean) against a float64 sum; and
+    omt_pointwise_layouts, an NCHW operand meeting a channels_last one (the pool's broadcast gradient meeting the ReLU
+    mask), equal to PyTorch CPU's op bit for bit with the output in either order."""
+    from omarchy_mac_torch import _lib
+    rng = np.random.default_rng(11)
+    for n, c, h, w in ((32, 512, 2, 2), (4, 96, 7, 7), (2, 3, 56, 56), (5, 70, 9, 11), (3, 300, 1, 2)):
+        x = rnd(rng, n, c, h, w) + 2
+        got = ops.plane_sum_nhwc(dev_cl(x, cuda), 1.0 / (h * w))
+        want = x.astype(np.float64).mean(axis=(2, 3))
+        assert orc.rel_l2(got.cpu().numpy(), want) <= 1e-6, (n, c, h, w)
+    g, y = rnd(rng, 4, 24, 5, 6), rnd(rng, 4, 24, 5, 6)
+    tg, ty = torch.from_numpy(g), torch.from_numpy(y)
+    for out_nhwc in (True, False):
+        out = ops.pointwise_layouts(_lib.OMT_PW_THRESHOLD_BWD, dev(g, cuda), dev_cl(y, cuda), 0.0, out_nhwc)
+        assert out.is_contiguous(memory_format=CL if out_nhwc else torch.contiguous_format)
+        assert torch.equal(out.cpu(), torch.ops.aten.threshold_backward(tg, ty, 0.0))
+        out = ops.pointwise_layouts(_lib.OMT_PW_ADD, dev_cl(g, cuda), dev(y, cuda), 0.5, out_nhwc)
+        assert torch.equal(out.cpu(), torch.add(tg, ty, alpha=0.5))
+        out = ops.pointwise_layouts(_lib.OMT_PW_RELU, dev_cl(g, cuda), None, 0.0, out_nhwc)
+        assert torch.equal(out.cpu(), torch.relu(tg))
