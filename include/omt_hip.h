@@ -236,9 +236,11 @@ int omt_slice_sums(const omt_slice_sum* sums, int count, void* stream);
  * written without a layout change. The reference makes every input contiguous NCHW first (base0,
  * csrc/device.cpp:60-66, before gemm_forward / gemm_grad_input / gemm_grad_weight, csrc/conv.cpp:70-114); these
  * entry points replace that copy and those GEMMs for channels-last callers. Coverage beyond the dense geometry:
- * forward needs ci % 16 == 0, grad input co % 16 == 0, grad weight ci % 4 == 0 and co % 4 == 0 (else
- * OMT_UNSUPPORTED). Plans: directions OMT_DIR_FWD_NHWC, OMT_DIR_DGRAD_NHWC, OMT_DIR_WGRAD_NHWC (tile indices below
- * omt_conv_num_tiles of the direction). Bias and ReLU epilogue bits as in omt_conv_fwd; no BN loader. */
+ * grad input needs co % 16 == 0, grad weight co % 4 == 0 (else OMT_UNSUPPORTED). A forward of ci % 16 != 0 (the
+ * 3-channel stem) gathers element by element on one fixed plan, a grad weight of ci % 4 != 0 loads its columns one
+ * by one: same LDS staging and MFMA order, no tuning of the forward. Plans: directions OMT_DIR_FWD_NHWC,
+ * OMT_DIR_DGRAD_NHWC, OMT_DIR_WGRAD_NHWC (tile indices below omt_conv_num_tiles of the direction). Bias and ReLU
+ * epilogue bits as in omt_conv_fwd; no BN loader. */
 size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g);
 int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias, unsigned epilogue,
                       float* y, void* workspace, size_t workspace_bytes, void* stream);
@@ -398,7 +400,8 @@ int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g_parts, int
 /* Channels-last (NHWC) BatchNorm: x, y, z, residual, g, g2, act_in, gx, gz [n][hw][c] (the memory of a channels_last
  * [n][c][h][w] tensor). Same operations, arguments and statistics as omt_bn_train_fwd_res, omt_bn_eval_fwd and the
  * backward of omt_bn_bwd_act / omt_bn_bwd_res (g2 and gz may be NULL; gz, when set, receives the gradient through
- * the activation, for a residual branch); the shifted float64 sums run in another order than the NCHW kernels', so
+ * the activation, for a residual branch; g_nchw: g alone is in NCHW order, read in place, as a channels-last
+ * model's global-average-pool gradient arrives); the shifted float64 sums run in another order than the NCHW kernels', so
  * the results agree with theirs to float64 rounding. Three launches each way (partial sums, finalize, apply; the
  * backward with gx and gz NULL stops after the finalize); workspace of omt_bn_nhwc_workspace bytes. No counterpart
  * in the reference, which makes every operand contiguous NCHW (csrc/device.cpp:60-66) and runs batch_norm_ /
@@ -411,8 +414,8 @@ int omt_bn_train_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, cons
 int omt_bn_eval_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* gamma, const float* beta,
                          const float* running_mean, const float* running_var, double eps, int act, float* y,
                          void* stream);
-int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x, int act,
-                    const float* act_in, const float* save_mean, const float* save_invstd, const float* gamma,
+int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, int g_nchw, const float* g2, const float* x,
+                    int act, const float* act_in, const float* save_mean, const float* save_invstd, const float* gamma,
                     float* gx, float* dgamma, float* dbeta, float* gz, void* workspace, size_t workspace_bytes,
                     void* stream);
 

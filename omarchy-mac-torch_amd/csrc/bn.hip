@@ -1412,6 +1412,8 @@ struct NhwcSplit {
   int slices;       // row slices of the reductions
   int64_t rows;     // n * hw
   int64_t per_slice;
+  int hw;           // positions per image, and its divider: a row r is image r / hw, position r % hw
+  FastDiv div_hw;
 };
 
 static NhwcSplit nhwc_split(int64_t n, int64_t c, int64_t hw, bool aligned) {
@@ -1427,7 +1429,23 @@ static NhwcSplit nhwc_split(int64_t n, int64_t c, int64_t hw, bool aligned) {
   want = min64(min64(want, by_rows), kNhwcMaxSlices);
   sp.per_slice = cdiv(sp.rows, want);
   sp.slices = (int)cdiv(sp.rows, sp.per_slice);
+  sp.hw = (int)hw;
+  sp.div_hw = make_fastdiv((uint32_t)hw);
   return sp;
+}
+
+// The incoming gradient's VEC channels j VEC .. of row r, from a channels-last g, or (g_nchw) from an NCHW g: a
+// channels-last model's global-average-pool gradient, broadcast over its planes in NCHW order, read in place.
+template <int VEC>
+__device__ __forceinline__ typename VecT<VEC>::T nhwc_grad(const float* __restrict__ g, int g_nchw, int64_t r, int j,
+                                                           int c, const NhwcSplit& sp) {
+  using V = typename VecT<VEC>::T;
+  if (!g_nchw) return *reinterpret_cast<const V*>(g + r * c + (int64_t)j * VEC);
+  const uint32_t img = fdiv((uint32_t)r, sp.div_hw), pos = (uint32_t)r - img * (uint32_t)sp.hw;
+  V v;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) vset(v, i, g[((int64_t)img * c + j * VEC + i) * sp.hw + pos]);
+  return v;
 }
 
 // Row lanes' sums of the block's channels added in lane order: thread t < cb * VEC ends with channel vector t / VEC,
@@ -1571,7 +1589,7 @@ __global__ void __launch_bounds__(256) bn_nhwc_bwd_part_kernel(const float* __re
                                                                const float* __restrict__ mean,
                                                                const float* __restrict__ invstd,
                                                                double* __restrict__ part, int c, int act,
-                                                               const NhwcSplit sp) {
+                                                               const NhwcSplit sp, int g_nchw) {
   using V = typename VecT<VEC>::T;
   const int jl = threadIdx.x % sp.cb, lane = threadIdx.x / sp.cb, j = blockIdx.x * sp.cb + jl;
   const bool on = lane < sp.rl && j < sp.cv;
@@ -1590,7 +1608,7 @@ __global__ void __launch_bounds__(256) bn_nhwc_bwd_part_kernel(const float* __re
       for (int u = 0; u < 4; ++u) {
         if (r + u * step < r1) {
           const int64_t off = (r + u * step) * c + (int64_t)j * VEC;
-          vg[u] = *reinterpret_cast<const V*>(g + off);
+          vg[u] = nhwc_grad<VEC>(g, g_nchw, r + u * step, j, c, sp);
           if (g2) vadd(vg[u], *reinterpret_cast<const V*>(g2 + off));
           vx[u] = *reinterpret_cast<const V*>(x + off);
           if (ry) vr[u] = *reinterpret_cast<const V*>(ry + off);
@@ -1653,7 +1671,8 @@ __global__ void __launch_bounds__(256) bn_nhwc_bwd_apply_kernel(const float* __r
                                                                 const float* __restrict__ ry,
                                                                 const float* __restrict__ kc, float* __restrict__ gx,
                                                                 float* __restrict__ gzo, int c, int act,
-                                                                const NhwcSplit sp, int64_t rows_per_chunk) {
+                                                                const NhwcSplit sp, int64_t rows_per_chunk,
+                                                                int g_nchw) {
   using V = typename VecT<VEC>::T;
   const int jl = threadIdx.x % sp.cb, lane = threadIdx.x / sp.cb, j = blockIdx.x * sp.cb + jl;
   if (lane >= sp.rl || j >= sp.cv) return;
@@ -1665,7 +1684,7 @@ __global__ void __launch_bounds__(256) bn_nhwc_bwd_apply_kernel(const float* __r
   const int64_t r0 = blockIdx.y * rows_per_chunk, r1 = min64(sp.rows, r0 + rows_per_chunk);
   for (int64_t r = r0 + lane; r < r1; r += sp.rl) {
     const int64_t off = r * c + (int64_t)j * VEC;
-    V vg = *reinterpret_cast<const V*>(g + off);
+    V vg = nhwc_grad<VEC>(g, g_nchw, r, j, c, sp);
     if (g2) vadd(vg, *reinterpret_cast<const V*>(g2 + off));
     const V vx = *reinterpret_cast<const V*>(x + off);
     V vr = vg;
@@ -1766,10 +1785,10 @@ OMT_EXPORT int omt_bn_eval_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const floa
   return launch_check("bn_nhwc_apply_kernel");
 }
 
-OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, const float* g2, const float* x,
-                               int act, const float* act_in, const float* save_mean, const float* save_invstd,
-                               const float* gamma, float* gx, float* dgamma, float* dbeta, float* gz, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, int g_nchw, const float* g2,
+                               const float* x, int act, const float* act_in, const float* save_mean,
+                               const float* save_invstd, const float* gamma, float* gx, float* dgamma, float* dbeta,
+                               float* gz, void* workspace, size_t workspace_bytes, void* stream) {
   if (!g || !x || !save_mean || !save_invstd || ((gx || gz) && !gamma) || (act != OMT_ACT_NONE && !act_in))
     return fail(OMT_INVALID, "omt_bn_bwd_nhwc: null pointer");
   if (act < OMT_ACT_NONE || act > OMT_ACT_HARDSWISH) return fail(OMT_INVALID, "omt_bn_bwd_nhwc: activation %d", act);
@@ -1778,16 +1797,17 @@ OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g,
     return fail(OMT_INVALID, "omt_bn_bwd_nhwc: workspace too small");
   hipStream_t s = stream_of(stream);
   const float* ry = act == OMT_ACT_NONE ? nullptr : act_in;
-  const NhwcSplit sp = nhwc_split(n, c, hw, al16(g) && al16(g2) && al16(x) && al16(ry) && al16(gx) && al16(gz));
+  const NhwcSplit sp =
+      nhwc_split(n, c, hw, (g_nchw || al16(g)) && al16(g2) && al16(x) && al16(ry) && al16(gx) && al16(gz));
   double* part = (double*)workspace;
   float* kc = (float*)(part + c * kNhwcMaxSlices * 2);
   const dim3 pg((unsigned)sp.cblocks, (unsigned)sp.slices);
   if (sp.vec == 4)
     hipLaunchKernelGGL(bn_nhwc_bwd_part_kernel<4>, pg, dim3(256), 0, s, g, g2, x, ry, save_mean, save_invstd, part,
-                       (int)c, act, sp);
+                       (int)c, act, sp, g_nchw ? 1 : 0);
   else
     hipLaunchKernelGGL(bn_nhwc_bwd_part_kernel<1>, pg, dim3(256), 0, s, g, g2, x, ry, save_mean, save_invstd, part,
-                       (int)c, act, sp);
+                       (int)c, act, sp, g_nchw ? 1 : 0);
   if (int st = launch_check("bn_nhwc_bwd_part_kernel")) return st;
   hipLaunchKernelGGL(bn_nhwc_bwd_fin_kernel, dim3((unsigned)cdiv(c, 4)), dim3(256), 0, s, (const double*)part, (int)c,
                      sp.slices, save_mean, save_invstd, (gx || gz) ? gamma : nullptr, (double)(n * hw), kc, dgamma,
@@ -1798,9 +1818,9 @@ OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g,
   const dim3 ag = nhwc_apply_grid(sp, rpc);
   if (sp.vec == 4)
     hipLaunchKernelGGL(bn_nhwc_bwd_apply_kernel<4>, ag, dim3(256), 0, s, g, g2, x, ry, (const float*)kc, gx, gz,
-                       (int)c, act, sp, rpc);
+                       (int)c, act, sp, rpc, g_nchw ? 1 : 0);
   else
     hipLaunchKernelGGL(bn_nhwc_bwd_apply_kernel<1>, ag, dim3(256), 0, s, g, g2, x, ry, (const float*)kc, gx, gz,
-                       (int)c, act, sp, rpc);
+                       (int)c, act, sp, rpc, g_nchw ? 1 : 0);
   return launch_check("bn_nhwc_bwd_apply_kernel");
 }

@@ -62,9 +62,11 @@ constexpr int kTileGroup = 8;
 __device__ __forceinline__ float f4get(const float4& v, int s) { return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w; }
 
 // Gather K orders: channel-major (generic), tap-major over a re-packed filter, tap-major reading the filter in place
-// (grad weight uses the first two), and tap-major over a channels-last (NHWC) source, whose K-blocks of channels are
-// contiguous runs of each pixel.
-enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2, kNhwc = 3 };
+// (grad weight uses the first two), tap-major over a channels-last (NHWC) source, whose K-blocks of channels are
+// contiguous runs of each pixel, and tap-major over a channels-last source of too few channels for whole K-blocks
+// (kNhwcNarrow: the ResNet stem's 3; element by element like the generic order, k = (ky, kx, c), which is also the
+// memory order of a channels-last filter).
+enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2, kNhwc = 3, kNhwcNarrow = 4 };
 
 struct Phase {
   int KH, KW, S, PH, PW;  // gather window, stride and (signed) padding
@@ -407,7 +409,8 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       const uint32_t oy = fdiv(r, ph.div_ow), ox = r - oy * (uint32_t)ph.OW;
       iy0 = (int)oy * ph.S - ph.PH;
       ix0 = (int)ox * ph.S - ph.PW;
-      lbase = (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
+      lbase = MODE == kNhwcNarrow ? (uint32_t)((((int)n * H + iy0) * W + ix0) * a.C * 4)
+                                  : (uint32_t)(((int)n * a.C * HW + iy0 * W + ix0) * 4);
     }
   }
   // Channels-last source: thread t loads channels 4 (t % KQN) .. + 3 of each K-block at the NPX tile pixels
@@ -453,7 +456,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   // e / (BK / 4), k 4 (e % (BK / 4)).
   // With the filter read in place (a.wplace) a run is four channels of one tap, w_cst bytes apart: four 4-byte loads
   // whose block-uniform part (first channel, tap) travels in the scalar offset.
-  constexpr bool TAP = MODE != kGeneric;  // tap-major K order
+  constexpr bool TAP = MODE != kGeneric && MODE != kNhwcNarrow;  // tap-major K order in whole K-blocks
   constexpr bool A4 = TAP && BP * BK >= 4 * NT;
   constexpr int AR4 = A4 ? BP * BK / (4 * NT) : 1, KQ = BK / 4;
   uint32_t aoff4[AR4];
@@ -534,6 +537,26 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
       const uint32_t voff = ok ? lbase + (uint32_t)((ky * W + kx) * 4) : kOOB;
 #pragma unroll
       for (int j = 0; j < BR; ++j) rb[set][j] = bload(xr, voff, (uint32_t)((c0 + j) * HW * 4));
+      return;
+    }
+    if constexpr (MODE == kNhwcNarrow) {  // k = (ky, kx, c)
+      const uint32_t kb = (uint32_t)(k0 + rbase);
+      const int tap = (int)fdiv(kb, a.div_c);
+      sc = (int)kb - tap * a.C;
+      sky = (int)fdiv((uint32_t)tap, ph.div_kw);
+      skx = tap - sky * KW;
+#pragma unroll
+      for (int j = 0; j < BR; ++j) {
+        const bool ok = k0 + rbase + j < K && (unsigned)(iy0 + sky) < (unsigned)H && (unsigned)(ix0 + skx) < (unsigned)W;
+        rb[set][j] = bload(xr, ok ? lbase + (uint32_t)(((sky * W + skx) * a.C + sc) * 4) : kOOB, 0);
+        if (++sc == a.C) {
+          sc = 0;
+          if (++skx == KW) {
+            skx = 0;
+            ++sky;
+          }
+        }
+      }
       return;
     }
     {
@@ -662,7 +685,7 @@ __device__ __forceinline__ void gather_tile(const GatherArgs& a, const int bx, c
   }
 
   static_assert(4 * row_epi_floats<WQ>() <= gather_lds_floats<BP, BQ, BK>(), "row epilogue fits the tile's LDS");
-  if constexpr (MODE == kNhwc)
+  if constexpr (MODE == kNhwc || MODE == kNhwcNarrow)
     gather_epilogue_nhwc<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane, zs);
   else if (a.d2s && !a.part)
     d2s_epilogue<TI, TJ, WP, WQ>(a, ph, acc, q0, p0, wp, wq, lane);
@@ -1201,11 +1224,13 @@ __global__ void __launch_bounds__(256, 2) conv_wgrad_kernel(const WgradArgs a) {
 // pixels is staged as rows of k (pitch BP + 16 and BQ + 16 floats: the four lane groups of an MFMA operand read, at
 // rows 4 s + g, fall on disjoint banks), loaded as float4 runs of four co / four ci of one pixel, and the MFMA
 // operands are read one float per lane. Lane group g supplies k = 4 s + g of the block at MFMA step s. Needs
-// C % 4 == 0 (a run of four ci stays inside one tap) and P % 4 == 0.
+// P % 4 == 0, and C % 4 == 0 (a run of four ci stays inside one tap) unless NARROW: then each of a thread's four
+// columns is its own tap and channel (a 3-channel stem's columns cross taps), loaded element by element into the same
+// float4 slot, so the staging and the MFMA order are unchanged.
 template <int BP, int BQ>
 constexpr int wgrad_nhwc_lds_floats() { return 64 * ((BP + 16) + (BQ + 16)); }
 
-template <int BP, int BQ, int WP, int WQ, int PF>
+template <int BP, int BQ, int WP, int WQ, int PF, bool NARROW = false>
 __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx, const int by, const int bz,
                                                 float* __restrict__ lds) {
   constexpr int NT = 256, BK = 64;
@@ -1244,6 +1269,21 @@ __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx
     ky = (int)fdiv((uint32_t)tap, a.div_ks);
     kx = tap - ky * a.KS;
   }
+  // NARROW: column qb + e is tap (eky, ekx), channel eci (eq: inside the filter's columns)
+  int eky[4] = {0, 0, 0, 0}, ekx[4] = {0, 0, 0, 0}, eci[4] = {0, 0, 0, 0};
+  bool eq[4] = {false, false, false, false};
+  if constexpr (NARROW) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      eq[e] = qb + e < Q;
+      if (eq[e]) {
+        const int tap = (int)fdiv((uint32_t)(qb + e), a.div_c);
+        eci[e] = qb + e - tap * C;
+        eky[e] = (int)fdiv((uint32_t)tap, a.div_ks);
+        ekx[e] = tap - eky[e] * a.KS;
+      }
+    }
+  }
 
   // The pixel (n, oy, ox) of each of this thread's x rows, for the next K-block gload reads: decomposed once, then
   // advanced by one block (64 pixels) per call as a mixed-radix addition with one carry per digit.
@@ -1273,10 +1313,21 @@ __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int k = k0 + br + BRW * j;
-      const int iy = roy[j] * a.S - a.PAD + ky, ix = rox[j] * a.S - a.PAD + kx;
-      const bool ok = qok & (k < kend) & ((unsigned)iy < (unsigned)H) & ((unsigned)ix < (unsigned)W);
-      const uint32_t off = (uint32_t)((((rn[j] * H + iy) * W + ix) * C + ci) * 4);
-      rb4[set][j] = bload4(xr, ok ? off : kOOB, 0);
+      if constexpr (NARROW) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int iy = roy[j] * a.S - a.PAD + eky[e], ix = rox[j] * a.S - a.PAD + ekx[e];
+          const bool ok = eq[e] & (k < kend) & ((unsigned)iy < (unsigned)H) & ((unsigned)ix < (unsigned)W);
+          v[e] = bload(xr, ok ? (uint32_t)((((rn[j] * H + iy) * W + ix) * C + eci[e]) * 4) : kOOB, 0);
+        }
+        rb4[set][j] = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        const int iy = roy[j] * a.S - a.PAD + ky, ix = rox[j] * a.S - a.PAD + kx;
+        const bool ok = qok & (k < kend) & ((unsigned)iy < (unsigned)H) & ((unsigned)ix < (unsigned)W);
+        const uint32_t off = (uint32_t)((((rn[j] * H + iy) * W + ix) * C + ci) * 4);
+        rb4[set][j] = bload4(xr, ok ? off : kOOB, 0);
+      }
       // the next block's pixel of this row
       int ox = rox[j] + a.step_ox, oy = roy[j] + a.step_oy, n = rn[j] + a.step_n;
       const int cx = ox >= a.OW;
@@ -1364,11 +1415,11 @@ __device__ __forceinline__ void wgrad_nhwc_tile(const WgradArgs& a, const int bx
   }
 }
 
-template <int BP, int BQ, int WP, int WQ, int PF>
+template <int BP, int BQ, int WP, int WQ, int PF, bool NARROW = false>
 __global__ void __launch_bounds__(256, 2) conv_wgrad_nhwc_kernel(const WgradArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[wgrad_nhwc_lds_floats<BP, BQ>()];
   const TileId t = xcd_block_tile(kTileGroup);
-  wgrad_nhwc_tile<BP, BQ, WP, WQ, PF>(a, t.x, t.y, t.z, lds);
+  wgrad_nhwc_tile<BP, BQ, WP, WQ, PF, NARROW>(a, t.x, t.y, t.z, lds);
 }
 
 // Grad input and grad weight of one convolution in one launch (omt_conv_bwd), both on 64 x 64 tiles: the first
@@ -1969,12 +2020,13 @@ static void wgrad_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s)
   }
 }
 
+template <bool NARROW>
 static void wgrad_nhwc_dispatch(int ti, const WgradArgs& a, dim3 grid, hipStream_t s) {
   switch (ti) {
-    case 0: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<64, 128, 32, 64, 1>), grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<128, 64, 32, 64, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<64, 64, 32, 32, 2>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<32, 128, 16, 64, 2>), grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<64, 128, 32, 64, 1, NARROW>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<128, 64, 32, 64, 1, NARROW>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<64, 64, 32, 32, 2, NARROW>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_wgrad_nhwc_kernel<32, 128, 16, 64, 2, NARROW>), grid, dim3(256), 0, s, a); break;
   }
 }
 
@@ -2779,9 +2831,10 @@ OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* 
 // tap-major [P][K] operand of the forward gather; the grad-input phases re-pack it; grad weight writes its
 // tap-major columns in place. Plans live under their own directions (OMT_DIR_*_NHWC).
 
-static bool nhwc_fwd_ok(const omt_conv_geo* g) { return g->ci % 16 == 0; }
 static bool nhwc_dgrad_ok(const omt_conv_geo* g) { return g->co % 16 == 0; }
-static bool nhwc_wgrad_ok(const omt_conv_geo* g) { return g->ci % 4 == 0 && g->co % 4 == 0; }
+// grad weight: output channels a multiple of 4 (float4 runs of gy); input channels not a multiple of 4 take the
+// element-by-element column loads (NARROW)
+static bool nhwc_wgrad_ok(const omt_conv_geo* g) { return g->co % 4 == 0; }
 
 static GatherPlan fwd_nhwc_plan(const omt_conv_geo* g) {
   omt_conv_plan cp;
@@ -2799,9 +2852,14 @@ static GatherPlan dgrad_nhwc_plan(const omt_conv_geo* g) {
   return gather_plan(g->ci, maxq, maxk, a.nphase, have ? &cp : nullptr, g->co);
 }
 
+// Narrow channels-last forward (input channels not a multiple of 16, e.g. the ResNet stem's 3): one plan, the 64 x 64
+// staged tile gathering element by element (kNhwcNarrow), no K split.
+constexpr int kNarrowTile = 5;
+static bool nhwc_narrow(const omt_conv_geo* g) { return g->ci % 16 != 0; }
+
 // Launches a channels-last gather (and, split over K, its slice sum); `part`: the partials of the plan's size.
 static int run_gather_nhwc(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part,
-                           hipStream_t s) {
+                           hipStream_t s, bool narrow = false) {
   const Tile& tl = gtile(pl.tile);
   a.nhwc = 1;
   a.kslice = (int)pl.kslice;
@@ -2811,23 +2869,29 @@ static int run_gather_nhwc(GatherArgs& a, const GatherPlan& pl, int64_t n, int64
   a.rows = 0;
   a.vec_out = a.P % 4 == 0 && (uintptr_t)a.y % 16 == 0 && (uintptr_t)a.part % 16 == 0;
   const dim3 grid((unsigned)cdiv(maxq, tl.bq), (unsigned)cdiv(a.P, tl.bp), (unsigned)(a.nphase * pl.slices));
-  gather_nhwc_dispatch(pl.tile, a, grid, s);
+  if (narrow)
+    hipLaunchKernelGGL((conv_gather_kernel<64, 64, 32, 32, 16, kNhwcNarrow, false, 2>), grid, dim3(256), 0, s, a);
+  else
+    gather_nhwc_dispatch(pl.tile, a, grid, s);
   if (int st = launch_check("conv_gather_kernel (nhwc)")) return st;
   return launch_gather_sum(gather_sum_of(a, pl), s);
 }
 
 static size_t fwd_nhwc_workspace_one(const omt_conv_geo* g) {
+  if (nhwc_narrow(g)) return 0;
   const GatherPlan pl = fwd_nhwc_plan(g);
   return pl.slices > 1 ? (size_t)(pl.slices * g->n * g->co * g->oh * g->ow) * sizeof(float) : 0;
 }
 
 OMT_EXPORT size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g) {
-  return g && dense_geo_ok(g) && nhwc_fwd_ok(g) ? chunks_max(g, fwd_nhwc_workspace_one) : 0;
+  return g && dense_geo_ok(g) ? chunks_max(g, fwd_nhwc_workspace_one) : 0;
 }
 
 static int conv_fwd_nhwc_one(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
                              unsigned epilogue, float* y, void* workspace, hipStream_t s) {
-  const GatherPlan pl = fwd_nhwc_plan(g);
+  const bool narrow = nhwc_narrow(g);
+  const GatherPlan pl =
+      narrow ? GatherPlan{kNarrowTile, 1, cdiv(g->ci * g->ks * g->ks, 16) * 16} : fwd_nhwc_plan(g);
   GatherArgs a{};
   a.x = x;
   a.w = w;  // [co][ky][kx][ci]: the tap-major [P][K] operand as it is
@@ -2857,7 +2921,7 @@ static int conv_fwd_nhwc_one(const omt_conv_geo* g, const float* x, const float*
   p.div_kk = make_fastdiv((uint32_t)(g->ks * g->ks));
   p.div_kw = make_fastdiv((uint32_t)g->ks);
   a.div_c = make_fastdiv((uint32_t)a.C);
-  return run_gather_nhwc(a, pl, g->n, p.Q, (float*)workspace, s);
+  return run_gather_nhwc(a, pl, g->n, p.Q, (float*)workspace, s, narrow);
 }
 
 OMT_EXPORT int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias,
@@ -2865,7 +2929,6 @@ OMT_EXPORT int omt_conv_fwd_nhwc(const omt_conv_geo* g, const float* x, const fl
   if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: null pointer");
   Chunks ch;
   if (int st = chunk_check(g, "omt_conv_fwd_nhwc", ch)) return st;
-  if (!nhwc_fwd_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_fwd_nhwc: input channels not a multiple of 16");
   if ((epilogue & OMT_EPI_BIAS) && !bias) return fail(OMT_INVALID, "omt_conv_fwd_nhwc: bias epilogue without bias");
   const size_t need = omt_conv_fwd_nhwc_workspace(g);
   if (need && (!workspace || workspace_bytes < need))
@@ -2952,7 +3015,10 @@ static int conv_wgrad_nhwc_one(const omt_conv_geo* g, const float* x, const floa
   WgradArgs a;
   WgradPlan pl;
   const dim3 grid = wgrad_prepare(g, x, gy, gw, workspace, a, pl, OMT_DIR_WGRAD_NHWC);
-  wgrad_nhwc_dispatch(pl.tile, a, grid, s);
+  if (g->ci % 4 == 0)
+    wgrad_nhwc_dispatch<false>(pl.tile, a, grid, s);
+  else
+    wgrad_nhwc_dispatch<true>(pl.tile, a, grid, s);
   if (int st = launch_check("conv_wgrad_nhwc_kernel")) return st;
   return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
 }
@@ -2962,7 +3028,7 @@ OMT_EXPORT int omt_conv_wgrad_nhwc(const omt_conv_geo* g, const float* x, const 
   if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: null pointer");
   Chunks ch;
   if (int st = chunk_check(g, "omt_conv_wgrad_nhwc", ch)) return st;
-  if (!nhwc_wgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad_nhwc: channels not multiples of 4");
+  if (!nhwc_wgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_wgrad_nhwc: output channels not a multiple of 4");
   const size_t need = omt_conv_wgrad_nhwc_workspace(g);
   if (need && (!workspace || workspace_bytes < need))
     return fail(OMT_INVALID, "omt_conv_wgrad_nhwc: workspace of %zu bytes needed", need);

@@ -153,7 +153,7 @@ SIGNATURES = {
     "omt_bn_train_fwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, F64, I32, VP, VP, VP, VP, VP, VP, VP, VP,
                                     SZ, VP]),
     "omt_bn_eval_fwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, VP, VP, F64, I32, VP, VP]),
-    "omt_bn_bwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, I32, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
+    "omt_bn_bwd_nhwc": (I32, [I64, I64, I64, VP, I32, VP, VP, I32, VP, VP, VP, VP, VP, VP, VP, VP, VP, SZ, VP]),
     "omt_maxpool_fwd_nhwc": (I32, [I64] * 14 + [VP, VP, VP, VP]),
     "omt_maxpool_bwd_nhwc": (I32, [I64] * 14 + [VP, VP, VP, VP]),
     "omt_avgpool_fwd_nhwc": (I32, [I64] * 12 + [I32, I64, VP, VP, VP]),

@@ -569,17 +569,19 @@ def batch_norm_eval_nhwc(x, gamma, beta, running_mean, running_var, eps=1e-5, ac
 
 
 def batch_norm_backward_nhwc(g, x, save_mean, save_invstd, gamma, act=_lib.OMT_ACT_NONE, act_in=None, g2=None,
-                             want_gz=False, output_mask=(True, True, True)):
+                             want_gz=False, output_mask=(True, True, True), g_nchw=False):
     """BatchNorm backward over channels-last tensors (omt_bn_bwd_nhwc): gz = (g + g2) through the activation's
-    gradient, then (gx, dgamma, dbeta) of gz, and gz itself when want_gz. Returns (gx, dgamma, dbeta, gz)."""
-    g, x, act_in, g2 = _need_cl(g, "g"), _need_cl(x, "x"), _need_cl(act_in, "act_in"), _need_cl(g2, "g2")
+    gradient, then (gx, dgamma, dbeta) of gz, and gz itself when want_gz. g_nchw: g is read in NCHW order (made
+    contiguous), the rest channels-last. Returns (gx, dgamma, dbeta, gz)."""
+    g = _need(g, "g", 4) if g_nchw else _need_cl(g, "g")
+    x, act_in, g2 = _need_cl(x, "x"), _need_cl(act_in, "act_in"), _need_cl(g2, "g2")
     n, c, h, w = x.shape
     gx = torch.empty_like(x, memory_format=_CL) if output_mask[0] else None
     dg = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[1] else None
     db = torch.empty((c,), device=x.device, dtype=torch.float32) if output_mask[2] else None
     gz = torch.empty_like(x, memory_format=_CL) if want_gz else None
     ws, nb = _workspace(L.omt_bn_nhwc_workspace(n, c, h * w), x.device)
-    check(L.omt_bn_bwd_nhwc(n, c, h * w, _ptr(g), _ptr(g2), _ptr(x), int(act), _ptr(act_in),
+    check(L.omt_bn_bwd_nhwc(n, c, h * w, _ptr(g), int(g_nchw), _ptr(g2), _ptr(x), int(act), _ptr(act_in),
                             _ptr(_need(save_mean, "mean", 1)), _ptr(_need(save_invstd, "invstd", 1)),
                             _ptr(_need(gamma, "gamma", 1)), _ptr(gx), _ptr(dg), _ptr(db), _ptr(gz), _ptr(ws), nb,
                             _stream(x.device)), "batch_norm_backward_nhwc")

@@ -47,12 +47,13 @@ static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::option
   Tensor b = defined(bias) ? contig(*bias) : Tensor();
   const bool cl = kind == OMT_CONV_DENSE && channels_last(x_, w_);
   unsigned epi = (b.defined() ? OMT_EPI_BIAS : 0u) | (relu ? OMT_EPI_RELU : 0u);
-  if (cl && x_.size(1) % 16 == 0) {
+  if (cl) {
     Tensor x = contig_cl(x_), w = contig_cl(w_);
     omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
     cover(g.oh >= 1 && g.ow >= 1, "empty output");
     Tensor y = empty_dev_cl({g.n, g.co, g.oh, g.ow});
-    tune_conv(OMT_DIR_FWD_NHWC, g);
+    // input channels not a multiple of 16 (the 3-channel stem) run one fixed element-by-element gather: nothing to tune
+    if (g.ci % 16 == 0) tune_conv(OMT_DIR_FWD_NHWC, g);
     Tensor ws = workspace(omt_conv_fwd_nhwc_workspace(&g));
     check(omt_conv_fwd_nhwc(&g, fp(x), fp(w), fp(b), epi, fpm(y), wsptr(ws), wsbytes(ws), cur_stream()),
           "convolution (channels last)");
@@ -72,8 +73,7 @@ static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::option
     check(omt_dw_fwd(&g, fp(x), fp(w), fp(b), nullptr, nullptr, nullptr, nullptr, 1e-5f, fpm(y), cur_stream()),
           "convolution (depthwise)");
   }
-  // a channels-last convolution the NHWC kernels do not cover (input channels not a multiple of 16) ran in NCHW
-  return cl ? contig_cl(y) : y;
+  return y;
 }
 
 static Tensor convolution_(const Tensor& x, const Tensor& w, const std::optional<Tensor>& bias, IntArrayRef stride,
@@ -82,7 +82,7 @@ static Tensor convolution_(const Tensor& x, const Tensor& w, const std::optional
 }
 
 // Backward of a channels-last dense convolution: grads in channels-last order, each from the NHWC kernels where they
-// cover it (grad input: co % 16 == 0; grad weight: ci and co multiples of 4), else from the NCHW kernels.
+// cover it (grad input: co % 16 == 0; grad weight: co a multiple of 4), else from the NCHW kernels.
 static std::tuple<Tensor, Tensor, Tensor> conv_backward_cl(const Tensor& gy_, const Tensor& x_, const Tensor& w_,
                                                            IntArrayRef stride, IntArrayRef padding,
                                                            std::array<bool, 3> mask) {
@@ -110,7 +110,7 @@ static std::tuple<Tensor, Tensor, Tensor> conv_backward_cl(const Tensor& gy_, co
     }
   }
   if (mask[1]) {
-    if (g.ci % 4 == 0 && g.co % 4 == 0) {
+    if (g.co % 4 == 0) {
       Tensor x = contig_cl(x_);
       gw = empty_dev_cl(w_.sizes());
       tune_conv(OMT_DIR_WGRAD_NHWC, g);
@@ -126,10 +126,9 @@ static std::tuple<Tensor, Tensor, Tensor> conv_backward_cl(const Tensor& gy_, co
       gw = contig_cl(t);
     }
   }
-  if (mask[2]) {  // the bias-grad kernel sums NCHW planes (one workgroup per channel)
-    Tensor gyc = contig(gy_);
+  if (mask[2]) {  // channels-last gy is [n oh ow][co]: the column sums of those rows
     gb = empty_dev({g.co});
-    check(omt_bias_grad(g.n, g.co, g.oh * g.ow, fp(gyc), fpm(gb), s), "convolution_backward (bias)");
+    check(omt_bias_grad(g.n * g.oh * g.ow, g.co, 1, fp(gy), fpm(gb), s), "convolution_backward (bias)");
   }
   return {gx, gw, gb};
 }
@@ -198,7 +197,9 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_backward_cl4(const Tensor& 
                                                                   const Tensor& invstd, std::array<bool, 3> mask,
                                                                   bool want_gz, const char* what) {
   const int64_t n = x.size(0), c = x.size(1), hw = x.size(2) * x.size(3);
-  Tensor g = contig_cl(g_);
+  // an NCHW g (a global average pool's gradient broadcast over its planes) is read in place
+  const bool g_nchw = hw > 1 && c > 1 && !is_cl(g_) && g_.is_contiguous();
+  Tensor g = g_nchw ? g_ : contig_cl(g_);
   Tensor g2 = g2_ ? contig_cl(*g2_) : Tensor();
   Tensor r = act_in_ ? contig_cl(*act_in_) : Tensor();
   Tensor gx = mask[0] ? empty_dev_cl(x.sizes()) : Tensor();
@@ -206,7 +207,8 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor> bn_backward_cl4(const Tensor& 
   Tensor db = mask[2] ? empty_dev({c}) : Tensor();
   Tensor gz = want_gz ? empty_dev_cl(x.sizes()) : Tensor();
   Tensor ws = workspace(omt_bn_nhwc_workspace(n, c, hw));
-  check(omt_bn_bwd_nhwc(n, c, hw, fp(g), g2.defined() ? fp(g2) : nullptr, fp(x), act, r.defined() ? fp(r) : nullptr,
+  check(omt_bn_bwd_nhwc(n, c, hw, fp(g), g_nchw ? 1 : 0, g2.defined() ? fp(g2) : nullptr, fp(x), act,
+                        r.defined() ? fp(r) : nullptr,
                         fp(mean), fp(invstd), fp(w), fpm(gx), fpm(dg), fpm(db), fpm(gz), wsptr(ws), wsbytes(ws),
                         cur_stream()),
         what);
@@ -656,8 +658,13 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_train_dev(cons
   cover(act >= OMT_ACT_NONE && act <= OMT_ACT_HARDSWISH, "activation none, ReLU or hardswish");
   cover(stride.size() == 2 && padding.size() == 2 && stride[0] == stride[1] && padding[0] == padding[1],
         "uniform 2-D stride and padding");
-  cover(kind_of(x_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && !channels_last(x_, cw_),
-        "dense NCHW convolution");
+  if (kind_of(x_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && channels_last(x_, cw_)) {
+    // channels-last: the NHWC convolution, then the NHWC BatchNorm of its output (no partials to fold)
+    Tensor conv = conv_forward(x_, cw_, std::nullopt, stride, padding, {1, 1}, false, 1, false);
+    auto r = bn_train_inplace_dev(conv, w, b, rm, rv, mom, eps, act, res_);
+    return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r), conv};
+  }
+  cover(kind_of(x_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE, "dense convolution");
   cover(whole(w) && whole(b) && whole(rm) && whole(rv), "contiguous float32 BatchNorm parameters");
   Tensor x = contig(x_), cw = contig(cw_);
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), cw.size(0), x.size(2), x.size(3), cw.size(2), stride[0], padding[0]);
@@ -826,9 +833,20 @@ static std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> conv_bn_backward_dev(
   cover(res || !defined(other_), "a second gradient only with a residual branch");
   cover(stride.size() == 2 && padding.size() == 2 && stride[0] == stride[1] && padding[0] == padding[1],
         "uniform 2-D stride and padding");
-  cover(kind_of(cx_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && !channels_last(cx_, cw_) &&
-            f32(gy_) && gy_.dim() == 4,
-        "dense NCHW convolution");
+  if (kind_of(cx_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && channels_last(cx_, cw_) &&
+      f32(gy_) && gy_.dim() == 4) {
+    // channels-last: the NHWC convolution backward, then the NHWC BatchNorm backward of its grad input
+    auto cb = convolution_backward_(gy_, cx_, cw_, std::nullopt, stride, padding, {1, 1}, false, {0, 0}, 1,
+                                    {true, true, false});
+    if (res) {
+      auto b = bn_relu_res_backward_dev(std::get<0>(cb), other_, x_, r_, w, mean, invstd, mask);
+      return {std::get<1>(cb), std::get<0>(b), std::get<1>(b), std::get<2>(b), std::get<3>(b)};
+    }
+    auto b = bn_act_backward_dev(std::get<0>(cb), x_, r_, w, mean, invstd, act, mask);
+    return {std::get<1>(cb), std::get<0>(b), std::get<1>(b), std::get<2>(b), Tensor()};
+  }
+  cover(kind_of(cx_, cw_, stride, padding, {1, 1}, false, 1) == OMT_CONV_DENSE && f32(gy_) && gy_.dim() == 4,
+        "dense convolution");
   cover(f32(x_) && f32(r_) && x_.dim() == 4 && cx_.sizes() == x_.sizes() && r_.sizes() == x_.sizes() && whole(w) &&
             whole(mean) && whole(invstd) && (!defined(other_) || (f32(*other_) && other_->sizes() == x_.sizes())),
         "4-D float32 BatchNorm operands of the convolution input's shape");

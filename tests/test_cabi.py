@@ -375,8 +375,9 @@ def test_ctypes_structs_match_the_header(tmp_path):
 def test_nhwc_plans_and_workspaces_host_side():
     """Channels-last directions: their own tile tables (the nine staged gather tiles; the four grad-weight tiles), a
     plan whose K-block does not divide the gathered channels runs as tile 5, workspaces of the plans' sizes (grad
-    input always re-packs the filter), and the coverage conditions (forward ci % 16, grad input co % 16, grad weight
-    ci and co % 4) as empty workspaces and OMT_UNSUPPORTED, all without a GPU."""
+    input always re-packs the filter), and the coverage conditions (grad input co % 16, grad weight co % 4; a forward
+    of ci % 16 != 0 runs its fixed element-by-element plan, no K split, so no workspace) as empty workspaces and
+    OMT_UNSUPPORTED, all without a GPU."""
     from omarchy_mac_torch import _lib
     L = _lib.L
     L.omt_conv_clear_plans()
@@ -413,7 +414,6 @@ def test_nhwc_plans_and_workspaces_host_side():
         for ws in (L.omt_conv_fwd_nhwc_workspace, L.omt_conv_dgrad_nhwc_workspace, L.omt_conv_wgrad_nhwc_workspace):
             assert ws(ctypes.byref(odd)) == 0
         fake = ctypes.c_void_p(16)
-        assert L.omt_conv_fwd_nhwc(ctypes.byref(odd), fake, fake, None, 0, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
         assert L.omt_conv_dgrad_nhwc(ctypes.byref(odd), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
         assert L.omt_conv_wgrad_nhwc(ctypes.byref(odd), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
         assert L.omt_conv_fwd_nhwc(ctypes.byref(g), None, fake, None, 0, fake, None, 0, None) == _lib.OMT_INVALID

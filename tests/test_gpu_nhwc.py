@@ -54,6 +54,11 @@ NHWC_SHAPES = [
     (4, 512, 512, 2, 2, 3, 1, 1),     # ResNet-18 layer4 at 64x64: the cost model splits K
     (3, 16, 36, 10, 10, 3, 1, 1),     # 36 output channels: a partial row tile (grad input then not covered)
     (2, 32, 18, 8, 6, 11, 4, 5),      # 11x11 stride 4, 18 output channels: scalar stores, neither grad covered
+    # input channels not a multiple of 16: the forward gathers element by element; of 4: so do grad weight's columns
+    (2, 3, 64, 32, 32, 7, 2, 3),      # the ResNet stem (at 64x64 input: 32x32 here)
+    (3, 6, 16, 9, 11, 3, 1, 1),
+    (2, 20, 32, 10, 10, 3, 2, 1),     # 20 channels: narrow forward, float4 grad-weight columns
+    (2, 1, 16, 12, 12, 5, 1, 2),      # one input channel
 ]
 
 
@@ -64,8 +69,8 @@ def _ids(s):
 @pytest.mark.parametrize("shape", NHWC_SHAPES, ids=_ids)
 def test_conv_nhwc_fwd_dgrad_wgrad(cuda, ops, shape):
     """Forward (bias + ReLU), grad input and grad weight of channels-last tensors against the oracle; the outputs
-    come back channels_last. Grad input needs co % 16 == 0 and grad weight ci, co multiples of 4: other shapes raise
-    Unsupported (the device then runs the NCHW kernels)."""
+    come back channels_last. Any input channel count; grad input needs co % 16 == 0 and grad weight co % 4 == 0:
+    other shapes raise Unsupported (the device then runs the NCHW kernels)."""
     from omarchy_mac_torch._lib import Unsupported
     n, ci, co, h, w, ks, s, p = shape
     rng = np.random.default_rng(sum(shape))
@@ -91,15 +96,15 @@ def test_conv_nhwc_fwd_dgrad_wgrad(cuda, ops, shape):
             ops.conv2d_wgrad_nhwc(dev_cl(x, cuda), dev_cl(gy, cuda), ks, s, p)
 
 
-def test_conv_nhwc_input_channels_not_covered(cuda, ops):
-    """Forward needs ci % 16 == 0 and grad weight ci % 4 == 0: other inputs raise Unsupported, nothing runs."""
+def test_conv_nhwc_output_channels_not_covered(cuda, ops):
+    """Grad input needs co % 16 == 0 and grad weight co % 4 == 0: other outputs raise Unsupported, nothing runs."""
     from omarchy_mac_torch._lib import Unsupported
     rng = np.random.default_rng(3)
-    x, wt = rnd(rng, 2, 6, 8, 8), rnd(rng, 16, 6, 3, 3)
+    x, wt, gy = rnd(rng, 2, 6, 8, 8), rnd(rng, 18, 6, 3, 3), rnd(rng, 2, 18, 8, 8)
     with pytest.raises(Unsupported):
-        ops.conv2d_nhwc(dev_cl(x, cuda), dev_cl(wt, cuda), None, 1, 1)
+        ops.conv2d_dgrad_nhwc(dev_cl(gy, cuda), dev_cl(wt, cuda), x.shape, 1, 1)
     with pytest.raises(Unsupported):
-        ops.conv2d_wgrad_nhwc(dev_cl(x, cuda), dev_cl(rnd(rng, 2, 16, 8, 8), cuda), 3, 1, 1)
+        ops.conv2d_wgrad_nhwc(dev_cl(x, cuda), dev_cl(gy, cuda), 3, 1, 1)
 
 
 NHWC_PLAN_SHAPES = [
@@ -235,7 +240,7 @@ def test_conv_nhwc_full_size(cuda, ops, name, shape):
 CL_CASES = [
     # (n, ci, co, h, ks, s, p, bias): covered by the NHWC kernels in every direction
     (2, 32, 64, 14, 3, 1, 1, False), (2, 64, 32, 9, 1, 2, 0, True), (3, 16, 48, 11, 5, 2, 2, False),
-    # input channels not a multiple of 16 (forward in NCHW, output converted), 36 output channels (grad input in NCHW)
+    # 3 input channels (the narrow NHWC forward and grad weight), 36 output channels (grad input in NCHW)
     (2, 3, 16, 23, 7, 2, 3, False), (2, 16, 36, 10, 3, 1, 1, True),
 ]
 
@@ -339,6 +344,12 @@ def test_batch_norm_nhwc(cuda, ops, n, c, h, w):
         assert orc.rel_l2(host(dg), dg_ref) <= TOL and orc.rel_l2(host(db), db_ref) <= TOL
         scale = np.linalg.norm(gz_ref.astype(np.float64)) * np.abs(gam * host(si)).max()
         assert np.linalg.norm(host(gx).astype(np.float64) - gx_ref) <= TOL * max(scale, 1e-30)
+        # the incoming gradient in NCHW order (a global pool's broadcast gradient), read in place: the same results
+        gx4, dg4, db4, gz4 = ops.batch_norm_backward_nhwc(dev(g, cuda), dev_cl(x, cuda), sm, si, tg, act=act,
+                                                          act_in=act_in, g2=dev_cl(g2, cuda), want_gz=True,
+                                                          g_nchw=True)
+        for a_, b_ in ((gx4, gx), (dg4, dg), (db4, db), (gz4, gz)):
+            assert torch.equal(a_.cpu(), b_.cpu()), act
         # grads only (no gx, no gz): the apply pass is skipped
         _, dg3, db3, _ = ops.batch_norm_backward_nhwc(dev_cl(g, cuda), dev_cl(x, cuda), sm, si, tg, act=act,
                                                       act_in=act_in, g2=dev_cl(g2, cuda),
