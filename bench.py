@@ -815,6 +815,15 @@ def train_step_bench(cfg, dev_name, steps, warmup, cpu_steps, cpu, compiled=Fals
             "how": "the graphed step with the model under torch.compile(backend=\"omarchy_mac_torch\"): BatchNorm "
                    "running statistics updated in place, BatchNorm + ReLU and BatchNorm + residual add + ReLU fused, "
                    "batch counters in one launch"}
+    if compiled and key == "resnet18_b32":
+        cl = torch.channels_last
+        cl_batches = [(x.contiguous(memory_format=cl), t) for x, t in dev_batches]
+        cl_model = copy.deepcopy(base).to(memory_format=cl).to(dev_name)
+        c_ms, variants["channels_last_compiled_graphed"] = run_graphed(cl_model, cl_batches, 3, True)
+        out["channels_last_compiled_graphed"] = {
+            "ms_per_step": round(c_ms, 3), "steps": len(dev_batches) - 3, "eager_warmup": 3,
+            "how": "the compiled + graphed step with the model and its batches in torch.channels_last memory order: "
+                   "the NHWC convolution, BatchNorm and pooling kernels, no layout conversion"}
     if not cpu:
         return out
     threads = len(os.sched_getaffinity(0))

@@ -236,9 +236,9 @@ int omt_slice_sums(const omt_slice_sum* sums, int count, void* stream);
  * written without a layout change. The reference makes every input contiguous NCHW first (base0,
  * csrc/device.cpp:60-66, before gemm_forward / gemm_grad_input / gemm_grad_weight, csrc/conv.cpp:70-114); these
  * entry points replace that copy and those GEMMs for channels-last callers. Coverage beyond the dense geometry:
- * grad input needs co % 16 == 0, grad weight co % 4 == 0 (else OMT_UNSUPPORTED). A forward of ci % 16 != 0 (the
- * 3-channel stem) gathers element by element on one fixed plan, a grad weight of ci % 4 != 0 loads its columns one
- * by one: same LDS staging and MFMA order, no tuning of the forward. Plans: directions OMT_DIR_FWD_NHWC,
+ * grad weight needs co % 4 == 0 (else OMT_UNSUPPORTED). A forward of ci % 16 != 0 (the 3-channel stem) and a grad
+ * input of co % 16 != 0 gather element by element on one fixed plan, a grad weight of ci % 4 != 0 loads its columns
+ * one by one: same LDS staging and MFMA order; those gathers are not tuned. Plans: directions OMT_DIR_FWD_NHWC,
  * OMT_DIR_DGRAD_NHWC, OMT_DIR_WGRAD_NHWC (tile indices below omt_conv_num_tiles of the direction). Bias and ReLU
  * epilogue bits as in omt_conv_fwd; no BN loader. */
 size_t omt_conv_fwd_nhwc_workspace(const omt_conv_geo* g);
@@ -294,6 +294,16 @@ int omt_dw_dgrad(const omt_conv_geo* g, const float* gy, const float* w, float* 
 size_t omt_dw_wgrad_workspace(const omt_conv_geo* g);
 int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
                  size_t workspace_bytes, void* stream);
+/* The same over channels-last tensors: x / gx [n][ih][iw][C], y / gy [n][oh][ow][C], the filter and its gradient
+ * [C][ks][ks] (a channels_last [C][1][ks][ks] filter's memory); n * ih * iw * C and n * oh * ow * C below 2^31. No
+ * BN loader. Forward and grad input compute each output as the general NCHW kernels do (same taps, same order); grad
+ * weight sums pixel slices into a workspace of omt_dw_wgrad_nhwc_workspace bytes, then the slices in order. No
+ * counterpart in the reference, which makes every operand contiguous NCHW first (csrc/device.cpp:60-66). */
+int omt_dw_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias, float* y, void* stream);
+int omt_dw_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* stream);
+size_t omt_dw_wgrad_nhwc_workspace(const omt_conv_geo* g);
+int omt_dw_wgrad_nhwc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* ---- BatchNorm (NCHW, affine) ----------------------------------------------------------------------------- */
 
@@ -507,6 +517,10 @@ int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float scale, float
  * tensor's memory), y [n][c]; n <= 65535. No counterpart in the reference, which reduces contiguous NCHW copies
  * (csrc/reduce.cpp, csrc/device.cpp:60-66). */
 int omt_plane_sum_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, float scale, float* y, void* stream);
+/* y[img][p][ch] = x[img][p][ch] * s[img][ch]: omt_channel_scale over channels-last planes (x, y [n][hw][c], s [n][c]).
+ * No counterpart in the reference (see omt_plane_sum_nhwc). */
+int omt_channel_scale_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* scale, float* y,
+                           void* stream);
 /* omt_pointwise over [n][c][hw] operands stored in different orders: each of a, b and out NCHW (flag 0) or
  * channels-last NHWC (flag 1); out[i] = op(a, b) at the same logical element. Unary and binary ops only (not
  * OMT_PW_FILL). For the one op per step where a channels-last model meets an NCHW gradient (a global average pool's

@@ -2831,7 +2831,12 @@ OMT_EXPORT int omt_conv_bwd(const omt_conv_geo* g, const float* x, const float* 
 // tap-major [P][K] operand of the forward gather; the grad-input phases re-pack it; grad weight writes its
 // tap-major columns in place. Plans live under their own directions (OMT_DIR_*_NHWC).
 
-static bool nhwc_dgrad_ok(const omt_conv_geo* g) { return g->co % 16 == 0; }
+// Narrow channels-last gathers (channels not a multiple of 16: the forward's input channels, e.g. the ResNet stem's
+// 3, or grad input's source channels co): one plan, the 64 x 64 staged tile gathering element by element
+// (kNhwcNarrow), no K split.
+constexpr int kNarrowTile = 5;
+static bool nhwc_narrow(const omt_conv_geo* g) { return g->ci % 16 != 0; }
+static bool nhwc_dgrad_narrow(const omt_conv_geo* g) { return g->co % 16 != 0; }
 // grad weight: output channels a multiple of 4 (float4 runs of gy); input channels not a multiple of 4 take the
 // element-by-element column loads (NARROW)
 static bool nhwc_wgrad_ok(const omt_conv_geo* g) { return g->co % 4 == 0; }
@@ -2847,15 +2852,12 @@ static GatherPlan dgrad_nhwc_plan(const omt_conv_geo* g) {
   int64_t maxq = 0, maxk = 0;
   dgrad_phases(g, a, pk, maxq);
   for (int i = 0; i < a.nphase; ++i) maxk = std::max<int64_t>(maxk, a.ph[i].K);
+  if (nhwc_dgrad_narrow(g)) return GatherPlan{kNarrowTile, 1, std::max<int64_t>(16, cdiv(maxk, 16) * 16)};
   omt_conv_plan cp;
   const bool have = cached_plan(OMT_DIR_DGRAD_NHWC, g, &cp);
   return gather_plan(g->ci, maxq, maxk, a.nphase, have ? &cp : nullptr, g->co);
 }
 
-// Narrow channels-last forward (input channels not a multiple of 16, e.g. the ResNet stem's 3): one plan, the 64 x 64
-// staged tile gathering element by element (kNhwcNarrow), no K split.
-constexpr int kNarrowTile = 5;
-static bool nhwc_narrow(const omt_conv_geo* g) { return g->ci % 16 != 0; }
 
 // Launches a channels-last gather (and, split over K, its slice sum); `part`: the partials of the plan's size.
 static int run_gather_nhwc(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t maxq, float* part,
@@ -2949,7 +2951,7 @@ static size_t dgrad_nhwc_workspace_one(const omt_conv_geo* g) {
 }
 
 OMT_EXPORT size_t omt_conv_dgrad_nhwc_workspace(const omt_conv_geo* g) {
-  return g && dense_geo_ok(g) && nhwc_dgrad_ok(g) ? chunks_max(g, dgrad_nhwc_workspace_one) : 0;
+  return g && dense_geo_ok(g) ? chunks_max(g, dgrad_nhwc_workspace_one) : 0;
 }
 
 static int conv_dgrad_nhwc_one(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
@@ -2982,7 +2984,7 @@ static int conv_dgrad_nhwc_one(const omt_conv_geo* g, const float* gy, const flo
   a.YW = (int)g->iw;
   a.div_c = make_fastdiv((uint32_t)a.C);
   float* part = (float*)((char*)workspace + align256((size_t)packed * sizeof(float)));
-  return run_gather_nhwc(a, pl, g->n, maxq, part, s);
+  return run_gather_nhwc(a, pl, g->n, maxq, part, s, nhwc_dgrad_narrow(g));
 }
 
 OMT_EXPORT int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* workspace,
@@ -2990,7 +2992,6 @@ OMT_EXPORT int omt_conv_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const
   if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: null pointer");
   Chunks ch;
   if (int st = chunk_check(g, "omt_conv_dgrad_nhwc", ch)) return st;
-  if (!nhwc_dgrad_ok(g)) return fail(OMT_UNSUPPORTED, "omt_conv_dgrad_nhwc: output channels not a multiple of 16");
   const size_t need = omt_conv_dgrad_nhwc_workspace(g);
   if (!workspace || workspace_bytes < need)
     return fail(OMT_INVALID, "omt_conv_dgrad_nhwc: workspace of %zu bytes needed", need);

@@ -16,6 +16,7 @@
 
 #include "lds_dma.h"
 #include "omt_internal.h"
+#include "slice_sum.h"
 
 namespace omt {
 
@@ -848,6 +849,239 @@ static int64_t dw_slices(const omt_conv_geo* g) {
   return want < 1 ? 1 : want;
 }
 
+// ---- channels-last (NHWC) depthwise -----------------------------------------------------------------------------
+// x / gx [n][ih][iw][c], y / gy [n][oh][ow][c]; the filter [c][ks][ks] (a channels_last [c][1][ks][ks] filter has
+// that memory order too). Forward and grad input: one thread per (pixel, vector of VEC channels: float4 when c % 4 ==
+// 0 and the tensors are 16-byte aligned), so a wave reads runs of channels; the taps in the general kernels' order
+// with the same fma chain, so each output is the general NCHW kernel's bit for bit. Grad weight: workgroup (channel
+// block, filter row ky, pixel slice), thread (channel vector, row lane) accumulating the row's ks taps over its pixels,
+// the row lanes added in lane order, the slices summed in order by a second launch.
+template <int VEC>
+struct DwVec;
+template <>
+struct DwVec<4> {
+  using T = float4;
+  static __device__ __forceinline__ float get(const float4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+  }
+  static __device__ __forceinline__ void set(float4& v, int i, float f) {
+    if (i == 0) v.x = f; else if (i == 1) v.y = f; else if (i == 2) v.z = f; else v.w = f;
+  }
+};
+template <>
+struct DwVec<1> {
+  using T = float;
+  static __device__ __forceinline__ float get(const float& v, int) { return v; }
+  static __device__ __forceinline__ void set(float& v, int, float f) { v = f; }
+};
+
+struct DwNhwc {
+  DwGeo g;
+  int cv;                 // channel vectors per pixel
+  FastDiv d_cv, d_w, d_h;  // by cv, and the width and height of the plane a thread's pixel lies in
+};
+
+__device__ __forceinline__ void dw_nhwc_pos(uint32_t i, const DwNhwc& d, int W, int H, int64_t& img, int& y, int& x,
+                                            int& j) {
+  const uint32_t pix = fdiv(i, d.d_cv), t = fdiv(pix, d.d_w), im = fdiv(t, d.d_h);
+  j = (int)(i - pix * (uint32_t)d.cv);
+  x = (int)(pix - t * (uint32_t)W);
+  y = (int)(t - im * (uint32_t)H);
+  img = im;
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) dw_fwd_nhwc_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          const float* __restrict__ bias, float* __restrict__ y,
+                                                          uint32_t total, DwNhwc d) {
+  using DV = DwVec<VEC>;
+  using V = typename DV::T;
+  const DwGeo& g = d.g;
+  const int kk = g.ks * g.ks;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int oy, ox, j;
+    dw_nhwc_pos(i, d, g.ow, g.oh, img, oy, ox, j);
+    const int y0 = oy * g.s - g.p, x0 = ox * g.s - g.p;
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int ky = 0; ky < g.ks; ++ky) {
+      const int yy = y0 + ky;
+      if ((unsigned)yy >= (unsigned)g.ih) continue;
+      for (int kx = 0; kx < g.ks; ++kx) {
+        const int xx = x0 + kx;
+        if ((unsigned)xx >= (unsigned)g.iw) continue;
+        const V v = *reinterpret_cast<const V*>(x + ((img * g.ih + yy) * g.iw + xx) * g.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(DV::get(v, e), w[(j * VEC + e) * kk + ky * g.ks + kx], acc[e]);
+      }
+    }
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) DV::set(out, e, bias ? acc[e] + bias[j * VEC + e] : acc[e]);
+    *reinterpret_cast<V*>(y + ((img * g.oh + oy) * g.ow + ox) * g.c + (int64_t)j * VEC) = out;
+  }
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) dw_dgrad_nhwc_kernel(const float* __restrict__ gy, const float* __restrict__ w,
+                                                            float* __restrict__ gx, uint32_t total, DwNhwc d) {
+  using DV = DwVec<VEC>;
+  using V = typename DV::T;
+  const DwGeo& g = d.g;
+  const int kk = g.ks * g.ks;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    int64_t img;
+    int yy, xx, j;
+    dw_nhwc_pos(i, d, g.iw, g.ih, img, yy, xx, j);
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int ky = 0; ky < g.ks; ++ky) {
+      const int ty = yy + g.p - ky;
+      if (ty < 0 || ty % g.s) continue;
+      const int oy = ty / g.s;
+      if (oy >= g.oh) continue;
+      for (int kx = 0; kx < g.ks; ++kx) {
+        const int tx = xx + g.p - kx;
+        if (tx < 0 || tx % g.s) continue;
+        const int ox = tx / g.s;
+        if (ox >= g.ow) continue;
+        const V v = *reinterpret_cast<const V*>(gy + ((img * g.oh + oy) * g.ow + ox) * g.c + (int64_t)j * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(DV::get(v, e), w[(j * VEC + e) * kk + ky * g.ks + kx], acc[e]);
+      }
+    }
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) DV::set(out, e, acc[e]);
+    *reinterpret_cast<V*>(gx + ((img * g.ih + yy) * g.iw + xx) * g.c + (int64_t)j * VEC) = out;
+  }
+}
+
+constexpr int kDwMaxKs = 11, kDwNhwcMaxSlices = 128;
+
+struct DwNhwcW {
+  int cb, rl, cblocks, slices;  // channel vectors per workgroup row, row lanes, channel blocks, pixel slices
+  int64_t per_slice;            // output pixels per slice
+};
+
+// grid (cblocks, ks, slices): part[slice][ch][ky * ks + kx] = the slice's sum of gy[pixel][ch] x[tap (ky, kx)][ch]
+template <int VEC>
+__global__ void __launch_bounds__(256) dw_wgrad_nhwc_kernel(const float* __restrict__ x, const float* __restrict__ gy,
+                                                            float* __restrict__ part, DwGeo g, int cv, DwNhwcW wp,
+                                                            FastDiv d_ohw, FastDiv d_ow) {
+  using DV = DwVec<VEC>;
+  using V = typename DV::T;
+  __shared__ float red[256 * VEC];
+  const int jl = threadIdx.x % wp.cb, lane = threadIdx.x / wp.cb, j = blockIdx.x * wp.cb + jl;
+  const int ky = blockIdx.y, sl = blockIdx.z;
+  const bool on = lane < wp.rl && j < cv;
+  float acc[kDwMaxKs][VEC];
+#pragma unroll
+  for (int kx = 0; kx < kDwMaxKs; ++kx)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[kx][e] = 0.f;
+  if (on) {
+    const int64_t total = (int64_t)g.n * g.oh * g.ow;
+    const int64_t k0 = sl * wp.per_slice, k1 = min(total, k0 + wp.per_slice);
+    const uint32_t ohw = (uint32_t)(g.oh * g.ow);
+    for (int64_t k = k0 + lane; k < k1; k += wp.rl) {
+      const uint32_t n = fdiv((uint32_t)k, d_ohw), r = (uint32_t)k - n * ohw;
+      const uint32_t oy = fdiv(r, d_ow), ox = r - oy * (uint32_t)g.ow;
+      const int yy = (int)oy * g.s - g.p + ky;
+      if ((unsigned)yy >= (unsigned)g.ih) continue;
+      const V gv = *reinterpret_cast<const V*>(gy + k * g.c + (int64_t)j * VEC);
+      const float* xrow = x + (((int64_t)n * g.ih + yy) * g.iw) * g.c + (int64_t)j * VEC;
+      const int x0 = (int)ox * g.s - g.p;
+#pragma unroll
+      for (int kx = 0; kx < kDwMaxKs; ++kx) {
+        const int xx = x0 + kx;
+        if (kx < g.ks && (unsigned)xx < (unsigned)g.iw) {
+          const V xv = *reinterpret_cast<const V*>(xrow + (int64_t)xx * g.c);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[kx][e] = fmaf(DV::get(gv, e), DV::get(xv, e), acc[kx][e]);
+        }
+      }
+    }
+  }
+  // the row lanes' sums of each tap, added in lane order
+  for (int kx = 0; kx < g.ks; ++kx) {
+    float v[VEC];
+#pragma unroll
+    for (int t = 0; t < kDwMaxKs; ++t)
+      if (t == kx)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = acc[t][e];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[threadIdx.x * VEC + e] = v[e];
+    __syncthreads();
+    const int q = threadIdx.x;
+    if (q < wp.cb * VEC) {
+      const int ql = q / VEC, e = q - ql * VEC, ch = (blockIdx.x * wp.cb + ql) * VEC + e;
+      if (ch < g.c) {
+        float s = 0.f;
+        for (int r = 0; r < wp.rl; ++r) s += red[(r * wp.cb + ql) * VEC + e];
+        part[((int64_t)sl * g.c + ch) * g.ks * g.ks + ky * g.ks + kx] = s;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(256) dw_nhwc_sum_kernel(const SplitSum r) {
+  if (r.vec4)
+    split_sum_any<4>(r, blockIdx.x, gridDim.x);
+  else
+    split_sum_any<1>(r, blockIdx.x, gridDim.x);
+}
+
+static bool dw_nhwc_vec(const omt_conv_geo* g, std::initializer_list<const void*> ptrs) {
+  if (g->ci % 4) return false;
+  for (const void* p : ptrs)
+    if (p && (uintptr_t)p % 16) return false;
+  return true;
+}
+static DwNhwc dw_nhwc(const omt_conv_geo* g, bool vec, int64_t W, int64_t H) {
+  DwNhwc d;
+  d.g = DwGeo{(int)g->n, (int)g->ci, (int)g->ih, (int)g->iw, (int)g->oh, (int)g->ow, (int)g->ks, (int)g->stride,
+              (int)g->pad};
+  d.cv = (int)(vec ? g->ci / 4 : g->ci);
+  d.d_cv = make_fastdiv((uint32_t)d.cv);
+  d.d_w = make_fastdiv((uint32_t)W);
+  d.d_h = make_fastdiv((uint32_t)H);
+  return d;
+}
+static DwNhwcW dw_nhwc_wsplit(const omt_conv_geo* g, bool vec) {
+  DwNhwcW wp;
+  const int cv = (int)(vec ? g->ci / 4 : g->ci);
+  wp.cb = cv < 64 ? cv : 64;
+  wp.rl = 256 / wp.cb;
+  wp.cblocks = (int)cdiv(cv, wp.cb);
+  const int64_t total = g->n * g->oh * g->ow;
+  int64_t want = cdiv(1024, (int64_t)wp.cblocks * g->ks);
+  const int64_t by_rows = std::max<int64_t>(1, total / (8 * (int64_t)wp.rl));  // at least 8 pixels per thread
+  want = std::min<int64_t>(std::min<int64_t>(want, by_rows), kDwNhwcMaxSlices);
+  wp.per_slice = cdiv(total, want);
+  wp.slices = (int)cdiv(total, wp.per_slice);
+  return wp;
+}
+// pixels x channel vectors below 2^31 (32-bit thread indices whose grid-stride steps never wrap)
+static bool dw_nhwc_ok(const omt_conv_geo* g) {
+  return dw_ok(g) && g->n * g->ih * g->iw * g->ci < ((int64_t)1 << 31) &&
+         g->n * g->oh * g->ow * g->ci < ((int64_t)1 << 31);
+}
+
+#define OMT_DW_NHWC(K, vec, total, s, ...)                                                       \
+  do {                                                                                           \
+    if (vec)                                                                                     \
+      hipLaunchKernelGGL(K<4>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);          \
+    else                                                                                         \
+      hipLaunchKernelGGL(K<1>, dim3(grid1d(total, 256)), dim3(256), 0, s, __VA_ARGS__);          \
+  } while (0)
+
+
 }  // namespace omt
 
 using namespace omt;
@@ -959,4 +1193,56 @@ OMT_EXPORT int omt_dw_wgrad(const omt_conv_geo* g, const float* x, const float* 
   hipLaunchKernelGGL(dw_wgrad_reduce_kernel, dim3(grid1d(n, 256, 4096)), dim3(256), 0, s, (const float*)part, gw, n,
                      (int)slices);
   return launch_check("dw_wgrad_reduce_kernel");
+}
+
+OMT_EXPORT int omt_dw_fwd_nhwc(const omt_conv_geo* g, const float* x, const float* w, const float* bias, float* y,
+                               void* stream) {
+  if (!g || !x || !w || !y) return fail(OMT_INVALID, "omt_dw_fwd_nhwc: null pointer");
+  if (!dw_nhwc_ok(g)) return fail(OMT_UNSUPPORTED, "omt_dw_fwd_nhwc: geometry not covered");
+  const bool vec = dw_nhwc_vec(g, {x, y});
+  const DwNhwc d = dw_nhwc(g, vec, g->ow, g->oh);
+  const int64_t total = g->n * g->oh * g->ow * d.cv;
+  OMT_DW_NHWC(dw_fwd_nhwc_kernel, vec, total, stream_of(stream), x, w, bias, y, (uint32_t)total, d);
+  return launch_check("dw_fwd_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_dw_dgrad_nhwc(const omt_conv_geo* g, const float* gy, const float* w, float* gx, void* stream) {
+  if (!g || !gy || !w || !gx) return fail(OMT_INVALID, "omt_dw_dgrad_nhwc: null pointer");
+  if (!dw_nhwc_ok(g)) return fail(OMT_UNSUPPORTED, "omt_dw_dgrad_nhwc: geometry not covered");
+  const bool vec = dw_nhwc_vec(g, {gy, gx});
+  const DwNhwc d = dw_nhwc(g, vec, g->iw, g->ih);
+  const int64_t total = g->n * g->ih * g->iw * d.cv;
+  OMT_DW_NHWC(dw_dgrad_nhwc_kernel, vec, total, stream_of(stream), gy, w, gx, (uint32_t)total, d);
+  return launch_check("dw_dgrad_nhwc_kernel");
+}
+
+// the slices' partial filter gradients [slices][c][ks][ks] (the float4 split of the aligned case, which has the most)
+OMT_EXPORT size_t omt_dw_wgrad_nhwc_workspace(const omt_conv_geo* g) {
+  if (!g || !dw_nhwc_ok(g)) return 0;
+  const int sl = std::max(dw_nhwc_wsplit(g, g->ci % 4 == 0).slices, dw_nhwc_wsplit(g, false).slices);
+  return (size_t)(sl * g->ci * g->ks * g->ks) * sizeof(float);
+}
+
+OMT_EXPORT int omt_dw_wgrad_nhwc(const omt_conv_geo* g, const float* x, const float* gy, float* gw, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (!g || !x || !gy || !gw) return fail(OMT_INVALID, "omt_dw_wgrad_nhwc: null pointer");
+  if (!dw_nhwc_ok(g)) return fail(OMT_UNSUPPORTED, "omt_dw_wgrad_nhwc: geometry not covered");
+  const size_t need = omt_dw_wgrad_nhwc_workspace(g);
+  if (!workspace || workspace_bytes < need)
+    return fail(OMT_INVALID, "omt_dw_wgrad_nhwc: workspace of %zu bytes needed", need);
+  hipStream_t s = stream_of(stream);
+  const bool vec = dw_nhwc_vec(g, {x, gy});
+  const DwNhwcW wp = dw_nhwc_wsplit(g, vec);
+  const int cv = (int)(vec ? g->ci / 4 : g->ci);
+  float* part = (float*)workspace;
+  const dim3 grid((unsigned)wp.cblocks, (unsigned)g->ks, (unsigned)wp.slices);
+  const FastDiv d_ohw = make_fastdiv((uint32_t)(g->oh * g->ow)), d_ow = make_fastdiv((uint32_t)g->ow);
+  if (vec)
+    hipLaunchKernelGGL(dw_wgrad_nhwc_kernel<4>, grid, dim3(256), 0, s, x, gy, part, dgeo(g), cv, wp, d_ohw, d_ow);
+  else
+    hipLaunchKernelGGL(dw_wgrad_nhwc_kernel<1>, grid, dim3(256), 0, s, x, gy, part, dgeo(g), cv, wp, d_ohw, d_ow);
+  if (int st = launch_check("dw_wgrad_nhwc_kernel")) return st;
+  const SplitSum r = split_sum_of(part, gw, g->ci * g->ks * g->ks, wp.slices);
+  hipLaunchKernelGGL(dw_nhwc_sum_kernel, dim3((unsigned)r.blocks), dim3(256), 0, s, r);
+  return launch_check("dw_nhwc_sum_kernel");
 }

@@ -336,6 +336,23 @@ __global__ void __launch_bounds__(256) pointwise_layouts_kernel(const float* __r
   }
 }
 
+// y[img][p][ch] = x[img][p][ch] * s[img][ch] over channels-last planes; VEC channels per thread.
+template <int VEC>
+__global__ void __launch_bounds__(256) channel_scale_nhwc_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ s, float* __restrict__ y,
+                                                                 int64_t total_v, int64_t cv, int64_t hwcv) {
+  using V = typename std::conditional<VEC == 4, float4, float>::type;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
+    const int64_t img = i / hwcv, j = i % cv;
+    const V v = reinterpret_cast<const V*>(x)[i];
+    const V f = reinterpret_cast<const V*>(s + img * cv * VEC)[j];
+    if constexpr (VEC == 4)
+      reinterpret_cast<V*>(y)[i] = make_float4(v.x * f.x, v.y * f.y, v.z * f.z, v.w * f.w);
+    else
+      y[i] = v * f;
+  }
+}
+
 // y[img][ch] = scale * sum over the hw positions of x [n][hw][c] (channels-last planes). Workgroup (channel block,
 // image): thread t owns channel j = block * cb + t % cb and sums positions t / cb, + rl, ... (four loads in flight),
 // then the row lanes' sums are added in lane order: a fixed order.
@@ -587,4 +604,21 @@ OMT_EXPORT int omt_plane_sum_nhwc(int64_t n, int64_t c, int64_t hw, const float*
   const dim3 grid((unsigned)cdiv(c, cb), (unsigned)n);
   hipLaunchKernelGGL(plane_sum_nhwc_kernel, grid, dim3(256), 0, stream_of(stream), x, y, (int)c, (int)hw, cb, scale);
   return launch_check("plane_sum_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_channel_scale_nhwc(int64_t n, int64_t c, int64_t hw, const float* x, const float* scale, float* y,
+                                      void* stream) {
+  if (!x || !scale || !y) return fail(OMT_INVALID, "omt_channel_scale_nhwc: null pointer");
+  if (n < 0 || c < 1 || hw < 0 || n * c * hw >= ((int64_t)1 << 46)) return fail(OMT_INVALID, "omt_channel_scale_nhwc: size");
+  if (n == 0 || hw == 0) return OMT_OK;
+  const bool v4 = c % 4 == 0 && al16(x) && al16(scale) && al16(y);
+  const int64_t cv = v4 ? c / 4 : c, total_v = n * hw * cv;
+  const dim3 grid(grid1d(total_v, 256, 8192));
+  if (v4)
+    hipLaunchKernelGGL(channel_scale_nhwc_kernel<4>, grid, dim3(256), 0, stream_of(stream), x, scale, y, total_v, cv,
+                       hw * cv);
+  else
+    hipLaunchKernelGGL(channel_scale_nhwc_kernel<1>, grid, dim3(256), 0, stream_of(stream), x, scale, y, total_v, cv,
+                       hw * cv);
+  return launch_check("channel_scale_nhwc_kernel");
 }

@@ -143,6 +143,11 @@ SIGNATURES = {
     "omt_plane_broadcast": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
     "omt_plane_sum": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
     "omt_plane_sum_nhwc": (I32, [I64, I64, I64, VP, ctypes.c_float, VP, VP]),
+    "omt_channel_scale_nhwc": (I32, [I64, I64, I64, VP, VP, VP, VP]),
+    "omt_dw_fwd_nhwc": (I32, [VP, VP, VP, VP, VP, VP]),
+    "omt_dw_dgrad_nhwc": (I32, [VP, VP, VP, VP, VP]),
+    "omt_dw_wgrad_nhwc_workspace": (SZ, [VP]),
+    "omt_dw_wgrad_nhwc": (I32, [VP, VP, VP, VP, VP, SZ, VP]),
     "omt_pointwise_layouts": (I32, [ctypes.c_int, I64, I64, I64, VP, ctypes.c_int, VP, ctypes.c_int, ctypes.c_float, VP,
                                     ctypes.c_int, VP]),
     "omt_log_softmax_fwd": (I32, [I64, I64, VP, VP, VP]),

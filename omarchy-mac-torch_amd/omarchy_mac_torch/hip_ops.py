@@ -656,6 +656,48 @@ def adaptive_avg_pool2d_backward_nhwc(g, x_shape):
     return gx
 
 
+def depthwise_conv2d_nhwc(x, w, bias=None, stride=1, padding=None):
+    """Depthwise convolution over channels-last x (omt_dw_fwd_nhwc); y channels_last."""
+    x, w, bias = _need_cl(x, "x"), _need(w, "w", 4), _need(bias, "bias", 1)
+    padding = w.shape[2] // 2 if padding is None else padding
+    g = _dw_geo(x.shape, w.shape, stride, padding)
+    y = torch.empty((g.n, g.co, g.oh, g.ow), device=x.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_dw_fwd_nhwc(ctypes.byref(g), _ptr(x), _ptr(w), _ptr(bias), _ptr(y), _stream(x.device)),
+          "depthwise_conv2d_nhwc")
+    return y
+
+
+def depthwise_dgrad_nhwc(gy, w, x_shape, stride=1, padding=None):
+    gy, w = _need_cl(gy, "gy"), _need(w, "w", 4)
+    padding = w.shape[2] // 2 if padding is None else padding
+    g = _dw_geo(x_shape, w.shape, stride, padding)
+    gx = torch.empty(tuple(x_shape), device=gy.device, dtype=torch.float32, memory_format=_CL)
+    check(L.omt_dw_dgrad_nhwc(ctypes.byref(g), _ptr(gy), _ptr(w), _ptr(gx), _stream(gy.device)),
+          "depthwise_dgrad_nhwc")
+    return gx
+
+
+def depthwise_wgrad_nhwc(x, gy, ks, stride=1, padding=None):
+    x, gy = _need_cl(x, "x"), _need_cl(gy, "gy")
+    padding = ks // 2 if padding is None else padding
+    n, c, ih, iw = x.shape
+    g = _lib.conv_geo(n, c, c, ih, iw, ks, stride, padding)
+    gw = torch.empty((c, 1, ks, ks), device=x.device, dtype=torch.float32)
+    ws, nb = _workspace(L.omt_dw_wgrad_nhwc_workspace(ctypes.byref(g)), x.device)
+    check(L.omt_dw_wgrad_nhwc(ctypes.byref(g), _ptr(x), _ptr(gy), _ptr(gw), _ptr(ws), nb, _stream(x.device)),
+          "depthwise_wgrad_nhwc")
+    return gw
+
+
+def channel_scale_nhwc(x, s):
+    """x * s for channels-last x [n, c, h, w] and s [n, c, 1, 1] (omt_channel_scale_nhwc); channels_last output."""
+    x, s = _need_cl(x, "x"), _need(s, "s", 4)
+    n, c, h, w = x.shape
+    y = torch.empty_like(x, memory_format=_CL)
+    check(L.omt_channel_scale_nhwc(n, c, h * w, _ptr(x), _ptr(s), _ptr(y), _stream(x.device)), "channel_scale_nhwc")
+    return y
+
+
 def plane_sum_nhwc(x, scale=1.0):
     """scale * the sum of each channels-last plane of x: [n, c] (omt_plane_sum_nhwc)."""
     x = _need_cl(x, "x")

@@ -59,6 +59,17 @@ static Tensor conv_forward(const Tensor& x_, const Tensor& w_, const std::option
           "convolution (channels last)");
     return y;
   }
+  if (kind != OMT_CONV_DENSE && is_cl(x_)) {  // channels-last depthwise: the NHWC kernel, a channels-last output
+    Tensor w = contig(w_);  // [c][1][ks][ks]: the same memory in either order
+    omt_conv_geo g = conv_geo(x_.size(0), x_.size(1), w.size(0), x_.size(2), x_.size(3), w.size(2), stride[0],
+                              padding[0]);
+    cover(g.oh >= 1 && g.ow >= 1, "empty output");
+    Tensor y = empty_dev_cl({g.n, g.co, g.oh, g.ow});
+    const int st = omt_dw_fwd_nhwc(&g, fp(x_), fp(w), fp(b), fpm(y), cur_stream());
+    cover(st != OMT_UNSUPPORTED, "channels-last depthwise size");
+    check(st, "convolution (depthwise, channels last)");
+    return y;
+  }
   Tensor x = contig(x_), w = contig(w_);
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
   cover(g.oh >= 1 && g.ow >= 1, "empty output");
@@ -81,8 +92,8 @@ static Tensor convolution_(const Tensor& x, const Tensor& w, const std::optional
   return conv_forward(x, w, bias, stride, padding, dilation, transposed, groups, false);
 }
 
-// Backward of a channels-last dense convolution: grads in channels-last order, each from the NHWC kernels where they
-// cover it (grad input: co % 16 == 0; grad weight: co a multiple of 4), else from the NCHW kernels.
+// Backward of a channels-last dense convolution: grads in channels-last order, from the NHWC kernels (grad weight of
+// co not a multiple of 4: the NCHW kernel and its result converted).
 static std::tuple<Tensor, Tensor, Tensor> conv_backward_cl(const Tensor& gy_, const Tensor& x_, const Tensor& w_,
                                                            IntArrayRef stride, IntArrayRef padding,
                                                            std::array<bool, 3> mask) {
@@ -93,21 +104,13 @@ static std::tuple<Tensor, Tensor, Tensor> conv_backward_cl(const Tensor& gy_, co
   Tensor gx, gw, gb;
   void* s = cur_stream();
   if (mask[0]) {
-    if (g.co % 16 == 0) {
-      Tensor w = contig_cl(w_);
-      gx = empty_dev_cl(x_.sizes());
-      tune_conv(OMT_DIR_DGRAD_NHWC, g);
-      Tensor ws = workspace(omt_conv_dgrad_nhwc_workspace(&g));
-      check(omt_conv_dgrad_nhwc(&g, fp(gy), fp(w), fpm(gx), wsptr(ws), wsbytes(ws), s),
-            "convolution_backward (input, channels last)");
-    } else {
-      Tensor gyc = contig(gy_), w = contig(w_);
-      Tensor t = empty_dev(x_.sizes());
-      tune_conv(OMT_DIR_DGRAD, g);
-      Tensor ws = workspace(omt_conv_dgrad_workspace(&g));
-      check(omt_conv_dgrad(&g, fp(gyc), fp(w), fpm(t), wsptr(ws), wsbytes(ws), s), "convolution_backward (input)");
-      gx = contig_cl(t);
-    }
+    Tensor w = contig_cl(w_);
+    gx = empty_dev_cl(x_.sizes());
+    // co not a multiple of 16: one fixed element-by-element gather, nothing to tune
+    if (g.co % 16 == 0) tune_conv(OMT_DIR_DGRAD_NHWC, g);
+    Tensor ws = workspace(omt_conv_dgrad_nhwc_workspace(&g));
+    check(omt_conv_dgrad_nhwc(&g, fp(gy), fp(w), fpm(gx), wsptr(ws), wsbytes(ws), s),
+          "convolution_backward (input, channels last)");
   }
   if (mask[1]) {
     if (g.co % 4 == 0) {
@@ -141,6 +144,32 @@ static std::tuple<Tensor, Tensor, Tensor> convolution_backward_(const Tensor& gy
   const int kind = kind_of(x_, w_, stride, padding, dilation, transposed, groups);
   cover(kind != OMT_CONV_NONE && f32(gy_), "dilated, transposed, grouped or non-square convolution");
   if (kind == OMT_CONV_DENSE && channels_last(x_, w_)) return conv_backward_cl(gy_, x_, w_, stride, padding, mask);
+  if (kind != OMT_CONV_DENSE && is_cl(x_)) {  // channels-last depthwise
+    Tensor gy = contig_cl(gy_), w = contig(w_);
+    omt_conv_geo g = conv_geo(x_.size(0), x_.size(1), w.size(0), x_.size(2), x_.size(3), w.size(2), stride[0],
+                              padding[0]);
+    cover(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");
+    Tensor gx, gw, gb;
+    void* s = cur_stream();
+    if (mask[0]) {
+      gx = empty_dev_cl(x_.sizes());
+      const int st = omt_dw_dgrad_nhwc(&g, fp(gy), fp(w), fpm(gx), s);
+      cover(st != OMT_UNSUPPORTED, "channels-last depthwise size");
+      check(st, "convolution_backward (depthwise input, channels last)");
+    }
+    if (mask[1]) {
+      gw = empty_dev(w.sizes());
+      Tensor ws = workspace(omt_dw_wgrad_nhwc_workspace(&g));
+      const int st = omt_dw_wgrad_nhwc(&g, fp(x_), fp(gy), fpm(gw), wsptr(ws), wsbytes(ws), s);
+      cover(st != OMT_UNSUPPORTED, "channels-last depthwise size");
+      check(st, "convolution_backward (depthwise weight, channels last)");
+    }
+    if (mask[2]) {  // [n oh ow][c] rows: their column sums
+      gb = empty_dev({g.co});
+      check(omt_bias_grad(g.n * g.oh * g.ow, g.co, 1, fp(gy), fpm(gb), s), "convolution_backward (bias)");
+    }
+    return {gx, gw, gb};
+  }
   Tensor gy = contig(gy_), x = contig(x_), w = contig(w_);
   omt_conv_geo g = conv_geo(x.size(0), x.size(1), w.size(0), x.size(2), x.size(3), w.size(2), stride[0], padding[0]);
   cover(gy.size(0) == g.n && gy.size(1) == g.co && gy.size(2) == g.oh && gy.size(3) == g.ow, "gradient shape");

@@ -101,6 +101,12 @@ Tensor& add_t_(Tensor& a, const Tensor& b, const at::Scalar& alpha) {
     pw(OMT_PW_ADD_SCALAR, a, nullptr, (float)(alpha.toDouble() * b.item<double>()), a);
     return a;
   }
+  if (mixed_flat(a, b)) {  // a += alpha * b with b in the other memory order (autograd's gradient accumulation)
+    check(omt_pointwise_layouts(OMT_PW_ADD, a.size(0), a.size(1), a.size(2) * a.size(3), fp(a), is_cl(a) ? 1 : 0,
+                                fp(b), is_cl(b) ? 1 : 0, alpha.toFloat(), fpm(a), is_cl(a) ? 1 : 0, cur_stream()),
+          "add_ (mixed memory orders)");
+    return a;
+  }
   cover(same_flat(a, b), "contiguous float32, one shape");
   pw(OMT_PW_ADD, a, &b, alpha.toFloat(), a);
   return a;
@@ -123,8 +129,23 @@ bool channel_pair(const Tensor& big, const Tensor& s) {
   return dense(big) && dense(s) && big.dim() == 4 && s.dim() == 4 && s.size(0) == big.size(0) &&
          s.size(1) == big.size(1) && s.size(2) == 1 && s.size(3) == 1 && big.numel() > s.numel();
 }
+// x channels-last [N, C, H, W] times s [N, C, 1, 1]
+bool channel_pair_cl(const Tensor& big, const Tensor& s) {
+  return is_dev(big) && f32(big) && is_cl(big) && dense(s) && s.dim() == 4 && s.size(0) == big.size(0) &&
+         s.size(1) == big.size(1) && s.size(2) == 1 && s.size(3) == 1;
+}
 Tensor mul_t(const Tensor& a, const Tensor& b) {
   if (host_scalar(b) && flat(a) && b.is_floating_point()) return unary(OMT_PW_SCALE, a, b.item<float>());
+  const bool abl = channel_pair_cl(a, b), bal = channel_pair_cl(b, a);
+  if (abl || bal) {
+    const Tensor& big = abl ? a : b;
+    const Tensor& s = abl ? b : a;
+    Tensor y = empty_dev_cl(big.sizes());
+    check(omt_channel_scale_nhwc(big.size(0), big.size(1), big.size(2) * big.size(3), fp(big), fp(s), fpm(y),
+                                 cur_stream()),
+          "mul (channel scale, channels last)");
+    return y;
+  }
   const bool ab = channel_pair(a, b), ba = channel_pair(b, a);
   if (ab || ba) {
     const Tensor& big = ab ? a : b;

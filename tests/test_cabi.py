@@ -375,9 +375,9 @@ def test_ctypes_structs_match_the_header(tmp_path):
 def test_nhwc_plans_and_workspaces_host_side():
     """Channels-last directions: their own tile tables (the nine staged gather tiles; the four grad-weight tiles), a
     plan whose K-block does not divide the gathered channels runs as tile 5, workspaces of the plans' sizes (grad
-    input always re-packs the filter), and the coverage conditions (grad input co % 16, grad weight co % 4; a forward
-    of ci % 16 != 0 runs its fixed element-by-element plan, no K split, so no workspace) as empty workspaces and
-    OMT_UNSUPPORTED, all without a GPU."""
+    input always re-packs the filter), and the coverage condition (grad weight co % 4; a forward of ci % 16 != 0 and
+    a grad input of co % 16 != 0 run their fixed element-by-element plan, no K split: the forward needs no
+    workspace, grad input only its packed filter) as workspaces and OMT_UNSUPPORTED, all without a GPU."""
     from omarchy_mac_torch import _lib
     L = _lib.L
     L.omt_conv_clear_plans()
@@ -411,10 +411,10 @@ def test_nhwc_plans_and_workspaces_host_side():
         assert L.omt_conv_set_plan(W, ctypes.byref(g), ctypes.byref(_lib.ConvPlan(4, 1))) == _lib.OMT_INVALID
         # coverage: no workspace and OMT_UNSUPPORTED before anything is launched (pointers are never touched)
         odd = _lib.conv_geo(2, 6, 18, 8, 8, 3, 1, 1)
-        for ws in (L.omt_conv_fwd_nhwc_workspace, L.omt_conv_dgrad_nhwc_workspace, L.omt_conv_wgrad_nhwc_workspace):
-            assert ws(ctypes.byref(odd)) == 0
+        assert L.omt_conv_fwd_nhwc_workspace(ctypes.byref(odd)) == 0
+        assert L.omt_conv_wgrad_nhwc_workspace(ctypes.byref(odd)) == 0
+        assert L.omt_conv_dgrad_nhwc_workspace(ctypes.byref(odd)) == 18 * 6 * 9 * 4  # the packed filter alone
         fake = ctypes.c_void_p(16)
-        assert L.omt_conv_dgrad_nhwc(ctypes.byref(odd), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
         assert L.omt_conv_wgrad_nhwc(ctypes.byref(odd), fake, fake, fake, None, 0, None) == _lib.OMT_UNSUPPORTED
         assert L.omt_conv_fwd_nhwc(ctypes.byref(g), None, fake, None, 0, fake, None, 0, None) == _lib.OMT_INVALID
     finally:

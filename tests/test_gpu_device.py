@@ -624,18 +624,19 @@ def _train_channels_last(base, data, make_opt, device, compiled=False):
     return out
 
 
+@pytest.mark.parametrize("name", ["resnet18", "mobilenet_v3_small"])
 @pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
-def test_channels_last_resnet18_against_cpu(model_plans, compiled):
-    """BASELINE config 3 with the model and its batches channels_last, eager and under the compile backend (its
+def test_channels_last_models_against_cpu(model_plans, name, compiled):
+    """BASELINE configs 3 and 4 with the model and its batches channels_last, eager and under the compile backend (its
     fused convolution + BatchNorm ops composed from the channels-last kernels): five training steps within 1e-3 of
-    PyTorch CPU fp32 (on this trajectory CPU fp32 itself is 2.6e-3 from float64 at the sixth,
-    where the bound measures rounding noise: the NCHW test of the same data keeps six), no fallbacks, and nothing
-    delegated to torch's kernels: BatchNorm, the
-    pools, the activations, the global pool's gradient meeting the ReLU mask, the 3-channel stem convolution and the
-    optimizer run channels-last kernels: a step converts no tensor's memory order."""
+    PyTorch CPU fp32 (on the ResNet-18 trajectory CPU fp32 itself is 2.6e-3 from float64 at the
+    sixth, where the bound measures rounding noise: the NCHW test of the same data keeps six), no fallbacks, and
+    nothing delegated to torch's kernels: the convolutions (the 3-channel stem and the depthwise ones too),
+    BatchNorm, the pools, the activations, the squeeze-excite scale and sums, the global pool's gradient meeting the
+    ReLU mask and the optimizer run channels-last kernels: a step converts no tensor's memory order."""
     omt = model_plans
     core = omt.native.core
-    base, data, make_opt = _config_data("resnet18", steps=5)
+    base, data, make_opt = _config_data(name, steps=5)
     cpu, cpu64 = _train(base, data, make_opt, "cpu"), _train(base, data, make_opt, "cpu", torch.float64)
     core.count_delegated(True)
     try:
@@ -643,7 +644,7 @@ def test_channels_last_resnet18_against_cpu(model_plans, compiled):
         delegated = dict(core.delegated_counts())
     finally:
         core.count_delegated(False)
-    _assert_north_star(dev, cpu, cpu64, f"resnet18 channels_last {'compiled' if compiled else 'eager'}")
+    _assert_north_star(dev, cpu, cpu64, f"{name} channels_last {'compiled' if compiled else 'eager'}")
     conv = {k: delegated.pop(k) for k in list(delegated) if k.startswith("copy_ (layout conversion)")}
     print(f"layout conversions in {len(data)} steps: {conv}", flush=True)
     assert not delegated, delegated

@@ -52,13 +52,15 @@ NHWC_SHAPES = [
     (2, 64, 256, 56, 56, 1, 1, 0),
     (2, 256, 64, 28, 28, 1, 1, 0),
     (4, 512, 512, 2, 2, 3, 1, 1),     # ResNet-18 layer4 at 64x64: the cost model splits K
-    (3, 16, 36, 10, 10, 3, 1, 1),     # 36 output channels: a partial row tile (grad input then not covered)
-    (2, 32, 18, 8, 6, 11, 4, 5),      # 11x11 stride 4, 18 output channels: scalar stores, neither grad covered
+    (3, 16, 36, 10, 10, 3, 1, 1),     # 36 output channels: a partial row tile, a narrow grad input
+    (2, 32, 18, 8, 6, 11, 4, 5),      # 11x11 stride 4, 18 output channels: scalar stores, grad weight not covered
     # input channels not a multiple of 16: the forward gathers element by element; of 4: so do grad weight's columns
     (2, 3, 64, 32, 32, 7, 2, 3),      # the ResNet stem (at 64x64 input: 32x32 here)
     (3, 6, 16, 9, 11, 3, 1, 1),
     (2, 20, 32, 10, 10, 3, 2, 1),     # 20 channels: narrow forward, float4 grad-weight columns
     (2, 1, 16, 12, 12, 5, 1, 2),      # one input channel
+    (2, 24, 88, 14, 14, 1, 1, 0),     # MobileNetV3's expand: 88 output channels, a narrow grad input
+    (2, 16, 24, 9, 9, 3, 2, 1),       # stride 2, narrow grad input over four phases
 ]
 
 
@@ -69,8 +71,8 @@ def _ids(s):
 @pytest.mark.parametrize("shape", NHWC_SHAPES, ids=_ids)
 def test_conv_nhwc_fwd_dgrad_wgrad(cuda, ops, shape):
     """Forward (bias + ReLU), grad input and grad weight of channels-last tensors against the oracle; the outputs
-    come back channels_last. Any input channel count; grad input needs co % 16 == 0 and grad weight co % 4 == 0:
-    other shapes raise Unsupported (the device then runs the NCHW kernels)."""
+    come back channels_last. Any channel counts but grad weight's co % 4 != 0, which raises Unsupported (the device
+    then runs the NCHW kernel)."""
     from omarchy_mac_torch._lib import Unsupported
     n, ci, co, h, w, ks, s, p = shape
     rng = np.random.default_rng(sum(shape))
@@ -80,13 +82,9 @@ def test_conv_nhwc_fwd_dgrad_wgrad(cuda, ops, shape):
     y_ref = orc.conv_fwd(x, wt, b, s, p, relu=True)
     assert orc.rel_l2(host(y), y_ref) <= TOL
     gy = rnd(rng, *y_ref.shape)
-    if co % 16 == 0:
-        gx = ops.conv2d_dgrad_nhwc(dev_cl(gy, cuda), dev_cl(wt, cuda), x.shape, s, p)
-        assert gx.is_contiguous(memory_format=CL)
-        assert orc.rel_l2(host(gx), orc.conv_dgrad(gy, wt, x.shape, s, p)) <= TOL
-    else:
-        with pytest.raises(Unsupported):
-            ops.conv2d_dgrad_nhwc(dev_cl(gy, cuda), dev_cl(wt, cuda), x.shape, s, p)
+    gx = ops.conv2d_dgrad_nhwc(dev_cl(gy, cuda), dev_cl(wt, cuda), x.shape, s, p)
+    assert gx.is_contiguous(memory_format=CL)
+    assert orc.rel_l2(host(gx), orc.conv_dgrad(gy, wt, x.shape, s, p)) <= TOL
     if co % 4 == 0:
         gw = ops.conv2d_wgrad_nhwc(dev_cl(x, cuda), dev_cl(gy, cuda), ks, s, p)
         assert gw.is_contiguous(memory_format=CL)
@@ -97,12 +95,10 @@ def test_conv_nhwc_fwd_dgrad_wgrad(cuda, ops, shape):
 
 
 def test_conv_nhwc_output_channels_not_covered(cuda, ops):
-    """Grad input needs co % 16 == 0 and grad weight co % 4 == 0: other outputs raise Unsupported, nothing runs."""
+    """Grad weight needs co % 4 == 0: other outputs raise Unsupported, nothing runs."""
     from omarchy_mac_torch._lib import Unsupported
     rng = np.random.default_rng(3)
-    x, wt, gy = rnd(rng, 2, 6, 8, 8), rnd(rng, 18, 6, 3, 3), rnd(rng, 2, 18, 8, 8)
-    with pytest.raises(Unsupported):
-        ops.conv2d_dgrad_nhwc(dev_cl(gy, cuda), dev_cl(wt, cuda), x.shape, 1, 1)
+    x, gy = rnd(rng, 2, 6, 8, 8), rnd(rng, 2, 18, 8, 8)
     with pytest.raises(Unsupported):
         ops.conv2d_wgrad_nhwc(dev_cl(x, cuda), dev_cl(gy, cuda), 3, 1, 1)
 
@@ -240,7 +236,7 @@ def test_conv_nhwc_full_size(cuda, ops, name, shape):
 CL_CASES = [
     # (n, ci, co, h, ks, s, p, bias): covered by the NHWC kernels in every direction
     (2, 32, 64, 14, 3, 1, 1, False), (2, 64, 32, 9, 1, 2, 0, True), (3, 16, 48, 11, 5, 2, 2, False),
-    # 3 input channels (the narrow NHWC forward and grad weight), 36 output channels (grad input in NCHW)
+    # 3 input channels (the narrow NHWC forward and grad weight), 36 output channels (a narrow grad input)
     (2, 3, 16, 23, 7, 2, 3, False), (2, 16, 36, 10, 3, 1, 1, True),
 ]
 
@@ -435,3 +431,50 @@ def test_plane_sum_nhwc_and_mixed_order_pointwise(cuda, ops):
         assert torch.equal(out.cpu(), torch.add(tg, ty, alpha=0.5))
         out = ops.pointwise_layouts(_lib.OMT_PW_RELU, dev_cl(g, cuda), None, 0.0, out_nhwc)
         assert torch.equal(out.cpu(), torch.relu(tg))
+
+
+DW_NHWC = [
+    # (n, c, h, w, ks, stride, pad)
+    (2, 96, 28, 28, 5, 1, 2),   # MobileNetV3 layers
+    (4, 16, 56, 56, 3, 2, 1),
+    (2, 576, 7, 7, 5, 1, 2),
+    (2, 6, 9, 11, 3, 1, 1),     # c % 4 != 0: one channel per thread
+    (3, 40, 14, 14, 7, 1, 3),
+    (2, 8, 10, 10, 4, 3, 1),
+    (1, 12, 5, 5, 11, 1, 5),    # the largest filter
+]
+
+
+@pytest.mark.parametrize("case", DW_NHWC, ids=lambda c: "n{}c{}h{}w{}k{}s{}p{}".format(*c))
+def test_depthwise_nhwc(cuda, ops, case):
+    """omt_dw_fwd_nhwc (with bias) / omt_dw_dgrad_nhwc / omt_dw_wgrad_nhwc over channels_last tensors against the
+    oracle, outputs channels_last; forward and grad input equal to the general NCHW kernels' results bit for bit
+    where those run (stride != 1 or an unmatched padding: not the LDS-tiled stride-1 kernels)."""
+    n, c, h, w, ks, s, p = case
+    rng = np.random.default_rng(sum(case))
+    x, wt, b = rnd(rng, n, c, h, w), rnd(rng, c, 1, ks, ks, scale=ks ** -1.0), rnd(rng, c, scale=0.1)
+    tw, tb = dev(wt, cuda), dev(b, cuda)
+    y = ops.depthwise_conv2d_nhwc(dev_cl(x, cuda), tw, tb, s, p)
+    assert y.is_contiguous(memory_format=CL)
+    y_ref = orc.dw_fwd(x, wt, b, s, p)
+    assert orc.rel_l2(host(y), y_ref) <= TOL
+    gy = rnd(rng, *y_ref.shape)
+    gx = ops.depthwise_dgrad_nhwc(dev_cl(gy, cuda), tw, x.shape, s, p)
+    assert gx.is_contiguous(memory_format=CL)
+    assert orc.rel_l2(host(gx), orc.dw_dgrad(gy, wt, x.shape, s, p)) <= TOL
+    gw = ops.depthwise_wgrad_nhwc(dev_cl(x, cuda), dev_cl(gy, cuda), ks, s, p)
+    assert orc.rel_l2(host(gw), orc.dw_wgrad(x, gy, ks, s, p)) <= TOL
+    if s != 1 or 2 * p != ks - 1:
+        assert np.array_equal(host(y), host(ops.depthwise_conv2d(dev(x, cuda), tw, tb, s, p)))
+        assert np.array_equal(host(gx), host(ops.depthwise_dgrad(dev(gy, cuda), tw, x.shape, s, p)))
+
+
+def test_channel_scale_nhwc(cuda, ops):
+    """The squeeze-excite scale over channels_last planes, x * s with s [n, c, 1, 1], equal to PyTorch CPU's product
+    bit for bit (float4 and scalar channel runs)."""
+    rng = np.random.default_rng(5)
+    for n, c, h, w in ((4, 96, 14, 14), (2, 6, 5, 7), (3, 576, 7, 7)):
+        x, sc = rnd(rng, n, c, h, w), rnd(rng, n, c, 1, 1)
+        y = ops.channel_scale_nhwc(dev_cl(x, cuda), dev(sc, cuda))
+        assert y.is_contiguous(memory_format=CL)
+        assert torch.equal(y.cpu(), torch.from_numpy(x) * torch.from_numpy(sc))
