@@ -71,9 +71,11 @@ __device__ __forceinline__ int64_t voffset(int v, int ch, int c, int hw, int hwv
   return ((int64_t)nn * c + ch) * hw + (int64_t)e * vec;
 }
 
-// Block-wide sum of two doubles over 256 threads; result valid in thread 0.
+// Block-wide sum of two doubles over NT threads (the wave sums added in wave order); result valid in thread 0.
+template <int NT = 256>
 __device__ __forceinline__ void block_sum2(double& a, double& b) {
-  __shared__ double sa[4], sb[4];
+  constexpr int NW = NT / 64;
+  __shared__ double sa[NW], sb[NW];
   a = wave_sum(a);
   b = wave_sum(b);
   const int wave = threadIdx.x >> 6;
@@ -83,8 +85,13 @@ __device__ __forceinline__ void block_sum2(double& a, double& b) {
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    a = sa[0] + sa[1] + sa[2] + sa[3];
-    b = sb[0] + sb[1] + sb[2] + sb[3];
+    if constexpr (NW == 4) {  // the 256-thread order, kept as it was
+      a = sa[0] + sa[1] + sa[2] + sa[3];
+      b = sb[0] + sb[1] + sb[2] + sb[3];
+    } else {
+      a = sa[0], b = sb[0];
+      for (int w = 1; w < NW; ++w) a += sa[w], b += sb[w];
+    }
   }
 }
 
@@ -554,6 +561,15 @@ constexpr int64_t kFusedMax = 8192;
 // leaving ResNet-18's 512-channel layers and MobileNet's 576-channel 7x7 layers two rounds of workgroups). Unused
 // register slots hold values that add exact zeros, so both sizes give the same results.
 constexpr int64_t kFusedSmall = 2048;
+// Channels of up to kFusedLarge elements run the same one-launch kernels with 1024 threads (16 waves) per workgroup,
+// at most 32 floats per thread (MobileNetV3's 28x28 layers at batch 32, 25088 elements, otherwise two or three
+// launches: forward 11.5 against 16 us; backward 9-11 against 14.5 us at 24-40 channels, 19.5-20 against 21 us at
+// 88-96, where one CU's bandwidth per channel bounds it). The backward holds three operands: up to kFusedLargeBwd elements, float4
+// vectors only (28 floats per operand in the 128 registers a thread of a 1024-thread workgroup has; the scalar form
+// would spill). The BatchNorm + max pool keeps its two launches above kFusedMax: the pool pass of one workgroup per
+// channel, reading its outputs back, took twice as long as the split apply + pool.
+constexpr int64_t kFusedLarge = 32768, kFusedLargeBwd = 28672;
+constexpr int kFusedLargeThreads = 1024;
 
 // PARTS: x holds `slices` convolution partials of pstride elements each; every element is summed over them in slice
 // order (the convolution slice sum's order, so xo, written with the sums, equals the summed convolution output).
@@ -588,8 +604,8 @@ __device__ __forceinline__ void pool_window(const PoolArgs& pa, int oy, int ox, 
 }
 
 // POOL: the channel's outputs also go to LDS, from which the workgroup max-pools every image of the channel.
-template <int VEC, bool PARTS = false, bool POOL = false, int MAXE = (int)kFusedMax>
-__global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __restrict__ x,
+template <int VEC, bool PARTS = false, bool POOL = false, int MAXE = (int)kFusedMax, int NT = 256>
+__global__ void __launch_bounds__(NT) bn_train_fused_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
                                                              const float* rm, const float* rv, double momentum,
@@ -603,16 +619,18 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
                                                              const PoolArgs pool = PoolArgs{}) {
   using V = typename VecT<VEC>::T;
   __shared__ float coef[2];
-  __shared__ float chan[POOL ? MAXE : 1];  // POOL: the channel's outputs, image by image
+  // POOL: the channel's outputs, image by image, in LDS (MAXE <= kFusedMax)
+  static_assert(!POOL || MAXE <= (int)kFusedMax, "the pool reads the channel from LDS");
+  __shared__ float chan[POOL ? MAXE : 1];
   const int ch = blockIdx.x;
   float shift = x[(int64_t)ch * hw];
   if (PARTS)
     for (int z = 1; z < slices; ++z) shift += x[z * pstride + (int64_t)ch * hw];
-  constexpr int NR = MAXE / (256 * VEC);  // vectors per thread
+  constexpr int NR = MAXE / (NT * VEC);  // vectors per thread
   V r[NR];
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
-    const int vv = (int)threadIdx.x + u * 256;
+    const int vv = (int)threadIdx.x + u * NT;
     if (vv < sp.nv) {
       r[u] = *reinterpret_cast<const V*>(x + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
     } else {
@@ -620,7 +638,7 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       for (int i = 0; i < VEC; ++i) vset(r[u], i, shift);
     }
   }
-  if (PARTS && sp.nv <= 256) {  // one vector per thread: kReduceBatch slices' loads in flight, added in slice order
+  if (PARTS && sp.nv <= NT) {  // one vector per thread: kReduceBatch slices' loads in flight, added in slice order
     const int vv = (int)threadIdx.x;
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
@@ -639,18 +657,18 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       V t[NR];
 #pragma unroll
       for (int u = 0; u < NR; ++u) {
-        const int vv = (int)threadIdx.x + u * 256;
+        const int vv = (int)threadIdx.x + u * NT;
         if (vv < sp.nv) t[u] = *reinterpret_cast<const V*>(x + z * pstride + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
       }
 #pragma unroll
       for (int u = 0; u < NR; ++u)
-        if ((int)threadIdx.x + u * 256 < sp.nv) vadd(r[u], t[u]);
+        if ((int)threadIdx.x + u * NT < sp.nv) vadd(r[u], t[u]);
     }
   }
   if (PARTS) {
 #pragma unroll
     for (int u = 0; u < NR; ++u) {
-      const int vv = (int)threadIdx.x + u * 256;
+      const int vv = (int)threadIdx.x + u * NT;
       if (vv < sp.nv) *reinterpret_cast<V*>(xo + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)) = r[u];
     }
   }
@@ -663,7 +681,7 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
       s1 += d;
       s2 += d * d;
     }
-  block_sum2(s1, s2);
+  block_sum2<NT>(s1, s2);
   if (threadIdx.x == 0) {
     const BnStats st = bn_finalize(s1, s2, (double)shift, (double)sp.nv * VEC, momentum, eps, rm, rv, save_mean,
                                    save_invstd, new_rm, new_rv, ch, true);
@@ -675,7 +693,7 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
   const float sc = coef[0], sh = coef[1];
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
-    const int vv = (int)threadIdx.x + u * 256;
+    const int vv = (int)threadIdx.x + u * NT;
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
       V t = r[u], q, z;
@@ -697,7 +715,7 @@ __global__ void __launch_bounds__(256) bn_train_fused_kernel(const float* __rest
   if constexpr (POOL) {
     __syncthreads();
     const int per = pool.oh * pool.ow, total = sp.nv * VEC / hw * per;
-    for (int o = (int)threadIdx.x; o < total; o += 256) {
+    for (int o = (int)threadIdx.x; o < total; o += NT) {
       const int img = o / per, r = o - img * per, oy = r / pool.ow, ox = r - oy * pool.ow;
       const float* cp = chan + img * hw;
       float best;
@@ -800,8 +818,8 @@ __device__ __forceinline__ void run_side_sum(const SideSums& ss, int64_t b) {
 
 // PARTS: g holds `slices` convolution partials of pstride elements each, summed here in slice order (the convolution
 // slice sum's order) before g2 is added; workgroups past the c channels run the side slice sums.
-template <int VEC, bool RES, bool PARTS = false, int MAXE = (int)kFusedMax>
-__global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ g2,
+template <int VEC, bool RES, bool PARTS = false, int MAXE = (int)kFusedMax, int NT = 256>
+__global__ void __launch_bounds__(NT) bn_bwd_fused_kernel(const float* __restrict__ g, const float* __restrict__ g2,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ ry,
                                                            const float* __restrict__ mean,
@@ -819,11 +837,11 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   }
   const int ch = blockIdx.x;
   const float mu = mean[ch], inv = invstd[ch];
-  constexpr int NR = MAXE / (256 * VEC);  // vectors per thread
+  constexpr int NR = MAXE / (NT * VEC);  // vectors per thread
   V rg[NR], rx[NR], rr[NR];
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
-    const int vv = (int)threadIdx.x + u * 256;
+    const int vv = (int)threadIdx.x + u * NT;
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
       rg[u] = *reinterpret_cast<const V*>(g + off);
@@ -839,7 +857,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       }
     }
   }
-  if (PARTS && sp.nv <= 256) {  // one vector per thread: kReduceBatch slices' loads in flight, added in slice order
+  if (PARTS && sp.nv <= NT) {  // one vector per thread: kReduceBatch slices' loads in flight, added in slice order
     const int vv = (int)threadIdx.x;
     if (vv < sp.nv) {
       const int64_t off = voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC);
@@ -858,19 +876,19 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       V t[NR];
 #pragma unroll
       for (int u = 0; u < NR; ++u) {
-        const int vv = (int)threadIdx.x + u * 256;
+        const int vv = (int)threadIdx.x + u * NT;
         if (vv < sp.nv) t[u] = *reinterpret_cast<const V*>(g + z * pstride + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC));
       }
 #pragma unroll
       for (int u = 0; u < NR; ++u)
-        if ((int)threadIdx.x + u * 256 < sp.nv) vadd(rg[u], t[u]);
+        if ((int)threadIdx.x + u * NT < sp.nv) vadd(rg[u], t[u]);
     }
   }
   if (PARTS) {  // then g2
     if (RES && g2) {
 #pragma unroll
       for (int u = 0; u < NR; ++u) {
-        const int vv = (int)threadIdx.x + u * 256;
+        const int vv = (int)threadIdx.x + u * NT;
         if (vv < sp.nv) vadd(rg[u], *reinterpret_cast<const V*>(g2 + voffset(vv, ch, c, hw, sp.hwv, sp.div_hwv, VEC)));
       }
     }
@@ -886,7 +904,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
       s1 += (double)gz;
       s2 += (double)gz * (double)xhat;
     }
-  block_sum2(s1, s2);
+  block_sum2<NT>(s1, s2);
   if (threadIdx.x == 0) {
     if (dbeta) dbeta[ch] = (float)s1;
     if (dgamma) dgamma[ch] = (float)s2;
@@ -899,7 +917,7 @@ __global__ void __launch_bounds__(256) bn_bwd_fused_kernel(const float* __restri
   for (int i = 0; i < 5; ++i) k[i] = kc[i];
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
-    const int vv = (int)threadIdx.x + u * 256;
+    const int vv = (int)threadIdx.x + u * NT;
     if (vv < sp.nv) {
       V o, z;
 #pragma unroll
@@ -1026,6 +1044,17 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
       if (sm) OMT_BN_FUSED(1, (int)kFusedSmall); else OMT_BN_FUSED(1, (int)kFusedMax);
     }
 #undef OMT_BN_FUSED
+    return launch_check("bn_train_fused_kernel");
+  }
+  if (n * hw <= kFusedLarge) {
+    const bool vec = sp.vec == 4 && al16(y) && (!residual || al16(residual)) && al16(z);
+    const Split f = vec ? sp : bn_split(n, c, hw, false);
+#define OMT_BN_FUSED_L(V)                                                                                          \
+  hipLaunchKernelGGL((bn_train_fused_kernel<V, false, false, (int)kFusedLarge, kFusedLargeThreads>), dim3((unsigned)c), \
+                     dim3(kFusedLargeThreads), 0, s, x, gamma, beta, running_mean, running_var, momentum, eps, relu,      \
+                     residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f, 1, 0, nullptr, z)
+    if (vec) OMT_BN_FUSED_L(4); else OMT_BN_FUSED_L(1);
+#undef OMT_BN_FUSED_L
     return launch_check("bn_train_fused_kernel");
   }
   double* part = (double*)workspace;
@@ -1248,6 +1277,12 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
       if (sm) OMT_BN_BWD(1, (int)kFusedSmall); else OMT_BN_BWD(1, (int)kFusedMax);
     }
 #undef OMT_BN_BWD
+    return launch_check("bn_bwd_fused_kernel");
+  }
+  if (n * hw <= kFusedLargeBwd && sp.vec == 4) {
+    hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES, false, (int)kFusedLargeBwd, kFusedLargeThreads>),
+                       dim3((unsigned)c), dim3(kFusedLargeThreads), 0, s, g, g2, x, relu_y, save_mean, save_invstd,
+                       gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act);
     return launch_check("bn_bwd_fused_kernel");
   }
   double* part = (double*)workspace;

@@ -787,7 +787,8 @@ def test_depthwise_bn_loader_and_mobilenet_size(cuda, ops):
                                      (32, 64, 16, 16), (32, 512, 2, 2), (1, 16, 57, 31), (3, 5, 37, 41),
                                      (64, 16, 28, 28), (8, 3, 7, 9), (9, 5, 33, 35), (4, 8, 56, 56),
                                      (64, 64, 64, 64), (64, 64, 63, 65), (32, 96, 7, 7), (8, 16, 16, 16),
-                                     (9, 12, 15, 15), (2, 8, 33, 32)])
+                                     (9, 12, 15, 15), (2, 8, 33, 32), (32, 24, 28, 28), (32, 8, 32, 32),
+                                     (7, 3, 64, 64), (29, 4, 31, 33)])
 @pytest.mark.parametrize("relu", [False, True])
 def test_batch_norm_train_and_backward(cuda, ops, n, c, h, w, relu):
     rng = np.random.default_rng(n * 1000 + c)
