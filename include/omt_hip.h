@@ -513,6 +513,18 @@ int omt_channel_scale(int64_t planes, int64_t hw, const float* x, const float* s
 int omt_plane_broadcast(int64_t planes, int64_t hw, const float* v, float scale, float* y, void* stream);
 /* y[p] = scale * sum_i x[p][i] (sum or mean over the last two dims of an NCHW tensor). */
 int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float scale, float* y, void* stream);
+/* y[p] = scale * sum_i a[p][i] * b[p][i], each product rounded and the terms summed as omt_plane_sum sums (so equal to
+ * omt_pointwise(OMT_PW_MUL) followed by omt_plane_sum): a squeeze-excite gate's gradient, sum over a plane of g * x, in
+ * one launch. No counterpart in the reference (a multiply and a sum, csrc/elementwise.cpp, reduce.cpp). */
+int omt_plane_dot(int64_t planes, int64_t hw, const float* a, const float* b, float scale, float* y, void* stream);
+/* y[p][i] = g[p][i] * s[p] + v[p] * scale, each product rounded, then added (equal to omt_channel_scale,
+ * omt_plane_broadcast and an add): the gradient reaching a squeeze-excite block's input through the gate and through
+ * the plane mean, in one launch. No counterpart in the reference (three ops there). */
+int omt_se_gate_bwd(int64_t planes, int64_t hw, const float* g, const float* s, const float* v, float scale, float* y,
+                    void* stream);
+/* The same over channels-last planes: g, y [n][hw][c], s, v [n][c]. */
+int omt_se_gate_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, const float* s, const float* v, float scale,
+                         float* y, void* stream);
 /* The same over channels-last planes: y[img][ch] = scale * sum_p x[img][p][ch], x [n][hw][c] (a channels_last
  * tensor's memory), y [n][c]; n <= 65535. No counterpart in the reference, which reduces contiguous NCHW copies
  * (csrc/reduce.cpp, csrc/device.cpp:60-66). */

@@ -78,19 +78,56 @@ __global__ void __launch_bounds__(256) plane_scale_kernel(const float* __restric
   }
 }
 
+// A value the compiler must materialize as it stands: a product passed through it is rounded to float before any
+// later addition (no multiply-add contraction across it), as when a separate kernel stores it.
+__device__ __forceinline__ float rounded(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// The gradient reaching a squeeze-excite block's input through its two uses: y[p][i] = g[p][i] * s[p] + v[p] * scale
+// (the scale's gradient through the gate, plus the plane mean's broadcast gradient), the two products rounded and then
+// added as the separate multiply, broadcast and add would (no fused multiply-add).
+template <int VEC>
+__global__ void __launch_bounds__(256) se_gate_bwd_kernel(const float* __restrict__ g, const float* __restrict__ s,
+                                                          const float* __restrict__ v, float* __restrict__ y,
+                                                          int64_t planes, int hw, float scale, FastDiv dv) {
+  const int hv = hw / VEC;
+  const int64_t total = planes * hv;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t p = total < ((int64_t)1 << 32) ? (int64_t)fdiv((uint32_t)i, dv) : i / hv;
+    const float m = s[p], a = rounded(v[p] * scale);
+    if constexpr (VEC == 4) {
+      const float4 t = reinterpret_cast<const float4*>(g)[i];
+      reinterpret_cast<float4*>(y)[i] =
+          make_float4(rounded(t.x * m) + a, rounded(t.y * m) + a, rounded(t.z * m) + a, rounded(t.w * m) + a);
+    } else {
+      y[i] = rounded(g[i] * m) + a;
+    }
+  }
+}
+
 // y[p] = scale * sum_i x[p][i], one wave per plane, four planes per workgroup. Each lane sums a strided part of the
-// plane in order, then the wave adds the 64 lane sums with DPP (a fixed order).
+// plane in order, then the wave adds the 64 lane sums with DPP (a fixed order). DOT: the terms are x[p][i] * b[p][i]
+// (rounded products, as a separate multiply would store them), summed in the same order.
+template <bool DOT = false>
 __global__ void __launch_bounds__(256) plane_sum_kernel(const float* __restrict__ x, float* __restrict__ y,
-                                                        int64_t planes, int hw, float scale) {
+                                                        int64_t planes, int hw, float scale,
+                                                        const float* __restrict__ b = nullptr) {
   const int64_t plane = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (plane >= planes) return;  // whole waves leave together: wave_sum below runs with all 64 lanes
   const int lane = threadIdx.x & 63;
   const float* xp = x + plane * hw;
+  const float* bp = DOT ? b + plane * hw : nullptr;
   float acc = 0.f;
   for (int e0 = lane; e0 < hw; e0 += 256) {  // four loads in flight, added in the same order as one at a time
     float v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = e0 + 64 * j < hw ? xp[e0 + 64 * j] : 0.f;
+    for (int j = 0; j < 4; ++j) {
+      v[j] = e0 + 64 * j < hw ? xp[e0 + 64 * j] : 0.f;
+      if (DOT) v[j] = rounded(v[j] * (e0 + 64 * j < hw ? bp[e0 + 64 * j] : 0.f));
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (e0 + 64 * j < hw) acc += v[j];
@@ -102,20 +139,31 @@ __global__ void __launch_bounds__(256) plane_sum_kernel(const float* __restrict_
 // Large planes (kPlaneWG elements and more): one workgroup per plane. Each thread sums its float4 vectors (stride
 // 256, four loads in flight), then the wave sums (DPP) are added in wave order.
 constexpr int kPlaneWG = 1024;
-template <int VEC>
+template <int VEC, bool DOT = false>
 __global__ void __launch_bounds__(256) plane_sum_wg_kernel(const float* __restrict__ x, float* __restrict__ y, int hw,
-                                                           float scale) {
+                                                           float scale, const float* __restrict__ b = nullptr) {
   using V = typename std::conditional<VEC == 4, float4, float>::type;
   __shared__ float red[4];
   const int64_t plane = blockIdx.x;
   const V* xp = reinterpret_cast<const V*>(x + plane * hw);
+  const V* bp = DOT ? reinterpret_cast<const V*>(b + plane * hw) : nullptr;
   const int nv = hw / VEC;
   float acc = 0.f;
   for (int e0 = threadIdx.x; e0 < nv; e0 += 1024) {
     V v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (e0 + 256 * j < nv) v[j] = xp[e0 + 256 * j];
+      if (e0 + 256 * j < nv) {
+        v[j] = xp[e0 + 256 * j];
+        if constexpr (DOT) {
+          const V w = bp[e0 + 256 * j];
+          if constexpr (VEC == 4)
+            v[j] = make_float4(rounded(v[j].x * w.x), rounded(v[j].y * w.y), rounded(v[j].z * w.z),
+                               rounded(v[j].w * w.w));
+          else
+            v[j] = rounded(v[j] * w);
+        }
+      }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (e0 + 256 * j < nv) {
@@ -353,6 +401,26 @@ __global__ void __launch_bounds__(256) channel_scale_nhwc_kernel(const float* __
   }
 }
 
+// omt_se_gate_bwd over channels-last planes: y[img][p][ch] = g[img][p][ch] * s[img][ch] + v[img][ch] * scale.
+template <int VEC>
+__global__ void __launch_bounds__(256) se_gate_bwd_nhwc_kernel(const float* __restrict__ g, const float* __restrict__ s,
+                                                               const float* __restrict__ v, float* __restrict__ y,
+                                                               int64_t total_v, int64_t cv, int64_t hwcv, float scale) {
+  using V = typename std::conditional<VEC == 4, float4, float>::type;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total_v; i += (int64_t)gridDim.x * 256) {
+    const int64_t img = i / hwcv, j = i % cv;
+    const V t = reinterpret_cast<const V*>(g)[i];
+    const V m = reinterpret_cast<const V*>(s + img * cv * VEC)[j];
+    const V w = reinterpret_cast<const V*>(v + img * cv * VEC)[j];
+    if constexpr (VEC == 4)
+      reinterpret_cast<V*>(y)[i] = make_float4(
+          rounded(t.x * m.x) + rounded(w.x * scale), rounded(t.y * m.y) + rounded(w.y * scale),
+          rounded(t.z * m.z) + rounded(w.z * scale), rounded(t.w * m.w) + rounded(w.w * scale));
+    else
+      y[i] = rounded(t * m) + rounded(w * scale);
+  }
+}
+
 // y[img][ch] = scale * sum over the hw positions of x [n][hw][c] (channels-last planes). Workgroup (channel block,
 // image): thread t owns channel j = block * cb + t % cb and sums positions t / cb, + rl, ... (four loads in flight),
 // then the row lanes' sums are added in lane order: a fixed order.
@@ -490,16 +558,54 @@ OMT_EXPORT int omt_plane_sum(int64_t planes, int64_t hw, const float* x, float s
   if (planes == 0) return OMT_OK;
   if (hw >= kPlaneWG && planes < ((int64_t)1 << 31)) {
     if (hw % 4 == 0 && ((uintptr_t)x & 15) == 0)
-      hipLaunchKernelGGL(plane_sum_wg_kernel<4>, dim3((unsigned)planes), dim3(256), 0, stream_of(stream), x, y, (int)hw,
-                         scale);
+      hipLaunchKernelGGL((plane_sum_wg_kernel<4, false>), dim3((unsigned)planes), dim3(256), 0, stream_of(stream), x, y,
+                         (int)hw, scale, nullptr);
     else
-      hipLaunchKernelGGL(plane_sum_wg_kernel<1>, dim3((unsigned)planes), dim3(256), 0, stream_of(stream), x, y, (int)hw,
-                         scale);
+      hipLaunchKernelGGL((plane_sum_wg_kernel<1, false>), dim3((unsigned)planes), dim3(256), 0, stream_of(stream), x, y,
+                         (int)hw, scale, nullptr);
     return launch_check("plane_sum_wg_kernel");
   }
-  hipLaunchKernelGGL(plane_sum_kernel, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, stream_of(stream), x, y, planes,
-                     (int)hw, scale);
+  hipLaunchKernelGGL(plane_sum_kernel<false>, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, stream_of(stream), x, y,
+                     planes, (int)hw, scale, nullptr);
   return launch_check("plane_sum_kernel");
+}
+
+OMT_EXPORT int omt_plane_dot(int64_t planes, int64_t hw, const float* a, const float* b, float scale, float* y,
+                             void* stream) {
+  if (!a || !b || !y) return fail(OMT_INVALID, "omt_plane_dot: null pointer");
+  if (planes < 0 || hw < 0 || hw >= ((int64_t)1 << 31) || cdiv(planes, 4) >= ((int64_t)1 << 31))
+    return fail(OMT_INVALID, "omt_plane_dot: size");
+  if (planes == 0) return OMT_OK;
+  if (hw >= kPlaneWG && planes < ((int64_t)1 << 31)) {
+    if (hw % 4 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0)
+      hipLaunchKernelGGL((plane_sum_wg_kernel<4, true>), dim3((unsigned)planes), dim3(256), 0, stream_of(stream), a, y,
+                         (int)hw, scale, b);
+    else
+      hipLaunchKernelGGL((plane_sum_wg_kernel<1, true>), dim3((unsigned)planes), dim3(256), 0, stream_of(stream), a, y,
+                         (int)hw, scale, b);
+    return launch_check("plane_sum_wg_kernel (dot)");
+  }
+  hipLaunchKernelGGL(plane_sum_kernel<true>, dim3((unsigned)cdiv(planes, 4)), dim3(256), 0, stream_of(stream), a, y,
+                     planes, (int)hw, scale, b);
+  return launch_check("plane_sum_kernel (dot)");
+}
+
+OMT_EXPORT int omt_se_gate_bwd(int64_t planes, int64_t hw, const float* g, const float* s, const float* v,
+                               float scale, float* y, void* stream) {
+  if (!g || !s || !v || !y) return fail(OMT_INVALID, "omt_se_gate_bwd: null pointer");
+  if (planes < 0 || hw < 0 || hw >= ((int64_t)1 << 31)) return fail(OMT_INVALID, "omt_se_gate_bwd: size");
+  if (planes == 0 || hw == 0) return OMT_OK;
+  const bool v4 = hw % 4 == 0 && al16(y) && al16(g);
+  const int64_t total = planes * (v4 ? hw / 4 : hw);
+  const dim3 grid(grid1d(total, 256, 8192));
+  const FastDiv dv = make_fastdiv((uint32_t)(v4 ? hw / 4 : hw));
+  if (v4)
+    hipLaunchKernelGGL(se_gate_bwd_kernel<4>, grid, dim3(256), 0, stream_of(stream), g, s, v, y, planes, (int)hw,
+                       scale, dv);
+  else
+    hipLaunchKernelGGL(se_gate_bwd_kernel<1>, grid, dim3(256), 0, stream_of(stream), g, s, v, y, planes, (int)hw,
+                       scale, dv);
+  return launch_check("se_gate_bwd_kernel");
 }
 
 OMT_EXPORT int omt_log_softmax_fwd(int64_t rows, int64_t cols, const float* x, float* y, void* stream) {
@@ -621,4 +727,21 @@ OMT_EXPORT int omt_channel_scale_nhwc(int64_t n, int64_t c, int64_t hw, const fl
     hipLaunchKernelGGL(channel_scale_nhwc_kernel<1>, grid, dim3(256), 0, stream_of(stream), x, scale, y, total_v, cv,
                        hw * cv);
   return launch_check("channel_scale_nhwc_kernel");
+}
+
+OMT_EXPORT int omt_se_gate_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g, const float* s, const float* v,
+                                    float scale, float* y, void* stream) {
+  if (!g || !s || !v || !y) return fail(OMT_INVALID, "omt_se_gate_bwd_nhwc: null pointer");
+  if (n < 0 || c < 1 || hw < 0 || n * c * hw >= ((int64_t)1 << 46)) return fail(OMT_INVALID, "omt_se_gate_bwd_nhwc: size");
+  if (n == 0 || hw == 0) return OMT_OK;
+  const bool v4 = c % 4 == 0 && al16(g) && al16(s) && al16(v) && al16(y);
+  const int64_t cv = v4 ? c / 4 : c, total_v = n * hw * cv;
+  const dim3 grid(grid1d(total_v, 256, 8192));
+  if (v4)
+    hipLaunchKernelGGL(se_gate_bwd_nhwc_kernel<4>, grid, dim3(256), 0, stream_of(stream), g, s, v, y, total_v, cv,
+                       hw * cv, scale);
+  else
+    hipLaunchKernelGGL(se_gate_bwd_nhwc_kernel<1>, grid, dim3(256), 0, stream_of(stream), g, s, v, y, total_v, cv,
+                       hw * cv, scale);
+  return launch_check("se_gate_bwd_nhwc_kernel");
 }

@@ -143,6 +143,9 @@ SIGNATURES = {
     "omt_plane_broadcast": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
     "omt_plane_sum": (I32, [I64, I64, VP, ctypes.c_float, VP, VP]),
     "omt_plane_sum_nhwc": (I32, [I64, I64, I64, VP, ctypes.c_float, VP, VP]),
+    "omt_plane_dot": (I32, [I64, I64, VP, VP, ctypes.c_float, VP, VP]),
+    "omt_se_gate_bwd": (I32, [I64, I64, VP, VP, VP, ctypes.c_float, VP, VP]),
+    "omt_se_gate_bwd_nhwc": (I32, [I64, I64, I64, VP, VP, VP, ctypes.c_float, VP, VP]),
     "omt_channel_scale_nhwc": (I32, [I64, I64, I64, VP, VP, VP, VP]),
     "omt_dw_fwd_nhwc": (I32, [VP, VP, VP, VP, VP, VP]),
     "omt_dw_dgrad_nhwc": (I32, [VP, VP, VP, VP, VP]),

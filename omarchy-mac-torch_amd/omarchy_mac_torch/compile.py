@@ -6,9 +6,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
 
   0. training BatchNorm whose new running statistics are only copied back into its running-stat inputs
      -> omt.bn_train_ (statistics updated in place, no copies), taking along a following ReLU, residual add + ReLU
-     (y = relu(bn(x) + r), the end of a ResNet basic block) or hardswish (MobileNetV3; the hardswish's input, saved
-     for its backward, comes out as a fourth output); the batch counters' increments (one add and one copy each)
-     become a single _foreach_add_;
+     (y = relu(bn(x) + r), the end of a ResNet basic block), residual add (y = bn(x) + r, the end of a MobileNetV3
+     inverted residual) or hardswish (MobileNetV3; the hardswish's input, saved for its backward, comes out as a
+     fourth output); the batch counters' increments (one add and one copy each) become a single _foreach_add_;
   1. training BatchNorm (`_native_batch_norm_legit_functional`) whose normalized output only feeds a ReLU
      -> omt.bn_relu_train (statistics, normalize and ReLU in the library's BN kernels);
   2. its backward, `native_batch_norm_backward(threshold_backward(g, y, 0), ...)` -> omt.bn_relu_backward (the ReLU
@@ -23,7 +23,9 @@ The rewrites then route the hot path to fused device ops, and the graph runs op 
      max-pooled: omt.bn_train_ -> max_pool2d_with_indices -> omt.bn_train_pool_ (the pool inside the BatchNorm's
      apply pass: the ResNet stem); a BatchNorm backward
      (2, or a plain training one) whose incoming gradient is a dense convolution's grad input -> omt.conv_bn_backward,
-     where the BatchNorm backward sums the convolution's grad-input partials and runs its grad-weight slice sum.
+     where the BatchNorm backward sums the convolution's grad-input partials and runs its grad-weight slice sum;
+  4. a squeeze-excite block's backward: sum(mul(g, x), [2, 3]) -> omt.plane_dot, and mul(g, gate) plus the plane
+     mean's broadcast gradient -> omt.se_gate_backward (one launch each instead of two and three).
 
 Before AOTAutograd, on the graph Dynamo hands the backend: a squeeze-excite block's excitation MLP,
 hardsigmoid(linear(relu(linear(z)))) -> omt.se_mlp (two launches; its registered backward, omt.se_mlp_backward, two).
@@ -116,7 +118,7 @@ def _same_shape(a, b):
 
 
 def fuse_bn_train_in_place(graph):
-    count = {"bn": 0, "relu": 0, "add_relu": 0, "hardswish": 0}
+    count = {"bn": 0, "relu": 0, "add_relu": 0, "add": 0, "hardswish": 0}
     for n in list(graph.nodes):
         if n.op != "call_function" or n.target is not aten._native_batch_norm_legit_functional.default:
             continue
@@ -151,9 +153,11 @@ def fuse_bn_train_in_place(graph):
             # saved statistics must come later
             stats_later = all(order[v] > order[u] for i in (1, 2) if outs.get(i) is not None for v in outs[i].users)
             if (other is not out0 and isinstance(other, Node) and _on_device_f32(other, 4) and _same_shape(other, x)
-                    and relu is not None and relu.op == "call_function" and relu.target is aten.relu.default
                     and stats_later):
-                act, res, last, add, anchor = 1, other, relu, u, u
+                if relu is not None and relu.op == "call_function" and relu.target is aten.relu.default:
+                    act, res, last, add, anchor = 1, other, relu, u, u
+                else:  # a residual add with no activation after it (MobileNetV3's inverted residuals)
+                    act, res, last, anchor = 0, other, u, u
         fused = _call_before(graph, anchor, omt.bn_train_.default, (x, w, b, rm, rv, momentum, eps, act, res))
         y = _call_before(graph, anchor, operator.getitem, (fused, 0), meta_from=last)
         for i in (1, 2):
@@ -179,7 +183,7 @@ def fuse_bn_train_in_place(graph):
             graph.erase_node(dead)
         count["bn"] += 1
         if res is not None:
-            count["add_relu"] += 1
+            count["add_relu" if act == 1 else "add"] += 1
         elif act:
             count["relu" if act == 1 else "hardswish"] += 1
     return count
@@ -521,13 +525,75 @@ def fuse_conv_bn_backward(graph):
     return count
 
 
+# ---- the squeeze-excite backward ----
+
+def _shape(n):
+    v = _meta(n)
+    return tuple(v.shape) if isinstance(v, torch.Tensor) else None
+
+
+def fuse_se_backward(graph):
+    """The backward of a squeeze-excite block x * gate(mean(x)) as AOTAutograd traces it, in two rewrites:
+    sum(mul(g, x), [2, 3], keepdim) -> omt.plane_dot(g, x) (the gate's gradient, one launch instead of two), and
+    add(mul(g, s), div(expand(v), hw)) with s, v [N, C, 1, 1] -> omt.se_gate_backward(g, s, v, 1 / hw) (the input's
+    gradient through the gate and through the mean, one launch instead of three). The intermediate values must have
+    no other use; float32 device tensors."""
+    count = {"plane_dot": 0, "gate": 0}
+    for n in list(graph.nodes):
+        if n.op != "call_function":
+            continue
+        if n.target is aten.sum.dim_IntList and len(n.args) >= 3 and n.args[2] is True and not n.kwargs:
+            m = n.args[0]
+            dims = sorted(d % 4 for d in n.args[1]) if isinstance(n.args[1], (list, tuple)) else None
+            if (dims == [2, 3] and isinstance(m, Node) and m.op == "call_function" and m.target is aten.mul.Tensor
+                    and _sole_user(m) is n and len(m.args) == 2 and not m.kwargs
+                    and all(_on_device_f32(a, 4) for a in m.args) and _shape(m.args[0]) == _shape(m.args[1])):
+                fused = _call_before(graph, n, omt.plane_dot.default, m.args, meta_from=n)
+                n.replace_all_uses_with(fused)
+                graph.erase_node(n)
+                graph.erase_node(m)
+                count["plane_dot"] += 1
+            continue
+        if n.target is not aten.add.Tensor or len(n.args) != 2 or n.kwargs or not _on_device_f32(n, 4):
+            continue
+        shape = _shape(n)
+        mul = div = None
+        for a in n.args:
+            if not (isinstance(a, Node) and a.op == "call_function" and _sole_user(a) is n):
+                continue
+            if a.target is aten.mul.Tensor and len(a.args) == 2 and not a.kwargs:
+                mul = a
+            elif a.target is aten.div.Scalar and len(a.args) == 2 and not a.kwargs:
+                div = a
+        if mul is None or div is None:
+            continue
+        e = div.args[0]
+        if not (isinstance(e, Node) and e.op == "call_function" and e.target is aten.expand.default
+                and _sole_user(e) is div and isinstance(div.args[1], (int, float)) and div.args[1] != 0):
+            continue
+        v = e.args[0]
+        gate = [a for a in mul.args if _shape(a) == shape[:2] + (1, 1)]
+        big = [a for a in mul.args if _shape(a) == shape]
+        if len(gate) != 1 or len(big) != 1 or _shape(v) != shape[:2] + (1, 1):
+            continue
+        if not all(_on_device_f32(t, 4) for t in (gate[0], big[0], v)):
+            continue
+        fused = _call_before(graph, n, omt.se_gate_backward.default, (big[0], gate[0], v, 1.0 / div.args[1]),
+                             meta_from=n)
+        n.replace_all_uses_with(fused)
+        for dead in (n, mul, div, e):
+            graph.erase_node(dead)
+        count["gate"] += 1
+    return count
+
+
 def _rewrite(gm):
     g = gm.graph
     stats = {"bn_train_in_place": fuse_bn_train_in_place(g), "batch_counters": merge_batch_counters(g),
              "bn_relu": fuse_bn_relu_train(g), "bn_relu_res_backward": fuse_bn_relu_res_backward(g),
              "bn_relu_backward": fuse_bn_relu_backward(g), "bn_hardswish_backward": fuse_bn_hardswish_backward(g),
              "bn_train_pool": fuse_bn_train_pool(g), "conv_bn_train": fuse_conv_bn_train(g),
-             "conv_bn_backward": fuse_conv_bn_backward(g),
+             "conv_bn_backward": fuse_conv_bn_backward(g), "se_backward": fuse_se_backward(g),
              "conv_epilogue": fuse_conv_epilogues(g)}
     g.eliminate_dead_code()
     g.lint()

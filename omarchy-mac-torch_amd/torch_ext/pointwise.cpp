@@ -298,7 +298,65 @@ Tensor nll_bwd(const Tensor& g, const Tensor& x, const Tensor& t, const std::opt
   return gx;
 }
 
+// ---- squeeze-excite backward (omt:: ops the compile backend rewrites to) ----
+
+// g * s + v * scale, s and v [N, C, 1, 1] (or [N, C]): the gradient reaching a squeeze-excite input through the gate
+// and through the plane mean (a multiply, the mean's broadcast and an add in the graph)
+Tensor se_gate_backward_ref(const Tensor& g, const Tensor& s, const Tensor& v, double scale) {
+  const int64_t n = g.size(0), c = g.size(1);
+  return at::add(at::mul(g, s.reshape({n, c, 1, 1})), at::mul(v.reshape({n, c, 1, 1}), scale));
+}
+Tensor se_gate_backward_dev(const Tensor& g, const Tensor& s, const Tensor& v, double scale) {
+  cover(g.dim() == 4 && s.numel() == g.size(0) * g.size(1) && v.numel() == s.numel(), "[N, C, H, W] with [N, C] gates");
+  cover(dense(s) && dense(v), "contiguous float32 gates");
+  if (is_cl(g) && f32(g)) {  // channels-last planes
+    Tensor y = empty_dev_cl(g.sizes());
+    check(omt_se_gate_bwd_nhwc(g.size(0), g.size(1), g.size(2) * g.size(3), fp(g), fp(s), fp(v), (float)scale, fpm(y),
+                               cur_stream()),
+          "omt::se_gate_backward (channels last)");
+    return y;
+  }
+  cover(dense(g), "contiguous float32");
+  Tensor y = empty_dev(g.sizes());
+  check(omt_se_gate_bwd(g.size(0) * g.size(1), g.size(2) * g.size(3), fp(g), fp(s), fp(v), (float)scale, fpm(y),
+                        cur_stream()),
+        "omt::se_gate_backward");
+  return y;
+}
+Tensor se_gate_backward_k(const Tensor& g, const Tensor& s, const Tensor& v, double scale) {
+  return dev_or_ref<&se_gate_backward_dev, &se_gate_backward_ref>("omt::se_gate_backward", g, s, v, scale);
+}
+
+// sum over the last two dims of a * b, [N, C, 1, 1] (a multiply and a sum in the graph)
+Tensor plane_dot_ref(const Tensor& a, const Tensor& b) { return at::sum(at::mul(a, b), {2, 3}, true); }
+Tensor plane_dot_dev(const Tensor& a, const Tensor& b) {
+  cover(a.dim() == 4 && a.sizes().equals(b.sizes()), "two [N, C, H, W] operands");
+  if (is_cl(a) || is_cl(b)) return plane_dot_ref(a, b);  // channels-last: the elementwise and plane-sum kernels
+  cover(dense(a) && dense(b), "contiguous float32");
+  const int64_t n = a.size(0), c = a.size(1);
+  Tensor y = empty_dev({n, c, 1, 1});
+  check(omt_plane_dot(n * c, a.size(2) * a.size(3), fp(a), fp(b), 1.f, fpm(y), cur_stream()), "omt::plane_dot");
+  return y;
+}
+Tensor plane_dot_k(const Tensor& a, const Tensor& b) {
+  return dev_or_ref<&plane_dot_dev, &plane_dot_ref>("omt::plane_dot", a, b);
+}
+
 }  // namespace
+
+TORCH_LIBRARY_FRAGMENT(omt, m) {
+  // g * s + v * scale (s, v: [N, C] gates of [N, C, H, W] planes); the sum of a * b over each plane, [N, C, 1, 1]
+  m.def("se_gate_backward(Tensor g, Tensor s, Tensor v, float scale) -> Tensor");
+  m.def("plane_dot(Tensor a, Tensor b) -> Tensor");
+}
+TORCH_LIBRARY_IMPL(omt, CompositeExplicitAutograd, m) {
+  m.impl("se_gate_backward", &se_gate_backward_ref);
+  m.impl("plane_dot", &plane_dot_ref);
+}
+TORCH_LIBRARY_IMPL(omt, PrivateUse1, m) {
+  m.impl("se_gate_backward", &se_gate_backward_k);
+  m.impl("plane_dot", &plane_dot_k);
+}
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   HotOps(m)

@@ -27,7 +27,8 @@ def _fake(mode, dev, shape, dtype=torch.float32):
 
 
 def _block_tail_graph(oc, tail, save_stats=False):
-    """Forward graph of BatchNorm(x) followed by `tail` ("relu", "add_relu" or "none"), plus two batch counters.
+    """Forward graph of BatchNorm(x) followed by `tail` ("relu", "add_relu", "add", "hardswish" or "none"), plus two
+    batch counters.
     save_stats: the new running statistics are also graph outputs (AOTAutograd saves them for the backward)."""
     dev = oc.DEVICE
     mode = FakeTensorMode()
@@ -53,6 +54,8 @@ def _block_tail_graph(oc, tail, save_stats=False):
         s = g.call_function(aten.add.Tensor, (gi[0], r))
         s.meta["val"] = _fake(mode, dev, shp)
         y = g.call_function(aten.relu.default, (s,))
+    elif tail == "add":  # a residual add with no activation (MobileNetV3's inverted residuals)
+        y = g.call_function(aten.add.Tensor, (r, gi[0]))
     y.meta["val"] = _fake(mode, dev, shp)
     a1 = g.call_function(aten.add.Tensor, (t1, 1))
     a2 = g.call_function(aten.add.Tensor, (t2, 1))
@@ -78,12 +81,13 @@ def _targets(gm):
 
 
 @pytest.mark.parametrize("save_stats", [False, True])
-@pytest.mark.parametrize("tail", ["relu", "add_relu", "none", "hardswish"])
+@pytest.mark.parametrize("tail", ["relu", "add_relu", "add", "none", "hardswish"])
 def test_bn_train_in_place_and_counters(oc, tail, save_stats):
     gm = _block_tail_graph(oc, tail, save_stats)
     ref = copy.deepcopy(gm)
     stats = oc.fuse_bn_train_in_place(gm.graph)
     assert stats["bn"] == 1 and stats["add_relu"] == (tail == "add_relu") and stats["relu"] == (tail == "relu")
+    assert stats["add"] == (tail == "add")
     assert stats["hardswish"] == (tail == "hardswish")
     assert oc.merge_batch_counters(gm.graph) == 2
     gm.graph.eliminate_dead_code()
@@ -94,8 +98,8 @@ def test_bn_train_in_place_and_counters(oc, tail, save_stats):
     assert aten.copy_.default not in t and aten._native_batch_norm_legit_functional.default not in t
     assert aten.relu.default not in t and aten.add.Tensor not in t and aten.hardswish.default not in t
     fused = next(n for n in gm.graph.nodes if n.target is torch.ops.omt.bn_train_.default)
-    assert fused.args[7] == {"none": 0, "relu": 1, "add_relu": 1, "hardswish": 2}[tail]
-    assert (fused.args[8] is not None) == (tail == "add_relu")
+    assert fused.args[7] == {"none": 0, "relu": 1, "add_relu": 1, "add": 0, "hardswish": 2}[tail]
+    assert (fused.args[8] is not None) == (tail in ("add_relu", "add"))
     # same results and buffer updates as the original graph, on CPU tensors
     a, b = _inputs(1), _inputs(1)
     out_ref, out_new = ref(*a), gm(*b)
@@ -519,3 +523,59 @@ def test_squeeze_excite_rewrite(oc, case):
     gy = torch.randn(y.shape, generator=gen)
     for a, b in zip(torch.autograd.grad(y_ref, args, gy), torch.autograd.grad(y, args2, gy)):
         torch.testing.assert_close(b, a, rtol=1e-6, atol=1e-6)
+
+
+def _se_backward_graph(oc, case):
+    """Backward graph of a squeeze-excite block x * s (s the gate, [N, C, 1, 1]) as AOTAutograd traces it: the gate's
+    gradient sum(mul(g, x), [2, 3], keepdim) and the input's gradient mul(g, s) + div(expand(v), hw), with the
+    variations `case` names."""
+    dev = oc.DEVICE
+    mode = FakeTensorMode()
+    g = Graph()
+    n, c, h, w = 2, 3, 4, 5
+
+    def ph(name, shape):
+        node = g.placeholder(name)
+        node.meta["val"] = _fake(mode, dev, shape)
+        return node
+
+    def call(target, args, shape):
+        node = g.call_function(target, args)
+        node.meta["val"] = _fake(mode, dev, shape)
+        return node
+
+    go, x, s4, v4 = ph("g", (n, c, h, w)), ph("x", (n, c, h, w)), ph("s", (n, c, 1, 1)), ph("v", (n, c, 1, 1))
+    m1 = call(aten.mul.Tensor, (go, x), (n, c, h, w))
+    sm = call(aten.sum.dim_IntList, (m1, [2, 3] if case != "other_dims" else [1, 2], True),
+              (n, c, 1, 1) if case != "other_dims" else (n, 1, 1, w))
+    m2 = call(aten.mul.Tensor, (s4, go) if case == "gate_first" else (go, s4), (n, c, h, w))
+    e = call(aten.expand.default, (v4, [n, c, h, w]), (n, c, h, w))
+    d = call(aten.div.Scalar, (e, h * w), (n, c, h, w))
+    a = call(aten.add.Tensor, (d, m2) if case == "gate_first" else (m2, d), (n, c, h, w))
+    outs = (sm, a) + ((m2,) if case == "second_use" else ())
+    g.output(outs)
+    return GraphModule(torch.nn.Module(), g), (n, c, h, w)
+
+
+@pytest.mark.parametrize("case", ["plain", "gate_first", "second_use", "other_dims"])
+def test_se_backward_rewrite(oc, case):
+    """The squeeze-excite backward becomes omt.plane_dot (gate gradient) and omt.se_gate_backward (input gradient),
+    with the same values on CPU tensors; a second use of the gated product keeps the input gradient apart, a sum over
+    other dims keeps the gate gradient apart."""
+    gm, (n, c, h, w) = _se_backward_graph(oc, case)
+    ref = copy.deepcopy(gm)
+    stats = oc.fuse_se_backward(gm.graph)
+    gm.graph.eliminate_dead_code()
+    gm.graph.lint()
+    gm.recompile()
+    assert stats == {"plane_dot": 0 if case == "other_dims" else 1, "gate": 0 if case == "second_use" else 1}
+    t = _targets(gm)
+    assert t.count(torch.ops.omt.plane_dot.default) == stats["plane_dot"]
+    assert t.count(torch.ops.omt.se_gate_backward.default) == stats["gate"]
+    if stats["gate"]:
+        assert aten.div.Scalar not in t and aten.expand.default not in t and aten.add.Tensor not in t
+    gen = torch.Generator().manual_seed(5)
+    args = [torch.randn(n, c, h, w, generator=gen), torch.randn(n, c, h, w, generator=gen),
+            torch.randn(n, c, 1, 1, generator=gen), torch.randn(n, c, 1, 1, generator=gen)]
+    for got, want in zip(gm(*args), ref(*args)):
+        torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-7)

@@ -1209,7 +1209,8 @@ def test_autograd_over_cuda_tensors_is_refused_clearly(clean):
 
 def test_compiled_squeeze_excite_runs_fused(clean):
     """Under the compile backend each of MobileNetV3's six squeeze-excite MLPs runs as omt.se_mlp (two launches forward,
-    two backward: counted per kernel), with the loss and the gradients matching the model run op by op: all gradients
+    two backward: counted per kernel) and each block's backward as omt.plane_dot and omt.se_gate_backward (one launch
+    each), with the loss and the gradients matching the model run op by op: all gradients
     together at rel-L2 1e-4, each parameter's within 1e-3 of its norm plus 1e-6 of the whole gradient's (the bias of a
     BatchNorm that feeds a convolution and another BatchNorm has a gradient that is zero but for rounding, ~1e-8,
     where both paths' rounding differs entirely), and no fallback."""
@@ -1230,7 +1231,9 @@ def test_compiled_squeeze_excite_runs_fused(clean):
     torch.cuda.synchronize()
     counts = core.kernel_counts(True)
     se = {k: v for k, v in counts.items() if k.startswith("se_")}
-    assert se == {k: 6 for k in ("se_hidden_kernel", "se_out_kernel", "se_bwd_hidden_kernel", "se_bwd_input_kernel")}, se
+    assert se == {k: 6 for k in ("se_hidden_kernel", "se_out_kernel", "se_bwd_hidden_kernel", "se_bwd_input_kernel",
+                                 "se_gate_bwd_kernel")}, se
+    assert sum(v for k, v in counts.items() if k.endswith("(dot)")) == 6, counts
     assert abs(float(l_comp) - float(l_eager)) <= 1e-4 * abs(float(l_eager))
     ge = torch.cat([p.grad.cpu().reshape(-1) for p in eager.parameters()])
     gc = torch.cat([p.grad.cpu().reshape(-1) for p in comp.parameters()])

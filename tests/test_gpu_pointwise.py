@@ -338,3 +338,25 @@ def test_squeeze_excite_mlp(omt, n, c, r):
     for got, ref in zip(dgrads, grads):
         assert got.shape == ref.shape and rel(got, ref) <= 1e-5
     assert not omt.FALLBACKS, dict(omt.FALLBACKS)
+
+
+@pytest.mark.parametrize("n,c,h,w", [(32, 576, 7, 7), (32, 16, 112, 112), (3, 5, 9, 11), (32, 96, 28, 28)])
+def test_squeeze_excite_backward_ops(omt, n, c, h, w):
+    """omt::plane_dot (the gate's gradient, sum over each plane of g * x) and omt::se_gate_backward (g * s plus the
+    plane mean's broadcast gradient v / hw) on the device: the same bits as the separate multiply, plane sum,
+    channel scale, broadcast and add they replace (wave-per-plane and workgroup-per-plane sums, float4 and scalar
+    planes, channels-last planes), and against float64 CPU sums; no fallback."""
+    omt.FALLBACKS.clear()
+    g = torch.Generator().manual_seed(n + c + h)
+    go, x = torch.randn(n, c, h, w, generator=g), torch.randn(n, c, h, w, generator=g)
+    s, v = torch.rand(n, c, 1, 1, generator=g), torch.randn(n, c, 1, 1, generator=g)
+    dg, dx, ds, dv = (t.to(omt.DEVICE) for t in (go, x, s, v))
+    dot = torch.ops.omt.plane_dot(dg, dx)
+    assert torch.equal(dot.cpu(), (dg * dx).sum((2, 3), keepdim=True).cpu())
+    assert rel(dot, (go.double() * x.double()).sum((2, 3), keepdim=True)) <= 1e-6
+    gate = torch.ops.omt.se_gate_backward(dg, ds, dv, 1.0 / (h * w))
+    assert torch.equal(gate.cpu(), (dg * ds + dv.expand(n, c, h, w) / (h * w)).cpu())
+    assert rel(gate, go.double() * s.double() + v.double() / (h * w)) <= 1e-6
+    gate_cl = torch.ops.omt.se_gate_backward(dg.contiguous(memory_format=torch.channels_last), ds, dv, 1.0 / (h * w))
+    assert gate_cl.is_contiguous(memory_format=torch.channels_last) and torch.equal(gate_cl.cpu(), gate.cpu())
+    assert not omt.FALLBACKS, dict(omt.FALLBACKS)
