@@ -17,8 +17,8 @@ configs 2, 3 and 4 (plaincnn_b128, resnet18_b32, mobilenetv3_b32): device ms/ste
 the same steps on PyTorch CPU fp32 from the same weights and data, the speed-up and the 5-step loss agreement.
 
 The roofline object reports the dominant kernel, the implicit-GEMM gather (conv_gather_kernel, its direct-to-LDS
-form conv_gather_dl_kernel, or the persistent 1x1 conv1x1_stream_kernel, whichever the tuned plan of each layer
-runs), from its forward launches: algorithmic FLOPs per launch over the launch's HIP-event duration, measured on the
+form conv_gather_dl_kernel, or the persistent 1x1 kernels conv1x1_stream_kernel and conv1x1_wst_kernel, whichever
+the tuned plan of each layer runs), from its forward launches: algorithmic FLOPs per launch over the launch's HIP-event duration, measured on the
 launch stream inside the timed steps. cpu_baseline is the reference's CPU path, PyTorch CPU fp32 convolutions (the
 reference runs and checks these ops on PyTorch's CPU kernels), timed on a bounded sample of the same workload with
 every host core and, as the reference's README states its CPU numbers, with 4 threads; oracle_cpu_baseline times
@@ -168,12 +168,12 @@ def torch_cpu_baseline(layers, batch, secs_per_layer=0.8):
                              "sample": f"the same at 4 threads, {gf4:.0f} GFLOP in {secs4:.1f} s"}}
 
 
-GATHER_KERNELS = ("conv_gather_kernel", "conv_gather_dl_kernel", "conv1x1_stream_kernel")
+GATHER_KERNELS = ("conv_gather_kernel", "conv_gather_dl_kernel", "conv1x1_stream_kernel", "conv1x1_wst_kernel")
 
 
 def _is_gather(kernel_name):
     """The implicit-GEMM gather kernels: staged conv_gather_kernel, direct-to-LDS conv_gather_dl_kernel and the
-    persistent 1x1 conv1x1_stream_kernel."""
+    persistent 1x1 conv1x1_stream_kernel and conv1x1_wst_kernel."""
     return any(k in kernel_name for k in GATHER_KERNELS)
 
 
@@ -1226,7 +1226,8 @@ def main():
                                 "C1 AlexNet conv1 b16 3x224x224 -> 64x55x55, 11x11 s4 p2, fwd+dgrad+wgrad"),
                    "gflop_per_step": round(sw["step_flops"] / 1e9, 2), "layout": "NCHW"},
         "frac_of_peak": round(value * 1e12 / PEAK_FP32_MFMA, 4),
-        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel / conv1x1_stream_kernel (forward launches)",
+        "roofline": {"kernel": "conv_gather_kernel / conv_gather_dl_kernel / conv1x1_stream_kernel / conv1x1_wst_kernel "
+                               "(forward launches)",
                      "bound": "mfma", "achieved": round(sw["achieved"], 3), "peak": PEAK_FP32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": round(sw["achieved"] * 1e12 / PEAK_FP32_MFMA, 4),
                      "traffic": traffic["bytes"] if traffic else None,

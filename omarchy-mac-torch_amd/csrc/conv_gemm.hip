@@ -824,6 +824,177 @@ __global__ void __launch_bounds__(256, 2) conv1x1_stream_kernel(const GatherArgs
   }
 }
 
+// 1x1, stride 1, unpadded convolutions (and their grad input) whose reduction K = C is 64 or 128: at ResNet-50's
+// 56^2 and 28^2 expansions the output is four times the input, and a launch that computes a tile and then stores it
+// adds the store time to the MFMA time (the workgroups of a CU run in step and store together). Filter-stationary:
+// each wave keeps its 16 TJ output channels' whole filter rows in registers for the workgroup's life, and only the
+// input streams, pixel tile by pixel tile (BQ pixels x K), through two LDS buffers: the loads of tile v + 2 are
+// issued when tile v starts and tile v + 1 goes to LDS before tile v's MFMAs, one barrier per tile. Two accumulator
+// sets: tile v - 1's outputs leave 16 channels at a time between tile v's K-blocks, so the stores stream out while
+// the MFMAs run. The GEMM runs transposed, pixels as the MFMA rows: accumulator rows 4 g + r of lane group g are
+// four consecutive pixels of one output channel, staged through the wave's LDS rows into whole row runs. At MFMA step s
+// lane group g supplies k = 16 b + 4 g + s of K-block b, the staged tiles' k order, so each output sums its K terms in
+// their order. The host checks: one 1x1 s1 unpadded phase, no split, no BN loader or epilogue statistics, H W % 4 == 0
+// (float4 pixel runs stay in one image), x and y 16-byte aligned, y below 2 GiB.
+template <int K, int TJ, int BQ, int OCC>
+__global__ void __launch_bounds__(256, OCC) conv1x1_wst_kernel(const GatherArgs a, const int tpw) {
+  constexpr int KP = K + 4, TI = BQ / 16, KB = K / 16, NP = K * BQ / 2048;  // NP: float4 pairs per thread per tile
+  static_assert(BQ == 32 || BQ == 64, "pixel tile");
+  constexpr int GPB = (TJ + KB - 1) / KB;  // 16-channel store groups after each K-block
+  constexpr int SP = BQ + 4, LPR = BQ / 4, RPI = 64 / LPR;  // staging pitch; lanes per output row, rows per store
+  static_assert(K == 64 || K == 128, "K");
+  // row pitch K + 4: the 16 lanes of a ds_read_b128 quarter read rows 16 i + 0..15 at 16-byte offsets 4 apart mod 64
+  // banks, disjoint
+  __shared__ __attribute__((aligned(16))) float xs[2][BQ * KP];
+  __shared__ __attribute__((aligned(16))) float stg_all[4][16 * SP];  // each wave's output staging rows
+
+  const TileId tile = xcd_block_tile(kTileGroup);
+  const Phase ph = a.ph[0];
+  const int Q = ph.Q, ntq = (Q + BQ - 1) / BQ;
+  const int tq0 = tile.x * tpw, ntiles = min(ntq, tq0 + tpw) - tq0;
+  if (ntiles <= 0) return;
+  const int t = threadIdx.x, lane = t & 63, g = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int P = a.P, HW = a.H * a.W, C = a.C;
+  const int pw = tile.y * (64 * TJ) + wave * (16 * TJ);  // the wave's first output channel
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+  const __amdgpu_buffer_rsrc_t yr = make_rsrc(a.y, (uint32_t)((int64_t)Q * P * 4));
+  float* const stg = stg_all[wave];
+
+  // the wave's filter rows: wv[j][4 b + s] = A[pw + 16 j + l16][16 b + 4 g + s], 0 past P
+  float wv[TJ][K / 4], bj[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int p = pw + 16 * j + l16;
+#pragma unroll
+    for (int b = 0; b < KB; ++b)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        wv[j][4 * b + s] = bload(wr, p < P ? (uint32_t)((ph.woff + p * K + 16 * b + 4 * g + s) * 4) : kOOB, 0);
+    bj[j] = a.bias && p < P ? a.bias[p] : 0.f;
+  }
+
+  // input tile loads: thread t takes pixel quad pq = t % (BQ / 4) of the tile and k rows KR r + 2 kp + {0, 1}
+  // (kp = t / (BQ / 4), KR = 512 / BQ k rows per pass)
+  constexpr int NQ = BQ / 4, KR = 2 * 256 / NQ;
+  const int pq = t % NQ, kp = t / NQ;
+  // byte offset of x[n][2 kp][pixel] for the thread's quad of tile tq (past Q: out of range; the rows' uniform terms
+  // go in the scalar offset)
+  auto xbase = [&](int tq) __attribute__((always_inline)) -> uint32_t {
+    const int q = tq * BQ + 4 * pq;
+    if (q >= Q) return kOOB;
+    const uint32_t n = fdiv((uint32_t)q, ph.div_ohw);
+    return (uint32_t)(((int)n * C * HW + 2 * kp * HW + (q - (int)n * HW)) * 4);
+  };
+  float4 ld[2][NP][2];
+  auto gload = [&](int tq, const int set) __attribute__((always_inline)) {
+    const uint32_t xb = xbase(tq);
+#pragma unroll
+    for (int r = 0; r < NP; ++r)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) ld[set][r][u] = bload4(xr, xb, (uint32_t)((KR * r + u) * HW * 4));
+  };
+  // transposed into xs[buf][pixel][k]: each of the four pixels' k pair as one 8-byte store
+  auto sstore = [&](int buf, const int set) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < NP; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        *reinterpret_cast<float2*>(&xs[buf][(4 * pq + v) * KP + KR * r + 2 * kp]) =
+            make_float2(f4get(ld[set][r][0], v), f4get(ld[set][r][1], v));
+  };
+
+  omt_f32x4 acc[2][TI][TJ];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[c][i][j] = omt_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Store group j of a tile: acc[c][i][j][r] is output channel pw + 16 j + l16 at pixel tq BQ + 16 i + 4 g + r. Bias
+  // and ReLU, then the 16 channels x BQ pixels pass through the wave's staging rows (as [channel][pixel]) and leave as
+  // whole row runs, LPR lanes x 16 bytes per output row, RPI rows per store: a store of 16 rows x 64 bytes straight
+  // from the MFMA layout measured a quarter slower at these sizes. The registers are cleared for the tile after next.
+  // Range-checked buffer stores issued by every lane (past P or Q at an out-of-range offset, dropped): stores behind
+  // branches would leave the compiler unsure how many are in flight, and its wait for the next tile's loads would
+  // then drain them all. The staging rows are the wave's own, and LDS runs a wave's accesses in order.
+  auto store_group = [&](const int c, int tq, const int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v[r] = acc[c][i][j][r] + bj[j];
+        if (a.relu) v[r] = fmaxf(v[r], 0.f);
+        acc[c][i][j][r] = 0.f;
+      }
+      *reinterpret_cast<float4*>(&stg[l16 * SP + 16 * i + 4 * g]) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    const int q = tq * BQ + 4 * (lane % LPR);
+    const uint32_t n = fdiv((uint32_t)min(max(q, 0), Q - 1), ph.div_ohw);
+    const uint32_t yq = (uint32_t)(((int)n * P * HW + (q - (int)n * HW)) * 4);
+#pragma unroll
+    for (int h = 0; h < TI; ++h) {
+      const int row = RPI * h + lane / LPR, p = pw + 16 * j + row;
+      const float4 w4 = *reinterpret_cast<const float4*>(&stg[row * SP + 4 * (lane % LPR)]);
+      const uint32_t off = tq >= 0 && p < P && q < Q ? yq + (uint32_t)(p * HW * 4) : kOOB;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(omt_u32x4, w4), yr, (int)off, 0, 0);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  };
+  // tile v's MFMAs into acc[c] from buffer c, tile v - 1's stores from acc[c ^ 1] between its K-blocks (before the
+  // first tile, tq_prev = -1: every store out of range, issued all the same so that the count in flight is fixed)
+  auto mfma_tile = [&](const int c, int tq_prev) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      float4 xv[TI];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) xv[i] = *reinterpret_cast<const float4*>(&xs[c][(16 * i + l16) * KP + 16 * b + 4 * g]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            acc[c][i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(xv[i], s), wv[j][4 * b + s], acc[c][i][j], 0, 0, 0);
+#pragma unroll
+      for (int j = b * GPB; j < (b + 1) * GPB && j < TJ; ++j) store_group(c ^ 1, tq_prev, j);
+    }
+  };
+
+  // Tile v uses register set, LDS buffer and accumulator set v & 1. Loads run two tiles ahead and past the run's end
+  // (tiles past it are never stored to y: they fill a buffer no MFMA reads), so every load and LDS store is
+  // unconditional and the compiler's waits count them exactly.
+  gload(tq0, 0);
+  gload(tq0 + 1, 1);
+  sstore(0, 0);
+  __syncthreads();
+  auto step = [&](int v, auto setc) __attribute__((always_inline)) {
+    constexpr int S = decltype(setc)::value;
+    gload(tq0 + v + 2, S);  // the set tile v vacated when it went to LDS
+    sstore(S ^ 1, S ^ 1);   // tile v + 1 into the buffer tile v - 1 read before the last barrier
+    mfma_tile(S, v > 0 ? tq0 + v - 1 : -1);
+    __syncthreads();  // tile v + 1 in LDS for every wave; buffer S free for tile v + 2
+  };
+  for (int v = 0; v < ntiles; v += 2) {
+    step(v, std::integral_constant<int, 0>{});
+    if (v + 1 < ntiles) step(v + 1, std::integral_constant<int, 1>{});
+  }
+  // the last tile's stores
+  if ((ntiles - 1) & 1) {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) store_group(1, tq0 + ntiles - 1, j);
+  } else {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) store_group(0, tq0 + ntiles - 1, j);
+  }
+}
+
 template <int BP, int BQ, int WP, int WQ, int BK, int MODE, bool BN, int PF>
 __global__ void __launch_bounds__(256, 2) conv_gather_kernel(const GatherArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[gather_lds_floats<BP, BQ, BK>()];
@@ -1640,7 +1811,8 @@ struct Tile {
   float eff;    // relative MFMA efficiency of the wave tile (operand reuse)
   int bk = 16;  // K-block (gather kernels)
   int ns = 0;   // > 0: direct global -> LDS loads into an ns-stage ring (tap-major order; else the staged kernel)
-  int stream = 0;  // 1x1 stride-1 convolutions only: conv1x1_stream_kernel (runs of pixel tiles per workgroup)
+  int stream = 0;  // 1x1 stride-1 convolutions only: 1 conv1x1_stream_kernel (runs of pixel tiles per workgroup),
+                   // 2 conv1x1_wst_kernel (K of 64 or 128, the filter held in registers)
 };
 
 // Picks the tile with the smallest estimated makespan: rounds of `slots` concurrent workgroups times the padded
@@ -1673,6 +1845,7 @@ static const Tile kGatherTiles[] = {
     {64, 64, 32, 32, 0.85f, 16, 4}, {64, 128, 32, 64, 0.95f, 16, 3}, {64, 64, 32, 32, 0.90f, 32, 3},
     {64, 128, 32, 64, 0.97f, 32, 2}, {64, 128, 32, 64, 0.95f, 16, 0, 1},
     {32, 64, 16, 32, 0.60f}, {32, 64, 16, 32, 0.65f, 32}, {32, 64, 16, 32, 0.65f, 64},
+    {256, 32, 64, 32, 1.00f, 16, 0, 2}, {128, 32, 32, 32, 1.00f, 16, 0, 2}, {128, 64, 32, 64, 1.00f, 16, 0, 2},
 };
 // Plan tile index t < 3 * kNGather: kGatherTiles[t % kNGather] in one of three variants. t < kNGather: tap-major K
 // order where it applies, over a re-packed filter; kNGather <= t < 2 kNGather: channel-major order (no filter
@@ -1681,6 +1854,13 @@ static const Tile kGatherTiles[] = {
 // load), on tiles whose filter tile has whole runs per thread (BP BK >= 1024) and that are not the 1x1 streaming
 // tile; elsewhere it runs as the first variant.
 constexpr int kNGather = (int)(sizeof(kGatherTiles) / sizeof(kGatherTiles[0]));
+constexpr int kStreamTile = 13;
+// The filter-stationary tiles 17-19 (conv1x1_wst_kernel): 64 TJ output channels per workgroup at K 64 (TJ 4, 2, 2),
+// half as many at K 128 (the same filter registers), pixel tiles of 32, 32 and 64; their resident workgroups per CU
+// (waves per SIMD) at K 64 and 128, the kernels' launch bounds.
+constexpr int kWstFirst = 17;
+constexpr int kWstOcc[3][2] = {{2, 3}, {4, 3}, {2, 1}};  // as registers and LDS (input + staging) allow
+static int wst_shape(int t) { return t % kNGather - kWstFirst; }  // conv1x1_stream_kernel; tile 17 (conv1x1_wst_kernel) runs as it where it does not apply
 static const Tile& gtile(int t) { return kGatherTiles[t % kNGather]; }
 static bool gcm(int t) { return t >= kNGather && t < 2 * kNGather; }
 static bool wplace_tile(int t) {
@@ -1832,6 +2012,12 @@ static dim3 gather_grid(GatherArgs& a, const GatherPlan& pl, int64_t n, int64_t 
   a.part_stride = n * a.P * a.YH * a.YW;
   a.tpw = 0;
   a.rows = rows_ok(a, pl.slices > 1);
+  if (tl.stream == 2) {  // the shape's resident workgroups per CU; tl.bp output channels per workgroup at K 64, half
+    const int sh = wst_shape(pl.tile), k64 = a.ph[0].K == 64;
+    const int64_t ntq = cdiv(maxq, tl.bq), ntp = cdiv(a.P, k64 ? tl.bp : tl.bp / 2);
+    a.tpw = (int)std::max<int64_t>(1, cdiv(ntq * ntp, kWstOcc[sh][k64 ? 0 : 1] * kCUs));
+    return dim3((unsigned)cdiv(ntq, a.tpw), (unsigned)ntp, 1);
+  }
   if (tl.stream) {  // a workgroup per resident slot (four per CU, three with the statistics' registers)
     const int64_t ntq = cdiv(maxq, tl.bq), ntp = cdiv(a.P, tl.bp);
     a.tpw = (int)std::max<int64_t>(1, cdiv(ntq * ntp, (a.stats ? 3 : 4) * kCUs));
@@ -1847,7 +2033,15 @@ static bool stream_ok(const GatherArgs& a, const GatherPlan& pl) {
   return !gcm(pl.tile) && pl.slices == 1 && !a.bn_mean && !a.wdirect && !a.wplace && p.KH == 1 && p.KW == 1 && p.S == 1 &&
          p.PH == 0 && p.PW == 0 && p.K % 16 == 0 && rows_ok(a, false);
 }
+// The filter-stationary 1x1 tile: the streaming tile's conditions, K of 64 or 128, no epilogue statistics, x 16-byte
+// aligned (float4 loads of four pixels).
+static bool wst_ok(const GatherArgs& a, const GatherPlan& pl) {
+  const int K = a.ph[0].K;
+  return stream_ok(a, pl) && (K == 64 || K == 128) && !a.stats && (uintptr_t)a.x % 16 == 0 &&
+         (int64_t)a.ph[0].Q * a.P * 4 <= kMaxBufBytes;
+}
 static GatherPlan eff_plan(const GatherArgs& a, GatherPlan pl) {
+  if (gtile(pl.tile).stream == 2 && !wst_ok(a, pl)) pl.tile = pl.tile - pl.tile % kNGather + kStreamTile;
   if (gtile(pl.tile).stream && !stream_ok(a, pl)) pl.tile = pl.tile - pl.tile % kNGather + 2;
   return pl;
 }
@@ -1899,6 +2093,23 @@ static int run_gather(GatherArgs& a, const GatherPlan& plan, int64_t n, int64_t 
     else unsummed = nullptr;
   }
   const dim3 grid = gather_grid(a, pl, n, maxq, part);
+  if (gtile(pl.tile).stream == 2) {
+    const bool k64 = a.ph[0].K == 64;
+    switch (wst_shape(pl.tile)) {
+      case 0:
+        if (k64) hipLaunchKernelGGL((conv1x1_wst_kernel<64, 4, 32, kWstOcc[0][0]>), grid, dim3(256), 0, s, a, a.tpw);
+        else hipLaunchKernelGGL((conv1x1_wst_kernel<128, 2, 32, kWstOcc[0][1]>), grid, dim3(256), 0, s, a, a.tpw);
+        break;
+      case 1:
+        if (k64) hipLaunchKernelGGL((conv1x1_wst_kernel<64, 2, 32, kWstOcc[1][0]>), grid, dim3(256), 0, s, a, a.tpw);
+        else hipLaunchKernelGGL((conv1x1_wst_kernel<128, 1, 32, kWstOcc[1][1]>), grid, dim3(256), 0, s, a, a.tpw);
+        break;
+      default:
+        if (k64) hipLaunchKernelGGL((conv1x1_wst_kernel<64, 2, 64, kWstOcc[2][0]>), grid, dim3(256), 0, s, a, a.tpw);
+        else hipLaunchKernelGGL((conv1x1_wst_kernel<128, 1, 64, kWstOcc[2][1]>), grid, dim3(256), 0, s, a, a.tpw);
+    }
+    return launch_check("conv1x1_wst_kernel");
+  }
   if (gtile(pl.tile).stream) {
     if (a.stats)
       hipLaunchKernelGGL((conv1x1_stream_kernel<64, 128, 32, 64, true>), grid, dim3(256), 0, s, a, a.tpw);
@@ -3188,7 +3399,7 @@ std::vector<omt_conv_plan> tune_candidates(int dir, const omt_conv_geo* g, int n
     if (nhwc && !nhwc_tile_ok(t, gather_c)) continue;
     if (t >= 2 * kNGather && !(wplace_tile(t) && packs && gather_tap_major(gather_c, false, tl.bk))) continue;
     if (tl.stream) {
-      if (stream_geo && t < kNGather) out.push_back({t, 1});
+      if (stream_geo && t < kNGather && (tl.stream == 1 || K == 64 || K == 128)) out.push_back({t, 1});
       continue;
     }
     const int64_t tiles = cdiv(P, tl.bp) * cdiv(Q, tl.bq) * z, nkb = cdiv(std::max<int64_t>(K, 1), tl.bk);

@@ -141,6 +141,7 @@ __device__ __forceinline__ double wave_sum(double v) {
 }  // namespace omt
 
 typedef float omt_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int omt_u32x4 __attribute__((ext_vector_type(4)));
 
 #define OMT_EXPORT extern "C" __attribute__((visibility("default")))
 

@@ -207,7 +207,66 @@ def test_conv1x1_stream_tile_matches_staged_tile(cuda, ops, shape):
     assert orc.rel_l2(host(out[STREAM_TILE][1]), orc.conv_dgrad(gy, wt, x.shape, 1, 0)) <= TOL
 
 
-@pytest.mark.parametrize("tile", [0, 2, 5, 10, STREAM_TILE])
+WST_TILES = (17, 18, 19)  # the filter-stationary 1x1 tiles (conv1x1_wst_kernel, K of 64 or 128)
+WST_TILE = WST_TILES[0]
+WST_SHAPES = [
+    (32, 64, 256, 56),   # ResNet-50 1x1 expansion at 56^2: forward K = 64 (grad input K = 256 runs as the stream tile)
+    (32, 256, 64, 56),   # its reduction: grad input K = 64
+    (8, 128, 512, 28),   # expansion at 28^2: forward K = 128, four workgroups' channel groups per pixel tile
+    (8, 512, 128, 28),   # grad input K = 128
+    (5, 64, 272, 18),    # P not a multiple of 256 (a second channel group of 16), 1620 pixels: a partial last tile
+    (3, 128, 40, 10),    # P below one workgroup's channels, grad input K = 40 (stream tile)
+    (7, 64, 100, 15),    # H W % 4 != 0: runs as tile 2
+]
+
+
+@pytest.mark.parametrize("shape", WST_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv1x1_wst_tile_matches_staged_tile(cuda, ops, shape):
+    """The filter-stationary 1x1 kernel (filter rows in registers, pixels as the MFMA rows, float4 stores from the
+    accumulators) sums each output's K terms in the staged tiles' order: forward (bias + ReLU) and grad input of its
+    three tile shapes bit-identical to tile 2 and to the stream tile, and against the oracle; where it does not apply
+    it runs as the stream tile or tile 2."""
+    n, ci, co, h = shape
+    rng = np.random.default_rng(sum(shape) + 7)
+    x, wt, b = rnd(rng, n, ci, h, h), rnd(rng, co, ci, 1, 1, scale=ci ** -0.5), rnd(rng, co)
+    gy = rnd(rng, n, co, h, h)
+    tx, tw, tb, tgy = dev(x, cuda), dev(wt, cuda), dev(b, cuda), dev(gy, cuda)
+    out = {}
+    try:
+        for tile in WST_TILES + (STREAM_TILE, 2):
+            ops.set_conv_plan("fwd", x.shape, wt.shape, 1, 0, tile, 1)
+            ops.set_conv_plan("dgrad", x.shape, wt.shape, 1, 0, tile, 1)
+            out[tile] = (ops.conv2d(tx, tw, tb, 1, 0, relu=True), ops.conv2d_dgrad(tgy, tw, x.shape, 1, 0))
+    finally:
+        ops.clear_conv_plans()
+    for d in range(2):
+        for tile in WST_TILES + (STREAM_TILE,):
+            assert torch.equal(out[tile][d], out[2][d]), (tile, d)
+    assert orc.rel_l2(host(out[WST_TILE][0]), orc.conv_fwd(x, wt, b, 1, 0, relu=True)) <= TOL
+    assert orc.rel_l2(host(out[WST_TILE][1]), orc.conv_dgrad(gy, wt, x.shape, 1, 0)) <= TOL
+
+
+def test_conv1x1_wst_tile_input_off_16_bytes(cuda, ops):
+    """An input 4 bytes past a 16-byte boundary cannot take the filter-stationary tile's float4 loads: the plan runs
+    as the stream tile, with the aligned input's results."""
+    n, ci, co, h = 4, 64, 256, 12
+    rng = np.random.default_rng(12)
+    x, wt = rnd(rng, n, ci, h, h), rnd(rng, co, ci, 1, 1, scale=ci ** -0.5)
+    tx, tw = dev(x, cuda), dev(wt, cuda)
+    base = torch.zeros(x.size + 1, device=cuda)
+    tx_off = base[1:].view(*x.shape)
+    tx_off.copy_(tx)
+    assert tx_off.data_ptr() % 16 == 4
+    try:
+        ops.set_conv_plan("fwd", x.shape, wt.shape, 1, 0, WST_TILE, 1)
+        y_off, y = ops.conv2d(tx_off, tw), ops.conv2d(tx, tw)
+    finally:
+        ops.clear_conv_plans()
+    assert torch.equal(y_off, y)
+    assert orc.rel_l2(host(y), orc.conv_fwd(x, wt, None, 1, 0)) <= TOL
+
+
+@pytest.mark.parametrize("tile", [0, 2, 5, 10, STREAM_TILE, WST_TILE])
 def test_conv1x1_filter_used_in_place_off_16_bytes(cuda, ops, tile):
     """A 1x1 filter is read in place; from a view 4 bytes past a 16-byte boundary the tap-major tiles' 16-byte filter
     loads (4-byte alignment suffices) and the stream tile give the aligned filter's results, and a direct-to-LDS tile
@@ -516,7 +575,7 @@ FULL = [
 BENCH_PLANS = {
     "C5_3x3_56": ([5, 1], [5, 1], [2, 114]), "C5_3x3_28": ([5, 1], [5, 1], [0, 112]),
     "C5_3x3_14": ([5, 1], [5, 1], [2, 16]), "C5_3x3_7": ([5, 4], [5, 4], [2, 4]),
-    "C5_1x1_exp_56": ([13, 1], [2, 1], [2, 256]), "C5_1x1_red_56": ([2, 1], [13, 1], [0, 256]),
+    "C5_1x1_exp_56": ([17, 1], [2, 1], [2, 256]), "C5_1x1_red_56": ([2, 1], [17, 1], [0, 256]),
     "C5_1x1_exp_28": ([2, 1], [5, 1], [2, 64]), "C5_1x1_red_28": ([5, 1], [2, 1], [0, 64]),
     "C5_1x1_exp_14": ([5, 1], [5, 1], [0, 16]), "C5_1x1_red_14": ([5, 1], [5, 1], [2, 16]),
     "C5_1x1_exp_7": ([5, 1], [5, 1], [0, 4]), "C5_1x1_red_7": ([5, 1], [5, 1], [0, 4]),
