@@ -180,7 +180,7 @@ def _is_gather(kernel_name):
 def trace_summary(trace_csv, steps, n_layers):
     """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of this bench (sweep only) and prints the
     timed region's per-kernel table as markdown. Warm-up and timed steps launch the same dispatch sequence, so the
-    step length D is the smallest period of the trace's tail; the timed region is the last `steps` x D dispatches.
+    timed region is the latest stretch of `steps` x D dispatches that repeats with period D (the step length).
     Each layer launches its forward, then its grad input through a gather kernel (the grad weight through the wgrad
     kernel), so the even-numbered gather dispatches of the region are the forward launches: their mean duration is
     the figure the bench's roofline.avg_launch_ms measures with HIP events."""
@@ -189,16 +189,24 @@ def trace_summary(trace_csv, steps, n_layers):
     rows = sorted((int(r["Dispatch_Id"]), r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
                   for r in csv.DictReader(open(trace_csv)))
     names = [r[1] for r in rows]
-    period = None
-    for d in range(1, len(rows) // steps + 1):
-        tail = names[len(names) - steps * d:]
-        if all(tail[i] == tail[i % d] for i in range(len(tail))) and \
-                sum(_is_gather(n) for n in tail[:d]) == 2 * n_layers:
-            period = d
-            break
-    if period is None:
-        raise SystemExit(f"no {steps}-fold periodic tail with {2 * n_layers} gather dispatches per step")
-    region = rows[len(rows) - steps * period:]
+    # the latest stretch that repeats one period `steps` times (the parity check after the timed steps launches
+    # other dispatches, so the timed region need not be the trace's tail)
+    n, gat = len(names), [0]
+    for nm in names:
+        gat.append(gat[-1] + _is_gather(nm))
+    found = None  # (end, period) with the latest end, then the shortest period
+    for d in range(2 * n_layers, min(n // steps, 40 * n_layers) + 1):
+        run = 0  # consecutive positions i with names[i] == names[i - d], ending at i
+        for i in range(n):
+            run = run + 1 if i >= d and names[i] == names[i - d] else 0
+            end = i + 1
+            if run >= (steps - 1) * d and gat[end] - gat[end - d] == 2 * n_layers and \
+                    (found is None or end > found[0]):
+                found = (end, d)
+    if found is None:
+        raise SystemExit(f"no {steps}-fold periodic stretch with {2 * n_layers} gather dispatches per step")
+    end, period = found
+    region = rows[end - steps * period:end]
     busy = sum(e - s for (_, _, s, e) in region) / 1e6
     span = (region[-1][3] - region[0][2]) / 1e6
     per = {}
@@ -638,16 +646,26 @@ def bw_pmc_summary(fetch_csv, write_csv):
     print("\n".join(lines))
 
 
-def pmc_probe(layers, dev):
+def pmc_probe(layers, dev, plans_log=None):
     """For the rocprofv3 --pmc passes: the forward plans are tuned first (as in the bench; those dispatches come
-    before the copy), then a 1 GiB device-to-device copy (1 GiB read + 1 GiB written: the FETCH_SIZE / WRITE_SIZE
-    calibration launch), then one forward conv per layer, each on its own freshly written input."""
+    before the copy) or, with plans_log, set to the forward plans of the bench run whose JSON line that file holds
+    (so that the traffic is measured on the plans that run timed), then a 1 GiB device-to-device copy (1 GiB read +
+    1 GiB written: the FETCH_SIZE / WRITE_SIZE calibration launch), then one forward conv per layer, each on its own
+    freshly written input."""
     import torch
 
     from omarchy_mac_torch import hip_ops
 
+    fixed = None
+    if plans_log:
+        line = [ln for ln in open(plans_log) if ln.startswith('{"metric"')][-1]
+        fixed = json.loads(line)["plans"]["tile_slices"]
     for (name, n, c, k, h, ks, s, p) in layers:
-        hip_ops.autotune_conv("fwd", (n, c, h, h), (k, c, ks, ks), s, p)
+        if fixed:
+            hip_ops.set_conv_plan("fwd", (n, c, h, h), (k, c, ks, ks), s, p, *fixed[name]["fwd"])
+        else:
+            hip_ops.autotune_conv("fwd", (n, c, h, h), (k, c, ks, ks), s, p)
+        print(name, "fwd plan", hip_ops.conv_plan("fwd", (n, c, h, h), (k, c, ks, ks), s, p)[:2], flush=True)
     torch.cuda.synchronize()
     src = torch.ones(256 * 1024 * 1024, device=dev)
     dst = torch.empty_like(src)
@@ -1152,6 +1170,9 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: one 1 GiB device copy (counter calibration), then one forward "
                          "launch per layer (with --workload bw: each HBM-bound op once, after a fill marker)")
+    ap.add_argument("--pmc-plans", metavar="BENCH_LOG",
+                    help="with --pmc-probe: the forward plans of the bench run whose JSON line BENCH_LOG holds, "
+                         "instead of tuning them again")
     args = ap.parse_args()
     if args.pmc_summary:
         if args.workload == "bw":
@@ -1202,7 +1223,7 @@ def main():
         return
     layers = C5_LAYERS if args.workload == "c5" else C1_LAYERS
     if args.pmc_probe:
-        pmc_probe(layers, dev)
+        pmc_probe(layers, dev, args.pmc_plans)
         return
     sw = conv_sweep(layers, dev, args.steps, args.warmup, not args.no_tune)
     value = sw["value"]
