@@ -31,6 +31,7 @@ captures, replays and op-by-op calls with their reasons.
 """
 
 import os
+import weakref
 
 import torch
 
@@ -41,8 +42,47 @@ WARMUP_CALLS = 2
 MAX_CAPTURES = 3
 _enabled = os.environ.get("OMARCHY_MAC_TORCH_COMPILE_GRAPHS", "1") != "0"
 # data pointers of storages that stay put while a captured graph lives (its inputs read in place, its input buffers,
-# its outputs): a backward whose inputs are among them reads them in place
-_static_ptrs = set()
+# its outputs), each with its number of holders: a backward whose inputs are among them reads them in place. A graph
+# holds its own memory (input buffers, outputs) until it is captured again; an input it reads in place is the
+# caller's, held only while that storage lives (a finalizer drops it when the memory is freed, so that a later
+# tensor at the same address is not taken for it)
+_static_ptrs = {}
+
+
+def _hold(p):
+    _static_ptrs[p] = _static_ptrs.get(p, 0) + 1
+
+
+def _drop(p):
+    n = _static_ptrs.get(p, 0) - 1
+    if n > 0:
+        _static_ptrs[p] = n
+    else:
+        _static_ptrs.pop(p, None)
+
+
+class _Holds:
+    """A captured graph's entries in _static_ptrs: its own memory, and the caller's storages it reads in place (each
+    dropped by a finalizer when that storage is freed). release() ends them all, once: when the graph is captured
+    again or garbage-collected."""
+
+    def __init__(self, owned, external):
+        self.owned = owned
+        self.external = {}
+        for p in owned:
+            _hold(p)
+        for p, t in external:
+            if p not in owned and p not in self.external:
+                _hold(p)
+                self.external[p] = weakref.finalize(t.untyped_storage(), _drop, p)
+
+    def release(self):
+        for p in self.owned:
+            _drop(p)
+        for p, fin in self.external.items():
+            if fin.detach() is not None:  # the storage still lives: this graph's hold ends here
+                _drop(p)
+        self.owned, self.external = set(), {}
 STATS = {"captures": 0, "replays": 0, "eager": 0, "reasons": {}}
 
 
@@ -184,12 +224,15 @@ class ReplayedGraph:
             self._forget()
             self.graph.release()
         self.graph = graph
-        self.owned = {_ptr(t) for t in inputs} | {_ptr(o) for o in outs if isinstance(o, torch.Tensor)}
-        _static_ptrs.update(self.owned)
+        self.holds = _Holds({_ptr(t) for t, keep in zip(inputs, static) if not keep} |
+                            {_ptr(o) for o in outs if isinstance(o, torch.Tensor)},
+                            [(_ptr(t), t) for t, keep in zip(inputs, static) if keep])
+        self.holds_gc = weakref.finalize(self, self.holds.release)
         return None
 
     def _forget(self):
-        _static_ptrs.difference_update(self.owned)
+        self.holds_gc.detach()
+        self.holds.release()
 
     # ---- replay ----
 

@@ -160,3 +160,33 @@ def test_autograd_over_cuda_tensors_is_refused_up_front():
     assert torch.equal(x.grad, torch.full((4,), 3.0))
     (gx,) = torch.autograd.grad((x * x).sum(), [x])
     assert torch.allclose(gx, 2 * x.detach())
+
+
+def test_replay_static_pointer_holds_end_with_the_storage():
+    """The compile backend's registry of memory that stays put while a captured graph lives: a graph's own memory is
+    held until release(); a caller's storage it reads in place is held only while that storage lives (then a later
+    tensor at the same address is not taken for it); two graphs holding one address keep it until both let go."""
+    import gc
+
+    import torch
+
+    from omarchy_mac_torch import replay
+
+    own = torch.empty(16)
+    param, other = torch.empty(16), torch.empty(16)
+    p_own, p_param, p_other = (t.untyped_storage().data_ptr() for t in (own, param, other))
+    before = dict(replay._static_ptrs)
+    a = replay._Holds({p_own}, [(p_param, param), (p_other, other)])
+    b = replay._Holds(set(), [(p_param, param)])
+    assert {p_own, p_param, p_other} <= set(replay._static_ptrs) and replay._static_ptrs[p_param] == 2
+    del other
+    gc.collect()
+    assert p_other not in replay._static_ptrs  # freed: dropped by its finalizer
+    a.release()
+    a.release()  # once only
+    assert p_own not in replay._static_ptrs and replay._static_ptrs[p_param] == 1
+    del param
+    gc.collect()
+    assert p_param not in replay._static_ptrs
+    b.release()
+    assert replay._static_ptrs == before
