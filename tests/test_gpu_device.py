@@ -558,14 +558,17 @@ def _assert_north_star(dev, cpu, cpu64, what):
 
 @pytest.fixture()
 def model_plans(clean):
-    """Plans from the library's cost model (no timing-based tuning), so that the device's summation orders, and so
-    its losses, are the same on every box: the loss tests assert a tight bound on a chaotic trajectory, and every
-    plan the tuner may pick is checked against the oracle per op elsewhere."""
+    """Plans from the library's cost model (no timing-based tuning, and none cached by earlier tests in the process),
+    so that the device's summation orders, and so its losses, are the same on every box and in every test order: the
+    loss tests assert a tight bound on a chaotic trajectory, and every plan the tuner may pick is checked against the
+    oracle per op elsewhere."""
     core = clean.native.core
     core.set_tuning(False, 0)
+    core.clear_plans()
     try:
         yield clean
     finally:
+        core.clear_plans()
         core.set_tuning(True, 0)
 
 
