@@ -2372,8 +2372,8 @@ static int conv_fwd_one(const omt_conv_geo* g, const float* x, const float* w, c
   float* part = (float*)((char*)workspace + align256(fwd_pack_bytes(g, pl)));
   if (parts) *parts = part;
   if (stats) {  // the statistics come from the epilogue of an unsplit plan (checked above, before any launch)
+    a.stats = stats;  // first: the tile that runs depends on it (the filter-stationary 1x1 tiles have no statistics)
     const GatherPlan ep = eff_plan(a, pl);
-    a.stats = stats;
     a.stats_groups = (int)cdiv(p.Q, gtile(ep.tile).wq);
     *groups = a.stats_groups;
   }
