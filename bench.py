@@ -257,6 +257,8 @@ RESNET_FAMILIES = [
     ("omt split-K sums (gather_reduce, split_reduce, dual_reduce)", ("gather_reduce", "split_reduce", "dual_reduce")),
     ("omt filter re-pack", ("pack_tapmajor", "pack_dgrad")),
     ("omt BatchNorm", ("omt::bn_",)),
+    ("omt depthwise convolution", ("omt::dw_",)),
+    ("omt squeeze-excite MLP, gate and plane sums", ("omt::se_", "plane_dot", "channel_scale")),
     ("omt pools", ("maxpool", "avgpool", "adapool", "gap_")),
     ("omt fused Adam / SGD (multi-tensor)", ("fused_adam_kernel", "fused_sgd_kernel")),
     ("omt log-softmax / NLL loss", ("log_softmax_", "nll_fwd_kernel", "nll_bwd_kernel")),
@@ -271,7 +273,8 @@ RESNET_FAMILIES = [
 
 
 def resnet_trace_summary(trace_csv, replays=22):
-    """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` and prints, for
+    """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` (or
+    `--workload mobilenet`) and prints, for
     the compiled graphed replays (the last run of `replays` identical steps), the eager-model graphed replays (the
     run before it) and the compiled model with the backend's own graph replay (the run before that: its 20 timed
     steps), kernel time per step by family as markdown. Replays of one graph launch the same dispatch sequence, so a
@@ -1141,8 +1144,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "resnet-layers", "models", "bw"], default="c5",
-                    help="resnet: only the ResNet-18 training-step measurement; resnet-layers: ResNet-18's "
+    ap.add_argument("--workload", choices=["c5", "c1", "resnet", "mobilenet", "resnet-layers", "models", "bw"],
+                    default="c5",
+                    help="resnet / mobilenet: only the ResNet-18 / MobileNetV3 training-step measurement; "
+                         "resnet-layers: ResNet-18's "
                          "convolutions one by one (tuned plans, per-call GPU time); models: only the training steps "
                          "of configs 2-4; bw: only the HBM-bound kernels (all three for profiling)")
     ap.add_argument("--no-bw", action="store_true", help="skip the HBM-bound kernel measurements")
@@ -1204,12 +1209,12 @@ def main():
     if args.workload == "resnet-layers":
         print(json.dumps({"resnet18_conv_layers": resnet_layer_table(dev, not args.no_tune)}), flush=True)
         return
-    if args.workload in ("resnet", "models"):
+    if args.workload in ("resnet", "mobilenet", "models"):
         import omarchy_mac_torch
 
         cfgs = train_configs()
-        if args.workload == "resnet":
-            cfgs = [c for c in cfgs if c[0] == "resnet18_b32"]
+        if args.workload != "models":
+            cfgs = [c for c in cfgs if c[0] == {"resnet": "resnet18_b32", "mobilenet": "mobilenetv3_b32"}[args.workload]]
         print(json.dumps({c[0]: train_step_bench(c, omarchy_mac_torch.DEVICE, args.model_steps, 5, 5, not args.no_cpu,
                                                  compiled=c[0] in ("resnet18_b32", "mobilenetv3_b32"),
                                                  fp64=c[0] == "resnet18_b32")
