@@ -66,7 +66,7 @@ __device__ __forceinline__ float f4get(const float4& v, int s) { return s == 0 ?
 // contiguous runs of each pixel, and tap-major over a channels-last source of too few channels for whole K-blocks
 // (kNhwcNarrow: the ResNet stem's 3; element by element like the generic order, k = (ky, kx, c), which is also the
 // memory order of a channels-last filter).
-enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2, kNhwc = 3, kNhwcNarrow = 4 };
+enum { kGeneric = 0, kTapMajor = 1, kTapInPlace = 2, kNhwc = 3, kNhwcNarrow = 4, kPix4 = 5 };
 
 struct Phase {
   int KH, KW, S, PH, PW;  // gather window, stride and (signed) padding
@@ -1259,8 +1259,31 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     kx0 = r0 - ky0 * KS;
   }
 
-  float ra[PF][AR], rb[PF][BR];  // PF register sets: loads PF K-blocks ahead of the MFMAs
+  // PF register sets: loads PF K-blocks ahead of the MFMAs. kPix4 (1x1, stride 1, unpadded, OH OW % 4 == 0): four
+  // consecutive reduction pixels of one row are contiguous in x and gy, so a lane loads them as one 16-byte load
+  // (lane: row rr = lane / 16 of four, pixels 4 kq .. 4 kq + 3 of the K-block, kq = lane % 16): a quarter of the load
+  // instructions, so four times the bytes in flight per outstanding-load slot, into the same LDS layout
+  constexpr bool P4 = MODE == kPix4;
+  float ra[PF][P4 ? 1 : AR], rb[PF][P4 ? 1 : BR];
+  float4 ra4[PF][P4 ? AR / 4 : 1], rb4[PF][P4 ? BR / 4 : 1];
+  const int rr = lane >> 4, kq = lane & 15;
   auto gload = [&](int k0, const int set) {
+    if constexpr (P4) {
+      const int k = k0 + 4 * kq;  // K and the slice bounds are multiples of 4: the run is whole or past kend
+      uint32_t gbase = kOOB, xbase = kOOB;
+      if (k < kend) {
+        const uint32_t n = fdiv((uint32_t)k, a.div_ohw), r = (uint32_t)k - n * (uint32_t)ohw;
+        gbase = (uint32_t)(((int)n * P * ohw + (int)r) * 4) + (uint32_t)(rr * ohw * 4);
+        xbase = (uint32_t)(((int)n * a.C * HW + (int)r) * 4) + (uint32_t)(rr * HW * 4);  // pixel = output pixel
+      }
+#pragma unroll
+      for (int i = 0; i < AR / 4; ++i)
+        ra4[set][i] = bload4(gr, pw0 + 4 * i + rr < P ? gbase : kOOB, (uint32_t)((pw0 + 4 * i) * ohw * 4));
+#pragma unroll
+      for (int j = 0; j < BR / 4; ++j)
+        rb4[set][j] = bload4(xr, qw0 + 4 * j + rr < Q ? xbase : kOOB, (uint32_t)((qw0 + 4 * j) * HW * 4));
+      return;
+    }
     const int k = k0 + lane;
     const bool kval = k < kend;
     uint32_t gbase = kOOB, xbase = kOOB;
@@ -1300,6 +1323,15 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, const int bx, con
     }
   };
   auto sstore = [&](const int set) {
+    if constexpr (P4) {
+#pragma unroll
+      for (int i = 0; i < AR / 4; ++i)
+        *reinterpret_cast<float4*>(&As[(wave * AR + 4 * i + rr) * PK + 4 * kq]) = ra4[set][i];
+#pragma unroll
+      for (int j = 0; j < BR / 4; ++j)
+        *reinterpret_cast<float4*>(&Bs[(wave * BR + 4 * j + rr) * PK + 4 * kq]) = rb4[set][j];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < AR; ++i) As[(wave * AR + i) * PK + lane] = ra[set][i];
 #pragma unroll
@@ -2726,6 +2758,17 @@ static dim3 wgrad_prepare(const omt_conv_geo* g, const float* x, const float* gy
 static bool wgrad_uses_tap_major(const omt_conv_geo* g, const WgradPlan& pl) {
   return g->ci % (kWgradTiles[pl.tile].bq / 4) == 0;
 }
+// The grad-weight GEMM of a plan in its loader mode: 16-byte loads of four reduction pixels for 1x1 stride-1 unpadded
+// layers whose planes are a multiple of 4 (kPix4), else one pixel per lane in tap-major or channel-major order.
+static void launch_wgrad_gemm(const omt_conv_geo* g, const WgradPlan& pl, const WgradArgs& a, dim3 grid,
+                              hipStream_t s) {
+  if (g->ks == 1 && g->stride == 1 && g->pad == 0 && (g->oh * g->ow) % 4 == 0)
+    wgrad_dispatch<kPix4>(pl.tile, a, grid, s);
+  else if (wgrad_uses_tap_major(g, pl))
+    wgrad_dispatch<kTapMajor>(pl.tile, a, grid, s);
+  else
+    wgrad_dispatch<kGeneric>(pl.tile, a, grid, s);
+}
 // The slice sum of a split grad-weight launch (blocks 0 if the plan does not split).
 static SplitSum wgrad_sum_of(const WgradArgs& a, const WgradPlan& pl, float* gw) {
   if (pl.slices <= 1) return SplitSum{};
@@ -2746,10 +2789,7 @@ static int run_wgrad(const omt_conv_geo* g, const float* x, const float* gy, flo
   WgradArgs a;
   WgradPlan pl;
   const dim3 grid = wgrad_prepare(g, x, gy, gw, workspace, a, pl);
-  if (wgrad_uses_tap_major(g, pl))
-    wgrad_dispatch<kTapMajor>(pl.tile, a, grid, s);
-  else
-    wgrad_dispatch<kGeneric>(pl.tile, a, grid, s);
+  launch_wgrad_gemm(g, pl, a, grid, s);
   if (int st = launch_check("conv_wgrad_kernel")) return st;
   return launch_split_sum(wgrad_sum_of(a, pl, gw), s);
 }
@@ -2868,10 +2908,7 @@ static int conv_bwd_one(const omt_conv_geo* g, const float* x, const float* gy, 
   const dim3 wgrid = wgrad_prepare(g, x, gy, gw, wws, wa, wp);
   if (!dual_tiles(dp, wp)) {
     if (int st = run_gather(ga, dp, g->n, maxq, part, s)) return st;
-    if (wgrad_uses_tap_major(g, wp))
-      wgrad_dispatch<kTapMajor>(wp.tile, wa, wgrid, s);
-    else
-      wgrad_dispatch<kGeneric>(wp.tile, wa, wgrid, s);
+    launch_wgrad_gemm(g, wp, wa, wgrid, s);
     if (int st = launch_check("conv_wgrad_kernel")) return st;
     return launch_split_sum(wgrad_sum_of(wa, wp, gw), s);
   }
@@ -2946,10 +2983,7 @@ static int conv_bwd_one_parts(const omt_conv_geo* g, const float* x, const float
       *gx_parts = ga.part;
       *gx_slices = unsummed;
     }
-    if (wgrad_uses_tap_major(g, wp))
-      wgrad_dispatch<kTapMajor>(wp.tile, wa, wgrid, s);
-    else
-      wgrad_dispatch<kGeneric>(wp.tile, wa, wgrid, s);
+    launch_wgrad_gemm(g, wp, wa, wgrid, s);
     return launch_check("conv_wgrad_kernel");
   }
   const dim3 ggrid = gather_grid(ga, dp, g->n, maxq, part);
