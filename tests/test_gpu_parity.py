@@ -315,6 +315,8 @@ BWD_SHAPES = [
     (2, 32, 48, 6, 5, 1, 1, 0),     # 1x1
     (3, 64, 96, 8, 6, 1, 1, 0),     # 1x1, planes of 48: the separate grad weight loads four pixels per lane (16 bytes)
     (2, 36, 50, 8, 8, 1, 1, 0),     # the same with rows (50 output channels) and columns (36) past a group of four
+    (2, 64, 48, 12, 12, 3, 1, 1),   # 3x3 pad 1, tap-major grad weight over rows of 12
+    (3, 32, 40, 4, 4, 3, 1, 1),     # rows of 4: every output's side taps reach the padding
     (2, 64, 64, 8, 8, 1, 2, 0),     # 1x1 stride 2: phases no tap reaches
     (2, 3, 64, 20, 20, 3, 2, 1),    # super-pixel grad input (3 channels, stride 2), split K summed by the scatter
     (16, 16, 24, 32, 32, 3, 1, 1),  # grad weight over 16384 pixels: 40 and 100 slices take the grouped slice sum
@@ -327,8 +329,8 @@ def test_conv_bwd_matches_separate_calls(cuda, ops, shape):
     """omt_conv_bwd (grad input and grad weight in one call; one launch when both plans use 64x64 tiles) is
     bit-identical to omt_conv_dgrad + omt_conv_wgrad under the same plans, and matches the oracle: dual and non-dual
     plan pairs, tap-major and channel-major grad input, split K on either side (grad weight up to 100 slices, whose
-    sums go by groups of slices). On 1x1 layers whose planes are a multiple of 4 the separate grad weight loads four
-    reduction pixels per lane and the one-launch kernel one: the same LDS layout, the same sums to the bit."""
+    sums go by groups of slices). On stride-1 1x1 layers whose planes are a multiple of 4 the separate grad weight loads
+    four reduction pixels per lane and the one-launch kernel one: the same LDS layout, the same sums to the bit."""
     n, ci, co, h, w, ks, s, p = shape
     rng = np.random.default_rng(sum(shape) + 5)
     x, wt = rnd(rng, n, ci, h, w), rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5)
