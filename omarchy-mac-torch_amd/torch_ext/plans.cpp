@@ -138,14 +138,268 @@ static Tensor own_ws(Plan& p, size_t bytes) {
   return own(p, {(int64_t)bytes}, at::kByte);
 }
 
-namespace {
-struct BackRec {
-  std::string kind;
-  Tensor x, y, sm, si, idx;
-  int param = -1;
-  int64_t n = 0, c = 0, co = 0, h = 0, w = 0, ks = 0;
+// ---- plan construction: a fusion pass over the layer list, then one emitter per fused stage ----------------------
+//
+// fuse_stages groups the layers into stages (what runs as one library call): an eval BatchNorm + ReLU whose consumer
+// can apply it in its input loader becomes part of that convolution's stage; a training BatchNorm + ReLU followed by a
+// 2x2 max pool is one stage (the pool inside the BatchNorm's apply pass). The emitters then allocate each stage's
+// buffers, append its forward steps and push onto a tape a closure that appends its backward steps; the tape runs in
+// reverse, each closure taking the gradient of the stage's output and leaving the gradient of its input.
+
+enum class StageOp { Conv, Depthwise, BatchNorm, BatchNormPool, MaxPool, AvgPool, GlobalPool };
+
+struct Stage {
+  StageOp op;
+  int layer = 0;           // the stage's (first) layer
+  int loader_bn = -1;      // eval: the BatchNorm layer the convolution applies in its input loader, or -1
 };
-}  // namespace
+
+// Whether an eval BatchNorm + ReLU may be applied by `consumer`'s input loader under the fold policy (0 never, 1 1x1
+// convolutions only, 2 every convolution and depthwise convolution).
+static bool loader_can_fold(const PlanLayer& consumer, int policy) {
+  if (policy <= 0) return false;
+  if (consumer.kind == "conv") return policy >= 2 || consumer.ks == 1;
+  return policy >= 2 && consumer.kind == "dw";
+}
+
+static std::vector<Stage> fuse_stages(const std::vector<PlanLayer>& layers, bool train, int policy) {
+  std::vector<Stage> out;
+  const int nl = (int)layers.size();
+  for (int li = 0; li < nl; ++li) {
+    const std::string& k = layers[li].kind;
+    const bool has_next = li + 1 < nl;
+    if (k == "bn") {
+      if (!train && has_next && loader_can_fold(layers[li + 1], policy)) {
+        out.push_back({layers[li + 1].kind == "dw" ? StageOp::Depthwise : StageOp::Conv, li + 1, li});
+        ++li;  // the consumer is this stage
+      } else if (train && has_next && layers[li + 1].kind == "pool") {
+        out.push_back({StageOp::BatchNormPool, li});
+        ++li;
+      } else {
+        out.push_back({StageOp::BatchNorm, li});
+      }
+    } else if (k == "conv" || k == "dw") {
+      out.push_back({k == "dw" ? StageOp::Depthwise : StageOp::Conv, li});
+    } else if (k == "pool" || k == "apool") {
+      out.push_back({k == "pool" ? StageOp::MaxPool : StageOp::AvgPool, li});
+    } else if (k == "gap") {
+      out.push_back({StageOp::GlobalPool, li});
+    } else {
+      throw NotCovered("unknown layer kind " + k);
+    }
+  }
+  return out;
+}
+
+// Walks the stages, tracking the activation's shape and the next parameter / running-statistics slots.
+struct PlanBuilder {
+  Plan& p;
+  const std::vector<PlanLayer>& layers;
+  Tensor cur;                // the current activation
+  int64_t n, c, h, w;        // its shape
+  int pi = 0, bi = 0;        // next parameter, next running-statistics pair
+  // each stage's backward emitter: (the gradient of its output -> the gradient of its input, and whether it is the
+  // network's first stage)
+  std::vector<std::function<void(Tensor&, bool)>> tape;
+
+  const float* param_ptr(int i) const { return fp(p.params[i]); }
+
+  void conv(const Stage& st) {
+    const PlanLayer& L = layers[st.layer];
+    const bool dw = st.op == StageOp::Depthwise;
+    // an eval BatchNorm applied in this convolution's loader consumes its gamma, beta and running statistics first
+    const float *bm = nullptr, *bv = nullptr, *bg = nullptr, *bb = nullptr;
+    if (st.loader_bn >= 0) {
+      cover(layers[st.loader_bn].ci == c && pi + 1 < (int)p.params.size() && bi < (int)p.rms.size(), "layer channels");
+      bg = param_ptr(pi);
+      bb = param_ptr(pi + 1);
+      bm = fp(p.rms[bi]);
+      bv = fp(p.rvs[bi]);
+      pi += 2;
+      ++bi;
+    }
+    const int64_t co = dw ? c : L.co, ks = L.ks;
+    cover(L.ci == c && pi < (int)p.params.size(), "layer channels");
+    const omt_conv_geo g = conv_geo(n, c, co, h, w, ks, 1, ks / 2);
+    cover(g.oh == h && g.ow == w, "'same' convolution");
+    const int wi = pi++;
+    const Tensor x = cur, wt = p.params[wi], y = own(p, {n, co, h, w});
+    if (dw) {
+      p.fwd.push_back([g, x, wt, y, bm, bv, bg, bb](Run&, void* s) {
+        check(omt_dw_fwd(&g, fp(x), fp(wt), nullptr, bm, bv, bg, bb, 1e-5f, fpm(y), s), "plan: depthwise conv");
+      });
+    } else {
+      tune_conv(OMT_DIR_FWD, g);
+      const Tensor ws = own_ws(p, omt_conv_fwd_workspace(&g));
+      p.fwd.push_back([g, x, wt, y, bm, bv, bg, bb, ws](Run&, void* s) {
+        check(omt_conv_fwd(&g, fp(x), fp(wt), nullptr, 0, bm, bv, bg, bb, 1e-5f, fpm(y), wsptr(ws), wsbytes(ws), s),
+              "plan: conv");
+      });
+    }
+    Plan& P = p;
+    tape.push_back([&P, g, x, wt, wi, dw](Tensor& gy, bool first) {
+      const bool gx_needed = !first || P.input_grad;
+      const Tensor go = gy;
+      if (!dw && gx_needed) {  // both gradients in one call: the two GEMMs share a launch when their plans allow it
+        tune_conv_bwd(g);
+        const Tensor gx = own(P, {g.n, g.ci, g.ih, g.iw}), ws = own_ws(P, omt_conv_bwd_workspace(&g));
+        P.bwd.push_back([g, x, go, wt, gx, wi, ws](Run& run, void* s) {
+          check(omt_conv_bwd(&g, fp(x), fp(go), fp(wt), fpm(gx), fpm(run.grads[wi]), wsptr(ws), wsbytes(ws), s),
+                "plan: input and weight gradients");
+        });
+        gy = gx;
+        return;
+      }
+      if (!dw) tune_conv(OMT_DIR_WGRAD, g);
+      const Tensor wws = own_ws(P, dw ? omt_dw_wgrad_workspace(&g) : omt_conv_wgrad_workspace(&g));
+      P.bwd.push_back([g, x, go, wi, wws, dw](Run& run, void* s) {
+        if (dw)
+          check(omt_dw_wgrad(&g, fp(x), fp(go), fpm(run.grads[wi]), wsptr(wws), wsbytes(wws), s),
+                "plan: depthwise weight gradient");
+        else
+          check(omt_conv_wgrad(&g, fp(x), fp(go), fpm(run.grads[wi]), wsptr(wws), wsbytes(wws), s),
+                "plan: weight gradient");
+      });
+      if (!gx_needed) return;
+      if (!dw) tune_conv(OMT_DIR_DGRAD, g);
+      const Tensor gx = own(P, {g.n, g.ci, g.ih, g.iw});
+      const Tensor dws = dw ? Tensor() : own_ws(P, omt_conv_dgrad_workspace(&g));
+      P.bwd.push_back([g, go, wt, gx, dws, dw](Run&, void* s) {
+        if (dw)
+          check(omt_dw_dgrad(&g, fp(go), fp(wt), fpm(gx), s), "plan: depthwise input gradient");
+        else
+          check(omt_conv_dgrad(&g, fp(go), fp(wt), fpm(gx), wsptr(dws), wsbytes(dws), s), "plan: input gradient");
+      });
+      gy = gx;
+    });
+    cur = y;
+    c = co;
+  }
+
+  void batch_norm(const Stage& st) {
+    const PlanLayer& L = layers[st.layer];
+    cover(L.ci == c && pi + 1 < (int)p.params.size() && bi < (int)p.rms.size(), "layer channels");
+    const bool pool = st.op == StageOp::BatchNormPool;
+    if (pool) cover(h >= 2 && w >= 2, "2x2 pool over an image smaller than 2x2");
+    const int gi = pi;
+    pi += 2;
+    const Tensor gamma = p.params[gi], beta = p.params[gi + 1], rm = p.rms[bi], rv = p.rvs[bi];
+    ++bi;
+    const int64_t n0 = n, c0 = c, h0 = h, w0 = w, hw = h * w;
+    const Tensor x = cur, y = own(p, {n, c, h, w});
+    if (!p.train) {
+      p.fwd.push_back([=](Run&, void* s) {
+        check(omt_bn_eval_fwd(n0, c0, hw, fp(x), fp(gamma), fp(beta), fp(rm), fp(rv), 1e-5, 1, fpm(y), s),
+              "plan: batch norm (eval)");
+      });
+      cur = y;
+      return;  // an eval plan has no backward
+    }
+    const Tensor sm = own(p, {c}), si = own(p, {c}), ws = own_ws(p, omt_bn_train_workspace(n, c, hw));
+    const double mom = L.momentum;
+    Tensor pooled, idx;
+    if (pool) {
+      pooled = own(p, {n, c, h / 2, w / 2});
+      idx = own(p, {n, c, h / 2, w / 2}, at::kLong);
+    }
+    p.fwd.push_back([=](Run&, void* s) {
+      float* rmp = rm.mutable_data_ptr<float>();
+      float* rvp = rv.mutable_data_ptr<float>();
+      if (pool)
+        check(omt_bn_train_fwd_pool(n0, c0, h0, w0, fp(x), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y),
+                                    fpm(sm), fpm(si), rmp, rvp, 2, 2, 2, 2, 0, 0, fpm(pooled),
+                                    idx.mutable_data_ptr<int64_t>(), wsptr(ws), wsbytes(ws), s),
+              "plan: batch norm + max pool");
+      else
+        check(omt_bn_train_fwd(n0, c0, hw, fp(x), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y), fpm(sm),
+                               fpm(si), rmp, rvp, wsptr(ws), wsbytes(ws), s),
+              "plan: batch norm");
+    });
+    Plan& P = p;
+    tape.push_back([&P, n0, c0, h0, w0, x, y, sm, si, gamma, gi, pool, idx](Tensor& gy, bool) {
+      if (pool) {  // the pool's gradient first: the fused forward's pooled output is this stage's output
+        const Tensor go = gy, gp = own(P, {n0, c0, h0, w0});
+        P.bwd.push_back([=](Run&, void* s) {
+          check(omt_maxpool_bwd(n0 * c0, h0, w0, h0 / 2, w0 / 2, 2, 2, 2, 2, 0, 0, 1, 1, fp(go),
+                                idx.data_ptr<int64_t>(), fpm(gp), s),
+                "plan: max pool backward");
+        });
+        gy = gp;
+      }
+      const Tensor go = gy, gx = own(P, {n0, c0, h0, w0}), ws = own_ws(P, omt_bn_bwd_workspace(n0, c0, h0 * w0));
+      P.bwd.push_back([=](Run& run, void* s) {
+        check(omt_bn_bwd(n0, c0, h0 * w0, fp(go), fp(x), fp(y), fp(sm), fp(si), fp(gamma), fpm(gx),
+                         fpm(run.grads[gi]), fpm(run.grads[gi + 1]), wsptr(ws), wsbytes(ws), s),
+              "plan: batch norm backward");
+      });
+      gy = gx;
+    });
+    if (pool) {
+      cur = pooled;
+      h /= 2;
+      w /= 2;
+    } else {
+      cur = y;
+    }
+  }
+
+  void pool(const Stage& st) {
+    const int64_t n0 = n, c0 = c, h0 = h, w0 = w;
+    const Tensor x = cur;
+    Plan& P = p;
+    if (st.op == StageOp::GlobalPool) {
+      const Tensor y = own(p, {n, c, 1, 1});
+      p.fwd.push_back([=](Run&, void* s) {
+        check(omt_adapool_fwd(n0 * c0, h0, w0, 1, 1, fp(x), fpm(y), s), "plan: global average pool");
+      });
+      tape.push_back([&P, n0, c0, h0, w0](Tensor& gy, bool) {
+        const Tensor go = gy, gx = own(P, {n0, c0, h0, w0});
+        P.bwd.push_back([=](Run&, void* s) {
+          check(omt_adapool_bwd(n0 * c0, h0, w0, 1, 1, fp(go), fpm(gx), s), "plan: global average pool backward");
+        });
+        gy = gx;
+      });
+      cur = y;
+      h = w = 1;
+      return;
+    }
+    cover(h >= 2 && w >= 2, "2x2 pool over an image smaller than 2x2");
+    const int64_t oh = h / 2, ow = w / 2;
+    const Tensor y = own(p, {n, c, oh, ow});
+    if (st.op == StageOp::MaxPool) {
+      const Tensor idx = own(p, {n, c, oh, ow}, at::kLong);
+      p.fwd.push_back([=](Run&, void* s) {
+        check(omt_maxpool_fwd(n0 * c0, h0, w0, oh, ow, 2, 2, 2, 2, 0, 0, 1, 1, fp(x), fpm(y),
+                              idx.mutable_data_ptr<int64_t>(), s),
+              "plan: max pool");
+      });
+      tape.push_back([&P, n0, c0, h0, w0, idx](Tensor& gy, bool) {
+        const Tensor go = gy, gx = own(P, {n0, c0, h0, w0});
+        P.bwd.push_back([=](Run&, void* s) {
+          check(omt_maxpool_bwd(n0 * c0, h0, w0, h0 / 2, w0 / 2, 2, 2, 2, 2, 0, 0, 1, 1, fp(go),
+                                idx.data_ptr<int64_t>(), fpm(gx), s),
+                "plan: max pool backward");
+        });
+        gy = gx;
+      });
+    } else {
+      p.fwd.push_back([=](Run&, void* s) {
+        check(omt_avgpool_fwd(n0 * c0, h0, w0, oh, ow, 2, 2, 2, 2, 0, 0, 1, 0, fp(x), fpm(y), s), "plan: avg pool");
+      });
+      tape.push_back([&P, n0, c0, h0, w0](Tensor& gy, bool) {
+        const Tensor go = gy, gx = own(P, {n0, c0, h0, w0});
+        P.bwd.push_back([=](Run&, void* s) {
+          check(omt_avgpool_bwd(n0 * c0, h0, w0, h0 / 2, w0 / 2, 2, 2, 2, 2, 0, 0, 1, 0, fp(go), fpm(gx), s),
+                "plan: avg pool backward");
+        });
+        gy = gx;
+      });
+    }
+    cur = y;
+    h = oh;
+    w = ow;
+  }
+};
 
 static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, std::vector<int64_t> shape, bool train,
                                         bool input_grad, std::vector<Tensor> params, std::vector<Tensor> rms,
@@ -155,275 +409,33 @@ static std::shared_ptr<Plan> build_plan(const std::vector<PlanLayer>& layers, st
   for (auto& t : params) cover(is_dev(t) && f32(t) && t.is_contiguous(), "plan parameters must be contiguous float32 device tensors");
   for (auto& t : rms) cover(is_dev(t) && f32(t) && t.is_contiguous(), "running statistics on the device");
   for (auto& t : rvs) cover(is_dev(t) && f32(t) && t.is_contiguous(), "running statistics on the device");
+  const std::vector<Stage> stages = fuse_stages(layers, train, g_fold);
   auto P = std::make_shared<Plan>();
   Plan& p = *P;
   p.train = train;
   p.input_grad = input_grad;
-  p.params = params;
-  p.rms = rms;
-  p.rvs = rvs;
+  p.params = std::move(params);
+  p.rms = std::move(rms);
+  p.rvs = std::move(rvs);
   p.in_shape = shape;
-  for (auto& t : params) p.grad_shapes.push_back(t.sizes().vec());
-  int64_t n = shape[0], c = shape[1], h = shape[2], w = shape[3];
-  p.xin = own(p, {n, c, h, w});
-  Tensor cur = p.xin;
-  std::vector<BackRec> recs;
-  int pi = 0, bi = 0;
-  struct Pending {
-    bool on = false;
-    int bn = -1, gamma = -1;
-  } pend;
-  for (size_t li = 0; li < layers.size(); ++li) {
-    const PlanLayer& L = layers[li];
-    if (L.kind == "conv" || L.kind == "dw") {
-      const bool dw = L.kind == "dw";
-      const int64_t co = dw ? c : L.co, ks = L.ks;
-      cover(L.ci == c && pi < (int)params.size(), "layer channels");
-      Tensor out = own(p, {n, co, h, w});
-      omt_conv_geo g = conv_geo(n, c, co, h, w, ks, 1, ks / 2);
-      cover(g.oh == h && g.ow == w, "'same' convolution");
-      Tensor wt = params[pi];
-      const float *bm = nullptr, *bv = nullptr, *bg = nullptr, *bb = nullptr;
-      if (pend.on) {  // eval: previous BatchNorm + ReLU applied by this conv's loader
-        bm = fp(rms[pend.bn]);
-        bv = fp(rvs[pend.bn]);
-        bg = fp(params[pend.gamma]);
-        bb = fp(params[pend.gamma + 1]);
-        pend.on = false;
-      }
-      if (dw) {
-        p.fwd.push_back([g, x = cur, wt, out, bm, bv, bg, bb](Run&, void* s) {
-          check(omt_dw_fwd(&g, fp(x), fp(wt), nullptr, bm, bv, bg, bb, 1e-5f, fpm(out), s), "plan: depthwise conv");
-        });
-      } else {
-        tune_conv(OMT_DIR_FWD, g);
-        Tensor ws = own_ws(p, omt_conv_fwd_workspace(&g));
-        p.fwd.push_back([g, x = cur, wt, out, bm, bv, bg, bb, ws](Run&, void* s) {
-          check(omt_conv_fwd(&g, fp(x), fp(wt), nullptr, 0, bm, bv, bg, bb, 1e-5f, fpm(out), wsptr(ws), wsbytes(ws), s),
-                "plan: conv");
-        });
-      }
-      BackRec r;
-      r.kind = L.kind;
-      r.x = cur;
-      r.param = pi;
-      r.n = n;
-      r.c = c;
-      r.co = co;
-      r.h = h;
-      r.w = w;
-      r.ks = ks;
-      recs.push_back(r);
-      cur = out;
-      c = co;
-      ++pi;
-    } else if (L.kind == "bn") {
-      cover(L.ci == c && pi + 1 < (int)params.size() && bi < (int)rms.size(), "layer channels");
-      bool next_conv = false;
-      if (li + 1 < layers.size() && g_fold > 0) {
-        const PlanLayer& N = layers[li + 1];
-        next_conv = g_fold >= 2 ? (N.kind == "conv" || N.kind == "dw") : (N.kind == "conv" && N.ks == 1);
-      }
-      if (!train && next_conv) {  // folded into the consumer's loader
-        pend.on = true;
-        pend.bn = bi;
-        pend.gamma = pi;
-        ++bi;
-        pi += 2;
-        continue;
-      }
-      const int64_t hw = h * w;
-      Tensor y = own(p, {n, c, h, w});
-      Tensor gamma = params[pi], beta = params[pi + 1], rm = rms[bi], rv = rvs[bi];
-      BackRec r;
-      // training: a following 2x2 max pool runs inside the BatchNorm's apply pass (one launch fewer, y not re-read)
-      const bool fuse_pool = train && li + 1 < layers.size() && layers[li + 1].kind == "pool" && h >= 2 && w >= 2;
-      Tensor pout, pidx;
-      if (fuse_pool) {
-        pout = own(p, {n, c, h / 2, w / 2});
-        pidx = own(p, {n, c, h / 2, w / 2}, at::kLong);
-      }
-      if (train) {
-        Tensor sm = own(p, {c}), si = own(p, {c});
-        Tensor ws = own_ws(p, omt_bn_train_workspace(n, c, hw));
-        const double mom = L.momentum;
-        const int64_t h0 = h, w0 = w;
-        p.fwd.push_back([=](Run&, void* s) {
-          float* rmp = rm.mutable_data_ptr<float>();
-          float* rvp = rv.mutable_data_ptr<float>();
-          if (fuse_pool)
-            check(omt_bn_train_fwd_pool(n, c, h0, w0, fp(cur), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y),
-                                        fpm(sm), fpm(si), rmp, rvp, 2, 2, 2, 2, 0, 0, fpm(pout),
-                                        pidx.mutable_data_ptr<int64_t>(), wsptr(ws), wsbytes(ws), s),
-                  "plan: batch norm + max pool");
-          else
-            check(omt_bn_train_fwd(n, c, hw, fp(cur), fp(gamma), fp(beta), rmp, rvp, mom, 1e-5, 1, fpm(y), fpm(sm),
-                                   fpm(si), rmp, rvp, wsptr(ws), wsbytes(ws), s),
-                  "plan: batch norm");
-        });
-        r.sm = sm;
-        r.si = si;
-      } else {
-        p.fwd.push_back([=](Run&, void* s) {
-          check(omt_bn_eval_fwd(n, c, hw, fp(cur), fp(gamma), fp(beta), fp(rm), fp(rv), 1e-5, 1, fpm(y), s),
-                "plan: batch norm (eval)");
-        });
-      }
-      r.kind = "bn";
-      r.x = cur;
-      r.y = y;
-      r.param = pi;
-      r.n = n;
-      r.c = c;
-      r.h = h;
-      r.w = w;
-      recs.push_back(r);
-      cur = y;
-      ++bi;
-      pi += 2;
-      if (fuse_pool) {  // the pool layer's record (its backward step is unchanged); the layer itself is done
-        BackRec pr;
-        pr.kind = "pool";
-        pr.idx = pidx;
-        pr.n = n;
-        pr.c = c;
-        pr.h = h;
-        pr.w = w;
-        recs.push_back(pr);
-        cur = pout;
-        h /= 2;
-        w /= 2;
-        ++li;
-      }
-    } else if (L.kind == "pool" || L.kind == "apool") {
-      cover(h >= 2 && w >= 2, "2x2 pool over an image smaller than 2x2");
-      const int64_t oh = h / 2, ow = w / 2;
-      Tensor out = own(p, {n, c, oh, ow});
-      BackRec r;
-      r.kind = L.kind;
-      if (L.kind == "pool") {
-        Tensor idx = own(p, {n, c, oh, ow}, at::kLong);
-        p.fwd.push_back([=](Run&, void* s) {
-          check(omt_maxpool_fwd(n * c, h, w, oh, ow, 2, 2, 2, 2, 0, 0, 1, 1, fp(cur), fpm(out),
-                                idx.mutable_data_ptr<int64_t>(), s),
-                "plan: max pool");
-        });
-        r.idx = idx;
-      } else {
-        p.fwd.push_back([=](Run&, void* s) {
-          check(omt_avgpool_fwd(n * c, h, w, oh, ow, 2, 2, 2, 2, 0, 0, 1, 0, fp(cur), fpm(out), s), "plan: avg pool");
-        });
-      }
-      r.n = n;
-      r.c = c;
-      r.h = h;
-      r.w = w;
-      recs.push_back(r);
-      cur = out;
-      h = oh;
-      w = ow;
-    } else if (L.kind == "gap") {
-      Tensor out = own(p, {n, c, 1, 1});
-      p.fwd.push_back([=](Run&, void* s) {
-        check(omt_adapool_fwd(n * c, h, w, 1, 1, fp(cur), fpm(out), s), "plan: global average pool");
-      });
-      BackRec r;
-      r.kind = "gap";
-      r.n = n;
-      r.c = c;
-      r.h = h;
-      r.w = w;
-      recs.push_back(r);
-      cur = out;
-      h = w = 1;
-    } else {
-      throw NotCovered("unknown layer kind " + L.kind);
+  for (auto& t : p.params) p.grad_shapes.push_back(t.sizes().vec());
+  p.xin = own(p, {shape[0], shape[1], shape[2], shape[3]});
+  PlanBuilder b{p, layers, p.xin, shape[0], shape[1], shape[2], shape[3]};
+  for (const Stage& st : stages) {
+    switch (st.op) {
+      case StageOp::Conv:
+      case StageOp::Depthwise: b.conv(st); break;
+      case StageOp::BatchNorm:
+      case StageOp::BatchNormPool: b.batch_norm(st); break;
+      default: b.pool(st); break;
     }
   }
-  cover(!pend.on, "a folded BatchNorm needs a following convolution");
-  p.xout = cur;
-  p.out_shape = {n, c, h, w};
+  p.xout = b.cur;
+  p.out_shape = {b.n, b.c, b.h, b.w};
   if (!train) return P;
-
-  // ---- backward, in reverse ----
   p.gout = own(p, p.out_shape);
   Tensor g = p.gout;
-  for (int ri = (int)recs.size() - 1; ri >= 0; --ri) {
-    const BackRec r = recs[ri];
-    const bool first = ri == 0;
-    const int64_t n_ = r.n, c_ = r.c, h_ = r.h, w_ = r.w;
-    if (r.kind == "pool" || r.kind == "apool" || r.kind == "gap") {
-      Tensor gx = own(p, {n_, c_, h_, w_});
-      if (r.kind == "pool") {
-        Tensor idx = r.idx;
-        p.bwd.push_back([=](Run&, void* s) {
-          check(omt_maxpool_bwd(n_ * c_, h_, w_, h_ / 2, w_ / 2, 2, 2, 2, 2, 0, 0, 1, 1, fp(g), idx.data_ptr<int64_t>(),
-                                fpm(gx), s),
-                "plan: max pool backward");
-        });
-      } else if (r.kind == "apool") {
-        p.bwd.push_back([=](Run&, void* s) {
-          check(omt_avgpool_bwd(n_ * c_, h_, w_, h_ / 2, w_ / 2, 2, 2, 2, 2, 0, 0, 1, 0, fp(g), fpm(gx), s),
-                "plan: avg pool backward");
-        });
-      } else {
-        p.bwd.push_back([=](Run&, void* s) {
-          check(omt_adapool_bwd(n_ * c_, h_, w_, 1, 1, fp(g), fpm(gx), s), "plan: global average pool backward");
-        });
-      }
-      g = gx;
-    } else if (r.kind == "bn") {
-      Tensor gx = own(p, {n_, c_, h_, w_});
-      Tensor ws = own_ws(p, omt_bn_bwd_workspace(n_, c_, h_ * w_));
-      Tensor x = r.x, y = r.y, sm = r.sm, si = r.si, gamma = params[r.param];
-      const int gi = r.param;
-      p.bwd.push_back([=](Run& run, void* s) {
-        check(omt_bn_bwd(n_, c_, h_ * w_, fp(g), fp(x), fp(y), fp(sm), fp(si), fp(gamma), fpm(gx), fpm(run.grads[gi]),
-                         fpm(run.grads[gi + 1]), wsptr(ws), wsbytes(ws), s),
-              "plan: batch norm backward");
-      });
-      g = gx;
-    } else {  // conv / dw
-      const bool dw = r.kind == "dw";
-      omt_conv_geo geo = conv_geo(n_, c_, r.co, h_, w_, r.ks, 1, r.ks / 2);
-      Tensor x = r.x, wt = params[r.param];
-      const int gi = r.param;
-      if (!dw && (!first || input_grad)) {
-        // dense with both gradients: one call, the two GEMMs share a launch when their plans allow it
-        tune_conv_bwd(geo);
-        Tensor gx = own(p, {n_, c_, h_, w_});
-        Tensor bws = own_ws(p, omt_conv_bwd_workspace(&geo));
-        p.bwd.push_back([=](Run& run, void* s) {
-          check(omt_conv_bwd(&geo, fp(x), fp(g), fp(wt), fpm(gx), fpm(run.grads[gi]), wsptr(bws), wsbytes(bws), s),
-                "plan: input and weight gradients");
-        });
-        g = gx;
-        continue;
-      }
-      if (!dw) tune_conv(OMT_DIR_WGRAD, geo);
-      Tensor wws = own_ws(p, dw ? omt_dw_wgrad_workspace(&geo) : omt_conv_wgrad_workspace(&geo));
-      p.bwd.push_back([=](Run& run, void* s) {
-        if (dw)
-          check(omt_dw_wgrad(&geo, fp(x), fp(g), fpm(run.grads[gi]), wsptr(wws), wsbytes(wws), s),
-                "plan: depthwise weight gradient");
-        else
-          check(omt_conv_wgrad(&geo, fp(x), fp(g), fpm(run.grads[gi]), wsptr(wws), wsbytes(wws), s),
-                "plan: weight gradient");
-      });
-      if (!first || input_grad) {
-        Tensor gx = own(p, {n_, c_, h_, w_});
-        if (!dw) tune_conv(OMT_DIR_DGRAD, geo);
-        Tensor dws = dw ? Tensor() : own_ws(p, omt_conv_dgrad_workspace(&geo));
-        p.bwd.push_back([=](Run&, void* s) {
-          if (dw)
-            check(omt_dw_dgrad(&geo, fp(g), fp(wt), fpm(gx), s), "plan: depthwise input gradient");
-          else
-            check(omt_conv_dgrad(&geo, fp(g), fp(wt), fpm(gx), wsptr(dws), wsbytes(dws), s), "plan: input gradient");
-        });
-        g = gx;
-      }
-    }
-  }
+  for (int i = (int)b.tape.size() - 1; i >= 0; --i) b.tape[i](g, i == 0);
   p.gin = g;
   return P;
 }

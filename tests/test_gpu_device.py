@@ -685,6 +685,16 @@ def test_fused_stack_matches_unfused_with_grad_accumulation_and_eval_fold(clean)
     with torch.no_grad():  # eval plan: BN+ReLU before the 1x1 conv folded into its loader
         xe = D(torch.randn(3, 4, 16, 16), omt)
         assert rel(fused(xe), ref(xe)) <= TOL
+        core = omt.native.core
+        prev = core.get_fold()
+        try:  # fold policies 0 (none) and 2 (every conv and depthwise conv: the 3x3, depthwise and 5x5 too); a new
+            # batch size per policy, so that each builds its own plan
+            for policy, nb in ((0, 4), (2, 5)):
+                core.set_fold(policy)
+                xe = D(torch.randn(nb, 4, 16, 16), omt)
+                assert rel(fused(xe), ref(xe)) <= TOL, policy
+        finally:
+            core.set_fold(prev)
 
 
 def test_compile_backend_residual_block(clean):
