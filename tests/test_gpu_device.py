@@ -232,6 +232,14 @@ def test_foreach_lists_and_fused_optimizers(clean):
             o_dev.step()
         for pc, pd in zip(p_cpu, p_dev):
             assert rel(pd, pc) <= 1e-5, cls
+    from omarchy_mac_torch import optim as fused_optim
+    p_dev = [D(torch.randn(3), omt).requires_grad_()]
+    assert torch.optim.Adam(p_dev, lr=1e-3, foreach=False).defaults["fused"] is None  # the caller's choice stands
+    assert torch.optim.SGD([{"params": p_dev}], lr=0.1).defaults["fused"] is True  # parameter groups
+    assert fused_optim.keeps_torch_default(p_dev, {"foreach": False}) == "foreach= given by the caller"
+    assert fused_optim.keeps_torch_default(p_dev + [torch.zeros(1)], {}) == "parameters not all on the device"
+    assert fused_optim.keeps_torch_default(p_dev, {"lr": torch.tensor(0.1)}) == "a tensor learning rate"
+    assert fused_optim.keeps_torch_default(p_dev, {"differentiable": True}) == "differentiable=True"
 
 
 OPTIM_CASES = [
