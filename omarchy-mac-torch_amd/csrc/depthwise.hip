@@ -766,10 +766,14 @@ static int64_t dw_s1_groups(const omt_conv_geo* g) {
 // (576 channels, 5x5), 14x14 18.5 -> 11.9 us (240 channels, 5x5); from 28x28 up the row-chunk kernel is faster
 // (28x28: 12.9 against 16.1 us), so larger planes keep it.
 constexpr int kDwBatchNT = 256, kDwBatchMaxHW = 256;
+constexpr int64_t kDwBatchMinWgs = 4 * 256;
 static DwBatch dw_batch(const omt_conv_geo* g) {
   DwBatch d{};
   const int64_t hw = g->ih * g->iw, tile = (g->ih + g->ks - 1) * (g->iw + g->ks - 1);
   int64_t b = std::min<int64_t>({(int64_t)kDwBatchEPT * kDwBatchNT / hw, g->n, (int64_t)kDwMaxLds / 4 / tile});
+  // fewer images per workgroup where a workgroup per channel (and image group) would leave under four per CU: each
+  // workgroup is one load -> LDS -> taps -> store chain, and more of them overlap their chains
+  b = std::min<int64_t>(b, std::max<int64_t>(1, cdiv(g->n, cdiv(kDwBatchMinWgs, g->ci))));
   d.B = (int)std::max<int64_t>(b, 0);
   d.tile = (int)tile;
   d.pitch = (int)(g->iw + g->ks - 1);
