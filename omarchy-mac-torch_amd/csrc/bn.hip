@@ -570,6 +570,9 @@ constexpr int64_t kFusedSmall = 2048;
 // channel, reading its outputs back, took twice as long as the split apply + pool.
 constexpr int64_t kFusedLarge = 32768, kFusedLargeBwd = 28672;
 constexpr int kFusedLargeThreads = 1024;
+// Channels of kFusedSmall .. kFusedMax elements with 16-byte vectors take 1024-thread workgroups too (two float4 per
+// thread and operand): a workgroup per channel is one load -> reduce -> apply chain, and with a few hundred channels
+// there is about one per CU, whose loads in flight the four times more threads multiply.
 
 // PARTS: x holds `slices` convolution partials of pstride elements each; every element is summed over them in slice
 // order (the convolution slice sum's order, so xo, written with the sums, equals the summed convolution output).
@@ -1039,7 +1042,13 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
                      new_rv, (int)c, (int)hw, f, 1, 0, nullptr, z)
     const bool sm = n * hw <= kFusedSmall;
     if (vec) {
-      if (sm) OMT_BN_FUSED(4, (int)kFusedSmall); else OMT_BN_FUSED(4, (int)kFusedMax);
+      if (sm)
+        OMT_BN_FUSED(4, (int)kFusedSmall);
+      else
+        hipLaunchKernelGGL((bn_train_fused_kernel<4, false, false, (int)kFusedMax, kFusedLargeThreads>),
+                           dim3((unsigned)c), dim3(kFusedLargeThreads), 0, s, x, gamma, beta, running_mean, running_var,
+                           momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f,
+                           1, 0, nullptr, z);
     } else {
       if (sm) OMT_BN_FUSED(1, (int)kFusedSmall); else OMT_BN_FUSED(1, (int)kFusedMax);
     }
@@ -1161,7 +1170,13 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
                      new_rv, (int)c, (int)hw, f, slices, total, x, z)
     const bool sm = n * hw <= kFusedSmall;
     if (vec) {
-      if (sm) OMT_BN_PARTS(4, (int)kFusedSmall); else OMT_BN_PARTS(4, (int)kFusedMax);
+      if (sm)
+        OMT_BN_PARTS(4, (int)kFusedSmall);
+      else
+        hipLaunchKernelGGL((bn_train_fused_kernel<4, true, false, (int)kFusedMax, kFusedLargeThreads>),
+                           dim3((unsigned)c), dim3(kFusedLargeThreads), 0, s, parts, gamma, beta, running_mean,
+                           running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
+                           (int)hw, f, slices, total, x, z);
     } else {
       if (sm) OMT_BN_PARTS(1, (int)kFusedSmall); else OMT_BN_PARTS(1, (int)kFusedMax);
     }
@@ -1272,7 +1287,12 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
                      save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act)
     const bool sm = n * hw <= kFusedSmall;
     if (sp.vec == 4) {
-      if (sm) OMT_BN_BWD(4, (int)kFusedSmall); else OMT_BN_BWD(4, (int)kFusedMax);
+      if (sm)
+        OMT_BN_BWD(4, (int)kFusedSmall);
+      else
+        hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES, false, (int)kFusedMax, kFusedLargeThreads>), dim3((unsigned)c),
+                           dim3(kFusedLargeThreads), 0, s, g, g2, x, relu_y, save_mean, save_invstd, gamma, gx, dgamma,
+                           dbeta, gzo, (int)c, (int)hw, sp, act);
     } else {
       if (sm) OMT_BN_BWD(1, (int)kFusedSmall); else OMT_BN_BWD(1, (int)kFusedMax);
     }
