@@ -835,6 +835,9 @@ __global__ void __launch_bounds__(NT) bn_bwd_fused_kernel(const float* __restric
   using V = typename VecT<VEC>::T;
   __shared__ float kc[5];
   if (PARTS && (int)blockIdx.x >= c) {
+    // the slice sums take kSumThreads threads; a larger workgroup's other waves end here, whole waves, and the sums'
+    // barriers wait for the waves still running only
+    if (NT > kSumThreads && (int)threadIdx.x >= kSumThreads) return;
     run_side_sum(side, (int64_t)blockIdx.x - c);
     return;
   }
@@ -1418,11 +1421,18 @@ OMT_EXPORT int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g
     if (n * hw <= kFusedSmall) OMT_BWD_PARTS(V, R, (int)kFusedSmall);               \
     else OMT_BWD_PARTS(V, R, (int)kFusedMax);                                        \
   } while (0)
-  if (sp.vec == 4) {
+#define OMT_BWD_PARTS_MID(R)                                                                                       \
+  hipLaunchKernelGGL((bn_bwd_fused_kernel<4, R, true, (int)kFusedMax, kFusedLargeThreads>), dim3((unsigned)blocks), \
+                     dim3(kFusedLargeThreads), 0, s, g_parts, g2, x, ry, save_mean, save_invstd, gamma, gx, dgamma,    \
+                     dbeta, gz, (int)c, (int)hw, sp, act, slices, pstride, side)
+  if (sp.vec == 4 && n * hw > kFusedSmall) {  // 1024-thread workgroups for channels of 2K-8K elements
+    if (gz) OMT_BWD_PARTS_MID(true); else OMT_BWD_PARTS_MID(false);
+  } else if (sp.vec == 4) {
     if (gz) OMT_BWD_PARTS_E(4, true); else OMT_BWD_PARTS_E(4, false);
   } else {
     if (gz) OMT_BWD_PARTS_E(1, true); else OMT_BWD_PARTS_E(1, false);
   }
+#undef OMT_BWD_PARTS_MID
 #undef OMT_BWD_PARTS_E
 #undef OMT_BWD_PARTS
   return launch_check("bn_bwd_fused_kernel");

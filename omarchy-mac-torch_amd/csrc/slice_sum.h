@@ -51,6 +51,9 @@ __device__ __forceinline__ void sum_slices(const typename VecF<VEC>::T* __restri
   }
 }
 
+// The slice sums run on kSumThreads threads of a workgroup (a larger workgroup's other waves end before them).
+constexpr int kSumThreads = 256;
+
 // Sums the slices in slice order (deterministic): out[i] = sum_z part[z][i]. VEC 4 needs n % 4 == 0. Workgroups
 // b0 .. b0 + nb - 1 of the launch stride over the vectors.
 template <int VEC>
@@ -58,7 +61,7 @@ __device__ __forceinline__ void split_sum(const float* __restrict__ part, float*
                                           int slices, int64_t b0, int64_t nb) {
   using T = typename VecF<VEC>::T;
   const int64_t nv = n / VEC;
-  for (int64_t i = b0 * blockDim.x + threadIdx.x; i < nv; i += nb * blockDim.x) {
+  for (int64_t i = b0 * kSumThreads + threadIdx.x; i < nv; i += nb * kSumThreads) {
     float v[VEC];
     sum_slices<VEC>(reinterpret_cast<const T*>(part), nv, i, slices, v);
     reinterpret_cast<T*>(out)[i] = VecF<VEC>::pack(v);
