@@ -253,7 +253,7 @@ RESNET_FAMILIES = [
     # (family, substrings of the kernel name), first match wins
     ("omt conv_bwd_dual_kernel (grad input + grad weight, one launch)", ("conv_bwd_dual_kernel",)),
     ("omt gather (forward; grad input alone)", GATHER_KERNELS),
-    ("omt conv_wgrad_kernel (grad weight alone)", ("conv_wgrad_kernel",)),
+    ("omt conv_wgrad_kernel (grad weight alone)", ("conv_wgrad_kernel", "conv_wgrad_nhwc_kernel")),
     ("omt split-K sums (gather_reduce, split_reduce, dual_reduce)", ("gather_reduce", "split_reduce", "dual_reduce")),
     ("omt filter re-pack", ("pack_tapmajor", "pack_dgrad")),
     ("omt BatchNorm", ("omt::bn_",)),
@@ -263,7 +263,7 @@ RESNET_FAMILIES = [
     ("omt fused Adam / SGD (multi-tensor)", ("fused_adam_kernel", "fused_sgd_kernel")),
     ("omt log-softmax / NLL loss", ("log_softmax_", "nll_fwd_kernel", "nll_bwd_kernel")),
     ("omt pointwise, plane sums, bias gradient, step counts and batch counters",
-     ("pointwise_kernel", "plane_s", "foreach_add_kernel", "zero_fill_kernel", "bias_grad_kernel")),
+     ("pointwise_kernel", "plane_s", "foreach_add_kernel", "zero_fill_kernel", "bias_grad_kernel", "bias_grad_cols")),
     ("torch fused Adam", ("FusedAdam",)),
     ("torch foreach / elementwise (counters, ReLU, add)", ("BinaryOpScalarFunctor", "foreach", "elementwise")),
     ("hipBLASLt / rocBLAS GEMM (linear layer)", ("Cijk", "hipblaslt", "rocblas")),
@@ -272,12 +272,13 @@ RESNET_FAMILIES = [
 ]
 
 
-def resnet_trace_summary(trace_csv, replays=22):
-    """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` (or
-    `--workload mobilenet`) and prints, for
-    the compiled graphed replays (the last run of `replays` identical steps), the eager-model graphed replays (the
-    run before it) and the compiled model with the backend's own graph replay (the run before that: its 20 timed
-    steps), kernel time per step by family as markdown. Replays of one graph launch the same dispatch sequence, so a
+def resnet_trace_summary(trace_csv, replays=22, channels_last=True):
+    """Reads the kernel_trace.csv of a `rocprofv3 --kernel-trace` run of `bench.py --workload resnet` (or, with
+    channels_last False, `--workload mobilenet`, which has no channels-last run) and prints, for the channels-last
+    compiled graphed replays (ResNet-18's last run), the compiled graphed replays (the last run of `replays`
+    identical steps before it), the eager-model graphed replays (the run before that) and the compiled model with
+    the backend's own graph replay (the run before that: its 20 timed steps), kernel time per step by family as
+    markdown. Replays of one graph launch the same dispatch sequence, so a
     run is the latest stretch of the trace that repeats with some period D `replays` times (20 for the third); any D
     consecutive dispatches of it are one step's launches."""
     import csv
@@ -300,14 +301,15 @@ def resnet_trace_summary(trace_csv, replays=22):
 
     runs = []
     hi = len(names)
-    for reps in (replays, replays, 20):
+    for reps in ((replays,) if channels_last else ()) + (replays, replays, 20):
         found = periodic_run(hi, max(0, hi - 20000), reps)
         if not found:
             break
         st, d = found
         runs.append((reps, rows[st:st + reps * d]))
         hi = st
-    titles = ("compiled model, whole step captured by the caller (graphs.Graph) and replayed",
+    titles = (("channels_last compiled model, whole step captured by the caller and replayed",) if channels_last
+              else ()) + ("compiled model, whole step captured by the caller (graphs.Graph) and replayed",
               "eager model, whole step captured by the caller and replayed",
               "compiled model alone: the backend replays its forward and backward graphs, the rest runs eagerly")
     for title, (replays, run) in zip(titles, runs):
@@ -1167,6 +1169,8 @@ def main():
                          "(--no-bw --no-models --no-cpu, same --steps)")
     ap.add_argument("--resnet-trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="kernel time per step by family of a rocprofv3 --kernel-trace run of --workload resnet")
+    ap.add_argument("--mobilenet-trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="the same for a run of --workload mobilenet (no channels-last run)")
     ap.add_argument("--resnet-layer-trace", metavar="KERNEL_TRACE_CSV",
                     help="ResNet-18's convolution launches per layer (workgroups, us) from a rocprofv3 --kernel-trace "
                          "run of --workload resnet-layers --no-tune")
@@ -1193,6 +1197,9 @@ def main():
         return
     if args.resnet_trace_summary:
         resnet_trace_summary(args.resnet_trace_summary)
+        return
+    if args.mobilenet_trace_summary:
+        resnet_trace_summary(args.mobilenet_trace_summary, channels_last=False)
         return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps, len(C5_LAYERS if args.workload == "c5" else C1_LAYERS))
