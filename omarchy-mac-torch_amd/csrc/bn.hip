@@ -570,6 +570,8 @@ constexpr int64_t kFusedSmall = 2048;
 // channel, reading its outputs back, took twice as long as the split apply + pool.
 constexpr int64_t kFusedLarge = 32768, kFusedLargeBwd = 28672;
 constexpr int kFusedLargeThreads = 1024;
+// and channels of kFusedSmall / 2 .. kFusedSmall elements with 16-byte vectors 512-thread ones (one vector each)
+constexpr int kFusedSmallThreads = 512;
 // Channels of kFusedSmall .. kFusedMax elements with 16-byte vectors take 1024-thread workgroups too (two float4 per
 // thread and operand): a workgroup per channel is one load -> reduce -> apply chain, and with a few hundred channels
 // there is about one per CU, whose loads in flight the four times more threads multiply.
@@ -1045,7 +1047,12 @@ OMT_EXPORT int omt_bn_train_fwd_res(int64_t n, int64_t c, int64_t hw, const floa
                      new_rv, (int)c, (int)hw, f, 1, 0, nullptr, z)
     const bool sm = n * hw <= kFusedSmall;
     if (vec) {
-      if (sm)
+      if (sm && n * hw > kFusedSmall / 2)
+        hipLaunchKernelGGL((bn_train_fused_kernel<4, false, false, (int)kFusedSmall, kFusedSmallThreads>),
+                           dim3((unsigned)c), dim3(kFusedSmallThreads), 0, s, x, gamma, beta, running_mean, running_var,
+                           momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c, (int)hw, f,
+                           1, 0, nullptr, z);
+      else if (sm)
         OMT_BN_FUSED(4, (int)kFusedSmall);
       else
         hipLaunchKernelGGL((bn_train_fused_kernel<4, false, false, (int)kFusedMax, kFusedLargeThreads>),
@@ -1173,7 +1180,12 @@ OMT_EXPORT int omt_bn_train_fwd_parts(int64_t n, int64_t c, int64_t hw, const fl
                      new_rv, (int)c, (int)hw, f, slices, total, x, z)
     const bool sm = n * hw <= kFusedSmall;
     if (vec) {
-      if (sm)
+      if (sm && n * hw > kFusedSmall / 2)
+        hipLaunchKernelGGL((bn_train_fused_kernel<4, true, false, (int)kFusedSmall, kFusedSmallThreads>),
+                           dim3((unsigned)c), dim3(kFusedSmallThreads), 0, s, parts, gamma, beta, running_mean,
+                           running_var, momentum, eps, relu, residual, y, save_mean, save_invstd, new_rm, new_rv, (int)c,
+                           (int)hw, f, slices, total, x, z);
+      else if (sm)
         OMT_BN_PARTS(4, (int)kFusedSmall);
       else
         hipLaunchKernelGGL((bn_train_fused_kernel<4, true, false, (int)kFusedMax, kFusedLargeThreads>),
@@ -1290,7 +1302,11 @@ static int bn_bwd_impl(int64_t n, int64_t c, int64_t hw, const float* g, const f
                      save_mean, save_invstd, gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act)
     const bool sm = n * hw <= kFusedSmall;
     if (sp.vec == 4) {
-      if (sm)
+      if (sm && n * hw > kFusedSmall / 2)
+        hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES, false, (int)kFusedSmall, kFusedSmallThreads>),
+                           dim3((unsigned)c), dim3(kFusedSmallThreads), 0, s, g, g2, x, relu_y, save_mean, save_invstd,
+                           gamma, gx, dgamma, dbeta, gzo, (int)c, (int)hw, sp, act);
+      else if (sm)
         OMT_BN_BWD(4, (int)kFusedSmall);
       else
         hipLaunchKernelGGL((bn_bwd_fused_kernel<4, RES, false, (int)kFusedMax, kFusedLargeThreads>), dim3((unsigned)c),
@@ -1425,13 +1441,20 @@ OMT_EXPORT int omt_bn_bwd_parts(int64_t n, int64_t c, int64_t hw, const float* g
   hipLaunchKernelGGL((bn_bwd_fused_kernel<4, R, true, (int)kFusedMax, kFusedLargeThreads>), dim3((unsigned)blocks), \
                      dim3(kFusedLargeThreads), 0, s, g_parts, g2, x, ry, save_mean, save_invstd, gamma, gx, dgamma,    \
                      dbeta, gz, (int)c, (int)hw, sp, act, slices, pstride, side)
+#define OMT_BWD_PARTS_SM(R)                                                                                          \
+  hipLaunchKernelGGL((bn_bwd_fused_kernel<4, R, true, (int)kFusedSmall, kFusedSmallThreads>), dim3((unsigned)blocks), \
+                     dim3(kFusedSmallThreads), 0, s, g_parts, g2, x, ry, save_mean, save_invstd, gamma, gx, dgamma,     \
+                     dbeta, gz, (int)c, (int)hw, sp, act, slices, pstride, side)
   if (sp.vec == 4 && n * hw > kFusedSmall) {  // 1024-thread workgroups for channels of 2K-8K elements
     if (gz) OMT_BWD_PARTS_MID(true); else OMT_BWD_PARTS_MID(false);
+  } else if (sp.vec == 4 && n * hw > kFusedSmall / 2) {  // 512-thread ones for 1K-2K
+    if (gz) OMT_BWD_PARTS_SM(true); else OMT_BWD_PARTS_SM(false);
   } else if (sp.vec == 4) {
     if (gz) OMT_BWD_PARTS_E(4, true); else OMT_BWD_PARTS_E(4, false);
   } else {
     if (gz) OMT_BWD_PARTS_E(1, true); else OMT_BWD_PARTS_E(1, false);
   }
+#undef OMT_BWD_PARTS_SM
 #undef OMT_BWD_PARTS_MID
 #undef OMT_BWD_PARTS_E
 #undef OMT_BWD_PARTS
