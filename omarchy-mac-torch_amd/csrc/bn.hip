@@ -1790,6 +1790,193 @@ __global__ void __launch_bounds__(256) bn_nhwc_bwd_apply_kernel(const float* __r
   }
 }
 
+// A channels-last BatchNorm of at most kNhwcFusedRows rows runs in one launch instead of three: workgroup j owns
+// channel vector j (VEC channels) over every row, thread t rows t, t + blockDim.x, ... (kNhwcFusedRpt of them, in
+// registers), so the sums, the finalize and the apply need no partials. Each lane reads VEC channels of a row, a
+// 16-byte run rows apart: one workgroup reads its vector at the rate one CU fetches scattered lines, which the
+// shortest tensors (ResNet-18 b32 64²'s last three stages: 2048 rows and fewer) finish sooner than three launches.
+// The sums are the shifted float64 sums of the three-launch path in another order (each thread's rows in order, the
+// wave sums in wave order); the finalize and apply arithmetic is the same.
+constexpr int64_t kNhwcFusedRows = 2048;
+constexpr int kNhwcFusedRpt = 2;
+
+static bool nhwc_fused_ok(const NhwcSplit& sp) { return sp.rows <= kNhwcFusedRows; }
+static unsigned nhwc_fused_threads(const NhwcSplit& sp) {
+  const int64_t t = cdiv(cdiv(sp.rows, kNhwcFusedRpt), 64) * 64;
+  return (unsigned)(t < 64 ? 64 : t);
+}
+
+// Block sums of VEC pairs of doubles over blockDim.x threads (whole waves, at most 1024): the wave sums added in
+// wave order, pair i valid in thread i.
+template <int VEC>
+__device__ __forceinline__ void nhwc_block_sums(double* a, double* b) {
+  __shared__ double sa[16][VEC], sb[16][VEC];
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    a[i] = wave_sum(a[i]);
+    b[i] = wave_sum(b[i]);
+    if ((threadIdx.x & 63) == 0) sa[wave][i] = a[i], sb[wave][i] = b[i];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < VEC) {
+    const int i = threadIdx.x;
+    double s = sa[0][i], q = sb[0][i];
+    for (int w = 1; w < nw; ++w) s += sa[w][i], q += sb[w][i];
+    a[0] = s, b[0] = q;
+  }
+}
+
+// grid cv (channel vectors), blockDim nhwc_fused_threads: the training forward of bn_nhwc_stats_kernel,
+// bn_nhwc_fin_kernel and bn_nhwc_apply_kernel in one pass over x
+template <int VEC>
+__global__ void __launch_bounds__(1024) bn_nhwc_fused_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, const float* rm,
+                                                             const float* rv, double momentum, double eps,
+                                                             const float* __restrict__ res, float* __restrict__ y,
+                                                             float* __restrict__ zo, float* __restrict__ save_mean,
+                                                             float* __restrict__ save_invstd, float* new_rm,
+                                                             float* new_rv,  // may alias rm / rv
+                                                             int c, int act, int64_t rows) {
+  using V = typename VecT<VEC>::T;
+  __shared__ float coef[2][VEC];
+  const int j = blockIdx.x, nt = blockDim.x;
+  const V shift = *reinterpret_cast<const V*>(x + (int64_t)j * VEC);
+  V r[kNhwcFusedRpt];
+#pragma unroll
+  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+    const int64_t row = threadIdx.x + (int64_t)u * nt;
+    r[u] = row < rows ? *reinterpret_cast<const V*>(x + row * c + (int64_t)j * VEC) : shift;  // d = 0 past the end
+  }
+  double s1[VEC], s2[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    s1[i] = 0.0, s2[i] = 0.0;
+#pragma unroll
+    for (int u = 0; u < kNhwcFusedRpt; ++u) {
+      const double d = (double)(vget(r[u], i) - vget(shift, i));
+      s1[i] += d;
+      s2[i] += d * d;
+    }
+  }
+  nhwc_block_sums<VEC>(s1, s2);
+  if ((int)threadIdx.x < VEC) {
+    const int i = threadIdx.x, ch = j * VEC + i;
+    const BnStats st = bn_finalize(s1[0], s2[0], (double)x[ch], (double)rows, momentum, eps, rm, rv, save_mean,
+                                   save_invstd, new_rm, new_rv, ch, true);
+    const float sc = st.invstd * gamma[ch];
+    coef[0][i] = sc;
+    coef[1][i] = beta[ch] - st.mean * sc;
+  }
+  __syncthreads();
+  float sc[VEC], sh[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) sc[i] = coef[0][i], sh[i] = coef[1][i];
+#pragma unroll
+  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+    const int64_t row = threadIdx.x + (int64_t)u * nt;
+    if (row < rows) {
+      const int64_t off = row * c + (int64_t)j * VEC;
+      V v = r[u], q, z;
+      if (res) q = *reinterpret_cast<const V*>(res + off);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float f = fmaf(vget(v, i), sc[i], sh[i]);
+        if (res) f += vget(q, i);
+        vset(z, i, f);
+        vset(v, i, bn_act(f, act));
+      }
+      if (zo) *reinterpret_cast<V*>(zo + off) = z;
+      *reinterpret_cast<V*>(y + off) = v;
+    }
+  }
+}
+
+// grid cv, blockDim nhwc_fused_threads: bn_nhwc_bwd_part_kernel, bn_nhwc_bwd_fin_kernel and bn_nhwc_bwd_apply_kernel
+// in one pass over g (+ g2), x and ry
+template <int VEC>
+__global__ void __launch_bounds__(1024) bn_nhwc_bwd_fused_kernel(const float* __restrict__ g,
+                                                                 const float* __restrict__ g2,
+                                                                 const float* __restrict__ x,
+                                                                 const float* __restrict__ ry,
+                                                                 const float* __restrict__ mean,
+                                                                 const float* __restrict__ invstd,
+                                                                 const float* __restrict__ gamma,
+                                                                 float* __restrict__ gx, float* __restrict__ dgamma,
+                                                                 float* __restrict__ dbeta, float* __restrict__ gzo,
+                                                                 int c, int act, const NhwcSplit sp, int g_nchw) {
+  using V = typename VecT<VEC>::T;
+  __shared__ float kc[VEC][5];
+  const int j = blockIdx.x, nt = blockDim.x;
+  float mu[VEC], inv[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) mu[i] = mean[j * VEC + i], inv[i] = invstd[j * VEC + i];
+  V vg[kNhwcFusedRpt], vx[kNhwcFusedRpt], vr[kNhwcFusedRpt];
+#pragma unroll
+  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+    const int64_t row = threadIdx.x + (int64_t)u * nt;
+    if (row < sp.rows) {
+      const int64_t off = row * c + (int64_t)j * VEC;
+      vg[u] = nhwc_grad<VEC>(g, g_nchw, row, j, c, sp);
+      if (g2) vadd(vg[u], *reinterpret_cast<const V*>(g2 + off));
+      vx[u] = *reinterpret_cast<const V*>(x + off);
+      if (ry) vr[u] = *reinterpret_cast<const V*>(ry + off);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        vset(vg[u], i, 0.f);  // gz = 0 contributes nothing
+        vset(vx[u], i, mu[i]);
+        vset(vr[u], i, 1.f);
+      }
+    }
+  }
+  double s1[VEC], s2[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    s1[i] = 0.0, s2[i] = 0.0;
+#pragma unroll
+    for (int u = 0; u < kNhwcFusedRpt; ++u) {
+      float gz = vget(vg[u], i);
+      if (ry) gz = bn_act_grad(gz, vget(vr[u], i), act);
+      const float xhat = (vget(vx[u], i) - mu[i]) * inv[i];
+      s1[i] += (double)gz;
+      s2[i] += (double)gz * (double)xhat;
+    }
+  }
+  nhwc_block_sums<VEC>(s1, s2);
+  if ((int)threadIdx.x < VEC) {
+    const int i = threadIdx.x, ch = j * VEC + i;
+    if (dbeta) dbeta[ch] = (float)s1[0];
+    if (dgamma) dgamma[ch] = (float)s2[0];
+    if (gx) bn_bwd_consts(s1[0], s2[0], (double)sp.rows, gamma[ch], mu[i], inv[i], kc[i]);
+  }
+  if (!gx && !gzo) return;  // uniform
+  __syncthreads();
+  float k[VEC][5];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int e = 0; e < 5; ++e) k[i][e] = kc[i][e];
+#pragma unroll
+  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+    const int64_t row = threadIdx.x + (int64_t)u * nt;
+    if (row < sp.rows) {
+      const int64_t off = row * c + (int64_t)j * VEC;
+      V o, z;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float gz = vget(vg[u], i);
+        if (ry) gz = bn_act_grad(gz, vget(vr[u], i), act);
+        vset(z, i, gz);
+        vset(o, i, bwd_elem(gz, vget(vx[u], i), 1.f, false, k[i]));
+      }
+      if (gx) *reinterpret_cast<V*>(gx + off) = o;
+      if (gzo) *reinterpret_cast<V*>(gzo + off) = z;
+    }
+  }
+}
+
 // apply-pass grid: (cblocks, chunks of about 8 rows per thread)
 static dim3 nhwc_apply_grid(const NhwcSplit& sp, int64_t& rows_per_chunk) {
   rows_per_chunk = 8 * (int64_t)sp.rl;
@@ -1830,6 +2017,17 @@ OMT_EXPORT int omt_bn_train_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const flo
     return fail(OMT_INVALID, "omt_bn_train_fwd_nhwc: workspace too small");
   hipStream_t s = stream_of(stream);
   const NhwcSplit sp = nhwc_split(n, c, hw, al16(x) && al16(y) && al16(residual) && al16(z));
+  if (nhwc_fused_ok(sp)) {
+    if (sp.vec == 4)
+      hipLaunchKernelGGL(bn_nhwc_fused_kernel<4>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, x, gamma,
+                         beta, running_mean, running_var, momentum, eps, residual, y, z, save_mean, save_invstd, new_rm,
+                         new_rv, (int)c, act, sp.rows);
+    else
+      hipLaunchKernelGGL(bn_nhwc_fused_kernel<1>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, x, gamma,
+                         beta, running_mean, running_var, momentum, eps, residual, y, z, save_mean, save_invstd, new_rm,
+                         new_rv, (int)c, act, sp.rows);
+    return launch_check("bn_nhwc_fused_kernel");
+  }
   double* part = (double*)workspace;
   const dim3 sg((unsigned)sp.cblocks, (unsigned)sp.slices);
   if (sp.vec == 4)
@@ -1887,6 +2085,16 @@ OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g,
   const float* ry = act == OMT_ACT_NONE ? nullptr : act_in;
   const NhwcSplit sp =
       nhwc_split(n, c, hw, (g_nchw || al16(g)) && al16(g2) && al16(x) && al16(ry) && al16(gx) && al16(gz));
+  if (nhwc_fused_ok(sp)) {
+    const float* gam = (gx || gz) ? gamma : nullptr;
+    if (sp.vec == 4)
+      hipLaunchKernelGGL(bn_nhwc_bwd_fused_kernel<4>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, g, g2,
+                         x, ry, save_mean, save_invstd, gam, gx, dgamma, dbeta, gz, (int)c, act, sp, g_nchw ? 1 : 0);
+    else
+      hipLaunchKernelGGL(bn_nhwc_bwd_fused_kernel<1>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, g, g2,
+                         x, ry, save_mean, save_invstd, gam, gx, dgamma, dbeta, gz, (int)c, act, sp, g_nchw ? 1 : 0);
+    return launch_check("bn_nhwc_bwd_fused_kernel");
+  }
   double* part = (double*)workspace;
   float* kc = (float*)(part + c * kNhwcMaxSlices * 2);
   const dim3 pg((unsigned)sp.cblocks, (unsigned)sp.slices);

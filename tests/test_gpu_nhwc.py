@@ -289,13 +289,14 @@ def dev(a, cuda):
 
 BN_NHWC = [(4, 6, 5, 7), (16, 8, 4, 4), (32, 64, 16, 16), (32, 512, 2, 2), (3, 5, 37, 41), (64, 16, 28, 28),
            (8, 3, 7, 9), (4, 8, 56, 56), (32, 96, 7, 7), (2, 576, 7, 7), (1, 16, 57, 31), (9, 12, 15, 15),
-           (128, 32, 32, 32), (2, 260, 3, 5)]
+           (128, 32, 32, 32), (2, 260, 3, 5), (8, 64, 16, 16), (1, 12, 41, 50)]
 
 
 @pytest.mark.parametrize("n,c,h,w", BN_NHWC, ids=lambda v: str(v))
 def test_batch_norm_nhwc(cuda, ops, n, c, h, w):
     """omt_bn_train_fwd_nhwc / omt_bn_eval_fwd_nhwc / omt_bn_bwd_nhwc over channels_last tensors (float4 channel runs
-    when c % 4 == 0, scalar otherwise; one and several channel blocks per row) against the oracle (the statistics
+    when c % 4 == 0, scalar otherwise; one and several channel blocks per row; one launch up to 2048 rows, three
+    above: 8 x 16², 2048 rows, and 41 x 50, 2050) against the oracle (the statistics
     from inputs of large mean), and against the NCHW kernels on the same data: the statistics agree to float64
     rounding (rel 1e-6), eval is the same arithmetic bit for bit, and the backward's gz (the gradient through the
     activation, with a second gradient added) is exact."""
