@@ -1791,10 +1791,12 @@ __global__ void __launch_bounds__(256) bn_nhwc_bwd_apply_kernel(const float* __r
 }
 
 // A channels-last BatchNorm of at most kNhwcFusedRows rows runs in one launch instead of three: workgroup j owns
-// channel vector j (VEC channels) over every row, thread t rows t, t + blockDim.x, ... (kNhwcFusedRpt of them, in
-// registers), so the sums, the finalize and the apply need no partials. Each lane reads VEC channels of a row, a
-// 16-byte run rows apart: one workgroup reads its vector at the rate one CU fetches scattered lines, which the
-// shortest tensors (ResNet-18 b32 64²'s last three stages: 2048 rows and fewer) finish sooner than three launches.
+// channel vector j (VEC channels) over every row, thread t rows t, t + blockDim.x, ... (RPT of them, in registers),
+// so the sums, the finalize and the apply need no partials. Each lane reads VEC channels of a row, a 16-byte run rows
+// apart: one workgroup reads its vector at the rate one CU fetches scattered lines, which the shortest tensors
+// (ResNet-18 b32 64²'s last three stages: 2048 rows and fewer) finish sooner than three launches; at 8192 rows (eight
+// per thread) the one workgroup per vector is slower than three launches over the whole chip. The backward keeps gz
+// (through the activation) and x, not g and ry.
 // The sums are the shifted float64 sums of the three-launch path in another order (each thread's rows in order, the
 // wave sums in wave order); the finalize and apply arithmetic is the same.
 constexpr int64_t kNhwcFusedRows = 2048;
@@ -1829,7 +1831,7 @@ __device__ __forceinline__ void nhwc_block_sums(double* a, double* b) {
 
 // grid cv (channel vectors), blockDim nhwc_fused_threads: the training forward of bn_nhwc_stats_kernel,
 // bn_nhwc_fin_kernel and bn_nhwc_apply_kernel in one pass over x
-template <int VEC>
+template <int VEC, int RPT>
 __global__ void __launch_bounds__(1024) bn_nhwc_fused_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta, const float* rm,
@@ -1843,9 +1845,9 @@ __global__ void __launch_bounds__(1024) bn_nhwc_fused_kernel(const float* __rest
   __shared__ float coef[2][VEC];
   const int j = blockIdx.x, nt = blockDim.x;
   const V shift = *reinterpret_cast<const V*>(x + (int64_t)j * VEC);
-  V r[kNhwcFusedRpt];
+  V r[RPT];
 #pragma unroll
-  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+  for (int u = 0; u < RPT; ++u) {
     const int64_t row = threadIdx.x + (int64_t)u * nt;
     r[u] = row < rows ? *reinterpret_cast<const V*>(x + row * c + (int64_t)j * VEC) : shift;  // d = 0 past the end
   }
@@ -1854,7 +1856,7 @@ __global__ void __launch_bounds__(1024) bn_nhwc_fused_kernel(const float* __rest
   for (int i = 0; i < VEC; ++i) {
     s1[i] = 0.0, s2[i] = 0.0;
 #pragma unroll
-    for (int u = 0; u < kNhwcFusedRpt; ++u) {
+    for (int u = 0; u < RPT; ++u) {
       const double d = (double)(vget(r[u], i) - vget(shift, i));
       s1[i] += d;
       s2[i] += d * d;
@@ -1874,7 +1876,7 @@ __global__ void __launch_bounds__(1024) bn_nhwc_fused_kernel(const float* __rest
 #pragma unroll
   for (int i = 0; i < VEC; ++i) sc[i] = coef[0][i], sh[i] = coef[1][i];
 #pragma unroll
-  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+  for (int u = 0; u < RPT; ++u) {
     const int64_t row = threadIdx.x + (int64_t)u * nt;
     if (row < rows) {
       const int64_t off = row * c + (int64_t)j * VEC;
@@ -1895,7 +1897,7 @@ __global__ void __launch_bounds__(1024) bn_nhwc_fused_kernel(const float* __rest
 
 // grid cv, blockDim nhwc_fused_threads: bn_nhwc_bwd_part_kernel, bn_nhwc_bwd_fin_kernel and bn_nhwc_bwd_apply_kernel
 // in one pass over g (+ g2), x and ry
-template <int VEC>
+template <int VEC, int RPT>
 __global__ void __launch_bounds__(1024) bn_nhwc_bwd_fused_kernel(const float* __restrict__ g,
                                                                  const float* __restrict__ g2,
                                                                  const float* __restrict__ x,
@@ -1912,22 +1914,25 @@ __global__ void __launch_bounds__(1024) bn_nhwc_bwd_fused_kernel(const float* __
   float mu[VEC], inv[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i) mu[i] = mean[j * VEC + i], inv[i] = invstd[j * VEC + i];
-  V vg[kNhwcFusedRpt], vx[kNhwcFusedRpt], vr[kNhwcFusedRpt];
+  V vg[RPT], vx[RPT];  // vg: gz, the gradient through the activation
 #pragma unroll
-  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+  for (int u = 0; u < RPT; ++u) {
     const int64_t row = threadIdx.x + (int64_t)u * nt;
     if (row < sp.rows) {
       const int64_t off = row * c + (int64_t)j * VEC;
       vg[u] = nhwc_grad<VEC>(g, g_nchw, row, j, c, sp);
       if (g2) vadd(vg[u], *reinterpret_cast<const V*>(g2 + off));
       vx[u] = *reinterpret_cast<const V*>(x + off);
-      if (ry) vr[u] = *reinterpret_cast<const V*>(ry + off);
+      if (ry) {
+        const V vr = *reinterpret_cast<const V*>(ry + off);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) vset(vg[u], i, bn_act_grad(vget(vg[u], i), vget(vr, i), act));
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         vset(vg[u], i, 0.f);  // gz = 0 contributes nothing
         vset(vx[u], i, mu[i]);
-        vset(vr[u], i, 1.f);
       }
     }
   }
@@ -1936,9 +1941,8 @@ __global__ void __launch_bounds__(1024) bn_nhwc_bwd_fused_kernel(const float* __
   for (int i = 0; i < VEC; ++i) {
     s1[i] = 0.0, s2[i] = 0.0;
 #pragma unroll
-    for (int u = 0; u < kNhwcFusedRpt; ++u) {
-      float gz = vget(vg[u], i);
-      if (ry) gz = bn_act_grad(gz, vget(vr[u], i), act);
+    for (int u = 0; u < RPT; ++u) {
+      const float gz = vget(vg[u], i);
       const float xhat = (vget(vx[u], i) - mu[i]) * inv[i];
       s1[i] += (double)gz;
       s2[i] += (double)gz * (double)xhat;
@@ -1959,20 +1963,15 @@ __global__ void __launch_bounds__(1024) bn_nhwc_bwd_fused_kernel(const float* __
 #pragma unroll
     for (int e = 0; e < 5; ++e) k[i][e] = kc[i][e];
 #pragma unroll
-  for (int u = 0; u < kNhwcFusedRpt; ++u) {
+  for (int u = 0; u < RPT; ++u) {
     const int64_t row = threadIdx.x + (int64_t)u * nt;
     if (row < sp.rows) {
       const int64_t off = row * c + (int64_t)j * VEC;
-      V o, z;
+      V o;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        float gz = vget(vg[u], i);
-        if (ry) gz = bn_act_grad(gz, vget(vr[u], i), act);
-        vset(z, i, gz);
-        vset(o, i, bwd_elem(gz, vget(vx[u], i), 1.f, false, k[i]));
-      }
+      for (int i = 0; i < VEC; ++i) vset(o, i, bwd_elem(vget(vg[u], i), vget(vx[u], i), 1.f, false, k[i]));
       if (gx) *reinterpret_cast<V*>(gx + off) = o;
-      if (gzo) *reinterpret_cast<V*>(gzo + off) = z;
+      if (gzo) *reinterpret_cast<V*>(gzo + off) = vg[u];
     }
   }
 }
@@ -2018,14 +2017,15 @@ OMT_EXPORT int omt_bn_train_fwd_nhwc(int64_t n, int64_t c, int64_t hw, const flo
   hipStream_t s = stream_of(stream);
   const NhwcSplit sp = nhwc_split(n, c, hw, al16(x) && al16(y) && al16(residual) && al16(z));
   if (nhwc_fused_ok(sp)) {
+#define OMT_NHWC_FUSED(V, R)                                                                                       \
+  hipLaunchKernelGGL((bn_nhwc_fused_kernel<V, R>), dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, x, gamma, \
+                     beta, running_mean, running_var, momentum, eps, residual, y, z, save_mean, save_invstd, new_rm,   \
+                     new_rv, (int)c, act, sp.rows)
     if (sp.vec == 4)
-      hipLaunchKernelGGL(bn_nhwc_fused_kernel<4>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, x, gamma,
-                         beta, running_mean, running_var, momentum, eps, residual, y, z, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, act, sp.rows);
+      OMT_NHWC_FUSED(4, kNhwcFusedRpt);
     else
-      hipLaunchKernelGGL(bn_nhwc_fused_kernel<1>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, x, gamma,
-                         beta, running_mean, running_var, momentum, eps, residual, y, z, save_mean, save_invstd, new_rm,
-                         new_rv, (int)c, act, sp.rows);
+      OMT_NHWC_FUSED(1, kNhwcFusedRpt);
+#undef OMT_NHWC_FUSED
     return launch_check("bn_nhwc_fused_kernel");
   }
   double* part = (double*)workspace;
@@ -2087,12 +2087,14 @@ OMT_EXPORT int omt_bn_bwd_nhwc(int64_t n, int64_t c, int64_t hw, const float* g,
       nhwc_split(n, c, hw, (g_nchw || al16(g)) && al16(g2) && al16(x) && al16(ry) && al16(gx) && al16(gz));
   if (nhwc_fused_ok(sp)) {
     const float* gam = (gx || gz) ? gamma : nullptr;
+#define OMT_NHWC_BWD_FUSED(V, R)                                                                                   \
+  hipLaunchKernelGGL((bn_nhwc_bwd_fused_kernel<V, R>), dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, g,    \
+                     g2, x, ry, save_mean, save_invstd, gam, gx, dgamma, dbeta, gz, (int)c, act, sp, g_nchw ? 1 : 0)
     if (sp.vec == 4)
-      hipLaunchKernelGGL(bn_nhwc_bwd_fused_kernel<4>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, g, g2,
-                         x, ry, save_mean, save_invstd, gam, gx, dgamma, dbeta, gz, (int)c, act, sp, g_nchw ? 1 : 0);
+      OMT_NHWC_BWD_FUSED(4, kNhwcFusedRpt);
     else
-      hipLaunchKernelGGL(bn_nhwc_bwd_fused_kernel<1>, dim3((unsigned)sp.cv), dim3(nhwc_fused_threads(sp)), 0, s, g, g2,
-                         x, ry, save_mean, save_invstd, gam, gx, dgamma, dbeta, gz, (int)c, act, sp, g_nchw ? 1 : 0);
+      OMT_NHWC_BWD_FUSED(1, kNhwcFusedRpt);
+#undef OMT_NHWC_BWD_FUSED
     return launch_check("bn_nhwc_bwd_fused_kernel");
   }
   double* part = (double*)workspace;
