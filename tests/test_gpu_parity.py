@@ -493,6 +493,34 @@ def test_conv_epilogue_bn_statistics(cuda, ops, shape):
         ops.clear_conv_plans()
 
 
+def test_conv_epilogue_bn_statistics_large_mean(cuda, ops):
+    """The epilogue's statistics are unshifted float64 sums of y and y^2 (finalized with shift 0), where the
+    three-pass path subtracts a per-channel shift first. Outputs whose mean is 75-90 times their spread (positive
+    inputs, offset by 4, and positive filters, no padding) still normalize to the oracle's: fp32 squares of fp32
+    values are exact in float64 and their sums lose ~1e-16 each, so E[y^2] - E[y]^2 keeps ~1e-16 * (mean / std)^2
+    ~ 1e-12 relative, far under the test's bounds."""
+    shape = (4, 16, 24, 12, 12, 3, 1, 0)  # no padding: every window sums all its taps
+    n, ci, co, h, w, ks, s, p = shape
+    rng = np.random.default_rng(2024)
+    x = np.abs(rnd(rng, n, ci, h, w)) + 4.0  # every window sums many positive terms: mean >> spread
+    wt = np.abs(rnd(rng, co, ci, ks, ks, scale=(ci * ks * ks) ** -0.5))
+    gam, bet, rm, rv = rnd(rng, co), rnd(rng, co), rnd(rng, co), np.abs(rnd(rng, co)) + 0.5
+    try:
+        ops.set_conv_plan("fwd", x.shape, wt.shape, s, p, 5, 1)
+        y, st, groups = ops.conv2d_stats(dev(x, cuda), dev(wt, cuda), s, p)
+        y_in = orc.conv_fwd(x, wt, None, s, p)
+        assert (y_in.mean(axis=(0, 2, 3)) / y_in.std(axis=(0, 2, 3))).min() > 50
+        trm, trv = dev(rm, cuda), dev(rv, cuda)
+        yb, sm, si = ops.batch_norm_train_stats(y, st, groups, dev(gam, cuda), dev(bet, cuda), trm, trv, 0.1, 1e-5,
+                                                False, None)
+        y_bn, m_ref, i_ref, nrm, nrv = orc.bn_train(y_in, gam, bet, rm, rv, 0.1, 1e-5, False)
+        assert orc.rel_l2(host(yb), y_bn) <= TOL
+        assert orc.rel_l2(host(sm), m_ref) <= 1e-6 and orc.rel_l2(host(si), i_ref) <= 1e-5
+        assert orc.rel_l2(host(trm), nrm) <= 1e-6 and orc.rel_l2(host(trv), nrv) <= 1e-5
+    finally:
+        ops.clear_conv_plans()
+
+
 def test_autotune_caches_a_plan(cuda, ops):
     """omt_conv_autotune times the candidates and caches the fastest; calls then use it (reference autotune,
     csrc/conv.cpp:116-155)."""
