@@ -1744,6 +1744,27 @@ __global__ void __launch_bounds__(256) pack_dgrad_weights_kernel(const PackArgs 
   }
 }
 
+// The stride-1 case of pack_dgrad_weights_kernel for a channels-last filter in tap-major order (one phase, all KK
+// taps, ky0 = kx0 = 0): out[ci][t][co] = w[co][KK - 1 - t][ci], a transpose of (co, ci) per tap, run as 32 x 32 tiles
+// through LDS (grid: ci tiles, co tiles, taps) so that the reads (runs of ci) and the writes (runs of co) are whole
+// 128-byte lines instead of one line per element on the read side.
+__global__ void __launch_bounds__(256) pack_dgrad_krsc_s1_kernel(const float* __restrict__ w, float* __restrict__ out,
+                                                                 int CO, int CI, int KK) {
+  __shared__ float tile[32][33];
+  const int tap = blockIdx.z, co0 = blockIdx.y * 32, ci0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8) {
+    const int co = co0 + r, ci = ci0 + tx;
+    if (co < CO && ci < CI) tile[r][tx] = w[((int64_t)co * KK + tap) * CI + ci];
+  }
+  __syncthreads();
+  const int t = KK - 1 - tap;  // the flipped tap
+  for (int r = ty; r < 32; r += 8) {
+    const int ci = ci0 + r, co = co0 + tx;
+    if (co < CO && ci < CI) out[((int64_t)ci * KK + t) * CO + co] = tile[tx][r];
+  }
+}
+
 // Super-pixel grad-input filter W'[p = (py s + px) CI + c][k]: k = (dy L + dx) CO + co (tap-major) or
 // co L L + dy L + dx, the L x L window of gy rows i + dy - PH around grid pixel i. Phase (py, px) reaches gy row
 // i + qy - a' through filter row ky0 + s a' (a' < jy; ky0 = (py + pad) mod s, qy = (py + pad - ky0) / s), so window row
@@ -3214,8 +3235,16 @@ static int conv_dgrad_nhwc_one(const omt_conv_geo* g, const float* gy, const flo
   pk.S = (int)g->stride;
   pk.tap_major = 1;
   pk.src_krsc = 1;
-  hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
-  if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
+  const int kk = (int)(g->ks * g->ks);
+  if (g->stride == 1 && pk.nphase == 1 && pk.ph[0].ky0 == 0 && pk.ph[0].kx0 == 0 && pk.ph[0].jy == (int)g->ks &&
+      pk.ph[0].jx == (int)g->ks && pk.ph[0].woff == 0 && (int64_t)packed == g->co * g->ci * kk) {
+    hipLaunchKernelGGL(pack_dgrad_krsc_s1_kernel, dim3((unsigned)cdiv(g->ci, 32), (unsigned)cdiv(g->co, 32), (unsigned)kk),
+                       dim3(256), 0, s, w, (float*)workspace, (int)g->co, (int)g->ci, kk);
+    if (int st = launch_check("pack_dgrad_krsc_s1_kernel")) return st;
+  } else {
+    hipLaunchKernelGGL(pack_dgrad_weights_kernel, dim3(grid1d(packed, 256, 4096)), dim3(256), 0, s, pk);
+    if (int st = launch_check("pack_dgrad_weights_kernel")) return st;
+  }
   a.x = gy;
   a.w = (const float*)workspace;
   a.w_bytes = (uint32_t)(packed * 4);
